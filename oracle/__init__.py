@@ -1,0 +1,364 @@
+"""ctypes view of the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` -- as the checker, or as the timed CPU port of
+the reference.  The product package ``klearu_amd`` never imports this module.
+
+Each wrapper converts numpy arrays and calls the C restatement in ``oracle.c`` /
+``oracle_avx2.c``; the reference citations live there.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_SO = os.path.join(_HERE, "liboracle.so")
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the committed Makefile."""
+    if force or not os.path.exists(_SO):
+        subprocess.run(["make", "-s", "-C", _HERE, "-B" if force else "all"], check=True)
+    return _SO
+
+
+def _load() -> C.CDLL:
+    if not os.path.exists(_SO):
+        build()
+    return C.CDLL(_SO)
+
+
+lib = _load()
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+_u64p = np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_i64 = C.c_int64
+_int = C.c_int
+_f = C.c_float
+
+
+def _sig(name, res, *args):
+    fn = getattr(lib, name)
+    fn.restype = res
+    fn.argtypes = list(args)
+    return fn
+
+
+_sig("or_dense_dot_avx2_order", _f, _f32p, _f32p, _i64)
+_sig("or_dense_dot_scalar", _f, _f32p, _f32p, _i64)
+_sig("or_avx2_dense_dot", _f, _f32p, _f32p, _i64)
+_sig("or_sparse_dot_dense_avx2_order", _f, _u32p, _f32p, _i64, _f32p)
+_sig("or_sparse_dot_dense_scalar", _f, _u32p, _f32p, _i64, _f32p)
+_sig("or_avx2_sparse_dot_dense", _f, _u32p, _f32p, _i64, _f32p)
+_sig("or_scatter_add", None, _u32p, _f32p, _i64, _f32p, _f)
+_sig("or_bf16_from_f32", C.c_uint16, _f)
+_sig("or_bf16_to_f32", _f, C.c_uint16)
+_sig("or_bf16_from_f32_n", None, _f32p, _u16p, _i64)
+_sig("or_bf16_dot_f32", _f, _u16p, _f32p, _i64)
+_sig("or_bf16_full_dot", _f, _u16p, _u16p, _i64)
+_sig("or_bf16_update_from_f32", None, _u16p, _f32p, _i64)
+_sig("or_chacha_block", None, _u32p, _int, _u32p)
+_sig("or_pcg32_output", C.c_uint32, C.c_uint64)
+_sig("or_simhash_planes", None, _int, _int, _int, C.c_uint64, _i8p)
+_sig("or_srp_planes", None, _int, _int, _int, _f, C.c_uint64, _i8p)
+_sig("or_hash_dense", C.c_uint64, _i8p, _int, _int, _int, _f32p)
+_sig("or_hash_sparse", C.c_uint64, _i8p, _int, _int, _int, _u32p, _f32p, _i64)
+_sig("or_hash_dense_batch", None, _i8p, _int, _int, _int, _f32p, _i64, _u32p)
+_sig("or_reservoir_rand", C.c_uint64, C.c_uint64, C.c_uint64)
+_sig("or_lsh_insert_many", None, _int, _int, _int, _int, _u32p, _u32p, _u64p, _i64, _u32p, _u32p)
+_sig("or_lsh_query", _i64, _int, _int, _int, _u32p, _u32p, _u32p, _u32p, _u32p)
+_sig("or_sample_topk", _i64, _u32p, _u32p, _i64, _i64, _u32p)
+_sig("or_sample_threshold", _i64, _u32p, _u32p, _i64, C.c_uint32, _u32p)
+_sig("or_neuron_forward", _f, _f32p, _f, _f32p, _i64)
+_sig("or_neuron_forward_sparse", _f, _f32p, _f, _u32p, _f32p, _i64)
+_sig("or_layer_activate", None, _f32p, _i64, _int, _f32p)
+_sig("or_predictor_predict", None, _f32p, _f32p, _f32p, _f32p, _int, _int, _int, _f32p, _f32p, _f32p)
+_sig("or_predictor_predict_bf16", None, _u16p, _f32p, _u16p, _f32p, _int, _int, _int, _f32p, _f32p,
+     _f32p)
+_sig("or_select_top_k", None, _f32p, _i64, _i64, _i64p)
+_sig("or_sigmoid", _f, _f)
+_sig("or_silu", _f, _f)
+_sig("or_sparse_mlp_forward_bf16", None, _u16p, _u16p, _u16p, _int, _int, _f32p, _i64p, _i64, _f32p,
+     _f32p)
+_sig("or_rmsnorm", None, _f32p, _f32p, _i64, _f)
+_sig("or_rope_tables", None, _int, _int, _f, _f32p, _f32p)
+_sig("or_rope_apply", None, _f32p, _int, _f32p, _f32p, _i64)
+_sig("or_linear_forward_bf16", None, _u16p, _int, _int, _f32p, _f32p)
+_sig("or_sparse_attention_forward_bf16", None, _u16p, _u16p, _u16p, _u16p, _int, _int, _int, _int,
+     _f32p, _i64, _f32p, _f32p, _f32p, _f32p, _i64, _i64p, _i64, _f32p)
+_sig("or_dejavu_linear_forward_sparse", None, _f32p, _f32p, _int, _f32p, _i64p, _i64, _f32p)
+_sig("or_dejavu_sparse_mlp_forward", None, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _int, _int,
+     _f32p, _i64p, _i64, _f32p)
+_sig("or_cpu_dejavu_ffn_layer", None, _f32p, _f32p, _f32p, _f32p, _f, _f32p, _f32p, _f32p, _f32p, _int,
+     _int, _int, _i64, _f32p, _f32p, _i64p)
+
+ACT = {"relu": 0, "sigmoid": 1, "tanh": 2, "softmax": 3, "identity": 4}
+FIFO, RESERVOIR = 0, 1
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def u32(a):
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+def i64(a):
+    return np.ascontiguousarray(a, dtype=np.int64)
+
+
+# --------------------------------------------------------------------------- accel
+def dense_dot(a, b):
+    a, b = f32(a), f32(b)
+    return np.float32(lib.or_dense_dot_avx2_order(a, b, a.size))
+
+
+def dense_dot_avx2(a, b):
+    a, b = f32(a), f32(b)
+    return np.float32(lib.or_avx2_dense_dot(a, b, a.size))
+
+
+def dense_dot_scalar(a, b):
+    a, b = f32(a), f32(b)
+    return np.float32(lib.or_dense_dot_scalar(a, b, a.size))
+
+
+def sparse_dot_dense(idx, val, dense):
+    idx, val, dense = u32(idx), f32(val), f32(dense)
+    return np.float32(lib.or_sparse_dot_dense_avx2_order(idx, val, idx.size, dense))
+
+
+def sparse_dot_dense_avx2(idx, val, dense):
+    idx, val, dense = u32(idx), f32(val), f32(dense)
+    return np.float32(lib.or_avx2_sparse_dot_dense(idx, val, idx.size, dense))
+
+
+def sparse_dot_dense_scalar(idx, val, dense):
+    idx, val, dense = u32(idx), f32(val), f32(dense)
+    return np.float32(lib.or_sparse_dot_dense_scalar(idx, val, idx.size, dense))
+
+
+def scatter_add(idx, val, dense, scale):
+    idx, val = u32(idx), f32(val)
+    out = f32(dense).copy()
+    lib.or_scatter_add(idx, val, idx.size, out, float(scale))
+    return out
+
+
+def bf16_from_f32(x):
+    x = f32(x)
+    out = np.empty(x.shape, np.uint16)
+    lib.or_bf16_from_f32_n(x.ravel(), out.reshape(-1), x.size)
+    return out
+
+
+def bf16_to_f32(b):
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_dot_f32(w, x):
+    w, x = np.ascontiguousarray(w, np.uint16), f32(x)
+    return np.float32(lib.or_bf16_dot_f32(w, x, w.size))
+
+
+def bf16_full_dot(a, b):
+    a, b = np.ascontiguousarray(a, np.uint16), np.ascontiguousarray(b, np.uint16)
+    return np.float32(lib.or_bf16_full_dot(a, b, a.size))
+
+
+def bf16_update_from_f32(w, delta):
+    w = np.ascontiguousarray(w, np.uint16).copy()
+    lib.or_bf16_update_from_f32(w, f32(delta), w.size)
+    return w
+
+
+# --------------------------------------------------------------------------- rng / hash
+def chacha_block(words16, rounds):
+    inp = u32(words16)
+    out = np.zeros(16, np.uint32)
+    lib.or_chacha_block(inp, rounds, out)
+    return out
+
+
+def simhash_planes(dim, k, num_tables, seed):
+    p = np.empty(num_tables * k * dim, np.int8)
+    lib.or_simhash_planes(dim, k, num_tables, seed, p)
+    return p.reshape(num_tables, k, dim)
+
+
+def srp_planes(dim, k, num_tables, sparsity, seed):
+    p = np.empty(num_tables * k * dim, np.int8)
+    lib.or_srp_planes(dim, k, num_tables, float(sparsity), seed, p)
+    return p.reshape(num_tables, k, dim)
+
+
+def hash_dense(planes, x, table):
+    L, k, dim = planes.shape
+    return int(lib.or_hash_dense(np.ascontiguousarray(planes).reshape(-1), dim, k, table, f32(x)))
+
+
+def hash_sparse(planes, idx, val, table):
+    L, k, dim = planes.shape
+    idx, val = u32(idx), f32(val)
+    return int(lib.or_hash_sparse(np.ascontiguousarray(planes).reshape(-1), dim, k, table, idx, val,
+                                  idx.size))
+
+
+def hash_dense_batch(planes, X):
+    L, k, dim = planes.shape
+    X = f32(X).reshape(-1, dim)
+    codes = np.zeros((X.shape[0], L), np.uint32)
+    lib.or_hash_dense_batch(np.ascontiguousarray(planes).reshape(-1), dim, k, L, X.reshape(-1),
+                            X.shape[0], codes.reshape(-1))
+    return codes
+
+
+class LshIndex:
+    """Dense bucket tables [L][2^K][cap] filled by the reference insert rules."""
+
+    def __init__(self, num_tables, k, cap, bucket_type):
+        self.L, self.k, self.cap, self.type = num_tables, k, cap, bucket_type
+        nb = 1 << k
+        self.data = np.zeros(num_tables * nb * cap, np.uint32)
+        self.len = np.zeros(num_tables * nb, np.uint32)
+        self.count = np.zeros(num_tables * nb, np.uint64)
+
+    def insert_many(self, ids, codes):
+        ids, codes = u32(ids), u32(codes).reshape(-1)
+        lib.or_lsh_insert_many(self.L, self.k, self.cap, self.type, self.data, self.len, self.count,
+                               ids.size, ids, codes)
+
+    def query(self, codes):
+        codes = u32(codes).reshape(-1)
+        ids = np.zeros(self.L * self.cap + 1, np.uint32)
+        cnt = np.zeros(self.L * self.cap + 1, np.uint32)
+        n = lib.or_lsh_query(self.L, self.k, self.cap, self.data, self.len, codes, ids, cnt)
+        return ids[:n].copy(), cnt[:n].copy()
+
+    def bucket(self, t, b):
+        nb = 1 << self.k
+        s = t * nb + b
+        return self.data[s * self.cap: s * self.cap + int(self.len[s])].copy()
+
+
+def sample_topk(ids, counts, k):
+    ids, counts = u32(ids), u32(counts)
+    out = np.zeros(max(ids.size, 1), np.uint32)
+    n = lib.or_sample_topk(ids, counts, ids.size, k, out)
+    return out[:n].copy()
+
+
+def sample_threshold(ids, counts, t):
+    ids, counts = u32(ids), u32(counts)
+    out = np.zeros(max(ids.size, 1), np.uint32)
+    n = lib.or_sample_threshold(ids, counts, ids.size, t, out)
+    return out[:n].copy()
+
+
+# --------------------------------------------------------------------------- SLIDE
+def neuron_forward(w, b, x):
+    w, x = f32(w), f32(x)
+    return np.float32(lib.or_neuron_forward(w, float(b), x, w.size))
+
+
+def neuron_forward_sparse(w, b, idx, val):
+    w, idx, val = f32(w), u32(idx), f32(val)
+    return np.float32(lib.or_neuron_forward_sparse(w, float(b), idx, val, idx.size))
+
+
+def layer_activate(pre, act):
+    pre = f32(pre)
+    out = np.zeros_like(pre)
+    lib.or_layer_activate(pre, pre.size, ACT[act] if isinstance(act, str) else act, out)
+    return out
+
+
+# --------------------------------------------------------------------------- Deja Vu
+def predictor_predict(w1, b1, w2, b2, x):
+    hid, ind = w1.shape
+    out = w2.shape[0]
+    scores = np.zeros(out, np.float32)
+    h = np.zeros(hid, np.float32)
+    if w1.dtype == np.uint16:
+        lib.or_predictor_predict_bf16(np.ascontiguousarray(w1).reshape(-1), f32(b1),
+                                      np.ascontiguousarray(w2).reshape(-1), f32(b2), ind, hid, out,
+                                      f32(x), scores, h)
+    else:
+        lib.or_predictor_predict(f32(w1).reshape(-1), f32(b1), f32(w2).reshape(-1), f32(b2), ind,
+                                 hid, out, f32(x), scores, h)
+    return scores, h
+
+
+def select_top_k(scores, k):
+    scores = f32(scores)
+    m = min(k, scores.size)
+    out = np.zeros(max(m, 1), np.int64)
+    lib.or_select_top_k(scores, scores.size, k, out)
+    return out[:m].copy()
+
+
+def sparse_mlp_forward_bf16(wg, wu, wd, x, active):
+    inter, hidden = wg.shape
+    active = i64(active)
+    y = np.zeros(hidden, np.float32)
+    h = np.zeros(max(active.size, 1), np.float32)
+    lib.or_sparse_mlp_forward_bf16(np.ascontiguousarray(wg).reshape(-1),
+                                   np.ascontiguousarray(wu).reshape(-1),
+                                   np.ascontiguousarray(wd).reshape(-1), hidden, inter, f32(x),
+                                   active, active.size, y, h)
+    return y, h[:active.size].copy()
+
+
+def rmsnorm(x, w, eps):
+    x = f32(x).copy()
+    lib.or_rmsnorm(x, f32(w), x.size, float(eps))
+    return x
+
+
+def rope_tables(head_dim, max_seq, theta):
+    c = np.zeros(max_seq * (head_dim // 2), np.float32)
+    s = np.zeros_like(c)
+    lib.or_rope_tables(head_dim, max_seq, float(theta), c, s)
+    return c, s
+
+
+def linear_forward_bf16(w, x):
+    out_f, in_f = w.shape
+    y = np.zeros(out_f, np.float32)
+    lib.or_linear_forward_bf16(np.ascontiguousarray(w).reshape(-1), out_f, in_f, f32(x), y)
+    return y
+
+
+def sparse_attention_forward_bf16(wq, wk, wv, wo, num_heads, num_kv_heads, head_dim, x, pos, cos_t,
+                                  sin_t, k_cache, v_cache, heads):
+    """k_cache/v_cache: float32 [kv_heads][max_seq][d], modified in place (row pos appended)."""
+    hidden = wq.shape[1]
+    max_seq = k_cache.shape[1]
+    out = np.zeros(hidden, np.float32)
+    heads = i64(heads)
+    lib.or_sparse_attention_forward_bf16(
+        np.ascontiguousarray(wq).reshape(-1), np.ascontiguousarray(wk).reshape(-1),
+        np.ascontiguousarray(wv).reshape(-1), np.ascontiguousarray(wo).reshape(-1), hidden,
+        num_heads, num_kv_heads, head_dim, f32(x), pos, cos_t, sin_t, k_cache.reshape(-1),
+        v_cache.reshape(-1), max_seq, heads, heads.size, out)
+    return out
+
+
+def dejavu_sparse_mlp_forward(wg, bg, wu, bu, wd, bd, x, sel):
+    inter, hidden = wg.shape
+    sel = i64(sel)
+    y = np.zeros(hidden, np.float32)
+    lib.or_dejavu_sparse_mlp_forward(f32(wg).reshape(-1), f32(bg), f32(wu).reshape(-1), f32(bu),
+                                     f32(wd).reshape(-1), f32(bd), hidden, inter, f32(x), sel,
+                                     sel.size, y)
+    return y

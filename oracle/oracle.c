@@ -1,0 +1,841 @@
+/*
+ * oracle.c -- CPU restatement of klearu's activation-sparse inference path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): the checker for the HIP library and
+ * the timed CPU port for bench.py's cpu_baseline.  Never linked by the product.
+ *
+ * Build: gcc -O2 -fPIC -shared -ffp-contract=off -fno-fast-math oracle.c -lm
+ * (no -mfma: fmaf() is then glibc's correctly rounded fused multiply-add, the
+ * same single rounding as _mm256_fmadd_ps).
+ *
+ * Citations are path:line in the reference tree (QuilibriumNetwork/klearu).
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ======================================================================== */
+/* klearu-accel: crates/klearu-accel/src/simd/mod.rs                         */
+/* ======================================================================== */
+
+/* hsum_avx2 (simd/mod.rs:128-141): [v0+v4, v1+v5, v2+v6, v3+v7] -> movehdup
+ * pairs lane 1 into lane 0 and lane 3 into lane 2 -> movehl brings lane 2 down
+ * -> add_ss.  Result: ((v0+v4)+(v1+v5)) + ((v2+v6)+(v3+v7)).
+ * Pinned: brute-force equality with the AVX2 intrinsic build (oracle_avx2.c)
+ * in tests/test_oracle_accel.py. */
+static float hsum8(const float v[8]) {
+  float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+  float t0 = s0 + s1;
+  float t2 = s2 + s3;
+  return t0 + t2;
+}
+
+/* dense_dot_dense_avx2 (simd/mod.rs:174-207): two 8-lane FMA accumulators over
+ * 16-element chunks, an optional extra 8-chunk into acc0, hsum(acc0+acc1), then
+ * a scalar tail `sum += a[i]*b[i]` (product rounded, then added).
+ * Pinned: KATs simd/mod.rs:428 (=32), AVX2 intrinsic build equality. */
+float or_dense_dot_avx2_order(const float* a, const float* b, int64_t n) {
+  float acc0[8], acc1[8];
+  for (int l = 0; l < 8; ++l) acc0[l] = acc1[l] = 0.0f;
+  int64_t chunks = n / 16;
+  for (int64_t c = 0; c < chunks; ++c) {
+    const int64_t o = c * 16;
+    for (int l = 0; l < 8; ++l) acc0[l] = fmaf(a[o + l], b[o + l], acc0[l]);
+    for (int l = 0; l < 8; ++l) acc1[l] = fmaf(a[o + 8 + l], b[o + 8 + l], acc1[l]);
+  }
+  int64_t rs = chunks * 16;
+  int extra = (rs + 8 <= n);
+  if (extra)
+    for (int l = 0; l < 8; ++l) acc0[l] = fmaf(a[rs + l], b[rs + l], acc0[l]);
+  float v[8];
+  for (int l = 0; l < 8; ++l) v[l] = acc0[l] + acc1[l];
+  float sum = hsum8(v);
+  for (int64_t i = extra ? rs + 8 : rs; i < n; ++i) {
+    float p = a[i] * b[i];
+    sum = sum + p;
+  }
+  return sum;
+}
+
+/* dense_dot_dense_scalar (simd/mod.rs:74-76): iterator sum of products. */
+float or_dense_dot_scalar(const float* a, const float* b, int64_t n) {
+  float s = -0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    float p = a[i] * b[i];
+    s = s + p;
+  }
+  return s;
+}
+
+/* sparse_dot_dense_avx2 (simd/mod.rs:145-170): one 8-lane FMA accumulator over
+ * chunks of 8 gathered values, hsum, then a scalar tail. */
+float or_sparse_dot_dense_avx2_order(const uint32_t* idx, const float* val, int64_t nnz,
+                                     const float* dense) {
+  float acc[8];
+  for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
+  int64_t chunks = nnz / 8;
+  for (int64_t c = 0; c < chunks; ++c)
+    for (int l = 0; l < 8; ++l)
+      acc[l] = fmaf(val[c * 8 + l], dense[idx[c * 8 + l]], acc[l]);
+  float sum = hsum8(acc);
+  for (int64_t i = chunks * 8; i < nnz; ++i) {
+    float p = val[i] * dense[idx[i]];
+    sum = sum + p;
+  }
+  return sum;
+}
+
+/* sparse_dot_dense_scalar (simd/mod.rs:39-45): `let mut sum = 0.0f32`. */
+float or_sparse_dot_dense_scalar(const uint32_t* idx, const float* val, int64_t nnz,
+                                 const float* dense) {
+  float s = 0.0f;
+  for (int64_t i = 0; i < nnz; ++i) {
+    float p = val[i] * dense[idx[i]];
+    s = s + p;
+  }
+  return s;
+}
+
+/* scatter_add_avx2 (simd/mod.rs:211-236): scaled = val*scale (vector multiply,
+ * same rounding as scalar), then sequential `dense[idx] += scaled` in index
+ * order, so duplicate indices accumulate in order.  The scalar tail
+ * (`dense[idx] += values[i] * scale`) has identical arithmetic. */
+void or_scatter_add(const uint32_t* idx, const float* val, int64_t n, float* dense, float scale) {
+  for (int64_t i = 0; i < n; ++i) {
+    float s = val[i] * scale;
+    dense[idx[i]] = dense[idx[i]] + s;
+  }
+}
+
+/* ======================================================================== */
+/* klearu-accel: crates/klearu-accel/src/bf16/mod.rs (half 2.x bf16)         */
+/* ======================================================================== */
+
+/* bf16::from_f32 (half crate, used at bf16/mod.rs:38,57,87): round to nearest,
+ * ties to even; NaN keeps its sign and top payload bits and is forced quiet.
+ * Pinned: closed form + round-trip KATs in tests. */
+uint16_t or_bf16_from_f32(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  uint32_t lsb = (u >> 16) & 1u;
+  uint32_t r = u + 0x7fffu + lsb;
+  return (uint16_t)(r >> 16);
+}
+
+/* bf16::to_f32: the bf16 bits are the high half of the f32. */
+float or_bf16_to_f32(uint16_t b) {
+  uint32_t u = ((uint32_t)b) << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+void or_bf16_from_f32_n(const float* x, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = or_bf16_from_f32(x[i]);
+}
+
+/* Bf16Weights::dot_f32 (bf16/mod.rs:64-77): iterator sum of w.to_f32()*x. */
+float or_bf16_dot_f32(const uint16_t* w, const float* x, int64_t n) {
+  float s = -0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    float p = or_bf16_to_f32(w[i]) * x[i];
+    s = s + p;
+  }
+  return s;
+}
+
+/* Bf16FullMode::dot (bf16/mod.rs:122-134). */
+float or_bf16_full_dot(const uint16_t* a, const uint16_t* b, int64_t n) {
+  float s = -0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    float p = or_bf16_to_f32(a[i]) * or_bf16_to_f32(b[i]);
+    s = s + p;
+  }
+  return s;
+}
+
+/* Bf16Weights::update_from_f32 (bf16/mod.rs:85-88) applied to every element. */
+void or_bf16_update_from_f32(uint16_t* w, const float* delta, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    float c = or_bf16_to_f32(w[i]);
+    w[i] = or_bf16_from_f32(c + delta[i]);
+  }
+}
+
+/* ======================================================================== */
+/* rand 0.8.5 StdRng = rand_chacha 0.3.1 ChaCha12Rng, seeded by rand_core     */
+/* 0.6.4 SeedableRng::seed_from_u64.  Third-party crates, not in the reference */
+/* tree; restated from their published algorithms (ChaCha: RFC 7539 block     */
+/* function with djb's 64-bit counter / 64-bit stream layout; PCG32 XSH-RR).  */
+/* Call sites: klearu-core/src/hash/simhash.rs:38-71, hash/srp.rs:55-75.     */
+/* Parity: block function pinned by RFC 7539 vectors; PCG32 output function   */
+/* pinned by the PCG reference demo vector; the composed seed->plane stream is */
+/* parity unpinned (no reference test holds a drawn value).                   */
+/* ======================================================================== */
+
+#define ROTL32(v, s) (((v) << (s)) | ((v) >> (32 - (s))))
+#define CHACHA_QR(a, b, c, d)                 \
+  do {                                        \
+    a += b; d ^= a; d = ROTL32(d, 16);        \
+    c += d; b ^= c; b = ROTL32(b, 12);        \
+    a += b; d ^= a; d = ROTL32(d, 8);         \
+    c += d; b ^= c; b = ROTL32(b, 7);         \
+  } while (0)
+
+void or_chacha_block(const uint32_t in[16], int rounds, uint32_t out[16]) {
+  uint32_t x[16];
+  memcpy(x, in, sizeof(x));
+  for (int r = 0; r < rounds; r += 2) {
+    CHACHA_QR(x[0], x[4], x[8], x[12]);
+    CHACHA_QR(x[1], x[5], x[9], x[13]);
+    CHACHA_QR(x[2], x[6], x[10], x[14]);
+    CHACHA_QR(x[3], x[7], x[11], x[15]);
+    CHACHA_QR(x[0], x[5], x[10], x[15]);
+    CHACHA_QR(x[1], x[6], x[11], x[12]);
+    CHACHA_QR(x[2], x[7], x[8], x[13]);
+    CHACHA_QR(x[3], x[4], x[9], x[14]);
+  }
+  for (int i = 0; i < 16; ++i) out[i] = x[i] + in[i];
+}
+
+/* PCG32 XSH-RR output permutation of a 64-bit LCG state. */
+uint32_t or_pcg32_output(uint64_t s) {
+  uint32_t xs = (uint32_t)(((s >> 18) ^ s) >> 27);
+  uint32_t rot = (uint32_t)(s >> 59);
+  return (xs >> rot) | (xs << ((32u - rot) & 31u));
+}
+
+static void stdrng_refill(or_stdrng* r) {
+  uint32_t in[16];
+  in[0] = 0x61707865u; in[1] = 0x3320646eu; in[2] = 0x79622d32u; in[3] = 0x6b206574u;
+  for (int i = 0; i < 8; ++i) in[4 + i] = r->key[i];
+  in[14] = 0; in[15] = 0; /* stream id 0 */
+  for (int blk = 0; blk < 4; ++blk) {
+    uint64_t c = r->counter + (uint64_t)blk;
+    in[12] = (uint32_t)c;
+    in[13] = (uint32_t)(c >> 32);
+    or_chacha_block(in, 12, r->buf + 16 * blk);
+  }
+  r->counter += 4;
+  r->idx = 0;
+}
+
+void or_stdrng_from_seed(or_stdrng* r, const uint8_t seed[32]) {
+  for (int i = 0; i < 8; ++i)
+    r->key[i] = (uint32_t)seed[4 * i] | ((uint32_t)seed[4 * i + 1] << 8) |
+                ((uint32_t)seed[4 * i + 2] << 16) | ((uint32_t)seed[4 * i + 3] << 24);
+  r->counter = 0;
+  r->idx = 64;
+}
+
+/* rand_core 0.6.4 seed_from_u64: advance the PCG32 LCG first, then output;
+ * eight 32-bit outputs fill the 32-byte seed in little-endian order. */
+void or_stdrng_seed_from_u64(or_stdrng* r, uint64_t state) {
+  uint8_t seed[32];
+  for (int i = 0; i < 8; ++i) {
+    state = state * 6364136223846793005ull + 11634580027462260723ull;
+    uint32_t x = or_pcg32_output(state);
+    seed[4 * i] = (uint8_t)x;
+    seed[4 * i + 1] = (uint8_t)(x >> 8);
+    seed[4 * i + 2] = (uint8_t)(x >> 16);
+    seed[4 * i + 3] = (uint8_t)(x >> 24);
+  }
+  or_stdrng_from_seed(r, seed);
+}
+
+uint32_t or_stdrng_next_u32(or_stdrng* r) {
+  if (r->idx >= 64) stdrng_refill(r);
+  return r->buf[r->idx++];
+}
+
+/* BlockRng::next_u64: low word first; a u64 that straddles a refill takes the
+ * last word of the old buffer as its low half. */
+uint64_t or_stdrng_next_u64(or_stdrng* r) {
+  if (r->idx < 63) {
+    uint64_t lo = r->buf[r->idx], hi = r->buf[r->idx + 1];
+    r->idx += 2;
+    return (hi << 32) | lo;
+  }
+  if (r->idx >= 64) {
+    stdrng_refill(r);
+    uint64_t lo = r->buf[0], hi = r->buf[1];
+    r->idx = 2;
+    return (hi << 32) | lo;
+  }
+  uint64_t lo = r->buf[63];
+  stdrng_refill(r);
+  uint64_t hi = r->buf[0];
+  r->idx = 1;
+  return (hi << 32) | lo;
+}
+
+/* Standard distribution for f64 (rand 0.8): 53 high bits times 2^-53. */
+double or_stdrng_gen_f64(or_stdrng* r) {
+  uint64_t v = or_stdrng_next_u64(r) >> 11;
+  return (double)v * (1.0 / 9007199254740992.0);
+}
+
+/* ======================================================================== */
+/* Hash families                                                             */
+/* ======================================================================== */
+
+/* SimHash::new + sample_ternary (hash/simhash.rs:37-71): table -> bit -> dim
+ * order, r < 1/6 -> -1, r < 1/6 + 2/3 -> 0, else +1.  planes[L][k][dim]. */
+void or_simhash_planes(int dim, int k, int num_tables, uint64_t seed, int8_t* planes) {
+  or_stdrng r;
+  or_stdrng_seed_from_u64(&r, seed);
+  const double lo = 1.0 / 6.0, hi = 1.0 / 6.0 + 2.0 / 3.0;
+  int64_t n = (int64_t)num_tables * k * dim;
+  for (int64_t i = 0; i < n; ++i) {
+    double v = or_stdrng_gen_f64(&r);
+    planes[i] = v < lo ? -1 : (v < hi ? 0 : 1);
+  }
+}
+
+/* SparseRandomProjection::new (hash/srp.rs:43-84): per projection t*k+b, per
+ * dim d: r < s/2 -> -1; r >= s/2 + (1-s) -> +1; else 0 (s widened to f64).
+ * Emitted as dense ternary planes[L*k][dim]; the sparse (idx, sign) list of
+ * the reference is exactly the nonzero entries in ascending d. */
+void or_srp_planes(int dim, int k, int num_tables, float sparsity, uint64_t seed, int8_t* planes) {
+  or_stdrng r;
+  or_stdrng_seed_from_u64(&r, seed);
+  const double pneg = (double)sparsity / 2.0;
+  const double pzero_end = pneg + (1.0 - (double)sparsity);
+  int64_t n = (int64_t)num_tables * k * dim;
+  for (int64_t i = 0; i < n; ++i) {
+    double v = or_stdrng_gen_f64(&r);
+    planes[i] = v < pneg ? -1 : (v >= pzero_end ? 1 : 0);
+  }
+}
+
+/* dot_ternary_dense + hash_dense (hash/simhash.rs:75-85, :103-113); SRP's
+ * dot_sparse_dense (hash/srp.rs:95-106) visits the same nonzero planes in the
+ * same ascending-d order, so the same code serves both families.
+ * Pinned: zero vector -> 2^k-1 (simhash.rs:232-240), dense==sparse
+ * (simhash.rs:173,218), brute force in tests. */
+uint64_t or_hash_dense(const int8_t* planes, int dim, int k, int table, const float* x) {
+  uint64_t h = 0;
+  for (int b = 0; b < k; ++b) {
+    const int8_t* p = planes + ((int64_t)table * k + b) * dim;
+    float s = 0.0f;
+    for (int d = 0; d < dim; ++d) {
+      if (p[d] == 1) s = s + x[d];
+      else if (p[d] == -1) s = s - x[d];
+    }
+    if (s >= 0.0f) h |= 1ull << b;
+  }
+  return h;
+}
+
+/* dot_ternary_sparse + hash_sparse (hash/simhash.rs:89-100, :116-126). */
+uint64_t or_hash_sparse(const int8_t* planes, int dim, int k, int table, const uint32_t* idx,
+                        const float* val, int64_t nnz) {
+  uint64_t h = 0;
+  for (int b = 0; b < k; ++b) {
+    const int8_t* p = planes + ((int64_t)table * k + b) * dim;
+    float s = 0.0f;
+    for (int64_t i = 0; i < nnz; ++i) {
+      int8_t r = p[idx[i]];
+      if (r == 1) s = s + val[i];
+      else if (r == -1) s = s - val[i];
+    }
+    if (s >= 0.0f) h |= 1ull << b;
+  }
+  return h;
+}
+
+void or_hash_dense_batch(const int8_t* planes, int dim, int k, int num_tables, const float* x,
+                         int64_t batch, uint32_t* codes) {
+  for (int64_t i = 0; i < batch; ++i)
+    for (int t = 0; t < num_tables; ++t)
+      codes[i * num_tables + t] = (uint32_t)or_hash_dense(planes, dim, k, t, x + i * dim);
+}
+
+/* ======================================================================== */
+/* Buckets and the LSH index                                                 */
+/* ======================================================================== */
+
+/* ReservoirBucket::deterministic_rand (bucket/reservoir.rs:40-47): SplitMix64
+ * finaliser of seed + golden gamma, reduced modulo bound. */
+uint64_t or_reservoir_rand(uint64_t seed, uint64_t bound) {
+  uint64_t z = seed + 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  z = z ^ (z >> 31);
+  return z % bound;
+}
+
+/* FifoBucket::insert (bucket/fifo.rs:27-33): evict index 0 when full. */
+static void fifo_insert(uint32_t* d, uint32_t* len, int cap, uint32_t id) {
+  if (*len >= (uint32_t)cap) {
+    memmove(d, d + 1, sizeof(uint32_t) * (*len - 1));
+    *len -= 1;
+  }
+  d[(*len)++] = id;
+}
+
+/* ReservoirBucket::insert (bucket/reservoir.rs:51-67). */
+static void reservoir_insert(uint32_t* d, uint32_t* len, uint64_t* count, int cap, uint32_t id) {
+  *count += 1;
+  if (*len < (uint32_t)cap) {
+    d[(*len)++] = id;
+    return;
+  }
+  uint64_t seed = *count * 0x517cc1b727220a95ull + (uint64_t)id;
+  uint64_t j = or_reservoir_rand(seed, *count);
+  if (j < (uint64_t)cap) {
+    uint64_t slot = or_reservoir_rand(seed + 1, (uint64_t)cap);
+    d[slot] = id;
+  }
+}
+
+/* LshIndex::insert (lsh/index.rs:257-262) for ids in the given order, tables
+ * inner; bucket = code & (2^k - 1) (index.rs:208-211).  data[L][2^k][cap],
+ * len[L][2^k], count[L][2^k] (count is used by reservoir buckets only). */
+void or_lsh_insert_many(int num_tables, int k, int cap, int bucket_type, uint32_t* data,
+                        uint32_t* len, uint64_t* count, int64_t n, const uint32_t* ids,
+                        const uint32_t* codes) {
+  const int64_t nb = (int64_t)1 << k;
+  for (int64_t i = 0; i < n; ++i)
+    for (int t = 0; t < num_tables; ++t) {
+      int64_t b = (int64_t)(codes[i * num_tables + t] & (uint32_t)(nb - 1));
+      int64_t slot = (int64_t)t * nb + b;
+      if (bucket_type == OR_BUCKET_FIFO)
+        fifo_insert(data + slot * cap, len + slot, cap, ids[i]);
+      else
+        reservoir_insert(data + slot * cap, len + slot, count + slot, cap, ids[i]);
+    }
+}
+
+static int cmp_u32(const void* a, const void* b) {
+  uint32_t x = *(const uint32_t*)a, y = *(const uint32_t*)b;
+  return x < y ? -1 : (x > y ? 1 : 0);
+}
+
+/* collect_counts (lsh/index.rs:219-234): every occurrence of an id in the L
+ * query buckets adds one to its count.  The reference returns HashMap order
+ * (randomised per process); the canonical order here is ascending id.
+ * Returns the number of unique ids; out arrays need L*cap entries. */
+int64_t or_lsh_query(int num_tables, int k, int cap, const uint32_t* data, const uint32_t* len,
+                     const uint32_t* codes, uint32_t* out_ids, uint32_t* out_counts) {
+  const int64_t nb = (int64_t)1 << k;
+  uint32_t* all = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)num_tables * cap + 4);
+  int64_t m = 0;
+  for (int t = 0; t < num_tables; ++t) {
+    int64_t slot = (int64_t)t * nb + (codes[t] & (uint32_t)(nb - 1));
+    for (uint32_t j = 0; j < len[slot]; ++j) all[m++] = data[slot * cap + j];
+  }
+  qsort(all, (size_t)m, sizeof(uint32_t), cmp_u32);
+  int64_t u = 0;
+  for (int64_t i = 0; i < m;) {
+    int64_t j = i;
+    while (j < m && all[j] == all[i]) ++j;
+    out_ids[u] = all[i];
+    if (out_counts) out_counts[u] = (uint32_t)(j - i);
+    ++u;
+    i = j;
+  }
+  free(all);
+  return u;
+}
+
+/* ======================================================================== */
+/* Sampling strategies                                                       */
+/* ======================================================================== */
+
+typedef struct { uint32_t id, count; } pair_ic;
+static int cmp_topk(const void* a, const void* b) {
+  const pair_ic* x = (const pair_ic*)a;
+  const pair_ic* y = (const pair_ic*)b;
+  if (x->count != y->count) return x->count > y->count ? -1 : 1;
+  return x->id < y->id ? -1 : (x->id > y->id ? 1 : 0);
+}
+
+/* TopKSampling::select (sampling/topk.rs:19-34): count desc, id asc, take k. */
+int64_t or_sample_topk(const uint32_t* ids, const uint32_t* counts, int64_t n, int64_t k,
+                       uint32_t* out) {
+  pair_ic* p = (pair_ic*)malloc(sizeof(pair_ic) * (size_t)(n + 1));
+  for (int64_t i = 0; i < n; ++i) { p[i].id = ids[i]; p[i].count = counts[i]; }
+  qsort(p, (size_t)n, sizeof(pair_ic), cmp_topk);
+  int64_t m = n < k ? n : k;
+  for (int64_t i = 0; i < m; ++i) out[i] = p[i].id;
+  free(p);
+  return m;
+}
+
+/* ThresholdSampling::select (sampling/threshold.rs:20-43): count >= t in input
+ * order; if none pass, the single best (highest count, then lowest id). */
+int64_t or_sample_threshold(const uint32_t* ids, const uint32_t* counts, int64_t n,
+                            uint32_t threshold, uint32_t* out) {
+  if (n == 0) return 0;
+  int64_t m = 0;
+  for (int64_t i = 0; i < n; ++i)
+    if (counts[i] >= threshold) out[m++] = ids[i];
+  if (m > 0) return m;
+  int64_t best = 0;
+  for (int64_t i = 1; i < n; ++i)
+    if (counts[i] > counts[best] || (counts[i] == counts[best] && ids[i] < ids[best])) best = i;
+  out[0] = ids[best];
+  return 1;
+}
+
+/* ======================================================================== */
+/* SLIDE neuron / layer                                                      */
+/* ======================================================================== */
+
+/* Neuron::forward (network/neuron.rs:47-62): iterator sum of w*x, then +bias. */
+float or_neuron_forward(const float* w, float bias, const float* x, int64_t dim) {
+  float s = -0.0f;
+  for (int64_t d = 0; d < dim; ++d) {
+    float p = w[d] * x[d];
+    s = s + p;
+  }
+  return s + bias;
+}
+
+/* Neuron::forward_sparse (network/neuron.rs:66-68) via SparseVector::dot_dense
+ * (tensor/sparse.rs:89-101): iterator sum of val*w[idx] over stored entries. */
+float or_neuron_forward_sparse(const float* w, float bias, const uint32_t* idx, const float* val,
+                               int64_t nnz) {
+  float s = -0.0f;
+  for (int64_t i = 0; i < nnz; ++i) {
+    float p = val[i] * w[idx[i]];
+    s = s + p;
+  }
+  return s + bias;
+}
+
+/* apply_activation / apply_softmax (network/layer.rs:250-261, :286-308). */
+void or_layer_activate(const float* pre, int64_t n, int act, float* out) {
+  if (act == OR_ACT_SOFTMAX) {
+    if (n == 0) return;
+    float mx = -INFINITY;
+    for (int64_t i = 0; i < n; ++i) mx = fmaxf(mx, pre[i]);
+    float s = -0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+      out[i] = expf(pre[i] - mx);
+      s = s + out[i];
+    }
+    if (s > 0.0f) {
+      for (int64_t i = 0; i < n; ++i) out[i] = out[i] / s;
+    } else {
+      float u = 1.0f / (float)n;
+      for (int64_t i = 0; i < n; ++i) out[i] = u;
+    }
+    return;
+  }
+  for (int64_t i = 0; i < n; ++i) {
+    float x = pre[i];
+    switch (act) {
+      case OR_ACT_RELU: out[i] = fmaxf(x, 0.0f); break;
+      case OR_ACT_SIGMOID: out[i] = 1.0f / (1.0f + expf(-x)); break;
+      case OR_ACT_TANH: out[i] = tanhf(x); break;
+      default: out[i] = x; break;
+    }
+  }
+}
+
+/* ======================================================================== */
+/* Deja Vu predictor: crates/klearu-dejavu/src/predictor/mlp_predictor.rs     */
+/* ======================================================================== */
+
+/* 1 / (1 + exp(-z)) in f32 with glibc expf (mlp_predictor.rs:121). */
+float or_sigmoid(float z) {
+  float e = expf(-z);
+  float d = 1.0f + e;
+  return 1.0f / d;
+}
+
+/* SparsityPredictor::predict (mlp_predictor.rs:102-124): both layers are
+ * iterator sums (sequential f32, product rounded before the add). */
+void or_predictor_predict(const float* w1, const float* b1, const float* w2, const float* b2,
+                          int in_dim, int hid, int out_dim, const float* x, float* scores,
+                          float* hidden) {
+  float* h = hidden ? hidden : (float*)malloc(sizeof(float) * (size_t)hid);
+  for (int i = 0; i < hid; ++i) {
+    float s = -0.0f;
+    const float* row = w1 + (int64_t)i * in_dim;
+    for (int j = 0; j < in_dim; ++j) {
+      float p = row[j] * x[j];
+      s = s + p;
+    }
+    h[i] = fmaxf(s + b1[i], 0.0f);
+  }
+  for (int o = 0; o < out_dim; ++o) {
+    float s = -0.0f;
+    const float* row = w2 + (int64_t)o * hid;
+    for (int i = 0; i < hid; ++i) {
+      float p = row[i] * h[i];
+      s = s + p;
+    }
+    scores[o] = or_sigmoid(s + b2[o]);
+  }
+  if (!hidden) free(h);
+}
+
+/* Same, with BF16-valued weights widened exactly (bits << 16). */
+void or_predictor_predict_bf16(const uint16_t* w1, const float* b1, const uint16_t* w2,
+                               const float* b2, int in_dim, int hid, int out_dim, const float* x,
+                               float* scores, float* hidden) {
+  float* h = hidden ? hidden : (float*)malloc(sizeof(float) * (size_t)hid);
+  for (int i = 0; i < hid; ++i) {
+    float s = -0.0f;
+    const uint16_t* row = w1 + (int64_t)i * in_dim;
+    for (int j = 0; j < in_dim; ++j) {
+      float p = or_bf16_to_f32(row[j]) * x[j];
+      s = s + p;
+    }
+    h[i] = fmaxf(s + b1[i], 0.0f);
+  }
+  for (int o = 0; o < out_dim; ++o) {
+    float s = -0.0f;
+    const uint16_t* row = w2 + (int64_t)o * hid;
+    for (int i = 0; i < hid; ++i) {
+      float p = or_bf16_to_f32(row[i]) * h[i];
+      s = s + p;
+    }
+    scores[o] = or_sigmoid(s + b2[o]);
+  }
+  if (!hidden) free(h);
+}
+
+/* Stable merge sort of indices by score descending (ties keep index order),
+ * as `sort_by(|a, b| b.1.partial_cmp(&a.1))` (a stable sort) does at
+ * mlp_predictor.rs:127-132.  -0.0 and +0.0 compare equal there and here. */
+static void merge_desc(const float* s, int64_t* a, int64_t* tmp, int64_t n) {
+  if (n < 2) return;
+  int64_t m = n / 2;
+  merge_desc(s, a, tmp, m);
+  merge_desc(s, a + m, tmp, n - m);
+  int64_t i = 0, j = m, o = 0;
+  while (i < m && j < n) {
+    if (s[a[j]] > s[a[i]]) tmp[o++] = a[j++];
+    else tmp[o++] = a[i++];
+  }
+  while (i < m) tmp[o++] = a[i++];
+  while (j < n) tmp[o++] = a[j++];
+  memcpy(a, tmp, sizeof(int64_t) * (size_t)n);
+}
+
+void or_select_top_k(const float* scores, int64_t n, int64_t k, int64_t* out) {
+  int64_t* a = (int64_t*)malloc(sizeof(int64_t) * (size_t)(n + 1));
+  int64_t* t = (int64_t*)malloc(sizeof(int64_t) * (size_t)(n + 1));
+  for (int64_t i = 0; i < n; ++i) a[i] = i;
+  merge_desc(scores, a, t, n);
+  int64_t m = k < n ? k : n;
+  memcpy(out, a, sizeof(int64_t) * (size_t)m);
+  free(a);
+  free(t);
+}
+
+/* ======================================================================== */
+/* klearu-llm sparse decode blocks                                           */
+/* ======================================================================== */
+
+/* silu (sparse/sparse_mlp.rs:39-42). */
+float or_silu(float x) {
+  float e = expf(-x);
+  float d = 1.0f + e;
+  return x / d;
+}
+
+static void widen_row(const uint16_t* w, int64_t n, float* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = or_bf16_to_f32(w[i]);
+}
+
+/* sparse_mlp::forward_sparse (sparse/sparse_mlp.rs:4-37) with
+ * Linear::forward_sparse (model/linear.rs:107-114) = dense_dot_dense_simd per
+ * active row.  Weights are BF16 values (the reference widens them to f32 at
+ * load, weight/safetensors.rs:150-152; widening is exact).  wg, wu:
+ * [inter][hidden]; wd: [hidden][inter] (reference layout).  The down
+ * projection is a sequential sum in active-list order starting at +0.0. */
+void or_sparse_mlp_forward_bf16(const uint16_t* wg, const uint16_t* wu, const uint16_t* wd,
+                                int hidden, int inter, const float* x, const int64_t* active,
+                                int64_t k, float* y, float* h_out) {
+  float* row = (float*)malloc(sizeof(float) * (size_t)hidden);
+  float* h = (float*)malloc(sizeof(float) * (size_t)(k + 1));
+  for (int64_t i = 0; i < k; ++i) {
+    widen_row(wg + active[i] * hidden, hidden, row);
+    float g = or_dense_dot_avx2_order(row, x, hidden);
+    widen_row(wu + active[i] * hidden, hidden, row);
+    float u = or_dense_dot_avx2_order(row, x, hidden);
+    h[i] = or_silu(g) * u;
+  }
+  for (int j = 0; j < hidden; ++j) {
+    const uint16_t* w = wd + (int64_t)j * inter;
+    float s = 0.0f;
+    for (int64_t i = 0; i < k; ++i) {
+      float p = or_bf16_to_f32(w[active[i]]) * h[i];
+      s = s + p;
+    }
+    y[j] = s;
+  }
+  if (h_out) memcpy(h_out, h, sizeof(float) * (size_t)k);
+  free(row);
+  free(h);
+}
+
+/* RmsNorm::forward (model/rms_norm.rs:43-64), plain-weight variant. */
+void or_rmsnorm(float* x, const float* w, int64_t n, float eps) {
+  float ss = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    float p = x[i] * x[i];
+    ss = ss + p;
+  }
+  float rms = sqrtf(ss / (float)n + eps);
+  float inv = 1.0f / rms;
+  for (int64_t i = 0; i < n; ++i) {
+    float t = x[i] * inv;
+    x[i] = t * w[i];
+  }
+}
+
+/* RotaryEmbedding::new_partial with rotary_dim == head_dim (model/rope.rs:17-46):
+ * freq = 1 / theta^(2i/d), angle = pos*freq, tables [max_seq][d/2]. */
+void or_rope_tables(int head_dim, int max_seq, float theta, float* cos_t, float* sin_t) {
+  int half = head_dim / 2;
+  for (int p = 0; p < max_seq; ++p)
+    for (int i = 0; i < half; ++i) {
+      float e = (2.0f * (float)i) / (float)head_dim;
+      float freq = 1.0f / powf(theta, e);
+      float ang = (float)p * freq;
+      cos_t[(int64_t)p * half + i] = cosf(ang);
+      sin_t[(int64_t)p * half + i] = sinf(ang);
+    }
+}
+
+/* RotaryEmbedding::apply (model/rope.rs:75-87): NeoX half-split rotation. */
+void or_rope_apply(float* x, int half, const float* cos_t, const float* sin_t, int64_t pos) {
+  for (int i = 0; i < half; ++i) {
+    float c = cos_t[pos * half + i], s = sin_t[pos * half + i];
+    float x0 = x[i], x1 = x[half + i];
+    float a = x0 * c, b = x1 * s;
+    float e = x1 * c, f = x0 * s;
+    x[i] = a - b;
+    x[half + i] = e + f;
+  }
+}
+
+/* Linear::forward (model/linear.rs:79-104): one AVX2-order dot per row. */
+void or_linear_forward_bf16(const uint16_t* w, int out_f, int in_f, const float* x, float* y) {
+  float* row = (float*)malloc(sizeof(float) * (size_t)in_f);
+  for (int o = 0; o < out_f; ++o) {
+    widen_row(w + (int64_t)o * in_f, in_f, row);
+    y[o] = or_dense_dot_avx2_order(row, x, in_f);
+  }
+  free(row);
+}
+
+/* sparse_attention::forward_sparse (sparse/sparse_attention.rs:7-79) with
+ * softmax_inplace (:81-95) and KvCache::append (model/kv_cache.rs:33-48).
+ * Caches are [num_kv_heads][max_seq][head_dim] f32 holding pos valid rows on
+ * entry; this call appends row pos.  Weights are BF16 values in the reference
+ * [out][in] layout. */
+void or_sparse_attention_forward_bf16(const uint16_t* wq, const uint16_t* wk, const uint16_t* wv,
+                                      const uint16_t* wo, int hidden, int num_heads,
+                                      int num_kv_heads, int head_dim, const float* x, int64_t pos,
+                                      const float* cos_t, const float* sin_t, float* k_cache,
+                                      float* v_cache, int64_t max_seq, const int64_t* heads,
+                                      int64_t n_heads, float* out) {
+  const int group = num_heads / num_kv_heads;
+  const int qd = num_heads * head_dim, kvd = num_kv_heads * head_dim;
+  const int half = head_dim / 2;
+  float* q = (float*)malloc(sizeof(float) * (size_t)qd);
+  float* kk = (float*)malloc(sizeof(float) * (size_t)kvd);
+  float* vv = (float*)malloc(sizeof(float) * (size_t)kvd);
+  or_linear_forward_bf16(wq, qd, hidden, x, q);
+  or_linear_forward_bf16(wk, kvd, hidden, x, kk);
+  or_linear_forward_bf16(wv, kvd, hidden, x, vv);
+  for (int h = 0; h < num_heads; ++h) or_rope_apply(q + h * head_dim, half, cos_t, sin_t, pos);
+  for (int h = 0; h < num_kv_heads; ++h) or_rope_apply(kk + h * head_dim, half, cos_t, sin_t, pos);
+  for (int h = 0; h < num_kv_heads; ++h) {
+    memcpy(k_cache + ((int64_t)h * max_seq + pos) * head_dim, kk + h * head_dim,
+           sizeof(float) * (size_t)head_dim);
+    memcpy(v_cache + ((int64_t)h * max_seq + pos) * head_dim, vv + h * head_dim,
+           sizeof(float) * (size_t)head_dim);
+  }
+  const int64_t seq = pos + 1;
+  const float inv_sqrt = 1.0f / sqrtf((float)head_dim);
+  float* concat = (float*)calloc((size_t)qd, sizeof(float));
+  float* sc = (float*)malloc(sizeof(float) * (size_t)seq);
+  for (int64_t a = 0; a < n_heads; ++a) {
+    int64_t h = heads[a];
+    if (h >= num_heads) continue;
+    int64_t kvh = h / group;
+    const float* qh = q + h * head_dim;
+    for (int64_t j = 0; j < seq; ++j)
+      sc[j] = or_dense_dot_avx2_order(qh, k_cache + (kvh * max_seq + j) * head_dim, head_dim) *
+              inv_sqrt;
+    float mx = -INFINITY;
+    for (int64_t j = 0; j < seq; ++j) mx = fmaxf(mx, sc[j]);
+    float sum = 0.0f;
+    for (int64_t j = 0; j < seq; ++j) {
+      sc[j] = expf(sc[j] - mx);
+      sum = sum + sc[j];
+    }
+    float inv = 1.0f / sum;
+    for (int64_t j = 0; j < seq; ++j) sc[j] = sc[j] * inv;
+    float* ho = concat + h * head_dim;
+    for (int64_t j = 0; j < seq; ++j) {
+      const float* vj = v_cache + (kvh * max_seq + j) * head_dim;
+      for (int d = 0; d < head_dim; ++d) {
+        float p = sc[j] * vj[d];
+        ho[d] = ho[d] + p;
+      }
+    }
+  }
+  or_linear_forward_bf16(wo, hidden, qd, concat, out);
+  free(q); free(kk); free(vv); free(concat); free(sc);
+}
+
+/* ======================================================================== */
+/* klearu-dejavu toy layer (f32 weights with bias)                           */
+/* ======================================================================== */
+
+/* dejavu Linear::forward_sparse (klearu-dejavu/src/transformer/mod.rs:126-134). */
+void or_dejavu_linear_forward_sparse(const float* w, const float* bias, int in_f,
+                                     const float* x, const int64_t* idx, int64_t n, float* out) {
+  for (int64_t a = 0; a < n; ++a) {
+    const float* row = w + idx[a] * in_f;
+    float s = -0.0f;
+    for (int j = 0; j < in_f; ++j) {
+      float p = row[j] * x[j];
+      s = s + p;
+    }
+    out[a] = s + bias[idx[a]];
+  }
+}
+
+/* SparseMlp::forward (klearu-dejavu/src/mlp.rs:23-58): SwiGLU over selected
+ * neurons; the down projection adds column idx of wd [hidden][inter] times the
+ * activation into every output, in selection order, then adds the bias. */
+void or_dejavu_sparse_mlp_forward(const float* wg, const float* bg, const float* wu,
+                                  const float* bu, const float* wd, const float* bd, int hidden,
+                                  int inter, const float* x, const int64_t* sel, int64_t n,
+                                  float* y) {
+  float* g = (float*)malloc(sizeof(float) * (size_t)(n + 1));
+  float* u = (float*)malloc(sizeof(float) * (size_t)(n + 1));
+  float* sh = (float*)calloc((size_t)inter, sizeof(float));
+  or_dejavu_linear_forward_sparse(wg, bg, hidden, x, sel, n, g);
+  or_dejavu_linear_forward_sparse(wu, bu, hidden, x, sel, n, u);
+  for (int64_t a = 0; a < n; ++a) {
+    float e = expf(-g[a]);
+    float d = 1.0f + e;
+    float si = g[a] / d;
+    sh[sel[a]] = si * u[a];
+  }
+  for (int j = 0; j < hidden; ++j) y[j] = 0.0f;
+  for (int64_t a = 0; a < n; ++a) {
+    float v = sh[sel[a]];
+    if (v != 0.0f)
+      for (int j = 0; j < hidden; ++j) {
+        float p = wd[(int64_t)j * inter + sel[a]] * v;
+        y[j] = y[j] + p;
+      }
+  }
+  for (int j = 0; j < hidden; ++j) y[j] = y[j] + bd[j];
+  free(g); free(u); free(sh);
+}
