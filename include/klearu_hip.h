@@ -1,0 +1,306 @@
+/*
+ * klearu_hip.h -- C ABI of libklearu_hip.so, the MI355X (gfx950) implementation
+ * of klearu's activation-sparse inference path.
+ *
+ * Each entry point names the reference interface it replaces (path:line in
+ * QuilibriumNetwork/klearu).  Conventions:
+ *   - Every function returns int: KH_OK (0) or a negative KH_ERR_* code; the
+ *     message of the last failure on the calling thread is kh_last_error().
+ *     Nothing aborts: the reference's panics on length mismatch become
+ *     KH_ERR_ARG.
+ *   - Pointers named *_dev are device pointers (hipMalloc'd or torch tensors);
+ *     pointers named *_host are host pointers.  `stream` is a hipStream_t
+ *     (NULL = the legacy default stream).  Compute calls are asynchronous on
+ *     that stream unless stated otherwise.
+ *   - Handles are device-resident and immutable after creation except where a
+ *     function says it mutates the handle (the reference's `&mut self`).  A
+ *     handle owns a scratch workspace: calls on one handle must be ordered
+ *     (same stream, or synchronised); distinct handles may run concurrently.
+ *   - Selections (hash codes, active sets, top-k) are bit-exact with the
+ *     reference's sequential f32 arithmetic.  Sets whose reference order is a
+ *     HashMap iteration order are returned in ascending id order.
+ */
+#ifndef KLEARU_HIP_H
+#define KLEARU_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KH_OK 0
+#define KH_ERR_ARG (-1)         /* bad shape / argument (reference: assert panic) */
+#define KH_ERR_HIP (-2)         /* HIP runtime error */
+#define KH_ERR_CAPACITY (-3)    /* output capacity too small */
+#define KH_ERR_ALLOC (-4)       /* device allocation failed */
+#define KH_ERR_UNSUPPORTED (-5) /* shape outside what the kernels support */
+
+const char* kh_last_error(void);
+int kh_version(void);
+
+/* ======================================================================== */
+/* klearu-accel entry points (crates/klearu-accel/src/simd/mod.rs,          */
+/* crates/klearu-accel/src/bf16/mod.rs)                                     */
+/* ======================================================================== */
+
+/* dense_dot_dense_simd (simd/mod.rs:54-72), batched over rows:
+ * out[r] = dot(a[r*lda .. r*lda+n], b[0..n]) in the AVX2 order of
+ * simd/mod.rs:174-207 (bit-exact). */
+int kh_dense_dot_dense(const float* a_dev, int64_t rows, int64_t lda, const float* b_dev,
+                       int64_t n, float* out_dev, void* stream);
+
+/* sparse_dot_dense_simd (simd/mod.rs:19-36): out[0] = sum_i val[i]*dense[idx[i]]
+ * in the AVX2 gather order of simd/mod.rs:145-170 (bit-exact). */
+int kh_sparse_dot_dense(const uint32_t* idx_dev, const float* val_dev, int64_t nnz,
+                        const float* dense_dev, int64_t dense_len, float* out_dev,
+                        void* stream);
+
+/* scatter_add_simd (simd/mod.rs:86-109): dense[idx[i]] += val[i]*scale, with
+ * duplicate indices applied in index order (bit-exact, atomic-free). */
+int kh_scatter_add(const uint32_t* idx_dev, const float* val_dev, int64_t n, float* dense_dev,
+                   int64_t dense_len, float scale, void* stream);
+
+/* Bf16Weights::from_f32 (bf16/mod.rs:37-41): round to nearest even. */
+int kh_bf16_from_f32(const float* x_dev, uint16_t* out_dev, int64_t n, void* stream);
+/* Bf16Weights::to_f32 (bf16/mod.rs:44-46). */
+int kh_bf16_to_f32(const uint16_t* x_dev, float* out_dev, int64_t n, void* stream);
+/* Bf16Weights::dot_f32 (bf16/mod.rs:64-77), rows batched like kh_dense_dot_dense;
+ * sequential f32 sum (bit-exact). */
+int kh_bf16_dot_f32(const uint16_t* w_dev, int64_t rows, int64_t ldw, const float* x_dev,
+                    int64_t n, float* out_dev, void* stream);
+/* Bf16FullMode::dot (bf16/mod.rs:122-134), sequential f32 sum (bit-exact). */
+int kh_bf16_full_dot(const uint16_t* a_dev, const uint16_t* b_dev, int64_t n, float* out_dev,
+                     void* stream);
+/* Bf16Weights::update_from_f32 (bf16/mod.rs:85-88) for every element:
+ * w[i] = bf16(f32(w[i]) + delta[i]). */
+int kh_bf16_update_from_f32(uint16_t* w_dev, const float* delta_dev, int64_t n, void* stream);
+
+/* ======================================================================== */
+/* LSH hash families (crates/klearu-core/src/hash/)                         */
+/* ======================================================================== */
+
+typedef struct kh_hash_family kh_hash_family;
+
+/* SimHash::new(input_dim, k, num_tables, seed) (hash/simhash.rs:37-58):
+ * ternary planes drawn from rand 0.8 StdRng (ChaCha12) in table->bit->dim order. */
+int kh_simhash_create(int input_dim, int k, int num_tables, uint64_t seed, kh_hash_family** out);
+/* SparseRandomProjection::new (hash/srp.rs:43-84). */
+int kh_srp_create(int input_dim, int k, int num_tables, float sparsity, uint64_t seed,
+                  kh_hash_family** out);
+/* A family from explicit ternary planes planes_host[num_tables][k][input_dim]
+ * with entries in {-1, 0, +1}. */
+int kh_hash_family_from_planes(int input_dim, int k, int num_tables, const int8_t* planes_host,
+                               kh_hash_family** out);
+int kh_hash_family_destroy(kh_hash_family* h);
+/* HashFamily::k / input_dim / num_tables (hash/mod.rs:31-38). */
+int kh_hash_family_dims(const kh_hash_family* h, int* k, int* input_dim, int* num_tables);
+/* Copies the planes back as planes_host[num_tables][k][input_dim]. */
+int kh_hash_family_planes(const kh_hash_family* h, int8_t* planes_host);
+/* HashFamily::hash_dense (hash/mod.rs:26) for every table and a batch:
+ * codes[b][t] = hash_dense(x[b], t), x_dev [batch][input_dim]. */
+int kh_hash_dense(const kh_hash_family* h, const float* x_dev, int64_t batch, uint32_t* codes_dev,
+                  void* stream);
+/* HashFamily::hash_sparse (hash/mod.rs:29) for a CSR batch: row b is
+ * (idx[off[b]..off[b+1]], val[...]) with ascending idx (SparseVector). */
+int kh_hash_sparse(const kh_hash_family* h, const int64_t* off_dev, const uint32_t* idx_dev,
+                   const float* val_dev, int64_t batch, uint32_t* codes_dev, void* stream);
+
+/* ======================================================================== */
+/* LSH index (crates/klearu-core/src/lsh/index.rs, bucket/)                 */
+/* ======================================================================== */
+
+#define KH_BUCKET_FIFO 0      /* FifoBucket (bucket/fifo.rs:26-55) */
+#define KH_BUCKET_RESERVOIR 1 /* ReservoirBucket (bucket/reservoir.rs:50-90) */
+
+typedef struct kh_lsh_index kh_lsh_index;
+
+/* LshIndex::new(hash_family, bucket_type, capacity) (lsh/index.rs:193-204).
+ * The index keeps a reference to `h`, which must outlive it. */
+int kh_lsh_index_create(const kh_hash_family* h, int bucket_type, int capacity,
+                        kh_lsh_index** out);
+int kh_lsh_index_destroy(kh_lsh_index* idx);
+/* LshIndexTrait::insert (lsh/index.rs:257-262) for n vectors in order:
+ * ids[i] with dense weights w[i*ldw .. i*ldw+input_dim] (tables inner). Mutates. */
+int kh_lsh_index_insert(kh_lsh_index* idx, const uint32_t* ids_dev, const float* w_dev,
+                        int64_t n, int64_t ldw, void* stream);
+/* Same from precomputed codes[n][num_tables] (e.g. from kh_hash_dense). */
+int kh_lsh_index_insert_codes(kh_lsh_index* idx, const uint32_t* ids_dev,
+                              const uint32_t* codes_dev, int64_t n, void* stream);
+/* LshIndexTrait::clear (lsh/index.rs:313-315). Mutates. */
+int kh_lsh_index_clear(kh_lsh_index* idx, void* stream);
+/* LshIndexTrait::query / query_with_counts (lsh/index.rs:282-284, :294-296)
+ * for a batch of dense inputs.  Output is CSR: the unique ids of sample b are
+ * ids_dev[off[b]..off[b+1]] in ascending order with counts_dev (number of
+ * table hits; may be NULL for query_union, index.rs:286-288).  off_dev has
+ * batch+1 entries; off[batch] is the total even when it exceeds capacity, in
+ * which case nothing past capacity is written and the call returns
+ * KH_ERR_CAPACITY (this check synchronises the stream). */
+int kh_lsh_index_query(const kh_lsh_index* idx, const float* x_dev, int64_t batch,
+                       int64_t* off_dev, uint32_t* ids_dev, uint32_t* counts_dev,
+                       int64_t capacity, void* stream);
+/* query_sparse_union / query_sparse_with_counts (lsh/index.rs:290-299), CSR input. */
+int kh_lsh_index_query_sparse(const kh_lsh_index* idx, const int64_t* xoff_dev,
+                              const uint32_t* xidx_dev, const float* xval_dev, int64_t batch,
+                              int64_t* off_dev, uint32_t* ids_dev, uint32_t* counts_dev,
+                              int64_t capacity, void* stream);
+/* Bucket contents for parity checks (synchronous): data_host[L][2^k][cap],
+ * len_host[L][2^k], count_host[L][2^k] (reservoir insertion counters). */
+int kh_lsh_index_buckets(const kh_lsh_index* idx, uint32_t* data_host, uint32_t* len_host,
+                         uint64_t* count_host);
+
+/* ======================================================================== */
+/* SLIDE sparse layer (crates/klearu-core/src/network/layer.rs)             */
+/* ======================================================================== */
+
+#define KH_SAMPLING_VANILLA 0   /* sampling/vanilla.rs:8-12 */
+#define KH_SAMPLING_TOPK 1      /* sampling/topk.rs:19-34 */
+#define KH_SAMPLING_THRESHOLD 2 /* sampling/threshold.rs:20-43 */
+
+#define KH_ACT_RELU 0     /* layer.rs:252 */
+#define KH_ACT_SIGMOID 1  /* layer.rs:253 */
+#define KH_ACT_TANH 2     /* layer.rs:254 */
+#define KH_ACT_SOFTMAX 3  /* layer.rs:286-308 */
+#define KH_ACT_IDENTITY 4 /* layer.rs:255 */
+
+typedef struct kh_slide_layer kh_slide_layer;
+
+/* Layer{neurons, lsh_index, sampling, config} (layer.rs:10-15) built from
+ * explicit weights: w_host[num_neurons][input_dim] f32, bias_host[num_neurons].
+ * The index is built by inserting neurons 0..n-1 in order (layer.rs:42-44).
+ * `index` must have been created over a family with this input_dim and stay
+ * alive; the layer inserts into it. */
+int kh_slide_layer_create(int input_dim, int num_neurons, const float* w_host,
+                          const float* bias_host, kh_lsh_index* index, int sampling, int top_k,
+                          int threshold, int activation, kh_slide_layer** out);
+int kh_slide_layer_destroy(kh_slide_layer* l);
+/* Layer::forward (layer.rs:65-120) for a batch of dense inputs x_dev[batch][input_dim].
+ * Active neurons of sample b: act_ids[off[b]..off[b+1]] (ascending id), with
+ * pre-activations and activations in the same order (either may be NULL).
+ * Same capacity rules as kh_lsh_index_query. */
+int kh_slide_layer_forward(const kh_slide_layer* l, const float* x_dev, int64_t batch,
+                           int64_t* off_dev, uint32_t* act_ids_dev, float* pre_dev,
+                           float* act_dev, int64_t capacity, void* stream);
+/* Same for CSR sparse inputs (Neuron::forward_sparse, neuron.rs:66-68; the
+ * hash uses hash_sparse). */
+int kh_slide_layer_forward_sparse(const kh_slide_layer* l, const int64_t* xoff_dev,
+                                  const uint32_t* xidx_dev, const float* xval_dev, int64_t batch,
+                                  int64_t* off_dev, uint32_t* act_ids_dev, float* pre_dev,
+                                  float* act_dev, int64_t capacity, void* stream);
+
+/* Dense layer over sparse inputs: y[b][o] = act(Neuron::forward_sparse) for all
+ * neurons (the 128-d hidden layer of the extreme-classification net).
+ * w_host[num_neurons][input_dim]. */
+typedef struct kh_dense_layer kh_dense_layer;
+int kh_dense_layer_create(int input_dim, int num_neurons, const float* w_host,
+                          const float* bias_host, int activation, kh_dense_layer** out);
+int kh_dense_layer_destroy(kh_dense_layer* l);
+int kh_dense_layer_forward_sparse(const kh_dense_layer* l, const int64_t* xoff_dev,
+                                  const uint32_t* xidx_dev, const float* xval_dev, int64_t batch,
+                                  float* y_dev, void* stream);
+
+/* ======================================================================== */
+/* Deja Vu predictor + top-k (crates/klearu-dejavu/src/predictor/,          */
+/* crates/klearu-llm/src/sparse/predictor_store.rs)                         */
+/* ======================================================================== */
+
+typedef struct kh_predictor kh_predictor;
+
+/* SparsityPredictor::from_weights (mlp_predictor.rs:66-84): w1_host[hidden][input],
+ * b1_host[hidden], w2_host[output][hidden], b2_host[output], all f32 as the
+ * reference stores them. */
+int kh_predictor_create(int input_dim, int hidden_dim, int output_dim, const float* w1_host,
+                        const float* b1_host, const float* w2_host, const float* b2_host,
+                        kh_predictor** out);
+int kh_predictor_destroy(kh_predictor* p);
+/* SparsityPredictor::predict (mlp_predictor.rs:102-124) for x_dev[batch][input]:
+ * scores_dev[batch][output] (sigmoid), bit-exact with the reference. */
+int kh_predictor_predict(const kh_predictor* p, const float* x_dev, int64_t batch,
+                         float* scores_dev, void* stream);
+
+#define KH_ORDER_SCORE 0     /* reference order: score descending, ties by index */
+#define KH_ORDER_ASCENDING 1 /* same set, ascending index */
+
+/* SparsityPredictor::select_top_k (mlp_predictor.rs:127-132) /
+ * PredictorStore::predict_neurons|predict_heads (predictor_store.rs:31-45):
+ * ids_dev[batch][min(k, output)] (int32). */
+int kh_predictor_select_top_k(const kh_predictor* p, const float* x_dev, int64_t batch, int k,
+                              int order, int32_t* ids_dev, void* stream);
+/* The stable top-k of arbitrary scores (the sort of mlp_predictor.rs:129-131):
+ * scores_dev[batch][n] -> ids_dev[batch][min(k, n)].  NaN scores are not supported. */
+int kh_topk_select(const float* scores_dev, int64_t batch, int n, int k, int order,
+                   int32_t* ids_dev, void* stream);
+/* Union of batch top-k sets (the shared active set of a multi-token decode
+ * step): ids_dev[batch][k] over [0, n) -> union_dev[<= n] ascending and
+ * *count_dev (device int32). */
+int kh_union_active(const int32_t* ids_dev, int64_t batch, int k, int n, int32_t* union_dev,
+                    int32_t* count_dev, void* stream);
+
+/* ======================================================================== */
+/* Sparse SwiGLU FFN (crates/klearu-llm/src/sparse/sparse_mlp.rs)           */
+/* ======================================================================== */
+
+typedef struct kh_sparse_ffn kh_sparse_ffn;
+
+/* Mlp{gate_proj, up_proj, down_proj} (model/mlp.rs:6-21) from BF16 bits in the
+ * reference layout: w_gate/w_up [inter][hidden], w_down [hidden][inter].
+ * max_batch bounds the token batch of later forward calls (1..16). */
+int kh_sparse_ffn_create(int hidden, int inter, const uint16_t* w_gate_host,
+                         const uint16_t* w_up_host, const uint16_t* w_down_host, int max_batch,
+                         kh_sparse_ffn** out);
+/* Same from device arrays in the reference layout (weights already in HBM);
+ * repacks on the device and synchronises. */
+int kh_sparse_ffn_create_dev(int hidden, int inter, const uint16_t* w_gate_dev,
+                             const uint16_t* w_up_dev, const uint16_t* w_down_dev, int max_batch,
+                             kh_sparse_ffn** out);
+int kh_sparse_ffn_destroy(kh_sparse_ffn* f);
+/* sparse_mlp::forward_sparse (sparse_mlp.rs:4-37) for a batch of tokens sharing
+ * one active set: y[b] (=, or += when accumulate != 0) sum over active neurons a
+ * of Wd[:, a] * silu(Wg[a].x[b]) * (Wu[a].x[b]).  active_dev: int32 neuron ids
+ * (unique, any order); n_active is used as is, or, when n_active_dev is not
+ * NULL, *n_active_dev is read on the device and n_active is its upper bound. */
+int kh_sparse_ffn_forward(const kh_sparse_ffn* f, const float* x_dev, int64_t batch,
+                          const int32_t* active_dev, int n_active, const int32_t* n_active_dev,
+                          float* y_dev, int accumulate, void* stream);
+/* Per-neuron activations h[b][i] = silu(g)*u of the last forward, for tests. */
+int kh_sparse_ffn_last_hidden(const kh_sparse_ffn* f, float* h_dev, int64_t batch, int n_active,
+                              void* stream);
+
+/* RmsNorm::forward (model/rms_norm.rs:43-64): y[b] = x[b] * inv_rms * w. */
+int kh_rmsnorm(const float* x_dev, const float* w_dev, int64_t batch, int n, float eps,
+               float* y_dev, void* stream);
+
+/* ======================================================================== */
+/* Head-sparse decode attention (crates/klearu-llm/src/sparse/sparse_attention.rs) */
+/* ======================================================================== */
+
+typedef struct kh_sparse_attn kh_sparse_attn;
+
+/* Attention{q,k,v,o}_proj (model/attention.rs) + KvCache (model/kv_cache.rs:5-25)
+ * + RotaryEmbedding (model/rope.rs:17-46): BF16 weights in the reference
+ * layout wq[nh*d][hidden], wk/wv[nkv*d][hidden], wo[hidden][nh*d].  The cache
+ * holds max_batch sequences of max_seq positions, BF16, [seq][kv_head][pos][d]. */
+int kh_sparse_attn_create(int hidden, int num_heads, int num_kv_heads, int head_dim,
+                          int max_seq, int max_batch, float rope_theta, const uint16_t* wq_host,
+                          const uint16_t* wk_host, const uint16_t* wv_host,
+                          const uint16_t* wo_host, kh_sparse_attn** out);
+int kh_sparse_attn_destroy(kh_sparse_attn* a);
+/* Fill positions [0, len) of sequence b of the cache from f32 host arrays
+ * k_host/v_host [kv_heads][len][d] (rounded to BF16); sets that sequence's length. */
+int kh_sparse_attn_load_cache(kh_sparse_attn* a, int64_t b, const float* k_host,
+                              const float* v_host, int64_t len);
+/* sparse_attention::forward_sparse (sparse_attention.rs:7-79) for one decode
+ * step of `batch` sequences: x_dev[batch][hidden] at positions pos_dev[batch]
+ * (int64, = current cache length of each sequence), heads_dev[batch][n_heads]
+ * (int32; ids >= num_heads are skipped as at :48-50).  Appends this step's
+ * K/V for every kv head, computes softmax attention for the selected heads only
+ * and the output projection over the selected heads' columns only.
+ * out_dev[batch][hidden]. Mutates the cache. */
+int kh_sparse_attn_forward(kh_sparse_attn* a, const float* x_dev, int64_t batch,
+                           const int64_t* pos_dev, const int32_t* heads_dev, int n_heads,
+                           float* out_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KLEARU_HIP_H */

@@ -1,0 +1,212 @@
+// common.hpp -- shared helpers for libklearu_hip.so (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/klearu_hip.h"
+
+namespace kh {
+
+// ---------------------------------------------------------------- errors
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+#define KH_CHECK_ARG(cond, ...)        \
+  do {                                 \
+    if (!(cond)) {                     \
+      ::kh::set_error(__VA_ARGS__);    \
+      return KH_ERR_ARG;               \
+    }                                  \
+  } while (0)
+
+#define KH_HIP(call)                                                                \
+  do {                                                                              \
+    hipError_t e_ = (call);                                                         \
+    if (e_ != hipSuccess) {                                                         \
+      ::kh::set_error("%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, \
+                      __LINE__);                                                    \
+      return KH_ERR_HIP;                                                            \
+    }                                                                               \
+  } while (0)
+
+// Checks the launch that was just enqueued.
+#define KH_LAUNCHED()                                                              \
+  do {                                                                             \
+    hipError_t e_ = hipGetLastError();                                             \
+    if (e_ != hipSuccess) {                                                        \
+      ::kh::set_error("kernel launch failed: %s (%s:%d)", hipGetErrorString(e_),   \
+                      __FILE__, __LINE__);                                         \
+      return KH_ERR_HIP;                                                           \
+    }                                                                              \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Device allocation that records the failure; returns nullptr on error.
+void* dev_alloc(size_t bytes);
+void dev_free(void* p);
+
+// ---------------------------------------------------------------- device helpers
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+// Round to nearest even; NaN keeps its top bits and is forced quiet.
+__host__ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Sum over the 64 lanes of a wave (result valid in every lane).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// expf exactly as glibc computes it on x86-64 (the libm behind Rust's
+// f32::exp): the published ARM optimized-routines algorithm with a 32-entry
+// table of 2^(i/32) and a cubic in double precision, with the FMAs of glibc's
+// FMA build (range reduction fused into both of its uses).  Checked equal to
+// glibc expf for every non-NaN f32 input.
+__device__ __constant__ const uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+template <typename Tab>
+__device__ __forceinline__ float expf_glibc_t(float x, const Tab& tab) {
+  if (x != x) return x + x;
+  if (x > 0x1.62e42ep6f) return __int_as_float(0x7f800000);
+  if (x < -0x1.9fe368p6f) return 0.0f;
+  const double kInvLn2N = 0x1.71547652b82fep+0 * 32;
+  const double kShift = 0x1.8p+52;
+  const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
+  const double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+  const double c2 = 0x1.62e42ff0c52d6p-1 / 32;
+  const double xd = static_cast<double>(x);
+  double kd = fma(kInvLn2N, xd, kShift);
+  const uint64_t ki = static_cast<uint64_t>(__double_as_longlong(kd));
+  kd = kd - kShift;
+  const double r = fma(kInvLn2N, xd, -kd);
+  const uint64_t t = tab[ki % 32] + (ki << 47);
+  const double s = __longlong_as_double(static_cast<long long>(t));
+  const double z = fma(c0, r, c1);
+  const double r2 = r * r;
+  double y = fma(c2, r, 1.0);
+  y = fma(z, r2, y);
+  y = y * s;
+  return static_cast<float>(y);
+}
+
+__device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kExp2Tab); }
+
+// 1 / (1 + exp(-z)) with IEEE f32 add and divide; `tab` may be an LDS copy of
+// kExp2Tab when many lanes evaluate different arguments.
+template <typename Tab>
+__device__ __forceinline__ float sigmoid_ref_t(float z, const Tab& tab) {
+  float e = expf_glibc_t(-z, tab);
+  float d = __fadd_rn(1.0f, e);
+  return __fdiv_rn(1.0f, d);
+}
+// 1 / (1 + exp(-z)) with IEEE f32 add and divide.
+__device__ __forceinline__ float sigmoid_ref(float z) {
+  float e = expf_glibc(-z);
+  float d = __fadd_rn(1.0f, e);
+  return __fdiv_rn(1.0f, d);
+}
+// z / (1 + exp(-z)).
+__device__ __forceinline__ float silu_ref(float z) {
+  float e = expf_glibc(-z);
+  float d = __fadd_rn(1.0f, e);
+  return __fdiv_rn(z, d);
+}
+
+// Order-preserving key of an f32 (larger float -> larger key); -0.0 maps to
+// the key of +0.0 so that they compare equal, as partial_cmp does.
+__device__ __forceinline__ uint32_t f32_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Exclusive prefix sum of v over the block (blockDim.x a multiple of 64, at
+// most 1024).  wsum: shared scratch of blockDim.x/64 ints; *total (shared)
+// receives the block total.  Contains three __syncthreads.
+__device__ __forceinline__ int block_excl_scan(int v, int* wsum, int* total) {
+  // inclusive scan within the wave
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[w] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    const int nw = blockDim.x >> 6;
+    for (int i = 0; i < nw; ++i) {
+      int t = wsum[i];
+      wsum[i] = acc;
+      acc += t;
+    }
+    *total = acc;
+  }
+  __syncthreads();
+  const int r = wsum[w] + x - v;
+  __syncthreads();
+  return r;
+}
+
+// Workgroup barrier that waits only for LDS traffic.  __syncthreads() on gfx9
+// also waits for every outstanding vector-memory load (vmcnt counts loads and
+// stores together), which would drain global prefetches issued before it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Block-cooperative copy of n4 float4s from global memory to LDS with four
+// loads in flight per thread before any store (a plain strided loop would
+// wait one memory round trip per iteration).
+__device__ __forceinline__ void stage_f4(float4* __restrict__ dst, const float4* __restrict__ src,
+                                         int n4) {
+  constexpr int U = 4;
+  for (int base = threadIdx.x; base < n4; base += blockDim.x * U) {
+    float4 v[U];
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      const int i = base + q * blockDim.x;
+      v[q] = i < n4 ? src[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      const int i = base + q * blockDim.x;
+      if (i < n4) dst[i] = v[q];
+    }
+  }
+}
+
+inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) / b); }
+
+}  // namespace kh

@@ -1,0 +1,636 @@
+// ffn.hip -- Deja Vu sparse SwiGLU FFN over an active neuron set (gfx950).
+//
+// Replaces sparse_mlp::forward_sparse (crates/klearu-llm/src/sparse/sparse_mlp.rs:4-37)
+// and Linear::forward_sparse (crates/klearu-llm/src/model/linear.rs:107-114).
+//
+// HBM layout (BF16, written once at create):
+//   Wgu [inter][2][hidden]  gate row then up row of each neuron: one active
+//                           neuron is one contiguous 2*hidden*2-byte stretch.
+//   WdT [inter][hidden]     down projection transposed, so the down column of
+//                           an active neuron is one contiguous row.
+// Every weight byte of an active neuron is read exactly once per call with
+// 16-byte (dwordx4) loads; that is the algorithmic traffic 3*k*hidden*2 bytes.
+//
+// Kernels (all loads of a wave are issued before its first wait; the decode
+// path is bound by HBM latency and bandwidth, not arithmetic):
+//   batch 1:  ffn_fused1   one wave per active neuron loads its gate, up and
+//                          down rows together, h = silu(g)*u, scales the down
+//                          row and the block's waves are added in LDS into one
+//                          partial row per block;
+//             ffn_reduce   adds the partial rows in block order (a kernel
+//                          boundary instead of device-scope fences, which on
+//                          gfx950 write back and invalidate the whole L2).
+//   batch>1:  ffn_gateup   one wave per active neuron, tokens staged in LDS;
+//             ffn_down     (column slice x row group) partials;
+//             ffn_reduce   as above.
+// No float atomics: the summation order is fixed, so outputs are deterministic.
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
+#include "common.hpp"
+
+namespace kh {
+
+constexpr int kSlice = 256;      // output columns per down block
+constexpr int kMaxDynLds = 152 * 1024;  // dynamic LDS ceiling (160 KB per CU minus static use)
+constexpr int kMaxGroups = 128;  // row groups per slice (partials)
+constexpr int kDownThreads = 256;
+
+constexpr int kGuWaves = 4;       // neurons per gate/up block
+constexpr int kGuChunks = 8;      // 16-byte chunks per lane held in flight (H <= 4096 in one pass)
+constexpr int kGuTok = 4;         // tokens staged in LDS at a time
+
+// One wave per active neuron.  x (up to kGuTok tokens at a time) is staged in
+// LDS once per block; each lane then issues all of its gate and up loads
+// (kGuChunks x 16 B each) before the first use, so a wave keeps 16 KB in
+// flight and the whole kernel is one round trip of HBM latency deep.
+template <int NB>
+__global__ __launch_bounds__(64 * kGuWaves) void ffn_gateup_kernel(
+    const uint16_t* __restrict__ Wgu, const float* __restrict__ x, int batch, int H,
+    const int32_t* __restrict__ active, int n_active, const int32_t* __restrict__ n_active_dev,
+    float* __restrict__ hbuf, int hstride) {
+  extern __shared__ float4 xs4[];  // [kGuTok][H/4]
+  int n = n_active;
+  if (n_active_dev) n = min(n, *n_active_dev);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int item = blockIdx.x * kGuWaves + wave;
+  if (blockIdx.x * kGuWaves >= n) return;  // whole block idle (uniform)
+  const bool live = item < n;
+  const int neuron = active[live ? item : n - 1];
+  const uint4* __restrict__ g = reinterpret_cast<const uint4*>(Wgu + (size_t)neuron * 2 * H);
+  const uint4* __restrict__ u = g + (H >> 3);
+  const int nchunk = H >> 3;
+  const int H4 = H >> 2;
+  constexpr int TB = NB < kGuTok ? NB : kGuTok;
+  float ag[NB], au[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) ag[b] = au[b] = 0.0f;
+  for (int cbase = 0; cbase < nchunk; cbase += 64 * kGuChunks) {
+    uint4 wg[kGuChunks], wu[kGuChunks];
+#pragma unroll
+    for (int q = 0; q < kGuChunks; ++q) {
+      // clamped, branch-free loads: chunks past the row end are never used
+      const int c = min(cbase + lane + 64 * q, nchunk - 1);
+      wg[q] = g[c];
+      wu[q] = u[c];
+    }
+#pragma unroll
+    for (int t0 = 0; t0 < NB; t0 += TB) {
+      if (t0 >= batch) break;
+      lds_barrier();
+      const int nt = min(TB, batch - t0);
+      stage_f4(xs4, reinterpret_cast<const float4*>(x + (size_t)t0 * H), nt * H4);
+      lds_barrier();
+#pragma unroll
+      for (int q = 0; q < kGuChunks; ++q) {
+        const int c = cbase + lane + 64 * q;
+        if (c >= nchunk) break;
+        float wgf[8], wuf[8];
+        wgf[0] = bf16_lo(wg[q].x); wgf[1] = bf16_hi(wg[q].x); wgf[2] = bf16_lo(wg[q].y); wgf[3] = bf16_hi(wg[q].y);
+        wgf[4] = bf16_lo(wg[q].z); wgf[5] = bf16_hi(wg[q].z); wgf[6] = bf16_lo(wg[q].w); wgf[7] = bf16_hi(wg[q].w);
+        wuf[0] = bf16_lo(wu[q].x); wuf[1] = bf16_hi(wu[q].x); wuf[2] = bf16_lo(wu[q].y); wuf[3] = bf16_hi(wu[q].y);
+        wuf[4] = bf16_lo(wu[q].z); wuf[5] = bf16_hi(wu[q].z); wuf[6] = bf16_lo(wu[q].w); wuf[7] = bf16_hi(wu[q].w);
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+          if (t < nt) {
+            const float4 x0 = xs4[t * H4 + 2 * c], x1 = xs4[t * H4 + 2 * c + 1];
+            const float xf[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const int b = t0 + t;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              ag[b] = fmaf(wgf[e], xf[e], ag[b]);
+              au[b] = fmaf(wuf[e], xf[e], au[b]);
+            }
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (b < batch) {
+      const float gs = wave_sum(ag[b]);
+      const float us = wave_sum(au[b]);
+      if (lane == 0 && live) hbuf[(size_t)b * hstride + item] = silu_ref(gs) * us;
+    }
+  }
+}
+
+constexpr int kDownRows = 128;  // max rows per down block (16 per row lane)
+
+// Column slice (256 outputs) x row group.  The group's active ids and h values
+// are staged in LDS; every thread then issues all of its (<= 16) row loads of
+// 16 bytes before accumulating.  Row lane `sub` (0..7, half a wave each) takes
+// rows sub, sub+8, ...; partial sums are reduced across row lanes in LDS and
+// written per group; ffn_reduce_kernel then adds the groups' partials in group
+// order, so the result is deterministic.
+template <int NB>
+__global__ __launch_bounds__(kDownThreads) void ffn_down_kernel(
+    const uint16_t* __restrict__ WdT, int H, const int32_t* __restrict__ active, int n_active,
+    const int32_t* __restrict__ n_active_dev, const float* __restrict__ hbuf, int hstride,
+    int batch, int groups, float* __restrict__ partial) {
+  __shared__ float red[4][NB][kSlice];
+  __shared__ int s_ids[kDownRows];
+  __shared__ float s_h[NB][kDownRows];
+  int n = n_active;
+  if (n_active_dev) n = min(n, *n_active_dev);
+  const int slice = blockIdx.x, grp = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int sub = tid >> 5;
+  const int cl = tid & 31;
+  const int col = slice * kSlice + cl * 8;
+  const bool colok = col < H;
+  const int per = (n + groups - 1) / groups;
+  const int r0 = min(n, grp * per);
+  const int r1 = min(n, r0 + per);
+  const int nr = r1 - r0;  // <= kDownRows by construction of `groups`
+  for (int i = tid; i < nr; i += blockDim.x) s_ids[i] = active[r0 + i];
+  for (int i = tid; i < nr * NB; i += blockDim.x) {
+    const int b = i / nr, r = i - b * nr;
+    s_h[b][r] = b < batch ? hbuf[(size_t)b * hstride + r0 + r] : 0.0f;
+  }
+  __syncthreads();
+  constexpr int RPL = kDownRows / 8;  // rows per row lane
+  uint4 w[RPL];
+#pragma unroll
+  for (int m = 0; m < RPL; ++m) {
+    const int r = sub + 8 * m;
+    w[m] = (r < nr && colok) ? *reinterpret_cast<const uint4*>(WdT + (size_t)s_ids[r] * H + col)
+                             : make_uint4(0, 0, 0, 0);
+  }
+  float acc[NB][8];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[b][e] = 0.0f;
+#pragma unroll
+  for (int m = 0; m < RPL; ++m) {
+    const int r = sub + 8 * m;
+    if (r >= nr) break;
+    const float wf[8] = {bf16_lo(w[m].x), bf16_hi(w[m].x), bf16_lo(w[m].y), bf16_hi(w[m].y),
+                         bf16_lo(w[m].z), bf16_hi(w[m].z), bf16_lo(w[m].w), bf16_hi(w[m].w)};
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float hv = s_h[b][r];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[b][e] = fmaf(hv, wf[e], acc[b][e]);
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[b][e] += __shfl_xor(acc[b][e], 32, 64);
+  const int wv = tid >> 6;
+  if ((tid & 63) < 32) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[wv][b][cl * 8 + e] = acc[b][e];
+  }
+  __syncthreads();
+  const int ocol = slice * kSlice + tid;
+  for (int b = 0; b < batch; ++b) {
+    const float sm = (red[0][b][tid] + red[1][b][tid]) + (red[2][b][tid] + red[3][b][tid]);
+    if (ocol < H) partial[((size_t)grp * NB + b) * H + ocol] = sm;
+  }
+}
+
+// Single-token fused FFN: one wave per active neuron, kFuWaves neurons per
+// block.  Each lane issues its gate, up and down-row loads together (the down
+// row does not depend on h), so a wave has 3*H*2 bytes in flight at once; then
+// h = silu(g)*u, the down row is scaled by h (H/64 outputs per lane) and the
+// block adds its waves' rows in LDS in wave order into one partial row,
+// partial[block][H].  ffn_reduce_kernel adds the partials in block order.
+constexpr int kFuWaves = 8;
+constexpr int kFuMaxH = 4096;              // 8 chunks of 16 B per lane per row
+constexpr int kFuChunks = kFuMaxH / 512;
+
+__global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
+    const uint16_t* __restrict__ Wgu, const uint16_t* __restrict__ WdT,
+    const float* __restrict__ x, int H, const int32_t* __restrict__ active, int n_active,
+    const int32_t* __restrict__ n_active_dev, float* __restrict__ hbuf,
+    float* __restrict__ partial) {
+  extern __shared__ float4 smem4[];
+  float4* xs4 = smem4;                                    // [H/4]
+  float* red = reinterpret_cast<float*>(smem4 + (H >> 2));  // [4][H]
+  int n = n_active;
+  if (n_active_dev) n = min(n, *n_active_dev);
+  if (blockIdx.x * kFuWaves >= n) return;  // uniform per block
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int item = blockIdx.x * kFuWaves + wave;
+  const bool live = item < n;
+  const int neuron = active[live ? item : n - 1];
+  const int nchunk = H >> 3;
+  const uint4* __restrict__ g = reinterpret_cast<const uint4*>(Wgu + (size_t)neuron * 2 * H);
+  const uint4* __restrict__ u = g + nchunk;
+  const uint4* __restrict__ d = reinterpret_cast<const uint4*>(WdT + (size_t)neuron * H);
+  // x loads first, then the weight rows: vmcnt counts in issue order, so x
+  // can be written to LDS while every weight load is still in flight.
+  const int n4 = H >> 2;
+  const float4* __restrict__ xsrc = reinterpret_cast<const float4*>(x);
+  constexpr int kXq = kFuMaxH / 4 / (64 * kFuWaves);  // float4 of x per thread
+  float4 xv[kXq];
+#pragma unroll
+  for (int q = 0; q < kXq; ++q) xv[q] = xsrc[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)];
+  uint4 wg[kFuChunks], wu[kFuChunks], wd[kFuChunks];
+#pragma unroll
+  for (int q = 0; q < kFuChunks; ++q) {
+    const int c = min(lane + 64 * q, nchunk - 1);
+    wg[q] = g[c];
+    wu[q] = u[c];
+    wd[q] = d[c];
+  }
+#pragma unroll
+  for (int q = 0; q < kXq; ++q) {
+    const int i = threadIdx.x + q * 64 * kFuWaves;
+    if (i < n4) xs4[i] = xv[q];
+  }
+  lds_barrier();
+  float ag = 0.0f, au = 0.0f;
+#pragma unroll
+  for (int q = 0; q < kFuChunks; ++q) {
+    const int c = lane + 64 * q;
+    if (c < nchunk) {
+      const float4 x0 = xs4[2 * c], x1 = xs4[2 * c + 1];
+      ag = fmaf(bf16_lo(wg[q].x), x0.x, ag); au = fmaf(bf16_lo(wu[q].x), x0.x, au);
+      ag = fmaf(bf16_hi(wg[q].x), x0.y, ag); au = fmaf(bf16_hi(wu[q].x), x0.y, au);
+      ag = fmaf(bf16_lo(wg[q].y), x0.z, ag); au = fmaf(bf16_lo(wu[q].y), x0.z, au);
+      ag = fmaf(bf16_hi(wg[q].y), x0.w, ag); au = fmaf(bf16_hi(wu[q].y), x0.w, au);
+      ag = fmaf(bf16_lo(wg[q].z), x1.x, ag); au = fmaf(bf16_lo(wu[q].z), x1.x, au);
+      ag = fmaf(bf16_hi(wg[q].z), x1.y, ag); au = fmaf(bf16_hi(wu[q].z), x1.y, au);
+      ag = fmaf(bf16_lo(wg[q].w), x1.z, ag); au = fmaf(bf16_lo(wu[q].w), x1.z, au);
+      ag = fmaf(bf16_hi(wg[q].w), x1.w, ag); au = fmaf(bf16_hi(wu[q].w), x1.w, au);
+    }
+  }
+  // wave-uniform values: the exp table lookup inside silu becomes a scalar load
+  const float gs = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_sum(ag))));
+  const float us = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_sum(au))));
+  const float h = live ? silu_ref(gs) * us : 0.0f;
+  // h * down row; waves 0-3 write their rows, waves 4-7 add theirs, then the
+  // four rows are added in fixed order.
+  float* my = red + (size_t)(wave & 3) * H;
+  if (wave < 4) {
+#pragma unroll
+    for (int q = 0; q < kFuChunks; ++q) {
+      const int c = lane + 64 * q;
+      if (c < nchunk) {
+        float4* o = reinterpret_cast<float4*>(my + 8 * c);
+        o[0] = make_float4(h * bf16_lo(wd[q].x), h * bf16_hi(wd[q].x), h * bf16_lo(wd[q].y), h * bf16_hi(wd[q].y));
+        o[1] = make_float4(h * bf16_lo(wd[q].z), h * bf16_hi(wd[q].z), h * bf16_lo(wd[q].w), h * bf16_hi(wd[q].w));
+      }
+    }
+  }
+  __syncthreads();
+  if (wave >= 4) {
+#pragma unroll
+    for (int q = 0; q < kFuChunks; ++q) {
+      const int c = lane + 64 * q;
+      if (c < nchunk) {
+        float4* o = reinterpret_cast<float4*>(my + 8 * c);
+        float4 a = o[0], b = o[1];
+        a.x = fmaf(h, bf16_lo(wd[q].x), a.x); a.y = fmaf(h, bf16_hi(wd[q].x), a.y);
+        a.z = fmaf(h, bf16_lo(wd[q].y), a.z); a.w = fmaf(h, bf16_hi(wd[q].y), a.w);
+        b.x = fmaf(h, bf16_lo(wd[q].z), b.x); b.y = fmaf(h, bf16_hi(wd[q].z), b.y);
+        b.z = fmaf(h, bf16_lo(wd[q].w), b.z); b.w = fmaf(h, bf16_hi(wd[q].w), b.w);
+        o[0] = a;
+        o[1] = b;
+      }
+    }
+  }
+  __syncthreads();
+  float* prow = partial + (size_t)blockIdx.x * H;
+  for (int j = threadIdx.x * 4; j < H; j += blockDim.x * 4) {
+    const float4 r0 = *reinterpret_cast<const float4*>(red + j);
+    const float4 r1 = *reinterpret_cast<const float4*>(red + H + j);
+    const float4 r2 = *reinterpret_cast<const float4*>(red + 2 * H + j);
+    const float4 r3 = *reinterpret_cast<const float4*>(red + 3 * H + j);
+    *reinterpret_cast<float4*>(prow + j) =
+        make_float4((r0.x + r1.x) + (r2.x + r3.x), (r0.y + r1.y) + (r2.y + r3.y),
+                    (r0.z + r1.z) + (r2.z + r3.z), (r0.w + r1.w) + (r2.w + r3.w));
+  }
+  if (lane == 0 && live && hbuf) hbuf[item] = h;
+}
+
+// y[b][j] (=, or +=) sum over g of partial[g][b][j].  A block owns 64 columns;
+// its 16 waves take partial rows w, w+16, ... (all loads of a thread issued
+// before the first add), then the 16 wave sums are added in wave order, so the
+// summation order is fixed for a given number of partial rows.
+constexpr int kRedWaves = 16;
+template <int NB>
+__global__ __launch_bounds__(64 * kRedWaves) void ffn_reduce_kernel(const float* __restrict__ partial,
+                                                                    int H, int groups,
+                                                                    float* __restrict__ y,
+                                                                    int accumulate) {
+  __shared__ float sums[kRedWaves][64];
+  const int b = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int j = blockIdx.x * 64 + lane;
+  const int jc = min(j, H - 1);
+  constexpr int U = 16;
+  float t = 0.0f;
+  for (int g0 = wave; g0 < groups; g0 += kRedWaves * U) {
+    float v[U];
+#pragma unroll
+    for (int q = 0; q < U; ++q)
+      v[q] = partial[((size_t)min(g0 + kRedWaves * q, groups - 1) * NB + b) * H + jc];
+#pragma unroll
+    for (int q = 0; q < U; ++q)
+      if (g0 + kRedWaves * q < groups) t += v[q];
+  }
+  sums[wave][lane] = t;
+  __syncthreads();
+  if (wave == 0 && j < H) {
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kRedWaves; ++w) tot += sums[w][lane];
+    float* yp = y + (size_t)b * H + j;
+    *yp = accumulate ? (*yp + tot) : tot;
+  }
+}
+
+// dst[i][j] = src[j][i] for a [rows][cols] u16 matrix (32x32 LDS tiles).
+__global__ __launch_bounds__(256) void transpose_u16_kernel(const uint16_t* __restrict__ src,
+                                                            int rows, int cols,
+                                                            uint16_t* __restrict__ dst) {
+  __shared__ uint16_t tile[32][33];
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int r = ty; r < 32; r += 8)
+    if (r0 + r < rows && c0 + tx < cols) tile[r][tx] = src[(size_t)(r0 + r) * cols + c0 + tx];
+  __syncthreads();
+  for (int c = ty; c < 32; c += 8)
+    if (c0 + c < cols && r0 + tx < rows) dst[(size_t)(c0 + c) * rows + r0 + tx] = tile[tx][c];
+}
+
+// RmsNorm::forward (crates/klearu-llm/src/model/rms_norm.rs:43-64): one block
+// of 1024 threads per row; each thread loads its (<= 4) float4s before reducing.
+__global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ w, int n,
+                                                       float eps, float* __restrict__ y) {
+  __shared__ float part[16];
+  const float* xr = x + (size_t)blockIdx.x * n;
+  float* yr = y + (size_t)blockIdx.x * n;
+  const bool vec = (n & 3) == 0;
+  float s = 0.0f;
+  if (vec) {
+    const int n4 = n >> 2;
+    float4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = threadIdx.x + q * 1024;
+      v[q] = i < n4 ? reinterpret_cast<const float4*>(xr)[i] : make_float4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      s = fmaf(v[q].x, v[q].x, fmaf(v[q].y, v[q].y, fmaf(v[q].z, v[q].z, fmaf(v[q].w, v[q].w, s))));
+    for (int i = threadIdx.x + 4 * 1024; i < n4; i += 1024) {
+      const float4 t = reinterpret_cast<const float4*>(xr)[i];
+      s = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, s))));
+    }
+  } else {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) s = fmaf(xr[i], xr[i], s);
+  }
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) tot += part[i];
+  const float rms = sqrtf(tot / static_cast<float>(n) + eps);
+  const float inv = 1.0f / rms;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = (xr[i] * inv) * w[i];
+}
+
+}  // namespace kh
+
+using namespace kh;
+
+struct kh_sparse_ffn {
+  int hidden = 0, inter = 0, max_batch = 0;
+  uint16_t* wgu = nullptr;   // [inter][2][hidden]
+  uint16_t* wdt = nullptr;   // [inter][hidden]
+  float* hbuf = nullptr;     // [max_batch][inter]
+  float* partial = nullptr;  // [max(kMaxGroups*nb_tmpl, fused blocks)][hidden]
+  int nslices = 0;
+};
+
+static size_t partial_rows(int inter, int nbt) {
+  return std::max<size_t>((size_t)kMaxGroups * nbt, (size_t)ceil_div(inter, kFuWaves));
+}
+
+static int ffn_tmpl(int64_t batch) {
+  return batch <= 1 ? 1 : batch <= 2 ? 2 : batch <= 4 ? 4 : batch <= 8 ? 8 : 16;
+}
+
+extern "C" int kh_sparse_ffn_create(int hidden, int inter, const uint16_t* w_gate_host,
+                                    const uint16_t* w_up_host, const uint16_t* w_down_host,
+                                    int max_batch, kh_sparse_ffn** out) {
+  KH_CHECK_ARG(out && w_gate_host && w_up_host && w_down_host, "null argument");
+  KH_CHECK_ARG(hidden > 0 && inter > 0 && hidden % 8 == 0,
+               "hidden (%d) must be a positive multiple of 8, inter (%d) positive", hidden, inter);
+  KH_CHECK_ARG(max_batch >= 1 && max_batch <= 16, "max_batch %d not in [1,16]", max_batch);
+  *out = nullptr;
+  auto* f = new kh_sparse_ffn();
+  f->hidden = hidden;
+  f->inter = inter;
+  f->max_batch = max_batch;
+  f->nslices = ceil_div(hidden, kSlice);
+  const size_t H = hidden, I = inter;
+  // Host-side repack into the device layouts.
+  uint16_t* gu = static_cast<uint16_t*>(malloc(sizeof(uint16_t) * 2 * H * I));
+  uint16_t* dt = static_cast<uint16_t*>(malloc(sizeof(uint16_t) * H * I));
+  if (!gu || !dt) {
+    free(gu);
+    free(dt);
+    delete f;
+    set_error("host allocation failed");
+    return KH_ERR_ALLOC;
+  }
+  for (size_t i = 0; i < I; ++i) {
+    memcpy(gu + i * 2 * H, w_gate_host + i * H, sizeof(uint16_t) * H);
+    memcpy(gu + i * 2 * H + H, w_up_host + i * H, sizeof(uint16_t) * H);
+  }
+  const size_t TB = 64;
+  for (size_t j0 = 0; j0 < H; j0 += TB)
+    for (size_t i0 = 0; i0 < I; i0 += TB)
+      for (size_t j = j0; j < std::min(H, j0 + TB); ++j)
+        for (size_t i = i0; i < std::min(I, i0 + TB); ++i) dt[i * H + j] = w_down_host[j * I + i];
+  const int nbt = ffn_tmpl(max_batch);
+  f->wgu = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * 2 * H * I));
+  f->wdt = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * H * I));
+  f->hbuf = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * I));
+  f->partial = static_cast<float*>(dev_alloc(sizeof(float) * partial_rows(inter, nbt) * H));
+  int rc = KH_OK;
+  if (!f->wgu || !f->wdt || !f->hbuf || !f->partial) rc = KH_ERR_ALLOC;
+  if (rc == KH_OK) {
+    if (hipMemcpy(f->wgu, gu, sizeof(uint16_t) * 2 * H * I, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(f->wdt, dt, sizeof(uint16_t) * H * I, hipMemcpyHostToDevice) != hipSuccess) {
+      set_error("weight upload failed");
+      rc = KH_ERR_HIP;
+    }
+  }
+  free(gu);
+  free(dt);
+  if (rc != KH_OK) {
+    kh_sparse_ffn_destroy(f);
+    return rc;
+  }
+  *out = f;
+  return KH_OK;
+}
+
+extern "C" int kh_sparse_ffn_create_dev(int hidden, int inter, const uint16_t* w_gate_dev,
+                                        const uint16_t* w_up_dev, const uint16_t* w_down_dev,
+                                        int max_batch, kh_sparse_ffn** out) {
+  KH_CHECK_ARG(out && w_gate_dev && w_up_dev && w_down_dev, "null argument");
+  KH_CHECK_ARG(hidden > 0 && inter > 0 && hidden % 8 == 0,
+               "hidden (%d) must be a positive multiple of 8, inter (%d) positive", hidden, inter);
+  KH_CHECK_ARG(max_batch >= 1 && max_batch <= 16, "max_batch %d not in [1,16]", max_batch);
+  *out = nullptr;
+  auto* f = new kh_sparse_ffn();
+  f->hidden = hidden;
+  f->inter = inter;
+  f->max_batch = max_batch;
+  f->nslices = ceil_div(hidden, kSlice);
+  const size_t H = hidden, I = inter;
+  const int nbt = ffn_tmpl(max_batch);
+  f->wgu = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * 2 * H * I));
+  f->wdt = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * H * I));
+  f->hbuf = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * I));
+  f->partial = static_cast<float*>(dev_alloc(sizeof(float) * partial_rows(inter, nbt) * H));
+  if (!f->wgu || !f->wdt || !f->hbuf || !f->partial) {
+    kh_sparse_ffn_destroy(f);
+    return KH_ERR_ALLOC;
+  }
+  const size_t rowb = sizeof(uint16_t) * H;
+  hipError_t e = hipMemcpy2D(f->wgu, 2 * rowb, w_gate_dev, rowb, rowb, I, hipMemcpyDeviceToDevice);
+  if (e == hipSuccess)
+    e = hipMemcpy2D(f->wgu + H, 2 * rowb, w_up_dev, rowb, rowb, I, hipMemcpyDeviceToDevice);
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(transpose_u16_kernel, dim3(ceil_div(I, 32), ceil_div(H, 32)), dim3(256), 0,
+                       0, w_down_dev, hidden, inter, f->wdt);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    set_error("device weight repack failed: %s", hipGetErrorString(e));
+    kh_sparse_ffn_destroy(f);
+    return KH_ERR_HIP;
+  }
+  *out = f;
+  return KH_OK;
+}
+
+extern "C" int kh_sparse_ffn_destroy(kh_sparse_ffn* f) {
+  if (!f) return KH_OK;
+  dev_free(f->wgu);
+  dev_free(f->wdt);
+  dev_free(f->hbuf);
+  dev_free(f->partial);
+  delete f;
+  return KH_OK;
+}
+
+template <int NB>
+static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const int32_t* active,
+                      int n_active, const int32_t* n_active_dev, float* y, int accumulate,
+                      hipStream_t st) {
+  const int H = f->hidden;
+  dim3 g1(ceil_div(n_active, kGuWaves));
+  const size_t lds1 = sizeof(float) * std::min(NB, kGuTok) * H;
+  static bool attr_set = false;
+  if (!attr_set) {
+    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_gateup_kernel<NB>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+    attr_set = true;
+  }
+  if (lds1 > (size_t)kMaxDynLds) {
+    set_error("hidden %d too large for %d staged tokens", H, std::min(NB, kGuTok));
+    return KH_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL(ffn_gateup_kernel<NB>, g1, dim3(64 * kGuWaves), lds1, st, f->wgu, x, batch,
+                     H, active, n_active, n_active_dev, f->hbuf, f->inter);
+  KH_LAUNCHED();
+  // Row groups: enough blocks to cover the chip, at most kDownRows rows each.
+  int groups = ceil_div(512, f->nslices);
+  groups = std::max(groups, ceil_div(n_active, kDownRows));
+  groups = std::max(1, std::min(groups, ceil_div(n_active, 8)));
+  if (ceil_div(n_active, groups) > kDownRows || groups > kMaxGroups) {
+    set_error("n_active %d too large for the down kernel", n_active);
+    return KH_ERR_UNSUPPORTED;
+  }
+  dim3 g2(f->nslices, groups);
+  hipLaunchKernelGGL(ffn_down_kernel<NB>, g2, dim3(kDownThreads), 0, st, f->wdt, H, active,
+                     n_active, n_active_dev, f->hbuf, f->inter, batch, groups, f->partial);
+  KH_LAUNCHED();
+  hipLaunchKernelGGL(ffn_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch), dim3(64 * kRedWaves),
+                     0, st, f->partial, H, groups, y, accumulate);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
+extern "C" int kh_sparse_ffn_forward(const kh_sparse_ffn* f, const float* x_dev, int64_t batch,
+                                     const int32_t* active_dev, int n_active,
+                                     const int32_t* n_active_dev, float* y_dev, int accumulate,
+                                     void* stream) {
+  KH_CHECK_ARG(f && x_dev && y_dev, "null argument");
+  KH_CHECK_ARG(batch >= 1 && batch <= f->max_batch, "batch %lld not in [1,%d]", (long long)batch,
+               f->max_batch);
+  KH_CHECK_ARG(n_active >= 0 && n_active <= f->inter, "n_active %d not in [0,%d]", n_active,
+               f->inter);
+  hipStream_t st = as_stream(stream);
+  if (n_active == 0) {
+    if (!accumulate) KH_HIP(hipMemsetAsync(y_dev, 0, sizeof(float) * batch * f->hidden, st));
+    return KH_OK;
+  }
+  KH_CHECK_ARG(active_dev != nullptr, "null active list");
+  const int b = static_cast<int>(batch);
+  if (batch == 1 && f->hidden <= kFuMaxH) {
+    const int H = f->hidden;
+    const int blocks = ceil_div(n_active, kFuWaves);
+    const size_t lds = sizeof(float) * (size_t)H * 5;
+    static bool attr = false;
+    if (!attr) {
+      KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+      attr = true;
+    }
+    hipLaunchKernelGGL(ffn_fused1_kernel, dim3(blocks), dim3(64 * kFuWaves), lds, st, f->wgu,
+                       f->wdt, x_dev, H, active_dev, n_active, n_active_dev, f->hbuf, f->partial);
+    KH_LAUNCHED();
+    hipLaunchKernelGGL(ffn_reduce_kernel<1>, dim3(ceil_div(H, 64), 1), dim3(64 * kRedWaves), 0,
+                       st, f->partial, H, blocks, y_dev, accumulate);
+    KH_LAUNCHED();
+    return KH_OK;
+  }
+  switch (ffn_tmpl(batch)) {
+    case 1: return ffn_launch<1>(f, x_dev, b, active_dev, n_active, n_active_dev, y_dev, accumulate, st);
+    case 2: return ffn_launch<2>(f, x_dev, b, active_dev, n_active, n_active_dev, y_dev, accumulate, st);
+    case 4: return ffn_launch<4>(f, x_dev, b, active_dev, n_active, n_active_dev, y_dev, accumulate, st);
+    case 8: return ffn_launch<8>(f, x_dev, b, active_dev, n_active, n_active_dev, y_dev, accumulate, st);
+    default: return ffn_launch<16>(f, x_dev, b, active_dev, n_active, n_active_dev, y_dev, accumulate, st);
+  }
+}
+
+extern "C" int kh_sparse_ffn_last_hidden(const kh_sparse_ffn* f, float* h_dev, int64_t batch,
+                                         int n_active, void* stream) {
+  KH_CHECK_ARG(f && h_dev, "null argument");
+  KH_CHECK_ARG(batch >= 1 && batch <= f->max_batch && n_active >= 0 && n_active <= f->inter,
+               "bad batch/n_active");
+  KH_HIP(hipMemcpy2DAsync(h_dev, sizeof(float) * n_active, f->hbuf, sizeof(float) * f->inter,
+                          sizeof(float) * n_active, batch, hipMemcpyDeviceToDevice,
+                          as_stream(stream)));
+  return KH_OK;
+}
+
+extern "C" int kh_rmsnorm(const float* x_dev, const float* w_dev, int64_t batch, int n, float eps,
+                          float* y_dev, void* stream) {
+  KH_CHECK_ARG(x_dev && w_dev && y_dev, "null argument");
+  KH_CHECK_ARG(batch >= 0 && n > 0, "bad shape");
+  if (batch == 0) return KH_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(batch), dim3(1024), 0, as_stream(stream), x_dev, w_dev,
+                     n, eps, y_dev);
+  KH_LAUNCHED();
+  return KH_OK;
+}

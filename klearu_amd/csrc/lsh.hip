@@ -1,0 +1,719 @@
+// lsh.hip -- SimHash / SRP hashing and the LSH index on the GPU (gfx950).
+//
+// Replaces HashFamily::hash_dense / hash_sparse (crates/klearu-core/src/hash/
+// simhash.rs:75-126, hash/srp.rs:95-161), LshIndexTrait insert / query /
+// query_union / clear (crates/klearu-core/src/lsh/index.rs:219-316) and the
+// FIFO / reservoir buckets (bucket/fifo.rs:27-33, bucket/reservoir.rs:40-67).
+//
+// Hashing.  A code bit is the sign of a sequential f32 sum over the input
+// dimensions in ascending order, +x where the plane is +1 and -x where it is
+// -1.  One thread owns one (table, bit) plane and replays that exact sum over
+// the plane's nonzeros (CSR list, ascending dimension), so codes are
+// bit-identical to the reference.  SRP is the same computation with a
+// different plane distribution.
+//
+// Index build.  Inserting ids in order into L tables is, per bucket, a
+// sequence of ids in insertion order.  The build hashes all vectors, sorts the
+// (bucket, position) pairs with a stable radix sort so that every bucket's
+// inserts are contiguous and in order, then one thread per bucket applies
+// them: FIFO keeps the last `cap` ids; the reservoir replays Algorithm R with
+// the reference's SplitMix64 draws.  Buckets are dense [L][2^k][cap] u32 with
+// len[L][2^k] and the reservoir insertion count[L][2^k].
+//
+// Query.  One block per input gathers its L buckets.  When ids are below
+// 12288 it counts hits in an LDS array indexed by id and compacts in id
+// order; otherwise it sorts the gathered ids in LDS (bitonic) and counts runs.
+// Output order is ascending id (the reference returns HashMap order).
+#include <rocprim/device/device_radix_sort.hpp>
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "lsh_internal.hpp"
+#include "rng.hpp"
+
+namespace kh {
+
+constexpr int kHashThreads = 256;
+constexpr int kQueryThreads = 256;
+constexpr int kDirectIds = 12288;  // LDS counting when all ids are below this
+constexpr int kMaxGather = 8192;   // L * cap limit of the sort path
+
+// ------------------------------------------------------------------ kernels
+__global__ __launch_bounds__(kHashThreads) void hash_dense_kernel(
+    const int32_t* __restrict__ off, const uint32_t* __restrict__ ent, int k, int L, int dim,
+    const float* __restrict__ x, int64_t ldx, int64_t batch, uint32_t* __restrict__ codes,
+    int x_in_lds) {
+  extern __shared__ float xs[];
+  uint32_t* cw = reinterpret_cast<uint32_t*>(xs + (x_in_lds ? dim : 0));
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * ldx;
+  if (x_in_lds)
+    for (int d = threadIdx.x; d < dim; d += blockDim.x) xs[d] = xr[d];
+  for (int t = threadIdx.x; t < L; t += blockDim.x) cw[t] = 0u;
+  __syncthreads();
+  const float* xv = x_in_lds ? xs : xr;
+  const int P = L * k;
+  for (int p = threadIdx.x; p < P; p += blockDim.x) {
+    float s = 0.0f;
+    const int e1 = off[p + 1];
+    for (int e = off[p]; e < e1; ++e) {
+      const uint32_t v = ent[e];
+      const float xd = xv[v >> 1];
+      s = (v & 1u) ? __fsub_rn(s, xd) : __fadd_rn(s, xd);
+    }
+    if (s >= 0.0f) atomicOr(&cw[p / k], 1u << (p % k));
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < L; t += blockDim.x) codes[row * L + t] = cw[t];
+}
+
+__global__ __launch_bounds__(kHashThreads) void hash_sparse_kernel(
+    const int8_t* __restrict__ planes, int k, int L, int dim, const int64_t* __restrict__ xoff,
+    const uint32_t* __restrict__ xidx, const float* __restrict__ xval,
+    uint32_t* __restrict__ codes) {
+  __shared__ uint32_t cw[256];
+  const int64_t row = blockIdx.x;
+  const int64_t a = xoff[row], b = xoff[row + 1];
+  for (int t = threadIdx.x; t < L; t += blockDim.x) cw[t] = 0u;
+  __syncthreads();
+  const int P = L * k;
+  for (int p = threadIdx.x; p < P; p += blockDim.x) {
+    const int8_t* pl = planes + (size_t)p * dim;
+    float s = 0.0f;
+    for (int64_t e = a; e < b; ++e) {
+      const int8_t r = pl[xidx[e]];
+      if (r == 1) s = __fadd_rn(s, xval[e]);
+      else if (r == -1) s = __fsub_rn(s, xval[e]);
+    }
+    if (s >= 0.0f) atomicOr(&cw[p / k], 1u << (p % k));
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < L; t += blockDim.x) codes[row * L + t] = cw[t];
+}
+
+// (bucket key, insertion position) pairs: key = t * 2^k + (code_t & mask).
+__global__ void build_keys_kernel(const uint32_t* __restrict__ codes, int64_t n, int L, int k,
+                                  uint32_t* __restrict__ keys, uint32_t* __restrict__ pos) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= n * L) return;
+  const int t = (int)(q % L);
+  const uint32_t mask = (1u << k) - 1u;
+  keys[q] = ((uint32_t)t << k) | (codes[q] & mask);
+  pos[q] = (uint32_t)(q / L);
+}
+
+__global__ void seg_bounds_kernel(const uint32_t* __restrict__ skeys, int64_t m,
+                                  uint32_t* __restrict__ start, uint32_t* __restrict__ end) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= m) return;
+  const uint32_t key = skeys[j];
+  if (j == 0 || skeys[j - 1] != key) start[key] = (uint32_t)j;
+  if (j == m - 1 || skeys[j + 1] != key) end[key] = (uint32_t)(j + 1);
+}
+
+__device__ __forceinline__ uint64_t splitmix_mod(uint64_t seed, uint64_t bound) {
+  uint64_t z = seed + 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  z = z ^ (z >> 31);
+  return z % bound;
+}
+
+__global__ void apply_buckets_kernel(int nbuckets, int cap, int type,
+                                     const uint32_t* __restrict__ start,
+                                     const uint32_t* __restrict__ end,
+                                     const uint32_t* __restrict__ spos,
+                                     const uint32_t* __restrict__ ids, uint32_t* __restrict__ data,
+                                     uint32_t* __restrict__ len, uint64_t* __restrict__ count) {
+  const int key = blockIdx.x * blockDim.x + threadIdx.x;
+  if (key >= nbuckets) return;
+  const uint32_t s = start[key], e = end[key];
+  if (e <= s) return;
+  uint32_t* d = data + (size_t)key * cap;
+  uint32_t l = len[key];
+  if (type == KH_BUCKET_FIFO) {
+    const uint32_t m = e - s;
+    const uint32_t total = l + m;
+    const uint32_t keep = min(total, (uint32_t)cap);
+    const uint32_t drop = total - keep;
+    uint32_t o = 0;
+    for (uint32_t q = drop; q < l; ++q) d[o++] = d[q];
+    const uint32_t skip = drop > l ? drop - l : 0u;
+    for (uint32_t j = s + skip; j < e; ++j) d[o++] = ids[spos[j]];
+    len[key] = keep;
+  } else {
+    uint64_t c = count[key];
+    for (uint32_t j = s; j < e; ++j) {
+      const uint32_t id = ids[spos[j]];
+      c += 1;
+      if (l < (uint32_t)cap) {
+        d[l++] = id;
+      } else {
+        const uint64_t seed = c * 0x517cc1b727220a95ull + (uint64_t)id;
+        if (splitmix_mod(seed, c) < (uint64_t)cap) d[splitmix_mod(seed + 1, (uint64_t)cap)] = id;
+      }
+    }
+    len[key] = l;
+    count[key] = c;
+  }
+}
+
+__global__ void max_id_kernel(const uint32_t* __restrict__ ids, int64_t n, uint32_t* __restrict__ mx) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) atomicMax(mx, ids[i] + 1u);
+}
+
+__global__ void index_clear_kernel(uint32_t* __restrict__ len, uint64_t* __restrict__ count, int nb) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < nb) {
+    len[i] = 0u;
+    count[i] = 0ull;
+  }
+}
+
+// One block per query row: unique bucket ids in ascending order with counts.
+__global__ __launch_bounds__(kQueryThreads) void query_kernel(
+    const uint32_t* __restrict__ qcodes, int L, int k, int cap, const uint32_t* __restrict__ data,
+    const uint32_t* __restrict__ len, uint32_t id_bound, int stride, uint32_t* __restrict__ out_ids,
+    uint32_t* __restrict__ out_cnt, int32_t* __restrict__ out_len) {
+  extern __shared__ uint32_t sm[];
+  __shared__ int wsum[kQueryThreads / 64];
+  __shared__ int s_total;
+  __shared__ uint32_t bstart[65], bslot[64];
+  const int64_t row = blockIdx.x;
+  const uint32_t mask = (1u << k) - 1u;
+  uint32_t* oids = out_ids + row * (int64_t)stride;
+  uint32_t* ocnt = out_cnt ? out_cnt + row * (int64_t)stride : nullptr;
+  if (threadIdx.x == 0) {
+    uint32_t acc = 0;
+    for (int t = 0; t < L; ++t) {
+      const uint32_t slot = ((uint32_t)t << k) | (qcodes[row * L + t] & mask);
+      bslot[t] = slot;
+      bstart[t] = acc;
+      acc += len[slot];
+    }
+    bstart[L] = acc;
+  }
+  __syncthreads();
+  const uint32_t m = bstart[L];
+  if (id_bound <= (uint32_t)kDirectIds) {
+    for (uint32_t i = threadIdx.x; i < id_bound; i += blockDim.x) sm[i] = 0u;
+    __syncthreads();
+    for (int t = 0; t < L; ++t) {
+      const uint32_t n = bstart[t + 1] - bstart[t];
+      const uint32_t* bd = data + (size_t)bslot[t] * cap;
+      for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) atomicAdd(&sm[bd[j]], 1u);
+    }
+    __syncthreads();
+    int base = 0;
+    for (uint32_t c0 = 0; c0 < id_bound; c0 += blockDim.x) {
+      const uint32_t i = c0 + threadIdx.x;
+      const uint32_t c = i < id_bound ? sm[i] : 0u;
+      const int pos = block_excl_scan(c ? 1 : 0, wsum, &s_total) + base;
+      if (c) {
+        oids[pos] = i;
+        if (ocnt) ocnt[pos] = c;
+      }
+      base += s_total;
+    }
+    if (threadIdx.x == 0) out_len[row] = base;
+    return;
+  }
+  // Sort path: gather, bitonic sort ascending, count runs.
+  int P = 1;
+  while (P < (int)m) P <<= 1;
+  for (int t = 0; t < L; ++t) {
+    const uint32_t n = bstart[t + 1] - bstart[t];
+    const uint32_t* bd = data + (size_t)bslot[t] * cap;
+    for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) sm[bstart[t] + j] = bd[j];
+  }
+  for (int i = (int)m + threadIdx.x; i < P; i += blockDim.x) sm[i] = 0xffffffffu;
+  __syncthreads();
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int st = size >> 1; st > 0; st >>= 1) {
+      for (int i = threadIdx.x; i < P; i += blockDim.x) {
+        const int j = i ^ st;
+        if (j > i) {
+          const bool up = (i & size) == 0;
+          const uint32_t a = sm[i], c = sm[j];
+          if (up ? (a > c) : (a < c)) {
+            sm[i] = c;
+            sm[j] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  int base = 0;
+  for (int c0 = 0; c0 < (int)m; c0 += blockDim.x) {
+    const int i = c0 + threadIdx.x;
+    const bool head = i < (int)m && (i == 0 || sm[i] != sm[i - 1]);
+    const int pos = block_excl_scan(head ? 1 : 0, wsum, &s_total) + base;
+    if (head) {
+      int e = i + 1;
+      while (e < (int)m && sm[e] == sm[i]) ++e;
+      oids[pos] = sm[i];
+      if (ocnt) ocnt[pos] = (uint32_t)(e - i);
+    }
+    base += s_total;
+  }
+  if (threadIdx.x == 0) out_len[row] = base;
+}
+
+__global__ __launch_bounds__(1024) void csr_offsets_kernel(const int32_t* __restrict__ lens,
+                                                           int64_t batch, int64_t* __restrict__ off) {
+  __shared__ int wsum[16];
+  __shared__ int s_total;
+  int64_t base = 0;
+  for (int64_t c0 = 0; c0 < batch; c0 += blockDim.x) {
+    const int64_t i = c0 + threadIdx.x;
+    const int v = i < batch ? lens[i] : 0;
+    const int p = block_excl_scan(v, wsum, &s_total);
+    if (i < batch) off[i] = base + p;
+    base += s_total;
+  }
+  if (threadIdx.x == 0) off[batch] = base;
+}
+
+__global__ void csr_copy_u32_kernel(const uint32_t* __restrict__ src, int stride,
+                                    const int32_t* __restrict__ lens,
+                                    const int64_t* __restrict__ off, int64_t capacity,
+                                    uint32_t* __restrict__ dst) {
+  const int64_t row = blockIdx.y;
+  const int n = lens[row];
+  const int64_t o = off[row];
+  for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < n; j += gridDim.x * blockDim.x)
+    if (o + j < capacity) dst[o + j] = src[row * (int64_t)stride + j];
+}
+
+__global__ void csr_copy_f32_kernel(const float* __restrict__ src, int stride,
+                                    const int32_t* __restrict__ lens,
+                                    const int64_t* __restrict__ off, int64_t capacity,
+                                    float* __restrict__ dst) {
+  const int64_t row = blockIdx.y;
+  const int n = lens[row];
+  const int64_t o = off[row];
+  for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < n; j += gridDim.x * blockDim.x)
+    if (o + j < capacity) dst[o + j] = src[row * (int64_t)stride + j];
+}
+
+// ------------------------------------------------------------------ host helpers
+Scratch::~Scratch() { dev_free(p); }
+void* Scratch::get(size_t bytes) {
+  if (bytes <= cap) return p;
+  dev_free(p);
+  p = dev_alloc(bytes);
+  cap = p ? bytes : 0;
+  return p;
+}
+
+int hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx, int64_t batch,
+                      uint32_t* codes, hipStream_t st) {
+  if (batch == 0) return KH_OK;
+  const int in_lds = h->dim <= 12288 ? 1 : 0;
+  const size_t lds = sizeof(float) * (in_lds ? h->dim : 0) + sizeof(uint32_t) * h->L;
+  for (int64_t b0 = 0; b0 < batch; b0 += 65535 * 16) {
+    const int64_t nb = std::min<int64_t>(batch - b0, 65535 * 16);
+    hipLaunchKernelGGL(hash_dense_kernel, dim3((unsigned)nb), dim3(kHashThreads), lds, st,
+                       h->csr_off, h->csr_ent, h->k, h->L, h->dim, x + b0 * ldx, ldx, nb,
+                       codes + b0 * h->L, in_lds);
+    KH_LAUNCHED();
+  }
+  return KH_OK;
+}
+
+int hash_sparse_launch(const kh_hash_family* h, const int64_t* xoff, const uint32_t* xidx,
+                       const float* xval, int64_t batch, uint32_t* codes, hipStream_t st) {
+  if (batch == 0) return KH_OK;
+  KH_CHECK_ARG(h->L <= 256, "hash_sparse supports at most 256 tables");
+  hipLaunchKernelGGL(hash_sparse_kernel, dim3((unsigned)batch), dim3(kHashThreads), 0, st,
+                     h->planes_dev, h->k, h->L, h->dim, xoff, xidx, xval, codes);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
+int query_launch(const kh_lsh_index* idx, const uint32_t* qcodes, int64_t batch, uint32_t* qids,
+                 uint32_t* qcnt, int stride, int32_t* ulen, hipStream_t st) {
+  if (batch == 0) return KH_OK;
+  const uint32_t bound = idx->id_bound;
+  size_t lds;
+  if (bound <= (uint32_t)kDirectIds) {
+    lds = sizeof(uint32_t) * std::max<uint32_t>(bound, 1);
+  } else {
+    KH_CHECK_ARG(idx->L * idx->cap <= kMaxGather,
+                 "query over ids >= %d needs L*cap <= %d (got %d)", kDirectIds, kMaxGather,
+                 idx->L * idx->cap);
+    int P = 1;
+    while (P < idx->L * idx->cap) P <<= 1;
+    lds = sizeof(uint32_t) * P;
+  }
+  hipLaunchKernelGGL(query_kernel, dim3((unsigned)batch), dim3(kQueryThreads), lds, st, qcodes,
+                     idx->L, idx->k, idx->cap, idx->data, idx->len, bound, stride, qids, qcnt,
+                     ulen);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
+int query_stride(const kh_lsh_index* idx) {
+  const int64_t g = (int64_t)idx->L * idx->cap;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(g, std::max<uint32_t>(idx->id_bound, 1)));
+}
+
+int csr_finish(const uint32_t* qids, const uint32_t* qcnt, const float* f1, const float* f2,
+               int stride, const int32_t* ulen, int64_t batch, int64_t* off, uint32_t* ids,
+               uint32_t* cnts, float* o1, float* o2, int64_t capacity, hipStream_t st) {
+  hipLaunchKernelGGL(csr_offsets_kernel, dim3(1), dim3(1024), 0, st, ulen, batch, off);
+  KH_LAUNCHED();
+  dim3 g(std::max(1, std::min(64, ceil_div(stride, 256))), (unsigned)batch);
+  if (ids) hipLaunchKernelGGL(csr_copy_u32_kernel, g, dim3(256), 0, st, qids, stride, ulen, off, capacity, ids);
+  if (cnts && qcnt) hipLaunchKernelGGL(csr_copy_u32_kernel, g, dim3(256), 0, st, qcnt, stride, ulen, off, capacity, cnts);
+  if (o1 && f1) hipLaunchKernelGGL(csr_copy_f32_kernel, g, dim3(256), 0, st, f1, stride, ulen, off, capacity, o1);
+  if (o2 && f2) hipLaunchKernelGGL(csr_copy_f32_kernel, g, dim3(256), 0, st, f2, stride, ulen, off, capacity, o2);
+  KH_LAUNCHED();
+  int64_t total = 0;
+  KH_HIP(hipMemcpyAsync(&total, off + batch, sizeof(int64_t), hipMemcpyDeviceToHost, st));
+  KH_HIP(hipStreamSynchronize(st));
+  if (total > capacity) {
+    set_error("output needs %lld entries, capacity is %lld", (long long)total, (long long)capacity);
+    return KH_ERR_CAPACITY;
+  }
+  return KH_OK;
+}
+
+}  // namespace kh
+
+using namespace kh;
+
+// ====================================================================== families
+static int family_finish(kh_hash_family* h, kh_hash_family** out) {
+  const int P = h->L * h->k;
+  std::vector<int32_t> off(P + 1, 0);
+  std::vector<uint32_t> ent;
+  for (int p = 0; p < P; ++p) {
+    const int8_t* pl = h->planes_host.data() + (size_t)p * h->dim;
+    for (int d = 0; d < h->dim; ++d) {
+      if (pl[d] == 1) ent.push_back((uint32_t)d << 1);
+      else if (pl[d] == -1) ent.push_back(((uint32_t)d << 1) | 1u);
+    }
+    off[p + 1] = (int32_t)ent.size();
+  }
+  h->planes_dev = static_cast<int8_t*>(dev_alloc(h->planes_host.size()));
+  h->csr_off = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * off.size()));
+  h->csr_ent = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * std::max<size_t>(ent.size(), 1)));
+  if (!h->planes_dev || !h->csr_off || !h->csr_ent) {
+    kh_hash_family_destroy(h);
+    return KH_ERR_ALLOC;
+  }
+  if (hipMemcpy(h->planes_dev, h->planes_host.data(), h->planes_host.size(), hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(h->csr_off, off.data(), sizeof(int32_t) * off.size(), hipMemcpyHostToDevice) != hipSuccess ||
+      (ent.size() && hipMemcpy(h->csr_ent, ent.data(), sizeof(uint32_t) * ent.size(), hipMemcpyHostToDevice) != hipSuccess)) {
+    set_error("plane upload failed");
+    kh_hash_family_destroy(h);
+    return KH_ERR_HIP;
+  }
+  *out = h;
+  return KH_OK;
+}
+
+static int family_check(int input_dim, int k, int num_tables, kh_hash_family** out) {
+  KH_CHECK_ARG(out != nullptr, "null out");
+  KH_CHECK_ARG(input_dim > 0 && num_tables > 0 && num_tables <= 256,
+               "input_dim must be positive and num_tables in [1,256]");
+  KH_CHECK_ARG(k >= 1 && k <= 24, "k (%d) must be in [1,24] (2^k buckets per table)", k);
+  return KH_OK;
+}
+
+extern "C" int kh_simhash_create(int input_dim, int k, int num_tables, uint64_t seed,
+                                 kh_hash_family** out) {
+  int rc = family_check(input_dim, k, num_tables, out);
+  if (rc != KH_OK) return rc;
+  auto* h = new kh_hash_family();
+  h->dim = input_dim;
+  h->k = k;
+  h->L = num_tables;
+  h->planes_host.resize((size_t)num_tables * k * input_dim);
+  simhash_planes(input_dim, k, num_tables, seed, h->planes_host.data());
+  return family_finish(h, out);
+}
+
+extern "C" int kh_srp_create(int input_dim, int k, int num_tables, float sparsity, uint64_t seed,
+                             kh_hash_family** out) {
+  int rc = family_check(input_dim, k, num_tables, out);
+  if (rc != KH_OK) return rc;
+  KH_CHECK_ARG(sparsity >= 0.0f && sparsity <= 1.0f, "sparsity must be in [0, 1]");
+  auto* h = new kh_hash_family();
+  h->dim = input_dim;
+  h->k = k;
+  h->L = num_tables;
+  h->planes_host.resize((size_t)num_tables * k * input_dim);
+  srp_planes(input_dim, k, num_tables, sparsity, seed, h->planes_host.data());
+  return family_finish(h, out);
+}
+
+extern "C" int kh_hash_family_from_planes(int input_dim, int k, int num_tables,
+                                          const int8_t* planes_host, kh_hash_family** out) {
+  int rc = family_check(input_dim, k, num_tables, out);
+  if (rc != KH_OK) return rc;
+  KH_CHECK_ARG(planes_host != nullptr, "null planes");
+  const size_t n = (size_t)num_tables * k * input_dim;
+  for (size_t i = 0; i < n; ++i)
+    KH_CHECK_ARG(planes_host[i] >= -1 && planes_host[i] <= 1, "plane entry %zu not in {-1,0,1}", i);
+  auto* h = new kh_hash_family();
+  h->dim = input_dim;
+  h->k = k;
+  h->L = num_tables;
+  h->planes_host.assign(planes_host, planes_host + n);
+  return family_finish(h, out);
+}
+
+extern "C" int kh_hash_family_destroy(kh_hash_family* h) {
+  if (!h) return KH_OK;
+  dev_free(h->planes_dev);
+  dev_free(h->csr_off);
+  dev_free(h->csr_ent);
+  delete h;
+  return KH_OK;
+}
+
+extern "C" int kh_hash_family_dims(const kh_hash_family* h, int* k, int* input_dim,
+                                   int* num_tables) {
+  KH_CHECK_ARG(h != nullptr, "null family");
+  if (k) *k = h->k;
+  if (input_dim) *input_dim = h->dim;
+  if (num_tables) *num_tables = h->L;
+  return KH_OK;
+}
+
+extern "C" int kh_hash_family_planes(const kh_hash_family* h, int8_t* planes_host) {
+  KH_CHECK_ARG(h && planes_host, "null argument");
+  memcpy(planes_host, h->planes_host.data(), h->planes_host.size());
+  return KH_OK;
+}
+
+extern "C" int kh_hash_dense(const kh_hash_family* h, const float* x_dev, int64_t batch,
+                             uint32_t* codes_dev, void* stream) {
+  KH_CHECK_ARG(h && codes_dev && (x_dev || batch == 0), "null argument");
+  KH_CHECK_ARG(batch >= 0, "bad batch");
+  return hash_dense_launch(h, x_dev, h->dim, batch, codes_dev, as_stream(stream));
+}
+
+extern "C" int kh_hash_sparse(const kh_hash_family* h, const int64_t* off_dev,
+                              const uint32_t* idx_dev, const float* val_dev, int64_t batch,
+                              uint32_t* codes_dev, void* stream) {
+  KH_CHECK_ARG(h && off_dev && codes_dev, "null argument");
+  KH_CHECK_ARG(batch >= 0 && batch <= 0x7fffffff, "bad batch");
+  return hash_sparse_launch(h, off_dev, idx_dev, val_dev, batch, codes_dev, as_stream(stream));
+}
+
+// ====================================================================== index
+extern "C" int kh_lsh_index_create(const kh_hash_family* h, int bucket_type, int capacity,
+                                   kh_lsh_index** out) {
+  KH_CHECK_ARG(h && out, "null argument");
+  KH_CHECK_ARG(capacity > 0, "bucket capacity must be positive");
+  KH_CHECK_ARG(bucket_type == KH_BUCKET_FIFO || bucket_type == KH_BUCKET_RESERVOIR,
+               "bad bucket type %d", bucket_type);
+  *out = nullptr;
+  auto* idx = new kh_lsh_index();
+  idx->h = h;
+  idx->type = bucket_type;
+  idx->cap = capacity;
+  idx->L = h->L;
+  idx->k = h->k;
+  idx->nb = 1 << h->k;
+  const size_t nbk = (size_t)idx->L * idx->nb;
+  idx->data = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * nbk * capacity));
+  idx->len = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * nbk));
+  idx->count = static_cast<uint64_t*>(dev_alloc(sizeof(uint64_t) * nbk));
+  if (!idx->data || !idx->len || !idx->count) {
+    kh_lsh_index_destroy(idx);
+    return KH_ERR_ALLOC;
+  }
+  if (hipMemset(idx->len, 0, sizeof(uint32_t) * nbk) != hipSuccess ||
+      hipMemset(idx->count, 0, sizeof(uint64_t) * nbk) != hipSuccess ||
+      hipMemset(idx->data, 0, sizeof(uint32_t) * nbk * capacity) != hipSuccess) {
+    set_error("index init failed");
+    kh_lsh_index_destroy(idx);
+    return KH_ERR_HIP;
+  }
+  *out = idx;
+  return KH_OK;
+}
+
+extern "C" int kh_lsh_index_destroy(kh_lsh_index* idx) {
+  if (!idx) return KH_OK;
+  dev_free(idx->data);
+  dev_free(idx->len);
+  dev_free(idx->count);
+  delete idx;
+  return KH_OK;
+}
+
+extern "C" int kh_lsh_index_clear(kh_lsh_index* idx, void* stream) {
+  KH_CHECK_ARG(idx != nullptr, "null index");
+  const int nbk = idx->L * idx->nb;
+  hipLaunchKernelGGL(index_clear_kernel, dim3(ceil_div(nbk, 256)), dim3(256), 0,
+                     as_stream(stream), idx->len, idx->count, nbk);
+  KH_LAUNCHED();
+  idx->id_bound = 0;
+  return KH_OK;
+}
+
+extern "C" int kh_lsh_index_insert_codes(kh_lsh_index* idx, const uint32_t* ids_dev,
+                                         const uint32_t* codes_dev, int64_t n, void* stream) {
+  KH_CHECK_ARG(idx != nullptr, "null index");
+  KH_CHECK_ARG(n >= 0, "bad n");
+  if (n == 0) return KH_OK;
+  KH_CHECK_ARG(ids_dev && codes_dev, "null argument");
+  KH_CHECK_ARG(n * idx->L < (int64_t)0x7fffffff, "too many inserts in one call");
+  hipStream_t st = as_stream(stream);
+  const int64_t m = n * idx->L;
+  const int nbk = idx->L * idx->nb;
+  unsigned end_bit = 1;
+  while ((1ull << end_bit) < (unsigned long long)nbk) ++end_bit;
+  // scratch: keys, pos, sorted keys, sorted pos, start, end, max id
+  uint32_t *keys = nullptr, *pos = nullptr, *skeys = nullptr, *spos = nullptr, *start = nullptr,
+           *end = nullptr, *mx = nullptr;
+  void* tmp = nullptr;
+  size_t tmp_bytes = 0;
+  int rc = KH_OK;
+  keys = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * m));
+  pos = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * m));
+  skeys = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * m));
+  spos = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * m));
+  start = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * nbk));
+  end = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * nbk));
+  mx = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t)));
+  if (!keys || !pos || !skeys || !spos || !start || !end || !mx) rc = KH_ERR_ALLOC;
+  if (rc == KH_OK &&
+      rocprim::radix_sort_pairs(nullptr, tmp_bytes, keys, skeys, pos, spos, (unsigned)m, 0u,
+                                end_bit, st) != hipSuccess) {
+    set_error("radix sort sizing failed");
+    rc = KH_ERR_HIP;
+  }
+  if (rc == KH_OK) {
+    tmp = dev_alloc(tmp_bytes);
+    if (!tmp) rc = KH_ERR_ALLOC;
+  }
+  if (rc == KH_OK) {
+    hipLaunchKernelGGL(build_keys_kernel, dim3(ceil_div(m, 256)), dim3(256), 0, st, codes_dev, n,
+                       idx->L, idx->k, keys, pos);
+    if (rocprim::radix_sort_pairs(tmp, tmp_bytes, keys, skeys, pos, spos, (unsigned)m, 0u,
+                                  end_bit, st) != hipSuccess) {
+      set_error("radix sort failed");
+      rc = KH_ERR_HIP;
+    }
+  }
+  if (rc == KH_OK) {
+    (void)hipMemsetAsync(start, 0, sizeof(uint32_t) * nbk, st);
+    (void)hipMemsetAsync(end, 0, sizeof(uint32_t) * nbk, st);
+    (void)hipMemsetAsync(mx, 0, sizeof(uint32_t), st);
+    hipLaunchKernelGGL(seg_bounds_kernel, dim3(ceil_div(m, 256)), dim3(256), 0, st, skeys, m,
+                       start, end);
+    hipLaunchKernelGGL(apply_buckets_kernel, dim3(ceil_div(nbk, 64)), dim3(64), 0, st, nbk,
+                       idx->cap, idx->type, start, end, spos, ids_dev, idx->data, idx->len,
+                       idx->count);
+    hipLaunchKernelGGL(max_id_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, st, ids_dev, n, mx);
+    uint32_t bound = 0;
+    if (hipGetLastError() != hipSuccess ||
+        hipMemcpyAsync(&bound, mx, sizeof(uint32_t), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+      set_error("index build failed");
+      rc = KH_ERR_HIP;
+    } else {
+      idx->id_bound = std::max(idx->id_bound, bound);
+    }
+  }
+  dev_free(keys);
+  dev_free(pos);
+  dev_free(skeys);
+  dev_free(spos);
+  dev_free(start);
+  dev_free(end);
+  dev_free(mx);
+  dev_free(tmp);
+  return rc;
+}
+
+extern "C" int kh_lsh_index_insert(kh_lsh_index* idx, const uint32_t* ids_dev, const float* w_dev,
+                                   int64_t n, int64_t ldw, void* stream) {
+  KH_CHECK_ARG(idx != nullptr, "null index");
+  KH_CHECK_ARG(n >= 0 && ldw >= idx->h->dim, "bad n/ldw");
+  if (n == 0) return KH_OK;
+  KH_CHECK_ARG(ids_dev && w_dev, "null argument");
+  hipStream_t st = as_stream(stream);
+  uint32_t* codes = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * n * idx->L));
+  if (!codes) return KH_ERR_ALLOC;
+  int rc = hash_dense_launch(idx->h, w_dev, ldw, n, codes, st);
+  if (rc == KH_OK) rc = kh_lsh_index_insert_codes(idx, ids_dev, codes, n, stream);
+  dev_free(codes);
+  return rc;
+}
+
+static int query_common(const kh_lsh_index* idx, const uint32_t* qcodes, int64_t batch,
+                        int64_t* off, uint32_t* ids, uint32_t* counts, int64_t capacity,
+                        hipStream_t st) {
+  auto* mi = const_cast<kh_lsh_index*>(idx);
+  const int stride = query_stride(idx);
+  uint32_t* qids = static_cast<uint32_t*>(mi->q_ids.get(sizeof(uint32_t) * batch * stride));
+  uint32_t* qcnt = static_cast<uint32_t*>(mi->q_cnt.get(sizeof(uint32_t) * batch * stride));
+  int32_t* ulen = static_cast<int32_t*>(mi->q_len.get(sizeof(int32_t) * batch));
+  if (!qids || !qcnt || !ulen) return KH_ERR_ALLOC;
+  int rc = query_launch(idx, qcodes, batch, qids, counts ? qcnt : nullptr, stride, ulen, st);
+  if (rc != KH_OK) return rc;
+  return csr_finish(qids, qcnt, nullptr, nullptr, stride, ulen, batch, off, ids, counts, nullptr,
+                    nullptr, capacity, st);
+}
+
+extern "C" int kh_lsh_index_query(const kh_lsh_index* idx, const float* x_dev, int64_t batch,
+                                  int64_t* off_dev, uint32_t* ids_dev, uint32_t* counts_dev,
+                                  int64_t capacity, void* stream) {
+  KH_CHECK_ARG(idx && off_dev && ids_dev, "null argument");
+  KH_CHECK_ARG(batch >= 0 && batch <= 0x7fffffff && capacity >= 0, "bad batch/capacity");
+  hipStream_t st = as_stream(stream);
+  if (batch == 0) {
+    KH_HIP(hipMemsetAsync(off_dev, 0, sizeof(int64_t), st));
+    return KH_OK;
+  }
+  KH_CHECK_ARG(x_dev != nullptr, "null input");
+  auto* mi = const_cast<kh_lsh_index*>(idx);
+  uint32_t* qcodes = static_cast<uint32_t*>(mi->q_codes.get(sizeof(uint32_t) * batch * idx->L));
+  if (!qcodes) return KH_ERR_ALLOC;
+  int rc = hash_dense_launch(idx->h, x_dev, idx->h->dim, batch, qcodes, st);
+  if (rc != KH_OK) return rc;
+  return query_common(idx, qcodes, batch, off_dev, ids_dev, counts_dev, capacity, st);
+}
+
+extern "C" int kh_lsh_index_query_sparse(const kh_lsh_index* idx, const int64_t* xoff_dev,
+                                         const uint32_t* xidx_dev, const float* xval_dev,
+                                         int64_t batch, int64_t* off_dev, uint32_t* ids_dev,
+                                         uint32_t* counts_dev, int64_t capacity, void* stream) {
+  KH_CHECK_ARG(idx && off_dev && ids_dev && xoff_dev, "null argument");
+  KH_CHECK_ARG(batch >= 0 && batch <= 0x7fffffff && capacity >= 0, "bad batch/capacity");
+  hipStream_t st = as_stream(stream);
+  if (batch == 0) {
+    KH_HIP(hipMemsetAsync(off_dev, 0, sizeof(int64_t), st));
+    return KH_OK;
+  }
+  auto* mi = const_cast<kh_lsh_index*>(idx);
+  uint32_t* qcodes = static_cast<uint32_t*>(mi->q_codes.get(sizeof(uint32_t) * batch * idx->L));
+  if (!qcodes) return KH_ERR_ALLOC;
+  int rc = hash_sparse_launch(idx->h, xoff_dev, xidx_dev, xval_dev, batch, qcodes, st);
+  if (rc != KH_OK) return rc;
+  return query_common(idx, qcodes, batch, off_dev, ids_dev, counts_dev, capacity, st);
+}
+
+extern "C" int kh_lsh_index_buckets(const kh_lsh_index* idx, uint32_t* data_host,
+                                    uint32_t* len_host, uint64_t* count_host) {
+  KH_CHECK_ARG(idx != nullptr, "null index");
+  const size_t nbk = (size_t)idx->L * idx->nb;
+  KH_HIP(hipDeviceSynchronize());
+  if (data_host)
+    KH_HIP(hipMemcpy(data_host, idx->data, sizeof(uint32_t) * nbk * idx->cap, hipMemcpyDeviceToHost));
+  if (len_host) KH_HIP(hipMemcpy(len_host, idx->len, sizeof(uint32_t) * nbk, hipMemcpyDeviceToHost));
+  if (count_host)
+    KH_HIP(hipMemcpy(count_host, idx->count, sizeof(uint64_t) * nbk, hipMemcpyDeviceToHost));
+  return KH_OK;
+}

@@ -1,0 +1,53 @@
+// lsh_internal.hpp -- handle layouts shared by lsh.hip and slide.hip.
+#pragma once
+#include <vector>
+
+#include "common.hpp"
+
+namespace kh {
+
+// Grow-only device buffer owned by a handle.
+struct Scratch {
+  void* p = nullptr;
+  size_t cap = 0;
+  ~Scratch();
+  void* get(size_t bytes);
+};
+
+}  // namespace kh
+
+struct kh_hash_family {
+  int dim = 0, k = 0, L = 0;
+  std::vector<int8_t> planes_host;  // [L][k][dim]
+  int8_t* planes_dev = nullptr;     // [L*k][dim]
+  int32_t* csr_off = nullptr;       // [L*k + 1] nonzero lists per plane
+  uint32_t* csr_ent = nullptr;      // (dim << 1) | (sign < 0)
+};
+
+struct kh_lsh_index {
+  const kh_hash_family* h = nullptr;
+  int type = 0, cap = 0, L = 0, k = 0, nb = 0;
+  uint32_t* data = nullptr;   // [L][nb][cap]
+  uint32_t* len = nullptr;    // [L][nb]
+  uint64_t* count = nullptr;  // [L][nb]
+  uint32_t id_bound = 0;      // 1 + largest id inserted so far
+  kh::Scratch q_codes, q_ids, q_cnt, q_len;
+};
+
+namespace kh {
+
+int hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx, int64_t batch,
+                      uint32_t* codes, hipStream_t st);
+int hash_sparse_launch(const kh_hash_family* h, const int64_t* xoff, const uint32_t* xidx,
+                       const float* xval, int64_t batch, uint32_t* codes, hipStream_t st);
+// Per-row unique ids (ascending) and hit counts into [batch][stride] buffers.
+int query_launch(const kh_lsh_index* idx, const uint32_t* qcodes, int64_t batch, uint32_t* qids,
+                 uint32_t* qcnt, int stride, int32_t* ulen, hipStream_t st);
+int query_stride(const kh_lsh_index* idx);
+// Row lengths -> CSR offsets, copies of up to four per-row arrays, then a
+// synchronising capacity check.
+int csr_finish(const uint32_t* qids, const uint32_t* qcnt, const float* f1, const float* f2,
+               int stride, const int32_t* ulen, int64_t batch, int64_t* off, uint32_t* ids,
+               uint32_t* cnts, float* o1, float* o2, int64_t capacity, hipStream_t st);
+
+}  // namespace kh

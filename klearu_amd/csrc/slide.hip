@@ -1,0 +1,465 @@
+// slide.hip -- SLIDE sparse layer forward on the GPU (gfx950).
+//
+// Replaces Layer::forward (crates/klearu-core/src/network/layer.rs:65-120) with
+// Neuron::forward / forward_sparse (network/neuron.rs:47-68), the sampling
+// strategies (sampling/{vanilla,topk,threshold}.rs) and the activations
+// (layer.rs:250-308); plus a dense layer over sparse inputs (every neuron,
+// Neuron::forward_sparse) for the hidden layer of the extreme-classification net.
+//
+// Per batch: hash (lsh.hip) -> query (unique ids + hit counts, ascending) ->
+// select_kernel (sampling, empty -> all neurons, ids < n) -> neuron_kernel
+// (one block per sample; each thread replays the reference's sequential f32
+// sum for one active neuron over the sample's nonzero inputs, then the
+// activation; softmax reduces over the block) -> CSR.
+//
+// Skipping zero inputs leaves a sequential sum unchanged (adding +-0 to a
+// nonzero partial sum returns it; a zero partial sum only changes the sign of
+// zero), so pre-activations are bit-identical to the reference's dense loop.
+#include <algorithm>
+#include <vector>
+
+#include "lsh_internal.hpp"
+
+namespace kh {
+
+constexpr int kSlideThreads = 256;
+constexpr int kMaxCountBins = 8193;
+
+__global__ __launch_bounds__(kSlideThreads) void select_kernel(
+    const uint32_t* __restrict__ qids, const uint32_t* __restrict__ qcnt,
+    const int32_t* __restrict__ qlen, int qstride, int sampling, int top_k, int threshold,
+    int num_neurons, int nbins, uint32_t* __restrict__ aids, int astride,
+    int32_t* __restrict__ alen) {
+  extern __shared__ unsigned hist[];
+  __shared__ int wsum[kSlideThreads / 64];
+  __shared__ int s_total;
+  __shared__ int s_cstar, s_take, s_best_c, s_best_id;
+  const int64_t row = blockIdx.x;
+  const uint32_t* ids = qids + row * (int64_t)qstride;
+  const uint32_t* cnt = qcnt + row * (int64_t)qstride;
+  uint32_t* out = aids + row * (int64_t)astride;
+  const int m = qlen[row];
+  int cstar = 0, take_eq = 0;  // topk: take count > cstar, plus take_eq of count == cstar
+  int mode = sampling;
+  if (sampling == KH_SAMPLING_TOPK) {
+    if (m <= top_k) {
+      mode = KH_SAMPLING_VANILLA;
+    } else {
+      for (int i = threadIdx.x; i < nbins; i += blockDim.x) hist[i] = 0u;
+      __syncthreads();
+      for (int i = threadIdx.x; i < m; i += blockDim.x) atomicAdd(&hist[min(cnt[i], (uint32_t)nbins - 1)], 1u);
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        int above = 0, c = nbins - 1;
+        for (; c > 0; --c) {
+          if (above + (int)hist[c] >= top_k) break;
+          above += hist[c];
+        }
+        s_cstar = c;
+        s_take = top_k - above;
+      }
+      __syncthreads();
+      cstar = s_cstar;
+      take_eq = s_take;
+    }
+  }
+  int n_sel = 0;
+  if (mode == KH_SAMPLING_THRESHOLD) {
+    int any = 0;
+    int base = 0;
+    for (int c0 = 0; c0 < m; c0 += blockDim.x) {
+      const int i = c0 + threadIdx.x;
+      const int sel = (i < m && (int)cnt[i] >= threshold) ? 1 : 0;
+      const int id = i < m ? (int)ids[i] : 0;
+      const int keep = sel && id < num_neurons;
+      const int pos = block_excl_scan(keep, wsum, &s_total) + base;
+      if (keep) out[pos] = (uint32_t)id;
+      base += s_total;
+      any |= 0;
+    }
+    n_sel = base;
+    if (m > 0) {
+      // none passing -> the single best (highest count, lowest id), when none passed at all
+      int passed = 0;
+      {
+        int b2 = 0;
+        for (int c0 = 0; c0 < m; c0 += blockDim.x) {
+          const int i = c0 + threadIdx.x;
+          const int sel = (i < m && (int)cnt[i] >= threshold) ? 1 : 0;
+          block_excl_scan(sel, wsum, &s_total);
+          b2 += s_total;
+        }
+        passed = b2;
+      }
+      if (passed == 0) {
+        if (threadIdx.x == 0) {
+          int bc = -1, bi = 0;
+          for (int i = 0; i < m; ++i)
+            if ((int)cnt[i] > bc) {  // ids ascending: first max has the lowest id
+              bc = (int)cnt[i];
+              bi = (int)ids[i];
+            }
+          s_best_id = bi;
+        }
+        __syncthreads();
+        n_sel = 0;
+        if (s_best_id < num_neurons) {
+          if (threadIdx.x == 0) out[0] = (uint32_t)s_best_id;
+          n_sel = 1;
+        }
+      }
+    }
+  } else {
+    int base = 0, base_eq = 0;
+    for (int c0 = 0; c0 < m; c0 += blockDim.x) {
+      const int i = c0 + threadIdx.x;
+      int sel = i < m ? 1 : 0;
+      if (mode == KH_SAMPLING_TOPK) {
+        const int c = i < m ? (int)min(cnt[i], (uint32_t)nbins - 1) : 0;
+        const int eq = (i < m && c == cstar) ? 1 : 0;
+        const int r = block_excl_scan(eq, wsum, &s_total) + base_eq;
+        base_eq += s_total;
+        sel = (i < m) && (c > cstar || (eq && r < take_eq));
+      }
+      const int id = i < m ? (int)ids[i] : 0;
+      const int keep = sel && id < num_neurons;
+      const int pos = block_excl_scan(keep, wsum, &s_total) + base;
+      if (keep) out[pos] = (uint32_t)id;
+      base += s_total;
+    }
+    n_sel = base;
+  }
+  // empty selection -> every neuron (layer.rs:82-84)
+  if (n_sel == 0 && !(mode == KH_SAMPLING_THRESHOLD && m > 0 && false)) {
+    for (int i = threadIdx.x; i < num_neurons; i += blockDim.x) out[i] = (uint32_t)i;
+    n_sel = num_neurons;
+  }
+  if (threadIdx.x == 0) alen[row] = n_sel;
+}
+
+// One block per sample.  x is either dense [batch][dim] (zeros skipped) or CSR.
+template <bool SPARSE>
+__global__ __launch_bounds__(kSlideThreads) void neuron_kernel(
+    const float* __restrict__ W, const float* __restrict__ bias, int dim,
+    const float* __restrict__ x, const int64_t* __restrict__ xoff,
+    const uint32_t* __restrict__ xidx, const float* __restrict__ xval,
+    const uint32_t* __restrict__ aids, int astride, const int32_t* __restrict__ alen, int act,
+    int max_nz, float* __restrict__ pre, float* __restrict__ post) {
+  extern __shared__ unsigned char smem[];
+  uint32_t* nzi = reinterpret_cast<uint32_t*>(smem);
+  float* nzv = reinterpret_cast<float*>(smem + sizeof(uint32_t) * max_nz);
+  __shared__ int wsum[kSlideThreads / 64];
+  __shared__ int s_total;
+  __shared__ float red[kSlideThreads / 64];
+  const int64_t row = blockIdx.x;
+  int nnz;
+  const uint32_t* li;
+  const float* lv;
+  if (SPARSE) {
+    const int64_t a = xoff[row];
+    nnz = (int)(xoff[row + 1] - a);
+    if (nnz <= max_nz) {
+      for (int i = threadIdx.x; i < nnz; i += blockDim.x) {
+        nzi[i] = xidx[a + i];
+        nzv[i] = xval[a + i];
+      }
+      __syncthreads();
+      li = nzi;
+      lv = nzv;
+    } else {
+      li = xidx + a;
+      lv = xval + a;
+    }
+  } else {
+    const float* xr = x + row * (int64_t)dim;
+    int base = 0;
+    for (int c0 = 0; c0 < dim; c0 += blockDim.x) {
+      const int d = c0 + threadIdx.x;
+      const float v = d < dim ? xr[d] : 0.0f;
+      const int nz = v != 0.0f ? 1 : 0;
+      const int pos = block_excl_scan(nz, wsum, &s_total) + base;
+      if (nz) {
+        nzi[pos] = (uint32_t)d;
+        nzv[pos] = v;
+      }
+      base += s_total;
+    }
+    nnz = base;
+    __syncthreads();
+    li = nzi;
+    lv = nzv;
+  }
+  const int n = alen[row];
+  const uint32_t* ids = aids + row * (int64_t)astride;
+  float* prow = pre + row * (int64_t)astride;
+  float* orow = post + row * (int64_t)astride;
+  float lmax = -INFINITY;
+  for (int a = threadIdx.x; a < n; a += blockDim.x) {
+    const uint32_t id = ids[a];
+    const float* w = W + (size_t)id * dim;
+    float s = -0.0f;
+    for (int e = 0; e < nnz; ++e) s = __fadd_rn(s, __fmul_rn(w[li[e]], lv[e]));
+    const float z = __fadd_rn(s, bias[id]);
+    prow[a] = z;
+    lmax = fmaxf(lmax, z);
+  }
+  if (act != KH_ACT_SOFTMAX) {
+    for (int a = threadIdx.x; a < n; a += blockDim.x) {
+      const float z = prow[a];
+      float r;
+      if (act == KH_ACT_RELU) r = fmaxf(z, 0.0f);
+      else if (act == KH_ACT_SIGMOID) r = sigmoid_ref(z);
+      else if (act == KH_ACT_TANH) r = tanhf(z);
+      else r = z;
+      orow[a] = r;
+    }
+    return;
+  }
+  // softmax over the active set (layer.rs:286-308)
+  lmax = wave_max(lmax);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = lmax;
+  __syncthreads();
+  float mx = red[0];
+  for (int i = 1; i < (int)(blockDim.x >> 6); ++i) mx = fmaxf(mx, red[i]);
+  __syncthreads();
+  float ls = 0.0f;
+  for (int a = threadIdx.x; a < n; a += blockDim.x) {
+    const float e = expf(prow[a] - mx);
+    orow[a] = e;
+    ls += e;
+  }
+  ls = wave_sum(ls);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ls;
+  __syncthreads();
+  float tot = 0.0f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) tot += red[i];
+  if (tot > 0.0f) {
+    for (int a = threadIdx.x; a < n; a += blockDim.x) orow[a] = orow[a] / tot;
+  } else {
+    const float u = 1.0f / (float)n;
+    for (int a = threadIdx.x; a < n; a += blockDim.x) orow[a] = u;
+  }
+}
+
+// Dense layer over CSR inputs: y[b][o] = act(sum_e val_e * W^T[idx_e][o] + bias[o]).
+__global__ __launch_bounds__(256) void dense_sparse_kernel(const float* __restrict__ WT, int n,
+                                                           const float* __restrict__ bias,
+                                                           const int64_t* __restrict__ xoff,
+                                                           const uint32_t* __restrict__ xidx,
+                                                           const float* __restrict__ xval,
+                                                           int act, float* __restrict__ y) {
+  const int64_t row = blockIdx.y;
+  const int o = blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= n) return;
+  const int64_t a = xoff[row], b = xoff[row + 1];
+  float s = -0.0f;
+  for (int64_t e = a; e < b; ++e) s = __fadd_rn(s, __fmul_rn(xval[e], WT[(size_t)xidx[e] * n + o]));
+  const float z = __fadd_rn(s, bias[o]);
+  float r;
+  if (act == KH_ACT_RELU) r = fmaxf(z, 0.0f);
+  else if (act == KH_ACT_SIGMOID) r = sigmoid_ref(z);
+  else if (act == KH_ACT_TANH) r = tanhf(z);
+  else r = z;
+  y[row * (int64_t)n + o] = r;
+}
+
+}  // namespace kh
+
+using namespace kh;
+
+struct kh_slide_layer {
+  int dim = 0, n = 0;
+  float* w = nullptr;
+  float* bias = nullptr;
+  kh_lsh_index* index = nullptr;
+  int sampling = 0, top_k = 0, threshold = 0, act = 0;
+  Scratch codes, qids, qcnt, qlen, aids, alen, pre, post;
+};
+
+struct kh_dense_layer {
+  int dim = 0, n = 0, act = 0;
+  float* wt = nullptr;  // [dim][n]
+  float* bias = nullptr;
+};
+
+extern "C" int kh_slide_layer_create(int input_dim, int num_neurons, const float* w_host,
+                                     const float* bias_host, kh_lsh_index* index, int sampling,
+                                     int top_k, int threshold, int activation,
+                                     kh_slide_layer** out) {
+  KH_CHECK_ARG(out && w_host && bias_host && index, "null argument");
+  KH_CHECK_ARG(input_dim > 0 && num_neurons > 0, "dims must be positive");
+  KH_CHECK_ARG(index->h->dim == input_dim, "index input_dim %d != layer input_dim %d",
+               index->h->dim, input_dim);
+  KH_CHECK_ARG(sampling >= 0 && sampling <= 2 && activation >= 0 && activation <= 4,
+               "bad sampling / activation");
+  KH_CHECK_ARG(top_k >= 0 && threshold >= 0, "bad top_k / threshold");
+  *out = nullptr;
+  auto* l = new kh_slide_layer();
+  l->dim = input_dim;
+  l->n = num_neurons;
+  l->index = index;
+  l->sampling = sampling;
+  l->top_k = top_k;
+  l->threshold = threshold;
+  l->act = activation;
+  const size_t nw = (size_t)input_dim * num_neurons;
+  l->w = static_cast<float*>(dev_alloc(sizeof(float) * nw));
+  l->bias = static_cast<float*>(dev_alloc(sizeof(float) * num_neurons));
+  uint32_t* ids = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * num_neurons));
+  int rc = (l->w && l->bias && ids) ? KH_OK : KH_ERR_ALLOC;
+  if (rc == KH_OK) {
+    std::vector<uint32_t> h(num_neurons);
+    for (int i = 0; i < num_neurons; ++i) h[i] = (uint32_t)i;
+    if (hipMemcpy(l->w, w_host, sizeof(float) * nw, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(l->bias, bias_host, sizeof(float) * num_neurons, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(ids, h.data(), sizeof(uint32_t) * num_neurons, hipMemcpyHostToDevice) != hipSuccess) {
+      set_error("layer upload failed");
+      rc = KH_ERR_HIP;
+    }
+  }
+  // Layer::new inserts neurons 0..n-1 in order (layer.rs:42-44).
+  if (rc == KH_OK) rc = kh_lsh_index_insert(index, ids, l->w, num_neurons, input_dim, nullptr);
+  dev_free(ids);
+  if (rc != KH_OK) {
+    kh_slide_layer_destroy(l);
+    return rc;
+  }
+  *out = l;
+  return KH_OK;
+}
+
+extern "C" int kh_slide_layer_destroy(kh_slide_layer* l) {
+  if (!l) return KH_OK;
+  dev_free(l->w);
+  dev_free(l->bias);
+  delete l;
+  return KH_OK;
+}
+
+static int slide_forward_common(const kh_slide_layer* lc, const float* x, const int64_t* xoff,
+                                const uint32_t* xidx, const float* xval, int64_t batch,
+                                int64_t* off, uint32_t* act_ids, float* pre_out, float* act_out,
+                                int64_t capacity, hipStream_t st) {
+  auto* l = const_cast<kh_slide_layer*>(lc);
+  const kh_lsh_index* idx = l->index;
+  const int L = idx->L;
+  uint32_t* codes = static_cast<uint32_t*>(l->codes.get(sizeof(uint32_t) * batch * L));
+  const int qs = query_stride(idx);
+  uint32_t* qids = static_cast<uint32_t*>(l->qids.get(sizeof(uint32_t) * batch * qs));
+  uint32_t* qcnt = static_cast<uint32_t*>(l->qcnt.get(sizeof(uint32_t) * batch * qs));
+  int32_t* qlen = static_cast<int32_t*>(l->qlen.get(sizeof(int32_t) * batch));
+  const int as = std::max(qs, l->n);
+  uint32_t* aids = static_cast<uint32_t*>(l->aids.get(sizeof(uint32_t) * batch * as));
+  int32_t* alen = static_cast<int32_t*>(l->alen.get(sizeof(int32_t) * batch));
+  float* pre = static_cast<float*>(l->pre.get(sizeof(float) * batch * as));
+  float* post = static_cast<float*>(l->post.get(sizeof(float) * batch * as));
+  if (!codes || !qids || !qcnt || !qlen || !aids || !alen || !pre || !post) return KH_ERR_ALLOC;
+  int rc = xoff ? hash_sparse_launch(idx->h, xoff, xidx, xval, batch, codes, st)
+                : hash_dense_launch(idx->h, x, l->dim, batch, codes, st);
+  if (rc != KH_OK) return rc;
+  rc = query_launch(idx, codes, batch, qids, qcnt, qs, qlen, st);
+  if (rc != KH_OK) return rc;
+  const int nbins = std::min(kMaxCountBins, L * idx->cap + 1);
+  hipLaunchKernelGGL(select_kernel, dim3((unsigned)batch), dim3(kSlideThreads),
+                     sizeof(unsigned) * nbins, st, qids, qcnt, qlen, qs, l->sampling, l->top_k,
+                     l->threshold, l->n, nbins, aids, as, alen);
+  KH_LAUNCHED();
+  const int max_nz = xoff ? 4096 : l->dim;
+  KH_CHECK_ARG(xoff || l->dim <= 8192, "dense SLIDE input supports input_dim <= 8192");
+  const size_t lds = (sizeof(uint32_t) + sizeof(float)) * max_nz;
+  if (xoff)
+    hipLaunchKernelGGL(neuron_kernel<true>, dim3((unsigned)batch), dim3(kSlideThreads), lds, st,
+                       l->w, l->bias, l->dim, nullptr, xoff, xidx, xval, aids, as, alen, l->act,
+                       max_nz, pre, post);
+  else
+    hipLaunchKernelGGL(neuron_kernel<false>, dim3((unsigned)batch), dim3(kSlideThreads), lds, st,
+                       l->w, l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, alen, l->act,
+                       max_nz, pre, post);
+  KH_LAUNCHED();
+  return csr_finish(aids, nullptr, pre, post, as, alen, batch, off, act_ids, nullptr, pre_out,
+                    act_out, capacity, st);
+}
+
+extern "C" int kh_slide_layer_forward(const kh_slide_layer* l, const float* x_dev, int64_t batch,
+                                      int64_t* off_dev, uint32_t* act_ids_dev, float* pre_dev,
+                                      float* act_dev, int64_t capacity, void* stream) {
+  KH_CHECK_ARG(l && off_dev && act_ids_dev, "null argument");
+  KH_CHECK_ARG(batch >= 0 && batch <= 0x7fffffff && capacity >= 0, "bad batch/capacity");
+  hipStream_t st = as_stream(stream);
+  if (batch == 0) {
+    KH_HIP(hipMemsetAsync(off_dev, 0, sizeof(int64_t), st));
+    return KH_OK;
+  }
+  KH_CHECK_ARG(x_dev != nullptr, "null input");
+  return slide_forward_common(l, x_dev, nullptr, nullptr, nullptr, batch, off_dev, act_ids_dev,
+                              pre_dev, act_dev, capacity, st);
+}
+
+extern "C" int kh_slide_layer_forward_sparse(const kh_slide_layer* l, const int64_t* xoff_dev,
+                                             const uint32_t* xidx_dev, const float* xval_dev,
+                                             int64_t batch, int64_t* off_dev,
+                                             uint32_t* act_ids_dev, float* pre_dev, float* act_dev,
+                                             int64_t capacity, void* stream) {
+  KH_CHECK_ARG(l && off_dev && act_ids_dev && xoff_dev, "null argument");
+  KH_CHECK_ARG(batch >= 0 && batch <= 0x7fffffff && capacity >= 0, "bad batch/capacity");
+  hipStream_t st = as_stream(stream);
+  if (batch == 0) {
+    KH_HIP(hipMemsetAsync(off_dev, 0, sizeof(int64_t), st));
+    return KH_OK;
+  }
+  return slide_forward_common(l, nullptr, xoff_dev, xidx_dev, xval_dev, batch, off_dev,
+                              act_ids_dev, pre_dev, act_dev, capacity, st);
+}
+
+extern "C" int kh_dense_layer_create(int input_dim, int num_neurons, const float* w_host,
+                                     const float* bias_host, int activation,
+                                     kh_dense_layer** out) {
+  KH_CHECK_ARG(out && w_host && bias_host, "null argument");
+  KH_CHECK_ARG(input_dim > 0 && num_neurons > 0 && activation >= 0 && activation <= 4 &&
+                   activation != KH_ACT_SOFTMAX,
+               "bad dims / activation (softmax is not supported on a dense layer)");
+  *out = nullptr;
+  auto* l = new kh_dense_layer();
+  l->dim = input_dim;
+  l->n = num_neurons;
+  l->act = activation;
+  const size_t nw = (size_t)input_dim * num_neurons;
+  std::vector<float> wt(nw);
+  for (int o = 0; o < num_neurons; ++o)
+    for (int d = 0; d < input_dim; ++d) wt[(size_t)d * num_neurons + o] = w_host[(size_t)o * input_dim + d];
+  l->wt = static_cast<float*>(dev_alloc(sizeof(float) * nw));
+  l->bias = static_cast<float*>(dev_alloc(sizeof(float) * num_neurons));
+  if (!l->wt || !l->bias) {
+    kh_dense_layer_destroy(l);
+    return KH_ERR_ALLOC;
+  }
+  if (hipMemcpy(l->wt, wt.data(), sizeof(float) * nw, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(l->bias, bias_host, sizeof(float) * num_neurons, hipMemcpyHostToDevice) != hipSuccess) {
+    set_error("dense layer upload failed");
+    kh_dense_layer_destroy(l);
+    return KH_ERR_HIP;
+  }
+  *out = l;
+  return KH_OK;
+}
+
+extern "C" int kh_dense_layer_destroy(kh_dense_layer* l) {
+  if (!l) return KH_OK;
+  dev_free(l->wt);
+  dev_free(l->bias);
+  delete l;
+  return KH_OK;
+}
+
+extern "C" int kh_dense_layer_forward_sparse(const kh_dense_layer* l, const int64_t* xoff_dev,
+                                             const uint32_t* xidx_dev, const float* xval_dev,
+                                             int64_t batch, float* y_dev, void* stream) {
+  KH_CHECK_ARG(l && xoff_dev && y_dev, "null argument");
+  KH_CHECK_ARG(batch >= 0 && batch <= 65535, "bad batch");
+  if (batch == 0) return KH_OK;
+  hipLaunchKernelGGL(dense_sparse_kernel, dim3(ceil_div(l->n, 256), (unsigned)batch), dim3(256), 0,
+                     as_stream(stream), l->wt, l->n, l->bias, xoff_dev, xidx_dev, xval_dev, l->act,
+                     y_dev);
+  KH_LAUNCHED();
+  return KH_OK;
+}

@@ -1,0 +1,172 @@
+"""GPU parity: Deja Vu predictor, top-k, union and sparse SwiGLU FFN vs the oracle.
+
+Bars (north_star): selections bit-exact; BF16-weight outputs within 2e-3
+relative (max-abs printed).  Shapes are the BASELINE configs (1.1B: H2048 I5632
+k564, predictor 2048->128->5632; 7B: H4096 I11008 k1652, rank 256; heads
+4096->128->32 k16) plus small edge cases.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 2e-3
+
+
+def bf16(orc, a):
+    return orc.bf16_from_f32(np.asarray(a, np.float32))
+
+
+def make_predictor(orc, rng, ind, hid, out, bias=False):
+    w1 = bf16(orc, rng.normal(0, 0.02, (hid, ind)))
+    w2 = bf16(orc, rng.normal(0, 0.02 if hid > 64 else 0.1, (out, hid)))
+    b1 = (rng.normal(0, 0.1, hid) if bias else np.zeros(hid)).astype(np.float32)
+    b2 = (rng.normal(0, 0.1, out) if bias else np.zeros(out)).astype(np.float32)
+    return w1, b1, w2, b2
+
+
+@pytest.mark.parametrize("ind,hid,out,batch,bias", [
+    (2048, 128, 5632, 1, False),   # cfg2 neuron predictor
+    (4096, 256, 11008, 1, False),  # cfg3 neuron predictor
+    (4096, 256, 11008, 16, False),  # cfg3 batch 16
+    (4096, 128, 32, 8, False),     # cfg4 head predictor
+    (100, 13, 77, 3, True),        # ragged shapes, biases
+])
+def test_predictor_scores_bit_exact(kh, orc, ind, hid, out, batch, bias):
+    from klearu_amd.dejavu import SparsityPredictor
+    rng = np.random.default_rng(ind + hid + out + batch)
+    w1, b1, w2, b2 = make_predictor(orc, rng, ind, hid, out, bias)
+    p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
+    x = rng.standard_normal((batch, ind)).astype(np.float32)
+    got = p.predict(torch.from_numpy(x).cuda()).cpu().numpy()
+    for b in range(batch):
+        ref, _ = orc.predictor_predict(w1, b1, w2, b2, x[b])
+        np.testing.assert_array_equal(got[b].view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("ind,hid,out,k,batch", [
+    (2048, 128, 5632, 564, 1), (4096, 256, 11008, 1652, 1), (4096, 256, 11008, 1652, 4),
+    (4096, 128, 32, 16, 8), (64, 32, 12, 5, 1), (64, 32, 12, 20, 1)])
+def test_select_top_k_bit_exact(kh, orc, ind, hid, out, k, batch):
+    from klearu_amd.dejavu import ORDER_ASCENDING, SparsityPredictor
+    rng = np.random.default_rng(k + batch)
+    w1, b1, w2, b2 = make_predictor(orc, rng, ind, hid, out)
+    p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
+    x = rng.standard_normal((batch, ind)).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    got = p.select_top_k(xd, k).cpu().numpy()
+    got_asc = p.select_top_k(xd, k, ORDER_ASCENDING).cpu().numpy()
+    for b in range(batch):
+        s, _ = orc.predictor_predict(w1, b1, w2, b2, x[b])
+        ref = orc.select_top_k(s, k)
+        np.testing.assert_array_equal(got[b], ref)
+        np.testing.assert_array_equal(got_asc[b], np.sort(ref))
+
+
+@pytest.mark.parametrize("n,k", [(11008, 1652), (5632, 564), (32, 16), (1000, 1000), (1000, 1),
+                                 (20000, 3000), (7, 0)])
+def test_topk_ties_and_edges(kh, orc, n, k):
+    from klearu_amd.dejavu import ORDER_ASCENDING, topk_select
+    rng = np.random.default_rng(n + k)
+    s = rng.random((3, n)).astype(np.float32)
+    s[0, rng.random(n) < 0.5] = 0.5          # heavy ties at the threshold
+    s[1] = np.round(s[1] * 4) / 4            # only five distinct values
+    s[2, : n // 2] = -0.0                    # -0.0 ties +0.0
+    s[2, n // 2:] = 0.0
+    got = topk_select(torch.from_numpy(s).cuda(), k).cpu().numpy()
+    asc = topk_select(torch.from_numpy(s).cuda(), k, ORDER_ASCENDING).cpu().numpy()
+    for b in range(3):
+        ref = orc.select_top_k(s[b], k)
+        np.testing.assert_array_equal(got[b], ref)
+        np.testing.assert_array_equal(asc[b], np.sort(ref))
+
+
+def test_union_active(kh):
+    from klearu_amd.dejavu import union_active
+    rng = np.random.default_rng(9)
+    ids = np.stack([rng.choice(11008, 1652, replace=False) for _ in range(16)]).astype(np.int32)
+    u, c = union_active(torch.from_numpy(ids).cuda(), 11008)
+    n = int(c.item())
+    np.testing.assert_array_equal(u[:n].cpu().numpy(), np.unique(ids))
+
+
+def _ffn_case(orc, rng, H, I, k, batch):
+    wg = bf16(orc, rng.normal(0, 0.02, (I, H)))
+    wu = bf16(orc, rng.normal(0, 0.02, (I, H)))
+    wd = bf16(orc, rng.normal(0, 0.02, (H, I)))
+    x = rng.standard_normal((batch, H)).astype(np.float32)
+    act = rng.choice(I, k, replace=False).astype(np.int64)
+    return wg, wu, wd, x, act
+
+
+@pytest.mark.parametrize("H,I,k,batch", [
+    (4096, 11008, 1652, 1),   # cfg3 headline shape
+    (2048, 5632, 564, 1),     # cfg2
+    (4096, 11008, 1652, 2),
+    (4096, 11008, 1652, 16),  # cfg3 batch 16 shared set
+    (264, 100, 37, 3),        # ragged hidden (not a multiple of 256)
+    (512, 64, 64, 1),         # every neuron active
+    (512, 64, 1, 1),          # a single neuron
+])
+def test_sparse_ffn_matches_oracle(kh, orc, H, I, k, batch):
+    from klearu_amd.dejavu import Mlp
+    rng = np.random.default_rng(H + I + k + batch)
+    wg, wu, wd, x, act = _ffn_case(orc, rng, H, I, k, batch)
+    mlp = Mlp(wg, wu, wd, max_batch=16)
+    xd = torch.from_numpy(x).cuda()
+    ad = torch.from_numpy(act.astype(np.int32)).cuda()
+    y = torch.empty_like(xd)
+    mlp.forward_sparse_into(xd, ad, y)
+    h = mlp.last_hidden(batch, k).cpu().numpy()
+    y = y.cpu().numpy()
+    for b in range(batch):
+        yr, hr = orc.sparse_mlp_forward_bf16(wg, wu, wd, x[b], act)
+        scale = float(np.max(np.abs(yr)))
+        err = float(np.max(np.abs(y[b] - yr)))
+        print(f"H{H} I{I} k{k} b{b}: max-abs {err:.3e} (max |y| {scale:.3e}), "
+              f"h max-abs {float(np.max(np.abs(h[b] - hr))):.3e}")
+        np.testing.assert_allclose(h[b], hr, rtol=RTOL, atol=1e-6 * float(np.max(np.abs(hr))))
+        np.testing.assert_allclose(y[b], yr, rtol=RTOL, atol=1e-4 * scale)
+
+
+def test_sparse_ffn_accumulate_and_device_count(kh, orc):
+    from klearu_amd.dejavu import Mlp
+    rng = np.random.default_rng(77)
+    H, I, k = 1024, 2816, 400
+    wg, wu, wd, x, act = _ffn_case(orc, rng, H, I, k, 2)
+    mlp = Mlp(wg, wu, wd, max_batch=4)
+    xd = torch.from_numpy(x).cuda()
+    full = torch.from_numpy(np.concatenate([act, np.arange(I)[~np.isin(np.arange(I), act)]])
+                            .astype(np.int32)).cuda()
+    y0 = torch.from_numpy(rng.standard_normal((2, H)).astype(np.float32)).cuda()
+    y = y0.clone()
+    cnt = torch.tensor([k], dtype=torch.int32, device="cuda")
+    mlp.forward_sparse_into(xd, full, y, accumulate=True, n_active_dev=cnt, n_active=I)
+    y = y.cpu().numpy()
+    for b in range(2):
+        yr, _ = orc.sparse_mlp_forward_bf16(wg, wu, wd, x[b], act)
+        np.testing.assert_allclose(y[b] - y0[b].cpu().numpy(), yr, rtol=RTOL,
+                                   atol=1e-4 * float(np.max(np.abs(yr))))
+
+
+def test_sparse_ffn_rejects_bad_shapes(kh, orc):
+    from klearu_amd import KlearuError
+    from klearu_amd.dejavu import Mlp
+    rng = np.random.default_rng(1)
+    wg, wu, wd, x, act = _ffn_case(orc, rng, 256, 64, 8, 1)
+    mlp = Mlp(wg, wu, wd, max_batch=2)
+    xd = torch.zeros(3, 256, device="cuda")
+    with pytest.raises(KlearuError):
+        mlp.forward_sparse_into(xd, torch.zeros(8, dtype=torch.int32, device="cuda"),
+                                torch.empty_like(xd))
+
+
+def test_rmsnorm(kh, orc):
+    from klearu_amd.dejavu import rmsnorm
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((4, 4096)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 4096).astype(np.float32)
+    got = rmsnorm(torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), 1e-5).cpu().numpy()
+    for b in range(4):
+        np.testing.assert_allclose(got[b], orc.rmsnorm(x[b], w, 1e-5), rtol=1e-5, atol=1e-6)
