@@ -33,7 +33,7 @@ __global__ __launch_bounds__(kSlideThreads) void select_kernel(
   extern __shared__ unsigned hist[];
   __shared__ int wsum[kSlideThreads / 64];
   __shared__ int s_total;
-  __shared__ int s_cstar, s_take, s_best_c, s_best_id;
+  __shared__ int s_cstar, s_take, s_best_id;
   const int64_t row = blockIdx.x;
   const uint32_t* ids = qids + row * (int64_t)qstride;
   const uint32_t* cnt = qcnt + row * (int64_t)qstride;
@@ -47,66 +47,72 @@ __global__ __launch_bounds__(kSlideThreads) void select_kernel(
     } else {
       for (int i = threadIdx.x; i < nbins; i += blockDim.x) hist[i] = 0u;
       __syncthreads();
-      for (int i = threadIdx.x; i < m; i += blockDim.x) atomicAdd(&hist[min(cnt[i], (uint32_t)nbins - 1)], 1u);
+      for (int i = threadIdx.x; i < m; i += blockDim.x) atomicAdd(&hist[cnt[i]], 1u);
       __syncthreads();
+      // Find the count c* where the number of candidates with count >= c*
+      // first reaches top_k.  Thread t owns a run of bins, thread 0 the
+      // highest; an exclusive scan gives each run the number of candidates
+      // above it, and the run holding the crossing walks its bins downwards.
       if (threadIdx.x == 0) {
-        int above = 0, c = nbins - 1;
-        for (; c > 0; --c) {
-          if (above + (int)hist[c] >= top_k) break;
-          above += hist[c];
+        s_cstar = 0;
+        s_take = top_k;
+      }
+      const int seg = (nbins + (int)blockDim.x - 1) / (int)blockDim.x;
+      const int hi = nbins - 1 - (int)threadIdx.x * seg;
+      const int lo = max(hi - seg + 1, 0);
+      int run = 0;
+      for (int c = hi; c >= lo; --c) run += (int)hist[c];
+      const int above = block_excl_scan(run, wsum, &s_total);
+      if (hi >= 0 && above < top_k && above + run >= top_k) {
+        int a = above, c = hi;
+        for (; c > lo; --c) {
+          if (a + (int)hist[c] >= top_k) break;
+          a += (int)hist[c];
         }
         s_cstar = c;
-        s_take = top_k - above;
+        s_take = top_k - a;
       }
       __syncthreads();
       cstar = s_cstar;
       take_eq = s_take;
     }
   }
-  int n_sel = 0;
+  // n_pre counts the sampler's picks before ids >= num_neurons are dropped:
+  // the all-neurons fallback (layer.rs:82-84) runs before that filter (:87).
+  int n_sel = 0, n_pre = 0;
   if (mode == KH_SAMPLING_THRESHOLD) {
-    int any = 0;
-    int base = 0;
+    int base = 0, passed = 0;
     for (int c0 = 0; c0 < m; c0 += blockDim.x) {
       const int i = c0 + threadIdx.x;
-      const int sel = (i < m && (int)cnt[i] >= threshold) ? 1 : 0;
+      const int sel = (i < m && cnt[i] >= (uint32_t)threshold) ? 1 : 0;
       const int id = i < m ? (int)ids[i] : 0;
-      const int keep = sel && id < num_neurons;
+      const int keep = sel && (uint32_t)id < (uint32_t)num_neurons;
+      block_excl_scan(sel, wsum, &s_total);
+      passed += s_total;
       const int pos = block_excl_scan(keep, wsum, &s_total) + base;
       if (keep) out[pos] = (uint32_t)id;
       base += s_total;
-      any |= 0;
     }
     n_sel = base;
-    if (m > 0) {
-      // none passing -> the single best (highest count, lowest id), when none passed at all
-      int passed = 0;
-      {
-        int b2 = 0;
-        for (int c0 = 0; c0 < m; c0 += blockDim.x) {
-          const int i = c0 + threadIdx.x;
-          const int sel = (i < m && (int)cnt[i] >= threshold) ? 1 : 0;
-          block_excl_scan(sel, wsum, &s_total);
-          b2 += s_total;
-        }
-        passed = b2;
+    n_pre = passed;
+    if (m > 0 && passed == 0) {
+      // threshold.rs:37-42: the single best candidate (highest count, then
+      // lowest id; ids are ascending, so the first maximum).
+      if (threadIdx.x == 0) {
+        uint32_t bc = 0, bi = ids[0];
+        for (int i = 0; i < m; ++i)
+          if (cnt[i] > bc || i == 0) {
+            bc = cnt[i];
+            bi = ids[i];
+          }
+        s_best_id = (int)bi;
       }
-      if (passed == 0) {
-        if (threadIdx.x == 0) {
-          int bc = -1, bi = 0;
-          for (int i = 0; i < m; ++i)
-            if ((int)cnt[i] > bc) {  // ids ascending: first max has the lowest id
-              bc = (int)cnt[i];
-              bi = (int)ids[i];
-            }
-          s_best_id = bi;
-        }
-        __syncthreads();
-        n_sel = 0;
-        if (s_best_id < num_neurons) {
-          if (threadIdx.x == 0) out[0] = (uint32_t)s_best_id;
-          n_sel = 1;
-        }
+      __syncthreads();
+      n_pre = 1;
+      n_sel = 0;
+      if ((uint32_t)s_best_id < (uint32_t)num_neurons) {
+        if (threadIdx.x == 0) out[0] = (uint32_t)s_best_id;
+        n_sel = 1;
       }
     }
   } else {
@@ -115,22 +121,23 @@ __global__ __launch_bounds__(kSlideThreads) void select_kernel(
       const int i = c0 + threadIdx.x;
       int sel = i < m ? 1 : 0;
       if (mode == KH_SAMPLING_TOPK) {
-        const int c = i < m ? (int)min(cnt[i], (uint32_t)nbins - 1) : 0;
+        const int c = i < m ? (int)cnt[i] : 0;
         const int eq = (i < m && c == cstar) ? 1 : 0;
         const int r = block_excl_scan(eq, wsum, &s_total) + base_eq;
         base_eq += s_total;
         sel = (i < m) && (c > cstar || (eq && r < take_eq));
       }
       const int id = i < m ? (int)ids[i] : 0;
-      const int keep = sel && id < num_neurons;
+      const int keep = sel && (uint32_t)id < (uint32_t)num_neurons;
       const int pos = block_excl_scan(keep, wsum, &s_total) + base;
       if (keep) out[pos] = (uint32_t)id;
       base += s_total;
     }
     n_sel = base;
+    n_pre = mode == KH_SAMPLING_TOPK ? min(m, top_k) : m;
   }
   // empty selection -> every neuron (layer.rs:82-84)
-  if (n_sel == 0 && !(mode == KH_SAMPLING_THRESHOLD && m > 0 && false)) {
+  if (n_pre == 0) {
     for (int i = threadIdx.x; i < num_neurons; i += blockDim.x) out[i] = (uint32_t)i;
     n_sel = num_neurons;
   }
@@ -224,7 +231,7 @@ __global__ __launch_bounds__(kSlideThreads) void neuron_kernel(
   __syncthreads();
   float ls = 0.0f;
   for (int a = threadIdx.x; a < n; a += blockDim.x) {
-    const float e = expf(prow[a] - mx);
+    const float e = expf_glibc(prow[a] - mx);
     orow[a] = e;
     ls += e;
   }
@@ -359,9 +366,12 @@ static int slide_forward_common(const kh_slide_layer* lc, const float* x, const 
   if (rc != KH_OK) return rc;
   rc = query_launch(idx, codes, batch, qids, qcnt, qs, qlen, st);
   if (rc != KH_OK) return rc;
-  const int nbins = std::min(kMaxCountBins, L * idx->cap + 1);
+  // A candidate's hit count is at most L * cap (every slot of its L buckets).
+  const int nbins = L * idx->cap + 1;
+  KH_CHECK_ARG(l->sampling != KH_SAMPLING_TOPK || nbins <= kMaxCountBins,
+               "top-k sampling supports num_tables * bucket_capacity <= %d", kMaxCountBins - 1);
   hipLaunchKernelGGL(select_kernel, dim3((unsigned)batch), dim3(kSlideThreads),
-                     sizeof(unsigned) * nbins, st, qids, qcnt, qlen, qs, l->sampling, l->top_k,
+                     l->sampling == KH_SAMPLING_TOPK ? sizeof(unsigned) * nbins : 0, st, qids, qcnt, qlen, qs, l->sampling, l->top_k,
                      l->threshold, l->n, nbins, aids, as, alen);
   KH_LAUNCHED();
   const int max_nz = xoff ? 4096 : l->dim;

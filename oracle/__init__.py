@@ -100,6 +100,9 @@ _sig("or_dejavu_sparse_mlp_forward", None, _f32p, _f32p, _f32p, _f32p, _f32p, _f
 _sig("or_cpu_dejavu_ffn_layer", None, _f32p, _f32p, _f32p, _f32p, _f, _f32p, _f32p, _f32p, _f32p, _int,
      _int, _int, _i64, _f32p, _f32p, _i64p)
 
+_sig("or_slide_forward", _i64, _i8p, _int, _int, _int, _int, _u32p, _u32p, _f32p, _f32p, _int, _f32p,
+     _int, _int, _int, _int, _u32p, _f32p, _f32p)
+
 ACT = {"relu": 0, "sigmoid": 1, "tanh": 2, "softmax": 3, "identity": 4}
 FIFO, RESERVOIR = 0, 1
 
@@ -362,3 +365,27 @@ def dejavu_sparse_mlp_forward(wg, bg, wu, bu, wd, bd, x, sel):
                                      f32(wd).reshape(-1), f32(bd), hidden, inter, f32(x), sel,
                                      sel.size, y)
     return y
+
+
+def slide_layer_oracle(planes, cap, bucket_type, W, b, X, sampling=0, top_k=0, threshold=2, act="relu",
+                       index=None):
+    """Build the index like Layer::new (neurons 0..n-1 in order) and run
+    Layer::forward for every row of X.  Returns a list of (ids, pre, act)."""
+    L, k, dim = planes.shape
+    W = f32(W)
+    n = W.shape[0]
+    if index is None:
+        index = LshIndex(L, k, cap, bucket_type)
+        index.insert_many(np.arange(n, dtype=np.uint32), hash_dense_batch(planes, W))
+    pl = np.ascontiguousarray(planes).reshape(-1)
+    m = max(n, L * cap) + 1
+    out = []
+    for x in f32(X).reshape(-1, dim):
+        ids = np.zeros(m, np.uint32)
+        pre = np.zeros(m, np.float32)
+        a_ = np.zeros(m, np.float32)
+        cnt = lib.or_slide_forward(pl, dim, k, L, cap, index.data, index.len, W.reshape(-1), f32(b), n,
+                                   np.ascontiguousarray(x), sampling, top_k, threshold,
+                                   ACT[act] if isinstance(act, str) else act, ids, pre, a_)
+        out.append((ids[:cnt].copy(), pre[:cnt].copy(), a_[:cnt].copy()))
+    return out, index

@@ -839,3 +839,53 @@ void or_dejavu_sparse_mlp_forward(const float* wg, const float* bg, const float*
   for (int j = 0; j < hidden; ++j) y[j] = y[j] + bd[j];
   free(g); free(u); free(sh);
 }
+
+/* ======================================================================== */
+/* SLIDE Layer::forward for one dense input (network/layer.rs:65-120)        */
+/* ======================================================================== */
+
+static int cmp_u32_asc(const void* a, const void* b) { return cmp_u32(a, b); }
+
+/* Query (lsh/index.rs:282-284) -> sampling (layer.rs:78; sampling 0 vanilla,
+ * 1 top-k, 2 threshold) -> empty set falls back to every neuron (:82-84) ->
+ * ids < n (:87) -> Neuron::forward per active id (:90-93) -> activation
+ * (:96-107).  Active ids are returned ascending (the reference's order is
+ * HashMap order for vanilla/threshold).  Returns the number of active ids;
+ * out arrays need max(n, L*cap) entries. */
+int64_t or_slide_forward(const int8_t* planes, int dim, int k, int num_tables, int cap,
+                         const uint32_t* data, const uint32_t* len, const float* W,
+                         const float* bias, int n, const float* x, int sampling, int top_k,
+                         int threshold, int act, uint32_t* out_ids, float* out_pre,
+                         float* out_act) {
+  uint32_t* codes = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)num_tables);
+  or_hash_dense_batch(planes, dim, k, num_tables, x, 1, codes);
+  const int64_t m = (int64_t)num_tables * cap + 1;
+  uint32_t* ids = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)m);
+  uint32_t* cnt = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)m);
+  int64_t u = or_lsh_query(num_tables, k, cap, data, len, codes, ids, cnt);
+  int64_t a = 0;
+  if (sampling == 1) {
+    a = or_sample_topk(ids, cnt, u, top_k, out_ids);
+  } else if (sampling == 2) {
+    a = or_sample_threshold(ids, cnt, u, (uint32_t)threshold, out_ids);
+  } else {
+    memcpy(out_ids, ids, sizeof(uint32_t) * (size_t)u);
+    a = u;
+  }
+  if (a == 0) {
+    for (int i = 0; i < n; ++i) out_ids[i] = (uint32_t)i;
+    a = n;
+  }
+  int64_t r = 0;
+  for (int64_t i = 0; i < a; ++i)
+    if (out_ids[i] < (uint32_t)n) out_ids[r++] = out_ids[i];
+  a = r;
+  qsort(out_ids, (size_t)a, sizeof(uint32_t), cmp_u32_asc);
+  for (int64_t i = 0; i < a; ++i)
+    out_pre[i] = or_neuron_forward(W + (int64_t)out_ids[i] * dim, bias[out_ids[i]], x, dim);
+  or_layer_activate(out_pre, a, act, out_act);
+  free(codes);
+  free(ids);
+  free(cnt);
+  return a;
+}

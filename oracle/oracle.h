@@ -92,6 +92,12 @@ float or_neuron_forward_sparse(const float* w, float bias, const uint32_t* idx, 
                                int64_t nnz);
 void or_layer_activate(const float* pre, int64_t n, int act, float* out);
 
+int64_t or_slide_forward(const int8_t* planes, int dim, int k, int num_tables, int cap,
+                         const uint32_t* data, const uint32_t* len, const float* W,
+                         const float* bias, int n, const float* x, int sampling, int top_k,
+                         int threshold, int act, uint32_t* out_ids, float* out_pre,
+                         float* out_act);
+
 /* ---- klearu-dejavu predictor/mlp_predictor.rs ---- */
 void or_predictor_predict(const float* w1, const float* b1, const float* w2, const float* b2,
                           int in_dim, int hid, int out_dim, const float* x, float* scores,
