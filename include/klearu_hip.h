@@ -276,29 +276,53 @@ int kh_rmsnorm(const float* x_dev, const float* w_dev, int64_t batch, int n, flo
 
 typedef struct kh_sparse_attn kh_sparse_attn;
 
-/* Attention{q,k,v,o}_proj (model/attention.rs) + KvCache (model/kv_cache.rs:5-25)
- * + RotaryEmbedding (model/rope.rs:17-46): BF16 weights in the reference
- * layout wq[nh*d][hidden], wk/wv[nkv*d][hidden], wo[hidden][nh*d].  The cache
- * holds max_batch sequences of max_seq positions, BF16, [seq][kv_head][pos][d]. */
+#define KH_KV_BF16 0 /* cache rows rounded to BF16 (half the bytes per step) */
+#define KH_KV_F32 1  /* cache rows kept in f32, as KvCache stores them */
+
+/* Attention{q,k,v,o}_proj (model/attention.rs:8-64) + KvCache (model/kv_cache.rs:5-25)
+ * + RotaryEmbedding::new(head_dim, max_seq, rope_theta) (model/rope.rs:17-46)
+ * for max_batch independent sequences of at most max_seq positions.
+ * Weights are BF16 in the reference layout: wq[nh*d][hidden],
+ * wk/wv[nkv*d][hidden], wo[hidden][nh*d].  head_dim in {64, 128, 256};
+ * hidden a multiple of 8; num_heads a multiple of num_kv_heads (GQA). */
 int kh_sparse_attn_create(int hidden, int num_heads, int num_kv_heads, int head_dim,
-                          int max_seq, int max_batch, float rope_theta, const uint16_t* wq_host,
-                          const uint16_t* wk_host, const uint16_t* wv_host,
-                          const uint16_t* wo_host, kh_sparse_attn** out);
+                          int max_seq, int max_batch, float rope_theta, int kv_dtype,
+                          const uint16_t* wq_host, const uint16_t* wk_host,
+                          const uint16_t* wv_host, const uint16_t* wo_host, kh_sparse_attn** out);
+/* Same with the four weight matrices already in device memory (same layouts). */
+int kh_sparse_attn_create_dev(int hidden, int num_heads, int num_kv_heads, int head_dim,
+                              int max_seq, int max_batch, float rope_theta, int kv_dtype,
+                              const uint16_t* wq_dev, const uint16_t* wk_dev,
+                              const uint16_t* wv_dev, const uint16_t* wo_dev,
+                              kh_sparse_attn** out);
 int kh_sparse_attn_destroy(kh_sparse_attn* a);
-/* Fill positions [0, len) of sequence b of the cache from f32 host arrays
- * k_host/v_host [kv_heads][len][d] (rounded to BF16); sets that sequence's length. */
+/* Fill positions [0, len) of sequence b from f32 host arrays k_host/v_host
+ * [nkv][len][d] (rounded to BF16 for a KH_KV_BF16 cache) and set its length
+ * (KvCache::append repeated, kv_cache.rs:33-48).  Synchronous. */
 int kh_sparse_attn_load_cache(kh_sparse_attn* a, int64_t b, const float* k_host,
                               const float* v_host, int64_t len);
+/* Copy positions [0, len) of sequence b back as f32 [nkv][len][d]. Synchronous. */
+int kh_sparse_attn_read_cache(const kh_sparse_attn* a, int64_t b, float* k_host, float* v_host,
+                              int64_t len);
+/* KvCache::current_len (kv_cache.rs:27-29) of sequence b (reads the device
+ * counter, synchronous). */
+int kh_sparse_attn_cache_len(kh_sparse_attn* a, int64_t b, int64_t* len);
+/* KvCache::clear (kv_cache.rs:75-78) for every sequence. */
+int kh_sparse_attn_clear(kh_sparse_attn* a, void* stream);
 /* sparse_attention::forward_sparse (sparse_attention.rs:7-79) for one decode
- * step of `batch` sequences: x_dev[batch][hidden] at positions pos_dev[batch]
- * (int64, = current cache length of each sequence), heads_dev[batch][n_heads]
- * (int32; ids >= num_heads are skipped as at :48-50).  Appends this step's
- * K/V for every kv head, computes softmax attention for the selected heads only
- * and the output projection over the selected heads' columns only.
- * out_dev[batch][hidden]. Mutates the cache. */
+ * step of sequences 0..batch-1: x_dev[batch][hidden]; RoPE positions
+ * pos_dev[batch] (int64; NULL = each sequence's current length, the usual
+ * decode position); heads_dev[batch][n_heads] int32 selected heads per token
+ * (ids outside [0, num_heads) are skipped as at :48-50; a repeated id adds
+ * its head output again, as the reference's += does).  Projects K/V for every
+ * kv head and appends them (:39), projects Q and runs softmax attention for
+ * the selected heads only, and runs o_proj over the selected heads' columns
+ * only.  out_dev[batch][hidden] is written (accumulate = 0) or added to.
+ * Returns KH_ERR_CAPACITY when a sequence's cache is full (the reference
+ * panics, kv_cache.rs:36).  Mutates the cache. */
 int kh_sparse_attn_forward(kh_sparse_attn* a, const float* x_dev, int64_t batch,
                            const int64_t* pos_dev, const int32_t* heads_dev, int n_heads,
-                           float* out_dev, void* stream);
+                           float* out_dev, int accumulate, void* stream);
 
 #ifdef __cplusplus
 }

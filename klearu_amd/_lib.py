@@ -87,10 +87,14 @@ SIGS = {
     "kh_sparse_ffn_forward": (I, [P, P, I64, P, I, P, P, I, P]),
     "kh_sparse_ffn_last_hidden": (I, [P, P, I64, I, P]),
     "kh_rmsnorm": (I, [P, P, I64, I, F, P, P]),
-    "kh_sparse_attn_create": (I, [I, I, I, I, I, I, F, P, P, P, P, PP]),
+    "kh_sparse_attn_create": (I, [I, I, I, I, I, I, F, I, P, P, P, P, PP]),
+    "kh_sparse_attn_create_dev": (I, [I, I, I, I, I, I, F, I, P, P, P, P, PP]),
     "kh_sparse_attn_destroy": (I, [P]),
     "kh_sparse_attn_load_cache": (I, [P, I64, P, P, I64]),
-    "kh_sparse_attn_forward": (I, [P, P, I64, P, P, I, P, P]),
+    "kh_sparse_attn_read_cache": (I, [P, I64, P, P, I64]),
+    "kh_sparse_attn_cache_len": (I, [P, I64, P]),
+    "kh_sparse_attn_clear": (I, [P, P]),
+    "kh_sparse_attn_forward": (I, [P, P, I64, P, P, I, P, I, P]),
 }
 
 

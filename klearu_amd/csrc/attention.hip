@@ -1,0 +1,772 @@
+// attention.hip -- head-sparse decode attention (gfx950).
+//
+// Replaces sparse_attention::forward_sparse
+// (crates/klearu-llm/src/sparse/sparse_attention.rs:7-95) together with
+// KvCache::append (model/kv_cache.rs:33-48), RotaryEmbedding (model/rope.rs:17-87)
+// and Linear::forward (model/linear.rs:79-104) for q/k/v/o_proj.
+//
+// HBM layout (written once at create):
+//   Wkvq [2*kvd + nh*D][hidden] BF16   K rows, V rows, then Q rows head by head
+//   WoT  [nh*D][hidden]        BF16    o_proj transposed: the columns of head h
+//                                      are the contiguous rows h*D .. h*D+D-1
+//   K, V cache [max_batch][nkv][max_seq][D]  BF16 (default) or f32; all positions
+//                                      of one kv head are contiguous, so one
+//                                      (token, head) reads 2*len*D*elt bytes
+//   cos, sin [max_seq][D/2] f32        rope.rs:23-37, computed with the host libm
+//   len [max_batch] int32              cache lengths, advanced by every step
+//
+// One decode step of `batch` sequences, each with its own selected heads:
+//   attn_qkv      one wave per row of Wkvq for every token (tokens staged in LDS):
+//                 every K and V row (the cache takes every kv head, :39) and the
+//                 Q rows of heads that some token selected; its last block writes
+//                 the union of selected heads as the row list of the o_proj gather.
+//   attn_decode   split-K over cache positions (a chunk per block) for every
+//                 (token, selected head): RoPE on q and on the current k, scores
+//                 from 16-byte K loads, chunk max / exp-sum and the un-normalised
+//                 V sum.  The current position's K/V come from this step's f32
+//                 projections, so the step sees them unrounded as the reference does.
+//   attn_combine  merges the chunks of each (token, head) into the head output, in
+//                 union order with zeros where a token did not select a union head
+//                 (the reference's zero-filled attn_concat, :44), and appends this
+//                 step's roped K and V to the cache.
+//   gather_rows + partials_reduce (gather.hpp)
+//                 o_proj over the union heads' WoT rows only; the reduce advances
+//                 each sequence's cache length once its output is complete.
+// Bytes per token at 7B shape (hidden 4096, 32 heads x 128, 16 selected, len
+// 2048, BF16 cache): K/V rows 2*4096*4096*2 = 64 MiB, Q rows 16 MiB, o_proj
+// 16 MiB, cache 16*2048*128*2*2 = 16 MiB.
+//
+// Parity: q/k/v/o projections and the softmax sums use a different (parallel)
+// summation order from the reference's AVX2 dot and sequential loops, so
+// outputs agree to rounding (BF16-weight tolerance), not bit for bit.
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "gather.hpp"
+
+namespace kh {
+
+constexpr int kAttnThreads = 256;
+constexpr int kAttnPasses = 8;      // cache rows per thread per chunk (K and V loads in flight)
+constexpr int kQkvWaves = 8;        // rows per projection block
+constexpr int kQkvChunks = 8;       // 16-byte chunks per lane in flight (hidden <= 4096 per pass)
+constexpr int kQkvTok = 4;          // tokens staged in LDS at a time
+constexpr int kMaxAttnHeads = 1024;
+
+// RotaryEmbedding::apply (rope.rs:75-87) for element i of a head vector x:
+// x[i] = x0*cos - x1*sin and x[half+i] = x1*cos + x0*sin, products rounded
+// separately (no FMA contraction in this build).
+template <int HALF>
+__device__ __forceinline__ float rope_elem(const float* __restrict__ x, const float* __restrict__ c,
+                                           const float* __restrict__ s, int i) {
+  if (i < HALF) return x[i] * c[i] - x[i + HALF] * s[i];
+  const int k = i - HALF;
+  return x[i] * c[k] + x[k] * s[k];
+}
+
+__device__ __forceinline__ void widen16(const uint4& v, float* f, uint16_t) {
+  f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
+  f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
+}
+__device__ __forceinline__ void widen16(const uint4& v, float* f, float) {
+  f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
+  f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
+}
+__device__ __forceinline__ void store_kv(uint16_t* p, float v) { *p = f32_to_bf16(v); }
+__device__ __forceinline__ void store_kv(float* p, float v) { *p = v; }
+
+// y[b][row] = Wkvq[row] . x[b] for the K/V rows and the Q rows of selected
+// heads.  The grid has one extra (last) block that writes the o_proj row list.
+template <int NB>
+__global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
+    const uint16_t* __restrict__ W, const float* __restrict__ x, int batch, int H, int kvrows,
+    int D, int nh, const int32_t* __restrict__ heads, int nsel, float* __restrict__ y,
+    int ystride, int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows) {
+  extern __shared__ float4 xs4[];  // [kQkvTok][H/4]; the plan block's flags / union list
+  __shared__ int wsum[kQkvWaves];
+  __shared__ int s_total;
+  const int nent = batch * nsel;
+  if (blockIdx.x == gridDim.x - 1) {
+    // Union of selected heads in ascending order -> rows h*D + r of WoT.
+    int* s_flag = reinterpret_cast<int*>(xs4);
+    int* s_uh = s_flag + nh;
+    for (int h = threadIdx.x; h < nh; h += blockDim.x) s_flag[h] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < nent; i += blockDim.x) {
+      const int h = heads[i];
+      if (h >= 0 && h < nh) s_flag[h] = 1;
+    }
+    __syncthreads();
+    int base = 0;
+    for (int h0 = 0; h0 < nh; h0 += blockDim.x) {
+      const int h = h0 + threadIdx.x;
+      const int f = h < nh ? s_flag[h] : 0;
+      const int u = block_excl_scan(f, wsum, &s_total) + base;
+      if (f) s_uh[u] = h;
+      base += s_total;
+    }
+    __syncthreads();
+    const int nq = base * D;
+    for (int i = threadIdx.x; i < nq; i += blockDim.x) qrows[i] = s_uh[i / D] * D + i % D;
+    if (threadIdx.x == 0) *nqrows = nq;
+    return;
+  }
+  const int row0 = blockIdx.x * kQkvWaves;
+  if (row0 >= kvrows) {
+    // Q rows of head h (D is a multiple of kQkvWaves): skip unless selected.
+    const int h = (row0 - kvrows) / D;
+    int any = 0;
+    for (int i = threadIdx.x; i < nent; i += blockDim.x) any |= heads[i] == h;
+    if (!__syncthreads_or(any)) return;
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = row0 + wave;
+  const uint4* __restrict__ w = reinterpret_cast<const uint4*>(W + (size_t)row * H);
+  const int nchunk = H >> 3, H4 = H >> 2;
+  constexpr int TB = NB < kQkvTok ? NB : kQkvTok;
+  float acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
+  for (int cbase = 0; cbase < nchunk; cbase += 64 * kQkvChunks) {
+    uint4 wv[kQkvChunks];
+#pragma unroll
+    for (int q = 0; q < kQkvChunks; ++q) wv[q] = w[min(cbase + lane + 64 * q, nchunk - 1)];
+#pragma unroll
+    for (int t0 = 0; t0 < NB; t0 += TB) {
+      if (t0 >= batch) break;
+      lds_barrier();
+      const int nt = min(TB, batch - t0);
+      stage_f4(xs4, reinterpret_cast<const float4*>(x + (size_t)t0 * H), nt * H4);
+      lds_barrier();
+#pragma unroll
+      for (int q = 0; q < kQkvChunks; ++q) {
+        const int c = cbase + lane + 64 * q;
+        if (c >= nchunk) break;
+        float wf[8];
+        widen16(wv[q], wf, uint16_t());
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+          if (t < nt) {
+            const float4 x0 = xs4[t * H4 + 2 * c], x1 = xs4[t * H4 + 2 * c + 1];
+            float a = acc[t0 + t];
+            a = fmaf(wf[0], x0.x, a); a = fmaf(wf[1], x0.y, a);
+            a = fmaf(wf[2], x0.z, a); a = fmaf(wf[3], x0.w, a);
+            a = fmaf(wf[4], x1.x, a); a = fmaf(wf[5], x1.y, a);
+            a = fmaf(wf[6], x1.z, a); a = fmaf(wf[7], x1.w, a);
+            acc[t0 + t] = a;
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (b < batch) {
+      const float s = wave_sum(acc[b]);
+      if (lane == 0) y[(size_t)b * ystride + row] = s;
+    }
+  }
+}
+
+// Cache positions per decode block: kAttnPasses rows per thread.
+template <typename KV, int D>
+constexpr int attn_chunk() {
+  return kAttnThreads / (D / (16 / (int)sizeof(KV))) * kAttnPasses;
+}
+
+// One block per (chunk s, selected-head entry a, token b).  Writes the chunk's
+// un-normalised head output po[b][a][s][D] and (max, exp-sum) pml[b][a][s].
+template <typename KV, int D>
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
+    const KV* __restrict__ kc, const KV* __restrict__ vc, const float* __restrict__ y,
+    int ystride, int nkv, int nh, const int32_t* __restrict__ heads, int nsel,
+    const int32_t* __restrict__ lens, const int64_t* __restrict__ positions,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int max_seq,
+    float inv_sqrt, int nsplit, float* __restrict__ po, float2* __restrict__ pml) {
+  constexpr int EPL = 16 / sizeof(KV);          // elements per 16-byte load
+  constexpr int LPR = D / EPL;                  // lanes per cache row
+  constexpr int RPP = kAttnThreads / LPR;       // rows per pass
+  constexpr int NP = kAttnPasses;               // passes per chunk
+  constexpr int CH = RPP * NP;                  // positions per chunk
+  constexpr int HALF = D / 2;
+  static_assert(LPR <= 64 && kAttnThreads % LPR == 0 && CH <= kAttnThreads, "tiling");
+  static_assert(HALF % EPL == 0, "a lane's slice lies in one half of the head");
+  __shared__ float s_p[CH];
+  __shared__ float s_red[RPP][D];
+  __shared__ float s_wm[kAttnThreads / 64], s_wl[kAttnThreads / 64];
+  const int s = blockIdx.x, a = blockIdx.y, b = blockIdx.z;
+  const int h = heads[(size_t)b * nsel + a];
+  if (h < 0 || h >= nh) return;  // sparse_attention.rs:48-50
+  const int len = lens[b];
+  if (len >= max_seq) return;    // full cache: the step is refused for this sequence
+  const int start = s * CH;
+  if (start > len) return;
+  const int n = min(CH, len + 1 - start);
+  const int kvh = h / (nh / nkv);
+  int64_t pos = positions ? positions[b] : len;
+  pos = pos < 0 ? 0 : (pos >= max_seq ? max_seq - 1 : pos);
+  const int t = threadIdx.x, sl = t % LPR, r0 = t / LPR;
+  const int e0 = sl * EPL;
+  const int kvd = nkv * D;
+  const float* yb = y + (size_t)b * ystride;
+  const float* qsrc = yb + 2 * kvd + h * D;
+  const float* kcur = yb + kvh * D;
+  const float* vcur = yb + kvd + kvh * D;
+  const float* ct = cos_t + pos * HALF;
+  const float* st = sin_t + pos * HALF;
+  // This lane's q, current k and current v slices (with RoPE partners) first ...
+  float qv[EPL], kn[EPL], vn[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    qv[e] = rope_elem<HALF>(qsrc, ct, st, e0 + e);
+    kn[e] = rope_elem<HALF>(kcur, ct, st, e0 + e);
+    vn[e] = vcur[e0 + e];
+  }
+  // ... then every K and V load of the chunk, all in flight before first use.
+  // Rows past the last cached one are clamped to it (position len itself is
+  // taken from kn/vn; with an empty cache row 0 is read and never used).
+  const size_t rowbase = ((size_t)b * nkv + kvh) * (size_t)max_seq;
+  const int last = len > 0 ? len - 1 : 0;
+  uint4 kr[NP], vr[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int j = min(start + p * RPP + r0, last);
+    kr[p] = *reinterpret_cast<const uint4*>(kc + (rowbase + j) * D + e0);
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int j = min(start + p * RPP + r0, last);
+    vr[p] = *reinterpret_cast<const uint4*>(vc + (rowbase + j) * D + e0);
+  }
+  // scores: dense_dot(q, k_j) * inv_sqrt_dk (:55-58)
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int j = start + p * RPP + r0;
+    float kf[EPL];
+    widen16(kr[p], kf, KV());
+    if (j == len) {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) kf[e] = kn[e];
+    }
+    float d = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) d = fmaf(qv[e], kf[e], d);
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+    if (sl == 0 && j - start < n) s_p[j - start] = d * inv_sqrt;
+  }
+  lds_barrier();
+  // chunk max and exp-sum (softmax_inplace, :81-95, split over chunks)
+  float m = t < n ? s_p[t] : -INFINITY;
+  m = wave_max(m);
+  if ((t & 63) == 0) s_wm[t >> 6] = m;
+  lds_barrier();
+  m = s_wm[0];
+#pragma unroll
+  for (int w = 1; w < kAttnThreads / 64; ++w) m = fmaxf(m, s_wm[w]);
+  float ex = 0.0f;
+  if (t < n) {
+    ex = expf_glibc(s_p[t] - m);
+    s_p[t] = ex;
+  }
+  const float ls = wave_sum(ex);
+  if ((t & 63) == 0) s_wl[t >> 6] = ls;
+  lds_barrier();
+  // un-normalised V sum over the chunk (:61-67)
+  float acc[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.0f;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int jj = p * RPP + r0;
+    if (jj < n) {
+      float vf[EPL];
+      widen16(vr[p], vf, KV());
+      if (start + jj == len) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) vf[e] = vn[e];
+      }
+      const float pj = s_p[jj];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] = fmaf(pj, vf[e], acc[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) s_red[r0][e0 + e] = acc[e];
+  lds_barrier();
+  const size_t slot = ((size_t)b * nsel + a) * nsplit + s;
+  for (int i = t; i < D; i += kAttnThreads) {
+    float o = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RPP; ++r) o += s_red[r][i];
+    po[slot * D + i] = o;
+  }
+  if (t == 0) {
+    float l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnThreads / 64; ++w) l += s_wl[w];
+    pml[slot] = make_float2(m, l);
+  }
+}
+
+// One block per (head h, token b): the head output of token b in union order
+// (cat[b][u*D + i], zero when b did not select h), and, for h < nkv, the
+// append of this step's roped K and V of kv head h at position len[b].
+template <typename KV>
+__global__ __launch_bounds__(256) void attn_combine_kernel(
+    const float* __restrict__ po, const float2* __restrict__ pml, int nsplit, int chunk,
+    const int32_t* __restrict__ heads, int nsel, int batch, int nh, int nkv, int D,
+    const int32_t* __restrict__ lens, const int64_t* __restrict__ positions,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int max_seq,
+    const float* __restrict__ y, int ystride, KV* __restrict__ kc, KV* __restrict__ vc,
+    float* __restrict__ cat, int catstride) {
+  __shared__ int s_flag[kMaxAttnHeads];
+  __shared__ int s_u;
+  const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int len = lens[b];
+  const bool valid = len < max_seq;
+  const int half = D / 2;
+  if (h < nkv && valid) {
+    // KvCache::append (kv_cache.rs:33-48) of the roped k (sparse_attention.rs:33-39)
+    int64_t pos = positions ? positions[b] : len;
+    pos = pos < 0 ? 0 : (pos >= max_seq ? max_seq - 1 : pos);
+    const float* ct = cos_t + pos * half;
+    const float* st = sin_t + pos * half;
+    const float* kx = y + (size_t)b * ystride + (size_t)h * D;
+    const float* vx = kx + (size_t)nkv * D;
+    const size_t dst = (((size_t)b * nkv + h) * max_seq + len) * D;
+    for (int i = t; i < D; i += blockDim.x) {
+      float kr;
+      if (i < half) kr = kx[i] * ct[i] - kx[i + half] * st[i];
+      else kr = kx[i] * ct[i - half] + kx[i - half] * st[i - half];
+      store_kv(kc + dst + i, kr);
+      store_kv(vc + dst + i, vx[i]);
+    }
+  }
+  for (int i = t; i < nh; i += blockDim.x) s_flag[i] = 0;
+  if (t == 0) s_u = 0;
+  __syncthreads();
+  for (int i = t; i < batch * nsel; i += blockDim.x) {
+    const int hh = heads[i];
+    if (hh >= 0 && hh < nh) s_flag[hh] = 1;
+  }
+  __syncthreads();
+  if (!s_flag[h]) return;
+  int below = 0;
+  for (int i = t; i < h; i += blockDim.x) below += s_flag[i];
+  if (below) atomicAdd(&s_u, below);
+  __syncthreads();
+  const int u = s_u;
+  const int ns = valid ? (len + chunk) / chunk : 0;  // chunks covering len+1 rows
+  for (int i = t; i < D; i += blockDim.x) {
+    float out = 0.0f;
+    if (valid) {
+      for (int a = 0; a < nsel; ++a) {
+        if (heads[(size_t)b * nsel + a] != h) continue;
+        const size_t slot0 = ((size_t)b * nsel + a) * nsplit;
+        float M = -INFINITY;
+        for (int s = 0; s < ns; ++s) M = fmaxf(M, pml[slot0 + s].x);
+        float L = 0.0f, o = 0.0f;
+        for (int s = 0; s < ns; ++s) {
+          const float2 ml = pml[slot0 + s];
+          const float w = expf_glibc(ml.x - M);
+          L = fmaf(ml.y, w, L);
+          o = fmaf(po[(slot0 + s) * D + i], w, o);
+        }
+        out += o / L;
+      }
+    }
+    cat[(size_t)b * catstride + (size_t)u * D + i] = out;
+  }
+}
+
+__global__ void attn_set_len_kernel(int32_t* __restrict__ lens, int n, int value) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) lens[i] = value;
+}
+
+}  // namespace kh
+
+using namespace kh;
+
+struct kh_sparse_attn {
+  int hidden = 0, nh = 0, nkv = 0, d = 0, max_seq = 0, max_batch = 0, kv_f32 = 0;
+  uint16_t* wkvq = nullptr;  // [2*kvd + nh*d][hidden]
+  uint16_t* wot = nullptr;   // [nh*d][hidden]
+  void* kc = nullptr;        // [max_batch][nkv][max_seq][d]
+  void* vc = nullptr;
+  float* cos_t = nullptr;    // [max_seq][d/2]
+  float* sin_t = nullptr;
+  int32_t* lens = nullptr;   // [max_batch]
+  float* y = nullptr;        // [max_batch][2*kvd + nh*d]
+  float* cat = nullptr;      // [max_batch][nh*d]
+  int32_t* qrows = nullptr;  // [nh*d + 1]; the count is stored after the rows
+  std::vector<int64_t> len_host;
+  Scratch po, pml, partial;
+  int kvd() const { return nkv * d; }
+  int ystride() const { return 2 * nkv * d + nh * d; }
+  size_t elt() const { return kv_f32 ? sizeof(float) : sizeof(uint16_t); }
+  size_t seq_elems() const { return (size_t)nkv * max_seq * d; }
+};
+
+extern "C" int kh_sparse_attn_destroy(kh_sparse_attn* a) {
+  if (!a) return KH_OK;
+  dev_free(a->wkvq);
+  dev_free(a->wot);
+  dev_free(a->kc);
+  dev_free(a->vc);
+  dev_free(a->cos_t);
+  dev_free(a->sin_t);
+  dev_free(a->lens);
+  dev_free(a->y);
+  dev_free(a->cat);
+  dev_free(a->qrows);
+  delete a;
+  return KH_OK;
+}
+
+// Shape checks, allocation and the RoPE tables; weights are filled by the caller.
+static int attn_alloc(int hidden, int num_heads, int num_kv_heads, int head_dim, int max_seq,
+                      int max_batch, float rope_theta, int kv_dtype, kh_sparse_attn** out) {
+  KH_CHECK_ARG(out != nullptr, "null out");
+  *out = nullptr;
+  KH_CHECK_ARG(hidden > 0 && hidden % 8 == 0, "hidden (%d) must be a positive multiple of 8",
+               hidden);
+  KH_CHECK_ARG(head_dim == 64 || head_dim == 128 || head_dim == 256,
+               "head_dim %d not supported (64, 128 or 256)", head_dim);
+  KH_CHECK_ARG(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
+                   num_heads <= kMaxAttnHeads,
+               "num_heads (%d) must be a multiple of num_kv_heads (%d) and <= %d", num_heads,
+               num_kv_heads, kMaxAttnHeads);
+  KH_CHECK_ARG(max_seq > 0 && max_batch >= 1 && max_batch <= 16,
+               "max_seq must be positive and max_batch in [1,16]");
+  KH_CHECK_ARG(kv_dtype == KH_KV_BF16 || kv_dtype == KH_KV_F32, "bad kv_dtype %d", kv_dtype);
+  KH_CHECK_ARG(rope_theta > 0.0f, "rope_theta must be positive");
+  auto* a = new kh_sparse_attn();
+  a->hidden = hidden;
+  a->nh = num_heads;
+  a->nkv = num_kv_heads;
+  a->d = head_dim;
+  a->max_seq = max_seq;
+  a->max_batch = max_batch;
+  a->kv_f32 = kv_dtype == KH_KV_F32;
+  a->len_host.assign(max_batch, 0);
+  const size_t H = hidden, qd = (size_t)num_heads * head_dim, kvd = (size_t)num_kv_heads * head_dim;
+  const size_t half = head_dim / 2;
+  a->wkvq = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * (2 * kvd + qd) * H));
+  a->wot = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * qd * H));
+  a->kc = dev_alloc(a->elt() * a->seq_elems() * max_batch);
+  a->vc = dev_alloc(a->elt() * a->seq_elems() * max_batch);
+  a->cos_t = static_cast<float*>(dev_alloc(sizeof(float) * max_seq * half));
+  a->sin_t = static_cast<float*>(dev_alloc(sizeof(float) * max_seq * half));
+  a->lens = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * max_batch));
+  a->y = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * a->ystride()));
+  a->cat = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * qd));
+  a->qrows = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * (qd + 1)));
+  if (!a->wkvq || !a->wot || !a->kc || !a->vc || !a->cos_t || !a->sin_t || !a->lens || !a->y ||
+      !a->cat || !a->qrows) {
+    kh_sparse_attn_destroy(a);
+    return KH_ERR_ALLOC;
+  }
+  // RotaryEmbedding::new_partial (rope.rs:23-37) with the full head rotated,
+  // evaluated in f32 with the host libm as the reference does.
+  std::vector<float> c(max_seq * half), s(max_seq * half);
+  for (int p = 0; p < max_seq; ++p)
+    for (size_t i = 0; i < half; ++i) {
+      const float e = (2.0f * static_cast<float>(i)) / static_cast<float>(head_dim);
+      const float freq = 1.0f / powf(rope_theta, e);
+      const float ang = static_cast<float>(p) * freq;
+      c[p * half + i] = cosf(ang);
+      s[p * half + i] = sinf(ang);
+    }
+  if (hipMemcpy(a->cos_t, c.data(), sizeof(float) * c.size(), hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(a->sin_t, s.data(), sizeof(float) * s.size(), hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemset(a->lens, 0, sizeof(int32_t) * max_batch) != hipSuccess) {
+    set_error("attention table upload failed");
+    kh_sparse_attn_destroy(a);
+    return KH_ERR_HIP;
+  }
+  *out = a;
+  return KH_OK;
+}
+
+extern "C" int kh_sparse_attn_create(int hidden, int num_heads, int num_kv_heads, int head_dim,
+                                     int max_seq, int max_batch, float rope_theta, int kv_dtype,
+                                     const uint16_t* wq_host, const uint16_t* wk_host,
+                                     const uint16_t* wv_host, const uint16_t* wo_host,
+                                     kh_sparse_attn** out) {
+  KH_CHECK_ARG(wq_host && wk_host && wv_host && wo_host, "null weights");
+  kh_sparse_attn* a = nullptr;
+  int rc = attn_alloc(hidden, num_heads, num_kv_heads, head_dim, max_seq, max_batch, rope_theta,
+                      kv_dtype, &a);
+  if (rc != KH_OK) return rc;
+  const size_t H = hidden, qd = (size_t)num_heads * head_dim, kvd = (size_t)num_kv_heads * head_dim;
+  const size_t row = sizeof(uint16_t) * H;
+  uint16_t* ot = static_cast<uint16_t*>(malloc(sizeof(uint16_t) * qd * H));
+  if (!ot) {
+    kh_sparse_attn_destroy(a);
+    set_error("host allocation failed");
+    return KH_ERR_ALLOC;
+  }
+  // wo[hidden][qd] -> WoT[qd][hidden], blocked for locality
+  const size_t TB = 64;
+  for (size_t j0 = 0; j0 < H; j0 += TB)
+    for (size_t i0 = 0; i0 < qd; i0 += TB)
+      for (size_t j = j0; j < std::min(H, j0 + TB); ++j)
+        for (size_t i = i0; i < std::min(qd, i0 + TB); ++i) ot[i * H + j] = wo_host[j * qd + i];
+  hipError_t e = hipMemcpy(a->wkvq, wk_host, row * kvd, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(a->wkvq + kvd * H, wv_host, row * kvd, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(a->wkvq + 2 * kvd * H, wq_host, row * qd, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(a->wot, ot, row * qd, hipMemcpyHostToDevice);
+  free(ot);
+  if (e != hipSuccess) {
+    set_error("attention weight upload failed: %s", hipGetErrorString(e));
+    kh_sparse_attn_destroy(a);
+    return KH_ERR_HIP;
+  }
+  *out = a;
+  return KH_OK;
+}
+
+extern "C" int kh_sparse_attn_create_dev(int hidden, int num_heads, int num_kv_heads,
+                                         int head_dim, int max_seq, int max_batch,
+                                         float rope_theta, int kv_dtype, const uint16_t* wq_dev,
+                                         const uint16_t* wk_dev, const uint16_t* wv_dev,
+                                         const uint16_t* wo_dev, kh_sparse_attn** out) {
+  KH_CHECK_ARG(wq_dev && wk_dev && wv_dev && wo_dev, "null weights");
+  kh_sparse_attn* a = nullptr;
+  int rc = attn_alloc(hidden, num_heads, num_kv_heads, head_dim, max_seq, max_batch, rope_theta,
+                      kv_dtype, &a);
+  if (rc != KH_OK) return rc;
+  const size_t H = hidden, qd = (size_t)num_heads * head_dim, kvd = (size_t)num_kv_heads * head_dim;
+  const size_t row = sizeof(uint16_t) * H;
+  hipError_t e = hipMemcpy(a->wkvq, wk_dev, row * kvd, hipMemcpyDeviceToDevice);
+  if (e == hipSuccess) e = hipMemcpy(a->wkvq + kvd * H, wv_dev, row * kvd, hipMemcpyDeviceToDevice);
+  if (e == hipSuccess) e = hipMemcpy(a->wkvq + 2 * kvd * H, wq_dev, row * qd, hipMemcpyDeviceToDevice);
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(transpose_kernel<uint16_t>, dim3(ceil_div(qd, 32), ceil_div(H, 32)), dim3(256), 0,
+                       0, wo_dev, hidden, static_cast<int>(qd), a->wot);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    set_error("attention weight repack failed: %s", hipGetErrorString(e));
+    kh_sparse_attn_destroy(a);
+    return KH_ERR_HIP;
+  }
+  *out = a;
+  return KH_OK;
+}
+
+extern "C" int kh_sparse_attn_load_cache(kh_sparse_attn* a, int64_t b, const float* k_host,
+                                         const float* v_host, int64_t len) {
+  KH_CHECK_ARG(a != nullptr, "null handle");
+  KH_CHECK_ARG(b >= 0 && b < a->max_batch, "sequence %lld not in [0,%d)", (long long)b, a->max_batch);
+  KH_CHECK_ARG(len >= 0 && len <= a->max_seq, "len %lld not in [0,%d]", (long long)len, a->max_seq);
+  KH_CHECK_ARG(len == 0 || (k_host && v_host), "null cache data");
+  const size_t D = a->d, rows = (size_t)len;
+  const size_t seq_bytes = a->elt() * a->seq_elems();
+  for (int kv = 0; kv < 2; ++kv) {
+    const float* src = kv ? v_host : k_host;
+    char* base = static_cast<char*>(kv ? a->vc : a->kc) + (size_t)b * seq_bytes;
+    for (int hh = 0; hh < a->nkv; ++hh) {
+      if (rows == 0) break;
+      const float* s = src + (size_t)hh * rows * D;
+      char* dst = base + (size_t)hh * a->max_seq * D * a->elt();
+      if (a->kv_f32) {
+        KH_HIP(hipMemcpy(dst, s, sizeof(float) * rows * D, hipMemcpyHostToDevice));
+      } else {
+        std::vector<uint16_t> tmp(rows * D);
+        for (size_t i = 0; i < tmp.size(); ++i) tmp[i] = f32_to_bf16(s[i]);
+        KH_HIP(hipMemcpy(dst, tmp.data(), sizeof(uint16_t) * tmp.size(), hipMemcpyHostToDevice));
+      }
+    }
+  }
+  const int32_t l32 = static_cast<int32_t>(len);
+  KH_HIP(hipMemcpy(a->lens + b, &l32, sizeof(int32_t), hipMemcpyHostToDevice));
+  a->len_host[b] = len;
+  return KH_OK;
+}
+
+extern "C" int kh_sparse_attn_read_cache(const kh_sparse_attn* a, int64_t b, float* k_host,
+                                         float* v_host, int64_t len) {
+  KH_CHECK_ARG(a != nullptr, "null handle");
+  KH_CHECK_ARG(b >= 0 && b < a->max_batch, "sequence %lld not in [0,%d)", (long long)b, a->max_batch);
+  KH_CHECK_ARG(len >= 0 && len <= a->max_seq, "len %lld not in [0,%d]", (long long)len, a->max_seq);
+  KH_CHECK_ARG(len == 0 || (k_host && v_host), "null output");
+  const size_t D = a->d, rows = (size_t)len;
+  const size_t seq_bytes = a->elt() * a->seq_elems();
+  for (int kv = 0; kv < 2 && rows; ++kv) {
+    float* dstf = kv ? v_host : k_host;
+    const char* base = static_cast<const char*>(kv ? a->vc : a->kc) + (size_t)b * seq_bytes;
+    for (int hh = 0; hh < a->nkv; ++hh) {
+      const char* src = base + (size_t)hh * a->max_seq * D * a->elt();
+      float* d = dstf + (size_t)hh * rows * D;
+      if (a->kv_f32) {
+        KH_HIP(hipMemcpy(d, src, sizeof(float) * rows * D, hipMemcpyDeviceToHost));
+      } else {
+        std::vector<uint16_t> tmp(rows * D);
+        KH_HIP(hipMemcpy(tmp.data(), src, sizeof(uint16_t) * tmp.size(), hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < tmp.size(); ++i) {
+          const uint32_t u = static_cast<uint32_t>(tmp[i]) << 16;
+          memcpy(d + i, &u, 4);
+        }
+      }
+    }
+  }
+  return KH_OK;
+}
+
+extern "C" int kh_sparse_attn_cache_len(kh_sparse_attn* a, int64_t b, int64_t* len) {
+  KH_CHECK_ARG(a && len, "null argument");
+  KH_CHECK_ARG(b >= 0 && b < a->max_batch, "sequence %lld not in [0,%d)", (long long)b, a->max_batch);
+  int32_t l = 0;
+  KH_HIP(hipMemcpy(&l, a->lens + b, sizeof(int32_t), hipMemcpyDeviceToHost));
+  a->len_host[b] = l;
+  *len = l;
+  return KH_OK;
+}
+
+extern "C" int kh_sparse_attn_clear(kh_sparse_attn* a, void* stream) {
+  KH_CHECK_ARG(a != nullptr, "null handle");
+  hipLaunchKernelGGL(attn_set_len_kernel, dim3(1), dim3(64), 0, as_stream(stream), a->lens,
+                     a->max_batch, 0);
+  KH_LAUNCHED();
+  std::fill(a->len_host.begin(), a->len_host.end(), 0);
+  return KH_OK;
+}
+
+static int attn_chunk_of(int kv_f32, int D) {
+  if (kv_f32) return D == 64 ? attn_chunk<float, 64>() : D == 128 ? attn_chunk<float, 128>()
+                                                                   : attn_chunk<float, 256>();
+  return D == 64 ? attn_chunk<uint16_t, 64>() : D == 128 ? attn_chunk<uint16_t, 128>()
+                                                         : attn_chunk<uint16_t, 256>();
+}
+
+template <typename KV, int D>
+static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
+                              const int32_t* heads, int nsel, int nsplit, float* po, float2* pml,
+                              hipStream_t st) {
+  const KV* kc = static_cast<const KV*>(a->kc);
+  const KV* vc = static_cast<const KV*>(a->vc);
+  hipLaunchKernelGGL((attn_decode_kernel<KV, D>), dim3(nsplit, nsel, batch), dim3(kAttnThreads), 0,
+                     st, kc, vc, a->y, a->ystride(), a->nkv, a->nh, heads, nsel, a->lens, pos,
+                     a->cos_t, a->sin_t, a->max_seq, 1.0f / sqrtf(static_cast<float>(D)), nsplit,
+                     po, pml);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
+template <int NB>
+static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64_t* pos,
+                       const int32_t* heads, int nsel, float* out, int accumulate,
+                       hipStream_t st) {
+  const int H = a->hidden, D = a->d, qd = a->nh * D, kvrows = 2 * a->kvd();
+  // 1. projections (+ the o_proj row list in the last block)
+  static bool attr_set = false;
+  if (!attr_set) {
+    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_qkv_kernel<NB>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+    attr_set = true;
+  }
+  const size_t lds = std::max(sizeof(float) * std::min(NB, kQkvTok) * H,
+                              2 * sizeof(int) * (size_t)a->nh);
+  if (lds > (size_t)kMaxDynLds) {
+    set_error("hidden %d too large to stage %d tokens", H, std::min(NB, kQkvTok));
+    return KH_ERR_UNSUPPORTED;
+  }
+  const int rows = kvrows + qd;
+  hipLaunchKernelGGL(attn_qkv_kernel<NB>, dim3(rows / kQkvWaves + 1), dim3(64 * kQkvWaves), lds,
+                     st, a->wkvq, x, batch, H, kvrows, D, a->nh, heads, nsel, a->y, a->ystride(),
+                     a->qrows, a->qrows + qd);
+  KH_LAUNCHED();
+  // 2. split-K decode over the cache
+  const int chunk = attn_chunk_of(a->kv_f32, D);
+  const int nsplit = ceil_div(a->max_seq, chunk);
+  const size_t slots = (size_t)batch * nsel * nsplit;
+  float* po = static_cast<float*>(a->po.get(sizeof(float) * slots * D));
+  float2* pml = static_cast<float2*>(a->pml.get(sizeof(float2) * slots));
+  if (!po || !pml) return KH_ERR_ALLOC;
+  int rc;
+  if (a->kv_f32) {
+    rc = D == 64 ? attn_decode_launch<float, 64>(a, batch, pos, heads, nsel, nsplit, po, pml, st)
+       : D == 128 ? attn_decode_launch<float, 128>(a, batch, pos, heads, nsel, nsplit, po, pml, st)
+                  : attn_decode_launch<float, 256>(a, batch, pos, heads, nsel, nsplit, po, pml, st);
+  } else {
+    rc = D == 64 ? attn_decode_launch<uint16_t, 64>(a, batch, pos, heads, nsel, nsplit, po, pml, st)
+       : D == 128 ? attn_decode_launch<uint16_t, 128>(a, batch, pos, heads, nsel, nsplit, po, pml, st)
+                  : attn_decode_launch<uint16_t, 256>(a, batch, pos, heads, nsel, nsplit, po, pml, st);
+  }
+  if (rc != KH_OK) return rc;
+  // 3. combine chunks -> head outputs in union order; append K/V
+  if (a->kv_f32)
+    hipLaunchKernelGGL(attn_combine_kernel<float>, dim3(a->nh, batch), dim3(256), 0, st, po, pml,
+                       nsplit, chunk, heads, nsel, batch, a->nh, a->nkv, D, a->lens, pos, a->cos_t,
+                       a->sin_t, a->max_seq, a->y, a->ystride(), static_cast<float*>(a->kc),
+                       static_cast<float*>(a->vc), a->cat, qd);
+  else
+    hipLaunchKernelGGL(attn_combine_kernel<uint16_t>, dim3(a->nh, batch), dim3(256), 0, st, po,
+                       pml, nsplit, chunk, heads, nsel, batch, a->nh, a->nkv, D, a->lens, pos, a->cos_t,
+                       a->sin_t, a->max_seq, a->y, a->ystride(), static_cast<uint16_t*>(a->kc),
+                       static_cast<uint16_t*>(a->vc), a->cat, qd);
+  KH_LAUNCHED();
+  // 4. o_proj over the union heads' rows of WoT, then the ordered reduce
+  const int nslices = ceil_div(H, kSlice);
+  const int groups = gather_groups(qd, nslices);
+  if (groups == 0) {
+    set_error("num_heads*head_dim %d too large for the o_proj gather", qd);
+    return KH_ERR_UNSUPPORTED;
+  }
+  float* partial = static_cast<float*>(a->partial.get(sizeof(float) * groups * NB * H));
+  if (!partial) return KH_ERR_ALLOC;
+  hipLaunchKernelGGL(gather_rows_kernel<NB>, dim3(nslices, groups), dim3(kDownThreads), 0, st,
+                     a->wot, H, a->qrows, qd, a->qrows + qd, a->cat, qd, batch, groups, partial);
+  KH_LAUNCHED();
+  hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch),
+                     dim3(64 * kRedWaves), 0, st, partial, H, groups, out, accumulate, a->lens,
+                     a->max_seq);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
+extern "C" int kh_sparse_attn_forward(kh_sparse_attn* a, const float* x_dev, int64_t batch,
+                                      const int64_t* pos_dev, const int32_t* heads_dev,
+                                      int n_heads, float* out_dev, int accumulate, void* stream) {
+  KH_CHECK_ARG(a && x_dev && out_dev, "null argument");
+  KH_CHECK_ARG(batch >= 1 && batch <= a->max_batch, "batch %lld not in [1,%d]", (long long)batch,
+               a->max_batch);
+  KH_CHECK_ARG(n_heads >= 0 && n_heads <= 4 * a->nh, "n_heads %d not in [0,%d]", n_heads, 4 * a->nh);
+  KH_CHECK_ARG(n_heads == 0 || heads_dev, "null head list");
+  for (int64_t b = 0; b < batch; ++b)
+    if (a->len_host[b] >= a->max_seq) {
+      set_error("KV cache of sequence %lld is full (%d positions)", (long long)b, a->max_seq);
+      return KH_ERR_CAPACITY;
+    }
+  hipStream_t st = as_stream(stream);
+  // An empty head list is a list whose only entry is skipped.
+  static int32_t* none = nullptr;
+  if (n_heads == 0) {
+    if (!none) {
+      none = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * 16));
+      if (!none) return KH_ERR_ALLOC;
+      KH_HIP(hipMemset(none, 0xff, sizeof(int32_t) * 16));
+    }
+    heads_dev = none;
+    n_heads = 1;
+  }
+  const int b = static_cast<int>(batch);
+  int rc;
+  switch (b <= 1 ? 1 : b <= 2 ? 2 : b <= 4 ? 4 : b <= 8 ? 8 : 16) {
+    case 1: rc = attn_launch<1>(a, x_dev, b, pos_dev, heads_dev, n_heads, out_dev, accumulate, st); break;
+    case 2: rc = attn_launch<2>(a, x_dev, b, pos_dev, heads_dev, n_heads, out_dev, accumulate, st); break;
+    case 4: rc = attn_launch<4>(a, x_dev, b, pos_dev, heads_dev, n_heads, out_dev, accumulate, st); break;
+    case 8: rc = attn_launch<8>(a, x_dev, b, pos_dev, heads_dev, n_heads, out_dev, accumulate, st); break;
+    default: rc = attn_launch<16>(a, x_dev, b, pos_dev, heads_dev, n_heads, out_dev, accumulate, st); break;
+  }
+  if (rc == KH_OK)
+    for (int64_t i = 0; i < batch; ++i) a->len_host[i] += 1;
+  return rc;
+}

@@ -49,6 +49,18 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 void* dev_alloc(size_t bytes);
 void dev_free(void* p);
 
+// Grow-only device buffer owned by a handle (growing frees the old buffer,
+// which hipFree orders after the work already queued on the device).
+struct Scratch {
+  void* p = nullptr;
+  size_t cap = 0;
+  Scratch() = default;
+  Scratch(const Scratch&) = delete;
+  Scratch& operator=(const Scratch&) = delete;
+  ~Scratch();
+  void* get(size_t bytes);
+};
+
 // ---------------------------------------------------------------- device helpers
 constexpr int kWave = 64;
 

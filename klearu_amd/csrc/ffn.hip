@@ -17,25 +17,21 @@
 //                          down rows together, h = silu(g)*u, scales the down
 //                          row and the block's waves are added in LDS into one
 //                          partial row per block;
-//             ffn_reduce   adds the partial rows in block order (a kernel
+//             partials_reduce  adds the partial rows in block order (a kernel
 //                          boundary instead of device-scope fences, which on
 //                          gfx950 write back and invalidate the whole L2).
 //   batch>1:  ffn_gateup   one wave per active neuron, tokens staged in LDS;
-//             ffn_down     (column slice x row group) partials;
-//             ffn_reduce   as above.
+//             gather_rows  (column slice x row group) partials (gather.hpp);
+//             partials_reduce  as above.
 // No float atomics: the summation order is fixed, so outputs are deterministic.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
-#include "common.hpp"
+#include "gather.hpp"
 
 namespace kh {
 
-constexpr int kSlice = 256;      // output columns per down block
-constexpr int kMaxDynLds = 152 * 1024;  // dynamic LDS ceiling (160 KB per CU minus static use)
-constexpr int kMaxGroups = 128;  // row groups per slice (partials)
-constexpr int kDownThreads = 256;
 
 constexpr int kGuWaves = 4;       // neurons per gate/up block
 constexpr int kGuChunks = 8;      // 16-byte chunks per lane held in flight (H <= 4096 in one pass)
@@ -117,91 +113,12 @@ __global__ __launch_bounds__(64 * kGuWaves) void ffn_gateup_kernel(
   }
 }
 
-constexpr int kDownRows = 128;  // max rows per down block (16 per row lane)
-
-// Column slice (256 outputs) x row group.  The group's active ids and h values
-// are staged in LDS; every thread then issues all of its (<= 16) row loads of
-// 16 bytes before accumulating.  Row lane `sub` (0..7, half a wave each) takes
-// rows sub, sub+8, ...; partial sums are reduced across row lanes in LDS and
-// written per group; ffn_reduce_kernel then adds the groups' partials in group
-// order, so the result is deterministic.
-template <int NB>
-__global__ __launch_bounds__(kDownThreads) void ffn_down_kernel(
-    const uint16_t* __restrict__ WdT, int H, const int32_t* __restrict__ active, int n_active,
-    const int32_t* __restrict__ n_active_dev, const float* __restrict__ hbuf, int hstride,
-    int batch, int groups, float* __restrict__ partial) {
-  __shared__ float red[4][NB][kSlice];
-  __shared__ int s_ids[kDownRows];
-  __shared__ float s_h[NB][kDownRows];
-  int n = n_active;
-  if (n_active_dev) n = min(n, *n_active_dev);
-  const int slice = blockIdx.x, grp = blockIdx.y;
-  const int tid = threadIdx.x;
-  const int sub = tid >> 5;
-  const int cl = tid & 31;
-  const int col = slice * kSlice + cl * 8;
-  const bool colok = col < H;
-  const int per = (n + groups - 1) / groups;
-  const int r0 = min(n, grp * per);
-  const int r1 = min(n, r0 + per);
-  const int nr = r1 - r0;  // <= kDownRows by construction of `groups`
-  for (int i = tid; i < nr; i += blockDim.x) s_ids[i] = active[r0 + i];
-  for (int i = tid; i < nr * NB; i += blockDim.x) {
-    const int b = i / nr, r = i - b * nr;
-    s_h[b][r] = b < batch ? hbuf[(size_t)b * hstride + r0 + r] : 0.0f;
-  }
-  __syncthreads();
-  constexpr int RPL = kDownRows / 8;  // rows per row lane
-  uint4 w[RPL];
-#pragma unroll
-  for (int m = 0; m < RPL; ++m) {
-    const int r = sub + 8 * m;
-    w[m] = (r < nr && colok) ? *reinterpret_cast<const uint4*>(WdT + (size_t)s_ids[r] * H + col)
-                             : make_uint4(0, 0, 0, 0);
-  }
-  float acc[NB][8];
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[b][e] = 0.0f;
-#pragma unroll
-  for (int m = 0; m < RPL; ++m) {
-    const int r = sub + 8 * m;
-    if (r >= nr) break;
-    const float wf[8] = {bf16_lo(w[m].x), bf16_hi(w[m].x), bf16_lo(w[m].y), bf16_hi(w[m].y),
-                         bf16_lo(w[m].z), bf16_hi(w[m].z), bf16_lo(w[m].w), bf16_hi(w[m].w)};
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const float hv = s_h[b][r];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[b][e] = fmaf(hv, wf[e], acc[b][e]);
-    }
-  }
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[b][e] += __shfl_xor(acc[b][e], 32, 64);
-  const int wv = tid >> 6;
-  if ((tid & 63) < 32) {
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) red[wv][b][cl * 8 + e] = acc[b][e];
-  }
-  __syncthreads();
-  const int ocol = slice * kSlice + tid;
-  for (int b = 0; b < batch; ++b) {
-    const float sm = (red[0][b][tid] + red[1][b][tid]) + (red[2][b][tid] + red[3][b][tid]);
-    if (ocol < H) partial[((size_t)grp * NB + b) * H + ocol] = sm;
-  }
-}
-
 // Single-token fused FFN: one wave per active neuron, kFuWaves neurons per
 // block.  Each lane issues its gate, up and down-row loads together (the down
 // row does not depend on h), so a wave has 3*H*2 bytes in flight at once; then
 // h = silu(g)*u, the down row is scaled by h (H/64 outputs per lane) and the
 // block adds its waves' rows in LDS in wave order into one partial row,
-// partial[block][H].  ffn_reduce_kernel adds the partials in block order.
+// partial[block][H].  partials_reduce_kernel adds the partials in block order.
 constexpr int kFuWaves = 8;
 constexpr int kFuMaxH = 4096;              // 8 chunks of 16 B per lane per row
 constexpr int kFuChunks = kFuMaxH / 512;
@@ -310,57 +227,6 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
                     (r0.z + r1.z) + (r2.z + r3.z), (r0.w + r1.w) + (r2.w + r3.w));
   }
   if (lane == 0 && live && hbuf) hbuf[item] = h;
-}
-
-// y[b][j] (=, or +=) sum over g of partial[g][b][j].  A block owns 64 columns;
-// its 16 waves take partial rows w, w+16, ... (all loads of a thread issued
-// before the first add), then the 16 wave sums are added in wave order, so the
-// summation order is fixed for a given number of partial rows.
-constexpr int kRedWaves = 16;
-template <int NB>
-__global__ __launch_bounds__(64 * kRedWaves) void ffn_reduce_kernel(const float* __restrict__ partial,
-                                                                    int H, int groups,
-                                                                    float* __restrict__ y,
-                                                                    int accumulate) {
-  __shared__ float sums[kRedWaves][64];
-  const int b = blockIdx.y;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int j = blockIdx.x * 64 + lane;
-  const int jc = min(j, H - 1);
-  constexpr int U = 16;
-  float t = 0.0f;
-  for (int g0 = wave; g0 < groups; g0 += kRedWaves * U) {
-    float v[U];
-#pragma unroll
-    for (int q = 0; q < U; ++q)
-      v[q] = partial[((size_t)min(g0 + kRedWaves * q, groups - 1) * NB + b) * H + jc];
-#pragma unroll
-    for (int q = 0; q < U; ++q)
-      if (g0 + kRedWaves * q < groups) t += v[q];
-  }
-  sums[wave][lane] = t;
-  __syncthreads();
-  if (wave == 0 && j < H) {
-    float tot = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kRedWaves; ++w) tot += sums[w][lane];
-    float* yp = y + (size_t)b * H + j;
-    *yp = accumulate ? (*yp + tot) : tot;
-  }
-}
-
-// dst[i][j] = src[j][i] for a [rows][cols] u16 matrix (32x32 LDS tiles).
-__global__ __launch_bounds__(256) void transpose_u16_kernel(const uint16_t* __restrict__ src,
-                                                            int rows, int cols,
-                                                            uint16_t* __restrict__ dst) {
-  __shared__ uint16_t tile[32][33];
-  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-  for (int r = ty; r < 32; r += 8)
-    if (r0 + r < rows && c0 + tx < cols) tile[r][tx] = src[(size_t)(r0 + r) * cols + c0 + tx];
-  __syncthreads();
-  for (int c = ty; c < 32; c += 8)
-    if (c0 + c < cols && r0 + tx < rows) dst[(size_t)(c0 + c) * rows + r0 + tx] = tile[tx][c];
 }
 
 // RmsNorm::forward (crates/klearu-llm/src/model/rms_norm.rs:43-64): one block
@@ -508,7 +374,7 @@ extern "C" int kh_sparse_ffn_create_dev(int hidden, int inter, const uint16_t* w
   if (e == hipSuccess)
     e = hipMemcpy2D(f->wgu + H, 2 * rowb, w_up_dev, rowb, rowb, I, hipMemcpyDeviceToDevice);
   if (e == hipSuccess) {
-    hipLaunchKernelGGL(transpose_u16_kernel, dim3(ceil_div(I, 32), ceil_div(H, 32)), dim3(256), 0,
+    hipLaunchKernelGGL(transpose_kernel<uint16_t>, dim3(ceil_div(I, 32), ceil_div(H, 32)), dim3(256), 0,
                        0, w_down_dev, hidden, inter, f->wdt);
     e = hipGetLastError();
   }
@@ -552,20 +418,17 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
   hipLaunchKernelGGL(ffn_gateup_kernel<NB>, g1, dim3(64 * kGuWaves), lds1, st, f->wgu, x, batch,
                      H, active, n_active, n_active_dev, f->hbuf, f->inter);
   KH_LAUNCHED();
-  // Row groups: enough blocks to cover the chip, at most kDownRows rows each.
-  int groups = ceil_div(512, f->nslices);
-  groups = std::max(groups, ceil_div(n_active, kDownRows));
-  groups = std::max(1, std::min(groups, ceil_div(n_active, 8)));
-  if (ceil_div(n_active, groups) > kDownRows || groups > kMaxGroups) {
+  const int groups = gather_groups(n_active, f->nslices);
+  if (groups == 0) {
     set_error("n_active %d too large for the down kernel", n_active);
     return KH_ERR_UNSUPPORTED;
   }
   dim3 g2(f->nslices, groups);
-  hipLaunchKernelGGL(ffn_down_kernel<NB>, g2, dim3(kDownThreads), 0, st, f->wdt, H, active,
+  hipLaunchKernelGGL(gather_rows_kernel<NB>, g2, dim3(kDownThreads), 0, st, f->wdt, H, active,
                      n_active, n_active_dev, f->hbuf, f->inter, batch, groups, f->partial);
   KH_LAUNCHED();
-  hipLaunchKernelGGL(ffn_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch), dim3(64 * kRedWaves),
-                     0, st, f->partial, H, groups, y, accumulate);
+  hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch), dim3(64 * kRedWaves),
+                     0, st, f->partial, H, groups, y, accumulate, nullptr, 0);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -599,8 +462,8 @@ extern "C" int kh_sparse_ffn_forward(const kh_sparse_ffn* f, const float* x_dev,
     hipLaunchKernelGGL(ffn_fused1_kernel, dim3(blocks), dim3(64 * kFuWaves), lds, st, f->wgu,
                        f->wdt, x_dev, H, active_dev, n_active, n_active_dev, f->hbuf, f->partial);
     KH_LAUNCHED();
-    hipLaunchKernelGGL(ffn_reduce_kernel<1>, dim3(ceil_div(H, 64), 1), dim3(64 * kRedWaves), 0,
-                       st, f->partial, H, blocks, y_dev, accumulate);
+    hipLaunchKernelGGL(partials_reduce_kernel<1>, dim3(ceil_div(H, 64), 1), dim3(64 * kRedWaves), 0,
+                       st, f->partial, H, blocks, y_dev, accumulate, nullptr, 0);
     KH_LAUNCHED();
     return KH_OK;
   }

@@ -1,0 +1,167 @@
+// gather.hpp -- row-gather kernels shared by the sparse FFN and attention.
+//
+// gather_rows_kernel computes, per column slice and row group, the partial
+// sums  sum_r h[b][r] * M[rows[r]][:]  over a list of rows of a [*][H] BF16
+// matrix (the down projection over active neurons, the output projection over
+// selected heads); partials_reduce_kernel adds the groups' partials in a fixed
+// order.  Splitting at a kernel boundary replaces device-scope fences, which
+// on gfx950 write back and invalidate the whole L2.
+#pragma once
+
+#include "common.hpp"
+
+namespace kh {
+
+constexpr int kSlice = 256;             // output columns per gather block
+constexpr int kMaxDynLds = 152 * 1024;  // dynamic LDS ceiling (160 KB per CU minus static use)
+constexpr int kMaxGroups = 128;         // row groups per slice (partials)
+constexpr int kDownThreads = 256;
+
+constexpr int kDownRows = 128;  // max rows per down block (16 per row lane)
+
+// Column slice (256 outputs) x row group.  The group's active ids and h values
+// are staged in LDS; every thread then issues all of its (<= 16) row loads of
+// 16 bytes before accumulating.  Row lane `sub` (0..7, half a wave each) takes
+// rows sub, sub+8, ...; partial sums are reduced across row lanes in LDS and
+// written per group; ffn_reduce_kernel then adds the groups' partials in group
+// order, so the result is deterministic.
+template <int NB>
+__global__ __launch_bounds__(kDownThreads) void gather_rows_kernel(
+    const uint16_t* __restrict__ WdT, int H, const int32_t* __restrict__ active, int n_active,
+    const int32_t* __restrict__ n_active_dev, const float* __restrict__ hbuf, int hstride,
+    int batch, int groups, float* __restrict__ partial) {
+  __shared__ float red[4][NB][kSlice];
+  __shared__ int s_ids[kDownRows];
+  __shared__ float s_h[NB][kDownRows];
+  int n = n_active;
+  if (n_active_dev) n = min(n, *n_active_dev);
+  const int slice = blockIdx.x, grp = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int sub = tid >> 5;
+  const int cl = tid & 31;
+  const int col = slice * kSlice + cl * 8;
+  const bool colok = col < H;
+  const int per = (n + groups - 1) / groups;
+  const int r0 = min(n, grp * per);
+  const int r1 = min(n, r0 + per);
+  const int nr = r1 - r0;  // <= kDownRows by construction of `groups`
+  for (int i = tid; i < nr; i += blockDim.x) s_ids[i] = active[r0 + i];
+  for (int i = tid; i < nr * NB; i += blockDim.x) {
+    const int b = i / nr, r = i - b * nr;
+    s_h[b][r] = b < batch ? hbuf[(size_t)b * hstride + r0 + r] : 0.0f;
+  }
+  __syncthreads();
+  constexpr int RPL = kDownRows / 8;  // rows per row lane
+  uint4 w[RPL];
+#pragma unroll
+  for (int m = 0; m < RPL; ++m) {
+    const int r = sub + 8 * m;
+    w[m] = (r < nr && colok) ? *reinterpret_cast<const uint4*>(WdT + (size_t)s_ids[r] * H + col)
+                             : make_uint4(0, 0, 0, 0);
+  }
+  float acc[NB][8];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[b][e] = 0.0f;
+#pragma unroll
+  for (int m = 0; m < RPL; ++m) {
+    const int r = sub + 8 * m;
+    if (r >= nr) break;
+    const float wf[8] = {bf16_lo(w[m].x), bf16_hi(w[m].x), bf16_lo(w[m].y), bf16_hi(w[m].y),
+                         bf16_lo(w[m].z), bf16_hi(w[m].z), bf16_lo(w[m].w), bf16_hi(w[m].w)};
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float hv = s_h[b][r];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[b][e] = fmaf(hv, wf[e], acc[b][e]);
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[b][e] += __shfl_xor(acc[b][e], 32, 64);
+  const int wv = tid >> 6;
+  if ((tid & 63) < 32) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[wv][b][cl * 8 + e] = acc[b][e];
+  }
+  __syncthreads();
+  const int ocol = slice * kSlice + tid;
+  for (int b = 0; b < batch; ++b) {
+    const float sm = (red[0][b][tid] + red[1][b][tid]) + (red[2][b][tid] + red[3][b][tid]);
+    if (ocol < H) partial[((size_t)grp * NB + b) * H + ocol] = sm;
+  }
+}
+
+// y[b][j] (=, or +=) sum over g of partial[g][b][j].  A block owns 64 columns;
+// its 16 waves take partial rows w, w+16, ... (all loads of a thread issued
+// before the first add), then the 16 wave sums are added in wave order, so the
+// summation order is fixed for a given number of partial rows.
+constexpr int kRedWaves = 16;
+template <int NB>
+__global__ __launch_bounds__(64 * kRedWaves) void partials_reduce_kernel(const float* __restrict__ partial,
+                                                                    int H, int groups,
+                                                                    float* __restrict__ y,
+                                                                    int accumulate,
+                                                                    int32_t* __restrict__ bump,
+                                                                    int bump_limit) {
+  __shared__ float sums[kRedWaves][64];
+  const int b = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int j = blockIdx.x * 64 + lane;
+  const int jc = min(j, H - 1);
+  constexpr int U = 16;
+  float t = 0.0f;
+  for (int g0 = wave; g0 < groups; g0 += kRedWaves * U) {
+    float v[U];
+#pragma unroll
+    for (int q = 0; q < U; ++q)
+      v[q] = partial[((size_t)min(g0 + kRedWaves * q, groups - 1) * NB + b) * H + jc];
+#pragma unroll
+    for (int q = 0; q < U; ++q)
+      if (g0 + kRedWaves * q < groups) t += v[q];
+  }
+  sums[wave][lane] = t;
+  __syncthreads();
+  if (wave == 0 && j < H) {
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kRedWaves; ++w) tot += sums[w][lane];
+    float* yp = y + (size_t)b * H + j;
+    *yp = accumulate ? (*yp + tot) : tot;
+  }
+  // Optional per-row counter advanced once the row's output is complete
+  // (the KV-cache length of decode attention).
+  if (bump && blockIdx.x == 0 && threadIdx.x == 0 && bump[b] < bump_limit) bump[b] += 1;
+}
+
+// dst[i][j] = src[j][i] for a [rows][cols] matrix (32x32 LDS tiles).
+// (A template, so that each translation unit including this header keeps its own copy.)
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ src, int rows,
+                                                        int cols, T* __restrict__ dst) {
+  __shared__ T tile[32][33];
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int r = ty; r < 32; r += 8)
+    if (r0 + r < rows && c0 + tx < cols) tile[r][tx] = src[(size_t)(r0 + r) * cols + c0 + tx];
+  __syncthreads();
+  for (int c = ty; c < 32; c += 8)
+    if (c0 + c < cols && r0 + tx < rows) dst[(size_t)(c0 + c) * rows + r0 + tx] = tile[tx][c];
+}
+
+// Row groups for gather_rows_kernel: enough blocks to cover the chip, at most
+// kDownRows rows each.  Returns 0 when n_rows cannot be covered.
+inline int gather_groups(int n_rows, int nslices) {
+  int groups = ceil_div(512, nslices);
+  groups = groups > ceil_div(n_rows, kDownRows) ? groups : ceil_div(n_rows, kDownRows);
+  const int cap = ceil_div(n_rows, 8) > 1 ? ceil_div(n_rows, 8) : 1;
+  groups = groups < cap ? groups : cap;
+  if (ceil_div(n_rows, groups) > kDownRows || groups > kMaxGroups) return 0;
+  return groups;
+}
+
+}  // namespace kh

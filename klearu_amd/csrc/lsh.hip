@@ -301,15 +301,6 @@ __global__ void csr_copy_f32_kernel(const float* __restrict__ src, int stride,
 }
 
 // ------------------------------------------------------------------ host helpers
-Scratch::~Scratch() { dev_free(p); }
-void* Scratch::get(size_t bytes) {
-  if (bytes <= cap) return p;
-  dev_free(p);
-  p = dev_alloc(bytes);
-  cap = p ? bytes : 0;
-  return p;
-}
-
 int hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx, int64_t batch,
                       uint32_t* codes, hipStream_t st) {
   if (batch == 0) return KH_OK;

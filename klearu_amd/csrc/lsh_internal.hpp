@@ -4,18 +4,6 @@
 
 #include "common.hpp"
 
-namespace kh {
-
-// Grow-only device buffer owned by a handle.
-struct Scratch {
-  void* p = nullptr;
-  size_t cap = 0;
-  ~Scratch();
-  void* get(size_t bytes);
-};
-
-}  // namespace kh
-
 struct kh_hash_family {
   int dim = 0, k = 0, L = 0;
   std::vector<int8_t> planes_host;  // [L][k][dim]

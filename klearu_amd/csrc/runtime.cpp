@@ -33,6 +33,16 @@ void dev_free(void* p) {
   if (p) (void)hipFree(p);
 }
 
+Scratch::~Scratch() { dev_free(p); }
+
+void* Scratch::get(size_t bytes) {
+  if (bytes <= cap) return p;
+  dev_free(p);
+  p = dev_alloc(bytes);
+  cap = p ? bytes : 0;
+  return p;
+}
+
 }  // namespace kh
 
 extern "C" const char* kh_last_error(void) { return kh::g_last_error.c_str(); }

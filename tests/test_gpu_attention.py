@@ -1,0 +1,188 @@
+"""GPU parity: head-sparse decode attention vs the oracle.
+
+Bar (north_star): BF16-weight outputs within 2e-3 relative, elementwise, with
+an absolute floor of 1e-4 x max|ref| for entries near zero (max-abs printed).
+The oracle restates sparse_attention::forward_sparse with an f32 KvCache.  A
+BF16 cache (the default) stores rows rounded to BF16; the oracle's cache is
+fed the same BF16-valued rows, and in multi-step runs the oracle's appended
+rows are rounded to BF16 too, so both sides hold the same cache.
+Shapes: cfg4 (hidden 4096, 32 heads x 128, cache 2048, 16 heads selected,
+batch 1 and 8) plus small edge cases (GQA, empty cache, duplicate and
+out-of-range head ids, full cache, explicit positions).
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 2e-3
+
+
+def close(got, ref, what=""):
+    scale = float(np.max(np.abs(ref))) if ref.size else 0.0
+    err = float(np.max(np.abs(got - ref))) if ref.size else 0.0
+    print(f"{what} max|ref|={scale:.4g} max-abs-err={err:.3g}")
+    np.testing.assert_allclose(got, ref, rtol=RTOL, atol=1e-4 * scale + 1e-30)
+
+
+def close_row(got, ref, kv, what=""):
+    """An appended cache row.  Both sides round their own f32 projection to
+    BF16, so a projection that differs in its last f32 bit can land one BF16
+    step (2^-8 relative) away."""
+    if kv == 1:
+        return close(got, ref, what)
+    err = float(np.max(np.abs(got - ref)))
+    print(f"{what} max-abs-err={err:.3g} (bf16 rows)")
+    np.testing.assert_allclose(got, ref, rtol=2.0 ** -7, atol=1e-30)
+    assert np.mean(got != ref) < 0.01
+
+
+def bf16_round(orc, a):
+    return orc.bf16_to_f32(orc.bf16_from_f32(np.asarray(a, np.float32)))
+
+
+class Case:
+    """Weights, a preloaded cache per sequence and the oracle's own f32 caches."""
+
+    def __init__(self, orc, rng, hidden, nh, nkv, d, max_seq, batch, pre_len, kv_dtype=0, theta=10000.0):
+        from klearu_amd.attention import SparseAttention
+        self.orc, self.hidden, self.nh, self.nkv, self.d, self.max_seq = orc, hidden, nh, nkv, d, max_seq
+        self.kv_bf16 = kv_dtype == 0
+        b16 = lambda shape, s: orc.bf16_from_f32(rng.normal(0, s, shape).astype(np.float32))  # noqa: E731
+        self.wq = b16((nh * d, hidden), 0.02)
+        self.wk = b16((nkv * d, hidden), 0.02)
+        self.wv = b16((nkv * d, hidden), 0.02)
+        self.wo = b16((hidden, nh * d), 0.02)
+        self.attn = SparseAttention(hidden, nh, nkv, d, self.wq, self.wk, self.wv, self.wo, max_seq, batch,
+                                    theta, kv_dtype)
+        self.cos, self.sin = orc.rope_tables(d, max_seq, theta)
+        self.kc = np.zeros((batch, nkv, max_seq, d), np.float32)
+        self.vc = np.zeros_like(self.kc)
+        self.len = [0] * batch
+        for b in range(batch):
+            L = pre_len[b] if isinstance(pre_len, (list, tuple)) else pre_len
+            k = bf16_round(orc, rng.standard_normal((nkv, L, d)))
+            v = bf16_round(orc, rng.standard_normal((nkv, L, d)))
+            self.kc[b, :, :L] = k
+            self.vc[b, :, :L] = v
+            self.attn.load_cache(b, k, v)
+            self.len[b] = L
+
+    def oracle_step(self, b, x, heads, pos=None):
+        p = self.len[b] if pos is None else pos
+        assert p == self.len[b], "the oracle appends at the RoPE position"
+        kc, vc = self.kc[b].copy(), self.vc[b].copy()
+        out = self.orc.sparse_attention_forward_bf16(self.wq, self.wk, self.wv, self.wo, self.nh, self.nkv, self.d,
+                                                     x, p, self.cos, self.sin, kc, vc, [h for h in heads])
+        if self.kv_bf16:
+            kc[:, p] = bf16_round(self.orc, kc[:, p])
+            vc[:, p] = bf16_round(self.orc, vc[:, p])
+        self.kc[b], self.vc[b] = kc, vc
+        self.len[b] += 1
+        return out
+
+
+@pytest.mark.parametrize("hidden,nh,nkv,d,max_seq,pre,kv", [
+    (512, 8, 8, 64, 400, 300, 0),
+    (512, 8, 2, 128, 300, 129, 0),   # GQA, chunk boundary
+    (256, 4, 4, 256, 200, 100, 0),
+    (512, 8, 8, 64, 400, 255, 1),    # f32 cache
+    (512, 8, 2, 128, 300, 64, 1),
+    (256, 4, 1, 256, 100, 0, 0),     # empty cache: first token
+])
+def test_decode_step_matches_oracle(kh, orc, hidden, nh, nkv, d, max_seq, pre, kv):
+    rng = np.random.default_rng(hidden + nh + d + pre + kv)
+    c = Case(orc, rng, hidden, nh, nkv, d, max_seq, 1, pre, kv)
+    heads = sorted(rng.choice(nh, nh // 2, replace=False).tolist())
+    x = rng.standard_normal(hidden).astype(np.float32)
+    got = c.attn.forward_sparse(x[None], [heads])[0].cpu().numpy()
+    ref = c.oracle_step(0, x, heads)
+    close(got, ref, f"step nh{nh} nkv{nkv} d{d} pre{pre} kv{kv}")
+    assert c.attn.current_len(0) == pre + 1
+    # appended row (roped k, v) equals the oracle's, to rounding
+    k, v = c.attn.read_cache(0, pre + 1)
+    close_row(k[:, pre], c.kc[0][:, pre], kv, "appended k")
+    close_row(v[:, pre], c.vc[0][:, pre], kv, "appended v")
+    np.testing.assert_array_equal(k[:, :pre], c.kc[0][:, :pre])
+
+
+@pytest.mark.parametrize("kv", [0, 1])
+def test_multi_step_decode(kh, orc, kv):
+    rng = np.random.default_rng(5 + kv)
+    c = Case(orc, rng, 384, 6, 3, 64, 64, 1, 60, kv)
+    for step in range(4):   # fills the cache exactly
+        heads = sorted(rng.choice(6, 3, replace=False).tolist())
+        x = rng.standard_normal(384).astype(np.float32)
+        got = c.attn.forward_sparse(x[None], [heads])[0].cpu().numpy()
+        close(got, c.oracle_step(0, x, heads), f"step {step}")
+    assert c.attn.current_len(0) == 64
+    from klearu_amd import KlearuError
+    with pytest.raises(KlearuError) as e:
+        c.attn.forward_sparse(np.zeros((1, 384), np.float32), [[0]])
+    assert e.value.code == -3
+    c.attn.clear()
+    assert c.attn.current_len(0) == 0
+
+
+def test_head_list_edge_cases(kh, orc):
+    rng = np.random.default_rng(9)
+    c = Case(orc, rng, 256, 8, 4, 64, 100, 1, 50)
+    x = rng.standard_normal(256).astype(np.float32)
+    # duplicates add the head output twice; ids >= num_heads are skipped
+    heads = [3, 1, 3, 8, 100]
+    got = c.attn.forward_sparse(x[None], [heads])[0].cpu().numpy()
+    close(got, c.oracle_step(0, x, heads), "duplicates / out of range")
+    # negative ids are skipped too (the reference's ids are unsigned)
+    x = rng.standard_normal(256).astype(np.float32)
+    got = c.attn.forward_sparse(x[None], [[-1, 5, -7]])[0].cpu().numpy()
+    close(got, c.oracle_step(0, x, [5]), "negative ids")
+    # no heads: zero output, but K/V are still appended
+    x = rng.standard_normal(256).astype(np.float32)
+    got = c.attn.forward_sparse(x[None], np.zeros((1, 0), np.int32))[0].cpu().numpy()
+    ref = c.oracle_step(0, x, [])
+    np.testing.assert_array_equal(got, np.zeros(256, np.float32))
+    np.testing.assert_array_equal(ref, np.zeros(256, np.float32))
+    assert c.attn.current_len(0) == 53
+    k, v = c.attn.read_cache(0, 53)
+    close_row(k[:, 52], c.kc[0][:, 52], 0, "k appended with no heads")
+
+
+def test_accumulate_and_explicit_positions(kh, orc):
+    rng = np.random.default_rng(11)
+    c = Case(orc, rng, 256, 4, 4, 64, 80, 2, [10, 30])
+    x = rng.standard_normal((2, 256)).astype(np.float32)
+    heads = [[0, 2], [1, 3]]
+    base = torch.from_numpy(rng.standard_normal((2, 256)).astype(np.float32)).cuda()
+    out = base.clone()
+    c.attn.forward_sparse(x, heads, positions=[10, 30], out=out, accumulate=True)
+    got = (out - base).cpu().numpy()
+    for b in range(2):
+        close(got[b], c.oracle_step(b, x[b], heads[b]), f"seq {b}")
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_cfg4_7b_shape(kh, orc, batch):
+    """cfg4: hidden 4096, 32 heads x 128, KV cache of 2048 positions (2047
+    filled, this step writes the last), 16 of 32 heads per token."""
+    rng = np.random.default_rng(4096 + batch)
+    pre = [2047 - 97 * b for b in range(batch)]   # ragged lengths across the batch
+    c = Case(orc, rng, 4096, 32, 32, 128, 2048, batch, pre)
+    x = rng.standard_normal((batch, 4096)).astype(np.float32)
+    heads = [sorted(rng.choice(32, 16, replace=False).tolist()) for _ in range(batch)]
+    got = c.attn.forward_sparse(x, heads).cpu().numpy()
+    for b in range(batch):
+        close(got[b], c.oracle_step(b, x[b], heads[b]), f"cfg4 b{b}")
+
+
+def test_rejects_bad_shapes(kh, orc):
+    from klearu_amd import KlearuError
+    from klearu_amd.attention import SparseAttention
+    w = np.zeros((4 * 96, 64), np.uint16)
+    wo = np.zeros((64, 4 * 96), np.uint16)
+    with pytest.raises(KlearuError):
+        SparseAttention(64, 4, 4, 96, w, w, w, wo, 16)     # head_dim 96 unsupported
+    w = np.zeros((3 * 64, 64), np.uint16)
+    with pytest.raises(KlearuError):
+        SparseAttention(64, 3, 2, 64, w, np.zeros((128, 64), np.uint16), np.zeros((128, 64), np.uint16),
+                        np.zeros((64, 192), np.uint16), 16)   # 3 heads over 2 kv heads
