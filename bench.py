@@ -1,30 +1,34 @@
 #!/usr/bin/env python3
-"""Benchmark: Deja Vu sparse SwiGLU FFN decode at LLaMA-7B shape on one MI355X.
+"""Benchmark of klearu's activation-sparse inference path on one MI355X.
 
-Workload (the metric's config): 32 layers, hidden 4096,
-intermediate 11008, BF16 weights ~N(0, 0.02), predictor 4096 -> 256 -> 11008
-(BF16-valued), keep ceil(11008 * 0.15) = 1652 neurons, batch-1 decode, synthetic
-activations.  One step = one token through all 32 layers of
+Headline (BASELINE.json metric, configs[2]): Deja Vu sparse SwiGLU FFN decode at
+LLaMA-7B shape -- 32 layers, hidden 4096, intermediate 11008, BF16 weights
+~N(0, 0.02), predictor 4096 -> 256 -> 11008 (BF16-valued), keep ceil(11008 *
+0.15) = 1652 neurons, batch-1 decode.  One step = one token through all 32
+layers of
 
     norm = RmsNorm(hidden); active = predictor.select_top_k(norm, k);
     hidden += sparse_mlp::forward_sparse(norm, active)
 
 (crates/klearu-llm/src/sparse/mod.rs:115-142), captured in one HIP graph.
 
-Reported:
-  value            tokens/s of the full step (predictor + exact top-k + FFN)
-  ffn_only         tokens/s and HBM GB/s of the FFN kernels alone (32 layers,
-                   fixed active sets), the gathered-weight roofline leg
-  roofline         dominant kernel pair (gate/up + down): algorithmic bytes
-                   3*k*H*2 per layer over its measured duration
-  cpu_baseline     the oracle's port of the reference CPU path (AVX2 dots,
-                   sequential predictor/down projection, 1 thread) on a
-                   bounded sample of the same layer shape
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 1|16]
+JSON line fields beyond the driver contract:
+  ffn_only      the FFN calls alone (32 layers, fixed active sets): tokens/s and
+                gathered-weight GB/s -- the roofline leg
+  roofline      one kh_sparse_ffn_forward call (ffn_fused1 + partials_reduce):
+                algorithmic bytes 3*k*H*2 per call over its event-timed duration
+  cpu_baseline  the oracle's port of the reference CPU path (AVX2 dots,
+                sequential predictor / down projection, 1 thread) on a bounded
+                sample of the same layer shape
+  configs       the other BASELINE configs (SLIDE hidden layer, 1.1B FFN, 7B
+                batch 16, head-sparse attention b1/b8, extreme classification),
+                each with GPU throughput, HBM fraction and its CPU port timing
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--legs all|cfg3,...]
 """
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import math
 import os
@@ -38,23 +42,77 @@ sys.path.insert(0, ROOT)
 
 METRIC = "sparse FFN tokens/s @7B shape; gathered-weight HBM GB/s vs roofline"
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ffn_fused1_cfg3_traffic.txt")
+ALL_LEGS = ["cfg3", "cfg3b16", "cfg2", "cfg4", "cfg4b8", "cfg1", "cfg5"]
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def build_model(layers, H, I, R, seed, max_batch):
+def bf16_round(a):
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return (u.astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_bits(a):
+    return (bf16_round(a).view(np.uint32) >> 16).astype(np.uint16)
+
+
+class Timer:
+    """Graph replays timed with HIP events on the stream they run on."""
+
+    def __init__(self, stream):
+        self.s = stream
+
+    def graph(self, fn):
+        import torch
+        with torch.cuda.stream(self.s):
+            fn()                       # eager warm-up: allocates scratch before capture
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=self.s):
+                fn()
+        torch.cuda.synchronize()
+        return g
+
+    def time(self, run, n, warmup=3):
+        import torch
+        with torch.cuda.stream(self.s):
+            for _ in range(warmup):
+                run()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(self.s)
+            for _ in range(n):
+                run()
+            e1.record(self.s)
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n     # ms per run
+
+
+def timed_cpu(fn, seconds, min_reps=3):
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= min_reps:
+            return el / n, n, el
+
+
+# --------------------------------------------------------------------------- Deja Vu FFN
+def build_ffn_model(layers, H, I, R, seed, max_batch):
     import torch
     from klearu_amd import _lib
     from klearu_amd.dejavu import Mlp, SparsityPredictor
-    import ctypes as C
 
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     rng = np.random.default_rng(seed)
     mlps, preds = [], []
-    for l in range(layers):
+    for _ in range(layers):
         ws = [(torch.randn(shape, generator=g, device="cuda") * 0.02).to(torch.bfloat16).view(torch.int16)
               for shape in ((I, H), (I, H), (H, I))]
         h = C.c_void_p()
@@ -64,145 +122,334 @@ def build_model(layers, H, I, R, seed, max_batch):
         m._h, m.hidden_size, m.intermediate_size, m.max_batch = h, H, I, max_batch
         mlps.append(m)
         del ws
-        w1 = _bf16_round(rng.normal(0, 0.02, (R, H)).astype(np.float32))
-        w2 = _bf16_round(rng.normal(0, 0.02, (I, R)).astype(np.float32))
+        w1 = bf16_round(rng.normal(0, 0.02, (R, H)))
+        w2 = bf16_round(rng.normal(0, 0.02, (I, R)))
         preds.append(SparsityPredictor(w1, np.zeros(R, np.float32), w2, np.zeros(I, np.float32)))
     torch.cuda.synchronize()
     return mlps, preds
 
 
-def _bf16_round(a):
-    u = a.view(np.uint32).astype(np.uint64)
-    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
-    return (u.astype(np.uint32) << 16).view(np.float32)
-
-
-def gpu_bench(args):
+def ffn_leg(name, L, H, I, R, frac, B, steps, warmup, seed, model=None, timer=None):
+    """Full decode step and FFN-only graphs of a Deja Vu model; returns metrics."""
     import torch
     from klearu_amd import _lib
     from klearu_amd._dev import ptr, stream_ptr
     from klearu_amd.dejavu import ORDER_ASCENDING, keep_count
 
-    L, H, I, R, B = args.layers, 4096, 11008, 256, args.batch
-    k = keep_count(I, 0.15)
+    k = keep_count(I, frac)
     t0 = time.time()
-    mlps, preds = build_model(L, H, I, R, args.seed, max(B, 1))
-    log(f"[bench] built {L} layers in {time.time() - t0:.1f}s (k={k}, batch={B})")
+    mlps, preds = model if model is not None else build_ffn_model(L, H, I, R, seed, max(B, 1))
+    log(f"[bench] {name}: {L} layers ready in {time.time() - t0:.1f}s (k={k}, batch={B})")
     dev = "cuda"
     w_norm = torch.ones(H, device=dev)
     gen = torch.Generator(device=dev)
-    gen.manual_seed(args.seed + 1)
+    gen.manual_seed(seed + 1)
     hidden = torch.randn(B, H, generator=gen, device=dev)
     norm = torch.empty_like(hidden)
     active = [torch.empty(B, k, dtype=torch.int32, device=dev) for _ in range(L)]
     union = [torch.empty(I, dtype=torch.int32, device=dev) for _ in range(L)]
     ucount = [torch.zeros(1, dtype=torch.int32, device=dev) for _ in range(L)]
-    s = torch.cuda.Stream()
+
+    def ffn_call(l, st):
+        if B == 1:
+            _lib.call("kh_sparse_ffn_forward", mlps[l]._h, ptr(norm), B, ptr(active[l]), k, None, ptr(hidden), 1, st)
+        else:
+            _lib.call("kh_sparse_ffn_forward", mlps[l]._h, ptr(norm), B, ptr(union[l]), I, ptr(ucount[l]),
+                      ptr(hidden), 1, st)
 
     def step():
         st = stream_ptr()
         for l in range(L):
             _lib.call("kh_rmsnorm", ptr(hidden), ptr(w_norm), B, H, 1e-5, ptr(norm), st)
-            _lib.call("kh_predictor_select_top_k", preds[l]._h, ptr(norm), B, k, ORDER_ASCENDING,
-                      ptr(active[l]), st)
-            if B == 1:
-                _lib.call("kh_sparse_ffn_forward", mlps[l]._h, ptr(norm), B, ptr(active[l]), k, None,
-                          ptr(hidden), 1, st)
-            else:
+            _lib.call("kh_predictor_select_top_k", preds[l]._h, ptr(norm), B, k, ORDER_ASCENDING, ptr(active[l]), st)
+            if B > 1:
                 _lib.call("kh_union_active", ptr(active[l]), B, k, I, ptr(union[l]), ptr(ucount[l]), st)
-                _lib.call("kh_sparse_ffn_forward", mlps[l]._h, ptr(norm), B, ptr(union[l]), I,
-                          ptr(ucount[l]), ptr(hidden), 1, st)
+            ffn_call(l, st)
 
     def ffn_only():
         st = stream_ptr()
         for l in range(L):
-            if B == 1:
-                _lib.call("kh_sparse_ffn_forward", mlps[l]._h, ptr(norm), B, ptr(active[l]), k, None,
-                          ptr(hidden), 1, st)
-            else:
-                _lib.call("kh_sparse_ffn_forward", mlps[l]._h, ptr(norm), B, ptr(union[l]), I,
-                          ptr(ucount[l]), ptr(hidden), 1, st)
+            ffn_call(l, st)
 
-    with torch.cuda.stream(s):
-        step()  # eager warm-up (allocates predictor scratch before capture)
-        torch.cuda.synchronize()
-        g_full = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g_full, stream=s):
-            step()
-        g_ffn = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g_ffn, stream=s):
-            ffn_only()
-    torch.cuda.synchronize()
-
-    def timed(graph, n):
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(s):
-            torch.cuda.synchronize()
-            ev0.record(s)
-            for _ in range(n):
-                graph.replay()
-            ev1.record(s)
-            torch.cuda.synchronize()
-        return ev0.elapsed_time(ev1) / n  # ms per replay
-
-    for _ in range(args.warmup):
-        g_full.replay()
-    torch.cuda.synchronize()
+    g_full = timer.graph(step)
+    g_ffn = timer.graph(ffn_only)
     t_wall = time.time()
-    ms_step = timed(g_full, args.steps)
+    ms_step = timer.time(g_full.replay, steps, warmup)
     wall = time.time() - t_wall
-    if args.only != "full":
-        for _ in range(3):
-            g_ffn.replay()
-        ms_ffn = timed(g_ffn, max(args.steps, 20))
-    else:
-        ms_ffn = float("nan")
-
-    # union sizes (batch > 1): bytes per layer depend on |U|
-    if B == 1:
-        rows = [k] * L
-    else:
-        rows = [int(c.item()) for c in ucount]
-    bytes_per_step = sum(3 * r * H * 2 for r in rows)
-    tok_s = B * 1000.0 / ms_step
-    ffn_tok_s = B * 1000.0 / ms_ffn
-    ffn_gbs = bytes_per_step / (ms_ffn * 1e-3) / 1e9
-    return dict(ms_step=ms_step, wall=wall, tok_s=tok_s, ms_ffn=ms_ffn, ffn_tok_s=ffn_tok_s,
-                ffn_gbs=ffn_gbs, bytes_per_layer=bytes_per_step / L, rows=rows, k=k)
+    ms_ffn = timer.time(g_ffn.replay, max(steps, 20))
+    rows = [k] * L if B == 1 else [int(c.item()) for c in ucount]
+    bytes_step = sum(3 * r * H * 2 for r in rows)
+    pred_bytes = L * (R * H + I * R) * 2
+    gbs = bytes_step / (ms_ffn * 1e-3) / 1e9
+    return dict(ms_step=ms_step, wall=wall, tok_s=B * 1000.0 / ms_step, ms_ffn=ms_ffn,
+                ffn_tok_s=B * 1000.0 / ms_ffn, ffn_gbs=gbs, bytes_per_call=bytes_step / L,
+                step_gbs=(bytes_step + pred_bytes) / (ms_step * 1e-3) / 1e9, mean_rows=float(np.mean(rows)), k=k)
 
 
-def cpu_baseline(seconds: float, seed: int):
-    """Time the oracle's port of the reference CPU path on one 7B-shape layer."""
+def cpu_ffn(seconds, seed, H, I, R, frac, layers):
+    """The oracle's port of the reference CPU path on one layer of this shape."""
     import oracle
 
-    H, I, R = 4096, 11008, 256
-    k = int(math.ceil(float(np.float32(I) * np.float32(0.15))))
+    k = int(math.ceil(float(np.float32(I) * np.float32(frac))))
     rng = np.random.default_rng(seed)
-    bf = lambda a: _bf16_round(a.astype(np.float32))
-    wg = bf(rng.normal(0, 0.02, (I, H)))
-    wu = bf(rng.normal(0, 0.02, (I, H)))
-    wd = bf(rng.normal(0, 0.02, (H, I)))
-    pw1 = bf(rng.normal(0, 0.02, (R, H)))
-    pw2 = bf(rng.normal(0, 0.02, (I, R)))
+    wg, wu = bf16_round(rng.normal(0, 0.02, (I, H))), bf16_round(rng.normal(0, 0.02, (I, H)))
+    wd = bf16_round(rng.normal(0, 0.02, (H, I)))
+    pw1, pw2 = bf16_round(rng.normal(0, 0.02, (R, H))), bf16_round(rng.normal(0, 0.02, (I, R)))
     pb1, pb2 = np.zeros(R, np.float32), np.zeros(I, np.float32)
     wn = np.ones(H, np.float32)
     hstate = rng.standard_normal(H).astype(np.float32)
     scratch = np.zeros(H + I + R + k + H + 16, np.float32)
     act = np.zeros(k, np.int64)
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        oracle.lib.or_cpu_dejavu_ffn_layer(wg.reshape(-1), wu.reshape(-1), wd.reshape(-1), wn, 1e-5,
-                                           pw1.reshape(-1), pb1, pw2.reshape(-1), pb2, R, H, I, k,
-                                           hstate, scratch, act)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and n >= 3:
-            break
-    per_layer = el / n
-    return dict(value=1.0 / (32 * per_layer), unit="tokens/s", cores=1, kind="port",
-                sample=f"{n} token-layers of one 7B-shape layer (f32 weights as the reference holds "
-                       f"them) in {el:.1f}s, 1 thread; tokens/s = 1/(32 x {per_layer * 1e3:.1f} ms)")
+    per, n, el = timed_cpu(lambda: oracle.lib.or_cpu_dejavu_ffn_layer(
+        wg.reshape(-1), wu.reshape(-1), wd.reshape(-1), wn, 1e-5, pw1.reshape(-1), pb1, pw2.reshape(-1), pb2,
+        R, H, I, k, hstate, scratch, act), seconds)
+    return dict(value=round(1.0 / (layers * per), 4), unit="tokens/s", cores=1, kind="port",
+                sample=f"{n} token-layers of one layer at this shape (f32 weights as the reference holds "
+                       f"them) in {el:.1f}s, 1 thread; tokens/s = 1/({layers} x {per * 1e3:.2f} ms)")
+
+
+# --------------------------------------------------------------------------- attention (cfg4)
+def attn_leg(name, L, B, steps, warmup, seed, timer, cpu_seconds):
+    import torch
+    from klearu_amd import _lib
+    from klearu_amd._dev import ptr, stream_ptr
+    from klearu_amd.attention import SparseAttention
+    from klearu_amd.dejavu import ORDER_ASCENDING, SparsityPredictor
+
+    H, nh, nkv, d, S, R, k = 4096, 32, 32, 128, 2048, 128, 16
+    pre = S - (warmup + steps + 8)        # every replay appends one position per sequence
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    t0 = time.time()
+    layers, preds = [], []
+    kv = torch.randn(2, nkv, pre, d, generator=g, device="cuda")
+    for _ in range(L):
+        ws = [(torch.randn(shape, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+              for shape in ((nh * d, H), (nkv * d, H), (nkv * d, H), (H, nh * d))]
+        a = SparseAttention(H, nh, nkv, d, *ws, S, B, 10000.0)
+        for b in range(B):
+            a.load_cache_dev(b, kv[0], kv[1])
+        layers.append(a)
+        del ws
+        w1 = bf16_round(rng.normal(0, 0.02, (R, H)))
+        w2 = bf16_round(rng.normal(0, 0.1, (nh, R)))
+        preds.append(SparsityPredictor(w1, np.zeros(R, np.float32), w2, np.zeros(nh, np.float32)))
+    del kv
+    torch.cuda.synchronize()
+    log(f"[bench] {name}: {L} attention layers ready in {time.time() - t0:.1f}s (cache {pre}, batch {B})")
+    w_norm = torch.ones(H, device="cuda")
+    hidden = torch.randn(B, H, generator=g, device="cuda")
+    norm = torch.empty_like(hidden)
+    heads = [torch.empty(B, k, dtype=torch.int32, device="cuda") for _ in range(L)]
+
+    def step():
+        st = stream_ptr()
+        for l in range(L):
+            _lib.call("kh_rmsnorm", ptr(hidden), ptr(w_norm), B, H, 1e-5, ptr(norm), st)
+            _lib.call("kh_predictor_select_top_k", preds[l]._h, ptr(norm), B, k, ORDER_ASCENDING, ptr(heads[l]), st)
+            _lib.call("kh_sparse_attn_forward", layers[l]._h, ptr(norm), B, None, ptr(heads[l]), k, ptr(hidden),
+                      1, st)
+
+    gr = timer.graph(step)
+    ms = timer.time(gr.replay, steps, warmup)
+    ctx = pre + 1 + warmup + steps // 2 + 1          # mean context length over the timed steps
+    uni = float(np.mean([len(np.unique(h.cpu().numpy())) for h in heads]))
+    bytes_layer = (2 * nkv * d * H * 2                 # Wk, Wv (every kv head is appended)
+                   + 2 * uni * d * H * 2               # Wq rows and Wo columns of the union heads
+                   + B * k * ctx * d * 2 * 2           # selected heads' K and V (BF16)
+                   + (R * H + nh * R) * 2)             # head predictor
+    gbs = L * bytes_layer / (ms * 1e-3) / 1e9
+    res = dict(workload=f"cfg4: head-sparse decode attention, 7B shape (32x128 MHA, KV {S} BF16 with RoPE, "
+                        f"predictor 4096->128->32, 16 heads), batch {B}, {L} layers",
+               unit="tokens/s", value=round(B * 1000.0 / ms, 2), ms_per_step=round(ms, 4),
+               hbm_gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4),
+               bytes_per_token_layer=int(bytes_layer / B), mean_context=ctx, union_heads=float(uni))
+    del layers, preds
+    torch.cuda.empty_cache()
+    if cpu_seconds > 0 and B == 1:
+        res["cpu"] = cpu_attention(cpu_seconds, seed, L)
+    return res
+
+
+def cpu_attention(seconds, seed, layers):
+    import oracle
+
+    H, nh, nkv, d, S, R, k = 4096, 32, 32, 128, 2048, 128, 16
+    rng = np.random.default_rng(seed)
+    wq, wk, wv, wo = (bf16_round(rng.normal(0, 0.02, s)) for s in ((nh * d, H), (nkv * d, H), (nkv * d, H),
+                                                                 (H, nh * d)))
+    p1, p2 = bf16_round(rng.normal(0, 0.02, (R, H))), bf16_round(rng.normal(0, 0.1, (nh, R)))
+    b1, b2 = np.zeros(R, np.float32), np.zeros(nh, np.float32)
+    cos_t, sin_t = oracle.rope_tables(d, S, 10000.0)
+    pos = S - 1
+    kc = rng.standard_normal((nkv, S, d)).astype(np.float32)
+    vc = rng.standard_normal((nkv, S, d)).astype(np.float32)
+    hs = rng.standard_normal(H).astype(np.float32)
+    scratch = np.zeros(2 * H + 2 * nh * d + 2 * nkv * d + nh + R + S + 16, np.float32)
+    heads = np.zeros(k, np.int64)
+    wn = np.ones(H, np.float32)
+    per, n, el = timed_cpu(lambda: oracle.lib.or_cpu_sparse_attention_layer(
+        wq.reshape(-1), wk.reshape(-1), wv.reshape(-1), wo.reshape(-1), wn, 1e-5, p1.reshape(-1), b1,
+        p2.reshape(-1), b2, R, H, nh, nkv, d, k, cos_t, sin_t, kc.reshape(-1), vc.reshape(-1), S, pos, hs,
+        scratch, heads), seconds)
+    return dict(value=round(1.0 / (layers * per), 4), unit="tokens/s", cores=1, kind="port",
+                sample=f"{n} token-layers at context {S} in {el:.1f}s, 1 thread; "
+                       f"tokens/s = 1/({layers} x {per * 1e3:.2f} ms)")
+
+
+# --------------------------------------------------------------------------- SLIDE (cfg1, cfg5)
+def slide_cfg1_leg(steps, seed, timer, cpu_seconds):
+    import torch
+    from klearu_amd.lsh import LshConfig
+    from klearu_amd.slide import Layer, LayerConfig
+
+    rng = np.random.default_rng(seed)
+    n, dim, B = 1024, 784, 128
+    W = rng.normal(0, 0.01, (n, dim)).astype(np.float32)
+    b = np.zeros(n, np.float32)
+    cfg = LayerConfig(dim, n, "Relu", LshConfig(num_tables=50, num_hashes=6, bucket_capacity=128), "Vanilla", 2, 0)
+    t0 = time.time()
+    layer = Layer(cfg, W, b, 42)
+    torch.cuda.synchronize()
+    build_ms = (time.time() - t0) * 1e3
+    X = rng.uniform(0, 1, (B, dim)).astype(np.float32)
+    X[rng.uniform(0, 1, (B, dim)) < 0.8] = 0.0
+    Xd = torch.from_numpy(X).cuda()
+    cap = B * max(n, 50 * 128)
+    off = torch.empty(B + 1, dtype=torch.int64, device="cuda")
+    ids = torch.empty(cap, dtype=torch.int32, device="cuda")
+    pre = torch.empty(cap, dtype=torch.float32, device="cuda")
+    act = torch.empty(cap, dtype=torch.float32, device="cuda")
+    from klearu_amd import _lib
+    from klearu_amd._dev import ptr, stream_ptr
+
+    def run():
+        _lib.call("kh_slide_layer_forward", layer._h, ptr(Xd), B, ptr(off), ptr(ids), ptr(pre), ptr(act), cap,
+                  stream_ptr())
+
+    ms = timer.time(run, steps, 3)
+    o = off.cpu().numpy()
+    A = np.diff(o)
+    bytes_call = int(A.sum()) * (dim * 4 + 8) + B * dim * 4 + B * 50 * 16 * 4
+    gbs = bytes_call / (ms * 1e-3) / 1e9
+    res = dict(workload="cfg1: SLIDE hidden layer 1024x784 f32, batch 128 (80% zeros), SimHash K6 L50 FIFO 128, "
+                        "active = union, ReLU", unit="samples/s", value=round(B * 1000.0 / ms, 1),
+               ms_per_step=round(ms, 4), hbm_gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4),
+               mean_active=float(A.mean()), index_build_ms=round(build_ms, 2),
+               note="eager calls: the CSR capacity check synchronises each call")
+    if cpu_seconds > 0:
+        import oracle
+        data, ln, _ = layer.index.buckets()
+        planes = layer.index.hash_family.planes()
+        pl = np.ascontiguousarray(planes).reshape(-1)
+        m = max(n, 50 * 128) + 1
+        oid, opre, oact = np.zeros(m, np.uint32), np.zeros(m, np.float32), np.zeros(m, np.float32)
+        d32, l32 = np.ascontiguousarray(data.reshape(-1)), np.ascontiguousarray(ln.reshape(-1))
+        Wf = W.reshape(-1)
+        i = [0]
+
+        def one():
+            x = X[i[0] % B]
+            i[0] += 1
+            oracle.lib.or_slide_forward(pl, dim, 6, 50, 128, d32, l32, Wf, b, n, x, 0, 0, 2, 0, oid, opre, oact)
+
+        per, cnt, el = timed_cpu(one, cpu_seconds, 10)
+        res["cpu"] = dict(value=round(1.0 / per, 2), unit="samples/s", cores=1, kind="port",
+                          sample=f"{cnt} samples of the same batch (Layer::forward: hash, query, union, "
+                                 f"sequential neuron sums) in {el:.1f}s, 1 thread")
+    del layer
+    return res
+
+
+def slide_cfg5_leg(steps, seed, timer, cpu_seconds):
+    import torch
+    from klearu_amd import _lib
+    from klearu_amd._dev import ptr, stream_ptr
+    from klearu_amd.lsh import LshConfig, SparseVector, csr_batch
+    from klearu_amd.slide import DenseLayer, Layer, LayerConfig
+
+    D_in, Hd, n, B = 135909, 128, 670091, 256
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    W1 = (torch.randn(Hd, D_in, generator=g) * 0.01).numpy()
+    W2 = (torch.randn(n, Hd, generator=g) * 0.01).numpy()
+    b1, b2 = np.zeros(Hd, np.float32), np.zeros(n, np.float32)
+    hidden = DenseLayer(W1, b1, "Relu")
+    cfg = LayerConfig(Hd, n, "Softmax", LshConfig(num_tables=50, num_hashes=9, bucket_capacity=128,
+                                                  bucket_type="Reservoir"), "Vanilla", 2, 0, True)
+    torch.cuda.synchronize()
+    t0 = time.time()
+    out = Layer(cfg, W2, b2, seed)
+    torch.cuda.synchronize()
+    build_ms = (time.time() - t0) * 1e3
+    rows = []
+    for _ in range(B):
+        nnz = int(rng.integers(50, 101))
+        idx = np.sort(rng.choice(D_in, nnz, replace=False)).astype(np.uint32)
+        rows.append(SparseVector(idx, rng.uniform(0, 1, nnz).astype(np.float32), D_in))
+    xo, xi, xv = csr_batch(rows)
+    h = torch.empty(B, Hd, dtype=torch.float32, device="cuda")
+    cap = B * 50 * 128
+    off = torch.empty(B + 1, dtype=torch.int64, device="cuda")
+    ids = torch.empty(cap, dtype=torch.int32, device="cuda")
+    pre = torch.empty(cap, dtype=torch.float32, device="cuda")
+    act = torch.empty(cap, dtype=torch.float32, device="cuda")
+
+    def run():
+        st = stream_ptr()
+        _lib.call("kh_dense_layer_forward_sparse", hidden._h, ptr(xo), ptr(xi), ptr(xv), B, ptr(h), st)
+        _lib.call("kh_slide_layer_forward", out._h, ptr(h), B, ptr(off), ptr(ids), ptr(pre), ptr(act), cap, st)
+
+    ms = timer.time(run, steps, 3)
+    o = off.cpu().numpy()
+    A = np.diff(o)
+    nnz_tot = int(xo[-1].item())
+    bytes_call = nnz_tot * Hd * 4 + B * 50 * 128 * 4 + int(A.sum()) * (Hd * 4 + 4 + 8)
+    gbs = bytes_call / (ms * 1e-3) / 1e9
+    res = dict(workload="cfg5: SLIDE extreme classification, sparse 135909-d inputs (50-100 nnz) -> 128 ReLU -> "
+                        "670091-way sampled softmax (SimHash K9 L50 reservoir 128), batch 256",
+               unit="samples/s", value=round(B * 1000.0 / ms, 1), ms_per_step=round(ms, 4), hbm_gbs=round(gbs, 1),
+               frac=round(gbs / HBM_PEAK_GBS, 4), mean_active=float(A.mean()), index_build_ms=round(build_ms, 1),
+               note="eager calls: the CSR capacity check synchronises each call")
+    if cpu_seconds > 0:
+        import oracle
+        data, ln, _ = out.index.buckets()
+        planes = out.index.hash_family.planes()
+        pl = np.ascontiguousarray(planes).reshape(-1)
+        d32, l32 = np.ascontiguousarray(data.reshape(-1)), np.ascontiguousarray(ln.reshape(-1))
+        m = max(n, 50 * 128) + 1
+        oid, opre, oact = np.zeros(m, np.uint32), np.zeros(m, np.float32), np.zeros(m, np.float32)
+        W2f = W2.reshape(-1)
+        hcpu = np.zeros(Hd, np.float32)
+        i = [0]
+
+        def one():
+            r = rows[i[0] % B]
+            i[0] += 1
+            for j in range(Hd):
+                hcpu[j] = max(oracle.lib.or_neuron_forward_sparse(W1[j], 0.0, r.indices, r.values, r.nnz()), 0.0)
+            oracle.lib.or_slide_forward(pl, Hd, 9, 50, 128, d32, l32, W2f, b2, n, hcpu, 0, 0, 2, 3, oid, opre, oact)
+
+        per, cnt, el = timed_cpu(one, cpu_seconds, 5)
+        res["cpu"] = dict(value=round(1.0 / per, 2), unit="samples/s", cores=1, kind="port",
+                          sample=f"{cnt} samples (sparse hidden layer + Layer::forward with softmax over the "
+                                 f"union, index downloaded from the GPU) in {el:.1f}s, 1 thread")
+    del out, hidden
+    torch.cuda.empty_cache()
+    return res
+
+
+# --------------------------------------------------------------------------- main
+def read_traffic():
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_call:"):
+                return int(float(line.split(":", 1)[1].split()[0]))
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -210,26 +457,65 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--batch", type=int, default=1, choices=[1, 2, 4, 8, 16])
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="headline CPU baseline sample")
+    ap.add_argument("--leg-cpu-seconds", type=float, default=4.0, help="CPU sample per extra config")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "full"], default="all")
+    ap.add_argument("--legs", default="all", help="comma list of " + ",".join(ALL_LEGS))
     args = ap.parse_args()
     ws = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or ws != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is "
-                                   "described in DESIGN.md and not implemented", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is described in "
+                                   "DESIGN.md and not implemented", "n_gpus": args.gpus}))
         return 2
-    r = gpu_bench(args)
-    log(f"[bench] step {r['ms_step']:.3f} ms  ffn-only {r['ms_ffn']:.3f} ms  "
-        f"ffn {r['ffn_gbs']:.0f} GB/s")
+    import torch
+    legs = ALL_LEGS if args.legs == "all" else [x for x in args.legs.split(",") if x]
+    timer = Timer(torch.cuda.Stream())
+    leg_cpu = 0.0 if args.no_cpu else args.leg_cpu_seconds
+    extra = {}
+    # headline: cfg3 batch 1 (and batch 16 on the same layers)
+    model = build_ffn_model(args.layers, 4096, 11008, 256, args.seed, 16)
+    r = ffn_leg("cfg3", args.layers, 4096, 11008, 256, 0.15, 1, args.steps, args.warmup, args.seed, model, timer)
+    log(f"[bench] cfg3 step {r['ms_step']:.3f} ms  ffn-only {r['ms_ffn']:.3f} ms  ffn {r['ffn_gbs']:.0f} GB/s")
+    if "cfg3b16" in legs:
+        r16 = ffn_leg("cfg3b16", args.layers, 4096, 11008, 256, 0.15, 16, min(args.steps, 20), 3, args.seed,
+                      model, timer)
+        extra["cfg3_batch16"] = dict(
+            workload="cfg3 at batch 16 (16 tokens share the union of their top-k sets)", unit="tokens/s",
+            value=round(r16["tok_s"], 2), ms_per_step=round(r16["ms_step"], 4),
+            ffn_only_tokens_per_s=round(r16["ffn_tok_s"], 2), ffn_hbm_gbs=round(r16["ffn_gbs"], 1),
+            frac=round(r16["ffn_gbs"] / HBM_PEAK_GBS, 4), mean_union=r16["mean_rows"])
+        log(f"[bench] cfg3b16 step {r16['ms_step']:.3f} ms  ffn {r16['ffn_gbs']:.0f} GB/s |U|={r16['mean_rows']:.0f}")
+    del model
+    torch.cuda.empty_cache()
+    if "cfg2" in legs:
+        r2 = ffn_leg("cfg2", 22, 2048, 5632, 128, 0.10, 1, min(args.steps, 30), 3, args.seed + 2, None, timer)
+        extra["cfg2"] = dict(workload="cfg2: Deja Vu sparse SwiGLU FFN decode, 1.1B shape (H2048, I5632, 22 layers, "
+                                      "predictor rank 128, keep 10% = 564), batch 1", unit="tokens/s",
+                             value=round(r2["tok_s"], 2), ms_per_step=round(r2["ms_step"], 4),
+                             ffn_only_tokens_per_s=round(r2["ffn_tok_s"], 2), ffn_hbm_gbs=round(r2["ffn_gbs"], 1),
+                             frac=round(r2["ffn_gbs"] / HBM_PEAK_GBS, 4))
+        if leg_cpu > 0:
+            extra["cfg2"]["cpu"] = cpu_ffn(leg_cpu, args.seed, 2048, 5632, 128, 0.10, 22)
+        torch.cuda.empty_cache()
+        log(f"[bench] cfg2 step {r2['ms_step']:.3f} ms  ffn {r2['ffn_gbs']:.0f} GB/s")
+    for name, B in (("cfg4", 1), ("cfg4b8", 8)):
+        if name in legs:
+            extra[name] = attn_leg(name, args.layers, B, min(args.steps, 30), 3, args.seed + 4, timer, leg_cpu)
+            log(f"[bench] {name} {extra[name]['ms_per_step']:.3f} ms  {extra[name]['hbm_gbs']:.0f} GB/s")
+    if "cfg1" in legs:
+        extra["cfg1"] = slide_cfg1_leg(min(args.steps, 30), args.seed, timer, leg_cpu)
+        log(f"[bench] cfg1 {extra['cfg1']['ms_per_step']:.3f} ms  |A|={extra['cfg1']['mean_active']:.0f}")
+    if "cfg5" in legs:
+        extra["cfg5"] = slide_cfg5_leg(min(args.steps, 20), args.seed, timer, leg_cpu)
+        log(f"[bench] cfg5 {extra['cfg5']['ms_per_step']:.3f} ms  |A|={extra['cfg5']['mean_active']:.0f}")
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(args.cpu_seconds, args.seed)
+        cpu = cpu_ffn(args.cpu_seconds, args.seed, 4096, 11008, 256, 0.15, args.layers)
         log(f"[bench] cpu baseline {cpu['value']:.3f} tokens/s")
-    per_layer_ms = r["ms_ffn"] / args.layers
+    per_call_ms = r["ms_ffn"] / args.layers
+    traffic = read_traffic()
     out = {
         "metric": METRIC,
         "value": round(r["tok_s"], 2),
@@ -243,19 +529,19 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16 weights, f32 arithmetic",
         "data": "synthetic (seeded N(0,0.02) BF16 weights, N(0,1) activations)",
-        "config": {"workload": "cfg3: Deja Vu sparse SwiGLU FFN decode, LLaMA-7B shape "
-                               "(H4096, I11008, 32 layers, predictor rank 256, keep 15% = 1652), "
-                               f"batch {args.batch}", "layers": args.layers, "hidden": 4096,
-                   "intermediate": 11008, "k": r["k"], "predictor_rank": 256, "batch": args.batch,
-                   "parallelism": "single GPU"},
+        "config": {"workload": "cfg3: Deja Vu sparse SwiGLU FFN decode, LLaMA-7B shape (H4096, I11008, "
+                               "32 layers, predictor rank 256, keep 15% = 1652), batch 1",
+                   "layers": args.layers, "hidden": 4096, "intermediate": 11008, "k": r["k"],
+                   "predictor_rank": 256, "batch": 1, "parallelism": "single GPU"},
         "ffn_only": {"tokens_per_s": round(r["ffn_tok_s"], 2), "ms_per_token": round(r["ms_ffn"], 4),
                      "hbm_gbs": round(r["ffn_gbs"], 1)},
-        "roofline": {"bound": "hbm", "achieved": round(r["ffn_gbs"], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(r["ffn_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "ffn_gateup + ffn_down per layer",
-                     "bytes_per_launch": int(r["bytes_per_layer"]),
-                     "launch_us": round(per_layer_ms * 1e3, 3)},
+        "step_hbm_gbs": round(r["step_gbs"], 1),
+        "roofline": {"bound": "hbm", "achieved": round(r["ffn_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(r["ffn_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "kh_sparse_ffn_forward (ffn_fused1_kernel + partials_reduce_kernel)",
+                     "bytes_per_launch": int(r["bytes_per_call"]), "launch_us": round(per_call_ms * 1e3, 3)},
         "cpu_baseline": cpu,
+        "configs": extra,
     }
     print(json.dumps(out), flush=True)
     return 0

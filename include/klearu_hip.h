@@ -301,6 +301,9 @@ int kh_sparse_attn_destroy(kh_sparse_attn* a);
  * (KvCache::append repeated, kv_cache.rs:33-48).  Synchronous. */
 int kh_sparse_attn_load_cache(kh_sparse_attn* a, int64_t b, const float* k_host,
                               const float* v_host, int64_t len);
+/* Same from f32 device arrays (e.g. a prefill's K/V), enqueued on `stream`. */
+int kh_sparse_attn_load_cache_dev(kh_sparse_attn* a, int64_t b, const float* k_dev,
+                                  const float* v_dev, int64_t len, void* stream);
 /* Copy positions [0, len) of sequence b back as f32 [nkv][len][d]. Synchronous. */
 int kh_sparse_attn_read_cache(const kh_sparse_attn* a, int64_t b, float* k_host, float* v_host,
                               int64_t len);

@@ -91,6 +91,7 @@ SIGS = {
     "kh_sparse_attn_create_dev": (I, [I, I, I, I, I, I, F, I, P, P, P, P, PP]),
     "kh_sparse_attn_destroy": (I, [P]),
     "kh_sparse_attn_load_cache": (I, [P, I64, P, P, I64]),
+    "kh_sparse_attn_load_cache_dev": (I, [P, I64, P, P, I64, P]),
     "kh_sparse_attn_read_cache": (I, [P, I64, P, P, I64]),
     "kh_sparse_attn_cache_len": (I, [P, I64, P]),
     "kh_sparse_attn_clear": (I, [P, P]),

@@ -72,6 +72,14 @@ class SparseAttention:
             raise ValueError("cache arrays must be [num_kv_heads][len][head_dim]")
         _lib.call("kh_sparse_attn_load_cache", self._h, b, hptr(k), hptr(v), k.shape[1])
 
+    def load_cache_dev(self, b, k, v, stream=None):
+        """Device f32 tensors [num_kv_heads][len][head_dim] -> sequence b (enqueued)."""
+        k = to_device(k, np.float32)
+        v = to_device(v, np.float32)
+        if k.shape != v.shape or k.dim() != 3 or k.shape[0] != self.num_kv_heads or k.shape[2] != self.head_dim:
+            raise ValueError("cache tensors must be [num_kv_heads][len][head_dim]")
+        _lib.call("kh_sparse_attn_load_cache_dev", self._h, b, ptr(k), ptr(v), k.shape[1], stream_ptr(stream))
+
     def read_cache(self, b, length):
         k = np.zeros((self.num_kv_heads, length, self.head_dim), np.float32)
         v = np.zeros_like(k)

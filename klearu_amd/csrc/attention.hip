@@ -388,6 +388,18 @@ __global__ void attn_set_len_kernel(int32_t* __restrict__ lens, int n, int value
   if (i < n) lens[i] = value;
 }
 
+// src [nkv][len][D] f32 -> one sequence's cache rows 0..len-1 (dst [nkv][max_seq][D]).
+template <typename KV>
+__global__ __launch_bounds__(256) void attn_fill_cache_kernel(const float* __restrict__ src,
+                                                              int64_t len, int D, int64_t total,
+                                                              int max_seq, KV* __restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int64_t per = len * D;
+  const int64_t h = i / per, r = i - h * per;
+  store_kv(dst + (h * max_seq) * (int64_t)D + r, src[i]);
+}
+
 }  // namespace kh
 
 using namespace kh;
@@ -587,6 +599,37 @@ extern "C" int kh_sparse_attn_load_cache(kh_sparse_attn* a, int64_t b, const flo
   }
   const int32_t l32 = static_cast<int32_t>(len);
   KH_HIP(hipMemcpy(a->lens + b, &l32, sizeof(int32_t), hipMemcpyHostToDevice));
+  a->len_host[b] = len;
+  return KH_OK;
+}
+
+extern "C" int kh_sparse_attn_load_cache_dev(kh_sparse_attn* a, int64_t b, const float* k_dev,
+                                             const float* v_dev, int64_t len, void* stream) {
+  KH_CHECK_ARG(a != nullptr, "null handle");
+  KH_CHECK_ARG(b >= 0 && b < a->max_batch, "sequence %lld not in [0,%d)", (long long)b, a->max_batch);
+  KH_CHECK_ARG(len >= 0 && len <= a->max_seq, "len %lld not in [0,%d]", (long long)len, a->max_seq);
+  KH_CHECK_ARG(len == 0 || (k_dev && v_dev), "null cache data");
+  hipStream_t st = as_stream(stream);
+  const int64_t total = (int64_t)a->nkv * len * a->d;
+  if (total > 0) {
+    const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
+    const size_t off = (size_t)b * a->seq_elems();
+    if (a->kv_f32) {
+      hipLaunchKernelGGL(attn_fill_cache_kernel<float>, dim3(blocks), dim3(256), 0, st, k_dev, len,
+                         a->d, total, a->max_seq, static_cast<float*>(a->kc) + off);
+      hipLaunchKernelGGL(attn_fill_cache_kernel<float>, dim3(blocks), dim3(256), 0, st, v_dev, len,
+                         a->d, total, a->max_seq, static_cast<float*>(a->vc) + off);
+    } else {
+      hipLaunchKernelGGL(attn_fill_cache_kernel<uint16_t>, dim3(blocks), dim3(256), 0, st, k_dev,
+                         len, a->d, total, a->max_seq, static_cast<uint16_t*>(a->kc) + off);
+      hipLaunchKernelGGL(attn_fill_cache_kernel<uint16_t>, dim3(blocks), dim3(256), 0, st, v_dev,
+                         len, a->d, total, a->max_seq, static_cast<uint16_t*>(a->vc) + off);
+    }
+    KH_LAUNCHED();
+  }
+  hipLaunchKernelGGL(attn_set_len_kernel, dim3(1), dim3(64), 0, st, a->lens + b, 1,
+                     static_cast<int>(len));
+  KH_LAUNCHED();
   a->len_host[b] = len;
   return KH_OK;
 }

@@ -100,6 +100,9 @@ _sig("or_dejavu_sparse_mlp_forward", None, _f32p, _f32p, _f32p, _f32p, _f32p, _f
 _sig("or_cpu_dejavu_ffn_layer", None, _f32p, _f32p, _f32p, _f32p, _f, _f32p, _f32p, _f32p, _f32p, _int,
      _int, _int, _i64, _f32p, _f32p, _i64p)
 
+_sig("or_cpu_sparse_attention_layer", None, _f32p, _f32p, _f32p, _f32p, _f32p, _f, _f32p, _f32p, _f32p,
+     _f32p, _int, _int, _int, _int, _int, _i64, _f32p, _f32p, _f32p, _f32p, _i64, _i64, _f32p, _f32p,
+     _i64p)
 _sig("or_slide_forward", _i64, _i8p, _int, _int, _int, _int, _u32p, _u32p, _f32p, _f32p, _int, _f32p,
      _int, _int, _int, _int, _u32p, _f32p, _f32p)
 

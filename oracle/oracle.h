@@ -124,6 +124,22 @@ void or_sparse_attention_forward_bf16(const uint16_t* wq, const uint16_t* wk, co
                                       float* v_cache, int64_t max_seq, const int64_t* heads,
                                       int64_t n_heads, float* out);
 
+/* ---- timed CPU ports (oracle_avx2.c) ---- */
+float or_avx2_dense_dot(const float* a, const float* b, int64_t n);
+float or_avx2_sparse_dot_dense(const uint32_t* idx, const float* val, int64_t nnz,
+                               const float* dense);
+void or_cpu_dejavu_ffn_layer(const float* wg, const float* wu, const float* wd,
+                             const float* w_norm, float eps, const float* pw1, const float* pb1,
+                             const float* pw2, const float* pb2, int hid_p, int hidden, int inter,
+                             int64_t k, float* hstate, float* scratch, int64_t* active_out);
+void or_cpu_sparse_attention_layer(const float* wq, const float* wk, const float* wv,
+                                   const float* wo, const float* w_norm, float eps,
+                                   const float* pw1, const float* pb1, const float* pw2,
+                                   const float* pb2, int hid_p, int hidden, int nh, int nkv,
+                                   int d, int64_t k, const float* cos_t, const float* sin_t,
+                                   float* k_cache, float* v_cache, int64_t max_seq, int64_t pos,
+                                   float* hstate, float* scratch, int64_t* heads_out);
+
 /* ---- klearu-dejavu mlp.rs / attention.rs / transformer Linear (toy layer, f32 + bias) ---- */
 void or_dejavu_linear_forward_sparse(const float* w, const float* bias, int in_f,
                                      const float* x, const int64_t* idx, int64_t n, float* out);

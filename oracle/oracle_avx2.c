@@ -106,3 +106,80 @@ void or_cpu_dejavu_ffn_layer(const float* wg, const float* wu, const float* wd,
   }
   for (int j = 0; j < hidden; ++j) hstate[j] = hstate[j] + y[j];
 }
+
+/* Linear::forward (model/linear.rs:79-104): one AVX2 dot per output row. */
+static void avx2_linear(const float* w, int out_f, int in_f, const float* x, float* y) {
+  for (int o = 0; o < out_f; ++o) y[o] = or_avx2_dense_dot(w + (int64_t)o * in_f, x, in_f);
+}
+
+/*
+ * One token of the reference's head-sparse attention block for one layer
+ * (crates/klearu-llm/src/sparse/mod.rs:76-113 decode path):
+ *   norm = RmsNorm(hidden); heads = predictor.select_top_k(norm, k)
+ *   out = sparse_attention::forward_sparse(norm, pos, heads) (sparse_attention.rs:7-79)
+ *   hidden += out
+ * f32 weights wq[nh*d][H], wk/wv[nkv*d][H], wo[H][nh*d]; caches [nkv][max_seq][d]
+ * with pos valid rows (row pos is written).  Projections use the AVX2 dot, the
+ * rest is the reference's sequential scalar code.  scratch: 2*H + nh*d*2 + 2*nkv*d
+ * + n_out + hid_p + max_seq floats.
+ */
+void or_cpu_sparse_attention_layer(const float* wq, const float* wk, const float* wv,
+                                   const float* wo, const float* w_norm, float eps,
+                                   const float* pw1, const float* pb1, const float* pw2,
+                                   const float* pb2, int hid_p, int hidden, int nh, int nkv,
+                                   int d, int64_t k, const float* cos_t, const float* sin_t,
+                                   float* k_cache, float* v_cache, int64_t max_seq, int64_t pos,
+                                   float* hstate, float* scratch, int64_t* heads_out) {
+  const int qd = nh * d, kvd = nkv * d, half = d / 2, group = nh / nkv;
+  float* norm = scratch;
+  float* q = norm + hidden;
+  float* kk = q + qd;
+  float* vv = kk + kvd;
+  float* concat = vv + kvd;
+  float* out = concat + qd;
+  float* scores = out + hidden;
+  float* ph = scores + nh;
+  float* sc = ph + hid_p;
+  memcpy(norm, hstate, sizeof(float) * (size_t)hidden);
+  or_rmsnorm(norm, w_norm, hidden, eps);
+  or_predictor_predict(pw1, pb1, pw2, pb2, hidden, hid_p, nh, norm, scores, ph);
+  or_select_top_k(scores, nh, k, heads_out);
+  avx2_linear(wq, qd, hidden, norm, q);
+  avx2_linear(wk, kvd, hidden, norm, kk);
+  avx2_linear(wv, kvd, hidden, norm, vv);
+  for (int h = 0; h < nh; ++h) or_rope_apply(q + h * d, half, cos_t, sin_t, pos);
+  for (int h = 0; h < nkv; ++h) or_rope_apply(kk + h * d, half, cos_t, sin_t, pos);
+  for (int h = 0; h < nkv; ++h) {
+    memcpy(k_cache + ((int64_t)h * max_seq + pos) * d, kk + h * d, sizeof(float) * (size_t)d);
+    memcpy(v_cache + ((int64_t)h * max_seq + pos) * d, vv + h * d, sizeof(float) * (size_t)d);
+  }
+  const int64_t seq = pos + 1;
+  const float inv_sqrt = 1.0f / sqrtf((float)d);
+  memset(concat, 0, sizeof(float) * (size_t)qd);
+  for (int64_t a = 0; a < k && a < nh; ++a) {
+    const int64_t h = heads_out[a];
+    const int64_t kvh = h / group;
+    const float* qh = q + h * d;
+    for (int64_t j = 0; j < seq; ++j)
+      sc[j] = or_avx2_dense_dot(qh, k_cache + (kvh * max_seq + j) * d, d) * inv_sqrt;
+    float mx = -INFINITY;
+    for (int64_t j = 0; j < seq; ++j) mx = fmaxf(mx, sc[j]);
+    float sum = 0.0f;
+    for (int64_t j = 0; j < seq; ++j) {
+      sc[j] = expf(sc[j] - mx);
+      sum = sum + sc[j];
+    }
+    const float inv = 1.0f / sum;
+    for (int64_t j = 0; j < seq; ++j) sc[j] = sc[j] * inv;
+    float* ho = concat + h * d;
+    for (int64_t j = 0; j < seq; ++j) {
+      const float* vj = v_cache + (kvh * max_seq + j) * d;
+      for (int e = 0; e < d; ++e) {
+        float p = sc[j] * vj[e];
+        ho[e] = ho[e] + p;
+      }
+    }
+  }
+  avx2_linear(wo, hidden, qd, concat, out);
+  for (int j = 0; j < hidden; ++j) hstate[j] = hstate[j] + out[j];
+}

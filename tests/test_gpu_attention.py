@@ -175,6 +175,23 @@ def test_cfg4_7b_shape(kh, orc, batch):
         close(got[b], c.oracle_step(b, x[b], heads[b]), f"cfg4 b{b}")
 
 
+@pytest.mark.parametrize("kv", [0, 1])
+def test_load_cache_dev_matches_host_load(kh, orc, kv):
+    rng = np.random.default_rng(21 + kv)
+    c = Case(orc, rng, 256, 4, 2, 64, 50, 2, [0, 0], kv)
+    k = rng.standard_normal((2, 37, 64)).astype(np.float32)
+    v = rng.standard_normal((2, 37, 64)).astype(np.float32)
+    c.attn.load_cache(0, k, v)
+    c.attn.load_cache_dev(1, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    assert c.attn.current_len(0) == 37 and c.attn.current_len(1) == 37
+    k0, v0 = c.attn.read_cache(0, 37)
+    k1, v1 = c.attn.read_cache(1, 37)
+    np.testing.assert_array_equal(k0, k1)
+    np.testing.assert_array_equal(v0, v1)
+    want = k if kv == 1 else bf16_round(orc, k)
+    np.testing.assert_array_equal(k1, want)
+
+
 def test_rejects_bad_shapes(kh, orc):
     from klearu_amd import KlearuError
     from klearu_amd.attention import SparseAttention

@@ -204,3 +204,62 @@ def test_dejavu_toy_mlp_sparse_equals_dense(orc):
     u = wu.astype(np.float64) @ x
     ref = wd.astype(np.float64) @ (g / (1 + np.exp(-g)) * u)
     np.testing.assert_allclose(y, ref, atol=1e-4)
+
+
+def _bf(orc, rng, shape, s=0.02):
+    return orc.bf16_to_f32(orc.bf16_from_f32(rng.normal(0, s, shape).astype(np.float32)))
+
+
+def test_cpu_ffn_port_equals_composition(orc):
+    """The timed AVX2 port (bench cpu_baseline) computes exactly rmsnorm ->
+    predictor -> stable top-k -> sparse SwiGLU -> residual of the portable oracle."""
+    rng = np.random.default_rng(3)
+    H, I, R, k = 64, 160, 16, 24
+    wg, wu, wd = _bf(orc, rng, (I, H)), _bf(orc, rng, (I, H)), _bf(orc, rng, (H, I))
+    p1, p2 = _bf(orc, rng, (R, H)), _bf(orc, rng, (I, R))
+    b1, b2 = np.zeros(R, np.float32), np.zeros(I, np.float32)
+    wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    x = rng.standard_normal(H).astype(np.float32)
+    hs = x.copy()
+    scratch = np.zeros(H + I + R + k + H + 16, np.float32)
+    act = np.zeros(k, np.int64)
+    orc.lib.or_cpu_dejavu_ffn_layer(wg.reshape(-1), wu.reshape(-1), wd.reshape(-1), wn, 1e-5, p1.reshape(-1),
+                                    b1, p2.reshape(-1), b2, R, H, I, k, hs, scratch, act)
+    norm = orc.rmsnorm(x, wn, 1e-5)
+    scores, _ = orc.predictor_predict(p1, b1, p2, b2, norm)
+    sel = orc.select_top_k(scores, k)
+    np.testing.assert_array_equal(act, sel)
+    y, _ = orc.sparse_mlp_forward_bf16(orc.bf16_from_f32(wg), orc.bf16_from_f32(wu), orc.bf16_from_f32(wd),
+                                       norm, sel)
+    np.testing.assert_array_equal(hs, x + y)
+
+
+def test_cpu_attention_port_equals_composition(orc):
+    rng = np.random.default_rng(4)
+    H, nh, nkv, d, R, k, S, pos = 128, 8, 4, 16, 12, 3, 40, 17
+    wq, wk, wv, wo = (_bf(orc, rng, s) for s in ((nh * d, H), (nkv * d, H), (nkv * d, H), (H, nh * d)))
+    p1, p2 = _bf(orc, rng, (R, H)), _bf(orc, rng, (nh, R))
+    b1, b2 = np.zeros(R, np.float32), np.zeros(nh, np.float32)
+    wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    cos_t, sin_t = orc.rope_tables(d, S, 10000.0)
+    kc = np.zeros((nkv, S, d), np.float32)
+    vc = np.zeros_like(kc)
+    kc[:, :pos] = rng.standard_normal((nkv, pos, d))
+    vc[:, :pos] = rng.standard_normal((nkv, pos, d))
+    kc2, vc2 = kc.copy(), vc.copy()
+    x = rng.standard_normal(H).astype(np.float32)
+    hs = x.copy()
+    scratch = np.zeros(2 * H + 2 * nh * d + 2 * nkv * d + nh + R + S + 16, np.float32)
+    heads = np.zeros(k, np.int64)
+    orc.lib.or_cpu_sparse_attention_layer(wq.reshape(-1), wk.reshape(-1), wv.reshape(-1), wo.reshape(-1), wn,
+                                          1e-5, p1.reshape(-1), b1, p2.reshape(-1), b2, R, H, nh, nkv, d, k,
+                                          cos_t, sin_t, kc.reshape(-1), vc.reshape(-1), S, pos, hs, scratch,
+                                          heads)
+    norm = orc.rmsnorm(x, wn, 1e-5)
+    scores, _ = orc.predictor_predict(p1, b1, p2, b2, norm)
+    sel = orc.select_top_k(scores, k)
+    np.testing.assert_array_equal(heads, sel)
+    out = orc.sparse_attention_forward_bf16(*(orc.bf16_from_f32(w) for w in (wq, wk, wv, wo)), nh, nkv, d, norm,
+                                            pos, cos_t, sin_t, kc2, vc2, sel)
+    np.testing.assert_array_equal(hs, x + out)
+    np.testing.assert_array_equal(kc, kc2)
