@@ -254,8 +254,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     float d = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) d = fmaf(qv[e], kf[e], d);
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+    if constexpr (LPR <= 16) {
+      d = group_sum<LPR>(d);
+    } else {
+      d = group_sum<16>(d);
+      d += __shfl_xor(d, 16, 64);
+      if constexpr (LPR == 64) d += __shfl_xor(d, 32, 64);
+    }
     if (sl == 0 && j - start < n) s_p[j - start] = d * inv_sqrt;
   }
   lds_barrier();

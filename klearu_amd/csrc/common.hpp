@@ -78,16 +78,78 @@ __host__ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
-// Sum over the 64 lanes of a wave (result valid in every lane).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+// ---------------------------------------------------------------- DPP lane moves
+// Cross-lane moves through the DPP operand modifier (GFX9 encodings): a VALU
+// operand read from another lane, with no LDS round trip (ds_bpermute, behind
+// __shfl*, costs an LDS latency per step).  Every lane of the wave must be
+// active where these are used.
+constexpr int kDppQuadSwap1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppRowMirror = 0x140;     // lane i <- 15 - i within a row of 16
+constexpr int kDppRowHalfMirror = 0x141; // lane i <- 7 - i within each half row
+constexpr int kDppRowBcast15 = 0x142;    // lane 15 of row r -> row r + 1
+constexpr int kDppRowBcast31 = 0x143;    // lane 31 -> rows 2 and 3
+
+// Value of lane (permutation CTRL); rows outside ROWS, and lanes whose source
+// lies outside their row, read 0.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ int dpp(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xf, false);
+}
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float dppf(float v) {
+  return __int_as_float(dpp<CTRL, ROWS>(__float_as_int(v)));
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Sum over each aligned group of G lanes (G = 2, 4, 8 or 16); every lane of
+// the group gets the same value (a butterfly: each step adds a lane pairing).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dppf<kDppQuadSwap1>(v);
+  if (G >= 4) v += dppf<kDppQuadSwap2>(v);
+  if (G >= 8) v += dppf<kDppRowHalfMirror>(v);
+  if (G >= 16) v += dppf<kDppRowMirror>(v);
   return v;
 }
+
+// Sum over the 64 lanes of a wave (result valid in every lane).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = group_sum<16>(v);
+  return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+  v = fmaxf(v, dppf<kDppQuadSwap1>(v));
+  v = fmaxf(v, dppf<kDppQuadSwap2>(v));
+  v = fmaxf(v, dppf<kDppRowHalfMirror>(v));
+  v = fmaxf(v, dppf<kDppRowMirror>(v));
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)),
+               fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)dpp<kDppQuadSwap1>((int)v));
+  v = max(v, (uint32_t)dpp<kDppQuadSwap2>((int)v));
+  v = max(v, (uint32_t)dpp<kDppRowHalfMirror>((int)v));
+  v = max(v, (uint32_t)dpp<kDppRowMirror>((int)v));
+  return max(max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16)),
+             max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48)));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  return ~wave_max_u32(~v);
+}
+// Inclusive prefix sum over the lanes of a wave (Hillis-Steele within rows
+// of 16, then the row totals carried across rows).
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += dpp<kDppRowShr1>(x);
+  x += dpp<kDppRowShr2>(x);
+  x += dpp<kDppRowShr4>(x);
+  x += dpp<kDppRowShr8>(x);
+  x += dpp<kDppRowBcast15, 0xa>(x);
+  x += dpp<kDppRowBcast31, 0xc>(x);
+  return x;
 }
 
 // expf exactly as glibc computes it on x86-64 (the libm behind Rust's
@@ -163,32 +225,40 @@ __device__ __forceinline__ uint32_t f32_key(float f) {
 
 // Exclusive prefix sum of v over the block (blockDim.x a multiple of 64, at
 // most 1024).  wsum: shared scratch of blockDim.x/64 ints; *total (shared)
-// receives the block total.  Contains three __syncthreads.
+// receives the block total.  Contains two __syncthreads.
 __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int* total) {
-  // inclusive scan within the wave
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
+  const int x = wave_incl_scan(v);
   if (lane == 63) wsum[w] = x;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int acc = 0;
-    const int nw = blockDim.x >> 6;
-    for (int i = 0; i < nw; ++i) {
-      int t = wsum[i];
-      wsum[i] = acc;
-      acc += t;
-    }
-    *total = acc;
+  const int nw = blockDim.x >> 6;
+  int before = 0, tot = 0;
+  for (int i = 0; i < nw; ++i) {
+    const int t = wsum[i];
+    before += i < w ? t : 0;
+    tot += t;
   }
+  if (threadIdx.x == 0) *total = tot;
   __syncthreads();
-  const int r = wsum[w] + x - v;
+  return before + x - v;
+}
+
+// Same for unsigned 32-bit sums (wrapping arithmetic), e.g. two packed 16-bit counts.
+__device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* wsum) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint32_t x = v;
+  x += (uint32_t)dpp<kDppRowShr1>((int)x);
+  x += (uint32_t)dpp<kDppRowShr2>((int)x);
+  x += (uint32_t)dpp<kDppRowShr4>((int)x);
+  x += (uint32_t)dpp<kDppRowShr8>((int)x);
+  x += (uint32_t)dpp<kDppRowBcast15, 0xa>((int)x);
+  x += (uint32_t)dpp<kDppRowBcast31, 0xc>((int)x);
+  if (lane == 63) wsum[w] = x;
   __syncthreads();
-  return r;
+  uint32_t before = 0;
+  for (int i = 0; i < w; ++i) before += wsum[i];
+  __syncthreads();
+  return before + x - v;
 }
 
 // Workgroup barrier that waits only for LDS traffic.  __syncthreads() on gfx9

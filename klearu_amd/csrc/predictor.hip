@@ -14,7 +14,7 @@
 // and the shared input value is a wave-uniform (scalar) load.
 //
 // Top-k is a radix select over order-preserving 32-bit keys of the scores
-// (4 passes of 8 bits with LDS histograms) that finds the exact k-th key T;
+// (passes of up to 11 bits with LDS histograms) that finds the exact k-th key T;
 // the selected set is {key > T} plus the lowest-index entries with key == T,
 // which is exactly what the reference's stable descending sort keeps.
 #include <cstring>
@@ -45,18 +45,22 @@ template <> struct Blk8<float> {
   static __device__ __forceinline__ V zero() { return V{make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0)}; }
 };
 
-// Layer 1 (long chains).  One block = one consumer wave (wave 0, 64 chains =
-// 64 hidden units of one input row) + kProd producer waves.  The producers
-// prefetch the blocked weights [ceil(n_in/8)][hid][8] kPre stages ahead in
-// registers, form the rounded products w*x for a stage of 64 steps and write
-// them to a two-stage LDS ring laid out [stage][step/4][chain][4]; the consumer
-// adds them in step order with one ds_read_b128 per four steps.  Output
-// h[b][i] = max(sum + b1[i], 0).
-constexpr int kProd = 4;          // producer waves
-constexpr int kStage = 64;        // steps per stage (8 blocks of 8)
-constexpr int kPre = 16;          // stages of weights in flight per producer
-constexpr int kL1Threads = 64 * (1 + kProd);
+// Layer 1 (long chains).  A block owns kL1Chains consecutive hidden units: one
+// consumer wave (lanes < kL1Chains, one chain each) adds the products in step
+// order while one producer wave streams the blocked weights
+// [ceil(n_in/8)][hid][8] kL1Pre stages ahead in registers, forms the rounded
+// products w*x of a stage of kL1Stage steps and writes them to a two-stage LDS
+// ring laid out [stage][step/4][chain][4], so that the consumer reads four steps
+// with one ds_read_b128.  Few chains per block spread the weight stream over
+// many CUs; the time is then set by the chain itself (one dependent add per
+// step, about 8 cycles on gfx950).  Output h[b][i] = max(sum + b1[i], 0).
+constexpr int kL1Chains = 8;
+constexpr int kL1Stage = 128;     // steps per stage
+constexpr int kL1Pre = 8;         // stages of weights in flight in the producer
+constexpr int kL1Threads = 128;   // consumer wave + producer wave
+constexpr int kL1Q = (kL1Stage / 8) * kL1Chains / 64;  // weight loads per producer lane per stage
 constexpr int kMaxL1In = 8192;    // x row staged in LDS
+static_assert(kL1Q * 64 == (kL1Stage / 8) * kL1Chains, "stage tiling");
 
 template <typename W>
 __global__ __launch_bounds__(kL1Threads) void pred_l1_kernel(
@@ -65,93 +69,95 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_kernel(
   using B8 = Blk8<W>;
   using V = typename B8::V;
   __shared__ __align__(16) float xs[kMaxL1In];
-  __shared__ float4 ring[2][kStage / 4][64];
+  __shared__ float4 ring[2][kL1Stage / 4][kL1Chains];
   const int b = blockIdx.y;
-  const int c0 = blockIdx.x * 64;
+  const int c0 = blockIdx.x * kL1Chains;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int chain = c0 + lane;
-  const bool chain_ok = chain < hid;
-  const int nblk = (n_in + 7) >> 3;               // 8-step blocks
-  const int nst = (n_in + kStage - 1) / kStage;   // stages
+  const int nblk = (n_in + 7) >> 3;                 // 8-step blocks
+  const int nst = (n_in + kL1Stage - 1) / kL1Stage;  // stages
+  const float bv = bias[min(c0 + (lane & (kL1Chains - 1)), hid - 1)];  // loaded with x, used at the end
   if ((n_in & 3) == 0)
     stage_f4(reinterpret_cast<float4*>(xs), reinterpret_cast<const float4*>(x + (size_t)b * n_in),
              n_in >> 2);
   else
     for (int j = threadIdx.x; j < n_in; j += blockDim.x) xs[j] = x[(size_t)b * n_in + j];
   const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
-  // producer wave pw owns blocks pw and pw + kProd of every stage
-  const int pw = wave - 1;
-  V pre[kPre][2];
-  // Unconditional (clamped) loads: out-of-range blocks and chains are never
-  // consumed, and branch-free loads let the compiler count them precisely
-  // (a conditional load makes it wait for every outstanding load).
-  const int chain_c = chain_ok ? chain : hid - 1;
-  auto load_stage = [&](int st, V (&r)[2]) {
+  V pre[kL1Pre][kL1Q];
+  // Producer lane l, load q covers pair p = l + 64q: 8-step block p / kL1Chains
+  // of the stage and chain p % kL1Chains.  Loads are unconditional (clamped):
+  // out-of-range blocks and chains are never consumed, and branch-free loads
+  // let the compiler count them precisely (a conditional load makes it wait
+  // for every outstanding load).
+  auto load_stage = [&](int st, V (&r)[kL1Q]) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int jb = min(st * (kStage / 8) + pw + kProd * q, nblk - 1);
-      r[q] = wv[(size_t)jb * hid + chain_c];
+    for (int q = 0; q < kL1Q; ++q) {
+      const int pr = lane + 64 * q;
+      const int jb = min(st * (kL1Stage / 8) + pr / kL1Chains, nblk - 1);
+      const int ch = min(c0 + pr % kL1Chains, hid - 1);
+      r[q] = wv[(size_t)jb * hid + ch];
     }
   };
-  auto make_stage = [&](int st, const V (&r)[2]) {
-    float4(*dst)[64] = ring[st & 1];
+  auto make_stage = [&](int st, const V (&r)[kL1Q]) {
+    float4(*dst)[kL1Chains] = ring[st & 1];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int jl = pw + kProd * q;  // block within the stage
-      const int j0 = (st * (kStage / 8) + jl) * 8;
+    for (int q = 0; q < kL1Q; ++q) {
+      const int pr = lane + 64 * q;
+      const int blk = pr / kL1Chains, ch = pr % kL1Chains;
+      const int j0 = (st * (kL1Stage / 8) + blk) * 8;
       float w[8], p[8];
       B8::widen(r[q], w);
 #pragma unroll
       for (int e = 0; e < 8; ++e) p[e] = __fmul_rn(w[e], xs[min(j0 + e, kMaxL1In - 1)]);
-      dst[2 * jl][lane] = make_float4(p[0], p[1], p[2], p[3]);
-      dst[2 * jl + 1][lane] = make_float4(p[4], p[5], p[6], p[7]);
+      dst[2 * blk][ch] = make_float4(p[0], p[1], p[2], p[3]);
+      dst[2 * blk + 1][ch] = make_float4(p[4], p[5], p[6], p[7]);
     }
   };
   __syncthreads();  // xs ready (nothing else in flight yet)
   if (wave > 0) {
 #pragma unroll
-    for (int d = 0; d < kPre; ++d) load_stage(d, pre[d]);
+    for (int d = 0; d < kL1Pre; ++d) load_stage(d, pre[d]);
     make_stage(0, pre[0]);
-    load_stage(kPre, pre[0]);
+    load_stage(kL1Pre, pre[0]);
   }
   lds_barrier();
-  // Producers and the consumer run separate loops with the same number of
-  // barriers (one per stage, nst rounded up to a multiple of kPre).  The
-  // producer body is branch-free -- it also forms (unused) stages past the end
-  // -- so the compiler can wait for exactly the stage it needs rather than
-  // for every outstanding prefetch.
-  const int nst_pad = (nst + kPre - 1) / kPre * kPre;
+  // Producer and consumer run separate loops with the same number of barriers
+  // (one per stage, nst rounded up to a multiple of kL1Pre).  The producer body
+  // is branch-free -- it also forms (unused) stages past the end -- so the
+  // compiler can wait for exactly the stage it needs rather than for every
+  // outstanding prefetch.
+  const int nst_pad = (nst + kL1Pre - 1) / kL1Pre * kL1Pre;
   float s = -0.0f;
   if (wave > 0) {
-    for (int st0 = 0; st0 < nst_pad; st0 += kPre) {
+    for (int st0 = 0; st0 < nst_pad; st0 += kL1Pre) {
 #pragma unroll
-      for (int d = 0; d < kPre; ++d) {
+      for (int d = 0; d < kL1Pre; ++d) {
         const int st = st0 + d;
-        make_stage(st + 1, pre[(d + 1) % kPre]);
-        load_stage(st + 1 + kPre, pre[(d + 1) % kPre]);
+        make_stage(st + 1, pre[(d + 1) % kL1Pre]);
+        load_stage(st + 1 + kL1Pre, pre[(d + 1) % kL1Pre]);
         lds_barrier();
       }
     }
   } else {
-    for (int st0 = 0; st0 < nst_pad; st0 += kPre) {
+    const int ln = lane < kL1Chains ? lane : kL1Chains - 1;
+    for (int st0 = 0; st0 < nst_pad; st0 += kL1Pre) {
 #pragma unroll
-      for (int d = 0; d < kPre; ++d) {
+      for (int d = 0; d < kL1Pre; ++d) {
         const int st = st0 + d;
-        const float4(*src)[64] = ring[st & 1];
-        const int steps = min(kStage, n_in - st * kStage);
-        if (steps == kStage) {
+        const float4(*src)[kL1Chains] = ring[st & 1];
+        const int steps = min(kL1Stage, n_in - st * kL1Stage);
+        if (steps == kL1Stage) {
 #pragma unroll
-          for (int q = 0; q < kStage / 4; ++q) {
-            const float4 v = src[q][lane];
+          for (int q = 0; q < kL1Stage / 4; ++q) {
+            const float4 v = src[q][ln];
             s = __fadd_rn(s, v.x);
             s = __fadd_rn(s, v.y);
             s = __fadd_rn(s, v.z);
             s = __fadd_rn(s, v.w);
           }
         } else if (steps > 0) {
-          for (int q = 0; q < kStage / 4; ++q) {
+          for (int q = 0; q < kL1Stage / 4; ++q) {
             if (4 * q >= steps) break;
-            const float4 v = src[q][lane];
+            const float4 v = src[q][ln];
             const float e[4] = {v.x, v.y, v.z, v.w};
             for (int u = 0; u < 4 && 4 * q + u < steps; ++u) s = __fadd_rn(s, e[u]);
           }
@@ -160,15 +166,20 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_kernel(
       }
     }
   }
-  if (wave == 0 && chain_ok) h[(size_t)b * hid + chain] = fmaxf(__fadd_rn(s, bias[chain]), 0.0f);
+  const int chain = c0 + lane;
+  if (wave == 0 && lane < kL1Chains && chain < hid)
+    h[(size_t)b * hid + chain] = fmaxf(__fadd_rn(s, bv), 0.0f);
 }
 
 // Layer 2 (short chains): one lane per output, the whole weight row in
 // registers (n_hid <= 256), the hidden vector in LDS.  Scores = sigmoid.
+// One wave per block, so the weight stream is spread over as many CUs as
+// there are waves.
 constexpr int kMaxL2Hid = 256;
+constexpr int kL2Threads = 64;
 
 template <typename W>
-__global__ __launch_bounds__(256) void pred_l2_kernel(const W* __restrict__ Wb,
+__global__ __launch_bounds__(kL2Threads) void pred_l2_kernel(const W* __restrict__ Wb,
                                                       const float* __restrict__ bias,
                                                       const float* __restrict__ hin, int n_hid,
                                                       int n_out, float* __restrict__ out) {
@@ -184,6 +195,7 @@ __global__ __launch_bounds__(256) void pred_l2_kernel(const W* __restrict__ Wb,
   const int oc = ok ? o : 0;
   const int nblk = (n_hid + 7) >> 3;
   const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
+  const float bv = bias[oc];  // issued with the weights, used after the chain
   V w[kMaxL2Hid / 8];
 #pragma unroll
   for (int jb = 0; jb < kMaxL2Hid / 8; ++jb)
@@ -200,7 +212,7 @@ __global__ __launch_bounds__(256) void pred_l2_kernel(const W* __restrict__ Wb,
         if (jb * 8 + e < n_hid) s = __fadd_rn(s, __fmul_rn(wf[e], hs[jb * 8 + e]));
     }
   }
-  if (ok) out[(size_t)b * n_out + o] = sigmoid_ref_t(__fadd_rn(s, bias[o]), tab);
+  if (ok) out[(size_t)b * n_out + o] = sigmoid_ref_t(__fadd_rn(s, bv), tab);
 }
 
 // Generic layer for shapes outside the fast kernels' limits: one lane per
@@ -233,160 +245,17 @@ __global__ __launch_bounds__(64) void chain_layer_kernel(const W* __restrict__ W
 
 // ---------------------------------------------------------------- top-k
 constexpr int kTopkThreads = 1024;
-constexpr int kTopkLdsKeys = 12288;  // keys kept in LDS when n fits
+constexpr int kTopkRegMax = kTopkThreads * 64 - 1;  // keys per thread in registers: 16, 32 or 64
+constexpr int kTopkCand = 256;       // boundary bins up to this size are ranked directly
+constexpr int kTopkDigit = 11;       // radix digit (2048 bins)
 
-__global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restrict__ scores,
-                                                            int n, int k, int order,
-                                                            int32_t* __restrict__ out,
-                                                            uint64_t* __restrict__ sortbuf) {
-  extern __shared__ __align__(16) uint32_t lkeys[];
-  __shared__ unsigned hist[256];
-  __shared__ int wgt[kTopkThreads / 64], weq[kTopkThreads / 64];
-  __shared__ uint32_t s_prefix, s_mask;
-  __shared__ int s_kk, s_hi;
-  const int b = blockIdx.x;
-  const float* sc = scores + (size_t)b * n;
-  const bool in_lds = n <= kTopkLdsKeys;
-  const int kk0 = min(k, n);
-  int32_t* ob = out + (size_t)b * kk0;
-  if (kk0 <= 0) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (in_lds) {
-    if ((n & 3) == 0 && ((reinterpret_cast<uintptr_t>(sc) & 15) == 0))
-      stage_f4(reinterpret_cast<float4*>(lkeys), reinterpret_cast<const float4*>(sc), n >> 2);
-    else
-      for (int i = threadIdx.x; i < n; i += blockDim.x) lkeys[i] = __float_as_uint(sc[i]);
-    __syncthreads();
-    for (int i = threadIdx.x; i < n; i += blockDim.x) lkeys[i] = f32_key(__uint_as_float(lkeys[i]));
-  }
-  // Highest bit where the keys differ: bits above it are common to every key,
-  // so the radix passes start there (scores cluster, and a pass over shared
-  // high bits would put every key in one or two bins).
-  uint32_t kmax = 0u, kmin = 0xffffffffu;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const uint32_t key = in_lds ? lkeys[i] : f32_key(sc[i]);
-    kmax = max(kmax, key);
-    kmin = min(kmin, key);
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
-    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
-  }
-  if (lane == 0) {
-    wgt[wave] = (int)kmax;
-    weq[wave] = (int)kmin;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t mx = 0u, mn = 0xffffffffu;
-    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
-      mx = max(mx, (uint32_t)wgt[w]);
-      mn = min(mn, (uint32_t)weq[w]);
-    }
-    const uint32_t diff = mx ^ mn;
-    const int hb = diff ? 31 - __clz(diff) : -1;
-    const uint32_t common = hb >= 31 ? 0u : ~((2u << hb) - 1u);
-    s_mask = hb < 0 ? 0xffffffffu : common;
-    s_prefix = mx & s_mask;
-    s_kk = kk0;
-    s_hi = hb;
-  }
-  __syncthreads();
-  for (int hi = s_hi; hi >= 0;) {
-    const int lo = max(0, hi - 7);
-    const int shift = lo;
-    const uint32_t binmask = (2u << (hi - lo)) - 1u;
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0;
-    __syncthreads();
-    const uint32_t prefix = s_prefix, mask = s_mask;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-      const uint32_t key = in_lds ? lkeys[i] : f32_key(sc[i]);
-      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & binmask], 1u);
-    }
-    __syncthreads();
-    if (threadIdx.x < 64) {
-      // lane l owns bins 4l..4l+3; suffix sums from the top bin down
-      const int l = threadIdx.x;
-      const int h0 = hist[4 * l], h1 = hist[4 * l + 1], h2 = hist[4 * l + 2], h3 = hist[4 * l + 3];
-      const int local = h0 + h1 + h2 + h3;
-      int suf = local;  // inclusive suffix over lanes >= l
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        int y = __shfl_down(suf, o, 64);
-        if (l + o < 64) suf += y;
-      }
-      const int above = suf - local;  // count in bins of lanes > l
-      const int kk = s_kk;
-      if (above < kk && kk <= suf) {
-        int cum = above, sel = 4 * l;
-        const int hs[4] = {h0, h1, h2, h3};
-        for (int q = 3; q >= 0; --q) {
-          if (cum + hs[q] >= kk) {
-            sel = 4 * l + q;
-            break;
-          }
-          cum += hs[q];
-        }
-        s_kk = kk - cum;
-        s_prefix = prefix | ((uint32_t)sel << shift);
-        s_mask = mask | (binmask << shift);
-      }
-    }
-    __syncthreads();
-    hi = lo - 1;
-  }
-  const uint32_t T = s_prefix;
-  const int ties = s_kk;  // entries equal to T to keep, lowest index first
-  // Compaction in ascending index order: wave w owns the contiguous segment
-  // [w*seg, (w+1)*seg); counts first, then ballot prefix sums inside waves.
-  const int nw = blockDim.x >> 6;
-  const int seg = ((n + nw - 1) / nw + 63) & ~63;
-  const int s0 = min(n, wave * seg), s1 = min(n, s0 + seg);
-  int cgt = 0, ceq = 0;
-  for (int i0 = s0; i0 < s1; i0 += 64) {
-    const int i = i0 + lane;
-    const uint32_t key = i < s1 ? (in_lds ? lkeys[i] : f32_key(sc[i])) : 0u;
-    cgt += __popcll(__ballot(i < s1 && key > T));
-    ceq += __popcll(__ballot(i < s1 && key == T));
-  }
-  if (lane == 0) {
-    wgt[wave] = cgt;
-    weq[wave] = ceq;
-  }
-  __syncthreads();
-  int gt_before = 0, eq_before = 0;
-  for (int w = 0; w < wave; ++w) {
-    gt_before += wgt[w];
-    eq_before += weq[w];
-  }
-  int pos_base = gt_before + min(eq_before, ties);
-  int eq_run = eq_before;
-  for (int i0 = s0; i0 < s1; i0 += 64) {
-    const int i = i0 + lane;
-    const uint32_t key = i < s1 ? (in_lds ? lkeys[i] : f32_key(sc[i])) : 0u;
-    const bool eq = i < s1 && key == T;
-    const bool gt = i < s1 && key > T;
-    const uint64_t meq = __ballot(eq);
-    const int eq_rank = eq_run + (int)__popcll(meq & ((1ull << lane) - 1ull));
-    const bool sel = gt || (eq && eq_rank < ties);
-    const uint64_t msel = __ballot(sel);
-    const int pos = pos_base + (int)__popcll(msel & ((1ull << lane) - 1ull));
-    if (sel) {
-      if (order == KH_ORDER_ASCENDING) ob[pos] = i;
-      else sortbuf[(size_t)b * kk0 + pos] = ((uint64_t)key << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
-    }
-    pos_base += (int)__popcll(msel);
-    eq_run += (int)__popcll(meq);
-  }
-  if (order == KH_ORDER_ASCENDING) return;
-  // Score order: bitonic sort (descending) of the selected (key, ~index) pairs.
-  __syncthreads();
-  uint64_t* sv = reinterpret_cast<uint64_t*>(lkeys);
+// Score-order output: bitonic sort (descending) of the selected (key, ~index)
+// pairs staged in sortbuf, then the indices.
+__device__ void topk_score_order(const uint64_t* __restrict__ src, int kk, int32_t* __restrict__ ob,
+                                 uint64_t* __restrict__ sv) {
   int P = 1;
-  while (P < kk0) P <<= 1;
-  for (int i = threadIdx.x; i < P; i += blockDim.x)
-    sv[i] = i < kk0 ? sortbuf[(size_t)b * kk0 + i] : 0ull;
+  while (P < kk) P <<= 1;
+  for (int i = threadIdx.x; i < P; i += blockDim.x) sv[i] = i < kk ? src[i] : 0ull;
   __syncthreads();
   for (int size = 2; size <= P; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
@@ -404,8 +273,182 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
       __syncthreads();
     }
   }
-  for (int i = threadIdx.x; i < kk0; i += blockDim.x)
+  for (int i = threadIdx.x; i < kk; i += blockDim.x)
     ob[i] = (int32_t)(0xffffffffu - (uint32_t)(sv[i] & 0xffffffffu));
+}
+
+// One block per row.  Thread t holds the keys of the contiguous index range
+// [t*kpt, (t+1)*kpt) in registers, so every pass runs from registers and the
+// selected indices come out in ascending order from one exclusive scan.
+//   1. common high bits of all keys (wave/block max and min);
+//   2. radix pass over the next kTopkDigit bits: LDS histogram, block scan
+//      from the top bin down -> the bin holding the k-th key;
+//   3. if that bin holds at most kTopkCand keys, they are gathered and ranked
+//      directly by (key desc, index asc); otherwise radix passes continue;
+//   4. compaction: keys above the k-th key T plus the lowest-index keys equal
+//      to T -- exactly the first k of the reference's stable descending sort.
+template <int kTopkPerThread>
+__global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restrict__ scores,
+                                                            int n, int k, int order,
+                                                            int32_t* __restrict__ out,
+                                                            uint64_t* __restrict__ sortbuf) {
+  extern __shared__ __align__(16) uint64_t sort_lds[];
+  __shared__ unsigned hist[1 << kTopkDigit];
+  __shared__ uint64_t cand[kTopkCand];
+  __shared__ int wsum[kTopkThreads / 64];
+  __shared__ uint32_t uwsum[kTopkThreads / 64];
+  __shared__ uint32_t wmax[kTopkThreads / 64], wmin[kTopkThreads / 64];
+  __shared__ uint32_t s_prefix, s_mask, s_T;
+  __shared__ int s_kk, s_total, s_bincount, s_ncand, s_ties;
+  const int b = blockIdx.x;
+  const float* sc = scores + (size_t)b * n;
+  const int kk0 = min(k, n);
+  if (kk0 <= 0) return;
+  int32_t* ob = out + (size_t)b * kk0;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kpt = (n + kTopkThreads - 1) / kTopkThreads;  // <= kTopkPerThread (host-checked)
+  const int i0 = threadIdx.x * kpt;
+  const int cnt = max(0, min(kpt, n - i0));
+  uint32_t key[kTopkPerThread];
+#pragma unroll
+  for (int j = 0; j < kTopkPerThread; ++j) key[j] = f32_key(sc[min(i0 + j, n - 1)]);
+  for (int i = threadIdx.x; i < (1 << kTopkDigit); i += kTopkThreads) hist[i] = 0;
+  if (threadIdx.x == 0) s_ncand = 0;
+  // 1. bits common to every key: the radix passes start below them (scores
+  // cluster, so a pass over shared high bits would fill one or two bins).
+  uint32_t kmax = 0u, kmin = 0xffffffffu;
+#pragma unroll
+  for (int j = 0; j < kTopkPerThread; ++j)
+    if (j < cnt) {
+      kmax = max(kmax, key[j]);
+      kmin = min(kmin, key[j]);
+    }
+  kmax = wave_max_u32(kmax);
+  kmin = wave_min_u32(kmin);
+  if (lane == 0) {
+    wmax[wave] = kmax;
+    wmin[wave] = kmin;
+  }
+  __syncthreads();
+  uint32_t mx = 0u, mn = 0xffffffffu;
+#pragma unroll
+  for (int w = 0; w < kTopkThreads / 64; ++w) {
+    mx = max(mx, wmax[w]);
+    mn = min(mn, wmin[w]);
+  }
+  const uint32_t diff = mx ^ mn;
+  int hi = diff ? 31 - __clz(diff) : -1;
+  uint32_t mask = hi < 0 ? 0xffffffffu : (hi >= 31 ? 0u : ~((2u << hi) - 1u));
+  uint32_t prefix = mx & mask;
+  int kk = kk0;
+  uint32_t T = prefix;
+  int ties = kk0;
+  bool first = true;
+  while (hi >= 0) {
+    // 2. one radix pass over bits [lo, hi] of the keys matching prefix/mask
+    const int lo = max(0, hi - (kTopkDigit - 1));
+    const int nbins = 2 << (hi - lo);
+    const uint32_t binmask = (uint32_t)nbins - 1u;
+    if (!first) {
+      for (int i = threadIdx.x; i < nbins; i += kTopkThreads) hist[i] = 0;
+      __syncthreads();
+    }
+    first = false;
+#pragma unroll
+    for (int j = 0; j < kTopkPerThread; ++j)
+      if (j < cnt && (key[j] & mask) == prefix) atomicAdd(&hist[(key[j] >> lo) & binmask], 1u);
+    __syncthreads();
+    // Thread t owns bins [nbins-(t+1)*per, nbins-t*per), thread 0 the highest;
+    // the exclusive scan in thread order counts the keys in higher bins.
+    const int per = (nbins + kTopkThreads - 1) / kTopkThreads;
+    const int top = nbins - (int)threadIdx.x * per;
+    const int bot = max(top - per, 0);
+    int local = 0;
+    for (int j = bot; j < top; ++j) local += (int)hist[j];
+    const int above = block_excl_scan(local, wsum, &s_total);
+    if (top > 0 && above < kk && kk <= above + local) {
+      int cum = above, sel = bot;
+      for (int j = top - 1; j >= bot; --j) {
+        if (cum + (int)hist[j] >= kk) {
+          sel = j;
+          break;
+        }
+        cum += (int)hist[j];
+      }
+      s_kk = kk - cum;
+      s_prefix = prefix | ((uint32_t)sel << lo);
+      s_mask = mask | (binmask << lo);
+      s_bincount = (int)hist[sel];
+    }
+    __syncthreads();
+    kk = s_kk;
+    prefix = s_prefix;
+    mask = s_mask;
+    hi = lo - 1;
+    T = prefix;
+    ties = kk;
+    if (hi < 0) break;  // every bit resolved: the bin is one key value
+    if (s_bincount <= kTopkCand) {
+      // 3. rank the boundary bin's keys directly
+#pragma unroll
+      for (int j = 0; j < kTopkPerThread; ++j)
+        if (j < cnt && (key[j] & mask) == prefix) {
+          const int c = atomicAdd(&s_ncand, 1);
+          cand[c] = ((uint64_t)key[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)(i0 + j));
+        }
+      __syncthreads();
+      const int m = s_ncand;
+      if ((int)threadIdx.x < m) {
+        const uint64_t me = cand[threadIdx.x];
+        const uint32_t mk = (uint32_t)(me >> 32);
+        int rank = 0, gt = 0;
+        for (int j = 0; j < m; ++j) {
+          const uint64_t o = cand[j];
+          rank += o > me;
+          gt += (uint32_t)(o >> 32) > mk;
+        }
+        if (rank == kk - 1) {
+          s_T = mk;
+          s_ties = kk - gt;
+        }
+      }
+      __syncthreads();
+      T = s_T;
+      ties = s_ties;
+      break;
+    }
+  }
+  // 4. compaction in ascending index order (one scan of packed counts:
+  // keys > T in the low 16 bits, keys == T in the high 16 bits; n < 65536).
+  int cgt = 0, ceq = 0;
+#pragma unroll
+  for (int j = 0; j < kTopkPerThread; ++j)
+    if (j < cnt) {
+      cgt += key[j] > T;
+      ceq += key[j] == T;
+    }
+  const uint32_t ex = block_excl_scan_u32((uint32_t)cgt | ((uint32_t)ceq << 16), uwsum);
+  const int gt_before = (int)(ex & 0xffffu), eq_before = (int)(ex >> 16);
+  int pos = gt_before + min(eq_before, ties);
+  int eq_rank = eq_before;
+  uint64_t* stage = sortbuf + (size_t)b * kk0;
+#pragma unroll
+  for (int j = 0; j < kTopkPerThread; ++j) {
+    if (j < cnt) {
+      const bool eq = key[j] == T;
+      const bool sel = key[j] > T || (eq && eq_rank < ties);
+      eq_rank += eq;
+      if (sel && pos < kk0) {
+        if (order == KH_ORDER_ASCENDING) ob[pos] = i0 + j;
+        else stage[pos] = ((uint64_t)key[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)(i0 + j));
+        ++pos;
+      }
+    }
+  }
+  if (order == KH_ORDER_ASCENDING) return;
+  __threadfence_block();
+  __syncthreads();
+  topk_score_order(stage, kk0, ob, sort_lds);
 }
 
 // ---------------------------------------------------------------- union
@@ -566,14 +609,14 @@ static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* 
   const W* w1 = static_cast<const W*>(p->w1b);
   const W* w2 = static_cast<const W*>(p->w2b);
   if (p->in_dim <= kMaxL1In)
-    hipLaunchKernelGGL(pred_l1_kernel<W>, dim3(ceil_div(p->hid, 64), batch), dim3(kL1Threads), 0,
+    hipLaunchKernelGGL(pred_l1_kernel<W>, dim3(ceil_div(p->hid, kL1Chains), batch), dim3(kL1Threads), 0,
                        st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
   else
     hipLaunchKernelGGL((chain_layer_kernel<0, W>), dim3(ceil_div(p->hid, 64), batch), dim3(64), 0,
                        st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
   KH_LAUNCHED();
   if (p->hid <= kMaxL2Hid)
-    hipLaunchKernelGGL(pred_l2_kernel<W>, dim3(ceil_div(p->out_dim, 256), batch), dim3(256), 0, st,
+    hipLaunchKernelGGL(pred_l2_kernel<W>, dim3(ceil_div(p->out_dim, kL2Threads), batch), dim3(kL2Threads), 0, st,
                        w2, p->b2, p->hbuf, p->hid, p->out_dim, scores);
   else
     hipLaunchKernelGGL((chain_layer_kernel<1, W>), dim3(ceil_div(p->out_dim, 64), batch), dim3(64),
@@ -603,13 +646,15 @@ static int topk_launch(const float* scores, int64_t batch, int n, int k, int ord
                        hipStream_t st) {
   const int kk = std::min(k, n);
   if (kk <= 0 || batch == 0) return KH_OK;
+  KH_CHECK_ARG(n <= kTopkRegMax, "top-k supports n <= %d scores per row (got %d)", kTopkRegMax, n);
+  static_assert(kTopkRegMax < 65536, "packed compaction counts");
   uint64_t* sortbuf = nullptr;
-  size_t lds = n <= kTopkLdsKeys ? sizeof(uint32_t) * n : 0;
+  size_t lds = 0;
   if (order == KH_ORDER_SCORE) {
     KH_CHECK_ARG(kk <= 4096, "score-ordered top-k supports k <= 4096 (got %d)", kk);
     int P = 1;
     while (P < kk) P <<= 1;
-    lds = std::max(lds, sizeof(uint64_t) * P);
+    lds = sizeof(uint64_t) * P;
     static thread_local uint64_t* buf = nullptr;
     static thread_local size_t cap = 0;
     const size_t need = sizeof(uint64_t) * batch * kk;
@@ -621,8 +666,15 @@ static int topk_launch(const float* scores, int64_t batch, int n, int k, int ord
     }
     sortbuf = buf;
   }
-  hipLaunchKernelGGL(topk_kernel, dim3(batch), dim3(kTopkThreads), lds, st, scores, n, k, order,
-                     ids, sortbuf);
+  if (n <= kTopkThreads * 16)
+    hipLaunchKernelGGL(topk_kernel<16>, dim3(batch), dim3(kTopkThreads), lds, st, scores, n, k,
+                       order, ids, sortbuf);
+  else if (n <= kTopkThreads * 32)
+    hipLaunchKernelGGL(topk_kernel<32>, dim3(batch), dim3(kTopkThreads), lds, st, scores, n, k,
+                       order, ids, sortbuf);
+  else
+    hipLaunchKernelGGL(topk_kernel<64>, dim3(batch), dim3(kTopkThreads), lds, st, scores, n, k,
+                       order, ids, sortbuf);
   KH_LAUNCHED();
   return KH_OK;
 }
