@@ -45,58 +45,79 @@ template <> struct Blk8<float> {
   static __device__ __forceinline__ V zero() { return V{make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0)}; }
 };
 
-// Layer 1 (long chains).  A block owns kL1Chains consecutive hidden units: one
-// consumer wave (lanes < kL1Chains, one chain each) adds the products in step
-// order while one producer wave streams the blocked weights
-// [ceil(n_in/8)][hid][8] kL1Pre stages ahead in registers, forms the rounded
-// products w*x of a stage of kL1Stage steps and writes them to a two-stage LDS
-// ring laid out [stage][step/4][chain][4], so that the consumer reads four steps
-// with one ds_read_b128.  Few chains per block spread the weight stream over
-// many CUs; the time is then set by the chain itself (one dependent add per
-// step, about 8 cycles on gfx950).  Output h[b][i] = max(sum + b1[i], 0).
+// Layer 1 (long chains).  A block owns kL1Chains consecutive hidden units.
+// Its kL1Prod producer waves request every weight the block needs -- the
+// blocked layout [ceil(n_in/8)][hid][8] gives 16-byte loads of one 8-step
+// block of one chain -- in the first few hundred cycles, each holding SPP
+// stages of kL1Stage steps in registers, so HBM latency is paid once.  Stage
+// by stage, the producer that owns the next stage forms the rounded products
+// w*x and writes them to a two-stage LDS ring laid out [stage][step/4][chain][4],
+// while the consumer wave (lanes < kL1Chains, one chain each) adds the current
+// stage in step order with one ds_read_b128 per four steps.  The time is then
+// set by the chain itself: one dependent add per step, about 6 cycles on
+// gfx950.  Output h[b][i] = max(sum + b1[i], 0).
 constexpr int kL1Chains = 8;
 constexpr int kL1Stage = 128;     // steps per stage
-constexpr int kL1Pre = 8;         // stages of weights in flight in the producer
-constexpr int kL1Threads = 128;   // consumer wave + producer wave
+constexpr int kL1Prod = 4;        // producer waves
+constexpr int kL1Threads = 64 * (1 + kL1Prod);
 constexpr int kL1Q = (kL1Stage / 8) * kL1Chains / 64;  // weight loads per producer lane per stage
-constexpr int kMaxL1In = 8192;    // x row staged in LDS
+constexpr int kMaxL1In = 8192;    // x row staged in LDS (16 stages per producer)
 static_assert(kL1Q * 64 == (kL1Stage / 8) * kL1Chains, "stage tiling");
 
-template <typename W>
+template <typename W, int SPP>
 __global__ __launch_bounds__(kL1Threads) void pred_l1_kernel(
     const W* __restrict__ Wb, const float* __restrict__ bias, const float* __restrict__ x,
     int n_in, int hid, float* __restrict__ h) {
   using B8 = Blk8<W>;
   using V = typename B8::V;
-  __shared__ __align__(16) float xs[kMaxL1In];
+  constexpr int kStages = SPP * kL1Prod;                     // stages the loop runs
+  constexpr int kXq = (kStages * kL1Stage / 4 + kL1Threads - 1) / kL1Threads;  // x float4 per thread
+  __shared__ __align__(16) float xs[kStages * kL1Stage];
   __shared__ float4 ring[2][kL1Stage / 4][kL1Chains];
   const int b = blockIdx.y;
   const int c0 = blockIdx.x * kL1Chains;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nblk = (n_in + 7) >> 3;                 // 8-step blocks
-  const int nst = (n_in + kL1Stage - 1) / kL1Stage;  // stages
-  const float bv = bias[min(c0 + (lane & (kL1Chains - 1)), hid - 1)];  // loaded with x, used at the end
-  if ((n_in & 3) == 0)
-    stage_f4(reinterpret_cast<float4*>(xs), reinterpret_cast<const float4*>(x + (size_t)b * n_in),
-             n_in >> 2);
-  else
-    for (int j = threadIdx.x; j < n_in; j += blockDim.x) xs[j] = x[(size_t)b * n_in + j];
-  const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
-  V pre[kL1Pre][kL1Q];
-  // Producer lane l, load q covers pair p = l + 64q: 8-step block p / kL1Chains
-  // of the stage and chain p % kL1Chains.  Loads are unconditional (clamped):
-  // out-of-range blocks and chains are never consumed, and branch-free loads
-  // let the compiler count them precisely (a conditional load makes it wait
-  // for every outstanding load).
-  auto load_stage = [&](int st, V (&r)[kL1Q]) {
+  const int nst = (n_in + kL1Stage - 1) / kL1Stage;  // stages holding steps
+  const int p = wave - 1;                            // producer index (consumer: -1)
+  // 1. x loads (first, so that waiting for them leaves the weight loads in flight)
+  const float* xr = x + (size_t)b * n_in;
+  const bool vec = (n_in & 3) == 0;
+  float4 xv[kXq];
 #pragma unroll
-    for (int q = 0; q < kL1Q; ++q) {
-      const int pr = lane + 64 * q;
-      const int jb = min(st * (kL1Stage / 8) + pr / kL1Chains, nblk - 1);
-      const int ch = min(c0 + pr % kL1Chains, hid - 1);
-      r[q] = wv[(size_t)jb * hid + ch];
+  for (int q = 0; q < kXq; ++q) {
+    const int i = threadIdx.x + q * kL1Threads;
+    xv[q] = vec ? reinterpret_cast<const float4*>(xr)[min(i, (n_in >> 2) - 1)] : make_float4(0, 0, 0, 0);
+  }
+  const float bv = bias[min(c0 + (lane & (kL1Chains - 1)), hid - 1)];
+  // 2. every weight of the block: producer p owns stages p, p + kL1Prod, ...
+  // Loads are unconditional (clamped): out-of-range blocks and chains are
+  // never consumed, and branch-free loads let the compiler count them.
+  V pre[SPP][kL1Q];
+  if (wave > 0) {
+    const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
+#pragma unroll
+    for (int i = 0; i < SPP; ++i)
+#pragma unroll
+      for (int q = 0; q < kL1Q; ++q) {
+        const int st = p + kL1Prod * i;
+        const int pr = lane + 64 * q;
+        const int jb = min(st * (kL1Stage / 8) + pr / kL1Chains, nblk - 1);
+        const int ch = min(c0 + pr % kL1Chains, hid - 1);
+        pre[i][q] = wv[(size_t)jb * hid + ch];
+      }
+  }
+  // 3. x to LDS
+  if (vec) {
+#pragma unroll
+    for (int q = 0; q < kXq; ++q) {
+      const int i = threadIdx.x + q * kL1Threads;
+      if (i < (n_in >> 2)) reinterpret_cast<float4*>(xs)[i] = xv[q];
     }
-  };
+  } else {
+    for (int j = threadIdx.x; j < n_in; j += kL1Threads) xs[j] = xr[j];
+  }
+  lds_barrier();
   auto make_stage = [&](int st, const V (&r)[kL1Q]) {
     float4(*dst)[kL1Chains] = ring[st & 1];
 #pragma unroll
@@ -104,71 +125,169 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_kernel(
       const int pr = lane + 64 * q;
       const int blk = pr / kL1Chains, ch = pr % kL1Chains;
       const int j0 = (st * (kL1Stage / 8) + blk) * 8;
-      float w[8], p[8];
+      float w[8], pv[8];
       B8::widen(r[q], w);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) p[e] = __fmul_rn(w[e], xs[min(j0 + e, kMaxL1In - 1)]);
-      dst[2 * blk][ch] = make_float4(p[0], p[1], p[2], p[3]);
-      dst[2 * blk + 1][ch] = make_float4(p[4], p[5], p[6], p[7]);
+      for (int e = 0; e < 8; ++e) pv[e] = __fmul_rn(w[e], xs[min(j0 + e, kStages * kL1Stage - 1)]);
+      dst[2 * blk][ch] = make_float4(pv[0], pv[1], pv[2], pv[3]);
+      dst[2 * blk + 1][ch] = make_float4(pv[4], pv[5], pv[6], pv[7]);
     }
   };
-  __syncthreads();  // xs ready (nothing else in flight yet)
-  if (wave > 0) {
-#pragma unroll
-    for (int d = 0; d < kL1Pre; ++d) load_stage(d, pre[d]);
-    make_stage(0, pre[0]);
-    load_stage(kL1Pre, pre[0]);
-  }
-  lds_barrier();
-  // Producer and consumer run separate loops with the same number of barriers
-  // (one per stage, nst rounded up to a multiple of kL1Pre).  The producer body
-  // is branch-free -- it also forms (unused) stages past the end -- so the
-  // compiler can wait for exactly the stage it needs rather than for every
-  // outstanding prefetch.
-  const int nst_pad = (nst + kL1Pre - 1) / kL1Pre * kL1Pre;
+  // 4. kStages + 1 barriers on every wave: stage st is written before
+  // barrier st and read between barriers st and st + 1.
   float s = -0.0f;
   if (wave > 0) {
-    for (int st0 = 0; st0 < nst_pad; st0 += kL1Pre) {
 #pragma unroll
-      for (int d = 0; d < kL1Pre; ++d) {
-        const int st = st0 + d;
-        make_stage(st + 1, pre[(d + 1) % kL1Pre]);
-        load_stage(st + 1 + kL1Pre, pre[(d + 1) % kL1Pre]);
-        lds_barrier();
-      }
+    for (int st = 0; st < kStages; ++st) {
+      if (st % kL1Prod == p) make_stage(st, pre[st / kL1Prod]);
+      lds_barrier();
     }
+    lds_barrier();
   } else {
     const int ln = lane < kL1Chains ? lane : kL1Chains - 1;
-    for (int st0 = 0; st0 < nst_pad; st0 += kL1Pre) {
+    lds_barrier();
+    for (int st = 0; st < kStages; ++st) {
+      const float4(*src)[kL1Chains] = ring[st & 1];
+      const int steps = min(kL1Stage, n_in - st * kL1Stage);
+      if (steps == kL1Stage) {
 #pragma unroll
-      for (int d = 0; d < kL1Pre; ++d) {
-        const int st = st0 + d;
-        const float4(*src)[kL1Chains] = ring[st & 1];
-        const int steps = min(kL1Stage, n_in - st * kL1Stage);
-        if (steps == kL1Stage) {
-#pragma unroll
-          for (int q = 0; q < kL1Stage / 4; ++q) {
-            const float4 v = src[q][ln];
-            s = __fadd_rn(s, v.x);
-            s = __fadd_rn(s, v.y);
-            s = __fadd_rn(s, v.z);
-            s = __fadd_rn(s, v.w);
-          }
-        } else if (steps > 0) {
-          for (int q = 0; q < kL1Stage / 4; ++q) {
-            if (4 * q >= steps) break;
-            const float4 v = src[q][ln];
-            const float e[4] = {v.x, v.y, v.z, v.w};
-            for (int u = 0; u < 4 && 4 * q + u < steps; ++u) s = __fadd_rn(s, e[u]);
-          }
+        for (int q = 0; q < kL1Stage / 4; ++q) {
+          const float4 v = src[q][ln];
+          s = __fadd_rn(s, v.x);
+          s = __fadd_rn(s, v.y);
+          s = __fadd_rn(s, v.z);
+          s = __fadd_rn(s, v.w);
         }
-        lds_barrier();
+      } else if (steps > 0) {
+        for (int q = 0; q < kL1Stage / 4; ++q) {
+          if (4 * q >= steps) break;
+          const float4 v = src[q][ln];
+          const float e[4] = {v.x, v.y, v.z, v.w};
+          for (int u = 0; u < 4 && 4 * q + u < steps; ++u) s = __fadd_rn(s, e[u]);
+        }
       }
+      lds_barrier();
     }
   }
+  (void)nst;
   const int chain = c0 + lane;
   if (wave == 0 && lane < kL1Chains && chain < hid)
     h[(size_t)b * hid + chain] = fmaxf(__fadd_rn(s, bv), 0.0f);
+}
+
+// Layer 1 for n_in <= kL1LdsIn: the block's products w*x for every step are
+// formed into LDS first (kL1Chains * n_in floats; all weight loads of the
+// block are in flight at once), then the consumer wave runs its chains over
+// them with no further barrier, reading 32 steps ahead of the adds.
+constexpr int kL1LdsIn = 4096;
+constexpr int kL1LdsBytes = (kL1Chains + 1) * kL1LdsIn * 4;  // products + x
+
+template <typename W>
+__global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
+    const W* __restrict__ Wb, const float* __restrict__ bias, const float* __restrict__ x,
+    int n_in, int hid, float* __restrict__ h) {
+  using B8 = Blk8<W>;
+  using V = typename B8::V;
+  constexpr int SPP = kL1LdsIn / kL1Stage / kL1Prod;                  // stages per producer
+  constexpr int kXq = (kL1LdsIn / 4 + kL1Threads - 1) / kL1Threads;  // x float4 per thread
+  extern __shared__ float4 lds4[];
+  float4(*P)[kL1Chains] = reinterpret_cast<float4(*)[kL1Chains]>(lds4);  // [n_in/4][chain]
+  float* xs = reinterpret_cast<float*>(lds4 + (kL1LdsIn / 4) * kL1Chains);
+  const int b = blockIdx.y;
+  const int c0 = blockIdx.x * kL1Chains;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nblk = (n_in + 7) >> 3;
+  const int p = wave - 1;
+  const float* xr = x + (size_t)b * n_in;
+  const bool vec = (n_in & 3) == 0;
+  float4 xv[kXq];
+#pragma unroll
+  for (int q = 0; q < kXq; ++q) {
+    const int i = threadIdx.x + q * kL1Threads;
+    xv[q] = vec ? reinterpret_cast<const float4*>(xr)[min(i, (n_in >> 2) - 1)] : make_float4(0, 0, 0, 0);
+  }
+  const float bv = bias[min(c0 + (lane & (kL1Chains - 1)), hid - 1)];
+  V pre[SPP][kL1Q];
+  if (wave > 0) {
+    const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
+#pragma unroll
+    for (int i = 0; i < SPP; ++i)
+#pragma unroll
+      for (int q = 0; q < kL1Q; ++q) {
+        const int st = p + kL1Prod * i;
+        const int pr = lane + 64 * q;
+        const int jb = min(st * (kL1Stage / 8) + pr / kL1Chains, nblk - 1);
+        const int ch = min(c0 + pr % kL1Chains, hid - 1);
+        pre[i][q] = wv[(size_t)jb * hid + ch];
+      }
+  }
+  if (vec) {
+#pragma unroll
+    for (int q = 0; q < kXq; ++q) {
+      const int i = threadIdx.x + q * kL1Threads;
+      if (i < (n_in >> 2)) reinterpret_cast<float4*>(xs)[i] = xv[q];
+    }
+  } else {
+    for (int j = threadIdx.x; j < n_in; j += kL1Threads) xs[j] = xr[j];
+  }
+  lds_barrier();
+  if (wave > 0) {
+    // products in stage order; loads arrive in issue order, so each stage
+    // waits only for its own weights
+#pragma unroll
+    for (int i = 0; i < SPP; ++i) {
+      const int st = p + kL1Prod * i;
+#pragma unroll
+      for (int q = 0; q < kL1Q; ++q) {
+        const int pr = lane + 64 * q;
+        const int blk = pr / kL1Chains, ch = pr % kL1Chains;
+        const int j0 = (st * (kL1Stage / 8) + blk) * 8;
+        float w[8], pv[8];
+        B8::widen(pre[i][q], w);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = __fmul_rn(w[e], xs[min(j0 + e, kL1LdsIn - 1)]);
+        P[j0 / 4][ch] = make_float4(pv[0], pv[1], pv[2], pv[3]);
+        P[j0 / 4 + 1][ch] = make_float4(pv[4], pv[5], pv[6], pv[7]);
+      }
+    }
+  }
+  lds_barrier();
+  if (wave > 0) return;
+  // Consumer: the chains over the products.  A window of kWin quads (4 steps
+  // each) is in flight; each quad is added, then its register is refilled with
+  // the quad kWin ahead, so the only VALU work per step is the dependent add
+  // (LDS addresses are immediate offsets from one base pointer).  The window
+  // may read past the last product (still inside the block's LDS); those
+  // values are never added.
+  constexpr int kWin = 16;   // quads in flight (64 steps)
+  constexpr int kSup = 64;   // quads per unrolled loop body (256 steps)
+  static_assert((kL1LdsIn / 4 + kWin) * kL1Chains <= (kL1LdsBytes / 16), "window stays in LDS");
+  const int ln = lane < kL1Chains ? lane : kL1Chains - 1;
+  const float4* bp = &P[0][ln];
+  float s = -0.0f;
+  float4 r[kWin];
+#pragma unroll
+  for (int q = 0; q < kWin; ++q) r[q] = bp[q * kL1Chains];
+  const int nsup = n_in / (4 * kSup);
+  for (int c = 0; c < nsup; ++c) {
+#pragma unroll
+    for (int q = 0; q < kSup; ++q) {
+      s = __fadd_rn(s, r[q % kWin].x);
+      s = __fadd_rn(s, r[q % kWin].y);
+      s = __fadd_rn(s, r[q % kWin].z);
+      s = __fadd_rn(s, r[q % kWin].w);
+      r[q % kWin] = bp[(q + kWin) * kL1Chains];
+      // keep the refill here: the scheduler would otherwise sink it to its use
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    bp += kSup * kL1Chains;
+  }
+  // remaining steps (fewer than 4 * kSup), one by one in order
+  const float* Pf = reinterpret_cast<const float*>(lds4);
+  for (int j = nsup * 4 * kSup; j < n_in; ++j)
+    s = __fadd_rn(s, Pf[((j >> 2) * kL1Chains + ln) * 4 + (j & 3)]);
+  const int chain = c0 + lane;
+  if (lane < kL1Chains && chain < hid) h[(size_t)b * hid + chain] = fmaxf(__fadd_rn(s, bv), 0.0f);
 }
 
 // Layer 2 (short chains): one lane per output, the whole weight row in
@@ -608,9 +727,24 @@ static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* 
                          hipStream_t st) {
   const W* w1 = static_cast<const W*>(p->w1b);
   const W* w2 = static_cast<const W*>(p->w2b);
-  if (p->in_dim <= kMaxL1In)
-    hipLaunchKernelGGL(pred_l1_kernel<W>, dim3(ceil_div(p->hid, kL1Chains), batch), dim3(kL1Threads), 0,
-                       st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
+  const int l1_stages = ceil_div(p->in_dim, kL1Stage);
+  static bool l1_attr = false;
+  if (!l1_attr) {
+    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pred_l1_lds_kernel<uint16_t>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kL1LdsBytes));
+    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pred_l1_lds_kernel<float>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kL1LdsBytes));
+    l1_attr = true;
+  }
+  if (p->in_dim <= kL1LdsIn)
+    hipLaunchKernelGGL(pred_l1_lds_kernel<W>, dim3(ceil_div(p->hid, kL1Chains), batch),
+                       dim3(kL1Threads), kL1LdsBytes, st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
+  else if (l1_stages <= 8 * kL1Prod)
+    hipLaunchKernelGGL((pred_l1_kernel<W, 8>), dim3(ceil_div(p->hid, kL1Chains), batch),
+                       dim3(kL1Threads), 0, st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
+  else if (p->in_dim <= kMaxL1In)
+    hipLaunchKernelGGL((pred_l1_kernel<W, 16>), dim3(ceil_div(p->hid, kL1Chains), batch),
+                       dim3(kL1Threads), 0, st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
   else
     hipLaunchKernelGGL((chain_layer_kernel<0, W>), dim3(ceil_div(p->hid, 64), batch), dim3(64), 0,
                        st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
