@@ -304,31 +304,72 @@ __global__ __launch_bounds__(kL2Threads) void pred_l2_kernel(const W* __restrict
                                                       int n_out, float* __restrict__ out) {
   using B8 = Blk8<W>;
   using V = typename B8::V;
-  __shared__ float hs[kMaxL2Hid];
+  constexpr int kHw = 4;  // float4 of the hidden vector read ahead (16 steps)
+  __shared__ __align__(16) float hs[kMaxL2Hid + 4 * kHw];
   __shared__ uint64_t tab[32];
   const int b = blockIdx.y;
   const int o = blockIdx.x * blockDim.x + threadIdx.x;
-  for (int i = threadIdx.x; i < n_hid; i += blockDim.x) hs[i] = hin[(size_t)b * n_hid + i];
-  if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  // The hidden vector (one float4 per thread) is requested first, then the
+  // bias and the weight row, and only then stored to LDS: waiting for the
+  // hidden values leaves the weight loads in flight.
+  const bool vec = (n_hid & 3) == 0 && n_hid <= 4 * kL2Threads;
+  const float4 hv = vec ? reinterpret_cast<const float4*>(hin + (size_t)b * n_hid)
+                              [min((int)threadIdx.x, (n_hid >> 2) - 1)]
+                        : make_float4(0, 0, 0, 0);
   const bool ok = o < n_out;
   const int oc = ok ? o : 0;
   const int nblk = (n_hid + 7) >> 3;
   const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
-  const float bv = bias[oc];  // issued with the weights, used after the chain
+  const float bv = bias[oc];  // used after the chain
   V w[kMaxL2Hid / 8];
 #pragma unroll
   for (int jb = 0; jb < kMaxL2Hid / 8; ++jb)
     w[jb] = jb < nblk ? wv[(size_t)jb * n_out + oc] : B8::zero();
+  if (vec) {
+    if ((int)threadIdx.x < (n_hid >> 2)) reinterpret_cast<float4*>(hs)[threadIdx.x] = hv;
+  } else {
+    for (int i = threadIdx.x; i < n_hid; i += blockDim.x) hs[i] = hin[(size_t)b * n_hid + i];
+  }
+  if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   __syncthreads();
   float s = -0.0f;
+  if ((n_hid & 7) == 0) {
+    // Whole 8-step blocks: no per-step test.  The hidden values come from LDS
+    // through a window of kHw float4 read ahead of their use (pinned, or the
+    // scheduler sinks each read to its use and the chain waits on LDS).
+    const float4* h4 = reinterpret_cast<const float4*>(hs);
+    float4 hw[kHw];
 #pragma unroll
-  for (int jb = 0; jb < kMaxL2Hid / 8; ++jb) {
-    if (jb < nblk) {
-      float wf[8];
-      B8::widen(w[jb], wf);
+    for (int q = 0; q < kHw; ++q) hw[q] = h4[q];
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (jb * 8 + e < n_hid) s = __fadd_rn(s, __fmul_rn(wf[e], hs[jb * 8 + e]));
+    for (int jb = 0; jb < kMaxL2Hid / 8; ++jb) {
+      if (jb < nblk) {
+        float wf[8];
+        B8::widen(w[jb], wf);
+        const float4 a = hw[(2 * jb) % kHw], c = hw[(2 * jb + 1) % kHw];
+        s = __fadd_rn(s, __fmul_rn(wf[0], a.x));
+        s = __fadd_rn(s, __fmul_rn(wf[1], a.y));
+        s = __fadd_rn(s, __fmul_rn(wf[2], a.z));
+        s = __fadd_rn(s, __fmul_rn(wf[3], a.w));
+        s = __fadd_rn(s, __fmul_rn(wf[4], c.x));
+        s = __fadd_rn(s, __fmul_rn(wf[5], c.y));
+        s = __fadd_rn(s, __fmul_rn(wf[6], c.z));
+        s = __fadd_rn(s, __fmul_rn(wf[7], c.w));
+        hw[(2 * jb) % kHw] = h4[2 * jb + kHw];
+        hw[(2 * jb + 1) % kHw] = h4[2 * jb + 1 + kHw];
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int jb = 0; jb < kMaxL2Hid / 8; ++jb) {
+      if (jb < nblk) {
+        float wf[8];
+        B8::widen(w[jb], wf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (jb * 8 + e < n_hid) s = __fadd_rn(s, __fmul_rn(wf[e], hs[jb * 8 + e]));
+      }
     }
   }
   if (ok) out[(size_t)b * n_out + o] = sigmoid_ref_t(__fadd_rn(s, bv), tab);
@@ -366,6 +407,7 @@ __global__ __launch_bounds__(64) void chain_layer_kernel(const W* __restrict__ W
 constexpr int kTopkThreads = 1024;
 constexpr int kTopkRegMax = kTopkThreads * 64 - 1;  // keys per thread in registers: 16, 32 or 64
 constexpr int kTopkCand = 256;       // boundary bins up to this size are ranked directly
+constexpr int kTopkStage = 32768;    // rows up to this size are loaded through LDS
 constexpr int kTopkDigit = 11;       // radix digit (2048 bins)
 
 // Score-order output: bitonic sort (descending) of the selected (key, ~index)
@@ -428,11 +470,34 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
   const int kpt = (n + kTopkThreads - 1) / kTopkThreads;  // <= kTopkPerThread (host-checked)
   const int i0 = threadIdx.x * kpt;
   const int cnt = max(0, min(kpt, n - i0));
-  uint32_t key[kTopkPerThread];
+  // Coalesced loads through LDS (a thread's own contiguous range would make
+  // every wave load touch dozens of cache lines), then each thread reads its
+  // range; the odd-or-power-of-two strides keep the LDS reads conflict-light.
+  uint32_t* sstage = reinterpret_cast<uint32_t*>(sort_lds);
+  const bool staged = n <= kTopkStage;
+  if (!staged) {
+    // too many scores to stage: each thread loads its own range directly
+  } else if ((n & 3) == 0 && ((reinterpret_cast<uintptr_t>(sc) & 15) == 0)) {
+    const float4* s4 = reinterpret_cast<const float4*>(sc);
+    constexpr int kQ = kTopkPerThread / 4;
+    float4 v[kQ];
 #pragma unroll
-  for (int j = 0; j < kTopkPerThread; ++j) key[j] = f32_key(sc[min(i0 + j, n - 1)]);
+    for (int q = 0; q < kQ; ++q) v[q] = s4[min((int)threadIdx.x + q * kTopkThreads, (n >> 2) - 1)];
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const int i = threadIdx.x + q * kTopkThreads;
+      if (i < (n >> 2)) reinterpret_cast<float4*>(sstage)[i] = v[q];
+    }
+  } else {
+    for (int i = threadIdx.x; i < n; i += kTopkThreads) sstage[i] = __float_as_uint(sc[i]);
+  }
   for (int i = threadIdx.x; i < (1 << kTopkDigit); i += kTopkThreads) hist[i] = 0;
   if (threadIdx.x == 0) s_ncand = 0;
+  lds_barrier();
+  uint32_t key[kTopkPerThread];
+#pragma unroll
+  for (int j = 0; j < kTopkPerThread; ++j)
+    key[j] = f32_key(staged ? __uint_as_float(sstage[min(i0 + j, n - 1)]) : sc[min(i0 + j, n - 1)]);
   // 1. bits common to every key: the radix passes start below them (scores
   // cluster, so a pass over shared high bits would fill one or two bins).
   uint32_t kmax = 0u, kmin = 0xffffffffu;
@@ -783,12 +848,22 @@ static int topk_launch(const float* scores, int64_t batch, int n, int k, int ord
   KH_CHECK_ARG(n <= kTopkRegMax, "top-k supports n <= %d scores per row (got %d)", kTopkRegMax, n);
   static_assert(kTopkRegMax < 65536, "packed compaction counts");
   uint64_t* sortbuf = nullptr;
-  size_t lds = 0;
+  size_t lds = n <= kTopkStage ? sizeof(uint32_t) * ((n + 3) & ~3) : 0;  // staged scores
+  static bool attr = false;
+  if (!attr) {
+    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<16>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 136 * 1024));
+    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<32>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 136 * 1024));
+    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<64>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 136 * 1024));
+    attr = true;
+  }
   if (order == KH_ORDER_SCORE) {
     KH_CHECK_ARG(kk <= 4096, "score-ordered top-k supports k <= 4096 (got %d)", kk);
     int P = 1;
     while (P < kk) P <<= 1;
-    lds = sizeof(uint64_t) * P;
+    lds = std::max(lds, sizeof(uint64_t) * P);
     static thread_local uint64_t* buf = nullptr;
     static thread_local size_t cap = 0;
     const size_t need = sizeof(uint64_t) * batch * kk;
