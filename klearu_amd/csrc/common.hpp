@@ -270,22 +270,19 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Block-cooperative copy of n4 float4s from global memory to LDS with four
 // loads in flight per thread before any store (a plain strided loop would
-// wait one memory round trip per iteration).
+// wait one memory round trip per iteration).  Loads and stores are clamped,
+// not conditional: a conditional store lets the compiler sink each load into
+// its branch, one round trip per load.  Past the end a thread rewrites the
+// last float4 with the value it loaded from there.
 __device__ __forceinline__ void stage_f4(float4* __restrict__ dst, const float4* __restrict__ src,
                                          int n4) {
   constexpr int U = 4;
   for (int base = threadIdx.x; base < n4; base += blockDim.x * U) {
     float4 v[U];
 #pragma unroll
-    for (int q = 0; q < U; ++q) {
-      const int i = base + q * blockDim.x;
-      v[q] = i < n4 ? src[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
+    for (int q = 0; q < U; ++q) v[q] = src[min(base + q * (int)blockDim.x, n4 - 1)];
 #pragma unroll
-    for (int q = 0; q < U; ++q) {
-      const int i = base + q * blockDim.x;
-      if (i < n4) dst[i] = v[q];
-    }
+    for (int q = 0; q < U; ++q) dst[min(base + q * (int)blockDim.x, n4 - 1)] = v[q];
   }
 }
 

@@ -131,25 +131,34 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
   extern __shared__ float4 smem4[];
   float4* xs4 = smem4;                                    // [H/4]
   float* red = reinterpret_cast<float*>(smem4 + (H >> 2));  // [4][H]
-  int n = n_active;
-  if (n_active_dev) n = min(n, *n_active_dev);
-  if (blockIdx.x * kFuWaves >= n) return;  // uniform per block
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int item = blockIdx.x * kFuWaves + wave;
-  const bool live = item < n;
-  const int neuron = active[live ? item : n - 1];
-  const int nchunk = H >> 3;
-  const uint4* __restrict__ g = reinterpret_cast<const uint4*>(Wgu + (size_t)neuron * 2 * H);
-  const uint4* __restrict__ u = g + nchunk;
-  const uint4* __restrict__ d = reinterpret_cast<const uint4*>(WdT + (size_t)neuron * H);
-  // x loads first, then the weight rows: vmcnt counts in issue order, so x
-  // can be written to LDS while every weight load is still in flight.
+  // x, the active index and the device count are requested together (one
+  // round trip), and x is in LDS before any weight load is issued: the weight
+  // loads are then waited for only where their data is used (vmcnt counts in
+  // issue order, so an x load behind them would wait for every weight).
   const int n4 = H >> 2;
   const float4* __restrict__ xsrc = reinterpret_cast<const float4*>(x);
   constexpr int kXq = kFuMaxH / 4 / (64 * kFuWaves);  // float4 of x per thread
   float4 xv[kXq];
 #pragma unroll
   for (int q = 0; q < kXq; ++q) xv[q] = xsrc[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)];
+  const int cand = active[min(item, n_active - 1)];
+  int n = n_active;
+  if (n_active_dev) n = min(n, *n_active_dev);
+  // Unconditional stores (a thread past the end rewrites the last float4 with
+  // the value it loaded from there): a conditional store lets the compiler
+  // sink each load into its branch, one round trip per load.
+#pragma unroll
+  for (int q = 0; q < kXq; ++q) xs4[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)] = xv[q];
+  if (blockIdx.x * kFuWaves >= n) return;  // uniform per block (before any barrier)
+  const bool live = item < n;
+  const int neuron = live ? cand : 0;  // idle waves read a valid row, never used
+  __builtin_amdgcn_sched_barrier(0);
+  const int nchunk = H >> 3;
+  const uint4* __restrict__ g = reinterpret_cast<const uint4*>(Wgu + (size_t)neuron * 2 * H);
+  const uint4* __restrict__ u = g + nchunk;
+  const uint4* __restrict__ d = reinterpret_cast<const uint4*>(WdT + (size_t)neuron * H);
   uint4 wg[kFuChunks], wu[kFuChunks], wd[kFuChunks];
 #pragma unroll
   for (int q = 0; q < kFuChunks; ++q) {
@@ -157,11 +166,6 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
     wg[q] = g[c];
     wu[q] = u[c];
     wd[q] = d[c];
-  }
-#pragma unroll
-  for (int q = 0; q < kXq; ++q) {
-    const int i = threadIdx.x + q * 64 * kFuWaves;
-    if (i < n4) xs4[i] = xv[q];
   }
   lds_barrier();
   float ag = 0.0f, au = 0.0f;

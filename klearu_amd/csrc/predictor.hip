@@ -109,11 +109,10 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_kernel(
   }
   // 3. x to LDS
   if (vec) {
+    // clamped, unconditional stores (see stage_f4)
 #pragma unroll
-    for (int q = 0; q < kXq; ++q) {
-      const int i = threadIdx.x + q * kL1Threads;
-      if (i < (n_in >> 2)) reinterpret_cast<float4*>(xs)[i] = xv[q];
-    }
+    for (int q = 0; q < kXq; ++q)
+      reinterpret_cast<float4*>(xs)[min((int)threadIdx.x + q * kL1Threads, (n_in >> 2) - 1)] = xv[q];
   } else {
     for (int j = threadIdx.x; j < n_in; j += kL1Threads) xs[j] = xr[j];
   }
@@ -188,8 +187,8 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
     int n_in, int hid, float* __restrict__ h) {
   using B8 = Blk8<W>;
   using V = typename B8::V;
-  constexpr int SPP = kL1LdsIn / kL1Stage / kL1Prod;                  // stages per producer
-  constexpr int kXq = (kL1LdsIn / 4 + kL1Threads - 1) / kL1Threads;  // x float4 per thread
+  constexpr int SPP = kL1LdsIn / kL1Stage / kL1Prod;  // stages per producer
+  constexpr int kXq = kL1LdsIn / 4 / 64;              // x float4 per consumer lane
   extern __shared__ float4 lds4[];
   float4(*P)[kL1Chains] = reinterpret_cast<float4(*)[kL1Chains]>(lds4);  // [n_in/4][chain]
   float* xs = reinterpret_cast<float*>(lds4 + (kL1LdsIn / 4) * kL1Chains);
@@ -199,16 +198,24 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
   const int nblk = (n_in + 7) >> 3;
   const int p = wave - 1;
   const float* xr = x + (size_t)b * n_in;
-  const bool vec = (n_in & 3) == 0;
-  float4 xv[kXq];
-#pragma unroll
-  for (int q = 0; q < kXq; ++q) {
-    const int i = threadIdx.x + q * kL1Threads;
-    xv[q] = vec ? reinterpret_cast<const float4*>(xr)[min(i, (n_in >> 2) - 1)] : make_float4(0, 0, 0, 0);
-  }
-  const float bv = bias[min(c0 + (lane & (kL1Chains - 1)), hid - 1)];
+  const int n4 = n_in >> 2;
+  // The consumer wave stages x (one round trip) while the producers issue
+  // every weight load: no wave waits for another's loads before the barrier.
   V pre[SPP][kL1Q];
-  if (wave > 0) {
+  float bv = 0.0f;
+  if (wave == 0) {
+    bv = bias[min(c0 + (lane & (kL1Chains - 1)), hid - 1)];
+    if ((n_in & 3) == 0) {
+      float4 xv[kXq];
+#pragma unroll
+      for (int q = 0; q < kXq; ++q) xv[q] = reinterpret_cast<const float4*>(xr)[min(lane + 64 * q, n4 - 1)];
+#pragma unroll
+      for (int q = 0; q < kXq; ++q)  // clamped, unconditional (see stage_f4)
+        reinterpret_cast<float4*>(xs)[min(lane + 64 * q, n4 - 1)] = xv[q];
+    } else {
+      for (int j = lane; j < n_in; j += 64) xs[j] = xr[j];
+    }
+  } else {
     const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
 #pragma unroll
     for (int i = 0; i < SPP; ++i)
@@ -221,71 +228,71 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
         pre[i][q] = wv[(size_t)jb * hid + ch];
       }
   }
-  if (vec) {
-#pragma unroll
-    for (int q = 0; q < kXq; ++q) {
-      const int i = threadIdx.x + q * kL1Threads;
-      if (i < (n_in >> 2)) reinterpret_cast<float4*>(xs)[i] = xv[q];
-    }
-  } else {
-    for (int j = threadIdx.x; j < n_in; j += kL1Threads) xs[j] = xr[j];
-  }
   lds_barrier();
-  if (wave > 0) {
-    // products in stage order; loads arrive in issue order, so each stage
-    // waits only for its own weights
+  // products of stage p + kL1Prod*i; loads arrive in issue order, so each
+  // stage waits only for its own weights
+  auto make = [&](int i) {
+    const int st = p + kL1Prod * i;
 #pragma unroll
-    for (int i = 0; i < SPP; ++i) {
-      const int st = p + kL1Prod * i;
+    for (int q = 0; q < kL1Q; ++q) {
+      const int pr = lane + 64 * q;
+      const int blk = pr / kL1Chains, ch = pr % kL1Chains;
+      const int j0 = (st * (kL1Stage / 8) + blk) * 8;
+      float w[8], pv[8];
+      B8::widen(pre[i][q], w);
 #pragma unroll
-      for (int q = 0; q < kL1Q; ++q) {
-        const int pr = lane + 64 * q;
-        const int blk = pr / kL1Chains, ch = pr % kL1Chains;
-        const int j0 = (st * (kL1Stage / 8) + blk) * 8;
-        float w[8], pv[8];
-        B8::widen(pre[i][q], w);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pv[e] = __fmul_rn(w[e], xs[min(j0 + e, kL1LdsIn - 1)]);
-        P[j0 / 4][ch] = make_float4(pv[0], pv[1], pv[2], pv[3]);
-        P[j0 / 4 + 1][ch] = make_float4(pv[4], pv[5], pv[6], pv[7]);
-      }
+      for (int e = 0; e < 8; ++e) pv[e] = __fmul_rn(w[e], xs[min(j0 + e, kL1LdsIn - 1)]);
+      P[j0 / 4][ch] = make_float4(pv[0], pv[1], pv[2], pv[3]);
+      P[j0 / 4 + 1][ch] = make_float4(pv[4], pv[5], pv[6], pv[7]);
     }
-  }
-  lds_barrier();
-  if (wave > 0) return;
-  // Consumer: the chains over the products.  A window of kWin quads (4 steps
-  // each) is in flight; each quad is added, then its register is refilled with
-  // the quad kWin ahead, so the only VALU work per step is the dependent add
-  // (LDS addresses are immediate offsets from one base pointer).  The window
-  // may read past the last product (still inside the block's LDS); those
-  // values are never added.
+  };
+  // Consumer chain over steps [j0, j1) (j0 a multiple of 4): a window of kWin
+  // quads is in flight; each quad is added, then its register is refilled
+  // with the quad kWin ahead, so the only VALU work per step is the dependent
+  // add (LDS addresses are immediate offsets from one base pointer).  Window
+  // reads past j1 are never added (they stay inside the block's LDS).
   constexpr int kWin = 16;   // quads in flight (64 steps)
   constexpr int kSup = 64;   // quads per unrolled loop body (256 steps)
   static_assert((kL1LdsIn / 4 + kWin) * kL1Chains <= (kL1LdsBytes / 16), "window stays in LDS");
   const int ln = lane < kL1Chains ? lane : kL1Chains - 1;
-  const float4* bp = &P[0][ln];
   float s = -0.0f;
-  float4 r[kWin];
+  auto run = [&](int j0, int j1) {
+    const float4* bp = &P[j0 >> 2][ln];
+    float4 r[kWin];
 #pragma unroll
-  for (int q = 0; q < kWin; ++q) r[q] = bp[q * kL1Chains];
-  const int nsup = n_in / (4 * kSup);
-  for (int c = 0; c < nsup; ++c) {
+    for (int q = 0; q < kWin; ++q) r[q] = bp[q * kL1Chains];
+    const int nsup = (j1 - j0) / (4 * kSup);
+    for (int c = 0; c < nsup; ++c) {
 #pragma unroll
-    for (int q = 0; q < kSup; ++q) {
-      s = __fadd_rn(s, r[q % kWin].x);
-      s = __fadd_rn(s, r[q % kWin].y);
-      s = __fadd_rn(s, r[q % kWin].z);
-      s = __fadd_rn(s, r[q % kWin].w);
-      r[q % kWin] = bp[(q + kWin) * kL1Chains];
-      // keep the refill here: the scheduler would otherwise sink it to its use
-      __builtin_amdgcn_sched_barrier(0);
+      for (int q = 0; q < kSup; ++q) {
+        s = __fadd_rn(s, r[q % kWin].x);
+        s = __fadd_rn(s, r[q % kWin].y);
+        s = __fadd_rn(s, r[q % kWin].z);
+        s = __fadd_rn(s, r[q % kWin].w);
+        r[q % kWin] = bp[(q + kWin) * kL1Chains];
+        // keep the refill here: the scheduler would otherwise sink it to its use
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      bp += kSup * kL1Chains;
     }
-    bp += kSup * kL1Chains;
+    const float* Pf = reinterpret_cast<const float*>(lds4);
+    for (int j = j0 + nsup * 4 * kSup; j < j1; ++j)
+      s = __fadd_rn(s, Pf[((j >> 2) * kL1Chains + ln) * 4 + (j & 3)]);
+  };
+  // The first round of stages (one per producer) is published first, so the
+  // chain starts while the producers form the rest.
+  constexpr int kSeg = kL1Prod * kL1Stage;
+  if (wave > 0) make(0);
+  lds_barrier();
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 1; i < SPP; ++i) make(i);
+  } else {
+    run(0, min(n_in, kSeg));
   }
-  // remaining steps (fewer than 4 * kSup), one by one in order
-  const float* Pf = reinterpret_cast<const float*>(lds4);
-  for (int j = nsup * 4 * kSup; j < n_in; ++j)
-    s = __fadd_rn(s, Pf[((j >> 2) * kL1Chains + ln) * 4 + (j & 3)]);
+  lds_barrier();
+  if (wave > 0) return;
+  if (n_in > kSeg) run(kSeg, n_in);
   const int chain = c0 + lane;
   if (lane < kL1Chains && chain < hid) h[(size_t)b * hid + chain] = fmaxf(__fadd_rn(s, bv), 0.0f);
 }
@@ -326,7 +333,7 @@ __global__ __launch_bounds__(kL2Threads) void pred_l2_kernel(const W* __restrict
   for (int jb = 0; jb < kMaxL2Hid / 8; ++jb)
     w[jb] = jb < nblk ? wv[(size_t)jb * n_out + oc] : B8::zero();
   if (vec) {
-    if ((int)threadIdx.x < (n_hid >> 2)) reinterpret_cast<float4*>(hs)[threadIdx.x] = hv;
+    reinterpret_cast<float4*>(hs)[min((int)threadIdx.x, (n_hid >> 2) - 1)] = hv;  // clamped (see stage_f4)
   } else {
     for (int i = threadIdx.x; i < n_hid; i += blockDim.x) hs[i] = hin[(size_t)b * n_hid + i];
   }
@@ -484,10 +491,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
 #pragma unroll
     for (int q = 0; q < kQ; ++q) v[q] = s4[min((int)threadIdx.x + q * kTopkThreads, (n >> 2) - 1)];
 #pragma unroll
-    for (int q = 0; q < kQ; ++q) {
-      const int i = threadIdx.x + q * kTopkThreads;
-      if (i < (n >> 2)) reinterpret_cast<float4*>(sstage)[i] = v[q];
-    }
+    for (int q = 0; q < kQ; ++q)  // clamped, unconditional (see stage_f4)
+      reinterpret_cast<float4*>(sstage)[min((int)threadIdx.x + q * kTopkThreads, (n >> 2) - 1)] = v[q];
   } else {
     for (int i = threadIdx.x; i < n; i += kTopkThreads) sstage[i] = __float_as_uint(sc[i]);
   }
