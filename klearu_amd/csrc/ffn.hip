@@ -113,14 +113,15 @@ __global__ __launch_bounds__(64 * kGuWaves) void ffn_gateup_kernel(
   }
 }
 
-// Single-token fused FFN: one wave per active neuron, kFuWaves neurons per
-// block.  Each lane issues its gate, up and down-row loads together (the down
-// row does not depend on h), so a wave has 3*H*2 bytes in flight at once; then
-// h = silu(g)*u, the down row is scaled by h (H/64 outputs per lane) and the
-// block adds its waves' rows in LDS in wave order into one partial row,
-// partial[block][H].  partials_reduce_kernel adds the partials in block order.
+// Single-token fused FFN: kFuWaves active neurons per block.  Wave w loads the
+// gate and up rows of neuron w and, for the down projection, column slice w
+// (H/kFuWaves columns) of all kFuWaves neurons' down rows, so every wave has
+// 3*H*2 bytes in flight at once.  h = silu(g)*u of each neuron is shared
+// through LDS, then each wave adds its column slice over the block's neurons
+// in neuron order and writes it to partial[block][H]: no LDS row reduction.
+// partials_reduce_kernel adds the partials in block order.
 constexpr int kFuWaves = 8;
-constexpr int kFuMaxH = 4096;              // 8 chunks of 16 B per lane per row
+constexpr int kFuMaxH = 4096;              // 8 chunks of 16 B per lane per gate/up row
 constexpr int kFuChunks = kFuMaxH / 512;
 
 __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
@@ -129,21 +130,23 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
     const int32_t* __restrict__ n_active_dev, float* __restrict__ hbuf,
     float* __restrict__ partial) {
   extern __shared__ float4 smem4[];
-  float4* xs4 = smem4;                                    // [H/4]
-  float* red = reinterpret_cast<float*>(smem4 + (H >> 2));  // [4][H]
+  float4* xs4 = smem4;                                          // [H/4]
+  float* hs = reinterpret_cast<float*>(smem4 + (kFuMaxH >> 2));  // [kFuWaves]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int item = blockIdx.x * kFuWaves + wave;
-  // x, the active index and the device count are requested together (one
-  // round trip), and x is in LDS before any weight load is issued: the weight
-  // loads are then waited for only where their data is used (vmcnt counts in
-  // issue order, so an x load behind them would wait for every weight).
+  const int first = blockIdx.x * kFuWaves;
+  // x, the block's active indices and the device count are requested together
+  // (one round trip), and x is in LDS before any weight load is issued: the
+  // weight loads are then waited for only where their data is used (vmcnt
+  // counts in issue order, so an x load behind them would wait for all).
   const int n4 = H >> 2;
   const float4* __restrict__ xsrc = reinterpret_cast<const float4*>(x);
   constexpr int kXq = kFuMaxH / 4 / (64 * kFuWaves);  // float4 of x per thread
   float4 xv[kXq];
 #pragma unroll
   for (int q = 0; q < kXq; ++q) xv[q] = xsrc[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)];
-  const int cand = active[min(item, n_active - 1)];
+  int cand[kFuWaves];
+#pragma unroll
+  for (int k = 0; k < kFuWaves; ++k) cand[k] = active[min(first + k, n_active - 1)];
   int n = n_active;
   if (n_active_dev) n = min(n, *n_active_dev);
   // Unconditional stores (a thread past the end rewrites the last float4 with
@@ -151,22 +154,29 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
   // sink each load into its branch, one round trip per load.
 #pragma unroll
   for (int q = 0; q < kXq; ++q) xs4[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)] = xv[q];
-  if (blockIdx.x * kFuWaves >= n) return;  // uniform per block (before any barrier)
-  const bool live = item < n;
-  const int neuron = live ? cand : 0;  // idle waves read a valid row, never used
+  if (first >= n) return;  // uniform per block (before any barrier)
+  const int nlive = min(kFuWaves, n - first);
+  int nid[kFuWaves];
+#pragma unroll
+  for (int k = 0; k < kFuWaves; ++k) nid[k] = k < nlive ? cand[k] : 0;  // idle slots read row 0, unused
   __builtin_amdgcn_sched_barrier(0);
   const int nchunk = H >> 3;
-  const uint4* __restrict__ g = reinterpret_cast<const uint4*>(Wgu + (size_t)neuron * 2 * H);
+  const int own = nid[wave];
+  const uint4* __restrict__ g = reinterpret_cast<const uint4*>(Wgu + (size_t)own * 2 * H);
   const uint4* __restrict__ u = g + nchunk;
-  const uint4* __restrict__ d = reinterpret_cast<const uint4*>(WdT + (size_t)neuron * H);
-  uint4 wg[kFuChunks], wu[kFuChunks], wd[kFuChunks];
+  uint4 wg[kFuChunks], wu[kFuChunks], wd[kFuWaves];
 #pragma unroll
   for (int q = 0; q < kFuChunks; ++q) {
     const int c = min(lane + 64 * q, nchunk - 1);
     wg[q] = g[c];
     wu[q] = u[c];
-    wd[q] = d[c];
   }
+  // column slice of this wave: H / kFuWaves columns, 8 per lane
+  const int slice = H / kFuWaves;
+  const int col = wave * slice + 8 * min(lane, slice / 8 - 1);
+#pragma unroll
+  for (int k = 0; k < kFuWaves; ++k)
+    wd[k] = *reinterpret_cast<const uint4*>(WdT + (size_t)nid[k] * H + col);
   lds_barrier();
   float ag = 0.0f, au = 0.0f;
 #pragma unroll
@@ -187,50 +197,28 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
   // wave-uniform values: the exp table lookup inside silu becomes a scalar load
   const float gs = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_sum(ag))));
   const float us = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_sum(au))));
-  const float h = live ? silu_ref(gs) * us : 0.0f;
-  // h * down row; waves 0-3 write their rows, waves 4-7 add theirs, then the
-  // four rows are added in fixed order.
-  float* my = red + (size_t)(wave & 3) * H;
-  if (wave < 4) {
+  const float h = wave < nlive ? silu_ref(gs) * us : 0.0f;
+  if (lane == 0) hs[wave] = h;
+  if (lane == 0 && wave < nlive && hbuf) hbuf[first + wave] = h;
+  lds_barrier();
+  float acc[8];
 #pragma unroll
-    for (int q = 0; q < kFuChunks; ++q) {
-      const int c = lane + 64 * q;
-      if (c < nchunk) {
-        float4* o = reinterpret_cast<float4*>(my + 8 * c);
-        o[0] = make_float4(h * bf16_lo(wd[q].x), h * bf16_hi(wd[q].x), h * bf16_lo(wd[q].y), h * bf16_hi(wd[q].y));
-        o[1] = make_float4(h * bf16_lo(wd[q].z), h * bf16_hi(wd[q].z), h * bf16_lo(wd[q].w), h * bf16_hi(wd[q].w));
-      }
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kFuWaves; ++k) {
+    if (k < nlive) {
+      const float hk = hs[k];
+      acc[0] = fmaf(hk, bf16_lo(wd[k].x), acc[0]); acc[1] = fmaf(hk, bf16_hi(wd[k].x), acc[1]);
+      acc[2] = fmaf(hk, bf16_lo(wd[k].y), acc[2]); acc[3] = fmaf(hk, bf16_hi(wd[k].y), acc[3]);
+      acc[4] = fmaf(hk, bf16_lo(wd[k].z), acc[4]); acc[5] = fmaf(hk, bf16_hi(wd[k].z), acc[5]);
+      acc[6] = fmaf(hk, bf16_lo(wd[k].w), acc[6]); acc[7] = fmaf(hk, bf16_hi(wd[k].w), acc[7]);
     }
   }
-  __syncthreads();
-  if (wave >= 4) {
-#pragma unroll
-    for (int q = 0; q < kFuChunks; ++q) {
-      const int c = lane + 64 * q;
-      if (c < nchunk) {
-        float4* o = reinterpret_cast<float4*>(my + 8 * c);
-        float4 a = o[0], b = o[1];
-        a.x = fmaf(h, bf16_lo(wd[q].x), a.x); a.y = fmaf(h, bf16_hi(wd[q].x), a.y);
-        a.z = fmaf(h, bf16_lo(wd[q].y), a.z); a.w = fmaf(h, bf16_hi(wd[q].y), a.w);
-        b.x = fmaf(h, bf16_lo(wd[q].z), b.x); b.y = fmaf(h, bf16_hi(wd[q].z), b.y);
-        b.z = fmaf(h, bf16_lo(wd[q].w), b.z); b.w = fmaf(h, bf16_hi(wd[q].w), b.w);
-        o[0] = a;
-        o[1] = b;
-      }
-    }
+  if (8 * lane < slice) {
+    float4* o = reinterpret_cast<float4*>(partial + (size_t)blockIdx.x * H + col);
+    o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
   }
-  __syncthreads();
-  float* prow = partial + (size_t)blockIdx.x * H;
-  for (int j = threadIdx.x * 4; j < H; j += blockDim.x * 4) {
-    const float4 r0 = *reinterpret_cast<const float4*>(red + j);
-    const float4 r1 = *reinterpret_cast<const float4*>(red + H + j);
-    const float4 r2 = *reinterpret_cast<const float4*>(red + 2 * H + j);
-    const float4 r3 = *reinterpret_cast<const float4*>(red + 3 * H + j);
-    *reinterpret_cast<float4*>(prow + j) =
-        make_float4((r0.x + r1.x) + (r2.x + r3.x), (r0.y + r1.y) + (r2.y + r3.y),
-                    (r0.z + r1.z) + (r2.z + r3.z), (r0.w + r1.w) + (r2.w + r3.w));
-  }
-  if (lane == 0 && live && hbuf) hbuf[item] = h;
 }
 
 // RmsNorm::forward (crates/klearu-llm/src/model/rms_norm.rs:43-64): one block
@@ -453,10 +441,10 @@ extern "C" int kh_sparse_ffn_forward(const kh_sparse_ffn* f, const float* x_dev,
   }
   KH_CHECK_ARG(active_dev != nullptr, "null active list");
   const int b = static_cast<int>(batch);
-  if (batch == 1 && f->hidden <= kFuMaxH) {
+  if (batch == 1 && f->hidden <= kFuMaxH && f->hidden % (8 * kFuWaves) == 0) {
     const int H = f->hidden;
     const int blocks = ceil_div(n_active, kFuWaves);
-    const size_t lds = sizeof(float) * (size_t)H * 5;
+    const size_t lds = sizeof(float) * ((size_t)kFuMaxH + kFuWaves);
     static bool attr = false;
     if (!attr) {
       KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel),

@@ -111,6 +111,8 @@ def _ffn_case(orc, rng, H, I, k, batch):
     (4096, 11008, 1652, 2),
     (4096, 11008, 1652, 16),  # cfg3 batch 16 shared set
     (264, 100, 37, 3),        # ragged hidden (not a multiple of 256)
+    (264, 100, 37, 1),        # single token, hidden not a multiple of 64 (general path)
+    (1024, 2816, 403, 1),     # single token, partial last block
     (512, 64, 64, 1),         # every neuron active
     (512, 64, 1, 1),          # a single neuron
 ])
