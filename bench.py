@@ -10,7 +10,9 @@ layers of
     norm = RmsNorm(hidden); active = predictor.select_top_k(norm, k);
     hidden += sparse_mlp::forward_sparse(norm, active)
 
-(crates/klearu-llm/src/sparse/mod.rs:115-142), captured in one HIP graph.
+(crates/klearu-llm/src/sparse/mod.rs:115-142), captured in one HIP graph.  At
+batch 1 each layer is one kh_dejavu_mlp_block call (the RmsNorm runs inside
+the predictor and FFN kernels).
 
 JSON line fields beyond the driver contract:
   ffn_only      the FFN calls alone (32 layers, fixed active sets): tokens/s and
@@ -157,13 +159,22 @@ def ffn_leg(name, L, H, I, R, frac, B, steps, warmup, seed, model=None, timer=No
             _lib.call("kh_sparse_ffn_forward", mlps[l]._h, ptr(norm), B, ptr(union[l]), I, ptr(ucount[l]),
                       ptr(hidden), 1, st)
 
+    stats = torch.empty(B, (H + 63) // 64, dtype=torch.float32, device=dev)
+
     def step():
         st = stream_ptr()
+        if B == 1:
+            # fused block: the RmsNorm runs inside the predictor and FFN kernels
+            # from per-block sums of squares that each block hands to the next
+            _lib.call("kh_rms_stats", ptr(hidden), 1, H, ptr(stats), st)
+            for l in range(L):
+                _lib.call("kh_dejavu_mlp_block", preds[l]._h, mlps[l]._h, ptr(hidden), ptr(w_norm), 1e-5, k,
+                          ptr(active[l]), ptr(stats), st)
+            return
         for l in range(L):
             _lib.call("kh_rmsnorm", ptr(hidden), ptr(w_norm), B, H, 1e-5, ptr(norm), st)
             _lib.call("kh_predictor_select_top_k", preds[l]._h, ptr(norm), B, k, ORDER_ASCENDING, ptr(active[l]), st)
-            if B > 1:
-                _lib.call("kh_union_active", ptr(active[l]), B, k, I, ptr(union[l]), ptr(ucount[l]), st)
+            _lib.call("kh_union_active", ptr(active[l]), B, k, I, ptr(union[l]), ptr(ucount[l]), st)
             ffn_call(l, st)
 
     def ffn_only():

@@ -270,6 +270,24 @@ int kh_sparse_ffn_last_hidden(const kh_sparse_ffn* f, float* h_dev, int64_t batc
 int kh_rmsnorm(const float* x_dev, const float* w_dev, int64_t batch, int n, float eps,
                float* y_dev, void* stream);
 
+/* Per-block sums of squares x[b][64*i .. 64*i+63]^2 -> stats[b][i]
+ * (ceil(n/64) per row): the RmsNorm statistics kh_dejavu_mlp_block reads. */
+int kh_rms_stats(const float* x_dev, int64_t batch, int n, float* stats_dev, void* stream);
+/* One decode step (batch 1) of the Deja Vu MLP block as
+ * SparseModel::forward_decode_sparse runs it (crates/klearu-llm/src/sparse/mod.rs:115-142):
+ *   norm = RmsNorm(hidden) (model/rms_norm.rs:43-64, weight norm_w, eps);
+ *   active = predictor.select_top_k(norm, k) (ascending ids into active_dev[k]);
+ *   hidden += sparse_mlp::forward_sparse(norm, active).
+ * The norm is applied inside the predictor and FFN kernels from stats_dev
+ * (ceil(hidden/64) sums of squares of the current hidden row, from
+ * kh_rms_stats or from the previous block); on return stats_dev holds those of
+ * the updated row, so consecutive blocks need no separate norm pass.
+ * Requires predictor input_dim == hidden, output_dim == intermediate, hidden a
+ * multiple of 64 and at most 4096. */
+int kh_dejavu_mlp_block(const kh_predictor* p, const kh_sparse_ffn* f, float* hidden_dev,
+                        const float* norm_w_dev, float eps, int k, int32_t* active_dev,
+                        float* stats_dev, void* stream);
+
 /* ======================================================================== */
 /* Head-sparse decode attention (crates/klearu-llm/src/sparse/sparse_attention.rs) */
 /* ======================================================================== */

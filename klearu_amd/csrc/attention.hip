@@ -775,7 +775,7 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   KH_LAUNCHED();
   hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch),
                      dim3(64 * kRedWaves), 0, st, partial, H, groups, out, accumulate, a->lens,
-                     a->max_seq);
+                     a->max_seq, nullptr);
   KH_LAUNCHED();
   return KH_OK;
 }

@@ -261,6 +261,35 @@ __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* ws
   return before + x - v;
 }
 
+// RmsNorm scale 1/sqrt(sum(x^2)/n + eps) (model/rms_norm.rs:49-54) from
+// per-block sums of squares stats[0..nparts): the parts are added with a
+// fixed lane assignment and butterfly, so every wave that calls this gets the
+// same bits.  A whole wave must call it.
+__device__ __forceinline__ float rms_inv(const float* __restrict__ stats, int nparts, int n,
+                                         float eps) {
+  const int lane = threadIdx.x & 63;
+  float v = 0.0f;
+  for (int i = lane; i < nparts; i += 64) v += stats[i];
+  const float tot = wave_sum(v);
+  const float rms = sqrtf(tot / static_cast<float>(n) + eps);
+  return 1.0f / rms;
+}
+
+// RmsNorm applied inside a consumer kernel: weight, per-block sums of squares
+// of the row (nparts per row) and eps; w == nullptr means the input is used as is.
+struct NormIn {
+  const float* w = nullptr;
+  const float* stats = nullptr;
+  int nparts = 0;
+  float eps = 0.0f;
+};
+
+// Cross-file helpers of the fused Deja Vu MLP block (predictor.hip).
+int predictor_in_dim(const kh_predictor* p);
+int predictor_out_dim(const kh_predictor* p);
+int predictor_topk_normed(const kh_predictor* p, const float* hidden, int k, int32_t* ids,
+                          const NormIn& nrm, hipStream_t st);
+
 // Workgroup barrier that waits only for LDS traffic.  __syncthreads() on gfx9
 // also waits for every outstanding vector-memory load (vmcnt counts loads and
 // stores together), which would drain global prefetches issued before it.

@@ -128,7 +128,8 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
     const uint16_t* __restrict__ Wgu, const uint16_t* __restrict__ WdT,
     const float* __restrict__ x, int H, const int32_t* __restrict__ active, int n_active,
     const int32_t* __restrict__ n_active_dev, float* __restrict__ hbuf,
-    float* __restrict__ partial) {
+    float* __restrict__ partial, const float* __restrict__ norm_w,
+    const float* __restrict__ stats, int nparts, float eps) {
   extern __shared__ float4 smem4[];
   float4* xs4 = smem4;                                          // [H/4]
   float* hs = reinterpret_cast<float*>(smem4 + (kFuMaxH >> 2));  // [kFuWaves]
@@ -149,6 +150,22 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
   for (int k = 0; k < kFuWaves; ++k) cand[k] = active[min(first + k, n_active - 1)];
   int n = n_active;
   if (n_active_dev) n = min(n, *n_active_dev);
+  if (norm_w) {
+    // RmsNorm of the hidden row (x * inv) * w, inv from the row's per-block
+    // sums of squares exactly as the predictor computes it
+    float4 wn[kXq];
+#pragma unroll
+    for (int q = 0; q < kXq; ++q)
+      wn[q] = reinterpret_cast<const float4*>(norm_w)[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)];
+    const float inv = rms_inv(stats, nparts, H, eps);
+#pragma unroll
+    for (int q = 0; q < kXq; ++q) {
+      xv[q].x = (xv[q].x * inv) * wn[q].x;
+      xv[q].y = (xv[q].y * inv) * wn[q].y;
+      xv[q].z = (xv[q].z * inv) * wn[q].z;
+      xv[q].w = (xv[q].w * inv) * wn[q].w;
+    }
+  }
   // Unconditional stores (a thread past the end rewrites the last float4 with
   // the value it loaded from there): a conditional store lets the compiler
   // sink each load into its branch, one round trip per load.
@@ -420,7 +437,36 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
                      n_active, n_active_dev, f->hbuf, f->inter, batch, groups, f->partial);
   KH_LAUNCHED();
   hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch), dim3(64 * kRedWaves),
-                     0, st, f->partial, H, groups, y, accumulate, nullptr, 0);
+                     0, st, f->partial, H, groups, y, accumulate, nullptr, 0, nullptr);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
+static bool ffn_fused_ok(const kh_sparse_ffn* f, int64_t batch) {
+  return batch == 1 && f->hidden <= kFuMaxH && f->hidden % (8 * kFuWaves) == 0;
+}
+
+// Single-token fused FFN + ordered reduce.  With nrm.w set, x is the
+// un-normalised hidden row (RmsNorm applied in the kernel); with stats_out
+// set, the reduce also writes the per-block sums of squares of y.
+static int ffn_fused_launch(const kh_sparse_ffn* f, const float* x, const int32_t* active,
+                            int n_active, const int32_t* n_active_dev, float* y, int accumulate,
+                            const NormIn& nrm, float* stats_out, hipStream_t st) {
+  const int H = f->hidden;
+  const int blocks = ceil_div(n_active, kFuWaves);
+  const size_t lds = sizeof(float) * ((size_t)kFuMaxH + kFuWaves);
+  static bool attr = false;
+  if (!attr) {
+    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+    attr = true;
+  }
+  hipLaunchKernelGGL(ffn_fused1_kernel, dim3(blocks), dim3(64 * kFuWaves), lds, st, f->wgu, f->wdt,
+                     x, H, active, n_active, n_active_dev, f->hbuf, f->partial, nrm.w, nrm.stats,
+                     nrm.nparts, nrm.eps);
+  KH_LAUNCHED();
+  hipLaunchKernelGGL(partials_reduce_kernel<1>, dim3(ceil_div(H, 64), 1), dim3(64 * kRedWaves), 0,
+                     st, f->partial, H, blocks, y, accumulate, nullptr, 0, stats_out);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -441,24 +487,9 @@ extern "C" int kh_sparse_ffn_forward(const kh_sparse_ffn* f, const float* x_dev,
   }
   KH_CHECK_ARG(active_dev != nullptr, "null active list");
   const int b = static_cast<int>(batch);
-  if (batch == 1 && f->hidden <= kFuMaxH && f->hidden % (8 * kFuWaves) == 0) {
-    const int H = f->hidden;
-    const int blocks = ceil_div(n_active, kFuWaves);
-    const size_t lds = sizeof(float) * ((size_t)kFuMaxH + kFuWaves);
-    static bool attr = false;
-    if (!attr) {
-      KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
-      attr = true;
-    }
-    hipLaunchKernelGGL(ffn_fused1_kernel, dim3(blocks), dim3(64 * kFuWaves), lds, st, f->wgu,
-                       f->wdt, x_dev, H, active_dev, n_active, n_active_dev, f->hbuf, f->partial);
-    KH_LAUNCHED();
-    hipLaunchKernelGGL(partials_reduce_kernel<1>, dim3(ceil_div(H, 64), 1), dim3(64 * kRedWaves), 0,
-                       st, f->partial, H, blocks, y_dev, accumulate, nullptr, 0);
-    KH_LAUNCHED();
-    return KH_OK;
-  }
+  if (ffn_fused_ok(f, batch))
+    return ffn_fused_launch(f, x_dev, active_dev, n_active, n_active_dev, y_dev, accumulate,
+                            NormIn{}, nullptr, st);
   switch (ffn_tmpl(batch)) {
     case 1: return ffn_launch<1>(f, x_dev, b, active_dev, n_active, n_active_dev, y_dev, accumulate, st);
     case 2: return ffn_launch<2>(f, x_dev, b, active_dev, n_active, n_active_dev, y_dev, accumulate, st);
@@ -488,4 +519,49 @@ extern "C" int kh_rmsnorm(const float* x_dev, const float* w_dev, int64_t batch,
                      n, eps, y_dev);
   KH_LAUNCHED();
   return KH_OK;
+}
+
+namespace kh {
+// Per-block (64 columns) sums of squares of each row: the RmsNorm statistics
+// consumed by kernels that apply the norm themselves (rms_inv).
+__global__ __launch_bounds__(64) void rms_stats_kernel(const float* __restrict__ x, int n,
+                                                      float* __restrict__ stats) {
+  const int b = blockIdx.y;
+  const int j = blockIdx.x * 64 + threadIdx.x;
+  const float v = j < n ? x[(size_t)b * n + j] : 0.0f;
+  const float sq = wave_sum(v * v);
+  if (threadIdx.x == 0) stats[(size_t)b * gridDim.x + blockIdx.x] = sq;
+}
+}  // namespace kh
+
+extern "C" int kh_rms_stats(const float* x_dev, int64_t batch, int n, float* stats_dev,
+                            void* stream) {
+  KH_CHECK_ARG(x_dev && stats_dev, "null argument");
+  KH_CHECK_ARG(batch >= 0 && batch <= 65535 && n > 0, "bad shape");
+  if (batch == 0) return KH_OK;
+  hipLaunchKernelGGL(rms_stats_kernel, dim3(ceil_div(n, 64), batch), dim3(64), 0,
+                     as_stream(stream), x_dev, n, stats_dev);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
+extern "C" int kh_dejavu_mlp_block(const kh_predictor* p, const kh_sparse_ffn* f, float* hidden_dev,
+                                   const float* norm_w_dev, float eps, int k, int32_t* active_dev,
+                                   float* stats_dev, void* stream) {
+  KH_CHECK_ARG(p && f && hidden_dev && norm_w_dev && active_dev && stats_dev, "null argument");
+  KH_CHECK_ARG(k >= 1 && k <= f->inter, "k %d not in [1,%d]", k, f->inter);
+  KH_CHECK_ARG(predictor_in_dim(p) == f->hidden && predictor_out_dim(p) == f->inter,
+               "predictor %d->%d does not match the FFN (hidden %d, intermediate %d)",
+               predictor_in_dim(p), predictor_out_dim(p), f->hidden, f->inter);
+  KH_CHECK_ARG(ffn_fused_ok(f, 1) && f->hidden <= 4096,
+               "the fused block needs hidden <= 4096 and a multiple of %d", 8 * kFuWaves);
+  hipStream_t st = as_stream(stream);
+  NormIn nrm;
+  nrm.w = norm_w_dev;
+  nrm.stats = stats_dev;
+  nrm.nparts = ceil_div(f->hidden, 64);
+  nrm.eps = eps;
+  int rc = predictor_topk_normed(p, hidden_dev, k, active_dev, nrm, st);
+  if (rc != KH_OK) return rc;
+  return ffn_fused_launch(f, hidden_dev, active_dev, k, nullptr, hidden_dev, 1, nrm, stats_dev, st);
 }

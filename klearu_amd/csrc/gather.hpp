@@ -107,13 +107,16 @@ __global__ __launch_bounds__(64 * kRedWaves) void partials_reduce_kernel(const f
                                                                     float* __restrict__ y,
                                                                     int accumulate,
                                                                     int32_t* __restrict__ bump,
-                                                                    int bump_limit) {
+                                                                    int bump_limit,
+                                                                    float* __restrict__ ss_out) {
   __shared__ float sums[kRedWaves][64];
   const int b = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int j = blockIdx.x * 64 + lane;
   const int jc = min(j, H - 1);
   constexpr int U = 16;
+  // the value accumulated into is requested with the partials, not after them
+  const float y0 = (accumulate && wave == 0) ? y[(size_t)b * H + jc] : 0.0f;
   float t = 0.0f;
   for (int g0 = wave; g0 < groups; g0 += kRedWaves * U) {
     float v[U];
@@ -126,12 +129,18 @@ __global__ __launch_bounds__(64 * kRedWaves) void partials_reduce_kernel(const f
   }
   sums[wave][lane] = t;
   __syncthreads();
-  if (wave == 0 && j < H) {
+  if (wave == 0) {
     float tot = 0.0f;
 #pragma unroll
     for (int w = 0; w < kRedWaves; ++w) tot += sums[w][lane];
-    float* yp = y + (size_t)b * H + j;
-    *yp = accumulate ? (*yp + tot) : tot;
+    const float yn = accumulate ? y0 + tot : tot;
+    if (j < H) y[(size_t)b * H + j] = yn;
+    // Sum of squares of this block's 64 outputs: the RmsNorm statistics of
+    // the updated row (rms_inv adds the blocks' values in a fixed order).
+    if (ss_out) {
+      const float sq = wave_sum(j < H ? yn * yn : 0.0f);
+      if (lane == 0) ss_out[(size_t)b * gridDim.x + blockIdx.x] = sq;
+    }
   }
   // Optional per-row counter advanced once the row's output is complete
   // (the KV-cache length of decode attention).

@@ -181,10 +181,14 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_kernel(
 constexpr int kL1LdsIn = 4096;
 constexpr int kL1LdsBytes = (kL1Chains + 1) * kL1LdsIn * 4;  // products + x
 
+// With norm_w set, x is the un-normalised hidden row and the kernel applies
+// RmsNorm first: (x * inv) * norm_w with inv from the per-block sums of squares
+// `stats` (rms_inv), as every other consumer of the row computes it.
 template <typename W>
 __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
     const W* __restrict__ Wb, const float* __restrict__ bias, const float* __restrict__ x,
-    int n_in, int hid, float* __restrict__ h) {
+    int n_in, int hid, float* __restrict__ h, const float* __restrict__ norm_w,
+    const float* __restrict__ stats, int nparts, float eps) {
   using B8 = Blk8<W>;
   using V = typename B8::V;
   constexpr int SPP = kL1LdsIn / kL1Stage / kL1Prod;  // stages per producer
@@ -209,11 +213,25 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
       float4 xv[kXq];
 #pragma unroll
       for (int q = 0; q < kXq; ++q) xv[q] = reinterpret_cast<const float4*>(xr)[min(lane + 64 * q, n4 - 1)];
+      if (norm_w) {
+        float4 wn[kXq];
+#pragma unroll
+        for (int q = 0; q < kXq; ++q) wn[q] = reinterpret_cast<const float4*>(norm_w)[min(lane + 64 * q, n4 - 1)];
+        const float inv = rms_inv(stats + (size_t)b * nparts, nparts, n_in, eps);
+#pragma unroll
+        for (int q = 0; q < kXq; ++q) {
+          xv[q].x = (xv[q].x * inv) * wn[q].x;
+          xv[q].y = (xv[q].y * inv) * wn[q].y;
+          xv[q].z = (xv[q].z * inv) * wn[q].z;
+          xv[q].w = (xv[q].w * inv) * wn[q].w;
+        }
+      }
 #pragma unroll
       for (int q = 0; q < kXq; ++q)  // clamped, unconditional (see stage_f4)
         reinterpret_cast<float4*>(xs)[min(lane + 64 * q, n4 - 1)] = xv[q];
     } else {
-      for (int j = lane; j < n_in; j += 64) xs[j] = xr[j];
+      const float inv = norm_w ? rms_inv(stats + (size_t)b * nparts, nparts, n_in, eps) : 1.0f;
+      for (int j = lane; j < n_in; j += 64) xs[j] = norm_w ? (xr[j] * inv) * norm_w[j] : xr[j];
     }
   } else {
     const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
@@ -794,7 +812,7 @@ static int ensure_batch(kh_predictor* p, int64_t batch) {
 
 template <typename W>
 static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* scores,
-                         hipStream_t st) {
+                         hipStream_t st, const NormIn& nrm) {
   const W* w1 = static_cast<const W*>(p->w1b);
   const W* w2 = static_cast<const W*>(p->w2b);
   const int l1_stages = ceil_div(p->in_dim, kL1Stage);
@@ -808,7 +826,12 @@ static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* 
   }
   if (p->in_dim <= kL1LdsIn)
     hipLaunchKernelGGL(pred_l1_lds_kernel<W>, dim3(ceil_div(p->hid, kL1Chains), batch),
-                       dim3(kL1Threads), kL1LdsBytes, st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
+                       dim3(kL1Threads), kL1LdsBytes, st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf,
+                       nrm.w, nrm.stats, nrm.nparts, nrm.eps);
+  else if (nrm.w) {
+    set_error("the fused RmsNorm supports predictor inputs up to %d", kL1LdsIn);
+    return KH_ERR_UNSUPPORTED;
+  }
   else if (l1_stages <= 8 * kL1Prod)
     hipLaunchKernelGGL((pred_l1_kernel<W, 8>), dim3(ceil_div(p->hid, kL1Chains), batch),
                        dim3(kL1Threads), 0, st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
@@ -830,12 +853,12 @@ static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* 
 }
 
 static int predict_into(const kh_predictor* pc, const float* x, int64_t batch, float* scores,
-                        hipStream_t st) {
+                        hipStream_t st, const NormIn& nrm = NormIn{}) {
   auto* p = const_cast<kh_predictor*>(pc);
   int rc = ensure_batch(p, batch);
   if (rc != KH_OK) return rc;
-  return p->bf16 ? predict_typed<uint16_t>(p, x, batch, scores, st)
-                 : predict_typed<float>(p, x, batch, scores, st);
+  return p->bf16 ? predict_typed<uint16_t>(p, x, batch, scores, st, nrm)
+                 : predict_typed<float>(p, x, batch, scores, st, nrm);
 }
 
 extern "C" int kh_predictor_predict(const kh_predictor* p, const float* x_dev, int64_t batch,
@@ -926,3 +949,19 @@ extern "C" int kh_union_active(const int32_t* ids_dev, int64_t batch, int k, int
   KH_LAUNCHED();
   return KH_OK;
 }
+
+namespace kh {
+int predictor_in_dim(const kh_predictor* p) { return p->in_dim; }
+int predictor_out_dim(const kh_predictor* p) { return p->out_dim; }
+// Predictor scores of RmsNorm(hidden) (norm applied inside layer 1) and the
+// top-k ids in ascending order, batch 1.
+int predictor_topk_normed(const kh_predictor* pc, const float* hidden, int k, int32_t* ids,
+                          const NormIn& nrm, hipStream_t st) {
+  auto* p = const_cast<kh_predictor*>(pc);
+  int rc = ensure_batch(p, 1);
+  if (rc != KH_OK) return rc;
+  rc = predict_into(p, hidden, 1, p->sbuf, st, nrm);
+  if (rc != KH_OK) return rc;
+  return topk_launch(p->sbuf, 1, p->out_dim, k, KH_ORDER_ASCENDING, ids, st);
+}
+}  // namespace kh

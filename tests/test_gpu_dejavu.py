@@ -177,3 +177,44 @@ def test_rmsnorm(kh, orc):
     got = rmsnorm(torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), 1e-5).cpu().numpy()
     for b in range(4):
         np.testing.assert_allclose(got[b], orc.rmsnorm(x[b], w, 1e-5), rtol=1e-5, atol=1e-6)
+
+
+def test_mlp_block_three_layers(kh, orc):
+    """kh_dejavu_mlp_block chained over three layers (stats carried between
+    blocks) against the oracle's rmsnorm -> predictor -> top-k -> SwiGLU ->
+    residual.  The fused norm sums squares in a different order, so the
+    predictor sees inputs within rounding of the oracle's: the selections must
+    agree except for neurons whose oracle score lies within 1e-6 relative of
+    the k-th score; outputs within the BF16-weight tolerance."""
+    from klearu_amd.dejavu import Mlp, SparsityPredictor, mlp_block
+    rng = np.random.default_rng(31)
+    H, I, R, k = 1024, 2816, 64, 423
+    hidden = rng.standard_normal(H).astype(np.float32)
+    wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    hd = torch.from_numpy(hidden.copy()).cuda()
+    wnd = torch.from_numpy(wn).cuda()
+    stats = None
+    ref = hidden.copy()
+    for layer in range(3):
+        wg, wu, wd, _, _ = _ffn_case(orc, rng, H, I, k, 1)
+        w1, b1, w2, b2 = make_predictor(orc, rng, H, R, I, bias=True)
+        p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
+        mlp = Mlp(wg, wu, wd, max_batch=1)
+        act, stats = mlp_block(p, mlp, hd, wnd, 1e-5, k, stats=stats)
+        norm = orc.rmsnorm(ref, wn, 1e-5)
+        scores, _ = orc.predictor_predict(w1, b1, w2, b2, norm)
+        sel = np.sort(orc.select_top_k(scores, k))
+        got = act.cpu().numpy()
+        kth = np.sort(scores)[::-1][k - 1]
+        diff = np.setxor1d(got, sel)
+        assert np.all(np.abs(scores[diff] - kth) <= 1e-6 * abs(kth)), (layer, diff)
+        y, _ = orc.sparse_mlp_forward_bf16(wg, wu, wd, norm, got.astype(np.int64))
+        ref = ref + y
+        out = hd.cpu().numpy()
+        scale = float(np.max(np.abs(ref)))
+        print(f"layer {layer}: max-abs {float(np.max(np.abs(out - ref))):.3e} (max |hidden| {scale:.3e}), "
+              f"{diff.size} boundary swaps")
+        np.testing.assert_allclose(out, ref, rtol=RTOL, atol=1e-4 * scale)
+        ref = out.astype(np.float32)   # continue from the GPU state (selections may differ at ties)
+        np.testing.assert_allclose(stats.cpu().numpy().sum(), float(np.sum(out.astype(np.float64) ** 2)),
+                                   rtol=1e-5)
