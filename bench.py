@@ -147,7 +147,7 @@ def ffn_leg(name, L, H, I, R, frac, B, steps, warmup, seed, model=None, timer=No
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed + 1)
     hidden = torch.randn(B, H, generator=gen, device=dev)
-    norm = torch.empty_like(hidden)
+    norm = torch.randn(B, H, generator=gen, device=dev)
     active = [torch.empty(B, k, dtype=torch.int32, device=dev) for _ in range(L)]
     union = [torch.empty(I, dtype=torch.int32, device=dev) for _ in range(L)]
     ucount = [torch.zeros(1, dtype=torch.int32, device=dev) for _ in range(L)]
@@ -453,6 +453,38 @@ def slide_cfg5_leg(steps, seed, timer, cpu_seconds):
 
 
 # --------------------------------------------------------------------------- main
+def traffic_probe(seed):
+    """Eager dispatches for the rocprofv3 --pmc traffic runs (FETCH_SIZE, then
+    WRITE_SIZE): a calibration kernel of known size (y = 2x over 256 MiB f32:
+    256 MiB read, 256 MiB written), then one kh_sparse_ffn_forward at cfg3
+    shape on each of 8 layers (cold weights), each with its own k = 1652 active
+    set.  Prints the sizes the counters are compared with."""
+    import torch
+    from klearu_amd import _lib
+    from klearu_amd._dev import ptr, stream_ptr
+    from klearu_amd.dejavu import keep_count
+
+    H, I, L = 4096, 11008, 8
+    k = keep_count(I, 0.15)
+    mlps, _ = build_ffn_model(L, H, I, 256, seed, 1)
+    src = torch.randn(64 << 20, device="cuda")
+    dst = torch.empty_like(src)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 7)
+    x = torch.randn(1, H, generator=g, device="cuda")
+    y = torch.zeros(1, H, device="cuda")
+    act = [torch.sort(torch.randperm(I, generator=g, device="cuda")[:k])[0].to(torch.int32) for _ in range(L)]
+    torch.cuda.synchronize()
+    for _ in range(3):
+        torch.mul(src, 2.0, out=dst)
+    torch.cuda.synchronize()
+    for l in range(L):
+        _lib.call("kh_sparse_ffn_forward", mlps[l]._h, ptr(x), 1, ptr(act[l]), k, None, ptr(y), 1, stream_ptr())
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_kernel": "mul (256 MiB f32 in, 256 MiB out)", "calibration_bytes": 256 << 20,
+                      "ffn_calls": L, "algorithmic_bytes_per_call": 3 * k * H * 2}), flush=True)
+
+
 def read_traffic():
     try:
         for line in open(TRAFFIC_FILE):
@@ -474,6 +506,8 @@ def main():
     ap.add_argument("--leg-cpu-seconds", type=float, default=4.0, help="CPU sample per extra config")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--legs", default="all", help="comma list of " + ",".join(ALL_LEGS))
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run the dispatches the rocprofv3 --pmc traffic runs count")
     args = ap.parse_args()
     ws = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or ws != 1:
@@ -481,6 +515,9 @@ def main():
                                    "DESIGN.md and not implemented", "n_gpus": args.gpus}))
         return 2
     import torch
+    if args.traffic_probe:
+        traffic_probe(args.seed)
+        return 0
     legs = ALL_LEGS if args.legs == "all" else [x for x in args.legs.split(",") if x]
     timer = Timer(torch.cuda.Stream())
     leg_cpu = 0.0 if args.no_cpu else args.leg_cpu_seconds

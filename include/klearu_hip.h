@@ -76,6 +76,12 @@ int kh_bf16_full_dot(const uint16_t* a_dev, const uint16_t* b_dev, int64_t n, fl
  * w[i] = bf16(f32(w[i]) + delta[i]). */
 int kh_bf16_update_from_f32(uint16_t* w_dev, const float* delta_dev, int64_t n, void* stream);
 
+/* f32::exp as Rust evaluates it on x86-64 Linux (glibc expf), elementwise:
+ * the exponential inside the predictor's sigmoid (mlp_predictor.rs:121),
+ * SiLU (sparse_mlp.rs:41), the SLIDE activations (layer.rs:253, :295) and the
+ * attention softmax (sparse_attention.rs:88).  Bit-identical to glibc expf. */
+int kh_expf(const float* x_dev, float* y_dev, int64_t n, void* stream);
+
 /* ======================================================================== */
 /* LSH hash families (crates/klearu-core/src/hash/)                         */
 /* ======================================================================== */

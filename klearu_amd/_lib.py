@@ -45,6 +45,7 @@ SIGS = {
     "kh_last_error": (C.c_char_p, []),
     "kh_version": (I, []),
     "kh_dense_dot_dense": (I, [P, I64, I64, P, I64, P, P]),
+    "kh_expf": (I, [P, P, I64, P]),
     "kh_sparse_dot_dense": (I, [P, P, I64, P, I64, P, P]),
     "kh_scatter_add": (I, [P, P, I64, P, I64, F, P]),
     "kh_bf16_from_f32": (I, [P, P, I64, P]),

@@ -47,6 +47,15 @@ def scatter_add_simd(indices, values, dense: torch.Tensor, scale: float, stream=
     return dense
 
 
+def exp_f32(x, stream=None) -> torch.Tensor:
+    """f32::exp of every element, bit-identical to glibc expf (the exponential
+    of every sigmoid, SiLU and softmax kernel in this library)."""
+    x = to_device(x, np.float32).contiguous()
+    y = torch.empty_like(x)
+    _lib.call("kh_expf", ptr(x), ptr(y), x.numel(), stream_ptr(stream))
+    return y
+
+
 class Bf16Weights:
     """BF16 storage with f32 arithmetic (bf16/mod.rs:22-107); data is int16 bits on device."""
 

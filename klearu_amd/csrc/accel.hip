@@ -133,6 +133,13 @@ __global__ void bf16_full_dot_kernel(const uint16_t* __restrict__ a, const uint1
   *o = s;
 }
 
+// f32::exp of every element, the same expf_glibc the predictor, SiLU and
+// softmax kernels evaluate.
+__global__ void expf_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = expf_glibc(x[i]);
+}
+
 }  // namespace kh
 
 using namespace kh;
@@ -219,4 +226,10 @@ extern "C" int kh_bf16_full_dot(const uint16_t* a_dev, const uint16_t* b_dev, in
                      n, out_dev);
   KH_LAUNCHED();
   return KH_OK;
+}
+
+extern "C" int kh_expf(const float* x_dev, float* y_dev, int64_t n, void* stream) {
+  KH_CHECK_ARG((x_dev && y_dev) || n == 0, "null argument");
+  KH_CHECK_ARG(n >= 0 && n <= ((int64_t)1 << 38), "bad n");
+  KH_ELEMENTWISE(expf_kernel, x_dev, y_dev, n);
 }

@@ -13,10 +13,11 @@
 //
 // Kernels (all loads of a wave are issued before its first wait; the decode
 // path is bound by HBM latency and bandwidth, not arithmetic):
-//   batch 1:  ffn_fused1   one wave per active neuron loads its gate, up and
-//                          down rows together, h = silu(g)*u, scales the down
-//                          row and the block's waves are added in LDS into one
-//                          partial row per block;
+//   batch 1:  ffn_fused1   8 active neurons per block; wave w loads the gate
+//                          and up rows of neuron w and column slice w of all 8
+//                          down rows together, h = silu(g)*u is shared through
+//                          LDS, and each wave writes its column slice of the
+//                          block's partial row;
 //             partials_reduce  adds the partial rows in block order (a kernel
 //                          boundary instead of device-scope fences, which on
 //                          gfx950 write back and invalidate the whole L2).

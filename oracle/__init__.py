@@ -65,6 +65,7 @@ _sig("or_bf16_from_f32_n", None, _f32p, _u16p, _i64)
 _sig("or_bf16_dot_f32", _f, _u16p, _f32p, _i64)
 _sig("or_bf16_full_dot", _f, _u16p, _u16p, _i64)
 _sig("or_bf16_update_from_f32", None, _u16p, _f32p, _i64)
+_sig("or_expf_n", None, _f32p, _f32p, _i64)
 _sig("or_chacha_block", None, _u32p, _int, _u32p)
 _sig("or_pcg32_output", C.c_uint32, C.c_uint64)
 _sig("or_simhash_planes", None, _int, _int, _int, C.c_uint64, _i8p)
@@ -180,6 +181,14 @@ def bf16_dot_f32(w, x):
 def bf16_full_dot(a, b):
     a, b = np.ascontiguousarray(a, np.uint16), np.ascontiguousarray(b, np.uint16)
     return np.float32(lib.or_bf16_full_dot(a, b, a.size))
+
+
+def expf(x):
+    """glibc expf of every element (float32 in, float32 out)."""
+    x = f32(x)
+    y = np.empty_like(x)
+    lib.or_expf_n(x.reshape(-1), y.reshape(-1), x.size)
+    return y
 
 
 def bf16_update_from_f32(w, delta):

@@ -157,6 +157,14 @@ float or_bf16_full_dot(const uint16_t* a, const uint16_t* b, int64_t n) {
   return s;
 }
 
+/* f32::exp (Rust std -> glibc expf on x86-64 Linux) of every element; the
+ * reference's sigmoid / SiLU / softmax call it (mlp_predictor.rs:121,
+ * sparse_mlp.rs:41, layer.rs:295, sparse_attention.rs:88).
+ * Pinned: it is the platform libm itself. */
+void or_expf_n(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = expf(x[i]);
+}
+
 /* Bf16Weights::update_from_f32 (bf16/mod.rs:85-88) applied to every element. */
 void or_bf16_update_from_f32(uint16_t* w, const float* delta, int64_t n) {
   for (int64_t i = 0; i < n; ++i) {

@@ -45,6 +45,7 @@ void or_bf16_from_f32_n(const float* x, uint16_t* out, int64_t n);
 float or_bf16_dot_f32(const uint16_t* w, const float* x, int64_t n);
 float or_bf16_full_dot(const uint16_t* a, const uint16_t* b, int64_t n);
 void or_bf16_update_from_f32(uint16_t* w, const float* delta, int64_t n);
+void or_expf_n(const float* x, float* y, int64_t n);
 
 /* ---- rand 0.8.5 StdRng (ChaCha12) as used by SimHash::new / SRP::new ---- */
 void or_chacha_block(const uint32_t in[16], int rounds, uint32_t out[16]);

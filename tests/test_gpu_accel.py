@@ -71,3 +71,23 @@ def test_bf16_ops(kh, orc):
     bw.update_from_f32(torch.from_numpy(delta).cuda())
     np.testing.assert_array_equal(bw.data.cpu().numpy().view(np.uint16),
                                   orc.bf16_update_from_f32(ref_bits, delta))
+
+
+def test_expf_matches_glibc(kh, orc):
+    """The device exp equals glibc expf (Rust's f32::exp) bit for bit: a strided
+    sweep over all 2^32 bit patterns plus every pattern in windows around 0,
+    the overflow / underflow thresholds and the subnormal results."""
+    from klearu_amd.accel import exp_f32
+    u = np.arange(0, 1 << 32, 251, dtype=np.uint64).astype(np.uint32)
+    windows = []
+    for centre in (0.0, 1.0, -1.0, 88.72283, 88.72284, -103.97208, -87.33655, -100.0, 1e-8, -1e-8):
+        c = int(np.array([centre], np.float32).view(np.uint32)[0])
+        windows.append(np.arange(max(c - (1 << 16), 0), min(c + (1 << 16), (1 << 32) - 1), dtype=np.uint64))
+    u = np.concatenate([u.astype(np.uint64)] + windows).astype(np.uint32)
+    x = u.view(np.float32)
+    x = x[~np.isnan(x)]
+    print(f"expf sweep: {x.size} inputs", flush=True)
+    got = exp_f32(torch.from_numpy(x).cuda()).cpu().numpy()
+    ref = orc.expf(x)
+    bad = np.nonzero(bits(got) != bits(ref))[0]
+    assert bad.size == 0, f"{bad.size} mismatches, first x={x[bad[0]]!r} got={got[bad[0]]!r} ref={ref[bad[0]]!r}"

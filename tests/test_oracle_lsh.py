@@ -180,3 +180,60 @@ def test_activations(orc):
     # reference falls back to the uniform distribution (layer.rs:301-307)
     u = orc.layer_activate(np.full(4, -np.inf, np.float32), "softmax")
     np.testing.assert_array_equal(u, np.full(4, 0.25, np.float32))
+
+
+def _union_below(idx, codes, n):
+    """Brute-force active set of Layer::forward under Vanilla sampling
+    (layer.rs:67-86): the union of the L query buckets; all neurons when the
+    union is empty; then ids >= n dropped."""
+    allv = np.concatenate([idx.bucket(t, int(codes[t])) for t in range(idx.L)])
+    u = np.unique(allv)
+    if u.size == 0:
+        return np.arange(n, dtype=np.uint32)
+    return u[u < n]
+
+
+def test_slide_forward_invariants(orc):
+    """or_slide_forward against its parts checked independently: the active
+    set is the brute-force bucket union (empty -> all neurons, ids >= n
+    dropped after the fallback), pre-activations lie within the sequential-sum
+    error bound of float64 W x + b, ReLU is max(pre, 0), softmax matches the
+    float64 softmax over the active set and sums to 1; TopK sampling keeps the
+    sample_topk KATs' order."""
+    rng = np.random.default_rng(11)
+    L, K, dim, n, cap = 6, 4, 32, 40, 6
+    planes = rng.choice(np.array([-1, 0, 1], np.int8), size=(L, K, dim), p=[1 / 6, 2 / 3, 1 / 6])
+    W = rng.normal(0, 0.1, (n, dim)).astype(np.float32)
+    b = rng.normal(0, 0.1, n).astype(np.float32)
+    X = rng.random((8, dim)).astype(np.float32)
+    X[rng.random(X.shape) < 0.5] = 0.0
+    idx = orc.LshIndex(L, K, cap, FIFO)
+    idx.insert_many(np.arange(n, dtype=np.uint32), orc.hash_dense_batch(planes, W))
+    # ids beyond the layer share buckets too and must be filtered out
+    idx.insert_many(np.arange(n, n + 12, dtype=np.uint32), orc.hash_dense_batch(planes, X[:4].repeat(3, 0)))
+    codes = orc.hash_dense_batch(planes, X)
+    for act in ("relu", "softmax"):
+        out, _ = orc.slide_layer_oracle(planes, cap, FIFO, W, b, X, act=act, index=idx)
+        for r, (ids, pre, a) in enumerate(out):
+            np.testing.assert_array_equal(ids, _union_below(idx, codes[r], n))
+            ref = W[ids].astype(np.float64) @ X[r].astype(np.float64) + b[ids]
+            bound = (dim + 1) * 2 ** -23 * (np.abs(W[ids].astype(np.float64)) @ np.abs(X[r]) + np.abs(b[ids]))
+            assert np.all(np.abs(pre - ref) <= bound + 1e-30)
+            if act == "relu":
+                np.testing.assert_array_equal(a, np.maximum(pre, 0))
+            else:
+                e = np.exp(pre.astype(np.float64) - pre.max())
+                np.testing.assert_allclose(a, e / e.sum(), rtol=1e-5, atol=1e-7)
+                assert abs(float(a.astype(np.float64).sum()) - 1.0) < 1e-5
+    # TopK sampling: the k best by (count desc, id asc), then ids >= n dropped
+    out, _ = orc.slide_layer_oracle(planes, cap, FIFO, W, b, X, sampling=1, top_k=5, index=idx)
+    for r, (ids, _, _) in enumerate(out):
+        u, c = idx.query(codes[r])
+        sel = orc.sample_topk(u, c, 5)
+        sel = np.arange(n, dtype=np.uint32) if sel.size == 0 else sel
+        np.testing.assert_array_equal(ids, np.sort(sel[sel < n]))
+    # empty index: every neuron is active
+    empty = orc.LshIndex(L, K, cap, FIFO)
+    out, _ = orc.slide_layer_oracle(planes, cap, FIFO, W, b, X[:2], index=empty)
+    for ids, _, _ in out:
+        np.testing.assert_array_equal(ids, np.arange(n, dtype=np.uint32))
