@@ -295,6 +295,56 @@ int kh_dejavu_mlp_block(const kh_predictor* p, const kh_sparse_ffn* f, float* hi
                         float* stats_dev, void* stream);
 
 /* ======================================================================== */
+/* klearu-dejavu transformer layer: f32 Linear with bias, SparseMlp,        */
+/* SparseAttention (crates/klearu-dejavu/src/{transformer/mod.rs,mlp.rs,     */
+/* attention.rs}).  Outputs are bit-identical to the reference.  Index lists */
+/* are host arrays (the reference's &[usize]); these calls wait until the   */
+/* list is uploaded, then leave the kernels queued on `stream`.             */
+/* ======================================================================== */
+
+typedef struct kh_dejavu_linear kh_dejavu_linear;
+
+/* Linear{weight [out][in], bias [out]} (transformer/mod.rs:79-111) from host arrays. */
+int kh_dejavu_linear_create(int in_features, int out_features, const float* w_host,
+                            const float* b_host, kh_dejavu_linear** out);
+int kh_dejavu_linear_destroy(kh_dejavu_linear* l);
+/* Linear::forward (transformer/mod.rs:114-123): y_dev[batch][out] from x_dev[batch][in]. */
+int kh_dejavu_linear_forward(const kh_dejavu_linear* l, const float* x_dev, int64_t batch,
+                             float* y_dev, void* stream);
+/* Linear::forward_sparse (transformer/mod.rs:126-134): y_dev[b][a] = row idx_host[a]
+ * (any order, repeats allowed).  Out-of-range indices are KH_ERR_ARG (the
+ * reference panics).  Uses the handle's index buffer: calls must be ordered. */
+int kh_dejavu_linear_forward_sparse(kh_dejavu_linear* l, const float* x_dev, int64_t batch,
+                                    const int64_t* idx_host, int64_t n_idx, float* y_dev,
+                                    void* stream);
+
+typedef struct kh_dejavu_sparse_mlp kh_dejavu_sparse_mlp;
+
+/* SparseMlp::new(hidden_size, intermediate_size) (mlp.rs:11-16). */
+int kh_dejavu_sparse_mlp_create(int hidden, int inter, kh_dejavu_sparse_mlp** out);
+int kh_dejavu_sparse_mlp_destroy(kh_dejavu_sparse_mlp* m);
+/* SparseMlp::forward (mlp.rs:23-58) for every row of x_dev[batch][hidden] with the
+ * same selected neurons: y_dev[batch][hidden]. */
+int kh_dejavu_sparse_mlp_forward(kh_dejavu_sparse_mlp* m, const float* x_dev, int64_t batch,
+                                 const kh_dejavu_linear* gate, const kh_dejavu_linear* up,
+                                 const kh_dejavu_linear* down, const int64_t* sel_host,
+                                 int64_t n_sel, float* y_dev, void* stream);
+
+typedef struct kh_dejavu_sparse_attention kh_dejavu_sparse_attention;
+
+/* SparseAttention::new(config) (attention.rs:9-11): hidden, heads, head_dim. */
+int kh_dejavu_sparse_attention_create(int hidden, int num_heads, int head_dim,
+                                      kh_dejavu_sparse_attention** out);
+int kh_dejavu_sparse_attention_destroy(kh_dejavu_sparse_attention* a);
+/* SparseAttention::forward (attention.rs:18-74) for every row of x_dev[batch][hidden]
+ * with the same selected heads: y_dev[batch][hidden]. */
+int kh_dejavu_sparse_attention_forward(kh_dejavu_sparse_attention* a, const float* x_dev,
+                                       int64_t batch, const kh_dejavu_linear* q,
+                                       const kh_dejavu_linear* k, const kh_dejavu_linear* v,
+                                       const kh_dejavu_linear* o, const int64_t* heads_host,
+                                       int64_t n_heads, float* y_dev, void* stream);
+
+/* ======================================================================== */
 /* Head-sparse decode attention (crates/klearu-llm/src/sparse/sparse_attention.rs) */
 /* ======================================================================== */
 

@@ -46,6 +46,16 @@ SIGS = {
     "kh_version": (I, []),
     "kh_dense_dot_dense": (I, [P, I64, I64, P, I64, P, P]),
     "kh_expf": (I, [P, P, I64, P]),
+    "kh_dejavu_linear_create": (I, [I, I, P, P, P]),
+    "kh_dejavu_linear_destroy": (I, [P]),
+    "kh_dejavu_linear_forward": (I, [P, P, I64, P, P]),
+    "kh_dejavu_linear_forward_sparse": (I, [P, P, I64, P, I64, P, P]),
+    "kh_dejavu_sparse_mlp_create": (I, [I, I, P]),
+    "kh_dejavu_sparse_mlp_destroy": (I, [P]),
+    "kh_dejavu_sparse_mlp_forward": (I, [P, P, I64, P, P, P, P, I64, P, P]),
+    "kh_dejavu_sparse_attention_create": (I, [I, I, I, P]),
+    "kh_dejavu_sparse_attention_destroy": (I, [P]),
+    "kh_dejavu_sparse_attention_forward": (I, [P, P, I64, P, P, P, P, P, I64, P, P]),
     "kh_sparse_dot_dense": (I, [P, P, I64, P, I64, P, P]),
     "kh_scatter_add": (I, [P, P, I64, P, I64, F, P]),
     "kh_bf16_from_f32": (I, [P, P, I64, P]),

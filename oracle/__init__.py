@@ -98,6 +98,9 @@ _sig("or_sparse_attention_forward_bf16", None, _u16p, _u16p, _u16p, _u16p, _int,
 _sig("or_dejavu_linear_forward_sparse", None, _f32p, _f32p, _int, _f32p, _i64p, _i64, _f32p)
 _sig("or_dejavu_sparse_mlp_forward", None, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _int, _int,
      _f32p, _i64p, _i64, _f32p)
+_sig("or_dejavu_linear_forward", None, _f32p, _f32p, _int, _int, _f32p, _f32p)
+_sig("or_dejavu_sparse_attention_forward", None, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+     _int, _int, _int, _f32p, _i64p, _i64, _f32p)
 _sig("or_cpu_dejavu_ffn_layer", None, _f32p, _f32p, _f32p, _f32p, _f, _f32p, _f32p, _f32p, _f32p, _int,
      _int, _int, _i64, _f32p, _f32p, _i64p)
 
@@ -376,6 +379,30 @@ def dejavu_sparse_mlp_forward(wg, bg, wu, bu, wd, bd, x, sel):
     lib.or_dejavu_sparse_mlp_forward(f32(wg).reshape(-1), f32(bg), f32(wu).reshape(-1), f32(bu),
                                      f32(wd).reshape(-1), f32(bd), hidden, inter, f32(x), sel,
                                      sel.size, y)
+    return y
+
+
+def dejavu_linear_forward(w, b, x):
+    out_f, in_f = w.shape
+    y = np.zeros(out_f, np.float32)
+    lib.or_dejavu_linear_forward(f32(w).reshape(-1), f32(b), in_f, out_f, f32(x), y)
+    return y
+
+
+def dejavu_linear_forward_sparse(w, b, x, idx):
+    idx = i64(idx)
+    y = np.zeros(max(idx.size, 1), np.float32)
+    lib.or_dejavu_linear_forward_sparse(f32(w).reshape(-1), f32(b), w.shape[1], f32(x), idx, idx.size, y)
+    return y[:idx.size].copy()
+
+
+def dejavu_sparse_attention_forward(wq, bq, wk, bk, wv, bv, wo, bo, num_heads, head_dim, x, heads):
+    hidden = wq.shape[1]
+    heads = i64(heads)
+    y = np.zeros(hidden, np.float32)
+    lib.or_dejavu_sparse_attention_forward(f32(wq).reshape(-1), f32(bq), f32(wk).reshape(-1), f32(bk),
+                                           f32(wv).reshape(-1), f32(bv), f32(wo).reshape(-1), f32(bo), hidden,
+                                           num_heads, head_dim, f32(x), heads, heads.size, y)
     return y
 
 

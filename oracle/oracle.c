@@ -817,6 +817,70 @@ void or_dejavu_linear_forward_sparse(const float* w, const float* bias, int in_f
   }
 }
 
+/* dejavu Linear::forward (klearu-dejavu/src/transformer/mod.rs:114-123): every
+ * row, a sequential sum from -0.0 of the rounded products, plus the bias.
+ * Pinned: float64 bound and equality with forward_sparse over every row
+ * (tests/test_oracle_dejavu.py). */
+void or_dejavu_linear_forward(const float* w, const float* bias, int in_f, int out_f,
+                              const float* x, float* out) {
+  for (int r = 0; r < out_f; ++r) {
+    const float* row = w + (int64_t)r * in_f;
+    float s = -0.0f;
+    for (int j = 0; j < in_f; ++j) {
+      float p = row[j] * x[j];
+      s = s + p;
+    }
+    out[r] = s + bias[r];
+  }
+}
+
+/* SparseAttention::forward (klearu-dejavu/src/attention.rs:18-74): q/k/v rows
+ * of the selected heads only (zeros elsewhere), per selected head the score
+ * sigmoid(dot(q_h, k_h) / sqrt(head_dim)) scales v_h, then o_proj runs dense
+ * over the whole concatenation.  Heads are taken in list order; a repeated
+ * head recomputes the same values.
+ * Pinned: all heads selected equals the reference's dense restatement
+ * (attention.rs:119-160) and a float64 bound (tests/test_oracle_dejavu.py). */
+void or_dejavu_sparse_attention_forward(const float* wq, const float* bq, const float* wk,
+                                        const float* bk, const float* wv, const float* bv,
+                                        const float* wo, const float* bo, int hidden,
+                                        int num_heads, int head_dim, const float* x,
+                                        const int64_t* heads, int64_t n_heads, float* y) {
+  const int64_t qd = (int64_t)num_heads * head_dim;
+  float* q = (float*)calloc((size_t)qd, sizeof(float));
+  float* k = (float*)calloc((size_t)qd, sizeof(float));
+  float* v = (float*)calloc((size_t)qd, sizeof(float));
+  float* att = (float*)calloc((size_t)qd, sizeof(float));
+  int64_t* idx = (int64_t*)malloc(sizeof(int64_t) * (size_t)head_dim);
+  float* tmp = (float*)malloc(sizeof(float) * (size_t)head_dim);
+  for (int64_t a = 0; a < n_heads; ++a) {
+    const int64_t st = heads[a] * head_dim;
+    for (int d = 0; d < head_dim; ++d) idx[d] = st + d;
+    or_dejavu_linear_forward_sparse(wq, bq, hidden, x, idx, head_dim, tmp);
+    for (int d = 0; d < head_dim; ++d) q[st + d] = tmp[d];
+    or_dejavu_linear_forward_sparse(wk, bk, hidden, x, idx, head_dim, tmp);
+    for (int d = 0; d < head_dim; ++d) k[st + d] = tmp[d];
+    or_dejavu_linear_forward_sparse(wv, bv, hidden, x, idx, head_dim, tmp);
+    for (int d = 0; d < head_dim; ++d) v[st + d] = tmp[d];
+  }
+  const float scale = sqrtf((float)head_dim);
+  for (int64_t a = 0; a < n_heads; ++a) {
+    const int64_t st = heads[a] * head_dim;
+    float s = -0.0f;
+    for (int d = 0; d < head_dim; ++d) {
+      float p = q[st + d] * k[st + d];
+      s = s + p;
+    }
+    s = s / scale;
+    float e = expf(-s);
+    float den = 1.0f + e;
+    float sc = 1.0f / den;
+    for (int d = 0; d < head_dim; ++d) att[st + d] = v[st + d] * sc;
+  }
+  or_dejavu_linear_forward(wo, bo, (int)qd, hidden, att, y);
+  free(q); free(k); free(v); free(att); free(idx); free(tmp);
+}
+
 /* SparseMlp::forward (klearu-dejavu/src/mlp.rs:23-58): SwiGLU over selected
  * neurons; the down projection adds column idx of wd [hidden][inter] times the
  * activation into every output, in selection order, then adds the bias. */

@@ -148,6 +148,13 @@ void or_dejavu_sparse_mlp_forward(const float* wg, const float* bg, const float*
                                   const float* bu, const float* wd, const float* bd, int hidden,
                                   int inter, const float* x, const int64_t* sel, int64_t n,
                                   float* y);
+void or_dejavu_linear_forward(const float* w, const float* bias, int in_f, int out_f,
+                              const float* x, float* out);
+void or_dejavu_sparse_attention_forward(const float* wq, const float* bq, const float* wk,
+                                        const float* bk, const float* wv, const float* bv,
+                                        const float* wo, const float* bo, int hidden,
+                                        int num_heads, int head_dim, const float* x,
+                                        const int64_t* heads, int64_t n_heads, float* y);
 
 #ifdef __cplusplus
 }

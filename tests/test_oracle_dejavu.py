@@ -263,3 +263,50 @@ def test_cpu_attention_port_equals_composition(orc):
                                             pos, cos_t, sin_t, kc2, vc2, sel)
     np.testing.assert_array_equal(hs, x + out)
     np.testing.assert_array_equal(kc, kc2)
+
+
+def _xavier(rng, out_f, in_f):
+    return rng.normal(0, np.sqrt(2.0 / (in_f + out_f)), (out_f, in_f)).astype(np.float32)
+
+
+def test_dejavu_linear_dense_and_sparse(orc):
+    """transformer/mod.rs:114-134: forward over all rows == forward_sparse over
+    0..out, rows in any order and repeated; float64 bound on every output."""
+    rng = np.random.default_rng(8)
+    w, b = _xavier(rng, 48, 40), rng.normal(0, 0.1, 48).astype(np.float32)
+    x = rng.standard_normal(40).astype(np.float32)
+    d = orc.dejavu_linear_forward(w, b, x)
+    np.testing.assert_array_equal(d, orc.dejavu_linear_forward_sparse(w, b, x, np.arange(48)))
+    idx = np.array([7, 3, 3, 47, 0])
+    np.testing.assert_array_equal(orc.dejavu_linear_forward_sparse(w, b, x, idx), d[idx])
+    ref = w.astype(np.float64) @ x + b
+    bound = 41 * 2 ** -23 * (np.abs(w.astype(np.float64)) @ np.abs(x) + np.abs(b))
+    assert np.all(np.abs(d - ref) <= bound)
+
+
+def test_dejavu_toy_attention_all_heads_equals_dense(orc):
+    """attention.rs:119-160 (hidden 64, 4 heads x 16): every head selected ==
+    the dense restatement (full q/k/v, sigmoid score per head, dense o_proj)
+    within 1e-5; two heads selected == the dense formula with the other
+    heads' outputs zeroed, in float64 within 1e-5."""
+    rng = np.random.default_rng(10)
+    H, nh, hd = 64, 4, 16
+    ws = [_xavier(rng, nh * hd, H) for _ in range(3)] + [_xavier(rng, H, nh * hd)]
+    bs = [np.zeros(nh * hd, np.float32)] * 3 + [np.zeros(H, np.float32)]
+    x = np.full(H, 0.5, np.float32)
+
+    def dense(sel):
+        q, k, v = (w.astype(np.float64) @ x for w in ws[:3])
+        att = np.zeros(nh * hd)
+        for h in sel:
+            s = slice(h * hd, (h + 1) * hd)
+            att[s] = v[s] / (1 + np.exp(-(q[s] @ k[s]) / np.sqrt(hd)))
+        return ws[3].astype(np.float64) @ att
+
+    args = [a for pair in zip(ws, bs) for a in pair]
+    y = orc.dejavu_sparse_attention_forward(*args, nh, hd, x, np.arange(nh))
+    np.testing.assert_allclose(y, dense(range(nh)), atol=1e-5)
+    y2 = orc.dejavu_sparse_attention_forward(*args, nh, hd, x, [2, 0])
+    np.testing.assert_allclose(y2, dense([0, 2]), atol=1e-5)
+    # repeated heads recompute the same values
+    np.testing.assert_array_equal(orc.dejavu_sparse_attention_forward(*args, nh, hd, x, [2, 0, 2]), y2)
