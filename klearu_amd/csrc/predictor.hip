@@ -265,12 +265,16 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
     }
   };
   // Consumer chain over steps [j0, j1) (j0 a multiple of 4): a window of kWin
-  // quads is in flight; each quad is added, then its register is refilled
-  // with the quad kWin ahead, so the only VALU work per step is the dependent
-  // add (LDS addresses are immediate offsets from one base pointer).  Window
-  // reads past j1 are never added (they stay inside the block's LDS).
-  constexpr int kWin = 16;   // quads in flight (64 steps)
-  constexpr int kSup = 64;   // quads per unrolled loop body (256 steps)
+  // quads is in flight; every kRefill quads are added, then their registers
+  // are refilled with the quads kWin ahead, so the only VALU work per step is
+  // the dependent add (LDS addresses are immediate offsets from one base
+  // pointer).  Refilling in batches keeps the waits for the LDS counter to one
+  // per batch: a read and a wait after every quad cost about 2 cycles per add.
+  // Window reads past j1 are never added (they stay inside the block's LDS).
+  constexpr int kWin = 32;    // quads in flight (128 steps)
+  constexpr int kRefill = 8;  // quads added between refills
+  constexpr int kSup = 64;    // quads per unrolled loop body (256 steps)
+  static_assert(kSup % kWin == 0 && kWin % kRefill == 0, "window layout");
   static_assert((kL1LdsIn / 4 + kWin) * kL1Chains <= (kL1LdsBytes / 16), "window stays in LDS");
   const int ln = lane < kL1Chains ? lane : kL1Chains - 1;
   float s = -0.0f;
@@ -282,13 +286,17 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
     const int nsup = (j1 - j0) / (4 * kSup);
     for (int c = 0; c < nsup; ++c) {
 #pragma unroll
-      for (int q = 0; q < kSup; ++q) {
-        s = __fadd_rn(s, r[q % kWin].x);
-        s = __fadd_rn(s, r[q % kWin].y);
-        s = __fadd_rn(s, r[q % kWin].z);
-        s = __fadd_rn(s, r[q % kWin].w);
-        r[q % kWin] = bp[(q + kWin) * kL1Chains];
-        // keep the refill here: the scheduler would otherwise sink it to its use
+      for (int q = 0; q < kSup; q += kRefill) {
+#pragma unroll
+        for (int u = 0; u < kRefill; ++u) {
+          s = __fadd_rn(s, r[(q + u) % kWin].x);
+          s = __fadd_rn(s, r[(q + u) % kWin].y);
+          s = __fadd_rn(s, r[(q + u) % kWin].z);
+          s = __fadd_rn(s, r[(q + u) % kWin].w);
+        }
+#pragma unroll
+        for (int u = 0; u < kRefill; ++u) r[(q + u) % kWin] = bp[(q + u + kWin) * kL1Chains];
+        // keep the refills here: the scheduler would otherwise sink them to their uses
         __builtin_amdgcn_sched_barrier(0);
       }
       bp += kSup * kL1Chains;
