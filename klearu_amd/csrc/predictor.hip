@@ -330,11 +330,15 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
 constexpr int kMaxL2Hid = 256;
 constexpr int kL2Threads = 64;
 
+// With mm set, each block also writes the (min, max) order-preserving keys of
+// its scores to mm[b][block]: the key bounds the top-k kernel starts from
+// (one slot per block, so no atomics contend on a single address).
 template <typename W>
 __global__ __launch_bounds__(kL2Threads) void pred_l2_kernel(const W* __restrict__ Wb,
                                                       const float* __restrict__ bias,
                                                       const float* __restrict__ hin, int n_hid,
-                                                      int n_out, float* __restrict__ out) {
+                                                      int n_out, float* __restrict__ out,
+                                                      uint32_t* __restrict__ mm) {
   using B8 = Blk8<W>;
   using V = typename B8::V;
   constexpr int kHw = 4;  // float4 of the hidden vector read ahead (16 steps)
@@ -405,7 +409,15 @@ __global__ __launch_bounds__(kL2Threads) void pred_l2_kernel(const W* __restrict
       }
     }
   }
-  if (ok) out[(size_t)b * n_out + o] = sigmoid_ref_t(__fadd_rn(s, bv), tab);
+  const float score = sigmoid_ref_t(__fadd_rn(s, bv), tab);
+  if (ok) out[(size_t)b * n_out + o] = score;
+  if (mm) {
+    const uint32_t key = f32_key(score);
+    const uint32_t kmax = wave_max_u32(ok ? key : 0u);
+    const uint32_t kmin = wave_min_u32(ok ? key : 0xffffffffu);
+    if (threadIdx.x == 0)
+      reinterpret_cast<uint2*>(mm)[(size_t)b * gridDim.x + blockIdx.x] = make_uint2(kmin, kmax);
+  }
 }
 
 // Generic layer for shapes outside the fast kernels' limits: one lane per
@@ -485,7 +497,9 @@ template <int kTopkPerThread>
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restrict__ scores,
                                                             int n, int k, int order,
                                                             int32_t* __restrict__ out,
-                                                            uint64_t* __restrict__ sortbuf) {
+                                                            uint64_t* __restrict__ sortbuf,
+                                                            const uint32_t* __restrict__ mm,
+                                                            int nmm) {
   extern __shared__ __align__(16) uint64_t sort_lds[];
   __shared__ unsigned hist[1 << kTopkDigit];
   __shared__ uint64_t cand[kTopkCand];
@@ -501,6 +515,11 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
   int32_t* ob = out + (size_t)b * kk0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kpt = (n + kTopkThreads - 1) / kTopkThreads;  // <= kTopkPerThread (host-checked)
+  // per-block key bounds written by the producing kernel (nmm slots per row),
+  // requested with the scores
+  const uint2 mmv = (mm && (int)threadIdx.x < nmm)
+                        ? reinterpret_cast<const uint2*>(mm)[(size_t)b * nmm + threadIdx.x]
+                        : make_uint2(0xffffffffu, 0u);
   const int i0 = threadIdx.x * kpt;
   const int cnt = max(0, min(kpt, n - i0));
   // Coalesced loads through LDS (a thread's own contiguous range would make
@@ -531,13 +550,15 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
     key[j] = f32_key(staged ? __uint_as_float(sstage[min(i0 + j, n - 1)]) : sc[min(i0 + j, n - 1)]);
   // 1. bits common to every key: the radix passes start below them (scores
   // cluster, so a pass over shared high bits would fill one or two bins).
-  uint32_t kmax = 0u, kmin = 0xffffffffu;
+  uint32_t kmax = mmv.y, kmin = mmv.x;
+  if (!mm) {
 #pragma unroll
-  for (int j = 0; j < kTopkPerThread; ++j)
-    if (j < cnt) {
-      kmax = max(kmax, key[j]);
-      kmin = min(kmin, key[j]);
-    }
+    for (int j = 0; j < kTopkPerThread; ++j)
+      if (j < cnt) {
+        kmax = max(kmax, key[j]);
+        kmin = min(kmin, key[j]);
+      }
+  }
   kmax = wave_max_u32(kmax);
   kmin = wave_min_u32(kmin);
   if (lane == 0) {
@@ -613,19 +634,29 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
         }
       __syncthreads();
       const int m = s_ncand;
-      if ((int)threadIdx.x < m) {
-        const uint64_t me = cand[threadIdx.x];
-        const uint32_t mk = (uint32_t)(me >> 32);
-        int rank = 0, gt = 0;
-        for (int j = 0; j < m; ++j) {
+      // Four threads per candidate: thread t ranks candidate t/4 against a
+      // quarter of the list; the quarters are added across the lane quad.
+      const int ci = (int)threadIdx.x >> 2, part = (int)threadIdx.x & 3;
+      int rank = 0, gt = 0;
+      uint32_t mk = 0u;
+      if (ci < m) {
+        const uint64_t me = cand[ci];
+        mk = (uint32_t)(me >> 32);
+        const int q = (m + 3) >> 2;
+        const int j1 = min(part * q + q, m);
+        for (int j = part * q; j < j1; ++j) {
           const uint64_t o = cand[j];
           rank += o > me;
           gt += (uint32_t)(o >> 32) > mk;
         }
-        if (rank == kk - 1) {
-          s_T = mk;
-          s_ties = kk - gt;
-        }
+      }
+      rank += dpp<kDppQuadSwap1>(rank);
+      rank += dpp<kDppQuadSwap2>(rank);
+      gt += dpp<kDppQuadSwap1>(gt);
+      gt += dpp<kDppQuadSwap2>(gt);
+      if (ci < m && part == 0 && rank == kk - 1) {
+        s_T = mk;
+        s_ties = kk - gt;
       }
       __syncthreads();
       T = s_T;
@@ -643,6 +674,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
       ceq += key[j] == T;
     }
   const uint32_t ex = block_excl_scan_u32((uint32_t)cgt | ((uint32_t)ceq << 16), uwsum);
+
   const int gt_before = (int)(ex & 0xffffu), eq_before = (int)(ex >> 16);
   int pos = gt_before + min(eq_before, ties);
   int eq_rank = eq_before;
@@ -712,6 +744,7 @@ struct kh_predictor {
   float* b2 = nullptr;
   float* hbuf = nullptr;  // [batch_cap][hid]
   float* sbuf = nullptr;  // [batch_cap][out]
+  uint32_t* mm = nullptr; // [batch_cap][layer-2 blocks][2] score key bounds per block
   int batch_cap = 0;
 };
 
@@ -800,17 +833,22 @@ extern "C" int kh_predictor_destroy(kh_predictor* p) {
   dev_free(p->b2);
   dev_free(p->hbuf);
   dev_free(p->sbuf);
+  dev_free(p->mm);
   delete p;
   return KH_OK;
 }
+
+static int l2_blocks(const kh_predictor* p) { return ceil_div(p->out_dim, kL2Threads); }
 
 static int ensure_batch(kh_predictor* p, int64_t batch) {
   if (batch <= p->batch_cap) return KH_OK;
   dev_free(p->hbuf);
   dev_free(p->sbuf);
+  dev_free(p->mm);
   p->hbuf = static_cast<float*>(dev_alloc(sizeof(float) * batch * p->hid));
   p->sbuf = static_cast<float*>(dev_alloc(sizeof(float) * batch * p->out_dim));
-  if (!p->hbuf || !p->sbuf) {
+  p->mm = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * 2 * batch * l2_blocks(p)));
+  if (!p->hbuf || !p->sbuf || !p->mm) {
     p->batch_cap = 0;
     return KH_ERR_ALLOC;
   }
@@ -820,7 +858,7 @@ static int ensure_batch(kh_predictor* p, int64_t batch) {
 
 template <typename W>
 static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* scores,
-                         hipStream_t st, const NormIn& nrm) {
+                         hipStream_t st, const NormIn& nrm, uint32_t* mm) {
   const W* w1 = static_cast<const W*>(p->w1b);
   const W* w2 = static_cast<const W*>(p->w2b);
   const int l1_stages = ceil_div(p->in_dim, kL1Stage);
@@ -851,8 +889,8 @@ static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* 
                        st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
   KH_LAUNCHED();
   if (p->hid <= kMaxL2Hid)
-    hipLaunchKernelGGL(pred_l2_kernel<W>, dim3(ceil_div(p->out_dim, kL2Threads), batch), dim3(kL2Threads), 0, st,
-                       w2, p->b2, p->hbuf, p->hid, p->out_dim, scores);
+    hipLaunchKernelGGL(pred_l2_kernel<W>, dim3(l2_blocks(p), batch), dim3(kL2Threads), 0, st,
+                       w2, p->b2, p->hbuf, p->hid, p->out_dim, scores, mm);
   else
     hipLaunchKernelGGL((chain_layer_kernel<1, W>), dim3(ceil_div(p->out_dim, 64), batch), dim3(64),
                        0, st, w2, p->b2, p->hbuf, p->hid, p->out_dim, scores);
@@ -860,13 +898,19 @@ static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* 
   return KH_OK;
 }
 
+// With bounds set, layer 2 also folds the score key bounds into p->mm (when
+// its fast kernel runs; *bounds is then p->mm, else nullptr).
 static int predict_into(const kh_predictor* pc, const float* x, int64_t batch, float* scores,
-                        hipStream_t st, const NormIn& nrm = NormIn{}) {
+                        hipStream_t st, const NormIn& nrm = NormIn{},
+                        uint32_t** bounds = nullptr) {
   auto* p = const_cast<kh_predictor*>(pc);
   int rc = ensure_batch(p, batch);
   if (rc != KH_OK) return rc;
-  return p->bf16 ? predict_typed<uint16_t>(p, x, batch, scores, st, nrm)
-                 : predict_typed<float>(p, x, batch, scores, st, nrm);
+  // the bounds fit one slot per top-k thread
+  uint32_t* mm = (bounds && p->hid <= kMaxL2Hid && l2_blocks(p) <= kTopkThreads) ? p->mm : nullptr;
+  if (bounds) *bounds = mm;
+  return p->bf16 ? predict_typed<uint16_t>(p, x, batch, scores, st, nrm, mm)
+                 : predict_typed<float>(p, x, batch, scores, st, nrm, mm);
 }
 
 extern "C" int kh_predictor_predict(const kh_predictor* p, const float* x_dev, int64_t batch,
@@ -877,8 +921,17 @@ extern "C" int kh_predictor_predict(const kh_predictor* p, const float* x_dev, i
   return predict_into(p, x_dev, batch, scores_dev, as_stream(stream));
 }
 
+template <int KPT>
+static int topk_attr() {
+  KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<KPT>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, 136 * 1024));
+  return KH_OK;
+}
+
+// mm: per-block key bounds from layer 2, nmm slots per row (or nullptr: the
+// kernel finds the bounds from the scores).
 static int topk_launch(const float* scores, int64_t batch, int n, int k, int order, int32_t* ids,
-                       hipStream_t st) {
+                       hipStream_t st, const uint32_t* mm = nullptr, int nmm = 0) {
   const int kk = std::min(k, n);
   if (kk <= 0 || batch == 0) return KH_OK;
   KH_CHECK_ARG(n <= kTopkRegMax, "top-k supports n <= %d scores per row (got %d)", kTopkRegMax, n);
@@ -887,12 +940,12 @@ static int topk_launch(const float* scores, int64_t batch, int n, int k, int ord
   size_t lds = n <= kTopkStage ? sizeof(uint32_t) * ((n + 3) & ~3) : 0;  // staged scores
   static bool attr = false;
   if (!attr) {
-    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<16>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 136 * 1024));
-    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<32>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 136 * 1024));
-    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<64>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 136 * 1024));
+    int rc = topk_attr<8>();
+    if (rc == KH_OK) rc = topk_attr<12>();
+    if (rc == KH_OK) rc = topk_attr<16>();
+    if (rc == KH_OK) rc = topk_attr<32>();
+    if (rc == KH_OK) rc = topk_attr<64>();
+    if (rc != KH_OK) return rc;
     attr = true;
   }
   if (order == KH_ORDER_SCORE) {
@@ -911,15 +964,18 @@ static int topk_launch(const float* scores, int64_t batch, int n, int k, int ord
     }
     sortbuf = buf;
   }
-  if (n <= kTopkThreads * 16)
-    hipLaunchKernelGGL(topk_kernel<16>, dim3(batch), dim3(kTopkThreads), lds, st, scores, n, k,
-                       order, ids, sortbuf);
+  // keys per thread: the smallest instantiation that holds the row
+  const dim3 g(static_cast<unsigned>(batch)), t(kTopkThreads);
+  if (n <= kTopkThreads * 8)
+    hipLaunchKernelGGL(topk_kernel<8>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
+  else if (n <= kTopkThreads * 12)
+    hipLaunchKernelGGL(topk_kernel<12>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
+  else if (n <= kTopkThreads * 16)
+    hipLaunchKernelGGL(topk_kernel<16>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
   else if (n <= kTopkThreads * 32)
-    hipLaunchKernelGGL(topk_kernel<32>, dim3(batch), dim3(kTopkThreads), lds, st, scores, n, k,
-                       order, ids, sortbuf);
+    hipLaunchKernelGGL(topk_kernel<32>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
   else
-    hipLaunchKernelGGL(topk_kernel<64>, dim3(batch), dim3(kTopkThreads), lds, st, scores, n, k,
-                       order, ids, sortbuf);
+    hipLaunchKernelGGL(topk_kernel<64>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -934,9 +990,10 @@ extern "C" int kh_predictor_select_top_k(const kh_predictor* p, const float* x_d
   auto* pm = const_cast<kh_predictor*>(p);
   int rc = ensure_batch(pm, batch);
   if (rc != KH_OK) return rc;
-  rc = predict_into(p, x_dev, batch, pm->sbuf, st);
+  uint32_t* mm = nullptr;
+  rc = predict_into(p, x_dev, batch, pm->sbuf, st, NormIn{}, &mm);
   if (rc != KH_OK) return rc;
-  return topk_launch(pm->sbuf, batch, p->out_dim, k, order, ids_dev, st);
+  return topk_launch(pm->sbuf, batch, p->out_dim, k, order, ids_dev, st, mm, l2_blocks(p));
 }
 
 extern "C" int kh_topk_select(const float* scores_dev, int64_t batch, int n, int k, int order,
@@ -968,8 +1025,9 @@ int predictor_topk_normed(const kh_predictor* pc, const float* hidden, int k, in
   auto* p = const_cast<kh_predictor*>(pc);
   int rc = ensure_batch(p, 1);
   if (rc != KH_OK) return rc;
-  rc = predict_into(p, hidden, 1, p->sbuf, st, nrm);
+  uint32_t* mm = nullptr;
+  rc = predict_into(p, hidden, 1, p->sbuf, st, nrm, &mm);
   if (rc != KH_OK) return rc;
-  return topk_launch(p->sbuf, 1, p->out_dim, k, KH_ORDER_ASCENDING, ids, st);
+  return topk_launch(p->sbuf, 1, p->out_dim, k, KH_ORDER_ASCENDING, ids, st, mm, l2_blocks(p));
 }
 }  // namespace kh
