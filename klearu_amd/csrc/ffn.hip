@@ -136,44 +136,33 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
   float* hs = reinterpret_cast<float*>(smem4 + (kFuMaxH >> 2));  // [kFuWaves]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int first = blockIdx.x * kFuWaves;
-  // x, the block's active indices and the device count are requested together
-  // (one round trip), and x is in LDS before any weight load is issued: the
-  // weight loads are then waited for only where their data is used (vmcnt
-  // counts in issue order, so an x load behind them would wait for all).
+  // Requests in this order: x, the norm weights and the row statistics
+  // (vector loads), then the block's active indices and the device count
+  // (scalar loads).  The weight loads go out as soon as the indices arrive;
+  // x is waited for after them, which costs nothing because vector loads
+  // complete in issue order and x was requested first.
   const int n4 = H >> 2;
   const float4* __restrict__ xsrc = reinterpret_cast<const float4*>(x);
   constexpr int kXq = kFuMaxH / 4 / (64 * kFuWaves);  // float4 of x per thread
-  float4 xv[kXq];
+  float4 xv[kXq], wn[kXq];
 #pragma unroll
   for (int q = 0; q < kXq; ++q) xv[q] = xsrc[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)];
+  // Branch-free requests (without a norm they read x again, unused): a load
+  // inside a branch is waited for at the branch's end.  nparts = H/64 <= 64,
+  // one statistic per lane.
+  const float4* __restrict__ nsrc = reinterpret_cast<const float4*>(norm_w ? norm_w : x);
+  const float* __restrict__ ssrc = norm_w ? stats : x;
+#pragma unroll
+  for (int q = 0; q < kXq; ++q) wn[q] = nsrc[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)];
+  const float st = ssrc[min(lane, max(nparts, 1) - 1)];
   int cand[kFuWaves];
 #pragma unroll
   for (int k = 0; k < kFuWaves; ++k) cand[k] = active[min(first + k, n_active - 1)];
   int n = n_active;
   if (n_active_dev) n = min(n, *n_active_dev);
-  if (norm_w) {
-    // RmsNorm of the hidden row (x * inv) * w, inv from the row's per-block
-    // sums of squares exactly as the predictor computes it
-    float4 wn[kXq];
-#pragma unroll
-    for (int q = 0; q < kXq; ++q)
-      wn[q] = reinterpret_cast<const float4*>(norm_w)[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)];
-    const float inv = rms_inv(stats, nparts, H, eps);
-#pragma unroll
-    for (int q = 0; q < kXq; ++q) {
-      xv[q].x = (xv[q].x * inv) * wn[q].x;
-      xv[q].y = (xv[q].y * inv) * wn[q].y;
-      xv[q].z = (xv[q].z * inv) * wn[q].z;
-      xv[q].w = (xv[q].w * inv) * wn[q].w;
-    }
-  }
-  // Unconditional stores (a thread past the end rewrites the last float4 with
-  // the value it loaded from there): a conditional store lets the compiler
-  // sink each load into its branch, one round trip per load.
-#pragma unroll
-  for (int q = 0; q < kXq; ++q) xs4[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)] = xv[q];
-  if (first >= n) return;  // uniform per block (before any barrier)
-  const int nlive = min(kFuWaves, n - first);
+  // A block past the device count still runs (reading row 0, unused) so that
+  // it writes its partial row as zeros for the reduce.
+  const int nlive = max(0, min(kFuWaves, n - first));
   int nid[kFuWaves];
 #pragma unroll
   for (int k = 0; k < kFuWaves; ++k) nid[k] = k < nlive ? cand[k] : 0;  // idle slots read row 0, unused
@@ -195,6 +184,24 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
 #pragma unroll
   for (int k = 0; k < kFuWaves; ++k)
     wd[k] = *reinterpret_cast<const uint4*>(WdT + (size_t)nid[k] * H + col);
+  __builtin_amdgcn_sched_barrier(0);
+  if (norm_w) {
+    // RmsNorm of the hidden row (x * inv) * w, inv from the row's per-block
+    // sums of squares exactly as the predictor computes it
+    const float inv = rms_inv_part(lane < nparts ? 0.0f + st : 0.0f, H, eps);
+#pragma unroll
+    for (int q = 0; q < kXq; ++q) {
+      xv[q].x = (xv[q].x * inv) * wn[q].x;
+      xv[q].y = (xv[q].y * inv) * wn[q].y;
+      xv[q].z = (xv[q].z * inv) * wn[q].z;
+      xv[q].w = (xv[q].w * inv) * wn[q].w;
+    }
+  }
+  // Unconditional stores (a thread past the end rewrites the last float4 with
+  // the value it loaded from there): a conditional store lets the compiler
+  // sink each load into its branch, one round trip per load.
+#pragma unroll
+  for (int q = 0; q < kXq; ++q) xs4[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)] = xv[q];
   lds_barrier();
   float ag = 0.0f, au = 0.0f;
 #pragma unroll

@@ -157,6 +157,31 @@ def test_sparse_ffn_accumulate_and_device_count(kh, orc):
                                    atol=1e-4 * float(np.max(np.abs(yr))))
 
 
+@pytest.mark.parametrize("cnt_k", [400, 401, 0])
+def test_sparse_ffn_batch1_device_count(kh, orc, cnt_k):
+    """Batch 1 (the fused kernel) with a device-side count below n_active: the
+    blocks past the count contribute nothing, whatever the scratch held."""
+    from klearu_amd.dejavu import Mlp
+    rng = np.random.default_rng(78 + cnt_k)
+    H, I = 1024, 2816
+    wg, wu, wd, x, act = _ffn_case(orc, rng, H, I, 400, 1)
+    act = np.sort(np.concatenate([act, rng.choice(np.setdiff1d(np.arange(I), act), 1)]))[:max(cnt_k, 1)]
+    mlp = Mlp(wg, wu, wd, max_batch=1)
+    xd = torch.from_numpy(x).cuda()
+    full = torch.from_numpy(np.concatenate([act, np.arange(I)[~np.isin(np.arange(I), act)]])
+                            .astype(np.int32)).cuda()
+    # fill the scratch partial rows with a full-width call first
+    mlp.forward_sparse_into(xd, full, torch.empty_like(xd))
+    y0 = torch.from_numpy(rng.standard_normal((1, H)).astype(np.float32)).cuda()
+    y = y0.clone()
+    cnt = torch.tensor([cnt_k], dtype=torch.int32, device="cuda")
+    mlp.forward_sparse_into(xd, full, y, accumulate=True, n_active_dev=cnt, n_active=I)
+    yr = orc.sparse_mlp_forward_bf16(wg, wu, wd, x[0], act[:cnt_k])[0] if cnt_k else np.zeros(H, np.float32)
+    got = y.cpu().numpy()[0] - y0.cpu().numpy()[0]
+    print(f"count {cnt_k}: max-abs {float(np.max(np.abs(got - yr))):.3e}")
+    np.testing.assert_allclose(got, yr, rtol=RTOL, atol=1e-4 * max(float(np.max(np.abs(yr))), 1e-3))
+
+
 def test_sparse_ffn_rejects_bad_shapes(kh, orc):
     from klearu_amd import KlearuError
     from klearu_amd.dejavu import Mlp
