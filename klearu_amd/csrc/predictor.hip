@@ -256,12 +256,15 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
       const int pr = lane + 64 * q;
       const int blk = pr / kL1Chains, ch = pr % kL1Chains;
       const int j0 = (st * (kL1Stage / 8) + blk) * 8;
-      float w[8], pv[8];
+      float w[8];
       B8::widen(pre[i][q], w);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = __fmul_rn(w[e], xs[min(j0 + e, kL1LdsIn - 1)]);
-      P[j0 / 4][ch] = make_float4(pv[0], pv[1], pv[2], pv[3]);
-      P[j0 / 4 + 1][ch] = make_float4(pv[4], pv[5], pv[6], pv[7]);
+      // j0 + 7 < kL1LdsIn for every stage: two aligned float4 reads of x
+      const float4 xa = reinterpret_cast<const float4*>(xs)[j0 / 4];
+      const float4 xb = reinterpret_cast<const float4*>(xs)[j0 / 4 + 1];
+      P[j0 / 4][ch] = make_float4(__fmul_rn(w[0], xa.x), __fmul_rn(w[1], xa.y),
+                                  __fmul_rn(w[2], xa.z), __fmul_rn(w[3], xa.w));
+      P[j0 / 4 + 1][ch] = make_float4(__fmul_rn(w[4], xb.x), __fmul_rn(w[5], xb.y),
+                                      __fmul_rn(w[6], xb.z), __fmul_rn(w[7], xb.w));
     }
   };
   // Consumer chain over steps [j0, j1) (j0 a multiple of 4): a window of kWin
