@@ -525,6 +525,15 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
                         : make_uint2(0xffffffffu, 0u);
   const int i0 = threadIdx.x * kpt;
   const int cnt = max(0, min(kpt, n - i0));
+  if (mm) {
+    // reduced per wave while the scores are still in flight (requested first,
+    // so waiting for them does not wait for the scores)
+    const uint32_t a = wave_max_u32(mmv.y), c = wave_min_u32(mmv.x);
+    if (lane == 0) {
+      wmax[wave] = a;
+      wmin[wave] = c;
+    }
+  }
   // Coalesced loads through LDS (a thread's own contiguous range would make
   // every wave load touch dozens of cache lines), then each thread reads its
   // range; the odd-or-power-of-two strides keep the LDS reads conflict-light.
@@ -553,22 +562,22 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
     key[j] = f32_key(staged ? __uint_as_float(sstage[min(i0 + j, n - 1)]) : sc[min(i0 + j, n - 1)]);
   // 1. bits common to every key: the radix passes start below them (scores
   // cluster, so a pass over shared high bits would fill one or two bins).
-  uint32_t kmax = mmv.y, kmin = mmv.x;
   if (!mm) {
+    uint32_t kmax = 0u, kmin = 0xffffffffu;
 #pragma unroll
     for (int j = 0; j < kTopkPerThread; ++j)
       if (j < cnt) {
         kmax = max(kmax, key[j]);
         kmin = min(kmin, key[j]);
       }
+    kmax = wave_max_u32(kmax);
+    kmin = wave_min_u32(kmin);
+    if (lane == 0) {
+      wmax[wave] = kmax;
+      wmin[wave] = kmin;
+    }
+    __syncthreads();
   }
-  kmax = wave_max_u32(kmax);
-  kmin = wave_min_u32(kmin);
-  if (lane == 0) {
-    wmax[wave] = kmax;
-    wmin[wave] = kmin;
-  }
-  __syncthreads();
   uint32_t mx = 0u, mn = 0xffffffffu;
 #pragma unroll
   for (int w = 0; w < kTopkThreads / 64; ++w) {
