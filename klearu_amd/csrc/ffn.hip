@@ -114,6 +114,114 @@ __global__ __launch_bounds__(64 * kGuWaves) void ffn_gateup_kernel(
   }
 }
 
+// ---------------------------------------------------------------- batched gate/up on MFMA
+// Tokens 2..16 share the active rows: G[n][t] = sum_k W[n][k] x[t][k] is a
+// 16-row x 16-token tile product per wave on v_mfma_f32_16x16x32_bf16, with
+// the BF16 weight rows as they are stored and x split into two BF16 terms
+// (x = hi + lo + r, |r| <= 2^-17 |x|), so the products are those of f32 x
+// to well within the BF16-weight tolerance and accumulate in f32.
+// Lane (r = lane % 16, kb = lane / 16) holds row r and, in each 64-wide
+// k-step s, k = 64 s + 32 e + 8 kb + [0, 8) for the two MFMAs e = 0, 1.  Both
+// operands use this k order, so every k is summed once, and each load
+// instruction reads 64 contiguous bytes of each of the 16 rows.  Four waves
+// split k in quarters for each 16 rows (more loads in flight, twice the
+// blocks); the first adds the others' accumulators through LDS in a fixed
+// order, so results are deterministic.
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 kh_bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float kh_f32x4;
+
+constexpr int kMfSplit = 4;   // waves sharing one 16-row group (k quarters)
+constexpr int kMfWaves = 8;   // 2 row groups of 16 per block
+constexpr int kMfDepth = 4;   // k-steps of loads in flight per wave
+
+__device__ __forceinline__ kh_bf16x8 as_bf16x8(const uint4& v) {
+  return __builtin_bit_cast(kh_bf16x8, v);
+}
+
+// x [batch][H] f32 -> hi, lo [16][H] BF16 bits; rows >= batch are zero.
+__global__ void ffn_xsplit_kernel(const float* __restrict__ x, int batch, int H,
+                                  uint16_t* __restrict__ hi, uint16_t* __restrict__ lo) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 16LL * H) return;
+  const float v = i / H < batch ? x[i] : 0.0f;
+  const uint16_t h = f32_to_bf16(v);
+  hi[i] = h;
+  lo[i] = f32_to_bf16(v - bf16_to_f32(h));  // exact difference
+}
+
+__global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
+    const uint16_t* __restrict__ Wgu, const uint16_t* __restrict__ xhi,
+    const uint16_t* __restrict__ xlo, int batch, int H, const int32_t* __restrict__ active,
+    int n_active, const int32_t* __restrict__ n_active_dev, float* __restrict__ hbuf, int hstride) {
+  constexpr int kGroups = kMfWaves / kMfSplit;
+  __shared__ kh_f32x4 part[kGroups][kMfSplit - 1][4][64];
+  int n = n_active;
+  if (n_active_dev) n = min(n, *n_active_dev);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int grp = wave / kMfSplit, qtr = wave % kMfSplit;
+  const int base = (blockIdx.x * kGroups + grp) * 16;
+  const bool live = base < n;  // uniform per row group
+  const int r = lane & 15, kb = lane >> 4;
+  const int neuron = active[min(base + r, max(n, 1) - 1)];
+  const int qsteps = H / (64 * kMfSplit);  // k-steps per quarter
+  const int s0 = qtr * qsteps;
+  const uint4* __restrict__ g = reinterpret_cast<const uint4*>(Wgu + (size_t)neuron * 2 * H) + kb + 8 * s0;
+  const uint4* __restrict__ u = g + (H >> 3);
+  const uint4* __restrict__ xh = reinterpret_cast<const uint4*>(xhi + (size_t)r * H) + kb + 8 * s0;
+  const uint4* __restrict__ xl = reinterpret_cast<const uint4*>(xlo + (size_t)r * H) + kb + 8 * s0;
+  kh_f32x4 cg0 = {0, 0, 0, 0}, cg1 = cg0, cu0 = cg0, cu1 = cg0;
+  if (live) {
+    uint4 bg[kMfDepth][2], bu[kMfDepth][2], bh[kMfDepth][2], bl[kMfDepth][2];
+    auto load = [&](int d, int s) {  // clamped, unconditional (past the end: reread, unused)
+      const int o = 8 * min(s, qsteps - 1);
+      bg[d][0] = g[o]; bg[d][1] = g[o + 4];
+      bu[d][0] = u[o]; bu[d][1] = u[o + 4];
+      bh[d][0] = xh[o]; bh[d][1] = xh[o + 4];
+      bl[d][0] = xl[o]; bl[d][1] = xl[o + 4];
+    };
+#pragma unroll
+    for (int d = 0; d < kMfDepth; ++d) load(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+    // qsteps is a multiple of kMfDepth (host-checked): no test inside the
+    // loop, whose branches would make every iteration wait for all loads
+    for (int s = 0; s < qsteps; s += kMfDepth) {
+#pragma unroll
+      for (int d = 0; d < kMfDepth; ++d) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          cg0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bg[d][e]), as_bf16x8(bh[d][e]), cg0, 0, 0, 0);
+          cg1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bg[d][e]), as_bf16x8(bl[d][e]), cg1, 0, 0, 0);
+          cu0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bu[d][e]), as_bf16x8(bh[d][e]), cu0, 0, 0, 0);
+          cu1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bu[d][e]), as_bf16x8(bl[d][e]), cu1, 0, 0, 0);
+        }
+        load(d, s + d + kMfDepth);
+        // keep the prefetch here: the scheduler would otherwise sink it to its use
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  // C[n][t]: lane holds rows n = 4 kb + q (q = 0..3) of token t = r
+  if (qtr > 0) {
+    part[grp][qtr - 1][0][lane] = cg0;
+    part[grp][qtr - 1][1][lane] = cg1;
+    part[grp][qtr - 1][2][lane] = cu0;
+    part[grp][qtr - 1][3][lane] = cu1;
+  }
+  __syncthreads();
+  if (qtr > 0 || !live) return;
+  kh_f32x4 tg = cg0 + cg1, tu = cu0 + cu1;
+#pragma unroll
+  for (int j = 0; j < kMfSplit - 1; ++j) {
+    tg += part[grp][j][0][lane] + part[grp][j][1][lane];
+    tu += part[grp][j][2][lane] + part[grp][j][3][lane];
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int item = base + 4 * kb + q;
+    if (r < batch && item < n) hbuf[(size_t)r * hstride + item] = silu_ref(tg[q]) * tu[q];
+  }
+}
+
 // Single-token fused FFN: kFuWaves active neurons per block.  Wave w loads the
 // gate and up rows of neuron w and, for the down projection, column slice w
 // (H/kFuWaves columns) of all kFuWaves neurons' down rows, so every wave has
@@ -295,6 +403,7 @@ struct kh_sparse_ffn {
   uint16_t* wdt = nullptr;   // [inter][hidden]
   float* hbuf = nullptr;     // [max_batch][inter]
   float* partial = nullptr;  // [max(kMaxGroups*nb_tmpl, fused blocks)][hidden]
+  uint16_t* xsplit = nullptr;  // [2][16][hidden] BF16 hi / lo terms of x (batch > 1)
   int nslices = 0;
 };
 
@@ -344,8 +453,9 @@ extern "C" int kh_sparse_ffn_create(int hidden, int inter, const uint16_t* w_gat
   f->wdt = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * H * I));
   f->hbuf = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * I));
   f->partial = static_cast<float*>(dev_alloc(sizeof(float) * partial_rows(inter, nbt) * H));
+  if (max_batch > 1) f->xsplit = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * 2 * 16 * H));
   int rc = KH_OK;
-  if (!f->wgu || !f->wdt || !f->hbuf || !f->partial) rc = KH_ERR_ALLOC;
+  if (!f->wgu || !f->wdt || !f->hbuf || !f->partial || (max_batch > 1 && !f->xsplit)) rc = KH_ERR_ALLOC;
   if (rc == KH_OK) {
     if (hipMemcpy(f->wgu, gu, sizeof(uint16_t) * 2 * H * I, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(f->wdt, dt, sizeof(uint16_t) * H * I, hipMemcpyHostToDevice) != hipSuccess) {
@@ -382,7 +492,8 @@ extern "C" int kh_sparse_ffn_create_dev(int hidden, int inter, const uint16_t* w
   f->wdt = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * H * I));
   f->hbuf = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * I));
   f->partial = static_cast<float*>(dev_alloc(sizeof(float) * partial_rows(inter, nbt) * H));
-  if (!f->wgu || !f->wdt || !f->hbuf || !f->partial) {
+  if (max_batch > 1) f->xsplit = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * 2 * 16 * H));
+  if (!f->wgu || !f->wdt || !f->hbuf || !f->partial || (max_batch > 1 && !f->xsplit)) {
     kh_sparse_ffn_destroy(f);
     return KH_ERR_ALLOC;
   }
@@ -411,6 +522,7 @@ extern "C" int kh_sparse_ffn_destroy(kh_sparse_ffn* f) {
   dev_free(f->wdt);
   dev_free(f->hbuf);
   dev_free(f->partial);
+  dev_free(f->xsplit);
   delete f;
   return KH_OK;
 }
@@ -432,8 +544,20 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
     set_error("hidden %d too large for %d staged tokens", H, std::min(NB, kGuTok));
     return KH_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL(ffn_gateup_kernel<NB>, g1, dim3(64 * kGuWaves), lds1, st, f->wgu, x, batch,
-                     H, active, n_active, n_active_dev, f->hbuf, f->inter);
+  if (NB > 1 && f->xsplit && H % (64 * kMfSplit * kMfDepth) == 0) {
+    // several tokens: gate/up as 16 x 16 tile products on MFMA
+    uint16_t* xhi = f->xsplit;
+    uint16_t* xlo = f->xsplit + 16 * (size_t)H;
+    hipLaunchKernelGGL(ffn_xsplit_kernel, dim3(ceil_div(16 * H, 256)), dim3(256), 0, st, x, batch, H,
+                       xhi, xlo);
+    KH_LAUNCHED();
+    hipLaunchKernelGGL(ffn_gateup_mfma_kernel, dim3(ceil_div(n_active, 16 * (kMfWaves / kMfSplit))),
+                       dim3(64 * kMfWaves), 0, st, f->wgu, xhi, xlo, batch, H, active, n_active,
+                       n_active_dev, f->hbuf, f->inter);
+  } else {
+    hipLaunchKernelGGL(ffn_gateup_kernel<NB>, g1, dim3(64 * kGuWaves), lds1, st, f->wgu, x, batch,
+                       H, active, n_active, n_active_dev, f->hbuf, f->inter);
+  }
   KH_LAUNCHED();
   const int groups = gather_groups(n_active, f->nslices);
   if (groups == 0) {
