@@ -559,14 +559,23 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
                        H, active, n_active, n_active_dev, f->hbuf, f->inter);
   }
   KH_LAUNCHED();
-  const int groups = gather_groups(n_active, f->nslices);
-  if (groups == 0) {
-    set_error("n_active %d too large for the down kernel", n_active);
-    return KH_ERR_UNSUPPORTED;
+  int groups;
+  if (NB > 1 && H % 8 == 0) {
+    // several tokens: 512-row groups streamed with the next rows in flight
+    groups = ceil_div(n_active, kDnGroupRows);
+    hipLaunchKernelGGL(down_rows_kernel<NB>, dim3(f->nslices, groups), dim3(kDownThreads), 0, st,
+                       f->wdt, H, active, n_active, n_active_dev, f->hbuf, f->inter, batch,
+                       f->partial);
+  } else {
+    groups = gather_groups(n_active, f->nslices);
+    if (groups == 0) {
+      set_error("n_active %d too large for the down kernel", n_active);
+      return KH_ERR_UNSUPPORTED;
+    }
+    dim3 g2(f->nslices, groups);
+    hipLaunchKernelGGL(gather_rows_kernel<NB>, g2, dim3(kDownThreads), 0, st, f->wdt, H, active,
+                       n_active, n_active_dev, f->hbuf, f->inter, batch, groups, f->partial);
   }
-  dim3 g2(f->nslices, groups);
-  hipLaunchKernelGGL(gather_rows_kernel<NB>, g2, dim3(kDownThreads), 0, st, f->wdt, H, active,
-                     n_active, n_active_dev, f->hbuf, f->inter, batch, groups, f->partial);
   KH_LAUNCHED();
   hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch), dim3(64 * kRedWaves),
                      0, st, f->partial, H, groups, y, accumulate, nullptr, 0, nullptr);

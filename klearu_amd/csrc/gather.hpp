@@ -96,6 +96,101 @@ __global__ __launch_bounds__(kDownThreads) void gather_rows_kernel(
   }
 }
 
+// Down projection of several tokens over many rows: column slice (256
+// outputs, 8 per thread) x row group of kDnGroupRows rows.  The group's ids
+// and h values are staged in LDS; the rows are then streamed in chunks of 64
+// (8 per row lane), the next chunk's loads in flight while the current one is
+// accumulated, so one block covers 512 rows and the partial rows written for
+// the reduce are few (ceil(n / 512) groups).  Rows past the list end reload
+// the last row with h = 0.  The row lanes' sums are added in a fixed order.
+constexpr int kDnGroupRows = 512;
+constexpr int kDnChunk = 8;  // rows per row lane per chunk
+
+template <int NB>
+__global__ __launch_bounds__(kDownThreads) void down_rows_kernel(
+    const uint16_t* __restrict__ WdT, int H, const int32_t* __restrict__ active, int n_active,
+    const int32_t* __restrict__ n_active_dev, const float* __restrict__ hbuf, int hstride,
+    int batch, float* __restrict__ partial) {
+  constexpr int TB = NB < 4 ? NB : 4;  // tokens per reduction pass
+  __shared__ int s_ids[kDnGroupRows];
+  __shared__ float s_h[NB][kDnGroupRows];
+  __shared__ float red[kDownThreads / 64][TB][kSlice];
+  int n = n_active;
+  if (n_active_dev) n = min(n, *n_active_dev);
+  const int slice = blockIdx.x, grp = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int r0 = grp * kDnGroupRows;
+  const int nr = max(0, min(kDnGroupRows, n - r0));
+  for (int i = tid; i < kDnGroupRows; i += kDownThreads) s_ids[i] = active[min(r0 + i, max(n, 1) - 1)];
+  for (int i = tid; i < kDnGroupRows * NB; i += kDownThreads) {
+    const int b = i / kDnGroupRows, r = i - b * kDnGroupRows;
+    s_h[b][r] = (b < batch && r < nr) ? hbuf[(size_t)b * hstride + r0 + r] : 0.0f;
+  }
+  __syncthreads();
+  const int sub = tid >> 5, cl = tid & 31;
+  const int col = min(slice * kSlice + cl * 8, H - 8);  // clamped; columns past H are not written
+  float acc[NB][8];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[b][e] = 0.0f;
+  const int nchunks = (nr + 8 * kDnChunk - 1) / (8 * kDnChunk);
+  uint4 wa[kDnChunk], wb[kDnChunk];
+  auto load = [&](uint4 (&w)[kDnChunk], int c) {
+#pragma unroll
+    for (int m = 0; m < kDnChunk; ++m) {
+      const int r = min(c * 8 * kDnChunk + sub + 8 * m, kDnGroupRows - 1);
+      w[m] = *reinterpret_cast<const uint4*>(WdT + (size_t)s_ids[r] * H + col);
+    }
+  };
+  auto accum = [&](const uint4 (&w)[kDnChunk], int c) {
+#pragma unroll
+    for (int m = 0; m < kDnChunk; ++m) {
+      const int r = min(c * 8 * kDnChunk + sub + 8 * m, kDnGroupRows - 1);
+      const float wf[8] = {bf16_lo(w[m].x), bf16_hi(w[m].x), bf16_lo(w[m].y), bf16_hi(w[m].y),
+                           bf16_lo(w[m].z), bf16_hi(w[m].z), bf16_lo(w[m].w), bf16_hi(w[m].w)};
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float hv = s_h[b][r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[b][e] = fmaf(hv, wf[e], acc[b][e]);
+      }
+    }
+  };
+  if (nchunks > 0) load(wa, 0);
+  for (int c = 0; c < nchunks; c += 2) {
+    load(wb, c + 1);  // past the last chunk: clamped rereads, h = 0
+    __builtin_amdgcn_sched_barrier(0);
+    accum(wa, c);
+    load(wa, c + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    accum(wb, c + 1);
+  }
+  // the two row lanes of a wave, then the waves in order
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[b][e] += __shfl_xor(acc[b][e], 32, 64);
+  const int wv = tid >> 6;
+  const int ocol = slice * kSlice + tid;
+#pragma unroll
+  for (int b0 = 0; b0 < NB; b0 += TB) {
+    if ((tid & 63) < 32) {
+#pragma unroll
+      for (int t = 0; t < TB; ++t)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[wv][t][cl * 8 + e] = acc[b0 + t][e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+      const float sm = (red[0][t][tid] + red[1][t][tid]) + (red[2][t][tid] + red[3][t][tid]);
+      if (ocol < H && b0 + t < batch) partial[((size_t)grp * NB + b0 + t) * H + ocol] = sm;
+    }
+    __syncthreads();
+  }
+}
+
 // y[b][j] (=, or +=) sum over g of partial[g][b][j].  A block owns 64 columns;
 // its 16 waves take partial rows w, w+16, ... (all loads of a thread issued
 // before the first add), then the 16 wave sums are added in wave order, so the

@@ -720,9 +720,17 @@ __global__ __launch_bounds__(1024) void union_kernel(const int32_t* __restrict__
   const int nw = (n + 31) >> 5;
   for (int i = threadIdx.x; i < nw; i += blockDim.x) bits[i] = 0;
   __syncthreads();
-  for (int i = threadIdx.x; i < batch * k; i += blockDim.x) {
-    const int v = ids[i];
-    if (v >= 0 && v < n) atomicOr(&bits[v >> 5], 1u << (v & 31));
+  // ids requested eight per thread at a time (clamped, unconditional), so a
+  // thread waits one round trip per eight ids rather than per id
+  const int total = batch * k;
+  for (int i0 = 0; i0 < total; i0 += 8 * (int)blockDim.x) {
+    int v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = ids[min(i0 + (int)threadIdx.x + u * (int)blockDim.x, total - 1)];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (i0 + (int)threadIdx.x + u * (int)blockDim.x < total && v[u] >= 0 && v[u] < n)
+        atomicOr(&bits[v[u] >> 5], 1u << (v[u] & 31));
   }
   __syncthreads();
   int base = 0;
@@ -1020,6 +1028,7 @@ extern "C" int kh_union_active(const int32_t* ids_dev, int64_t batch, int k, int
                                int32_t* union_dev, int32_t* count_dev, void* stream) {
   KH_CHECK_ARG(ids_dev && union_dev && count_dev, "null argument");
   KH_CHECK_ARG(n > 0 && n <= 32 * 12288 && k >= 0 && batch >= 0, "bad shape (n <= 393216)");
+  KH_CHECK_ARG(batch * (int64_t)k < (int64_t)1 << 31, "batch * k too large");
   const size_t lds = sizeof(uint32_t) * ((n + 31) / 32);
   hipLaunchKernelGGL(union_kernel, dim3(1), dim3(1024), lds, as_stream(stream), ids_dev,
                      static_cast<int>(batch), k, n, union_dev, count_dev);
