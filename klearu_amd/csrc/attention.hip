@@ -25,10 +25,11 @@
 //                 from 16-byte K loads, chunk max / exp-sum and the un-normalised
 //                 V sum.  The current position's K/V come from this step's f32
 //                 projections, so the step sees them unrounded as the reference does.
-//   attn_combine  merges the chunks of each (token, head) into the head output, in
-//                 union order with zeros where a token did not select a union head
-//                 (the reference's zero-filled attn_concat, :44), and appends this
-//                 step's roped K and V to the cache.
+//                 One extra row of blocks appends this step's roped K and V to the
+//                 cache and zero-fills the union heads a token did not select (the
+//                 reference's zero-filled attn_concat, :44).
+//   attn_merge    merges the chunks of each (token, selected head) into the head
+//                 output, in union order.
 //   gather_rows + partials_reduce (gather.hpp)
 //                 o_proj over the union heads' WoT rows only; the reduce advances
 //                 each sequence's cache length once its output is complete.
@@ -84,7 +85,8 @@ template <int NB>
 __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
     const uint16_t* __restrict__ W, const float* __restrict__ x, int batch, int H, int kvrows,
     int D, int nh, const int32_t* __restrict__ heads, int nsel, float* __restrict__ y,
-    int ystride, int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows) {
+    int ystride, int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows,
+    int32_t* __restrict__ urank) {
   extern __shared__ float4 xs4[];  // [kQkvTok][H/4]; the plan block's flags / union list
   __shared__ int wsum[kQkvWaves];
   __shared__ int s_total;
@@ -106,6 +108,7 @@ __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
       const int f = h < nh ? s_flag[h] : 0;
       const int u = block_excl_scan(f, wsum, &s_total) + base;
       if (f) s_uh[u] = h;
+      if (h < nh) urank[h] = f ? u : -1;
       base += s_total;
     }
     __syncthreads();
@@ -177,57 +180,112 @@ constexpr int attn_chunk() {
   return kAttnThreads / (D / (16 / (int)sizeof(KV))) * kAttnPasses;
 }
 
-// One block per (chunk s, selected-head entry a, token b).  Writes the chunk's
-// un-normalised head output po[b][a][s][D] and (max, exp-sum) pml[b][a][s].
+// n floats (a multiple of 4) from 16-byte aligned p.
+template <int N>
+__device__ __forceinline__ void load_f4s(const float* __restrict__ p, float* f) {
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) {
+    const float4 v = reinterpret_cast<const float4*>(p)[i];
+    f[4 * i] = v.x; f[4 * i + 1] = v.y; f[4 * i + 2] = v.z; f[4 * i + 3] = v.w;
+  }
+}
+
+// Grid (nsplit, nsel + 1, batch).
+// Block (s, a < nsel, b): chunk s of the cache for token b's selected-head entry
+// a -> the un-normalised head output po[b][a][s][D] and (max, exp-sum)
+// pml[b][a][s] (attn_merge_kernel merges the chunks).
+// Block (s, nsel, b): appends this step's roped K and V of kv heads s, s+nsplit,
+// ... at position len[b] (decode blocks never read row len), and writes zeros
+// for union heads s, s+nsplit, ... that token b did not select (the
+// reference's zero-filled attn_concat, :44).
 template <typename KV, int D>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
-    const KV* __restrict__ kc, const KV* __restrict__ vc, const float* __restrict__ y,
-    int ystride, int nkv, int nh, const int32_t* __restrict__ heads, int nsel,
-    const int32_t* __restrict__ lens, const int64_t* __restrict__ positions,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int max_seq,
-    float inv_sqrt, int nsplit, float* __restrict__ po, float2* __restrict__ pml) {
+    KV* __restrict__ kc, KV* __restrict__ vc, const float* __restrict__ y, int ystride, int nkv,
+    int nh, const int32_t* __restrict__ heads, int nsel, const int32_t* __restrict__ lens,
+    const int64_t* __restrict__ positions, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, int max_seq, float inv_sqrt, int nsplit,
+    const int32_t* __restrict__ urank, float* __restrict__ po, float2* __restrict__ pml,
+    float* __restrict__ cat, int catstride) {
   constexpr int EPL = 16 / sizeof(KV);          // elements per 16-byte load
   constexpr int LPR = D / EPL;                  // lanes per cache row
   constexpr int RPP = kAttnThreads / LPR;       // rows per pass
   constexpr int NP = kAttnPasses;               // passes per chunk
   constexpr int CH = RPP * NP;                  // positions per chunk
   constexpr int HALF = D / 2;
+  constexpr int NW = kAttnThreads / 64;
   static_assert(LPR <= 64 && kAttnThreads % LPR == 0 && CH <= kAttnThreads, "tiling");
-  static_assert(HALF % EPL == 0, "a lane's slice lies in one half of the head");
+  static_assert(HALF % EPL == 0 && EPL % 4 == 0, "a lane's slice lies in one half of the head");
   __shared__ float s_p[CH];
   __shared__ float s_red[RPP][D];
-  __shared__ float s_wm[kAttnThreads / 64], s_wl[kAttnThreads / 64];
-  const int s = blockIdx.x, a = blockIdx.y, b = blockIdx.z;
-  const int h = heads[(size_t)b * nsel + a];
-  if (h < 0 || h >= nh) return;  // sparse_attention.rs:48-50
+  __shared__ float s_wm[NW], s_wl[NW];
+  __shared__ uint64_t s_tab[32];  // kExp2Tab
+  const int s = blockIdx.x, a = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
   const int len = lens[b];
-  if (len >= max_seq) return;    // full cache: the step is refused for this sequence
+  const bool valid = len < max_seq;  // a full cache refuses the step for this sequence
+  int64_t pos = positions ? positions[b] : len;
+  pos = pos < 0 ? 0 : (pos >= max_seq ? max_seq - 1 : pos);
+  const int kvd = nkv * D;
+  const float* yb = y + (size_t)b * ystride;
+  const float* ct = cos_t + pos * HALF;
+  const float* st = sin_t + pos * HALF;
+  const int32_t* hb = heads + (size_t)b * nsel;
+  if (a == nsel) {
+    if (valid) {
+      // KvCache::append (kv_cache.rs:33-48) of the roped k (sparse_attention.rs:33-39)
+      for (int hh = s; hh < nkv; hh += nsplit) {
+        const float* kx = yb + (size_t)hh * D;
+        const float* vx = kx + kvd;
+        const size_t dst = (((size_t)b * nkv + hh) * max_seq + len) * D;
+        for (int i = t; i < D; i += kAttnThreads) {
+          float kr;
+          if (i < HALF) kr = kx[i] * ct[i] - kx[i + HALF] * st[i];
+          else kr = kx[i] * ct[i - HALF] + kx[i - HALF] * st[i - HALF];
+          store_kv(kc + dst + i, kr);
+          store_kv(vc + dst + i, vx[i]);
+        }
+      }
+    }
+    for (int hu = s; hu < nh; hu += nsplit) {
+      const int u = urank[hu];
+      if (u < 0) continue;
+      int sel = 0;
+      if (valid)
+        for (int i = 0; i < nsel; ++i) sel |= hb[i] == hu;
+      if (!sel)
+        for (int i = t; i < D; i += kAttnThreads) cat[(size_t)b * catstride + (size_t)u * D + i] = 0.0f;
+    }
+    return;
+  }
+  const int h = hb[a];
+  if (h < 0 || h >= nh || !valid) return;  // sparse_attention.rs:48-50
   const int start = s * CH;
   if (start > len) return;
   const int n = min(CH, len + 1 - start);
   const int kvh = h / (nh / nkv);
-  int64_t pos = positions ? positions[b] : len;
-  pos = pos < 0 ? 0 : (pos >= max_seq ? max_seq - 1 : pos);
-  const int t = threadIdx.x, sl = t % LPR, r0 = t / LPR;
+  const int sl = t % LPR, r0 = t / LPR;
   const int e0 = sl * EPL;
-  const int kvd = nkv * D;
-  const float* yb = y + (size_t)b * ystride;
+  // This lane's q, current k and v slices with their RoPE partners (unconditional
+  // 16-byte loads), then every K and V load of the chunk, all in flight before
+  // the first use.  RotaryEmbedding::apply (rope.rs:75-87): x[i]*cos -
+  // x[i+half]*sin in the first half, x[i]*cos + x[i-half]*sin in the second
+  // (products rounded separately; x - y is x + (-y) exactly).
+  const uint64_t tabv = kExp2Tab[t & 31];
+  const bool first = e0 < HALF;
+  const int ec = first ? e0 : e0 - HALF;
+  const int ep = first ? e0 + HALF : e0 - HALF;
   const float* qsrc = yb + 2 * kvd + h * D;
   const float* kcur = yb + kvh * D;
-  const float* vcur = yb + kvd + kvh * D;
-  const float* ct = cos_t + pos * HALF;
-  const float* st = sin_t + pos * HALF;
-  // This lane's q, current k and current v slices (with RoPE partners) first ...
-  float qv[EPL], kn[EPL], vn[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    qv[e] = rope_elem<HALF>(qsrc, ct, st, e0 + e);
-    kn[e] = rope_elem<HALF>(kcur, ct, st, e0 + e);
-    vn[e] = vcur[e0 + e];
-  }
-  // ... then every K and V load of the chunk, all in flight before first use.
+  float qx[EPL], qp[EPL], kx[EPL], kp[EPL], vn[EPL], cs[EPL], sn[EPL];
+  load_f4s<EPL>(qsrc + e0, qx);
+  load_f4s<EPL>(qsrc + ep, qp);
+  load_f4s<EPL>(kcur + e0, kx);
+  load_f4s<EPL>(kcur + ep, kp);
+  load_f4s<EPL>(kcur + kvd + e0, vn);
+  load_f4s<EPL>(ct + ec, cs);
+  load_f4s<EPL>(st + ec, sn);
+  __builtin_amdgcn_sched_barrier(0);
   // Rows past the last cached one are clamped to it (position len itself is
-  // taken from kn/vn; with an empty cache row 0 is read and never used).
+  // taken from this step's k/v; with an empty cache row 0 is read and never used).
   const size_t rowbase = ((size_t)b * nkv + kvh) * (size_t)max_seq;
   const int last = len > 0 ? len - 1 : 0;
   uint4 kr[NP], vr[NP];
@@ -240,6 +298,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   for (int p = 0; p < NP; ++p) {
     const int j = min(start + p * RPP + r0, last);
     vr[p] = *reinterpret_cast<const uint4*>(vc + (rowbase + j) * D + e0);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load above is issued before any wait
+  float qv[EPL], kn[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    qv[e] = qx[e] * cs[e] + (first ? -qp[e] : qp[e]) * sn[e];
+    kn[e] = kx[e] * cs[e] + (first ? -kp[e] : kp[e]) * sn[e];
   }
   // scores: dense_dot(q, k_j) * inv_sqrt_dk (:55-58)
 #pragma unroll
@@ -263,6 +328,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     }
     if (sl == 0 && j - start < n) s_p[j - start] = d * inv_sqrt;
   }
+  if (t < 32) s_tab[t] = tabv;
   lds_barrier();
   // chunk max and exp-sum (softmax_inplace, :81-95, split over chunks)
   float m = t < n ? s_p[t] : -INFINITY;
@@ -271,10 +337,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   lds_barrier();
   m = s_wm[0];
 #pragma unroll
-  for (int w = 1; w < kAttnThreads / 64; ++w) m = fmaxf(m, s_wm[w]);
+  for (int w = 1; w < NW; ++w) m = fmaxf(m, s_wm[w]);
   float ex = 0.0f;
   if (t < n) {
-    ex = expf_glibc(s_p[t] - m);
+    ex = expf_glibc_t(s_p[t] - m, s_tab);
     s_p[t] = ex;
   }
   const float ls = wave_sum(ex);
@@ -303,89 +369,77 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   for (int e = 0; e < EPL; ++e) s_red[r0][e0 + e] = acc[e];
   lds_barrier();
   const size_t slot = ((size_t)b * nsel + a) * nsplit + s;
-  for (int i = t; i < D; i += kAttnThreads) {
+  if (t < D) {
     float o = 0.0f;
 #pragma unroll
-    for (int r = 0; r < RPP; ++r) o += s_red[r][i];
-    po[slot * D + i] = o;
+    for (int r = 0; r < RPP; ++r) o += s_red[r][t];
+    po[slot * D + t] = o;
   }
   if (t == 0) {
     float l = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kAttnThreads / 64; ++w) l += s_wl[w];
+    for (int w = 0; w < NW; ++w) l += s_wl[w];
     pml[slot] = make_float2(m, l);
   }
 }
 
-// One block per (head h, token b): the head output of token b in union order
-// (cat[b][u*D + i], zero when b did not select h), and, for h < nkv, the
-// append of this step's roped K and V of kv head h at position len[b].
-template <typename KV>
-__global__ __launch_bounds__(256) void attn_combine_kernel(
+// One block per (selected-head entry a, token b) whose head h is valid and not
+// named by an earlier entry of b: merges the chunks of every entry of b naming
+// h (duplicates summed in entry order, as the reference's += into one
+// attn_concat slice) into the head output cat[b][u*D ..], u = union rank of h.
+// Chunk j's weight is exp(m_j - M) with M the largest chunk max; the head
+// output is sum_j w_j po_j / sum_j w_j l_j.
+template <int D>
+__global__ __launch_bounds__(D) void attn_merge_kernel(
     const float* __restrict__ po, const float2* __restrict__ pml, int nsplit, int chunk,
-    const int32_t* __restrict__ heads, int nsel, int batch, int nh, int nkv, int D,
-    const int32_t* __restrict__ lens, const int64_t* __restrict__ positions,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int max_seq,
-    const float* __restrict__ y, int ystride, KV* __restrict__ kc, KV* __restrict__ vc,
-    float* __restrict__ cat, int catstride) {
-  __shared__ int s_flag[kMaxAttnHeads];
-  __shared__ int s_u;
-  const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    const int32_t* __restrict__ heads, int nsel, int nh, const int32_t* __restrict__ lens,
+    int max_seq, const int32_t* __restrict__ urank, float* __restrict__ cat, int catstride) {
+  __shared__ uint64_t s_tab[32];  // kExp2Tab
+  const int a = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int32_t* hb = heads + (size_t)b * nsel;
+  const int h = hb[a];
   const int len = lens[b];
-  const bool valid = len < max_seq;
-  const int half = D / 2;
-  if (h < nkv && valid) {
-    // KvCache::append (kv_cache.rs:33-48) of the roped k (sparse_attention.rs:33-39)
-    int64_t pos = positions ? positions[b] : len;
-    pos = pos < 0 ? 0 : (pos >= max_seq ? max_seq - 1 : pos);
-    const float* ct = cos_t + pos * half;
-    const float* st = sin_t + pos * half;
-    const float* kx = y + (size_t)b * ystride + (size_t)h * D;
-    const float* vx = kx + (size_t)nkv * D;
-    const size_t dst = (((size_t)b * nkv + h) * max_seq + len) * D;
-    for (int i = t; i < D; i += blockDim.x) {
-      float kr;
-      if (i < half) kr = kx[i] * ct[i] - kx[i + half] * st[i];
-      else kr = kx[i] * ct[i - half] + kx[i - half] * st[i - half];
-      store_kv(kc + dst + i, kr);
-      store_kv(vc + dst + i, vx[i]);
+  if (h < 0 || h >= nh || len >= max_seq) return;
+  for (int i = 0; i < a; ++i)
+    if (hb[i] == h) return;
+  const uint64_t tabv = kExp2Tab[t & 31];
+  const int ns = (len + chunk) / chunk;  // chunks covering len+1 rows
+  if (t < 32) s_tab[t] = tabv;
+  __syncthreads();
+  float out = 0.0f;
+  for (int a2 = a; a2 < nsel; ++a2) {
+    if (hb[a2] != h) continue;
+    const size_t slot0 = ((size_t)b * nsel + a2) * nsplit;
+    float M = -INFINITY;
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      float mx[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) mx[k] = pml[slot0 + min(s0 + k, ns - 1)].x;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) M = fmaxf(M, mx[k]);
     }
-  }
-  for (int i = t; i < nh; i += blockDim.x) s_flag[i] = 0;
-  if (t == 0) s_u = 0;
-  __syncthreads();
-  for (int i = t; i < batch * nsel; i += blockDim.x) {
-    const int hh = heads[i];
-    if (hh >= 0 && hh < nh) s_flag[hh] = 1;
-  }
-  __syncthreads();
-  if (!s_flag[h]) return;
-  int below = 0;
-  for (int i = t; i < h; i += blockDim.x) below += s_flag[i];
-  if (below) atomicAdd(&s_u, below);
-  __syncthreads();
-  const int u = s_u;
-  const int ns = valid ? (len + chunk) / chunk : 0;  // chunks covering len+1 rows
-  for (int i = t; i < D; i += blockDim.x) {
-    float out = 0.0f;
-    if (valid) {
-      for (int a = 0; a < nsel; ++a) {
-        if (heads[(size_t)b * nsel + a] != h) continue;
-        const size_t slot0 = ((size_t)b * nsel + a) * nsplit;
-        float M = -INFINITY;
-        for (int s = 0; s < ns; ++s) M = fmaxf(M, pml[slot0 + s].x);
-        float L = 0.0f, o = 0.0f;
-        for (int s = 0; s < ns; ++s) {
-          const float2 ml = pml[slot0 + s];
-          const float w = expf_glibc(ml.x - M);
-          L = fmaf(ml.y, w, L);
-          o = fmaf(po[(slot0 + s) * D + i], w, o);
+    float L = 0.0f, o = 0.0f;
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      float2 ml[8];
+      float pv[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const size_t sk = slot0 + min(s0 + k, ns - 1);
+        ml[k] = pml[sk];
+        pv[k] = po[sk * D + t];
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (s0 + k < ns) {
+          const float w = expf_glibc_t(ml[k].x - M, s_tab);
+          L = fmaf(ml[k].y, w, L);
+          o = fmaf(pv[k], w, o);
         }
-        out += o / L;
       }
     }
-    cat[(size_t)b * catstride + (size_t)u * D + i] = out;
+    out += o / L;
   }
+  cat[(size_t)b * catstride + (size_t)urank[h] * D + t] = out;
 }
 
 __global__ void attn_set_len_kernel(int32_t* __restrict__ lens, int n, int value) {
@@ -420,7 +474,7 @@ struct kh_sparse_attn {
   int32_t* lens = nullptr;   // [max_batch]
   float* y = nullptr;        // [max_batch][2*kvd + nh*d]
   float* cat = nullptr;      // [max_batch][nh*d]
-  int32_t* qrows = nullptr;  // [nh*d + 1]; the count is stored after the rows
+  int32_t* qrows = nullptr;  // [nh*d + 1 + nh]: rows, their count, union rank per head (-1: none)
   std::vector<int64_t> len_host;
   Scratch po, pml, partial;
   int kvd() const { return nkv * d; }
@@ -482,7 +536,7 @@ static int attn_alloc(int hidden, int num_heads, int num_kv_heads, int head_dim,
   a->lens = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * max_batch));
   a->y = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * a->ystride()));
   a->cat = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * qd));
-  a->qrows = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * (qd + 1)));
+  a->qrows = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * (qd + 1 + num_heads)));
   if (!a->wkvq || !a->wot || !a->kc || !a->vc || !a->cos_t || !a->sin_t || !a->lens || !a->y ||
       !a->cat || !a->qrows) {
     kh_sparse_attn_destroy(a);
@@ -698,12 +752,16 @@ template <typename KV, int D>
 static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
                               const int32_t* heads, int nsel, int nsplit, float* po, float2* pml,
                               hipStream_t st) {
-  const KV* kc = static_cast<const KV*>(a->kc);
-  const KV* vc = static_cast<const KV*>(a->vc);
-  hipLaunchKernelGGL((attn_decode_kernel<KV, D>), dim3(nsplit, nsel, batch), dim3(kAttnThreads), 0,
-                     st, kc, vc, a->y, a->ystride(), a->nkv, a->nh, heads, nsel, a->lens, pos,
-                     a->cos_t, a->sin_t, a->max_seq, 1.0f / sqrtf(static_cast<float>(D)), nsplit,
-                     po, pml);
+  const int qd = a->nh * D;
+  hipLaunchKernelGGL((attn_decode_kernel<KV, D>), dim3(nsplit, nsel + 1, batch),
+                     dim3(kAttnThreads), 0, st, static_cast<KV*>(a->kc), static_cast<KV*>(a->vc),
+                     a->y, a->ystride(), a->nkv, a->nh, heads, nsel, a->lens, pos, a->cos_t,
+                     a->sin_t, a->max_seq, 1.0f / sqrtf(static_cast<float>(D)), nsplit,
+                     a->qrows + qd + 1, po, pml, a->cat, qd);
+  KH_LAUNCHED();
+  hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(nsel, batch), dim3(D), 0, st, po, pml, nsplit,
+                     attn_chunk<KV, D>(), heads, nsel, a->nh, a->lens, a->max_seq,
+                     a->qrows + qd + 1, a->cat, qd);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -729,9 +787,9 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   const int rows = kvrows + qd;
   hipLaunchKernelGGL(attn_qkv_kernel<NB>, dim3(rows / kQkvWaves + 1), dim3(64 * kQkvWaves), lds,
                      st, a->wkvq, x, batch, H, kvrows, D, a->nh, heads, nsel, a->y, a->ystride(),
-                     a->qrows, a->qrows + qd);
+                     a->qrows, a->qrows + qd, a->qrows + qd + 1);
   KH_LAUNCHED();
-  // 2. split-K decode over the cache
+  // 2. split-K decode over the cache and the K/V append, then the merge of each head's chunks
   const int chunk = attn_chunk_of(a->kv_f32, D);
   const int nsplit = ceil_div(a->max_seq, chunk);
   const size_t slots = (size_t)batch * nsel * nsplit;
@@ -749,19 +807,7 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
                   : attn_decode_launch<uint16_t, 256>(a, batch, pos, heads, nsel, nsplit, po, pml, st);
   }
   if (rc != KH_OK) return rc;
-  // 3. combine chunks -> head outputs in union order; append K/V
-  if (a->kv_f32)
-    hipLaunchKernelGGL(attn_combine_kernel<float>, dim3(a->nh, batch), dim3(256), 0, st, po, pml,
-                       nsplit, chunk, heads, nsel, batch, a->nh, a->nkv, D, a->lens, pos, a->cos_t,
-                       a->sin_t, a->max_seq, a->y, a->ystride(), static_cast<float*>(a->kc),
-                       static_cast<float*>(a->vc), a->cat, qd);
-  else
-    hipLaunchKernelGGL(attn_combine_kernel<uint16_t>, dim3(a->nh, batch), dim3(256), 0, st, po,
-                       pml, nsplit, chunk, heads, nsel, batch, a->nh, a->nkv, D, a->lens, pos, a->cos_t,
-                       a->sin_t, a->max_seq, a->y, a->ystride(), static_cast<uint16_t*>(a->kc),
-                       static_cast<uint16_t*>(a->vc), a->cat, qd);
-  KH_LAUNCHED();
-  // 4. o_proj over the union heads' rows of WoT, then the ordered reduce
+  // 3. o_proj over the union heads' rows of WoT, then the ordered reduce
   const int nslices = ceil_div(H, kSlice);
   const int groups = gather_groups(qd, nslices);
   if (groups == 0) {
