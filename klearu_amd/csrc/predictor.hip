@@ -336,12 +336,17 @@ constexpr int kL2Threads = 64;
 // With mm set, each block also writes the (min, max) order-preserving keys of
 // its scores to mm[b][block]: the key bounds the top-k kernel starts from
 // (one slot per block, so no atomics contend on a single address).
-template <typename W>
+// TOPK (n_out <= 64, one block per row): the block also selects the top k
+// scores of its row, as topk_kernel does (key descending, ties by index), and
+// writes their indices to ids[b][min(k, n_out)] in `order`.
+template <typename W, bool TOPK = false>
 __global__ __launch_bounds__(kL2Threads) void pred_l2_kernel(const W* __restrict__ Wb,
                                                       const float* __restrict__ bias,
                                                       const float* __restrict__ hin, int n_hid,
                                                       int n_out, float* __restrict__ out,
-                                                      uint32_t* __restrict__ mm) {
+                                                      uint32_t* __restrict__ mm, int k = 0,
+                                                      int order = 0,
+                                                      int32_t* __restrict__ ids = nullptr) {
   using B8 = Blk8<W>;
   using V = typename B8::V;
   constexpr int kHw = 4;  // float4 of the hidden vector read ahead (16 steps)
@@ -420,6 +425,22 @@ __global__ __launch_bounds__(kL2Threads) void pred_l2_kernel(const W* __restrict
     const uint32_t kmin = wave_min_u32(ok ? key : 0xffffffffu);
     if (threadIdx.x == 0)
       reinterpret_cast<uint2*>(mm)[(size_t)b * gridDim.x + blockIdx.x] = make_uint2(kmin, kmax);
+  }
+  if constexpr (TOPK) {
+    // select_top_k's stable descending sort (mlp_predictor.rs:128-131) over
+    // the row's n_out <= 64 scores: lane o's rank among them
+    const uint32_t key = f32_key(score);
+    int rank = 0;
+    for (int j = 0; j < n_out; ++j) {
+      const uint32_t kj = __builtin_amdgcn_readlane(key, j);
+      rank += (kj > key || (kj == key && j < o)) ? 1 : 0;
+    }
+    const int kk = min(k, n_out);
+    const bool sel = ok && rank < kk;
+    const uint64_t bal = __ballot(sel);
+    const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0));
+    if (sel) ids[(size_t)b * kk + (order == KH_ORDER_SCORE ? rank : below)] = o;
   }
 }
 
@@ -876,9 +897,16 @@ static int ensure_batch(kh_predictor* p, int64_t batch) {
   return KH_OK;
 }
 
+// A top-k request that layer 2 may serve itself (done = true when it did).
+struct TopkReq {
+  int k = 0, order = 0;
+  int32_t* ids = nullptr;
+  bool done = false;
+};
+
 template <typename W>
 static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* scores,
-                         hipStream_t st, const NormIn& nrm, uint32_t* mm) {
+                         hipStream_t st, const NormIn& nrm, uint32_t* mm, TopkReq* tk) {
   const W* w1 = static_cast<const W*>(p->w1b);
   const W* w2 = static_cast<const W*>(p->w2b);
   const int l1_stages = ceil_div(p->in_dim, kL1Stage);
@@ -908,7 +936,12 @@ static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* 
     hipLaunchKernelGGL((chain_layer_kernel<0, W>), dim3(ceil_div(p->hid, 64), batch), dim3(64), 0,
                        st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
   KH_LAUNCHED();
-  if (p->hid <= kMaxL2Hid)
+  if (p->hid <= kMaxL2Hid && tk && p->out_dim <= kL2Threads) {
+    hipLaunchKernelGGL((pred_l2_kernel<W, true>), dim3(1, batch), dim3(kL2Threads), 0, st, w2,
+                       p->b2, p->hbuf, p->hid, p->out_dim, scores, nullptr, tk->k, tk->order,
+                       tk->ids);
+    tk->done = true;
+  } else if (p->hid <= kMaxL2Hid)
     hipLaunchKernelGGL(pred_l2_kernel<W>, dim3(l2_blocks(p), batch), dim3(kL2Threads), 0, st,
                        w2, p->b2, p->hbuf, p->hid, p->out_dim, scores, mm);
   else
@@ -919,18 +952,19 @@ static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* 
 }
 
 // With bounds set, layer 2 also folds the score key bounds into p->mm (when
-// its fast kernel runs; *bounds is then p->mm, else nullptr).
+// its fast kernel runs; *bounds is then p->mm, else nullptr).  With tk set,
+// layer 2 selects the top k itself when the row fits one wave (tk->done).
 static int predict_into(const kh_predictor* pc, const float* x, int64_t batch, float* scores,
                         hipStream_t st, const NormIn& nrm = NormIn{},
-                        uint32_t** bounds = nullptr) {
+                        uint32_t** bounds = nullptr, TopkReq* tk = nullptr) {
   auto* p = const_cast<kh_predictor*>(pc);
   int rc = ensure_batch(p, batch);
   if (rc != KH_OK) return rc;
   // the bounds fit one slot per top-k thread
   uint32_t* mm = (bounds && p->hid <= kMaxL2Hid && l2_blocks(p) <= kTopkThreads) ? p->mm : nullptr;
   if (bounds) *bounds = mm;
-  return p->bf16 ? predict_typed<uint16_t>(p, x, batch, scores, st, nrm, mm)
-                 : predict_typed<float>(p, x, batch, scores, st, nrm, mm);
+  return p->bf16 ? predict_typed<uint16_t>(p, x, batch, scores, st, nrm, mm, tk)
+                 : predict_typed<float>(p, x, batch, scores, st, nrm, mm, tk);
 }
 
 extern "C" int kh_predictor_predict(const kh_predictor* p, const float* x_dev, int64_t batch,
@@ -1011,8 +1045,9 @@ extern "C" int kh_predictor_select_top_k(const kh_predictor* p, const float* x_d
   int rc = ensure_batch(pm, batch);
   if (rc != KH_OK) return rc;
   uint32_t* mm = nullptr;
-  rc = predict_into(p, x_dev, batch, pm->sbuf, st, NormIn{}, &mm);
-  if (rc != KH_OK) return rc;
+  TopkReq tk{k, order, ids_dev};
+  rc = predict_into(p, x_dev, batch, pm->sbuf, st, NormIn{}, &mm, &tk);
+  if (rc != KH_OK || tk.done) return rc;
   return topk_launch(pm->sbuf, batch, p->out_dim, k, order, ids_dev, st, mm, l2_blocks(p));
 }
 
@@ -1047,8 +1082,9 @@ int predictor_topk_normed(const kh_predictor* pc, const float* hidden, int k, in
   int rc = ensure_batch(p, 1);
   if (rc != KH_OK) return rc;
   uint32_t* mm = nullptr;
-  rc = predict_into(p, hidden, 1, p->sbuf, st, nrm, &mm);
-  if (rc != KH_OK) return rc;
+  TopkReq tk{k, KH_ORDER_ASCENDING, ids};
+  rc = predict_into(p, hidden, 1, p->sbuf, st, nrm, &mm, &tk);
+  if (rc != KH_OK || tk.done) return rc;
   return topk_launch(p->sbuf, 1, p->out_dim, k, KH_ORDER_ASCENDING, ids, st, mm, l2_blocks(p));
 }
 }  // namespace kh

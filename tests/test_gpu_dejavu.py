@@ -64,6 +64,33 @@ def test_select_top_k_bit_exact(kh, orc, ind, hid, out, k, batch):
         np.testing.assert_array_equal(got_asc[b], np.sort(ref))
 
 
+@pytest.mark.parametrize("out,k,batch", [(40, 7, 3), (64, 33, 2), (64, 64, 1), (65, 20, 2), (1, 1, 2)])
+def test_select_top_k_small_rows_ties(kh, orc, out, k, batch):
+    """Rows of up to 64 scores are selected inside layer 2; duplicated and
+    zeroed weight rows make exact score ties (zero rows give sigmoid(0)), so
+    the index tie-break is exercised.  65 scores take the separate top-k."""
+    from klearu_amd.dejavu import ORDER_ASCENDING, SparsityPredictor
+    rng = np.random.default_rng(out * 100 + k)
+    ind, hid = 96, 24
+    w1, b1, w2, b2 = make_predictor(orc, rng, ind, hid, out)
+    w2 = orc.bf16_to_f32(w2).copy()
+    w2[out // 3:: 4] = 0.0
+    if out > 6:
+        w2[5] = w2[2]
+        w2[out - 1] = w2[2]
+    p = SparsityPredictor(orc.bf16_to_f32(w1), b1, w2, b2)
+    x = rng.standard_normal((batch, ind)).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    got = p.select_top_k(xd, k).cpu().numpy()
+    got_asc = p.select_top_k(xd, k, ORDER_ASCENDING).cpu().numpy()
+    for b in range(batch):
+        s, _ = orc.predictor_predict(w1, b1, bf16(orc, w2), b2, x[b])
+        ref = orc.select_top_k(s, k)
+        assert len(np.unique(s)) < out or out == 1
+        np.testing.assert_array_equal(got[b], ref)
+        np.testing.assert_array_equal(got_asc[b], np.sort(ref))
+
+
 @pytest.mark.parametrize("n,k", [(11008, 1652), (5632, 564), (32, 16), (1000, 1000), (1000, 1),
                                  (20000, 3000), (40000, 4000), (65535, 64), (7, 0)])
 def test_topk_ties_and_edges(kh, orc, n, k):
