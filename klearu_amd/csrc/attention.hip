@@ -29,8 +29,9 @@
 //                 cache and zero-fills the union heads a token did not select (the
 //                 reference's zero-filled attn_concat, :44).
 //   attn_merge    merges the chunks of each (token, selected head) into the head
-//                 output, in union order.
-//   gather_rows + partials_reduce (gather.hpp)
+//                 output, in union order (batch > 2, or head lists longer than
+//                 kOprojMaxSel; otherwise attn_oproj merges the chunks of its rows).
+//   attn_oproj (or gather_rows) + partials_reduce (gather.hpp)
 //                 o_proj over the union heads' WoT rows only; the reduce advances
 //                 each sequence's cache length once its output is complete.
 // Bytes per token at 7B shape (hidden 4096, 32 heads x 128, 16 selected, len
@@ -383,63 +384,82 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   }
 }
 
+// One entry's head output, for R head dimensions e[r] per lane, from its ns
+// decode chunks at slots sa .. sa+ns-1: out[r] += sum_j w_j po_j[e] / sum_j w_j l_j
+// with w_j = exp(m_j - M), M the largest chunk max; both sums sequential in j.
+// The weights are formed one per lane, so the whole wave must be active.
+template <int R>
+__device__ __forceinline__ void merge_chunks(const float* __restrict__ po,
+                                             const float2* __restrict__ pml, size_t sa, int ns,
+                                             int D, const int (&e)[R], const uint64_t* tab,
+                                             float (&out)[R]) {
+  const int lane = threadIdx.x & 63;
+  float M = -INFINITY;
+  for (int s0 = 0; s0 < ns; s0 += 64)
+    M = fmaxf(M, wave_max(s0 + lane < ns ? pml[sa + min(s0 + lane, ns - 1)].x : -INFINITY));
+  float L = 0.0f, o[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) o[r] = 0.0f;
+  for (int s0 = 0; s0 < ns; s0 += 64) {
+    const float2 mlv = pml[sa + min(s0 + lane, ns - 1)];
+    const float wv = expf_glibc_t(mlv.x - M, tab);
+    const int cnt = min(64, ns - s0);
+    for (int k0 = 0; k0 < cnt; k0 += 16) {
+      float pv[R][16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const size_t sl = sa + s0 + min(k0 + k, cnt - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) pv[r][k] = po[sl * D + e[r]];
+      }
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        if (k0 + k < cnt) {
+          const float wk = readlane_f(wv, k0 + k);
+          L = fmaf(readlane_f(mlv.y, k0 + k), wk, L);
+#pragma unroll
+          for (int r = 0; r < R; ++r) o[r] = fmaf(pv[r][k], wk, o[r]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) out[r] += o[r] / L;
+}
+
 // One block per (selected-head entry a, token b) whose head h is valid and not
 // named by an earlier entry of b: merges the chunks of every entry of b naming
 // h (duplicates summed in entry order, as the reference's += into one
 // attn_concat slice) into the head output cat[b][u*D ..], u = union rank of h.
-// Chunk j's weight is exp(m_j - M) with M the largest chunk max; the head
-// output is sum_j w_j po_j / sum_j w_j l_j.
 template <int D>
 __global__ __launch_bounds__(D) void attn_merge_kernel(
     const float* __restrict__ po, const float2* __restrict__ pml, int nsplit, int chunk,
     const int32_t* __restrict__ heads, int nsel, int nh, const int32_t* __restrict__ lens,
     int max_seq, const int32_t* __restrict__ urank, float* __restrict__ cat, int catstride) {
+  static_assert(D % 64 == 0, "whole waves");
   __shared__ uint64_t s_tab[32];  // kExp2Tab
-  const int a = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int a = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63;
   const int32_t* hb = heads + (size_t)b * nsel;
   const int h = hb[a];
   const int len = lens[b];
   if (h < 0 || h >= nh || len >= max_seq) return;
-  for (int i = 0; i < a; ++i)
-    if (hb[i] == h) return;
   const uint64_t tabv = kExp2Tab[t & 31];
+  for (int i0 = 0; i0 < a; i0 += 64)
+    if (__ballot(i0 + lane < a && hb[min(i0 + lane, a - 1)] == h)) return;  // not the first
   const int ns = (len + chunk) / chunk;  // chunks covering len+1 rows
   if (t < 32) s_tab[t] = tabv;
   __syncthreads();
-  float out = 0.0f;
-  for (int a2 = a; a2 < nsel; ++a2) {
-    if (hb[a2] != h) continue;
-    const size_t slot0 = ((size_t)b * nsel + a2) * nsplit;
-    float M = -INFINITY;
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-      float mx[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) mx[k] = pml[slot0 + min(s0 + k, ns - 1)].x;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) M = fmaxf(M, mx[k]);
+  float out[1] = {0.0f};
+  const int e[1] = {t};
+  for (int a0 = a; a0 < nsel; a0 += 64) {
+    uint64_t hit = __ballot(a0 + lane < nsel && hb[min(a0 + lane, nsel - 1)] == h);
+    while (hit) {
+      const int a2 = a0 + __builtin_ctzll(hit);
+      hit &= hit - 1;
+      merge_chunks<1>(po, pml, ((size_t)b * nsel + a2) * nsplit, ns, D, e, s_tab, out);
     }
-    float L = 0.0f, o = 0.0f;
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-      float2 ml[8];
-      float pv[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const size_t sk = slot0 + min(s0 + k, ns - 1);
-        ml[k] = pml[sk];
-        pv[k] = po[sk * D + t];
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        if (s0 + k < ns) {
-          const float w = expf_glibc_t(ml[k].x - M, s_tab);
-          L = fmaf(ml[k].y, w, L);
-          o = fmaf(pv[k], w, o);
-        }
-      }
-    }
-    out += o / L;
   }
-  cat[(size_t)b * catstride + (size_t)urank[h] * D + t] = out;
+  cat[(size_t)b * catstride + (size_t)urank[h] * D + t] = out[0];
 }
 
 __global__ void attn_set_len_kernel(int32_t* __restrict__ lens, int n, int value) {
@@ -458,6 +478,134 @@ __global__ __launch_bounds__(256) void attn_fill_cache_kernel(const float* __res
   const int64_t h = i / per, r = i - h * per;
   store_kv(dst + (h * max_seq) * (int64_t)D + r, src[i]);
 }
+
+// o_proj for batch <= 2 with the chunk merge folded in: gather_rows_kernel's
+// column slice x row group over the union rows of WoT, where the value of row
+// h*D + e for token b is computed in the block from the decode chunks (the
+// attn_merge_kernel arithmetic, so the result is the same).  Waves 0-3 issue
+// the weight loads and accumulate; waves 4-7 merge the chunks meanwhile (each
+// wave waits only for its own loads).
+constexpr int kOprojMaxSel = 256;  // head-list entries staged per token
+constexpr int kOprojThreads = 2 * kDownThreads;
+template <int NB>
+__global__ __launch_bounds__(kOprojThreads) void attn_oproj_kernel(
+    const uint16_t* __restrict__ WoT, int H, int D, const int32_t* __restrict__ rows,
+    int n_rows, const int32_t* __restrict__ n_rows_dev, const float* __restrict__ po,
+    const float2* __restrict__ pml, int nsplit, int chunk, const int32_t* __restrict__ heads,
+    int nsel, const int32_t* __restrict__ lens, int max_seq, int batch, int groups,
+    float* __restrict__ partial) {
+  __shared__ float red[4][NB][kSlice];
+  __shared__ int s_ids[kDownRows];
+  __shared__ float s_h[NB][kDownRows];
+  __shared__ int s_hd[NB][kOprojMaxSel];
+  __shared__ uint64_t s_tab[32];  // kExp2Tab
+  __shared__ int s_len[NB];
+  const int n = min(n_rows, *n_rows_dev);
+  const int slice = blockIdx.x, grp = blockIdx.y;
+  const int tid = threadIdx.x;
+  const bool gather = tid < kDownThreads;
+  const int per = (n + groups - 1) / groups;
+  const int r0 = min(n, grp * per);
+  const int r1 = min(n, r0 + per);
+  const int nr = r1 - r0;  // <= kDownRows by construction of `groups`
+  const int rlast = max(nr, 1) - 1;
+  const uint64_t tabv = kExp2Tab[tid & 31];
+  if (tid < nr) s_ids[tid] = rows[r0 + tid];
+  if (tid == 0 && nr == 0) s_ids[0] = 0;  // an empty group reads row 0, unused
+  for (int i = tid; i < NB * nsel; i += kOprojThreads) {
+    const int b = i / nsel;
+    s_hd[b][i - b * nsel] = b < batch ? heads[i] : -1;
+  }
+  if (tid < NB) s_len[tid] = tid < batch ? lens[tid] : max_seq;
+  if (tid < 32) s_tab[tid] = tabv;
+  __syncthreads();
+  constexpr int RPL = kDownRows / 8;  // rows per row lane
+  const int sub = (tid & (kDownThreads - 1)) >> 5;
+  const int cl = tid & 31;
+  const int col = slice * kSlice + cl * 8;
+  uint4 w[RPL];
+  if (gather) {
+    // Unconditional (clamped) loads: rows past the group and columns past H
+    // re-read valid ones that are never used.
+    const int colc = col < H ? col : H - 8;
+#pragma unroll
+    for (int m = 0; m < RPL; ++m)
+      w[m] = *reinterpret_cast<const uint4*>(WoT + (size_t)s_ids[min(sub + 8 * m, rlast)] * H + colc);
+  } else {
+    // Merge waves: one (token b, head slot j) pair per wave at a time; a slot
+    // is the run of the group's rows that belong to one head.  For each entry
+    // of b naming the head (ascending), the chunk weights w_j = exp(m_j - M)
+    // are formed one per lane, and each lane accumulates its rows (at most
+    // two) as sum_j w_j po_j / sum_j w_j l_j, sequential in j.  Heads b did
+    // not select give 0.
+    const int mw = (tid - kDownThreads) >> 6, lane = tid & 63;
+    const int i0 = s_ids[0] % D;  // head dimension of the group's first row
+    const int nslot = nr > 0 ? (i0 + nr - 1) / D + 1 : 0;
+    for (int p = mw; p < batch * nslot; p += kDownThreads / 64) {
+      const int b = p / nslot, j = p - b * nslot;
+      const int rb = max(0, j * D - i0), re = min(nr, (j + 1) * D - i0);  // rows [rb, re)
+      const int h = s_ids[rb] / D;
+      const int len = s_len[b];
+      const int ns = len < max_seq ? (len + chunk) / chunk : 0;  // chunks covering len+1 rows
+      const int ra = rb + lane, rc = rb + lane + 64;
+      const int ea = (i0 + min(ra, re - 1)) % D, ec = (i0 + min(rc, re - 1)) % D;
+      float out[2] = {0.0f, 0.0f};
+      const int ee[2] = {ea, ec};
+      for (int a0 = 0; a0 < nsel && ns > 0; a0 += 64) {
+        uint64_t hit = __ballot(a0 + lane < nsel && s_hd[b][min(a0 + lane, nsel - 1)] == h);
+        while (hit) {
+          const int a = a0 + __builtin_ctzll(hit);
+          hit &= hit - 1;
+          merge_chunks<2>(po, pml, ((size_t)b * nsel + a) * nsplit, ns, D, ee, s_tab, out);
+        }
+      }
+      const float outa = out[0], outc = out[1];
+      if (b < NB && ra < re) s_h[b][ra] = outa;
+      if (b < NB && rc < re) s_h[b][rc] = outc;
+    }
+  }
+  __syncthreads();
+  if (gather) {
+    float acc[NB][8];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[b][e] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < RPL; ++m) {
+      const int r = sub + 8 * m;
+      if (r >= nr) break;
+      const float wf[8] = {bf16_lo(w[m].x), bf16_hi(w[m].x), bf16_lo(w[m].y), bf16_hi(w[m].y),
+                           bf16_lo(w[m].z), bf16_hi(w[m].z), bf16_lo(w[m].w), bf16_hi(w[m].w)};
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float hv = s_h[b][r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[b][e] = fmaf(hv, wf[e], acc[b][e]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[b][e] += __shfl_xor(acc[b][e], 32, 64);
+    const int wv = tid >> 6;
+    if ((tid & 63) < 32) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[wv][b][cl * 8 + e] = acc[b][e];
+    }
+  }
+  __syncthreads();
+  if (gather) {
+    const int ocol = slice * kSlice + tid;
+    for (int b = 0; b < batch; ++b) {
+      const float sm = (red[0][b][tid] + red[1][b][tid]) + (red[2][b][tid] + red[3][b][tid]);
+      if (ocol < H) partial[((size_t)grp * NB + b) * H + ocol] = sm;
+    }
+  }
+}
+
 
 }  // namespace kh
 
@@ -751,7 +899,7 @@ static int attn_chunk_of(int kv_f32, int D) {
 template <typename KV, int D>
 static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
                               const int32_t* heads, int nsel, int nsplit, float* po, float2* pml,
-                              hipStream_t st) {
+                              bool merge, hipStream_t st) {
   const int qd = a->nh * D;
   hipLaunchKernelGGL((attn_decode_kernel<KV, D>), dim3(nsplit, nsel + 1, batch),
                      dim3(kAttnThreads), 0, st, static_cast<KV*>(a->kc), static_cast<KV*>(a->vc),
@@ -759,6 +907,7 @@ static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
                      a->sin_t, a->max_seq, 1.0f / sqrtf(static_cast<float>(D)), nsplit,
                      a->qrows + qd + 1, po, pml, a->cat, qd);
   KH_LAUNCHED();
+  if (!merge) return KH_OK;
   hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(nsel, batch), dim3(D), 0, st, po, pml, nsplit,
                      attn_chunk<KV, D>(), heads, nsel, a->nh, a->lens, a->max_seq,
                      a->qrows + qd + 1, a->cat, qd);
@@ -789,22 +938,27 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
                      st, a->wkvq, x, batch, H, kvrows, D, a->nh, heads, nsel, a->y, a->ystride(),
                      a->qrows, a->qrows + qd, a->qrows + qd + 1);
   KH_LAUNCHED();
-  // 2. split-K decode over the cache and the K/V append, then the merge of each head's chunks
+  // 2. split-K decode over the cache and the K/V append (then, for batch > 2 or head
+  //    lists longer than kOprojMaxSel, the merge of each head's chunks)
   const int chunk = attn_chunk_of(a->kv_f32, D);
   const int nsplit = ceil_div(a->max_seq, chunk);
   const size_t slots = (size_t)batch * nsel * nsplit;
   float* po = static_cast<float*>(a->po.get(sizeof(float) * slots * D));
   float2* pml = static_cast<float2*>(a->pml.get(sizeof(float2) * slots));
   if (!po || !pml) return KH_ERR_ALLOC;
+  // batch <= 2: the merge runs inside the o_proj kernel (for more tokens the
+  // separate merge, one block per (entry, token), is faster)
+  constexpr int kFoldNB = NB <= 2 ? NB : 2;
+  const bool fold = NB <= 2 && nsel <= kOprojMaxSel;
   int rc;
   if (a->kv_f32) {
-    rc = D == 64 ? attn_decode_launch<float, 64>(a, batch, pos, heads, nsel, nsplit, po, pml, st)
-       : D == 128 ? attn_decode_launch<float, 128>(a, batch, pos, heads, nsel, nsplit, po, pml, st)
-                  : attn_decode_launch<float, 256>(a, batch, pos, heads, nsel, nsplit, po, pml, st);
+    rc = D == 64 ? attn_decode_launch<float, 64>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st)
+       : D == 128 ? attn_decode_launch<float, 128>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st)
+                  : attn_decode_launch<float, 256>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st);
   } else {
-    rc = D == 64 ? attn_decode_launch<uint16_t, 64>(a, batch, pos, heads, nsel, nsplit, po, pml, st)
-       : D == 128 ? attn_decode_launch<uint16_t, 128>(a, batch, pos, heads, nsel, nsplit, po, pml, st)
-                  : attn_decode_launch<uint16_t, 256>(a, batch, pos, heads, nsel, nsplit, po, pml, st);
+    rc = D == 64 ? attn_decode_launch<uint16_t, 64>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st)
+       : D == 128 ? attn_decode_launch<uint16_t, 128>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st)
+                  : attn_decode_launch<uint16_t, 256>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st);
   }
   if (rc != KH_OK) return rc;
   // 3. o_proj over the union heads' rows of WoT, then the ordered reduce
@@ -816,8 +970,14 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   }
   float* partial = static_cast<float*>(a->partial.get(sizeof(float) * groups * NB * H));
   if (!partial) return KH_ERR_ALLOC;
-  hipLaunchKernelGGL(gather_rows_kernel<NB>, dim3(nslices, groups), dim3(kDownThreads), 0, st,
-                     a->wot, H, a->qrows, qd, a->qrows + qd, a->cat, qd, batch, groups, partial);
+  if (fold)
+    hipLaunchKernelGGL(attn_oproj_kernel<kFoldNB>, dim3(nslices, groups), dim3(kOprojThreads), 0,
+                       st, a->wot, H, D, a->qrows, qd, a->qrows + qd, po, pml, nsplit, chunk,
+                       heads, nsel, a->lens, a->max_seq, batch, groups, partial);
+  else
+    hipLaunchKernelGGL(gather_rows_kernel<NB>, dim3(nslices, groups), dim3(kDownThreads), 0, st,
+                       a->wot, H, a->qrows, qd, a->qrows + qd, a->cat, qd, batch, groups,
+                       partial);
   KH_LAUNCHED();
   hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch),
                      dim3(64 * kRedWaves), 0, st, partial, H, groups, out, accumulate, a->lens,
