@@ -48,6 +48,7 @@
 #include <vector>
 
 #include "gather.hpp"
+#include "mfma.hpp"
 
 namespace kh {
 
@@ -80,6 +81,35 @@ __device__ __forceinline__ void widen16(const uint4& v, float* f, float) {
 __device__ __forceinline__ void store_kv(uint16_t* p, float v) { *p = f32_to_bf16(v); }
 __device__ __forceinline__ void store_kv(float* p, float v) { *p = v; }
 
+// The union of selected heads in ascending order -> rows h*D + r of WoT
+// (qrows, their count in *nqrows) and each head's union rank (urank, -1 for
+// heads no token selected).  Block-wide; s_flag and s_uh hold nh ints each.
+__device__ void qkv_plan(const int32_t* __restrict__ heads, int nent, int nh, int D,
+                         int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows,
+                         int32_t* __restrict__ urank, int* s_flag, int* s_uh, int* wsum,
+                         int* s_total) {
+  for (int h = threadIdx.x; h < nh; h += blockDim.x) s_flag[h] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < nent; i += blockDim.x) {
+    const int h = heads[i];
+    if (h >= 0 && h < nh) s_flag[h] = 1;
+  }
+  __syncthreads();
+  int base = 0;
+  for (int h0 = 0; h0 < nh; h0 += blockDim.x) {
+    const int h = h0 + threadIdx.x;
+    const int f = h < nh ? s_flag[h] : 0;
+    const int u = block_excl_scan(f, wsum, s_total) + base;
+    if (f) s_uh[u] = h;
+    if (h < nh) urank[h] = f ? u : -1;
+    base += *s_total;
+  }
+  __syncthreads();
+  const int nq = base * D;
+  for (int i = threadIdx.x; i < nq; i += blockDim.x) qrows[i] = s_uh[i / D] * D + i % D;
+  if (threadIdx.x == 0) *nqrows = nq;
+}
+
 // y[b][row] = Wkvq[row] . x[b] for the K/V rows and the Q rows of selected
 // heads.  The grid has one extra (last) block that writes the o_proj row list.
 template <int NB>
@@ -93,29 +123,8 @@ __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
   __shared__ int s_total;
   const int nent = batch * nsel;
   if (blockIdx.x == gridDim.x - 1) {
-    // Union of selected heads in ascending order -> rows h*D + r of WoT.
     int* s_flag = reinterpret_cast<int*>(xs4);
-    int* s_uh = s_flag + nh;
-    for (int h = threadIdx.x; h < nh; h += blockDim.x) s_flag[h] = 0;
-    __syncthreads();
-    for (int i = threadIdx.x; i < nent; i += blockDim.x) {
-      const int h = heads[i];
-      if (h >= 0 && h < nh) s_flag[h] = 1;
-    }
-    __syncthreads();
-    int base = 0;
-    for (int h0 = 0; h0 < nh; h0 += blockDim.x) {
-      const int h = h0 + threadIdx.x;
-      const int f = h < nh ? s_flag[h] : 0;
-      const int u = block_excl_scan(f, wsum, &s_total) + base;
-      if (f) s_uh[u] = h;
-      if (h < nh) urank[h] = f ? u : -1;
-      base += s_total;
-    }
-    __syncthreads();
-    const int nq = base * D;
-    for (int i = threadIdx.x; i < nq; i += blockDim.x) qrows[i] = s_uh[i / D] * D + i % D;
-    if (threadIdx.x == 0) *nqrows = nq;
+    qkv_plan(heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_flag + nh, wsum, &s_total);
     return;
   }
   const int row0 = blockIdx.x * kQkvWaves;
@@ -172,6 +181,103 @@ __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
       const float s = wave_sum(acc[b]);
       if (lane == 0) y[(size_t)b * ystride + row] = s;
     }
+  }
+}
+
+// Batched q/k/v projections (2..16 tokens) on the matrix cores: the K and V
+// rows and the Q rows of heads that some token selected, in groups of 32 rows
+// (two 16-row tiles per wave sharing the x operand), computed as
+// ffn_gateup_mfma_kernel computes its rows (x split into BF16 hi/lo terms, k
+// in quarters over four waves whose sums are added in a fixed order).  The
+// last block writes the o_proj row list as attn_qkv_kernel does.
+__global__ __launch_bounds__(64 * kMfWaves) void attn_qkv_mfma_kernel(
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ xhi,
+    const uint16_t* __restrict__ xlo, int batch, int H, int kvrows, int rows, int D, int nh,
+    const int32_t* __restrict__ heads, int nsel, float* __restrict__ y, int ystride,
+    int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows, int32_t* __restrict__ urank) {
+  constexpr int kGroups = kMfWaves / kMfSplit;
+  __shared__ kh_f32x4 part[kGroups][kMfSplit - 1][4][64];
+  __shared__ int s_flag[kMaxAttnHeads], s_uh[kMaxAttnHeads];
+  __shared__ int wsum[kMfWaves];
+  __shared__ int s_total;
+  const int nent = batch * nsel;
+  if (blockIdx.x == gridDim.x - 1) {
+    qkv_plan(heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_uh, wsum, &s_total);
+    return;
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int grp = wave / kMfSplit, qtr = wave % kMfSplit;
+  const int base = (blockIdx.x * kGroups + grp) * 32;
+  bool live = base < rows;
+  if (live && base >= kvrows) {
+    // Q rows of head h (D is a multiple of 32): skipped unless some token selected h
+    const int h = (base - kvrows) / D;
+    int any = 0;
+    for (int i = lane; i < nent; i += 64) any |= heads[i] == h;
+    live = __ballot(any) != 0;
+  }
+  const int r = lane & 15, kb = lane >> 4;
+  const int qsteps = H / (64 * kMfSplit);  // k-steps per quarter
+  const int s0 = qtr * qsteps;
+  const uint4* __restrict__ wa =
+      reinterpret_cast<const uint4*>(W + (size_t)min(base + r, rows - 1) * H) + kb + 8 * s0;
+  const uint4* __restrict__ wb =
+      reinterpret_cast<const uint4*>(W + (size_t)min(base + 16 + r, rows - 1) * H) + kb + 8 * s0;
+  // tokens past the batch re-read the last token's row (the same cache lines,
+  // so no extra traffic); their results are never written
+  const int xr = min(r, batch - 1);
+  const uint4* __restrict__ xh = reinterpret_cast<const uint4*>(xhi + (size_t)xr * H) + kb + 8 * s0;
+  const uint4* __restrict__ xl = reinterpret_cast<const uint4*>(xlo + (size_t)xr * H) + kb + 8 * s0;
+  kh_f32x4 ca0 = {0, 0, 0, 0}, ca1 = ca0, cb0 = ca0, cb1 = ca0;
+  if (live) {
+    uint4 ba[kMfDepth][2], bb[kMfDepth][2], bh[kMfDepth][2], bl[kMfDepth][2];
+    auto load = [&](int d, int st) {  // clamped, unconditional (past the end: reread, unused)
+      const int o = 8 * min(st, qsteps - 1);
+      ba[d][0] = wa[o]; ba[d][1] = wa[o + 4];
+      bb[d][0] = wb[o]; bb[d][1] = wb[o + 4];
+      bh[d][0] = xh[o]; bh[d][1] = xh[o + 4];
+      bl[d][0] = xl[o]; bl[d][1] = xl[o + 4];
+    };
+#pragma unroll
+    for (int d = 0; d < kMfDepth; ++d) load(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+    // qsteps is a multiple of kMfDepth (host-checked): no test inside the loop
+    for (int st = 0; st < qsteps; st += kMfDepth) {
+#pragma unroll
+      for (int d = 0; d < kMfDepth; ++d) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          ca0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ba[d][e]), as_bf16x8(bh[d][e]), ca0, 0, 0, 0);
+          ca1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ba[d][e]), as_bf16x8(bl[d][e]), ca1, 0, 0, 0);
+          cb0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bb[d][e]), as_bf16x8(bh[d][e]), cb0, 0, 0, 0);
+          cb1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bb[d][e]), as_bf16x8(bl[d][e]), cb1, 0, 0, 0);
+        }
+        load(d, st + d + kMfDepth);
+        // keep the prefetch here: the scheduler would otherwise sink it to its use
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  // C[row][token]: lane holds rows 4 kb + q (q = 0..3) of each tile, token r
+  if (qtr > 0) {
+    part[grp][qtr - 1][0][lane] = ca0;
+    part[grp][qtr - 1][1][lane] = ca1;
+    part[grp][qtr - 1][2][lane] = cb0;
+    part[grp][qtr - 1][3][lane] = cb1;
+  }
+  __syncthreads();
+  if (qtr > 0 || !live) return;
+  kh_f32x4 ta = ca0 + ca1, tb = cb0 + cb1;
+#pragma unroll
+  for (int j = 0; j < kMfSplit - 1; ++j) {
+    ta += part[grp][j][0][lane] + part[grp][j][1][lane];
+    tb += part[grp][j][2][lane] + part[grp][j][3][lane];
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int item = base + 4 * kb + q;
+    if (r < batch && item < rows) y[(size_t)r * ystride + item] = ta[q];
+    if (r < batch && item + 16 < rows) y[(size_t)r * ystride + item + 16] = tb[q];
   }
 }
 
@@ -623,6 +729,7 @@ struct kh_sparse_attn {
   float* y = nullptr;        // [max_batch][2*kvd + nh*d]
   float* cat = nullptr;      // [max_batch][nh*d]
   int32_t* qrows = nullptr;  // [nh*d + 1 + nh]: rows, their count, union rank per head (-1: none)
+  uint16_t* xsplit = nullptr;  // [2][16][hidden] BF16 hi / lo terms of x (max_batch > 1)
   std::vector<int64_t> len_host;
   Scratch po, pml, partial;
   int kvd() const { return nkv * d; }
@@ -643,6 +750,7 @@ extern "C" int kh_sparse_attn_destroy(kh_sparse_attn* a) {
   dev_free(a->y);
   dev_free(a->cat);
   dev_free(a->qrows);
+  dev_free(a->xsplit);
   delete a;
   return KH_OK;
 }
@@ -685,8 +793,9 @@ static int attn_alloc(int hidden, int num_heads, int num_kv_heads, int head_dim,
   a->y = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * a->ystride()));
   a->cat = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * qd));
   a->qrows = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * (qd + 1 + num_heads)));
+  if (max_batch > 1) a->xsplit = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * 2 * 16 * H));
   if (!a->wkvq || !a->wot || !a->kc || !a->vc || !a->cos_t || !a->sin_t || !a->lens || !a->y ||
-      !a->cat || !a->qrows) {
+      !a->cat || !a->qrows || (max_batch > 1 && !a->xsplit)) {
     kh_sparse_attn_destroy(a);
     return KH_ERR_ALLOC;
   }
@@ -921,23 +1030,36 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
                        hipStream_t st) {
   const int H = a->hidden, D = a->d, qd = a->nh * D, kvrows = 2 * a->kvd();
   // 1. projections (+ the o_proj row list in the last block)
-  static bool attr_set = false;
-  if (!attr_set) {
-    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_qkv_kernel<NB>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
-    attr_set = true;
-  }
-  const size_t lds = std::max(sizeof(float) * std::min(NB, kQkvTok) * H,
-                              2 * sizeof(int) * (size_t)a->nh);
-  if (lds > (size_t)kMaxDynLds) {
-    set_error("hidden %d too large to stage %d tokens", H, std::min(NB, kQkvTok));
-    return KH_ERR_UNSUPPORTED;
-  }
   const int rows = kvrows + qd;
-  hipLaunchKernelGGL(attn_qkv_kernel<NB>, dim3(rows / kQkvWaves + 1), dim3(64 * kQkvWaves), lds,
-                     st, a->wkvq, x, batch, H, kvrows, D, a->nh, heads, nsel, a->y, a->ystride(),
-                     a->qrows, a->qrows + qd, a->qrows + qd + 1);
-  KH_LAUNCHED();
+  if (NB > 1 && a->xsplit && H % (64 * kMfSplit * kMfDepth) == 0) {
+    uint16_t* xhi = a->xsplit;
+    uint16_t* xlo = a->xsplit + 16 * (size_t)H;
+    hipLaunchKernelGGL(xsplit_kernel<>, dim3(ceil_div(16 * H, 256)), dim3(256), 0, st, x, batch,
+                       H, xhi, xlo);
+    KH_LAUNCHED();
+    hipLaunchKernelGGL(attn_qkv_mfma_kernel, dim3(ceil_div(rows, 32 * (kMfWaves / kMfSplit)) + 1),
+                       dim3(64 * kMfWaves), 0, st, a->wkvq, xhi, xlo, batch, H, kvrows, rows, D,
+                       a->nh, heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
+                       a->qrows + qd + 1);
+    KH_LAUNCHED();
+  } else {
+    static bool attr_set = false;
+    if (!attr_set) {
+      KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_qkv_kernel<NB>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+      attr_set = true;
+    }
+    const size_t lds = std::max(sizeof(float) * std::min(NB, kQkvTok) * H,
+                                2 * sizeof(int) * (size_t)a->nh);
+    if (lds > (size_t)kMaxDynLds) {
+      set_error("hidden %d too large to stage %d tokens", H, std::min(NB, kQkvTok));
+      return KH_ERR_UNSUPPORTED;
+    }
+    hipLaunchKernelGGL(attn_qkv_kernel<NB>, dim3(rows / kQkvWaves + 1), dim3(64 * kQkvWaves), lds,
+                       st, a->wkvq, x, batch, H, kvrows, D, a->nh, heads, nsel, a->y, a->ystride(),
+                       a->qrows, a->qrows + qd, a->qrows + qd + 1);
+    KH_LAUNCHED();
+  }
   // 2. split-K decode over the cache and the K/V append (then, for batch > 2 or head
   //    lists longer than kOprojMaxSel, the merge of each head's chunks)
   const int chunk = attn_chunk_of(a->kv_f32, D);

@@ -30,6 +30,7 @@
 #include <cstring>
 
 #include "gather.hpp"
+#include "mfma.hpp"
 
 namespace kh {
 
@@ -127,28 +128,6 @@ __global__ __launch_bounds__(64 * kGuWaves) void ffn_gateup_kernel(
 // split k in quarters for each 16 rows (more loads in flight, twice the
 // blocks); the first adds the others' accumulators through LDS in a fixed
 // order, so results are deterministic.
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 kh_bf16x8;
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float kh_f32x4;
-
-constexpr int kMfSplit = 4;   // waves sharing one 16-row group (k quarters)
-constexpr int kMfWaves = 8;   // 2 row groups of 16 per block
-constexpr int kMfDepth = 4;   // k-steps of loads in flight per wave
-
-__device__ __forceinline__ kh_bf16x8 as_bf16x8(const uint4& v) {
-  return __builtin_bit_cast(kh_bf16x8, v);
-}
-
-// x [batch][H] f32 -> hi, lo [16][H] BF16 bits; rows >= batch are zero.
-__global__ void ffn_xsplit_kernel(const float* __restrict__ x, int batch, int H,
-                                  uint16_t* __restrict__ hi, uint16_t* __restrict__ lo) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= 16LL * H) return;
-  const float v = i / H < batch ? x[i] : 0.0f;
-  const uint16_t h = f32_to_bf16(v);
-  hi[i] = h;
-  lo[i] = f32_to_bf16(v - bf16_to_f32(h));  // exact difference
-}
-
 __global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
     const uint16_t* __restrict__ Wgu, const uint16_t* __restrict__ xhi,
     const uint16_t* __restrict__ xlo, int batch, int H, const int32_t* __restrict__ active,
@@ -167,8 +146,11 @@ __global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
   const int s0 = qtr * qsteps;
   const uint4* __restrict__ g = reinterpret_cast<const uint4*>(Wgu + (size_t)neuron * 2 * H) + kb + 8 * s0;
   const uint4* __restrict__ u = g + (H >> 3);
-  const uint4* __restrict__ xh = reinterpret_cast<const uint4*>(xhi + (size_t)r * H) + kb + 8 * s0;
-  const uint4* __restrict__ xl = reinterpret_cast<const uint4*>(xlo + (size_t)r * H) + kb + 8 * s0;
+  // tokens past the batch re-read the last token's row (the same cache lines,
+  // so no extra traffic); their results are never written
+  const int xr = min(r, batch - 1);
+  const uint4* __restrict__ xh = reinterpret_cast<const uint4*>(xhi + (size_t)xr * H) + kb + 8 * s0;
+  const uint4* __restrict__ xl = reinterpret_cast<const uint4*>(xlo + (size_t)xr * H) + kb + 8 * s0;
   kh_f32x4 cg0 = {0, 0, 0, 0}, cg1 = cg0, cu0 = cg0, cu1 = cg0;
   if (live) {
     uint4 bg[kMfDepth][2], bu[kMfDepth][2], bh[kMfDepth][2], bl[kMfDepth][2];
@@ -548,7 +530,7 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
     // several tokens: gate/up as 16 x 16 tile products on MFMA
     uint16_t* xhi = f->xsplit;
     uint16_t* xlo = f->xsplit + 16 * (size_t)H;
-    hipLaunchKernelGGL(ffn_xsplit_kernel, dim3(ceil_div(16 * H, 256)), dim3(256), 0, st, x, batch, H,
+    hipLaunchKernelGGL(xsplit_kernel<>, dim3(ceil_div(16 * H, 256)), dim3(256), 0, st, x, batch, H,
                        xhi, xlo);
     KH_LAUNCHED();
     hipLaunchKernelGGL(ffn_gateup_mfma_kernel, dim3(ceil_div(n_active, 16 * (kMfWaves / kMfSplit))),

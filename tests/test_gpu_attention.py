@@ -165,10 +165,11 @@ def test_accumulate_and_explicit_positions(kh, orc):
 def test_long_context_and_duplicates(kh, orc, batch):
     """More than 16 cache chunks per head (head_dim 256: 64 positions per
     chunk) and repeated heads, with the chunks merged inside the o_proj kernel
-    (batch <= 2) and by the separate merge kernel (batch > 2)."""
+    (batch <= 2) and by the separate merge kernel (batch > 2); hidden 1024
+    puts the batched q/k/v projections on the matrix cores."""
     rng = np.random.default_rng(77 + batch)
-    c = Case(orc, rng, 512, 4, 2, 256, 1400, batch, [1300 - 40 * b for b in range(batch)])
-    x = rng.standard_normal((batch, 512)).astype(np.float32)
+    c = Case(orc, rng, 1024, 4, 2, 256, 1400, batch, [1300 - 40 * b for b in range(batch)])
+    x = rng.standard_normal((batch, 1024)).astype(np.float32)
     heads = [[(b + 2) % 4, b % 4, (b + 2) % 4] for b in range(batch)]
     got = c.attn.forward_sparse(x, heads).cpu().numpy()
     for b in range(batch):
