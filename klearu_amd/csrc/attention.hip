@@ -185,20 +185,25 @@ __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
 }
 
 // Batched q/k/v projections (2..16 tokens) on the matrix cores: the K and V
-// rows and the Q rows of heads that some token selected, in groups of 32 rows
-// (two 16-row tiles per wave sharing the x operand), computed as
-// ffn_gateup_mfma_kernel computes its rows (x split into BF16 hi/lo terms, k
-// in quarters over four waves whose sums are added in a fixed order).  The
-// last block writes the o_proj row list as attn_qkv_kernel does.
-__global__ __launch_bounds__(64 * kMfWaves) void attn_qkv_mfma_kernel(
+// rows and the Q rows of heads that some token selected, 64 rows per block
+// (four 16-row tiles per wave sharing the x operand), each of the 8 waves
+// taking one eighth of k; x is split into BF16 hi/lo terms as for the batched
+// FFN, and the eighths are added in a fixed order through LDS.  The last
+// block writes the o_proj row list as attn_qkv_kernel does.
+constexpr int kQmTiles = 4;                  // 16-row tiles per wave
+constexpr int kQmSplit = 8;                  // waves per block, one k-eighth each
+constexpr int kQmDepth = 2;                  // k-steps of loads in flight per wave
+constexpr int kQmRows = 16 * kQmTiles;       // rows per block
+constexpr int kQmAlign = 64 * kQmSplit * kQmDepth;  // hidden must be a multiple
+__global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ xhi,
     const uint16_t* __restrict__ xlo, int batch, int H, int kvrows, int rows, int D, int nh,
     const int32_t* __restrict__ heads, int nsel, float* __restrict__ y, int ystride,
     int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows, int32_t* __restrict__ urank) {
-  constexpr int kGroups = kMfWaves / kMfSplit;
-  __shared__ kh_f32x4 part[kGroups][kMfSplit - 1][4][64];
+  constexpr int T = kQmTiles, S = kQmSplit, DEP = kQmDepth;
+  __shared__ kh_f32x4 part[S - 1][2 * T][64];
   __shared__ int s_flag[kMaxAttnHeads], s_uh[kMaxAttnHeads];
-  __shared__ int wsum[kMfWaves];
+  __shared__ int wsum[S];
   __shared__ int s_total;
   const int nent = batch * nsel;
   if (blockIdx.x == gridDim.x - 1) {
@@ -206,78 +211,82 @@ __global__ __launch_bounds__(64 * kMfWaves) void attn_qkv_mfma_kernel(
     return;
   }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int grp = wave / kMfSplit, qtr = wave % kMfSplit;
-  const int base = (blockIdx.x * kGroups + grp) * 32;
+  const int base = blockIdx.x * kQmRows;
   bool live = base < rows;
   if (live && base >= kvrows) {
-    // Q rows of head h (D is a multiple of 32): skipped unless some token selected h
+    // Q rows of head h (D is a multiple of 64): skipped unless some token selected h
     const int h = (base - kvrows) / D;
     int any = 0;
     for (int i = lane; i < nent; i += 64) any |= heads[i] == h;
     live = __ballot(any) != 0;
   }
   const int r = lane & 15, kb = lane >> 4;
-  const int qsteps = H / (64 * kMfSplit);  // k-steps per quarter
-  const int s0 = qtr * qsteps;
-  const uint4* __restrict__ wa =
-      reinterpret_cast<const uint4*>(W + (size_t)min(base + r, rows - 1) * H) + kb + 8 * s0;
-  const uint4* __restrict__ wb =
-      reinterpret_cast<const uint4*>(W + (size_t)min(base + 16 + r, rows - 1) * H) + kb + 8 * s0;
+  const int qsteps = H / (64 * S);  // k-steps per eighth
+  const int s0 = wave * qsteps;
+  const uint4* __restrict__ wp[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+    wp[t] = reinterpret_cast<const uint4*>(W + (size_t)min(base + 16 * t + r, rows - 1) * H) + kb + 8 * s0;
   // tokens past the batch re-read the last token's row (the same cache lines,
   // so no extra traffic); their results are never written
   const int xr = min(r, batch - 1);
   const uint4* __restrict__ xh = reinterpret_cast<const uint4*>(xhi + (size_t)xr * H) + kb + 8 * s0;
   const uint4* __restrict__ xl = reinterpret_cast<const uint4*>(xlo + (size_t)xr * H) + kb + 8 * s0;
-  kh_f32x4 ca0 = {0, 0, 0, 0}, ca1 = ca0, cb0 = ca0, cb1 = ca0;
+  kh_f32x4 c[T][2];
+#pragma unroll
+  for (int t = 0; t < T; ++t) c[t][0] = c[t][1] = kh_f32x4{0, 0, 0, 0};
   if (live) {
-    uint4 ba[kMfDepth][2], bb[kMfDepth][2], bh[kMfDepth][2], bl[kMfDepth][2];
+    uint4 bw[DEP][T][2], bh[DEP][2], bl[DEP][2];
     auto load = [&](int d, int st) {  // clamped, unconditional (past the end: reread, unused)
       const int o = 8 * min(st, qsteps - 1);
-      ba[d][0] = wa[o]; ba[d][1] = wa[o + 4];
-      bb[d][0] = wb[o]; bb[d][1] = wb[o + 4];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        bw[d][t][0] = wp[t][o];
+        bw[d][t][1] = wp[t][o + 4];
+      }
       bh[d][0] = xh[o]; bh[d][1] = xh[o + 4];
       bl[d][0] = xl[o]; bl[d][1] = xl[o + 4];
     };
 #pragma unroll
-    for (int d = 0; d < kMfDepth; ++d) load(d, d);
+    for (int d = 0; d < DEP; ++d) load(d, d);
     __builtin_amdgcn_sched_barrier(0);
-    // qsteps is a multiple of kMfDepth (host-checked): no test inside the loop
-    for (int st = 0; st < qsteps; st += kMfDepth) {
+    // qsteps is a multiple of DEP (host-checked): no test inside the loop
+    for (int st = 0; st < qsteps; st += DEP) {
 #pragma unroll
-      for (int d = 0; d < kMfDepth; ++d) {
+      for (int d = 0; d < DEP; ++d) {
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          ca0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ba[d][e]), as_bf16x8(bh[d][e]), ca0, 0, 0, 0);
-          ca1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ba[d][e]), as_bf16x8(bl[d][e]), ca1, 0, 0, 0);
-          cb0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bb[d][e]), as_bf16x8(bh[d][e]), cb0, 0, 0, 0);
-          cb1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bb[d][e]), as_bf16x8(bl[d][e]), cb1, 0, 0, 0);
-        }
-        load(d, st + d + kMfDepth);
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            c[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bw[d][t][e]), as_bf16x8(bh[d][e]), c[t][0], 0, 0, 0);
+            c[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bw[d][t][e]), as_bf16x8(bl[d][e]), c[t][1], 0, 0, 0);
+          }
+        load(d, st + d + DEP);
         // keep the prefetch here: the scheduler would otherwise sink it to its use
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
-  // C[row][token]: lane holds rows 4 kb + q (q = 0..3) of each tile, token r
-  if (qtr > 0) {
-    part[grp][qtr - 1][0][lane] = ca0;
-    part[grp][qtr - 1][1][lane] = ca1;
-    part[grp][qtr - 1][2][lane] = cb0;
-    part[grp][qtr - 1][3][lane] = cb1;
+  // C[row][token]: lane holds rows 16 t + 4 kb + q (q = 0..3) of token r
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      part[wave - 1][2 * t][lane] = c[t][0];
+      part[wave - 1][2 * t + 1][lane] = c[t][1];
+    }
   }
   __syncthreads();
-  if (qtr > 0 || !live) return;
-  kh_f32x4 ta = ca0 + ca1, tb = cb0 + cb1;
+  if (wave > 0 || !live) return;
 #pragma unroll
-  for (int j = 0; j < kMfSplit - 1; ++j) {
-    ta += part[grp][j][0][lane] + part[grp][j][1][lane];
-    tb += part[grp][j][2][lane] + part[grp][j][3][lane];
-  }
+  for (int t = 0; t < T; ++t) {
+    kh_f32x4 acc = c[t][0] + c[t][1];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int item = base + 4 * kb + q;
-    if (r < batch && item < rows) y[(size_t)r * ystride + item] = ta[q];
-    if (r < batch && item + 16 < rows) y[(size_t)r * ystride + item + 16] = tb[q];
+    for (int j = 0; j < S - 1; ++j) acc += part[j][2 * t][lane] + part[j][2 * t + 1][lane];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int item = base + 16 * t + 4 * kb + q;
+      if (r < batch && item < rows) y[(size_t)r * ystride + item] = acc[q];
+    }
   }
 }
 
@@ -1031,14 +1040,14 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   const int H = a->hidden, D = a->d, qd = a->nh * D, kvrows = 2 * a->kvd();
   // 1. projections (+ the o_proj row list in the last block)
   const int rows = kvrows + qd;
-  if (NB > 1 && a->xsplit && H % (64 * kMfSplit * kMfDepth) == 0) {
+  if (NB > 1 && a->xsplit && H % kQmAlign == 0) {
     uint16_t* xhi = a->xsplit;
     uint16_t* xlo = a->xsplit + 16 * (size_t)H;
     hipLaunchKernelGGL(xsplit_kernel<>, dim3(ceil_div(16 * H, 256)), dim3(256), 0, st, x, batch,
                        H, xhi, xlo);
     KH_LAUNCHED();
-    hipLaunchKernelGGL(attn_qkv_mfma_kernel, dim3(ceil_div(rows, 32 * (kMfWaves / kMfSplit)) + 1),
-                       dim3(64 * kMfWaves), 0, st, a->wkvq, xhi, xlo, batch, H, kvrows, rows, D,
+    hipLaunchKernelGGL(attn_qkv_mfma_kernel, dim3(ceil_div(rows, kQmRows) + 1),
+                       dim3(64 * kQmSplit), 0, st, a->wkvq, xhi, xlo, batch, H, kvrows, rows, D,
                        a->nh, heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
                        a->qrows + qd + 1);
     KH_LAUNCHED();
