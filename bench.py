@@ -253,9 +253,18 @@ def attn_leg(name, L, B, steps, warmup, seed, timer, cpu_seconds):
     hidden = torch.randn(B, H, generator=g, device="cuda")
     norm = torch.empty_like(hidden)
     heads = [torch.empty(B, k, dtype=torch.int32, device="cuda") for _ in range(L)]
+    stats = torch.empty(B, (H + 63) // 64, dtype=torch.float32, device="cuda")
 
     def step():
         st = stream_ptr()
+        if B == 1:
+            # fused block: the RmsNorm runs inside the predictor and q/k/v kernels
+            # from per-block sums of squares that each block hands to the next
+            _lib.call("kh_rms_stats", ptr(hidden), 1, H, ptr(stats), st)
+            for l in range(L):
+                _lib.call("kh_dejavu_attn_block", preds[l]._h, layers[l]._h, ptr(hidden), ptr(w_norm), 1e-5, k,
+                          ptr(heads[l]), ptr(stats), st)
+            return
         for l in range(L):
             _lib.call("kh_rmsnorm", ptr(hidden), ptr(w_norm), B, H, 1e-5, ptr(norm), st)
             _lib.call("kh_predictor_select_top_k", preds[l]._h, ptr(norm), B, k, ORDER_ASCENDING, ptr(heads[l]), st)

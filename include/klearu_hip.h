@@ -401,6 +401,23 @@ int kh_sparse_attn_forward(kh_sparse_attn* a, const float* x_dev, int64_t batch,
                            const int64_t* pos_dev, const int32_t* heads_dev, int n_heads,
                            float* out_dev, int accumulate, void* stream);
 
+/* One decode step (batch 1, sequence 0) of the attention half of a sparse
+ * decoder layer as SparseModel::forward_decode_sparse runs it
+ * (crates/klearu-llm/src/sparse/mod.rs:56-112):
+ *   norm = RmsNorm(hidden) (model/rms_norm.rs:43-64, weight norm_w, eps);
+ *   heads = predictor.select_top_k(norm, k) (PredictorStore::predict_heads,
+ *           sparse/predictor_store.rs:38-45; ascending ids into heads_dev[k]);
+ *   hidden += sparse_attention::forward_sparse(norm, position = cache length, heads).
+ * The norm is applied inside the predictor and q/k/v kernels from stats_dev
+ * (hidden/64 sums of squares of the current hidden row, from kh_rms_stats or
+ * the previous block); on return stats_dev holds those of the updated row, so
+ * it chains with kh_dejavu_mlp_block without a separate norm pass.  Requires
+ * predictor input_dim == hidden, output_dim == num_heads, hidden a multiple of
+ * 64 and at most 4096.  Returns KH_ERR_CAPACITY when the cache is full. */
+int kh_dejavu_attn_block(const kh_predictor* p, kh_sparse_attn* a, float* hidden_dev,
+                         const float* norm_w_dev, float eps, int k, int32_t* heads_dev,
+                         float* stats_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -112,12 +112,15 @@ __device__ void qkv_plan(const int32_t* __restrict__ heads, int nent, int nh, in
 
 // y[b][row] = Wkvq[row] . x[b] for the K/V rows and the Q rows of selected
 // heads.  The grid has one extra (last) block that writes the o_proj row list.
-template <int NB>
+// NORM (batch 1): x is the un-normalised hidden row and RmsNorm (weight nw) is
+// applied while staging it, from the row's per-64-column sums of squares.
+template <int NB, bool NORM = false>
 __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
     const uint16_t* __restrict__ W, const float* __restrict__ x, int batch, int H, int kvrows,
     int D, int nh, const int32_t* __restrict__ heads, int nsel, float* __restrict__ y,
     int ystride, int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows,
-    int32_t* __restrict__ urank) {
+    int32_t* __restrict__ urank, const float* __restrict__ nw, const float* __restrict__ stats,
+    int nparts, float eps) {
   extern __shared__ float4 xs4[];  // [kQkvTok][H/4]; the plan block's flags / union list
   __shared__ int wsum[kQkvWaves];
   __shared__ int s_total;
@@ -140,6 +143,57 @@ __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
   const uint4* __restrict__ w = reinterpret_cast<const uint4*>(W + (size_t)row * H);
   const int nchunk = H >> 3, H4 = H >> 2;
   constexpr int TB = NB < kQkvTok ? NB : kQkvTok;
+  if constexpr (NORM) {
+    // One token, H <= 4096 (one pass, no loop): the row, the norm weights and
+    // the statistics are requested first, then the weight row; the norm is
+    // formed while the weights stream in (loads complete in issue order).
+    constexpr int kXq = 4096 / 4 / (64 * kQkvWaves);
+    float4 xv[kXq], wn[kXq];
+#pragma unroll
+    for (int q = 0; q < kXq; ++q) {
+      const int i = min((int)threadIdx.x + q * 64 * kQkvWaves, H4 - 1);
+      xv[q] = reinterpret_cast<const float4*>(x)[i];
+      wn[q] = reinterpret_cast<const float4*>(nw)[i];
+    }
+    // nparts = H/64 <= 64: one statistic per lane, one clamped load (no branch)
+    const float stv = stats[min(lane, nparts - 1)];
+    uint4 wv[kQkvChunks];
+#pragma unroll
+    for (int q = 0; q < kQkvChunks; ++q) wv[q] = w[min(lane + 64 * q, nchunk - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    // RmsNorm (model/rms_norm.rs:56-60): (x * inv) * w
+    const float inv = rms_inv_part(lane < nparts ? 0.0f + stv : 0.0f, H, eps);
+#pragma unroll
+    for (int q = 0; q < kXq; ++q) {
+      float4 v = xv[q];
+      v.x = (v.x * inv) * wn[q].x;
+      v.y = (v.y * inv) * wn[q].y;
+      v.z = (v.z * inv) * wn[q].z;
+      v.w = (v.w * inv) * wn[q].w;
+      xs4[min((int)threadIdx.x + q * 64 * kQkvWaves, H4 - 1)] = v;  // clamped (see stage_f4)
+    }
+    lds_barrier();
+    // branch-free (a branch here lets the compiler sink each weight load to its
+    // use): chunks past the row add zero weights times a valid x
+    float a = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kQkvChunks; ++q) {
+      const int c = lane + 64 * q;
+      const int cc = min(c, nchunk - 1);
+      float wf[8];
+      widen16(wv[q], wf, uint16_t());
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wf[e] = c < nchunk ? wf[e] : 0.0f;
+      const float4 x0 = xs4[2 * cc], x1 = xs4[2 * cc + 1];
+      a = fmaf(wf[0], x0.x, a); a = fmaf(wf[1], x0.y, a);
+      a = fmaf(wf[2], x0.z, a); a = fmaf(wf[3], x0.w, a);
+      a = fmaf(wf[4], x1.x, a); a = fmaf(wf[5], x1.y, a);
+      a = fmaf(wf[6], x1.z, a); a = fmaf(wf[7], x1.w, a);
+    }
+    const float sum = wave_sum(a);
+    if (lane == 0) y[row] = sum;
+    return;
+  }
   float acc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
@@ -1033,14 +1087,17 @@ static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
   return KH_OK;
 }
 
+// nrm.w set (batch 1 only): x is the un-normalised hidden row, normalised
+// inside the projection kernel; ss_out receives the output row's RmsNorm
+// statistics (per-64-column sums of squares) when set.
 template <int NB>
 static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64_t* pos,
                        const int32_t* heads, int nsel, float* out, int accumulate,
-                       hipStream_t st) {
+                       hipStream_t st, const NormIn& nrm = NormIn{}, float* ss_out = nullptr) {
   const int H = a->hidden, D = a->d, qd = a->nh * D, kvrows = 2 * a->kvd();
   // 1. projections (+ the o_proj row list in the last block)
   const int rows = kvrows + qd;
-  if (NB > 1 && a->xsplit && H % kQmAlign == 0) {
+  if (NB > 1 && a->xsplit && H % kQmAlign == 0 && !nrm.w) {
     uint16_t* xhi = a->xsplit;
     uint16_t* xlo = a->xsplit + 16 * (size_t)H;
     hipLaunchKernelGGL(xsplit_kernel<>, dim3(ceil_div(16 * H, 256)), dim3(256), 0, st, x, batch,
@@ -1056,6 +1113,8 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
     if (!attr_set) {
       KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_qkv_kernel<NB>),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+      KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_qkv_kernel<1, true>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
       attr_set = true;
     }
     const size_t lds = std::max(sizeof(float) * std::min(NB, kQkvTok) * H,
@@ -1064,9 +1123,16 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
       set_error("hidden %d too large to stage %d tokens", H, std::min(NB, kQkvTok));
       return KH_ERR_UNSUPPORTED;
     }
-    hipLaunchKernelGGL(attn_qkv_kernel<NB>, dim3(rows / kQkvWaves + 1), dim3(64 * kQkvWaves), lds,
-                       st, a->wkvq, x, batch, H, kvrows, D, a->nh, heads, nsel, a->y, a->ystride(),
-                       a->qrows, a->qrows + qd, a->qrows + qd + 1);
+    if (nrm.w && NB == 1)
+      hipLaunchKernelGGL((attn_qkv_kernel<1, true>), dim3(rows / kQkvWaves + 1),
+                         dim3(64 * kQkvWaves), lds, st, a->wkvq, x, batch, H, kvrows, D, a->nh,
+                         heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
+                         a->qrows + qd + 1, nrm.w, nrm.stats, nrm.nparts, nrm.eps);
+    else
+      hipLaunchKernelGGL(attn_qkv_kernel<NB>, dim3(rows / kQkvWaves + 1), dim3(64 * kQkvWaves),
+                         lds, st, a->wkvq, x, batch, H, kvrows, D, a->nh, heads, nsel, a->y,
+                         a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1, nullptr,
+                         nullptr, 0, 0.0f);
     KH_LAUNCHED();
   }
   // 2. split-K decode over the cache and the K/V append (then, for batch > 2 or head
@@ -1112,7 +1178,7 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   KH_LAUNCHED();
   hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch),
                      dim3(64 * kRedWaves), 0, st, partial, H, groups, out, accumulate, a->lens,
-                     a->max_seq, nullptr);
+                     a->max_seq, ss_out);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -1153,5 +1219,32 @@ extern "C" int kh_sparse_attn_forward(kh_sparse_attn* a, const float* x_dev, int
   }
   if (rc == KH_OK)
     for (int64_t i = 0; i < batch; ++i) a->len_host[i] += 1;
+  return rc;
+}
+
+extern "C" int kh_dejavu_attn_block(const kh_predictor* p, kh_sparse_attn* a, float* hidden_dev,
+                                    const float* norm_w_dev, float eps, int k, int32_t* heads_dev,
+                                    float* stats_dev, void* stream) {
+  KH_CHECK_ARG(p && a && hidden_dev && norm_w_dev && heads_dev && stats_dev, "null argument");
+  KH_CHECK_ARG(k >= 1 && k <= a->nh, "k %d not in [1,%d]", k, a->nh);
+  KH_CHECK_ARG(predictor_in_dim(p) == a->hidden && predictor_out_dim(p) == a->nh,
+               "predictor %d->%d does not match the attention (hidden %d, %d heads)",
+               predictor_in_dim(p), predictor_out_dim(p), a->hidden, a->nh);
+  KH_CHECK_ARG(a->hidden % 64 == 0 && a->hidden <= 4096,
+               "the fused block needs hidden <= 4096 and a multiple of 64 (got %d)", a->hidden);
+  if (a->len_host[0] >= a->max_seq) {
+    set_error("KV cache of sequence 0 is full (%d positions)", a->max_seq);
+    return KH_ERR_CAPACITY;
+  }
+  hipStream_t st = as_stream(stream);
+  NormIn nrm;
+  nrm.w = norm_w_dev;
+  nrm.stats = stats_dev;
+  nrm.nparts = a->hidden / 64;
+  nrm.eps = eps;
+  int rc = predictor_topk_normed(p, hidden_dev, k, heads_dev, nrm, st);
+  if (rc != KH_OK) return rc;
+  rc = attn_launch<1>(a, hidden_dev, 1, nullptr, heads_dev, k, hidden_dev, 1, st, nrm, stats_dev);
+  if (rc == KH_OK) a->len_host[0] += 1;
   return rc;
 }
