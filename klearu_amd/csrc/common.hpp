@@ -330,4 +330,13 @@ __device__ __forceinline__ void stage_f4(float4* __restrict__ dst, const float4*
 
 inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) / b); }
 
+// p[0..n) = v.  A kernel rather than hipMemsetAsync, so that callers may
+// capture it in a HIP graph.  (A template, so that each translation unit
+// including this header keeps its own copy.)
+template <int Unused = 0>
+__global__ void fill_f32_kernel(float* __restrict__ p, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
 }  // namespace kh

@@ -605,7 +605,11 @@ extern "C" int kh_sparse_ffn_forward(const kh_sparse_ffn* f, const float* x_dev,
                f->inter);
   hipStream_t st = as_stream(stream);
   if (n_active == 0) {
-    if (!accumulate) KH_HIP(hipMemsetAsync(y_dev, 0, sizeof(float) * batch * f->hidden, st));
+    if (!accumulate) {
+      const int64_t n = batch * f->hidden;
+      hipLaunchKernelGGL(fill_f32_kernel<>, dim3(ceil_div(n, 256)), dim3(256), 0, st, y_dev, n, 0.0f);
+      KH_LAUNCHED();
+    }
     return KH_OK;
   }
   KH_CHECK_ARG(active_dev != nullptr, "null active list");

@@ -35,13 +35,17 @@
 
 namespace kh {
 
-constexpr int kHashThreads = 256;
+constexpr int kHashThreads = 256;   // hash_sparse_kernel; hash_dense_kernel takes one plane per thread (<= 1024)
+constexpr int kHashBatch = 16;      // plane entries in flight per thread
 constexpr int kQueryThreads = 256;
 constexpr int kDirectIds = 12288;  // LDS counting when all ids are below this
+constexpr int kQueryBatch = 8;     // bucket entries in flight per thread
+constexpr int kMaxTables = 256;    // hash tables per index (one per query thread)
+static_assert(kQueryThreads == kMaxTables, "one table per query thread");
 constexpr int kMaxGather = 8192;   // L * cap limit of the sort path
 
 // ------------------------------------------------------------------ kernels
-__global__ __launch_bounds__(kHashThreads) void hash_dense_kernel(
+__global__ __launch_bounds__(1024) void hash_dense_kernel(
     const int32_t* __restrict__ off, const uint32_t* __restrict__ ent, int k, int L, int dim,
     const float* __restrict__ x, int64_t ldx, int64_t batch, uint32_t* __restrict__ codes,
     int x_in_lds) {
@@ -56,12 +60,20 @@ __global__ __launch_bounds__(kHashThreads) void hash_dense_kernel(
   const float* xv = x_in_lds ? xs : xr;
   const int P = L * k;
   for (int p = threadIdx.x; p < P; p += blockDim.x) {
+    // The plane's entries are requested kHashBatch at a time (clamped, so every
+    // load is in bounds) and then added in order: the sum stays sequential.
     float s = 0.0f;
     const int e1 = off[p + 1];
-    for (int e = off[p]; e < e1; ++e) {
-      const uint32_t v = ent[e];
-      const float xd = xv[v >> 1];
-      s = (v & 1u) ? __fsub_rn(s, xd) : __fadd_rn(s, xd);
+    for (int e0 = off[p]; e0 < e1; e0 += kHashBatch) {
+      uint32_t v[kHashBatch];
+#pragma unroll
+      for (int j = 0; j < kHashBatch; ++j) v[j] = ent[min(e0 + j, e1 - 1)];
+      float xd[kHashBatch];
+#pragma unroll
+      for (int j = 0; j < kHashBatch; ++j) xd[j] = xv[v[j] >> 1];
+#pragma unroll
+      for (int j = 0; j < kHashBatch; ++j)
+        if (e0 + j < e1) s = (v[j] & 1u) ? __fsub_rn(s, xd[j]) : __fadd_rn(s, xd[j]);
     }
     if (s >= 0.0f) atomicOr(&cw[p / k], 1u << (p % k));
   }
@@ -174,6 +186,23 @@ __global__ void index_clear_kernel(uint32_t* __restrict__ len, uint64_t* __restr
 }
 
 // One block per query row: unique bucket ids in ascending order with counts.
+__host__ __device__ constexpr int hash_threads(int planes) {
+  return planes >= 1024 ? 1024 : (planes <= 64 ? 64 : (planes + 63) / 64 * 64);
+}
+
+// Offset in `data` of entry i of the concatenated buckets (bstart: exclusive
+// scan of the L bucket lengths, bstart[L] = total; i < total).
+__device__ __forceinline__ size_t bucket_entry(const uint32_t* bstart, const uint32_t* bslot,
+                                               int L, int cap, uint32_t i) {
+  int lo = 0, hi = L;  // bstart[lo] <= i < bstart[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (bstart[mid] <= i) lo = mid;
+    else hi = mid;
+  }
+  return (size_t)bslot[lo] * cap + (i - bstart[lo]);
+}
+
 __global__ __launch_bounds__(kQueryThreads) void query_kernel(
     const uint32_t* __restrict__ qcodes, int L, int k, int cap, const uint32_t* __restrict__ data,
     const uint32_t* __restrict__ len, uint32_t id_bound, int stride, uint32_t* __restrict__ out_ids,
@@ -181,30 +210,37 @@ __global__ __launch_bounds__(kQueryThreads) void query_kernel(
   extern __shared__ uint32_t sm[];
   __shared__ int wsum[kQueryThreads / 64];
   __shared__ int s_total;
-  __shared__ uint32_t bstart[65], bslot[64];
+  __shared__ uint32_t bstart[kMaxTables + 1], bslot[kMaxTables];
   const int64_t row = blockIdx.x;
   const uint32_t mask = (1u << k) - 1u;
   uint32_t* oids = out_ids + row * (int64_t)stride;
   uint32_t* ocnt = out_cnt ? out_cnt + row * (int64_t)stride : nullptr;
-  if (threadIdx.x == 0) {
-    uint32_t acc = 0;
-    for (int t = 0; t < L; ++t) {
-      const uint32_t slot = ((uint32_t)t << k) | (qcodes[row * L + t] & mask);
+  // bucket of each table (one per thread: L <= kMaxTables = blockDim) and the
+  // exclusive scan of the bucket lengths
+  {
+    const int t = threadIdx.x, tc = min(t, L - 1);
+    const uint32_t slot = ((uint32_t)tc << k) | (qcodes[row * L + tc] & mask);
+    const uint32_t n = len[slot];  // every thread reads a valid slot (table tc); used for t < L
+    const int excl = block_excl_scan(t < L ? (int)n : 0, wsum, &s_total);
+    if (t < L) {
       bslot[t] = slot;
-      bstart[t] = acc;
-      acc += len[slot];
+      bstart[t] = (uint32_t)excl;
     }
-    bstart[L] = acc;
+    if (t == 0) bstart[L] = (uint32_t)s_total;
   }
   __syncthreads();
   const uint32_t m = bstart[L];
   if (id_bound <= (uint32_t)kDirectIds) {
     for (uint32_t i = threadIdx.x; i < id_bound; i += blockDim.x) sm[i] = 0u;
     __syncthreads();
-    for (int t = 0; t < L; ++t) {
-      const uint32_t n = bstart[t + 1] - bstart[t];
-      const uint32_t* bd = data + (size_t)bslot[t] * cap;
-      for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) atomicAdd(&sm[bd[j]], 1u);
+    // every bucket entry of every table, kQueryBatch per thread in flight
+    for (uint32_t i0 = threadIdx.x; i0 < m; i0 += blockDim.x * kQueryBatch) {
+      uint32_t id[kQueryBatch];
+#pragma unroll
+      for (int q = 0; q < kQueryBatch; ++q) id[q] = data[bucket_entry(bstart, bslot, L, cap, min(i0 + q * blockDim.x, m - 1))];
+#pragma unroll
+      for (int q = 0; q < kQueryBatch; ++q)
+        if (i0 + q * blockDim.x < m) atomicAdd(&sm[id[q]], 1u);
     }
     __syncthreads();
     int base = 0;
@@ -224,10 +260,13 @@ __global__ __launch_bounds__(kQueryThreads) void query_kernel(
   // Sort path: gather, bitonic sort ascending, count runs.
   int P = 1;
   while (P < (int)m) P <<= 1;
-  for (int t = 0; t < L; ++t) {
-    const uint32_t n = bstart[t + 1] - bstart[t];
-    const uint32_t* bd = data + (size_t)bslot[t] * cap;
-    for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) sm[bstart[t] + j] = bd[j];
+  for (uint32_t i0 = threadIdx.x; i0 < m; i0 += blockDim.x * kQueryBatch) {
+    uint32_t id[kQueryBatch];
+#pragma unroll
+    for (int q = 0; q < kQueryBatch; ++q) id[q] = data[bucket_entry(bstart, bslot, L, cap, min(i0 + q * blockDim.x, m - 1))];
+#pragma unroll
+    for (int q = 0; q < kQueryBatch; ++q)
+      if (i0 + q * blockDim.x < m) sm[i0 + q * blockDim.x] = id[q];
   }
   for (int i = (int)m + threadIdx.x; i < P; i += blockDim.x) sm[i] = 0xffffffffu;
   __syncthreads();
@@ -308,7 +347,7 @@ int hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx, int6
   const size_t lds = sizeof(float) * (in_lds ? h->dim : 0) + sizeof(uint32_t) * h->L;
   for (int64_t b0 = 0; b0 < batch; b0 += 65535 * 16) {
     const int64_t nb = std::min<int64_t>(batch - b0, 65535 * 16);
-    hipLaunchKernelGGL(hash_dense_kernel, dim3((unsigned)nb), dim3(kHashThreads), lds, st,
+    hipLaunchKernelGGL(hash_dense_kernel, dim3((unsigned)nb), dim3(hash_threads(h->L * h->k)), lds, st,
                        h->csr_off, h->csr_ent, h->k, h->L, h->dim, x + b0 * ldx, ldx, nb,
                        codes + b0 * h->L, in_lds);
     KH_LAUNCHED();

@@ -209,6 +209,38 @@ def test_sparse_ffn_batch1_device_count(kh, orc, cnt_k):
     np.testing.assert_allclose(got, yr, rtol=RTOL, atol=1e-4 * max(float(np.max(np.abs(yr))), 1e-3))
 
 
+def test_sparse_ffn_empty_active_list(kh, orc):
+    """No active neurons: the output is zero (written by a fill kernel, so the
+    call stays capturable in a HIP graph), or left unchanged when accumulating;
+    the same inside a captured graph replayed several times."""
+    from klearu_amd.dejavu import Mlp
+    rng = np.random.default_rng(3)
+    H, I = 256, 512
+    wg, wu, wd, _, _ = _ffn_case(orc, rng, H, I, 4, 1)
+    mlp = Mlp(wg, wu, wd, max_batch=2)
+    x = torch.from_numpy(rng.standard_normal((2, H)).astype(np.float32)).cuda()
+    act = torch.zeros(1, dtype=torch.int32, device="cuda")
+    y = torch.full((2, H), 7.0, device="cuda")
+    mlp.forward_sparse_into(x, act, y, n_active=0)
+    assert torch.count_nonzero(y).item() == 0
+    y.fill_(3.0)
+    mlp.forward_sparse_into(x, act, y, accumulate=True, n_active=0)
+    assert torch.all(y == 3.0).item()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        mlp.forward_sparse_into(x, act, y, n_active=0, stream=s)   # sizes nothing; warm
+        s.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            mlp.forward_sparse_into(x, act, y, n_active=0, stream=s)
+    for _ in range(3):
+        y.fill_(5.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(y).item() == 0
+
+
 def test_sparse_ffn_rejects_bad_shapes(kh, orc):
     from klearu_amd import KlearuError
     from klearu_amd.dejavu import Mlp

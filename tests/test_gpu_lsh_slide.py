@@ -217,6 +217,31 @@ def test_query_large_ids_sort_path(kh, orc):
         np.testing.assert_array_equal(gc[off[b]:off[b + 1]], rc)
 
 
+@pytest.mark.parametrize("L,k,n", [(100, 4, 3000), (256, 3, 600), (200, 7, 20000)])
+def test_query_many_tables(kh, orc, L, k, n):
+    """More than 64 tables (up to the 256 an index may hold): dense hashing
+    with one plane per thread over more than 256 planes, and both query paths
+    (LDS counting below 12288 ids, sort-based dedup above)."""
+    from klearu_amd.lsh import SimHash
+    rng = np.random.default_rng(L + k)
+    fam = SimHash(96, k, L, 5 + L)
+    W = rng.normal(0, 0.01, (n, 96)).astype(np.float32)
+    idx, ref = build_pair(kh, orc, fam, FIFO, 16, W)
+    assert_buckets_equal(idx, ref)
+    X = rng.standard_normal((9, 96)).astype(np.float32)
+    np.testing.assert_array_equal(fam.hash_dense_batch(X).cpu().numpy().view(np.uint32),
+                                  orc.hash_dense_batch(fam.planes(), X))
+    off, gi, gc = idx.query_batch(X)
+    off = off.cpu().numpy()
+    gi = gi.cpu().numpy().view(np.uint32)
+    gc = gc.cpu().numpy().view(np.uint32)
+    codes = orc.hash_dense_batch(fam.planes(), X)
+    for b in range(9):
+        ri, rc = ref.query(codes[b])
+        np.testing.assert_array_equal(gi[off[b]:off[b + 1]], ri)
+        np.testing.assert_array_equal(gc[off[b]:off[b + 1]], rc)
+
+
 def test_query_sparse_and_capacity(kh, orc):
     from klearu_amd._lib import KlearuError
     from klearu_amd.lsh import SimHash
