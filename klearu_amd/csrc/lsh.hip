@@ -35,8 +35,9 @@
 
 namespace kh {
 
-constexpr int kHashThreads = 256;   // hash_sparse_kernel; hash_dense_kernel takes one plane per thread (<= 1024)
-constexpr int kHashBatch = 16;      // plane entries in flight per thread
+constexpr int kHashThreads = 256;   // hash_sparse_kernel
+constexpr int kHashBatch = 32;      // plane entries in flight per thread
+constexpr int kHashDenseMax = 512;  // hash_dense_kernel threads (one plane each; more planes loop)
 constexpr int kQueryThreads = 256;
 constexpr int kDirectIds = 12288;  // LDS counting when all ids are below this
 constexpr int kQueryBatch = 8;     // bucket entries in flight per thread
@@ -45,8 +46,8 @@ static_assert(kQueryThreads == kMaxTables, "one table per query thread");
 constexpr int kMaxGather = 8192;   // L * cap limit of the sort path
 
 // ------------------------------------------------------------------ kernels
-__global__ __launch_bounds__(1024) void hash_dense_kernel(
-    const int32_t* __restrict__ off, const uint32_t* __restrict__ ent, int k, int L, int dim,
+__global__ __launch_bounds__(kHashDenseMax) void hash_dense_kernel(
+    const int32_t* __restrict__ nnz, const uint32_t* __restrict__ ent_t, int k, int L, int dim,
     const float* __restrict__ x, int64_t ldx, int64_t batch, uint32_t* __restrict__ codes,
     int x_in_lds) {
   extern __shared__ float xs[];
@@ -60,14 +61,15 @@ __global__ __launch_bounds__(1024) void hash_dense_kernel(
   const float* xv = x_in_lds ? xs : xr;
   const int P = L * k;
   for (int p = threadIdx.x; p < P; p += blockDim.x) {
-    // The plane's entries are requested kHashBatch at a time (clamped, so every
-    // load is in bounds) and then added in order: the sum stays sequential.
+    // The plane's entries are requested kHashBatch at a time (the padded rows
+    // keep every load in bounds; lanes read adjacent planes, so each load is
+    // coalesced) and then added in order: the sum stays sequential.
     float s = 0.0f;
-    const int e1 = off[p + 1];
-    for (int e0 = off[p]; e0 < e1; e0 += kHashBatch) {
+    const int e1 = nnz[p];
+    for (int e0 = 0; e0 < e1; e0 += kHashBatch) {
       uint32_t v[kHashBatch];
 #pragma unroll
-      for (int j = 0; j < kHashBatch; ++j) v[j] = ent[min(e0 + j, e1 - 1)];
+      for (int j = 0; j < kHashBatch; ++j) v[j] = ent_t[(size_t)(e0 + j) * P + p];
       float xd[kHashBatch];
 #pragma unroll
       for (int j = 0; j < kHashBatch; ++j) xd[j] = xv[v[j] >> 1];
@@ -185,9 +187,9 @@ __global__ void index_clear_kernel(uint32_t* __restrict__ len, uint64_t* __restr
   }
 }
 
-// One block per query row: unique bucket ids in ascending order with counts.
+// Threads of a hash_dense_kernel block for `planes` planes (whole waves).
 __host__ __device__ constexpr int hash_threads(int planes) {
-  return planes >= 1024 ? 1024 : (planes <= 64 ? 64 : (planes + 63) / 64 * 64);
+  return planes >= kHashDenseMax ? kHashDenseMax : (planes <= 64 ? 64 : (planes + 63) / 64 * 64);
 }
 
 // Offset in `data` of entry i of the concatenated buckets (bstart: exclusive
@@ -203,6 +205,7 @@ __device__ __forceinline__ size_t bucket_entry(const uint32_t* bstart, const uin
   return (size_t)bslot[lo] * cap + (i - bstart[lo]);
 }
 
+// One block per query row: unique bucket ids in ascending order with counts.
 __global__ __launch_bounds__(kQueryThreads) void query_kernel(
     const uint32_t* __restrict__ qcodes, int L, int k, int cap, const uint32_t* __restrict__ data,
     const uint32_t* __restrict__ len, uint32_t id_bound, int stride, uint32_t* __restrict__ out_ids,
@@ -348,7 +351,7 @@ int hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx, int6
   for (int64_t b0 = 0; b0 < batch; b0 += 65535 * 16) {
     const int64_t nb = std::min<int64_t>(batch - b0, 65535 * 16);
     hipLaunchKernelGGL(hash_dense_kernel, dim3((unsigned)nb), dim3(hash_threads(h->L * h->k)), lds, st,
-                       h->csr_off, h->csr_ent, h->k, h->L, h->dim, x + b0 * ldx, ldx, nb,
+                       h->nnz, h->ent_t, h->k, h->L, h->dim, x + b0 * ldx, ldx, nb,
                        codes + b0 * h->L, in_lds);
     KH_LAUNCHED();
   }
@@ -420,26 +423,32 @@ using namespace kh;
 // ====================================================================== families
 static int family_finish(kh_hash_family* h, kh_hash_family** out) {
   const int P = h->L * h->k;
-  std::vector<int32_t> off(P + 1, 0);
-  std::vector<uint32_t> ent;
+  std::vector<int32_t> nnz(P, 0);
   for (int p = 0; p < P; ++p) {
     const int8_t* pl = h->planes_host.data() + (size_t)p * h->dim;
+    for (int d = 0; d < h->dim; ++d) nnz[p] += pl[d] != 0;
+  }
+  const int mx = P ? *std::max_element(nnz.begin(), nnz.end()) : 0;
+  h->ent_rows = std::max(kHashBatch, (mx + kHashBatch - 1) / kHashBatch * kHashBatch);
+  std::vector<uint32_t> ent((size_t)h->ent_rows * P, 0u);
+  for (int p = 0; p < P; ++p) {
+    const int8_t* pl = h->planes_host.data() + (size_t)p * h->dim;
+    size_t j = 0;
     for (int d = 0; d < h->dim; ++d) {
-      if (pl[d] == 1) ent.push_back((uint32_t)d << 1);
-      else if (pl[d] == -1) ent.push_back(((uint32_t)d << 1) | 1u);
+      if (pl[d] == 1) ent[j++ * P + p] = (uint32_t)d << 1;
+      else if (pl[d] == -1) ent[j++ * P + p] = ((uint32_t)d << 1) | 1u;
     }
-    off[p + 1] = (int32_t)ent.size();
   }
   h->planes_dev = static_cast<int8_t*>(dev_alloc(h->planes_host.size()));
-  h->csr_off = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * off.size()));
-  h->csr_ent = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * std::max<size_t>(ent.size(), 1)));
-  if (!h->planes_dev || !h->csr_off || !h->csr_ent) {
+  h->nnz = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * std::max(P, 1)));
+  h->ent_t = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * ent.size()));
+  if (!h->planes_dev || !h->nnz || !h->ent_t) {
     kh_hash_family_destroy(h);
     return KH_ERR_ALLOC;
   }
   if (hipMemcpy(h->planes_dev, h->planes_host.data(), h->planes_host.size(), hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemcpy(h->csr_off, off.data(), sizeof(int32_t) * off.size(), hipMemcpyHostToDevice) != hipSuccess ||
-      (ent.size() && hipMemcpy(h->csr_ent, ent.data(), sizeof(uint32_t) * ent.size(), hipMemcpyHostToDevice) != hipSuccess)) {
+      hipMemcpy(h->nnz, nnz.data(), sizeof(int32_t) * P, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(h->ent_t, ent.data(), sizeof(uint32_t) * ent.size(), hipMemcpyHostToDevice) != hipSuccess) {
     set_error("plane upload failed");
     kh_hash_family_destroy(h);
     return KH_ERR_HIP;
@@ -502,8 +511,8 @@ extern "C" int kh_hash_family_from_planes(int input_dim, int k, int num_tables,
 extern "C" int kh_hash_family_destroy(kh_hash_family* h) {
   if (!h) return KH_OK;
   dev_free(h->planes_dev);
-  dev_free(h->csr_off);
-  dev_free(h->csr_ent);
+  dev_free(h->nnz);
+  dev_free(h->ent_t);
   delete h;
   return KH_OK;
 }

@@ -8,8 +8,12 @@ struct kh_hash_family {
   int dim = 0, k = 0, L = 0;
   std::vector<int8_t> planes_host;  // [L][k][dim]
   int8_t* planes_dev = nullptr;     // [L*k][dim]
-  int32_t* csr_off = nullptr;       // [L*k + 1] nonzero lists per plane
-  uint32_t* csr_ent = nullptr;      // (dim << 1) | (sign < 0)
+  // Nonzero lists of the planes, transposed so that the planes handled by
+  // consecutive lanes are adjacent: entry j of plane p at ent_t[j*L*k + p],
+  // (dim << 1) | (sign < 0), in dimension order; rows past a plane's nnz are 0.
+  int32_t* nnz = nullptr;           // [L*k]
+  uint32_t* ent_t = nullptr;        // [ent_rows][L*k]
+  int ent_rows = 0;                 // max nnz rounded up to the hash kernel's batch
 };
 
 struct kh_lsh_index {
