@@ -249,6 +249,7 @@ __global__ __launch_bounds__(kSlideThreads) void neuron_kernel(
 }
 
 // Dense layer over CSR inputs: y[b][o] = act(sum_e val_e * W^T[idx_e][o] + bias[o]).
+constexpr int kChainBatch = 16;  // entries in flight per sequential sum
 __global__ __launch_bounds__(256) void dense_sparse_kernel(const float* __restrict__ WT, int n,
                                                            const float* __restrict__ bias,
                                                            const int64_t* __restrict__ xoff,
@@ -259,8 +260,24 @@ __global__ __launch_bounds__(256) void dense_sparse_kernel(const float* __restri
   const int o = blockIdx.x * blockDim.x + threadIdx.x;
   if (o >= n) return;
   const int64_t a = xoff[row], b = xoff[row + 1];
+  // kChainBatch entries at a time (indices, then the weight rows, all in
+  // flight), then added in order: the sum stays sequential
   float s = -0.0f;
-  for (int64_t e = a; e < b; ++e) s = __fadd_rn(s, __fmul_rn(xval[e], WT[(size_t)xidx[e] * n + o]));
+  for (int64_t e0 = a; e0 < b; e0 += kChainBatch) {
+    uint32_t ix[kChainBatch];
+    float xv[kChainBatch], wv[kChainBatch];
+#pragma unroll
+    for (int j = 0; j < kChainBatch; ++j) {
+      const int64_t e = min(e0 + j, b - 1);
+      ix[j] = xidx[e];
+      xv[j] = xval[e];
+    }
+#pragma unroll
+    for (int j = 0; j < kChainBatch; ++j) wv[j] = WT[(size_t)ix[j] * n + o];
+#pragma unroll
+    for (int j = 0; j < kChainBatch; ++j)
+      if (e0 + j < b) s = __fadd_rn(s, __fmul_rn(xv[j], wv[j]));
+  }
   const float z = __fadd_rn(s, bias[o]);
   float r;
   if (act == KH_ACT_RELU) r = fmaxf(z, 0.0f);
