@@ -63,6 +63,7 @@ struct Scratch {
 
 // ---------------------------------------------------------------- device helpers
 constexpr int kWave = 64;
+constexpr int kMaxDynLds = 152 * 1024;  // dynamic LDS ceiling (160 KB per CU minus static use)
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

@@ -13,7 +13,6 @@
 namespace kh {
 
 constexpr int kSlice = 256;             // output columns per gather block
-constexpr int kMaxDynLds = 152 * 1024;  // dynamic LDS ceiling (160 KB per CU minus static use)
 constexpr int kMaxGroups = 128;         // row groups per slice (partials)
 constexpr int kDownThreads = 256;
 

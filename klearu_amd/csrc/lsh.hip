@@ -38,12 +38,15 @@ namespace kh {
 constexpr int kHashThreads = 256;   // hash_sparse_kernel
 constexpr int kHashBatch = 32;      // plane entries in flight per thread
 constexpr int kHashDenseMax = 512;  // hash_dense_kernel threads (one plane each; more planes loop)
-constexpr int kQueryThreads = 256;
+constexpr int kQueryThreads = 256;      // query_direct_kernel
+constexpr int kQueryBigThreads = 1024;  // query_bitmap_kernel, query_sort_kernel
 constexpr int kDirectIds = 12288;  // LDS counting when all ids are below this
 constexpr int kQueryBatch = 8;     // bucket entries in flight per thread
 constexpr int kMaxTables = 256;    // hash tables per index (one per query thread)
-static_assert(kQueryThreads == kMaxTables, "one table per query thread");
-constexpr int kMaxGather = 8192;   // L * cap limit of the sort path
+static_assert(kQueryThreads >= kMaxTables && kQueryBigThreads >= kMaxTables,
+              "one table per query thread");
+constexpr int kMaxGather = 8192;   // L * cap limit of the bitmap and sort paths
+constexpr int kGroupWords = 8;     // bitmap words per group offset
 
 // ------------------------------------------------------------------ kernels
 __global__ __launch_bounds__(kHashDenseMax) void hash_dense_kernel(
@@ -205,8 +208,29 @@ __device__ __forceinline__ size_t bucket_entry(const uint32_t* bstart, const uin
   return (size_t)bslot[lo] * cap + (i - bstart[lo]);
 }
 
+// Bucket of each table (one per thread: L <= kMaxTables <= blockDim) and the
+// exclusive scan of the bucket lengths; returns the number of bucket entries.
+__device__ __forceinline__ uint32_t query_buckets(const uint32_t* __restrict__ qcodes, int64_t row,
+                                                  int L, int k, const uint32_t* __restrict__ len,
+                                                  uint32_t* bstart, uint32_t* bslot, int* wsum,
+                                                  int* s_total) {
+  const uint32_t mask = (1u << k) - 1u;
+  const int t = threadIdx.x, tc = min(t, L - 1);
+  const uint32_t slot = ((uint32_t)tc << k) | (qcodes[row * L + tc] & mask);
+  const uint32_t n = len[slot];  // every thread reads a valid slot (table tc); used for t < L
+  const int excl = block_excl_scan(t < L ? (int)n : 0, wsum, s_total);
+  if (t < L) {
+    bslot[t] = slot;
+    bstart[t] = (uint32_t)excl;
+  }
+  if (t == 0) bstart[L] = (uint32_t)*s_total;
+  __syncthreads();
+  return bstart[L];
+}
+
 // One block per query row: unique bucket ids in ascending order with counts.
-__global__ __launch_bounds__(kQueryThreads) void query_kernel(
+// Direct path (ids < kDirectIds): a count per id in LDS, then a scan.
+__global__ __launch_bounds__(kQueryThreads) void query_direct_kernel(
     const uint32_t* __restrict__ qcodes, int L, int k, int cap, const uint32_t* __restrict__ data,
     const uint32_t* __restrict__ len, uint32_t id_bound, int stride, uint32_t* __restrict__ out_ids,
     uint32_t* __restrict__ out_cnt, int32_t* __restrict__ out_len) {
@@ -215,52 +239,123 @@ __global__ __launch_bounds__(kQueryThreads) void query_kernel(
   __shared__ int s_total;
   __shared__ uint32_t bstart[kMaxTables + 1], bslot[kMaxTables];
   const int64_t row = blockIdx.x;
-  const uint32_t mask = (1u << k) - 1u;
   uint32_t* oids = out_ids + row * (int64_t)stride;
   uint32_t* ocnt = out_cnt ? out_cnt + row * (int64_t)stride : nullptr;
-  // bucket of each table (one per thread: L <= kMaxTables = blockDim) and the
-  // exclusive scan of the bucket lengths
-  {
-    const int t = threadIdx.x, tc = min(t, L - 1);
-    const uint32_t slot = ((uint32_t)tc << k) | (qcodes[row * L + tc] & mask);
-    const uint32_t n = len[slot];  // every thread reads a valid slot (table tc); used for t < L
-    const int excl = block_excl_scan(t < L ? (int)n : 0, wsum, &s_total);
-    if (t < L) {
-      bslot[t] = slot;
-      bstart[t] = (uint32_t)excl;
-    }
-    if (t == 0) bstart[L] = (uint32_t)s_total;
+  for (uint32_t i = threadIdx.x; i < id_bound; i += blockDim.x) sm[i] = 0u;
+  const uint32_t m = query_buckets(qcodes, row, L, k, len, bstart, bslot, wsum, &s_total);
+  // every bucket entry of every table, kQueryBatch per thread in flight
+  for (uint32_t i0 = threadIdx.x; i0 < m; i0 += blockDim.x * kQueryBatch) {
+    uint32_t id[kQueryBatch];
+#pragma unroll
+    for (int q = 0; q < kQueryBatch; ++q) id[q] = data[bucket_entry(bstart, bslot, L, cap, min(i0 + q * blockDim.x, m - 1))];
+#pragma unroll
+    for (int q = 0; q < kQueryBatch; ++q)
+      if (i0 + q * blockDim.x < m) atomicAdd(&sm[id[q]], 1u);
   }
   __syncthreads();
-  const uint32_t m = bstart[L];
-  if (id_bound <= (uint32_t)kDirectIds) {
-    for (uint32_t i = threadIdx.x; i < id_bound; i += blockDim.x) sm[i] = 0u;
-    __syncthreads();
-    // every bucket entry of every table, kQueryBatch per thread in flight
-    for (uint32_t i0 = threadIdx.x; i0 < m; i0 += blockDim.x * kQueryBatch) {
-      uint32_t id[kQueryBatch];
-#pragma unroll
-      for (int q = 0; q < kQueryBatch; ++q) id[q] = data[bucket_entry(bstart, bslot, L, cap, min(i0 + q * blockDim.x, m - 1))];
-#pragma unroll
-      for (int q = 0; q < kQueryBatch; ++q)
-        if (i0 + q * blockDim.x < m) atomicAdd(&sm[id[q]], 1u);
+  int base = 0;
+  for (uint32_t c0 = 0; c0 < id_bound; c0 += blockDim.x) {
+    const uint32_t i = c0 + threadIdx.x;
+    const uint32_t c = i < id_bound ? sm[i] : 0u;
+    const int pos = block_excl_scan(c ? 1 : 0, wsum, &s_total) + base;
+    if (c) {
+      oids[pos] = i;
+      if (ocnt) ocnt[pos] = c;
     }
-    __syncthreads();
-    int base = 0;
-    for (uint32_t c0 = 0; c0 < id_bound; c0 += blockDim.x) {
-      const uint32_t i = c0 + threadIdx.x;
-      const uint32_t c = i < id_bound ? sm[i] : 0u;
-      const int pos = block_excl_scan(c ? 1 : 0, wsum, &s_total) + base;
-      if (c) {
-        oids[pos] = i;
-        if (ocnt) ocnt[pos] = c;
-      }
-      base += s_total;
-    }
-    if (threadIdx.x == 0) out_len[row] = base;
-    return;
+    base += s_total;
   }
-  // Sort path: gather, bitonic sort ascending, count runs.
+  if (threadIdx.x == 0) out_len[row] = base;
+}
+
+// Bitmap path (when the LDS below fits in kMaxDynLds): one presence bit per id.  The
+// ids come out in ascending order from a scan of popcounts over groups of
+// kGroupWords words; an entry's output position (its rank) is its group's
+// offset plus the bits below it, so the counts are LDS increments at the rank.
+// LDS: bitmap [W] | group offsets [ceil(W / kGroupWords)] | counts [L * cap].
+__global__ __launch_bounds__(kQueryBigThreads) void query_bitmap_kernel(
+    const uint32_t* __restrict__ qcodes, int L, int k, int cap, const uint32_t* __restrict__ data,
+    const uint32_t* __restrict__ len, uint32_t id_bound, int stride, uint32_t* __restrict__ out_ids,
+    uint32_t* __restrict__ out_cnt, int32_t* __restrict__ out_len) {
+  extern __shared__ uint32_t sm[];
+  __shared__ int wsum[kQueryBigThreads / 64];
+  __shared__ int s_total;
+  __shared__ uint32_t bstart[kMaxTables + 1], bslot[kMaxTables];
+  const int64_t row = blockIdx.x;
+  uint32_t* oids = out_ids + row * (int64_t)stride;
+  uint32_t* ocnt = out_cnt ? out_cnt + row * (int64_t)stride : nullptr;
+  const int W = (int)((id_bound + 31u) >> 5);
+  const int G = (W + kGroupWords - 1) / kGroupWords;
+  uint32_t* bm = sm;
+  uint32_t* goff = sm + W;
+  uint32_t* cnt = goff + G;
+  for (int i = threadIdx.x; i < W; i += blockDim.x) bm[i] = 0u;
+  if (ocnt)
+    for (int i = threadIdx.x; i < L * cap; i += blockDim.x) cnt[i] = 0u;
+  const uint32_t m = query_buckets(qcodes, row, L, k, len, bstart, bslot, wsum, &s_total);
+  for (uint32_t i0 = threadIdx.x; i0 < m; i0 += blockDim.x * kQueryBatch) {
+    uint32_t id[kQueryBatch];
+#pragma unroll
+    for (int q = 0; q < kQueryBatch; ++q) id[q] = data[bucket_entry(bstart, bslot, L, cap, min(i0 + q * blockDim.x, m - 1))];
+#pragma unroll
+    for (int q = 0; q < kQueryBatch; ++q)
+      if (i0 + q * blockDim.x < m) atomicOr(&bm[id[q] >> 5], 1u << (id[q] & 31u));
+  }
+  __syncthreads();
+  int base = 0;
+  for (int g0 = 0; g0 < G; g0 += blockDim.x) {
+    const int g = g0 + threadIdx.x;
+    const int w0 = g * kGroupWords, w1 = min(w0 + kGroupWords, W);
+    int c = 0;
+    for (int w = w0; w < w1; ++w) c += __popc(bm[w]);
+    int pos = block_excl_scan(c, wsum, &s_total) + base;
+    if (g < G) {
+      goff[g] = (uint32_t)pos;
+      for (int w = w0; w < w1; ++w) {
+        uint32_t bits = bm[w];
+        while (bits) {
+          oids[pos++] = ((uint32_t)w << 5) | (uint32_t)(__ffs(bits) - 1);
+          bits &= bits - 1u;
+        }
+      }
+    }
+    base += s_total;
+  }
+  if (threadIdx.x == 0) out_len[row] = base;
+  if (!ocnt) return;
+  __syncthreads();
+  for (uint32_t i0 = threadIdx.x; i0 < m; i0 += blockDim.x * kQueryBatch) {
+    uint32_t id[kQueryBatch];
+#pragma unroll
+    for (int q = 0; q < kQueryBatch; ++q) id[q] = data[bucket_entry(bstart, bslot, L, cap, min(i0 + q * blockDim.x, m - 1))];
+#pragma unroll
+    for (int q = 0; q < kQueryBatch; ++q) {
+      if (i0 + q * blockDim.x < m) {
+        const int w = (int)(id[q] >> 5);
+        const int g = w / kGroupWords;
+        uint32_t r = goff[g];
+        for (int j = g * kGroupWords; j < w; ++j) r += __popc(bm[j]);
+        r += __popc(bm[w] & ((1u << (id[q] & 31u)) - 1u));
+        atomicAdd(&cnt[r], 1u);
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < base; i += blockDim.x) ocnt[i] = cnt[i];
+}
+
+// Sort path (any id): gather, bitonic sort ascending, count runs.
+__global__ __launch_bounds__(kQueryBigThreads) void query_sort_kernel(
+    const uint32_t* __restrict__ qcodes, int L, int k, int cap, const uint32_t* __restrict__ data,
+    const uint32_t* __restrict__ len, int stride, uint32_t* __restrict__ out_ids,
+    uint32_t* __restrict__ out_cnt, int32_t* __restrict__ out_len) {
+  extern __shared__ uint32_t sm[];
+  __shared__ int wsum[kQueryBigThreads / 64];
+  __shared__ int s_total;
+  __shared__ uint32_t bstart[kMaxTables + 1], bslot[kMaxTables];
+  const int64_t row = blockIdx.x;
+  uint32_t* oids = out_ids + row * (int64_t)stride;
+  uint32_t* ocnt = out_cnt ? out_cnt + row * (int64_t)stride : nullptr;
+  const uint32_t m = query_buckets(qcodes, row, L, k, len, bstart, bslot, wsum, &s_total);
   int P = 1;
   while (P < (int)m) P <<= 1;
   for (uint32_t i0 = threadIdx.x; i0 < m; i0 += blockDim.x * kQueryBatch) {
@@ -368,24 +463,46 @@ int hash_sparse_launch(const kh_hash_family* h, const int64_t* xoff, const uint3
   return KH_OK;
 }
 
+// LDS bytes of query_bitmap_kernel for ids < bound over L * cap entries.
+static size_t bitmap_lds(uint32_t bound, int gather) {
+  const size_t W = (bound + 31u) / 32u;
+  return sizeof(uint32_t) * (W + (W + kGroupWords - 1) / kGroupWords + (size_t)gather);
+}
+
 int query_launch(const kh_lsh_index* idx, const uint32_t* qcodes, int64_t batch, uint32_t* qids,
                  uint32_t* qcnt, int stride, int32_t* ulen, hipStream_t st) {
   if (batch == 0) return KH_OK;
   const uint32_t bound = idx->id_bound;
-  size_t lds;
   if (bound <= (uint32_t)kDirectIds) {
-    lds = sizeof(uint32_t) * std::max<uint32_t>(bound, 1);
-  } else {
-    KH_CHECK_ARG(idx->L * idx->cap <= kMaxGather,
-                 "query over ids >= %d needs L*cap <= %d (got %d)", kDirectIds, kMaxGather,
-                 idx->L * idx->cap);
-    int P = 1;
-    while (P < idx->L * idx->cap) P <<= 1;
-    lds = sizeof(uint32_t) * P;
+    const size_t lds = sizeof(uint32_t) * std::max<uint32_t>(bound, 1);
+    hipLaunchKernelGGL(query_direct_kernel, dim3((unsigned)batch), dim3(kQueryThreads), lds, st,
+                       qcodes, idx->L, idx->k, idx->cap, idx->data, idx->len, bound, stride, qids,
+                       qcnt, ulen);
+    KH_LAUNCHED();
+    return KH_OK;
   }
-  hipLaunchKernelGGL(query_kernel, dim3((unsigned)batch), dim3(kQueryThreads), lds, st, qcodes,
-                     idx->L, idx->k, idx->cap, idx->data, idx->len, bound, stride, qids, qcnt,
-                     ulen);
+  const int gather = idx->L * idx->cap;
+  KH_CHECK_ARG(gather <= kMaxGather, "query over ids >= %d needs L*cap <= %d (got %d)", kDirectIds,
+               kMaxGather, gather);
+  const size_t blds = bitmap_lds(bound, gather);
+  if (blds <= (size_t)kMaxDynLds) {
+    static bool attr_set = false;
+    if (!attr_set) {
+      KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&query_bitmap_kernel),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+      attr_set = true;
+    }
+    hipLaunchKernelGGL(query_bitmap_kernel, dim3((unsigned)batch), dim3(kQueryBigThreads), blds, st,
+                       qcodes, idx->L, idx->k, idx->cap, idx->data, idx->len, bound, stride, qids,
+                       qcnt, ulen);
+    KH_LAUNCHED();
+    return KH_OK;
+  }
+  int P = 1;
+  while (P < gather) P <<= 1;
+  hipLaunchKernelGGL(query_sort_kernel, dim3((unsigned)batch), dim3(kQueryBigThreads),
+                     sizeof(uint32_t) * P, st, qcodes, idx->L, idx->k, idx->cap, idx->data,
+                     idx->len, stride, qids, qcnt, ulen);
   KH_LAUNCHED();
   return KH_OK;
 }

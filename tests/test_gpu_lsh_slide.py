@@ -217,6 +217,41 @@ def test_query_large_ids_sort_path(kh, orc):
         np.testing.assert_array_equal(gc[off[b]:off[b + 1]], rc)
 
 
+@pytest.mark.parametrize("max_id,path", [(924_000, "bitmap"), (924_700, "bitmap"),
+                                          (925_000, "sort"), (670_090, "bitmap")])
+def test_query_bitmap_limits(kh, orc, max_id, path):
+    """Ids above 12288 are deduplicated with an LDS bitmap while its
+    ceil(bound/32) * 9/8 words plus L*cap counts fit in 152 KB (L=50, cap=128:
+    ids < 924_672), else by sorting.  Ids sit on both sides of that limit and
+    in the bitmap's last word; unions are checked with and without counts."""
+    from klearu_amd.lsh import SimHash
+    rng = np.random.default_rng(max_id % 1000)
+    fam = SimHash(64, 9, 50, 31)
+    n = 6000
+    ids = np.sort(rng.choice(max_id, n - 1, replace=False)).astype(np.uint32)
+    ids = np.append(ids, np.uint32(max_id))  # id_bound = max_id + 1
+    W = rng.normal(0, 0.01, (n, 64)).astype(np.float32)
+    idx, ref = build_pair(kh, orc, fam, RESERVOIR, 128, W, ids=ids)
+    words = (max_id + 1 + 31) // 32
+    fits = 4 * (words + (words + 7) // 8 + 50 * 128) <= 152 * 1024
+    assert fits == (path == "bitmap")
+    X = np.concatenate([rng.standard_normal((12, 64)), W[-3:]]).astype(np.float32)
+    codes = orc.hash_dense_batch(fam.planes(), X)
+    off, gi, gc = idx.query_batch(X)
+    off2, gi2, _ = idx.query_batch(X, counts=False)
+    off, off2 = off.cpu().numpy(), off2.cpu().numpy()
+    gi, gi2 = gi.cpu().numpy().view(np.uint32), gi2.cpu().numpy().view(np.uint32)
+    gc = gc.cpu().numpy().view(np.uint32)
+    np.testing.assert_array_equal(off, off2)
+    for b in range(X.shape[0]):
+        ri, rc = ref.query(codes[b])
+        np.testing.assert_array_equal(gi[off[b]:off[b + 1]], ri)
+        np.testing.assert_array_equal(gc[off[b]:off[b + 1]], rc)
+        np.testing.assert_array_equal(gi2[off[b]:off[b + 1]], ri)
+    # the rows that hash like the last inserted vector find the largest id
+    assert np.uint32(max_id) in gi[off[-2]:off[-1]]
+
+
 @pytest.mark.parametrize("L,k,n", [(100, 4, 3000), (256, 3, 600), (200, 7, 20000)])
 def test_query_many_tables(kh, orc, L, k, n):
     """More than 64 tables (up to the 256 an index may hold): dense hashing
