@@ -159,7 +159,7 @@ __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
     const float stv = stats[min(lane, nparts - 1)];
     uint4 wv[kQkvChunks];
 #pragma unroll
-    for (int q = 0; q < kQkvChunks; ++q) wv[q] = w[min(lane + 64 * q, nchunk - 1)];
+    for (int q = 0; q < kQkvChunks; ++q) wv[q] = ld_stream(w + min(lane + 64 * q, nchunk - 1));
     __builtin_amdgcn_sched_barrier(0);
     // RmsNorm (model/rms_norm.rs:56-60): (x * inv) * w
     const float inv = rms_inv_part(lane < nparts ? 0.0f + stv : 0.0f, H, eps);
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
   for (int cbase = 0; cbase < nchunk; cbase += 64 * kQkvChunks) {
     uint4 wv[kQkvChunks];
 #pragma unroll
-    for (int q = 0; q < kQkvChunks; ++q) wv[q] = w[min(cbase + lane + 64 * q, nchunk - 1)];
+    for (int q = 0; q < kQkvChunks; ++q) wv[q] = ld_stream(w + min(cbase + lane + 64 * q, nchunk - 1));
 #pragma unroll
     for (int t0 = 0; t0 < NB; t0 += TB) {
       if (t0 >= batch) break;
@@ -295,8 +295,8 @@ __global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
       const int o = 8 * min(st, qsteps - 1);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        bw[d][t][0] = wp[t][o];
-        bw[d][t][1] = wp[t][o + 4];
+        bw[d][t][0] = ld_stream(wp[t] + o);
+        bw[d][t][1] = ld_stream(wp[t] + o + 4);
       }
       bh[d][0] = xh[o]; bh[d][1] = xh[o + 4];
       bl[d][0] = xl[o]; bl[d][1] = xl[o + 4];
@@ -462,12 +462,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int j = min(start + p * RPP + r0, last);
-    kr[p] = *reinterpret_cast<const uint4*>(kc + (rowbase + j) * D + e0);
+    kr[p] = ld_stream(reinterpret_cast<const uint4*>(kc + (rowbase + j) * D + e0));
   }
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int j = min(start + p * RPP + r0, last);
-    vr[p] = *reinterpret_cast<const uint4*>(vc + (rowbase + j) * D + e0);
+    vr[p] = ld_stream(reinterpret_cast<const uint4*>(vc + (rowbase + j) * D + e0));
   }
   __builtin_amdgcn_sched_barrier(0);  // every load above is issued before any wait
   float qv[EPL], kn[EPL];
@@ -699,7 +699,7 @@ __global__ __launch_bounds__(kOprojThreads) void attn_oproj_kernel(
     const int colc = col < H ? col : H - 8;
 #pragma unroll
     for (int m = 0; m < RPL; ++m)
-      w[m] = *reinterpret_cast<const uint4*>(WoT + (size_t)s_ids[min(sub + 8 * m, rlast)] * H + colc);
+      w[m] = ld_stream(reinterpret_cast<const uint4*>(WoT + (size_t)s_ids[min(sub + 8 * m, rlast)] * H + colc));
   } else {
     // Merge waves: one (token b, head slot j) pair per wave at a time; a slot
     // is the run of the group's rows that belong to one head.  For each entry

@@ -70,6 +70,21 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
+// Streaming 16-byte load / store (nontemporal hint): for weight rows that are
+// read exactly once per call and for per-block partial rows that another
+// kernel reads back.  Measured on the batch-1 FFN gather: 10.2 -> 9.3 us for
+// 40.6 MB of rows, against plain loads.
+typedef unsigned kh_u32x4 __attribute__((ext_vector_type(4)));
+typedef float kh_f32x4_st __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+  const kh_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const kh_u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_stream(float4* p, float4 v) {
+  const kh_f32x4_st t = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(t, reinterpret_cast<kh_f32x4_st*>(p));
+}
+
 // Round to nearest even; NaN keeps its top bits and is forced quiet.
 __host__ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   uint32_t u;

@@ -70,8 +70,8 @@ __global__ __launch_bounds__(64 * kGuWaves) void ffn_gateup_kernel(
     for (int q = 0; q < kGuChunks; ++q) {
       // clamped, branch-free loads: chunks past the row end are never used
       const int c = min(cbase + lane + 64 * q, nchunk - 1);
-      wg[q] = g[c];
-      wu[q] = u[c];
+      wg[q] = ld_stream(g + c);
+      wu[q] = ld_stream(u + c);
     }
 #pragma unroll
     for (int t0 = 0; t0 < NB; t0 += TB) {
@@ -265,15 +265,15 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
 #pragma unroll
   for (int q = 0; q < kFuChunks; ++q) {
     const int c = min(lane + 64 * q, nchunk - 1);
-    wg[q] = g[c];
-    wu[q] = u[c];
+    wg[q] = ld_stream(g + c);
+    wu[q] = ld_stream(u + c);
   }
   // column slice of this wave: H / kFuWaves columns, 8 per lane
   const int slice = H / kFuWaves;
   const int col = wave * slice + 8 * min(lane, slice / 8 - 1);
 #pragma unroll
   for (int k = 0; k < kFuWaves; ++k)
-    wd[k] = *reinterpret_cast<const uint4*>(WdT + (size_t)nid[k] * H + col);
+    wd[k] = ld_stream(reinterpret_cast<const uint4*>(WdT + (size_t)nid[k] * H + col));
   __builtin_amdgcn_sched_barrier(0);
   if (norm_w) {
     // RmsNorm of the hidden row (x * inv) * w, inv from the row's per-block
@@ -331,8 +331,8 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
   }
   if (8 * lane < slice) {
     float4* o = reinterpret_cast<float4*>(partial + (size_t)blockIdx.x * H + col);
-    o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    st_stream(o, make_float4(acc[0], acc[1], acc[2], acc[3]));
+    st_stream(o + 1, make_float4(acc[4], acc[5], acc[6], acc[7]));
   }
 }
 

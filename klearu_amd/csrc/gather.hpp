@@ -55,7 +55,7 @@ __global__ __launch_bounds__(kDownThreads) void gather_rows_kernel(
 #pragma unroll
   for (int m = 0; m < RPL; ++m) {
     const int r = sub + 8 * m;
-    w[m] = (r < nr && colok) ? *reinterpret_cast<const uint4*>(WdT + (size_t)s_ids[r] * H + col)
+    w[m] = (r < nr && colok) ? ld_stream(reinterpret_cast<const uint4*>(WdT + (size_t)s_ids[r] * H + col))
                              : make_uint4(0, 0, 0, 0);
   }
   float acc[NB][8];
