@@ -18,6 +18,7 @@
 // the selected set is {key > T} plus the lowest-index entries with key == T,
 // which is exactly what the reference's stable descending sort keeps.
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
@@ -699,31 +700,51 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
   }
   // 4. compaction in ascending index order (one scan of packed counts:
   // keys > T in the low 16 bits, keys == T in the high 16 bits; n < 65536).
-  int cgt = 0, ceq = 0;
+  // Each thread turns its keys into two bit masks first, so the per-key work
+  // after the scan is one iteration per selected key, not one per key.
+  using M = typename std::conditional<(kTopkPerThread > 32), unsigned long long, uint32_t>::type;
+  auto popc = [](M m) { return (int)__popcll((unsigned long long)m); };
+  auto lowest = [](M m) { return __ffsll((unsigned long long)m) - 1; };
+  auto highest = [](M m) { return 63 - __clzll((unsigned long long)m); };
+  M gtm = 0, eqm = 0;
 #pragma unroll
   for (int j = 0; j < kTopkPerThread; ++j)
     if (j < cnt) {
-      cgt += key[j] > T;
-      ceq += key[j] == T;
+      gtm |= (M)(key[j] > T) << j;
+      eqm |= (M)(key[j] == T) << j;
     }
-  const uint32_t ex = block_excl_scan_u32((uint32_t)cgt | ((uint32_t)ceq << 16), uwsum);
-
+  const int ceq = popc(eqm);
+  const uint32_t ex = block_excl_scan_u32((uint32_t)popc(gtm) | ((uint32_t)ceq << 16), uwsum);
   const int gt_before = (int)(ex & 0xffffu), eq_before = (int)(ex >> 16);
+  // keys equal to T are taken in index order until `ties` of them are taken
+  const int take = max(0, min(ceq, ties - eq_before));
+  M em = eqm;
+  for (int t = ceq; t > take; --t) em &= ~((M)1 << highest(em));  // drop the highest
+  M selm = gtm | em;
   int pos = gt_before + min(eq_before, ties);
-  int eq_rank = eq_before;
-  uint64_t* stage = sortbuf + (size_t)b * kk0;
-#pragma unroll
-  for (int j = 0; j < kTopkPerThread; ++j) {
-    if (j < cnt) {
-      const bool eq = key[j] == T;
-      const bool sel = key[j] > T || (eq && eq_rank < ties);
-      eq_rank += eq;
-      if (sel && pos < kk0) {
-        if (order == KH_ORDER_ASCENDING) ob[pos] = i0 + j;
-        else stage[pos] = ((uint64_t)key[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)(i0 + j));
-        ++pos;
-      }
+  if (order == KH_ORDER_ASCENDING && staged) {
+    // ids staged in LDS (the scores there are dead: the keys are in
+    // registers), then written with coalesced stores
+    int32_t* sids = reinterpret_cast<int32_t*>(sort_lds);
+    while (selm) {
+      const int j = lowest(selm);
+      if (pos < kk0) sids[pos] = i0 + j;
+      ++pos;
+      selm &= selm - 1;
     }
+    lds_barrier();
+    for (int i = threadIdx.x; i < kk0; i += kTopkThreads) ob[i] = sids[i];
+    return;
+  }
+  uint64_t* stage = sortbuf + (size_t)b * kk0;
+  while (selm) {
+    const int j = lowest(selm);
+    if (pos < kk0) {
+      if (order == KH_ORDER_ASCENDING) ob[pos] = i0 + j;
+      else stage[pos] = ((uint64_t)key[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)(i0 + j));
+    }
+    ++pos;
+    selm &= selm - 1;
   }
   if (order == KH_ORDER_ASCENDING) return;
   __threadfence_block();
