@@ -542,7 +542,19 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
   }
   KH_LAUNCHED();
   int groups;
-  if (NB > 1 && H % 8 == 0) {
+  if (NB > 1 && H % kDmCols == 0) {
+    // several tokens: 512-row groups on the matrix cores (f32 MFMA)
+    static bool dm_attr = false;
+    if (!dm_attr) {
+      KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&down_mfma_kernel<NB>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmLds));
+      dm_attr = true;
+    }
+    groups = ceil_div(n_active, kDmRows);
+    hipLaunchKernelGGL(down_mfma_kernel<NB>, dim3(H / kDmCols, groups), dim3(64 * kDmWaves), kDmLds,
+                       st, f->wdt, H, active, n_active, n_active_dev, f->hbuf, f->inter, batch,
+                       f->partial);
+  } else if (NB > 1 && H % 8 == 0) {
     // several tokens: 512-row groups streamed with the next rows in flight
     groups = ceil_div(n_active, kDnGroupRows);
     hipLaunchKernelGGL(down_rows_kernel<NB>, dim3(f->nslices, groups), dim3(kDownThreads), 0, st,

@@ -9,6 +9,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "mfma.hpp"
 
 namespace kh {
 
@@ -187,6 +188,127 @@ __global__ __launch_bounds__(kDownThreads) void down_rows_kernel(
       if (ocol < H && b0 + t < batch) partial[((size_t)grp * NB + b0 + t) * H + ocol] = sm;
     }
     __syncthreads();
+  }
+}
+
+// Down projection of up to 16 tokens on the matrix cores, fed from the
+// weight rows as stored (no transpose): v_mfma_f32_16x16x4_f32 takes its B
+// operand as B[k][j] = lane 16k + j, so each group of 16 lanes holds 16
+// columns of one row -- the natural layout of a 16-byte load per lane.  With
+// M = tokens, N = columns and K = four active rows:
+//   A[t][k] = h[t][row 4g+k]            (lane l: token l%16, row l/16)
+//   B[k][j] = WdT[id(4g+k)][col(j)]     (lane l: row l/16, 8 columns per load)
+//   D[t][j] -> lane l holds tokens 4(l/16)+q, column j = l%16, q = 0..3.
+// A lane's 16-byte load holds columns c..c+7 of one row; element e of it
+// feeds MFMA number e, so MFMA e covers the columns c0 + 8p + e (p = l%16).
+// The products are f32 x f32 (no rounding of h or of the weights), so the
+// result equals an f32 dot up to summation order.  A block covers 256
+// columns (two 128-column halves per lane) and kDmRows rows; its 4 waves
+// take contiguous quarters of the rows, keep kDmDepth groups of loads in
+// flight, and their sums are added in wave order through LDS.  Rows past the
+// device count read the last valid row with h = 0.
+constexpr int kDmRows = 512;
+constexpr int kDmCols = 256;
+constexpr int kDmWaves = 4;
+constexpr int kDmDepth = 4;
+constexpr size_t kDmLds = sizeof(int) * kDmRows +
+                          sizeof(float) * (size_t)kDmWaves * 16 * kDmCols;  // ids + max(h, sums)
+
+template <int NB>
+__global__ __launch_bounds__(64 * kDmWaves) void down_mfma_kernel(
+    const uint16_t* __restrict__ WdT, int H, const int32_t* __restrict__ active, int n_active,
+    const int32_t* __restrict__ n_active_dev, const float* __restrict__ hbuf, int hstride,
+    int batch, float* __restrict__ partial) {
+  static_assert(NB <= 16, "16 token rows per MFMA tile");
+  extern __shared__ float dm_lds[];
+  int* s_ids = reinterpret_cast<int*>(dm_lds);  // [kDmRows]
+  float* s_h = dm_lds + kDmRows;                // [kDmRows][16] (then the wave sums)
+  float* red = s_h;                             // [kDmWaves][16][kDmCols]
+  int n = n_active;
+  if (n_active_dev) n = min(n, *n_active_dev);
+  const int slice = blockIdx.x, grp = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int r0 = grp * kDmRows;
+  const int nr = max(0, min(kDmRows, n - r0));
+  const int last = max(n, 1) - 1;
+  for (int i = tid; i < kDmRows; i += 64 * kDmWaves) s_ids[i] = active[min(r0 + i, last)];
+  // h of token t, row r -> s_h[r * 16 + t]; coalesced reads along the rows,
+  // eight loads per thread in flight
+  constexpr int kHPer = kDmRows * 16 / (64 * kDmWaves);
+  static_assert(kHPer % 8 == 0, "h staging batches");
+#pragma unroll
+  for (int q0 = 0; q0 < kHPer; q0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int i = tid + (q0 + q) * 64 * kDmWaves;
+      const int t = i / kDmRows, r = i - t * kDmRows;
+      v[q] = hbuf[(size_t)min(t, batch - 1) * hstride + min(r0 + r, last)];
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int i = tid + (q0 + q) * 64 * kDmWaves;
+      const int t = i / kDmRows, r = i - t * kDmRows;
+      s_h[r * 16 + t] = (t < batch && r < nr) ? v[q] : 0.0f;
+    }
+  }
+  __syncthreads();
+  const int wave = tid >> 6, lane = tid & 63;
+  const int kq = lane >> 4, p = lane & 15;
+  const uint16_t* __restrict__ wbase = WdT + (size_t)slice * kDmCols + 8 * p;
+  const int ngr = (nr + 3) >> 2;
+  const int per = (ngr + kDmWaves - 1) / kDmWaves;
+  const int g0 = min(ngr, wave * per), g1 = min(ngr, g0 + per);
+  kh_f32x4 acc[2][8];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[c][e] = kh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (g1 > g0) {
+    uint4 wb[kDmDepth][2];
+    // clamped, unconditional loads: groups past g1 reread the last group
+    auto ldw = [&](int g, uint4(&w)[2]) {
+      const int r = min(4 * min(g, g1 - 1) + kq, kDmRows - 1);
+      const uint16_t* row = wbase + (size_t)s_ids[r] * H;
+      w[0] = ld_stream(reinterpret_cast<const uint4*>(row));
+      w[1] = ld_stream(reinterpret_cast<const uint4*>(row + 128));
+    };
+#pragma unroll
+    for (int d = 0; d < kDmDepth; ++d) ldw(g0 + d, wb[d]);
+    for (int g = g0; g < g1; g += kDmDepth) {
+#pragma unroll
+      for (int d = 0; d < kDmDepth; ++d) {
+        if (g + d < g1) {  // wave-uniform
+          const float a = s_h[(4 * (g + d) + kq) * 16 + p];
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const uint32_t wv[4] = {wb[d][c].x, wb[d][c].y, wb[d][c].z, wb[d][c].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float bv = (e & 1) ? bf16_hi(wv[e >> 1]) : bf16_lo(wv[e >> 1]);
+              acc[c][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv, acc[c][e], 0, 0, 0);
+            }
+          }
+          ldw(g + d + kDmDepth, wb[d]);
+        }
+      }
+    }
+  }
+  __syncthreads();  // every wave is done with s_h before it is reused for the sums
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        red[(wave * 16 + 4 * kq + q) * kDmCols + c * 128 + 8 * p + e] = acc[c][e][q];
+  __syncthreads();
+  const int col = slice * kDmCols + tid;
+  for (int t = 0; t < batch; ++t) {
+    float sm = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kDmWaves; ++w) sm += red[(w * 16 + t) * kDmCols + tid];
+    partial[((size_t)grp * NB + t) * H + col] = sm;
   }
 }
 
