@@ -210,7 +210,7 @@ __global__ __launch_bounds__(kDownThreads) void down_rows_kernel(
 constexpr int kDmRows = 512;
 constexpr int kDmCols = 256;
 constexpr int kDmWaves = 4;
-constexpr int kDmDepth = 4;
+constexpr int kDmDepth = 8;  // 4-row groups of loads in flight per wave
 constexpr size_t kDmLds = sizeof(int) * kDmRows +
                           sizeof(float) * (size_t)kDmWaves * 16 * kDmCols;  // ids + max(h, sums)
 
@@ -231,68 +231,83 @@ __global__ __launch_bounds__(64 * kDmWaves) void down_mfma_kernel(
   const int r0 = grp * kDmRows;
   const int nr = max(0, min(kDmRows, n - r0));
   const int last = max(n, 1) - 1;
-  for (int i = tid; i < kDmRows; i += 64 * kDmWaves) s_ids[i] = active[min(r0 + i, last)];
-  // h of token t, row r -> s_h[r * 16 + t]; coalesced reads along the rows,
-  // eight loads per thread in flight
-  constexpr int kHPer = kDmRows * 16 / (64 * kDmWaves);
-  static_assert(kHPer % 8 == 0, "h staging batches");
-#pragma unroll
-  for (int q0 = 0; q0 < kHPer; q0 += 8) {
-    float v[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int i = tid + (q0 + q) * 64 * kDmWaves;
-      const int t = i / kDmRows, r = i - t * kDmRows;
-      v[q] = hbuf[(size_t)min(t, batch - 1) * hstride + min(r0 + r, last)];
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int i = tid + (q0 + q) * 64 * kDmWaves;
-      const int t = i / kDmRows, r = i - t * kDmRows;
-      s_h[r * 16 + t] = (t < batch && r < nr) ? v[q] : 0.0f;
-    }
+  if (nr == 0) {
+    // a group past the device count contributes zeros (the reduce adds every group)
+    for (int t = 0; t < batch; ++t) partial[((size_t)grp * NB + t) * H + slice * kDmCols + tid] = 0.0f;
+    return;
   }
-  __syncthreads();
+  for (int i = tid; i < kDmRows; i += 64 * kDmWaves) s_ids[i] = active[min(r0 + i, last)];
+  lds_barrier();
   const int wave = tid >> 6, lane = tid & 63;
   const int kq = lane >> 4, p = lane & 15;
   const uint16_t* __restrict__ wbase = WdT + (size_t)slice * kDmCols + 8 * p;
   const int ngr = (nr + 3) >> 2;
   const int per = (ngr + kDmWaves - 1) / kDmWaves;
   const int g0 = min(ngr, wave * per), g1 = min(ngr, g0 + per);
+  // clamped, unconditional loads: groups past g1 (or a wave's empty range in
+  // the last group) reread a valid row, whose h is 0
+  constexpr int kSlots = kDmDepth + 1;  // ring: the refill of group j + depth goes out before group j's products
+  uint4 wb[kSlots][2];
+  auto ldw = [&](int g, uint4(&w)[2]) {
+    const int r = min(4 * min(g, max(g1 - 1, 0)) + kq, kDmRows - 1);
+    const uint16_t* row = wbase + (size_t)s_ids[r] * H;
+    w[0] = ld_stream(reinterpret_cast<const uint4*>(row));
+    w[1] = ld_stream(reinterpret_cast<const uint4*>(row + 128));
+  };
+  // the first groups' weight loads go out before h is staged, so the two
+  // round trips overlap
+#pragma unroll
+  for (int d = 0; d < kDmDepth; ++d) ldw(g0 + d, wb[d]);
+  __builtin_amdgcn_sched_barrier(0);
+  // h of token t, row r -> s_h[r * 16 + t]; coalesced reads along the rows,
+  // every load in flight before the first store
+  constexpr int kHPer = kDmRows * 16 / (64 * kDmWaves);
+  {
+    float v[kHPer];
+#pragma unroll
+    for (int q = 0; q < kHPer; ++q) {
+      const int i = tid + q * 64 * kDmWaves;
+      const int t = i / kDmRows, r = i - t * kDmRows;
+      v[q] = hbuf[(size_t)min(t, batch - 1) * hstride + min(r0 + r, last)];
+    }
+#pragma unroll
+    for (int q = 0; q < kHPer; ++q) {
+      const int i = tid + q * 64 * kDmWaves;
+      const int t = i / kDmRows, r = i - t * kDmRows;
+      s_h[r * 16 + t] = (t < batch && r < nr) ? v[q] : 0.0f;
+    }
+  }
+  lds_barrier();
   kh_f32x4 acc[2][8];
 #pragma unroll
   for (int c = 0; c < 2; ++c)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[c][e] = kh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  if (g1 > g0) {
-    uint4 wb[kDmDepth][2];
-    // clamped, unconditional loads: groups past g1 reread the last group
-    auto ldw = [&](int g, uint4(&w)[2]) {
-      const int r = min(4 * min(g, g1 - 1) + kq, kDmRows - 1);
-      const uint16_t* row = wbase + (size_t)s_ids[r] * H;
-      w[0] = ld_stream(reinterpret_cast<const uint4*>(row));
-      w[1] = ld_stream(reinterpret_cast<const uint4*>(row + 128));
-    };
+  // Straight-line code over the wave's at most kDmRows / 4 / kDmWaves groups
+  // (groups past g1 multiply by h = 0): a loop, or a branch inside one, makes
+  // the compiler wait for every load in flight at the loop head, which
+  // serialises the prefetch; a branch around it lets the compiler sink the
+  // first loads below the h staging.
+  constexpr int kPerWave = kDmRows / 4 / kDmWaves;
 #pragma unroll
-    for (int d = 0; d < kDmDepth; ++d) ldw(g0 + d, wb[d]);
-    for (int g = g0; g < g1; g += kDmDepth) {
+  for (int j = 0; j < kPerWave; ++j) {
+    if (j + kDmDepth < kPerWave) ldw(g0 + j + kDmDepth, wb[(j + kDmDepth) % kSlots]);
+    const int gd = g0 + j;
+    const float hv = s_h[min(4 * gd + kq, kDmRows - 1) * 16 + p];
+    const float a = gd < g1 ? hv : 0.0f;
 #pragma unroll
-      for (int d = 0; d < kDmDepth; ++d) {
-        if (g + d < g1) {  // wave-uniform
-          const float a = s_h[(4 * (g + d) + kq) * 16 + p];
+    for (int c = 0; c < 2; ++c) {
+      const uint4 w = wb[j % kSlots][c];
+      const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            const uint32_t wv[4] = {wb[d][c].x, wb[d][c].y, wb[d][c].z, wb[d][c].w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float bv = (e & 1) ? bf16_hi(wv[e >> 1]) : bf16_lo(wv[e >> 1]);
-              acc[c][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv, acc[c][e], 0, 0, 0);
-            }
-          }
-          ldw(g + d + kDmDepth, wb[d]);
-        }
+      for (int e = 0; e < 8; ++e) {
+        const float bv = (e & 1) ? bf16_hi(wv[e >> 1]) : bf16_lo(wv[e >> 1]);
+        acc[c][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv, acc[c][e], 0, 0, 0);
       }
     }
+    // keep each group's refill ahead of its products (the scheduler would
+    // otherwise move the loads to the end, one round trip per pass)
+    __builtin_amdgcn_sched_barrier(0);
   }
   __syncthreads();  // every wave is done with s_h before it is reused for the sums
 #pragma unroll

@@ -753,28 +753,60 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
 }
 
 // ---------------------------------------------------------------- union
+// Rows up to this many neurons mark membership with one byte per neuron: the
+// marks are plain byte stores (every writer stores 1), where a bitmap needs
+// atomic ORs that serialise on the few words a batch of ids shares (26k ids
+// of a 7B batch land on 344 words).
+constexpr int kUnionFlagMax = 96 * 1024;
+
 __global__ __launch_bounds__(1024) void union_kernel(const int32_t* __restrict__ ids, int batch,
                                                      int k, int n, int32_t* __restrict__ uni,
                                                      int32_t* __restrict__ count) {
   extern __shared__ uint32_t bits[];
   __shared__ int wsum[16];
   __shared__ int s_total;
-  const int nw = (n + 31) >> 5;
+  const bool bytes = n <= kUnionFlagMax;
+  uint8_t* flags = reinterpret_cast<uint8_t*>(bits);
+  // words of marks: 4 neurons per word (byte flags) or 32 (bitmap)
+  const int nw = bytes ? (n + 3) >> 2 : (n + 31) >> 5;
   for (int i = threadIdx.x; i < nw; i += blockDim.x) bits[i] = 0;
   __syncthreads();
-  // ids requested eight per thread at a time (clamped, unconditional), so a
-  // thread waits one round trip per eight ids rather than per id
+  // ids requested 32 per thread at a time (clamped, unconditional), so the
+  // 16 rows of 1652 ids of a 7B batch arrive in one round trip
+  constexpr int U = 32;
   const int total = batch * k;
-  for (int i0 = 0; i0 < total; i0 += 8 * (int)blockDim.x) {
-    int v[8];
+  for (int i0 = 0; i0 < total; i0 += U * (int)blockDim.x) {
+    int v[U];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = ids[min(i0 + (int)threadIdx.x + u * (int)blockDim.x, total - 1)];
+    for (int u = 0; u < U; ++u) v[u] = ids[min(i0 + (int)threadIdx.x + u * (int)blockDim.x, total - 1)];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (i0 + (int)threadIdx.x + u * (int)blockDim.x < total && v[u] >= 0 && v[u] < n)
-        atomicOr(&bits[v[u] >> 5], 1u << (v[u] & 31));
+    for (int u = 0; u < U; ++u)
+      if (i0 + (int)threadIdx.x + u * (int)blockDim.x < total && v[u] >= 0 && v[u] < n) {
+        if (bytes) flags[v[u]] = 1;
+        else atomicOr(&bits[v[u] >> 5], 1u << (v[u] & 31));
+      }
   }
   __syncthreads();
+  // Compaction in ascending id order.  Byte flags: thread t owns the words
+  // [t*per, t*per + per) (set bytes hold 1, so a word's popcount counts its
+  // marks); one block scan.  Bitmap: one word per thread per round.
+  if (bytes) {
+    const int per = (nw + (int)blockDim.x - 1) / (int)blockDim.x;
+    const int w0 = (int)threadIdx.x * per;
+    int cnt = 0;
+    for (int j = 0; j < per; ++j) cnt += w0 + j < nw ? __popc(bits[w0 + j]) : 0;
+    int p = block_excl_scan(cnt, wsum, &s_total);
+    for (int j = 0; j < per && w0 + j < nw; ++j) {
+      uint32_t m = bits[w0 + j];
+      while (m) {
+        const int bit = __ffs(m) - 1;  // bit 8*b of byte b
+        uni[p++] = 4 * (w0 + j) + (bit >> 3);
+        m &= m - 1;
+      }
+    }
+    if (threadIdx.x == 0) *count = s_total;
+    return;
+  }
   int base = 0;
   for (int w0 = 0; w0 < nw; w0 += blockDim.x) {
     const int w = w0 + threadIdx.x;
@@ -1085,7 +1117,14 @@ extern "C" int kh_union_active(const int32_t* ids_dev, int64_t batch, int k, int
   KH_CHECK_ARG(ids_dev && union_dev && count_dev, "null argument");
   KH_CHECK_ARG(n > 0 && n <= 32 * 12288 && k >= 0 && batch >= 0, "bad shape (n <= 393216)");
   KH_CHECK_ARG(batch * (int64_t)k < (int64_t)1 << 31, "batch * k too large");
-  const size_t lds = sizeof(uint32_t) * ((n + 31) / 32);
+  const size_t lds = n <= kUnionFlagMax ? sizeof(uint32_t) * ((n + 3) / 4)
+                                        : sizeof(uint32_t) * ((n + 31) / 32);
+  static bool attr = false;
+  if (!attr) {
+    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&union_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
+    attr = true;
+  }
   hipLaunchKernelGGL(union_kernel, dim3(1), dim3(1024), lds, as_stream(stream), ids_dev,
                      static_cast<int>(batch), k, n, union_dev, count_dev);
   KH_LAUNCHED();

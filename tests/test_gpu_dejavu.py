@@ -114,13 +114,20 @@ def test_topk_ties_and_edges(kh, orc, n, k):
         np.testing.assert_array_equal(asc[b], np.sort(ref))
 
 
-def test_union_active(kh):
+@pytest.mark.parametrize("n,k,batch", [
+    (11008, 1652, 16),   # cfg3 batch 16 (byte marks)
+    (11007, 900, 3),     # ragged: n not a multiple of 4, ids up to n - 1
+    (5, 5, 2),           # every neuron, tiny row
+    (200000, 3000, 4),   # above the byte-mark limit: bitmap path
+])
+def test_union_active(kh, n, k, batch):
     from klearu_amd.dejavu import union_active
-    rng = np.random.default_rng(9)
-    ids = np.stack([rng.choice(11008, 1652, replace=False) for _ in range(16)]).astype(np.int32)
-    u, c = union_active(torch.from_numpy(ids).cuda(), 11008)
-    n = int(c.item())
-    np.testing.assert_array_equal(u[:n].cpu().numpy(), np.unique(ids))
+    rng = np.random.default_rng(9 + n)
+    ids = np.stack([rng.choice(n, k, replace=False) for _ in range(batch)]).astype(np.int32)
+    ids[0, 0] = n - 1  # the last neuron is always marked
+    u, c = union_active(torch.from_numpy(ids).cuda(), n)
+    cnt = int(c.item())
+    np.testing.assert_array_equal(u[:cnt].cpu().numpy(), np.unique(ids))
 
 
 def _ffn_case(orc, rng, H, I, k, batch):
