@@ -224,6 +224,15 @@ __device__ __forceinline__ float sigmoid_ref(float z) {
   float d = __fadd_rn(1.0f, e);
   return __fdiv_rn(1.0f, d);
 }
+// z / (1 + exp(-z)) with the 2^(i/32) table at `tab` (an LDS copy of
+// kExp2Tab: a lookup from constant memory whose index depends on the value
+// just computed costs a full memory round trip on the kernel's critical path).
+template <typename Tab>
+__device__ __forceinline__ float silu_ref_t(float z, const Tab& tab) {
+  float e = expf_glibc_t(-z, tab);
+  float d = __fadd_rn(1.0f, e);
+  return __fdiv_rn(z, d);
+}
 // z / (1 + exp(-z)).
 __device__ __forceinline__ float silu_ref(float z) {
   float e = expf_glibc(-z);

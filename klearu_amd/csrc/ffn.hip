@@ -134,6 +134,8 @@ __global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
     int n_active, const int32_t* __restrict__ n_active_dev, float* __restrict__ hbuf, int hstride) {
   constexpr int kGroups = kMfWaves / kMfSplit;
   __shared__ kh_f32x4 part[kGroups][kMfSplit - 1][4][64];
+  __shared__ uint64_t s_tab[32];  // kExp2Tab, for silu after the tile sums
+  const uint64_t tabv = kExp2Tab[threadIdx.x & 31];  // requested before the weights
   int n = n_active;
   if (n_active_dev) n = min(n, *n_active_dev);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -183,6 +185,7 @@ __global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
     }
   }
   // C[n][t]: lane holds rows n = 4 kb + q (q = 0..3) of token t = r
+  if (threadIdx.x < 32) s_tab[threadIdx.x] = tabv;
   if (qtr > 0) {
     part[grp][qtr - 1][0][lane] = cg0;
     part[grp][qtr - 1][1][lane] = cg1;
@@ -200,7 +203,7 @@ __global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int item = base + 4 * kb + q;
-    if (r < batch && item < n) hbuf[(size_t)r * hstride + item] = silu_ref(tg[q]) * tu[q];
+    if (r < batch && item < n) hbuf[(size_t)r * hstride + item] = silu_ref_t(tg[q], s_tab) * tu[q];
   }
 }
 
@@ -222,10 +225,14 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
     float* __restrict__ partial, const float* __restrict__ norm_w,
     const float* __restrict__ stats, int nparts, float eps) {
   extern __shared__ float4 smem4[];
+  __shared__ uint64_t s_tab[32];                                // kExp2Tab
   float4* xs4 = smem4;                                          // [H/4]
   float* hs = reinterpret_cast<float*>(smem4 + (kFuMaxH >> 2));  // [kFuWaves]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int first = blockIdx.x * kFuWaves;
+  // the exp table first (vector loads complete in order, so its store below
+  // waits for nothing else)
+  const uint64_t tabv = kExp2Tab[threadIdx.x & 31];
   // Requests in this order: x, the norm weights and the row statistics
   // (vector loads), then the block's active indices and the device count
   // (scalar loads).  The weight loads go out as soon as the indices arrive;
@@ -292,6 +299,7 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
   // sink each load into its branch, one round trip per load.
 #pragma unroll
   for (int q = 0; q < kXq; ++q) xs4[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)] = xv[q];
+  if (threadIdx.x < 32) s_tab[threadIdx.x] = tabv;
   lds_barrier();
   float ag = 0.0f, au = 0.0f;
 #pragma unroll
@@ -312,7 +320,7 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
   // wave-uniform values: the exp table lookup inside silu becomes a scalar load
   const float gs = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_sum(ag))));
   const float us = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_sum(au))));
-  const float h = wave < nlive ? silu_ref(gs) * us : 0.0f;
+  const float h = wave < nlive ? silu_ref_t(gs, s_tab) * us : 0.0f;
   if (lane == 0) hs[wave] = h;
   if (lane == 0 && wave < nlive && hbuf) hbuf[first + wave] = h;
   lds_barrier();
