@@ -249,6 +249,11 @@ constexpr int kQmSplit = 8;                  // waves per block, one k-eighth ea
 constexpr int kQmDepth = 2;                  // k-steps of loads in flight per wave
 constexpr int kQmRows = 16 * kQmTiles;       // rows per block
 constexpr int kQmAlign = 64 * kQmSplit * kQmDepth;  // hidden must be a multiple
+// TILED: W is the tiled copy (mfma_tile16x32), so that each weight load
+// instruction of a wave reads one contiguous 1 KB tile instead of 64 bytes
+// from each of 16 rows: measured 5.9 TB/s for such a stream against 3.2 TB/s
+// for the row-major gather.
+template <bool TILED>
 __global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ xhi,
     const uint16_t* __restrict__ xlo, int batch, int H, int kvrows, int rows, int D, int nh,
@@ -279,8 +284,13 @@ __global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
   const int s0 = wave * qsteps;
   const uint4* __restrict__ wp[T];
 #pragma unroll
-  for (int t = 0; t < T; ++t)
-    wp[t] = reinterpret_cast<const uint4*>(W + (size_t)min(base + 16 * t + r, rows - 1) * H) + kb + 8 * s0;
+  for (int t = 0; t < T; ++t) {
+    if constexpr (TILED)  // tile (16 rows, 32 k) = 64 uint4; lane l reads uint4 l of it
+      wp[t] = reinterpret_cast<const uint4*>(W) +
+              (size_t)min((base >> 4) + t, rows / 16 - 1) * (H / 32) * 64 + lane;
+    else
+      wp[t] = reinterpret_cast<const uint4*>(W + (size_t)min(base + 16 * t + r, rows - 1) * H) + kb + 8 * s0;
+  }
   // tokens past the batch re-read the last token's row (the same cache lines,
   // so no extra traffic); their results are never written
   const int xr = min(r, batch - 1);
@@ -295,8 +305,14 @@ __global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
       const int o = 8 * min(st, qsteps - 1);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        bw[d][t][0] = ld_stream(wp[t] + o);
-        bw[d][t][1] = ld_stream(wp[t] + o + 4);
+        if constexpr (TILED) {  // k-step sg = s0 + st covers the 32-k tiles 2 sg and 2 sg + 1
+          const size_t tl = (size_t)2 * (s0 + min(st, qsteps - 1)) * 64;
+          bw[d][t][0] = ld_stream(wp[t] + tl);
+          bw[d][t][1] = ld_stream(wp[t] + tl + 64);
+        } else {
+          bw[d][t][0] = ld_stream(wp[t] + o);
+          bw[d][t][1] = ld_stream(wp[t] + o + 4);
+        }
       }
       bh[d][0] = xh[o]; bh[d][1] = xh[o + 4];
       bl[d][0] = xl[o]; bl[d][1] = xl[o + 4];
@@ -780,6 +796,25 @@ __global__ __launch_bounds__(kOprojThreads) void attn_oproj_kernel(
 
 using namespace kh;
 
+// T[rt][kt][kb][r][e] = W[16 rt + r][32 kt + 8 kb + e] (BF16): each 16-row x
+// 32-k tile is one contiguous kilobyte, laid out so that lane l = 16 kb + r of
+// a wave reads exactly the 16 bytes it feeds to v_mfma_f32_16x16x32_bf16.
+// One thread per 16-byte piece (rows a multiple of 16, H of 32).
+__global__ void mfma_tile16x32_kernel(const uint16_t* __restrict__ W, int rows, int H,
+                                      uint16_t* __restrict__ T) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 16-byte piece of T
+  const int64_t n = (int64_t)rows * H / 8;
+  if (i >= n) return;
+  const int lane = (int)(i & 63);
+  const int64_t tile = i >> 6;
+  const int kts = H / 32;
+  const int64_t rt = tile / kts;
+  const int kt = (int)(tile - rt * kts);
+  const int r = lane & 15, kb = lane >> 4;
+  reinterpret_cast<uint4*>(T)[i] =
+      *reinterpret_cast<const uint4*>(W + (size_t)(16 * rt + r) * H + 32 * kt + 8 * kb);
+}
+
 struct kh_sparse_attn {
   int hidden = 0, nh = 0, nkv = 0, d = 0, max_seq = 0, max_batch = 0, kv_f32 = 0;
   uint16_t* wkvq = nullptr;  // [2*kvd + nh*d][hidden]
@@ -793,6 +828,7 @@ struct kh_sparse_attn {
   float* cat = nullptr;      // [max_batch][nh*d]
   int32_t* qrows = nullptr;  // [nh*d + 1 + nh]: rows, their count, union rank per head (-1: none)
   uint16_t* xsplit = nullptr;  // [2][16][hidden] BF16 hi / lo terms of x (max_batch > 1)
+  uint16_t* wkvq_t = nullptr;  // wkvq in 16 x 32 tiles (mfma_tile16x32) for the batched projections
   std::vector<int64_t> len_host;
   Scratch po, pml, partial;
   int kvd() const { return nkv * d; }
@@ -804,6 +840,7 @@ struct kh_sparse_attn {
 extern "C" int kh_sparse_attn_destroy(kh_sparse_attn* a) {
   if (!a) return KH_OK;
   dev_free(a->wkvq);
+  dev_free(a->wkvq_t);
   dev_free(a->wot);
   dev_free(a->kc);
   dev_free(a->vc);
@@ -857,6 +894,8 @@ static int attn_alloc(int hidden, int num_heads, int num_kv_heads, int head_dim,
   a->cat = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * qd));
   a->qrows = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * (qd + 1 + num_heads)));
   if (max_batch > 1) a->xsplit = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * 2 * 16 * H));
+  if (max_batch > 1 && H % 32 == 0 && (2 * kvd + qd) % 16 == 0)
+    a->wkvq_t = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * (2 * kvd + qd) * H));
   if (!a->wkvq || !a->wot || !a->kc || !a->vc || !a->cos_t || !a->sin_t || !a->lens || !a->y ||
       !a->cat || !a->qrows || (max_batch > 1 && !a->xsplit)) {
     kh_sparse_attn_destroy(a);
@@ -882,6 +921,17 @@ static int attn_alloc(int hidden, int num_heads, int num_kv_heads, int head_dim,
   }
   *out = a;
   return KH_OK;
+}
+
+// The tiled copy of wkvq for the batched projections (a no-op without one).
+static hipError_t attn_tile_weights(kh_sparse_attn* a) {
+  if (!a->wkvq_t) return hipSuccess;
+  const int rows = 2 * a->kvd() + a->nh * a->d;
+  const int64_t pieces = (int64_t)rows * a->hidden / 8;
+  hipLaunchKernelGGL(mfma_tile16x32_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, 0,
+                     a->wkvq, rows, a->hidden, a->wkvq_t);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? hipDeviceSynchronize() : e;
 }
 
 extern "C" int kh_sparse_attn_create(int hidden, int num_heads, int num_kv_heads, int head_dim,
@@ -913,6 +963,7 @@ extern "C" int kh_sparse_attn_create(int hidden, int num_heads, int num_kv_heads
   if (e == hipSuccess) e = hipMemcpy(a->wkvq + 2 * kvd * H, wq_host, row * qd, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(a->wot, ot, row * qd, hipMemcpyHostToDevice);
   free(ot);
+  if (e == hipSuccess) e = attn_tile_weights(a);
   if (e != hipSuccess) {
     set_error("attention weight upload failed: %s", hipGetErrorString(e));
     kh_sparse_attn_destroy(a);
@@ -942,6 +993,7 @@ extern "C" int kh_sparse_attn_create_dev(int hidden, int num_heads, int num_kv_h
                        0, wo_dev, hidden, static_cast<int>(qd), a->wot);
     e = hipGetLastError();
   }
+  if (e == hipSuccess) e = attn_tile_weights(a);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     set_error("attention weight repack failed: %s", hipGetErrorString(e));
@@ -1103,10 +1155,16 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
     hipLaunchKernelGGL(xsplit_kernel<>, dim3(ceil_div(16 * H, 256)), dim3(256), 0, st, x, batch,
                        H, xhi, xlo);
     KH_LAUNCHED();
-    hipLaunchKernelGGL(attn_qkv_mfma_kernel, dim3(ceil_div(rows, kQmRows) + 1),
-                       dim3(64 * kQmSplit), 0, st, a->wkvq, xhi, xlo, batch, H, kvrows, rows, D,
-                       a->nh, heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
-                       a->qrows + qd + 1);
+    if (a->wkvq_t)
+      hipLaunchKernelGGL(attn_qkv_mfma_kernel<true>, dim3(ceil_div(rows, kQmRows) + 1),
+                         dim3(64 * kQmSplit), 0, st, a->wkvq_t, xhi, xlo, batch, H, kvrows, rows, D,
+                         a->nh, heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
+                         a->qrows + qd + 1);
+    else
+      hipLaunchKernelGGL(attn_qkv_mfma_kernel<false>, dim3(ceil_div(rows, kQmRows) + 1),
+                         dim3(64 * kQmSplit), 0, st, a->wkvq, xhi, xlo, batch, H, kvrows, rows, D,
+                         a->nh, heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
+                         a->qrows + qd + 1);
     KH_LAUNCHED();
   } else {
     static bool attr_set = false;
