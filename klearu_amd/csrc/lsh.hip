@@ -523,6 +523,10 @@ int csr_finish(const uint32_t* qids, const uint32_t* qcnt, const float* f1, cons
   if (o1 && f1) hipLaunchKernelGGL(csr_copy_f32_kernel, g, dim3(256), 0, st, f1, stride, ulen, off, capacity, o1);
   if (o2 && f2) hipLaunchKernelGGL(csr_copy_f32_kernel, g, dim3(256), 0, st, f2, stride, ulen, off, capacity, o2);
   KH_LAUNCHED();
+  // Every row holds at most `stride` entries: with room for that many, no
+  // overflow is possible and the call stays asynchronous (no host round trip;
+  // capturable in a graph).  Otherwise the total is read back to report one.
+  if (capacity >= batch * (int64_t)stride) return KH_OK;
   int64_t total = 0;
   KH_HIP(hipMemcpyAsync(&total, off + batch, sizeof(int64_t), hipMemcpyDeviceToHost, st));
   KH_HIP(hipStreamSynchronize(st));
