@@ -18,6 +18,7 @@
 #include <algorithm>
 #include <vector>
 
+#include "gather.hpp"
 #include "lsh_internal.hpp"
 
 namespace kh {
@@ -144,10 +145,12 @@ __global__ __launch_bounds__(kSlideThreads) void select_kernel(
   if (threadIdx.x == 0) alen[row] = n_sel;
 }
 
-// One block per sample.  x is either dense [batch][dim] (zeros skipped) or CSR.
-template <bool SPARSE>
+// One block per sample (several per sample without softmax: blockIdx.y takes
+// every gridDim.y-th block of active ids).  x is either dense [batch][dim]
+// (zeros skipped) or CSR.  TRANS: W is the transposed copy [dim][nn].
+template <bool SPARSE, bool TRANS>
 __global__ __launch_bounds__(kSlideThreads) void neuron_kernel(
-    const float* __restrict__ W, const float* __restrict__ bias, int dim,
+    const float* __restrict__ W, int nn, const float* __restrict__ bias, int dim,
     const float* __restrict__ x, const int64_t* __restrict__ xoff,
     const uint32_t* __restrict__ xidx, const float* __restrict__ xval,
     const uint32_t* __restrict__ aids, int astride, const int32_t* __restrict__ alen, int act,
@@ -201,17 +204,23 @@ __global__ __launch_bounds__(kSlideThreads) void neuron_kernel(
   float* prow = pre + row * (int64_t)astride;
   float* orow = post + row * (int64_t)astride;
   float lmax = -INFINITY;
-  for (int a = threadIdx.x; a < n; a += blockDim.x) {
+  const int a0 = threadIdx.x + blockIdx.y * blockDim.x, astep = blockDim.x * gridDim.y;
+  for (int a = a0; a < n; a += astep) {
     const uint32_t id = ids[a];
-    const float* w = W + (size_t)id * dim;
     float s = -0.0f;
-    for (int e = 0; e < nnz; ++e) s = __fadd_rn(s, __fmul_rn(w[li[e]], lv[e]));
+    if (TRANS) {
+      const float* w = W + id;
+      for (int e = 0; e < nnz; ++e) s = __fadd_rn(s, __fmul_rn(w[(size_t)li[e] * nn], lv[e]));
+    } else {
+      const float* w = W + (size_t)id * dim;
+      for (int e = 0; e < nnz; ++e) s = __fadd_rn(s, __fmul_rn(w[li[e]], lv[e]));
+    }
     const float z = __fadd_rn(s, bias[id]);
     prow[a] = z;
     lmax = fmaxf(lmax, z);
   }
   if (act != KH_ACT_SOFTMAX) {
-    for (int a = threadIdx.x; a < n; a += blockDim.x) {
+    for (int a = a0; a < n; a += astep) {
       const float z = prow[a];
       float r;
       if (act == KH_ACT_RELU) r = fmaxf(z, 0.0f);
@@ -294,6 +303,7 @@ using namespace kh;
 struct kh_slide_layer {
   int dim = 0, n = 0;
   float* w = nullptr;
+  float* wtn = nullptr;  // [dim][n]: transposed copy for the non-softmax neuron kernel
   float* bias = nullptr;
   kh_lsh_index* index = nullptr;
   int sampling = 0, top_k = 0, threshold = 0, act = 0;
@@ -341,6 +351,21 @@ extern "C" int kh_slide_layer_create(int input_dim, int num_neurons, const float
       rc = KH_ERR_HIP;
     }
   }
+  // Transposed copy [dim][n] for the neuron kernel of non-softmax layers: the
+  // lanes of a wave take ascending active ids, so one load instruction reads a
+  // few adjacent cache lines of one input row instead of 64 weight rows.
+  if (rc == KH_OK && activation != KH_ACT_SOFTMAX) {
+    l->wtn = static_cast<float*>(dev_alloc(sizeof(float) * nw));
+    if (!l->wtn) rc = KH_ERR_ALLOC;
+    if (rc == KH_OK) {
+      hipLaunchKernelGGL(transpose_kernel<float>, dim3(ceil_div(input_dim, 32), ceil_div(num_neurons, 32)),
+                         dim3(256), 0, 0, l->w, num_neurons, input_dim, l->wtn);
+      if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        set_error("layer transpose failed");
+        rc = KH_ERR_HIP;
+      }
+    }
+  }
   // Layer::new inserts neurons 0..n-1 in order (layer.rs:42-44).
   if (rc == KH_OK) rc = kh_lsh_index_insert(index, ids, l->w, num_neurons, input_dim, nullptr);
   dev_free(ids);
@@ -355,6 +380,7 @@ extern "C" int kh_slide_layer_create(int input_dim, int num_neurons, const float
 extern "C" int kh_slide_layer_destroy(kh_slide_layer* l) {
   if (!l) return KH_OK;
   dev_free(l->w);
+  dev_free(l->wtn);
   dev_free(l->bias);
   delete l;
   return KH_OK;
@@ -394,13 +420,25 @@ static int slide_forward_common(const kh_slide_layer* lc, const float* x, const 
   const int max_nz = xoff ? 4096 : l->dim;
   KH_CHECK_ARG(xoff || l->dim <= 8192, "dense SLIDE input supports input_dim <= 8192");
   const size_t lds = (sizeof(uint32_t) + sizeof(float)) * max_nz;
-  if (xoff)
-    hipLaunchKernelGGL(neuron_kernel<true>, dim3((unsigned)batch), dim3(kSlideThreads), lds, st,
-                       l->w, l->bias, l->dim, nullptr, xoff, xidx, xval, aids, as, alen, l->act,
+  // Without softmax the active ids of a sample are split over kNeuronSplit
+  // blocks (softmax needs the whole row's max and sum in one block).
+  constexpr int kNeuronSplit = 4;
+  const dim3 ng((unsigned)batch, l->wtn ? kNeuronSplit : 1);
+  if (xoff && l->wtn)
+    hipLaunchKernelGGL((neuron_kernel<true, true>), ng, dim3(kSlideThreads), lds, st, l->wtn, l->n,
+                       l->bias, l->dim, nullptr, xoff, xidx, xval, aids, as, alen, l->act, max_nz,
+                       pre, post);
+  else if (xoff)
+    hipLaunchKernelGGL((neuron_kernel<true, false>), ng, dim3(kSlideThreads), lds, st, l->w, l->n,
+                       l->bias, l->dim, nullptr, xoff, xidx, xval, aids, as, alen, l->act, max_nz,
+                       pre, post);
+  else if (l->wtn)
+    hipLaunchKernelGGL((neuron_kernel<false, true>), ng, dim3(kSlideThreads), lds, st, l->wtn, l->n,
+                       l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, alen, l->act,
                        max_nz, pre, post);
   else
-    hipLaunchKernelGGL(neuron_kernel<false>, dim3((unsigned)batch), dim3(kSlideThreads), lds, st,
-                       l->w, l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, alen, l->act,
+    hipLaunchKernelGGL((neuron_kernel<false, false>), ng, dim3(kSlideThreads), lds, st, l->w, l->n,
+                       l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, alen, l->act,
                        max_nz, pre, post);
   KH_LAUNCHED();
   return csr_finish(aids, nullptr, pre, post, as, alen, batch, off, act_ids, nullptr, pre_out,
