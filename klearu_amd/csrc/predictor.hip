@@ -565,7 +565,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
     // too many scores to stage: each thread loads its own range directly
   } else if ((n & 3) == 0 && ((reinterpret_cast<uintptr_t>(sc) & 15) == 0)) {
     const float4* s4 = reinterpret_cast<const float4*>(sc);
-    constexpr int kQ = kTopkPerThread / 4;
+    constexpr int kQ = (kTopkPerThread + 3) / 4;
     float4 v[kQ];
 #pragma unroll
     for (int q = 0; q < kQ; ++q) v[q] = s4[min((int)threadIdx.x + q * kTopkThreads, (n >> 2) - 1)];
@@ -1048,6 +1048,7 @@ static int topk_launch(const float* scores, int64_t batch, int n, int k, int ord
   static bool attr = false;
   if (!attr) {
     int rc = topk_attr<8>();
+    if (rc == KH_OK) rc = topk_attr<11>();
     if (rc == KH_OK) rc = topk_attr<12>();
     if (rc == KH_OK) rc = topk_attr<16>();
     if (rc == KH_OK) rc = topk_attr<32>();
@@ -1075,6 +1076,8 @@ static int topk_launch(const float* scores, int64_t batch, int n, int k, int ord
   const dim3 g(static_cast<unsigned>(batch)), t(kTopkThreads);
   if (n <= kTopkThreads * 8)
     hipLaunchKernelGGL(topk_kernel<8>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
+  else if (n <= kTopkThreads * 11)  // 7B intermediate size 11008: no idle twelfth key per thread
+    hipLaunchKernelGGL(topk_kernel<11>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
   else if (n <= kTopkThreads * 12)
     hipLaunchKernelGGL(topk_kernel<12>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
   else if (n <= kTopkThreads * 16)
