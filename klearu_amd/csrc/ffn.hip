@@ -214,11 +214,13 @@ __global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
 // through LDS, then each wave adds its column slice over the block's neurons
 // in neuron order and writes it to partial[block][H]: no LDS row reduction.
 // partials_reduce_kernel adds the partials in block order.
-constexpr int kFuWaves = 8;
+constexpr int kFuWaves = 8;                // neurons (waves) per block; 4 for small hidden sizes
+constexpr int kFuWavesMin = 4;
 constexpr int kFuMaxH = 4096;              // 8 chunks of 16 B per lane per gate/up row
 constexpr int kFuChunks = kFuMaxH / 512;
 
-__global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
     const uint16_t* __restrict__ Wgu, const uint16_t* __restrict__ WdT,
     const float* __restrict__ x, int H, const int32_t* __restrict__ active, int n_active,
     const int32_t* __restrict__ n_active_dev, float* __restrict__ hbuf,
@@ -227,9 +229,9 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
   extern __shared__ float4 smem4[];
   __shared__ uint64_t s_tab[32];                                // kExp2Tab
   float4* xs4 = smem4;                                          // [H/4]
-  float* hs = reinterpret_cast<float*>(smem4 + (kFuMaxH >> 2));  // [kFuWaves]
+  float* hs = reinterpret_cast<float*>(smem4 + (kFuMaxH >> 2));  // [NW]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int first = blockIdx.x * kFuWaves;
+  const int first = blockIdx.x * NW;
   // the exp table first (vector loads complete in order, so its store below
   // waits for nothing else)
   const uint64_t tabv = kExp2Tab[threadIdx.x & 31];
@@ -240,46 +242,46 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
   // complete in issue order and x was requested first.
   const int n4 = H >> 2;
   const float4* __restrict__ xsrc = reinterpret_cast<const float4*>(x);
-  constexpr int kXq = kFuMaxH / 4 / (64 * kFuWaves);  // float4 of x per thread
+  constexpr int kXq = kFuMaxH / 4 / (64 * NW);  // float4 of x per thread
   float4 xv[kXq], wn[kXq];
 #pragma unroll
-  for (int q = 0; q < kXq; ++q) xv[q] = xsrc[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)];
+  for (int q = 0; q < kXq; ++q) xv[q] = xsrc[min((int)threadIdx.x + q * 64 * NW, n4 - 1)];
   // Branch-free requests (without a norm they read x again, unused): a load
   // inside a branch is waited for at the branch's end.  nparts = H/64 <= 64,
   // one statistic per lane.
   const float4* __restrict__ nsrc = reinterpret_cast<const float4*>(norm_w ? norm_w : x);
   const float* __restrict__ ssrc = norm_w ? stats : x;
 #pragma unroll
-  for (int q = 0; q < kXq; ++q) wn[q] = nsrc[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)];
+  for (int q = 0; q < kXq; ++q) wn[q] = nsrc[min((int)threadIdx.x + q * 64 * NW, n4 - 1)];
   const float st = ssrc[min(lane, max(nparts, 1) - 1)];
-  int cand[kFuWaves];
+  int cand[NW];
 #pragma unroll
-  for (int k = 0; k < kFuWaves; ++k) cand[k] = active[min(first + k, n_active - 1)];
+  for (int k = 0; k < NW; ++k) cand[k] = active[min(first + k, n_active - 1)];
   int n = n_active;
   if (n_active_dev) n = min(n, *n_active_dev);
   // A block past the device count still runs (reading row 0, unused) so that
   // it writes its partial row as zeros for the reduce.
-  const int nlive = max(0, min(kFuWaves, n - first));
-  int nid[kFuWaves];
+  const int nlive = max(0, min(NW, n - first));
+  int nid[NW];
 #pragma unroll
-  for (int k = 0; k < kFuWaves; ++k) nid[k] = k < nlive ? cand[k] : 0;  // idle slots read row 0, unused
+  for (int k = 0; k < NW; ++k) nid[k] = k < nlive ? cand[k] : 0;  // idle slots read row 0, unused
   __builtin_amdgcn_sched_barrier(0);
   const int nchunk = H >> 3;
   const int own = nid[wave];
   const uint4* __restrict__ g = reinterpret_cast<const uint4*>(Wgu + (size_t)own * 2 * H);
   const uint4* __restrict__ u = g + nchunk;
-  uint4 wg[kFuChunks], wu[kFuChunks], wd[kFuWaves];
+  uint4 wg[kFuChunks], wu[kFuChunks], wd[NW];
 #pragma unroll
   for (int q = 0; q < kFuChunks; ++q) {
     const int c = min(lane + 64 * q, nchunk - 1);
     wg[q] = ld_stream(g + c);
     wu[q] = ld_stream(u + c);
   }
-  // column slice of this wave: H / kFuWaves columns, 8 per lane
-  const int slice = H / kFuWaves;
+  // column slice of this wave: H / NW columns, 8 per lane
+  const int slice = H / NW;
   const int col = wave * slice + 8 * min(lane, slice / 8 - 1);
 #pragma unroll
-  for (int k = 0; k < kFuWaves; ++k)
+  for (int k = 0; k < NW; ++k)
     wd[k] = ld_stream(reinterpret_cast<const uint4*>(WdT + (size_t)nid[k] * H + col));
   __builtin_amdgcn_sched_barrier(0);
   if (norm_w) {
@@ -298,7 +300,7 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
   // the value it loaded from there): a conditional store lets the compiler
   // sink each load into its branch, one round trip per load.
 #pragma unroll
-  for (int q = 0; q < kXq; ++q) xs4[min((int)threadIdx.x + q * 64 * kFuWaves, n4 - 1)] = xv[q];
+  for (int q = 0; q < kXq; ++q) xs4[min((int)threadIdx.x + q * 64 * NW, n4 - 1)] = xv[q];
   if (threadIdx.x < 32) s_tab[threadIdx.x] = tabv;
   lds_barrier();
   float ag = 0.0f, au = 0.0f;
@@ -328,7 +330,7 @@ __global__ __launch_bounds__(64 * kFuWaves) void ffn_fused1_kernel(
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
 #pragma unroll
-  for (int k = 0; k < kFuWaves; ++k) {
+  for (int k = 0; k < NW; ++k) {
     if (k < nlive) {
       const float hk = hs[k];
       acc[0] = fmaf(hk, bf16_lo(wd[k].x), acc[0]); acc[1] = fmaf(hk, bf16_hi(wd[k].x), acc[1]);
@@ -398,7 +400,7 @@ struct kh_sparse_ffn {
 };
 
 static size_t partial_rows(int inter, int nbt) {
-  return std::max<size_t>((size_t)kMaxGroups * nbt, (size_t)ceil_div(inter, kFuWaves));
+  return std::max<size_t>((size_t)kMaxGroups * nbt, (size_t)ceil_div(inter, kFuWavesMin));
 }
 
 static int ffn_tmpl(int64_t batch) {
@@ -596,17 +598,29 @@ static int ffn_fused_launch(const kh_sparse_ffn* f, const float* x, const int32_
                             int n_active, const int32_t* n_active_dev, float* y, int accumulate,
                             const NormIn& nrm, float* stats_out, hipStream_t st) {
   const int H = f->hidden;
-  const int blocks = ceil_div(n_active, kFuWaves);
+  // Four neurons per block when the hidden size allows it (a wave's down
+  // slice is at most 512 columns) and eight would leave CUs idle: the 1.1B
+  // shape (hidden 2048, 564 active) gets 141 blocks instead of 71.
+  const bool small = H <= 512 * kFuWavesMin && n_active < 256 * kFuWaves;
+  const int nw = small ? kFuWavesMin : kFuWaves;
+  const int blocks = ceil_div(n_active, nw);
   const size_t lds = sizeof(float) * ((size_t)kFuMaxH + kFuWaves);
   static bool attr = false;
   if (!attr) {
-    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel),
+    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel<kFuWaves>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel<kFuWavesMin>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
     attr = true;
   }
-  hipLaunchKernelGGL(ffn_fused1_kernel, dim3(blocks), dim3(64 * kFuWaves), lds, st, f->wgu, f->wdt,
-                     x, H, active, n_active, n_active_dev, f->hbuf, f->partial, nrm.w, nrm.stats,
-                     nrm.nparts, nrm.eps);
+  if (small)
+    hipLaunchKernelGGL(ffn_fused1_kernel<kFuWavesMin>, dim3(blocks), dim3(64 * kFuWavesMin), lds, st,
+                       f->wgu, f->wdt, x, H, active, n_active, n_active_dev, f->hbuf, f->partial,
+                       nrm.w, nrm.stats, nrm.nparts, nrm.eps);
+  else
+    hipLaunchKernelGGL(ffn_fused1_kernel<kFuWaves>, dim3(blocks), dim3(64 * kFuWaves), lds, st,
+                       f->wgu, f->wdt, x, H, active, n_active, n_active_dev, f->hbuf, f->partial,
+                       nrm.w, nrm.stats, nrm.nparts, nrm.eps);
   KH_LAUNCHED();
   hipLaunchKernelGGL(partials_reduce_kernel<1>, dim3(ceil_div(H, 64), 1), dim3(64 * kRedWaves), 0,
                      st, f->partial, H, blocks, y, accumulate, nullptr, 0, stats_out);
