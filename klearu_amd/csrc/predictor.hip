@@ -1047,7 +1047,8 @@ static int topk_launch(const float* scores, int64_t batch, int n, int k, int ord
   size_t lds = n <= kTopkStage ? sizeof(uint32_t) * ((n + 3) & ~3) : 0;  // staged scores
   static bool attr = false;
   if (!attr) {
-    int rc = topk_attr<8>();
+    int rc = topk_attr<6>();
+    if (rc == KH_OK) rc = topk_attr<8>();
     if (rc == KH_OK) rc = topk_attr<11>();
     if (rc == KH_OK) rc = topk_attr<12>();
     if (rc == KH_OK) rc = topk_attr<16>();
@@ -1074,7 +1075,9 @@ static int topk_launch(const float* scores, int64_t batch, int n, int k, int ord
   }
   // keys per thread: the smallest instantiation that holds the row
   const dim3 g(static_cast<unsigned>(batch)), t(kTopkThreads);
-  if (n <= kTopkThreads * 8)
+  if (n <= kTopkThreads * 6)  // 1.1B intermediate size 5632
+    hipLaunchKernelGGL(topk_kernel<6>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
+  else if (n <= kTopkThreads * 8)
     hipLaunchKernelGGL(topk_kernel<8>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
   else if (n <= kTopkThreads * 11)  // 7B intermediate size 11008: no idle twelfth key per thread
     hipLaunchKernelGGL(topk_kernel<11>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);

@@ -93,7 +93,7 @@ def test_select_top_k_small_rows_ties(kh, orc, out, k, batch):
 
 @pytest.mark.parametrize("n,k", [(11008, 1652), (5632, 564), (32, 16), (1000, 1000), (1000, 1),
                                  (20000, 3000), (40000, 4000), (65535, 64), (7, 0),
-                                 (11264, 4000), (10001, 1500), (8193, 8193)])
+                                 (11264, 4000), (10001, 1500), (8193, 8193), (6143, 900)])
 def test_topk_ties_and_edges(kh, orc, n, k):
     """Rows: heavy ties at the threshold (radix passes to the last bit), five
     distinct values, signed zeros, sigmoid-clustered scores (boundary bin
