@@ -255,8 +255,8 @@ constexpr int kQmAlign = 64 * kQmSplit * kQmDepth;  // hidden must be a multiple
 // for the row-major gather.
 template <bool TILED>
 __global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
-    const uint16_t* __restrict__ W, const uint16_t* __restrict__ xhi,
-    const uint16_t* __restrict__ xlo, int batch, int H, int kvrows, int rows, int D, int nh,
+    const uint16_t* __restrict__ W, const float* __restrict__ x, int batch, int H, int kvrows,
+    int rows, int D, int nh,
     const int32_t* __restrict__ heads, int nsel, float* __restrict__ y, int ystride,
     int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows, int32_t* __restrict__ urank) {
   constexpr int T = kQmTiles, S = kQmSplit, DEP = kQmDepth;
@@ -294,13 +294,14 @@ __global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
   // tokens past the batch re-read the last token's row (the same cache lines,
   // so no extra traffic); their results are never written
   const int xr = min(r, batch - 1);
-  const uint4* __restrict__ xh = reinterpret_cast<const uint4*>(xhi + (size_t)xr * H) + kb + 8 * s0;
-  const uint4* __restrict__ xl = reinterpret_cast<const uint4*>(xlo + (size_t)xr * H) + kb + 8 * s0;
+  // x of token r: k-step s, MFMA e reads k = 64 s + 32 e + 8 kb + [0, 8) as two float4
+  const float4* __restrict__ xf = reinterpret_cast<const float4*>(x + (size_t)xr * H) + 2 * kb + 16 * s0;
   kh_f32x4 c[T][2];
 #pragma unroll
   for (int t = 0; t < T; ++t) c[t][0] = c[t][1] = kh_f32x4{0, 0, 0, 0};
   if (live) {
-    uint4 bw[DEP][T][2], bh[DEP][2], bl[DEP][2];
+    uint4 bw[DEP][T][2];
+    float4 bx[DEP][2][2];
     auto load = [&](int d, int st) {  // clamped, unconditional (past the end: reread, unused)
       const int o = 8 * min(st, qsteps - 1);
 #pragma unroll
@@ -314,8 +315,8 @@ __global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
           bw[d][t][1] = ld_stream(wp[t] + o + 4);
         }
       }
-      bh[d][0] = xh[o]; bh[d][1] = xh[o + 4];
-      bl[d][0] = xl[o]; bl[d][1] = xl[o + 4];
+      bx[d][0][0] = xf[2 * o]; bx[d][0][1] = xf[2 * o + 1];
+      bx[d][1][0] = xf[2 * o + 8]; bx[d][1][1] = xf[2 * o + 9];
     };
 #pragma unroll
     for (int d = 0; d < DEP; ++d) load(d, d);
@@ -325,12 +326,15 @@ __global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
 #pragma unroll
       for (int d = 0; d < DEP; ++d) {
 #pragma unroll
-        for (int e = 0; e < 2; ++e)
+        for (int e = 0; e < 2; ++e) {
+          uint4 xh, xl;
+          split_bf16x8(bx[d][e][0], bx[d][e][1], xh, xl);
 #pragma unroll
           for (int t = 0; t < T; ++t) {
-            c[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bw[d][t][e]), as_bf16x8(bh[d][e]), c[t][0], 0, 0, 0);
-            c[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bw[d][t][e]), as_bf16x8(bl[d][e]), c[t][1], 0, 0, 0);
+            c[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bw[d][t][e]), as_bf16x8(xh), c[t][0], 0, 0, 0);
+            c[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bw[d][t][e]), as_bf16x8(xl), c[t][1], 0, 0, 0);
           }
+        }
         load(d, st + d + DEP);
         // keep the prefetch here: the scheduler would otherwise sink it to its use
         __builtin_amdgcn_sched_barrier(0);
@@ -827,7 +831,6 @@ struct kh_sparse_attn {
   float* y = nullptr;        // [max_batch][2*kvd + nh*d]
   float* cat = nullptr;      // [max_batch][nh*d]
   int32_t* qrows = nullptr;  // [nh*d + 1 + nh]: rows, their count, union rank per head (-1: none)
-  uint16_t* xsplit = nullptr;  // [2][16][hidden] BF16 hi / lo terms of x (max_batch > 1)
   uint16_t* wkvq_t = nullptr;  // wkvq in 16 x 32 tiles (mfma_tile16x32) for the batched projections
   std::vector<int64_t> len_host;
   Scratch po, pml, partial;
@@ -850,7 +853,6 @@ extern "C" int kh_sparse_attn_destroy(kh_sparse_attn* a) {
   dev_free(a->y);
   dev_free(a->cat);
   dev_free(a->qrows);
-  dev_free(a->xsplit);
   delete a;
   return KH_OK;
 }
@@ -893,11 +895,10 @@ static int attn_alloc(int hidden, int num_heads, int num_kv_heads, int head_dim,
   a->y = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * a->ystride()));
   a->cat = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * qd));
   a->qrows = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * (qd + 1 + num_heads)));
-  if (max_batch > 1) a->xsplit = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * 2 * 16 * H));
   if (max_batch > 1 && H % 32 == 0 && (2 * kvd + qd) % 16 == 0)
     a->wkvq_t = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * (2 * kvd + qd) * H));
   if (!a->wkvq || !a->wot || !a->kc || !a->vc || !a->cos_t || !a->sin_t || !a->lens || !a->y ||
-      !a->cat || !a->qrows || (max_batch > 1 && !a->xsplit)) {
+      !a->cat || !a->qrows) {
     kh_sparse_attn_destroy(a);
     return KH_ERR_ALLOC;
   }
@@ -1149,20 +1150,15 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   const int H = a->hidden, D = a->d, qd = a->nh * D, kvrows = 2 * a->kvd();
   // 1. projections (+ the o_proj row list in the last block)
   const int rows = kvrows + qd;
-  if (NB > 1 && a->xsplit && H % kQmAlign == 0 && !nrm.w) {
-    uint16_t* xhi = a->xsplit;
-    uint16_t* xlo = a->xsplit + 16 * (size_t)H;
-    hipLaunchKernelGGL(xsplit_kernel<>, dim3(ceil_div(16 * H, 256)), dim3(256), 0, st, x, batch,
-                       H, xhi, xlo);
-    KH_LAUNCHED();
+  if (NB > 1 && H % kQmAlign == 0 && !nrm.w) {
     if (a->wkvq_t)
       hipLaunchKernelGGL(attn_qkv_mfma_kernel<true>, dim3(ceil_div(rows, kQmRows) + 1),
-                         dim3(64 * kQmSplit), 0, st, a->wkvq_t, xhi, xlo, batch, H, kvrows, rows, D,
+                         dim3(64 * kQmSplit), 0, st, a->wkvq_t, x, batch, H, kvrows, rows, D,
                          a->nh, heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
                          a->qrows + qd + 1);
     else
       hipLaunchKernelGGL(attn_qkv_mfma_kernel<false>, dim3(ceil_div(rows, kQmRows) + 1),
-                         dim3(64 * kQmSplit), 0, st, a->wkvq, xhi, xlo, batch, H, kvrows, rows, D,
+                         dim3(64 * kQmSplit), 0, st, a->wkvq, x, batch, H, kvrows, rows, D,
                          a->nh, heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
                          a->qrows + qd + 1);
     KH_LAUNCHED();

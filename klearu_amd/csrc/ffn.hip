@@ -129,8 +129,8 @@ __global__ __launch_bounds__(64 * kGuWaves) void ffn_gateup_kernel(
 // blocks); the first adds the others' accumulators through LDS in a fixed
 // order, so results are deterministic.
 __global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
-    const uint16_t* __restrict__ Wgu, const uint16_t* __restrict__ xhi,
-    const uint16_t* __restrict__ xlo, int batch, int H, const int32_t* __restrict__ active,
+    const uint16_t* __restrict__ Wgu, const float* __restrict__ x, int batch, int H,
+    const int32_t* __restrict__ active,
     int n_active, const int32_t* __restrict__ n_active_dev, float* __restrict__ hbuf, int hstride) {
   constexpr int kGroups = kMfWaves / kMfSplit;
   __shared__ kh_f32x4 part[kGroups][kMfSplit - 1][4][64];
@@ -151,17 +151,18 @@ __global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
   // tokens past the batch re-read the last token's row (the same cache lines,
   // so no extra traffic); their results are never written
   const int xr = min(r, batch - 1);
-  const uint4* __restrict__ xh = reinterpret_cast<const uint4*>(xhi + (size_t)xr * H) + kb + 8 * s0;
-  const uint4* __restrict__ xl = reinterpret_cast<const uint4*>(xlo + (size_t)xr * H) + kb + 8 * s0;
+  // x of token r: k-step s, MFMA e reads k = 64 s + 32 e + 8 kb + [0, 8) as two float4
+  const float4* __restrict__ xf = reinterpret_cast<const float4*>(x + (size_t)xr * H) + 2 * kb + 16 * s0;
   kh_f32x4 cg0 = {0, 0, 0, 0}, cg1 = cg0, cu0 = cg0, cu1 = cg0;
   if (live) {
-    uint4 bg[kMfDepth][2], bu[kMfDepth][2], bh[kMfDepth][2], bl[kMfDepth][2];
+    uint4 bg[kMfDepth][2], bu[kMfDepth][2];
+    float4 bx[kMfDepth][2][2];
     auto load = [&](int d, int s) {  // clamped, unconditional (past the end: reread, unused)
       const int o = 8 * min(s, qsteps - 1);
       bg[d][0] = g[o]; bg[d][1] = g[o + 4];
       bu[d][0] = u[o]; bu[d][1] = u[o + 4];
-      bh[d][0] = xh[o]; bh[d][1] = xh[o + 4];
-      bl[d][0] = xl[o]; bl[d][1] = xl[o + 4];
+      bx[d][0][0] = xf[2 * o]; bx[d][0][1] = xf[2 * o + 1];
+      bx[d][1][0] = xf[2 * o + 8]; bx[d][1][1] = xf[2 * o + 9];
     };
 #pragma unroll
     for (int d = 0; d < kMfDepth; ++d) load(d, d);
@@ -173,10 +174,12 @@ __global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
       for (int d = 0; d < kMfDepth; ++d) {
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          cg0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bg[d][e]), as_bf16x8(bh[d][e]), cg0, 0, 0, 0);
-          cg1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bg[d][e]), as_bf16x8(bl[d][e]), cg1, 0, 0, 0);
-          cu0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bu[d][e]), as_bf16x8(bh[d][e]), cu0, 0, 0, 0);
-          cu1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bu[d][e]), as_bf16x8(bl[d][e]), cu1, 0, 0, 0);
+          uint4 xh, xl;
+          split_bf16x8(bx[d][e][0], bx[d][e][1], xh, xl);
+          cg0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bg[d][e]), as_bf16x8(xh), cg0, 0, 0, 0);
+          cg1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bg[d][e]), as_bf16x8(xl), cg1, 0, 0, 0);
+          cu0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bu[d][e]), as_bf16x8(xh), cu0, 0, 0, 0);
+          cu1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bu[d][e]), as_bf16x8(xl), cu1, 0, 0, 0);
         }
         load(d, s + d + kMfDepth);
         // keep the prefetch here: the scheduler would otherwise sink it to its use
@@ -395,7 +398,6 @@ struct kh_sparse_ffn {
   uint16_t* wdt = nullptr;   // [inter][hidden]
   float* hbuf = nullptr;     // [max_batch][inter]
   float* partial = nullptr;  // [max(kMaxGroups*nb_tmpl, fused blocks)][hidden]
-  uint16_t* xsplit = nullptr;  // [2][16][hidden] BF16 hi / lo terms of x (batch > 1)
   int nslices = 0;
 };
 
@@ -445,9 +447,8 @@ extern "C" int kh_sparse_ffn_create(int hidden, int inter, const uint16_t* w_gat
   f->wdt = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * H * I));
   f->hbuf = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * I));
   f->partial = static_cast<float*>(dev_alloc(sizeof(float) * partial_rows(inter, nbt) * H));
-  if (max_batch > 1) f->xsplit = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * 2 * 16 * H));
   int rc = KH_OK;
-  if (!f->wgu || !f->wdt || !f->hbuf || !f->partial || (max_batch > 1 && !f->xsplit)) rc = KH_ERR_ALLOC;
+  if (!f->wgu || !f->wdt || !f->hbuf || !f->partial) rc = KH_ERR_ALLOC;
   if (rc == KH_OK) {
     if (hipMemcpy(f->wgu, gu, sizeof(uint16_t) * 2 * H * I, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(f->wdt, dt, sizeof(uint16_t) * H * I, hipMemcpyHostToDevice) != hipSuccess) {
@@ -484,8 +485,7 @@ extern "C" int kh_sparse_ffn_create_dev(int hidden, int inter, const uint16_t* w
   f->wdt = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * H * I));
   f->hbuf = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * I));
   f->partial = static_cast<float*>(dev_alloc(sizeof(float) * partial_rows(inter, nbt) * H));
-  if (max_batch > 1) f->xsplit = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * 2 * 16 * H));
-  if (!f->wgu || !f->wdt || !f->hbuf || !f->partial || (max_batch > 1 && !f->xsplit)) {
+  if (!f->wgu || !f->wdt || !f->hbuf || !f->partial) {
     kh_sparse_ffn_destroy(f);
     return KH_ERR_ALLOC;
   }
@@ -514,7 +514,6 @@ extern "C" int kh_sparse_ffn_destroy(kh_sparse_ffn* f) {
   dev_free(f->wdt);
   dev_free(f->hbuf);
   dev_free(f->partial);
-  dev_free(f->xsplit);
   delete f;
   return KH_OK;
 }
@@ -536,15 +535,10 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
     set_error("hidden %d too large for %d staged tokens", H, std::min(NB, kGuTok));
     return KH_ERR_UNSUPPORTED;
   }
-  if (NB > 1 && f->xsplit && H % (64 * kMfSplit * kMfDepth) == 0) {
+  if (NB > 1 && H % (64 * kMfSplit * kMfDepth) == 0) {
     // several tokens: gate/up as 16 x 16 tile products on MFMA
-    uint16_t* xhi = f->xsplit;
-    uint16_t* xlo = f->xsplit + 16 * (size_t)H;
-    hipLaunchKernelGGL(xsplit_kernel<>, dim3(ceil_div(16 * H, 256)), dim3(256), 0, st, x, batch, H,
-                       xhi, xlo);
-    KH_LAUNCHED();
     hipLaunchKernelGGL(ffn_gateup_mfma_kernel, dim3(ceil_div(n_active, 16 * (kMfWaves / kMfSplit))),
-                       dim3(64 * kMfWaves), 0, st, f->wgu, xhi, xlo, batch, H, active, n_active,
+                       dim3(64 * kMfWaves), 0, st, f->wgu, x, batch, H, active, n_active,
                        n_active_dev, f->hbuf, f->inter);
   } else {
     hipLaunchKernelGGL(ffn_gateup_kernel<NB>, g1, dim3(64 * kGuWaves), lds1, st, f->wgu, x, batch,

@@ -24,17 +24,23 @@ __device__ __forceinline__ kh_bf16x8 as_bf16x8(const uint4& v) {
   return __builtin_bit_cast(kh_bf16x8, v);
 }
 
-// x [batch][H] f32 -> hi, lo [16][H] BF16 bits; rows >= batch are zero.
-// (A template, so that each translation unit including this header keeps its own copy.)
-template <int Unused = 0>
-__global__ void xsplit_kernel(const float* __restrict__ x, int batch, int H,
-                              uint16_t* __restrict__ hi, uint16_t* __restrict__ lo) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= 16LL * H) return;
-  const float v = i / H < batch ? x[i] : 0.0f;
-  const uint16_t h = f32_to_bf16(v);
-  hi[i] = h;
-  lo[i] = f32_to_bf16(v - bf16_to_f32(h));  // exact difference
+// Eight f32 activations -> their BF16 hi and lo terms (x = hi + lo + r,
+// |r| <= 2^-17 |x|), both rounded to nearest even by v_cvt_pk_bf16_f32; the
+// difference x - hi is exact.  Done in registers by the MFMA kernels, so the
+// activations are read once as f32 (the same bytes as the two BF16 terms).
+typedef __bf16 kh_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_bf16x2(float p, float q) {
+  kh_bf16x2 r;
+  r.x = static_cast<__bf16>(p);
+  r.y = static_cast<__bf16>(q);
+  return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ void split_bf16x8(const float4& a, const float4& b, uint4& hi, uint4& lo) {
+  hi = make_uint4(cvt_bf16x2(a.x, a.y), cvt_bf16x2(a.z, a.w), cvt_bf16x2(b.x, b.y), cvt_bf16x2(b.z, b.w));
+  lo = make_uint4(cvt_bf16x2(a.x - bf16_lo(hi.x), a.y - bf16_hi(hi.x)),
+                  cvt_bf16x2(a.z - bf16_lo(hi.y), a.w - bf16_hi(hi.y)),
+                  cvt_bf16x2(b.x - bf16_lo(hi.z), b.y - bf16_hi(hi.z)),
+                  cvt_bf16x2(b.z - bf16_lo(hi.w), b.w - bf16_hi(hi.w)));
 }
 
 }  // namespace kh
