@@ -1230,9 +1230,13 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
                        a->wot, H, a->qrows, qd, a->qrows + qd, a->cat, qd, batch, groups,
                        partial);
   KH_LAUNCHED();
-  hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch),
-                     dim3(64 * kRedWaves), 0, st, partial, H, groups, out, accumulate, a->lens,
-                     a->max_seq, ss_out);
+  if (groups <= 64)  // few partial rows: 4-wave blocks (16 rows in flight per wave)
+    hipLaunchKernelGGL((partials_reduce_kernel<NB, 4>), dim3(ceil_div(H, 64), batch), dim3(64 * 4), 0,
+                       st, partial, H, groups, out, accumulate, a->lens, a->max_seq, ss_out);
+  else
+    hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch),
+                       dim3(64 * kRedWaves), 0, st, partial, H, groups, out, accumulate, a->lens,
+                       a->max_seq, ss_out);
   KH_LAUNCHED();
   return KH_OK;
 }

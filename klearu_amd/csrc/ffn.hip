@@ -575,8 +575,13 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
                        n_active, n_active_dev, f->hbuf, f->inter, batch, groups, f->partial);
   }
   KH_LAUNCHED();
-  hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch), dim3(64 * kRedWaves),
-                     0, st, f->partial, H, groups, y, accumulate, nullptr, 0, nullptr);
+  // few partial rows (at most 64: 4 waves x 16 rows in flight each): 4-wave blocks
+  if (groups <= 64)
+    hipLaunchKernelGGL((partials_reduce_kernel<NB, 4>), dim3(ceil_div(H, 64), batch), dim3(64 * 4), 0,
+                       st, f->partial, H, groups, y, accumulate, nullptr, 0, nullptr);
+  else
+    hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch), dim3(64 * kRedWaves),
+                       0, st, f->partial, H, groups, y, accumulate, nullptr, 0, nullptr);
   KH_LAUNCHED();
   return KH_OK;
 }

@@ -332,15 +332,16 @@ __global__ __launch_bounds__(64 * kDmWaves) void down_mfma_kernel(
 // before the first add), then the 16 wave sums are added in wave order, so the
 // summation order is fixed for a given number of partial rows.
 constexpr int kRedWaves = 16;
-template <int NB>
-__global__ __launch_bounds__(64 * kRedWaves) void partials_reduce_kernel(const float* __restrict__ partial,
+// RW waves per block (kRedWaves by default; 4 when there are few partial rows)
+template <int NB, int RW = kRedWaves>
+__global__ __launch_bounds__(64 * RW) void partials_reduce_kernel(const float* __restrict__ partial,
                                                                     int H, int groups,
                                                                     float* __restrict__ y,
                                                                     int accumulate,
                                                                     int32_t* __restrict__ bump,
                                                                     int bump_limit,
                                                                     float* __restrict__ ss_out) {
-  __shared__ float sums[kRedWaves][64];
+  __shared__ float sums[RW][64];
   const int b = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int j = blockIdx.x * 64 + lane;
@@ -349,21 +350,21 @@ __global__ __launch_bounds__(64 * kRedWaves) void partials_reduce_kernel(const f
   // the value accumulated into is requested with the partials, not after them
   const float y0 = (accumulate && wave == 0) ? y[(size_t)b * H + jc] : 0.0f;
   float t = 0.0f;
-  for (int g0 = wave; g0 < groups; g0 += kRedWaves * U) {
+  for (int g0 = wave; g0 < groups; g0 += RW * U) {
     float v[U];
 #pragma unroll
     for (int q = 0; q < U; ++q)
-      v[q] = partial[((size_t)min(g0 + kRedWaves * q, groups - 1) * NB + b) * H + jc];
+      v[q] = partial[((size_t)min(g0 + RW * q, groups - 1) * NB + b) * H + jc];
 #pragma unroll
     for (int q = 0; q < U; ++q)
-      if (g0 + kRedWaves * q < groups) t += v[q];
+      if (g0 + RW * q < groups) t += v[q];
   }
   sums[wave][lane] = t;
   __syncthreads();
   if (wave == 0) {
     float tot = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kRedWaves; ++w) tot += sums[w][lane];
+    for (int w = 0; w < RW; ++w) tot += sums[w][lane];
     const float yn = accumulate ? y0 + tot : tot;
     if (j < H) y[(size_t)b * H + j] = yn;
     // Sum of squares of this block's 64 outputs: the RmsNorm statistics of
