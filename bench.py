@@ -173,8 +173,8 @@ def ffn_leg(name, L, H, I, R, frac, B, steps, warmup, seed, model=None, timer=No
             return
         for l in range(L):
             _lib.call("kh_rmsnorm", ptr(hidden), ptr(w_norm), B, H, 1e-5, ptr(norm), st)
-            _lib.call("kh_predictor_select_top_k", preds[l]._h, ptr(norm), B, k, ORDER_ASCENDING, ptr(active[l]), st)
-            _lib.call("kh_union_active", ptr(active[l]), B, k, I, ptr(union[l]), ptr(ucount[l]), st)
+            _lib.call("kh_predictor_select_top_k_union", preds[l]._h, ptr(norm), B, k, ptr(active[l]),
+                      ptr(union[l]), ptr(ucount[l]), st)
             ffn_call(l, st)
 
     def ffn_only():

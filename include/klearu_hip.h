@@ -241,6 +241,14 @@ int kh_topk_select(const float* scores_dev, int64_t batch, int n, int k, int ord
  * *count_dev (device int32). */
 int kh_union_active(const int32_t* ids_dev, int64_t batch, int k, int n, int32_t* union_dev,
                     int32_t* count_dev, void* stream);
+/* kh_predictor_select_top_k (ascending order) and kh_union_active in one call:
+ * the top-k kernel marks the selected neurons and the union is read from the
+ * marks (mlp_predictor.rs:127-132 per row, then the shared active set).
+ * ids_dev[batch][min(k, output)], union_dev[<= output] ascending, *count_dev.
+ * Calls on one predictor handle must not overlap (the marks live in it). */
+int kh_predictor_select_top_k_union(const kh_predictor* p, const float* x_dev, int64_t batch,
+                                    int k, int32_t* ids_dev, int32_t* union_dev,
+                                    int32_t* count_dev, void* stream);
 
 /* ======================================================================== */
 /* Sparse SwiGLU FFN (crates/klearu-llm/src/sparse/sparse_mlp.rs)           */

@@ -92,6 +92,7 @@ SIGS = {
     "kh_predictor_select_top_k": (I, [P, P, I64, I, I, P, P]),
     "kh_topk_select": (I, [P, I64, I, I, I, P, P]),
     "kh_union_active": (I, [P, I64, I, I, P, P, P]),
+    "kh_predictor_select_top_k_union": (I, [P, P, I64, I, P, P, P, P]),
     "kh_sparse_ffn_create": (I, [I, I, P, P, P, I, PP]),
     "kh_sparse_ffn_create_dev": (I, [I, I, P, P, P, I, PP]),
     "kh_sparse_ffn_destroy": (I, [P]),

@@ -524,7 +524,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
                                                             int32_t* __restrict__ out,
                                                             uint64_t* __restrict__ sortbuf,
                                                             const uint32_t* __restrict__ mm,
-                                                            int nmm) {
+                                                            int nmm,
+                                                            uint8_t* __restrict__ marks) {
   extern __shared__ __align__(16) uint64_t sort_lds[];
   __shared__ unsigned hist[1 << kTopkDigit];
   __shared__ uint64_t cand[kTopkCand];
@@ -734,6 +735,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
     }
     lds_barrier();
     for (int i = threadIdx.x; i < kk0; i += kTopkThreads) ob[i] = sids[i];
+    // union marks shared by the rows of a batch: every writer stores 1
+    if (marks)
+      for (int i = threadIdx.x; i < kk0; i += kTopkThreads) marks[sids[i]] = 1;
     return;
   }
   uint64_t* stage = sortbuf + (size_t)b * kk0;
@@ -742,6 +746,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
     if (pos < kk0) {
       if (order == KH_ORDER_ASCENDING) ob[pos] = i0 + j;
       else stage[pos] = ((uint64_t)key[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)(i0 + j));
+      if (marks) marks[i0 + j] = 1;
     }
     ++pos;
     selm &= selm - 1;
@@ -825,6 +830,39 @@ __global__ __launch_bounds__(1024) void union_kernel(const int32_t* __restrict__
   if (threadIdx.x == 0) *count = base;
 }
 
+// Union from the byte marks the top-k kernel set (one byte per neuron, 1 if
+// some row selected it): ascending ids and the count; the marks are cleared
+// for the next call.  One block; thread t owns the mark words [t*per, ...).
+__global__ __launch_bounds__(1024) void marks_union_kernel(uint32_t* __restrict__ marks, int n,
+                                                           int32_t* __restrict__ uni,
+                                                           int32_t* __restrict__ count) {
+  __shared__ int wsum[16];
+  __shared__ int s_total;
+  const int nw = (n + 3) >> 2;
+  const int per = (nw + (int)blockDim.x - 1) / (int)blockDim.x;
+  const int w0 = (int)threadIdx.x * per;
+  constexpr int kMaxPer = 8;  // n <= 32768 (host-checked)
+  uint32_t w[kMaxPer];
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxPer; ++j) {
+    w[j] = (j < per && w0 + j < nw) ? marks[w0 + j] : 0u;
+    cnt += __popc(w[j]);  // set bytes hold 1
+  }
+  int p = block_excl_scan(cnt, wsum, &s_total);
+#pragma unroll
+  for (int j = 0; j < kMaxPer; ++j) {
+    uint32_t m = w[j];
+    while (m) {
+      const int bit = __ffs(m) - 1;
+      uni[p++] = 4 * (w0 + j) + (bit >> 3);
+      m &= m - 1;
+    }
+    if (j < per && w0 + j < nw && w[j]) marks[w0 + j] = 0u;
+  }
+  if (threadIdx.x == 0) *count = s_total;
+}
+
 }  // namespace kh
 
 using namespace kh;
@@ -839,6 +877,7 @@ struct kh_predictor {
   float* hbuf = nullptr;  // [batch_cap][hid]
   float* sbuf = nullptr;  // [batch_cap][out]
   uint32_t* mm = nullptr; // [batch_cap][layer-2 blocks][2] score key bounds per block
+  uint8_t* marks = nullptr;  // [round_up(out, 4)] union marks (zero between calls)
   int batch_cap = 0;
 };
 
@@ -921,6 +960,7 @@ extern "C" int kh_predictor_create(int input_dim, int hidden_dim, int output_dim
 
 extern "C" int kh_predictor_destroy(kh_predictor* p) {
   if (!p) return KH_OK;
+  dev_free(p->marks);
   dev_free(p->w1b);
   dev_free(p->b1);
   dev_free(p->w2b);
@@ -1038,7 +1078,8 @@ static int topk_attr() {
 // mm: per-block key bounds from layer 2, nmm slots per row (or nullptr: the
 // kernel finds the bounds from the scores).
 static int topk_launch(const float* scores, int64_t batch, int n, int k, int order, int32_t* ids,
-                       hipStream_t st, const uint32_t* mm = nullptr, int nmm = 0) {
+                       hipStream_t st, const uint32_t* mm = nullptr, int nmm = 0,
+                       uint8_t* marks = nullptr) {
   const int kk = std::min(k, n);
   if (kk <= 0 || batch == 0) return KH_OK;
   KH_CHECK_ARG(n <= kTopkRegMax, "top-k supports n <= %d scores per row (got %d)", kTopkRegMax, n);
@@ -1076,19 +1117,19 @@ static int topk_launch(const float* scores, int64_t batch, int n, int k, int ord
   // keys per thread: the smallest instantiation that holds the row
   const dim3 g(static_cast<unsigned>(batch)), t(kTopkThreads);
   if (n <= kTopkThreads * 6)  // 1.1B intermediate size 5632
-    hipLaunchKernelGGL(topk_kernel<6>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
+    hipLaunchKernelGGL(topk_kernel<6>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm, marks);
   else if (n <= kTopkThreads * 8)
-    hipLaunchKernelGGL(topk_kernel<8>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
+    hipLaunchKernelGGL(topk_kernel<8>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm, marks);
   else if (n <= kTopkThreads * 11)  // 7B intermediate size 11008: no idle twelfth key per thread
-    hipLaunchKernelGGL(topk_kernel<11>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
+    hipLaunchKernelGGL(topk_kernel<11>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm, marks);
   else if (n <= kTopkThreads * 12)
-    hipLaunchKernelGGL(topk_kernel<12>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
+    hipLaunchKernelGGL(topk_kernel<12>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm, marks);
   else if (n <= kTopkThreads * 16)
-    hipLaunchKernelGGL(topk_kernel<16>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
+    hipLaunchKernelGGL(topk_kernel<16>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm, marks);
   else if (n <= kTopkThreads * 32)
-    hipLaunchKernelGGL(topk_kernel<32>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
+    hipLaunchKernelGGL(topk_kernel<32>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm, marks);
   else
-    hipLaunchKernelGGL(topk_kernel<64>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm);
+    hipLaunchKernelGGL(topk_kernel<64>, g, t, lds, st, scores, n, k, order, ids, sortbuf, mm, nmm, marks);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -1108,6 +1149,42 @@ extern "C" int kh_predictor_select_top_k(const kh_predictor* p, const float* x_d
   rc = predict_into(p, x_dev, batch, pm->sbuf, st, NormIn{}, &mm, &tk);
   if (rc != KH_OK || tk.done) return rc;
   return topk_launch(pm->sbuf, batch, p->out_dim, k, order, ids_dev, st, mm, l2_blocks(p));
+}
+
+extern "C" int kh_predictor_select_top_k_union(const kh_predictor* p, const float* x_dev,
+                                               int64_t batch, int k, int32_t* ids_dev,
+                                               int32_t* union_dev, int32_t* count_dev,
+                                               void* stream) {
+  KH_CHECK_ARG(p && x_dev && ids_dev && union_dev && count_dev, "null argument");
+  KH_CHECK_ARG(k >= 0 && batch >= 0 && batch <= 65535, "bad k/batch");
+  hipStream_t st = as_stream(stream);
+  const int n = p->out_dim;
+  if (batch == 0 || k == 0 || n <= 64 || n > 32768) {
+    // nothing selected, rows selected inside layer 2, or rows beyond the
+    // marks kernel: ids first, then the union from them
+    int rc = kh_predictor_select_top_k(p, x_dev, batch, k, KH_ORDER_ASCENDING, ids_dev, stream);
+    if (rc != KH_OK) return rc;
+    return kh_union_active(ids_dev, batch, std::min(k, n), n, union_dev, count_dev, stream);
+  }
+  auto* pm = const_cast<kh_predictor*>(p);
+  if (!pm->marks) {
+    const size_t bytes = (size_t)((n + 3) & ~3);
+    pm->marks = static_cast<uint8_t*>(dev_alloc(bytes));
+    if (!pm->marks) return KH_ERR_ALLOC;
+    KH_HIP(hipMemset(pm->marks, 0, bytes));  // once; the union kernel clears what it reads
+  }
+  int rc = ensure_batch(pm, batch);
+  if (rc != KH_OK) return rc;
+  uint32_t* mm = nullptr;
+  rc = predict_into(p, x_dev, batch, pm->sbuf, st, NormIn{}, &mm, nullptr);
+  if (rc != KH_OK) return rc;
+  rc = topk_launch(pm->sbuf, batch, n, k, KH_ORDER_ASCENDING, ids_dev, st, mm, l2_blocks(p),
+                   pm->marks);
+  if (rc != KH_OK) return rc;
+  hipLaunchKernelGGL(marks_union_kernel, dim3(1), dim3(1024), 0, st,
+                     reinterpret_cast<uint32_t*>(pm->marks), n, union_dev, count_dev);
+  KH_LAUNCHED();
+  return KH_OK;
 }
 
 extern "C" int kh_topk_select(const float* scores_dev, int64_t batch, int n, int k, int order,

@@ -85,6 +85,18 @@ class SparsityPredictor:
                       stream_ptr(stream))
         return out[0] if squeeze else out
 
+    def select_top_k_union(self, x: torch.Tensor, k: int, stream=None):
+        """Ascending top-k ids [batch, min(k, output)] and their union (ids, device count)."""
+        x = to_device(x, np.float32)
+        xb = x.reshape(-1, self.input_dim)
+        kk = min(k, self.output_dim)
+        ids = torch.empty(xb.shape[0], kk, dtype=torch.int32, device=x.device)
+        uni = torch.empty(max(1, self.output_dim), dtype=torch.int32, device=x.device)
+        cnt = torch.zeros(1, dtype=torch.int32, device=x.device)
+        _lib.call("kh_predictor_select_top_k_union", self._h, ptr(xb), xb.shape[0], k, ptr(ids), ptr(uni),
+                  ptr(cnt), stream_ptr(stream))
+        return ids, uni, cnt
+
 
 class PredictorStore:
     """Per-layer head / neuron predictors; missing ones fall back to 0..k."""

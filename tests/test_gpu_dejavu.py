@@ -131,6 +131,31 @@ def test_union_active(kh, n, k, batch):
     np.testing.assert_array_equal(u[:cnt].cpu().numpy(), np.unique(ids))
 
 
+@pytest.mark.parametrize("ind,hid,out,k,batch", [
+    (4096, 256, 11008, 1652, 16),  # the 7B decode batch: union from the top-k marks
+    (2048, 128, 5630, 564, 3),     # ragged row (n % 4 != 0)
+    (256, 64, 32768, 9000, 2),     # the largest row on the marks path
+    (4096, 128, 32, 16, 8),        # rows selected inside layer 2: union from the ids
+    (64, 32, 12, 20, 2)])          # k > output: every neuron
+def test_select_top_k_union(kh, orc, ind, hid, out, k, batch):
+    from klearu_amd.dejavu import SparsityPredictor
+    rng = np.random.default_rng(out + batch)
+    w1, b1, w2, b2 = make_predictor(orc, rng, ind, hid, out)
+    p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
+    # two calls in a row, the second smaller: the marks must start clear
+    for bt in (batch, max(1, batch // 2)):
+        x = rng.standard_normal((bt, ind)).astype(np.float32)
+        ids, u, c = p.select_top_k_union(torch.from_numpy(x).cuda(), k)
+        ids = ids.cpu().numpy()
+        ref = []
+        for b in range(bt):
+            s, _ = orc.predictor_predict(w1, b1, w2, b2, x[b])
+            ref.append(np.sort(orc.select_top_k(s, k)))
+            np.testing.assert_array_equal(ids[b], ref[-1])
+        cnt = int(c.item())
+        np.testing.assert_array_equal(u[:cnt].cpu().numpy(), np.unique(np.concatenate(ref)))
+
+
 def _ffn_case(orc, rng, H, I, k, batch):
     wg = bf16(orc, rng.normal(0, 0.02, (I, H)))
     wu = bf16(orc, rng.normal(0, 0.02, (I, H)))
