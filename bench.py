@@ -159,17 +159,15 @@ def ffn_leg(name, L, H, I, R, frac, B, steps, warmup, seed, model=None, timer=No
             _lib.call("kh_sparse_ffn_forward", mlps[l]._h, ptr(norm), B, ptr(union[l]), I, ptr(ucount[l]),
                       ptr(hidden), 1, st)
 
-    stats = torch.empty(B, (H + 63) // 64, dtype=torch.float32, device=dev)
+    norm_ws = torch.empty(B, dtype=torch.float32, device=dev)
 
     def step():
         st = stream_ptr()
         if B == 1:
-            # fused block: the RmsNorm runs inside the predictor and FFN kernels
-            # from per-block sums of squares that each block hands to the next
-            _lib.call("kh_rms_stats", ptr(hidden), 1, H, ptr(stats), st)
+            # fused block: the exact RmsNorm runs inside the predictor and FFN kernels
             for l in range(L):
                 _lib.call("kh_dejavu_mlp_block", preds[l]._h, mlps[l]._h, ptr(hidden), ptr(w_norm), 1e-5, k,
-                          ptr(active[l]), ptr(stats), st)
+                          ptr(active[l]), ptr(norm_ws), st)
             return
         for l in range(L):
             _lib.call("kh_rmsnorm", ptr(hidden), ptr(w_norm), B, H, 1e-5, ptr(norm), st)
@@ -253,17 +251,15 @@ def attn_leg(name, L, B, steps, warmup, seed, timer, cpu_seconds):
     hidden = torch.randn(B, H, generator=g, device="cuda")
     norm = torch.empty_like(hidden)
     heads = [torch.empty(B, k, dtype=torch.int32, device="cuda") for _ in range(L)]
-    stats = torch.empty(B, (H + 63) // 64, dtype=torch.float32, device="cuda")
+    norm_ws = torch.empty(B, dtype=torch.float32, device="cuda")
 
     def step():
         st = stream_ptr()
         if B == 1:
-            # fused block: the RmsNorm runs inside the predictor and q/k/v kernels
-            # from per-block sums of squares that each block hands to the next
-            _lib.call("kh_rms_stats", ptr(hidden), 1, H, ptr(stats), st)
+            # fused block: the exact RmsNorm runs inside the predictor and q/k/v kernels
             for l in range(L):
                 _lib.call("kh_dejavu_attn_block", preds[l]._h, layers[l]._h, ptr(hidden), ptr(w_norm), 1e-5, k,
-                          ptr(heads[l]), ptr(stats), st)
+                          ptr(heads[l]), ptr(norm_ws), st)
             return
         for l in range(L):
             _lib.call("kh_rmsnorm", ptr(hidden), ptr(w_norm), B, H, 1e-5, ptr(norm), st)

@@ -280,27 +280,26 @@ int kh_sparse_ffn_forward(const kh_sparse_ffn* f, const float* x_dev, int64_t ba
 int kh_sparse_ffn_last_hidden(const kh_sparse_ffn* f, float* h_dev, int64_t batch, int n_active,
                               void* stream);
 
-/* RmsNorm::forward (model/rms_norm.rs:43-64): y[b] = x[b] * inv_rms * w. */
+/* RmsNorm::forward (model/rms_norm.rs:43-64): y[b] = (x[b] * inv_rms) * w with
+ * the sum of squares in the reference's sequential order (bit-identical). */
 int kh_rmsnorm(const float* x_dev, const float* w_dev, int64_t batch, int n, float eps,
                float* y_dev, void* stream);
 
-/* Per-block sums of squares x[b][64*i .. 64*i+63]^2 -> stats[b][i]
- * (ceil(n/64) per row): the RmsNorm statistics kh_dejavu_mlp_block reads. */
-int kh_rms_stats(const float* x_dev, int64_t batch, int n, float* stats_dev, void* stream);
 /* One decode step (batch 1) of the Deja Vu MLP block as
  * SparseModel::forward_decode_sparse runs it (crates/klearu-llm/src/sparse/mod.rs:115-142):
  *   norm = RmsNorm(hidden) (model/rms_norm.rs:43-64, weight norm_w, eps);
  *   active = predictor.select_top_k(norm, k) (ascending ids into active_dev[k]);
  *   hidden += sparse_mlp::forward_sparse(norm, active).
- * The norm is applied inside the predictor and FFN kernels from stats_dev
- * (ceil(hidden/64) sums of squares of the current hidden row, from
- * kh_rms_stats or from the previous block); on return stats_dev holds those of
- * the updated row, so consecutive blocks need no separate norm pass.
+ * The norm is applied inside the predictor and FFN kernels.  Its sum of squares
+ * is the reference's sequential f32 sum, so the normalised row, the scores and
+ * the selected set are bit-identical to the reference's for the same hidden
+ * row.  norm_ws_dev (>= 1 float, device) receives the row's scale 1/rms.
  * Requires predictor input_dim == hidden, output_dim == intermediate, hidden a
- * multiple of 64 and at most 4096. */
+ * multiple of 64 and at most 4096 (larger hidden sizes run the unfused calls:
+ * kh_rmsnorm, kh_predictor_select_top_k, kh_sparse_ffn_forward). */
 int kh_dejavu_mlp_block(const kh_predictor* p, const kh_sparse_ffn* f, float* hidden_dev,
                         const float* norm_w_dev, float eps, int k, int32_t* active_dev,
-                        float* stats_dev, void* stream);
+                        float* norm_ws_dev, void* stream);
 
 /* ======================================================================== */
 /* klearu-dejavu transformer layer: f32 Linear with bias, SparseMlp,        */
@@ -416,15 +415,15 @@ int kh_sparse_attn_forward(kh_sparse_attn* a, const float* x_dev, int64_t batch,
  *   heads = predictor.select_top_k(norm, k) (PredictorStore::predict_heads,
  *           sparse/predictor_store.rs:38-45; ascending ids into heads_dev[k]);
  *   hidden += sparse_attention::forward_sparse(norm, position = cache length, heads).
- * The norm is applied inside the predictor and q/k/v kernels from stats_dev
- * (hidden/64 sums of squares of the current hidden row, from kh_rms_stats or
- * the previous block); on return stats_dev holds those of the updated row, so
- * it chains with kh_dejavu_mlp_block without a separate norm pass.  Requires
- * predictor input_dim == hidden, output_dim == num_heads, hidden a multiple of
- * 64 and at most 4096.  Returns KH_ERR_CAPACITY when the cache is full. */
+ * The norm is applied inside the predictor and q/k/v kernels, bit-identical to
+ * the reference's (sequential sum of squares); norm_ws_dev (>= 1 float,
+ * device) receives the row's scale 1/rms.  Chains with kh_dejavu_mlp_block
+ * into a full decoder layer.  Requires predictor input_dim == hidden,
+ * output_dim == num_heads, hidden a multiple of 64 and at most 4096.  Returns
+ * KH_ERR_CAPACITY when the cache is full. */
 int kh_dejavu_attn_block(const kh_predictor* p, kh_sparse_attn* a, float* hidden_dev,
                          const float* norm_w_dev, float eps, int k, int32_t* heads_dev,
-                         float* stats_dev, void* stream);
+                         float* norm_ws_dev, void* stream);
 
 #ifdef __cplusplus
 }

@@ -99,7 +99,6 @@ SIGS = {
     "kh_sparse_ffn_forward": (I, [P, P, I64, P, I, P, P, I, P]),
     "kh_sparse_ffn_last_hidden": (I, [P, P, I64, I, P]),
     "kh_rmsnorm": (I, [P, P, I64, I, F, P, P]),
-    "kh_rms_stats": (I, [P, I64, I, P, P]),
     "kh_dejavu_mlp_block": (I, [P, P, P, P, F, I, P, P, P]),
     "kh_dejavu_attn_block": (I, [P, P, P, P, F, I, P, P, P]),
     "kh_sparse_attn_create": (I, [I, I, I, I, I, I, F, I, P, P, P, P, PP]),

@@ -123,17 +123,17 @@ def forward_sparse(attn: SparseAttention, input, position, active_heads):
 
 
 def attn_block(predictor, attn: SparseAttention, hidden: torch.Tensor, norm_w: torch.Tensor, eps: float, k: int,
-               heads: torch.Tensor | None = None, stats: torch.Tensor | None = None, stream=None):
+               heads: torch.Tensor | None = None, norm_ws: torch.Tensor | None = None, stream=None):
     """One decode step of the attention half of a sparse decoder layer for sequence 0
     (crates/klearu-llm/src/sparse/mod.rs:56-112), in place:
     hidden += forward_sparse(attn, RmsNorm(hidden), position, predictor.select_top_k(RmsNorm(hidden), k)).
-    `stats` carries the RmsNorm statistics between blocks (computed when None).
-    Returns (head ids ascending, stats of the updated hidden)."""
-    from .dejavu import rms_stats
-    if stats is None:
-        stats = rms_stats(hidden, stream)
+    The norm, and so the head selection, is bit-identical to the reference's.  `norm_ws` (one
+    float on the device, allocated when None) receives the row's RmsNorm scale.  Returns the
+    head ids (ascending)."""
+    if norm_ws is None:
+        norm_ws = torch.empty(1, dtype=torch.float32, device=hidden.device)
     if heads is None:
         heads = torch.empty(k, dtype=torch.int32, device=hidden.device)
     _lib.call("kh_dejavu_attn_block", predictor._h, attn._h, ptr(hidden), ptr(norm_w), float(eps), k, ptr(heads),
-              ptr(stats), stream_ptr(stream))
-    return heads, stats
+              ptr(norm_ws), stream_ptr(stream))
+    return heads

@@ -113,14 +113,15 @@ __device__ void qkv_plan(const int32_t* __restrict__ heads, int nent, int nh, in
 // y[b][row] = Wkvq[row] . x[b] for the K/V rows and the Q rows of selected
 // heads.  The grid has one extra (last) block that writes the o_proj row list.
 // NORM (batch 1): x is the un-normalised hidden row and RmsNorm (weight nw) is
-// applied while staging it, from the row's per-64-column sums of squares.
+// applied while staging it, with the exact scale at norm_inv (written by the
+// head predictor's layer 1 for this row).
 template <int NB, bool NORM = false>
 __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
     const uint16_t* __restrict__ W, const float* __restrict__ x, int batch, int H, int kvrows,
     int D, int nh, const int32_t* __restrict__ heads, int nsel, float* __restrict__ y,
     int ystride, int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows,
-    int32_t* __restrict__ urank, const float* __restrict__ nw, const float* __restrict__ stats,
-    int nparts, float eps) {
+    int32_t* __restrict__ urank, const float* __restrict__ nw,
+    const float* __restrict__ norm_inv) {
   extern __shared__ float4 xs4[];  // [kQkvTok][H/4]; the plan block's flags / union list
   __shared__ int wsum[kQkvWaves];
   __shared__ int s_total;
@@ -145,8 +146,8 @@ __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
   constexpr int TB = NB < kQkvTok ? NB : kQkvTok;
   if constexpr (NORM) {
     // One token, H <= 4096 (one pass, no loop): the row, the norm weights and
-    // the statistics are requested first, then the weight row; the norm is
-    // formed while the weights stream in (loads complete in issue order).
+    // the scale are requested first, then the weight row; the norm is formed
+    // while the weights stream in (loads complete in issue order).
     constexpr int kXq = 4096 / 4 / (64 * kQkvWaves);
     float4 xv[kXq], wn[kXq];
 #pragma unroll
@@ -155,21 +156,19 @@ __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
       xv[q] = reinterpret_cast<const float4*>(x)[i];
       wn[q] = reinterpret_cast<const float4*>(nw)[i];
     }
-    // nparts = H/64 <= 64: one statistic per lane, one clamped load (no branch)
-    const float stv = stats[min(lane, nparts - 1)];
+    const float inv = *norm_inv;
     uint4 wv[kQkvChunks];
 #pragma unroll
     for (int q = 0; q < kQkvChunks; ++q) wv[q] = ld_stream(w + min(lane + 64 * q, nchunk - 1));
     __builtin_amdgcn_sched_barrier(0);
     // RmsNorm (model/rms_norm.rs:56-60): (x * inv) * w
-    const float inv = rms_inv_part(lane < nparts ? 0.0f + stv : 0.0f, H, eps);
 #pragma unroll
     for (int q = 0; q < kXq; ++q) {
       float4 v = xv[q];
-      v.x = (v.x * inv) * wn[q].x;
-      v.y = (v.y * inv) * wn[q].y;
-      v.z = (v.z * inv) * wn[q].z;
-      v.w = (v.w * inv) * wn[q].w;
+      v.x = __fmul_rn(__fmul_rn(v.x, inv), wn[q].x);
+      v.y = __fmul_rn(__fmul_rn(v.y, inv), wn[q].y);
+      v.z = __fmul_rn(__fmul_rn(v.z, inv), wn[q].z);
+      v.w = __fmul_rn(__fmul_rn(v.w, inv), wn[q].w);
       xs4[min((int)threadIdx.x + q * 64 * kQkvWaves, H4 - 1)] = v;  // clamped (see stage_f4)
     }
     lds_barrier();
@@ -1141,12 +1140,11 @@ static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
 }
 
 // nrm.w set (batch 1 only): x is the un-normalised hidden row, normalised
-// inside the projection kernel; ss_out receives the output row's RmsNorm
-// statistics (per-64-column sums of squares) when set.
+// inside the projection kernel with the scale at nrm.inv.
 template <int NB>
 static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64_t* pos,
                        const int32_t* heads, int nsel, float* out, int accumulate,
-                       hipStream_t st, const NormIn& nrm = NormIn{}, float* ss_out = nullptr) {
+                       hipStream_t st, const NormIn& nrm = NormIn{}) {
   const int H = a->hidden, D = a->d, qd = a->nh * D, kvrows = 2 * a->kvd();
   // 1. projections (+ the o_proj row list in the last block)
   const int rows = kvrows + qd;
@@ -1181,12 +1179,12 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
       hipLaunchKernelGGL((attn_qkv_kernel<1, true>), dim3(rows / kQkvWaves + 1),
                          dim3(64 * kQkvWaves), lds, st, a->wkvq, x, batch, H, kvrows, D, a->nh,
                          heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
-                         a->qrows + qd + 1, nrm.w, nrm.stats, nrm.nparts, nrm.eps);
+                         a->qrows + qd + 1, nrm.w, nrm.inv);
     else
       hipLaunchKernelGGL(attn_qkv_kernel<NB>, dim3(rows / kQkvWaves + 1), dim3(64 * kQkvWaves),
                          lds, st, a->wkvq, x, batch, H, kvrows, D, a->nh, heads, nsel, a->y,
                          a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1, nullptr,
-                         nullptr, 0, 0.0f);
+                         nullptr);
     KH_LAUNCHED();
   }
   // 2. split-K decode over the cache and the K/V append (then, for batch > 2 or head
@@ -1232,11 +1230,11 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   KH_LAUNCHED();
   if (groups <= 64)  // few partial rows: 4-wave blocks (16 rows in flight per wave)
     hipLaunchKernelGGL((partials_reduce_kernel<NB, 4>), dim3(ceil_div(H, 64), batch), dim3(64 * 4), 0,
-                       st, partial, H, groups, out, accumulate, a->lens, a->max_seq, ss_out);
+                       st, partial, H, groups, out, accumulate, a->lens, a->max_seq);
   else
     hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch),
                        dim3(64 * kRedWaves), 0, st, partial, H, groups, out, accumulate, a->lens,
-                       a->max_seq, ss_out);
+                       a->max_seq);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -1282,8 +1280,8 @@ extern "C" int kh_sparse_attn_forward(kh_sparse_attn* a, const float* x_dev, int
 
 extern "C" int kh_dejavu_attn_block(const kh_predictor* p, kh_sparse_attn* a, float* hidden_dev,
                                     const float* norm_w_dev, float eps, int k, int32_t* heads_dev,
-                                    float* stats_dev, void* stream) {
-  KH_CHECK_ARG(p && a && hidden_dev && norm_w_dev && heads_dev && stats_dev, "null argument");
+                                    float* norm_ws_dev, void* stream) {
+  KH_CHECK_ARG(p && a && hidden_dev && norm_w_dev && heads_dev && norm_ws_dev, "null argument");
   KH_CHECK_ARG(k >= 1 && k <= a->nh, "k %d not in [1,%d]", k, a->nh);
   KH_CHECK_ARG(predictor_in_dim(p) == a->hidden && predictor_out_dim(p) == a->nh,
                "predictor %d->%d does not match the attention (hidden %d, %d heads)",
@@ -1297,12 +1295,11 @@ extern "C" int kh_dejavu_attn_block(const kh_predictor* p, kh_sparse_attn* a, fl
   hipStream_t st = as_stream(stream);
   NormIn nrm;
   nrm.w = norm_w_dev;
-  nrm.stats = stats_dev;
-  nrm.nparts = a->hidden / 64;
+  nrm.inv = norm_ws_dev;
   nrm.eps = eps;
   int rc = predictor_topk_normed(p, hidden_dev, k, heads_dev, nrm, st);
   if (rc != KH_OK) return rc;
-  rc = attn_launch<1>(a, hidden_dev, 1, nullptr, heads_dev, k, hidden_dev, 1, st, nrm, stats_dev);
+  rc = attn_launch<1>(a, hidden_dev, 1, nullptr, heads_dev, k, hidden_dev, 1, st, nrm);
   if (rc == KH_OK) a->len_host[0] += 1;
   return rc;
 }

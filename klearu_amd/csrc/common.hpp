@@ -286,39 +286,13 @@ __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* ws
   return before + x - v;
 }
 
-// RmsNorm scale 1/sqrt(sum(x^2)/n + eps) (model/rms_norm.rs:49-54) from
-// per-block sums of squares stats[0..nparts): the parts are added with a
-// fixed lane assignment and butterfly, so every wave that calls this gets the
-// same bits.  A whole wave must call it.
-// rms_part issues the lane's loads (so a kernel can request them early) and
-// rms_inv_part finishes; rms_inv(...) == rms_inv_part(rms_part(...), ...).
-__device__ __forceinline__ float rms_part(const float* __restrict__ stats, int nparts) {
-  const int lane = threadIdx.x & 63;
-  if (nparts <= 64) {
-    // one clamped, unconditional load (a loop would wait for it in place)
-    const float s = stats[min(lane, nparts - 1)];
-    return lane < nparts ? 0.0f + s : 0.0f;
-  }
-  float v = 0.0f;
-  for (int i = lane; i < nparts; i += 64) v += stats[i];
-  return v;
-}
-__device__ __forceinline__ float rms_inv_part(float v, int n, float eps) {
-  const float tot = wave_sum(v);
-  const float rms = sqrtf(tot / static_cast<float>(n) + eps);
-  return 1.0f / rms;
-}
-__device__ __forceinline__ float rms_inv(const float* __restrict__ stats, int nparts, int n,
-                                         float eps) {
-  return rms_inv_part(rms_part(stats, nparts), n, eps);
-}
-
-// RmsNorm applied inside a consumer kernel: weight, per-block sums of squares
-// of the row (nparts per row) and eps; w == nullptr means the input is used as is.
+// RmsNorm applied inside a consumer kernel.  The first kernel that reads the
+// un-normalised row (the predictor's layer 1) computes the reference's exact
+// scale 1/sqrt(sum_sq/n + eps) and writes it to inv[row]; the kernels after
+// it read inv.  w == nullptr means the input is used as is.
 struct NormIn {
   const float* w = nullptr;
-  const float* stats = nullptr;
-  int nparts = 0;
+  float* inv = nullptr;
   float eps = 0.0f;
 };
 

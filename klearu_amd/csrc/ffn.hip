@@ -29,6 +29,7 @@
 #include <cstdlib>
 #include <cstring>
 
+#include "exact_sum.hpp"
 #include "gather.hpp"
 #include "mfma.hpp"
 
@@ -228,7 +229,7 @@ __global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
     const float* __restrict__ x, int H, const int32_t* __restrict__ active, int n_active,
     const int32_t* __restrict__ n_active_dev, float* __restrict__ hbuf,
     float* __restrict__ partial, const float* __restrict__ norm_w,
-    const float* __restrict__ stats, int nparts, float eps) {
+    const float* __restrict__ norm_inv) {
   extern __shared__ float4 smem4[];
   __shared__ uint64_t s_tab[32];                                // kExp2Tab
   float4* xs4 = smem4;                                          // [H/4]
@@ -238,11 +239,11 @@ __global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
   // the exp table first (vector loads complete in order, so its store below
   // waits for nothing else)
   const uint64_t tabv = kExp2Tab[threadIdx.x & 31];
-  // Requests in this order: x, the norm weights and the row statistics
-  // (vector loads), then the block's active indices and the device count
-  // (scalar loads).  The weight loads go out as soon as the indices arrive;
-  // x is waited for after them, which costs nothing because vector loads
-  // complete in issue order and x was requested first.
+  // Requests in this order: x and the norm weights (vector loads), then the
+  // block's active indices, the device count and the norm scale (scalar
+  // loads).  The weight loads go out as soon as the indices arrive; x is
+  // waited for after them, which costs nothing because vector loads complete
+  // in issue order and x was requested first.
   const int n4 = H >> 2;
   const float4* __restrict__ xsrc = reinterpret_cast<const float4*>(x);
   constexpr int kXq = kFuMaxH / 4 / (64 * NW);  // float4 of x per thread
@@ -250,13 +251,11 @@ __global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
 #pragma unroll
   for (int q = 0; q < kXq; ++q) xv[q] = xsrc[min((int)threadIdx.x + q * 64 * NW, n4 - 1)];
   // Branch-free requests (without a norm they read x again, unused): a load
-  // inside a branch is waited for at the branch's end.  nparts = H/64 <= 64,
-  // one statistic per lane.
+  // inside a branch is waited for at the branch's end.
   const float4* __restrict__ nsrc = reinterpret_cast<const float4*>(norm_w ? norm_w : x);
-  const float* __restrict__ ssrc = norm_w ? stats : x;
 #pragma unroll
   for (int q = 0; q < kXq; ++q) wn[q] = nsrc[min((int)threadIdx.x + q * 64 * NW, n4 - 1)];
-  const float st = ssrc[min(lane, max(nparts, 1) - 1)];
+  const float inv_ld = *(norm_w ? norm_inv : x);  // unconditional scalar load
   int cand[NW];
 #pragma unroll
   for (int k = 0; k < NW; ++k) cand[k] = active[min(first + k, n_active - 1)];
@@ -288,15 +287,15 @@ __global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
     wd[k] = ld_stream(reinterpret_cast<const uint4*>(WdT + (size_t)nid[k] * H + col));
   __builtin_amdgcn_sched_barrier(0);
   if (norm_w) {
-    // RmsNorm of the hidden row (x * inv) * w, inv from the row's per-block
-    // sums of squares exactly as the predictor computes it
-    const float inv = rms_inv_part(lane < nparts ? 0.0f + st : 0.0f, H, eps);
+    // RmsNorm of the hidden row (model/rms_norm.rs:56-60): (x * inv) * w with
+    // the exact scale the predictor's layer 1 computed for this row
+    const float inv = inv_ld;
 #pragma unroll
     for (int q = 0; q < kXq; ++q) {
-      xv[q].x = (xv[q].x * inv) * wn[q].x;
-      xv[q].y = (xv[q].y * inv) * wn[q].y;
-      xv[q].z = (xv[q].z * inv) * wn[q].z;
-      xv[q].w = (xv[q].w * inv) * wn[q].w;
+      xv[q].x = __fmul_rn(__fmul_rn(xv[q].x, inv), wn[q].x);
+      xv[q].y = __fmul_rn(__fmul_rn(xv[q].y, inv), wn[q].y);
+      xv[q].z = __fmul_rn(__fmul_rn(xv[q].z, inv), wn[q].z);
+      xv[q].w = __fmul_rn(__fmul_rn(xv[q].w, inv), wn[q].w);
     }
   }
   // Unconditional stores (a thread past the end rewrites the last float4 with
@@ -350,42 +349,43 @@ __global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
 }
 
 // RmsNorm::forward (crates/klearu-llm/src/model/rms_norm.rs:43-64): one block
-// of 1024 threads per row; each thread loads its (<= 4) float4s before reducing.
-__global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__ x,
-                                                       const float* __restrict__ w, int n,
-                                                       float eps, float* __restrict__ y) {
-  __shared__ float part[16];
+// of kRnWaves waves per row.  The row's squares are staged in LDS and summed in
+// the reference's sequential order (exact_seq_sum); then y = (x * inv) * w.
+constexpr int kRnWaves = 8;
+constexpr int kRnMaxChunks = 64;  // rows up to 8192 (larger rows take rmsnorm_seq_kernel)
+constexpr int kRnMaxN = kEsChunk * kRnMaxChunks;
+
+__global__ __launch_bounds__(64 * kRnWaves) void rmsnorm_kernel(const float* __restrict__ x,
+                                                               const float* __restrict__ w, int n,
+                                                               float eps, float* __restrict__ y) {
+  __shared__ float sq[kRnMaxN];
+  __shared__ EsLds<kRnMaxChunks> es;
   const float* xr = x + (size_t)blockIdx.x * n;
   float* yr = y + (size_t)blockIdx.x * n;
-  const bool vec = (n & 3) == 0;
-  float s = 0.0f;
-  if (vec) {
-    const int n4 = n >> 2;
-    float4 v[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int i = threadIdx.x + q * 1024;
-      v[q] = i < n4 ? reinterpret_cast<const float4*>(xr)[i] : make_float4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      s = fmaf(v[q].x, v[q].x, fmaf(v[q].y, v[q].y, fmaf(v[q].z, v[q].z, fmaf(v[q].w, v[q].w, s))));
-    for (int i = threadIdx.x + 4 * 1024; i < n4; i += 1024) {
-      const float4 t = reinterpret_cast<const float4*>(xr)[i];
-      s = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, s))));
-    }
-  } else {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) s = fmaf(xr[i], xr[i], s);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const float v = xr[i];
+    sq[i] = __fmul_rn(v, v);
   }
-  s = wave_sum(s);
-  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  lds_barrier();
+  const float inv = rms_inv_exact(exact_seq_sum<kRnWaves, kRnMaxChunks>(sq, n, 0.0f, es), n, eps);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = __fmul_rn(__fmul_rn(xr[i], inv), w[i]);
+}
+
+// Rows longer than kRnMaxN: one lane runs the sequential sum.
+__global__ __launch_bounds__(256) void rmsnorm_seq_kernel(const float* __restrict__ x,
+                                                          const float* __restrict__ w, int n,
+                                                          float eps, float* __restrict__ y) {
+  __shared__ float s_inv;
+  const float* xr = x + (size_t)blockIdx.x * n;
+  float* yr = y + (size_t)blockIdx.x * n;
+  if (threadIdx.x == 0) {
+    float s = 0.0f;
+    for (int i = 0; i < n; ++i) s = __fadd_rn(s, __fmul_rn(xr[i], xr[i]));
+    s_inv = rms_inv_exact(s, n, eps);
+  }
   __syncthreads();
-  float tot = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) tot += part[i];
-  const float rms = sqrtf(tot / static_cast<float>(n) + eps);
-  const float inv = 1.0f / rms;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = (xr[i] * inv) * w[i];
+  const float inv = s_inv;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = __fmul_rn(__fmul_rn(xr[i], inv), w[i]);
 }
 
 }  // namespace kh
@@ -578,10 +578,10 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
   // few partial rows (at most 64: 4 waves x 16 rows in flight each): 4-wave blocks
   if (groups <= 64)
     hipLaunchKernelGGL((partials_reduce_kernel<NB, 4>), dim3(ceil_div(H, 64), batch), dim3(64 * 4), 0,
-                       st, f->partial, H, groups, y, accumulate, nullptr, 0, nullptr);
+                       st, f->partial, H, groups, y, accumulate, nullptr, 0);
   else
     hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch), dim3(64 * kRedWaves),
-                       0, st, f->partial, H, groups, y, accumulate, nullptr, 0, nullptr);
+                       0, st, f->partial, H, groups, y, accumulate, nullptr, 0);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -591,11 +591,10 @@ static bool ffn_fused_ok(const kh_sparse_ffn* f, int64_t batch) {
 }
 
 // Single-token fused FFN + ordered reduce.  With nrm.w set, x is the
-// un-normalised hidden row (RmsNorm applied in the kernel); with stats_out
-// set, the reduce also writes the per-block sums of squares of y.
+// un-normalised hidden row, normalised in the kernel with the scale at nrm.inv.
 static int ffn_fused_launch(const kh_sparse_ffn* f, const float* x, const int32_t* active,
                             int n_active, const int32_t* n_active_dev, float* y, int accumulate,
-                            const NormIn& nrm, float* stats_out, hipStream_t st) {
+                            const NormIn& nrm, hipStream_t st) {
   const int H = f->hidden;
   // Four neurons per block when the hidden size allows it (a wave's down
   // slice is at most 512 columns) and eight would leave CUs idle: the 1.1B
@@ -615,14 +614,14 @@ static int ffn_fused_launch(const kh_sparse_ffn* f, const float* x, const int32_
   if (small)
     hipLaunchKernelGGL(ffn_fused1_kernel<kFuWavesMin>, dim3(blocks), dim3(64 * kFuWavesMin), lds, st,
                        f->wgu, f->wdt, x, H, active, n_active, n_active_dev, f->hbuf, f->partial,
-                       nrm.w, nrm.stats, nrm.nparts, nrm.eps);
+                       nrm.w, nrm.inv);
   else
     hipLaunchKernelGGL(ffn_fused1_kernel<kFuWaves>, dim3(blocks), dim3(64 * kFuWaves), lds, st,
                        f->wgu, f->wdt, x, H, active, n_active, n_active_dev, f->hbuf, f->partial,
-                       nrm.w, nrm.stats, nrm.nparts, nrm.eps);
+                       nrm.w, nrm.inv);
   KH_LAUNCHED();
   hipLaunchKernelGGL(partials_reduce_kernel<1>, dim3(ceil_div(H, 64), 1), dim3(64 * kRedWaves), 0,
-                     st, f->partial, H, blocks, y, accumulate, nullptr, 0, stats_out);
+                     st, f->partial, H, blocks, y, accumulate, nullptr, 0);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -649,7 +648,7 @@ extern "C" int kh_sparse_ffn_forward(const kh_sparse_ffn* f, const float* x_dev,
   const int b = static_cast<int>(batch);
   if (ffn_fused_ok(f, batch))
     return ffn_fused_launch(f, x_dev, active_dev, n_active, n_active_dev, y_dev, accumulate,
-                            NormIn{}, nullptr, st);
+                            NormIn{}, st);
   switch (ffn_tmpl(batch)) {
     case 1: return ffn_launch<1>(f, x_dev, b, active_dev, n_active, n_active_dev, y_dev, accumulate, st);
     case 2: return ffn_launch<2>(f, x_dev, b, active_dev, n_active, n_active_dev, y_dev, accumulate, st);
@@ -675,40 +674,20 @@ extern "C" int kh_rmsnorm(const float* x_dev, const float* w_dev, int64_t batch,
   KH_CHECK_ARG(x_dev && w_dev && y_dev, "null argument");
   KH_CHECK_ARG(batch >= 0 && n > 0, "bad shape");
   if (batch == 0) return KH_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(batch), dim3(1024), 0, as_stream(stream), x_dev, w_dev,
-                     n, eps, y_dev);
-  KH_LAUNCHED();
-  return KH_OK;
-}
-
-namespace kh {
-// Per-block (64 columns) sums of squares of each row: the RmsNorm statistics
-// consumed by kernels that apply the norm themselves (rms_inv).
-__global__ __launch_bounds__(64) void rms_stats_kernel(const float* __restrict__ x, int n,
-                                                      float* __restrict__ stats) {
-  const int b = blockIdx.y;
-  const int j = blockIdx.x * 64 + threadIdx.x;
-  const float v = j < n ? x[(size_t)b * n + j] : 0.0f;
-  const float sq = wave_sum(v * v);
-  if (threadIdx.x == 0) stats[(size_t)b * gridDim.x + blockIdx.x] = sq;
-}
-}  // namespace kh
-
-extern "C" int kh_rms_stats(const float* x_dev, int64_t batch, int n, float* stats_dev,
-                            void* stream) {
-  KH_CHECK_ARG(x_dev && stats_dev, "null argument");
-  KH_CHECK_ARG(batch >= 0 && batch <= 65535 && n > 0, "bad shape");
-  if (batch == 0) return KH_OK;
-  hipLaunchKernelGGL(rms_stats_kernel, dim3(ceil_div(n, 64), batch), dim3(64), 0,
-                     as_stream(stream), x_dev, n, stats_dev);
+  if (n <= kRnMaxN)
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(batch), dim3(64 * kRnWaves), 0, as_stream(stream), x_dev,
+                       w_dev, n, eps, y_dev);
+  else
+    hipLaunchKernelGGL(rmsnorm_seq_kernel, dim3(batch), dim3(256), 0, as_stream(stream), x_dev,
+                       w_dev, n, eps, y_dev);
   KH_LAUNCHED();
   return KH_OK;
 }
 
 extern "C" int kh_dejavu_mlp_block(const kh_predictor* p, const kh_sparse_ffn* f, float* hidden_dev,
                                    const float* norm_w_dev, float eps, int k, int32_t* active_dev,
-                                   float* stats_dev, void* stream) {
-  KH_CHECK_ARG(p && f && hidden_dev && norm_w_dev && active_dev && stats_dev, "null argument");
+                                   float* norm_ws_dev, void* stream) {
+  KH_CHECK_ARG(p && f && hidden_dev && norm_w_dev && active_dev && norm_ws_dev, "null argument");
   KH_CHECK_ARG(k >= 1 && k <= f->inter, "k %d not in [1,%d]", k, f->inter);
   KH_CHECK_ARG(predictor_in_dim(p) == f->hidden && predictor_out_dim(p) == f->inter,
                "predictor %d->%d does not match the FFN (hidden %d, intermediate %d)",
@@ -718,10 +697,9 @@ extern "C" int kh_dejavu_mlp_block(const kh_predictor* p, const kh_sparse_ffn* f
   hipStream_t st = as_stream(stream);
   NormIn nrm;
   nrm.w = norm_w_dev;
-  nrm.stats = stats_dev;
-  nrm.nparts = ceil_div(f->hidden, 64);
+  nrm.inv = norm_ws_dev;
   nrm.eps = eps;
   int rc = predictor_topk_normed(p, hidden_dev, k, active_dev, nrm, st);
   if (rc != KH_OK) return rc;
-  return ffn_fused_launch(f, hidden_dev, active_dev, k, nullptr, hidden_dev, 1, nrm, stats_dev, st);
+  return ffn_fused_launch(f, hidden_dev, active_dev, k, nullptr, hidden_dev, 1, nrm, st);
 }

@@ -339,8 +339,7 @@ __global__ __launch_bounds__(64 * RW) void partials_reduce_kernel(const float* _
                                                                     float* __restrict__ y,
                                                                     int accumulate,
                                                                     int32_t* __restrict__ bump,
-                                                                    int bump_limit,
-                                                                    float* __restrict__ ss_out) {
+                                                                    int bump_limit) {
   __shared__ float sums[RW][64];
   const int b = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -367,12 +366,6 @@ __global__ __launch_bounds__(64 * RW) void partials_reduce_kernel(const float* _
     for (int w = 0; w < RW; ++w) tot += sums[w][lane];
     const float yn = accumulate ? y0 + tot : tot;
     if (j < H) y[(size_t)b * H + j] = yn;
-    // Sum of squares of this block's 64 outputs: the RmsNorm statistics of
-    // the updated row (rms_inv adds the blocks' values in a fixed order).
-    if (ss_out) {
-      const float sq = wave_sum(j < H ? yn * yn : 0.0f);
-      if (lane == 0) ss_out[(size_t)b * gridDim.x + blockIdx.x] = sq;
-    }
   }
   // Optional per-row counter advanced once the row's output is complete
   // (the KV-cache length of decode attention).

@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "exact_sum.hpp"
 
 namespace kh {
 
@@ -183,13 +184,21 @@ constexpr int kL1LdsIn = 4096;
 constexpr int kL1LdsBytes = (kL1Chains + 1) * kL1LdsIn * 4;  // products + x
 
 // With norm_w set, x is the un-normalised hidden row and the kernel applies
-// RmsNorm first: (x * inv) * norm_w with inv from the per-block sums of squares
-// `stats` (rms_inv), as every other consumer of the row computes it.
+// RmsNorm first (model/rms_norm.rs:43-64): the reference's sequential sum of
+// squares (exact_seq_sum, run by every wave while the weight loads are in
+// flight), its scale, then (x * inv) * norm_w.  Block 0 stores the scale in
+// inv_out[b] for the kernels that consume the same normalised row later.
+// The norm requires n_in % 4 == 0 (host-checked).
+constexpr int kL1EsChunks = kL1LdsIn / kEsChunk;
+static_assert(sizeof(float) * kL1LdsIn + sizeof(EsLds<kL1EsChunks>) <=
+                  sizeof(float4) * (kL1LdsIn / 4) * kL1Chains,
+              "squares and the exact-sum scratch fit in the products region");
+
 template <typename W>
 __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
     const W* __restrict__ Wb, const float* __restrict__ bias, const float* __restrict__ x,
     int n_in, int hid, float* __restrict__ h, const float* __restrict__ norm_w,
-    const float* __restrict__ stats, int nparts, float eps) {
+    float* __restrict__ inv_out, float eps) {
   using B8 = Blk8<W>;
   using V = typename B8::V;
   constexpr int SPP = kL1LdsIn / kL1Stage / kL1Prod;  // stages per producer
@@ -197,6 +206,10 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
   extern __shared__ float4 lds4[];
   float4(*P)[kL1Chains] = reinterpret_cast<float4(*)[kL1Chains]>(lds4);  // [n_in/4][chain]
   float* xs = reinterpret_cast<float*>(lds4 + (kL1LdsIn / 4) * kL1Chains);
+  // until the norm is known the products region holds the squares and the
+  // exact-sum scratch
+  float* sq = reinterpret_cast<float*>(lds4);
+  auto& es = *reinterpret_cast<EsLds<kL1EsChunks>*>(sq + kL1LdsIn);
   const int b = blockIdx.y;
   const int c0 = blockIdx.x * kL1Chains;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -208,31 +221,28 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
   // every weight load: no wave waits for another's loads before the barrier.
   V pre[SPP][kL1Q];
   float bv = 0.0f;
+  float4 xv[kXq], wn[kXq];
   if (wave == 0) {
     bv = bias[min(c0 + (lane & (kL1Chains - 1)), hid - 1)];
     if ((n_in & 3) == 0) {
-      float4 xv[kXq];
 #pragma unroll
       for (int q = 0; q < kXq; ++q) xv[q] = reinterpret_cast<const float4*>(xr)[min(lane + 64 * q, n4 - 1)];
       if (norm_w) {
-        float4 wn[kXq];
 #pragma unroll
         for (int q = 0; q < kXq; ++q) wn[q] = reinterpret_cast<const float4*>(norm_w)[min(lane + 64 * q, n4 - 1)];
-        const float inv = rms_inv(stats + (size_t)b * nparts, nparts, n_in, eps);
+        // squares as Rust forms them (v * v, rounded) for the sequential sum
 #pragma unroll
-        for (int q = 0; q < kXq; ++q) {
-          xv[q].x = (xv[q].x * inv) * wn[q].x;
-          xv[q].y = (xv[q].y * inv) * wn[q].y;
-          xv[q].z = (xv[q].z * inv) * wn[q].z;
-          xv[q].w = (xv[q].w * inv) * wn[q].w;
-        }
+        for (int q = 0; q < kXq; ++q)  // clamped, unconditional (see stage_f4)
+          reinterpret_cast<float4*>(sq)[min(lane + 64 * q, n4 - 1)] =
+              make_float4(__fmul_rn(xv[q].x, xv[q].x), __fmul_rn(xv[q].y, xv[q].y),
+                          __fmul_rn(xv[q].z, xv[q].z), __fmul_rn(xv[q].w, xv[q].w));
+      } else {
+#pragma unroll
+        for (int q = 0; q < kXq; ++q)  // clamped, unconditional (see stage_f4)
+          reinterpret_cast<float4*>(xs)[min(lane + 64 * q, n4 - 1)] = xv[q];
       }
-#pragma unroll
-      for (int q = 0; q < kXq; ++q)  // clamped, unconditional (see stage_f4)
-        reinterpret_cast<float4*>(xs)[min(lane + 64 * q, n4 - 1)] = xv[q];
     } else {
-      const float inv = norm_w ? rms_inv(stats + (size_t)b * nparts, nparts, n_in, eps) : 1.0f;
-      for (int j = lane; j < n_in; j += 64) xs[j] = norm_w ? (xr[j] * inv) * norm_w[j] : xr[j];
+      for (int j = lane; j < n_in; j += 64) xs[j] = xr[j];
     }
   } else {
     const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
@@ -248,6 +258,24 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
       }
   }
   lds_barrier();
+  if (norm_w) {
+    // sum_sq over the row in the reference's order (rms_norm.rs:48-51)
+    const float ss = exact_seq_sum<kL1Prod + 1, kL1EsChunks>(sq, n_in, 0.0f, es);
+    const float inv = rms_inv_exact(ss, n_in, eps);
+    if (wave == 0) {
+#pragma unroll
+      for (int q = 0; q < kXq; ++q) {
+        float4 v = xv[q];
+        v.x = __fmul_rn(__fmul_rn(v.x, inv), wn[q].x);
+        v.y = __fmul_rn(__fmul_rn(v.y, inv), wn[q].y);
+        v.z = __fmul_rn(__fmul_rn(v.z, inv), wn[q].z);
+        v.w = __fmul_rn(__fmul_rn(v.w, inv), wn[q].w);
+        reinterpret_cast<float4*>(xs)[min(lane + 64 * q, n4 - 1)] = v;
+      }
+      if (blockIdx.x == 0 && lane == 0) inv_out[b] = inv;
+    }
+    lds_barrier();
+  }
   // products of stage p + kL1Prod*i; loads arrive in issue order, so each
   // stage waits only for its own weights
   auto make = [&](int i) {
@@ -1003,6 +1031,10 @@ static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* 
   const W* w1 = static_cast<const W*>(p->w1b);
   const W* w2 = static_cast<const W*>(p->w2b);
   const int l1_stages = ceil_div(p->in_dim, kL1Stage);
+  if (nrm.w && (p->in_dim % 4 != 0 || !nrm.inv)) {
+    set_error("the fused RmsNorm needs an input size that is a multiple of 4 and a scale buffer");
+    return KH_ERR_ARG;
+  }
   static bool l1_attr = false;
   if (!l1_attr) {
     KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pred_l1_lds_kernel<uint16_t>),
@@ -1014,7 +1046,7 @@ static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* 
   if (p->in_dim <= kL1LdsIn)
     hipLaunchKernelGGL(pred_l1_lds_kernel<W>, dim3(ceil_div(p->hid, kL1Chains), batch),
                        dim3(kL1Threads), kL1LdsBytes, st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf,
-                       nrm.w, nrm.stats, nrm.nparts, nrm.eps);
+                       nrm.w, nrm.inv, nrm.eps);
   else if (nrm.w) {
     set_error("the fused RmsNorm supports predictor inputs up to %d", kL1LdsIn);
     return KH_ERR_UNSUPPORTED;

@@ -226,26 +226,17 @@ def rmsnorm(x, w, eps: float, stream=None) -> torch.Tensor:
     return y
 
 
-def rms_stats(x, stream=None) -> torch.Tensor:
-    """Per-64-column sums of squares of each row of x [batch, n] (RmsNorm statistics)."""
-    x = to_device(x, np.float32)
-    x2 = x.reshape(-1, x.shape[-1])
-    nparts = (x2.shape[1] + 63) // 64
-    out = torch.empty(x2.shape[0], nparts, dtype=torch.float32, device=x.device)
-    _lib.call("kh_rms_stats", ptr(x2), x2.shape[0], x2.shape[1], ptr(out), stream_ptr(stream))
-    return out
-
-
 def mlp_block(predictor: SparsityPredictor, mlp: Mlp, hidden: torch.Tensor, norm_w: torch.Tensor, eps: float,
-              k: int, active: torch.Tensor | None = None, stats: torch.Tensor | None = None, stream=None):
+              k: int, active: torch.Tensor | None = None, norm_ws: torch.Tensor | None = None, stream=None):
     """One decode step of the Deja Vu MLP block (crates/klearu-llm/src/sparse/mod.rs:115-142), in place:
     hidden += forward_sparse(mlp, RmsNorm(hidden), predictor.select_top_k(RmsNorm(hidden), k)).
-    `stats` carries the RmsNorm statistics from one block to the next (computed when None).
-    Returns (active ids ascending, stats of the updated hidden)."""
-    if stats is None:
-        stats = rms_stats(hidden, stream)
+    The norm, and so the selection, is bit-identical to the reference's.  `norm_ws` (one float on
+    the device, allocated when None) receives the row's RmsNorm scale.  Returns the active ids
+    (ascending)."""
+    if norm_ws is None:
+        norm_ws = torch.empty(1, dtype=torch.float32, device=hidden.device)
     if active is None:
         active = torch.empty(k, dtype=torch.int32, device=hidden.device)
     _lib.call("kh_dejavu_mlp_block", predictor._h, mlp._h, ptr(hidden), ptr(norm_w), float(eps), k, ptr(active),
-              ptr(stats), stream_ptr(stream))
-    return active, stats
+              ptr(norm_ws), stream_ptr(stream))
+    return active

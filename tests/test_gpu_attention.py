@@ -220,42 +220,38 @@ def test_rejects_bad_shapes(kh, orc):
                         np.zeros((64, 192), np.uint16), 16)   # 3 heads over 2 kv heads
 
 
-def test_attn_block_chained(kh, orc):
-    """kh_dejavu_attn_block over three decode steps, the RmsNorm statistics
-    carried from step to step, against the oracle's rmsnorm -> head predictor
-    -> top-k -> sparse attention -> residual.  The fused norm sums squares in
-    another order, so the predictor sees inputs within rounding of the
-    oracle's: selections may differ only at heads whose oracle score lies
-    within 1e-6 relative of the k-th; outputs within the BF16-weight tolerance."""
+@pytest.mark.parametrize("H,nh,nkv,d,R,k,pre,steps", [
+    (4096, 32, 32, 128, 128, 16, 2000, 4),   # cfg4 (7B): 32 heads x 128, cache ~2048, top 50% of heads
+    (512, 8, 4, 64, 32, 3, 20, 3),           # GQA, small
+])
+def test_attn_block_chained(kh, orc, H, nh, nkv, d, R, k, pre, steps):
+    """kh_dejavu_attn_block over several decode steps against the oracle's
+    RmsNorm -> head predictor -> select_top_k -> sparse attention -> residual
+    (crates/klearu-llm/src/sparse/mod.rs:56-112).  For each step the oracle
+    runs on the hidden row the GPU held before the block: the head set must
+    equal the oracle's own top-k exactly, and the updated row must match the
+    oracle's residual from the oracle's selection within the BF16-weight
+    tolerance."""
     from klearu_amd.attention import attn_block
     from klearu_amd.dejavu import SparsityPredictor
-    rng = np.random.default_rng(41)
-    H, nh, nkv, d, R, k = 512, 8, 4, 64, 32, 3
-    c = Case(orc, rng, H, nh, nkv, d, 64, 1, 20)
+    rng = np.random.default_rng(41 + H)
+    c = Case(orc, rng, H, nh, nkv, d, pre + steps + 4, 1, pre)
     w1 = orc.bf16_from_f32(rng.normal(0, 0.05, (R, H)).astype(np.float32))
     w2 = orc.bf16_from_f32(rng.normal(0, 0.3, (nh, R)).astype(np.float32))
     b1 = rng.normal(0, 0.1, R).astype(np.float32)
     b2 = rng.normal(0, 0.1, nh).astype(np.float32)
     p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
     wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
-    ref = rng.standard_normal(H).astype(np.float32)
-    hd = torch.from_numpy(ref.copy()).cuda()
+    hd = torch.from_numpy(rng.standard_normal(H).astype(np.float32)).cuda()
     wnd = torch.from_numpy(wn).cuda()
-    stats = None
-    for step in range(3):
-        heads, stats = attn_block(p, c.attn, hd, wnd, 1e-5, k, stats=stats)
-        norm = orc.rmsnorm(ref, wn, 1e-5)
+    for step in range(steps):
+        h_in = hd.cpu().numpy().copy()
+        heads = attn_block(p, c.attn, hd, wnd, 1e-5, k)
+        norm = orc.rmsnorm(h_in, wn, 1e-5)
         scores, _ = orc.predictor_predict(w1, b1, w2, b2, norm)
         sel = np.sort(orc.select_top_k(scores, k))
         got = heads.cpu().numpy()
-        assert np.all(np.diff(got) > 0)
-        kth = np.sort(scores)[::-1][k - 1]
-        diff = np.setxor1d(got, sel)
-        assert np.all(np.abs(scores[diff] - kth) <= 1e-6 * abs(kth)), (step, diff)
-        want = ref + c.oracle_step(0, norm, got.tolist())
-        out = hd.cpu().numpy()
-        close(out, want, f"step {step}")
-        ref = out.astype(np.float32)
-        np.testing.assert_allclose(stats.cpu().numpy().sum(), float(np.sum(out.astype(np.float64) ** 2)),
-                                   rtol=1e-5)
-    assert c.attn.current_len(0) == 23
+        np.testing.assert_array_equal(got, sel)
+        want = h_in + c.oracle_step(0, norm, sel.tolist())
+        close(hd.cpu().numpy(), want, f"step {step}")
+    assert c.attn.current_len(0) == pre + steps

@@ -286,52 +286,113 @@ def test_sparse_ffn_rejects_bad_shapes(kh, orc):
                                 torch.empty_like(xd))
 
 
-def test_rmsnorm(kh, orc):
+def _rms_rows(rng):
+    """Rows for the RmsNorm parity test, with the cases that stress the exact
+    parallel sum of squares: every chunk's speculative window missing (a
+    running sum stuck at 2^24 while the exact sum grows: each square 1.0 is a
+    tie that rounds back down), squares just above half an ulp (each rounds
+    up), zeros, tiny and huge magnitudes, a partial last chunk."""
+    rows = {}
+    rows["normal 4096"] = rng.standard_normal(4096)
+    rows["normal 2048"] = rng.standard_normal(2048)
+    rows["normal 8192"] = rng.standard_normal(8192)
+    rows["ragged 1000"] = rng.standard_normal(1000)
+    rows["ragged 130"] = rng.standard_normal(130)
+    rows["single"] = np.array([3.0])
+    stuck = np.ones(4096)
+    stuck[0] = 4096.0  # 4096^2 = 2^24, then + 1.0 ties back to 2^24 every step
+    rows["ties stuck at 2^24"] = stuck
+    up = np.full(4096, np.sqrt(1.0000001))
+    up[0] = 4096.0
+    rows["round-up drift"] = up
+    z = rng.standard_normal(4096)
+    z[:700] = 0.0
+    rows["leading zeros"] = z
+    rows["all zero"] = np.zeros(4096)
+    rows["tiny"] = rng.standard_normal(4096) * 1e-20
+    rows["huge"] = rng.standard_normal(4096) * 1e17
+    rows["wide range"] = rng.standard_normal(4096) * np.exp(rng.uniform(-20, 20, 4096))
+    rows["long 12288"] = rng.standard_normal(12288)   # past the parallel kernel's limit
+    return {k: v.astype(np.float32) for k, v in rows.items()}
+
+
+def test_rmsnorm_bit_exact(kh, orc):
+    """kh_rmsnorm against the oracle's RmsNorm::forward (rms_norm.rs:43-64):
+    bit-identical, including rows that force the sequential fallback of every
+    chunk, and a batch of 16 rows (the batched decode path's norm)."""
     from klearu_amd.dejavu import rmsnorm
     rng = np.random.default_rng(3)
-    x = rng.standard_normal((4, 4096)).astype(np.float32)
+    for name, x in _rms_rows(rng).items():
+        w = rng.uniform(0.5, 1.5, x.size).astype(np.float32)
+        got = rmsnorm(torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), 1e-5).cpu().numpy()
+        want = orc.rmsnorm(x, w, 1e-5)
+        print(f"{name}: {int(np.sum(got.view(np.uint32) != want.view(np.uint32)))} differing words")
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=name)
+    xb = rng.standard_normal((16, 4096)).astype(np.float32) * rng.uniform(0.1, 10, (16, 1)).astype(np.float32)
     w = rng.uniform(0.5, 1.5, 4096).astype(np.float32)
-    got = rmsnorm(torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), 1e-5).cpu().numpy()
-    for b in range(4):
-        np.testing.assert_allclose(got[b], orc.rmsnorm(x[b], w, 1e-5), rtol=1e-5, atol=1e-6)
+    got = rmsnorm(torch.from_numpy(xb).cuda(), torch.from_numpy(w).cuda(), 1e-6).cpu().numpy()
+    for b in range(16):
+        np.testing.assert_array_equal(got[b].view(np.uint32), orc.rmsnorm(xb[b], w, 1e-6).view(np.uint32))
 
 
-def test_mlp_block_three_layers(kh, orc):
-    """kh_dejavu_mlp_block chained over three layers (stats carried between
-    blocks) against the oracle's rmsnorm -> predictor -> top-k -> SwiGLU ->
-    residual.  The fused norm sums squares in a different order, so the
-    predictor sees inputs within rounding of the oracle's: the selections must
-    agree except for neurons whose oracle score lies within 1e-6 relative of
-    the k-th score; outputs within the BF16-weight tolerance."""
+@pytest.mark.parametrize("H,I,R,k,layers", [
+    (4096, 11008, 256, 1652, 4),   # cfg3 (7B): hidden 4096, 11008 neurons, rank 256, top 15%
+    (2048, 5632, 128, 564, 3),     # cfg2 (1.1B): top 10%
+])
+def test_mlp_block_chained_exact(kh, orc, H, I, R, k, layers):
+    """kh_dejavu_mlp_block chained over several layers against the oracle's
+    RmsNorm -> predictor -> select_top_k -> forward_sparse -> residual
+    (crates/klearu-llm/src/sparse/mod.rs:115-142).  For each layer, the
+    oracle runs on the hidden row the GPU held before the block: the active
+    set must equal the oracle's own top-k exactly (no boundary swaps), and the
+    updated row must match the oracle's residual, computed from the oracle's
+    selection, within the BF16-weight tolerance."""
     from klearu_amd.dejavu import Mlp, SparsityPredictor, mlp_block
-    rng = np.random.default_rng(31)
-    H, I, R, k = 1024, 2816, 64, 423
+    rng = np.random.default_rng(31 + H)
+    wg, wu, wd, _, _ = _ffn_case(orc, rng, H, I, k, 1)
+    mlp = Mlp(wg, wu, wd, max_batch=1)
     hidden = rng.standard_normal(H).astype(np.float32)
     wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
     hd = torch.from_numpy(hidden.copy()).cuda()
     wnd = torch.from_numpy(wn).cuda()
-    stats = None
-    ref = hidden.copy()
-    for layer in range(3):
-        wg, wu, wd, _, _ = _ffn_case(orc, rng, H, I, k, 1)
+    ws = torch.empty(1, dtype=torch.float32, device="cuda")
+    for layer in range(layers):
         w1, b1, w2, b2 = make_predictor(orc, rng, H, R, I, bias=True)
         p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
-        mlp = Mlp(wg, wu, wd, max_batch=1)
-        act, stats = mlp_block(p, mlp, hd, wnd, 1e-5, k, stats=stats)
-        norm = orc.rmsnorm(ref, wn, 1e-5)
+        h_in = hd.cpu().numpy().copy()
+        act = mlp_block(p, mlp, hd, wnd, 1e-5, k, norm_ws=ws)
+        norm = orc.rmsnorm(h_in, wn, 1e-5)
         scores, _ = orc.predictor_predict(w1, b1, w2, b2, norm)
         sel = np.sort(orc.select_top_k(scores, k))
         got = act.cpu().numpy()
-        kth = np.sort(scores)[::-1][k - 1]
-        diff = np.setxor1d(got, sel)
-        assert np.all(np.abs(scores[diff] - kth) <= 1e-6 * abs(kth)), (layer, diff)
-        y, _ = orc.sparse_mlp_forward_bf16(wg, wu, wd, norm, got.astype(np.int64))
-        ref = ref + y
+        print(f"layer {layer}: {np.setxor1d(got, sel).size} ids differ")
+        np.testing.assert_array_equal(got, sel)
+        y, _ = orc.sparse_mlp_forward_bf16(wg, wu, wd, norm, sel.astype(np.int64))
+        want = h_in + y
         out = hd.cpu().numpy()
-        scale = float(np.max(np.abs(ref)))
-        print(f"layer {layer}: max-abs {float(np.max(np.abs(out - ref))):.3e} (max |hidden| {scale:.3e}), "
-              f"{diff.size} boundary swaps")
-        np.testing.assert_allclose(out, ref, rtol=RTOL, atol=1e-4 * scale)
-        ref = out.astype(np.float32)   # continue from the GPU state (selections may differ at ties)
-        np.testing.assert_allclose(stats.cpu().numpy().sum(), float(np.sum(out.astype(np.float64) ** 2)),
-                                   rtol=1e-5)
+        scale = float(np.max(np.abs(want)))
+        print(f"layer {layer}: max-abs {float(np.max(np.abs(out - want))):.3e} (max |hidden| {scale:.3e})")
+        np.testing.assert_allclose(out, want, rtol=RTOL, atol=1e-4 * scale)
+
+
+def test_batched_norm_select_union_exact(kh, orc):
+    """The batch-16 decode path: kh_rmsnorm over 16 rows, then the predictor's
+    top-k of every row and their union, against the oracle per row (exact)."""
+    from klearu_amd.dejavu import SparsityPredictor, rmsnorm
+    rng = np.random.default_rng(77)
+    H, R, I, k, B = 4096, 256, 11008, 1652, 16
+    w1, b1, w2, b2 = make_predictor(orc, rng, H, R, I, bias=True)
+    p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
+    x = rng.standard_normal((B, H)).astype(np.float32)
+    wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    nd = rmsnorm(torch.from_numpy(x).cuda(), torch.from_numpy(wn).cuda(), 1e-5)
+    ids, uni, cnt = p.select_top_k_union(nd, k)
+    uni = uni[:int(cnt.item())]
+    want_u = set()
+    for b in range(B):
+        norm = orc.rmsnorm(x[b], wn, 1e-5)
+        scores, _ = orc.predictor_predict(w1, b1, w2, b2, norm)
+        sel = np.sort(orc.select_top_k(scores, k))
+        np.testing.assert_array_equal(ids[b].cpu().numpy(), sel)
+        want_u |= set(sel.tolist())
+    np.testing.assert_array_equal(uni.cpu().numpy(), np.array(sorted(want_u), np.int32))
