@@ -6,9 +6,9 @@
 // A dependent chain of 4096 adds costs about 10 us on one lane.  The block here
 // returns the same bits with most of the chain run in parallel:
 //
-//  1. The terms are cut into chunks of kEsChunk.  A guess of the running sum at
-//     the start of chunk c is formed from the chunk sums (f32, any order) with
-//     the prefix in f64, rounded to f32.  It is only a guess.
+//  1. The terms are cut into chunks of M.  A guess of the running sum at the
+//     start of chunk c is s0 plus the chunk sums before it (f32, any order).
+//     It is only a guess.
 //  2. Every chunk c >= 1 is run sequentially from kEsWin consecutive f32 start
 //     values centred on its guess, one lane per start value; chunk 0 runs from
 //     s0 itself.  Lane l of the wave owning chunk c ends with f_c(start_l), f_c
@@ -20,7 +20,7 @@
 //     the chunk is run sequentially from s.
 // The result is always the sequential sum; the guesses only decide how much of
 // it ran in parallel.  For a monotone running sum (sums of squares) the window
-// misses about once in 600 chunks at n = 4096.
+// misses about once in 600 chunks at n = 4096 (CPU model of this scheme).
 //
 // Start values are enumerated with an integer key that orders every f32 except
 // -0.0 (which shares +0.0's key): a running sum equal to -0.0, or not finite,
@@ -33,8 +33,8 @@
 
 namespace kh {
 
-constexpr int kEsChunk = 128;  // terms per chunk
-constexpr int kEsWin = 64;     // start values per chunk (the lanes of one wave)
+constexpr int kEsWin = 64;      // start values per chunk (the lanes of one wave)
+constexpr int kEsMaxChunks = 64;
 
 // Order-preserving integer key of an f32 (consecutive floats -> consecutive keys).
 __device__ __forceinline__ int es_key(float f) {
@@ -75,90 +75,194 @@ __device__ __forceinline__ float es_run(const float* __restrict__ t, int j0, int
   return s;
 }
 
-template <int MAXC>
+// Chunk c's window entry of lane l ends at e = E[c][l]: the lane of chunk c + 1
+// that started from e, or -1 when e is outside that window, not finite, or
+// -0.0.  Past the last chunk (c + 1 >= C) the path stays on its lane.
+__device__ __forceinline__ int es_next(float e, int gk_next, int c, int C) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t eb = __float_as_uint(e);
+  const int q = es_key(e) - gk_next + kEsWin / 2;
+  const bool ok = (eb & 0x7f800000u) != 0x7f800000u && eb != 0x80000000u &&
+                  static_cast<uint32_t>(q) < static_cast<uint32_t>(kEsWin);
+  return c + 1 >= C ? lane : (ok ? q : -1);
+}
+
+// P full chunks of M terms starting at chunk c0 (cnt <= P of them real; the
+// others repeat the last one and are not stored), each from the start value
+// `st[i]` of this lane, run as P interleaved chains: a dependent DPP add costs
+// about 10 cycles, P independent ones about 5 per wave (measured), so the
+// chains of a wave hide each other's latency.  Stores E and nx (es_next;
+// gkv holds the guessed start key of chunk `lane`) of every real chunk.
+template <int P, int M>
+__device__ __forceinline__ void es_windows(const float* __restrict__ t, int c0, int cnt, int C,
+                                           const float (&st)[P], int gkv, float* __restrict__ E,
+                                           int* __restrict__ NX) {
+  const int lane = threadIdx.x & 63;
+  float s[P];
+  int base[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    s[i] = st[i];
+    base[i] = (c0 + min(i, cnt - 1)) * M + (lane & 15);
+  }
+  float tv[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) tv[i] = t[base[i]];
+#pragma unroll
+  for (int g = 0; g < M / 16; ++g) {
+    // the next group's terms are requested before this group's adds
+    float tn[P];
+    const int gn = 16 * min(g + 1, M / 16 - 1);
+#pragma unroll
+    for (int i = 0; i < P; ++i) tn[i] = t[base[i] + gn];
+#define KH_ES_STEP(K)                                          \
+  _Pragma("unroll") for (int i = 0; i < P; ++i) es_add_bcast<K>(s[i], tv[i]);
+    KH_ES_STEP(0) KH_ES_STEP(1) KH_ES_STEP(2) KH_ES_STEP(3)
+    KH_ES_STEP(4) KH_ES_STEP(5) KH_ES_STEP(6) KH_ES_STEP(7)
+    KH_ES_STEP(8) KH_ES_STEP(9) KH_ES_STEP(10) KH_ES_STEP(11)
+    KH_ES_STEP(12) KH_ES_STEP(13) KH_ES_STEP(14) KH_ES_STEP(15)
+#undef KH_ES_STEP
+#pragma unroll
+    for (int i = 0; i < P; ++i) tv[i] = tn[i];
+  }
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int c = c0 + i;
+    if (i < cnt) {
+      E[c * kEsWin + lane] = s[i];
+      NX[c * kEsWin + lane] = es_next(s[i], __builtin_amdgcn_readlane(gkv, min(c + 1, kEsWin - 1)), c, C);
+    }
+  }
+}
+
+// Inclusive prefix sum of f32 over the lanes of a wave (any rounding: the
+// result only feeds guesses).
+__device__ __forceinline__ float es_wave_scan(float x) {
+  x += dppf<kDppRowShr1>(x);
+  x += dppf<kDppRowShr2>(x);
+  x += dppf<kDppRowShr4>(x);
+  x += dppf<kDppRowShr8>(x);
+  x += dppf<kDppRowBcast15, 0xa>(x);
+  x += dppf<kDppRowBcast31, 0xc>(x);
+  return x;
+}
+
+template <int MAXC = kEsMaxChunks>
 struct EsLds {
-  float E[MAXC][kEsWin];  // E[c][l] = f_c(start of lane l)
-  float D[MAXC];          // chunk sums (guesses only)
-  int gk[MAXC];           // key of the guessed start of chunk c
+  float E[MAXC * kEsWin];  // E[c*64 + l] = f_c(start value of lane l)
+  int nx[MAXC * kEsWin];   // lane of chunk c + 1 that started from E[c*64 + l], or -1
+  float D[MAXC];           // chunk sums (guesses only)
+  int gk[MAXC];            // key of the guessed start of chunk c
   float res;
 };
 
 // Sequential f32 sum s0 + t[0] + t[1] + ... + t[n-1] (left to right, rounding
-// after each add) of terms in LDS.  Every thread of the block (NW waves,
-// blockDim.x == 64 * NW) must call it; n <= kEsChunk * MAXC.  Returns the sum
-// in every thread.  Contains barriers that wait for LDS traffic only, so
-// global loads a wave has in flight stay in flight.
-template <int NW, int MAXC>
+// after each add) of terms in LDS, with chunks of M terms (M = 64 or 128,
+// n <= 64 M).  Every thread of the block (NW waves, blockDim.x == 64 * NW)
+// must call it.  Returns the sum in every thread.  Its barriers wait for LDS
+// traffic only, so global loads a wave has in flight stay in flight.
+template <int NW, int M>
 __device__ __forceinline__ float exact_seq_sum(const float* __restrict__ t, int n, float s0,
-                                              EsLds<MAXC>& es) {
-  static_assert(NW >= 1 && MAXC <= 64, "one composing wave holds every chunk");
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+                                              EsLds<>& es) {
+  static_assert(M == 64 || M == 128, "chunk of 64 or 128 terms");
+  constexpr int kMaxP = 16;
+  constexpr int kLpc = M / 8;  // lanes per chunk in the chunk sums (8 terms each)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   if (n <= 0) return s0;
-  const int C = (n + kEsChunk - 1) / kEsChunk;
-  // 1. chunk sums in f32 (any order: guesses only)
-  for (int c = wave; c < C; c += NW) {
-    const int j = c * kEsChunk + lane;
-    const float a = (j < n ? t[j] : 0.0f) + (j + 64 < n ? t[j + 64] : 0.0f);
-    const float d = wave_sum(a);
-    if (lane == 0) es.D[c] = d;
-  }
-  lds_barrier();
-  if (wave == 0) {
-    // exclusive prefix in f64 over lanes c < C, then the f32 guess
-    const double d = lane < C ? static_cast<double>(es.D[lane]) : 0.0;
-    double inc = d;
+  const int C = (n + M - 1) / M;  // chunks (the last may be partial)
+  const int Cf = n / M;           // full chunks
+  // 1. chunk sums (any order: guesses only).  A wave takes 512 terms at a
+  // time, 8 per lane, and adds them over the M/8 lanes of each chunk.
+  for (int r = wave; r * 512 < n; r += NW) {
+    const int j0 = r * 512 + 8 * lane;
+    float a = 0.0f;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const double o = __shfl_up(inc, off, 64);
-      if (lane >= off) inc += o;
-    }
-    double ex = __shfl_up(inc, 1, 64);
-    if (lane == 0) ex = 0.0;
-    if (lane < C) es.gk[lane] = es_key(static_cast<float>(static_cast<double>(s0) + ex));
+    for (int e = 0; e < 8; ++e) a += j0 + e < n ? t[j0 + e] : 0.0f;
+    a = group_sum<kLpc>(a);
+    const int c = (r * 512) / M + lane / kLpc;
+    if (lane % kLpc == 0 && c < C) es.D[c] = a;
   }
   lds_barrier();
-  // 2. every chunk from kEsWin start values.  Waves that share a SIMD with
-  // another wave of the block (round-robin placement: waves w and w + 4) take
-  // half the chunks of a wave alone on its SIMD.
+  // 2. guesses (every wave, for itself): exclusive prefix of the chunk sums;
+  // wave 0 also stores them for the composition
+  const float dl = lane < C ? es.D[lane] : 0.0f;
+  const float inc = es_wave_scan(dl);
+  float ex = __shfl_up(inc, 1, 64);
+  if (lane == 0) ex = 0.0f;
+  const int gkv = es_key(s0 + ex);  // key of the guessed start of chunk `lane`
+  if (wave == 0 && lane < C) es.gk[lane] = gkv;
+  // 3. this wave's chunks from kEsWin start values each.  Waves that share a
+  // SIMD with another wave of the block (round-robin placement: waves w and
+  // w + 4) take half as many chunks as a wave alone on its SIMD.
+  int tot = 0, before = 0, mine = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int wt = (NW <= 4 || NW >= 8) ? 1 : ((w + 4 < NW) || (w >= 4) ? 1 : 2);
+    before += w < wave ? wt : 0;
+    mine = w == wave ? wt : mine;
+    tot += wt;
+  }
+  const int c0 = (C * before) / tot, c1 = (C * (before + mine)) / tot;
   {
-    int wt[NW];
-    int tot = 0;
+    const int cf1 = min(c1, Cf);  // full chunks of this wave
+    for (int cb = c0; cb < cf1; cb += kMaxP) {
+      const int cnt = min(kMaxP, cf1 - cb);
+      float st[kMaxP];
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const int shared = (w + 4 < NW) || (w >= 4) ? 1 : 2;
-      wt[w] = (NW <= 4) ? 2 : shared;
-      tot += wt[w];
+      for (int i = 0; i < kMaxP; ++i) {
+        const int c = min(cb + i, cf1 - 1);
+        st[i] = c == 0 ? s0 : es_from_key(__builtin_amdgcn_readlane(gkv, c) + lane - kEsWin / 2);
+      }
+      if (cnt > 8) {
+        es_windows<kMaxP, M>(t, cb, cnt, C, st, gkv, es.E, es.nx);
+      } else {
+        float s8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s8[i] = st[i];
+        es_windows<8, M>(t, cb, cnt, C, s8, gkv, es.E, es.nx);
+      }
     }
-    int before = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) before += w < wave ? wt[w] : 0;
-    const int c0 = (C * before) / tot, c1 = (C * (before + wt[wave])) / tot;
-    for (int c = c0; c < c1; ++c) {
-      const float st = c == 0 ? s0 : es_from_key(es.gk[c] + lane - kEsWin / 2);
-      const int j0 = c * kEsChunk;
-      es.E[c][lane] = es_run(t, j0, min(n, j0 + kEsChunk), st);
+    if (Cf < C && c0 <= Cf && Cf < c1) {
+      // the partial last chunk
+      const float st = Cf == 0 ? s0 : es_from_key(__builtin_amdgcn_readlane(gkv, Cf) + lane - kEsWin / 2);
+      const float e = es_run(t, Cf * M, n, st);
+      es.E[Cf * kEsWin + lane] = e;
+      es.nx[Cf * kEsWin + lane] = es_next(e, 0, Cf, C);
     }
   }
   lds_barrier();
-  // 3. composition (wave 0)
+  // 4. composition (wave 0): the path starts at chunk 0 (every lane of which
+  // started from s0) and steps p <- nx[c] of lane p.  A miss anywhere on the
+  // path shows as a negative p (collected by OR); the sum is then redone on
+  // the slow path.
   if (wave == 0) {
-    float er[MAXC];
+    int nx[kEsMaxChunks];
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) er[c] = es.E[c][lane];
-    const int gkv = es.gk[min(lane, MAXC - 1)];
-    int s = __builtin_amdgcn_readlane(__float_as_int(er[0]), 0);
+    for (int c = 0; c + 1 < kEsMaxChunks; ++c) nx[c] = es.nx[c * kEsWin + lane];
+    int p = 0, any = 0;
 #pragma unroll
-    for (int c = 1; c < MAXC; ++c) {
-      if (c < C) {
+    for (int c = 0; c + 1 < kEsMaxChunks; ++c) {
+      if (c + 1 < C) {
+        p = __builtin_amdgcn_readlane(nx[c], p & (kEsWin - 1));
+        any |= p;
+      }
+    }
+    int s;
+    if (any >= 0) {
+      s = __float_as_int(es.E[(C - 1) * kEsWin + p]);
+    } else {
+      // slow path: chunk by chunk, lookups from LDS or sequential chunks
+      s = __float_as_int(es.E[0]);
+      for (int c = 1; c < C; ++c) {
         const uint32_t sb = static_cast<uint32_t>(s);
-        const int idx = es_key(__int_as_float(s)) - __builtin_amdgcn_readlane(gkv, c) + kEsWin / 2;
-        const bool hit = (sb & 0x7f800000u) != 0x7f800000u && sb != 0x80000000u && idx >= 0 &&
-                         idx < kEsWin;
-        if (hit) {
-          s = __builtin_amdgcn_readlane(__float_as_int(er[c]), idx);
+        const int idx = es_key(__int_as_float(s)) - es.gk[c] + kEsWin / 2;
+        const bool ok = (sb & 0x7f800000u) != 0x7f800000u && sb != 0x80000000u &&
+                        static_cast<uint32_t>(idx) < static_cast<uint32_t>(kEsWin);
+        if (ok) {
+          s = __float_as_int(es.E[c * kEsWin + idx]);
         } else {
-          const int j0 = c * kEsChunk;
-          const float v = es_run(t, j0, min(n, j0 + kEsChunk), __int_as_float(s));
+          const float v = es_run(t, c * M, min(n, c * M + M), __int_as_float(s));
           s = __builtin_amdgcn_readfirstlane(__float_as_int(v));
         }
       }

@@ -352,14 +352,13 @@ __global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
 // of kRnWaves waves per row.  The row's squares are staged in LDS and summed in
 // the reference's sequential order (exact_seq_sum); then y = (x * inv) * w.
 constexpr int kRnWaves = 8;
-constexpr int kRnMaxChunks = 64;  // rows up to 8192 (larger rows take rmsnorm_seq_kernel)
-constexpr int kRnMaxN = kEsChunk * kRnMaxChunks;
+constexpr int kRnMaxN = 128 * kEsMaxChunks;  // rows up to 8192 (longer rows: rmsnorm_seq_kernel)
 
 __global__ __launch_bounds__(64 * kRnWaves) void rmsnorm_kernel(const float* __restrict__ x,
                                                                const float* __restrict__ w, int n,
                                                                float eps, float* __restrict__ y) {
   __shared__ float sq[kRnMaxN];
-  __shared__ EsLds<kRnMaxChunks> es;
+  __shared__ EsLds<> es;
   const float* xr = x + (size_t)blockIdx.x * n;
   float* yr = y + (size_t)blockIdx.x * n;
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
@@ -367,7 +366,10 @@ __global__ __launch_bounds__(64 * kRnWaves) void rmsnorm_kernel(const float* __r
     sq[i] = __fmul_rn(v, v);
   }
   lds_barrier();
-  const float inv = rms_inv_exact(exact_seq_sum<kRnWaves, kRnMaxChunks>(sq, n, 0.0f, es), n, eps);
+  // chunks of 64 terms up to 4096 (more chunks run in parallel), else of 128
+  const float ss = n <= 64 * kEsMaxChunks ? exact_seq_sum<kRnWaves, 64>(sq, n, 0.0f, es)
+                                          : exact_seq_sum<kRnWaves, 128>(sq, n, 0.0f, es);
+  const float inv = rms_inv_exact(ss, n, eps);
   for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = __fmul_rn(__fmul_rn(xr[i], inv), w[i]);
 }
 

@@ -189,8 +189,8 @@ constexpr int kL1LdsBytes = (kL1Chains + 1) * kL1LdsIn * 4;  // products + x
 // flight), its scale, then (x * inv) * norm_w.  Block 0 stores the scale in
 // inv_out[b] for the kernels that consume the same normalised row later.
 // The norm requires n_in % 4 == 0 (host-checked).
-constexpr int kL1EsChunks = kL1LdsIn / kEsChunk;
-static_assert(sizeof(float) * kL1LdsIn + sizeof(EsLds<kL1EsChunks>) <=
+constexpr int kL1EsChunk = kL1LdsIn / kEsMaxChunks;  // terms per chunk of the exact sum
+static_assert(sizeof(float) * kL1LdsIn + sizeof(EsLds<>) <=
                   sizeof(float4) * (kL1LdsIn / 4) * kL1Chains,
               "squares and the exact-sum scratch fit in the products region");
 
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
   // until the norm is known the products region holds the squares and the
   // exact-sum scratch
   float* sq = reinterpret_cast<float*>(lds4);
-  auto& es = *reinterpret_cast<EsLds<kL1EsChunks>*>(sq + kL1LdsIn);
+  auto& es = *reinterpret_cast<EsLds<>*>(sq + kL1LdsIn);
   const int b = blockIdx.y;
   const int c0 = blockIdx.x * kL1Chains;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
   lds_barrier();
   if (norm_w) {
     // sum_sq over the row in the reference's order (rms_norm.rs:48-51)
-    const float ss = exact_seq_sum<kL1Prod + 1, kL1EsChunks>(sq, n_in, 0.0f, es);
+    const float ss = exact_seq_sum<kL1Prod + 1, kL1EsChunk>(sq, n_in, 0.0f, es);
     const float inv = rms_inv_exact(ss, n_in, eps);
     if (wave == 0) {
 #pragma unroll
