@@ -5,7 +5,11 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <memory>
+#include <mutex>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "../../include/klearu_hip.h"
 
@@ -49,16 +53,42 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 void* dev_alloc(size_t bytes);
 void dev_free(void* p);
 
-// Grow-only device buffer owned by a handle (growing frees the old buffer,
-// which hipFree orders after the work already queued on the device).
+// Grow-only device buffer owned by a handle.  A buffer that is replaced by a
+// larger one stays allocated until the owner is destroyed, so a HIP graph
+// captured before the growth never points at freed memory.
 struct Scratch {
   void* p = nullptr;
   size_t cap = 0;
+  std::vector<void*> retired;
   Scratch() = default;
   Scratch(const Scratch&) = delete;
   Scratch& operator=(const Scratch&) = delete;
   ~Scratch();
-  void* get(size_t bytes);
+  // At least `bytes` (grown by half again when it grows); zero-filled on
+  // allocation when `zero` (the fill is synchronous).
+  void* get(size_t bytes, bool zero = false);
+};
+
+// Device scratch of a handle, one set of kWsSlots buffers per stream.  Calls
+// on one stream are ordered by it and share a set; calls on different streams
+// get different sets, so a handle's non-mutating calls (the reference's
+// `&self` methods, which are Send + Sync) may run concurrently on distinct
+// streams and host threads.  Sets live until the handle is destroyed.
+constexpr int kWsSlots = 8;
+struct WsSet {
+  std::mutex mu;  // host threads sharing a stream
+  Scratch slot[kWsSlots];
+  void* get(int s, size_t bytes, bool zero = false) {
+    std::lock_guard<std::mutex> g(mu);
+    return slot[s].get(bytes, zero);
+  }
+};
+class StreamWs {
+ public:
+  WsSet* get(hipStream_t s);
+ private:
+  std::mutex mu_;
+  std::vector<std::pair<hipStream_t, std::unique_ptr<WsSet>>> sets_;
 };
 
 // ---------------------------------------------------------------- device helpers

@@ -902,12 +902,51 @@ struct kh_predictor {
   float* b1 = nullptr;
   void* w2b = nullptr;   // [ceil(hid/8)][out][8]
   float* b2 = nullptr;
-  float* hbuf = nullptr;  // [batch_cap][hid]
-  float* sbuf = nullptr;  // [batch_cap][out]
-  uint32_t* mm = nullptr; // [batch_cap][layer-2 blocks][2] score key bounds per block
-  uint8_t* marks = nullptr;  // [round_up(out, 4)] union marks (zero between calls)
-  int batch_cap = 0;
+  mutable StreamWs ws;   // scratch per stream (PredBufs)
 };
+
+namespace {
+
+// Scratch of one predictor call.  hbuf [batch][hid]: layer-1 outputs;
+// sbuf [batch][out]: scores; mm [batch][layer-2 blocks][2]: score key bounds
+// per block; sortbuf [batch][k]: score-ordered top-k staging (score order
+// only); marks [round_up(out, 4)]: union marks, zero between calls (union only).
+struct PredBufs {
+  float* hbuf = nullptr;
+  float* sbuf = nullptr;
+  uint32_t* mm = nullptr;
+  uint64_t* sortbuf = nullptr;
+  uint8_t* marks = nullptr;
+};
+enum { kWsH, kWsS, kWsMM, kWsSort, kWsMarks };
+
+int l2_blocks(const kh_predictor* p) { return ceil_div(p->out_dim, kL2Threads); }
+
+size_t sort_bytes(int64_t batch, int kk) { return sizeof(uint64_t) * (size_t)batch * (size_t)kk; }
+
+// Buffers of a call with `batch` rows from the handle's workspace for stream
+// st (sortbuf for a score-ordered top-k of kk per row when kk > 0; marks when
+// asked).
+int pred_bufs(const kh_predictor* p, hipStream_t st, int64_t batch, int kk, bool marks,
+              PredBufs* b) {
+  WsSet* w = p->ws.get(st);
+  b->hbuf = static_cast<float*>(w->get(kWsH, sizeof(float) * batch * p->hid));
+  b->sbuf = static_cast<float*>(w->get(kWsS, sizeof(float) * batch * p->out_dim));
+  b->mm = static_cast<uint32_t*>(w->get(kWsMM, sizeof(uint32_t) * 2 * batch * l2_blocks(p)));
+  if (!b->hbuf || !b->sbuf || !b->mm) return KH_ERR_ALLOC;
+  if (kk > 0) {
+    b->sortbuf = static_cast<uint64_t*>(w->get(kWsSort, sort_bytes(batch, kk)));
+    if (!b->sortbuf) return KH_ERR_ALLOC;
+  }
+  if (marks) {
+    // zero-filled once; the union kernel clears what it reads
+    b->marks = static_cast<uint8_t*>(w->get(kWsMarks, (size_t)((p->out_dim + 3) & ~3), true));
+    if (!b->marks) return KH_ERR_ALLOC;
+  }
+  return KH_OK;
+}
+
+}  // namespace
 
 static bool all_bf16(const float* w, size_t n) {
   for (size_t i = 0; i < n; ++i) {
@@ -988,33 +1027,11 @@ extern "C" int kh_predictor_create(int input_dim, int hidden_dim, int output_dim
 
 extern "C" int kh_predictor_destroy(kh_predictor* p) {
   if (!p) return KH_OK;
-  dev_free(p->marks);
   dev_free(p->w1b);
   dev_free(p->b1);
   dev_free(p->w2b);
   dev_free(p->b2);
-  dev_free(p->hbuf);
-  dev_free(p->sbuf);
-  dev_free(p->mm);
   delete p;
-  return KH_OK;
-}
-
-static int l2_blocks(const kh_predictor* p) { return ceil_div(p->out_dim, kL2Threads); }
-
-static int ensure_batch(kh_predictor* p, int64_t batch) {
-  if (batch <= p->batch_cap) return KH_OK;
-  dev_free(p->hbuf);
-  dev_free(p->sbuf);
-  dev_free(p->mm);
-  p->hbuf = static_cast<float*>(dev_alloc(sizeof(float) * batch * p->hid));
-  p->sbuf = static_cast<float*>(dev_alloc(sizeof(float) * batch * p->out_dim));
-  p->mm = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * 2 * batch * l2_blocks(p)));
-  if (!p->hbuf || !p->sbuf || !p->mm) {
-    p->batch_cap = 0;
-    return KH_ERR_ALLOC;
-  }
-  p->batch_cap = static_cast<int>(batch);
   return KH_OK;
 }
 
@@ -1025,9 +1042,38 @@ struct TopkReq {
   bool done = false;
 };
 
+static int set_kernel_attrs() {
+  static std::once_flag once;
+  static int rc = KH_OK;
+  std::call_once(once, [] {
+    auto lds = [](const void* f, int bytes) {
+      if (rc == KH_OK && hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) !=
+                             hipSuccess) {
+        set_error("hipFuncSetAttribute failed");
+        rc = KH_ERR_HIP;
+      }
+    };
+    lds(reinterpret_cast<const void*>(&pred_l1_lds_kernel<uint16_t>), kL1LdsBytes);
+    lds(reinterpret_cast<const void*>(&pred_l1_lds_kernel<float>), kL1LdsBytes);
+    lds(reinterpret_cast<const void*>(&topk_kernel<6>), 136 * 1024);
+    lds(reinterpret_cast<const void*>(&topk_kernel<8>), 136 * 1024);
+    lds(reinterpret_cast<const void*>(&topk_kernel<11>), 136 * 1024);
+    lds(reinterpret_cast<const void*>(&topk_kernel<12>), 136 * 1024);
+    lds(reinterpret_cast<const void*>(&topk_kernel<16>), 136 * 1024);
+    lds(reinterpret_cast<const void*>(&topk_kernel<32>), 136 * 1024);
+    lds(reinterpret_cast<const void*>(&topk_kernel<64>), 136 * 1024);
+    lds(reinterpret_cast<const void*>(&union_kernel), 96 * 1024);
+  });
+  return rc;
+}
+
+// Layers 1 and 2 into scores (b.sbuf or the caller's array).  With mm set,
+// layer 2 also writes the per-block score key bounds; with tk set, layer 2
+// selects the top k itself when the row fits one wave (tk->done).
 template <typename W>
-static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* scores,
-                         hipStream_t st, const NormIn& nrm, uint32_t* mm, TopkReq* tk) {
+static int predict_typed(const kh_predictor* p, const float* x, int64_t batch, float* scores,
+                         float* hbuf, hipStream_t st, const NormIn& nrm, uint32_t* mm,
+                         TopkReq* tk) {
   const W* w1 = static_cast<const W*>(p->w1b);
   const W* w2 = static_cast<const W*>(p->w2b);
   const int l1_stages = ceil_div(p->in_dim, kL1Stage);
@@ -1035,17 +1081,11 @@ static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* 
     set_error("the fused RmsNorm needs an input size that is a multiple of 4 and a scale buffer");
     return KH_ERR_ARG;
   }
-  static bool l1_attr = false;
-  if (!l1_attr) {
-    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pred_l1_lds_kernel<uint16_t>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kL1LdsBytes));
-    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&pred_l1_lds_kernel<float>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kL1LdsBytes));
-    l1_attr = true;
-  }
+  int rc = set_kernel_attrs();
+  if (rc != KH_OK) return rc;
   if (p->in_dim <= kL1LdsIn)
     hipLaunchKernelGGL(pred_l1_lds_kernel<W>, dim3(ceil_div(p->hid, kL1Chains), batch),
-                       dim3(kL1Threads), kL1LdsBytes, st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf,
+                       dim3(kL1Threads), kL1LdsBytes, st, w1, p->b1, x, p->in_dim, p->hid, hbuf,
                        nrm.w, nrm.inv, nrm.eps);
   else if (nrm.w) {
     set_error("the fused RmsNorm supports predictor inputs up to %d", kL1LdsIn);
@@ -1053,43 +1093,41 @@ static int predict_typed(kh_predictor* p, const float* x, int64_t batch, float* 
   }
   else if (l1_stages <= 8 * kL1Prod)
     hipLaunchKernelGGL((pred_l1_kernel<W, 8>), dim3(ceil_div(p->hid, kL1Chains), batch),
-                       dim3(kL1Threads), 0, st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
+                       dim3(kL1Threads), 0, st, w1, p->b1, x, p->in_dim, p->hid, hbuf);
   else if (p->in_dim <= kMaxL1In)
     hipLaunchKernelGGL((pred_l1_kernel<W, 16>), dim3(ceil_div(p->hid, kL1Chains), batch),
-                       dim3(kL1Threads), 0, st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
+                       dim3(kL1Threads), 0, st, w1, p->b1, x, p->in_dim, p->hid, hbuf);
   else
     hipLaunchKernelGGL((chain_layer_kernel<0, W>), dim3(ceil_div(p->hid, 64), batch), dim3(64), 0,
-                       st, w1, p->b1, x, p->in_dim, p->hid, p->hbuf);
+                       st, w1, p->b1, x, p->in_dim, p->hid, hbuf);
   KH_LAUNCHED();
   if (p->hid <= kMaxL2Hid && tk && p->out_dim <= kL2Threads) {
     hipLaunchKernelGGL((pred_l2_kernel<W, true>), dim3(1, batch), dim3(kL2Threads), 0, st, w2,
-                       p->b2, p->hbuf, p->hid, p->out_dim, scores, nullptr, tk->k, tk->order,
+                       p->b2, hbuf, p->hid, p->out_dim, scores, nullptr, tk->k, tk->order,
                        tk->ids);
     tk->done = true;
   } else if (p->hid <= kMaxL2Hid)
     hipLaunchKernelGGL(pred_l2_kernel<W>, dim3(l2_blocks(p), batch), dim3(kL2Threads), 0, st,
-                       w2, p->b2, p->hbuf, p->hid, p->out_dim, scores, mm);
+                       w2, p->b2, hbuf, p->hid, p->out_dim, scores, mm);
   else
     hipLaunchKernelGGL((chain_layer_kernel<1, W>), dim3(ceil_div(p->out_dim, 64), batch), dim3(64),
-                       0, st, w2, p->b2, p->hbuf, p->hid, p->out_dim, scores);
+                       0, st, w2, p->b2, hbuf, p->hid, p->out_dim, scores);
   KH_LAUNCHED();
   return KH_OK;
 }
 
-// With bounds set, layer 2 also folds the score key bounds into p->mm (when
-// its fast kernel runs; *bounds is then p->mm, else nullptr).  With tk set,
-// layer 2 selects the top k itself when the row fits one wave (tk->done).
-static int predict_into(const kh_predictor* pc, const float* x, int64_t batch, float* scores,
-                        hipStream_t st, const NormIn& nrm = NormIn{},
-                        uint32_t** bounds = nullptr, TopkReq* tk = nullptr) {
-  auto* p = const_cast<kh_predictor*>(pc);
-  int rc = ensure_batch(p, batch);
-  if (rc != KH_OK) return rc;
-  // the bounds fit one slot per top-k thread
-  uint32_t* mm = (bounds && p->hid <= kMaxL2Hid && l2_blocks(p) <= kTopkThreads) ? p->mm : nullptr;
-  if (bounds) *bounds = mm;
-  return p->bf16 ? predict_typed<uint16_t>(p, x, batch, scores, st, nrm, mm, tk)
-                 : predict_typed<float>(p, x, batch, scores, st, nrm, mm, tk);
+// The score key bounds are usable by the top-k kernel when layer 2's fast
+// kernel writes them and they fit one slot per top-k thread.
+static bool bounds_ok(const kh_predictor* p) {
+  return p->hid <= kMaxL2Hid && l2_blocks(p) <= kTopkThreads;
+}
+
+static int predict_into(const kh_predictor* p, const float* x, int64_t batch, float* scores,
+                        const PredBufs& b, hipStream_t st, const NormIn& nrm = NormIn{},
+                        bool bounds = false, TopkReq* tk = nullptr) {
+  uint32_t* mm = (bounds && bounds_ok(p)) ? b.mm : nullptr;
+  return p->bf16 ? predict_typed<uint16_t>(p, x, batch, scores, b.hbuf, st, nrm, mm, tk)
+                 : predict_typed<float>(p, x, batch, scores, b.hbuf, st, nrm, mm, tk);
 }
 
 extern "C" int kh_predictor_predict(const kh_predictor* p, const float* x_dev, int64_t batch,
@@ -1097,54 +1135,32 @@ extern "C" int kh_predictor_predict(const kh_predictor* p, const float* x_dev, i
   KH_CHECK_ARG(p && x_dev && scores_dev, "null argument");
   KH_CHECK_ARG(batch >= 0 && batch <= 65535, "bad batch");
   if (batch == 0) return KH_OK;
-  return predict_into(p, x_dev, batch, scores_dev, as_stream(stream));
-}
-
-template <int KPT>
-static int topk_attr() {
-  KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<KPT>),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, 136 * 1024));
-  return KH_OK;
+  hipStream_t st = as_stream(stream);
+  PredBufs b;
+  int rc = pred_bufs(p, st, batch, 0, false, &b);
+  if (rc != KH_OK) return rc;
+  return predict_into(p, x_dev, batch, scores_dev, b, st);
 }
 
 // mm: per-block key bounds from layer 2, nmm slots per row (or nullptr: the
-// kernel finds the bounds from the scores).
+// kernel finds the bounds from the scores).  sortbuf: [batch][min(k, n)]
+// staging for score order (unused for ascending order).
 static int topk_launch(const float* scores, int64_t batch, int n, int k, int order, int32_t* ids,
-                       hipStream_t st, const uint32_t* mm = nullptr, int nmm = 0,
-                       uint8_t* marks = nullptr) {
+                       hipStream_t st, uint64_t* sortbuf, const uint32_t* mm = nullptr,
+                       int nmm = 0, uint8_t* marks = nullptr) {
   const int kk = std::min(k, n);
   if (kk <= 0 || batch == 0) return KH_OK;
   KH_CHECK_ARG(n <= kTopkRegMax, "top-k supports n <= %d scores per row (got %d)", kTopkRegMax, n);
   static_assert(kTopkRegMax < 65536, "packed compaction counts");
-  uint64_t* sortbuf = nullptr;
+  int rc = set_kernel_attrs();
+  if (rc != KH_OK) return rc;
   size_t lds = n <= kTopkStage ? sizeof(uint32_t) * ((n + 3) & ~3) : 0;  // staged scores
-  static bool attr = false;
-  if (!attr) {
-    int rc = topk_attr<6>();
-    if (rc == KH_OK) rc = topk_attr<8>();
-    if (rc == KH_OK) rc = topk_attr<11>();
-    if (rc == KH_OK) rc = topk_attr<12>();
-    if (rc == KH_OK) rc = topk_attr<16>();
-    if (rc == KH_OK) rc = topk_attr<32>();
-    if (rc == KH_OK) rc = topk_attr<64>();
-    if (rc != KH_OK) return rc;
-    attr = true;
-  }
   if (order == KH_ORDER_SCORE) {
     KH_CHECK_ARG(kk <= 4096, "score-ordered top-k supports k <= 4096 (got %d)", kk);
+    KH_CHECK_ARG(sortbuf != nullptr, "score-ordered top-k needs a staging buffer");
     int P = 1;
     while (P < kk) P <<= 1;
     lds = std::max(lds, sizeof(uint64_t) * P);
-    static thread_local uint64_t* buf = nullptr;
-    static thread_local size_t cap = 0;
-    const size_t need = sizeof(uint64_t) * batch * kk;
-    if (need > cap) {
-      dev_free(buf);
-      buf = static_cast<uint64_t*>(dev_alloc(need));
-      cap = buf ? need : 0;
-      if (!buf) return KH_ERR_ALLOC;
-    }
-    sortbuf = buf;
   }
   // keys per thread: the smallest instantiation that holds the row
   const dim3 g(static_cast<unsigned>(batch)), t(kTopkThreads);
@@ -1166,6 +1182,17 @@ static int topk_launch(const float* scores, int64_t batch, int n, int k, int ord
   return KH_OK;
 }
 
+// select_top_k over buffers b (the handle's workspace, or the static scratch
+// of the allocation-free entry point).
+static int select_top_k_with(const kh_predictor* p, const float* x, int64_t batch, int k,
+                             int order, int32_t* ids, const PredBufs& b, hipStream_t st) {
+  TopkReq tk{k, order, ids};
+  int rc = predict_into(p, x, batch, b.sbuf, b, st, NormIn{}, true, &tk);
+  if (rc != KH_OK || tk.done) return rc;
+  return topk_launch(b.sbuf, batch, p->out_dim, k, order, ids, st, b.sortbuf,
+                     bounds_ok(p) ? b.mm : nullptr, l2_blocks(p));
+}
+
 extern "C" int kh_predictor_select_top_k(const kh_predictor* p, const float* x_dev, int64_t batch,
                                          int k, int order, int32_t* ids_dev, void* stream) {
   KH_CHECK_ARG(p && x_dev && ids_dev, "null argument");
@@ -1173,14 +1200,11 @@ extern "C" int kh_predictor_select_top_k(const kh_predictor* p, const float* x_d
   KH_CHECK_ARG(order == KH_ORDER_SCORE || order == KH_ORDER_ASCENDING, "bad order");
   if (batch == 0 || k == 0) return KH_OK;
   hipStream_t st = as_stream(stream);
-  auto* pm = const_cast<kh_predictor*>(p);
-  int rc = ensure_batch(pm, batch);
+  const int kk = std::min(k, p->out_dim);
+  PredBufs b;
+  int rc = pred_bufs(p, st, batch, order == KH_ORDER_SCORE ? kk : 0, false, &b);
   if (rc != KH_OK) return rc;
-  uint32_t* mm = nullptr;
-  TopkReq tk{k, order, ids_dev};
-  rc = predict_into(p, x_dev, batch, pm->sbuf, st, NormIn{}, &mm, &tk);
-  if (rc != KH_OK || tk.done) return rc;
-  return topk_launch(pm->sbuf, batch, p->out_dim, k, order, ids_dev, st, mm, l2_blocks(p));
+  return select_top_k_with(p, x_dev, batch, k, order, ids_dev, b, st);
 }
 
 extern "C" int kh_predictor_select_top_k_union(const kh_predictor* p, const float* x_dev,
@@ -1198,25 +1222,24 @@ extern "C" int kh_predictor_select_top_k_union(const kh_predictor* p, const floa
     if (rc != KH_OK) return rc;
     return kh_union_active(ids_dev, batch, std::min(k, n), n, union_dev, count_dev, stream);
   }
-  auto* pm = const_cast<kh_predictor*>(p);
-  if (!pm->marks) {
-    const size_t bytes = (size_t)((n + 3) & ~3);
-    pm->marks = static_cast<uint8_t*>(dev_alloc(bytes));
-    if (!pm->marks) return KH_ERR_ALLOC;
-    KH_HIP(hipMemset(pm->marks, 0, bytes));  // once; the union kernel clears what it reads
-  }
-  int rc = ensure_batch(pm, batch);
+  PredBufs b;
+  int rc = pred_bufs(p, st, batch, 0, true, &b);
   if (rc != KH_OK) return rc;
-  uint32_t* mm = nullptr;
-  rc = predict_into(p, x_dev, batch, pm->sbuf, st, NormIn{}, &mm, nullptr);
+  rc = predict_into(p, x_dev, batch, b.sbuf, b, st, NormIn{}, true, nullptr);
   if (rc != KH_OK) return rc;
-  rc = topk_launch(pm->sbuf, batch, n, k, KH_ORDER_ASCENDING, ids_dev, st, mm, l2_blocks(p),
-                   pm->marks);
+  rc = topk_launch(b.sbuf, batch, n, k, KH_ORDER_ASCENDING, ids_dev, st, nullptr,
+                   bounds_ok(p) ? b.mm : nullptr, l2_blocks(p), b.marks);
   if (rc != KH_OK) return rc;
   hipLaunchKernelGGL(marks_union_kernel, dim3(1), dim3(1024), 0, st,
-                     reinterpret_cast<uint32_t*>(pm->marks), n, union_dev, count_dev);
+                     reinterpret_cast<uint32_t*>(b.marks), n, union_dev, count_dev);
   KH_LAUNCHED();
   return KH_OK;
+}
+
+// Score-order staging of handle-less top-k calls, one buffer per stream.
+static StreamWs& topk_ws() {
+  static StreamWs* w = new StreamWs();  // lives until the process ends
+  return *w;
 }
 
 extern "C" int kh_topk_select(const float* scores_dev, int64_t batch, int n, int k, int order,
@@ -1224,7 +1247,14 @@ extern "C" int kh_topk_select(const float* scores_dev, int64_t batch, int n, int
   KH_CHECK_ARG(scores_dev && ids_dev, "null argument");
   KH_CHECK_ARG(n >= 0 && k >= 0 && batch >= 0 && batch <= 65535, "bad shape");
   KH_CHECK_ARG(order == KH_ORDER_SCORE || order == KH_ORDER_ASCENDING, "bad order");
-  return topk_launch(scores_dev, batch, n, k, order, ids_dev, as_stream(stream));
+  hipStream_t st = as_stream(stream);
+  uint64_t* sortbuf = nullptr;
+  const int kk = std::min(k, n);
+  if (order == KH_ORDER_SCORE && kk > 0 && batch > 0) {
+    sortbuf = static_cast<uint64_t*>(topk_ws().get(st)->get(0, sort_bytes(batch, kk)));
+    if (!sortbuf) return KH_ERR_ALLOC;
+  }
+  return topk_launch(scores_dev, batch, n, k, order, ids_dev, st, sortbuf);
 }
 
 extern "C" int kh_union_active(const int32_t* ids_dev, int64_t batch, int k, int n,
@@ -1234,12 +1264,8 @@ extern "C" int kh_union_active(const int32_t* ids_dev, int64_t batch, int k, int
   KH_CHECK_ARG(batch * (int64_t)k < (int64_t)1 << 31, "batch * k too large");
   const size_t lds = n <= kUnionFlagMax ? sizeof(uint32_t) * ((n + 3) / 4)
                                         : sizeof(uint32_t) * ((n + 31) / 32);
-  static bool attr = false;
-  if (!attr) {
-    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&union_kernel),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
-    attr = true;
-  }
+  int rc = set_kernel_attrs();
+  if (rc != KH_OK) return rc;
   hipLaunchKernelGGL(union_kernel, dim3(1), dim3(1024), lds, as_stream(stream), ids_dev,
                      static_cast<int>(batch), k, n, union_dev, count_dev);
   KH_LAUNCHED();
@@ -1251,15 +1277,15 @@ int predictor_in_dim(const kh_predictor* p) { return p->in_dim; }
 int predictor_out_dim(const kh_predictor* p) { return p->out_dim; }
 // Predictor scores of RmsNorm(hidden) (norm applied inside layer 1) and the
 // top-k ids in ascending order, batch 1.
-int predictor_topk_normed(const kh_predictor* pc, const float* hidden, int k, int32_t* ids,
+int predictor_topk_normed(const kh_predictor* p, const float* hidden, int k, int32_t* ids,
                           const NormIn& nrm, hipStream_t st) {
-  auto* p = const_cast<kh_predictor*>(pc);
-  int rc = ensure_batch(p, 1);
+  PredBufs b;
+  int rc = pred_bufs(p, st, 1, 0, false, &b);
   if (rc != KH_OK) return rc;
-  uint32_t* mm = nullptr;
   TopkReq tk{k, KH_ORDER_ASCENDING, ids};
-  rc = predict_into(p, hidden, 1, p->sbuf, st, nrm, &mm, &tk);
+  rc = predict_into(p, hidden, 1, b.sbuf, b, st, nrm, true, &tk);
   if (rc != KH_OK || tk.done) return rc;
-  return topk_launch(p->sbuf, 1, p->out_dim, k, KH_ORDER_ASCENDING, ids, st, mm, l2_blocks(p));
+  return topk_launch(b.sbuf, 1, p->out_dim, k, KH_ORDER_ASCENDING, ids, st, nullptr,
+                     bounds_ok(p) ? b.mm : nullptr, l2_blocks(p));
 }
 }  // namespace kh

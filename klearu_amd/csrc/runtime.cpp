@@ -1,4 +1,5 @@
 // runtime.cpp -- error reporting and device allocation for the C ABI.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -33,14 +34,33 @@ void dev_free(void* p) {
   if (p) (void)hipFree(p);
 }
 
-Scratch::~Scratch() { dev_free(p); }
-
-void* Scratch::get(size_t bytes) {
-  if (bytes <= cap) return p;
+Scratch::~Scratch() {
   dev_free(p);
-  p = dev_alloc(bytes);
-  cap = p ? bytes : 0;
+  for (void* r : retired) dev_free(r);
+}
+
+void* Scratch::get(size_t bytes, bool zero) {
+  if (bytes <= cap && p) return p;
+  const size_t want = cap ? std::max(bytes, cap + cap / 2) : bytes;
+  void* q = dev_alloc(want);
+  if (!q) return nullptr;
+  if (zero && hipMemset(q, 0, want) != hipSuccess) {
+    set_error("hipMemset of a new workspace failed");
+    dev_free(q);
+    return nullptr;
+  }
+  if (p) retired.push_back(p);
+  p = q;
+  cap = want;
   return p;
+}
+
+WsSet* StreamWs::get(hipStream_t s) {
+  std::lock_guard<std::mutex> g(mu_);
+  for (auto& e : sets_)
+    if (e.first == s) return e.second.get();
+  sets_.emplace_back(s, std::make_unique<WsSet>());
+  return sets_.back().second.get();
 }
 
 }  // namespace kh
