@@ -232,6 +232,17 @@ int kh_predictor_predict(const kh_predictor* p, const float* x_dev, int64_t batc
  * ids_dev[batch][min(k, output)] (int32). */
 int kh_predictor_select_top_k(const kh_predictor* p, const float* x_dev, int64_t batch, int k,
                               int order, int32_t* ids_dev, void* stream);
+/* No counterpart in the reference: kh_predictor_select_top_k for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid hipMalloc).  Same arguments and results, bit-identical; every
+ * buffer comes from one static 4 MiB device array per GPU, so it calls no
+ * hipMalloc/hipFree.  Requests needing more than 4 MiB of scratch
+ * (4*batch*(hidden + output) + 8*batch*ceil(output/64) bytes, plus
+ * 8*batch*min(k, output) for KH_ORDER_SCORE, each rounded up to 256) return
+ * KH_ERR_CAPACITY.  All calls on one GPU share the array: calls that overlap
+ * on one GPU (other streams, other threads) race and must be ordered. */
+int kh_predictor_select_top_k_noalloc(const kh_predictor* p, const float* x_dev, int64_t batch,
+                                      int k, int order, int32_t* ids_dev, void* stream);
 /* The stable top-k of arbitrary scores (the sort of mlp_predictor.rs:129-131):
  * scores_dev[batch][n] -> ids_dev[batch][min(k, n)].  NaN scores are not supported. */
 int kh_topk_select(const float* scores_dev, int64_t batch, int n, int k, int order,

@@ -90,6 +90,7 @@ SIGS = {
     "kh_predictor_destroy": (I, [P]),
     "kh_predictor_predict": (I, [P, P, I64, P, P]),
     "kh_predictor_select_top_k": (I, [P, P, I64, I, I, P, P]),
+    "kh_predictor_select_top_k_noalloc": (I, [P, P, I64, I, I, P, P]),
     "kh_topk_select": (I, [P, I64, I, I, I, P, P]),
     "kh_union_active": (I, [P, I64, I, I, P, P, P]),
     "kh_predictor_select_top_k_union": (I, [P, P, I64, I, P, P, P, P]),

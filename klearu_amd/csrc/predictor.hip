@@ -1207,6 +1207,71 @@ extern "C" int kh_predictor_select_top_k(const kh_predictor* p, const float* x_d
   return select_top_k_with(p, x_dev, batch, k, order, ids_dev, b, st);
 }
 
+// ---------------------------------------------------------------- allocation-free variant
+// kh_predictor_select_top_k_noalloc takes every buffer from this array (one
+// copy per GPU, held until the process ends) instead of allocating.  Host code
+// never uses the array's name as an address: the device address comes from
+// hipGetSymbolAddress, once per device, and is what the kernels receive.
+constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device.
+int scratch_ptr(uint8_t** out) {
+  int dev = 0;
+  KH_HIP(hipGetDevice(&dev));
+  KH_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+      return KH_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = static_cast<uint8_t*>(g_scratch_ptr[dev]);
+  return KH_OK;
+}
+
+size_t round256(size_t b) { return (b + 255) & ~size_t(255); }
+}  // namespace
+
+extern "C" int kh_predictor_select_top_k_noalloc(const kh_predictor* p, const float* x_dev,
+                                                 int64_t batch, int k, int order, int32_t* ids_dev,
+                                                 void* stream) {
+  KH_CHECK_ARG(p && x_dev && ids_dev, "null argument");
+  KH_CHECK_ARG(k >= 0 && batch >= 0 && batch <= 65535, "bad k/batch");
+  KH_CHECK_ARG(order == KH_ORDER_SCORE || order == KH_ORDER_ASCENDING, "bad order");
+  if (batch == 0 || k == 0) return KH_OK;
+  const int kk = std::min(k, p->out_dim);
+  const size_t hb = round256(sizeof(float) * batch * p->hid);
+  const size_t sb = round256(sizeof(float) * batch * p->out_dim);
+  const size_t mb = round256(sizeof(uint32_t) * 2 * batch * l2_blocks(p));
+  const size_t ob = order == KH_ORDER_SCORE ? round256(sort_bytes(batch, kk)) : 0;
+  const size_t need = hb + sb + mb + ob;
+  if (need > kNoAllocScratchBytes) {
+    set_error("kh_predictor_select_top_k_noalloc: batch %lld needs %zu bytes of scratch, more than "
+              "its %zu (use kh_predictor_select_top_k)",
+              (long long)batch, need, kNoAllocScratchBytes);
+    return KH_ERR_CAPACITY;
+  }
+  uint8_t* base = nullptr;
+  int rc = scratch_ptr(&base);
+  if (rc != KH_OK) return rc;
+  PredBufs b;
+  b.hbuf = reinterpret_cast<float*>(base);
+  b.sbuf = reinterpret_cast<float*>(base + hb);
+  b.mm = reinterpret_cast<uint32_t*>(base + hb + sb);
+  b.sortbuf = ob ? reinterpret_cast<uint64_t*>(base + hb + sb + mb) : nullptr;
+  return select_top_k_with(p, x_dev, batch, k, order, ids_dev, b, as_stream(stream));
+}
+
 extern "C" int kh_predictor_select_top_k_union(const kh_predictor* p, const float* x_dev,
                                                int64_t batch, int k, int32_t* ids_dev,
                                                int32_t* union_dev, int32_t* count_dev,
