@@ -13,9 +13,14 @@
  *     (NULL = the legacy default stream).  Compute calls are asynchronous on
  *     that stream unless stated otherwise.
  *   - Handles are device-resident and immutable after creation except where a
- *     function says it mutates the handle (the reference's `&mut self`).  A
- *     handle owns a scratch workspace: calls on one handle must be ordered
- *     (same stream, or synchronised); distinct handles may run concurrently.
+ *     function says it mutates the handle (the reference's `&mut self`, which
+ *     needs exclusive access).  Non-mutating calls (the reference's `&self`
+ *     methods of Send + Sync types) may run concurrently on one handle from
+ *     different streams and host threads: a handle keeps one scratch set per
+ *     stream, and calls on one stream are ordered by it.  Scratch is sized by
+ *     the first calls on a stream; warm a stream up before capturing it in a
+ *     HIP graph (buffers that are outgrown stay allocated until the handle is
+ *     destroyed, so earlier graphs stay valid).
  *   - Selections (hash codes, active sets, top-k) are bit-exact with the
  *     reference's sequential f32 arithmetic.  Sets whose reference order is a
  *     HashMap iteration order are returned in ascending id order.
@@ -133,6 +138,25 @@ int kh_lsh_index_insert(kh_lsh_index* idx, const uint32_t* ids_dev, const float*
 /* Same from precomputed codes[n][num_tables] (e.g. from kh_hash_dense). */
 int kh_lsh_index_insert_codes(kh_lsh_index* idx, const uint32_t* ids_dev,
                               const uint32_t* codes_dev, int64_t n, void* stream);
+/* LshIndexTrait::insert_sparse (lsh/index.rs:264-269) for n SparseVectors in
+ * order (CSR: vector i is xidx/xval[xoff[i]..xoff[i+1]], ascending indices),
+ * hashed with hash_sparse.  Mutates. */
+int kh_lsh_index_insert_sparse(kh_lsh_index* idx, const uint32_t* ids_dev, const int64_t* xoff_dev,
+                               const uint32_t* xidx_dev, const float* xval_dev, int64_t n,
+                               void* stream);
+/* LshIndexTrait::remove_with_weights (lsh/index.rs:271-276) for n vectors in
+ * order: in each table, the bucket the weights hash to drops the id's first
+ * entry by swap_remove (bucket/fifo.rs:35-42, bucket/reservoir.rs:69-76);
+ * reservoir insertion counts are unchanged.  Mutates; synchronises. */
+int kh_lsh_index_remove_with_weights(kh_lsh_index* idx, const uint32_t* ids_dev,
+                                     const float* w_dev, int64_t n, int64_t ldw, void* stream);
+/* Same from precomputed codes[n][num_tables]. */
+int kh_lsh_index_remove_codes(kh_lsh_index* idx, const uint32_t* ids_dev,
+                              const uint32_t* codes_dev, int64_t n, void* stream);
+/* LshIndexTrait::remove (lsh/index.rs:278-280, BucketStorage::remove_all
+ * :146-164): each id in order is removed (first entry, swap_remove) from every
+ * bucket of every table.  Mutates; synchronises. */
+int kh_lsh_index_remove(kh_lsh_index* idx, const uint32_t* ids_dev, int64_t n, void* stream);
 /* LshIndexTrait::clear (lsh/index.rs:313-315). Mutates. */
 int kh_lsh_index_clear(kh_lsh_index* idx, void* stream);
 /* LshIndexTrait::query / query_with_counts (lsh/index.rs:282-284, :294-296)
@@ -256,7 +280,7 @@ int kh_union_active(const int32_t* ids_dev, int64_t batch, int k, int n, int32_t
  * the top-k kernel marks the selected neurons and the union is read from the
  * marks (mlp_predictor.rs:127-132 per row, then the shared active set).
  * ids_dev[batch][min(k, output)], union_dev[<= output] ascending, *count_dev.
- * Calls on one predictor handle must not overlap (the marks live in it). */
+ * The marks live in the handle's per-stream scratch. */
 int kh_predictor_select_top_k_union(const kh_predictor* p, const float* x_dev, int64_t batch,
                                     int k, int32_t* ids_dev, int32_t* union_dev,
                                     int32_t* count_dev, void* stream);
@@ -287,7 +311,14 @@ int kh_sparse_ffn_destroy(kh_sparse_ffn* f);
 int kh_sparse_ffn_forward(const kh_sparse_ffn* f, const float* x_dev, int64_t batch,
                           const int32_t* active_dev, int n_active, const int32_t* n_active_dev,
                           float* y_dev, int accumulate, void* stream);
-/* Per-neuron activations h[b][i] = silu(g)*u of the last forward, for tests. */
+/* Ids in an active list must lie in [0, intermediate) (the reference panics,
+ * crates/klearu-accel/src/memory/mod.rs:87-92).  The kernels check every id:
+ * one outside the range reads row 0 instead (no access leaves the weights)
+ * and is recorded on the handle.  kh_sparse_ffn_status synchronises the
+ * device and returns KH_ERR_ARG (clearing the record) if any call since the
+ * last status call saw such an id, else KH_OK. */
+int kh_sparse_ffn_status(const kh_sparse_ffn* f);
+/* Per-neuron activations h[b][i] = silu(g)*u of the last forward on `stream`, for tests. */
 int kh_sparse_ffn_last_hidden(const kh_sparse_ffn* f, float* h_dev, int64_t batch, int n_active,
                               void* stream);
 
@@ -331,8 +362,8 @@ int kh_dejavu_linear_forward(const kh_dejavu_linear* l, const float* x_dev, int6
                              float* y_dev, void* stream);
 /* Linear::forward_sparse (transformer/mod.rs:126-134): y_dev[b][a] = row idx_host[a]
  * (any order, repeats allowed).  Out-of-range indices are KH_ERR_ARG (the
- * reference panics).  Uses the handle's index buffer: calls must be ordered. */
-int kh_dejavu_linear_forward_sparse(kh_dejavu_linear* l, const float* x_dev, int64_t batch,
+ * reference panics). */
+int kh_dejavu_linear_forward_sparse(const kh_dejavu_linear* l, const float* x_dev, int64_t batch,
                                     const int64_t* idx_host, int64_t n_idx, float* y_dev,
                                     void* stream);
 
@@ -343,7 +374,7 @@ int kh_dejavu_sparse_mlp_create(int hidden, int inter, kh_dejavu_sparse_mlp** ou
 int kh_dejavu_sparse_mlp_destroy(kh_dejavu_sparse_mlp* m);
 /* SparseMlp::forward (mlp.rs:23-58) for every row of x_dev[batch][hidden] with the
  * same selected neurons: y_dev[batch][hidden]. */
-int kh_dejavu_sparse_mlp_forward(kh_dejavu_sparse_mlp* m, const float* x_dev, int64_t batch,
+int kh_dejavu_sparse_mlp_forward(const kh_dejavu_sparse_mlp* m, const float* x_dev, int64_t batch,
                                  const kh_dejavu_linear* gate, const kh_dejavu_linear* up,
                                  const kh_dejavu_linear* down, const int64_t* sel_host,
                                  int64_t n_sel, float* y_dev, void* stream);
@@ -356,7 +387,7 @@ int kh_dejavu_sparse_attention_create(int hidden, int num_heads, int head_dim,
 int kh_dejavu_sparse_attention_destroy(kh_dejavu_sparse_attention* a);
 /* SparseAttention::forward (attention.rs:18-74) for every row of x_dev[batch][hidden]
  * with the same selected heads: y_dev[batch][hidden]. */
-int kh_dejavu_sparse_attention_forward(kh_dejavu_sparse_attention* a, const float* x_dev,
+int kh_dejavu_sparse_attention_forward(const kh_dejavu_sparse_attention* a, const float* x_dev,
                                        int64_t batch, const kh_dejavu_linear* q,
                                        const kh_dejavu_linear* k, const kh_dejavu_linear* v,
                                        const kh_dejavu_linear* o, const int64_t* heads_host,

@@ -76,6 +76,10 @@ SIGS = {
     "kh_lsh_index_insert": (I, [P, P, P, I64, I64, P]),
     "kh_lsh_index_insert_codes": (I, [P, P, P, I64, P]),
     "kh_lsh_index_clear": (I, [P, P]),
+    "kh_lsh_index_insert_sparse": (I, [P, P, P, P, P, I64, P]),
+    "kh_lsh_index_remove_codes": (I, [P, P, P, I64, P]),
+    "kh_lsh_index_remove_with_weights": (I, [P, P, P, I64, I64, P]),
+    "kh_lsh_index_remove": (I, [P, P, I64, P]),
     "kh_lsh_index_query": (I, [P, P, I64, P, P, P, I64, P]),
     "kh_lsh_index_query_sparse": (I, [P, P, P, P, I64, P, P, P, I64, P]),
     "kh_lsh_index_buckets": (I, [P, P, P, P]),
@@ -99,6 +103,7 @@ SIGS = {
     "kh_sparse_ffn_destroy": (I, [P]),
     "kh_sparse_ffn_forward": (I, [P, P, I64, P, I, P, P, I, P]),
     "kh_sparse_ffn_last_hidden": (I, [P, P, I64, I, P]),
+    "kh_sparse_ffn_status": (I, [P]),
     "kh_rmsnorm": (I, [P, P, I64, I, F, P, P]),
     "kh_dejavu_mlp_block": (I, [P, P, P, P, F, I, P, P, P]),
     "kh_dejavu_attn_block": (I, [P, P, P, P, F, I, P, P, P]),

@@ -1225,7 +1225,7 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
                        heads, nsel, a->lens, a->max_seq, batch, groups, partial);
   else
     hipLaunchKernelGGL(gather_rows_kernel<NB>, dim3(nslices, groups), dim3(kDownThreads), 0, st,
-                       a->wot, H, a->qrows, qd, a->qrows + qd, a->cat, qd, batch, groups,
+                       a->wot, H, a->qrows, qd, a->qrows + qd, qd, a->cat, qd, batch, groups,
                        partial);
   KH_LAUNCHED();
   if (groups <= 64)  // few partial rows: 4-wave blocks (16 rows in flight per wave)

@@ -359,6 +359,16 @@ __device__ __forceinline__ void stage_f4(float4* __restrict__ dst, const float4*
 
 inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) / b); }
 
+// A row index from a caller's list, kept inside [0, n): an index outside it
+// (the reference panics, crates/klearu-accel/src/memory/mod.rs:87-92) reads
+// row 0 instead and, when err is set, is recorded there for the handle's
+// status call.
+__device__ __forceinline__ int checked_row(int id, int n, int* err) {
+  if (static_cast<unsigned>(id) < static_cast<unsigned>(n)) return id;
+  if (err) atomicOr(err, 1);
+  return 0;
+}
+
 // p[0..n) = v.  A kernel rather than hipMemsetAsync, so that callers may
 // capture it in a HIP graph.  (A template, so that each translation unit
 // including this header keeps its own copy.)

@@ -32,17 +32,17 @@ struct kh_dejavu_linear {
   int in_f = 0, out_f = 0;
   float* wt = nullptr;    // [in_f][out_f]
   float* bias = nullptr;  // [out_f]
-  kh::Scratch idx;        // forward_sparse row list
+  mutable kh::StreamWs ws;  // forward_sparse row list, per stream
 };
 
 struct kh_dejavu_sparse_mlp {
   int hidden = 0, inter = 0;
-  kh::Scratch idx, h;
+  mutable kh::StreamWs ws;  // selected neurons and their activations, per stream
 };
 
 struct kh_dejavu_sparse_attention {
   int hidden = 0, num_heads = 0, head_dim = 0;
-  kh::Scratch idx, vec;
+  mutable kh::StreamWs ws;  // row lists and head vectors, per stream
 };
 
 namespace kh {
@@ -125,14 +125,15 @@ static unsigned grid_for(int64_t threads) {
   return (unsigned)((threads + kDlThreads - 1) / kDlThreads);
 }
 
-// Checks idx_host[0..n) against [0, bound) and uploads it to `s`.
-static int upload_indices(Scratch& s, const int64_t* idx_host, int64_t n, int64_t bound,
+// Checks idx_host[0..n) against [0, bound) and uploads it to slot 0 of the
+// stream's workspace w.
+static int upload_indices(WsSet* w, const int64_t* idx_host, int64_t n, int64_t bound,
                           const char* what, hipStream_t st, const int64_t** out) {
   for (int64_t a = 0; a < n; ++a)
     KH_CHECK_ARG(idx_host[a] >= 0 && idx_host[a] < bound,
                  "%s index %lld out of range (%lld)", what, (long long)idx_host[a],
                  (long long)bound);
-  int64_t* d = static_cast<int64_t*>(s.get(sizeof(int64_t) * (size_t)(n > 0 ? n : 1)));
+  int64_t* d = static_cast<int64_t*>(w->get(0, sizeof(int64_t) * (size_t)(n > 0 ? n : 1)));
   if (!d) return KH_ERR_ALLOC;
   if (n > 0) {
     KH_HIP(hipMemcpyAsync(d, idx_host, sizeof(int64_t) * (size_t)n, hipMemcpyHostToDevice, st));
@@ -216,7 +217,7 @@ extern "C" int kh_dejavu_linear_forward(const kh_dejavu_linear* l, const float* 
                      as_stream(stream));
 }
 
-extern "C" int kh_dejavu_linear_forward_sparse(kh_dejavu_linear* l, const float* x_dev,
+extern "C" int kh_dejavu_linear_forward_sparse(const kh_dejavu_linear* l, const float* x_dev,
                                                int64_t batch, const int64_t* idx_host,
                                                int64_t n_idx, float* y_dev, void* stream) {
   KH_CHECK_ARG(l && x_dev && y_dev && (idx_host || n_idx == 0), "null argument");
@@ -224,7 +225,7 @@ extern "C" int kh_dejavu_linear_forward_sparse(kh_dejavu_linear* l, const float*
   if (batch * n_idx == 0) return KH_OK;
   hipStream_t st = as_stream(stream);
   const int64_t* rows = nullptr;
-  int rc = upload_indices(l->idx, idx_host, n_idx, l->out_f, "row", st, &rows);
+  int rc = upload_indices(l->ws.get(st), idx_host, n_idx, l->out_f, "row", st, &rows);
   if (rc != KH_OK) return rc;
   return rows_launch(l, x_dev, l->in_f, batch, rows, n_idx, y_dev, n_idx, 0, st);
 }
@@ -244,7 +245,7 @@ extern "C" int kh_dejavu_sparse_mlp_destroy(kh_dejavu_sparse_mlp* m) {
   return KH_OK;
 }
 
-extern "C" int kh_dejavu_sparse_mlp_forward(kh_dejavu_sparse_mlp* m, const float* x_dev,
+extern "C" int kh_dejavu_sparse_mlp_forward(const kh_dejavu_sparse_mlp* m, const float* x_dev,
                                             int64_t batch, const kh_dejavu_linear* gate,
                                             const kh_dejavu_linear* up,
                                             const kh_dejavu_linear* down, const int64_t* sel_host,
@@ -259,9 +260,9 @@ extern "C" int kh_dejavu_sparse_mlp_forward(kh_dejavu_sparse_mlp* m, const float
   if (batch == 0) return KH_OK;
   hipStream_t st = as_stream(stream);
   const int64_t* sel = nullptr;
-  int rc = upload_indices(m->idx, sel_host, n_sel, I, "neuron", st, &sel);
+  int rc = upload_indices(m->ws.get(st), sel_host, n_sel, I, "neuron", st, &sel);
   if (rc != KH_OK) return rc;
-  float* h = static_cast<float*>(m->h.get(sizeof(float) * (size_t)(batch * n_sel + 1)));
+  float* h = static_cast<float*>(m->ws.get(st)->get(1, sizeof(float) * (size_t)(batch * n_sel + 1)));
   if (!h) return KH_ERR_ALLOC;
   if (batch * n_sel > 0) {
     hipLaunchKernelGGL(dl_gateup_kernel, dim3(grid_for(batch * n_sel)), dim3(kDlThreads), 0, st,
@@ -292,7 +293,7 @@ extern "C" int kh_dejavu_sparse_attention_destroy(kh_dejavu_sparse_attention* a)
 }
 
 extern "C" int kh_dejavu_sparse_attention_forward(
-    kh_dejavu_sparse_attention* a, const float* x_dev, int64_t batch, const kh_dejavu_linear* q,
+    const kh_dejavu_sparse_attention* a, const float* x_dev, int64_t batch, const kh_dejavu_linear* q,
     const kh_dejavu_linear* k, const kh_dejavu_linear* v, const kh_dejavu_linear* o,
     const int64_t* heads_host, int64_t n_heads, float* y_dev, void* stream) {
   KH_CHECK_ARG(a && q && k && v && o && x_dev && y_dev && (heads_host || n_heads == 0),
@@ -315,9 +316,9 @@ extern "C" int kh_dejavu_sparse_attention_forward(
     for (int d = 0; d < hd; ++d) lists[(size_t)(n_heads + i * hd + d)] = heads_host[i] * hd + d;
   }
   const int64_t* dl = nullptr;
-  int rc = upload_indices(a->idx, lists.data(), (int64_t)lists.size(), qd, "row", st, &dl);
+  int rc = upload_indices(a->ws.get(st), lists.data(), (int64_t)lists.size(), qd, "row", st, &dl);
   if (rc != KH_OK) return rc;
-  float* buf = static_cast<float*>(a->vec.get(sizeof(float) * (size_t)(4 * batch * qd)));
+  float* buf = static_cast<float*>(a->ws.get(st)->get(1, sizeof(float) * (size_t)(4 * batch * qd)));
   if (!buf) return KH_ERR_ALLOC;
   float *qv = buf, *kv = buf + batch * qd, *vv = buf + 2 * batch * qd, *att = buf + 3 * batch * qd;
   if ((rc = fill_zero(buf, 4 * batch * qd, st)) != KH_OK) return rc;

@@ -48,7 +48,7 @@ template <int NB>
 __global__ __launch_bounds__(64 * kGuWaves) void ffn_gateup_kernel(
     const uint16_t* __restrict__ Wgu, const float* __restrict__ x, int batch, int H,
     const int32_t* __restrict__ active, int n_active, const int32_t* __restrict__ n_active_dev,
-    float* __restrict__ hbuf, int hstride) {
+    int inter, int* __restrict__ err, float* __restrict__ hbuf, int hstride) {
   extern __shared__ float4 xs4[];  // [kGuTok][H/4]
   int n = n_active;
   if (n_active_dev) n = min(n, *n_active_dev);
@@ -56,7 +56,7 @@ __global__ __launch_bounds__(64 * kGuWaves) void ffn_gateup_kernel(
   const int item = blockIdx.x * kGuWaves + wave;
   if (blockIdx.x * kGuWaves >= n) return;  // whole block idle (uniform)
   const bool live = item < n;
-  const int neuron = active[live ? item : n - 1];
+  const int neuron = checked_row(active[live ? item : n - 1], inter, err);
   const uint4* __restrict__ g = reinterpret_cast<const uint4*>(Wgu + (size_t)neuron * 2 * H);
   const uint4* __restrict__ u = g + (H >> 3);
   const int nchunk = H >> 3;
@@ -132,7 +132,8 @@ __global__ __launch_bounds__(64 * kGuWaves) void ffn_gateup_kernel(
 __global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
     const uint16_t* __restrict__ Wgu, const float* __restrict__ x, int batch, int H,
     const int32_t* __restrict__ active,
-    int n_active, const int32_t* __restrict__ n_active_dev, float* __restrict__ hbuf, int hstride) {
+    int n_active, const int32_t* __restrict__ n_active_dev, int inter, int* __restrict__ err,
+    float* __restrict__ hbuf, int hstride) {
   constexpr int kGroups = kMfWaves / kMfSplit;
   __shared__ kh_f32x4 part[kGroups][kMfSplit - 1][4][64];
   __shared__ uint64_t s_tab[32];  // kExp2Tab, for silu after the tile sums
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
   const int base = (blockIdx.x * kGroups + grp) * 16;
   const bool live = base < n;  // uniform per row group
   const int r = lane & 15, kb = lane >> 4;
-  const int neuron = active[min(base + r, max(n, 1) - 1)];
+  const int neuron = checked_row(active[min(base + r, max(n, 1) - 1)], inter, err);
   const int qsteps = H / (64 * kMfSplit);  // k-steps per quarter
   const int s0 = qtr * qsteps;
   const uint4* __restrict__ g = reinterpret_cast<const uint4*>(Wgu + (size_t)neuron * 2 * H) + kb + 8 * s0;
@@ -227,8 +228,8 @@ template <int NW>
 __global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
     const uint16_t* __restrict__ Wgu, const uint16_t* __restrict__ WdT,
     const float* __restrict__ x, int H, const int32_t* __restrict__ active, int n_active,
-    const int32_t* __restrict__ n_active_dev, float* __restrict__ hbuf,
-    float* __restrict__ partial, const float* __restrict__ norm_w,
+    const int32_t* __restrict__ n_active_dev, int inter, int* __restrict__ err,
+    float* __restrict__ hbuf, float* __restrict__ partial, const float* __restrict__ norm_w,
     const float* __restrict__ norm_inv) {
   extern __shared__ float4 smem4[];
   __shared__ uint64_t s_tab[32];                                // kExp2Tab
@@ -266,7 +267,8 @@ __global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
   const int nlive = max(0, min(NW, n - first));
   int nid[NW];
 #pragma unroll
-  for (int k = 0; k < NW; ++k) nid[k] = k < nlive ? cand[k] : 0;  // idle slots read row 0, unused
+  for (int k = 0; k < NW; ++k)  // idle slots read row 0, unused
+    nid[k] = k < nlive ? checked_row(cand[k], inter, err) : 0;
   __builtin_amdgcn_sched_barrier(0);
   const int nchunk = H >> 3;
   const int own = nid[wave];
@@ -398,10 +400,13 @@ struct kh_sparse_ffn {
   int hidden = 0, inter = 0, max_batch = 0;
   uint16_t* wgu = nullptr;   // [inter][2][hidden]
   uint16_t* wdt = nullptr;   // [inter][hidden]
-  float* hbuf = nullptr;     // [max_batch][inter]
-  float* partial = nullptr;  // [max(kMaxGroups*nb_tmpl, fused blocks)][hidden]
+  int* err = nullptr;        // set when a call saw an active id outside [0, inter)
   int nslices = 0;
+  // per stream: hbuf [max_batch][inter], partial [partial_rows][hidden]
+  mutable StreamWs ws;
 };
+
+enum { kFwH, kFwPartial };
 
 static size_t partial_rows(int inter, int nbt) {
   return std::max<size_t>((size_t)kMaxGroups * nbt, (size_t)ceil_div(inter, kFuWavesMin));
@@ -444,13 +449,12 @@ extern "C" int kh_sparse_ffn_create(int hidden, int inter, const uint16_t* w_gat
     for (size_t i0 = 0; i0 < I; i0 += TB)
       for (size_t j = j0; j < std::min(H, j0 + TB); ++j)
         for (size_t i = i0; i < std::min(I, i0 + TB); ++i) dt[i * H + j] = w_down_host[j * I + i];
-  const int nbt = ffn_tmpl(max_batch);
   f->wgu = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * 2 * H * I));
   f->wdt = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * H * I));
-  f->hbuf = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * I));
-  f->partial = static_cast<float*>(dev_alloc(sizeof(float) * partial_rows(inter, nbt) * H));
+  f->err = static_cast<int*>(dev_alloc(sizeof(int)));
   int rc = KH_OK;
-  if (!f->wgu || !f->wdt || !f->hbuf || !f->partial) rc = KH_ERR_ALLOC;
+  if (!f->wgu || !f->wdt || !f->err) rc = KH_ERR_ALLOC;
+  if (rc == KH_OK && hipMemset(f->err, 0, sizeof(int)) != hipSuccess) rc = KH_ERR_HIP;
   if (rc == KH_OK) {
     if (hipMemcpy(f->wgu, gu, sizeof(uint16_t) * 2 * H * I, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(f->wdt, dt, sizeof(uint16_t) * H * I, hipMemcpyHostToDevice) != hipSuccess) {
@@ -482,12 +486,10 @@ extern "C" int kh_sparse_ffn_create_dev(int hidden, int inter, const uint16_t* w
   f->max_batch = max_batch;
   f->nslices = ceil_div(hidden, kSlice);
   const size_t H = hidden, I = inter;
-  const int nbt = ffn_tmpl(max_batch);
   f->wgu = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * 2 * H * I));
   f->wdt = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * H * I));
-  f->hbuf = static_cast<float*>(dev_alloc(sizeof(float) * max_batch * I));
-  f->partial = static_cast<float*>(dev_alloc(sizeof(float) * partial_rows(inter, nbt) * H));
-  if (!f->wgu || !f->wdt || !f->hbuf || !f->partial) {
+  f->err = static_cast<int*>(dev_alloc(sizeof(int)));
+  if (!f->wgu || !f->wdt || !f->err || hipMemset(f->err, 0, sizeof(int)) != hipSuccess) {
     kh_sparse_ffn_destroy(f);
     return KH_ERR_ALLOC;
   }
@@ -514,10 +516,18 @@ extern "C" int kh_sparse_ffn_destroy(kh_sparse_ffn* f) {
   if (!f) return KH_OK;
   dev_free(f->wgu);
   dev_free(f->wdt);
-  dev_free(f->hbuf);
-  dev_free(f->partial);
+  dev_free(f->err);
   delete f;
   return KH_OK;
+}
+
+// The stream's h and partial-row buffers of handle f.
+static int ffn_bufs(const kh_sparse_ffn* f, hipStream_t st, float** hbuf, float** partial) {
+  WsSet* w = f->ws.get(st);
+  *hbuf = static_cast<float*>(w->get(kFwH, sizeof(float) * f->max_batch * f->inter));
+  *partial = static_cast<float*>(
+      w->get(kFwPartial, sizeof(float) * partial_rows(f->inter, ffn_tmpl(f->max_batch)) * f->hidden));
+  return *hbuf && *partial ? KH_OK : KH_ERR_ALLOC;
 }
 
 template <int NB>
@@ -525,6 +535,9 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
                       int n_active, const int32_t* n_active_dev, float* y, int accumulate,
                       hipStream_t st) {
   const int H = f->hidden;
+  float *hbuf = nullptr, *partial = nullptr;
+  int rc = ffn_bufs(f, st, &hbuf, &partial);
+  if (rc != KH_OK) return rc;
   dim3 g1(ceil_div(n_active, kGuWaves));
   const size_t lds1 = sizeof(float) * std::min(NB, kGuTok) * H;
   static bool attr_set = false;
@@ -541,10 +554,10 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
     // several tokens: gate/up as 16 x 16 tile products on MFMA
     hipLaunchKernelGGL(ffn_gateup_mfma_kernel, dim3(ceil_div(n_active, 16 * (kMfWaves / kMfSplit))),
                        dim3(64 * kMfWaves), 0, st, f->wgu, x, batch, H, active, n_active,
-                       n_active_dev, f->hbuf, f->inter);
+                       n_active_dev, f->inter, f->err, hbuf, f->inter);
   } else {
     hipLaunchKernelGGL(ffn_gateup_kernel<NB>, g1, dim3(64 * kGuWaves), lds1, st, f->wgu, x, batch,
-                       H, active, n_active, n_active_dev, f->hbuf, f->inter);
+                       H, active, n_active, n_active_dev, f->inter, f->err, hbuf, f->inter);
   }
   KH_LAUNCHED();
   int groups;
@@ -558,14 +571,14 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
     }
     groups = ceil_div(n_active, kDmRows);
     hipLaunchKernelGGL(down_mfma_kernel<NB>, dim3(H / kDmCols, groups), dim3(64 * kDmWaves), kDmLds,
-                       st, f->wdt, H, active, n_active, n_active_dev, f->hbuf, f->inter, batch,
-                       f->partial);
+                       st, f->wdt, H, active, n_active, n_active_dev, f->inter, hbuf, f->inter,
+                       batch, partial);
   } else if (NB > 1 && H % 8 == 0) {
     // several tokens: 512-row groups streamed with the next rows in flight
     groups = ceil_div(n_active, kDnGroupRows);
     hipLaunchKernelGGL(down_rows_kernel<NB>, dim3(f->nslices, groups), dim3(kDownThreads), 0, st,
-                       f->wdt, H, active, n_active, n_active_dev, f->hbuf, f->inter, batch,
-                       f->partial);
+                       f->wdt, H, active, n_active, n_active_dev, f->inter, hbuf, f->inter, batch,
+                       partial);
   } else {
     groups = gather_groups(n_active, f->nslices);
     if (groups == 0) {
@@ -574,16 +587,16 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
     }
     dim3 g2(f->nslices, groups);
     hipLaunchKernelGGL(gather_rows_kernel<NB>, g2, dim3(kDownThreads), 0, st, f->wdt, H, active,
-                       n_active, n_active_dev, f->hbuf, f->inter, batch, groups, f->partial);
+                       n_active, n_active_dev, f->inter, hbuf, f->inter, batch, groups, partial);
   }
   KH_LAUNCHED();
   // few partial rows (at most 64: 4 waves x 16 rows in flight each): 4-wave blocks
   if (groups <= 64)
     hipLaunchKernelGGL((partials_reduce_kernel<NB, 4>), dim3(ceil_div(H, 64), batch), dim3(64 * 4), 0,
-                       st, f->partial, H, groups, y, accumulate, nullptr, 0);
+                       st, partial, H, groups, y, accumulate, nullptr, 0);
   else
     hipLaunchKernelGGL(partials_reduce_kernel<NB>, dim3(ceil_div(H, 64), batch), dim3(64 * kRedWaves),
-                       0, st, f->partial, H, groups, y, accumulate, nullptr, 0);
+                       0, st, partial, H, groups, y, accumulate, nullptr, 0);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -598,6 +611,9 @@ static int ffn_fused_launch(const kh_sparse_ffn* f, const float* x, const int32_
                             int n_active, const int32_t* n_active_dev, float* y, int accumulate,
                             const NormIn& nrm, hipStream_t st) {
   const int H = f->hidden;
+  float *hbuf = nullptr, *partial = nullptr;
+  int rc = ffn_bufs(f, st, &hbuf, &partial);
+  if (rc != KH_OK) return rc;
   // Four neurons per block when the hidden size allows it (a wave's down
   // slice is at most 512 columns) and eight would leave CUs idle: the 1.1B
   // shape (hidden 2048, 564 active) gets 141 blocks instead of 71.
@@ -615,15 +631,15 @@ static int ffn_fused_launch(const kh_sparse_ffn* f, const float* x, const int32_
   }
   if (small)
     hipLaunchKernelGGL(ffn_fused1_kernel<kFuWavesMin>, dim3(blocks), dim3(64 * kFuWavesMin), lds, st,
-                       f->wgu, f->wdt, x, H, active, n_active, n_active_dev, f->hbuf, f->partial,
-                       nrm.w, nrm.inv);
+                       f->wgu, f->wdt, x, H, active, n_active, n_active_dev, f->inter, f->err, hbuf,
+                       partial, nrm.w, nrm.inv);
   else
     hipLaunchKernelGGL(ffn_fused1_kernel<kFuWaves>, dim3(blocks), dim3(64 * kFuWaves), lds, st,
-                       f->wgu, f->wdt, x, H, active, n_active, n_active_dev, f->hbuf, f->partial,
-                       nrm.w, nrm.inv);
+                       f->wgu, f->wdt, x, H, active, n_active, n_active_dev, f->inter, f->err, hbuf,
+                       partial, nrm.w, nrm.inv);
   KH_LAUNCHED();
   hipLaunchKernelGGL(partials_reduce_kernel<1>, dim3(ceil_div(H, 64), 1), dim3(64 * kRedWaves), 0,
-                     st, f->partial, H, blocks, y, accumulate, nullptr, 0);
+                     st, partial, H, blocks, y, accumulate, nullptr, 0);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -665,10 +681,24 @@ extern "C" int kh_sparse_ffn_last_hidden(const kh_sparse_ffn* f, float* h_dev, i
   KH_CHECK_ARG(f && h_dev, "null argument");
   KH_CHECK_ARG(batch >= 1 && batch <= f->max_batch && n_active >= 0 && n_active <= f->inter,
                "bad batch/n_active");
-  KH_HIP(hipMemcpy2DAsync(h_dev, sizeof(float) * n_active, f->hbuf, sizeof(float) * f->inter,
-                          sizeof(float) * n_active, batch, hipMemcpyDeviceToDevice,
-                          as_stream(stream)));
+  hipStream_t st = as_stream(stream);
+  float *hbuf = nullptr, *partial = nullptr;
+  int rc = ffn_bufs(f, st, &hbuf, &partial);
+  if (rc != KH_OK) return rc;
+  KH_HIP(hipMemcpy2DAsync(h_dev, sizeof(float) * n_active, hbuf, sizeof(float) * f->inter,
+                          sizeof(float) * n_active, batch, hipMemcpyDeviceToDevice, st));
   return KH_OK;
+}
+
+extern "C" int kh_sparse_ffn_status(const kh_sparse_ffn* f) {
+  KH_CHECK_ARG(f != nullptr, "null argument");
+  KH_HIP(hipDeviceSynchronize());
+  int v = 0;
+  KH_HIP(hipMemcpy(&v, f->err, sizeof(int), hipMemcpyDeviceToHost));
+  if (v == 0) return KH_OK;
+  KH_HIP(hipMemset(f->err, 0, sizeof(int)));
+  set_error("an active neuron id was outside [0, %d) (rows clamped to 0)", f->inter);
+  return KH_ERR_ARG;
 }
 
 extern "C" int kh_rmsnorm(const float* x_dev, const float* w_dev, int64_t batch, int n, float eps,

@@ -28,8 +28,8 @@ constexpr int kDownRows = 128;  // max rows per down block (16 per row lane)
 template <int NB>
 __global__ __launch_bounds__(kDownThreads) void gather_rows_kernel(
     const uint16_t* __restrict__ WdT, int H, const int32_t* __restrict__ active, int n_active,
-    const int32_t* __restrict__ n_active_dev, const float* __restrict__ hbuf, int hstride,
-    int batch, int groups, float* __restrict__ partial) {
+    const int32_t* __restrict__ n_active_dev, int nrows, const float* __restrict__ hbuf,
+    int hstride, int batch, int groups, float* __restrict__ partial) {
   __shared__ float red[4][NB][kSlice];
   __shared__ int s_ids[kDownRows];
   __shared__ float s_h[NB][kDownRows];
@@ -45,7 +45,7 @@ __global__ __launch_bounds__(kDownThreads) void gather_rows_kernel(
   const int r0 = min(n, grp * per);
   const int r1 = min(n, r0 + per);
   const int nr = r1 - r0;  // <= kDownRows by construction of `groups`
-  for (int i = tid; i < nr; i += blockDim.x) s_ids[i] = active[r0 + i];
+  for (int i = tid; i < nr; i += blockDim.x) s_ids[i] = checked_row(active[r0 + i], nrows, nullptr);
   for (int i = tid; i < nr * NB; i += blockDim.x) {
     const int b = i / nr, r = i - b * nr;
     s_h[b][r] = b < batch ? hbuf[(size_t)b * hstride + r0 + r] : 0.0f;
@@ -109,8 +109,8 @@ constexpr int kDnChunk = 8;  // rows per row lane per chunk
 template <int NB>
 __global__ __launch_bounds__(kDownThreads) void down_rows_kernel(
     const uint16_t* __restrict__ WdT, int H, const int32_t* __restrict__ active, int n_active,
-    const int32_t* __restrict__ n_active_dev, const float* __restrict__ hbuf, int hstride,
-    int batch, float* __restrict__ partial) {
+    const int32_t* __restrict__ n_active_dev, int nrows, const float* __restrict__ hbuf,
+    int hstride, int batch, float* __restrict__ partial) {
   constexpr int TB = NB < 4 ? NB : 4;  // tokens per reduction pass
   __shared__ int s_ids[kDnGroupRows];
   __shared__ float s_h[NB][kDnGroupRows];
@@ -121,7 +121,8 @@ __global__ __launch_bounds__(kDownThreads) void down_rows_kernel(
   const int tid = threadIdx.x;
   const int r0 = grp * kDnGroupRows;
   const int nr = max(0, min(kDnGroupRows, n - r0));
-  for (int i = tid; i < kDnGroupRows; i += kDownThreads) s_ids[i] = active[min(r0 + i, max(n, 1) - 1)];
+  for (int i = tid; i < kDnGroupRows; i += kDownThreads)
+    s_ids[i] = checked_row(active[min(r0 + i, max(n, 1) - 1)], nrows, nullptr);
   for (int i = tid; i < kDnGroupRows * NB; i += kDownThreads) {
     const int b = i / kDnGroupRows, r = i - b * kDnGroupRows;
     s_h[b][r] = (b < batch && r < nr) ? hbuf[(size_t)b * hstride + r0 + r] : 0.0f;
@@ -217,8 +218,8 @@ constexpr size_t kDmLds = sizeof(int) * kDmRows +
 template <int NB>
 __global__ __launch_bounds__(64 * kDmWaves) void down_mfma_kernel(
     const uint16_t* __restrict__ WdT, int H, const int32_t* __restrict__ active, int n_active,
-    const int32_t* __restrict__ n_active_dev, const float* __restrict__ hbuf, int hstride,
-    int batch, float* __restrict__ partial) {
+    const int32_t* __restrict__ n_active_dev, int nrows, const float* __restrict__ hbuf,
+    int hstride, int batch, float* __restrict__ partial) {
   static_assert(NB <= 16, "16 token rows per MFMA tile");
   extern __shared__ float dm_lds[];
   int* s_ids = reinterpret_cast<int*>(dm_lds);  // [kDmRows]
@@ -236,7 +237,8 @@ __global__ __launch_bounds__(64 * kDmWaves) void down_mfma_kernel(
     for (int t = 0; t < batch; ++t) partial[((size_t)grp * NB + t) * H + slice * kDmCols + tid] = 0.0f;
     return;
   }
-  for (int i = tid; i < kDmRows; i += 64 * kDmWaves) s_ids[i] = active[min(r0 + i, last)];
+  for (int i = tid; i < kDmRows; i += 64 * kDmWaves)
+    s_ids[i] = checked_row(active[min(r0 + i, last)], nrows, nullptr);
   lds_barrier();
   const int wave = tid >> 6, lane = tid & 63;
   const int kq = lane >> 4, p = lane & 15;

@@ -177,9 +177,72 @@ __global__ void apply_buckets_kernel(int nbuckets, int cap, int type,
   }
 }
 
+// Bucket::remove (bucket/fifo.rs:35-42, bucket/reservoir.rs:69-76) of the ids
+// routed to each bucket, in call order: the first entry equal to the id is
+// replaced by the bucket's last entry (swap_remove); insertion counts stay.
+__global__ void remove_buckets_kernel(int nbuckets, int cap, const uint32_t* __restrict__ start,
+                                      const uint32_t* __restrict__ end,
+                                      const uint32_t* __restrict__ spos,
+                                      const uint32_t* __restrict__ ids, uint32_t* __restrict__ data,
+                                      uint32_t* __restrict__ len) {
+  const int key = blockIdx.x * blockDim.x + threadIdx.x;
+  if (key >= nbuckets) return;
+  const uint32_t s = start[key], e = end[key];
+  if (e <= s) return;
+  uint32_t* d = data + (size_t)key * cap;
+  uint32_t l = len[key];
+  for (uint32_t j = s; j < e; ++j) {
+    const uint32_t id = ids[spos[j]];
+    for (uint32_t q = 0; q < l; ++q)
+      if (d[q] == id) {
+        d[q] = d[l - 1];
+        --l;
+        break;
+      }
+  }
+  len[key] = l;
+}
+
+// LshIndexTrait::remove (lsh/index.rs:279-281 -> BucketStorage::remove_all,
+// :146-164): every bucket removes each listed id (its first occurrence) in
+// list order.  A bucket holding no listed id (bitmap over [0, bound)) is left
+// untouched; the others replay the list.
+__global__ void remove_all_kernel(int nbuckets, int cap, const uint32_t* __restrict__ ids,
+                                  int64_t n, const uint32_t* __restrict__ bits, uint32_t bound,
+                                  uint32_t* __restrict__ data, uint32_t* __restrict__ len) {
+  const int key = blockIdx.x * blockDim.x + threadIdx.x;
+  if (key >= nbuckets) return;
+  uint32_t* d = data + (size_t)key * cap;
+  uint32_t l = len[key];
+  bool any = false;
+  for (uint32_t q = 0; q < l && !any; ++q) {
+    const uint32_t v = d[q];
+    any = v < bound && ((bits[v >> 5] >> (v & 31)) & 1u);
+  }
+  if (!any) return;
+  for (int64_t i = 0; i < n && l > 0; ++i) {
+    const uint32_t id = ids[i];
+    for (uint32_t q = 0; q < l; ++q)
+      if (d[q] == id) {
+        d[q] = d[l - 1];
+        --l;
+        break;
+      }
+  }
+  len[key] = l;
+}
+
+__global__ void id_bits_kernel(const uint32_t* __restrict__ ids, int64_t n, uint32_t bound,
+                               uint32_t* __restrict__ bits) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n && ids[i] < bound) atomicOr(&bits[ids[i] >> 5], 1u << (ids[i] & 31));
+}
+
+// Largest id of the list (ids are below 2^31 for an index, checked by the
+// caller from this value).
 __global__ void max_id_kernel(const uint32_t* __restrict__ ids, int64_t n, uint32_t* __restrict__ mx) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) atomicMax(mx, ids[i] + 1u);
+  if (i < n) atomicMax(mx, ids[i]);
 }
 
 __global__ void index_clear_kernel(uint32_t* __restrict__ len, uint64_t* __restrict__ count, int nb) {
@@ -721,80 +784,107 @@ extern "C" int kh_lsh_index_clear(kh_lsh_index* idx, void* stream) {
   return KH_OK;
 }
 
+namespace {
+
+// Device scratch of one mutation call, freed on return (mutations are
+// `&mut self` calls and synchronise anyway).
+struct CallBufs {
+  std::vector<void*> v;
+  ~CallBufs() {
+    for (void* p : v) dev_free(p);
+  }
+  template <typename T>
+  T* get(size_t n) {
+    void* p = dev_alloc(sizeof(T) * (n ? n : 1));
+    if (p) v.push_back(p);
+    return static_cast<T*>(p);
+  }
+};
+
+// Largest id of ids_dev[0..n) (synchronises): ids of an index are below
+// 2^31, so that id + 1 bounds and bitmap word counts cannot wrap.
+int checked_max_id(const uint32_t* ids_dev, int64_t n, hipStream_t st, CallBufs& cb,
+                   uint32_t* out) {
+  uint32_t* mx = cb.get<uint32_t>(1);
+  if (!mx) return KH_ERR_ALLOC;
+  KH_HIP(hipMemsetAsync(mx, 0, sizeof(uint32_t), st));
+  hipLaunchKernelGGL(max_id_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, st, ids_dev, n, mx);
+  KH_LAUNCHED();
+  uint32_t v = 0;
+  KH_HIP(hipMemcpyAsync(&v, mx, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  KH_HIP(hipStreamSynchronize(st));
+  KH_CHECK_ARG(v < 0x80000000u, "neuron id %u out of range (ids must be below 2^31)", v);
+  *out = v;
+  return KH_OK;
+}
+
+// The (table, bucket) of every (vector, table) pair, grouped by bucket with
+// the vectors' order kept inside each group (stable radix sort): spos lists
+// vector positions, start/end delimit each bucket's run.
+struct Groups {
+  uint32_t *spos = nullptr, *start = nullptr, *end = nullptr;
+};
+int group_by_bucket(const kh_lsh_index* idx, const uint32_t* codes_dev, int64_t n, hipStream_t st,
+                    CallBufs& cb, Groups* g) {
+  KH_CHECK_ARG(n * idx->L < (int64_t)0x7fffffff, "too many vectors in one call");
+  const int64_t m = n * idx->L;
+  const int nbk = idx->L * idx->nb;
+  unsigned end_bit = 1;
+  while ((1ull << end_bit) < (unsigned long long)nbk) ++end_bit;
+  uint32_t* keys = cb.get<uint32_t>(m);
+  uint32_t* pos = cb.get<uint32_t>(m);
+  uint32_t* skeys = cb.get<uint32_t>(m);
+  g->spos = cb.get<uint32_t>(m);
+  g->start = cb.get<uint32_t>(nbk);
+  g->end = cb.get<uint32_t>(nbk);
+  if (!keys || !pos || !skeys || !g->spos || !g->start || !g->end) return KH_ERR_ALLOC;
+  size_t tmp_bytes = 0;
+  if (rocprim::radix_sort_pairs(nullptr, tmp_bytes, keys, skeys, pos, g->spos, (unsigned)m, 0u,
+                                end_bit, st) != hipSuccess) {
+    set_error("radix sort sizing failed");
+    return KH_ERR_HIP;
+  }
+  void* tmp = cb.get<uint8_t>(tmp_bytes);
+  if (!tmp) return KH_ERR_ALLOC;
+  hipLaunchKernelGGL(build_keys_kernel, dim3(ceil_div(m, 256)), dim3(256), 0, st, codes_dev, n,
+                     idx->L, idx->k, keys, pos);
+  KH_LAUNCHED();
+  if (rocprim::radix_sort_pairs(tmp, tmp_bytes, keys, skeys, pos, g->spos, (unsigned)m, 0u,
+                                end_bit, st) != hipSuccess) {
+    set_error("radix sort failed");
+    return KH_ERR_HIP;
+  }
+  KH_HIP(hipMemsetAsync(g->start, 0, sizeof(uint32_t) * nbk, st));
+  KH_HIP(hipMemsetAsync(g->end, 0, sizeof(uint32_t) * nbk, st));
+  hipLaunchKernelGGL(seg_bounds_kernel, dim3(ceil_div(m, 256)), dim3(256), 0, st, skeys, m,
+                     g->start, g->end);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
+}  // namespace
+
 extern "C" int kh_lsh_index_insert_codes(kh_lsh_index* idx, const uint32_t* ids_dev,
                                          const uint32_t* codes_dev, int64_t n, void* stream) {
   KH_CHECK_ARG(idx != nullptr, "null index");
   KH_CHECK_ARG(n >= 0, "bad n");
   if (n == 0) return KH_OK;
   KH_CHECK_ARG(ids_dev && codes_dev, "null argument");
-  KH_CHECK_ARG(n * idx->L < (int64_t)0x7fffffff, "too many inserts in one call");
   hipStream_t st = as_stream(stream);
-  const int64_t m = n * idx->L;
+  CallBufs cb;
+  uint32_t mx = 0;
+  int rc = checked_max_id(ids_dev, n, st, cb, &mx);  // before anything is inserted
+  if (rc != KH_OK) return rc;
+  Groups g;
+  rc = group_by_bucket(idx, codes_dev, n, st, cb, &g);
+  if (rc != KH_OK) return rc;
   const int nbk = idx->L * idx->nb;
-  unsigned end_bit = 1;
-  while ((1ull << end_bit) < (unsigned long long)nbk) ++end_bit;
-  // scratch: keys, pos, sorted keys, sorted pos, start, end, max id
-  uint32_t *keys = nullptr, *pos = nullptr, *skeys = nullptr, *spos = nullptr, *start = nullptr,
-           *end = nullptr, *mx = nullptr;
-  void* tmp = nullptr;
-  size_t tmp_bytes = 0;
-  int rc = KH_OK;
-  keys = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * m));
-  pos = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * m));
-  skeys = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * m));
-  spos = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * m));
-  start = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * nbk));
-  end = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * nbk));
-  mx = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t)));
-  if (!keys || !pos || !skeys || !spos || !start || !end || !mx) rc = KH_ERR_ALLOC;
-  if (rc == KH_OK &&
-      rocprim::radix_sort_pairs(nullptr, tmp_bytes, keys, skeys, pos, spos, (unsigned)m, 0u,
-                                end_bit, st) != hipSuccess) {
-    set_error("radix sort sizing failed");
-    rc = KH_ERR_HIP;
-  }
-  if (rc == KH_OK) {
-    tmp = dev_alloc(tmp_bytes);
-    if (!tmp) rc = KH_ERR_ALLOC;
-  }
-  if (rc == KH_OK) {
-    hipLaunchKernelGGL(build_keys_kernel, dim3(ceil_div(m, 256)), dim3(256), 0, st, codes_dev, n,
-                       idx->L, idx->k, keys, pos);
-    if (rocprim::radix_sort_pairs(tmp, tmp_bytes, keys, skeys, pos, spos, (unsigned)m, 0u,
-                                  end_bit, st) != hipSuccess) {
-      set_error("radix sort failed");
-      rc = KH_ERR_HIP;
-    }
-  }
-  if (rc == KH_OK) {
-    (void)hipMemsetAsync(start, 0, sizeof(uint32_t) * nbk, st);
-    (void)hipMemsetAsync(end, 0, sizeof(uint32_t) * nbk, st);
-    (void)hipMemsetAsync(mx, 0, sizeof(uint32_t), st);
-    hipLaunchKernelGGL(seg_bounds_kernel, dim3(ceil_div(m, 256)), dim3(256), 0, st, skeys, m,
-                       start, end);
-    hipLaunchKernelGGL(apply_buckets_kernel, dim3(ceil_div(nbk, 64)), dim3(64), 0, st, nbk,
-                       idx->cap, idx->type, start, end, spos, ids_dev, idx->data, idx->len,
-                       idx->count);
-    hipLaunchKernelGGL(max_id_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, st, ids_dev, n, mx);
-    uint32_t bound = 0;
-    if (hipGetLastError() != hipSuccess ||
-        hipMemcpyAsync(&bound, mx, sizeof(uint32_t), hipMemcpyDeviceToHost, st) != hipSuccess ||
-        hipStreamSynchronize(st) != hipSuccess) {
-      set_error("index build failed");
-      rc = KH_ERR_HIP;
-    } else {
-      idx->id_bound = std::max(idx->id_bound, bound);
-    }
-  }
-  dev_free(keys);
-  dev_free(pos);
-  dev_free(skeys);
-  dev_free(spos);
-  dev_free(start);
-  dev_free(end);
-  dev_free(mx);
-  dev_free(tmp);
-  return rc;
+  hipLaunchKernelGGL(apply_buckets_kernel, dim3(ceil_div(nbk, 64)), dim3(64), 0, st, nbk, idx->cap,
+                     idx->type, g.start, g.end, g.spos, ids_dev, idx->data, idx->len, idx->count);
+  KH_LAUNCHED();
+  KH_HIP(hipStreamSynchronize(st));  // the call's scratch is freed on return
+  idx->id_bound = std::max(idx->id_bound, mx + 1u);
+  return KH_OK;
 }
 
 extern "C" int kh_lsh_index_insert(kh_lsh_index* idx, const uint32_t* ids_dev, const float* w_dev,
@@ -804,22 +894,98 @@ extern "C" int kh_lsh_index_insert(kh_lsh_index* idx, const uint32_t* ids_dev, c
   if (n == 0) return KH_OK;
   KH_CHECK_ARG(ids_dev && w_dev, "null argument");
   hipStream_t st = as_stream(stream);
-  uint32_t* codes = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * n * idx->L));
+  CallBufs cb;
+  uint32_t* codes = cb.get<uint32_t>(n * idx->L);
   if (!codes) return KH_ERR_ALLOC;
   int rc = hash_dense_launch(idx->h, w_dev, ldw, n, codes, st);
   if (rc == KH_OK) rc = kh_lsh_index_insert_codes(idx, ids_dev, codes, n, stream);
-  dev_free(codes);
   return rc;
 }
+
+extern "C" int kh_lsh_index_insert_sparse(kh_lsh_index* idx, const uint32_t* ids_dev,
+                                          const int64_t* xoff_dev, const uint32_t* xidx_dev,
+                                          const float* xval_dev, int64_t n, void* stream) {
+  KH_CHECK_ARG(idx != nullptr, "null index");
+  KH_CHECK_ARG(n >= 0 && n <= 0x7fffffff, "bad n");
+  if (n == 0) return KH_OK;
+  KH_CHECK_ARG(ids_dev && xoff_dev, "null argument");
+  hipStream_t st = as_stream(stream);
+  CallBufs cb;
+  uint32_t* codes = cb.get<uint32_t>(n * idx->L);
+  if (!codes) return KH_ERR_ALLOC;
+  int rc = hash_sparse_launch(idx->h, xoff_dev, xidx_dev, xval_dev, n, codes, st);
+  if (rc == KH_OK) rc = kh_lsh_index_insert_codes(idx, ids_dev, codes, n, stream);
+  return rc;
+}
+
+extern "C" int kh_lsh_index_remove_codes(kh_lsh_index* idx, const uint32_t* ids_dev,
+                                         const uint32_t* codes_dev, int64_t n, void* stream) {
+  KH_CHECK_ARG(idx != nullptr, "null index");
+  KH_CHECK_ARG(n >= 0, "bad n");
+  if (n == 0) return KH_OK;
+  KH_CHECK_ARG(ids_dev && codes_dev, "null argument");
+  hipStream_t st = as_stream(stream);
+  CallBufs cb;
+  Groups g;
+  int rc = group_by_bucket(idx, codes_dev, n, st, cb, &g);
+  if (rc != KH_OK) return rc;
+  const int nbk = idx->L * idx->nb;
+  hipLaunchKernelGGL(remove_buckets_kernel, dim3(ceil_div(nbk, 64)), dim3(64), 0, st, nbk,
+                     idx->cap, g.start, g.end, g.spos, ids_dev, idx->data, idx->len);
+  KH_LAUNCHED();
+  KH_HIP(hipStreamSynchronize(st));
+  return KH_OK;
+}
+
+extern "C" int kh_lsh_index_remove_with_weights(kh_lsh_index* idx, const uint32_t* ids_dev,
+                                                const float* w_dev, int64_t n, int64_t ldw,
+                                                void* stream) {
+  KH_CHECK_ARG(idx != nullptr, "null index");
+  KH_CHECK_ARG(n >= 0 && ldw >= idx->h->dim, "bad n/ldw");
+  if (n == 0) return KH_OK;
+  KH_CHECK_ARG(ids_dev && w_dev, "null argument");
+  hipStream_t st = as_stream(stream);
+  CallBufs cb;
+  uint32_t* codes = cb.get<uint32_t>(n * idx->L);
+  if (!codes) return KH_ERR_ALLOC;
+  int rc = hash_dense_launch(idx->h, w_dev, ldw, n, codes, st);
+  if (rc == KH_OK) rc = kh_lsh_index_remove_codes(idx, ids_dev, codes, n, stream);
+  return rc;
+}
+
+extern "C" int kh_lsh_index_remove(kh_lsh_index* idx, const uint32_t* ids_dev, int64_t n,
+                                   void* stream) {
+  KH_CHECK_ARG(idx != nullptr, "null index");
+  KH_CHECK_ARG(n >= 0, "bad n");
+  if (n == 0 || idx->id_bound == 0) return KH_OK;
+  KH_CHECK_ARG(ids_dev != nullptr, "null argument");
+  hipStream_t st = as_stream(stream);
+  CallBufs cb;
+  const uint32_t words = (idx->id_bound + 31u) >> 5;  // id_bound <= 2^31
+  uint32_t* bits = cb.get<uint32_t>(words);
+  if (!bits) return KH_ERR_ALLOC;
+  KH_HIP(hipMemsetAsync(bits, 0, sizeof(uint32_t) * words, st));
+  hipLaunchKernelGGL(id_bits_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, st, ids_dev, n,
+                     idx->id_bound, bits);
+  KH_LAUNCHED();
+  const int nbk = idx->L * idx->nb;
+  hipLaunchKernelGGL(remove_all_kernel, dim3(ceil_div(nbk, 64)), dim3(64), 0, st, nbk, idx->cap,
+                     ids_dev, n, bits, idx->id_bound, idx->data, idx->len);
+  KH_LAUNCHED();
+  KH_HIP(hipStreamSynchronize(st));
+  return KH_OK;
+}
+
+enum { kQwCodes, kQwIds, kQwCnt, kQwLen };
 
 static int query_common(const kh_lsh_index* idx, const uint32_t* qcodes, int64_t batch,
                         int64_t* off, uint32_t* ids, uint32_t* counts, int64_t capacity,
                         hipStream_t st) {
-  auto* mi = const_cast<kh_lsh_index*>(idx);
+  WsSet* w = idx->ws.get(st);
   const int stride = query_stride(idx);
-  uint32_t* qids = static_cast<uint32_t*>(mi->q_ids.get(sizeof(uint32_t) * batch * stride));
-  uint32_t* qcnt = static_cast<uint32_t*>(mi->q_cnt.get(sizeof(uint32_t) * batch * stride));
-  int32_t* ulen = static_cast<int32_t*>(mi->q_len.get(sizeof(int32_t) * batch));
+  uint32_t* qids = static_cast<uint32_t*>(w->get(kQwIds, sizeof(uint32_t) * batch * stride));
+  uint32_t* qcnt = static_cast<uint32_t*>(w->get(kQwCnt, sizeof(uint32_t) * batch * stride));
+  int32_t* ulen = static_cast<int32_t*>(w->get(kQwLen, sizeof(int32_t) * batch));
   if (!qids || !qcnt || !ulen) return KH_ERR_ALLOC;
   int rc = query_launch(idx, qcodes, batch, qids, counts ? qcnt : nullptr, stride, ulen, st);
   if (rc != KH_OK) return rc;
@@ -838,8 +1004,7 @@ extern "C" int kh_lsh_index_query(const kh_lsh_index* idx, const float* x_dev, i
     return KH_OK;
   }
   KH_CHECK_ARG(x_dev != nullptr, "null input");
-  auto* mi = const_cast<kh_lsh_index*>(idx);
-  uint32_t* qcodes = static_cast<uint32_t*>(mi->q_codes.get(sizeof(uint32_t) * batch * idx->L));
+  uint32_t* qcodes = static_cast<uint32_t*>(idx->ws.get(st)->get(kQwCodes, sizeof(uint32_t) * batch * idx->L));
   if (!qcodes) return KH_ERR_ALLOC;
   int rc = hash_dense_launch(idx->h, x_dev, idx->h->dim, batch, qcodes, st);
   if (rc != KH_OK) return rc;
@@ -857,8 +1022,7 @@ extern "C" int kh_lsh_index_query_sparse(const kh_lsh_index* idx, const int64_t*
     KH_HIP(hipMemsetAsync(off_dev, 0, sizeof(int64_t), st));
     return KH_OK;
   }
-  auto* mi = const_cast<kh_lsh_index*>(idx);
-  uint32_t* qcodes = static_cast<uint32_t*>(mi->q_codes.get(sizeof(uint32_t) * batch * idx->L));
+  uint32_t* qcodes = static_cast<uint32_t*>(idx->ws.get(st)->get(kQwCodes, sizeof(uint32_t) * batch * idx->L));
   if (!qcodes) return KH_ERR_ALLOC;
   int rc = hash_sparse_launch(idx->h, xoff_dev, xidx_dev, xval_dev, batch, qcodes, st);
   if (rc != KH_OK) return rc;

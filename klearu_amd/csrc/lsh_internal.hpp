@@ -22,8 +22,8 @@ struct kh_lsh_index {
   uint32_t* data = nullptr;   // [L][nb][cap]
   uint32_t* len = nullptr;    // [L][nb]
   uint64_t* count = nullptr;  // [L][nb]
-  uint32_t id_bound = 0;      // 1 + largest id inserted so far
-  kh::Scratch q_codes, q_ids, q_cnt, q_len;
+  uint32_t id_bound = 0;      // 1 + largest id inserted so far (ids are below 2^31)
+  mutable kh::StreamWs ws;    // query scratch per stream
 };
 
 namespace kh {

@@ -307,7 +307,7 @@ struct kh_slide_layer {
   float* bias = nullptr;
   kh_lsh_index* index = nullptr;
   int sampling = 0, top_k = 0, threshold = 0, act = 0;
-  Scratch codes, qids, qcnt, qlen, aids, alen, pre, post;
+  mutable StreamWs ws;  // forward scratch per stream
 };
 
 struct kh_dense_layer {
@@ -390,19 +390,20 @@ static int slide_forward_common(const kh_slide_layer* lc, const float* x, const 
                                 const uint32_t* xidx, const float* xval, int64_t batch,
                                 int64_t* off, uint32_t* act_ids, float* pre_out, float* act_out,
                                 int64_t capacity, hipStream_t st) {
-  auto* l = const_cast<kh_slide_layer*>(lc);
+  const kh_slide_layer* l = lc;
   const kh_lsh_index* idx = l->index;
   const int L = idx->L;
-  uint32_t* codes = static_cast<uint32_t*>(l->codes.get(sizeof(uint32_t) * batch * L));
+  WsSet* w = l->ws.get(st);
+  uint32_t* codes = static_cast<uint32_t*>(w->get(0, sizeof(uint32_t) * batch * L));
   const int qs = query_stride(idx);
-  uint32_t* qids = static_cast<uint32_t*>(l->qids.get(sizeof(uint32_t) * batch * qs));
-  uint32_t* qcnt = static_cast<uint32_t*>(l->qcnt.get(sizeof(uint32_t) * batch * qs));
-  int32_t* qlen = static_cast<int32_t*>(l->qlen.get(sizeof(int32_t) * batch));
+  uint32_t* qids = static_cast<uint32_t*>(w->get(1, sizeof(uint32_t) * batch * qs));
+  uint32_t* qcnt = static_cast<uint32_t*>(w->get(2, sizeof(uint32_t) * batch * qs));
+  int32_t* qlen = static_cast<int32_t*>(w->get(3, sizeof(int32_t) * batch));
   const int as = std::max(qs, l->n);
-  uint32_t* aids = static_cast<uint32_t*>(l->aids.get(sizeof(uint32_t) * batch * as));
-  int32_t* alen = static_cast<int32_t*>(l->alen.get(sizeof(int32_t) * batch));
-  float* pre = static_cast<float*>(l->pre.get(sizeof(float) * batch * as));
-  float* post = static_cast<float*>(l->post.get(sizeof(float) * batch * as));
+  uint32_t* aids = static_cast<uint32_t*>(w->get(4, sizeof(uint32_t) * batch * as));
+  int32_t* alen = static_cast<int32_t*>(w->get(5, sizeof(int32_t) * batch));
+  float* pre = static_cast<float*>(w->get(6, sizeof(float) * batch * as));
+  float* post = static_cast<float*>(w->get(7, sizeof(float) * batch * as));
   if (!codes || !qids || !qcnt || !qlen || !aids || !alen || !pre || !post) return KH_ERR_ALLOC;
   int rc = xoff ? hash_sparse_launch(idx->h, xoff, xidx, xval, batch, codes, st)
                 : hash_dense_launch(idx->h, x, l->dim, batch, codes, st);

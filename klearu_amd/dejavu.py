@@ -202,6 +202,11 @@ class Mlp:
         _lib.call("kh_sparse_ffn_last_hidden", self._h, ptr(h), batch, n_active, stream_ptr(stream))
         return h
 
+    def status(self):
+        """Raise KlearuError (KH_ERR_ARG) if a forward since the last status call saw an
+        active id outside [0, intermediate) (the reference panics in get_weights)."""
+        _lib.call("kh_sparse_ffn_status", self._h)
+
 
 def forward_sparse(mlp: Mlp, x, active_neurons, stream=None) -> torch.Tensor:
     """sparse_mlp::forward_sparse: x [hidden] or [batch, hidden] sharing one active set."""

@@ -193,6 +193,34 @@ class LshIndex:
         codes = to_device(codes, np.uint32)
         _lib.call("kh_lsh_index_insert_codes", self._h, ptr(ids), ptr(codes), ids.numel(), stream_ptr(stream))
 
+    def insert_sparse_batch(self, ids, vectors, stream=None):
+        """insert_sparse (index.rs:264-269) for (id, SparseVector) pairs in order."""
+        ids = to_device(np.asarray(ids, np.uint32) if not isinstance(ids, torch.Tensor) else ids, np.uint32)
+        xo, xi, xv = csr_batch(vectors)
+        _lib.call("kh_lsh_index_insert_sparse", self._h, ptr(ids), ptr(xo), ptr(xi), ptr(xv), ids.numel(),
+                  stream_ptr(stream))
+
+    def insert_sparse(self, id: int, weights):
+        self.insert_sparse_batch(np.array([id], np.uint32), [weights])
+
+    def remove_with_weights_batch(self, ids, W, stream=None):
+        """remove_with_weights (index.rs:271-276) for (id, dense weights) pairs in order."""
+        ids = to_device(np.asarray(ids, np.uint32) if not isinstance(ids, torch.Tensor) else ids, np.uint32)
+        W = to_device(W, np.float32).reshape(ids.numel(), -1)
+        _lib.call("kh_lsh_index_remove_with_weights", self._h, ptr(ids), ptr(W), ids.numel(), W.shape[1],
+                  stream_ptr(stream))
+
+    def remove_with_weights(self, id: int, dense_weights):
+        self.remove_with_weights_batch(np.array([id], np.uint32), np.asarray(dense_weights, np.float32)[None, :])
+
+    def remove_batch(self, ids, stream=None):
+        """remove (index.rs:278-280) of each id, in order, from every bucket."""
+        ids = to_device(np.asarray(ids, np.uint32) if not isinstance(ids, torch.Tensor) else ids, np.uint32)
+        _lib.call("kh_lsh_index_remove", self._h, ptr(ids), ids.numel(), stream_ptr(stream))
+
+    def remove(self, id: int):
+        self.remove_batch(np.array([id], np.uint32))
+
     def clear(self, stream=None):
         _lib.call("kh_lsh_index_clear", self._h, stream_ptr(stream))
 

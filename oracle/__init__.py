@@ -75,6 +75,8 @@ _sig("or_hash_sparse", C.c_uint64, _i8p, _int, _int, _int, _u32p, _f32p, _i64)
 _sig("or_hash_dense_batch", None, _i8p, _int, _int, _int, _f32p, _i64, _u32p)
 _sig("or_reservoir_rand", C.c_uint64, C.c_uint64, C.c_uint64)
 _sig("or_lsh_insert_many", None, _int, _int, _int, _int, _u32p, _u32p, _u64p, _i64, _u32p, _u32p)
+_sig("or_lsh_remove_many", None, _int, _int, _int, _u32p, _u32p, _i64, _u32p, _u32p)
+_sig("or_lsh_remove_all", None, _int, _int, _int, _u32p, _u32p, _i64, _u32p)
 _sig("or_lsh_query", _i64, _int, _int, _int, _u32p, _u32p, _u32p, _u32p, _u32p)
 _sig("or_sample_topk", _i64, _u32p, _u32p, _i64, _i64, _u32p)
 _sig("or_sample_threshold", _i64, _u32p, _u32p, _i64, C.c_uint32, _u32p)
@@ -255,6 +257,16 @@ class LshIndex:
         ids, codes = u32(ids), u32(codes).reshape(-1)
         lib.or_lsh_insert_many(self.L, self.k, self.cap, self.type, self.data, self.len, self.count,
                                ids.size, ids, codes)
+
+    def remove_many(self, ids, codes):
+        """remove_with_weights for each (id, codes row) in order (lsh/index.rs:271-276)."""
+        ids, codes = u32(ids), u32(codes).reshape(-1)
+        lib.or_lsh_remove_many(self.L, self.k, self.cap, self.data, self.len, ids.size, ids, codes)
+
+    def remove_all(self, ids):
+        """remove for each id in order: every bucket drops the id (lsh/index.rs:278-280)."""
+        ids = u32(ids)
+        lib.or_lsh_remove_all(self.L, self.k, self.cap, self.data, self.len, ids.size, ids)
 
     def query(self, codes):
         codes = u32(codes).reshape(-1)

@@ -418,6 +418,42 @@ void or_lsh_insert_many(int num_tables, int k, int cap, int bucket_type, uint32_
     }
 }
 
+/* Bucket::remove for FIFO and reservoir buckets (bucket/fifo.rs:35-42,
+ * bucket/reservoir.rs:69-76): the first entry equal to id is replaced by the
+ * last entry (Vec::swap_remove); the insertion count is unchanged.  Returns 1
+ * when something was removed. */
+static int bucket_remove(uint32_t* d, uint32_t* len, uint32_t id) {
+  for (uint32_t q = 0; q < *len; ++q)
+    if (d[q] == id) {
+      d[q] = d[*len - 1];
+      *len -= 1;
+      return 1;
+    }
+  return 0;
+}
+
+/* LshIndexTrait::remove_with_weights (lsh/index.rs:271-276) for n vectors in
+ * order, tables inner, from their codes[n][num_tables]. */
+void or_lsh_remove_many(int num_tables, int k, int cap, uint32_t* data, uint32_t* len, int64_t n,
+                        const uint32_t* ids, const uint32_t* codes) {
+  const int64_t nb = (int64_t)1 << k;
+  for (int64_t i = 0; i < n; ++i)
+    for (int t = 0; t < num_tables; ++t) {
+      int64_t b = (int64_t)(codes[i * num_tables + t] & (uint32_t)(nb - 1));
+      int64_t slot = (int64_t)t * nb + b;
+      bucket_remove(data + slot * cap, len + slot, ids[i]);
+    }
+}
+
+/* LshIndexTrait::remove (lsh/index.rs:278-280 -> BucketStorage::remove_all,
+ * :146-164) for n ids in order: every bucket of every table removes the id. */
+void or_lsh_remove_all(int num_tables, int k, int cap, uint32_t* data, uint32_t* len, int64_t n,
+                       const uint32_t* ids) {
+  const int64_t nbk = (int64_t)num_tables << k;
+  for (int64_t i = 0; i < n; ++i)
+    for (int64_t slot = 0; slot < nbk; ++slot) bucket_remove(data + slot * cap, len + slot, ids[i]);
+}
+
 static int cmp_u32(const void* a, const void* b) {
   uint32_t x = *(const uint32_t*)a, y = *(const uint32_t*)b;
   return x < y ? -1 : (x > y ? 1 : 0);

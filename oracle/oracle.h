@@ -77,6 +77,10 @@ uint64_t or_reservoir_rand(uint64_t seed, uint64_t bound);
 void or_lsh_insert_many(int num_tables, int k, int cap, int bucket_type, uint32_t* data,
                         uint32_t* len, uint64_t* count, int64_t n, const uint32_t* ids,
                         const uint32_t* codes);
+void or_lsh_remove_many(int num_tables, int k, int cap, uint32_t* data, uint32_t* len, int64_t n,
+                        const uint32_t* ids, const uint32_t* codes);
+void or_lsh_remove_all(int num_tables, int k, int cap, uint32_t* data, uint32_t* len, int64_t n,
+                       const uint32_t* ids);
 int64_t or_lsh_query(int num_tables, int k, int cap, const uint32_t* data, const uint32_t* len,
                      const uint32_t* codes, uint32_t* out_ids, uint32_t* out_counts);
 

@@ -396,3 +396,76 @@ def test_batched_norm_select_union_exact(kh, orc):
         np.testing.assert_array_equal(ids[b].cpu().numpy(), sel)
         want_u |= set(sel.tolist())
     np.testing.assert_array_equal(uni.cpu().numpy(), np.array(sorted(want_u), np.int32))
+
+
+def test_sparse_ffn_out_of_range_ids_are_reported(kh, orc):
+    """An active id outside [0, intermediate) (the reference panics in
+    get_weights, crates/klearu-accel/src/memory/mod.rs:87-92) reads no memory
+    outside the weights and is reported by the handle's status call, once."""
+    from klearu_amd import KlearuError
+    from klearu_amd._lib import KH_ERR_ARG
+    from klearu_amd.dejavu import Mlp
+    rng = np.random.default_rng(4)
+    H, I = 512, 300
+    wg, wu, wd, x, _ = _ffn_case(orc, rng, H, I, 8, 2)
+    for batch in (1, 2):
+        mlp = Mlp(wg, wu, wd, max_batch=2)
+        mlp.status()
+        xd = torch.from_numpy(x[:batch].copy()).cuda()
+        for bad in (I, -1, 1 << 30):
+            act = torch.tensor([3, bad, 7], dtype=torch.int32, device="cuda")
+            y = torch.zeros(batch, H, device="cuda")
+            mlp.forward_sparse_into(xd, act, y)
+            with pytest.raises(KlearuError) as e:
+                mlp.status()
+            assert e.value.code == KH_ERR_ARG
+            mlp.status()   # the record was cleared
+        good = torch.tensor([3, 7], dtype=torch.int32, device="cuda")
+        mlp.forward_sparse_into(xd, good, torch.zeros(batch, H, device="cuda"))
+        mlp.status()
+
+
+def test_predictor_concurrent_streams(kh, orc):
+    """SparsityPredictor::select_top_k takes &self: two host threads on their
+    own streams select on one predictor at the same time; every selection is
+    the oracle's."""
+    import threading
+    from klearu_amd.dejavu import ORDER_ASCENDING, ORDER_SCORE, SparsityPredictor
+    rng = np.random.default_rng(12)
+    H, R, I, k = 4096, 256, 11008, 1652
+    w1, b1, w2, b2 = make_predictor(orc, rng, H, R, I, bias=True)
+    p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
+    xs = [rng.standard_normal((2, H)).astype(np.float32) for _ in range(2)]
+    want = []
+    for x in xs:
+        rows = []
+        for b in range(2):
+            s, _ = orc.predictor_predict(w1, b1, w2, b2, x[b])
+            rows.append(orc.select_top_k(s, k))
+        want.append(rows)
+    errors = []
+
+    def worker(t):
+        try:
+            s = torch.cuda.Stream()
+            xd = torch.from_numpy(xs[t]).cuda()
+            order = ORDER_SCORE if t == 0 else ORDER_ASCENDING
+            for _ in range(10):
+                with torch.cuda.stream(s):
+                    ids = p.select_top_k(xd, k, order, stream=s)
+                s.synchronize()
+                got = ids.cpu().numpy()
+                for b in range(2):
+                    w = want[t][b] if order == ORDER_SCORE else np.sort(want[t][b])
+                    if not np.array_equal(got[b], w):
+                        errors.append((t, b))
+                        return
+        except Exception as e:  # noqa: BLE001 -- reported below
+            errors.append((t, repr(e)))
+
+    th = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert not errors, errors

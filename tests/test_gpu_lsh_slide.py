@@ -436,3 +436,102 @@ def test_xc_network_scaled_cfg5(kh, orc):
     o = got[0].cpu().numpy()
     for r in range(24):
         assert abs(act[o[r]:o[r + 1]].astype(np.float64).sum() - 1.0) < 1e-4
+
+
+# ----------------------------------------------------------------------------- mutators
+@pytest.mark.parametrize("bt", [FIFO, RESERVOIR])
+def test_remove_and_reinsert_bit_exact(kh, orc, bt):
+    """insert -> remove_with_weights -> insert -> remove (every bucket) ->
+    insert_sparse, each against the oracle's replay of the reference's bucket
+    rules (swap_remove, counts kept, refills after removal): buckets, lengths
+    and insertion counts bit-exact.  The removal lists hold repeated ids and
+    ids that were never inserted."""
+    from klearu_amd.lsh import LshIndex, SimHash, SparseVector
+    rng = np.random.default_rng(5 + bt)
+    dim, k, L, cap = 64, 4, 8, 12
+    fam = SimHash(dim, k, L, 17)
+    planes = fam.planes()
+    idx = LshIndex(fam, bt, cap)
+    ref = orc.LshIndex(L, k, cap, bt)
+    W = rng.normal(0, 0.01, (600, dim)).astype(np.float32)
+    ids = np.arange(600, dtype=np.uint32)
+    idx.insert_batch(ids[:400], W[:400])
+    ref.insert_many(ids[:400], orc.hash_dense_batch(planes, W[:400]))
+    gone = np.concatenate([rng.choice(400, 80, replace=False), [5, 5, 599, 450]]).astype(np.uint32)
+    idx.remove_with_weights_batch(gone, W[gone])
+    ref.remove_many(gone, orc.hash_dense_batch(planes, W[gone]))
+    assert_buckets_equal(idx, ref)
+    idx.insert_batch(ids[400:], W[400:])
+    ref.insert_many(ids[400:], orc.hash_dense_batch(planes, W[400:]))
+    all_gone = np.concatenate([rng.choice(600, 50, replace=False), [7, 7, 12345]]).astype(np.uint32)
+    idx.remove_batch(all_gone)
+    ref.remove_all(all_gone)
+    assert_buckets_equal(idx, ref)
+    rows = [SparseVector(np.sort(rng.choice(dim, 9, replace=False)).astype(np.uint32),
+                         rng.normal(0, 1, 9).astype(np.float32), dim) for _ in range(40)]
+    sids = np.arange(1000, 1040, dtype=np.uint32)
+    idx.insert_sparse_batch(sids, rows)
+    dense = np.zeros((40, dim), np.float32)
+    for i, r in enumerate(rows):
+        dense[i, r.indices] = r.values
+    ref.insert_many(sids, orc.hash_dense_batch(planes, dense))
+    assert_buckets_equal(idx, ref)
+
+
+def test_index_rejects_ids_at_or_above_2_31(kh, orc):
+    """Ids must be below 2^31 (id + 1 bounds and bitmap sizes cannot wrap);
+    such an insert is refused before anything changes."""
+    from klearu_amd import KlearuError
+    from klearu_amd._lib import KH_ERR_ARG
+    from klearu_amd.lsh import LshIndex, SimHash
+    fam = SimHash(16, 3, 4, 5)
+    idx = LshIndex(fam, FIFO, 6)
+    codes = np.zeros((3, 4), np.uint32)
+    for bad in (0x80000000, 0xFFFFFFFF):
+        with pytest.raises(KlearuError) as e:
+            idx.insert_codes(np.array([1, bad, 2], np.uint32), codes)
+        assert e.value.code == KH_ERR_ARG
+    _, ln, cnt = idx.buckets()
+    assert ln.sum() == 0 and cnt.sum() == 0
+
+
+def test_concurrent_queries_two_streams_two_threads(kh, orc):
+    """The reference's LshIndex is Send + Sync and query takes &self: two host
+    threads, each on its own stream, query one index (and one SLIDE layer)
+    many times while the other does; every result matches the oracle."""
+    import threading
+    from klearu_amd.lsh import SimHash
+    rng = np.random.default_rng(23)
+    fam = SimHash(784, 6, 50, 42 + 1_000_000)
+    W = rng.normal(0, 0.01, (1024, 784)).astype(np.float32)
+    idx, ref = build_pair(kh, orc, fam, FIFO, 128, W)
+    X = [cfg1_inputs(rng, 32) for _ in range(2)]
+    codes = [orc.hash_dense_batch(fam.planes(), x) for x in X]
+    want = [[ref.query(c[b]) for b in range(32)] for c in codes]
+    errors = []
+
+    def worker(t):
+        try:
+            s = torch.cuda.Stream()
+            xd = torch.from_numpy(X[t]).cuda()
+            for _ in range(20):
+                with torch.cuda.stream(s):
+                    off, ids, cnt = idx.query_batch(xd, stream=s)
+                s.synchronize()
+                o = off.cpu().numpy()
+                i = ids.cpu().numpy().view(np.uint32)
+                c = cnt.cpu().numpy().view(np.uint32)
+                for b in range(32):
+                    if not (np.array_equal(i[o[b]:o[b + 1]], want[t][b][0]) and
+                            np.array_equal(c[o[b]:o[b + 1]], want[t][b][1])):
+                        errors.append((t, b))
+                        return
+        except Exception as e:  # noqa: BLE001 -- reported below
+            errors.append((t, repr(e)))
+
+    th = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert not errors, errors

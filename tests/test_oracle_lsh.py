@@ -237,3 +237,88 @@ def test_slide_forward_invariants(orc):
     out, _ = orc.slide_layer_oracle(planes, cap, FIFO, W, b, X[:2], index=empty)
     for ids, _, _ in out:
         np.testing.assert_array_equal(ids, np.arange(n, dtype=np.uint32))
+
+
+def _one_bucket(orc, cap, typ):
+    return orc.LshIndex(1, 1, cap, typ)
+
+
+@pytest.mark.parametrize("typ", [FIFO, RES])
+def test_remove_kats(orc, typ):
+    """Bucket::remove (fifo.rs:117-139, reservoir.rs:148-170): an existing id
+    goes, a missing id or an empty bucket changes nothing; the slot is filled
+    by the last entry as Vec::swap_remove documents (the removed element is
+    replaced by the last one), and the insertion count stays."""
+    z = lambda n: np.zeros(n, np.uint32)  # noqa: E731 -- every vector in bucket 0
+    b = _one_bucket(orc, 4, typ)
+    b.insert_many([1, 2, 3], z(3))
+    b.remove_many([2], z(1))
+    assert list(b.bucket(0, 0)) == [1, 3] and 2 not in b.bucket(0, 0)
+    b = _one_bucket(orc, 4, typ)
+    b.insert_many([1], z(1))
+    b.remove_many([99], z(1))
+    assert list(b.bucket(0, 0)) == [1]
+    b = _one_bucket(orc, 4, typ)
+    b.remove_many([1], z(1))
+    assert list(b.bucket(0, 0)) == []
+    # swap_remove: [1, 2, 3, 4] without 2 is [1, 4, 3]; only the first of two
+    # equal entries goes
+    b = _one_bucket(orc, 6, typ)
+    b.insert_many([1, 2, 3, 4, 2], z(5))
+    b.remove_many([2], z(1))
+    assert list(b.bucket(0, 0)) == [1, 2, 3, 4]
+    b = _one_bucket(orc, 4, typ)
+    b.insert_many([1, 2, 3, 4], z(4))
+    cnt = int(b.count[0])
+    b.remove_many([2], z(1))
+    assert list(b.bucket(0, 0)) == [1, 4, 3] and int(b.count[0]) == cnt
+
+
+def test_fifo_eviction_after_remove(orc):
+    """After a removal the FIFO appends while it has room and then evicts its
+    first entry (fifo.rs:27-33): [1,2,3,4] - 2 -> [1,4,3] + 5 -> [1,4,3,5]
+    + 6 -> [4,3,5,6]."""
+    z = lambda n: np.zeros(n, np.uint32)  # noqa: E731
+    b = _one_bucket(orc, 4, FIFO)
+    b.insert_many([1, 2, 3, 4], z(4))
+    b.remove_many([2], z(1))
+    b.insert_many([5], z(1))
+    assert list(b.bucket(0, 0)) == [1, 4, 3, 5]
+    b.insert_many([6], z(1))
+    assert list(b.bucket(0, 0)) == [4, 3, 5, 6]
+
+
+def test_reservoir_refills_after_remove(orc):
+    """A full reservoir bucket that loses an entry pushes the next insert
+    (len < cap) whatever its count (reservoir.rs:51-58)."""
+    z = lambda n: np.zeros(n, np.uint32)  # noqa: E731
+    b = _one_bucket(orc, 3, RES)
+    b.insert_many(list(range(10, 30)), z(20))
+    full = list(b.bucket(0, 0))
+    assert len(full) == 3 and int(b.count[0]) == 20
+    b.remove_many([full[0]], z(1))
+    b.insert_many([99], z(1))
+    assert list(b.bucket(0, 0)) == [full[2], full[1], 99] and int(b.count[0]) == 21
+
+
+@pytest.mark.parametrize("typ", [FIFO, RES])
+def test_remove_all_matches_targeted_remove(orc, typ):
+    """remove (every bucket, lsh/index.rs:278-280) leaves the same tables as
+    remove_with_weights (lsh/index.rs:271-276) for ids that live only in the
+    buckets their own codes name, and removed ids appear nowhere
+    (index.rs:455-483)."""
+    rng = np.random.default_rng(7)
+    L, k, cap, n = 6, 3, 8, 120
+    codes = rng.integers(0, 1 << k, (n, L)).astype(np.uint32)
+    ids = np.arange(n, dtype=np.uint32)
+    a, b = orc.LshIndex(L, k, cap, typ), orc.LshIndex(L, k, cap, typ)
+    a.insert_many(ids, codes)
+    b.insert_many(ids, codes)
+    gone = rng.choice(n, 30, replace=False).astype(np.uint32)
+    a.remove_many(gone, codes[gone])
+    b.remove_all(gone)
+    np.testing.assert_array_equal(a.len, b.len)
+    for t in range(L):
+        for bb in range(1 << k):
+            assert list(a.bucket(t, bb)) == list(b.bucket(t, bb))
+            assert not set(a.bucket(t, bb).tolist()) & set(gone.tolist())
