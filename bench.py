@@ -45,7 +45,7 @@ sys.path.insert(0, ROOT)
 METRIC = "sparse FFN tokens/s @7B shape; gathered-weight HBM GB/s vs roofline"
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ffn_fused1_cfg3_traffic.txt")
-ALL_LEGS = ["cfg3", "cfg3b16", "cfg2", "cfg4", "cfg4b8", "cfg1", "cfg5"]
+ALL_LEGS = ["cfg3", "cfg3b16", "cfg2", "cfg4", "cfg4b8", "decoder", "cfg1", "cfg5"]
 
 
 def log(*a):
@@ -285,6 +285,75 @@ def attn_leg(name, L, B, steps, warmup, seed, timer, cpu_seconds):
     torch.cuda.empty_cache()
     if cpu_seconds > 0 and B == 1:
         res["cpu"] = cpu_attention(cpu_seconds, seed, L)
+    return res
+
+
+def decoder_leg(L, steps, warmup, seed, timer, cpu_tok_s=None):
+    """cfg3 and cfg4 composed into sparse decoder layers, as
+    SparseModel::forward_decode_sparse runs them (crates/klearu-llm/src/sparse/mod.rs:55-143):
+    per layer kh_dejavu_attn_block (16 of 32 heads, KV ~2048 BF16) then
+    kh_dejavu_mlp_block (1652 of 11008 neurons), 7B shape, batch 1, one graph."""
+    import torch
+    from klearu_amd import _lib
+    from klearu_amd._dev import ptr, stream_ptr
+    from klearu_amd.attention import SparseAttention
+    from klearu_amd.dejavu import SparsityPredictor, keep_count
+
+    H, I, nh, nkv, d, S, Rh, Rn = 4096, 11008, 32, 32, 128, 2048, 128, 256
+    kh_, kn = keep_count(nh, 0.5), keep_count(I, 0.15)
+    pre = S - (warmup + steps + 8)        # every replay appends one position per layer
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    t0 = time.time()
+    mlps, npreds = build_ffn_model(L, H, I, Rn, seed + 1, 1)
+    attns, hpreds = [], []
+    kv = torch.randn(2, nkv, pre, d, generator=g, device="cuda")
+    for _ in range(L):
+        ws = [(torch.randn(shape, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+              for shape in ((nh * d, H), (nkv * d, H), (nkv * d, H), (H, nh * d))]
+        a = SparseAttention(H, nh, nkv, d, *ws, S, 1, 10000.0)
+        a.load_cache_dev(0, kv[0], kv[1])
+        attns.append(a)
+        del ws
+        w1 = bf16_round(rng.normal(0, 0.02, (Rh, H)))
+        w2 = bf16_round(rng.normal(0, 0.1, (nh, Rh)))
+        hpreds.append(SparsityPredictor(w1, np.zeros(Rh, np.float32), w2, np.zeros(nh, np.float32)))
+    del kv
+    torch.cuda.synchronize()
+    log(f"[bench] decoder: {L} layers ready in {time.time() - t0:.1f}s")
+    hidden = torch.randn(1, H, generator=g, device="cuda")
+    w_norm = torch.ones(H, device="cuda")
+    norm_ws = torch.empty(1, dtype=torch.float32, device="cuda")
+    heads = [torch.empty(kh_, dtype=torch.int32, device="cuda") for _ in range(L)]
+    active = [torch.empty(kn, dtype=torch.int32, device="cuda") for _ in range(L)]
+
+    def step():
+        st = stream_ptr()
+        for l in range(L):
+            _lib.call("kh_dejavu_attn_block", hpreds[l]._h, attns[l]._h, ptr(hidden), ptr(w_norm), 1e-5, kh_,
+                      ptr(heads[l]), ptr(norm_ws), st)
+            _lib.call("kh_dejavu_mlp_block", npreds[l]._h, mlps[l]._h, ptr(hidden), ptr(w_norm), 1e-5, kn,
+                      ptr(active[l]), ptr(norm_ws), st)
+
+    gr = timer.graph(step)
+    ms = timer.time(gr.replay, steps, warmup)
+    ctx = pre + 1 + warmup + steps // 2 + 1
+    bytes_layer = (2 * nkv * d * H * 2 + 2 * kh_ * d * H * 2 + kh_ * ctx * d * 2 * 2 + (Rh * H + nh * Rh) * 2
+                   + 3 * kn * H * 2 + (Rn * H + I * Rn) * 2)
+    gbs = L * bytes_layer / (ms * 1e-3) / 1e9
+    res = dict(workload=f"sparse decoder layers, 7B shape: per layer head-sparse attention (16 of 32 heads, KV "
+                        f"{S} BF16 with RoPE, head predictor rank {Rh}) then sparse SwiGLU FFN ({kn} of {I} "
+                        f"neurons, predictor rank {Rn}), batch 1, {L} layers",
+               unit="tokens/s", value=round(1000.0 / ms, 2), ms_per_step=round(ms, 4), hbm_gbs=round(gbs, 1),
+               frac=round(gbs / HBM_PEAK_GBS, 4), bytes_per_token_layer=int(bytes_layer), mean_context=ctx)
+    if cpu_tok_s:
+        # the CPU ports of the two halves, per token: 1 / (1/attention + 1/FFN)
+        res["cpu"] = dict(value=round(1.0 / (1.0 / cpu_tok_s[0] + 1.0 / cpu_tok_s[1]), 4), unit="tokens/s",
+                          cores=1, kind="port",
+                          sample="sum of the timed cfg4 (attention) and cfg3 (FFN) CPU port samples, per token")
+    del attns, hpreds, mlps, npreds
+    torch.cuda.empty_cache()
     return res
 
 
@@ -560,16 +629,22 @@ def main():
         if name in legs:
             extra[name] = attn_leg(name, args.layers, B, min(args.steps, 30), 3, args.seed + 4, timer, leg_cpu)
             log(f"[bench] {name} {extra[name]['ms_per_step']:.3f} ms  {extra[name]['hbm_gbs']:.0f} GB/s")
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_ffn(args.cpu_seconds, args.seed, 4096, 11008, 256, 0.15, args.layers)
+        log(f"[bench] cpu baseline {cpu['value']:.3f} tokens/s")
+    if "decoder" in legs:
+        halves = None
+        if cpu and "cpu" in extra.get("cfg4", {}):
+            halves = (extra["cfg4"]["cpu"]["value"], cpu["value"])
+        extra["decoder"] = decoder_leg(args.layers, min(args.steps, 30), 3, args.seed + 6, timer, halves)
+        log(f"[bench] decoder {extra['decoder']['ms_per_step']:.3f} ms  {extra['decoder']['hbm_gbs']:.0f} GB/s")
     if "cfg1" in legs:
         extra["cfg1"] = slide_cfg1_leg(min(args.steps, 30), args.seed, timer, leg_cpu)
         log(f"[bench] cfg1 {extra['cfg1']['ms_per_step']:.3f} ms  |A|={extra['cfg1']['mean_active']:.0f}")
     if "cfg5" in legs:
         extra["cfg5"] = slide_cfg5_leg(min(args.steps, 20), args.seed, timer, leg_cpu)
         log(f"[bench] cfg5 {extra['cfg5']['ms_per_step']:.3f} ms  |A|={extra['cfg5']['mean_active']:.0f}")
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_ffn(args.cpu_seconds, args.seed, 4096, 11008, 256, 0.15, args.layers)
-        log(f"[bench] cpu baseline {cpu['value']:.3f} tokens/s")
     per_call_ms = r["ms_ffn"] / args.layers
     traffic = read_traffic()
     out = {

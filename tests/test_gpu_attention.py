@@ -255,3 +255,52 @@ def test_attn_block_chained(kh, orc, H, nh, nkv, d, R, k, pre, steps):
         want = h_in + c.oracle_step(0, norm, sel.tolist())
         close(hd.cpu().numpy(), want, f"step {step}")
     assert c.attn.current_len(0) == pre + steps
+
+
+def test_decoder_layers_chained_7b(kh, orc):
+    """Two sparse decoder layers at the 7B shape, as
+    SparseModel::forward_decode_sparse runs them (crates/klearu-llm/src/sparse/mod.rs:55-143):
+    per layer kh_dejavu_attn_block (RmsNorm -> head predictor -> top 16 of 32
+    heads -> sparse attention over a ~2000-token cache -> residual) then
+    kh_dejavu_mlp_block (RmsNorm -> neuron predictor -> top 1652 of 11008 ->
+    sparse SwiGLU -> residual).  For every block the oracle runs on the
+    hidden row the GPU held before it: the selection must equal the oracle's
+    exactly, and the updated row the oracle's residual within the
+    BF16-weight tolerance."""
+    from klearu_amd.attention import attn_block
+    from klearu_amd.dejavu import Mlp, SparsityPredictor, mlp_block
+    rng = np.random.default_rng(2024)
+    H, nh, d, I, Rh, Rn, kh_, kn, pre = 4096, 32, 128, 11008, 128, 256, 16, 1652, 2000
+    bf = lambda a: orc.bf16_from_f32(np.asarray(a, np.float32))  # noqa: E731
+    hd = torch.from_numpy(rng.standard_normal(H).astype(np.float32)).cuda()
+    ws = torch.empty(1, dtype=torch.float32, device="cuda")
+    for layer in range(2):
+        c = Case(orc, rng, H, nh, nh, d, pre + 8, 1, pre)
+        hw1, hw2 = bf(rng.normal(0, 0.05, (Rh, H))), bf(rng.normal(0, 0.3, (nh, Rh)))
+        hb1, hb2 = rng.normal(0, 0.1, Rh).astype(np.float32), rng.normal(0, 0.1, nh).astype(np.float32)
+        hp = SparsityPredictor(orc.bf16_to_f32(hw1), hb1, orc.bf16_to_f32(hw2), hb2)
+        nw1, nw2 = bf(rng.normal(0, 0.02, (Rn, H))), bf(rng.normal(0, 0.02, (I, Rn)))
+        nb1, nb2 = rng.normal(0, 0.1, Rn).astype(np.float32), rng.normal(0, 0.1, I).astype(np.float32)
+        npred = SparsityPredictor(orc.bf16_to_f32(nw1), nb1, orc.bf16_to_f32(nw2), nb2)
+        wg, wu = bf(rng.normal(0, 0.02, (I, H))), bf(rng.normal(0, 0.02, (I, H)))
+        wd = bf(rng.normal(0, 0.02, (H, I)))
+        mlp = Mlp(wg, wu, wd, max_batch=1)
+        wn_a = rng.uniform(0.5, 1.5, H).astype(np.float32)
+        wn_m = rng.uniform(0.5, 1.5, H).astype(np.float32)
+        # attention half
+        h_in = hd.cpu().numpy().copy()
+        heads = attn_block(hp, c.attn, hd, torch.from_numpy(wn_a).cuda(), 1e-5, kh_, norm_ws=ws)
+        norm = orc.rmsnorm(h_in, wn_a, 1e-5)
+        s, _ = orc.predictor_predict(hw1, hb1, hw2, hb2, norm)
+        sel = np.sort(orc.select_top_k(s, kh_))
+        np.testing.assert_array_equal(heads.cpu().numpy(), sel)
+        close(hd.cpu().numpy(), h_in + c.oracle_step(0, norm, sel.tolist()), f"layer {layer} attention")
+        # MLP half
+        h_in = hd.cpu().numpy().copy()
+        act = mlp_block(npred, mlp, hd, torch.from_numpy(wn_m).cuda(), 1e-5, kn, norm_ws=ws)
+        norm = orc.rmsnorm(h_in, wn_m, 1e-5)
+        s, _ = orc.predictor_predict(nw1, nb1, nw2, nb2, norm)
+        sel = np.sort(orc.select_top_k(s, kn))
+        np.testing.assert_array_equal(act.cpu().numpy(), sel)
+        y, _ = orc.sparse_mlp_forward_bf16(wg, wu, wd, norm, sel.astype(np.int64))
+        close(hd.cpu().numpy(), h_in + y, f"layer {layer} MLP")
