@@ -535,3 +535,70 @@ def test_concurrent_queries_two_streams_two_threads(kh, orc):
     for t in th:
         t.join()
     assert not errors, errors
+
+
+def test_xc_network_full_cfg5(kh, orc):
+    """cfg5 at its BASELINE size: sparse 135909-d inputs (50-100 nnz, U[0,1]) ->
+    DenseLayer 128 ReLU -> SLIDE softmax output layer of 670091 neurons
+    (N(0, 0.01) weights, SimHash K9 L50, reservoir cap 128), batch 256.
+      - hash codes of a random sample of 4096 neurons are bit-exact against the
+        oracle's hash_dense (simhash.rs:103-114);
+      - every bucket (contents, lengths, insertion counts) is bit-exact against
+        the oracle's insert replay (reservoir.rs:50-67, neurons 0..n-1 in order)
+        from the GPU's codes of all 670091 neurons;
+      - for 16 of the 256 samples: hidden activations, active sets and
+        pre-activations bit-exact, softmax within 1e-5, against
+        Layer::forward (layer.rs:65-120) on the oracle's index.
+    |A| is reported: with untrained N(0, 0.01) weights every bucket is full
+    (670091 / 512 = 1309 inserts per bucket) and the 50 buckets of a query
+    rarely share a neuron, so |A| is close to 50 x 128 = 6400."""
+    from klearu_amd.lsh import LshConfig, SparseVector
+    from klearu_amd.slide import DenseLayer, Layer, LayerConfig
+    D_in, Hd, n, B, L, K, cap = 135909, 128, 670091, 256, 50, 9, 128
+    rng = np.random.default_rng(670091)
+    W1 = rng.normal(0, 0.01, (Hd, D_in)).astype(np.float32)
+    b1 = np.zeros(Hd, np.float32)
+    W2 = rng.normal(0, 0.01, (n, Hd)).astype(np.float32)
+    b2 = np.zeros(n, np.float32)
+    hidden = DenseLayer(W1, b1, "Relu")
+    cfg = LayerConfig(Hd, n, "Softmax", LshConfig(num_tables=L, num_hashes=K, bucket_capacity=cap,
+                                                  bucket_type="Reservoir"), "Vanilla", 2, 0, True)
+    out = Layer(cfg, W2, b2, 42)
+    fam = out.index.hash_family
+    planes = fam.planes()
+    # 1. codes of every neuron on the GPU; a sample against the oracle
+    codes = fam.hash_dense_batch(torch.from_numpy(W2).cuda()).cpu().numpy().view(np.uint32).reshape(n, L)
+    sample = np.sort(rng.choice(n, 4096, replace=False))
+    np.testing.assert_array_equal(codes[sample], orc.hash_dense_batch(planes, W2[sample]))
+    # 2. buckets against the oracle's replay of the inserts from those codes
+    ref = orc.LshIndex(L, K, cap, RESERVOIR)
+    ref.insert_many(np.arange(n, dtype=np.uint32), codes)
+    assert_buckets_equal(out.index, ref)
+    # 3. the network on 256 samples; 16 checked against the oracle
+    rows = []
+    for _ in range(B):
+        nnz = int(rng.integers(50, 101))
+        idx = np.sort(rng.choice(D_in, nnz, replace=False)).astype(np.uint32)
+        rows.append(SparseVector(idx, rng.uniform(0, 1, nnz).astype(np.float32), D_in))
+    h = hidden.forward_sparse(rows)
+    got = out.forward_batch(h)
+    hh = h.cpu().numpy()
+    off = got[0].cpu().numpy()
+    A = np.diff(off)
+    print(f"|A| mean {A.mean():.0f} min {A.min()} max {A.max()} (config: ~2-4k with trained weights)")
+    pick = np.sort(rng.choice(B, 16, replace=False))
+    for r in pick:
+        pre_h = np.array([orc.neuron_forward_sparse(W1[o], b1[o], rows[r].indices, rows[r].values)
+                          for o in range(Hd)], np.float32)
+        want_h = orc.layer_activate(pre_h, "relu")
+        np.testing.assert_array_equal(hh[r], want_h)
+    refrows, _ = orc.slide_layer_oracle(planes, cap, RESERVOIR, W2, b2, hh[pick], 0, 0, 2, "softmax", index=ref)
+    ids = got[1].cpu().numpy().view(np.uint32)
+    pre = got[2].cpu().numpy()
+    act = got[3].cpu().numpy()
+    for j, r in enumerate(pick):
+        s = slice(off[r], off[r + 1])
+        ri, rp, ra = refrows[j]
+        np.testing.assert_array_equal(ids[s], ri)
+        np.testing.assert_array_equal(pre[s], rp)
+        np.testing.assert_allclose(act[s], ra, rtol=1e-5, atol=1e-9)
