@@ -94,9 +94,13 @@ int kh_expf(const float* x_dev, float* y_dev, int64_t n, void* stream);
 typedef struct kh_hash_family kh_hash_family;
 
 /* SimHash::new(input_dim, k, num_tables, seed) (hash/simhash.rs:37-58):
- * ternary planes drawn from rand 0.8 StdRng (ChaCha12) in table->bit->dim order. */
+ * ternary planes drawn from a restatement of rand 0.8 StdRng (ChaCha12) in
+ * table->bit->dim order.  No reference test holds a drawn value, so the
+ * seed -> plane stream is unpinned; a caller that needs the reference's exact
+ * planes draws them with SimHash::new and passes them to
+ * kh_hash_family_from_planes. */
 int kh_simhash_create(int input_dim, int k, int num_tables, uint64_t seed, kh_hash_family** out);
-/* SparseRandomProjection::new (hash/srp.rs:43-84). */
+/* SparseRandomProjection::new (hash/srp.rs:43-84); same StdRng caveat. */
 int kh_srp_create(int input_dim, int k, int num_tables, float sparsity, uint64_t seed,
                   kh_hash_family** out);
 /* A family from explicit ternary planes planes_host[num_tables][k][input_dim]
