@@ -471,6 +471,85 @@ int kh_dejavu_attn_block(const kh_predictor* p, kh_sparse_attn* a, float* hidden
                          const float* norm_w_dev, float eps, int k, int32_t* heads_dev,
                          float* norm_ws_dev, void* stream);
 
+/* ======================================================================== */
+/* On-disk formats: safetensors weights and predictor JSON files            */
+/* ======================================================================== */
+
+/* Host-only calls except the *_create_from_* / load / save ones, which build
+ * or read device handles. */
+typedef struct kh_safetensors kh_safetensors;
+
+#define KH_DT_F32 0
+#define KH_DT_F16 1
+#define KH_DT_BF16 2
+
+/* SafeTensorsFile::open (crates/klearu-llm/src/weight/safetensors.rs:37-113):
+ * memory-maps `path` and parses its header.  `path` may also be a model
+ * directory: every *.safetensors file in it is opened in sorted path order
+ * (weight/loader.rs:30-49), a later file's tensor shadowing an earlier one of
+ * the same name.  A dtype other than F32 / F16 / BF16 fails the open
+ * (KH_ERR_UNSUPPORTED, as LlmError::UnsupportedDtype). */
+int kh_safetensors_open(const char* path, kh_safetensors** out);
+int kh_safetensors_close(kh_safetensors* st);
+/* Number of tensors, and the name of tensor i in sorted name order (NUL-
+ * terminated into buf[cap]; KH_ERR_CAPACITY if it does not fit). */
+int kh_safetensors_count(const kh_safetensors* st, int64_t* n);
+int kh_safetensors_name(const kh_safetensors* st, int64_t i, char* buf, int64_t cap);
+/* TensorInfo (safetensors.rs:7-14): dtype (KH_DT_*), ndim, and the first
+ * min(ndim, max_dims) extents into shape (may be NULL). */
+int kh_safetensors_info(const kh_safetensors* st, const char* name, int* dtype, int* ndim,
+                        int64_t* shape, int max_dims);
+/* tensor_to_f32 (safetensors.rs:135-159): the tensor's n elements converted
+ * exactly to f32.  n must equal the element count, and the tensor's bytes must
+ * lie in the file and hold exactly that many elements (KH_ERR_ARG otherwise,
+ * the reference's "data out of bounds"). */
+int kh_safetensors_read_f32(const kh_safetensors* st, const char* name, float* out_host, int64_t n);
+/* tensor_data (safetensors.rs:119-133): the tensor's raw little-endian bytes. */
+int kh_safetensors_read_raw(const kh_safetensors* st, const char* name, void* out_host,
+                            int64_t bytes);
+/* The Mlp of decoder layer `layer` (model/mlp.rs:6-21) straight from the
+ * file: {prefix}layers.{layer}.mlp.{gate,up,down}_proj.weight with prefix
+ * "model.", "model.language_model." or "" (weight/name_map.rs:36-98); hidden
+ * and intermediate come from gate_proj's shape.  BF16 tensors are uploaded as
+ * they are; F32 / F16 ones only when every value is a BF16 value
+ * (KH_ERR_UNSUPPORTED otherwise: the kernels keep BF16 weights).  Equivalent
+ * to kh_sparse_ffn_create on the same bits. */
+int kh_sparse_ffn_create_from_safetensors(const kh_safetensors* st, int layer, int max_batch,
+                                          kh_sparse_ffn** out);
+/* The attention of decoder layer `layer` from self_attn.{q,k,v,o}_proj.weight
+ * (same naming and dtype rules); hidden comes from q_proj's shape, the head
+ * geometry from the model config (config.rs).  Equivalent to
+ * kh_sparse_attn_create on the same bits. */
+int kh_sparse_attn_create_from_safetensors(const kh_safetensors* st, int layer, int num_heads,
+                                           int num_kv_heads, int head_dim, int max_seq,
+                                           int max_batch, float rope_theta, int kv_dtype,
+                                           kh_sparse_attn** out);
+
+/* SparsityPredictor::load (crates/klearu-dejavu/src/predictor/mlp_predictor.rs:94-98):
+ * the serde JSON object {w1: [[f32; input]; hidden], b1, w2: [[f32; hidden];
+ * output], b2, input_dim, hidden_dim, output_dim}, fields in any order.  Each
+ * number becomes the f32 nearest to the f64 nearest to its decimal, as
+ * serde_json reads an f32.  The dims must agree with the arrays (KH_ERR_ARG). */
+int kh_predictor_load(const char* path, kh_predictor** out);
+/* The same parse into host arrays.  The dims are always written; each array
+ * pointer may be NULL (to query the dims first). */
+int kh_predictor_read_json(const char* path, int* input_dim, int* hidden_dim, int* output_dim,
+                           float* w1_host, float* b1_host, float* w2_host, float* b2_host);
+/* SparsityPredictor::save (mlp_predictor.rs:87-92): the same object from host
+ * arrays, each f32 as its shortest round-trip decimal in serde_json's spelling
+ * ("1.0", "0.25", "1e-7"); non-finite values are rejected (serde_json would
+ * write null, which its reader then rejects). */
+int kh_predictor_write_json(const char* path, int input_dim, int hidden_dim, int output_dim,
+                            const float* w1_host, const float* b1_host, const float* w2_host,
+                            const float* b2_host);
+/* kh_predictor_write_json of a predictor handle's weights (synchronous). */
+int kh_predictor_save(const kh_predictor* p, const char* path);
+/* The handle's dims, and its weights copied back to host arrays w1[hidden][input],
+ * b1[hidden], w2[output][hidden], b2[output] (synchronous). */
+int kh_predictor_dims(const kh_predictor* p, int* input_dim, int* hidden_dim, int* output_dim);
+int kh_predictor_weights(const kh_predictor* p, float* w1_host, float* b1_host, float* w2_host,
+                         float* b2_host);
+
 #ifdef __cplusplus
 }
 #endif

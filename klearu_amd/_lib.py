@@ -40,6 +40,7 @@ I64 = C.c_int64
 U64 = C.c_uint64
 F = C.c_float
 PP = C.POINTER(C.c_void_p)
+S = C.c_char_p
 
 SIGS = {
     "kh_last_error": (C.c_char_p, []),
@@ -116,6 +117,21 @@ SIGS = {
     "kh_sparse_attn_cache_len": (I, [P, I64, P]),
     "kh_sparse_attn_clear": (I, [P, P]),
     "kh_sparse_attn_forward": (I, [P, P, I64, P, P, I, P, I, P]),
+    "kh_safetensors_open": (I, [S, PP]),
+    "kh_safetensors_close": (I, [P]),
+    "kh_safetensors_count": (I, [P, C.POINTER(I64)]),
+    "kh_safetensors_name": (I, [P, I64, C.c_char_p, I64]),
+    "kh_safetensors_info": (I, [P, S, C.POINTER(I), C.POINTER(I), P, I]),
+    "kh_safetensors_read_f32": (I, [P, S, P, I64]),
+    "kh_safetensors_read_raw": (I, [P, S, P, I64]),
+    "kh_sparse_ffn_create_from_safetensors": (I, [P, I, I, PP]),
+    "kh_sparse_attn_create_from_safetensors": (I, [P, I, I, I, I, I, I, F, I, PP]),
+    "kh_predictor_load": (I, [S, PP]),
+    "kh_predictor_read_json": (I, [S, C.POINTER(I), C.POINTER(I), C.POINTER(I), P, P, P, P]),
+    "kh_predictor_write_json": (I, [S, I, I, I, P, P, P, P]),
+    "kh_predictor_save": (I, [P, S]),
+    "kh_predictor_dims": (I, [P, C.POINTER(I), C.POINTER(I), C.POINTER(I)]),
+    "kh_predictor_weights": (I, [P, P, P, P, P]),
 }
 
 

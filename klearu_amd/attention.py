@@ -55,6 +55,21 @@ class SparseAttention:
                   float(rope_theta), kv_dtype, *args, C.byref(h))
         self._h = h
 
+    @classmethod
+    def from_safetensors(cls, st, layer, num_heads, num_kv_heads, head_dim, max_seq_len, max_batch=1,
+                         rope_theta=10000.0, kv_dtype=KV_BF16):
+        """Layer `layer`'s self_attn.{q,k,v,o}_proj.weight (weight/loader.rs:96-111) from a
+        formats.SafeTensorsFile, uploaded as BF16; the head geometry comes from the config."""
+        h = C.c_void_p()
+        _lib.call("kh_sparse_attn_create_from_safetensors", st._h, layer, num_heads, num_kv_heads, head_dim,
+                  max_seq_len, max_batch, float(rope_theta), kv_dtype, C.byref(h))
+        self = cls.__new__(cls)
+        self._h = h
+        self.hidden_size = st.info(st.layer_name(layer, "self_attn.q_proj.weight")).shape[1]
+        self.num_heads, self.num_kv_heads, self.head_dim = num_heads, num_kv_heads, head_dim
+        self.max_seq_len, self.max_batch = max_seq_len, max_batch
+        return self
+
     def __del__(self):
         h = getattr(self, "_h", None)
         if h:

@@ -1035,6 +1035,49 @@ extern "C" int kh_predictor_destroy(kh_predictor* p) {
   return KH_OK;
 }
 
+extern "C" int kh_predictor_dims(const kh_predictor* p, int* input_dim, int* hidden_dim, int* output_dim) {
+  KH_CHECK_ARG(p && input_dim && hidden_dim && output_dim, "null argument");
+  *input_dim = p->in_dim;
+  *hidden_dim = p->hid;
+  *output_dim = p->out_dim;
+  return KH_OK;
+}
+
+// Inverse of block_transpose for one stored matrix.
+template <typename T>
+static int download_blocked(const void* src, int n_out, int n_in, float* w) {
+  const int nb = (n_in + 7) / 8;
+  std::vector<T> o((size_t)nb * n_out * 8);
+  KH_HIP(hipMemcpy(o.data(), src, o.size() * sizeof(T), hipMemcpyDeviceToHost));
+  for (int r = 0; r < n_out; ++r)
+    for (int j = 0; j < n_in; ++j) {
+      const T t = o[((size_t)(j / 8) * n_out + r) * 8 + (j % 8)];
+      float v;
+      if constexpr (sizeof(T) == 2) {
+        const uint32_t u = uint32_t(t) << 16;
+        memcpy(&v, &u, 4);
+      } else {
+        v = t;
+      }
+      w[(size_t)r * n_in + j] = v;
+    }
+  return KH_OK;
+}
+
+extern "C" int kh_predictor_weights(const kh_predictor* p, float* w1_host, float* b1_host, float* w2_host,
+                                    float* b2_host) {
+  KH_CHECK_ARG(p && w1_host && b1_host && w2_host && b2_host, "null argument");
+  int rc = p->bf16 ? download_blocked<uint16_t>(p->w1b, p->hid, p->in_dim, w1_host)
+                   : download_blocked<float>(p->w1b, p->hid, p->in_dim, w1_host);
+  if (rc != KH_OK) return rc;
+  rc = p->bf16 ? download_blocked<uint16_t>(p->w2b, p->out_dim, p->hid, w2_host)
+               : download_blocked<float>(p->w2b, p->out_dim, p->hid, w2_host);
+  if (rc != KH_OK) return rc;
+  KH_HIP(hipMemcpy(b1_host, p->b1, sizeof(float) * p->hid, hipMemcpyDeviceToHost));
+  KH_HIP(hipMemcpy(b2_host, p->b2, sizeof(float) * p->out_dim, hipMemcpyDeviceToHost));
+  return KH_OK;
+}
+
 // A top-k request that layer 2 may serve itself (done = true when it did).
 struct TopkReq {
   int k = 0, order = 0;

@@ -11,7 +11,6 @@ All compute runs in libklearu_hip.so on the current torch stream.
 from __future__ import annotations
 
 import ctypes as C
-import json
 import math
 import os
 
@@ -49,12 +48,34 @@ class SparsityPredictor:
     from_weights = classmethod(lambda cls, w1, b1, w2, b2: cls(w1, b1, w2, b2))
 
     @classmethod
+    def _adopt(cls, h):
+        self = cls.__new__(cls)
+        self._h = h
+        din, dh, dout = C.c_int(), C.c_int(), C.c_int()
+        _lib.call("kh_predictor_dims", h, C.byref(din), C.byref(dh), C.byref(dout))
+        self.input_dim, self.hidden_dim, self.output_dim = din.value, dh.value, dout.value
+        return self
+
+    @classmethod
     def load(cls, path):
-        """SparsityPredictor::load (mlp_predictor.rs:94-98): serde JSON with w1,b1,w2,b2."""
-        with open(path) as f:
-            d = json.load(f)
-        return cls(np.array(d["w1"], np.float32).reshape(d["hidden_dim"], d["input_dim"]), d["b1"],
-                   np.array(d["w2"], np.float32).reshape(d["output_dim"], d["hidden_dim"]), d["b2"])
+        """SparsityPredictor::load (mlp_predictor.rs:94-98): the serde JSON file
+        {w1, b1, w2, b2, input_dim, hidden_dim, output_dim}, parsed natively."""
+        h = C.c_void_p()
+        _lib.call("kh_predictor_load", os.fsencode(path), C.byref(h))
+        return cls._adopt(h)
+
+    def save(self, path):
+        """SparsityPredictor::save (mlp_predictor.rs:87-92)."""
+        _lib.call("kh_predictor_save", self._h, os.fsencode(path))
+
+    def weights(self):
+        """(w1 [hidden][input], b1, w2 [output][hidden], b2) as f32 host arrays."""
+        w1 = np.empty((self.hidden_dim, self.input_dim), np.float32)
+        b1 = np.empty(self.hidden_dim, np.float32)
+        w2 = np.empty((self.output_dim, self.hidden_dim), np.float32)
+        b2 = np.empty(self.output_dim, np.float32)
+        _lib.call("kh_predictor_weights", self._h, hptr(w1), hptr(b1), hptr(w2), hptr(b2))
+        return w1, b1, w2, b2
 
     def __del__(self):
         h = getattr(self, "_h", None)
@@ -127,9 +148,20 @@ class PredictorStore:
     def predict_neurons(self, layer, x, k, order=ORDER_SCORE, stream=None):
         return self._pick(self.neuron_predictors[layer], x, k, order, stream)
 
+    def save(self, directory):
+        """PredictorStore::save (predictor_store.rs:59-74): layer_{i}_{head,neuron}.json."""
+        os.makedirs(directory, exist_ok=True)
+        for i, p in enumerate(self.head_predictors):
+            if p is not None:
+                p.save(os.path.join(directory, f"layer_{i}_head.json"))
+        for i, p in enumerate(self.neuron_predictors):
+            if p is not None:
+                p.save(os.path.join(directory, f"layer_{i}_neuron.json"))
+
     @classmethod
     def load(cls, directory, num_layers):
-        """PredictorStore::load (predictor_store.rs:76-89): layer_{i}_{head,neuron}.json."""
+        """PredictorStore::load (predictor_store.rs:76-89): layer_{i}_{head,neuron}.json;
+        a missing file leaves that layer on the first-k fallback."""
         s = cls(num_layers)
         for i in range(num_layers):
             hp = os.path.join(directory, f"layer_{i}_head.json")
@@ -180,6 +212,18 @@ class Mlp:
                   hptr(w_up), hptr(w_down), max_batch, C.byref(h))
         self._h = h
         self.max_batch = max_batch
+
+    @classmethod
+    def from_safetensors(cls, st, layer: int, max_batch: int = 16):
+        """Layer `layer`'s mlp.{gate,up,down}_proj.weight (weight/loader.rs:125-133) from a
+        formats.SafeTensorsFile, uploaded as BF16 without a host-side float copy."""
+        h = C.c_void_p()
+        _lib.call("kh_sparse_ffn_create_from_safetensors", st._h, layer, max_batch, C.byref(h))
+        self = cls.__new__(cls)
+        self._h = h
+        self.max_batch = max_batch
+        self.intermediate_size, self.hidden_size = st.info(st.layer_name(layer, "mlp.gate_proj.weight")).shape
+        return self
 
     def __del__(self):
         h = getattr(self, "_h", None)
