@@ -3,38 +3,38 @@
 // Rust's `let mut s = s0; for v in terms { s += v; }` rounds after every add,
 // so the result is one particular f32 that only the same order reproduces
 // (e.g. RmsNorm's sum of squares, crates/klearu-llm/src/model/rms_norm.rs:48-51).
-// A dependent chain of 4096 adds costs about 10 us on one lane.  The block here
-// returns the same bits with most of the chain run in parallel:
+// A dependent chain of 4096 adds costs about 7.5 us on one lane (4.3 cycles a
+// step).  The block here returns the same bits with most of the chain run in
+// parallel:
 //
-//  1. The terms are cut into chunks of M.  A guess of the running sum at the
+//  1. The terms are cut into CH chunks of M.  A guess of the running sum at the
 //     start of chunk c is s0 plus the chunk sums before it (f32, any order).
 //     It is only a guess.
-//  2. Every chunk c >= 1 is run sequentially from kEsWin consecutive f32 start
-//     values centred on its guess, one lane per start value; chunk 0 runs from
-//     s0 itself.  Lane l of the wave owning chunk c ends with f_c(start_l), f_c
-//     being the sequential pass over the chunk's terms.  The 16 terms of a group
-//     sit in the 16 lanes of every row and each add reads its term through a DPP
-//     row broadcast, so a step is one VALU instruction and no LDS traffic.
-//  3. One wave composes: s = f_0(s0); for each further chunk, if s is one of its
-//     start values, the lane that started there already holds f_c(s); otherwise
-//     the chunk is run sequentially from s.
+//  2. Every chunk c >= 1 is run sequentially from W consecutive f32 start
+//     values ("slots") centred on its guess; chunk 0 runs from s0 itself.
+//     Lane l of every wave works on chunk l % CH; its slots are spread over
+//     the waves, the 64 / CH lanes of a chunk and P chains per lane, and all
+//     of a lane's chains add the same term, read once from LDS.  f_c(slot k)
+//     is stored, and so is the slot of chunk c + 1 it equals (or -1).
+//  3. The path from chunk 0 follows those slot links: each wave follows every
+//     slot through a segment of chunks at once (lane gathers), then one wave
+//     chains the segments.  If the path leaves a window anywhere, that chunk
+//     is run sequentially from the exact running sum (the slow path).
 // The result is always the sequential sum; the guesses only decide how much of
 // it ran in parallel.  For a monotone running sum (sums of squares) the window
 // misses about once in 600 chunks at n = 4096 (CPU model of this scheme).
 //
-// Start values are enumerated with an integer key that orders every f32 except
-// -0.0 (which shares +0.0's key): a running sum equal to -0.0, or not finite,
-// always takes the sequential path.
+// Slots are enumerated with an integer key that orders every f32 except -0.0
+// (which shares +0.0's key): a running sum equal to -0.0, or not finite,
+// always takes the slow path.  Terms past n are stored as -0.0, which leaves
+// every sum unchanged (x + -0.0 == x for every x).
 #pragma once
-
-#include <utility>
 
 #include "common.hpp"
 
 namespace kh {
 
-constexpr int kEsWin = 64;      // start values per chunk (the lanes of one wave)
-constexpr int kEsMaxChunks = 64;
+constexpr int kEsW = 64;  // slots per chunk (window width, at most 64)
 
 // Order-preserving integer key of an f32 (consecutive floats -> consecutive keys).
 __device__ __forceinline__ int es_key(float f) {
@@ -44,95 +44,6 @@ __device__ __forceinline__ int es_key(float f) {
 __device__ __forceinline__ float es_from_key(int k) {
   const int i = k < 0 ? static_cast<int>(0x80000000u - static_cast<uint32_t>(k)) : k;
   return __int_as_float(i);
-}
-
-// s + (lane K of this lane's row of 16) as one v_add_f32 with a DPP
-// row_newbcast operand (the compiler emits the broadcast as a separate move).
-template <int K>
-__device__ __forceinline__ void es_add_bcast(float& s, float tv) {
-  float r;
-  asm("v_add_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
-      : "=v"(r)
-      : "v"(tv), "v"(s), "i"(K));
-  s = r;
-}
-template <int... K>
-__device__ __forceinline__ void es_add16(float& s, float tv, std::integer_sequence<int, K...>) {
-  (es_add_bcast<K>(s, tv), ...);
-}
-
-// Sequential pass over t[j0, j1) from s, in every lane of the wave (each lane
-// gets the same value).  Full 16-term groups use the row broadcast; the tail
-// reads LDS with a wave-uniform address.
-__device__ __forceinline__ float es_run(const float* __restrict__ t, int j0, int j1, float s) {
-  const int lane = threadIdx.x & 63;
-  int j = j0;
-  for (; j + 16 <= j1; j += 16) {
-    const float tv = t[j + (lane & 15)];
-    es_add16(s, tv, std::make_integer_sequence<int, 16>{});
-  }
-  for (; j < j1; ++j) s = __fadd_rn(s, t[j]);
-  return s;
-}
-
-// Chunk c's window entry of lane l ends at e = E[c][l]: the lane of chunk c + 1
-// that started from e, or -1 when e is outside that window, not finite, or
-// -0.0.  Past the last chunk (c + 1 >= C) the path stays on its lane.
-__device__ __forceinline__ int es_next(float e, int gk_next, int c, int C) {
-  const int lane = threadIdx.x & 63;
-  const uint32_t eb = __float_as_uint(e);
-  const int q = es_key(e) - gk_next + kEsWin / 2;
-  const bool ok = (eb & 0x7f800000u) != 0x7f800000u && eb != 0x80000000u &&
-                  static_cast<uint32_t>(q) < static_cast<uint32_t>(kEsWin);
-  return c + 1 >= C ? lane : (ok ? q : -1);
-}
-
-// P full chunks of M terms starting at chunk c0 (cnt <= P of them real; the
-// others repeat the last one and are not stored), each from the start value
-// `st[i]` of this lane, run as P interleaved chains: a dependent DPP add costs
-// about 10 cycles, P independent ones about 5 per wave (measured), so the
-// chains of a wave hide each other's latency.  Stores E and nx (es_next;
-// gkv holds the guessed start key of chunk `lane`) of every real chunk.
-template <int P, int M>
-__device__ __forceinline__ void es_windows(const float* __restrict__ t, int c0, int cnt, int C,
-                                           const float (&st)[P], int gkv, float* __restrict__ E,
-                                           int* __restrict__ NX) {
-  const int lane = threadIdx.x & 63;
-  float s[P];
-  int base[P];
-#pragma unroll
-  for (int i = 0; i < P; ++i) {
-    s[i] = st[i];
-    base[i] = (c0 + min(i, cnt - 1)) * M + (lane & 15);
-  }
-  float tv[P];
-#pragma unroll
-  for (int i = 0; i < P; ++i) tv[i] = t[base[i]];
-#pragma unroll
-  for (int g = 0; g < M / 16; ++g) {
-    // the next group's terms are requested before this group's adds
-    float tn[P];
-    const int gn = 16 * min(g + 1, M / 16 - 1);
-#pragma unroll
-    for (int i = 0; i < P; ++i) tn[i] = t[base[i] + gn];
-#define KH_ES_STEP(K)                                          \
-  _Pragma("unroll") for (int i = 0; i < P; ++i) es_add_bcast<K>(s[i], tv[i]);
-    KH_ES_STEP(0) KH_ES_STEP(1) KH_ES_STEP(2) KH_ES_STEP(3)
-    KH_ES_STEP(4) KH_ES_STEP(5) KH_ES_STEP(6) KH_ES_STEP(7)
-    KH_ES_STEP(8) KH_ES_STEP(9) KH_ES_STEP(10) KH_ES_STEP(11)
-    KH_ES_STEP(12) KH_ES_STEP(13) KH_ES_STEP(14) KH_ES_STEP(15)
-#undef KH_ES_STEP
-#pragma unroll
-    for (int i = 0; i < P; ++i) tv[i] = tn[i];
-  }
-#pragma unroll
-  for (int i = 0; i < P; ++i) {
-    const int c = c0 + i;
-    if (i < cnt) {
-      E[c * kEsWin + lane] = s[i];
-      NX[c * kEsWin + lane] = es_next(s[i], __builtin_amdgcn_readlane(gkv, min(c + 1, kEsWin - 1)), c, C);
-    }
-  }
 }
 
 // Inclusive prefix sum of f32 over the lanes of a wave (any rounding: the
@@ -147,127 +58,168 @@ __device__ __forceinline__ float es_wave_scan(float x) {
   return x;
 }
 
-template <int MAXC = kEsMaxChunks>
+// LDS of one exact sum: CH chunks of M terms (M a multiple of 4).
+template <int CH, int M>
 struct EsLds {
-  float E[MAXC * kEsWin];  // E[c*64 + l] = f_c(start value of lane l)
-  int nx[MAXC * kEsWin];   // lane of chunk c + 1 that started from E[c*64 + l], or -1
-  float D[MAXC];           // chunk sums (guesses only)
-  int gk[MAXC];            // key of the guessed start of chunk c
+  static constexpr int kS = M + 4;   // padded row: 16-byte aligned, conflict-light
+  static constexpr int kNS = CH + 4;
+  __align__(16) float TP[CH * kS];  // TP[c*kS + j] = t[c*M + j] (the caller fills it; es_slot)
+  float E[CH * kEsW];     // E[c*64 + k] = f_c(slot k)
+  int NXT[kEsW * kNS];    // NXT[k*kNS + c]: slot of chunk c + 1 equal to E[c*64 + k], or -1
+  int SM[16 * kEsW];      // SM[g*64 + k]: slot at the end of segment g from slot k, or -1
+  int gk[CH];             // key of the guessed start of chunk c
   float res;
 };
 
+// Index in EsLds::TP of term i.
+template <int CH, int M>
+__device__ __forceinline__ int es_slot(int i) {
+  return (i / M) * EsLds<CH, M>::kS + (i % M);
+}
+
 // Sequential f32 sum s0 + t[0] + t[1] + ... + t[n-1] (left to right, rounding
-// after each add) of terms in LDS, with chunks of M terms (M = 64 or 128,
-// n <= 64 M).  Every thread of the block (NW waves, blockDim.x == 64 * NW)
-// must call it.  Returns the sum in every thread.  Its barriers wait for LDS
-// traffic only, so global loads a wave has in flight stay in flight.
-template <int NW, int M>
-__device__ __forceinline__ float exact_seq_sum(const float* __restrict__ t, int n, float s0,
-                                              EsLds<>& es) {
-  static_assert(M == 64 || M == 128, "chunk of 64 or 128 terms");
-  constexpr int kMaxP = 16;
-  constexpr int kLpc = M / 8;  // lanes per chunk in the chunk sums (8 terms each)
+// after each add) of the terms the caller stored in es.TP (es_slot; -0.0 for
+// n <= i < CH*M), n <= CH*M.  Every thread of the block (NW waves, blockDim.x ==
+// 64 * NW) must call it after a barrier that publishes TP.  Returns the sum in
+// every thread.  Its barriers wait for LDS traffic only, so global loads a
+// wave has in flight stay in flight.
+template <int NW, int CH, int M>
+__device__ __forceinline__ float exact_seq_sum(int n, float s0, EsLds<CH, M>& es) {
+  using L_ = EsLds<CH, M>;
+  constexpr int G = 64 / CH;          // lanes per chunk
+  constexpr int P = kEsW / (G * NW);  // chains per lane
+  constexpr int W = P * G * NW;       // slots per chunk
+  constexpr int S = L_::kS, NS = L_::kNS;
+  constexpr int SEG = (CH + NW - 1) / NW;  // chunks per segment (one segment per wave)
+  static_assert(64 % CH == 0 && P >= 1 && M % (4 * G) == 0 && NW <= 16, "exact-sum layout");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (n <= 0) return s0;
-  const int C = (n + M - 1) / M;  // chunks (the last may be partial)
-  const int Cf = n / M;           // full chunks
-  // 1. chunk sums (any order: guesses only).  A wave takes 512 terms at a
-  // time, 8 per lane, and adds them over the M/8 lanes of each chunk.
-  for (int r = wave; r * 512 < n; r += NW) {
-    const int j0 = r * 512 + 8 * lane;
-    float a = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) a += j0 + e < n ? t[j0 + e] : 0.0f;
-    a = group_sum<kLpc>(a);
-    const int c = (r * 512) / M + lane / kLpc;
-    if (lane % kLpc == 0 && c < C) es.D[c] = a;
-  }
-  lds_barrier();
-  // 2. guesses (every wave, for itself): exclusive prefix of the chunk sums;
-  // wave 0 also stores them for the composition
-  const float dl = lane < C ? es.D[lane] : 0.0f;
-  const float inc = es_wave_scan(dl);
-  float ex = __shfl_up(inc, 1, 64);
-  if (lane == 0) ex = 0.0f;
-  const int gkv = es_key(s0 + ex);  // key of the guessed start of chunk `lane`
-  if (wave == 0 && lane < C) es.gk[lane] = gkv;
-  // 3. this wave's chunks from kEsWin start values each.  Waves that share a
-  // SIMD with another wave of the block (round-robin placement: waves w and
-  // w + 4) take half as many chunks as a wave alone on its SIMD.
-  int tot = 0, before = 0, mine = 0;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    const int wt = (NW <= 4 || NW >= 8) ? 1 : ((w + 4 < NW) || (w >= 4) ? 1 : 2);
-    before += w < wave ? wt : 0;
-    mine = w == wave ? wt : mine;
-    tot += wt;
-  }
-  const int c0 = (C * before) / tot, c1 = (C * (before + mine)) / tot;
-  {
-    const int cf1 = min(c1, Cf);  // full chunks of this wave
-    for (int cb = c0; cb < cf1; cb += kMaxP) {
-      const int cnt = min(kMaxP, cf1 - cb);
-      float st[kMaxP];
-#pragma unroll
-      for (int i = 0; i < kMaxP; ++i) {
-        const int c = min(cb + i, cf1 - 1);
-        st[i] = c == 0 ? s0 : es_from_key(__builtin_amdgcn_readlane(gkv, c) + lane - kEsWin / 2);
-      }
-      if (cnt > 8) {
-        es_windows<kMaxP, M>(t, cb, cnt, C, st, gkv, es.E, es.nx);
-      } else {
-        float s8[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) s8[i] = st[i];
-        es_windows<8, M>(t, cb, cnt, C, s8, gkv, es.E, es.nx);
-      }
-    }
-    if (Cf < C && c0 <= Cf && Cf < c1) {
-      // the partial last chunk
-      const float st = Cf == 0 ? s0 : es_from_key(__builtin_amdgcn_readlane(gkv, Cf) + lane - kEsWin / 2);
-      const float e = es_run(t, Cf * M, n, st);
-      es.E[Cf * kEsWin + lane] = e;
-      es.nx[Cf * kEsWin + lane] = es_next(e, 0, Cf, C);
-    }
-  }
-  lds_barrier();
-  // 4. composition (wave 0): the path starts at chunk 0 (every lane of which
-  // started from s0) and steps p <- nx[c] of lane p.  A miss anywhere on the
-  // path shows as a negative p (collected by OR); the sum is then redone on
-  // the slow path.
+  const int C = (n + M - 1) / M;  // chunks holding terms
+  // 1. chunk sums (each of a chunk's G lanes adds M/G terms) and guesses
   if (wave == 0) {
-    int nx[kEsMaxChunks];
+    constexpr int MG = M / G;
+    const float4* tp = reinterpret_cast<const float4*>(es.TP + min(lane % CH, C - 1) * S + (lane / CH) * MG);
+    float4 v[MG / 4];
 #pragma unroll
-    for (int c = 0; c + 1 < kEsMaxChunks; ++c) nx[c] = es.nx[c * kEsWin + lane];
-    int p = 0, any = 0;
+    for (int j = 0; j < MG / 4; ++j) v[j] = tp[j];
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
-    for (int c = 0; c + 1 < kEsMaxChunks; ++c) {
-      if (c + 1 < C) {
-        p = __builtin_amdgcn_readlane(nx[c], p & (kEsWin - 1));
-        any |= p;
+    for (int j = 0; j < MG / 4; ++j) {
+      a0 += v[j].x;
+      a1 += v[j].y;
+      a2 += v[j].z;
+      a3 += v[j].w;
+    }
+    float d = (a0 + a1) + (a2 + a3);
+#pragma unroll
+    for (int m = CH; m < 64; m <<= 1) d += __shfl_xor(d, m);
+    d = lane < C ? d : 0.0f;
+    const float inc = es_wave_scan(d);
+    float ex = __shfl_up(inc, 1, 64);
+    if (lane == 0) ex = 0.0f;
+    if (lane < CH) es.gk[lane] = es_key(s0 + ex);
+  }
+  lds_barrier();
+  // 2. windows
+  {
+    const int c = min(lane % CH, C - 1), h = lane / CH;
+    const int gkc = es.gk[c];
+    const int gkn = es.gk[min(c + 1, C - 1)];
+    const int k0 = (wave * G + h) * P;
+    float s[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) s[i] = c == 0 ? s0 : es_from_key(gkc + k0 + i - W / 2);
+    const float4* tp = reinterpret_cast<const float4*>(es.TP + c * S);
+    constexpr int B = 8;  // float4 of terms read ahead
+    float4 tv[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j) tv[j] = tp[min(j, M / 4 - 1)];
+    for (int j0 = 0; j0 < M / 4; j0 += B) {
+      float4 tn[B];
+#pragma unroll
+      for (int j = 0; j < B; ++j) tn[j] = tp[min(j0 + B + j, M / 4 - 1)];
+#pragma unroll
+      for (int j = 0; j < B; ++j) {
+        if (j0 + j < M / 4) {
+#pragma unroll
+          for (int i = 0; i < P; ++i) s[i] = __fadd_rn(s[i], tv[j].x);
+#pragma unroll
+          for (int i = 0; i < P; ++i) s[i] = __fadd_rn(s[i], tv[j].y);
+#pragma unroll
+          for (int i = 0; i < P; ++i) s[i] = __fadd_rn(s[i], tv[j].z);
+#pragma unroll
+          for (int i = 0; i < P; ++i) s[i] = __fadd_rn(s[i], tv[j].w);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < B; ++j) tv[j] = tn[j];
+    }
+    if ((lane % CH) < C) {
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        const int k = k0 + i;
+        const uint32_t eb = __float_as_uint(s[i]);
+        const int q = es_key(s[i]) - gkn + W / 2;
+        const bool ok = (eb & 0x7f800000u) != 0x7f800000u && eb != 0x80000000u &&
+                        static_cast<uint32_t>(q) < static_cast<uint32_t>(W);
+        es.E[c * kEsW + k] = s[i];
+        es.NXT[k * NS + c] = c + 1 >= C ? k : (ok ? q : -1);
       }
     }
-    int s;
-    if (any >= 0) {
-      s = __float_as_int(es.E[(C - 1) * kEsWin + p]);
+  }
+  lds_barrier();
+  // 3a. segment g (wave g) covers the links out of chunks g*SEG .. g*SEG+SEG-1:
+  // every slot is followed through it at once
+  const int nseg = (C - 1 + SEG - 1) / SEG;
+  if (wave < nseg) {
+    int nx[SEG];
+#pragma unroll
+    for (int i = 0; i < SEG; ++i) nx[i] = lane < W ? es.NXT[lane * NS + min(wave * SEG + i, CH - 1)] : -1;
+    int cur = lane < W ? lane : -1;
+    int bad = cur;
+#pragma unroll
+    for (int i = 0; i < SEG; ++i) {
+      if (wave * SEG + i + 1 < C) {
+        cur = __builtin_amdgcn_ds_bpermute(cur << 2, nx[i]);
+        bad |= cur;
+      }
+    }
+    es.SM[wave * kEsW + lane] = bad < 0 ? -1 : cur;
+  }
+  lds_barrier();
+  // 3b. one wave chains the segments from slot 0 of chunk 0 (all of chunk
+  // 0's slots started from s0)
+  if (wave == 0) {
+    int sm[NW];
+#pragma unroll
+    for (int g = 0; g < NW; ++g) sm[g] = g < nseg ? es.SM[g * kEsW + lane] : lane;
+    int p = 0, bad = 0;
+#pragma unroll
+    for (int g = 0; g < NW; ++g) {
+      p = __builtin_amdgcn_readlane(sm[g], p);
+      bad |= p;
+    }
+    float r;
+    if (bad >= 0) {
+      r = es.E[(C - 1) * kEsW + p];
     } else {
-      // slow path: chunk by chunk, lookups from LDS or sequential chunks
-      s = __float_as_int(es.E[0]);
+      // slow path: chunk by chunk, a window lookup or a sequential run
+      r = es.E[0];
       for (int c = 1; c < C; ++c) {
-        const uint32_t sb = static_cast<uint32_t>(s);
-        const int idx = es_key(__int_as_float(s)) - es.gk[c] + kEsWin / 2;
+        const uint32_t sb = __float_as_uint(r);
+        const int idx = es_key(r) - es.gk[c] + W / 2;
         const bool ok = (sb & 0x7f800000u) != 0x7f800000u && sb != 0x80000000u &&
-                        static_cast<uint32_t>(idx) < static_cast<uint32_t>(kEsWin);
+                        static_cast<uint32_t>(idx) < static_cast<uint32_t>(W);
         if (ok) {
-          s = __float_as_int(es.E[c * kEsWin + idx]);
+          r = es.E[c * kEsW + idx];
         } else {
-          const float v = es_run(t, c * M, min(n, c * M + M), __int_as_float(s));
-          s = __builtin_amdgcn_readfirstlane(__float_as_int(v));
+          const float* tp = es.TP + c * S;
+          for (int j = 0; j < M; ++j) r = __fadd_rn(r, tp[j]);
         }
       }
     }
-    if (lane == 0) es.res = __int_as_float(s);
+    if (lane == 0) es.res = r;
   }
   lds_barrier();
   return es.res;

@@ -345,32 +345,32 @@ __global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
   }
   if (8 * lane < slice) {
     float4* o = reinterpret_cast<float4*>(partial + (size_t)blockIdx.x * H + col);
-    st_stream(o, make_float4(acc[0], acc[1], acc[2], acc[3]));
-    st_stream(o + 1, make_float4(acc[4], acc[5], acc[6], acc[7]));
+    o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
   }
 }
 
 // RmsNorm::forward (crates/klearu-llm/src/model/rms_norm.rs:43-64): one block
 // of kRnWaves waves per row.  The row's squares are staged in LDS and summed in
-// the reference's sequential order (exact_seq_sum); then y = (x * inv) * w.
+// the reference's sequential order (exact_seq_sum, 32 chunks of M terms); then
+// y = (x * inv) * w.
 constexpr int kRnWaves = 8;
-constexpr int kRnMaxN = 128 * kEsMaxChunks;  // rows up to 8192 (longer rows: rmsnorm_seq_kernel)
+constexpr int kRnChunks = 32;
+constexpr int kRnMaxN = kRnChunks * 256;  // rows up to 8192 (longer rows: rmsnorm_seq_kernel)
 
+template <int M>
 __global__ __launch_bounds__(64 * kRnWaves) void rmsnorm_kernel(const float* __restrict__ x,
                                                                const float* __restrict__ w, int n,
                                                                float eps, float* __restrict__ y) {
-  __shared__ float sq[kRnMaxN];
-  __shared__ EsLds<> es;
+  __shared__ EsLds<kRnChunks, M> es;
   const float* xr = x + (size_t)blockIdx.x * n;
   float* yr = y + (size_t)blockIdx.x * n;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const float v = xr[i];
-    sq[i] = __fmul_rn(v, v);
+  for (int i = threadIdx.x; i < kRnChunks * M; i += blockDim.x) {
+    const float v = i < n ? xr[i] : 0.0f;
+    es.TP[es_slot<kRnChunks, M>(i)] = i < n ? __fmul_rn(v, v) : -0.0f;
   }
   lds_barrier();
-  // chunks of 64 terms up to 4096 (more chunks run in parallel), else of 128
-  const float ss = n <= 64 * kEsMaxChunks ? exact_seq_sum<kRnWaves, 64>(sq, n, 0.0f, es)
-                                          : exact_seq_sum<kRnWaves, 128>(sq, n, 0.0f, es);
+  const float ss = exact_seq_sum<kRnWaves, kRnChunks, M>(n, 0.0f, es);
   const float inv = rms_inv_exact(ss, n, eps);
   for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = __fmul_rn(__fmul_rn(xr[i], inv), w[i]);
 }
@@ -621,14 +621,13 @@ static int ffn_fused_launch(const kh_sparse_ffn* f, const float* x, const int32_
   const int nw = small ? kFuWavesMin : kFuWaves;
   const int blocks = ceil_div(n_active, nw);
   const size_t lds = sizeof(float) * ((size_t)kFuMaxH + kFuWaves);
-  static bool attr = false;
-  if (!attr) {
-    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel<kFuWaves>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
-    KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel<kFuWavesMin>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
-    attr = true;
-  }
+  static std::once_flag once;
+  std::call_once(once, [] {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel<kFuWaves>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds);
+    hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel<kFuWavesMin>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds);
+  });
   if (small)
     hipLaunchKernelGGL(ffn_fused1_kernel<kFuWavesMin>, dim3(blocks), dim3(64 * kFuWavesMin), lds, st,
                        f->wgu, f->wdt, x, H, active, n_active, n_active_dev, f->inter, f->err, hbuf,
@@ -638,8 +637,7 @@ static int ffn_fused_launch(const kh_sparse_ffn* f, const float* x, const int32_
                        f->wgu, f->wdt, x, H, active, n_active, n_active_dev, f->inter, f->err, hbuf,
                        partial, nrm.w, nrm.inv);
   KH_LAUNCHED();
-  hipLaunchKernelGGL(partials_reduce_kernel<1>, dim3(ceil_div(H, 64), 1), dim3(64 * kRedWaves), 0,
-                     st, partial, H, blocks, y, accumulate, nullptr, 0);
+  partials_reduce_launch(partial, H, blocks, y, accumulate, st);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -706,8 +704,11 @@ extern "C" int kh_rmsnorm(const float* x_dev, const float* w_dev, int64_t batch,
   KH_CHECK_ARG(x_dev && w_dev && y_dev, "null argument");
   KH_CHECK_ARG(batch >= 0 && n > 0, "bad shape");
   if (batch == 0) return KH_OK;
-  if (n <= kRnMaxN)
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(batch), dim3(64 * kRnWaves), 0, as_stream(stream), x_dev,
+  if (n <= kRnChunks * 128)
+    hipLaunchKernelGGL(rmsnorm_kernel<128>, dim3(batch), dim3(64 * kRnWaves), 0, as_stream(stream), x_dev,
+                       w_dev, n, eps, y_dev);
+  else if (n <= kRnMaxN)
+    hipLaunchKernelGGL(rmsnorm_kernel<256>, dim3(batch), dim3(64 * kRnWaves), 0, as_stream(stream), x_dev,
                        w_dev, n, eps, y_dev);
   else
     hipLaunchKernelGGL(rmsnorm_seq_kernel, dim3(batch), dim3(256), 0, as_stream(stream), x_dev,

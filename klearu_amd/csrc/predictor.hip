@@ -185,14 +185,15 @@ constexpr int kL1LdsBytes = (kL1Chains + 1) * kL1LdsIn * 4;  // products + x
 
 // With norm_w set, x is the un-normalised hidden row and the kernel applies
 // RmsNorm first (model/rms_norm.rs:43-64): the reference's sequential sum of
-// squares (exact_seq_sum, run by every wave while the weight loads are in
-// flight), its scale, then (x * inv) * norm_w.  Block 0 stores the scale in
-// inv_out[b] for the kernels that consume the same normalised row later.
-// The norm requires n_in % 4 == 0 (host-checked).
-constexpr int kL1EsChunk = kL1LdsIn / kEsMaxChunks;  // terms per chunk of the exact sum
-static_assert(sizeof(float) * kL1LdsIn + sizeof(EsLds<>) <=
-                  sizeof(float4) * (kL1LdsIn / 4) * kL1Chains,
-              "squares and the exact-sum scratch fit in the products region");
+// squares (exact_seq_sum over 32 chunks of 128 terms, run by every wave while
+// the weight loads are in flight), its scale, then (x * inv) * norm_w.  Block 0
+// stores the scale in inv_out[b] for the kernels that consume the same
+// normalised row later.  The norm requires n_in % 4 == 0 (host-checked).
+constexpr int kL1EsChunks = 32;
+constexpr int kL1EsM = kL1LdsIn / kL1EsChunks;  // terms per chunk of the exact sum
+using L1Es = EsLds<kL1EsChunks, kL1EsM>;
+static_assert(sizeof(L1Es) <= sizeof(float4) * (kL1LdsIn / 4) * kL1Chains,
+              "the exact-sum scratch fits in the products region");
 
 template <typename W>
 __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
@@ -202,14 +203,11 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
   using B8 = Blk8<W>;
   using V = typename B8::V;
   constexpr int SPP = kL1LdsIn / kL1Stage / kL1Prod;  // stages per producer
-  constexpr int kXq = kL1LdsIn / 4 / 64;              // x float4 per consumer lane
   extern __shared__ float4 lds4[];
   float4(*P)[kL1Chains] = reinterpret_cast<float4(*)[kL1Chains]>(lds4);  // [n_in/4][chain]
   float* xs = reinterpret_cast<float*>(lds4 + (kL1LdsIn / 4) * kL1Chains);
-  // until the norm is known the products region holds the squares and the
-  // exact-sum scratch
-  float* sq = reinterpret_cast<float*>(lds4);
-  auto& es = *reinterpret_cast<EsLds<>*>(sq + kL1LdsIn);
+  // until the norm is known the products region holds the exact-sum scratch
+  auto& es = *reinterpret_cast<L1Es*>(lds4);
   const int b = blockIdx.y;
   const int c0 = blockIdx.x * kL1Chains;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -217,34 +215,26 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
   const int p = wave - 1;
   const float* xr = x + (size_t)b * n_in;
   const int n4 = n_in >> 2;
-  // The consumer wave stages x (one round trip) while the producers issue
-  // every weight load: no wave waits for another's loads before the barrier.
-  V pre[SPP][kL1Q];
-  float bv = 0.0f;
-  float4 xv[kXq], wn[kXq];
-  if (wave == 0) {
-    bv = bias[min(c0 + (lane & (kL1Chains - 1)), hid - 1)];
-    if ((n_in & 3) == 0) {
+  // Every wave first requests its share of x (and of the norm weights), then
+  // the producers request every weight of the block: the small x loads sit
+  // ahead of the weight stream in the CU's queue, so the norm can start after
+  // one round trip while the weights are still arriving.
+  constexpr int kXs = (kL1LdsIn / 4 + kL1Threads - 1) / kL1Threads;  // float4 of x per thread
+  const bool vec = (n_in & 3) == 0;
+  float4 xv[kXs], wn[kXs];
+  const float bv = wave == 0 ? bias[min(c0 + (lane & (kL1Chains - 1)), hid - 1)] : 0.0f;
+  if (vec) {
 #pragma unroll
-      for (int q = 0; q < kXq; ++q) xv[q] = reinterpret_cast<const float4*>(xr)[min(lane + 64 * q, n4 - 1)];
-      if (norm_w) {
+    for (int q = 0; q < kXs; ++q)
+      xv[q] = reinterpret_cast<const float4*>(xr)[min((int)threadIdx.x + q * kL1Threads, n4 - 1)];
+    if (norm_w) {
 #pragma unroll
-        for (int q = 0; q < kXq; ++q) wn[q] = reinterpret_cast<const float4*>(norm_w)[min(lane + 64 * q, n4 - 1)];
-        // squares as Rust forms them (v * v, rounded) for the sequential sum
-#pragma unroll
-        for (int q = 0; q < kXq; ++q)  // clamped, unconditional (see stage_f4)
-          reinterpret_cast<float4*>(sq)[min(lane + 64 * q, n4 - 1)] =
-              make_float4(__fmul_rn(xv[q].x, xv[q].x), __fmul_rn(xv[q].y, xv[q].y),
-                          __fmul_rn(xv[q].z, xv[q].z), __fmul_rn(xv[q].w, xv[q].w));
-      } else {
-#pragma unroll
-        for (int q = 0; q < kXq; ++q)  // clamped, unconditional (see stage_f4)
-          reinterpret_cast<float4*>(xs)[min(lane + 64 * q, n4 - 1)] = xv[q];
-      }
-    } else {
-      for (int j = lane; j < n_in; j += 64) xs[j] = xr[j];
+      for (int q = 0; q < kXs; ++q)
+        wn[q] = reinterpret_cast<const float4*>(norm_w)[min((int)threadIdx.x + q * kL1Threads, n4 - 1)];
     }
-  } else {
+  }
+  V pre[SPP][kL1Q];
+  if (wave > 0) {
     const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
 #pragma unroll
     for (int i = 0; i < SPP; ++i)
@@ -257,23 +247,42 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
         pre[i][q] = wv[(size_t)jb * hid + ch];
       }
   }
+  if (vec) {
+    if (norm_w) {
+      // squares as Rust forms them (v * v, rounded) for the sequential sum,
+      // -0.0 past the row (four terms never straddle a chunk of 128)
+#pragma unroll
+      for (int q = 0; q < kXs; ++q) {
+        const int i4 = threadIdx.x + q * kL1Threads;
+        if (i4 < kL1LdsIn / 4)
+          *reinterpret_cast<float4*>(&es.TP[es_slot<kL1EsChunks, kL1EsM>(4 * i4)]) =
+              i4 < n4 ? make_float4(__fmul_rn(xv[q].x, xv[q].x), __fmul_rn(xv[q].y, xv[q].y),
+                                    __fmul_rn(xv[q].z, xv[q].z), __fmul_rn(xv[q].w, xv[q].w))
+                      : make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < kXs; ++q)  // clamped, unconditional (see stage_f4)
+        reinterpret_cast<float4*>(xs)[min((int)threadIdx.x + q * kL1Threads, n4 - 1)] = xv[q];
+    }
+  } else {
+    for (int j = threadIdx.x; j < n_in; j += kL1Threads) xs[j] = xr[j];
+  }
   lds_barrier();
   if (norm_w) {
     // sum_sq over the row in the reference's order (rms_norm.rs:48-51)
-    const float ss = exact_seq_sum<kL1Prod + 1, kL1EsChunk>(sq, n_in, 0.0f, es);
+    const float ss = exact_seq_sum<kL1Prod + 1, kL1EsChunks, kL1EsM>(n_in, 0.0f, es);
     const float inv = rms_inv_exact(ss, n_in, eps);
-    if (wave == 0) {
 #pragma unroll
-      for (int q = 0; q < kXq; ++q) {
-        float4 v = xv[q];
-        v.x = __fmul_rn(__fmul_rn(v.x, inv), wn[q].x);
-        v.y = __fmul_rn(__fmul_rn(v.y, inv), wn[q].y);
-        v.z = __fmul_rn(__fmul_rn(v.z, inv), wn[q].z);
-        v.w = __fmul_rn(__fmul_rn(v.w, inv), wn[q].w);
-        reinterpret_cast<float4*>(xs)[min(lane + 64 * q, n4 - 1)] = v;
-      }
-      if (blockIdx.x == 0 && lane == 0) inv_out[b] = inv;
+    for (int q = 0; q < kXs; ++q) {
+      float4 v = xv[q];
+      v.x = __fmul_rn(__fmul_rn(v.x, inv), wn[q].x);
+      v.y = __fmul_rn(__fmul_rn(v.y, inv), wn[q].y);
+      v.z = __fmul_rn(__fmul_rn(v.z, inv), wn[q].z);
+      v.w = __fmul_rn(__fmul_rn(v.w, inv), wn[q].w);
+      reinterpret_cast<float4*>(xs)[min((int)threadIdx.x + q * kL1Threads, n4 - 1)] = v;  // clamped
     }
+    if (blockIdx.x == 0 && threadIdx.x == 0) inv_out[b] = inv;
     lds_barrier();
   }
   // products of stage p + kL1Prod*i; loads arrive in issue order, so each

@@ -175,6 +175,8 @@ def _ffn_case(orc, rng, H, I, k, batch):
     (1024, 2816, 403, 1),     # single token, partial last block
     (512, 64, 64, 1),         # every neuron active
     (512, 64, 1, 1),          # a single neuron
+    (4096, 11008, 5000, 1),   # single token, more active rows than the consumers hold in registers
+    (2048, 5632, 5632, 1),    # single token, every neuron active
 ])
 def test_sparse_ffn_matches_oracle(kh, orc, H, I, k, batch):
     from klearu_amd.dejavu import Mlp
