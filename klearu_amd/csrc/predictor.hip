@@ -179,8 +179,12 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_kernel(
 // Layer 1 for n_in <= kL1LdsIn: the block's products w*x for every step are
 // formed into LDS first (kL1Chains * n_in floats; all weight loads of the
 // block are in flight at once), then the consumer wave runs its chains over
-// them with no further barrier, reading 32 steps ahead of the adds.
+// them with no further barrier, reading 32 steps ahead of the adds.  Wave 0
+// is the consumer, waves 1..kL1Prod the producers; kL1Help more waves only
+// stage x and share the RmsNorm sum (two waves per SIMD run its windows).
 constexpr int kL1LdsIn = 4096;
+constexpr int kL1Help = 3;  // waves that only stage x and share the RmsNorm sum
+constexpr int kL1LdsThreads = 64 * (1 + kL1Prod + kL1Help);
 constexpr int kL1LdsBytes = (kL1Chains + 1) * kL1LdsIn * 4;  // products + x
 
 // With norm_w set, x is the un-normalised hidden row and the kernel applies
@@ -196,7 +200,7 @@ static_assert(sizeof(L1Es) <= sizeof(float4) * (kL1LdsIn / 4) * kL1Chains,
               "the exact-sum scratch fits in the products region");
 
 template <typename W>
-__global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
+__global__ __launch_bounds__(kL1LdsThreads) void pred_l1_lds_kernel(
     const W* __restrict__ Wb, const float* __restrict__ bias, const float* __restrict__ x,
     int n_in, int hid, float* __restrict__ h, const float* __restrict__ norm_w,
     float* __restrict__ inv_out, float eps) {
@@ -219,22 +223,23 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
   // the producers request every weight of the block: the small x loads sit
   // ahead of the weight stream in the CU's queue, so the norm can start after
   // one round trip while the weights are still arriving.
-  constexpr int kXs = (kL1LdsIn / 4 + kL1Threads - 1) / kL1Threads;  // float4 of x per thread
+  constexpr int kXs = (kL1LdsIn / 4 + kL1LdsThreads - 1) / kL1LdsThreads;  // float4 of x per thread
   const bool vec = (n_in & 3) == 0;
   float4 xv[kXs], wn[kXs];
   const float bv = wave == 0 ? bias[min(c0 + (lane & (kL1Chains - 1)), hid - 1)] : 0.0f;
   if (vec) {
 #pragma unroll
     for (int q = 0; q < kXs; ++q)
-      xv[q] = reinterpret_cast<const float4*>(xr)[min((int)threadIdx.x + q * kL1Threads, n4 - 1)];
+      xv[q] = reinterpret_cast<const float4*>(xr)[min((int)threadIdx.x + q * kL1LdsThreads, n4 - 1)];
     if (norm_w) {
 #pragma unroll
       for (int q = 0; q < kXs; ++q)
-        wn[q] = reinterpret_cast<const float4*>(norm_w)[min((int)threadIdx.x + q * kL1Threads, n4 - 1)];
+        wn[q] = reinterpret_cast<const float4*>(norm_w)[min((int)threadIdx.x + q * kL1LdsThreads, n4 - 1)];
     }
   }
   V pre[SPP][kL1Q];
-  if (wave > 0) {
+  const bool prod = wave >= 1 && wave <= kL1Prod;
+  if (prod) {
     const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
 #pragma unroll
     for (int i = 0; i < SPP; ++i)
@@ -253,7 +258,7 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
       // -0.0 past the row (four terms never straddle a chunk of 128)
 #pragma unroll
       for (int q = 0; q < kXs; ++q) {
-        const int i4 = threadIdx.x + q * kL1Threads;
+        const int i4 = threadIdx.x + q * kL1LdsThreads;
         if (i4 < kL1LdsIn / 4)
           *reinterpret_cast<float4*>(&es.TP[es_slot<kL1EsChunks, kL1EsM>(4 * i4)]) =
               i4 < n4 ? make_float4(__fmul_rn(xv[q].x, xv[q].x), __fmul_rn(xv[q].y, xv[q].y),
@@ -263,15 +268,15 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
     } else {
 #pragma unroll
       for (int q = 0; q < kXs; ++q)  // clamped, unconditional (see stage_f4)
-        reinterpret_cast<float4*>(xs)[min((int)threadIdx.x + q * kL1Threads, n4 - 1)] = xv[q];
+        reinterpret_cast<float4*>(xs)[min((int)threadIdx.x + q * kL1LdsThreads, n4 - 1)] = xv[q];
     }
   } else {
-    for (int j = threadIdx.x; j < n_in; j += kL1Threads) xs[j] = xr[j];
+    for (int j = threadIdx.x; j < n_in; j += kL1LdsThreads) xs[j] = xr[j];
   }
   lds_barrier();
   if (norm_w) {
     // sum_sq over the row in the reference's order (rms_norm.rs:48-51)
-    const float ss = exact_seq_sum<kL1Prod + 1, kL1EsChunks, kL1EsM>(n_in, 0.0f, es);
+    const float ss = exact_seq_sum<kL1LdsThreads / 64, kL1EsChunks, kL1EsM>(n_in, 0.0f, es);
     const float inv = rms_inv_exact(ss, n_in, eps);
 #pragma unroll
     for (int q = 0; q < kXs; ++q) {
@@ -280,7 +285,7 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
       v.y = __fmul_rn(__fmul_rn(v.y, inv), wn[q].y);
       v.z = __fmul_rn(__fmul_rn(v.z, inv), wn[q].z);
       v.w = __fmul_rn(__fmul_rn(v.w, inv), wn[q].w);
-      reinterpret_cast<float4*>(xs)[min((int)threadIdx.x + q * kL1Threads, n4 - 1)] = v;  // clamped
+      reinterpret_cast<float4*>(xs)[min((int)threadIdx.x + q * kL1LdsThreads, n4 - 1)] = v;  // clamped
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) inv_out[b] = inv;
     lds_barrier();
@@ -349,12 +354,12 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_lds_kernel(
   // The first round of stages (one per producer) is published first, so the
   // chain starts while the producers form the rest.
   constexpr int kSeg = kL1Prod * kL1Stage;
-  if (wave > 0) make(0);
+  if (prod) make(0);
   lds_barrier();
-  if (wave > 0) {
+  if (prod) {
 #pragma unroll
     for (int i = 1; i < SPP; ++i) make(i);
-  } else {
+  } else if (wave == 0) {
     run(0, min(n_in, kSeg));
   }
   lds_barrier();
@@ -1137,7 +1142,7 @@ static int predict_typed(const kh_predictor* p, const float* x, int64_t batch, f
   if (rc != KH_OK) return rc;
   if (p->in_dim <= kL1LdsIn)
     hipLaunchKernelGGL(pred_l1_lds_kernel<W>, dim3(ceil_div(p->hid, kL1Chains), batch),
-                       dim3(kL1Threads), kL1LdsBytes, st, w1, p->b1, x, p->in_dim, p->hid, hbuf,
+                       dim3(kL1LdsThreads), kL1LdsBytes, st, w1, p->b1, x, p->in_dim, p->hid, hbuf,
                        nrm.w, nrm.inv, nrm.eps);
   else if (nrm.w) {
     set_error("the fused RmsNorm supports predictor inputs up to %d", kL1LdsIn);
