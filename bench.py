@@ -17,14 +17,17 @@ the predictor and FFN kernels).
 JSON line fields beyond the driver contract:
   ffn_only      the FFN calls alone (32 layers, fixed active sets): tokens/s and
                 gathered-weight GB/s -- the roofline leg
-  roofline      one kh_sparse_ffn_forward call (ffn_fused1 + partials_reduce):
-                algorithmic bytes 3*k*H*2 per call over its event-timed duration
+  roofline      one kh_sparse_ffn_forward call (ffn_fused1 + partials_reduce16):
+                algorithmic bytes 3*k*H*2 per call over its in-graph duration (HIP
+                events around graph replays); traffic from the committed rocprofv3
+                --pmc summary in profiles/ (labelled as not from this run)
   cpu_baseline  the oracle's port of the reference CPU path (AVX2 dots,
                 sequential predictor / down projection, 1 thread) on a bounded
                 sample of the same layer shape
   configs       the other BASELINE configs (SLIDE hidden layer, 1.1B FFN, 7B
                 batch 16, head-sparse attention b1/b8, extreme classification),
-                each with GPU throughput, HBM fraction and its CPU port timing
+                each with GPU throughput, HBM fraction (cfg1: achieved GB/s on
+                L2-resident data, no HBM fraction) and its CPU port timing
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--legs all|cfg3,...]
 """
 from __future__ import annotations
@@ -416,12 +419,18 @@ def slide_cfg1_leg(steps, seed, timer, cpu_seconds):
     ms = timer.time(run, steps, 3)
     o = off.cpu().numpy()
     A = np.diff(o)
-    bytes_call = int(A.sum()) * (dim * 4 + 8) + B * dim * 4 + B * 50 * 16 * 4
+    nnz = np.count_nonzero(X, axis=1)
+    # bytes the path must move per call: each active neuron's weights at the
+    # sample's nonzero columns, its bias and two outputs; x for hashing; the
+    # 50 queried buckets of 128 ids per sample
+    bytes_call = int(np.sum(A * (4 * nnz + 4 + 8))) + B * dim * 4 + B * 50 * 128 * 4
     gbs = bytes_call / (ms * 1e-3) / 1e9
     res = dict(workload="cfg1: SLIDE hidden layer 1024x784 f32, batch 128 (80% zeros), SimHash K6 L50 FIFO 128, "
                         "active = union, ReLU", unit="samples/s", value=round(B * 1000.0 / ms, 1),
-               ms_per_step=round(ms, 4), hbm_gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4),
-               mean_active=float(A.mean()), index_build_ms=round(build_ms, 2),
+               ms_per_step=round(ms, 4), achieved_gbs=round(gbs, 1), bytes_per_call=bytes_call,
+               bound="l2-resident: the 3.2 MB weight matrix and the index stay in L2/MALL across calls, so "
+                     "this is not an HBM roofline and no HBM fraction is given",
+               mean_active=float(A.mean()), mean_nnz=float(nnz.mean()), index_build_ms=round(build_ms, 2),
                note="eager calls, asynchronous (the output capacity covers every row's worst case)")
     if cpu_seconds > 0:
         import oracle
@@ -633,6 +642,14 @@ def main():
     if not args.no_cpu:
         cpu = cpu_ffn(args.cpu_seconds, args.seed, 4096, 11008, 256, 0.15, args.layers)
         log(f"[bench] cpu baseline {cpu['value']:.3f} tokens/s")
+        # The reference decodes a batch one token at a time (forward_decode_sparse
+        # per token), so its batched throughput is its per-token rate.
+        per_token = "the reference runs each token of a batch through forward_decode_sparse on its own, so " \
+                    "its batched rate is the per-token rate measured for the batch-1 leg"
+        if "cfg3_batch16" in extra:
+            extra["cfg3_batch16"]["cpu"] = dict(cpu, sample=cpu["sample"] + "; " + per_token)
+        if "cfg4b8" in extra and "cpu" in extra.get("cfg4", {}):
+            extra["cfg4b8"]["cpu"] = dict(extra["cfg4"]["cpu"], sample=extra["cfg4"]["cpu"]["sample"] + "; " + per_token)
     if "decoder" in legs:
         halves = None
         if cpu and "cpu" in extra.get("cfg4", {}):
@@ -669,8 +686,12 @@ def main():
         "step_hbm_gbs": round(r["step_gbs"], 1),
         "roofline": {"bound": "hbm", "achieved": round(r["ffn_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["ffn_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "kh_sparse_ffn_forward (ffn_fused1_kernel + partials_reduce_kernel)",
-                     "bytes_per_launch": int(r["bytes_per_call"]), "launch_us": round(per_call_ms * 1e3, 3)},
+                     "traffic_source": "profiles/ffn_fused1_cfg3_traffic.txt (rocprofv3 --pmc FETCH_SIZE and "
+                                       "WRITE_SIZE, scaled by a copy kernel; not this run)",
+                     "kernel": "kh_sparse_ffn_forward (ffn_fused1_kernel + partials_reduce16_kernel)",
+                     "bytes_per_launch": int(r["bytes_per_call"]), "launch_us": round(per_call_ms * 1e3, 3),
+                     "basis": "HIP events on the kernels' stream around replays of a graph of one call per "
+                              "layer: the in-graph time per call, launch gaps included"},
         "cpu_baseline": cpu,
         "configs": extra,
     }
