@@ -403,8 +403,16 @@ int kh_dejavu_sparse_attention_forward(const kh_dejavu_sparse_attention* a, cons
 
 typedef struct kh_sparse_attn kh_sparse_attn;
 
-#define KH_KV_BF16 0 /* cache rows rounded to BF16 (half the bytes per step) */
-#define KH_KV_F32 1  /* cache rows kept in f32, as KvCache stores them */
+/* Both kinds hold exactly the rows KvCache (model/kv_cache.rs:5-48) would hold.
+ * KH_KV_BF16 (default): rows loaded by kh_sparse_attn_load_cache whose values
+ *   are all BF16 values (a BF16 checkpoint's prefill) are stored as BF16, half
+ *   the bytes a decode step reads; every other row (appended by a decode step,
+ *   loaded from device memory, or loaded with bits BF16 cannot hold) is stored
+ *   in f32.  The handle keeps both a BF16 and an f32 array: 6 bytes per cache
+ *   element.
+ * KH_KV_F32: every row in f32 (4 bytes per cache element). */
+#define KH_KV_BF16 0
+#define KH_KV_F32 1
 
 /* Attention{q,k,v,o}_proj (model/attention.rs:8-64) + KvCache (model/kv_cache.rs:5-25)
  * + RotaryEmbedding::new(head_dim, max_seq, rope_theta) (model/rope.rs:17-46)
@@ -424,8 +432,9 @@ int kh_sparse_attn_create_dev(int hidden, int num_heads, int num_kv_heads, int h
                               kh_sparse_attn** out);
 int kh_sparse_attn_destroy(kh_sparse_attn* a);
 /* Fill positions [0, len) of sequence b from f32 host arrays k_host/v_host
- * [nkv][len][d] (rounded to BF16 for a KH_KV_BF16 cache) and set its length
- * (KvCache::append repeated, kv_cache.rs:33-48).  Synchronous. */
+ * [nkv][len][d] and set its length (KvCache::append repeated,
+ * kv_cache.rs:33-48); the values are kept exactly (BF16 storage only when
+ * every value of k and v is a BF16 value).  Synchronous. */
 int kh_sparse_attn_load_cache(kh_sparse_attn* a, int64_t b, const float* k_host,
                               const float* v_host, int64_t len);
 /* Same from f32 device arrays (e.g. a prefill's K/V), enqueued on `stream`. */

@@ -379,22 +379,31 @@ __device__ __forceinline__ void load_f4s(const float* __restrict__ p, float* f) 
   }
 }
 
-// Grid (nsplit, nsel + 1, batch).
-// Block (s, a < nsel, b): chunk s of the cache for token b's selected-head entry
-// a -> the un-normalised head output po[b][a][s][D] and (max, exp-sum)
-// pml[b][a][s] (attn_merge_kernel merges the chunks).
+// The cache of sequence b holds rows [0, pre[b]) in BF16 (kc16/vc16: rows
+// loaded as BF16 values, so the storage is exact) and rows [pre[b], len[b]) in
+// f32 (kc32/vc32: rows appended by decode steps, and loaded rows that are not
+// BF16 values), both arrays [max_batch][nkv][max_seq][D] at the rows'
+// positions.  Every row then holds exactly what the reference's f32 KvCache
+// holds (kv_cache.rs:33-48), and the bulk of a long prompt streams at BF16 width.
+//
+// Grid (n16 + n32, nsel + 1, batch).
+// Block (s < n16, a < nsel, b): BF16 chunk s (positions s*CH16 ..) of the prefix;
+// block (n16 + c, a, b): f32 chunk c (positions pre[b] + c*CH32 ..) of the rest,
+// including this step's row len[b] (taken from the projection).  Each writes
+// the un-normalised head output po[b][a][slot][D] and (max, exp-sum)
+// pml[b][a][slot] with slot = s, or ceil(pre[b] / CH16) + c: the slots of a
+// sequence follow its positions.  Blocks past the rows exit at once.
 // Block (s, nsel, b): appends this step's roped K and V of kv heads s, s+nsplit,
-// ... at position len[b] (decode blocks never read row len), and writes zeros
-// for union heads s, s+nsplit, ... that token b did not select (the
-// reference's zero-filled attn_concat, :44).
+// ... at position len[b] (f32 rows; decode blocks never read row len from the
+// cache), and writes zeros for union heads s, s+nsplit, ... that token b did
+// not select (the reference's zero-filled attn_concat, :44).
 template <typename KV, int D>
-__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
-    KV* __restrict__ kc, KV* __restrict__ vc, const float* __restrict__ y, int ystride, int nkv,
-    int nh, const int32_t* __restrict__ heads, int nsel, const int32_t* __restrict__ lens,
-    const int64_t* __restrict__ positions, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t, int max_seq, float inv_sqrt, int nsplit,
-    const int32_t* __restrict__ urank, float* __restrict__ po, float2* __restrict__ pml,
-    float* __restrict__ cat, int catstride) {
+__device__ __forceinline__ void attn_decode_chunk(
+    const KV* __restrict__ kc, const KV* __restrict__ vc, int start, int seg_end, int slot,
+    const float* __restrict__ yb, int kvd, int nh, int nkv, const int32_t* __restrict__ hb,
+    int a, int b, int len, const float* __restrict__ ct, const float* __restrict__ st,
+    int max_seq, float inv_sqrt, int nsel, int nsplit, float* __restrict__ po,
+    float2* __restrict__ pml) {
   constexpr int EPL = 16 / sizeof(KV);          // elements per 16-byte load
   constexpr int LPR = D / EPL;                  // lanes per cache row
   constexpr int RPP = kAttnThreads / LPR;       // rows per pass
@@ -408,48 +417,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   __shared__ float s_red[RPP][D];
   __shared__ float s_wm[NW], s_wl[NW];
   __shared__ uint64_t s_tab[32];  // kExp2Tab
-  const int s = blockIdx.x, a = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
-  const int len = lens[b];
-  const bool valid = len < max_seq;  // a full cache refuses the step for this sequence
-  int64_t pos = positions ? positions[b] : len;
-  pos = pos < 0 ? 0 : (pos >= max_seq ? max_seq - 1 : pos);
-  const int kvd = nkv * D;
-  const float* yb = y + (size_t)b * ystride;
-  const float* ct = cos_t + pos * HALF;
-  const float* st = sin_t + pos * HALF;
-  const int32_t* hb = heads + (size_t)b * nsel;
-  if (a == nsel) {
-    if (valid) {
-      // KvCache::append (kv_cache.rs:33-48) of the roped k (sparse_attention.rs:33-39)
-      for (int hh = s; hh < nkv; hh += nsplit) {
-        const float* kx = yb + (size_t)hh * D;
-        const float* vx = kx + kvd;
-        const size_t dst = (((size_t)b * nkv + hh) * max_seq + len) * D;
-        for (int i = t; i < D; i += kAttnThreads) {
-          float kr;
-          if (i < HALF) kr = kx[i] * ct[i] - kx[i + HALF] * st[i];
-          else kr = kx[i] * ct[i - HALF] + kx[i - HALF] * st[i - HALF];
-          store_kv(kc + dst + i, kr);
-          store_kv(vc + dst + i, vx[i]);
-        }
-      }
-    }
-    for (int hu = s; hu < nh; hu += nsplit) {
-      const int u = urank[hu];
-      if (u < 0) continue;
-      int sel = 0;
-      if (valid)
-        for (int i = 0; i < nsel; ++i) sel |= hb[i] == hu;
-      if (!sel)
-        for (int i = t; i < D; i += kAttnThreads) cat[(size_t)b * catstride + (size_t)u * D + i] = 0.0f;
-    }
-    return;
-  }
+  const int t = threadIdx.x;
   const int h = hb[a];
-  if (h < 0 || h >= nh || !valid) return;  // sparse_attention.rs:48-50
-  const int start = s * CH;
-  if (start > len) return;
-  const int n = min(CH, len + 1 - start);
+  if (h < 0 || h >= nh) return;  // sparse_attention.rs:48-50
+  if (start >= seg_end) return;
+  const int n = min(CH, seg_end - start);
   const int kvh = h / (nh / nkv);
   const int sl = t % LPR, r0 = t / LPR;
   const int e0 = sl * EPL;
@@ -473,10 +445,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   load_f4s<EPL>(ct + ec, cs);
   load_f4s<EPL>(st + ec, sn);
   __builtin_amdgcn_sched_barrier(0);
-  // Rows past the last cached one are clamped to it (position len itself is
-  // taken from this step's k/v; with an empty cache row 0 is read and never used).
+  // Rows past the segment's last cached one are clamped to it (position len
+  // itself is taken from this step's k/v; with no cached row in the segment,
+  // its first row is read and never used).
   const size_t rowbase = ((size_t)b * nkv + kvh) * (size_t)max_seq;
-  const int last = len > 0 ? len - 1 : 0;
+  const int last = max(0, min(seg_end, len) - 1);
   uint4 kr[NP], vr[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
@@ -557,19 +530,86 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
 #pragma unroll
   for (int e = 0; e < EPL; ++e) s_red[r0][e0 + e] = acc[e];
   lds_barrier();
-  const size_t slot = ((size_t)b * nsel + a) * nsplit + s;
+  const size_t so = ((size_t)b * nsel + a) * nsplit + slot;
   if (t < D) {
     float o = 0.0f;
 #pragma unroll
     for (int r = 0; r < RPP; ++r) o += s_red[r][t];
-    po[slot * D + t] = o;
+    po[so * D + t] = o;
   }
   if (t == 0) {
     float l = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) l += s_wl[w];
-    pml[slot] = make_float2(m, l);
+    pml[so] = make_float2(m, l);
   }
+}
+
+
+template <int D>
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
+    const uint16_t* __restrict__ kc16, const uint16_t* __restrict__ vc16, float* __restrict__ kc32,
+    float* __restrict__ vc32, const int32_t* __restrict__ pre, int n16, const float* __restrict__ y,
+    int ystride, int nkv, int nh, const int32_t* __restrict__ heads, int nsel,
+    const int32_t* __restrict__ lens, const int64_t* __restrict__ positions,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int max_seq, float inv_sqrt,
+    int nsplit, const int32_t* __restrict__ urank, float* __restrict__ po, float2* __restrict__ pml,
+    float* __restrict__ cat, int catstride) {
+  constexpr int HALF = D / 2;
+  constexpr int CH16 = attn_chunk<uint16_t, D>(), CH32 = attn_chunk<float, D>();
+  const int s = blockIdx.x, a = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
+  const int len = lens[b];
+  const bool valid = len < max_seq;  // a full cache refuses the step for this sequence
+  int64_t pos = positions ? positions[b] : len;
+  pos = pos < 0 ? 0 : (pos >= max_seq ? max_seq - 1 : pos);
+  const int kvd = nkv * D;
+  const float* yb = y + (size_t)b * ystride;
+  const float* ct = cos_t + pos * HALF;
+  const float* st = sin_t + pos * HALF;
+  const int32_t* hb = heads + (size_t)b * nsel;
+  if (a == nsel) {
+    if (valid) {
+      // KvCache::append (kv_cache.rs:33-48) of the roped k (sparse_attention.rs:33-39)
+      for (int hh = s; hh < nkv; hh += nsplit) {
+        const float* kx = yb + (size_t)hh * D;
+        const float* vx = kx + kvd;
+        const size_t dst = (((size_t)b * nkv + hh) * max_seq + len) * D;
+        for (int i = t; i < D; i += kAttnThreads) {
+          float kr;
+          if (i < HALF) kr = kx[i] * ct[i] - kx[i + HALF] * st[i];
+          else kr = kx[i] * ct[i - HALF] + kx[i - HALF] * st[i - HALF];
+          kc32[dst + i] = kr;
+          vc32[dst + i] = vx[i];
+        }
+      }
+    }
+    for (int hu = s; hu < nh; hu += nsplit) {
+      const int u = urank[hu];
+      if (u < 0) continue;
+      int sel = 0;
+      if (valid)
+        for (int i = 0; i < nsel; ++i) sel |= hb[i] == hu;
+      if (!sel)
+        for (int i = t; i < D; i += kAttnThreads) cat[(size_t)b * catstride + (size_t)u * D + i] = 0.0f;
+    }
+    return;
+  }
+  if (!valid) return;
+  const int pb = pre[b];
+  if (s < n16) {
+    attn_decode_chunk<uint16_t, D>(kc16, vc16, s * CH16, pb, s, yb, kvd, nh, nkv, hb, a, b, len, ct, st,
+                                   max_seq, inv_sqrt, nsel, nsplit, po, pml);
+  } else {
+    const int c = s - n16;
+    attn_decode_chunk<float, D>(kc32, vc32, pb + c * CH32, len + 1, (pb + CH16 - 1) / CH16 + c, yb, kvd, nh,
+                                nkv, hb, a, b, len, ct, st, max_seq, inv_sqrt, nsel, nsplit, po, pml);
+  }
+}
+
+// Decode slots of a sequence: the BF16 chunks covering rows [0, pre), then the
+// f32 chunks covering rows [pre, len] (len: this step's row).
+__device__ __forceinline__ int attn_nslots(int pre, int len, int ch16, int ch32) {
+  return (pre + ch16 - 1) / ch16 + (len + 1 - pre + ch32 - 1) / ch32;
 }
 
 // One entry's head output, for R head dimensions e[r] per lane, from its ns
@@ -621,9 +661,10 @@ __device__ __forceinline__ void merge_chunks(const float* __restrict__ po,
 // attn_concat slice) into the head output cat[b][u*D ..], u = union rank of h.
 template <int D>
 __global__ __launch_bounds__(D) void attn_merge_kernel(
-    const float* __restrict__ po, const float2* __restrict__ pml, int nsplit, int chunk,
-    const int32_t* __restrict__ heads, int nsel, int nh, const int32_t* __restrict__ lens,
-    int max_seq, const int32_t* __restrict__ urank, float* __restrict__ cat, int catstride) {
+    const float* __restrict__ po, const float2* __restrict__ pml, int nsplit, int ch16, int ch32,
+    const int32_t* __restrict__ pre, const int32_t* __restrict__ heads, int nsel, int nh,
+    const int32_t* __restrict__ lens, int max_seq, const int32_t* __restrict__ urank,
+    float* __restrict__ cat, int catstride) {
   static_assert(D % 64 == 0, "whole waves");
   __shared__ uint64_t s_tab[32];  // kExp2Tab
   const int a = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63;
@@ -634,7 +675,7 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(
   const uint64_t tabv = kExp2Tab[t & 31];
   for (int i0 = 0; i0 < a; i0 += 64)
     if (__ballot(i0 + lane < a && hb[min(i0 + lane, a - 1)] == h)) return;  // not the first
-  const int ns = (len + chunk) / chunk;  // chunks covering len+1 rows
+  const int ns = attn_nslots(pre[b], len, ch16, ch32);
   if (t < 32) s_tab[t] = tabv;
   __syncthreads();
   float out[1] = {0.0f};
@@ -679,15 +720,15 @@ template <int NB>
 __global__ __launch_bounds__(kOprojThreads) void attn_oproj_kernel(
     const uint16_t* __restrict__ WoT, int H, int D, const int32_t* __restrict__ rows,
     int n_rows, const int32_t* __restrict__ n_rows_dev, const float* __restrict__ po,
-    const float2* __restrict__ pml, int nsplit, int chunk, const int32_t* __restrict__ heads,
-    int nsel, const int32_t* __restrict__ lens, int max_seq, int batch, int groups,
-    float* __restrict__ partial) {
+    const float2* __restrict__ pml, int nsplit, int ch16, int ch32, const int32_t* __restrict__ pre,
+    const int32_t* __restrict__ heads, int nsel, const int32_t* __restrict__ lens, int max_seq,
+    int batch, int groups, float* __restrict__ partial) {
   __shared__ float red[4][NB][kSlice];
   __shared__ int s_ids[kDownRows];
   __shared__ float s_h[NB][kDownRows];
   __shared__ int s_hd[NB][kOprojMaxSel];
   __shared__ uint64_t s_tab[32];  // kExp2Tab
-  __shared__ int s_len[NB];
+  __shared__ int s_len[NB], s_pre[NB];
   const int n = min(n_rows, *n_rows_dev);
   const int slice = blockIdx.x, grp = blockIdx.y;
   const int tid = threadIdx.x;
@@ -705,6 +746,7 @@ __global__ __launch_bounds__(kOprojThreads) void attn_oproj_kernel(
     s_hd[b][i - b * nsel] = b < batch ? heads[i] : -1;
   }
   if (tid < NB) s_len[tid] = tid < batch ? lens[tid] : max_seq;
+  if (tid < NB) s_pre[tid] = tid < batch ? pre[tid] : 0;
   if (tid < 32) s_tab[tid] = tabv;
   __syncthreads();
   constexpr int RPL = kDownRows / 8;  // rows per row lane
@@ -734,7 +776,7 @@ __global__ __launch_bounds__(kOprojThreads) void attn_oproj_kernel(
       const int rb = max(0, j * D - i0), re = min(nr, (j + 1) * D - i0);  // rows [rb, re)
       const int h = s_ids[rb] / D;
       const int len = s_len[b];
-      const int ns = len < max_seq ? (len + chunk) / chunk : 0;  // chunks covering len+1 rows
+      const int ns = len < max_seq ? attn_nslots(s_pre[b], len, ch16, ch32) : 0;
       const int ra = rb + lane, rc = rb + lane + 64;
       const int ea = (i0 + min(ra, re - 1)) % D, ec = (i0 + min(rc, re - 1)) % D;
       float out[2] = {0.0f, 0.0f};
@@ -822,8 +864,13 @@ struct kh_sparse_attn {
   int hidden = 0, nh = 0, nkv = 0, d = 0, max_seq = 0, max_batch = 0, kv_f32 = 0;
   uint16_t* wkvq = nullptr;  // [2*kvd + nh*d][hidden]
   uint16_t* wot = nullptr;   // [nh*d][hidden]
-  void* kc = nullptr;        // [max_batch][nkv][max_seq][d]
-  void* vc = nullptr;
+  // cache rows of sequence b: [0, pre[b]) in kc16/vc16 (BF16 values, KH_KV_BF16
+  // handles only), [pre[b], len[b]) in kc32/vc32; all [max_batch][nkv][max_seq][d]
+  uint16_t* kc16 = nullptr;
+  uint16_t* vc16 = nullptr;
+  float* kc32 = nullptr;
+  float* vc32 = nullptr;
+  int32_t* pre = nullptr;    // [max_batch]
   float* cos_t = nullptr;    // [max_seq][d/2]
   float* sin_t = nullptr;
   int32_t* lens = nullptr;   // [max_batch]
@@ -831,11 +878,10 @@ struct kh_sparse_attn {
   float* cat = nullptr;      // [max_batch][nh*d]
   int32_t* qrows = nullptr;  // [nh*d + 1 + nh]: rows, their count, union rank per head (-1: none)
   uint16_t* wkvq_t = nullptr;  // wkvq in 16 x 32 tiles (mfma_tile16x32) for the batched projections
-  std::vector<int64_t> len_host;
+  std::vector<int64_t> len_host, pre_host;
   Scratch po, pml, partial;
   int kvd() const { return nkv * d; }
   int ystride() const { return 2 * nkv * d + nh * d; }
-  size_t elt() const { return kv_f32 ? sizeof(float) : sizeof(uint16_t); }
   size_t seq_elems() const { return (size_t)nkv * max_seq * d; }
 };
 
@@ -844,8 +890,11 @@ extern "C" int kh_sparse_attn_destroy(kh_sparse_attn* a) {
   dev_free(a->wkvq);
   dev_free(a->wkvq_t);
   dev_free(a->wot);
-  dev_free(a->kc);
-  dev_free(a->vc);
+  dev_free(a->kc16);
+  dev_free(a->vc16);
+  dev_free(a->kc32);
+  dev_free(a->vc32);
+  dev_free(a->pre);
   dev_free(a->cos_t);
   dev_free(a->sin_t);
   dev_free(a->lens);
@@ -882,12 +931,18 @@ static int attn_alloc(int hidden, int num_heads, int num_kv_heads, int head_dim,
   a->max_batch = max_batch;
   a->kv_f32 = kv_dtype == KH_KV_F32;
   a->len_host.assign(max_batch, 0);
+  a->pre_host.assign(max_batch, 0);
   const size_t H = hidden, qd = (size_t)num_heads * head_dim, kvd = (size_t)num_kv_heads * head_dim;
   const size_t half = head_dim / 2;
   a->wkvq = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * (2 * kvd + qd) * H));
   a->wot = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * qd * H));
-  a->kc = dev_alloc(a->elt() * a->seq_elems() * max_batch);
-  a->vc = dev_alloc(a->elt() * a->seq_elems() * max_batch);
+  if (!a->kv_f32) {
+    a->kc16 = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * a->seq_elems() * max_batch));
+    a->vc16 = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * a->seq_elems() * max_batch));
+  }
+  a->kc32 = static_cast<float*>(dev_alloc(sizeof(float) * a->seq_elems() * max_batch));
+  a->vc32 = static_cast<float*>(dev_alloc(sizeof(float) * a->seq_elems() * max_batch));
+  a->pre = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * max_batch));
   a->cos_t = static_cast<float*>(dev_alloc(sizeof(float) * max_seq * half));
   a->sin_t = static_cast<float*>(dev_alloc(sizeof(float) * max_seq * half));
   a->lens = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * max_batch));
@@ -896,8 +951,8 @@ static int attn_alloc(int hidden, int num_heads, int num_kv_heads, int head_dim,
   a->qrows = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * (qd + 1 + num_heads)));
   if (max_batch > 1 && H % 32 == 0 && (2 * kvd + qd) % 16 == 0)
     a->wkvq_t = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * (2 * kvd + qd) * H));
-  if (!a->wkvq || !a->wot || !a->kc || !a->vc || !a->cos_t || !a->sin_t || !a->lens || !a->y ||
-      !a->cat || !a->qrows) {
+  if (!a->wkvq || !a->wot || (!a->kv_f32 && (!a->kc16 || !a->vc16)) || !a->kc32 || !a->vc32 || !a->pre ||
+      !a->cos_t || !a->sin_t || !a->lens || !a->y || !a->cat || !a->qrows) {
     kh_sparse_attn_destroy(a);
     return KH_ERR_ALLOC;
   }
@@ -914,7 +969,8 @@ static int attn_alloc(int hidden, int num_heads, int num_kv_heads, int head_dim,
     }
   if (hipMemcpy(a->cos_t, c.data(), sizeof(float) * c.size(), hipMemcpyHostToDevice) != hipSuccess ||
       hipMemcpy(a->sin_t, s.data(), sizeof(float) * s.size(), hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemset(a->lens, 0, sizeof(int32_t) * max_batch) != hipSuccess) {
+      hipMemset(a->lens, 0, sizeof(int32_t) * max_batch) != hipSuccess ||
+      hipMemset(a->pre, 0, sizeof(int32_t) * max_batch) != hipSuccess) {
     set_error("attention table upload failed");
     kh_sparse_attn_destroy(a);
     return KH_ERR_HIP;
@@ -1010,27 +1066,35 @@ extern "C" int kh_sparse_attn_load_cache(kh_sparse_attn* a, int64_t b, const flo
   KH_CHECK_ARG(b >= 0 && b < a->max_batch, "sequence %lld not in [0,%d)", (long long)b, a->max_batch);
   KH_CHECK_ARG(len >= 0 && len <= a->max_seq, "len %lld not in [0,%d]", (long long)len, a->max_seq);
   KH_CHECK_ARG(len == 0 || (k_host && v_host), "null cache data");
-  const size_t D = a->d, rows = (size_t)len;
-  const size_t seq_bytes = a->elt() * a->seq_elems();
-  for (int kv = 0; kv < 2; ++kv) {
+  const size_t D = a->d, rows = (size_t)len, n = (size_t)a->nkv * rows * D;
+  // BF16 storage only when it holds the rows exactly
+  bool bf16 = !a->kv_f32 && rows > 0;
+  for (size_t i = 0; bf16 && i < n; ++i) {
+    uint32_t uk, uv;
+    memcpy(&uk, k_host + i, 4);
+    memcpy(&uv, v_host + i, 4);
+    bf16 = ((uk | uv) & 0xffffu) == 0;
+  }
+  for (int kv = 0; kv < 2 && rows; ++kv) {
     const float* src = kv ? v_host : k_host;
-    char* base = static_cast<char*>(kv ? a->vc : a->kc) + (size_t)b * seq_bytes;
     for (int hh = 0; hh < a->nkv; ++hh) {
-      if (rows == 0) break;
-      const float* s = src + (size_t)hh * rows * D;
-      char* dst = base + (size_t)hh * a->max_seq * D * a->elt();
-      if (a->kv_f32) {
-        KH_HIP(hipMemcpy(dst, s, sizeof(float) * rows * D, hipMemcpyHostToDevice));
-      } else {
+      const float* sp = src + (size_t)hh * rows * D;
+      const size_t off = ((size_t)b * a->nkv + hh) * a->max_seq * D;
+      if (bf16) {
         std::vector<uint16_t> tmp(rows * D);
-        for (size_t i = 0; i < tmp.size(); ++i) tmp[i] = f32_to_bf16(s[i]);
-        KH_HIP(hipMemcpy(dst, tmp.data(), sizeof(uint16_t) * tmp.size(), hipMemcpyHostToDevice));
+        for (size_t i = 0; i < tmp.size(); ++i) tmp[i] = f32_to_bf16(sp[i]);
+        KH_HIP(hipMemcpy((kv ? a->vc16 : a->kc16) + off, tmp.data(), sizeof(uint16_t) * tmp.size(),
+                         hipMemcpyHostToDevice));
+      } else {
+        KH_HIP(hipMemcpy((kv ? a->vc32 : a->kc32) + off, sp, sizeof(float) * rows * D, hipMemcpyHostToDevice));
       }
     }
   }
-  const int32_t l32 = static_cast<int32_t>(len);
+  const int32_t l32 = static_cast<int32_t>(len), p32 = bf16 ? l32 : 0;
   KH_HIP(hipMemcpy(a->lens + b, &l32, sizeof(int32_t), hipMemcpyHostToDevice));
+  KH_HIP(hipMemcpy(a->pre + b, &p32, sizeof(int32_t), hipMemcpyHostToDevice));
   a->len_host[b] = len;
+  a->pre_host[b] = p32;
   return KH_OK;
 }
 
@@ -1043,25 +1107,21 @@ extern "C" int kh_sparse_attn_load_cache_dev(kh_sparse_attn* a, int64_t b, const
   hipStream_t st = as_stream(stream);
   const int64_t total = (int64_t)a->nkv * len * a->d;
   if (total > 0) {
+    // device rows are stored in f32 (exact whatever their values)
     const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
     const size_t off = (size_t)b * a->seq_elems();
-    if (a->kv_f32) {
-      hipLaunchKernelGGL(attn_fill_cache_kernel<float>, dim3(blocks), dim3(256), 0, st, k_dev, len,
-                         a->d, total, a->max_seq, static_cast<float*>(a->kc) + off);
-      hipLaunchKernelGGL(attn_fill_cache_kernel<float>, dim3(blocks), dim3(256), 0, st, v_dev, len,
-                         a->d, total, a->max_seq, static_cast<float*>(a->vc) + off);
-    } else {
-      hipLaunchKernelGGL(attn_fill_cache_kernel<uint16_t>, dim3(blocks), dim3(256), 0, st, k_dev,
-                         len, a->d, total, a->max_seq, static_cast<uint16_t*>(a->kc) + off);
-      hipLaunchKernelGGL(attn_fill_cache_kernel<uint16_t>, dim3(blocks), dim3(256), 0, st, v_dev,
-                         len, a->d, total, a->max_seq, static_cast<uint16_t*>(a->vc) + off);
-    }
+    hipLaunchKernelGGL(attn_fill_cache_kernel<float>, dim3(blocks), dim3(256), 0, st, k_dev, len, a->d,
+                       total, a->max_seq, a->kc32 + off);
+    hipLaunchKernelGGL(attn_fill_cache_kernel<float>, dim3(blocks), dim3(256), 0, st, v_dev, len, a->d,
+                       total, a->max_seq, a->vc32 + off);
     KH_LAUNCHED();
   }
   hipLaunchKernelGGL(attn_set_len_kernel, dim3(1), dim3(64), 0, st, a->lens + b, 1,
                      static_cast<int>(len));
+  hipLaunchKernelGGL(attn_set_len_kernel, dim3(1), dim3(64), 0, st, a->pre + b, 1, 0);
   KH_LAUNCHED();
   a->len_host[b] = len;
+  a->pre_host[b] = 0;
   return KH_OK;
 }
 
@@ -1072,23 +1132,26 @@ extern "C" int kh_sparse_attn_read_cache(const kh_sparse_attn* a, int64_t b, flo
   KH_CHECK_ARG(len >= 0 && len <= a->max_seq, "len %lld not in [0,%d]", (long long)len, a->max_seq);
   KH_CHECK_ARG(len == 0 || (k_host && v_host), "null output");
   const size_t D = a->d, rows = (size_t)len;
-  const size_t seq_bytes = a->elt() * a->seq_elems();
+  int32_t pre = 0;
+  KH_HIP(hipMemcpy(&pre, a->pre + b, sizeof(int32_t), hipMemcpyDeviceToHost));
+  const size_t r16 = std::min(rows, (size_t)pre);
   for (int kv = 0; kv < 2 && rows; ++kv) {
     float* dstf = kv ? v_host : k_host;
-    const char* base = static_cast<const char*>(kv ? a->vc : a->kc) + (size_t)b * seq_bytes;
     for (int hh = 0; hh < a->nkv; ++hh) {
-      const char* src = base + (size_t)hh * a->max_seq * D * a->elt();
+      const size_t off = ((size_t)b * a->nkv + hh) * a->max_seq * D;
       float* d = dstf + (size_t)hh * rows * D;
-      if (a->kv_f32) {
-        KH_HIP(hipMemcpy(d, src, sizeof(float) * rows * D, hipMemcpyDeviceToHost));
-      } else {
-        std::vector<uint16_t> tmp(rows * D);
-        KH_HIP(hipMemcpy(tmp.data(), src, sizeof(uint16_t) * tmp.size(), hipMemcpyDeviceToHost));
+      if (r16) {
+        std::vector<uint16_t> tmp(r16 * D);
+        KH_HIP(hipMemcpy(tmp.data(), (kv ? a->vc16 : a->kc16) + off, sizeof(uint16_t) * tmp.size(),
+                         hipMemcpyDeviceToHost));
         for (size_t i = 0; i < tmp.size(); ++i) {
           const uint32_t u = static_cast<uint32_t>(tmp[i]) << 16;
           memcpy(d + i, &u, 4);
         }
       }
+      if (rows > r16)
+        KH_HIP(hipMemcpy(d + r16 * D, (kv ? a->vc32 : a->kc32) + off + r16 * D, sizeof(float) * (rows - r16) * D,
+                         hipMemcpyDeviceToHost));
     }
   }
   return KH_OK;
@@ -1108,33 +1171,28 @@ extern "C" int kh_sparse_attn_clear(kh_sparse_attn* a, void* stream) {
   KH_CHECK_ARG(a != nullptr, "null handle");
   hipLaunchKernelGGL(attn_set_len_kernel, dim3(1), dim3(64), 0, as_stream(stream), a->lens,
                      a->max_batch, 0);
+  hipLaunchKernelGGL(attn_set_len_kernel, dim3(1), dim3(64), 0, as_stream(stream), a->pre,
+                     a->max_batch, 0);
   KH_LAUNCHED();
   std::fill(a->len_host.begin(), a->len_host.end(), 0);
+  std::fill(a->pre_host.begin(), a->pre_host.end(), 0);
   return KH_OK;
 }
 
-static int attn_chunk_of(int kv_f32, int D) {
-  if (kv_f32) return D == 64 ? attn_chunk<float, 64>() : D == 128 ? attn_chunk<float, 128>()
-                                                                   : attn_chunk<float, 256>();
-  return D == 64 ? attn_chunk<uint16_t, 64>() : D == 128 ? attn_chunk<uint16_t, 128>()
-                                                         : attn_chunk<uint16_t, 256>();
-}
-
-template <typename KV, int D>
+template <int D>
 static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
-                              const int32_t* heads, int nsel, int nsplit, float* po, float2* pml,
-                              bool merge, hipStream_t st) {
+                              const int32_t* heads, int nsel, int n16, int nsplit, float* po,
+                              float2* pml, bool merge, hipStream_t st) {
   const int qd = a->nh * D;
-  hipLaunchKernelGGL((attn_decode_kernel<KV, D>), dim3(nsplit, nsel + 1, batch),
-                     dim3(kAttnThreads), 0, st, static_cast<KV*>(a->kc), static_cast<KV*>(a->vc),
-                     a->y, a->ystride(), a->nkv, a->nh, heads, nsel, a->lens, pos, a->cos_t,
-                     a->sin_t, a->max_seq, 1.0f / sqrtf(static_cast<float>(D)), nsplit,
-                     a->qrows + qd + 1, po, pml, a->cat, qd);
+  hipLaunchKernelGGL(attn_decode_kernel<D>, dim3(nsplit, nsel + 1, batch), dim3(kAttnThreads), 0, st,
+                     a->kc16, a->vc16, a->kc32, a->vc32, a->pre, n16, a->y, a->ystride(), a->nkv, a->nh,
+                     heads, nsel, a->lens, pos, a->cos_t, a->sin_t, a->max_seq,
+                     1.0f / sqrtf(static_cast<float>(D)), nsplit, a->qrows + qd + 1, po, pml, a->cat, qd);
   KH_LAUNCHED();
   if (!merge) return KH_OK;
   hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(nsel, batch), dim3(D), 0, st, po, pml, nsplit,
-                     attn_chunk<KV, D>(), heads, nsel, a->nh, a->lens, a->max_seq,
-                     a->qrows + qd + 1, a->cat, qd);
+                     attn_chunk<uint16_t, D>(), attn_chunk<float, D>(), a->pre, heads, nsel, a->nh,
+                     a->lens, a->max_seq, a->qrows + qd + 1, a->cat, qd);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -1189,8 +1247,15 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   }
   // 2. split-K decode over the cache and the K/V append (then, for batch > 2 or head
   //    lists longer than kOprojMaxSel, the merge of each head's chunks)
-  const int chunk = attn_chunk_of(a->kv_f32, D);
-  const int nsplit = ceil_div(a->max_seq, chunk);
+  const int ch16 = D == 64 ? attn_chunk<uint16_t, 64>() : D == 128 ? attn_chunk<uint16_t, 128>()
+                                                                  : attn_chunk<uint16_t, 256>();
+  const int ch32 = D == 64 ? attn_chunk<float, 64>() : D == 128 ? attn_chunk<float, 128>()
+                                                               : attn_chunk<float, 256>();
+  // worst-case chunk counts (a captured graph replays these launches as the
+  // cache grows): BF16 chunks over a full-length prefix, f32 chunks over a
+  // full-length rest
+  const int n16 = a->kv_f32 ? 0 : ceil_div(a->max_seq, ch16);
+  const int nsplit = n16 + ceil_div(a->max_seq, ch32);
   const size_t slots = (size_t)batch * nsel * nsplit;
   float* po = static_cast<float*>(a->po.get(sizeof(float) * slots * D));
   float2* pml = static_cast<float2*>(a->pml.get(sizeof(float2) * slots));
@@ -1199,16 +1264,9 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   // separate merge, one block per (entry, token), is faster)
   constexpr int kFoldNB = NB <= 2 ? NB : 2;
   const bool fold = NB <= 2 && nsel <= kOprojMaxSel;
-  int rc;
-  if (a->kv_f32) {
-    rc = D == 64 ? attn_decode_launch<float, 64>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st)
-       : D == 128 ? attn_decode_launch<float, 128>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st)
-                  : attn_decode_launch<float, 256>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st);
-  } else {
-    rc = D == 64 ? attn_decode_launch<uint16_t, 64>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st)
-       : D == 128 ? attn_decode_launch<uint16_t, 128>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st)
-                  : attn_decode_launch<uint16_t, 256>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st);
-  }
+  int rc = D == 64 ? attn_decode_launch<64>(a, batch, pos, heads, nsel, n16, nsplit, po, pml, !fold, st)
+         : D == 128 ? attn_decode_launch<128>(a, batch, pos, heads, nsel, n16, nsplit, po, pml, !fold, st)
+                    : attn_decode_launch<256>(a, batch, pos, heads, nsel, n16, nsplit, po, pml, !fold, st);
   if (rc != KH_OK) return rc;
   // 3. o_proj over the union heads' rows of WoT, then the ordered reduce
   const int nslices = ceil_div(H, kSlice);
@@ -1221,8 +1279,8 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   if (!partial) return KH_ERR_ALLOC;
   if (fold)
     hipLaunchKernelGGL(attn_oproj_kernel<kFoldNB>, dim3(nslices, groups), dim3(kOprojThreads), 0,
-                       st, a->wot, H, D, a->qrows, qd, a->qrows + qd, po, pml, nsplit, chunk,
-                       heads, nsel, a->lens, a->max_seq, batch, groups, partial);
+                       st, a->wot, H, D, a->qrows, qd, a->qrows + qd, po, pml, nsplit, ch16, ch32,
+                       a->pre, heads, nsel, a->lens, a->max_seq, batch, groups, partial);
   else
     hipLaunchKernelGGL(gather_rows_kernel<NB>, dim3(nslices, groups), dim3(kDownThreads), 0, st,
                        a->wot, H, a->qrows, qd, a->qrows + qd, qd, a->cat, qd, batch, groups,
