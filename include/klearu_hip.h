@@ -163,6 +163,10 @@ int kh_lsh_index_remove_codes(kh_lsh_index* idx, const uint32_t* ids_dev,
 int kh_lsh_index_remove(kh_lsh_index* idx, const uint32_t* ids_dev, int64_t n, void* stream);
 /* LshIndexTrait::clear (lsh/index.rs:313-315). Mutates. */
 int kh_lsh_index_clear(kh_lsh_index* idx, void* stream);
+/* LshIndexTrait::rebuild (lsh/index.rs:302-307): clear, then insert ids_dev[i]
+ * with weights w_dev + i*ldw in order.  Mutates; synchronises. */
+int kh_lsh_index_rebuild(kh_lsh_index* idx, const uint32_t* ids_dev, const float* w_dev,
+                         int64_t n, int64_t ldw, void* stream);
 /* LshIndexTrait::query / query_with_counts (lsh/index.rs:282-284, :294-296)
  * for a batch of dense inputs.  Output is CSR: the unique ids of sample b are
  * ids_dev[off[b]..off[b+1]] in ascending order with counts_dev (number of
@@ -232,6 +236,89 @@ int kh_dense_layer_destroy(kh_dense_layer* l);
 int kh_dense_layer_forward_sparse(const kh_dense_layer* l, const int64_t* xoff_dev,
                                   const uint32_t* xidx_dev, const float* xval_dev, int64_t batch,
                                   float* y_dev, void* stream);
+
+/* ======================================================================== */
+/* SLIDE training: backward, optimizers, rebuild scheduling                 */
+/* (network/layer.rs:124-233, network/net.rs:81-230, optim/, lsh/maintenance.rs) */
+/* ======================================================================== */
+
+/* RebuildScheduler (lsh/maintenance.rs:20-98): host-side state.  The interval
+ * after the i-th rebuild is (usize)(base * exp(decay * i)) (f64 exp, truncated,
+ * saturating), at least 1; the step arithmetic wraps as Rust's release build. */
+typedef struct kh_rebuild_scheduler {
+  uint64_t base_interval;
+  double decay;
+  uint64_t rebuild_count;
+  uint64_t next_rebuild_step;
+  uint64_t current_step;
+} kh_rebuild_scheduler;
+/* RebuildScheduler::new (maintenance.rs:36-44). */
+void kh_rebuild_scheduler_init(kh_rebuild_scheduler* s, uint64_t base_interval, double decay);
+/* RebuildScheduler::step (:48-62): 1 when a rebuild is due at the new step. */
+int kh_rebuild_scheduler_step(kh_rebuild_scheduler* s);
+/* RebuildScheduler::should_rebuild (:70-81): jump to `step`, 1 when due. */
+int kh_rebuild_scheduler_should_rebuild(kh_rebuild_scheduler* s, uint64_t step);
+
+#define KH_OPT_SGD 0  /* optim/sgd.rs:3-69 (momentum 0 = vanilla) */
+#define KH_OPT_ADAM 1 /* optim/adam.rs:3-90 */
+
+/* Layer::rebuild_index (layer.rs:228-233): clear the layer's index and insert
+ * neurons 0..n-1 from the current weights.  Mutates; synchronises. */
+int kh_slide_layer_rebuild_index(kh_slide_layer* l, void* stream);
+/* Optimizer::create_state for every neuron (net.rs:40-55): zeroed SGD momentum
+ * (momentum > 0) or Adam moments.  Replaces any earlier state.  Synchronous. */
+int kh_slide_layer_init_optimizer(kh_slide_layer* l, int optimizer, float momentum, float beta1,
+                                  float beta2, float eps);
+/* Copy the current weights [n][dim] and biases [n] back.  Synchronous. */
+int kh_slide_layer_weights(const kh_slide_layer* l, float* w_host, float* bias_host);
+/* Layer::backward (layer.rs:124-226) for one sample.  The LayerOutput is given
+ * on the device: act_ids_dev[0..*n_act_dev) in the order the forward produced
+ * them (the sums over active neurons follow it), pre_dev in the same order,
+ * act_dense_dev[n] the layer's dense activations; x_dev[dim] the layer's
+ * input; grad_out_dev[grad_out_len] (entries past the length read as 0).
+ * Computes grad_in_dev[dim] (may be NULL when not needed) from the weights
+ * before the update, then updates every active neuron's weights and bias with
+ * the layer's optimizer (kh_slide_layer_init_optimizer) at learning rate
+ * (f32)lr and step `step`.  Mutates the layer. */
+int kh_slide_layer_backward(kh_slide_layer* l, const float* x_dev, const uint32_t* act_ids_dev,
+                            const int32_t* n_act_dev, const float* pre_dev,
+                            const float* act_dense_dev, const float* grad_out_dev,
+                            int64_t grad_out_len, double lr, uint64_t step, float* grad_in_dev,
+                            void* stream);
+
+typedef struct kh_slide_network kh_slide_network;
+/* Network (net.rs:10-58) over existing layers (not owned; they must outlive
+ * the network, and layer i+1's input_dim must equal layer i's num_neurons).
+ * Initialises every layer's optimizer state (momentum / beta1 / beta2 / eps as
+ * Sgd::new / Adam::new take them; the reference's NetworkConfig uses
+ * Sgd::new(0.9) and Adam::default() = 0.9, 0.999, 1e-8) and a
+ * RebuildScheduler(rebuild_base, rebuild_decay).  Inputs of the first layer
+ * are dense with input_dim <= 65536; hidden widths <= 65536. */
+int kh_slide_network_create(kh_slide_layer* const* layers, int n_layers, int optimizer,
+                            float momentum, float beta1, float beta2, float eps,
+                            uint64_t rebuild_base, double rebuild_decay, kh_slide_network** out);
+int kh_slide_network_destroy(kh_slide_network* n);
+/* Network::train_step (net.rs:81-120, backward :122-146) over examples x_dev[batch][input_dim]
+ * (Example::features.to_dense()) with labels labels_host[label_off_host[b] ..
+ * label_off_host[b+1]]: per example in order, forward (Layer::forward with the
+ * sampler's order: top-k sampling lists the active neurons by count
+ * descending, then id; the other samplers by ascending id, where the
+ * reference's HashMap order differs from run to run), compute_loss /
+ * compute_loss_gradient (net.rs:180-230) and the backward pass of every
+ * layer, updating weights as it goes; then step += 1 and, when the scheduler
+ * says so, every layer's index is rebuilt.  *loss_out = total / batch (0 for
+ * an empty batch, which changes nothing).  Mutates; synchronises. */
+int kh_slide_network_train_step(kh_slide_network* n, const float* x_dev, int64_t batch,
+                                const int64_t* label_off_host, const uint32_t* labels_host,
+                                double lr, float* loss_out, void* stream);
+/* Network::predict (net.rs:151-154) for each row of x_dev[batch][input_dim]:
+ * out_dev[batch][num_neurons of the last layer], the last layer's dense
+ * activations. */
+int kh_slide_network_predict(kh_slide_network* n, const float* x_dev, int64_t batch,
+                             float* out_dev, void* stream);
+/* Network::step (net.rs:13) and the scheduler's state. */
+int kh_slide_network_state(const kh_slide_network* n, uint64_t* step,
+                           kh_rebuild_scheduler* scheduler);
 
 /* ======================================================================== */
 /* Deja Vu predictor + top-k (crates/klearu-dejavu/src/predictor/,          */

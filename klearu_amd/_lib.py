@@ -88,6 +88,19 @@ SIGS = {
     "kh_slide_layer_destroy": (I, [P]),
     "kh_slide_layer_forward": (I, [P, P, I64, P, P, P, P, I64, P]),
     "kh_slide_layer_forward_sparse": (I, [P, P, P, P, I64, P, P, P, P, I64, P]),
+    "kh_lsh_index_rebuild": (I, [P, P, P, I64, I64, P]),
+    "kh_rebuild_scheduler_init": (None, [P, U64, C.c_double]),
+    "kh_rebuild_scheduler_step": (I, [P]),
+    "kh_rebuild_scheduler_should_rebuild": (I, [P, U64]),
+    "kh_slide_layer_rebuild_index": (I, [P, P]),
+    "kh_slide_layer_init_optimizer": (I, [P, I, F, F, F, F]),
+    "kh_slide_layer_weights": (I, [P, P, P]),
+    "kh_slide_layer_backward": (I, [P, P, P, P, P, P, P, I64, C.c_double, U64, P, P]),
+    "kh_slide_network_create": (I, [P, I, I, F, F, F, F, U64, C.c_double, PP]),
+    "kh_slide_network_destroy": (I, [P]),
+    "kh_slide_network_train_step": (I, [P, P, I64, P, P, C.c_double, P, P]),
+    "kh_slide_network_predict": (I, [P, P, I64, P, P]),
+    "kh_slide_network_state": (I, [P, P, P]),
     "kh_dense_layer_create": (I, [I, I, P, P, I, PP]),
     "kh_dense_layer_destroy": (I, [P]),
     "kh_dense_layer_forward_sparse": (I, [P, P, P, P, I64, P, P]),

@@ -19,18 +19,89 @@
 #include <vector>
 
 #include "gather.hpp"
-#include "lsh_internal.hpp"
+#include "slide_internal.hpp"
 
 namespace kh {
 
 constexpr int kSlideThreads = 256;
 constexpr int kMaxCountBins = 8193;
 
+// Top-k sampling in the sampler's own order (count descending, then id, as
+// TopKSampling::select sorts, sampling/topk.rs:19-34): a stable counting sort
+// of the ascending candidates.  hist[c] becomes the number of candidates with
+// a count above c; wave 0 then walks the candidates in id order and places
+// each after the earlier ones of its count.  Returns min(m, top_k), the
+// sampler's pick count; picks with ids >= num_neurons are dropped in order.
+__device__ int select_topk_count_order(const uint32_t* __restrict__ ids,
+                                       const uint32_t* __restrict__ cnt, int m, int top_k,
+                                       int num_neurons, int nbins, unsigned* hist, int* wsum,
+                                       int* s_total, uint32_t* __restrict__ out, int* n_kept) {
+  for (int i = threadIdx.x; i < nbins; i += blockDim.x) hist[i] = 0u;
+  __syncthreads();
+  for (int i = threadIdx.x; i < m; i += blockDim.x) atomicAdd(&hist[cnt[i]], 1u);
+  __syncthreads();
+  // exclusive suffix sums: thread t owns a run of bins, thread 0 the highest
+  const int seg = (nbins + (int)blockDim.x - 1) / (int)blockDim.x;
+  const int hi = nbins - 1 - (int)threadIdx.x * seg;
+  const int lo = max(hi - seg + 1, 0);
+  int run = 0;
+  for (int c = hi; c >= lo; --c) run += (int)hist[c];
+  int above = block_excl_scan(run, wsum, s_total);
+  for (int c = hi; c >= lo; --c) {
+    const int h = (int)hist[c];
+    hist[c] = (unsigned)above;
+    above += h;
+  }
+  __syncthreads();
+  const int take = min(m, top_k);
+  if ((threadIdx.x >> 6) == 0) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (int c0 = 0; c0 < m; c0 += 64) {
+      const int i = c0 + lane;
+      const int c = i < m ? (int)cnt[i] : -1;
+      uint64_t pend = __ballot(i < m);
+      while (pend) {
+        const int leader = __ffsll((unsigned long long)pend) - 1;
+        const int cl = __shfl(c, leader);
+        const uint64_t same = __ballot(c == cl);
+        const int base = (int)hist[cl];
+        if (c == cl) {
+          const int pos = base + __popcll(same & below);
+          if (pos < take) out[pos] = ids[i];
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane == leader) hist[cl] = (unsigned)(base + __popcll(same));
+        __builtin_amdgcn_wave_barrier();
+        pend &= ~same;
+      }
+    }
+  }
+  __syncthreads();
+  // drop ids >= num_neurons, keeping the order (layer.rs:87)
+  int base = 0;
+  for (int c0 = 0; c0 < take; c0 += blockDim.x) {
+    const int i = c0 + threadIdx.x;
+    const uint32_t id = i < take ? out[i] : 0u;
+    const int keep = i < take && id < (uint32_t)num_neurons;
+    const int pos = block_excl_scan(keep, wsum, s_total) + base;
+    if (keep) out[pos] = id;
+    base += *s_total;
+    __syncthreads();
+  }
+  *n_kept = base;
+  return take;
+}
+
+// clear_dense (training): the row's dense activation vector [num_neurons];
+// the entries of the previous active list (aids/alen still hold it) are
+// zeroed before the new list is written.  count_order: top-k picks in the
+// sampler's order instead of ascending ids.
 __global__ __launch_bounds__(kSlideThreads) void select_kernel(
     const uint32_t* __restrict__ qids, const uint32_t* __restrict__ qcnt,
     const int32_t* __restrict__ qlen, int qstride, int sampling, int top_k, int threshold,
     int num_neurons, int nbins, uint32_t* __restrict__ aids, int astride,
-    int32_t* __restrict__ alen) {
+    int32_t* __restrict__ alen, int count_order, float* __restrict__ clear_dense) {
   extern __shared__ unsigned hist[];
   __shared__ int wsum[kSlideThreads / 64];
   __shared__ int s_total;
@@ -40,8 +111,26 @@ __global__ __launch_bounds__(kSlideThreads) void select_kernel(
   const uint32_t* cnt = qcnt + row * (int64_t)qstride;
   uint32_t* out = aids + row * (int64_t)astride;
   const int m = qlen[row];
+  if (clear_dense) {
+    float* dn = clear_dense + row * (int64_t)num_neurons;
+    const int old = alen[row];
+    for (int a = threadIdx.x; a < old; a += blockDim.x) dn[out[a]] = 0.0f;
+    __syncthreads();
+  }
   int cstar = 0, take_eq = 0;  // topk: take count > cstar, plus take_eq of count == cstar
   int mode = sampling;
+  if (sampling == KH_SAMPLING_TOPK && count_order) {
+    int n_kept = 0;
+    const int n_pre = select_topk_count_order(ids, cnt, m, top_k, num_neurons, nbins, hist, wsum,
+                                              &s_total, out, &n_kept);
+    int n_sel = n_kept;
+    if (n_pre == 0) {
+      for (int i = threadIdx.x; i < num_neurons; i += blockDim.x) out[i] = (uint32_t)i;
+      n_sel = num_neurons;
+    }
+    if (threadIdx.x == 0) alen[row] = n_sel;
+    return;
+  }
   if (sampling == KH_SAMPLING_TOPK) {
     if (m <= top_k) {
       mode = KH_SAMPLING_VANILLA;
@@ -296,19 +385,24 @@ __global__ __launch_bounds__(256) void dense_sparse_kernel(const float* __restri
   y[row * (int64_t)n + o] = r;
 }
 
+int select_launch(const kh_slide_layer* l, const uint32_t* qids, const uint32_t* qcnt,
+                  const int32_t* qlen, int qs, int64_t batch, uint32_t* aids, int as, int32_t* alen,
+                  bool count_order, float* clear_dense, hipStream_t st) {
+  // A candidate's hit count is at most L * cap (every slot of its L buckets).
+  const int nbins = l->index->L * l->index->cap + 1;
+  KH_CHECK_ARG(l->sampling != KH_SAMPLING_TOPK || nbins <= kMaxCountBins,
+               "top-k sampling supports num_tables * bucket_capacity <= %d", kMaxCountBins - 1);
+  hipLaunchKernelGGL(select_kernel, dim3((unsigned)batch), dim3(kSlideThreads),
+                     l->sampling == KH_SAMPLING_TOPK ? sizeof(unsigned) * nbins : 0, st, qids, qcnt,
+                     qlen, qs, l->sampling, l->top_k, l->threshold, l->n, nbins, aids, as, alen,
+                     count_order ? 1 : 0, clear_dense);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
 }  // namespace kh
 
 using namespace kh;
-
-struct kh_slide_layer {
-  int dim = 0, n = 0;
-  float* w = nullptr;
-  float* wtn = nullptr;  // [dim][n]: transposed copy for the non-softmax neuron kernel
-  float* bias = nullptr;
-  kh_lsh_index* index = nullptr;
-  int sampling = 0, top_k = 0, threshold = 0, act = 0;
-  mutable StreamWs ws;  // forward scratch per stream
-};
 
 struct kh_dense_layer {
   int dim = 0, n = 0, act = 0;
@@ -382,6 +476,7 @@ extern "C" int kh_slide_layer_destroy(kh_slide_layer* l) {
   dev_free(l->w);
   dev_free(l->wtn);
   dev_free(l->bias);
+  l->free_opt();
   delete l;
   return KH_OK;
 }
@@ -410,14 +505,8 @@ static int slide_forward_common(const kh_slide_layer* lc, const float* x, const 
   if (rc != KH_OK) return rc;
   rc = query_launch(idx, codes, batch, qids, qcnt, qs, qlen, st);
   if (rc != KH_OK) return rc;
-  // A candidate's hit count is at most L * cap (every slot of its L buckets).
-  const int nbins = L * idx->cap + 1;
-  KH_CHECK_ARG(l->sampling != KH_SAMPLING_TOPK || nbins <= kMaxCountBins,
-               "top-k sampling supports num_tables * bucket_capacity <= %d", kMaxCountBins - 1);
-  hipLaunchKernelGGL(select_kernel, dim3((unsigned)batch), dim3(kSlideThreads),
-                     l->sampling == KH_SAMPLING_TOPK ? sizeof(unsigned) * nbins : 0, st, qids, qcnt, qlen, qs, l->sampling, l->top_k,
-                     l->threshold, l->n, nbins, aids, as, alen);
-  KH_LAUNCHED();
+  rc = select_launch(l, qids, qcnt, qlen, qs, batch, aids, as, alen, false, nullptr, st);
+  if (rc != KH_OK) return rc;
   const int max_nz = xoff ? 4096 : l->dim;
   KH_CHECK_ARG(xoff || l->dim <= 8192, "dense SLIDE input supports input_dim <= 8192");
   const size_t lds = (sizeof(uint32_t) + sizeof(float)) * max_nz;

@@ -1,0 +1,839 @@
+// slide_train.hip -- SLIDE training on the GPU (gfx950).
+//
+// Replaces Layer::backward and Layer::rebuild_index
+// (crates/klearu-core/src/network/layer.rs:124-233), Network::train_step /
+// predict with compute_loss / compute_loss_gradient (network/net.rs:81-230),
+// the SGD and Adam updates (optim/sgd.rs, optim/adam.rs), LshIndexTrait::rebuild
+// (lsh/index.rs:302-307) and RebuildScheduler (lsh/maintenance.rs:20-98).
+//
+// The reference trains one example at a time and updates the weights after
+// each one, so example e+1's forward pass reads the weights example e wrote:
+// the examples of a batch are a chain.  Each example is a short sequence of
+// kernels on one stream; the parallel work is inside an example (the
+// neurons of a layer, the dimensions of a gradient, the weights of an update).
+//
+// Every f32 operation is the reference's, in its order: sums over the active
+// list run sequentially in the list's order (the Jacobian and grad_input
+// sums keep one lane per output, each lane a chain), the softmax denominator
+// is the reference's sequential sum computed by exact_seq_sum, and no
+// multiply-add is contracted (the library builds with -ffp-contract=off).
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "exact_sum.hpp"
+#include "slide_internal.hpp"
+
+namespace kh {
+
+constexpr int kTrThreads = 256;
+constexpr int kTrMaxLabels = 1024;   // labels of one example
+constexpr int kTrLdsNz = 8192;       // staged input nonzeros (beyond: read from global)
+constexpr int kTrMaxDim = 65536;     // network input / hidden widths
+constexpr int kJTile = 2048;         // Jacobian: (s, go) pairs per LDS tile
+constexpr int kGTile = 1024;         // grad_input: (id, lg) pairs per LDS tile
+constexpr int kSmCH = 64, kSmM = 128;  // exact softmax sum: 8192 terms per pass
+
+struct OptArgs {
+  int kind;       // KH_OPT_SGD / KH_OPT_ADAM
+  float lr, momentum, b1, b2, eps, c1, c2;
+  float* st_w1;   // SGD momentum / Adam first moments [n][dim]
+  float* st_w2;   // Adam second moments [n][dim]
+  float* st_b1;   // [n]
+  float* st_b2;   // [n]
+};
+
+// f32::powi with a run-time exponent: the __powisf2 builtin of Rust's
+// compiler-builtins (src/float/pow.rs), square-and-multiply from the low bit.
+static float powi_f32(float a, int32_t b) {
+  const bool recip = b < 0;
+  uint32_t p = recip ? 0u - static_cast<uint32_t>(b) : static_cast<uint32_t>(b);
+  float mul = 1.0f;
+  for (;;) {
+    if (p & 1u) mul = mul * a;
+    p >>= 1;
+    if (p == 0) break;
+    a = a * a;
+  }
+  return recip ? 1.0f / mul : mul;
+}
+
+static OptArgs opt_args(const kh_slide_layer* l, double lr, uint64_t step) {
+  OptArgs o{};
+  o.kind = l->opt;
+  o.lr = static_cast<float>(lr);
+  o.momentum = l->momentum;
+  o.b1 = l->beta1;
+  o.b2 = l->beta2;
+  o.eps = l->eps;
+  // Adam::update (adam.rs:38-47): step.max(1), `step as i32`
+  const uint64_t s = step < 1 ? 1 : step;
+  const int32_t si = static_cast<int32_t>(static_cast<uint32_t>(s));
+  o.c1 = 1.0f - powi_f32(l->beta1, si);
+  o.c2 = 1.0f - powi_f32(l->beta2, si);
+  o.st_w1 = l->st_w1;
+  o.st_w2 = l->st_w2;
+  o.st_b1 = l->st_b1;
+  o.st_b2 = l->st_b2;
+  return o;
+}
+
+// activation_derivative (layer.rs:266-283)
+__device__ __forceinline__ float act_deriv(float pre, float post, int act) {
+  if (act == KH_ACT_RELU) return pre > 0.0f ? 1.0f : 0.0f;
+  if (act == KH_ACT_SIGMOID) return post * (1.0f - post);
+  if (act == KH_ACT_TANH) return 1.0f - post * post;
+  return 1.0f;
+}
+
+// apply_activation (layer.rs:250-261)
+__device__ __forceinline__ float act_apply(float z, int act) {
+  if (act == KH_ACT_RELU) return fmaxf(z, 0.0f);
+  if (act == KH_ACT_SIGMOID) return sigmoid_ref(z);
+  if (act == KH_ACT_TANH) return tanhf(z);
+  return z;
+}
+
+// One optimizer step of a parameter (Sgd::update, sgd.rs:28-56; Adam::update,
+// adam.rs:50-76); s1/s2 its state slots.
+__device__ __forceinline__ float opt_step(float w, float g, float* s1, float* s2, const OptArgs& o) {
+  if (o.kind == KH_OPT_ADAM) {
+    const float m = o.b1 * *s1 + (1.0f - o.b1) * g;
+    const float gg = (1.0f - o.b2) * g;
+    const float v = o.b2 * *s2 + gg * g;
+    *s1 = m;
+    *s2 = v;
+    const float mh = m / o.c1;
+    const float vh = v / o.c2;
+    return w - (o.lr * mh) / (sqrtf(vh) + o.eps);
+  }
+  if (o.momentum > 0.0f) {
+    const float v = o.momentum * *s1 - o.lr * g;
+    *s1 = v;
+    return w + v;
+  }
+  return w - o.lr * g;
+}
+
+// Nonzeros of a dense vector in ascending order, as a one-row CSR (xoff[0..1]).
+// Dropping zero terms leaves every sequential sum over the vector unchanged
+// (x + 0 == x; a zero partial sum only changes the sign of zero), so hashes
+// and neuron sums over the list equal the reference's dense loops.
+__global__ __launch_bounds__(1024) void tr_stage_nz_kernel(const float* __restrict__ x, int dim,
+                                                           uint32_t* __restrict__ nzi,
+                                                           float* __restrict__ nzv,
+                                                           int64_t* __restrict__ xoff) {
+  __shared__ int wsum[16];
+  __shared__ int s_total;
+  int base = 0;
+  for (int c0 = 0; c0 < dim; c0 += blockDim.x) {
+    const int d = c0 + threadIdx.x;
+    const float v = d < dim ? x[d] : 0.0f;
+    const int nz = v != 0.0f ? 1 : 0;
+    const int pos = block_excl_scan(nz, wsum, &s_total) + base;
+    if (nz) {
+      nzi[pos] = static_cast<uint32_t>(d);
+      nzv[pos] = v;
+    }
+    base += s_total;
+  }
+  if (threadIdx.x == 0) {
+    xoff[0] = 0;
+    xoff[1] = base;
+  }
+}
+
+// Neuron::forward (neuron.rs:47-62) for one sample's active list: the
+// sequential sum of w*x over the staged nonzeros, + bias; then the
+// activation (not softmax) into post and the dense activation vector.
+__global__ __launch_bounds__(kTrThreads) void tr_neuron_kernel(
+    const float* __restrict__ W, const float* __restrict__ bias, int dim,
+    const uint32_t* __restrict__ nzi, const float* __restrict__ nzv,
+    const int64_t* __restrict__ xoff, const uint32_t* __restrict__ aids,
+    const int32_t* __restrict__ alen, int cap, int act, float* __restrict__ pre,
+    float* __restrict__ post, float* __restrict__ dense) {
+  extern __shared__ unsigned char smem[];
+  const int nnz = static_cast<int>(xoff[1]);
+  const uint32_t* li = nzi;
+  const float* lv = nzv;
+  if (nnz <= kTrLdsNz) {
+    uint32_t* si = reinterpret_cast<uint32_t*>(smem);
+    float* sv = reinterpret_cast<float*>(smem + sizeof(uint32_t) * kTrLdsNz);
+    for (int i = threadIdx.x; i < nnz; i += blockDim.x) {
+      si[i] = nzi[i];
+      sv[i] = nzv[i];
+    }
+    __syncthreads();
+    li = si;
+    lv = sv;
+  }
+  const int n = min(alen[0], cap);
+  for (int a = blockIdx.x * blockDim.x + threadIdx.x; a < n; a += gridDim.x * blockDim.x) {
+    const uint32_t id = aids[a];
+    const float* w = W + static_cast<size_t>(id) * dim;
+    float s = -0.0f;
+    int e = 0;
+    for (; e + 8 <= nnz; e += 8) {  // eight loads in flight, added in order
+      float wv[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) wv[q] = w[li[e + q]];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) s = s + wv[q] * lv[e + q];
+    }
+    for (; e < nnz; ++e) s = s + w[li[e]] * lv[e];
+    const float z = s + bias[id];
+    pre[a] = z;
+    if (act != KH_ACT_SOFTMAX) {
+      const float r = act_apply(z, act);
+      post[a] = r;
+      if (dense) dense[id] = r;
+    }
+  }
+}
+
+// apply_softmax (layer.rs:286-308) over the active list in its order: max,
+// exp(z - max) with glibc's expf, the sequential sum (exact_seq_sum, 8192
+// terms a pass), then e / sum (or 1/n when the sum is not positive).
+__global__ __launch_bounds__(kTrThreads) void tr_softmax_kernel(const float* __restrict__ pre,
+                                                                const uint32_t* __restrict__ aids,
+                                                                const int32_t* __restrict__ alen,
+                                                                int cap, float* __restrict__ post,
+                                                                float* __restrict__ dense) {
+  __shared__ EsLds<kSmCH, kSmM> es;
+  __shared__ float red[kTrThreads / 64];
+  const int n = min(alen[0], cap);
+  if (n <= 0) return;
+  float mx = -INFINITY;
+  for (int a = threadIdx.x; a < n; a += blockDim.x) mx = fmaxf(mx, pre[a]);
+  mx = wave_max(mx);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int i = 1; i < kTrThreads / 64; ++i) mx = fmaxf(mx, red[i]);
+  for (int a = threadIdx.x; a < n; a += blockDim.x) post[a] = expf_glibc(pre[a] - mx);
+  __syncthreads();
+  constexpr int kPass = kSmCH * kSmM;
+  float s = -0.0f;
+  for (int c0 = 0; c0 < n; c0 += kPass) {
+    const int cnt = min(kPass, n - c0);
+    for (int i = threadIdx.x; i < kPass; i += blockDim.x)
+      es.TP[es_slot<kSmCH, kSmM>(i)] = i < cnt ? post[c0 + i] : -0.0f;
+    __syncthreads();
+    s = exact_seq_sum<kTrThreads / 64, kSmCH, kSmM>(cnt, s, es);
+  }
+  const float u = 1.0f / static_cast<float>(n);
+  for (int a = threadIdx.x; a < n; a += blockDim.x) {
+    const float r = s > 0.0f ? post[a] / s : u;
+    post[a] = r;
+    if (dense) dense[aids[a]] = r;
+  }
+}
+
+// compute_loss and compute_loss_gradient (net.rs:180-230) of one example at
+// the last layer's active entries: go[a] = activations[id] minus 1/|labels|
+// per occurrence of id among the labels (all zero without labels); lg[a] =
+// go * activation_derivative unless the layer is softmax (the Jacobian kernel
+// follows).  One thread adds the example's loss to *loss_total, so the total
+// is the reference's sequential f32 sum over the batch.
+__global__ __launch_bounds__(kTrThreads) void tr_loss_grad_kernel(
+    const float* __restrict__ pre, const float* __restrict__ post,
+    const uint32_t* __restrict__ aids, const int32_t* __restrict__ alen, int cap, int act,
+    const float* __restrict__ dense, const uint32_t* __restrict__ labels, int nl,
+    float* __restrict__ go, float* __restrict__ lg, float* __restrict__ loss_total) {
+  __shared__ int found[kTrMaxLabels];
+  const int n = min(alen[0], cap);
+  for (int l = threadIdx.x; l < nl; l += blockDim.x) found[l] = 0;
+  __syncthreads();
+  const float w = nl > 0 ? 1.0f / static_cast<float>(nl) : 0.0f;
+  for (int a = threadIdx.x; a < n; a += blockDim.x) {
+    const uint32_t id = aids[a];
+    float g = nl > 0 ? post[a] : 0.0f;
+    for (int l = 0; l < nl; ++l)
+      if (labels[l] == id) {
+        g = g - w;
+        found[l] = 1;
+      }
+    go[a] = g;
+    if (act != KH_ACT_SOFTMAX) lg[a] = g * act_deriv(pre[a], post[a], act);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float loss = 0.0f;
+    if (nl > 0) {
+      const float eps = 1e-7f;
+      for (int l = 0; l < nl; ++l) {
+        const float prob = found[l] ? fmaxf(dense[labels[l]], eps) : eps;
+        loss = loss - logf(prob);
+      }
+      loss = loss / static_cast<float>(nl);
+    }
+    *loss_total = *loss_total + loss;
+  }
+}
+
+// The softmax branch of Layer::backward (layer.rs:141-175): lane i runs the
+// sequential sum over j of go_j*s_j*(1-s_j) (j == i) or go_j*(-s_i*s_j).
+__global__ __launch_bounds__(kTrThreads) void tr_softmax_jacobian_kernel(
+    const float* __restrict__ s, const float* __restrict__ go, const int32_t* __restrict__ alen,
+    int cap, float* __restrict__ lg) {
+  __shared__ float ts[kJTile], tg[kJTile];
+  const int n = min(alen[0], cap);
+  if (static_cast<int>(blockIdx.x * blockDim.x) >= n) return;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const float nsi = i < n ? -s[i] : 0.0f;
+  float r = 0.0f;
+  for (int j0 = 0; j0 < n; j0 += kJTile) {
+    const int cnt = min(kJTile, n - j0);
+    __syncthreads();
+    for (int j = threadIdx.x; j < cnt; j += blockDim.x) {
+      ts[j] = s[j0 + j];
+      tg[j] = go[j0 + j];
+    }
+    __syncthreads();
+    const int diag = i - j0;
+    for (int j = 0; j < cnt; ++j) {
+      const float sj = ts[j], gj = tg[j];
+      float t;
+      if (j == diag) {
+        t = gj * sj;
+        t = t * (1.0f - sj);
+      } else {
+        t = gj * (nsi * sj);
+      }
+      r = r + t;
+    }
+  }
+  if (i < n) lg[i] = r;
+}
+
+// Local gradients of a layer from the gradient w.r.t. its output: go = the
+// entry at the neuron's id (0 past the length); non-softmax layers get
+// lg = go * activation_derivative(pre, activations[id]); softmax layers keep
+// go for the Jacobian.
+__global__ __launch_bounds__(kTrThreads) void tr_local_grad_kernel(
+    const uint32_t* __restrict__ aids, const int32_t* __restrict__ alen, int cap,
+    const float* __restrict__ pre, const float* __restrict__ dense, int act,
+    const float* __restrict__ grad_out, int64_t grad_len, float* __restrict__ go,
+    float* __restrict__ lg) {
+  const int n = min(alen[0], cap);
+  const int a = blockIdx.x * blockDim.x + threadIdx.x;
+  if (a >= n) return;
+  const uint32_t id = aids[a];
+  const float g = static_cast<int64_t>(id) < grad_len ? grad_out[id] : 0.0f;
+  if (act == KH_ACT_SOFTMAX)
+    go[a] = g;
+  else
+    lg[a] = g * act_deriv(pre[a], dense[id], act);
+}
+
+// grad_input[j] = sum over the active list (in order, from +0.0) of
+// lg[a] * w[id_a][j], with the weights before this example's update
+// (layer.rs:203-207).  One lane per input dimension; each lane's sum is a chain.
+__global__ __launch_bounds__(kTrThreads) void tr_grad_input_kernel(
+    const float* __restrict__ W, int dim, const uint32_t* __restrict__ aids,
+    const int32_t* __restrict__ alen, int cap, const float* __restrict__ lg,
+    float* __restrict__ gi) {
+  __shared__ uint32_t tid_[kGTile];
+  __shared__ float tlg[kGTile];
+  const int n = min(alen[0], cap);
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  float r = 0.0f;
+  for (int a0 = 0; a0 < n; a0 += kGTile) {
+    const int cnt = min(kGTile, n - a0);
+    __syncthreads();
+    for (int a = threadIdx.x; a < cnt; a += blockDim.x) {
+      tid_[a] = aids[a0 + a];
+      tlg[a] = lg[a0 + a];
+    }
+    __syncthreads();
+    if (j < dim) {
+      int a = 0;
+      for (; a + 8 <= cnt; a += 8) {
+        float wv[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) wv[q] = W[static_cast<size_t>(tid_[a + q]) * dim + j];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) r = r + tlg[a + q] * wv[q];
+      }
+      for (; a < cnt; ++a) r = r + tlg[a] * W[static_cast<size_t>(tid_[a]) * dim + j];
+    }
+  }
+  if (j < dim) gi[j] = r;
+}
+
+// Optimizer::update of every active neuron (layer.rs:209-222): grad_weights[j]
+// = lg * x[j] over all dim inputs (zeros included: momentum and Adam state
+// move every step), grad_bias = lg.  The transposed copy follows the rows.
+__global__ __launch_bounds__(kTrThreads) void tr_update_kernel(
+    float* __restrict__ W, float* __restrict__ WTN, float* __restrict__ bias, int n, int dim,
+    const uint32_t* __restrict__ aids, const int32_t* __restrict__ alen, int cap,
+    const float* __restrict__ lg, const float* __restrict__ x, OptArgs o) {
+  const int na = min(alen[0], cap);
+  for (int a = blockIdx.x; a < na; a += gridDim.x) {
+    const uint32_t id = aids[a];
+    if (id >= static_cast<uint32_t>(n)) continue;
+    const float g = lg[a];
+    const size_t row = static_cast<size_t>(id) * dim;
+    float* w = W + row;
+    for (int j = threadIdx.x; j < dim; j += blockDim.x) {
+      const float gw = g * x[j];
+      float* s1 = o.st_w1 ? o.st_w1 + row + j : nullptr;
+      float* s2 = o.st_w2 ? o.st_w2 + row + j : nullptr;
+      const float nw = opt_step(w[j], gw, s1, s2, o);
+      w[j] = nw;
+      if (WTN) WTN[static_cast<size_t>(j) * n + id] = nw;
+    }
+    if (threadIdx.x == 0) {
+      float* s1 = o.st_b1 ? o.st_b1 + id : nullptr;
+      float* s2 = o.st_b2 ? o.st_b2 + id : nullptr;
+      bias[id] = opt_step(bias[id], g, s1, s2, o);
+    }
+  }
+}
+
+// Local gradients -> (grad_input) -> update of one layer for one example.
+// x: the layer's dense input; post: activations in list order (softmax only).
+static int layer_backward_launch(kh_slide_layer* l, const float* x, const uint32_t* aids,
+                                 const int32_t* alen, int cap, const float* pre,
+                                 const float* post, const float* dense, const float* grad_out,
+                                 int64_t grad_len, bool lg_ready, float* go, float* lg,
+                                 const OptArgs& o, float* gi, hipStream_t st) {
+  const unsigned ab = static_cast<unsigned>(ceil_div(cap, kTrThreads));
+  if (!lg_ready) {
+    hipLaunchKernelGGL(tr_local_grad_kernel, dim3(ab), dim3(kTrThreads), 0, st, aids, alen, cap,
+                       pre, dense, l->act, grad_out, grad_len, go, lg);
+    KH_LAUNCHED();
+  }
+  if (l->act == KH_ACT_SOFTMAX) {
+    hipLaunchKernelGGL(tr_softmax_jacobian_kernel, dim3(ab), dim3(kTrThreads), 0, st, post, go,
+                       alen, cap, lg);
+    KH_LAUNCHED();
+  }
+  if (gi) {
+    hipLaunchKernelGGL(tr_grad_input_kernel, dim3(ceil_div(l->dim, kTrThreads)), dim3(kTrThreads),
+                       0, st, l->w, l->dim, aids, alen, cap, lg, gi);
+    KH_LAUNCHED();
+  }
+  hipLaunchKernelGGL(tr_update_kernel, dim3(std::min(cap, 1024)), dim3(kTrThreads), 0, st, l->w,
+                     l->wtn, l->bias, l->n, l->dim, aids, alen, cap, lg, x, o);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
+}  // namespace kh
+
+using namespace kh;
+
+// ======================================================================== scheduler
+static uint64_t sched_interval(const kh_rebuild_scheduler* s) {
+  // (base as f64 * (decay * count as f64).exp()) as usize, then .max(1)
+  const double v = static_cast<double>(s->base_interval) *
+                   std::exp(s->decay * static_cast<double>(s->rebuild_count));
+  uint64_t n;
+  if (!(v > 0.0)) n = 0;                              // NaN and <= 0 saturate to 0
+  else if (v >= 18446744073709551616.0) n = UINT64_MAX;
+  else n = static_cast<uint64_t>(v);
+  return n < 1 ? 1 : n;
+}
+
+static int sched_due(kh_rebuild_scheduler* s) {
+  if (s->current_step >= s->next_rebuild_step) {
+    s->rebuild_count += 1;
+    s->next_rebuild_step = s->current_step + sched_interval(s);  // wraps as a release build
+    return 1;
+  }
+  return 0;
+}
+
+extern "C" void kh_rebuild_scheduler_init(kh_rebuild_scheduler* s, uint64_t base_interval,
+                                          double decay) {
+  if (!s) return;
+  s->base_interval = base_interval;
+  s->decay = decay;
+  s->rebuild_count = 0;
+  s->next_rebuild_step = base_interval;
+  s->current_step = 0;
+}
+
+extern "C" int kh_rebuild_scheduler_step(kh_rebuild_scheduler* s) {
+  if (!s) return 0;
+  s->current_step += 1;
+  return sched_due(s);
+}
+
+extern "C" int kh_rebuild_scheduler_should_rebuild(kh_rebuild_scheduler* s, uint64_t step) {
+  if (!s) return 0;
+  s->current_step = step;
+  return sched_due(s);
+}
+
+// ======================================================================== index / layer
+extern "C" int kh_lsh_index_rebuild(kh_lsh_index* idx, const uint32_t* ids_dev, const float* w_dev,
+                                    int64_t n, int64_t ldw, void* stream) {
+  KH_CHECK_ARG(idx != nullptr, "null index");
+  KH_CHECK_ARG(n >= 0 && ldw >= idx->h->dim, "bad n/ldw");
+  int rc = kh_lsh_index_clear(idx, stream);
+  if (rc != KH_OK || n == 0) return rc;
+  return kh_lsh_index_insert(idx, ids_dev, w_dev, n, ldw, stream);
+}
+
+extern "C" int kh_slide_layer_rebuild_index(kh_slide_layer* l, void* stream) {
+  KH_CHECK_ARG(l != nullptr, "null layer");
+  uint32_t* ids = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * l->n));
+  if (!ids) return KH_ERR_ALLOC;
+  std::vector<uint32_t> h(l->n);
+  for (int i = 0; i < l->n; ++i) h[i] = static_cast<uint32_t>(i);
+  hipStream_t st = as_stream(stream);
+  int rc = KH_OK;
+  if (hipMemcpyAsync(ids, h.data(), sizeof(uint32_t) * l->n, hipMemcpyHostToDevice, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess) {
+    set_error("rebuild upload failed");
+    rc = KH_ERR_HIP;
+  }
+  if (rc == KH_OK) rc = kh_lsh_index_rebuild(l->index, ids, l->w, l->n, l->dim, stream);
+  if (rc == KH_OK && hipStreamSynchronize(st) != hipSuccess) {
+    set_error("rebuild failed");
+    rc = KH_ERR_HIP;
+  }
+  dev_free(ids);
+  return rc;
+}
+
+extern "C" int kh_slide_layer_init_optimizer(kh_slide_layer* l, int optimizer, float momentum,
+                                             float beta1, float beta2, float eps) {
+  KH_CHECK_ARG(l != nullptr, "null layer");
+  KH_CHECK_ARG(optimizer == KH_OPT_SGD || optimizer == KH_OPT_ADAM, "bad optimizer %d", optimizer);
+  l->free_opt();
+  const size_t nw = static_cast<size_t>(l->n) * l->dim;
+  const bool two = optimizer == KH_OPT_ADAM;
+  const bool one = two || momentum > 0.0f;
+  if (one) {
+    l->st_w1 = static_cast<float*>(dev_alloc(sizeof(float) * nw));
+    l->st_b1 = static_cast<float*>(dev_alloc(sizeof(float) * l->n));
+    if (!l->st_w1 || !l->st_b1) {
+      l->free_opt();
+      return KH_ERR_ALLOC;
+    }
+  }
+  if (two) {
+    l->st_w2 = static_cast<float*>(dev_alloc(sizeof(float) * nw));
+    l->st_b2 = static_cast<float*>(dev_alloc(sizeof(float) * l->n));
+    if (!l->st_w2 || !l->st_b2) {
+      l->free_opt();
+      return KH_ERR_ALLOC;
+    }
+  }
+  float* bufs[4] = {l->st_w1, l->st_w2, l->st_b1, l->st_b2};
+  const size_t cnt[4] = {nw, nw, (size_t)l->n, (size_t)l->n};
+  for (int i = 0; i < 4; ++i)
+    if (bufs[i] && hipMemset(bufs[i], 0, sizeof(float) * cnt[i]) != hipSuccess) {
+      l->free_opt();
+      set_error("optimizer state clear failed");
+      return KH_ERR_HIP;
+    }
+  l->opt = optimizer;
+  l->momentum = momentum;
+  l->beta1 = beta1;
+  l->beta2 = beta2;
+  l->eps = eps;
+  return KH_OK;
+}
+
+extern "C" int kh_slide_layer_weights(const kh_slide_layer* l, float* w_host, float* bias_host) {
+  KH_CHECK_ARG(l != nullptr, "null layer");
+  if (w_host)
+    KH_HIP(hipMemcpy(w_host, l->w, sizeof(float) * l->n * (size_t)l->dim, hipMemcpyDeviceToHost));
+  if (bias_host) KH_HIP(hipMemcpy(bias_host, l->bias, sizeof(float) * l->n, hipMemcpyDeviceToHost));
+  return KH_OK;
+}
+
+extern "C" int kh_slide_layer_backward(kh_slide_layer* l, const float* x_dev,
+                                       const uint32_t* act_ids_dev, const int32_t* n_act_dev,
+                                       const float* pre_dev, const float* act_dense_dev,
+                                       const float* grad_out_dev, int64_t grad_out_len, double lr,
+                                       uint64_t step, float* grad_in_dev, void* stream) {
+  KH_CHECK_ARG(l != nullptr, "null layer");
+  KH_CHECK_ARG(l->opt >= 0, "kh_slide_layer_init_optimizer was not called");
+  KH_CHECK_ARG(x_dev && act_ids_dev && n_act_dev && pre_dev && act_dense_dev, "null argument");
+  KH_CHECK_ARG(grad_out_len >= 0 && (grad_out_len == 0 || grad_out_dev), "bad grad_out");
+  hipStream_t st = as_stream(stream);
+  // An active list holds distinct neuron ids, so at most n entries.
+  const int cap = l->n;
+  WsSet* w = l->ws.get(st);
+  float* go = static_cast<float*>(w->get(0, sizeof(float) * cap));
+  float* lg = static_cast<float*>(w->get(1, sizeof(float) * cap));
+  float* post = static_cast<float*>(w->get(2, sizeof(float) * cap));
+  if (!go || !lg || !post) return KH_ERR_ALLOC;
+  if (l->act == KH_ACT_SOFTMAX) {
+    // Layer::backward recomputes apply_softmax(pre_activations) (layer.rs:147)
+    hipLaunchKernelGGL(tr_softmax_kernel, dim3(1), dim3(kTrThreads), 0, st, pre_dev, act_ids_dev,
+                       n_act_dev, cap, post, nullptr);
+    KH_LAUNCHED();
+  }
+  return layer_backward_launch(l, x_dev, act_ids_dev, n_act_dev, cap, pre_dev, post,
+                               act_dense_dev, grad_out_dev, grad_out_len, false, go, lg,
+                               opt_args(l, lr, step), grad_in_dev, st);
+}
+
+// ======================================================================== network
+namespace {
+
+struct TrainBufs {
+  int qs = 0, as = 0;
+  uint32_t* codes = nullptr;
+  uint32_t* qids = nullptr;
+  uint32_t* qcnt = nullptr;
+  int32_t* qlen = nullptr;
+  uint32_t* aids = nullptr;
+  int32_t* alen = nullptr;
+  float* pre = nullptr;
+  float* post = nullptr;
+  float* dense = nullptr;  // [n] the layer's activations (Layer::forward's `activations`)
+  float* go = nullptr;
+  float* lg = nullptr;
+  float* gi = nullptr;     // [dim] gradient w.r.t. the layer's input
+  uint32_t* nzi = nullptr;
+  float* nzv = nullptr;
+  int64_t* xoff = nullptr;
+};
+
+}  // namespace
+
+struct kh_slide_network {
+  std::vector<kh_slide_layer*> layers;
+  std::vector<TrainBufs> b;
+  std::vector<void*> allocs;
+  uint64_t step = 0;
+  kh_rebuild_scheduler sched{};
+  float* loss_total = nullptr;
+  uint32_t* labels = nullptr;
+  size_t labels_cap = 0;
+  int in_dim = 0, out_dim = 0;
+  template <typename T>
+  T* alloc(size_t n, bool zero = false) {
+    void* p = dev_alloc(sizeof(T) * (n ? n : 1));
+    if (!p) return nullptr;
+    allocs.push_back(p);
+    if (zero && hipMemset(p, 0, sizeof(T) * (n ? n : 1)) != hipSuccess) return nullptr;
+    return static_cast<T*>(p);
+  }
+};
+
+extern "C" int kh_slide_network_destroy(kh_slide_network* n) {
+  if (!n) return KH_OK;
+  for (void* p : n->allocs) dev_free(p);
+  dev_free(n->labels);
+  delete n;
+  return KH_OK;
+}
+
+extern "C" int kh_slide_network_create(kh_slide_layer* const* layers, int n_layers, int optimizer,
+                                       float momentum, float beta1, float beta2, float eps,
+                                       uint64_t rebuild_base, double rebuild_decay,
+                                       kh_slide_network** out) {
+  KH_CHECK_ARG(out && layers && n_layers > 0, "null argument / no layers");
+  *out = nullptr;
+  for (int i = 0; i < n_layers; ++i) {
+    KH_CHECK_ARG(layers[i] != nullptr, "null layer %d", i);
+    KH_CHECK_ARG(layers[i]->dim <= kTrMaxDim, "layer %d input_dim %d > %d", i, layers[i]->dim,
+                 kTrMaxDim);
+    KH_CHECK_ARG(i == 0 || layers[i]->dim == layers[i - 1]->n,
+                 "layer %d input_dim %d != layer %d num_neurons %d", i, layers[i]->dim, i - 1,
+                 layers[i - 1]->n);
+    const kh_lsh_index* idx = layers[i]->index;
+    KH_CHECK_ARG(layers[i]->sampling != KH_SAMPLING_TOPK || idx->L * idx->cap + 1 <= 8193,
+                 "top-k sampling supports num_tables * bucket_capacity <= 8192");
+  }
+  auto* net = new kh_slide_network();
+  net->layers.assign(layers, layers + n_layers);
+  net->in_dim = layers[0]->dim;
+  net->out_dim = layers[n_layers - 1]->n;
+  kh_rebuild_scheduler_init(&net->sched, rebuild_base, rebuild_decay);
+  int rc = KH_OK;
+  for (int i = 0; i < n_layers && rc == KH_OK; ++i)
+    rc = kh_slide_layer_init_optimizer(layers[i], optimizer, momentum, beta1, beta2, eps);
+  net->b.resize(n_layers);
+  for (int i = 0; i < n_layers && rc == KH_OK; ++i) {
+    const kh_slide_layer* l = layers[i];
+    TrainBufs& t = net->b[i];
+    t.qs = l->index->L * l->index->cap;
+    t.as = std::max(t.qs, l->n);
+    t.codes = net->alloc<uint32_t>(l->index->L);
+    t.qids = net->alloc<uint32_t>(t.qs);
+    t.qcnt = net->alloc<uint32_t>(t.qs);
+    t.qlen = net->alloc<int32_t>(1, true);
+    t.aids = net->alloc<uint32_t>(t.as, true);
+    t.alen = net->alloc<int32_t>(1, true);
+    t.pre = net->alloc<float>(t.as);
+    t.post = net->alloc<float>(t.as);
+    t.dense = net->alloc<float>(l->n, true);
+    t.go = net->alloc<float>(t.as);
+    t.lg = net->alloc<float>(t.as);
+    t.gi = net->alloc<float>(l->dim);
+    t.nzi = net->alloc<uint32_t>(l->dim);
+    t.nzv = net->alloc<float>(l->dim);
+    t.xoff = net->alloc<int64_t>(2, true);
+    if (!t.codes || !t.qids || !t.qcnt || !t.qlen || !t.aids || !t.alen || !t.pre || !t.post ||
+        !t.dense || !t.go || !t.lg || !t.gi || !t.nzi || !t.nzv || !t.xoff)
+      rc = KH_ERR_ALLOC;
+  }
+  if (rc == KH_OK) {
+    net->loss_total = net->alloc<float>(1, true);
+    if (!net->loss_total) rc = KH_ERR_ALLOC;
+  }
+  if (rc != KH_OK) {
+    kh_slide_network_destroy(net);
+    return rc;
+  }
+  *out = net;
+  return KH_OK;
+}
+
+// Network::forward for one example (net.rs:62-78), layer by layer: nonzeros of
+// the input, hash, query, sampling in the sampler's order (clearing the
+// previous example's entries of the dense activations), neuron sums, softmax.
+static int net_forward_one(kh_slide_network* net, const float* x, hipStream_t st) {
+  const float* in = x;
+  for (size_t i = 0; i < net->layers.size(); ++i) {
+    kh_slide_layer* l = net->layers[i];
+    TrainBufs& t = net->b[i];
+    hipLaunchKernelGGL(tr_stage_nz_kernel, dim3(1), dim3(1024), 0, st, in, l->dim, t.nzi, t.nzv,
+                       t.xoff);
+    KH_LAUNCHED();
+    int rc = hash_sparse_launch(l->index->h, t.xoff, t.nzi, t.nzv, 1, t.codes, st);
+    if (rc != KH_OK) return rc;
+    const int qs = query_stride(l->index);
+    rc = query_launch(l->index, t.codes, 1, t.qids, t.qcnt, qs, t.qlen, st);
+    if (rc != KH_OK) return rc;
+    rc = select_launch(l, t.qids, t.qcnt, t.qlen, qs, 1, t.aids, t.as, t.alen, true, t.dense, st);
+    if (rc != KH_OK) return rc;
+    const unsigned nb = static_cast<unsigned>(std::min(ceil_div(t.as, kTrThreads), 64));
+    const size_t lds = (sizeof(uint32_t) + sizeof(float)) * kTrLdsNz;
+    hipLaunchKernelGGL(tr_neuron_kernel, dim3(nb), dim3(kTrThreads), lds, st, l->w, l->bias, l->dim,
+                       t.nzi, t.nzv, t.xoff, t.aids, t.alen, t.as, l->act, t.pre, t.post, t.dense);
+    KH_LAUNCHED();
+    if (l->act == KH_ACT_SOFTMAX) {
+      hipLaunchKernelGGL(tr_softmax_kernel, dim3(1), dim3(kTrThreads), 0, st, t.pre, t.aids, t.alen,
+                         t.as, t.post, t.dense);
+      KH_LAUNCHED();
+    }
+    in = t.dense;
+  }
+  return KH_OK;
+}
+
+static int net_setup_attrs() {
+  static int rc = [] {
+    const size_t lds = (sizeof(uint32_t) + sizeof(float)) * kTrLdsNz;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&tr_neuron_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) ==
+                   hipSuccess
+               ? KH_OK
+               : KH_ERR_HIP;
+  }();
+  if (rc != KH_OK) set_error("hipFuncSetAttribute failed");
+  return rc;
+}
+
+extern "C" int kh_slide_network_train_step(kh_slide_network* net, const float* x_dev, int64_t batch,
+                                           const int64_t* label_off_host,
+                                           const uint32_t* labels_host, double lr, float* loss_out,
+                                           void* stream) {
+  KH_CHECK_ARG(net && loss_out, "null argument");
+  KH_CHECK_ARG(batch >= 0, "bad batch");
+  *loss_out = 0.0f;
+  if (batch == 0) return KH_OK;  // net.rs:82-84: nothing changes
+  KH_CHECK_ARG(x_dev && label_off_host, "null input");
+  KH_CHECK_ARG(label_off_host[0] == 0, "label offsets must start at 0");
+  for (int64_t e = 0; e < batch; ++e)
+    KH_CHECK_ARG(label_off_host[e + 1] >= label_off_host[e] &&
+                     label_off_host[e + 1] - label_off_host[e] <= kTrMaxLabels,
+                 "example %lld: label offsets must be nondecreasing with at most %d labels",
+                 (long long)e, kTrMaxLabels);
+  const int64_t n_labels = label_off_host[batch];
+  KH_CHECK_ARG(n_labels == 0 || labels_host, "null labels");
+  int rc = net_setup_attrs();
+  if (rc != KH_OK) return rc;
+  hipStream_t st = as_stream(stream);
+  if (static_cast<size_t>(n_labels) > net->labels_cap) {
+    KH_HIP(hipStreamSynchronize(st));
+    dev_free(net->labels);
+    net->labels_cap = std::max<size_t>(n_labels, 2 * net->labels_cap);
+    net->labels = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * net->labels_cap));
+    if (!net->labels) {
+      net->labels_cap = 0;
+      return KH_ERR_ALLOC;
+    }
+  }
+  if (n_labels)
+    KH_HIP(hipMemcpyAsync(net->labels, labels_host, sizeof(uint32_t) * n_labels,
+                          hipMemcpyHostToDevice, st));
+  hipLaunchKernelGGL(fill_f32_kernel<>, dim3(1), dim3(64), 0, st, net->loss_total, (int64_t)1, 0.0f);
+  KH_LAUNCHED();
+  const int nl_layers = static_cast<int>(net->layers.size());
+  std::vector<OptArgs> oa(nl_layers);
+  for (int i = 0; i < nl_layers; ++i) oa[i] = opt_args(net->layers[i], lr, net->step);
+  for (int64_t e = 0; e < batch; ++e) {
+    const float* x = x_dev + e * static_cast<int64_t>(net->in_dim);
+    rc = net_forward_one(net, x, st);
+    if (rc != KH_OK) return rc;
+    const int last = nl_layers - 1;
+    kh_slide_layer* L = net->layers[last];
+    TrainBufs& T = net->b[last];
+    const int nl = static_cast<int>(label_off_host[e + 1] - label_off_host[e]);
+    hipLaunchKernelGGL(tr_loss_grad_kernel, dim3(1), dim3(kTrThreads), 0, st, T.pre, T.post, T.aids,
+                       T.alen, T.as, L->act, T.dense, net->labels + label_off_host[e], nl, T.go,
+                       T.lg, net->loss_total);
+    KH_LAUNCHED();
+    // Network::backward (net.rs:122-146): last layer down to the first
+    for (int i = last; i >= 0; --i) {
+      kh_slide_layer* l = net->layers[i];
+      TrainBufs& t = net->b[i];
+      const float* in = i == 0 ? x : net->b[i - 1].dense;
+      const float* grad_out = i == last ? nullptr : net->b[i + 1].gi;
+      // the first layer's grad_input is not used by anything (net.rs:139-144)
+      float* gi = i == 0 ? nullptr : t.gi;
+      rc = layer_backward_launch(l, in, t.aids, t.alen, t.as, t.pre, t.post, t.dense, grad_out,
+                                 l->n, i == last, t.go, t.lg, oa[i], gi, st);
+      if (rc != KH_OK) return rc;
+    }
+  }
+  float total = 0.0f;
+  KH_HIP(hipMemcpyAsync(&total, net->loss_total, sizeof(float), hipMemcpyDeviceToHost, st));
+  KH_HIP(hipStreamSynchronize(st));
+  net->step += 1;
+  if (kh_rebuild_scheduler_should_rebuild(&net->sched, net->step)) {
+    for (kh_slide_layer* l : net->layers) {
+      rc = kh_slide_layer_rebuild_index(l, stream);
+      if (rc != KH_OK) return rc;
+    }
+  }
+  *loss_out = total / static_cast<float>(batch);
+  return KH_OK;
+}
+
+extern "C" int kh_slide_network_predict(kh_slide_network* net, const float* x_dev, int64_t batch,
+                                        float* out_dev, void* stream) {
+  KH_CHECK_ARG(net != nullptr, "null network");
+  KH_CHECK_ARG(batch >= 0, "bad batch");
+  if (batch == 0) return KH_OK;
+  KH_CHECK_ARG(x_dev && out_dev, "null argument");
+  int rc = net_setup_attrs();
+  if (rc != KH_OK) return rc;
+  hipStream_t st = as_stream(stream);
+  for (int64_t e = 0; e < batch; ++e) {
+    rc = net_forward_one(net, x_dev + e * static_cast<int64_t>(net->in_dim), st);
+    if (rc != KH_OK) return rc;
+    KH_HIP(hipMemcpyAsync(out_dev + e * static_cast<int64_t>(net->out_dim), net->b.back().dense,
+                          sizeof(float) * net->out_dim, hipMemcpyDeviceToDevice, st));
+  }
+  return KH_OK;
+}
+
+extern "C" int kh_slide_network_state(const kh_slide_network* net, uint64_t* step,
+                                      kh_rebuild_scheduler* scheduler) {
+  KH_CHECK_ARG(net != nullptr, "null network");
+  if (step) *step = net->step;
+  if (scheduler) *scheduler = net->sched;
+  return KH_OK;
+}

@@ -144,7 +144,7 @@ def SparseRandomProjection(input_dim: int, k: int, num_tables: int, sparsity: fl
 
 @dataclass
 class LshConfig:
-    """config.rs:41-65 defaults; range_pow and the rebuild fields are not read by the index."""
+    """config.rs:41-65 defaults; range_pow is not read; the rebuild fields set a Network's scheduler."""
     hash_function: str = "SimHash"
     bucket_type: str = "Fifo"
     num_tables: int = 50
@@ -224,13 +224,14 @@ class LshIndex:
     def clear(self, stream=None):
         _lib.call("kh_lsh_index_clear", self._h, stream_ptr(stream))
 
-    def rebuild(self, neurons):
+    def rebuild(self, neurons, stream=None):
         """neurons: iterable of (id, dense weights); clear then insert in order (index.rs:302-307)."""
-        self.clear()
         neurons = list(neurons)
-        if neurons:
-            self.insert_batch(np.array([n[0] for n in neurons], np.uint32),
-                              np.stack([np.asarray(n[1], np.float32) for n in neurons]))
+        dim = self.hash_family.input_dim()
+        ids = to_device(np.array([n[0] for n in neurons], np.uint32)) if neurons else None
+        W = (to_device(np.stack([np.asarray(n[1], np.float32) for n in neurons]).reshape(-1, dim))
+             if neurons else None)
+        _lib.call("kh_lsh_index_rebuild", self._h, ptr(ids), ptr(W), len(neurons), dim, stream_ptr(stream))
 
     # -- queries (&self)
     def query_batch(self, X, counts=True, capacity=None, stream=None):

@@ -1,10 +1,11 @@
-"""SLIDE layer host mirror.
+"""SLIDE layer and network host mirror.
 
-Mirrors Layer / LayerConfig / LayerOutput (crates/klearu-core/src/network/layer.rs:10-120,
-crates/klearu-core/src/config.rs:67-105).  Weights are explicit (the reference's
-Xavier init draws from rand_distr and is not on the inference path); the LSH
-index is built like Layer::new (layer.rs:40-44): create_lsh_index with seed
-+ 1_000_000, then insert neurons 0..n-1 in order.
+Mirrors Layer / LayerConfig / LayerOutput (crates/klearu-core/src/network/layer.rs:10-233,
+crates/klearu-core/src/config.rs:67-105), Network (network/net.rs:10-174) and
+RebuildScheduler (lsh/maintenance.rs:20-98).  Weights are explicit (the
+reference's Xavier init draws from rand_distr); the LSH index is built like
+Layer::new (layer.rs:40-44): create_lsh_index with seed + 1_000_000, then
+insert neurons 0..n-1 in order.
 """
 from __future__ import annotations
 
@@ -108,6 +109,131 @@ class Layer:
         dense = np.zeros(self.config.num_neurons, np.float32)
         dense[a] = act[:n].cpu().numpy()
         return LayerOutput(dense, a, pre[:n].cpu().numpy())
+
+    # ------------------------------------------------------------ training side
+    def init_optimizer(self, optimizer="Sgd", momentum=0.9, beta1=0.9, beta2=0.999, eps=1e-8):
+        """Optimizer::create_state for every neuron (zeroed)."""
+        _lib.call("kh_slide_layer_init_optimizer", self._h, OPTIMIZER[optimizer], momentum, beta1, beta2, eps)
+
+    def backward(self, x, output: LayerOutput, grad_output, lr, step, want_grad_input=True, stream=None):
+        """Layer::backward (layer.rs:124-226) for one sample.  output.active_neurons
+        gives the order of the sums over active neurons.  Returns grad_input
+        (numpy) or None."""
+        ids = to_device(np.asarray(output.active_neurons, np.uint32))
+        n_act = to_device(np.array([ids.numel()], np.int32))
+        pre = to_device(np.asarray(output.pre_activations, np.float32))
+        dense = to_device(np.asarray(output.activations, np.float32))
+        g = to_device(np.asarray(grad_output, np.float32))
+        xd = to_device(np.asarray(x, np.float32))
+        gi = torch.empty(self.config.input_dim, dtype=torch.float32, device="cuda") if want_grad_input else None
+        _lib.call("kh_slide_layer_backward", self._h, ptr(xd), ptr(ids), ptr(n_act), ptr(pre), ptr(dense), ptr(g),
+                  g.numel(), float(lr), int(step), ptr(gi), stream_ptr(stream))
+        return gi.cpu().numpy() if gi is not None else None
+
+    def rebuild_index(self, stream=None):
+        """Layer::rebuild_index (layer.rs:228-233)."""
+        _lib.call("kh_slide_layer_rebuild_index", self._h, stream_ptr(stream))
+
+    def weights(self):
+        w = np.empty((self.config.num_neurons, self.config.input_dim), np.float32)
+        b = np.empty(self.config.num_neurons, np.float32)
+        _lib.call("kh_slide_layer_weights", self._h, hptr(w), hptr(b))
+        return w, b
+
+
+OPTIMIZER = {"Sgd": 0, "Adam": 1}
+
+
+class RebuildScheduler(C.Structure):
+    """RebuildScheduler (lsh/maintenance.rs:20-98); state lives in this struct."""
+
+    _fields_ = [("base_interval", C.c_uint64), ("decay", C.c_double), ("rebuild_count", C.c_uint64),
+                ("next_rebuild_step", C.c_uint64), ("current_step", C.c_uint64)]
+
+    def __init__(self, base_interval=100, decay=0.1):
+        super().__init__()
+        _lib.load().kh_rebuild_scheduler_init(C.byref(self), int(base_interval), float(decay))
+
+    def step(self) -> bool:
+        return bool(_lib.load().kh_rebuild_scheduler_step(C.byref(self)))
+
+    def should_rebuild(self, step) -> bool:
+        return bool(_lib.load().kh_rebuild_scheduler_should_rebuild(C.byref(self), int(step)))
+
+    def next_rebuild(self) -> int:
+        return int(self.next_rebuild_step)
+
+
+class Network:
+    """Network (net.rs:10-174) over Layer objects (kept alive here).
+
+    optimizer "Sgd" (Sgd::new(momentum), the reference config uses 0.9) or
+    "Adam" (Adam::new(beta1, beta2, eps), default 0.9 / 0.999 / 1e-8); the
+    scheduler takes the first layer's rebuild settings (net.rs:32-38)."""
+
+    def __init__(self, layers, optimizer="Sgd", momentum=0.9, beta1=0.9, beta2=0.999, eps=1e-8,
+                 rebuild_base=None, rebuild_decay=None):
+        self.layers = list(layers)
+        lsh = self.layers[0].config.lsh
+        base = getattr(lsh, "rebuild_interval_base", 100) if rebuild_base is None else rebuild_base
+        decay = getattr(lsh, "rebuild_decay", 0.1) if rebuild_decay is None else rebuild_decay
+        arr = (C.c_void_p * len(self.layers))(*[l._h.value for l in self.layers])
+        h = C.c_void_p()
+        _lib.call("kh_slide_network_create", arr, len(self.layers), OPTIMIZER[optimizer], momentum, beta1, beta2,
+                  eps, int(base), float(decay), C.byref(h))
+        self._h = h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            try:
+                _lib.load().kh_slide_network_destroy(h)
+            except Exception:
+                pass
+
+    def train_step(self, X, labels, lr, stream=None) -> float:
+        """Network::train_step (net.rs:81-120): X [B, input_dim] dense
+        (features.to_dense()), labels one id list per example."""
+        X = to_device(X, np.float32).reshape(-1, self.layers[0].config.input_dim)
+        B = X.shape[0]
+        off = np.zeros(B + 1, np.int64)
+        for i, lab in enumerate(labels[:B]):
+            off[i + 1] = off[i] + len(lab)
+        flat = np.ascontiguousarray(np.concatenate([np.asarray(l, np.uint32) for l in labels[:B]] or
+                                                   [np.zeros(0, np.uint32)]), np.uint32)
+        loss = C.c_float()
+        _lib.call("kh_slide_network_train_step", self._h, ptr(X), B, hptr(off), hptr(flat) if flat.size else None,
+                  float(lr), C.byref(loss), stream_ptr(stream))
+        return float(loss.value)
+
+    def predict_batch(self, X, stream=None) -> torch.Tensor:
+        """Network::predict (net.rs:151-154) per row: the last layer's dense activations."""
+        X = to_device(X, np.float32).reshape(-1, self.layers[0].config.input_dim)
+        out = torch.empty(X.shape[0], self.layers[-1].config.num_neurons, dtype=torch.float32, device=X.device)
+        _lib.call("kh_slide_network_predict", self._h, ptr(X), X.shape[0], ptr(out), stream_ptr(stream))
+        return out
+
+    def predict(self, x) -> np.ndarray:
+        return self.predict_batch(np.asarray(x, np.float32)[None, :])[0].cpu().numpy()
+
+    def predict_top_k(self, x, k):
+        """Network::predict_top_k (net.rs:159-174): (label, score) by score
+        descending; a stable sort, so ties keep ascending labels."""
+        out = self.predict(x)
+        order = sorted(range(out.size), key=lambda i: -out[i])[:k]
+        return [(i, float(out[i])) for i in order]
+
+    @property
+    def step(self) -> int:
+        s = C.c_uint64()
+        _lib.call("kh_slide_network_state", self._h, C.byref(s), None)
+        return int(s.value)
+
+    def scheduler(self) -> RebuildScheduler:
+        r = RebuildScheduler.__new__(RebuildScheduler)
+        C.Structure.__init__(r)
+        _lib.call("kh_slide_network_state", self._h, None, C.byref(r))
+        return r
 
 
 class DenseLayer:

@@ -112,6 +112,19 @@ _sig("or_cpu_sparse_attention_layer", None, _f32p, _f32p, _f32p, _f32p, _f32p, _
 _sig("or_slide_forward", _i64, _i8p, _int, _int, _int, _int, _u32p, _u32p, _f32p, _f32p, _int, _f32p,
      _int, _int, _int, _int, _u32p, _f32p, _f32p)
 
+_sig("or_slide_forward_ordered", _i64, _i8p, _int, _int, _int, _int, _u32p, _u32p, _f32p, _f32p, _int,
+     _f32p, _int, _int, _int, _int, _u32p, _f32p, _f32p)
+_sig("or_powi_f32", _f, _f, C.c_int32)
+_sig("or_sgd_update", None, _f32p, _f32p, _i64, _f32p, _f, C.c_double, _f, _f32p, _f32p)
+_sig("or_adam_update", None, _f32p, _f32p, _i64, _f32p, _f, C.c_double, C.c_uint64, _f, _f, _f, _f32p,
+     _f32p, _f32p, _f32p)
+_sig("or_activation_derivative", _f, _f, _f, _int)
+_sig("or_softmax_local_grads", None, _f32p, _f32p, _i64, _f32p)
+_sig("or_compute_loss", _f, _f32p, _u32p, _i64, _u32p, _i64)
+_sig("or_compute_loss_gradient", None, _f32p, _u32p, _i64, _u32p, _i64, _i64, _f32p)
+_sig("or_layer_backward", None, _f32p, _f32p, _int, _int, _int, _f32p, _u32p, _i64, _f32p, _f32p, _f32p,
+     _i64, _int, _f, _f, _f, _f, _f32p, _f32p, _f32p, _f32p, C.c_double, C.c_uint64, C.c_void_p)
+
 ACT = {"relu": 0, "sigmoid": 1, "tanh": 2, "softmax": 3, "identity": 4}
 FIFO, RESERVOIR = 0, 1
 
@@ -440,3 +453,185 @@ def slide_layer_oracle(planes, cap, bucket_type, W, b, X, sampling=0, top_k=0, t
                                    ACT[act] if isinstance(act, str) else act, ids, pre, a_)
         out.append((ids[:cnt].copy(), pre[:cnt].copy(), a_[:cnt].copy()))
     return out, index
+
+
+# --------------------------------------------------------------------------- SLIDE training
+SGD, ADAM = 0, 1
+_U64_MAX = (1 << 64) - 1
+
+
+def powi_f32(a, b):
+    return float(np.float32(lib.or_powi_f32(float(np.float32(a)), int(b))))
+
+
+def sgd_update(w, gw, bias, gb, lr, momentum=0.0, mw=None, mb=None):
+    """In place on w (f32 array), mw; returns (bias, mb) (optim/sgd.rs:18-57)."""
+    b = np.array([bias], np.float32)
+    mbv = np.array([0.0 if mb is None else mb], np.float32)
+    if mw is None:
+        mw = np.zeros_like(w)
+    lib.or_sgd_update(w, f32(gw), w.size, b, float(np.float32(gb)), float(lr), float(np.float32(momentum)), mw, mbv)
+    return float(b[0]), float(mbv[0])
+
+
+def adam_update(w, gw, bias, gb, lr, step, m_w, v_w, m_b, v_b, beta1=0.9, beta2=0.999, eps=1e-8):
+    """In place on w, m_w, v_w; returns (bias, m_b, v_b) (optim/adam.rs:28-77)."""
+    b = np.array([bias], np.float32)
+    mb = np.array([m_b], np.float32)
+    vb = np.array([v_b], np.float32)
+    lib.or_adam_update(w, f32(gw), w.size, b, float(np.float32(gb)), float(lr), int(step), float(np.float32(beta1)),
+                       float(np.float32(beta2)), float(np.float32(eps)), m_w, v_w, mb, vb)
+    return float(b[0]), float(mb[0]), float(vb[0])
+
+
+def softmax_local_grads(s, go):
+    s, go = f32(s), f32(go)
+    out = np.zeros(max(s.size, 1), np.float32)
+    lib.or_softmax_local_grads(s, go, s.size, out)
+    return out[:s.size].copy()
+
+
+def compute_loss(act_dense, active, labels):
+    return float(lib.or_compute_loss(f32(act_dense), u32(active), u32(active).size, u32(labels), u32(labels).size))
+
+
+def compute_loss_gradient(act_dense, active, labels, num_output):
+    g = np.zeros(max(num_output, 1), np.float32)
+    lib.or_compute_loss_gradient(f32(act_dense), u32(active), u32(active).size, u32(labels), u32(labels).size,
+                                 num_output, g)
+    return g[:num_output].copy()
+
+
+class RebuildScheduler:
+    """RebuildScheduler (lsh/maintenance.rs:20-98) in Python integers: the
+    interval after the i-th rebuild is (usize)(base * exp(decay * i)) -- f64
+    exp, truncation toward zero, saturating at 0 and 2^64-1 as `as usize` does
+    -- at least 1, and the step sum wraps modulo 2^64 (release arithmetic).
+    Pinned: the reference's own scheduler tests (maintenance.rs:103-207)."""
+
+    def __init__(self, base_interval, decay):
+        self.base_interval, self.decay = int(base_interval), float(decay)
+        self.rebuild_count, self.next_rebuild_step, self.current_step = 0, int(base_interval), 0
+
+    def _interval(self):
+        import math
+        v = float(self.base_interval) * math.exp(self.decay * float(self.rebuild_count))
+        if v != v or v <= 0.0:
+            n = 0
+        elif v >= 18446744073709551616.0:
+            n = _U64_MAX
+        else:
+            n = int(v)
+        return max(n, 1)
+
+    def _due(self):
+        if self.current_step >= self.next_rebuild_step:
+            self.rebuild_count += 1
+            self.next_rebuild_step = (self.current_step + self._interval()) & _U64_MAX
+            return True
+        return False
+
+    def step(self):
+        self.current_step = (self.current_step + 1) & _U64_MAX
+        return self._due()
+
+    def should_rebuild(self, step):
+        self.current_step = int(step) & _U64_MAX
+        return self._due()
+
+
+class SlideNetOracle:
+    """Network (network/net.rs:10-230) over explicit layer weights, each layer an
+    LSH index built like Layer::new (neurons 0..n-1 in order).  Forward lists
+    active neurons in the sampler's order (or_slide_forward_ordered).
+
+    layers: dicts with planes [L][k][dim] int8, cap, bucket_type, W [n][dim],
+    b [n], sampling, top_k, threshold, act."""
+
+    def __init__(self, layers, optimizer=SGD, momentum=0.9, beta1=0.9, beta2=0.999, eps=1e-8,
+                 rebuild_base=100, rebuild_decay=0.1):
+        self.layers = []
+        for spec in layers:
+            l = dict(spec)
+            l["W"] = f32(spec["W"]).copy()
+            l["b"] = f32(spec["b"]).copy()
+            n, dim = l["W"].shape
+            L, k, _ = l["planes"].shape
+            l["n"], l["dim"], l["L"], l["k"] = n, dim, L, k
+            l["act"] = ACT[l["act"]] if isinstance(l["act"], str) else l["act"]
+            l["pl"] = np.ascontiguousarray(l["planes"]).reshape(-1)
+            l["index"] = LshIndex(L, k, l["cap"], l["bucket_type"])
+            l["st_w1"] = np.zeros(n * dim, np.float32)
+            l["st_w2"] = np.zeros(n * dim, np.float32)
+            l["st_b1"] = np.zeros(n, np.float32)
+            l["st_b2"] = np.zeros(n, np.float32)
+            self.layers.append(l)
+            self.rebuild_layer(l)
+        self.opt, self.momentum, self.beta1, self.beta2, self.eps = optimizer, momentum, beta1, beta2, eps
+        self.step = 0
+        self.scheduler = RebuildScheduler(rebuild_base, rebuild_decay)
+
+    @staticmethod
+    def rebuild_layer(l):
+        """Layer::rebuild_index (layer.rs:228-233): clear, insert 0..n-1 in order."""
+        idx = l["index"]
+        idx.data[:] = 0
+        idx.len[:] = 0
+        idx.count[:] = 0
+        idx.insert_many(np.arange(l["n"], dtype=np.uint32), hash_dense_batch(l["planes"], l["W"]))
+
+    def layer_forward(self, l, x):
+        m = max(l["n"], l["L"] * l["cap"]) + 1
+        ids = np.zeros(m, np.uint32)
+        pre = np.zeros(m, np.float32)
+        a_ = np.zeros(m, np.float32)
+        cnt = lib.or_slide_forward_ordered(l["pl"], l["dim"], l["k"], l["L"], l["cap"], l["index"].data,
+                                           l["index"].len, l["W"].reshape(-1), l["b"], l["n"],
+                                           np.ascontiguousarray(f32(x)), l["sampling"], l["top_k"],
+                                           l["threshold"], l["act"], ids, pre, a_)
+        dense = np.zeros(l["n"], np.float32)
+        dense[ids[:cnt]] = a_[:cnt]
+        return ids[:cnt].copy(), pre[:cnt].copy(), dense
+
+    def forward(self, x):
+        """Network::forward (net.rs:62-78): per layer (ids, pre, dense activations)."""
+        outs, cur = [], f32(x)
+        for l in self.layers:
+            o = self.layer_forward(l, cur)
+            outs.append(o)
+            cur = o[2]
+        return outs
+
+    def predict(self, x):
+        return self.forward(x)[-1][2]
+
+    def layer_backward(self, l, x, out, grad_out, lr, want_grad_in=True):
+        ids, pre, dense = out
+        gi = np.zeros(l["dim"], np.float32) if want_grad_in else None
+        lib.or_layer_backward(l["W"].reshape(-1), l["b"], l["dim"], l["n"], l["act"], np.ascontiguousarray(f32(x)),
+                              u32(ids), ids.size, f32(pre), dense, f32(grad_out), grad_out.size, self.opt,
+                              float(np.float32(self.momentum)), float(np.float32(self.beta1)),
+                              float(np.float32(self.beta2)), float(np.float32(self.eps)), l["st_w1"], l["st_w2"],
+                              l["st_b1"], l["st_b2"], float(lr), int(self.step),
+                              gi.ctypes.data if gi is not None else None)
+        return gi
+
+    def train_step(self, X, labels, lr):
+        """Network::train_step (net.rs:81-120); labels: one id list per row."""
+        X = f32(X)
+        if X.shape[0] == 0:
+            return 0.0
+        total = np.float32(0.0)
+        for x, lab in zip(X, labels):
+            outs = self.forward(x)
+            ids, _, dense = outs[-1]
+            total = np.float32(total + np.float32(compute_loss(dense, ids, lab)))
+            grad = compute_loss_gradient(dense, ids, lab, self.layers[-1]["n"])
+            for i in range(len(self.layers) - 1, -1, -1):
+                inp = x if i == 0 else outs[i - 1][2]
+                grad = self.layer_backward(self.layers[i], inp, outs[i], grad, lr)
+        self.step += 1
+        if self.scheduler.should_rebuild(self.step):
+            for l in self.layers:
+                self.rebuild_layer(l)
+        return float(np.float32(total / np.float32(X.shape[0])))

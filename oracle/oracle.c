@@ -960,11 +960,11 @@ static int cmp_u32_asc(const void* a, const void* b) { return cmp_u32(a, b); }
  * (:96-107).  Active ids are returned ascending (the reference's order is
  * HashMap order for vanilla/threshold).  Returns the number of active ids;
  * out arrays need max(n, L*cap) entries. */
-int64_t or_slide_forward(const int8_t* planes, int dim, int k, int num_tables, int cap,
-                         const uint32_t* data, const uint32_t* len, const float* W,
-                         const float* bias, int n, const float* x, int sampling, int top_k,
-                         int threshold, int act, uint32_t* out_ids, float* out_pre,
-                         float* out_act) {
+static int64_t slide_forward_impl(const int8_t* planes, int dim, int k, int num_tables, int cap,
+                                  const uint32_t* data, const uint32_t* len, const float* W,
+                                  const float* bias, int n, const float* x, int sampling,
+                                  int top_k, int threshold, int act, uint32_t* out_ids,
+                                  float* out_pre, float* out_act, int sampler_order) {
   uint32_t* codes = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)num_tables);
   or_hash_dense_batch(planes, dim, k, num_tables, x, 1, codes);
   const int64_t m = (int64_t)num_tables * cap + 1;
@@ -988,7 +988,7 @@ int64_t or_slide_forward(const int8_t* planes, int dim, int k, int num_tables, i
   for (int64_t i = 0; i < a; ++i)
     if (out_ids[i] < (uint32_t)n) out_ids[r++] = out_ids[i];
   a = r;
-  qsort(out_ids, (size_t)a, sizeof(uint32_t), cmp_u32_asc);
+  if (!sampler_order) qsort(out_ids, (size_t)a, sizeof(uint32_t), cmp_u32_asc);
   for (int64_t i = 0; i < a; ++i)
     out_pre[i] = or_neuron_forward(W + (int64_t)out_ids[i] * dim, bias[out_ids[i]], x, dim);
   or_layer_activate(out_pre, a, act, out_act);
@@ -996,4 +996,239 @@ int64_t or_slide_forward(const int8_t* planes, int dim, int k, int num_tables, i
   free(ids);
   free(cnt);
   return a;
+}
+
+int64_t or_slide_forward(const int8_t* planes, int dim, int k, int num_tables, int cap,
+                         const uint32_t* data, const uint32_t* len, const float* W,
+                         const float* bias, int n, const float* x, int sampling, int top_k,
+                         int threshold, int act, uint32_t* out_ids, float* out_pre,
+                         float* out_act) {
+  return slide_forward_impl(planes, dim, k, num_tables, cap, data, len, W, bias, n, x, sampling,
+                            top_k, threshold, act, out_ids, out_pre, out_act, 0);
+}
+
+/* Layer::forward with the active list in the sampler's order, which the
+ * backward pass's sums follow: TopKSampling::select sorts by count descending,
+ * then id (sampling/topk.rs:19-34); the query's candidates come in ascending id
+ * order here (or_lsh_query), which vanilla and threshold sampling keep (the
+ * reference's HashMap order is not reproducible: its RandomState differs
+ * from run to run).  The softmax sum (layer.rs:298) follows the same order.
+ * Pinned: the count-order KAT in tests/test_oracle_train.py. */
+int64_t or_slide_forward_ordered(const int8_t* planes, int dim, int k, int num_tables, int cap,
+                                 const uint32_t* data, const uint32_t* len, const float* W,
+                                 const float* bias, int n, const float* x, int sampling,
+                                 int top_k, int threshold, int act, uint32_t* out_ids,
+                                 float* out_pre, float* out_act) {
+  return slide_forward_impl(planes, dim, k, num_tables, cap, data, len, W, bias, n, x, sampling,
+                            top_k, threshold, act, out_ids, out_pre, out_act, 1);
+}
+
+/* ======================================================================== */
+/* SLIDE training: network/layer.rs:124-226, network/net.rs:176-230, optim/   */
+/* ======================================================================== */
+
+/* f32::powi: llvm.powi with a run-time exponent is the __powisf2 libcall of
+ * Rust's compiler-builtins (src/float/pow.rs): square-and-multiply in f32 from
+ * the low exponent bit up, reciprocal for negative exponents.
+ * Pinned: closed forms (b^0 = 1, b^1 = b, b^2 = b*b, b^4 = (b*b)*(b*b),
+ * b^3 = b*(b*b)) in tests/test_oracle_train.py. */
+float or_powi_f32(float a, int32_t b) {
+  const int recip = b < 0;
+  uint32_t p = recip ? 0u - (uint32_t)b : (uint32_t)b;
+  float mul = 1.0f;
+  for (;;) {
+    if (p & 1u) mul = mul * a;
+    p >>= 1;
+    if (p == 0) break;
+    a = a * a;
+  }
+  return recip ? 1.0f / mul : mul;
+}
+
+/* Sgd::update (optim/sgd.rs:18-57): lr rounded to f32; with momentum
+ * v = momentum*m - lr*g, m = v, w += v; without, w -= lr*g.  mw/mb are
+ * ignored when momentum <= 0.
+ * Pinned: the reference's own expected values (sgd.rs:77-117) in
+ * tests/test_oracle_train.py. */
+void or_sgd_update(float* w, const float* gw, int64_t n, float* bias, float gb, double lr_d,
+                   float momentum, float* mw, float* mb) {
+  const float lr = (float)lr_d;
+  if (momentum > 0.0f) {
+    for (int64_t i = 0; i < n; ++i) {
+      float a = momentum * mw[i];
+      float b = lr * gw[i];
+      float v = a - b;
+      mw[i] = v;
+      w[i] = w[i] + v;
+    }
+    float a = momentum * *mb;
+    float b = lr * gb;
+    float vb = a - b;
+    *mb = vb;
+    *bias = *bias + vb;
+  } else {
+    for (int64_t i = 0; i < n; ++i) {
+      float b = lr * gw[i];
+      w[i] = w[i] - b;
+    }
+    float b = lr * gb;
+    *bias = *bias - b;
+  }
+}
+
+/* Adam::update (optim/adam.rs:28-77): corrections 1 - beta^step with
+ * f32::powi (or_powi_f32; step 0 counts as 1, `step as i32` wraps), then per
+ * weight m = b1*m + (1-b1)*g, v = b2*v + ((1-b2)*g)*g,
+ * w -= (lr*(m/c1)) / (sqrt(v/c2) + eps); the bias likewise.
+ * Pinned: hand-computed first steps (m = (1-b1) g, v = (1-b2) g^2) and the
+ * reference's sign / zero-gradient tests (adam.rs:131-254) in
+ * tests/test_oracle_train.py. */
+static float adam_one(float w, float g, float* m, float* v, float lr, float b1, float b2,
+                      float eps, float c1, float c2) {
+  float a = b1 * *m;
+  float b = (1.0f - b1) * g;
+  *m = a + b;
+  float c = b2 * *v;
+  float d = (1.0f - b2) * g;
+  d = d * g;
+  *v = c + d;
+  float mh = *m / c1;
+  float vh = *v / c2;
+  float num = lr * mh;
+  float den = sqrtf(vh) + eps;
+  return w - num / den;
+}
+
+void or_adam_update(float* w, const float* gw, int64_t n, float* bias, float gb, double lr_d,
+                    uint64_t step, float beta1, float beta2, float eps, float* m_w, float* v_w,
+                    float* m_b, float* v_b) {
+  const float lr = (float)lr_d;
+  const uint64_t st = step < 1 ? 1 : step;
+  const int32_t si = (int32_t)(uint32_t)st;
+  const float c1 = 1.0f - or_powi_f32(beta1, si);
+  const float c2 = 1.0f - or_powi_f32(beta2, si);
+  for (int64_t i = 0; i < n; ++i) w[i] = adam_one(w[i], gw[i], m_w + i, v_w + i, lr, beta1, beta2, eps, c1, c2);
+  *bias = adam_one(*bias, gb, m_b, v_b, lr, beta1, beta2, eps, c1, c2);
+}
+
+/* activation_derivative (layer.rs:266-283). */
+float or_activation_derivative(float pre, float post, int act) {
+  switch (act) {
+    case OR_ACT_RELU: return pre > 0.0f ? 1.0f : 0.0f;
+    case OR_ACT_SIGMOID: return post * (1.0f - post);
+    case OR_ACT_TANH: return 1.0f - post * post;
+    default: return 1.0f;
+  }
+}
+
+/* The softmax branch of Layer::backward (layer.rs:141-175): for each i, a
+ * sequential sum from +0.0 over j of go_j*s_j*(1-s_j) (i == j) or
+ * go_j*(-s_i*s_j), each product rounded left to right.
+ * Pinned: a cancellation KAT only the sequential order reproduces and the
+ * identity sum_j J_ij go_j = s_i (go_i - sum_j s_j go_j) within rounding, in
+ * tests/test_oracle_train.py. */
+void or_softmax_local_grads(const float* s, const float* go, int64_t n, float* out) {
+  for (int64_t i = 0; i < n; ++i) {
+    float r = 0.0f;
+    for (int64_t j = 0; j < n; ++j) {
+      float t;
+      if (i == j) {
+        t = go[j] * s[j];
+        t = t * (1.0f - s[j]);
+      } else {
+        float q = -s[i] * s[j];
+        t = go[j] * q;
+      }
+      r = r + t;
+    }
+    out[i] = r;
+  }
+}
+
+/* compute_loss (net.rs:180-201): -ln(max(p, 1e-7)) per label (1e-7 when the
+ * label is not active), summed in label order, divided by the label count.
+ * Pinned: the reference's expected values (net.rs:404-465). */
+float or_compute_loss(const float* act_dense, const uint32_t* active, int64_t n_act,
+                      const uint32_t* labels, int64_t n_labels) {
+  if (n_labels == 0) return 0.0f;
+  const float eps = 1e-7f;
+  float loss = 0.0f;
+  for (int64_t l = 0; l < n_labels; ++l) {
+    int found = 0;
+    for (int64_t a = 0; a < n_act; ++a)
+      if (active[a] == labels[l]) { found = 1; break; }
+    float prob = found ? fmaxf(act_dense[labels[l]], eps) : eps;
+    loss = loss - logf(prob);
+  }
+  return loss / (float)n_labels;
+}
+
+/* compute_loss_gradient (net.rs:205-230): grad = activations at active ids,
+ * then 1/|labels| subtracted once per label occurrence; all zero without labels.
+ * Pinned: the reference's expected values (net.rs:479-494). */
+void or_compute_loss_gradient(const float* act_dense, const uint32_t* active, int64_t n_act,
+                              const uint32_t* labels, int64_t n_labels, int64_t num_output,
+                              float* grad) {
+  for (int64_t i = 0; i < num_output; ++i) grad[i] = 0.0f;
+  if (n_labels == 0) return;
+  for (int64_t a = 0; a < n_act; ++a)
+    if ((int64_t)active[a] < num_output) grad[active[a]] = act_dense[active[a]];
+  const float w = 1.0f / (float)n_labels;
+  for (int64_t l = 0; l < n_labels; ++l)
+    if ((int64_t)labels[l] < num_output) grad[labels[l]] = grad[labels[l]] - w;
+}
+
+/* Layer::backward (layer.rs:124-226) for one sample: local gradients (softmax
+ * Jacobian or go * activation_derivative), then per active neuron in list
+ * order grad_in[j] += lg * w[j] (weights before the update; sequential from
+ * +0.0) and the optimizer update with grad_weights[j] = lg * input[j] and
+ * grad_bias = lg.  opt 0: SGD (st_w1/st_b1 = momentum buffers), 1: Adam
+ * (st_w1/st_b1 = first moments, st_w2/st_b2 = second).  grad_in may be NULL.
+ * Pinned: the pieces above, and a cancellation KAT for the grad_in order in
+ * tests/test_oracle_train.py. */
+void or_layer_backward(float* W, float* bias, int dim, int n, int act, const float* input,
+                       const uint32_t* active, int64_t n_act, const float* pre,
+                       const float* act_dense, const float* grad_out, int64_t grad_out_len,
+                       int opt, float momentum, float beta1, float beta2, float eps,
+                       float* st_w1, float* st_w2, float* st_b1, float* st_b2, double lr,
+                       uint64_t step, float* grad_in) {
+  if (grad_in)
+    for (int j = 0; j < dim; ++j) grad_in[j] = 0.0f;
+  if (n_act == 0) return;
+  float* lg = (float*)malloc(sizeof(float) * (size_t)n_act);
+  if (act == OR_ACT_SOFTMAX) {
+    float* sm = (float*)malloc(sizeof(float) * (size_t)n_act);
+    float* go = (float*)malloc(sizeof(float) * (size_t)n_act);
+    or_layer_activate(pre, n_act, OR_ACT_SOFTMAX, sm);
+    for (int64_t a = 0; a < n_act; ++a)
+      go[a] = (int64_t)active[a] < grad_out_len ? grad_out[active[a]] : 0.0f;
+    or_softmax_local_grads(sm, go, n_act, lg);
+    free(sm);
+    free(go);
+  } else {
+    for (int64_t a = 0; a < n_act; ++a) {
+      const uint32_t id = active[a];
+      const float go = (int64_t)id < grad_out_len ? grad_out[id] : 0.0f;
+      lg[a] = go * or_activation_derivative(pre[a], act_dense[id], act);
+    }
+  }
+  float* gw = (float*)malloc(sizeof(float) * (size_t)dim);
+  for (int64_t a = 0; a < n_act; ++a) {
+    const int64_t id = active[a];
+    float* w = W + id * dim;
+    for (int j = 0; j < dim; ++j) gw[j] = lg[a] * input[j];
+    if (grad_in)
+      for (int j = 0; j < dim; ++j) {
+        float p = lg[a] * w[j];
+        grad_in[j] = grad_in[j] + p;
+      }
+    (void)n;
+    if (opt == 1)
+      or_adam_update(w, gw, dim, bias + id, lg[a], lr, step, beta1, beta2, eps, st_w1 + id * dim,
+                     st_w2 + id * dim, st_b1 + id, st_b2 + id);
+    else
+      or_sgd_update(w, gw, dim, bias + id, lg[a], lr, momentum, st_w1 + id * dim, st_b1 + id);
+  }
+  free(gw);
+  free(lg);
 }

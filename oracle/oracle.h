@@ -102,6 +102,32 @@ int64_t or_slide_forward(const int8_t* planes, int dim, int k, int num_tables, i
                          const float* bias, int n, const float* x, int sampling, int top_k,
                          int threshold, int act, uint32_t* out_ids, float* out_pre,
                          float* out_act);
+int64_t or_slide_forward_ordered(const int8_t* planes, int dim, int k, int num_tables, int cap,
+                                 const uint32_t* data, const uint32_t* len, const float* W,
+                                 const float* bias, int n, const float* x, int sampling,
+                                 int top_k, int threshold, int act, uint32_t* out_ids,
+                                 float* out_pre, float* out_act);
+
+/* ---- SLIDE training: network/layer.rs, network/net.rs, optim/ ---- */
+float or_powi_f32(float a, int32_t b);
+void or_sgd_update(float* w, const float* gw, int64_t n, float* bias, float gb, double lr,
+                   float momentum, float* mw, float* mb);
+void or_adam_update(float* w, const float* gw, int64_t n, float* bias, float gb, double lr,
+                    uint64_t step, float beta1, float beta2, float eps, float* m_w, float* v_w,
+                    float* m_b, float* v_b);
+float or_activation_derivative(float pre, float post, int act);
+void or_softmax_local_grads(const float* s, const float* go, int64_t n, float* out);
+float or_compute_loss(const float* act_dense, const uint32_t* active, int64_t n_act,
+                      const uint32_t* labels, int64_t n_labels);
+void or_compute_loss_gradient(const float* act_dense, const uint32_t* active, int64_t n_act,
+                              const uint32_t* labels, int64_t n_labels, int64_t num_output,
+                              float* grad);
+void or_layer_backward(float* W, float* bias, int dim, int n, int act, const float* input,
+                       const uint32_t* active, int64_t n_act, const float* pre,
+                       const float* act_dense, const float* grad_out, int64_t grad_out_len,
+                       int opt, float momentum, float beta1, float beta2, float eps,
+                       float* st_w1, float* st_w2, float* st_b1, float* st_b2, double lr,
+                       uint64_t step, float* grad_in);
 
 /* ---- klearu-dejavu predictor/mlp_predictor.rs ---- */
 void or_predictor_predict(const float* w1, const float* b1, const float* w2, const float* b2,

@@ -31,3 +31,20 @@ def test_error_reporting_without_gpu():
     assert rc == _lib.KH_ERR_ARG
     assert b"null" in lib.kh_last_error()
     assert lib.kh_version() >= 1
+
+
+@pytest.mark.parametrize("base,decay,steps", [(10, 0.0, 40), (5, 0.0, 31), (10, 0.5, 400), (1, 0.0, 5),
+                                              (5, 2.0, 3000), (3, -1.0, 40), (7, 0.25, 1000)])
+def test_rebuild_scheduler_host_matches_oracle(base, decay, steps):
+    """RebuildScheduler is host logic (no GPU): the C entry points against the
+    oracle's scheduler, which the reference's own tests pin."""
+    import oracle
+    from klearu_amd.slide import RebuildScheduler
+    s, o = RebuildScheduler(base, decay), oracle.RebuildScheduler(base, decay)
+    for i in range(steps):
+        assert s.step() == o.step(), i
+        assert (s.rebuild_count, s.next_rebuild_step, s.current_step) == (
+            o.rebuild_count, o.next_rebuild_step, o.current_step)
+    for jump in (steps + 3, steps + 1000, 2 ** 40):
+        assert s.should_rebuild(jump) == o.should_rebuild(jump)
+        assert (s.rebuild_count, s.next_rebuild_step) == (o.rebuild_count, o.next_rebuild_step)
