@@ -48,7 +48,7 @@ sys.path.insert(0, ROOT)
 METRIC = "sparse FFN tokens/s @7B shape; gathered-weight HBM GB/s vs roofline"
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ffn_fused1_cfg3_traffic.txt")
-ALL_LEGS = ["cfg3", "cfg3b16", "cfg2", "cfg4", "cfg4b8", "decoder", "cfg1", "cfg5"]
+ALL_LEGS = ["cfg3", "cfg3b16", "cfg2", "cfg4", "cfg4b8", "decoder", "cfg1", "cfg5", "train5"]
 
 
 def log(*a):
@@ -538,6 +538,92 @@ def slide_cfg5_leg(steps, seed, timer, cpu_seconds):
     return res
 
 
+def slide_train5_leg(steps, seed, cpu_seconds):
+    """Network::train_step at cfg5's shape: sparse 135909-d inputs -> 128 ReLU
+    -> 670091-way softmax over the union of 50 reservoir buckets (SimHash K9);
+    Adam at lr 0.001 (NetworkConfig::default), batch 256, 1-5 labels per
+    example.  Every Network layer is an LSH layer; the hidden one uses 50
+    one-bit tables with top-k 128, so all 128 hidden neurons are active, as in
+    cfg5's dense hidden layer.  Examples run one after another, as the
+    reference trains them (each reads the weights the previous one wrote)."""
+    import torch
+    from klearu_amd.lsh import LshConfig, SparseVector, csr_batch
+    from klearu_amd.slide import Layer, LayerConfig, Network
+
+    D_in, Hd, n, B = 135909, 128, 670091, 256
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed + 50)
+    rng = np.random.default_rng(seed + 50)
+    W1 = (torch.randn(Hd, D_in, generator=g) * 0.01).numpy()
+    W2 = (torch.randn(n, Hd, generator=g) * 0.01).numpy()
+    b1, b2 = np.zeros(Hd, np.float32), np.zeros(n, np.float32)
+    lsh = dict(num_tables=50, num_hashes=9, bucket_capacity=128, bucket_type="Reservoir")
+    lsh_h = dict(num_tables=50, num_hashes=1, bucket_capacity=128, bucket_type="Fifo")
+    t0 = time.time()
+    hid = Layer(LayerConfig(D_in, Hd, "Relu", LshConfig(**lsh_h), "TopK", 2, Hd, False), W1, b1, seed)
+    out = Layer(LayerConfig(Hd, n, "Softmax", LshConfig(**lsh), "Vanilla", 2, 0, True), W2, b2, seed + 1)
+    net = Network([hid, out], "Adam")
+    torch.cuda.synchronize()
+    build_s = time.time() - t0
+    batches = []
+    for _ in range(2):
+        rows, labels = [], []
+        for _ in range(B):
+            nnz = int(rng.integers(50, 101))
+            idx = np.sort(rng.choice(D_in, nnz, replace=False)).astype(np.uint32)
+            rows.append(SparseVector(idx, rng.uniform(0, 1, nnz).astype(np.float32), D_in))
+            labels.append(sorted(rng.choice(n, int(rng.integers(1, 6)), replace=False).tolist()))
+        batches.append((rows, csr_batch(rows), labels))
+    cpu_state = None
+    if cpu_seconds > 0:   # the oracle starts from the untrained weights and indices
+        cpu_state = [(W1.copy(), b1.copy(), hid.index.buckets(), hid.index.hash_family.planes()),
+                     (W2.copy(), b2.copy(), out.index.buckets(), out.index.hash_family.planes())]
+    net.train_step_sparse(None, batches[0][2], 0.001, csr=batches[0][1])   # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    losses = []
+    for s_ in range(steps):
+        rows, csr, labels = batches[(s_ + 1) % 2]
+        losses.append(net.train_step_sparse(None, labels, 0.001, csr=csr))
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    res = dict(workload="train5: SLIDE Network::train_step at cfg5's shape: sparse 135909-d inputs (50-100 nnz) -> "
+                        "128 ReLU (all active) -> 670091-way softmax over the bucket union (SimHash K9 L50 "
+                        "reservoir 128), Adam lr 0.001, batch 256, 1-5 labels",
+               unit="samples/s", value=round(B * 1000.0 / ms, 1), ms_per_step=round(ms, 3),
+               us_per_example=round(ms * 1e3 / B, 2), loss_first=round(losses[0], 4), loss_last=round(losses[-1], 4),
+               build_s=round(build_s, 1),
+               note="each train_step call ends with a host synchronisation (the loss read back), "
+                    "timed by the host clock over the calls")
+    if cpu_state is not None:
+        import oracle
+        specs = []
+        for (W, b, (d, ln, cnt), planes), (samp, tk, act, bt) in zip(
+                cpu_state, [(1, Hd, "relu", oracle.FIFO), (0, 0, "softmax", oracle.RESERVOIR)]):
+            specs.append(dict(planes=planes, cap=128, bucket_type=bt, W=W, b=b, sampling=samp,
+                              top_k=tk, threshold=2, act=act, index=(d, ln, cnt)))
+        # no index rebuild inside the sample (the GPU steps timed above have none either)
+        onet = oracle.SlideNetOracle(specs, optimizer=oracle.ADAM, rebuild_base=1 << 40)
+        rows, _, labels = batches[0]
+        i = [0]
+
+        def one():
+            r = rows[i[0] % B]
+            x = np.zeros(D_in, np.float32)
+            x[r.indices] = r.values
+            onet.train_step(x[None, :], [labels[i[0] % B]], 0.001)
+            i[0] += 1
+
+        per, cnt_, el = timed_cpu(one, cpu_seconds, 2)
+        res["cpu"] = dict(value=round(1.0 / per, 3), unit="samples/s", cores=1, kind="port",
+                          sample=f"{cnt_} examples of Network::train_step (one example per call, no index "
+                                 f"rebuild) from the same untrained state in {el:.1f}s, 1 thread")
+        del onet
+    del net, hid, out
+    torch.cuda.empty_cache()
+    return res
+
+
 # --------------------------------------------------------------------------- main
 def traffic_probe(seed):
     """Eager dispatches for the rocprofv3 --pmc traffic runs (FETCH_SIZE, then
@@ -662,6 +748,9 @@ def main():
     if "cfg5" in legs:
         extra["cfg5"] = slide_cfg5_leg(min(args.steps, 20), args.seed, timer, leg_cpu)
         log(f"[bench] cfg5 {extra['cfg5']['ms_per_step']:.3f} ms  |A|={extra['cfg5']['mean_active']:.0f}")
+    if "train5" in legs:
+        extra["train5"] = slide_train5_leg(min(args.steps, 5), args.seed, leg_cpu)
+        log(f"[bench] train5 {extra['train5']['ms_per_step']:.3f} ms per batch of 256")
     per_call_ms = r["ms_ffn"] / args.layers
     traffic = read_traffic()
     out = {

@@ -292,8 +292,7 @@ typedef struct kh_slide_network kh_slide_network;
  * Initialises every layer's optimizer state (momentum / beta1 / beta2 / eps as
  * Sgd::new / Adam::new take them; the reference's NetworkConfig uses
  * Sgd::new(0.9) and Adam::default() = 0.9, 0.999, 1e-8) and a
- * RebuildScheduler(rebuild_base, rebuild_decay).  Inputs of the first layer
- * are dense with input_dim <= 65536; hidden widths <= 65536. */
+ * RebuildScheduler(rebuild_base, rebuild_decay). */
 int kh_slide_network_create(kh_slide_layer* const* layers, int n_layers, int optimizer,
                             float momentum, float beta1, float beta2, float eps,
                             uint64_t rebuild_base, double rebuild_decay, kh_slide_network** out);
@@ -311,11 +310,24 @@ int kh_slide_network_destroy(kh_slide_network* n);
 int kh_slide_network_train_step(kh_slide_network* n, const float* x_dev, int64_t batch,
                                 const int64_t* label_off_host, const uint32_t* labels_host,
                                 double lr, float* loss_out, void* stream);
+/* Same with the examples' features as CSR rows (SparseVector, at most 4096
+ * stored entries each): row b is xidx/xval[xoff[b]..xoff[b+1]), densified as
+ * SparseVector::to_dense does (tensor/sparse.rs:77-83: a later entry at the
+ * same index overwrites an earlier one); indices >= input_dim are skipped. */
+int kh_slide_network_train_step_sparse(kh_slide_network* n, const int64_t* xoff_dev,
+                                       const uint32_t* xidx_dev, const float* xval_dev,
+                                       int64_t batch, const int64_t* label_off_host,
+                                       const uint32_t* labels_host, double lr, float* loss_out,
+                                       void* stream);
 /* Network::predict (net.rs:151-154) for each row of x_dev[batch][input_dim]:
  * out_dev[batch][num_neurons of the last layer], the last layer's dense
  * activations. */
 int kh_slide_network_predict(kh_slide_network* n, const float* x_dev, int64_t batch,
                              float* out_dev, void* stream);
+/* Same for CSR rows (as kh_slide_network_train_step_sparse reads them). */
+int kh_slide_network_predict_sparse(kh_slide_network* n, const int64_t* xoff_dev,
+                                    const uint32_t* xidx_dev, const float* xval_dev,
+                                    int64_t batch, float* out_dev, void* stream);
 /* Network::step (net.rs:13) and the scheduler's state. */
 int kh_slide_network_state(const kh_slide_network* n, uint64_t* step,
                            kh_rebuild_scheduler* scheduler);

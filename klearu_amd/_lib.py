@@ -100,6 +100,8 @@ SIGS = {
     "kh_slide_network_destroy": (I, [P]),
     "kh_slide_network_train_step": (I, [P, P, I64, P, P, C.c_double, P, P]),
     "kh_slide_network_predict": (I, [P, P, I64, P, P]),
+    "kh_slide_network_train_step_sparse": (I, [P, P, P, P, I64, P, P, C.c_double, P, P]),
+    "kh_slide_network_predict_sparse": (I, [P, P, P, P, I64, P, P]),
     "kh_slide_network_state": (I, [P, P, P]),
     "kh_dense_layer_create": (I, [I, I, P, P, I, PP]),
     "kh_dense_layer_destroy": (I, [P]),

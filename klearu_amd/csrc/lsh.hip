@@ -86,28 +86,47 @@ __global__ __launch_bounds__(kHashDenseMax) void hash_dense_kernel(
   for (int t = threadIdx.x; t < L; t += blockDim.x) codes[row * L + t] = cw[t];
 }
 
+// One block per (row, group of whole tables): each thread owns one plane of
+// the group and walks the row's entries in stored order, kHashSparseBatch at
+// a time (the entries' loads are the same for every lane; the plane bytes of
+// a batch are all in flight), adding +-x in order: the sum stays sequential.
+constexpr int kHashSparseBatch = 16;
 __global__ __launch_bounds__(kHashThreads) void hash_sparse_kernel(
     const int8_t* __restrict__ planes, int k, int L, int dim, const int64_t* __restrict__ xoff,
     const uint32_t* __restrict__ xidx, const float* __restrict__ xval,
     uint32_t* __restrict__ codes) {
-  __shared__ uint32_t cw[256];
+  __shared__ uint32_t cw[kHashThreads];
   const int64_t row = blockIdx.x;
+  const int tpb = kHashThreads / k;           // tables per block
+  const int t0 = blockIdx.y * tpb, t1 = min(L, t0 + tpb);
   const int64_t a = xoff[row], b = xoff[row + 1];
-  for (int t = threadIdx.x; t < L; t += blockDim.x) cw[t] = 0u;
+  for (int t = threadIdx.x; t < t1 - t0; t += blockDim.x) cw[t] = 0u;
   __syncthreads();
-  const int P = L * k;
-  for (int p = threadIdx.x; p < P; p += blockDim.x) {
+  const int p = t0 * k + threadIdx.x;
+  if (p < t1 * k) {
     const int8_t* pl = planes + (size_t)p * dim;
     float s = 0.0f;
-    for (int64_t e = a; e < b; ++e) {
-      const int8_t r = pl[xidx[e]];
-      if (r == 1) s = __fadd_rn(s, xval[e]);
-      else if (r == -1) s = __fsub_rn(s, xval[e]);
+    for (int64_t e0 = a; e0 < b; e0 += kHashSparseBatch) {
+      int8_t r[kHashSparseBatch];
+      float xv[kHashSparseBatch];
+#pragma unroll
+      for (int j = 0; j < kHashSparseBatch; ++j) {
+        const int64_t e = min(e0 + j, b - 1);
+        xv[j] = xval[e];
+        r[j] = pl[xidx[e]];
+      }
+#pragma unroll
+      for (int j = 0; j < kHashSparseBatch; ++j) {
+        if (e0 + j < b) {
+          if (r[j] == 1) s = __fadd_rn(s, xv[j]);
+          else if (r[j] == -1) s = __fsub_rn(s, xv[j]);
+        }
+      }
     }
-    if (s >= 0.0f) atomicOr(&cw[p / k], 1u << (p % k));
+    if (s >= 0.0f) atomicOr(&cw[p / k - t0], 1u << (p % k));
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < L; t += blockDim.x) codes[row * L + t] = cw[t];
+  for (int t = threadIdx.x; t < t1 - t0; t += blockDim.x) codes[row * L + t0 + t] = cw[t];
 }
 
 // (bucket key, insertion position) pairs: key = t * 2^k + (code_t & mask).
@@ -520,8 +539,9 @@ int hash_sparse_launch(const kh_hash_family* h, const int64_t* xoff, const uint3
                        const float* xval, int64_t batch, uint32_t* codes, hipStream_t st) {
   if (batch == 0) return KH_OK;
   KH_CHECK_ARG(h->L <= 256, "hash_sparse supports at most 256 tables");
-  hipLaunchKernelGGL(hash_sparse_kernel, dim3((unsigned)batch), dim3(kHashThreads), 0, st,
-                     h->planes_dev, h->k, h->L, h->dim, xoff, xidx, xval, codes);
+  const int tpb = kHashThreads / h->k;
+  hipLaunchKernelGGL(hash_sparse_kernel, dim3((unsigned)batch, ceil_div(h->L, tpb)), dim3(kHashThreads),
+                     0, st, h->planes_dev, h->k, h->L, h->dim, xoff, xidx, xval, codes);
   KH_LAUNCHED();
   return KH_OK;
 }

@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "exact_sum.hpp"
+#include "gather.hpp"
 #include "slide_internal.hpp"
 
 namespace kh {
@@ -29,7 +30,7 @@ namespace kh {
 constexpr int kTrThreads = 256;
 constexpr int kTrMaxLabels = 1024;   // labels of one example
 constexpr int kTrLdsNz = 8192;       // staged input nonzeros (beyond: read from global)
-constexpr int kTrMaxDim = 65536;     // network input / hidden widths
+constexpr int kTrMaxNnz = 4096;      // stored entries of one sparse example
 constexpr int kJTile = 2048;         // Jacobian: (s, go) pairs per LDS tile
 constexpr int kGTile = 1024;         // grad_input: (id, lg) pairs per LDS tile
 constexpr int kSmCH = 64, kSmM = 128;  // exact softmax sum: 8192 terms per pass
@@ -143,6 +144,69 @@ __global__ __launch_bounds__(1024) void tr_stage_nz_kernel(const float* __restri
   }
 }
 
+// Example::features.to_dense() (tensor/sparse.rs:77-83) of CSR row `row`:
+// later stored entries overwrite earlier ones at the same index, so after a
+// sort by (index, position) the last entry of each index is the value; the
+// nonzero values in ascending index order become the row's staged list, and
+// x_dense gets them (the previous row's entries are cleared first).  Entries
+// with index >= dim are skipped (to_dense would panic on them).
+__global__ __launch_bounds__(1024) void tr_stage_csr_kernel(
+    const int64_t* __restrict__ xoff, const uint32_t* __restrict__ xidx,
+    const float* __restrict__ xval, int64_t row, int dim, uint32_t* __restrict__ nzi,
+    float* __restrict__ nzv, int64_t* __restrict__ nzoff, float* __restrict__ x_dense) {
+  __shared__ uint64_t key[kTrMaxNnz];
+  __shared__ int wsum[16];
+  __shared__ int s_total;
+  const int old = static_cast<int>(nzoff[1]);
+  for (int i = threadIdx.x; i < old; i += blockDim.x) x_dense[nzi[i]] = 0.0f;
+  const int64_t a = xoff[row];
+  const int cnt = static_cast<int>(min<int64_t>(xoff[row + 1] - a, kTrMaxNnz));
+  int P = 1;
+  while (P < cnt) P <<= 1;
+  for (int i = threadIdx.x; i < P; i += blockDim.x)
+    key[i] = i < cnt ? (static_cast<uint64_t>(xidx[a + i]) << 32) | static_cast<uint32_t>(i) : ~0ull;
+  __syncthreads();
+  for (int k = 2; k <= P; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < P; i += blockDim.x) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const uint64_t x = key[i], y = key[ixj];
+          if ((x > y) == ((i & k) == 0)) {
+            key[i] = y;
+            key[ixj] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  int base = 0;
+  for (int c0 = 0; c0 < P; c0 += blockDim.x) {
+    const int i = c0 + threadIdx.x;
+    int keep = 0;
+    uint32_t idx = 0;
+    float v = 0.0f;
+    if (i < cnt) {
+      idx = static_cast<uint32_t>(key[i] >> 32);
+      const bool last = i + 1 == cnt || static_cast<uint32_t>(key[i + 1] >> 32) != idx;
+      v = xval[a + static_cast<uint32_t>(key[i])];
+      keep = last && v != 0.0f && idx < static_cast<uint32_t>(dim);
+    }
+    const int pos = block_excl_scan(keep, wsum, &s_total) + base;
+    if (keep) {
+      nzi[pos] = idx;
+      nzv[pos] = v;
+      x_dense[idx] = v;
+    }
+    base += s_total;
+  }
+  if (threadIdx.x == 0) {
+    nzoff[0] = 0;
+    nzoff[1] = base;
+  }
+}
+
 // Neuron::forward (neuron.rs:47-62) for one sample's active list: the
 // sequential sum of w*x over the staged nonzeros, + bias; then the
 // activation (not softmax) into post and the dense activation vector.
@@ -173,12 +237,12 @@ __global__ __launch_bounds__(kTrThreads) void tr_neuron_kernel(
     const float* w = W + static_cast<size_t>(id) * dim;
     float s = -0.0f;
     int e = 0;
-    for (; e + 8 <= nnz; e += 8) {  // eight loads in flight, added in order
-      float wv[8];
+    for (; e + 16 <= nnz; e += 16) {  // sixteen loads in flight, added in order
+      float wv[16];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) wv[q] = w[li[e + q]];
+      for (int q = 0; q < 16; ++q) wv[q] = w[li[e + q]];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) s = s + wv[q] * lv[e + q];
+      for (int q = 0; q < 16; ++q) s = s + wv[q] * lv[e + q];
     }
     for (; e < nnz; ++e) s = s + w[li[e]] * lv[e];
     const float z = s + bias[id];
@@ -193,27 +257,64 @@ __global__ __launch_bounds__(kTrThreads) void tr_neuron_kernel(
 
 // apply_softmax (layer.rs:286-308) over the active list in its order: max,
 // exp(z - max) with glibc's expf, the sequential sum (exact_seq_sum, 8192
-// terms a pass), then e / sum (or 1/n when the sum is not positive).
+// terms a pass), then e / sum (or 1/n when the sum is not positive).  Lists
+// of up to 8192 stay in registers (32 per thread, all loads in flight);
+// longer ones go through `post` in passes.
 __global__ __launch_bounds__(kTrThreads) void tr_softmax_kernel(const float* __restrict__ pre,
                                                                 const uint32_t* __restrict__ aids,
                                                                 const int32_t* __restrict__ alen,
                                                                 int cap, float* __restrict__ post,
                                                                 float* __restrict__ dense) {
+  constexpr int kPass = kSmCH * kSmM;
+  constexpr int kPer = kPass / kTrThreads;
   __shared__ EsLds<kSmCH, kSmM> es;
   __shared__ float red[kTrThreads / 64];
+  __shared__ uint64_t s_tab[32];  // kExp2Tab: the exps' table lookups stay in LDS
   const int n = min(alen[0], cap);
   if (n <= 0) return;
+  if (threadIdx.x < 32) s_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  float v[kPer];
   float mx = -INFINITY;
-  for (int a = threadIdx.x; a < n; a += blockDim.x) mx = fmaxf(mx, pre[a]);
+  if (n <= kPass) {
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) v[k] = pre[min(k * kTrThreads + static_cast<int>(threadIdx.x), n - 1)];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k)
+      v[k] = k * kTrThreads + static_cast<int>(threadIdx.x) < n ? v[k] : -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) mx = fmaxf(mx, v[k]);
+  } else {
+    for (int a = threadIdx.x; a < n; a += blockDim.x) mx = fmaxf(mx, pre[a]);
+  }
   mx = wave_max(mx);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
   __syncthreads();
   mx = red[0];
   for (int i = 1; i < kTrThreads / 64; ++i) mx = fmaxf(mx, red[i]);
-  for (int a = threadIdx.x; a < n; a += blockDim.x) post[a] = expf_glibc(pre[a] - mx);
-  __syncthreads();
-  constexpr int kPass = kSmCH * kSmM;
   float s = -0.0f;
+  if (n <= kPass) {
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int a = k * kTrThreads + threadIdx.x;
+      v[k] = a < n ? expf_glibc_t(v[k] - mx, s_tab) : -0.0f;
+      es.TP[es_slot<kSmCH, kSmM>(a)] = v[k];
+    }
+    __syncthreads();
+    s = exact_seq_sum<kTrThreads / 64, kSmCH, kSmM>(n, s, es);
+    const float u = 1.0f / static_cast<float>(n);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int a = k * kTrThreads + threadIdx.x;
+      if (a < n) {
+        const float r = s > 0.0f ? v[k] / s : u;
+        post[a] = r;
+        if (dense) dense[aids[a]] = r;
+      }
+    }
+    return;
+  }
+  for (int a = threadIdx.x; a < n; a += blockDim.x) post[a] = expf_glibc_t(pre[a] - mx, s_tab);
+  __syncthreads();
   for (int c0 = 0; c0 < n; c0 += kPass) {
     const int cnt = min(kPass, n - c0);
     for (int i = threadIdx.x; i < kPass; i += blockDim.x)
@@ -241,15 +342,19 @@ __global__ __launch_bounds__(kTrThreads) void tr_loss_grad_kernel(
     const float* __restrict__ dense, const uint32_t* __restrict__ labels, int nl,
     float* __restrict__ go, float* __restrict__ lg, float* __restrict__ loss_total) {
   __shared__ int found[kTrMaxLabels];
+  __shared__ uint32_t lab[kTrMaxLabels];
   const int n = min(alen[0], cap);
-  for (int l = threadIdx.x; l < nl; l += blockDim.x) found[l] = 0;
+  for (int l = threadIdx.x; l < nl; l += blockDim.x) {
+    found[l] = 0;
+    lab[l] = labels[l];
+  }
   __syncthreads();
   const float w = nl > 0 ? 1.0f / static_cast<float>(nl) : 0.0f;
   for (int a = threadIdx.x; a < n; a += blockDim.x) {
     const uint32_t id = aids[a];
     float g = nl > 0 ? post[a] : 0.0f;
     for (int l = 0; l < nl; ++l)
-      if (labels[l] == id) {
+      if (lab[l] == id) {
         g = g - w;
         found[l] = 1;
       }
@@ -262,7 +367,7 @@ __global__ __launch_bounds__(kTrThreads) void tr_loss_grad_kernel(
     if (nl > 0) {
       const float eps = 1e-7f;
       for (int l = 0; l < nl; ++l) {
-        const float prob = found[l] ? fmaxf(dense[labels[l]], eps) : eps;
+        const float prob = found[l] ? fmaxf(dense[lab[l]], eps) : eps;
         loss = loss - logf(prob);
       }
       loss = loss / static_cast<float>(nl);
@@ -273,35 +378,108 @@ __global__ __launch_bounds__(kTrThreads) void tr_loss_grad_kernel(
 
 // The softmax branch of Layer::backward (layer.rs:141-175): lane i runs the
 // sequential sum over j of go_j*s_j*(1-s_j) (j == i) or go_j*(-s_i*s_j).
+// One term of the Jacobian sum: go_j*s_j*(1-s_j) on the diagonal, else
+// go_j*(-s_i*s_j).
+__device__ __forceinline__ float jac_term(float gj, float sj, float nsi, bool diag) {
+  const float d = (gj * sj) * (1.0f - sj);
+  const float o = gj * (nsi * sj);
+  return diag ? d : o;
+}
+
 __global__ __launch_bounds__(kTrThreads) void tr_softmax_jacobian_kernel(
     const float* __restrict__ s, const float* __restrict__ go, const int32_t* __restrict__ alen,
     int cap, float* __restrict__ lg) {
-  __shared__ float ts[kJTile], tg[kJTile];
+  __shared__ __align__(16) float ts[kJTile];
+  __shared__ __align__(16) float tg[kJTile];
+  constexpr int kLd = kJTile / kTrThreads;
   const int n = min(alen[0], cap);
   if (static_cast<int>(blockIdx.x * blockDim.x) >= n) return;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  const float nsi = i < n ? -s[i] : 0.0f;
+  const float si = i < n ? s[i] : 0.0f;
+  const float nsi = -si;
+  const float gi = i < n ? go[i] : 0.0f;
+  const float dterm = (gi * si) * (1.0f - si);  // the diagonal term, j == i
+  // the wave's lanes hold i in [w0, w0 + 64): only that window of j needs the
+  // diagonal test; elsewhere every term is go_j * (-s_i * s_j)
+  const int w0 = __builtin_amdgcn_readfirstlane(i - static_cast<int>(threadIdx.x & 63));
   float r = 0.0f;
   for (int j0 = 0; j0 < n; j0 += kJTile) {
     const int cnt = min(kJTile, n - j0);
     __syncthreads();
-    for (int j = threadIdx.x; j < cnt; j += blockDim.x) {
-      ts[j] = s[j0 + j];
-      tg[j] = go[j0 + j];
+    {
+      float a[kLd], b[kLd];
+      // unconditional loads (clamped index), so that all of them are in flight
+#pragma unroll
+      for (int k = 0; k < kLd; ++k) {
+        const int j = min(k * kTrThreads + static_cast<int>(threadIdx.x), cnt - 1);
+        a[k] = s[j0 + j];
+        b[k] = go[j0 + j];
+      }
+#pragma unroll
+      for (int k = 0; k < kLd; ++k) {
+        const bool in = k * kTrThreads + static_cast<int>(threadIdx.x) < cnt;
+        a[k] = in ? a[k] : 0.0f;
+        b[k] = in ? b[k] : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < kLd; ++k) {
+        ts[k * kTrThreads + threadIdx.x] = a[k];
+        tg[k * kTrThreads + threadIdx.x] = b[k];
+      }
     }
     __syncthreads();
-    const int diag = i - j0;
-    for (int j = 0; j < cnt; ++j) {
-      const float sj = ts[j], gj = tg[j];
-      float t;
-      if (j == diag) {
-        t = gj * sj;
-        t = t * (1.0f - sj);
-      } else {
-        t = gj * (nsi * sj);
+    const float4* s4 = reinterpret_cast<const float4*>(ts);
+    const float4* g4 = reinterpret_cast<const float4*>(tg);
+    // [0, d0) and [d1, cnt): off-diagonal only; [d0, d1): the diagonal window
+    const int d0 = min(max(w0 - j0, 0), cnt) & ~3;
+    const int d1 = min(max(w0 + 64 - j0, 0), cnt);
+    // off-diagonal terms of [ja, ja + ((jb - ja) & ~15)), ja a multiple of 4;
+    // the next 16 (s, go) pairs are read while the current 16 are added
+    auto run16 = [&](int ja, int jb) {
+      const int je = ja + ((jb - ja) & ~15);
+      if (je == ja) return ja;
+      float4 sv[4], gv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        sv[q] = s4[(ja >> 2) + q];
+        gv[q] = g4[(ja >> 2) + q];
       }
-      r = r + t;
+      for (int j = ja; j < je; j += 16) {
+        float4 sn[4], gn[4];
+        const int jn = min(j + 16, kJTile - 16) >> 2;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          sn[q] = s4[jn + q];
+          gn[q] = g4[jn + q];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float t0 = gv[q].x * (nsi * sv[q].x);
+          const float t1 = gv[q].y * (nsi * sv[q].y);
+          const float t2 = gv[q].z * (nsi * sv[q].z);
+          const float t3 = gv[q].w * (nsi * sv[q].w);
+          r = r + t0;
+          r = r + t1;
+          r = r + t2;
+          r = r + t3;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          sv[q] = sn[q];
+          gv[q] = gn[q];
+        }
+      }
+      return je;
+    };
+    const int diag = i - j0;
+    int j = run16(0, d0);
+    for (; j < d1; ++j) {
+      const float o = tg[j] * (nsi * ts[j]);
+      r = r + (j == diag ? dterm : o);
     }
+    for (; j < cnt && (j & 3); ++j) r = r + tg[j] * (nsi * ts[j]);
+    j = run16(j, cnt);
+    for (; j < cnt; ++j) r = r + tg[j] * (nsi * ts[j]);
   }
   if (i < n) lg[i] = r;
 }
@@ -328,54 +506,90 @@ __global__ __launch_bounds__(kTrThreads) void tr_local_grad_kernel(
 
 // grad_input[j] = sum over the active list (in order, from +0.0) of
 // lg[a] * w[id_a][j], with the weights before this example's update
-// (layer.rs:203-207).  One lane per input dimension; each lane's sum is a chain.
+// (layer.rs:203-207).  Each j is one chain of |A| dependent adds, so each
+// block owns one column: all its threads gather the column's products
+// lg[a] * w[id_a][j] into LDS (kGTile at a time, every load of a tile in
+// flight at once), then one lane adds them in order, reading four per LDS
+// load.  The chains of all columns run on separate CUs.
+constexpr int kGTileRows = 16384;  // products staged per pass (64 KB)
 __global__ __launch_bounds__(kTrThreads) void tr_grad_input_kernel(
     const float* __restrict__ W, int dim, const uint32_t* __restrict__ aids,
     const int32_t* __restrict__ alen, int cap, const float* __restrict__ lg,
     float* __restrict__ gi) {
-  __shared__ uint32_t tid_[kGTile];
-  __shared__ float tlg[kGTile];
+  __shared__ __align__(16) float prod[kGTileRows];
   const int n = min(alen[0], cap);
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  const int j = blockIdx.x;
   float r = 0.0f;
-  for (int a0 = 0; a0 < n; a0 += kGTile) {
-    const int cnt = min(kGTile, n - a0);
+  for (int a0 = 0; a0 < n; a0 += kGTileRows) {
+    const int cnt = min(kGTileRows, n - a0);
     __syncthreads();
-    for (int a = threadIdx.x; a < cnt; a += blockDim.x) {
-      tid_[a] = aids[a0 + a];
-      tlg[a] = lg[a0 + a];
-    }
-    __syncthreads();
-    if (j < dim) {
-      int a = 0;
-      for (; a + 8 <= cnt; a += 8) {
-        float wv[8];
+    constexpr int kU = 8;
+    for (int b0 = 0; b0 < cnt; b0 += kTrThreads * kU) {
+      uint32_t id[kU];
+      float l[kU], w[kU];
+      // unconditional loads (clamped index), so that all of them are in flight
 #pragma unroll
-        for (int q = 0; q < 8; ++q) wv[q] = W[static_cast<size_t>(tid_[a + q]) * dim + j];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) r = r + tlg[a + q] * wv[q];
+      for (int u = 0; u < kU; ++u) {
+        const int a = min(b0 + u * kTrThreads + static_cast<int>(threadIdx.x), cnt - 1);
+        id[u] = aids[a0 + a];
+        l[u] = lg[a0 + a];
       }
-      for (; a < cnt; ++a) r = r + tlg[a] * W[static_cast<size_t>(tid_[a]) * dim + j];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) w[u] = W[static_cast<size_t>(id[u]) * dim + j];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int a = b0 + u * kTrThreads + threadIdx.x;
+        if (a < cnt) prod[a] = l[u] * w[u];
+      }
+    }
+    for (int a = cnt + threadIdx.x; a < ((cnt + 3) & ~3); a += kTrThreads) prod[a] = 0.0f;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      // eight LDS loads (32 products) ahead of the adds
+      const float4* p4 = reinterpret_cast<const float4*>(prod);
+      const int c32 = cnt >> 5;
+      float4 v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = p4[q];
+      for (int b = 0; b < c32; ++b) {
+        float4 nv[8];
+        const int nb = min(b + 1, kGTileRows / 32 - 1) * 8;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) nv[q] = p4[nb + q];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          r = r + v[q].x;
+          r = r + v[q].y;
+          r = r + v[q].z;
+          r = r + v[q].w;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = nv[q];
+      }
+      for (int a = c32 * 32; a < cnt; ++a) r = r + prod[a];
     }
   }
-  if (j < dim) gi[j] = r;
+  if (threadIdx.x == 0) gi[j] = r;
 }
 
 // Optimizer::update of every active neuron (layer.rs:209-222): grad_weights[j]
 // = lg * x[j] over all dim inputs (zeros included: momentum and Adam state
 // move every step), grad_bias = lg.  The transposed copy follows the rows.
+// Grid: x over 2048-column slices of a row, y over active neurons.
+constexpr int kUCols = 2048;
 __global__ __launch_bounds__(kTrThreads) void tr_update_kernel(
     float* __restrict__ W, float* __restrict__ WTN, float* __restrict__ bias, int n, int dim,
     const uint32_t* __restrict__ aids, const int32_t* __restrict__ alen, int cap,
     const float* __restrict__ lg, const float* __restrict__ x, OptArgs o) {
   const int na = min(alen[0], cap);
-  for (int a = blockIdx.x; a < na; a += gridDim.x) {
+  const int j0 = blockIdx.x * kUCols, j1 = min(dim, j0 + kUCols);
+  for (int a = blockIdx.y; a < na; a += gridDim.y) {
     const uint32_t id = aids[a];
     if (id >= static_cast<uint32_t>(n)) continue;
     const float g = lg[a];
     const size_t row = static_cast<size_t>(id) * dim;
     float* w = W + row;
-    for (int j = threadIdx.x; j < dim; j += blockDim.x) {
+    for (int j = j0 + threadIdx.x; j < j1; j += blockDim.x) {
       const float gw = g * x[j];
       float* s1 = o.st_w1 ? o.st_w1 + row + j : nullptr;
       float* s2 = o.st_w2 ? o.st_w2 + row + j : nullptr;
@@ -383,7 +597,7 @@ __global__ __launch_bounds__(kTrThreads) void tr_update_kernel(
       w[j] = nw;
       if (WTN) WTN[static_cast<size_t>(j) * n + id] = nw;
     }
-    if (threadIdx.x == 0) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
       float* s1 = o.st_b1 ? o.st_b1 + id : nullptr;
       float* s2 = o.st_b2 ? o.st_b2 + id : nullptr;
       bias[id] = opt_step(bias[id], g, s1, s2, o);
@@ -393,11 +607,14 @@ __global__ __launch_bounds__(kTrThreads) void tr_update_kernel(
 
 // Local gradients -> (grad_input) -> update of one layer for one example.
 // x: the layer's dense input; post: activations in list order (softmax only).
+// keep_wtn: write updated rows into the transposed copy too (scattered
+// 4-byte stores, one per weight); a network step instead re-transposes once
+// after the whole batch (wtn_refresh).
 static int layer_backward_launch(kh_slide_layer* l, const float* x, const uint32_t* aids,
                                  const int32_t* alen, int cap, const float* pre,
                                  const float* post, const float* dense, const float* grad_out,
                                  int64_t grad_len, bool lg_ready, float* go, float* lg,
-                                 const OptArgs& o, float* gi, hipStream_t st) {
+                                 const OptArgs& o, float* gi, bool keep_wtn, hipStream_t st) {
   const unsigned ab = static_cast<unsigned>(ceil_div(cap, kTrThreads));
   if (!lg_ready) {
     hipLaunchKernelGGL(tr_local_grad_kernel, dim3(ab), dim3(kTrThreads), 0, st, aids, alen, cap,
@@ -410,12 +627,23 @@ static int layer_backward_launch(kh_slide_layer* l, const float* x, const uint32
     KH_LAUNCHED();
   }
   if (gi) {
-    hipLaunchKernelGGL(tr_grad_input_kernel, dim3(ceil_div(l->dim, kTrThreads)), dim3(kTrThreads),
-                       0, st, l->w, l->dim, aids, alen, cap, lg, gi);
+    hipLaunchKernelGGL(tr_grad_input_kernel, dim3(l->dim), dim3(kTrThreads), 0, st, l->w, l->dim,
+                       aids, alen, cap, lg, gi);
     KH_LAUNCHED();
   }
-  hipLaunchKernelGGL(tr_update_kernel, dim3(std::min(cap, 1024)), dim3(kTrThreads), 0, st, l->w,
-                     l->wtn, l->bias, l->n, l->dim, aids, alen, cap, lg, x, o);
+  const int xs = ceil_div(l->dim, kUCols);
+  const int ys = std::max(1, std::min(cap, std::max(1, 4096 / xs)));
+  hipLaunchKernelGGL(tr_update_kernel, dim3(xs, ys), dim3(kTrThreads), 0, st, l->w,
+                     keep_wtn ? l->wtn : nullptr, l->bias, l->n, l->dim, aids, alen, cap, lg, x, o);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
+// The transposed copy of a non-softmax layer rebuilt from the weights.
+static int wtn_refresh(kh_slide_layer* l, hipStream_t st) {
+  if (!l->wtn) return KH_OK;
+  hipLaunchKernelGGL(transpose_kernel<float>, dim3(ceil_div(l->dim, 32), ceil_div(l->n, 32)), dim3(256),
+                     0, st, l->w, l->n, l->dim, l->wtn);
   KH_LAUNCHED();
   return KH_OK;
 }
@@ -572,7 +800,7 @@ extern "C" int kh_slide_layer_backward(kh_slide_layer* l, const float* x_dev,
   }
   return layer_backward_launch(l, x_dev, act_ids_dev, n_act_dev, cap, pre_dev, post,
                                act_dense_dev, grad_out_dev, grad_out_len, false, go, lg,
-                               opt_args(l, lr, step), grad_in_dev, st);
+                               opt_args(l, lr, step), grad_in_dev, true, st);
 }
 
 // ======================================================================== network
@@ -606,6 +834,7 @@ struct kh_slide_network {
   uint64_t step = 0;
   kh_rebuild_scheduler sched{};
   float* loss_total = nullptr;
+  float* x_dense = nullptr;  // [in_dim] the current sparse example, densified
   uint32_t* labels = nullptr;
   size_t labels_cap = 0;
   int in_dim = 0, out_dim = 0;
@@ -635,8 +864,6 @@ extern "C" int kh_slide_network_create(kh_slide_layer* const* layers, int n_laye
   *out = nullptr;
   for (int i = 0; i < n_layers; ++i) {
     KH_CHECK_ARG(layers[i] != nullptr, "null layer %d", i);
-    KH_CHECK_ARG(layers[i]->dim <= kTrMaxDim, "layer %d input_dim %d > %d", i, layers[i]->dim,
-                 kTrMaxDim);
     KH_CHECK_ARG(i == 0 || layers[i]->dim == layers[i - 1]->n,
                  "layer %d input_dim %d != layer %d num_neurons %d", i, layers[i]->dim, i - 1,
                  layers[i - 1]->n);
@@ -679,7 +906,8 @@ extern "C" int kh_slide_network_create(kh_slide_layer* const* layers, int n_laye
   }
   if (rc == KH_OK) {
     net->loss_total = net->alloc<float>(1, true);
-    if (!net->loss_total) rc = KH_ERR_ALLOC;
+    net->x_dense = net->alloc<float>(net->in_dim, true);
+    if (!net->loss_total || !net->x_dense) rc = KH_ERR_ALLOC;
   }
   if (rc != KH_OK) {
     kh_slide_network_destroy(net);
@@ -689,17 +917,43 @@ extern "C" int kh_slide_network_create(kh_slide_layer* const* layers, int n_laye
   return KH_OK;
 }
 
+// Stage example e of a CSR batch as layer 0's input (to_dense semantics).
+static int net_stage_sparse(kh_slide_network* net, const int64_t* xoff, const uint32_t* xidx,
+                            const float* xval, int64_t e, hipStream_t st) {
+  TrainBufs& t = net->b[0];
+  hipLaunchKernelGGL(tr_stage_csr_kernel, dim3(1), dim3(1024), 0, st, xoff, xidx, xval, e,
+                     net->in_dim, t.nzi, t.nzv, t.xoff, net->x_dense);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
+// Host check of a CSR batch: offsets nondecreasing, at most kTrMaxNnz stored
+// entries per example (reads the offsets back; synchronous).
+static int net_check_csr(const int64_t* xoff, int64_t batch, hipStream_t st) {
+  std::vector<int64_t> off(batch + 1);
+  KH_HIP(hipMemcpyAsync(off.data(), xoff, sizeof(int64_t) * (batch + 1), hipMemcpyDeviceToHost, st));
+  KH_HIP(hipStreamSynchronize(st));
+  for (int64_t e = 0; e < batch; ++e)
+    KH_CHECK_ARG(off[e + 1] >= off[e] && off[e + 1] - off[e] <= kTrMaxNnz,
+                 "example %lld: offsets must be nondecreasing with at most %d entries", (long long)e,
+                 kTrMaxNnz);
+  return KH_OK;
+}
+
 // Network::forward for one example (net.rs:62-78), layer by layer: nonzeros of
 // the input, hash, query, sampling in the sampler's order (clearing the
 // previous example's entries of the dense activations), neuron sums, softmax.
+// x == nullptr: layer 0's input was staged from a sparse example.
 static int net_forward_one(kh_slide_network* net, const float* x, hipStream_t st) {
   const float* in = x;
   for (size_t i = 0; i < net->layers.size(); ++i) {
     kh_slide_layer* l = net->layers[i];
     TrainBufs& t = net->b[i];
-    hipLaunchKernelGGL(tr_stage_nz_kernel, dim3(1), dim3(1024), 0, st, in, l->dim, t.nzi, t.nzv,
-                       t.xoff);
-    KH_LAUNCHED();
+    if (in) {
+      hipLaunchKernelGGL(tr_stage_nz_kernel, dim3(1), dim3(1024), 0, st, in, l->dim, t.nzi, t.nzv,
+                         t.xoff);
+      KH_LAUNCHED();
+    }
     int rc = hash_sparse_launch(l->index->h, t.xoff, t.nzi, t.nzv, 1, t.codes, st);
     if (rc != KH_OK) return rc;
     const int qs = query_stride(l->index);
@@ -735,15 +989,16 @@ static int net_setup_attrs() {
   return rc;
 }
 
-extern "C" int kh_slide_network_train_step(kh_slide_network* net, const float* x_dev, int64_t batch,
-                                           const int64_t* label_off_host,
-                                           const uint32_t* labels_host, double lr, float* loss_out,
-                                           void* stream) {
+// Network::train_step over dense rows (x_dev) or CSR rows (xoff != nullptr).
+static int net_train_step(kh_slide_network* net, const float* x_dev, const int64_t* xoff,
+                          const uint32_t* xidx, const float* xval, int64_t batch,
+                          const int64_t* label_off_host, const uint32_t* labels_host, double lr,
+                          float* loss_out, void* stream) {
   KH_CHECK_ARG(net && loss_out, "null argument");
   KH_CHECK_ARG(batch >= 0, "bad batch");
   *loss_out = 0.0f;
   if (batch == 0) return KH_OK;  // net.rs:82-84: nothing changes
-  KH_CHECK_ARG(x_dev && label_off_host, "null input");
+  KH_CHECK_ARG((x_dev || xoff) && label_off_host, "null input");
   KH_CHECK_ARG(label_off_host[0] == 0, "label offsets must start at 0");
   for (int64_t e = 0; e < batch; ++e)
     KH_CHECK_ARG(label_off_host[e + 1] >= label_off_host[e] &&
@@ -755,6 +1010,10 @@ extern "C" int kh_slide_network_train_step(kh_slide_network* net, const float* x
   int rc = net_setup_attrs();
   if (rc != KH_OK) return rc;
   hipStream_t st = as_stream(stream);
+  if (xoff) {
+    rc = net_check_csr(xoff, batch, st);
+    if (rc != KH_OK) return rc;
+  }
   if (static_cast<size_t>(n_labels) > net->labels_cap) {
     KH_HIP(hipStreamSynchronize(st));
     dev_free(net->labels);
@@ -774,8 +1033,12 @@ extern "C" int kh_slide_network_train_step(kh_slide_network* net, const float* x
   std::vector<OptArgs> oa(nl_layers);
   for (int i = 0; i < nl_layers; ++i) oa[i] = opt_args(net->layers[i], lr, net->step);
   for (int64_t e = 0; e < batch; ++e) {
-    const float* x = x_dev + e * static_cast<int64_t>(net->in_dim);
-    rc = net_forward_one(net, x, st);
+    const float* x = xoff ? net->x_dense : x_dev + e * static_cast<int64_t>(net->in_dim);
+    if (xoff) {
+      rc = net_stage_sparse(net, xoff, xidx, xval, e, st);
+      if (rc != KH_OK) return rc;
+    }
+    rc = net_forward_one(net, xoff ? nullptr : x, st);
     if (rc != KH_OK) return rc;
     const int last = nl_layers - 1;
     kh_slide_layer* L = net->layers[last];
@@ -794,9 +1057,13 @@ extern "C" int kh_slide_network_train_step(kh_slide_network* net, const float* x
       // the first layer's grad_input is not used by anything (net.rs:139-144)
       float* gi = i == 0 ? nullptr : t.gi;
       rc = layer_backward_launch(l, in, t.aids, t.alen, t.as, t.pre, t.post, t.dense, grad_out,
-                                 l->n, i == last, t.go, t.lg, oa[i], gi, st);
+                                 l->n, i == last, t.go, t.lg, oa[i], gi, false, st);
       if (rc != KH_OK) return rc;
     }
+  }
+  for (kh_slide_layer* l : net->layers) {
+    rc = wtn_refresh(l, st);
+    if (rc != KH_OK) return rc;
   }
   float total = 0.0f;
   KH_HIP(hipMemcpyAsync(&total, net->loss_total, sizeof(float), hipMemcpyDeviceToHost, st));
@@ -812,22 +1079,61 @@ extern "C" int kh_slide_network_train_step(kh_slide_network* net, const float* x
   return KH_OK;
 }
 
-extern "C" int kh_slide_network_predict(kh_slide_network* net, const float* x_dev, int64_t batch,
-                                        float* out_dev, void* stream) {
+extern "C" int kh_slide_network_train_step(kh_slide_network* net, const float* x_dev, int64_t batch,
+                                           const int64_t* label_off_host,
+                                           const uint32_t* labels_host, double lr, float* loss_out,
+                                           void* stream) {
+  KH_CHECK_ARG(batch == 0 || x_dev, "null input");
+  return net_train_step(net, x_dev, nullptr, nullptr, nullptr, batch, label_off_host, labels_host,
+                        lr, loss_out, stream);
+}
+
+extern "C" int kh_slide_network_train_step_sparse(kh_slide_network* net, const int64_t* xoff_dev,
+                                                  const uint32_t* xidx_dev, const float* xval_dev,
+                                                  int64_t batch, const int64_t* label_off_host,
+                                                  const uint32_t* labels_host, double lr,
+                                                  float* loss_out, void* stream) {
+  KH_CHECK_ARG(batch == 0 || xoff_dev, "null input");
+  return net_train_step(net, nullptr, xoff_dev, xidx_dev, xval_dev, batch, label_off_host,
+                        labels_host, lr, loss_out, stream);
+}
+
+static int net_predict(kh_slide_network* net, const float* x_dev, const int64_t* xoff,
+                       const uint32_t* xidx, const float* xval, int64_t batch, float* out_dev,
+                       void* stream) {
   KH_CHECK_ARG(net != nullptr, "null network");
   KH_CHECK_ARG(batch >= 0, "bad batch");
   if (batch == 0) return KH_OK;
-  KH_CHECK_ARG(x_dev && out_dev, "null argument");
+  KH_CHECK_ARG((x_dev || xoff) && out_dev, "null argument");
   int rc = net_setup_attrs();
   if (rc != KH_OK) return rc;
   hipStream_t st = as_stream(stream);
+  if (xoff) {
+    rc = net_check_csr(xoff, batch, st);
+    if (rc != KH_OK) return rc;
+  }
   for (int64_t e = 0; e < batch; ++e) {
-    rc = net_forward_one(net, x_dev + e * static_cast<int64_t>(net->in_dim), st);
+    if (xoff) {
+      rc = net_stage_sparse(net, xoff, xidx, xval, e, st);
+      if (rc != KH_OK) return rc;
+    }
+    rc = net_forward_one(net, xoff ? nullptr : x_dev + e * static_cast<int64_t>(net->in_dim), st);
     if (rc != KH_OK) return rc;
     KH_HIP(hipMemcpyAsync(out_dev + e * static_cast<int64_t>(net->out_dim), net->b.back().dense,
                           sizeof(float) * net->out_dim, hipMemcpyDeviceToDevice, st));
   }
   return KH_OK;
+}
+
+extern "C" int kh_slide_network_predict(kh_slide_network* net, const float* x_dev, int64_t batch,
+                                        float* out_dev, void* stream) {
+  return net_predict(net, x_dev, nullptr, nullptr, nullptr, batch, out_dev, stream);
+}
+
+extern "C" int kh_slide_network_predict_sparse(kh_slide_network* net, const int64_t* xoff_dev,
+                                               const uint32_t* xidx_dev, const float* xval_dev,
+                                               int64_t batch, float* out_dev, void* stream) {
+  return net_predict(net, nullptr, xoff_dev, xidx_dev, xval_dev, batch, out_dev, stream);
 }
 
 extern "C" int kh_slide_network_state(const kh_slide_network* net, uint64_t* step,

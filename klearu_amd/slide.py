@@ -206,6 +206,29 @@ class Network:
                   float(lr), C.byref(loss), stream_ptr(stream))
         return float(loss.value)
 
+    def train_step_sparse(self, vectors, labels, lr, csr=None, stream=None) -> float:
+        """train_step with each example's features as a SparseVector (densified
+        as SparseVector::to_dense does); csr=(off, idx, val) device arrays
+        instead of `vectors` skips the host conversion."""
+        off, idx, val = csr if csr is not None else csr_batch(vectors)
+        B = off.numel() - 1
+        loff = np.zeros(B + 1, np.int64)
+        for i, lab in enumerate(labels[:B]):
+            loff[i + 1] = loff[i] + len(lab)
+        flat = np.ascontiguousarray(np.concatenate([np.asarray(l, np.uint32) for l in labels[:B]] or
+                                                   [np.zeros(0, np.uint32)]), np.uint32)
+        loss = C.c_float()
+        _lib.call("kh_slide_network_train_step_sparse", self._h, ptr(off), ptr(idx), ptr(val), B, hptr(loff),
+                  hptr(flat) if flat.size else None, float(lr), C.byref(loss), stream_ptr(stream))
+        return float(loss.value)
+
+    def predict_sparse(self, vectors, stream=None) -> torch.Tensor:
+        off, idx, val = csr_batch(vectors)
+        out = torch.empty(len(vectors), self.layers[-1].config.num_neurons, dtype=torch.float32, device="cuda")
+        _lib.call("kh_slide_network_predict_sparse", self._h, ptr(off), ptr(idx), ptr(val), len(vectors), ptr(out),
+                  stream_ptr(stream))
+        return out
+
     def predict_batch(self, X, stream=None) -> torch.Tensor:
         """Network::predict (net.rs:151-154) per row: the last layer's dense activations."""
         X = to_device(X, np.float32).reshape(-1, self.layers[0].config.input_dim)

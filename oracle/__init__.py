@@ -566,7 +566,15 @@ class SlideNetOracle:
             l["st_b1"] = np.zeros(n, np.float32)
             l["st_b2"] = np.zeros(n, np.float32)
             self.layers.append(l)
-            self.rebuild_layer(l)
+            if spec.get("index") is not None:
+                # a prebuilt index (e.g. downloaded from the GPU, whose buckets
+                # the tests pin bit-exact): data [L][2^K][cap], len, count
+                d, ln, cnt = spec["index"]
+                l["index"].data[:] = np.ascontiguousarray(d, np.uint32).reshape(-1)
+                l["index"].len[:] = np.ascontiguousarray(ln, np.uint32).reshape(-1)
+                l["index"].count[:] = np.ascontiguousarray(cnt, np.uint64).reshape(-1)
+            else:
+                self.rebuild_layer(l)
         self.opt, self.momentum, self.beta1, self.beta2, self.eps = optimizer, momentum, beta1, beta2, eps
         self.step = 0
         self.scheduler = RebuildScheduler(rebuild_base, rebuild_decay)

@@ -189,3 +189,34 @@ def test_rebuild_scheduler_and_index_rebuild(kh, orc):
             np.testing.assert_array_equal(d[t, b, :ln[t, b]], od[t, b, :ln[t, b]])
     idx.rebuild([])
     assert idx.buckets()[1].sum() == 0
+
+
+def test_sparse_examples_match_dense_training(kh, orc):
+    """train_step_sparse densifies each example as SparseVector::to_dense does
+    (unsorted entries, repeated indices: the later value wins, explicit zeros):
+    the same weights as training on the dense rows."""
+    from klearu_amd.lsh import SparseVector
+    rng = np.random.default_rng(31)
+    specs = [spec(rng, 200, 64, "Relu", top_k=48, k=5, L=6, cap=32, seed=61),
+             spec(rng, 64, 40, "Softmax", top_k=16, k=5, L=6, cap=32, seed=62)]
+    net, layers, onet = build(orc, specs, "Adam")
+    B = 12
+    vecs, X = [], np.zeros((B, 200), F)
+    for r in range(B):
+        idx = rng.choice(200, 30, replace=False)
+        val = rng.random(30).astype(F)
+        val[:3] = 0.0
+        idx = np.concatenate([idx, idx[5:9]])          # repeats: these later values win
+        val = np.concatenate([val, rng.random(4).astype(F)])
+        for i, v in zip(idx, val):
+            X[r, i] = v
+        vecs.append(SparseVector(idx.astype(np.uint32), val, 200))
+    labels = [[int(rng.integers(0, 40))] for _ in range(B)]
+    for step in range(2):
+        got = net.train_step_sparse(vecs, labels, 0.01)
+        want = onet.train_step(X, labels, 0.01)
+        assert got == pytest.approx(want, rel=1e-5)
+        check_same(layers, onet, f"sparse step {step}")
+    p = net.predict_sparse(vecs[:4]).cpu().numpy()
+    for i in range(4):
+        np.testing.assert_array_equal(p[i], onet.predict(X[i]))
