@@ -652,6 +652,34 @@ int kh_predictor_write_json(const char* path, int input_dim, int hidden_dim, int
                             const float* b2_host);
 /* kh_predictor_write_json of a predictor handle's weights (synchronous). */
 int kh_predictor_save(const kh_predictor* p, const char* path);
+
+/* LibSvmDataset (crates/klearu-core/src/data/libsvm.rs:31-183): a LibSVM /
+ * extreme-classification text file (`l1,l2,... idx:val ...` per line) parsed
+ * on the host as the reference parses it: blank and '#' lines skipped, an
+ * inline '#' token ends a line, 1-based indices detected and shifted (no
+ * index 0 anywhere and the smallest index 1), indices >= feature_dim clamped
+ * to feature_dim - 1, each example's pairs sorted by index with repeated
+ * indices summed (SparseVector::from_pairs).  Parse errors return KH_ERR_ARG
+ * with "line N: ..." as the reference's messages (:125-175). */
+typedef struct kh_libsvm kh_libsvm;
+int kh_libsvm_load(const char* path, int64_t feature_dim, int64_t num_labels, kh_libsvm** out);
+/* load_from_reader over an in-memory buffer of `len` bytes. */
+int kh_libsvm_parse(const char* data, int64_t len, int64_t feature_dim, int64_t num_labels,
+                    kh_libsvm** out);
+int kh_libsvm_free(kh_libsvm* ds);
+/* Examples, stored feature entries, labels in total, feature_dim, num_labels
+ * (any pointer may be NULL). */
+int kh_libsvm_dims(const kh_libsvm* ds, int64_t* n, int64_t* nnz, int64_t* n_labels,
+                   int64_t* feature_dim, int64_t* num_labels);
+/* Host copies: features as CSR off[n+1] / idx[nnz] / val[nnz] and labels as
+ * CSR label_off[n+1] / labels[n_labels] (any pointer may be NULL). */
+int kh_libsvm_copy(const kh_libsvm* ds, int64_t* off, uint32_t* idx, float* val,
+                   int64_t* label_off, uint32_t* labels);
+/* Examples [row0, row0 + rows) as device CSR (offsets from 0), the layout
+ * kh_slide_network_train_step_sparse and the *_sparse entry points read.
+ * Synchronous. */
+int kh_libsvm_upload(const kh_libsvm* ds, int64_t row0, int64_t rows, int64_t* off_dev,
+                     uint32_t* idx_dev, float* val_dev, void* stream);
 /* The handle's dims, and its weights copied back to host arrays w1[hidden][input],
  * b1[hidden], w2[output][hidden], b2[output] (synchronous). */
 int kh_predictor_dims(const kh_predictor* p, int* input_dim, int* hidden_dim, int* output_dim);

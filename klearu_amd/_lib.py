@@ -103,6 +103,12 @@ SIGS = {
     "kh_slide_network_train_step_sparse": (I, [P, P, P, P, I64, P, P, C.c_double, P, P]),
     "kh_slide_network_predict_sparse": (I, [P, P, P, P, I64, P, P]),
     "kh_slide_network_state": (I, [P, P, P]),
+    "kh_libsvm_load": (I, [S, I64, I64, PP]),
+    "kh_libsvm_parse": (I, [C.c_char_p, I64, I64, I64, PP]),
+    "kh_libsvm_free": (I, [P]),
+    "kh_libsvm_dims": (I, [P, P, P, P, P, P]),
+    "kh_libsvm_copy": (I, [P, P, P, P, P, P]),
+    "kh_libsvm_upload": (I, [P, I64, I64, P, P, P, P]),
     "kh_dense_layer_create": (I, [I, I, P, P, I, PP]),
     "kh_dense_layer_destroy": (I, [P]),
     "kh_dense_layer_forward_sparse": (I, [P, P, P, P, I64, P, P]),
