@@ -112,6 +112,39 @@ int kh_hash_family_destroy(kh_hash_family* h);
 int kh_hash_family_dims(const kh_hash_family* h, int* k, int* input_dim, int* num_tables);
 /* Copies the planes back as planes_host[num_tables][k][input_dim]. */
 int kh_hash_family_planes(const kh_hash_family* h, int8_t* planes_host);
+/* The rank-based families (crates/klearu-core/src/hash/wta.rs, dwta.rs,
+ * minhash.rs).  Their codes, as kh_hash_dense / kh_hash_sparse return them,
+ * are the low 32 bits of the reference's u64 code (an index keeps the low k).
+ * WtaHash::new(input_dim, k, num_tables, window_size, seed) (wta.rs:42-90):
+ * per table and hash function, the first window_size entries of a shuffle
+ * of 0..input_dim (rand 0.8.5 SliceRandom::shuffle on StdRng); k *
+ * ceil(log2(window_size)) <= 64.  The composed seed -> window stream is
+ * restated, not pinned by a reference value; kh_wta_from_windows takes
+ * windows drawn by the reference itself. */
+int kh_wta_create(int input_dim, int k, int num_tables, int window_size, uint64_t seed,
+                  kh_hash_family** out);
+/* DwtaHash::new (dwta.rs:40-88): WTA's windows; sparse inputs (sorted,
+ * distinct indices, as SparseVector holds them) hash over stored dimensions
+ * only, an empty window taking DefaultHasher((table, hash_fn)) % window_size. */
+int kh_dwta_create(int input_dim, int k, int num_tables, int window_size, uint64_t seed,
+                   kh_hash_family** out);
+/* WTA (dwta = 0) or DWTA (dwta = 1) from windows_host[num_tables][k][window_size]. */
+int kh_wta_from_windows(int dwta, int input_dim, int k, int num_tables, int window_size,
+                        const uint32_t* windows_host, kh_hash_family** out);
+/* MinHash::new (minhash.rs:38-60): one shuffled 0..input_dim per table; k bins. */
+int kh_minhash_create(int input_dim, int k, int num_tables, uint64_t seed, kh_hash_family** out);
+/* MinHash from perms_host[num_tables][input_dim] (permutations[table][dim]). */
+int kh_minhash_from_permutations(int input_dim, int k, int num_tables, const uint32_t* perms_host,
+                                 kh_hash_family** out);
+#define KH_FAMILY_TERNARY 0 /* SimHash / SparseRandomProjection hyperplanes */
+#define KH_FAMILY_WTA 1
+#define KH_FAMILY_DWTA 2
+#define KH_FAMILY_MINHASH 3
+/* The family's kind and window size (0 unless WTA / DWTA). */
+int kh_hash_family_kind(const kh_hash_family* h, int* kind, int* window_size);
+/* Copy WTA / DWTA windows [L][k][window_size] or MinHash permutations
+ * [L][input_dim] (KH_ERR_UNSUPPORTED for hyperplane families). */
+int kh_hash_family_tables(const kh_hash_family* h, uint32_t* out_host);
 /* HashFamily::hash_dense (hash/mod.rs:26) for every table and a batch:
  * codes[b][t] = hash_dense(x[b], t), x_dev [batch][input_dim]. */
 int kh_hash_dense(const kh_hash_family* h, const float* x_dev, int64_t batch, uint32_t* codes_dev,
@@ -182,6 +215,14 @@ int kh_lsh_index_query_sparse(const kh_lsh_index* idx, const int64_t* xoff_dev,
                               const uint32_t* xidx_dev, const float* xval_dev, int64_t batch,
                               int64_t* off_dev, uint32_t* ids_dev, uint32_t* counts_dev,
                               int64_t capacity, void* stream);
+/* LshSparsityPredictor::predict (crates/klearu-dejavu/src/predictor/
+ * lsh_predictor.rs:33-43) for a batch of dense inputs: the query's candidates
+ * sorted by hit count descending (ties: ascending id; the reference's follow
+ * HashMap order), the first top_k: ids_dev[batch][top_k] with n_dev[b] of them
+ * valid.  (build_from_observations, :22-30, is kh_lsh_index_clear then
+ * kh_lsh_index_insert of each observation's input once per important id.) */
+int kh_lsh_index_query_top_k(const kh_lsh_index* idx, const float* x_dev, int64_t batch,
+                             int64_t top_k, uint32_t* ids_dev, int32_t* n_dev, void* stream);
 /* Bucket contents for parity checks (synchronous): data_host[L][2^k][cap],
  * len_host[L][2^k], count_host[L][2^k] (reservoir insertion counters). */
 int kh_lsh_index_buckets(const kh_lsh_index* idx, uint32_t* data_host, uint32_t* len_host,
@@ -225,6 +266,18 @@ int kh_slide_layer_forward_sparse(const kh_slide_layer* l, const int64_t* xoff_d
                                   const uint32_t* xidx_dev, const float* xval_dev, int64_t batch,
                                   int64_t* off_dev, uint32_t* act_ids_dev, float* pre_dev,
                                   float* act_dev, int64_t capacity, void* stream);
+/* SparseInferenceEngine::infer (relu = 1) / infer_linear (relu = 0)
+ * (crates/klearu-bolt/src/sparse_inference.rs:36-111) over the layer's index
+ * and weights: effective_k = (base_top_k as f32 * sparsity_multiplier) as
+ * usize; the query's candidates sorted by hit count (descending; the
+ * reference's ties follow HashMap order, here ascending id), the first
+ * effective_k of them with id < num_neurons, each the sequential dot of x and
+ * its weights plus bias, then max(0) for infer.  No all-neurons fallback:
+ * an empty candidate set gives an empty row.  Output CSR as
+ * kh_slide_layer_forward (ids in that order; act_dev may be NULL). */
+int kh_sparse_inference(const kh_slide_layer* l, const float* x_dev, int64_t batch,
+                        int64_t base_top_k, float sparsity_multiplier, int relu, int64_t* off_dev,
+                        uint32_t* ids_dev, float* act_dev, int64_t capacity, void* stream);
 
 /* Dense layer over sparse inputs: y[b][o] = act(Neuron::forward_sparse) for all
  * neurons (the 128-d hidden layer of the extreme-classification net).

@@ -109,6 +109,15 @@ SIGS = {
     "kh_libsvm_dims": (I, [P, P, P, P, P, P]),
     "kh_libsvm_copy": (I, [P, P, P, P, P, P]),
     "kh_libsvm_upload": (I, [P, I64, I64, P, P, P, P]),
+    "kh_wta_create": (I, [I, I, I, I, U64, PP]),
+    "kh_dwta_create": (I, [I, I, I, I, U64, PP]),
+    "kh_wta_from_windows": (I, [I, I, I, I, I, P, PP]),
+    "kh_minhash_create": (I, [I, I, I, U64, PP]),
+    "kh_minhash_from_permutations": (I, [I, I, I, P, PP]),
+    "kh_hash_family_kind": (I, [P, P, P]),
+    "kh_hash_family_tables": (I, [P, P]),
+    "kh_sparse_inference": (I, [P, P, I64, I64, F, I, P, P, P, I64, P]),
+    "kh_lsh_index_query_top_k": (I, [P, P, I64, I64, P, P, P]),
     "kh_dense_layer_create": (I, [I, I, P, P, I, PP]),
     "kh_dense_layer_destroy": (I, [P]),
     "kh_dense_layer_forward_sparse": (I, [P, P, P, P, I64, P, P]),

@@ -523,6 +523,7 @@ __global__ void csr_copy_f32_kernel(const float* __restrict__ src, int stride,
 int hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx, int64_t batch,
                       uint32_t* codes, hipStream_t st) {
   if (batch == 0) return KH_OK;
+  if (h->kind != KH_FAMILY_TERNARY) return rank_hash_dense_launch(h, x, ldx, batch, codes, st);
   const int in_lds = h->dim <= 12288 ? 1 : 0;
   const size_t lds = sizeof(float) * (in_lds ? h->dim : 0) + sizeof(uint32_t) * h->L;
   for (int64_t b0 = 0; b0 < batch; b0 += 65535 * 16) {
@@ -538,6 +539,7 @@ int hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx, int6
 int hash_sparse_launch(const kh_hash_family* h, const int64_t* xoff, const uint32_t* xidx,
                        const float* xval, int64_t batch, uint32_t* codes, hipStream_t st) {
   if (batch == 0) return KH_OK;
+  if (h->kind != KH_FAMILY_TERNARY) return rank_hash_sparse_launch(h, xoff, xidx, xval, batch, codes, st);
   KH_CHECK_ARG(h->L <= 256, "hash_sparse supports at most 256 tables");
   const int tpb = kHashThreads / h->k;
   hipLaunchKernelGGL(hash_sparse_kernel, dim3((unsigned)batch, ceil_div(h->L, tpb)), dim3(kHashThreads),
@@ -717,6 +719,9 @@ extern "C" int kh_hash_family_destroy(kh_hash_family* h) {
   dev_free(h->planes_dev);
   dev_free(h->nnz);
   dev_free(h->ent_t);
+  dev_free(h->windows_dev);
+  dev_free(h->fallback_dev);
+  dev_free(h->perms_dev);
   delete h;
   return KH_OK;
 }
@@ -732,6 +737,10 @@ extern "C" int kh_hash_family_dims(const kh_hash_family* h, int* k, int* input_d
 
 extern "C" int kh_hash_family_planes(const kh_hash_family* h, int8_t* planes_host) {
   KH_CHECK_ARG(h && planes_host, "null argument");
+  if (h->kind != KH_FAMILY_TERNARY) {
+    set_error("the family has no hyperplanes (WTA, DWTA or MinHash)");
+    return KH_ERR_UNSUPPORTED;
+  }
   memcpy(planes_host, h->planes_host.data(), h->planes_host.size());
   return KH_OK;
 }

@@ -6,6 +6,13 @@
 
 struct kh_hash_family {
   int dim = 0, k = 0, L = 0;
+  int kind = KH_FAMILY_TERNARY;          // KH_FAMILY_*: hyperplanes or a rank-based family
+  int ws = 0, bits = 0;                  // WTA / DWTA: window size, bits per window
+  std::vector<uint32_t> windows_host;    // WTA / DWTA [L][k][ws]
+  uint32_t* windows_dev = nullptr;
+  uint32_t* fallback_dev = nullptr;      // DWTA [L][k]: empty-window position
+  std::vector<uint32_t> perms_host;      // MinHash [L][dim]
+  uint32_t* perms_dev = nullptr;
   std::vector<int8_t> planes_host;  // [L][k][dim]
   int8_t* planes_dev = nullptr;     // [L*k][dim]
   // Nonzero lists of the planes, transposed so that the planes handled by
@@ -36,6 +43,11 @@ int hash_sparse_launch(const kh_hash_family* h, const int64_t* xoff, const uint3
 int query_launch(const kh_lsh_index* idx, const uint32_t* qcodes, int64_t batch, uint32_t* qids,
                  uint32_t* qcnt, int stride, int32_t* ulen, hipStream_t st);
 int query_stride(const kh_lsh_index* idx);
+// The rank-based families (hash_rank.hip), called by the two launchers above.
+int rank_hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx, int64_t batch,
+                           uint32_t* codes, hipStream_t st);
+int rank_hash_sparse_launch(const kh_hash_family* h, const int64_t* xoff, const uint32_t* xidx,
+                            const float* xval, int64_t batch, uint32_t* codes, hipStream_t st);
 // Row lengths -> CSR offsets, copies of up to four per-row arrays, then a
 // synchronising capacity check.
 int csr_finish(const uint32_t* qids, const uint32_t* qcnt, const float* f1, const float* f2,

@@ -12,6 +12,9 @@
 // and scales by 2^-53.
 #include "rng.hpp"
 
+#include <algorithm>
+#include <vector>
+
 namespace kh {
 
 static inline uint32_t rotl(uint32_t v, int s) { return (v << s) | (v >> (32 - s)); }
@@ -82,6 +85,31 @@ uint64_t StdRng::next_u64() {
   return (static_cast<uint64_t>(buf_[0]) << 32) | lo;
 }
 
+uint32_t StdRng::next_u32() {
+  if (idx_ >= 64) refill();
+  return buf_[idx_++];
+}
+
+// sample_single_inclusive(0, n - 1) of rand 0.8.5's UniformInt<u32>: the high
+// word of draw * n, rejecting draws whose low word exceeds the conservative
+// zone (n << lzcnt(n)) - 1.
+uint32_t StdRng::gen_range_u32(uint32_t n) {
+  const uint32_t zone = (n << __builtin_clz(n)) - 1u;
+  for (;;) {
+    const uint64_t m = static_cast<uint64_t>(next_u32()) * n;
+    if (static_cast<uint32_t>(m) <= zone) return static_cast<uint32_t>(m >> 32);
+  }
+}
+
+void StdRng::shuffle(uint32_t* v, int64_t n) {
+  for (int64_t i = n - 1; i >= 1; --i) {
+    const uint32_t j = gen_range_u32(static_cast<uint32_t>(i + 1));
+    const uint32_t t = v[i];
+    v[i] = v[j];
+    v[j] = t;
+  }
+}
+
 double StdRng::gen_f64() {
   return static_cast<double>(next_u64() >> 11) * (1.0 / 9007199254740992.0);
 }
@@ -105,6 +133,54 @@ void srp_planes(int dim, int k, int num_tables, float sparsity, uint64_t seed, i
     const double v = r.gen_f64();
     planes[i] = v < pneg ? -1 : (v >= pzero_end ? 1 : 0);
   }
+}
+
+void wta_windows(int dim, int k, int num_tables, int ws, uint64_t seed, uint32_t* windows) {
+  StdRng r = StdRng::seed_from_u64(seed);
+  std::vector<uint32_t> perm(dim);
+  for (int t = 0; t < num_tables; ++t)
+    for (int f = 0; f < k; ++f) {
+      for (int d = 0; d < dim; ++d) perm[d] = static_cast<uint32_t>(d);
+      r.shuffle(perm.data(), dim);
+      std::copy(perm.begin(), perm.begin() + ws, windows + (static_cast<int64_t>(t) * k + f) * ws);
+    }
+}
+
+void minhash_perms(int dim, int num_tables, uint64_t seed, uint32_t* perms) {
+  StdRng r = StdRng::seed_from_u64(seed);
+  for (int t = 0; t < num_tables; ++t) {
+    uint32_t* p = perms + static_cast<int64_t>(t) * dim;
+    for (int d = 0; d < dim; ++d) p[d] = static_cast<uint32_t>(d);
+    r.shuffle(p, dim);
+  }
+}
+
+// SipHash-1-3: one compression round per 8-byte word, three finalisation
+// rounds (Aumasson & Bernstein's SipHash with c = 1, d = 3, as std's
+// DefaultHasher), keys k0 = k1 = 0.
+static inline uint64_t rotl64(uint64_t v, int s) { return (v << s) | (v >> (64 - s)); }
+static void sip_round(uint64_t& v0, uint64_t& v1, uint64_t& v2, uint64_t& v3) {
+  v0 += v1; v1 = rotl64(v1, 13); v1 ^= v0; v0 = rotl64(v0, 32);
+  v2 += v3; v3 = rotl64(v3, 16); v3 ^= v2;
+  v0 += v3; v3 = rotl64(v3, 21); v3 ^= v0;
+  v2 += v1; v1 = rotl64(v1, 17); v1 ^= v2; v2 = rotl64(v2, 32);
+}
+
+uint64_t default_hasher_u64x2(uint64_t a, uint64_t b) {
+  uint64_t v0 = 0x736f6d6570736575ull, v1 = 0x646f72616e646f6dull;
+  uint64_t v2 = 0x6c7967656e657261ull, v3 = 0x7465646279746573ull;
+  for (uint64_t m : {a, b}) {
+    v3 ^= m;
+    sip_round(v0, v1, v2, v3);
+    v0 ^= m;
+  }
+  const uint64_t fin = 16ull << 56;  // length byte, no tail
+  v3 ^= fin;
+  sip_round(v0, v1, v2, v3);
+  v0 ^= fin;
+  v2 ^= 0xff;
+  for (int r = 0; r < 3; ++r) sip_round(v0, v1, v2, v3);
+  return v0 ^ v1 ^ v2 ^ v3;
 }
 
 }  // namespace kh

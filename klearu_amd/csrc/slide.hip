@@ -101,7 +101,7 @@ __global__ __launch_bounds__(kSlideThreads) void select_kernel(
     const uint32_t* __restrict__ qids, const uint32_t* __restrict__ qcnt,
     const int32_t* __restrict__ qlen, int qstride, int sampling, int top_k, int threshold,
     int num_neurons, int nbins, uint32_t* __restrict__ aids, int astride,
-    int32_t* __restrict__ alen, int count_order, float* __restrict__ clear_dense) {
+    int32_t* __restrict__ alen, int count_order, float* __restrict__ clear_dense, int fallback) {
   extern __shared__ unsigned hist[];
   __shared__ int wsum[kSlideThreads / 64];
   __shared__ int s_total;
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(kSlideThreads) void select_kernel(
     const int n_pre = select_topk_count_order(ids, cnt, m, top_k, num_neurons, nbins, hist, wsum,
                                               &s_total, out, &n_kept);
     int n_sel = n_kept;
-    if (n_pre == 0) {
+    if (n_pre == 0 && fallback) {
       for (int i = threadIdx.x; i < num_neurons; i += blockDim.x) out[i] = (uint32_t)i;
       n_sel = num_neurons;
     }
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(kSlideThreads) void select_kernel(
     n_pre = mode == KH_SAMPLING_TOPK ? min(m, top_k) : m;
   }
   // empty selection -> every neuron (layer.rs:82-84)
-  if (n_pre == 0) {
+  if (n_pre == 0 && fallback) {
     for (int i = threadIdx.x; i < num_neurons; i += blockDim.x) out[i] = (uint32_t)i;
     n_sel = num_neurons;
   }
@@ -385,19 +385,36 @@ __global__ __launch_bounds__(256) void dense_sparse_kernel(const float* __restri
   y[row * (int64_t)n + o] = r;
 }
 
+// out[r][0..n[r]) = src[r*stride ..] (n[r] <= ld), the ids of a top-k pick.
+__global__ void copy_rows_kernel(const uint32_t* __restrict__ src, int stride,
+                                 const int32_t* __restrict__ n, uint32_t* __restrict__ out, int ld) {
+  const int64_t r = blockIdx.x;
+  const int m = min(n[r], ld);
+  for (int i = threadIdx.x; i < m; i += blockDim.x) out[r * ld + i] = src[r * (int64_t)stride + i];
+}
+
+int select_launch_with(const kh_lsh_index* idx, int sampling, int top_k, int threshold,
+                       int num_neurons, const uint32_t* qids, const uint32_t* qcnt,
+                       const int32_t* qlen, int qs, int64_t batch, uint32_t* aids, int as,
+                       int32_t* alen, bool count_order, float* clear_dense, bool fallback,
+                       hipStream_t st) {
+  // A candidate's hit count is at most L * cap (every slot of its L buckets).
+  const int nbins = idx->L * idx->cap + 1;
+  KH_CHECK_ARG(sampling != KH_SAMPLING_TOPK || nbins <= kMaxCountBins,
+               "top-k sampling supports num_tables * bucket_capacity <= %d", kMaxCountBins - 1);
+  hipLaunchKernelGGL(select_kernel, dim3((unsigned)batch), dim3(kSlideThreads),
+                     sampling == KH_SAMPLING_TOPK ? sizeof(unsigned) * nbins : 0, st, qids, qcnt,
+                     qlen, qs, sampling, top_k, threshold, num_neurons, nbins, aids, as, alen,
+                     count_order ? 1 : 0, clear_dense, fallback ? 1 : 0);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
 int select_launch(const kh_slide_layer* l, const uint32_t* qids, const uint32_t* qcnt,
                   const int32_t* qlen, int qs, int64_t batch, uint32_t* aids, int as, int32_t* alen,
                   bool count_order, float* clear_dense, hipStream_t st) {
-  // A candidate's hit count is at most L * cap (every slot of its L buckets).
-  const int nbins = l->index->L * l->index->cap + 1;
-  KH_CHECK_ARG(l->sampling != KH_SAMPLING_TOPK || nbins <= kMaxCountBins,
-               "top-k sampling supports num_tables * bucket_capacity <= %d", kMaxCountBins - 1);
-  hipLaunchKernelGGL(select_kernel, dim3((unsigned)batch), dim3(kSlideThreads),
-                     l->sampling == KH_SAMPLING_TOPK ? sizeof(unsigned) * nbins : 0, st, qids, qcnt,
-                     qlen, qs, l->sampling, l->top_k, l->threshold, l->n, nbins, aids, as, alen,
-                     count_order ? 1 : 0, clear_dense);
-  KH_LAUNCHED();
-  return KH_OK;
+  return select_launch_with(l->index, l->sampling, l->top_k, l->threshold, l->n, qids, qcnt, qlen,
+                            qs, batch, aids, as, alen, count_order, clear_dense, true, st);
 }
 
 }  // namespace kh
@@ -481,10 +498,19 @@ extern "C" int kh_slide_layer_destroy(kh_slide_layer* l) {
   return KH_OK;
 }
 
+// Sampling as a SparseInferenceEngine call makes it (bolt/sparse_inference.rs):
+// top-k by count in the sampler's order, no all-neurons fallback, and its own
+// activation.
+struct SelectOverride {
+  int top_k;
+  int act;
+};
+
 static int slide_forward_common(const kh_slide_layer* lc, const float* x, const int64_t* xoff,
                                 const uint32_t* xidx, const float* xval, int64_t batch,
                                 int64_t* off, uint32_t* act_ids, float* pre_out, float* act_out,
-                                int64_t capacity, hipStream_t st) {
+                                int64_t capacity, hipStream_t st,
+                                const SelectOverride* ov = nullptr) {
   const kh_slide_layer* l = lc;
   const kh_lsh_index* idx = l->index;
   const int L = idx->L;
@@ -505,8 +531,11 @@ static int slide_forward_common(const kh_slide_layer* lc, const float* x, const 
   if (rc != KH_OK) return rc;
   rc = query_launch(idx, codes, batch, qids, qcnt, qs, qlen, st);
   if (rc != KH_OK) return rc;
-  rc = select_launch(l, qids, qcnt, qlen, qs, batch, aids, as, alen, false, nullptr, st);
+  rc = ov ? select_launch_with(l->index, KH_SAMPLING_TOPK, ov->top_k, 0, l->n, qids, qcnt, qlen, qs,
+                              batch, aids, as, alen, true, nullptr, false, st)
+          : select_launch(l, qids, qcnt, qlen, qs, batch, aids, as, alen, false, nullptr, st);
   if (rc != KH_OK) return rc;
+  const int act = ov ? ov->act : l->act;
   const int max_nz = xoff ? 4096 : l->dim;
   KH_CHECK_ARG(xoff || l->dim <= 8192, "dense SLIDE input supports input_dim <= 8192");
   const size_t lds = (sizeof(uint32_t) + sizeof(float)) * max_nz;
@@ -516,19 +545,19 @@ static int slide_forward_common(const kh_slide_layer* lc, const float* x, const 
   const dim3 ng((unsigned)batch, l->wtn ? kNeuronSplit : 1);
   if (xoff && l->wtn)
     hipLaunchKernelGGL((neuron_kernel<true, true>), ng, dim3(kSlideThreads), lds, st, l->wtn, l->n,
-                       l->bias, l->dim, nullptr, xoff, xidx, xval, aids, as, alen, l->act, max_nz,
+                       l->bias, l->dim, nullptr, xoff, xidx, xval, aids, as, alen, act, max_nz,
                        pre, post);
   else if (xoff)
     hipLaunchKernelGGL((neuron_kernel<true, false>), ng, dim3(kSlideThreads), lds, st, l->w, l->n,
-                       l->bias, l->dim, nullptr, xoff, xidx, xval, aids, as, alen, l->act, max_nz,
+                       l->bias, l->dim, nullptr, xoff, xidx, xval, aids, as, alen, act, max_nz,
                        pre, post);
   else if (l->wtn)
     hipLaunchKernelGGL((neuron_kernel<false, true>), ng, dim3(kSlideThreads), lds, st, l->wtn, l->n,
-                       l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, alen, l->act,
+                       l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, alen, act,
                        max_nz, pre, post);
   else
     hipLaunchKernelGGL((neuron_kernel<false, false>), ng, dim3(kSlideThreads), lds, st, l->w, l->n,
-                       l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, alen, l->act,
+                       l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, alen, act,
                        max_nz, pre, post);
   KH_LAUNCHED();
   return csr_finish(aids, nullptr, pre, post, as, alen, batch, off, act_ids, nullptr, pre_out,
@@ -564,6 +593,61 @@ extern "C" int kh_slide_layer_forward_sparse(const kh_slide_layer* l, const int6
   }
   return slide_forward_common(l, nullptr, xoff_dev, xidx_dev, xval_dev, batch, off_dev,
                               act_ids_dev, pre_dev, act_dev, capacity, st);
+}
+
+extern "C" int kh_sparse_inference(const kh_slide_layer* l, const float* x_dev, int64_t batch,
+                                   int64_t base_top_k, float sparsity_multiplier, int relu,
+                                   int64_t* off_dev, uint32_t* ids_dev, float* act_dev,
+                                   int64_t capacity, void* stream) {
+  KH_CHECK_ARG(l && off_dev && ids_dev, "null argument");
+  KH_CHECK_ARG(batch >= 0 && batch <= 0x7fffffff && capacity >= 0 && base_top_k >= 0,
+               "bad batch/capacity/top_k");
+  hipStream_t st = as_stream(stream);
+  if (batch == 0) {
+    KH_HIP(hipMemsetAsync(off_dev, 0, sizeof(int64_t), st));
+    return KH_OK;
+  }
+  KH_CHECK_ARG(x_dev != nullptr, "null input");
+  // (base_top_k as f32 * multiplier) as usize: f32 product, truncated,
+  // saturating (NaN and negatives give 0)
+  const float ek = static_cast<float>(base_top_k) * sparsity_multiplier;
+  const int64_t eff = !(ek > 0.0f) ? 0 : (ek >= 2147483647.0f ? 0x7fffffff : static_cast<int64_t>(ek));
+  SelectOverride ov{static_cast<int>(eff), relu ? KH_ACT_RELU : KH_ACT_IDENTITY};
+  return slide_forward_common(l, x_dev, nullptr, nullptr, nullptr, batch, off_dev, ids_dev, nullptr,
+                              act_dev, capacity, st, &ov);
+}
+
+extern "C" int kh_lsh_index_query_top_k(const kh_lsh_index* idx, const float* x_dev, int64_t batch,
+                                        int64_t top_k, uint32_t* ids_dev, int32_t* n_dev,
+                                        void* stream) {
+  KH_CHECK_ARG(idx && n_dev && (ids_dev || top_k == 0), "null argument");
+  KH_CHECK_ARG(batch >= 0 && batch <= 0x7fffffff && top_k >= 0 && top_k <= 0x7fffffff, "bad batch/top_k");
+  if (batch == 0) return KH_OK;
+  KH_CHECK_ARG(x_dev != nullptr, "null input");
+  hipStream_t st = as_stream(stream);
+  WsSet* w = idx->ws.get(st);
+  const int L = idx->L;
+  const int qs = query_stride(idx);
+  uint32_t* codes = static_cast<uint32_t*>(w->get(4, sizeof(uint32_t) * batch * L));
+  uint32_t* qids = static_cast<uint32_t*>(w->get(5, sizeof(uint32_t) * batch * qs));
+  uint32_t* qcnt = static_cast<uint32_t*>(w->get(6, sizeof(uint32_t) * batch * qs));
+  int32_t* qlen = static_cast<int32_t*>(w->get(7, sizeof(int32_t) * batch));
+  if (!codes || !qids || !qcnt || !qlen) return KH_ERR_ALLOC;
+  int rc = hash_dense_launch(idx->h, x_dev, idx->h->dim, batch, codes, st);
+  if (rc == KH_OK) rc = query_launch(idx, codes, batch, qids, qcnt, qs, qlen, st);
+  if (rc != KH_OK) return rc;
+  // count descending, then id, into the codes' slot (the query has read the
+  // codes by then: the calls are ordered on the stream)
+  const int k = static_cast<int>(std::min<int64_t>(top_k, qs));
+  uint32_t* picks = static_cast<uint32_t*>(w->get(4, sizeof(uint32_t) * batch * std::max(qs, L)));
+  if (!picks) return KH_ERR_ALLOC;
+  rc = select_launch_with(idx, KH_SAMPLING_TOPK, k, 0, 0x7fffffff, qids, qcnt, qlen, qs, batch, picks,
+                          qs, n_dev, true, nullptr, false, st);
+  if (rc != KH_OK || top_k == 0) return rc;
+  hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)batch), dim3(256), 0, st, picks, qs, n_dev, ids_dev,
+                     static_cast<int>(top_k));
+  KH_LAUNCHED();
+  return KH_OK;
 }
 
 extern "C" int kh_dense_layer_create(int input_dim, int num_neurons, const float* w_host,

@@ -39,5 +39,12 @@ namespace kh {
 int select_launch(const kh_slide_layer* l, const uint32_t* qids, const uint32_t* qcnt,
                   const int32_t* qlen, int qs, int64_t batch, uint32_t* aids, int as, int32_t* alen,
                   bool count_order, float* clear_dense, hipStream_t st);
+// The same with explicit sampling parameters; fallback: an empty pick list
+// becomes every neuron 0..num_neurons-1 (layer.rs:82-84).
+int select_launch_with(const kh_lsh_index* idx, int sampling, int top_k, int threshold,
+                       int num_neurons, const uint32_t* qids, const uint32_t* qcnt,
+                       const int32_t* qlen, int qs, int64_t batch, uint32_t* aids, int as,
+                       int32_t* alen, bool count_order, float* clear_dense, bool fallback,
+                       hipStream_t st);
 
 }  // namespace kh

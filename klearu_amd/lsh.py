@@ -107,6 +107,20 @@ class HashFamily:
         _lib.call("kh_hash_family_planes", self._h, hptr(out))
         return out
 
+    def kind(self):
+        """"ternary", "wta", "dwta" or "minhash" and the window size."""
+        kd, ws = C.c_int(), C.c_int()
+        _lib.call("kh_hash_family_kind", self._h, C.byref(kd), C.byref(ws))
+        return ("ternary", "wta", "dwta", "minhash")[kd.value], ws.value
+
+    def tables(self):
+        """WTA / DWTA windows [L][k][ws] or MinHash permutations [L][dim]."""
+        kind, ws = self.kind()
+        shape = (self._L, self._dim) if kind == "minhash" else (self._L, self._k, ws)
+        out = np.empty(shape, np.uint32)
+        _lib.call("kh_hash_family_tables", self._h, hptr(out))
+        return out
+
     def hash_dense_batch(self, X, stream=None) -> torch.Tensor:
         """codes[b][t] for X [batch, input_dim] (int32 bit patterns of u32 codes)."""
         X = to_device(X, np.float32).reshape(-1, self._dim)
@@ -128,6 +142,45 @@ class HashFamily:
 
     def hash_sparse(self, sv: SparseVector, table: int) -> int:
         return int(self.hash_sparse_batch([sv])[0, table].item()) & 0xFFFFFFFF
+
+
+def WtaHash(input_dim: int, k: int, num_tables: int, window_size: int, seed: int) -> HashFamily:
+    """WtaHash::new (hash/wta.rs:42-90)."""
+    h = C.c_void_p()
+    _lib.call("kh_wta_create", input_dim, k, num_tables, window_size, seed, C.byref(h))
+    return HashFamily(h)
+
+
+def DwtaHash(input_dim: int, k: int, num_tables: int, window_size: int, seed: int) -> HashFamily:
+    """DwtaHash::new (hash/dwta.rs:40-88)."""
+    h = C.c_void_p()
+    _lib.call("kh_dwta_create", input_dim, k, num_tables, window_size, seed, C.byref(h))
+    return HashFamily(h)
+
+
+def MinHash(input_dim: int, k: int, num_tables: int, seed: int) -> HashFamily:
+    """MinHash::new (hash/minhash.rs:38-60)."""
+    h = C.c_void_p()
+    _lib.call("kh_minhash_create", input_dim, k, num_tables, seed, C.byref(h))
+    return HashFamily(h)
+
+
+def family_from_windows(windows, input_dim, dwta=False) -> HashFamily:
+    """WTA / DWTA over windows [L][k][window_size] drawn elsewhere (e.g. by the reference)."""
+    w = np.ascontiguousarray(windows, np.uint32)
+    L, k, ws = w.shape
+    h = C.c_void_p()
+    _lib.call("kh_wta_from_windows", 1 if dwta else 0, input_dim, k, L, ws, hptr(w), C.byref(h))
+    return HashFamily(h)
+
+
+def family_from_permutations(perms, k) -> HashFamily:
+    """MinHash over permutations [L][input_dim] (permutations[table][dim])."""
+    p = np.ascontiguousarray(perms, np.uint32)
+    L, dim = p.shape
+    h = C.c_void_p()
+    _lib.call("kh_minhash_from_permutations", dim, k, L, hptr(p), C.byref(h))
+    return HashFamily(h)
 
 
 def SimHash(input_dim: int, k: int, num_tables: int, seed: int) -> HashFamily:
@@ -281,6 +334,16 @@ class LshIndex:
         i, _ = self._unpack(*self.query_sparse_batch([sv], counts=False))
         return [int(a) for a in i]
 
+    def query_top_k(self, X, top_k, stream=None):
+        """Per row of X: the candidate ids by hit count descending (ties: ascending id), at most top_k."""
+        X = to_device(X, np.float32).reshape(-1, self.hash_family.input_dim())
+        B = X.shape[0]
+        ids = torch.empty(B, max(top_k, 1), dtype=torch.int32, device=X.device)
+        n = torch.empty(B, dtype=torch.int32, device=X.device)
+        _lib.call("kh_lsh_index_query_top_k", self._h, ptr(X), B, int(top_k), ptr(ids), ptr(n), stream_ptr(stream))
+        ids, n = ids.cpu().numpy().view(np.uint32), n.cpu().numpy()
+        return [ids[b, :n[b]].tolist() for b in range(B)]
+
     def buckets(self):
         """(data [L][2^K][cap], len [L][2^K], count [L][2^K]) copied to the host."""
         L, K = self.num_tables(), self.hash_family.k()
@@ -299,7 +362,40 @@ def create_lsh_index(config: LshConfig, input_dim: int, seed: int) -> LshIndex:
         hf = SimHash(input_dim, k, L, seed)
     elif config.hash_function == "SparseRandomProjection":
         hf = SparseRandomProjection(input_dim, k, L, 1.0 / 3.0, seed)
+    elif config.hash_function == "WtaHash":
+        hf = WtaHash(input_dim, k, L, min(8, input_dim), seed)      # DEFAULT_WINDOW_SIZE (index.rs:330)
+    elif config.hash_function == "DwtaHash":
+        hf = DwtaHash(input_dim, k, L, min(8, input_dim), seed)
+    elif config.hash_function == "MinHash":
+        hf = MinHash(input_dim, k, L, seed)
     else:
         raise NotImplementedError(f"hash family {config.hash_function} is not on the GPU path")
     bt = FIFO if config.bucket_type == "Fifo" else RESERVOIR
     return LshIndex(hf, bt, config.bucket_capacity)
+
+
+class LshSparsityPredictor:
+    """LshSparsityPredictor (crates/klearu-dejavu/src/predictor/lsh_predictor.rs:7-43):
+    an LSH index over observed inputs, one entry per (input, important id)."""
+
+    def __init__(self, config: LshConfig, input_dim: int, top_k: int, seed: int):
+        self.index = create_lsh_index(config, input_dim, seed)
+        self.top_k = top_k
+
+    def build_from_observations(self, observations):
+        """clear, then insert each input under each of its important ids, in order (:22-30)."""
+        self.index.clear()
+        ids, rows = [], []
+        for inp, important in observations:
+            for i in important:
+                ids.append(int(i))
+                rows.append(np.asarray(inp, np.float32))
+        if ids:
+            self.index.insert_batch(np.array(ids, np.uint32), np.stack(rows))
+
+    def predict(self, x):
+        """Ids by hit count descending, at most top_k (:33-43)."""
+        return self.index.query_top_k(np.asarray(x, np.float32)[None, :], self.top_k)[0]
+
+    def predict_batch(self, X):
+        return self.index.query_top_k(X, self.top_k)

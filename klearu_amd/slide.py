@@ -288,3 +288,38 @@ class DenseLayer:
     def forward_sparse(self, vectors, stream=None) -> torch.Tensor:
         off, idx, val = csr_batch(vectors)
         return self.forward_sparse_csr(off, idx, val, len(vectors), stream)
+
+
+class SparseInferenceEngine:
+    """SparseInferenceEngine (crates/klearu-bolt/src/sparse_inference.rs:8-111)
+    over a Layer's index and weights."""
+
+    def __init__(self, sparsity_multiplier: float):
+        self._m = float(np.float32(sparsity_multiplier))
+
+    def sparsity_multiplier(self) -> float:
+        return self._m
+
+    def _run(self, layer: Layer, X, base_top_k, relu, stream=None):
+        X = to_device(X, np.float32).reshape(-1, layer.config.input_dim)
+        B = X.shape[0]
+        cap = B * max(layer.config.num_neurons, layer.index.num_tables() * layer.index.cap)
+        off = torch.empty(B + 1, dtype=torch.int64, device=X.device)
+        ids = torch.empty(max(cap, 1), dtype=torch.int32, device=X.device)
+        act = torch.empty(max(cap, 1), dtype=torch.float32, device=X.device)
+        _lib.call("kh_sparse_inference", layer._h, ptr(X), B, int(base_top_k), self._m, 1 if relu else 0, ptr(off),
+                  ptr(ids), ptr(act), cap, stream_ptr(stream))
+        o = off.cpu().numpy()
+        i = ids.cpu().numpy().view(np.uint32)
+        a = act.cpu().numpy()
+        return [list(zip(i[o[b]:o[b + 1]].tolist(), a[o[b]:o[b + 1]].tolist())) for b in range(B)]
+
+    def infer(self, x, layer: Layer, base_top_k: int):
+        """(neuron_id, relu(w.x + b)) in hit-count order."""
+        return self._run(layer, np.asarray(x, np.float32)[None, :], base_top_k, True)[0]
+
+    def infer_linear(self, x, layer: Layer, base_top_k: int):
+        return self._run(layer, np.asarray(x, np.float32)[None, :], base_top_k, False)[0]
+
+    def infer_batch(self, X, layer: Layer, base_top_k: int, relu=True):
+        return self._run(layer, X, base_top_k, relu)

@@ -643,3 +643,79 @@ class SlideNetOracle:
             for l in self.layers:
                 self.rebuild_layer(l)
         return float(np.float32(total / np.float32(X.shape[0])))
+
+
+# --------------------------------------------------------------------------- WTA / DWTA / MinHash
+class _Rng(C.Structure):
+    _fields_ = [("key", C.c_uint32 * 8), ("counter", C.c_uint64), ("buf", C.c_uint32 * 64), ("idx", C.c_int)]
+
+
+_sig("or_stdrng_seed_from_u64", None, C.c_void_p, C.c_uint64)
+_sig("or_stdrng_next_u32", C.c_uint32, C.c_void_p)
+_sig("or_rand_gen_range_u32", C.c_uint32, C.c_void_p, C.c_uint32)
+_sig("or_rand_shuffle_u32", None, C.c_void_p, _u32p, _i64)
+_sig("or_wta_windows", None, _int, _int, _int, _int, C.c_uint64, _u32p)
+_sig("or_minhash_perms", None, _int, _int, C.c_uint64, _u32p)
+_sig("or_wta_bits", _int, _int)
+_sig("or_wta_hash_dense", C.c_uint64, _u32p, _int, _int, _int, _f32p)
+_sig("or_siphash", C.c_uint64, _int, _int, C.c_uint64, C.c_uint64, C.c_char_p, _i64)
+_sig("or_dwta_fallback", C.c_uint32, C.c_uint64, C.c_uint64, _int)
+_sig("or_dwta_hash_sparse", C.c_uint64, _u32p, _int, _int, _int, _u32p, _f32p, _i64)
+_sig("or_minhash_hash", C.c_uint64, _u32p, _int, _int, _int, _u32p, _i64)
+
+
+class StdRng:
+    """rand 0.8.5 StdRng restated in oracle.c (u32 stream and gen_range / shuffle)."""
+
+    def __init__(self, seed):
+        self._s = C.create_string_buffer(4096)   # larger than the C struct
+        lib.or_stdrng_seed_from_u64(C.cast(self._s, C.c_void_p), int(seed))
+
+    def next_u32(self):
+        return int(lib.or_stdrng_next_u32(C.cast(self._s, C.c_void_p)))
+
+    def gen_range(self, n):
+        return int(lib.or_rand_gen_range_u32(C.cast(self._s, C.c_void_p), int(n)))
+
+    def shuffle(self, a):
+        a = u32(a).copy()
+        lib.or_rand_shuffle_u32(C.cast(self._s, C.c_void_p), a, a.size)
+        return a
+
+
+def wta_windows(dim, k, L, ws, seed):
+    w = np.zeros(L * k * ws, np.uint32)
+    lib.or_wta_windows(dim, k, L, ws, seed, w)
+    return w.reshape(L, k, ws)
+
+
+def minhash_perms(dim, L, seed):
+    p = np.zeros(L * dim, np.uint32)
+    lib.or_minhash_perms(dim, L, seed, p)
+    return p.reshape(L, dim)
+
+
+def wta_hash_dense(windows, x, table):
+    L, k, ws = windows.shape
+    return int(lib.or_wta_hash_dense(np.ascontiguousarray(windows, np.uint32).reshape(-1), k, ws, table, f32(x)))
+
+
+def dwta_hash_sparse(windows, idx, val, table):
+    L, k, ws = windows.shape
+    idx, val = u32(idx), f32(val)
+    return int(lib.or_dwta_hash_sparse(np.ascontiguousarray(windows, np.uint32).reshape(-1), k, ws, table,
+                                       idx, val, idx.size))
+
+
+def siphash(c, d, k0, k1, msg):
+    return int(lib.or_siphash(c, d, k0, k1, bytes(msg), len(msg)))
+
+
+def minhash_hash(perms, k, table, nz):
+    L, dim = perms.shape
+    nz = u32(nz)
+    return int(lib.or_minhash_hash(np.ascontiguousarray(perms, np.uint32).reshape(-1), dim, k, table, nz, nz.size))
+
+
+def minhash_hash_dense(perms, k, table, x):
+    return minhash_hash(perms, k, table, np.nonzero(f32(x) != 0.0)[0].astype(np.uint32))

@@ -363,6 +363,197 @@ void or_hash_dense_batch(const int8_t* planes, int dim, int k, int num_tables, c
 }
 
 /* ======================================================================== */
+/* WTA / DWTA / MinHash (klearu-core/src/hash/wta.rs, dwta.rs, minhash.rs)    */
+/* ======================================================================== */
+
+/* rand 0.8.5 Rng::gen_range(0..n) for u32 (UniformInt::sample_single ->
+ * sample_single_inclusive): widening multiply of next_u32 by n, rejecting
+ * low words above zone = (n << lzcnt(n)) - 1.  Third-party (rand 0.8.5, not in
+ * the reference tree), restated from its published source; the composed
+ * draws are parity unpinned (no reference test holds a drawn window). */
+uint32_t or_rand_gen_range_u32(or_stdrng* r, uint32_t n) {
+  const uint32_t zone = (n << __builtin_clz(n)) - 1u;
+  for (;;) {
+    const uint64_t m = (uint64_t)or_stdrng_next_u32(r) * n;
+    if ((uint32_t)m <= zone) return (uint32_t)(m >> 32);
+  }
+}
+
+/* SliceRandom::shuffle (rand 0.8.5 seq/mod.rs): for i = len-1 down to 1,
+ * swap(i, gen_index(i + 1)); gen_index uses the u32 gen_range below 2^32. */
+void or_rand_shuffle_u32(or_stdrng* r, uint32_t* v, int64_t n) {
+  for (int64_t i = n - 1; i >= 1; --i) {
+    const uint32_t j = or_rand_gen_range_u32(r, (uint32_t)(i + 1));
+    const uint32_t t = v[i];
+    v[i] = v[j];
+    v[j] = t;
+  }
+}
+
+/* WtaHash::new / DwtaHash::new window draws (wta.rs:42-90, dwta.rs:40-88):
+ * per table, per hash function, shuffle a fresh 0..dim and keep the first
+ * window_size entries.  windows[L][k][ws]. */
+void or_wta_windows(int dim, int k, int num_tables, int ws, uint64_t seed, uint32_t* windows) {
+  or_stdrng r;
+  or_stdrng_seed_from_u64(&r, seed);
+  uint32_t* perm = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)dim);
+  for (int t = 0; t < num_tables; ++t)
+    for (int f = 0; f < k; ++f) {
+      for (int d = 0; d < dim; ++d) perm[d] = (uint32_t)d;
+      or_rand_shuffle_u32(&r, perm, dim);
+      memcpy(windows + ((int64_t)t * k + f) * ws, perm, sizeof(uint32_t) * (size_t)ws);
+    }
+  free(perm);
+}
+
+/* MinHash::new (minhash.rs:38-60): per table a shuffled 0..dim (u32). */
+void or_minhash_perms(int dim, int num_tables, uint64_t seed, uint32_t* perms) {
+  or_stdrng r;
+  or_stdrng_seed_from_u64(&r, seed);
+  for (int t = 0; t < num_tables; ++t) {
+    uint32_t* p = perms + (int64_t)t * dim;
+    for (int d = 0; d < dim; ++d) p[d] = (uint32_t)d;
+    or_rand_shuffle_u32(&r, p, dim);
+  }
+}
+
+/* bits_per_window (wta.rs:54-58): 1 for ws <= 1, else ceil(log2(ws)). */
+int or_wta_bits(int ws) { return ws <= 1 ? 1 : (int)ceil(log2((double)ws)); }
+
+/* argmax_dense (wta.rs:93-105): first strict maximum from -inf (NaN never
+ * wins; all -inf / NaN gives 0). */
+static int wta_argmax(const float* x, const uint32_t* win, int ws) {
+  int best = 0;
+  float bv = -INFINITY;
+  for (int p = 0; p < ws; ++p) {
+    const float v = x[win[p]];
+    if (v > bv) { bv = v; best = p; }
+  }
+  return best;
+}
+
+/* WtaHash::hash_dense (wta.rs:108-119), also DwtaHash::hash_dense: the k
+ * argmax positions packed from bit 0 up, bits per window each.
+ * Pinned: brute-force tie / NaN / -inf KATs and the reference's positive-
+ * scaling invariance (wta.rs:202-215) in tests/test_oracle_families.py. */
+uint64_t or_wta_hash_dense(const uint32_t* windows, int k, int ws, int table, const float* x) {
+  const int bits = or_wta_bits(ws);
+  uint64_t h = 0;
+  for (int f = 0; f < k; ++f)
+    h |= (uint64_t)wta_argmax(x, windows + ((int64_t)table * k + f) * ws, ws) << (bits * f);
+  return h;
+}
+
+/* SipHash-1-3 with keys 0, 0 over two little-endian u64 words: std's
+ * DefaultHasher after `table.hash(); hash_fn.hash();` (usize writes), then
+ * finish().  Pinned: the same round code with c = 2, d = 4 reproduces the
+ * SipHash paper's reference vectors (tests/test_oracle_families.py). */
+#define ROTL64(v, s) (((v) << (s)) | ((v) >> (64 - (s))))
+static void sip_round(uint64_t* v) {
+  v[0] += v[1]; v[1] = ROTL64(v[1], 13); v[1] ^= v[0]; v[0] = ROTL64(v[0], 32);
+  v[2] += v[3]; v[3] = ROTL64(v[3], 16); v[3] ^= v[2];
+  v[0] += v[3]; v[3] = ROTL64(v[3], 21); v[3] ^= v[0];
+  v[2] += v[1]; v[1] = ROTL64(v[1], 17); v[1] ^= v[2]; v[2] = ROTL64(v[2], 32);
+}
+uint64_t or_siphash(int c_rounds, int d_rounds, uint64_t k0, uint64_t k1, const uint8_t* msg,
+                    int64_t len) {
+  uint64_t v[4] = {k0 ^ 0x736f6d6570736575ull, k1 ^ 0x646f72616e646f6dull,
+                   k0 ^ 0x6c7967656e657261ull, k1 ^ 0x7465646279746573ull};
+  int64_t i = 0;
+  for (; i + 8 <= len; i += 8) {
+    uint64_t m = 0;
+    for (int b = 0; b < 8; ++b) m |= (uint64_t)msg[i + b] << (8 * b);
+    v[3] ^= m;
+    for (int r = 0; r < c_rounds; ++r) sip_round(v);
+    v[0] ^= m;
+  }
+  uint64_t b = (uint64_t)(len & 0xff) << 56;
+  for (int j = 0; i + j < len; ++j) b |= (uint64_t)msg[i + j] << (8 * j);
+  v[3] ^= b;
+  for (int r = 0; r < c_rounds; ++r) sip_round(v);
+  v[0] ^= b;
+  v[2] ^= 0xff;
+  for (int r = 0; r < d_rounds; ++r) sip_round(v);
+  return v[0] ^ v[1] ^ v[2] ^ v[3];
+}
+
+/* DwtaHash's empty-window fallback (dwta.rs:133-141): DefaultHasher of
+ * (table, hash_fn) modulo window_size. */
+uint32_t or_dwta_fallback(uint64_t table, uint64_t hash_fn, int ws) {
+  uint8_t m[16];
+  for (int b = 0; b < 8; ++b) {
+    m[b] = (uint8_t)(table >> (8 * b));
+    m[8 + b] = (uint8_t)(hash_fn >> (8 * b));
+  }
+  return (uint32_t)(or_siphash(1, 3, 0, 0, m, 16) % (uint64_t)ws);
+}
+
+/* DwtaHash::hash_sparse (dwta.rs:154-166, argmax_sparse :108-143): argmax over
+ * the window positions whose dimension is stored in the (sorted) sparse
+ * input, else the fallback.  WtaHash::hash_sparse is hash_dense of to_dense. */
+uint64_t or_dwta_hash_sparse(const uint32_t* windows, int k, int ws, int table, const uint32_t* idx,
+                             const float* val, int64_t nnz) {
+  const int bits = or_wta_bits(ws);
+  uint64_t h = 0;
+  for (int f = 0; f < k; ++f) {
+    const uint32_t* win = windows + ((int64_t)table * k + f) * ws;
+    int best = -1;
+    float bv = -INFINITY;
+    for (int p = 0; p < ws; ++p) {
+      int64_t lo = 0, hi = nnz;  /* binary search */
+      while (lo < hi) {
+        const int64_t mid = (lo + hi) / 2;
+        if (idx[mid] < win[p]) lo = mid + 1; else hi = mid;
+      }
+      if (lo < nnz && idx[lo] == win[p] && val[lo] > bv) { bv = val[lo]; best = p; }
+    }
+    const uint64_t pos = best >= 0 ? (uint64_t)best : or_dwta_fallback((uint64_t)table, (uint64_t)f, ws);
+    h |= pos << (bits * f);
+  }
+  return h;
+}
+
+/* MinHash hash_impl (minhash.rs:64-136): per-bin minimum permuted index over
+ * the nonzero dimensions (bin = permuted / ceil(dim/k), bins >= k dropped),
+ * empty bins take the next non-empty bin circularly (all empty -> all 0),
+ * then sum(h_i * P^i) with wrapping u64 arithmetic, P = 0x517cc1b727220a95,
+ * masked to k bits.  nz: the nonzero dims (dense: x != 0 in index order;
+ * sparse: every stored index).  Pinned: closed-form KATs in
+ * tests/test_oracle_families.py. */
+uint64_t or_minhash_hash(const uint32_t* perms, int dim, int k, int table, const uint32_t* nz,
+                         int64_t n_nz) {
+  const uint32_t* perm = perms + (int64_t)table * dim;
+  const int64_t bin_size = (dim + k - 1) / k;
+  uint32_t* mins = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)k);
+  for (int b = 0; b < k; ++b) mins[b] = 0xffffffffu;
+  for (int64_t i = 0; i < n_nz; ++i) {
+    const uint32_t pv = perm[nz[i]];
+    const int64_t bin = pv / bin_size;
+    if (bin < k && pv < mins[bin]) mins[bin] = pv;
+  }
+  int all_empty = 1;
+  for (int b = 0; b < k; ++b) if (mins[b] != 0xffffffffu) { all_empty = 0; break; }
+  if (all_empty) {
+    for (int b = 0; b < k; ++b) mins[b] = 0;
+  } else {
+    for (int b = 0; b < k; ++b)
+      if (mins[b] == 0xffffffffu) {
+        int j = (b + 1) % k;
+        while (mins[j] == 0xffffffffu) j = (j + 1) % k;
+        mins[b] = mins[j];
+      }
+  }
+  const uint64_t mask = k >= 64 ? ~0ull : ((1ull << k) - 1ull);
+  uint64_t h = 0, pp = 1;
+  for (int b = 0; b < k; ++b) {
+    h += (uint64_t)mins[b] * pp;
+    pp *= 0x517cc1b727220a95ull;
+  }
+  free(mins);
+  return h & mask;
+}
+
+/* ======================================================================== */
 /* Buckets and the LSH index                                                 */
 /* ======================================================================== */
 

@@ -61,6 +61,20 @@ void or_stdrng_from_seed(or_stdrng* r, const uint8_t seed[32]);
 uint32_t or_stdrng_next_u32(or_stdrng* r);
 uint64_t or_stdrng_next_u64(or_stdrng* r);
 double or_stdrng_gen_f64(or_stdrng* r);
+/* ---- hash/wta.rs, dwta.rs, minhash.rs (+ rand 0.8.5 shuffle, SipHash-1-3) ---- */
+uint32_t or_rand_gen_range_u32(or_stdrng* r, uint32_t n);
+void or_rand_shuffle_u32(or_stdrng* r, uint32_t* v, int64_t n);
+void or_wta_windows(int dim, int k, int num_tables, int ws, uint64_t seed, uint32_t* windows);
+void or_minhash_perms(int dim, int num_tables, uint64_t seed, uint32_t* perms);
+int or_wta_bits(int ws);
+uint64_t or_wta_hash_dense(const uint32_t* windows, int k, int ws, int table, const float* x);
+uint64_t or_siphash(int c_rounds, int d_rounds, uint64_t k0, uint64_t k1, const uint8_t* msg,
+                    int64_t len);
+uint32_t or_dwta_fallback(uint64_t table, uint64_t hash_fn, int ws);
+uint64_t or_dwta_hash_sparse(const uint32_t* windows, int k, int ws, int table, const uint32_t* idx,
+                             const float* val, int64_t nnz);
+uint64_t or_minhash_hash(const uint32_t* perms, int dim, int k, int table, const uint32_t* nz,
+                         int64_t n_nz);
 
 /* ---- hash families: hash/simhash.rs, hash/srp.rs ---- */
 void or_simhash_planes(int dim, int k, int num_tables, uint64_t seed, int8_t* planes);
