@@ -48,7 +48,7 @@ sys.path.insert(0, ROOT)
 METRIC = "sparse FFN tokens/s @7B shape; gathered-weight HBM GB/s vs roofline"
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ffn_fused1_cfg3_traffic.txt")
-ALL_LEGS = ["cfg3", "cfg3b16", "cfg2", "cfg4", "cfg4b8", "decoder", "cfg1", "cfg5", "train5"]
+ALL_LEGS = ["cfg3", "cfg3b16", "cfg2", "cfg4", "cfg4b8", "decoder", "cfg1", "cfg5", "train5", "families"]
 
 
 def log(*a):
@@ -624,6 +624,101 @@ def slide_train5_leg(steps, seed, cpu_seconds):
     return res
 
 
+def families_leg(steps, seed, timer, cpu_seconds):
+    """The remaining families and callers at cfg1's shape (784-d inputs, 80%
+    zeros, batch 128, K6 L50): WTA / DWTA / MinHash hashing, bolt's
+    SparseInferenceEngine over cfg1's layer (top 100 x 1.5 by hit count),
+    LshSparsityPredictor's top-k query, and the LibSVM loader on a synthetic
+    cfg5-shaped file (host MB/s)."""
+    import tempfile
+
+    import torch
+    from klearu_amd import _lib
+    from klearu_amd._dev import ptr, stream_ptr
+    from klearu_amd.formats import LibSvmDataset
+    from klearu_amd.lsh import DwtaHash, LshConfig, MinHash, WtaHash
+    from klearu_amd.slide import Layer, LayerConfig
+
+    rng = np.random.default_rng(seed + 70)
+    n, dim, B, L, k = 1024, 784, 128, 50, 6
+    X = rng.uniform(0, 1, (B, dim)).astype(np.float32)
+    X[rng.uniform(0, 1, (B, dim)) < 0.8] = 0.0
+    Xd = torch.from_numpy(X).cuda()
+    codes = torch.empty(B, L, dtype=torch.int32, device="cuda")
+    out = {}
+    fams = {"wta": WtaHash(dim, k, L, 8, 42), "dwta": DwtaHash(dim, k, L, 8, 42), "minhash": MinHash(dim, k, L, 42)}
+    for name, fam in fams.items():
+        def run(fam=fam):
+            _lib.call("kh_hash_dense", fam._h, ptr(Xd), B, ptr(codes), stream_ptr())
+        ms = timer.time(run, steps, 3)
+        out[name] = dict(unit="samples/s", value=round(B * 1000.0 / ms, 1), ms_per_batch=round(ms, 4))
+        if cpu_seconds > 0:
+            import oracle
+            tabs = fam.tables()
+            i = [0]
+
+            def one(name=name, tabs=tabs):
+                x = X[i[0] % B]
+                i[0] += 1
+                if name == "minhash":
+                    nz = np.nonzero(x)[0].astype(np.uint32)
+                    for t in range(L):
+                        oracle.lib.or_minhash_hash(tabs.reshape(-1), dim, k, t, nz, nz.size)
+                else:
+                    for t in range(L):
+                        oracle.lib.or_wta_hash_dense(tabs.reshape(-1), k, 8, t, x)
+
+            per, cnt, el = timed_cpu(one, min(cpu_seconds, 3.0), 10)
+            out[name]["cpu"] = dict(value=round(1.0 / per, 1), unit="samples/s", cores=1, kind="port",
+                                    sample=f"{cnt} rows x 50 tables through the oracle's C hash in {el:.1f}s "
+                                           f"(ctypes call per table included)")
+    # bolt over cfg1's layer
+    W = rng.normal(0, 0.01, (n, dim)).astype(np.float32)
+    b = np.zeros(n, np.float32)
+    layer = Layer(LayerConfig(dim, n, "Relu", LshConfig(num_tables=L, num_hashes=k, bucket_capacity=128), "Vanilla",
+                              2, 0), W, b, 42)
+    cap = B * max(n, L * 128)
+    off = torch.empty(B + 1, dtype=torch.int64, device="cuda")
+    ids = torch.empty(cap, dtype=torch.int32, device="cuda")
+    act = torch.empty(cap, dtype=torch.float32, device="cuda")
+
+    def run_bolt():
+        _lib.call("kh_sparse_inference", layer._h, ptr(Xd), B, 100, 1.5, 1, ptr(off), ptr(ids), ptr(act), cap,
+                  stream_ptr())
+    ms = timer.time(run_bolt, steps, 3)
+    out["bolt_infer"] = dict(unit="samples/s", value=round(B * 1000.0 / ms, 1), ms_per_batch=round(ms, 4),
+                             mean_active=float(np.diff(off.cpu().numpy()).mean()))
+    tk = torch.empty(B, 32, dtype=torch.int32, device="cuda")
+    tn = torch.empty(B, dtype=torch.int32, device="cuda")
+
+    def run_pred():
+        _lib.call("kh_lsh_index_query_top_k", layer.index._h, ptr(Xd), B, 32, ptr(tk), ptr(tn), stream_ptr())
+    ms = timer.time(run_pred, steps, 3)
+    out["lsh_predictor_top32"] = dict(unit="samples/s", value=round(B * 1000.0 / ms, 1), ms_per_batch=round(ms, 4))
+    del layer
+    # LibSVM: cfg5-shaped lines (5 labels of 670091, 50-100 features of 135909)
+    lines = []
+    for _ in range(20000):
+        nnz = int(rng.integers(50, 101))
+        idx = np.sort(rng.choice(135909, nnz, replace=False))
+        labs = ",".join(str(v) for v in rng.choice(670091, 5, replace=False))
+        lines.append(labs + " " + " ".join(f"{i}:{v:.6f}" for i, v in zip(idx, rng.uniform(0, 1, nnz))))
+    text = ("\n".join(lines) + "\n").encode()
+    with tempfile.NamedTemporaryFile(suffix=".txt", delete=False) as f:
+        f.write(text)
+        path = f.name
+    t0 = time.perf_counter()
+    ds = LibSvmDataset.load(path, 135909, 670091)
+    sec = time.perf_counter() - t0
+    os.unlink(path)
+    out["libsvm_load"] = dict(unit="MB/s", value=round(len(text) / sec / 1e6, 1), examples=len(ds),
+                              seconds=round(sec, 3), note="host parse of a 20000-line cfg5-shaped file")
+    return dict(workload="families: WTA / DWTA / MinHash hashing, bolt SparseInferenceEngine, LshSparsityPredictor "
+                         "top-k at cfg1's shape (784-d, 80% zeros, batch 128, K6 L50); LibSVM parse MB/s",
+                unit="samples/s", value=out["bolt_infer"]["value"], ms_per_step=out["bolt_infer"]["ms_per_batch"],
+                parts=out)
+
+
 # --------------------------------------------------------------------------- main
 def traffic_probe(seed):
     """Eager dispatches for the rocprofv3 --pmc traffic runs (FETCH_SIZE, then
@@ -748,6 +843,9 @@ def main():
     if "cfg5" in legs:
         extra["cfg5"] = slide_cfg5_leg(min(args.steps, 20), args.seed, timer, leg_cpu)
         log(f"[bench] cfg5 {extra['cfg5']['ms_per_step']:.3f} ms  |A|={extra['cfg5']['mean_active']:.0f}")
+    if "families" in legs:
+        extra["families"] = families_leg(min(args.steps, 30), args.seed, timer, leg_cpu)
+        log(f"[bench] families: bolt {extra['families']['ms_per_step']:.3f} ms per batch")
     if "train5" in legs:
         extra["train5"] = slide_train5_leg(min(args.steps, 5), args.seed, leg_cpu)
         log(f"[bench] train5 {extra['train5']['ms_per_step']:.3f} ms per batch of 256")
