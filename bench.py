@@ -762,6 +762,31 @@ def read_traffic():
     return None
 
 
+def run_only(args, timer, leg_cpu):
+    """One leg on its own (the per-leg kernel traces in profiles/ use this)."""
+    name = args.only
+    if name in ("cfg3", "cfg3b16"):
+        B = 1 if name == "cfg3" else 16
+        model = build_ffn_model(args.layers, 4096, 11008, 256, args.seed, B)
+        r = ffn_leg(name, args.layers, 4096, 11008, 256, 0.15, B, args.steps, args.warmup, args.seed, model, timer)
+        return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items() if not hasattr(v, "shape")}
+    if name == "cfg2":
+        r = ffn_leg("cfg2", 22, 2048, 5632, 128, 0.10, 1, args.steps, 3, args.seed + 2, None, timer)
+        return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items() if not hasattr(v, "shape")}
+    if name in ("cfg4", "cfg4b8"):
+        return attn_leg(name, args.layers, 1 if name == "cfg4" else 8, min(args.steps, 30), 3, args.seed + 4, timer,
+                        leg_cpu)
+    if name == "decoder":
+        return decoder_leg(args.layers, min(args.steps, 30), 3, args.seed + 6, timer, None)
+    if name == "cfg1":
+        return slide_cfg1_leg(min(args.steps, 30), args.seed, timer, leg_cpu)
+    if name == "cfg5":
+        return slide_cfg5_leg(min(args.steps, 20), args.seed, timer, leg_cpu)
+    if name == "train5":
+        return slide_train5_leg(min(args.steps, 5), args.seed, leg_cpu)
+    return families_leg(min(args.steps, 30), args.seed, timer, leg_cpu)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -775,6 +800,8 @@ def main():
     ap.add_argument("--legs", default="all", help="comma list of " + ",".join(ALL_LEGS))
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the dispatches the rocprofv3 --pmc traffic runs count")
+    ap.add_argument("--only", default=None, choices=ALL_LEGS,
+                    help="run one leg alone (no headline; for per-leg kernel traces) and print its JSON")
     args = ap.parse_args()
     ws = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or ws != 1:
@@ -788,6 +815,9 @@ def main():
     legs = ALL_LEGS if args.legs == "all" else [x for x in args.legs.split(",") if x]
     timer = Timer(torch.cuda.Stream())
     leg_cpu = 0.0 if args.no_cpu else args.leg_cpu_seconds
+    if args.only:
+        print(json.dumps({"leg": args.only, **run_only(args, timer, leg_cpu)}), flush=True)
+        return 0
     extra = {}
     # headline: cfg3 batch 1 (and batch 16 on the same layers)
     model = build_ffn_model(args.layers, 4096, 11008, 256, args.seed, 16)

@@ -375,50 +375,51 @@ __global__ __launch_bounds__(64 * RW) void partials_reduce_kernel(const float* _
 }
 
 // Single-row y (=, or +=) sum over g of partial[g][j] for many partial rows:
-// a block owns 16 columns (64 bytes of each partial row), so a 4096-wide row
-// spreads over 256 blocks.  Thread t adds rows t/16, t/16 + 16, ... (all loads
-// issued before the first add), then the 16 row strips are added in strip
-// order: the summation order is fixed for a given number of partial rows.
-// (A template, so that each translation unit including this header keeps its
-// own copy.)
-constexpr int kRed16Rows = 16;  // row strips per block (256 threads)
-constexpr int kRed16U = 16;     // loads per thread in flight (256 rows per pass)
-template <int U = kRed16U>
+// a block owns C columns (C * 4 bytes of each partial row; C = 32 reads whole
+// 128-byte lines), so a 4096-wide row spreads over 4096 / C blocks.  Thread t
+// adds rows t/C, t/C + 256/C, ... (all loads issued before the first add),
+// then the row strips are added in strip order: the summation order is fixed
+// for a given number of partial rows.  (A template, so that each translation
+// unit including this header keeps its own copy.)
+constexpr int kRedCols = 32;
+constexpr int kRed16U = 16;     // loads per thread in flight
+template <int C = kRedCols, int U = kRed16U>
 __global__ __launch_bounds__(256) void partials_reduce16_kernel(const float* __restrict__ partial, int H,
                                                                  int groups, float* __restrict__ y,
                                                                  int accumulate) {
-  __shared__ float sums[kRed16Rows][16];
+  constexpr int kStrips = 256 / C;
+  __shared__ float sums[kStrips][C];
   const int t = threadIdx.x;
-  const int c = t & 15, strip = t >> 4;
-  const int j = blockIdx.x * 16 + c;
+  const int c = t % C, strip = t / C;
+  const int j = blockIdx.x * C + c;
   const int jc = min(j, H - 1);
   const float y0 = (accumulate && strip == 0) ? y[jc] : 0.0f;
   float s = 0.0f;
-  for (int g0 = strip; g0 < groups; g0 += kRed16Rows * U) {
+  for (int g0 = strip; g0 < groups; g0 += kStrips * U) {
     float v[U];
 #pragma unroll
-    for (int q = 0; q < U; ++q) v[q] = partial[(size_t)min(g0 + kRed16Rows * q, groups - 1) * H + jc];
+    for (int q = 0; q < U; ++q) v[q] = partial[(size_t)min(g0 + kStrips * q, groups - 1) * H + jc];
 #pragma unroll
     for (int q = 0; q < U; ++q)
-      if (g0 + kRed16Rows * q < groups) s += v[q];
+      if (g0 + kStrips * q < groups) s += v[q];
   }
   sums[strip][c] = s;
   __syncthreads();
   if (strip == 0) {
     float tot = 0.0f;
 #pragma unroll
-    for (int r = 0; r < kRed16Rows; ++r) tot += sums[r][c];
+    for (int r = 0; r < kStrips; ++r) tot += sums[r][c];
     if (j < H) y[j] = accumulate ? y0 + tot : tot;
   }
 }
 
-// One output row from `groups` partial rows of width H: 16-column blocks
-// when there are enough rows to keep 256 blocks busy, else 64-column blocks.
+// One output row from `groups` partial rows of width H: 32-column blocks
+// when there are many rows, else 64-column blocks.
 inline void partials_reduce_launch(const float* partial, int H, int groups, float* y, int accumulate,
                                    hipStream_t st) {
   if (groups > 64)
-    hipLaunchKernelGGL(partials_reduce16_kernel<>, dim3(ceil_div(H, 16)), dim3(256), 0, st, partial, H, groups,
-                       y, accumulate);
+    hipLaunchKernelGGL(partials_reduce16_kernel<>, dim3(ceil_div(H, kRedCols)), dim3(256), 0, st, partial, H,
+                       groups, y, accumulate);
   else
     hipLaunchKernelGGL((partials_reduce_kernel<1, 4>), dim3(ceil_div(H, 64), 1), dim3(64 * 4), 0, st, partial,
                        H, groups, y, accumulate, nullptr, 0);
