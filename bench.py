@@ -235,7 +235,8 @@ def attn_leg(name, L, B, steps, warmup, seed, timer, cpu_seconds):
     rng = np.random.default_rng(seed)
     t0 = time.time()
     layers, preds = [], []
-    kv = torch.randn(2, nkv, pre, d, generator=g, device="cuda")
+    # BF16 K/V values (cfg4: BF16 Q/K/V): the default handle keeps them as a BF16 prefix
+    kv = torch.randn(2, nkv, pre, d, generator=g, device="cuda").to(torch.bfloat16).float()
     for _ in range(L):
         ws = [(torch.randn(shape, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
               for shape in ((nh * d, H), (nkv * d, H), (nkv * d, H), (H, nh * d))]
@@ -311,7 +312,8 @@ def decoder_leg(L, steps, warmup, seed, timer, cpu_tok_s=None):
     t0 = time.time()
     mlps, npreds = build_ffn_model(L, H, I, Rn, seed + 1, 1)
     attns, hpreds = [], []
-    kv = torch.randn(2, nkv, pre, d, generator=g, device="cuda")
+    # BF16 K/V values (cfg4: BF16 Q/K/V): the default handle keeps them as a BF16 prefix
+    kv = torch.randn(2, nkv, pre, d, generator=g, device="cuda").to(torch.bfloat16).float()
     for _ in range(L):
         ws = [(torch.randn(shape, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
               for shape in ((nh * d, H), (nkv * d, H), (nkv * d, H), (H, nh * d))]

@@ -589,7 +589,9 @@ int kh_sparse_attn_destroy(kh_sparse_attn* a);
  * every value of k and v is a BF16 value).  Synchronous. */
 int kh_sparse_attn_load_cache(kh_sparse_attn* a, int64_t b, const float* k_host,
                               const float* v_host, int64_t len);
-/* Same from f32 device arrays (e.g. a prefill's K/V), enqueued on `stream`. */
+/* Same from f32 device arrays (e.g. a prefill's K/V), enqueued on `stream`;
+ * a KH_KV_BF16 handle checks on the device whether every value is a BF16
+ * value and then keeps the rows in BF16, else in f32 (no host round trip). */
 int kh_sparse_attn_load_cache_dev(kh_sparse_attn* a, int64_t b, const float* k_dev,
                                   const float* v_dev, int64_t len, void* stream);
 /* Copy positions [0, len) of sequence b back as f32 [nkv][len][d]. Synchronous. */

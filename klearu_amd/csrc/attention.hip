@@ -708,6 +708,35 @@ __global__ __launch_bounds__(256) void attn_fill_cache_kernel(const float* __res
   store_kv(dst + (h * max_seq) * (int64_t)D + r, src[i]);
 }
 
+// Device-loaded rows of a KH_KV_BF16 handle: both the f32 and the BF16 copy
+// are written, and *notbf records whether any value of k or v carries bits a
+// BF16 cannot hold; attn_set_pre_kernel then makes the rows a BF16 prefix
+// only when none does (so the cache always holds the values exactly).
+__global__ __launch_bounds__(256) void attn_fill_cache2_kernel(
+    const float* __restrict__ k, const float* __restrict__ v, int64_t len, int D, int64_t total,
+    int max_seq, float* __restrict__ k32, float* __restrict__ v32, uint16_t* __restrict__ k16,
+    uint16_t* __restrict__ v16, int32_t* __restrict__ notbf) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  bool bad = false;
+  if (i < total) {
+    const int64_t per = len * D;
+    const int64_t h = i / per, r = i - h * per;
+    const int64_t o = (h * max_seq) * (int64_t)D + r;
+    const uint32_t kb = __float_as_uint(k[i]), vb = __float_as_uint(v[i]);
+    k32[o] = k[i];
+    v32[o] = v[i];
+    k16[o] = static_cast<uint16_t>(kb >> 16);
+    v16[o] = static_cast<uint16_t>(vb >> 16);
+    bad = ((kb | vb) & 0xffffu) != 0;
+  }
+  if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(notbf, 1);
+}
+
+__global__ void attn_set_pre_kernel(int32_t* __restrict__ pre, const int32_t* __restrict__ notbf,
+                                    int len) {
+  if (threadIdx.x == 0) pre[0] = notbf[0] ? 0 : len;
+}
+
 // o_proj for batch <= 2 with the chunk merge folded in: gather_rows_kernel's
 // column slice x row group over the union rows of WoT, where the value of row
 // h*D + e for token b is computed in the block from the decode chunks (the
@@ -871,6 +900,7 @@ struct kh_sparse_attn {
   float* kc32 = nullptr;
   float* vc32 = nullptr;
   int32_t* pre = nullptr;    // [max_batch]
+  int32_t* notbf = nullptr;  // [1] device-side load check (kh_sparse_attn_load_cache_dev)
   float* cos_t = nullptr;    // [max_seq][d/2]
   float* sin_t = nullptr;
   int32_t* lens = nullptr;   // [max_batch]
@@ -895,6 +925,7 @@ extern "C" int kh_sparse_attn_destroy(kh_sparse_attn* a) {
   dev_free(a->kc32);
   dev_free(a->vc32);
   dev_free(a->pre);
+  dev_free(a->notbf);
   dev_free(a->cos_t);
   dev_free(a->sin_t);
   dev_free(a->lens);
@@ -943,6 +974,7 @@ static int attn_alloc(int hidden, int num_heads, int num_kv_heads, int head_dim,
   a->kc32 = static_cast<float*>(dev_alloc(sizeof(float) * a->seq_elems() * max_batch));
   a->vc32 = static_cast<float*>(dev_alloc(sizeof(float) * a->seq_elems() * max_batch));
   a->pre = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * max_batch));
+  a->notbf = static_cast<int32_t*>(dev_alloc(sizeof(int32_t)));
   a->cos_t = static_cast<float*>(dev_alloc(sizeof(float) * max_seq * half));
   a->sin_t = static_cast<float*>(dev_alloc(sizeof(float) * max_seq * half));
   a->lens = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * max_batch));
@@ -951,7 +983,7 @@ static int attn_alloc(int hidden, int num_heads, int num_kv_heads, int head_dim,
   a->qrows = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * (qd + 1 + num_heads)));
   if (max_batch > 1 && H % 32 == 0 && (2 * kvd + qd) % 16 == 0)
     a->wkvq_t = static_cast<uint16_t*>(dev_alloc(sizeof(uint16_t) * (2 * kvd + qd) * H));
-  if (!a->wkvq || !a->wot || (!a->kv_f32 && (!a->kc16 || !a->vc16)) || !a->kc32 || !a->vc32 || !a->pre ||
+  if (!a->wkvq || !a->wot || (!a->kv_f32 && (!a->kc16 || !a->vc16)) || !a->kc32 || !a->vc32 || !a->pre || !a->notbf ||
       !a->cos_t || !a->sin_t || !a->lens || !a->y || !a->cat || !a->qrows) {
     kh_sparse_attn_destroy(a);
     return KH_ERR_ALLOC;
@@ -1106,22 +1138,31 @@ extern "C" int kh_sparse_attn_load_cache_dev(kh_sparse_attn* a, int64_t b, const
   KH_CHECK_ARG(len == 0 || (k_dev && v_dev), "null cache data");
   hipStream_t st = as_stream(stream);
   const int64_t total = (int64_t)a->nkv * len * a->d;
-  if (total > 0) {
-    // device rows are stored in f32 (exact whatever their values)
-    const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
-    const size_t off = (size_t)b * a->seq_elems();
-    hipLaunchKernelGGL(attn_fill_cache_kernel<float>, dim3(blocks), dim3(256), 0, st, k_dev, len, a->d,
-                       total, a->max_seq, a->kc32 + off);
-    hipLaunchKernelGGL(attn_fill_cache_kernel<float>, dim3(blocks), dim3(256), 0, st, v_dev, len, a->d,
-                       total, a->max_seq, a->vc32 + off);
-    KH_LAUNCHED();
+  const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
+  const size_t off = (size_t)b * a->seq_elems();
+  if (total > 0 && !a->kv_f32) {
+    // both copies, and on the device: a BF16 prefix when every value is a
+    // BF16 value (a BF16 model's prefill), else f32 rows (pre = 0)
+    hipLaunchKernelGGL(attn_set_len_kernel, dim3(1), dim3(64), 0, st, a->notbf, 1, 0);
+    hipLaunchKernelGGL(attn_fill_cache2_kernel, dim3(blocks), dim3(256), 0, st, k_dev, v_dev, len, a->d,
+                       total, a->max_seq, a->kc32 + off, a->vc32 + off, a->kc16 + off, a->vc16 + off,
+                       a->notbf);
+    hipLaunchKernelGGL(attn_set_pre_kernel, dim3(1), dim3(64), 0, st, a->pre + b, a->notbf,
+                       static_cast<int>(len));
+  } else {
+    if (total > 0) {
+      hipLaunchKernelGGL(attn_fill_cache_kernel<float>, dim3(blocks), dim3(256), 0, st, k_dev, len, a->d,
+                         total, a->max_seq, a->kc32 + off);
+      hipLaunchKernelGGL(attn_fill_cache_kernel<float>, dim3(blocks), dim3(256), 0, st, v_dev, len, a->d,
+                         total, a->max_seq, a->vc32 + off);
+    }
+    hipLaunchKernelGGL(attn_set_len_kernel, dim3(1), dim3(64), 0, st, a->pre + b, 1, 0);
   }
   hipLaunchKernelGGL(attn_set_len_kernel, dim3(1), dim3(64), 0, st, a->lens + b, 1,
                      static_cast<int>(len));
-  hipLaunchKernelGGL(attn_set_len_kernel, dim3(1), dim3(64), 0, st, a->pre + b, 1, 0);
   KH_LAUNCHED();
   a->len_host[b] = len;
-  a->pre_host[b] = 0;
+  a->pre_host[b] = -1;  // decided on the device
   return KH_OK;
 }
 

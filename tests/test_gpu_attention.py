@@ -199,6 +199,31 @@ def test_load_cache_dev_matches_host_load(kh, orc, kv):
     np.testing.assert_array_equal(k1, k)
 
 
+@pytest.mark.parametrize("bf16_values", [True, False])
+def test_device_load_decides_storage_exactly(kh, orc, bf16_values):
+    """load_cache_dev on a KH_KV_BF16 handle: BF16-valued rows (a BF16 model's
+    prefill) become a BF16 prefix, others stay f32; either way the decode
+    equals the host-loaded cache's and the unrounded oracle's."""
+    rng = np.random.default_rng(61 + bf16_values)
+    c = Case(orc, rng, 256, 4, 2, 64, 60, 2, [0, 0], 0)
+    k = rng.standard_normal((2, 45, 64)).astype(np.float32)
+    v = rng.standard_normal((2, 45, 64)).astype(np.float32)
+    if bf16_values:
+        k, v = bf16_round(orc, k), bf16_round(orc, v)
+    c.attn.load_cache(0, k, v)
+    c.attn.load_cache_dev(1, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    for b in range(2):
+        c.kc[b][:, :45], c.vc[b][:, :45], c.len[b] = k, v, 45
+    for step in range(3):
+        x = rng.standard_normal((2, 256)).astype(np.float32)
+        heads = [[0, 2], [0, 2]]
+        got = c.attn.forward_sparse(x, heads).cpu().numpy()
+        for b in range(2):
+            close(got[b], c.oracle_step(b, x[b], heads[b]), f"device load bf16={bf16_values} step {step}")
+    k1, _ = c.attn.read_cache(1, 48)
+    np.testing.assert_array_equal(k1[:, :45], k)
+
+
 def test_rejects_bad_shapes(kh, orc):
     from klearu_amd import KlearuError
     from klearu_amd.attention import SparseAttention
