@@ -169,7 +169,11 @@ int kh_lsh_index_create(const kh_hash_family* h, int bucket_type, int capacity,
                         kh_lsh_index** out);
 int kh_lsh_index_destroy(kh_lsh_index* idx);
 /* LshIndexTrait::insert (lsh/index.rs:257-262) for n vectors in order:
- * ids[i] with dense weights w[i*ldw .. i*ldw+input_dim] (tables inner). Mutates. */
+ * ids[i] with dense weights w[i*ldw .. i*ldw+input_dim] (tables inner). Mutates.
+ * Batches of 1024 or more vectors hash on the matrix cores with an exact
+ * sequential replay wherever the sign is not certain (same codes).  The
+ * mutation calls keep their device scratch in the index (about 20 bytes per
+ * vector and table of the largest call) until it is destroyed. */
 int kh_lsh_index_insert(kh_lsh_index* idx, const uint32_t* ids_dev, const float* w_dev,
                         int64_t n, int64_t ldw, void* stream);
 /* Same from precomputed codes[n][num_tables] (e.g. from kh_hash_dense). */

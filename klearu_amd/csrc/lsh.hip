@@ -12,13 +12,23 @@
 // bit-identical to the reference.  SRP is the same computation with a
 // different plane distribution.
 //
+// Large dense batches (index builds and rebuilds) hash on the matrix cores
+// instead: x is split into BF16 hi + lo terms, the ternary planes are exact in
+// BF16, and v_mfma_f32_16x16x32_bf16 gives every (row, plane) sum S' with
+// |S' - S| and |s_seq - S| both below a bound c * sum|x| (S the exact sum,
+// s_seq the reference's sequential f32 sum).  Where |S'| exceeds twice that
+// bound the sign of s_seq is the sign of S'; every other (row, plane) -- ties
+// near zero, non-finite input -- replays the sequential sum in its lane, so
+// codes stay bit-identical.
+//
 // Index build.  Inserting ids in order into L tables is, per bucket, a
 // sequence of ids in insertion order.  The build hashes all vectors, sorts the
 // (bucket, position) pairs with a stable radix sort so that every bucket's
-// inserts are contiguous and in order, then one thread per bucket applies
-// them: FIFO keeps the last `cap` ids; the reservoir replays Algorithm R with
-// the reference's SplitMix64 draws.  Buckets are dense [L][2^k][cap] u32 with
-// len[L][2^k] and the reservoir insertion count[L][2^k].
+// inserts are contiguous and in order, then applies them: FIFO (one thread per
+// bucket) keeps the last `cap` ids; the reservoir's Algorithm R, whose
+// SplitMix64 draws depend only on (count, id), runs one thread per insert, each
+// slot keeping the last insert that targeted it.  Buckets are dense
+// [L][2^k][cap] u32 with len[L][2^k] and the reservoir insertion count[L][2^k].
 //
 // Query.  One block per input gathers its L buckets.  When ids are below
 // 12288 it counts hits in an LDS array indexed by id and compacts in id
@@ -31,6 +41,7 @@
 #include <vector>
 
 #include "lsh_internal.hpp"
+#include "mfma.hpp"
 #include "rng.hpp"
 
 namespace kh {
@@ -84,6 +95,176 @@ __global__ __launch_bounds__(kHashDenseMax) void hash_dense_kernel(
   }
   __syncthreads();
   for (int t = threadIdx.x; t < L; t += blockDim.x) codes[row * L + t] = cw[t];
+}
+
+// Matrix-core hashing: a block of 4 waves hashes 64 rows; wave w owns rows
+// 16w..16w+15 and walks the plane tiles (16 planes each) in groups of kHmGroup
+// accumulators.  Operands follow mfma.hpp: A = x rows (lane l: row l % 16,
+// k (l / 16) * 8 + i), B = planes from the tiled copy bt (the 16 bytes lane l
+// feeds), C = row (l / 16) * 4 + q, plane l % 16 of the tile.  A (row, plane)
+// whose sign the bound does not settle is queued in LDS and replayed after the
+// matrix phase by all threads of the block at once (in place if the queue is
+// full), so the rare replays do not serialise the waves.
+constexpr int kHmRows = 64;
+constexpr int kHmGroup = 8;
+constexpr int kHmMaxPlanes = 1024;
+constexpr int kHmMaxDim = 8192;
+constexpr int kHmQueue = 1024;          // queued replays per block
+constexpr int kHmBatch = 8;             // plane entries in flight per replay
+constexpr int64_t kHmMinBatch = 1024;   // smaller batches take the per-plane kernel
+
+// Eight x values of row xr at dims d0..d0+7 (0 past dim); VEC: two aligned
+// float4 loads (dim a multiple of 32, rows 16-byte aligned).
+template <bool VEC>
+__device__ __forceinline__ void hm_load8(const float* __restrict__ xr, int d0, int dim, float4& a, float4& b) {
+  if constexpr (VEC) {
+    a = *reinterpret_cast<const float4*>(xr + d0);
+    b = *reinterpret_cast<const float4*>(xr + d0 + 4);
+  } else {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float t = xr[min(d0 + i, dim - 1)];
+      v[i] = d0 + i < dim ? t : 0.0f;
+    }
+    a = make_float4(v[0], v[1], v[2], v[3]);
+    b = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+// The reference's sequential sum for one (row, plane): its sign bit.
+__device__ __forceinline__ bool hm_replay(const float* __restrict__ xr, const int32_t* __restrict__ nnz,
+                                          const uint32_t* __restrict__ ent_t, int P, int pl) {
+  float s = 0.0f;
+  const int e1 = nnz[pl];
+  for (int e0 = 0; e0 < e1; e0 += kHmBatch) {
+    uint32_t v[kHmBatch];
+    float xd[kHmBatch];
+#pragma unroll
+    for (int j = 0; j < kHmBatch; ++j) v[j] = ent_t[(size_t)min(e0 + j, e1 - 1) * P + pl];
+#pragma unroll
+    for (int j = 0; j < kHmBatch; ++j) xd[j] = xr[v[j] >> 1];
+#pragma unroll
+    for (int j = 0; j < kHmBatch; ++j)
+      if (e0 + j < e1) s = (v[j] & 1u) ? __fsub_rn(s, xd[j]) : __fadd_rn(s, xd[j]);
+  }
+  return s >= 0.0f;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void hash_dense_mfma_kernel(
+    const uint4* __restrict__ bt, int ksteps, int ntiles, const int32_t* __restrict__ nnz,
+    const uint32_t* __restrict__ ent_t, int k, int L, int dim, const float* __restrict__ x,
+    int64_t ldx, int64_t batch, uint32_t* __restrict__ codes) {
+  constexpr int kW = kHmMaxPlanes / 32 + 1;  // 32-plane words per row (one spare for the code window)
+  __shared__ uint32_t pm[kHmRows][kW];
+  __shared__ uint32_t queue[kHmQueue];
+  __shared__ int nq;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int P = L * k;
+  const int64_t rb = (int64_t)blockIdx.x * kHmRows;
+  const int64_t r0 = rb + wave * 16;
+  for (int i = threadIdx.x; i < kHmRows * kW; i += blockDim.x) (&pm[0][0])[i] = 0u;
+  if (threadIdx.x == 0) nq = 0;
+  // A operand row of this lane (rows past the batch repeat the last one)
+  const float* __restrict__ xa = x + min(r0 + (lane & 15), batch - 1) * ldx;
+  const int kq = (lane >> 4) * 8;
+  // sum |x| of row lane % 16 (the four lanes of a row hold disjoint k ranges),
+  // then of the lane's four output rows
+  float ax = 0.0f;
+  for (int st = 0; st < ksteps; ++st) {
+    float4 a, b;
+    hm_load8<VEC>(xa, st * 32 + kq, dim, a, b);
+    ax += (fabsf(a.x) + fabsf(a.y)) + (fabsf(a.z) + fabsf(a.w)) + (fabsf(b.x) + fabsf(b.y)) + (fabsf(b.z) + fabsf(b.w));
+  }
+  ax += __shfl_xor(ax, 16);
+  ax += __shfl_xor(ax, 32);
+  // Bound on |S' - S| + |s_seq - S| per unit of sum|x|, generous: the lo term's
+  // residual (2^-17), the matrix cores' f32 accumulation over 2 * 32 * ksteps
+  // products (an ulp per add), the sequential sum's dim adds (half an ulp each),
+  // doubled; plus an absolute term for denormals flushed by the matrix cores.
+  const float rel = 2.0f * (0x1p-17f + (float)(2 * 32 * ksteps + dim) * 0x1p-23f);
+  const float abs_t = (float)(4 * 32 * ksteps + 16) * 0x1p-120f;
+  float bound[4];
+  bool fin[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float a = __shfl(ax, (lane >> 4) * 4 + q);
+    bound[q] = a * 1.01f * rel + abs_t;
+    fin[q] = a < 1e37f;   // also false for inf / NaN
+  }
+  __syncthreads();
+  for (int g0 = 0; g0 < ntiles; g0 += kHmGroup) {
+    kh_f32x4 c[kHmGroup];
+#pragma unroll
+    for (int t = 0; t < kHmGroup; ++t) c[t] = kh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // operands of step st + 1 are requested before the products of step st
+    float4 xa0, xb0;
+    uint4 w0[kHmGroup];
+    auto load = [&](int st, float4& a, float4& b, uint4 (&w)[kHmGroup]) {
+      hm_load8<VEC>(xa, st * 32 + kq, dim, a, b);
+      const uint4* __restrict__ bp = bt + ((size_t)st * ntiles + g0) * 64 + lane;
+#pragma unroll
+      for (int t = 0; t < kHmGroup; ++t) w[t] = bp[(size_t)min(t, ntiles - 1 - g0) * 64];
+    };
+    load(0, xa0, xb0, w0);
+    for (int st = 0; st < ksteps; ++st) {
+      float4 xa1, xb1;
+      uint4 w1[kHmGroup];
+      load(min(st + 1, ksteps - 1), xa1, xb1, w1);
+      uint4 hi, lo;
+      split_bf16x8(xa0, xb0, hi, lo);
+#pragma unroll
+      for (int t = 0; t < kHmGroup; ++t) {
+        c[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(hi), as_bf16x8(w0[t]), c[t], 0, 0, 0);
+        c[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(lo), as_bf16x8(w0[t]), c[t], 0, 0, 0);
+      }
+      xa0 = xa1;
+      xb0 = xb1;
+#pragma unroll
+      for (int t = 0; t < kHmGroup; ++t) w0[t] = w1[t];
+    }
+#pragma unroll
+    for (int t = 0; t < kHmGroup; ++t) {
+      const int tile = g0 + t;
+      if (tile >= ntiles) break;
+      const int pl = tile * 16 + (lane & 15);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int rr = wave * 16 + (lane >> 4) * 4 + q;  // row within the block
+        const float sv = c[t][q];
+        bool bit = sv > 0.0f;
+        if (!(fin[q] && fabsf(sv) > bound[q]) && pl < P && rb + rr < batch) {
+          const int slot = atomicAdd(&nq, 1);
+          if (slot < kHmQueue) {
+            queue[slot] = ((uint32_t)rr << 16) | (uint32_t)pl;
+            bit = false;   // set by the replay below
+          } else {
+            bit = hm_replay(x + (rb + rr) * ldx, nnz, ent_t, P, pl);
+          }
+        }
+        const uint64_t m = __ballot(bit && pl < P);
+        if (lane < 4 && (m >> (16 * lane)) & 0xffffull)
+          atomicOr(&pm[wave * 16 + lane * 4 + q][tile >> 1], (uint32_t)((m >> (16 * lane)) & 0xffffull) << (16 * (tile & 1)));
+      }
+    }
+  }
+  __syncthreads();
+  const int nrep = min(nq, kHmQueue);
+  for (int i = threadIdx.x; i < nrep; i += blockDim.x) {
+    const uint32_t e = queue[i];
+    const int rr = (int)(e >> 16), pl = (int)(e & 0xffffu);
+    if (hm_replay(x + (rb + rr) * ldx, nnz, ent_t, P, pl)) atomicOr(&pm[rr][pl >> 5], 1u << (pl & 31));
+  }
+  __syncthreads();
+  // codes: table t takes planes t*k .. t*k+k-1 of its row
+  for (int i = threadIdx.x; i < kHmRows * L; i += blockDim.x) {
+    const int r = i / L, t = i % L;
+    if (rb + r >= batch) continue;
+    const int p0 = t * k, w0 = p0 >> 5;
+    const uint64_t win = (uint64_t)pm[r][w0] | ((uint64_t)pm[r][w0 + 1] << 32);
+    codes[(rb + r) * L + t] = (uint32_t)((win >> (p0 & 31)) & ((1ull << k) - 1ull));
+  }
 }
 
 // One block per (row, group of whole tables): each thread owns one plane of
@@ -157,42 +338,75 @@ __device__ __forceinline__ uint64_t splitmix_mod(uint64_t seed, uint64_t bound) 
   return z % bound;
 }
 
-__global__ void apply_buckets_kernel(int nbuckets, int cap, int type,
-                                     const uint32_t* __restrict__ start,
-                                     const uint32_t* __restrict__ end,
-                                     const uint32_t* __restrict__ spos,
-                                     const uint32_t* __restrict__ ids, uint32_t* __restrict__ data,
-                                     uint32_t* __restrict__ len, uint64_t* __restrict__ count) {
+__global__ void fifo_apply_kernel(int nbuckets, int cap, const uint32_t* __restrict__ start,
+                                  const uint32_t* __restrict__ end,
+                                  const uint32_t* __restrict__ spos,
+                                  const uint32_t* __restrict__ ids, uint32_t* __restrict__ data,
+                                  uint32_t* __restrict__ len) {
   const int key = blockIdx.x * blockDim.x + threadIdx.x;
   if (key >= nbuckets) return;
   const uint32_t s = start[key], e = end[key];
   if (e <= s) return;
   uint32_t* d = data + (size_t)key * cap;
-  uint32_t l = len[key];
-  if (type == KH_BUCKET_FIFO) {
-    const uint32_t m = e - s;
-    const uint32_t total = l + m;
-    const uint32_t keep = min(total, (uint32_t)cap);
-    const uint32_t drop = total - keep;
-    uint32_t o = 0;
-    for (uint32_t q = drop; q < l; ++q) d[o++] = d[q];
-    const uint32_t skip = drop > l ? drop - l : 0u;
-    for (uint32_t j = s + skip; j < e; ++j) d[o++] = ids[spos[j]];
-    len[key] = keep;
+  const uint32_t l = len[key];
+  const uint32_t m = e - s;
+  const uint32_t total = l + m;
+  const uint32_t keep = min(total, (uint32_t)cap);
+  const uint32_t drop = total - keep;
+  uint32_t o = 0;
+  for (uint32_t q = drop; q < l; ++q) d[o++] = d[q];
+  const uint32_t skip = drop > l ? drop - l : 0u;
+  for (uint32_t j = s + skip; j < e; ++j) d[o++] = ids[spos[j]];
+  len[key] = keep;
+}
+
+// Reservoir inserts in parallel (ReservoirBucket::insert, bucket/reservoir.rs:
+// 50-67).  Insert j of a bucket's run happens at count c0 + j + 1; it pushes
+// into slot len0 + j while the bucket is not full, and otherwise replaces the
+// slot the reference's two draws pick, or nothing.  The draws depend only on
+// (count, id), so every insert's target is known up front and a slot ends up
+// holding the last insert that targeted it: each insert records j + 1 with
+// atomicMax, then one thread per slot copies the winner's id.
+__global__ void reservoir_targets_kernel(int64_t m, int cap, const uint32_t* __restrict__ skeys,
+                                         const uint32_t* __restrict__ start,
+                                         const uint32_t* __restrict__ spos,
+                                         const uint32_t* __restrict__ ids,
+                                         const uint32_t* __restrict__ len,
+                                         const uint64_t* __restrict__ count,
+                                         uint32_t* __restrict__ last) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= m) return;
+  const uint32_t key = skeys[i];
+  const uint32_t j = (uint32_t)(i - start[key]);
+  const uint32_t l0 = len[key];
+  const uint32_t id = ids[spos[i]];
+  uint32_t slot = 0xffffffffu;
+  if (l0 < (uint32_t)cap && j < (uint32_t)cap - l0) {
+    slot = l0 + j;
   } else {
-    uint64_t c = count[key];
-    for (uint32_t j = s; j < e; ++j) {
-      const uint32_t id = ids[spos[j]];
-      c += 1;
-      if (l < (uint32_t)cap) {
-        d[l++] = id;
-      } else {
-        const uint64_t seed = c * 0x517cc1b727220a95ull + (uint64_t)id;
-        if (splitmix_mod(seed, c) < (uint64_t)cap) d[splitmix_mod(seed + 1, (uint64_t)cap)] = id;
-      }
-    }
-    len[key] = l;
-    count[key] = c;
+    const uint64_t c = count[key] + j + 1;
+    const uint64_t seed = c * 0x517cc1b727220a95ull + (uint64_t)id;
+    if (splitmix_mod(seed, c) < (uint64_t)cap) slot = (uint32_t)splitmix_mod(seed + 1, (uint64_t)cap);
+  }
+  if (slot != 0xffffffffu) atomicMax(&last[(size_t)key * cap + slot], j + 1u);
+}
+
+__global__ void reservoir_apply_kernel(int64_t nslots, int cap, const uint32_t* __restrict__ start,
+                                       const uint32_t* __restrict__ end,
+                                       const uint32_t* __restrict__ spos,
+                                       const uint32_t* __restrict__ ids,
+                                       const uint32_t* __restrict__ last, uint32_t* __restrict__ data,
+                                       uint32_t* __restrict__ len, uint64_t* __restrict__ count) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= nslots) return;
+  const int64_t key = q / cap;
+  const uint32_t s = start[key], e = end[key];
+  if (e <= s) return;
+  const uint32_t w = last[q];
+  if (w) data[q] = ids[spos[s + w - 1]];
+  if (q % cap == 0) {
+    len[key] = min((uint32_t)cap, len[key] + (e - s));
+    count[key] += e - s;
   }
 }
 
@@ -259,9 +473,20 @@ __global__ void id_bits_kernel(const uint32_t* __restrict__ ids, int64_t n, uint
 
 // Largest id of the list (ids are below 2^31 for an index, checked by the
 // caller from this value).
-__global__ void max_id_kernel(const uint32_t* __restrict__ ids, int64_t n, uint32_t* __restrict__ mx) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) atomicMax(mx, ids[i]);
+// One atomic per block: every atomic on the single result word is serialised.
+__global__ __launch_bounds__(256) void max_id_kernel(const uint32_t* __restrict__ ids, int64_t n,
+                                                     uint32_t* __restrict__ mx) {
+  __shared__ uint32_t wm[4];
+  uint32_t m = 0u;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    m = max(m, ids[i]);
+  m = wave_max_u32(m);
+  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    m = max(max(wm[0], wm[1]), max(wm[2], wm[3]));
+    if (m) atomicMax(mx, m);
+  }
 }
 
 __global__ void index_clear_kernel(uint32_t* __restrict__ len, uint64_t* __restrict__ count, int nb) {
@@ -524,6 +749,18 @@ int hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx, int6
                       uint32_t* codes, hipStream_t st) {
   if (batch == 0) return KH_OK;
   if (h->kind != KH_FAMILY_TERNARY) return rank_hash_dense_launch(h, x, ldx, batch, codes, st);
+  if (h->bt_dev && batch >= kHmMinBatch) {
+    for (int64_t b0 = 0; b0 < batch; b0 += (int64_t)65535 * kHmRows) {
+      const int64_t nb = std::min<int64_t>(batch - b0, (int64_t)65535 * kHmRows);
+      const bool vec = h->dim % 32 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+      hipLaunchKernelGGL(vec ? hash_dense_mfma_kernel<true> : hash_dense_mfma_kernel<false>,
+                         dim3((unsigned)ceil_div(nb, kHmRows)), dim3(256), 0, st, h->bt_dev, h->bt_ksteps,
+                         h->bt_tiles, h->nnz, h->ent_t, h->k, h->L, h->dim, x + b0 * ldx, ldx, nb,
+                         codes + b0 * h->L);
+      KH_LAUNCHED();
+    }
+    return KH_OK;
+  }
   const int in_lds = h->dim <= 12288 ? 1 : 0;
   const size_t lds = sizeof(float) * (in_lds ? h->dim : 0) + sizeof(uint32_t) * h->L;
   for (int64_t b0 = 0; b0 < batch; b0 += 65535 * 16) {
@@ -645,6 +882,34 @@ static int family_finish(kh_hash_family* h, kh_hash_family** out) {
       else if (pl[d] == -1) ent[j++ * P + p] = ((uint32_t)d << 1) | 1u;
     }
   }
+  // BF16 copy of the planes in the matrix-core operand order (hashing large
+  // dense batches): entry (step, tile, lane) holds 8 k values of one plane
+  std::vector<uint16_t> bt;
+  if (P <= kHmMaxPlanes && h->dim <= kHmMaxDim) {
+    h->bt_ksteps = (h->dim + 31) / 32;
+    h->bt_tiles = (P + 15) / 16;
+    bt.assign((size_t)h->bt_ksteps * h->bt_tiles * 64 * 8, 0);
+    for (int st = 0; st < h->bt_ksteps; ++st)
+      for (int tile = 0; tile < h->bt_tiles; ++tile)
+        for (int l = 0; l < 64; ++l) {
+          const int p = tile * 16 + (l & 15);
+          for (int i = 0; i < 8; ++i) {
+            const int d = st * 32 + (l >> 4) * 8 + i;
+            const int8_t v = p < P && d < h->dim ? h->planes_host[(size_t)p * h->dim + d] : 0;
+            bt[(((size_t)st * h->bt_tiles + tile) * 64 + l) * 8 + i] = v == 1 ? 0x3F80 : (v == -1 ? 0xBF80 : 0);
+          }
+        }
+    h->bt_dev = static_cast<uint4*>(dev_alloc(sizeof(uint16_t) * bt.size()));
+    if (!h->bt_dev) {
+      kh_hash_family_destroy(h);
+      return KH_ERR_ALLOC;
+    }
+    if (hipMemcpy(h->bt_dev, bt.data(), sizeof(uint16_t) * bt.size(), hipMemcpyHostToDevice) != hipSuccess) {
+      set_error("plane upload failed");
+      kh_hash_family_destroy(h);
+      return KH_ERR_HIP;
+    }
+  }
   h->planes_dev = static_cast<int8_t*>(dev_alloc(h->planes_host.size()));
   h->nnz = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * std::max(P, 1)));
   h->ent_t = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * ent.size()));
@@ -719,6 +984,7 @@ extern "C" int kh_hash_family_destroy(kh_hash_family* h) {
   dev_free(h->planes_dev);
   dev_free(h->nnz);
   dev_free(h->ent_t);
+  dev_free(h->bt_dev);
   dev_free(h->windows_dev);
   dev_free(h->fallback_dev);
   dev_free(h->perms_dev);
@@ -815,18 +1081,29 @@ extern "C" int kh_lsh_index_clear(kh_lsh_index* idx, void* stream) {
 
 namespace {
 
-// Device scratch of one mutation call, freed on return (mutations are
-// `&mut self` calls and synchronise anyway).
+// Device scratch of one mutation call (mutations are `&mut self` calls and
+// synchronise before they return).  The buffers come from the index's arena,
+// a stack of grow-only slots: a call takes the next slots and gives them back
+// on return, so repeated inserts and rebuilds allocate nothing once the
+// largest call has run.
 struct CallBufs {
-  std::vector<void*> v;
-  ~CallBufs() {
-    for (void* p : v) dev_free(p);
-  }
+  kh::ScratchArena& a;
+  size_t mark;
+  explicit CallBufs(kh::ScratchArena& arena) : a(arena), mark(arena.cursor) {}
+  ~CallBufs() { a.cursor = mark; }
   template <typename T>
   T* get(size_t n) {
-    void* p = dev_alloc(sizeof(T) * (n ? n : 1));
-    if (p) v.push_back(p);
-    return static_cast<T*>(p);
+    const size_t bytes = sizeof(T) * (n ? n : 1);
+    if (a.cursor == a.slots.size()) a.slots.push_back({nullptr, 0});
+    auto& sl = a.slots[a.cursor];
+    if (sl.second < bytes) {
+      dev_free(sl.first);
+      sl.first = dev_alloc(bytes);
+      sl.second = sl.first ? bytes : 0;
+    }
+    if (!sl.first) return nullptr;
+    ++a.cursor;
+    return static_cast<T*>(sl.first);
   }
 };
 
@@ -837,7 +1114,8 @@ int checked_max_id(const uint32_t* ids_dev, int64_t n, hipStream_t st, CallBufs&
   uint32_t* mx = cb.get<uint32_t>(1);
   if (!mx) return KH_ERR_ALLOC;
   KH_HIP(hipMemsetAsync(mx, 0, sizeof(uint32_t), st));
-  hipLaunchKernelGGL(max_id_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, st, ids_dev, n, mx);
+  hipLaunchKernelGGL(max_id_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 256)), dim3(256), 0, st,
+                     ids_dev, n, mx);
   KH_LAUNCHED();
   uint32_t v = 0;
   KH_HIP(hipMemcpyAsync(&v, mx, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
@@ -851,7 +1129,7 @@ int checked_max_id(const uint32_t* ids_dev, int64_t n, hipStream_t st, CallBufs&
 // the vectors' order kept inside each group (stable radix sort): spos lists
 // vector positions, start/end delimit each bucket's run.
 struct Groups {
-  uint32_t *spos = nullptr, *start = nullptr, *end = nullptr;
+  uint32_t *spos = nullptr, *start = nullptr, *end = nullptr, *skeys = nullptr;
 };
 int group_by_bucket(const kh_lsh_index* idx, const uint32_t* codes_dev, int64_t n, hipStream_t st,
                     CallBufs& cb, Groups* g) {
@@ -863,6 +1141,7 @@ int group_by_bucket(const kh_lsh_index* idx, const uint32_t* codes_dev, int64_t 
   uint32_t* keys = cb.get<uint32_t>(m);
   uint32_t* pos = cb.get<uint32_t>(m);
   uint32_t* skeys = cb.get<uint32_t>(m);
+  g->skeys = skeys;
   g->spos = cb.get<uint32_t>(m);
   g->start = cb.get<uint32_t>(nbk);
   g->end = cb.get<uint32_t>(nbk);
@@ -900,7 +1179,7 @@ extern "C" int kh_lsh_index_insert_codes(kh_lsh_index* idx, const uint32_t* ids_
   if (n == 0) return KH_OK;
   KH_CHECK_ARG(ids_dev && codes_dev, "null argument");
   hipStream_t st = as_stream(stream);
-  CallBufs cb;
+  CallBufs cb(idx->arena);
   uint32_t mx = 0;
   int rc = checked_max_id(ids_dev, n, st, cb, &mx);  // before anything is inserted
   if (rc != KH_OK) return rc;
@@ -908,9 +1187,23 @@ extern "C" int kh_lsh_index_insert_codes(kh_lsh_index* idx, const uint32_t* ids_
   rc = group_by_bucket(idx, codes_dev, n, st, cb, &g);
   if (rc != KH_OK) return rc;
   const int nbk = idx->L * idx->nb;
-  hipLaunchKernelGGL(apply_buckets_kernel, dim3(ceil_div(nbk, 64)), dim3(64), 0, st, nbk, idx->cap,
-                     idx->type, g.start, g.end, g.spos, ids_dev, idx->data, idx->len, idx->count);
-  KH_LAUNCHED();
+  if (idx->type == KH_BUCKET_RESERVOIR) {
+    const int64_t m = n * idx->L, nslots = (int64_t)nbk * idx->cap;
+    uint32_t* last = cb.get<uint32_t>(nslots);
+    if (!last) return KH_ERR_ALLOC;
+    KH_HIP(hipMemsetAsync(last, 0, sizeof(uint32_t) * nslots, st));
+    hipLaunchKernelGGL(reservoir_targets_kernel, dim3((unsigned)ceil_div(m, 256)), dim3(256), 0, st, m,
+                       idx->cap, g.skeys, g.start, g.spos, ids_dev, idx->len, idx->count, last);
+    KH_LAUNCHED();
+    hipLaunchKernelGGL(reservoir_apply_kernel, dim3((unsigned)ceil_div(nslots, 256)), dim3(256), 0, st,
+                       nslots, idx->cap, g.start, g.end, g.spos, ids_dev, last, idx->data, idx->len,
+                       idx->count);
+    KH_LAUNCHED();
+  } else {
+    hipLaunchKernelGGL(fifo_apply_kernel, dim3(ceil_div(nbk, 64)), dim3(64), 0, st, nbk, idx->cap,
+                       g.start, g.end, g.spos, ids_dev, idx->data, idx->len);
+    KH_LAUNCHED();
+  }
   KH_HIP(hipStreamSynchronize(st));  // the call's scratch is freed on return
   idx->id_bound = std::max(idx->id_bound, mx + 1u);
   return KH_OK;
@@ -923,7 +1216,7 @@ extern "C" int kh_lsh_index_insert(kh_lsh_index* idx, const uint32_t* ids_dev, c
   if (n == 0) return KH_OK;
   KH_CHECK_ARG(ids_dev && w_dev, "null argument");
   hipStream_t st = as_stream(stream);
-  CallBufs cb;
+  CallBufs cb(idx->arena);
   uint32_t* codes = cb.get<uint32_t>(n * idx->L);
   if (!codes) return KH_ERR_ALLOC;
   int rc = hash_dense_launch(idx->h, w_dev, ldw, n, codes, st);
@@ -939,7 +1232,7 @@ extern "C" int kh_lsh_index_insert_sparse(kh_lsh_index* idx, const uint32_t* ids
   if (n == 0) return KH_OK;
   KH_CHECK_ARG(ids_dev && xoff_dev, "null argument");
   hipStream_t st = as_stream(stream);
-  CallBufs cb;
+  CallBufs cb(idx->arena);
   uint32_t* codes = cb.get<uint32_t>(n * idx->L);
   if (!codes) return KH_ERR_ALLOC;
   int rc = hash_sparse_launch(idx->h, xoff_dev, xidx_dev, xval_dev, n, codes, st);
@@ -954,7 +1247,7 @@ extern "C" int kh_lsh_index_remove_codes(kh_lsh_index* idx, const uint32_t* ids_
   if (n == 0) return KH_OK;
   KH_CHECK_ARG(ids_dev && codes_dev, "null argument");
   hipStream_t st = as_stream(stream);
-  CallBufs cb;
+  CallBufs cb(idx->arena);
   Groups g;
   int rc = group_by_bucket(idx, codes_dev, n, st, cb, &g);
   if (rc != KH_OK) return rc;
@@ -974,7 +1267,7 @@ extern "C" int kh_lsh_index_remove_with_weights(kh_lsh_index* idx, const uint32_
   if (n == 0) return KH_OK;
   KH_CHECK_ARG(ids_dev && w_dev, "null argument");
   hipStream_t st = as_stream(stream);
-  CallBufs cb;
+  CallBufs cb(idx->arena);
   uint32_t* codes = cb.get<uint32_t>(n * idx->L);
   if (!codes) return KH_ERR_ALLOC;
   int rc = hash_dense_launch(idx->h, w_dev, ldw, n, codes, st);
@@ -989,7 +1282,7 @@ extern "C" int kh_lsh_index_remove(kh_lsh_index* idx, const uint32_t* ids_dev, i
   if (n == 0 || idx->id_bound == 0) return KH_OK;
   KH_CHECK_ARG(ids_dev != nullptr, "null argument");
   hipStream_t st = as_stream(stream);
-  CallBufs cb;
+  CallBufs cb(idx->arena);
   const uint32_t words = (idx->id_bound + 31u) >> 5;  // id_bound <= 2^31
   uint32_t* bits = cb.get<uint32_t>(words);
   if (!bits) return KH_ERR_ALLOC;

@@ -21,7 +21,25 @@ struct kh_hash_family {
   int32_t* nnz = nullptr;           // [L*k]
   uint32_t* ent_t = nullptr;        // [ent_rows][L*k]
   int ent_rows = 0;                 // max nnz rounded up to the hash kernel's batch
+  // Planes as BF16 matrix-core operands (L*k <= 1024, dim <= 8192):
+  // [ceil(dim/32)][ceil(L*k/16)][64 lanes] x 8 values; null otherwise.
+  uint4* bt_dev = nullptr;
+  int bt_ksteps = 0, bt_tiles = 0;
 };
+
+namespace kh {
+// Grow-only device scratch slots of an index's mutation calls, used as a stack.
+struct ScratchArena {
+  std::vector<std::pair<void*, size_t>> slots;
+  size_t cursor = 0;
+  ScratchArena() = default;
+  ScratchArena(const ScratchArena&) = delete;
+  ScratchArena& operator=(const ScratchArena&) = delete;
+  ~ScratchArena() {
+    for (auto& s : slots) dev_free(s.first);
+  }
+};
+}  // namespace kh
 
 struct kh_lsh_index {
   const kh_hash_family* h = nullptr;
@@ -31,6 +49,7 @@ struct kh_lsh_index {
   uint64_t* count = nullptr;  // [L][nb]
   uint32_t id_bound = 0;      // 1 + largest id inserted so far (ids are below 2^31)
   mutable kh::StreamWs ws;    // query scratch per stream
+  kh::ScratchArena arena;     // insert / remove / rebuild scratch, kept between calls
 };
 
 namespace kh {

@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_kernel(
 // formed into LDS first (kL1Chains * n_in floats; all weight loads of the
 // block are in flight at once), then the consumer wave runs its chains over
 // them with no further barrier, reading 32 steps ahead of the adds.  Wave 0
-// is the consumer, waves 1..kL1Prod the producers; kL1Help more waves only
+// is the consumer, kL1Prod waves the producers; kL1Help more waves only
 // stage x and share the RmsNorm sum (two waves per SIMD run its windows).
 constexpr int kL1LdsIn = 4096;
 constexpr int kL1Help = 3;  // waves that only stage x and share the RmsNorm sum
@@ -216,7 +216,12 @@ __global__ __launch_bounds__(kL1LdsThreads) void pred_l1_lds_kernel(
   const int c0 = blockIdx.x * kL1Chains;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nblk = (n_in + 7) >> 3;
-  const int p = wave - 1;
+  // Waves are placed on the CU's four SIMDs in turn (wave w on SIMD w % 4), so
+  // the producers are waves 1, 2, 3 and 5 and the helpers 4, 6 and 7: the
+  // consumer (wave 0) shares its SIMD only with a helper, which is idle while
+  // the chain runs.
+  static_assert(kL1Prod == 4 && kL1Help == 3, "wave roles");
+  const int p = wave <= 3 ? wave - 1 : (wave == 5 ? 3 : -1);
   const float* xr = x + (size_t)b * n_in;
   const int n4 = n_in >> 2;
   // Every wave first requests its share of x (and of the norm weights), then
@@ -238,7 +243,7 @@ __global__ __launch_bounds__(kL1LdsThreads) void pred_l1_lds_kernel(
     }
   }
   V pre[SPP][kL1Q];
-  const bool prod = wave >= 1 && wave <= kL1Prod;
+  const bool prod = p >= 0;
   if (prod) {
     const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
 #pragma unroll

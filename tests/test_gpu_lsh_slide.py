@@ -67,6 +67,45 @@ def test_hash_dense_bit_exact(kh, orc, dim, k, L, batch):
     assert fam.hash_dense(x[2], L - 1) == orc.hash_dense(fam.planes(), x[2], L - 1)
 
 
+def _hard_rows(rng, batch, dim):
+    """Rows for the matrix-core hashing path (batches of >= 1024 rows): most are
+    N(0,1); the rest force its exact fallback -- small integers (many sums
+    exactly zero), zero and -0.0 rows, denormals, tiny and huge magnitudes,
+    overflowing sums, inf and NaN."""
+    x = rng.standard_normal((batch, dim)).astype(np.float32)
+    q = batch // 8
+    x[:q] = rng.integers(-2, 3, (q, dim)).astype(np.float32)
+    x[q] = 0.0
+    x[q + 1] = -0.0
+    x[q + 2] = rng.standard_normal(dim).astype(np.float32) * np.float32(1e-41)
+    x[q + 3] = rng.standard_normal(dim).astype(np.float32) * np.float32(1e-30)
+    x[q + 4] = rng.standard_normal(dim).astype(np.float32) * np.float32(1e36)
+    x[q + 5, ::3] = np.float32(3e38)
+    x[q + 6, dim // 2] = np.inf
+    x[q + 7, dim // 3] = np.nan
+    x[q + 8] = 1.0
+    x[q + 8, ::2] = -1.0
+    return x
+
+
+@pytest.mark.parametrize("dim,k,L,batch,srp", [(128, 9, 50, 4096, False), (100, 6, 7, 1500, False),
+                                               (784, 6, 50, 2048, False), (128, 9, 50, 1024, True),
+                                               (4096, 16, 8, 1100, False), (33, 24, 3, 1030, False)])
+def test_hash_dense_matrix_core_path_bit_exact(kh, orc, dim, k, L, batch, srp):
+    """Batches of >= 1024 rows hash on the matrix cores: a sign is taken from the
+    MFMA sum only where it exceeds the error bound, every other (row, plane)
+    replays the sequential sum.  Codes must equal the oracle's replay."""
+    from klearu_amd.lsh import SimHash, SparseRandomProjection
+    rng = np.random.default_rng(dim * 31 + k)
+    fam = SparseRandomProjection(dim, k, L, 1.0 / 3.0, 7) if srp else SimHash(dim, k, L, 42)
+    x = _hard_rows(rng, batch, dim)
+    got = fam.hash_dense_batch(x).cpu().numpy().view(np.uint32)
+    want = orc.hash_dense_batch(fam.planes(), x)
+    np.testing.assert_array_equal(got, want)
+    q = batch // 8
+    assert np.all(got[q] == (1 << k) - 1) and np.all(got[q + 1] == (1 << k) - 1)
+
+
 def test_hash_sparse_matches_dense(kh, orc):
     from klearu_amd.lsh import SparseVector, SimHash
     rng = np.random.default_rng(5)
