@@ -2,14 +2,14 @@
 // WtaHash (crates/klearu-core/src/hash/wta.rs), DwtaHash (hash/dwta.rs) and
 // MinHash / densified one-permutation hashing (hash/minhash.rs).
 //
-// One thread per (row, table).  WTA packs the k window argmax positions
+// WTA and DWTA: one thread per (row, table).  WTA packs the k window argmax positions
 // (first strict maximum from -inf) from bit 0 up, bits_per_window each;
 // DWTA's sparse form takes the argmax over the window dimensions that are
 // stored in the row and, for a window with none, a position fixed per
 // (table, window) by std's DefaultHasher (precomputed on the host); MinHash
 // takes per-bin minima of the permuted nonzero dimensions, fills empty bins
 // from the next non-empty bin (circularly) and combines them as
-// sum(h_i * P^i) in wrapping u64 arithmetic.  Codes are returned as their
+// sum(h_i * P^i) in wrapping u64 arithmetic (one block per row).  Codes are returned as their
 // low 32 bits (an index keeps the low k <= 24 bits).
 #include <algorithm>
 #include <cmath>
@@ -103,13 +103,96 @@ __global__ __launch_bounds__(kRankThreads) void dwta_sparse_kernel(
   codes[q] = static_cast<uint32_t>(h);
 }
 
-// MinHash over dense rows (nonzero = x != 0, in index order) or CSR rows
-// (every stored index, minhash.rs:151-153).
+// MinHash over dense rows (nonzero = x != 0) or CSR rows (every stored index
+// below dim, minhash.rs:151-153).  One block per row: a dense row's nonzero
+// dimensions are first collected in LDS (a bin minimum does not depend on the
+// order they are taken in); then each wave takes one table at a time, its
+// lanes striding over the nonzeros with an LDS atomicMin per (bin, value),
+// and lane 0 densifies and combines the table's k bins.
+constexpr int kMhThreads = 256;
+constexpr int kMhWaves = kMhThreads / 64;
+constexpr int kMhMaxStage = 16384;  // dense rows up to this dim stage their nonzeros in LDS
+constexpr int64_t kMhMaxRows = 1 << 22;  // rows (blocks) per launch
+
 template <bool SPARSE>
-__global__ __launch_bounds__(kRankThreads) void minhash_kernel(
+__global__ __launch_bounds__(kMhThreads) void minhash_rows_kernel(
     const uint32_t* __restrict__ perms, int dim, int k, int L, const float* __restrict__ x,
     int64_t ldx, const int64_t* __restrict__ xoff, const uint32_t* __restrict__ xidx,
-    int64_t batch, uint32_t* __restrict__ codes) {
+    uint32_t* __restrict__ codes) {
+  extern __shared__ uint32_t nzd[];  // dense: the row's nonzero dimensions (any order)
+  __shared__ uint32_t wmin[kMhWaves][kMaxMinHashBins];
+  __shared__ int nnz_s;
+  const int64_t row = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t* list;
+  int64_t nnz;
+  if constexpr (SPARSE) {
+    const int64_t a = xoff[row];
+    list = xidx + a;
+    nnz = xoff[row + 1] - a;
+  } else {
+    if (threadIdx.x == 0) nnz_s = 0;
+    __syncthreads();
+    const float* __restrict__ xr = x + row * ldx;
+    for (int d0 = 0; d0 < dim; d0 += kMhThreads) {  // one LDS atomic per wave and step
+      const int d = d0 + static_cast<int>(threadIdx.x);
+      const float v = xr[min(d, dim - 1)];
+      const bool nz = d < dim && v != 0.0f;
+      const uint64_t bal = __ballot(nz);
+      int base = 0;
+      if (lane == 0 && bal) base = atomicAdd(&nnz_s, static_cast<int>(__popcll(bal)));
+      base = __shfl(base, 0);
+      const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0));
+      if (nz) nzd[base + below] = static_cast<uint32_t>(d);
+    }
+    __syncthreads();
+    list = nzd;
+    nnz = nnz_s;
+  }
+  const uint32_t bin_size = static_cast<uint32_t>((dim + k - 1) / k);
+  for (int t0 = 0; t0 < L; t0 += kMhWaves) {
+    const int t = t0 + wave;
+    if (lane < kMaxMinHashBins) wmin[wave][lane] = 0xffffffffu;
+    __syncthreads();
+    if (t < L) {
+      const uint32_t* __restrict__ perm = perms + static_cast<size_t>(t) * dim;
+      for (int64_t e = lane; e < nnz; e += 64) {
+        const uint32_t d = list[e];
+        if (SPARSE && d >= static_cast<uint32_t>(dim)) continue;
+        const uint32_t pv = perm[d];
+        atomicMin(&wmin[wave][pv / bin_size], pv);
+      }
+    }
+    __syncthreads();
+    if (t < L && lane == 0) {
+      // densify (minhash.rs:76-104): an empty bin takes the next non-empty
+      // bin circularly, so one backward pass seeded with the first non-empty
+      // bin fills them all; with every bin empty all become 0
+      uint32_t first = 0xffffffffu;
+      for (int i = k - 1; i >= 0; --i)
+        if (wmin[wave][i] != 0xffffffffu) first = wmin[wave][i];
+      uint32_t cur = first == 0xffffffffu ? 0u : first;
+      uint32_t m[kMaxMinHashBins];
+      for (int i = k - 1; i >= 0; --i) {
+        if (wmin[wave][i] != 0xffffffffu) cur = wmin[wave][i];
+        m[i] = cur;
+      }
+      uint64_t h = 0, pp = 1;
+      for (int i = 0; i < k; ++i) {
+        h += static_cast<uint64_t>(m[i]) * pp;
+        pp *= kMinHashPrime;
+      }
+      codes[row * L + t] = static_cast<uint32_t>(h & ((1ull << k) - 1ull));
+    }
+  }
+}
+
+// MinHash over dense rows too wide to stage: one thread per (row, table),
+// walking the row in index order.
+__global__ __launch_bounds__(kRankThreads) void minhash_kernel(
+    const uint32_t* __restrict__ perms, int dim, int k, int L, const float* __restrict__ x,
+    int64_t ldx, int64_t batch, uint32_t* __restrict__ codes) {
   const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (q >= batch * L) return;
   const int64_t row = q / L;
@@ -119,25 +202,17 @@ __global__ __launch_bounds__(kRankThreads) void minhash_kernel(
   uint32_t mins[kMaxMinHashBins];
 #pragma unroll
   for (int i = 0; i < kMaxMinHashBins; ++i) mins[i] = 0xffffffffu;
-  auto take = [&](uint32_t d) {
+  const float* xr = x + row * ldx;
+  for (int d = 0; d < dim; ++d) {
+    if (xr[d] == 0.0f) continue;
     const uint32_t pv = perm[d];
     const uint32_t bin = pv / bin_size;
 #pragma unroll
     for (int i = 0; i < kMaxMinHashBins; ++i)
       if (i == static_cast<int>(bin) && pv < mins[i]) mins[i] = pv;
-  };
-  if (SPARSE) {
-    for (int64_t e = xoff[row]; e < xoff[row + 1]; ++e)
-      if (xidx[e] < static_cast<uint32_t>(dim)) take(xidx[e]);
-  } else {
-    const float* xr = x + row * ldx;
-    for (int d = 0; d < dim; ++d)
-      if (xr[d] != 0.0f) take(static_cast<uint32_t>(d));
   }
-  // densify (minhash.rs:76-104): an empty bin takes the next non-empty bin
-  // circularly, so one backward pass seeded with the first non-empty bin
-  // fills them all; with every bin empty all become 0.  All indices below are
-  // compile-time constants, so mins stays in registers.
+  // densify and combine as minhash_rows_kernel does; every index below is a
+  // compile-time constant, so mins stays in registers
   uint32_t first = 0xffffffffu;
 #pragma unroll
   for (int i = kMaxMinHashBins - 1; i >= 0; --i)
@@ -158,8 +233,7 @@ __global__ __launch_bounds__(kRankThreads) void minhash_kernel(
       pp *= kMinHashPrime;
     }
   }
-  const uint64_t mask = (1ull << k) - 1ull;
-  codes[q] = static_cast<uint32_t>(h & mask);
+  codes[q] = static_cast<uint32_t>(h & ((1ull << k) - 1ull));
 }
 
 int rank_hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx, int64_t batch,
@@ -167,9 +241,17 @@ int rank_hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx,
   if (batch == 0) return KH_OK;
   const int64_t n = batch * h->L;
   const unsigned blocks = static_cast<unsigned>((n + kRankThreads - 1) / kRankThreads);
-  if (h->kind == KH_FAMILY_MINHASH)
-    hipLaunchKernelGGL(minhash_kernel<false>, dim3(blocks), dim3(kRankThreads), 0, st, h->perms_dev,
-                       h->dim, h->k, h->L, x, ldx, nullptr, nullptr, batch, codes);
+  if (h->kind == KH_FAMILY_MINHASH && h->dim <= kMhMaxStage) {
+    for (int64_t b0 = 0; b0 < batch; b0 += kMhMaxRows) {
+      hipLaunchKernelGGL(minhash_rows_kernel<false>, dim3(static_cast<unsigned>(std::min(batch - b0, kMhMaxRows))),
+                         dim3(kMhThreads), sizeof(uint32_t) * h->dim, st, h->perms_dev, h->dim, h->k, h->L,
+                         x + b0 * ldx, ldx, nullptr, nullptr, codes + b0 * h->L);
+      KH_LAUNCHED();
+    }
+    return KH_OK;
+  } else if (h->kind == KH_FAMILY_MINHASH)
+    hipLaunchKernelGGL(minhash_kernel, dim3(blocks), dim3(kRankThreads), 0, st, h->perms_dev, h->dim,
+                       h->k, h->L, x, ldx, batch, codes);
   else  // WTA and DWTA hash dense rows alike (dwta.rs:143-152)
     hipLaunchKernelGGL(wta_hash_kernel<false>, dim3(blocks), dim3(kRankThreads), 0, st,
                        h->windows_dev, h->k, h->L, h->ws, h->bits, x, ldx, nullptr, nullptr, nullptr,
@@ -183,10 +265,15 @@ int rank_hash_sparse_launch(const kh_hash_family* h, const int64_t* xoff, const 
   if (batch == 0) return KH_OK;
   const int64_t n = batch * h->L;
   const unsigned blocks = static_cast<unsigned>((n + kRankThreads - 1) / kRankThreads);
-  if (h->kind == KH_FAMILY_MINHASH)
-    hipLaunchKernelGGL(minhash_kernel<true>, dim3(blocks), dim3(kRankThreads), 0, st, h->perms_dev,
-                       h->dim, h->k, h->L, nullptr, 0, xoff, xidx, batch, codes);
-  else if (h->kind == KH_FAMILY_DWTA)
+  if (h->kind == KH_FAMILY_MINHASH) {
+    for (int64_t b0 = 0; b0 < batch; b0 += kMhMaxRows) {
+      hipLaunchKernelGGL(minhash_rows_kernel<true>, dim3(static_cast<unsigned>(std::min(batch - b0, kMhMaxRows))),
+                         dim3(kMhThreads), 0, st, h->perms_dev, h->dim, h->k, h->L, nullptr, 0, xoff + b0,
+                         xidx, codes + b0 * h->L);
+      KH_LAUNCHED();
+    }
+    return KH_OK;
+  } else if (h->kind == KH_FAMILY_DWTA)
     hipLaunchKernelGGL(dwta_sparse_kernel, dim3(blocks), dim3(kRankThreads), 0, st, h->windows_dev,
                        h->fallback_dev, h->k, h->L, h->ws, h->bits, xoff, xidx, xval, batch, codes);
   else

@@ -63,8 +63,11 @@ def test_wta_sparse_is_to_dense_and_dwta_sparse_rules(kh, orc):
             assert gd[r, t] == orc.dwta_hash_sparse(ow, row.indices, row.values, t) & 0xFFFFFFFF
 
 
-@pytest.mark.parametrize("dim,k,L,seed", [(64, 4, 3, 42), (784, 6, 50, 7), (1000, 24, 5, 2), (10, 4, 2, 3)])
+@pytest.mark.parametrize("dim,k,L,seed", [(64, 4, 3, 42), (784, 6, 50, 7), (1000, 24, 5, 2), (10, 4, 2, 3),
+                                          (20000, 8, 3, 5)])
 def test_minhash_permutations_and_codes(kh, orc, dim, k, L, seed):
+    """Dense rows up to 16384 dims stage their nonzeros in LDS (one block per
+    row); wider rows (20000) take the per-(row, table) kernel."""
     from klearu_amd.lsh import MinHash
     rng = np.random.default_rng(seed)
     fam = MinHash(dim, k, L, seed)
@@ -73,6 +76,7 @@ def test_minhash_permutations_and_codes(kh, orc, dim, k, L, seed):
     X = (rng.uniform(-1, 1, (30, dim)) * (rng.random((30, dim)) < 0.1)).astype(F)
     X[0] = 0.0                      # all bins empty
     X[1, 3] = -0.0
+    X[2] = 1.0                      # every dimension nonzero
     got = codes_dense(fam, X)
     want = np.array([[orc.minhash_hash_dense(op, k, t, x) for t in range(L)] for x in X], np.uint32)
     np.testing.assert_array_equal(got, want)
