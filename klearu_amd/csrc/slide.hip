@@ -16,6 +16,7 @@
 // nonzero partial sum returns it; a zero partial sum only changes the sign of
 // zero), so pre-activations are bit-identical to the reference's dense loop.
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "gather.hpp"
@@ -346,6 +347,135 @@ __global__ __launch_bounds__(kSlideThreads) void neuron_kernel(
   }
 }
 
+// Row-major layers over dense inputs of at most kTileMaxDim features (cfg5's
+// output layer): each wave takes 64 active neurons at a time and loads their
+// weight rows cooperatively, 32 lanes per 512-byte row (two whole rows per load
+// instruction, instead of 64 scattered rows per instruction), into an LDS tile
+// whose odd row stride makes the per-lane column reads conflict-free; lane j
+// then runs neuron j's sequential sum over the input's nonzeros (ascending, as
+// neuron_kernel does).  The next tile's loads are in flight during the sums.
+constexpr int kTileN = 64;
+constexpr int kTileStride = 129;   // floats per LDS row
+constexpr int kTileMaxDim = 128;
+constexpr int kTileWaves = kSlideThreads / 64;
+constexpr size_t kTileLds = sizeof(float) * kTileWaves * kTileN * kTileStride;
+
+__global__ __launch_bounds__(kSlideThreads) void neuron_tile_kernel(
+    const float* __restrict__ W, const float* __restrict__ bias, int dim, const float* __restrict__ x,
+    const uint32_t* __restrict__ aids, int astride, const int32_t* __restrict__ alen, int act,
+    float* __restrict__ pre, float* __restrict__ post) {
+  extern __shared__ float tl[];
+  __shared__ uint32_t nzi[kTileMaxDim];
+  __shared__ float nzv[kTileMaxDim];
+  __shared__ int wsum[kTileWaves];
+  __shared__ int s_total;
+  __shared__ float red[kTileWaves];
+  const int64_t row = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // the input's nonzeros in ascending order (dim <= kSlideThreads)
+  {
+    const float v = (int)threadIdx.x < dim ? x[row * (int64_t)dim + threadIdx.x] : 0.0f;
+    const int nz = v != 0.0f ? 1 : 0;
+    const int pos = block_excl_scan(nz, wsum, &s_total);
+    if (nz) {
+      nzi[pos] = threadIdx.x;
+      nzv[pos] = v;
+    }
+  }
+  __syncthreads();
+  const int nnz = s_total;
+  const int n = alen[row];
+  const uint32_t* ids = aids + row * (int64_t)astride;
+  float* prow = pre + row * (int64_t)astride;
+  float* orow = post + row * (int64_t)astride;
+  float* buf = tl + (size_t)wave * kTileN * kTileStride;
+  const int q4 = dim >> 2;              // float4 per weight row (<= 32)
+  const int c = lane & 31;              // this lane's float4 of a row
+  const int half = lane >> 5;           // which of the two rows of a load
+  const int ntiles = (n + kTileN - 1) / kTileN;
+  float4 v[kTileN / 2];
+  // rows of tile t: neuron t*64 + j for j < 64 (clamped to the last active id)
+  auto issue = [&](int t) {
+    const uint32_t myid = ids[min(t * kTileN + lane, max(n - 1, 0))];
+#pragma unroll
+    for (int r = 0; r < kTileN / 2; ++r) {
+      const uint32_t id = (uint32_t)__shfl((int)myid, 2 * r + half);
+      v[r] = reinterpret_cast<const float4*>(W + (size_t)id * dim)[min(c, q4 - 1)];
+    }
+  };
+  float lmax = -INFINITY;
+  int t = wave;
+  if (t < ntiles) issue(t);
+  for (; t < ntiles; t += kTileWaves) {
+    // the tile to LDS (column 4c..4c+3 of row 2r + half)
+    if (c < q4) {
+#pragma unroll
+      for (int r = 0; r < kTileN / 2; ++r) {
+        float* dst = buf + (2 * r + half) * kTileStride + 4 * c;
+        dst[0] = v[r].x;
+        dst[1] = v[r].y;
+        dst[2] = v[r].z;
+        dst[3] = v[r].w;
+      }
+    }
+    if (t + kTileWaves < ntiles) issue(t + kTileWaves);
+    const int a = t * kTileN + lane;
+    const float* wr = buf + lane * kTileStride;
+    float s = -0.0f;
+    for (int e = 0; e < nnz; ++e) s = __fadd_rn(s, __fmul_rn(wr[nzi[e]], nzv[e]));
+    if (a < n) {
+      const float z = __fadd_rn(s, bias[ids[a]]);
+      prow[a] = z;
+      lmax = fmaxf(lmax, z);
+      if (act != KH_ACT_SOFTMAX) {
+        float r;
+        if (act == KH_ACT_RELU) r = fmaxf(z, 0.0f);
+        else if (act == KH_ACT_SIGMOID) r = sigmoid_ref(z);
+        else if (act == KH_ACT_TANH) r = tanhf(z);
+        else r = z;
+        orow[a] = r;
+      }
+    }
+  }
+  if (act != KH_ACT_SOFTMAX) return;
+  // softmax over the active set (layer.rs:286-308), as neuron_kernel
+  lmax = wave_max(lmax);
+  if (lane == 0) red[wave] = lmax;
+  __syncthreads();
+  float mx = red[0];
+  for (int i = 1; i < kTileWaves; ++i) mx = fmaxf(mx, red[i]);
+  __syncthreads();
+  float ls = 0.0f;
+  for (int a = threadIdx.x; a < n; a += blockDim.x) {
+    const float e = expf_glibc(prow[a] - mx);
+    orow[a] = e;
+    ls += e;
+  }
+  ls = wave_sum(ls);
+  if (lane == 0) red[wave] = ls;
+  __syncthreads();
+  float tot = 0.0f;
+  for (int i = 0; i < kTileWaves; ++i) tot += red[i];
+  if (tot > 0.0f) {
+    for (int a = threadIdx.x; a < n; a += blockDim.x) orow[a] = orow[a] / tot;
+  } else {
+    const float u = 1.0f / (float)n;
+    for (int a = threadIdx.x; a < n; a += blockDim.x) orow[a] = u;
+  }
+}
+
+// neuron_tile_kernel's LDS (above 64 KB) is allowed once per process.
+static int tile_kernel_ready() {
+  static std::once_flag once;
+  static int rc = KH_OK;
+  std::call_once(once, [] {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&neuron_tile_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kTileLds) != hipSuccess)
+      rc = KH_ERR_HIP;
+  });
+  return rc;
+}
+
 // Dense layer over CSR inputs: y[b][o] = act(sum_e val_e * W^T[idx_e][o] + bias[o]).
 constexpr int kChainBatch = 16;  // entries in flight per sequential sum
 __global__ __launch_bounds__(256) void dense_sparse_kernel(const float* __restrict__ WT, int n,
@@ -555,6 +685,9 @@ static int slide_forward_common(const kh_slide_layer* lc, const float* x, const 
     hipLaunchKernelGGL((neuron_kernel<false, true>), ng, dim3(kSlideThreads), lds, st, l->wtn, l->n,
                        l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, alen, act,
                        max_nz, pre, post);
+  else if (l->dim <= kTileMaxDim && l->dim % 4 == 0 && tile_kernel_ready() == KH_OK)
+    hipLaunchKernelGGL(neuron_tile_kernel, dim3((unsigned)batch), dim3(kSlideThreads), kTileLds, st, l->w,
+                       l->bias, l->dim, x, aids, as, alen, act, pre, post);
   else
     hipLaunchKernelGGL((neuron_kernel<false, false>), ng, dim3(kSlideThreads), lds, st, l->w, l->n,
                        l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, alen, act,
