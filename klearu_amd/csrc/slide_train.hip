@@ -31,7 +31,6 @@ constexpr int kTrThreads = 256;
 constexpr int kTrMaxLabels = 1024;   // labels of one example
 constexpr int kTrLdsNz = 8192;       // staged input nonzeros (beyond: read from global)
 constexpr int kTrMaxNnz = 4096;      // stored entries of one sparse example
-constexpr int kJTile = 2048;         // Jacobian: (s, go) pairs per LDS tile
 constexpr int kGTile = 1024;         // grad_input: (id, lg) pairs per LDS tile
 constexpr int kSmCH = 64, kSmM = 128;  // exact softmax sum: 8192 terms per pass
 
@@ -376,112 +375,162 @@ __global__ __launch_bounds__(kTrThreads) void tr_loss_grad_kernel(
   }
 }
 
-// The softmax branch of Layer::backward (layer.rs:141-175): lane i runs the
-// sequential sum over j of go_j*s_j*(1-s_j) (j == i) or go_j*(-s_i*s_j).
-// One term of the Jacobian sum: go_j*s_j*(1-s_j) on the diagonal, else
-// go_j*(-s_i*s_j).
-__device__ __forceinline__ float jac_term(float gj, float sj, float nsi, bool diag) {
-  const float d = (gj * sj) * (1.0f - sj);
-  const float o = gj * (nsi * sj);
-  return diag ? d : o;
+// Sequential sums r + t[0] + t[1] + ... over quads of one chain's terms in LDS
+// (quad q of this lane's chain at base[q * C]), with the LDS reads of the next
+// eight quads issued before the adds of the current ones and pinned there
+// (left to the scheduler, each read sinks to its first use and the chain waits
+// out the LDS latency every four adds).
+__device__ __forceinline__ float add_quads8(const float4* v, float r) {
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    r = r + v[b].x;
+    r = r + v[b].y;
+    r = r + v[b].z;
+    r = r + v[b].w;
+  }
+  return r;
 }
 
-__global__ __launch_bounds__(kTrThreads) void tr_softmax_jacobian_kernel(
+// NQ (a multiple of 8) quads, fully unrolled: every register index is a
+// compile-time constant, so no value is copied.
+template <int NQ, int C>
+__device__ __forceinline__ float chain_add_static(const float4* base, float r) {
+  static_assert(NQ % 8 == 0, "whole groups of quads");
+  float4 v[16];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) v[b] = base[b * C];
+#pragma unroll
+  for (int g = 0; g < NQ / 8; ++g) {
+    if (g + 1 < NQ / 8) {
+#pragma unroll
+      for (int b = 0; b < 8; ++b) v[((g + 1) % 2) * 8 + b] = base[((g + 1) * 8 + b) * C];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    r = add_quads8(&v[(g % 2) * 8], r);
+  }
+  return r;
+}
+
+// nq quads (a multiple of 8) as a loop over groups: the next group is read
+// into a second set of registers while the current one is added, then copied
+// over (measured faster than the copy-free pair loop for the long grad_input
+// chains).
+template <int C>
+__device__ __forceinline__ float chain_add_quads(const float4* base, int nq, float r) {
+  float4 v[8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) v[b] = base[b * C];
+  for (int g = 0; g < nq; g += 8) {
+    const float4* nb = base + min(g + 8, nq - 8) * C;  // the last group re-reads itself
+    float4 nv[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) nv[b] = nb[b * C];
+    __builtin_amdgcn_sched_barrier(0);
+    r = add_quads8(v, r);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) v[b] = nv[b];
+  }
+  return r;
+}
+
+// The softmax branch of Layer::backward (layer.rs:141-175): output i's local
+// gradient is the sequential sum over j (from +0.0) of go_j*s_j*(1-s_j) when
+// j == i, else go_j*(-s_i*s_j).  A block owns 64 outputs, one chain per lane
+// of wave 0 (the consumer).  The terms depend on (i, j) through two rounded
+// products each, so waves 1..3 form them into LDS one chunk of kJStep steps
+// ahead of the consumer, whose only work per step is the dependent add (four
+// steps per LDS read); wave 4 loads the (s, go) pairs two chunks ahead into a
+// ring of three LDS slots, so no other wave waits on global memory.  Blocks
+// loop over groups of 64 outputs.
+constexpr int kJc = 64;                      // chains per block
+constexpr int kJStep = 96;                   // steps per chunk
+constexpr int kJProd = 3;                    // producer waves
+constexpr int kJThreads = 64 * (2 + kJProd); // consumer, producers, loader
+constexpr int kJBlocks = 256;                // grid (groups of 64 outputs are strided over it)
+static_assert((kJStep / 4) % kJProd == 0 && (kJStep / 4) % 8 == 0 && kJStep <= 128, "chunk layout");
+
+__device__ __forceinline__ float jac_off(float gj, float sj, float nsi) { return gj * (nsi * sj); }
+
+__global__ __launch_bounds__(kJThreads) void tr_softmax_jacobian_kernel(
     const float* __restrict__ s, const float* __restrict__ go, const int32_t* __restrict__ alen,
     int cap, float* __restrict__ lg) {
-  __shared__ __align__(16) float ts[kJTile];
-  __shared__ __align__(16) float tg[kJTile];
-  constexpr int kLd = kJTile / kTrThreads;
+  __shared__ float4 jb[2][kJStep / 4][kJc];    // two chunks of terms, [step/4][chain]
+  __shared__ float4 ring[3][2][kJStep / 4];    // (s, go) of three chunks
   const int n = min(alen[0], cap);
-  if (static_cast<int>(blockIdx.x * blockDim.x) >= n) return;
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  const float si = i < n ? s[i] : 0.0f;
-  const float nsi = -si;
-  const float gi = i < n ? go[i] : 0.0f;
-  const float dterm = (gi * si) * (1.0f - si);  // the diagonal term, j == i
-  // the wave's lanes hold i in [w0, w0 + 64): only that window of j needs the
-  // diagonal test; elsewhere every term is go_j * (-s_i * s_j)
-  const int w0 = __builtin_amdgcn_readfirstlane(i - static_cast<int>(threadIdx.x & 63));
-  float r = 0.0f;
-  for (int j0 = 0; j0 < n; j0 += kJTile) {
-    const int cnt = min(kJTile, n - j0);
-    __syncthreads();
-    {
-      float a[kLd], b[kLd];
-      // unconditional loads (clamped index), so that all of them are in flight
-#pragma unroll
-      for (int k = 0; k < kLd; ++k) {
-        const int j = min(k * kTrThreads + static_cast<int>(threadIdx.x), cnt - 1);
-        a[k] = s[j0 + j];
-        b[k] = go[j0 + j];
-      }
-#pragma unroll
-      for (int k = 0; k < kLd; ++k) {
-        const bool in = k * kTrThreads + static_cast<int>(threadIdx.x) < cnt;
-        a[k] = in ? a[k] : 0.0f;
-        b[k] = in ? b[k] : 0.0f;
-      }
-#pragma unroll
-      for (int k = 0; k < kLd; ++k) {
-        ts[k * kTrThreads + threadIdx.x] = a[k];
-        tg[k * kTrThreads + threadIdx.x] = b[k];
-      }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nch = (n + kJStep - 1) / kJStep;
+  const int p = wave - 1;                      // producer index (waves 1..kJProd)
+  const bool prod = wave >= 1 && wave <= kJProd, loader = wave == kJProd + 1;
+  // loader: chunk c's (s, go) into ring slot c % 3 (past n: the last pair,
+  // formed but never added)
+  auto load = [&](int c) {
+    float* rs = reinterpret_cast<float*>(&ring[c % 3][0][0]);
+    float* rg = reinterpret_cast<float*>(&ring[c % 3][1][0]);
+    for (int k = lane; k < kJStep; k += 64) {
+      const int j = min(c * kJStep + k, n - 1);
+      rs[k] = s[j];
+      rg[k] = go[j];
     }
-    __syncthreads();
-    const float4* s4 = reinterpret_cast<const float4*>(ts);
-    const float4* g4 = reinterpret_cast<const float4*>(tg);
-    // [0, d0) and [d1, cnt): off-diagonal only; [d0, d1): the diagonal window
-    const int d0 = min(max(w0 - j0, 0), cnt) & ~3;
-    const int d1 = min(max(w0 + 64 - j0, 0), cnt);
-    // off-diagonal terms of [ja, ja + ((jb - ja) & ~15)), ja a multiple of 4;
-    // the next 16 (s, go) pairs are read while the current 16 are added
-    auto run16 = [&](int ja, int jb) {
-      const int je = ja + ((jb - ja) & ~15);
-      if (je == ja) return ja;
-      float4 sv[4], gv[4];
+  };
+  for (int i0 = blockIdx.x * kJc; i0 < n; i0 += gridDim.x * kJc) {
+    const int i = min(i0 + lane, n - 1);
+    const float si = s[i], gi = go[i];
+    const float nsi = -si;
+    const float dterm = (gi * si) * (1.0f - si);  // the diagonal term, j == i
+    // producer p forms quads p, p + kJProd, ... of chunk c
+    auto produce = [&](int c) {
+      const int jc = c * kJStep;
+      const bool diag = jc < i0 + kJc && i0 < jc + kJStep;  // the chunk meets this block's diagonal
+      constexpr int kQ = kJStep / 4 / kJProd;
+      float4 sv[kQ], gv[kQ];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        sv[q] = s4[(ja >> 2) + q];
-        gv[q] = g4[(ja >> 2) + q];
+      for (int u = 0; u < kQ; ++u) {
+        sv[u] = ring[c % 3][0][p + kJProd * u];
+        gv[u] = ring[c % 3][1][p + kJProd * u];
       }
-      for (int j = ja; j < je; j += 16) {
-        float4 sn[4], gn[4];
-        const int jn = min(j + 16, kJTile - 16) >> 2;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          sn[q] = s4[jn + q];
-          gn[q] = g4[jn + q];
+      for (int u = 0; u < kQ; ++u) {
+        const int q = p + kJProd * u;
+        float t0 = jac_off(gv[u].x, sv[u].x, nsi), t1 = jac_off(gv[u].y, sv[u].y, nsi);
+        float t2 = jac_off(gv[u].z, sv[u].z, nsi), t3 = jac_off(gv[u].w, sv[u].w, nsi);
+        if (diag) {
+          const int d = i0 + lane - (jc + 4 * q);
+          t0 = d == 0 ? dterm : t0;
+          t1 = d == 1 ? dterm : t1;
+          t2 = d == 2 ? dterm : t2;
+          t3 = d == 3 ? dterm : t3;
         }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float t0 = gv[q].x * (nsi * sv[q].x);
-          const float t1 = gv[q].y * (nsi * sv[q].y);
-          const float t2 = gv[q].z * (nsi * sv[q].z);
-          const float t3 = gv[q].w * (nsi * sv[q].w);
-          r = r + t0;
-          r = r + t1;
-          r = r + t2;
-          r = r + t3;
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          sv[q] = sn[q];
-          gv[q] = gn[q];
-        }
+        jb[c & 1][q][lane] = make_float4(t0, t1, t2, t3);
       }
-      return je;
     };
-    const int diag = i - j0;
-    int j = run16(0, d0);
-    for (; j < d1; ++j) {
-      const float o = tg[j] * (nsi * ts[j]);
-      r = r + (j == diag ? dterm : o);
+    float r = 0.0f;
+    lds_barrier();  // the previous group's last chunk is consumed
+    if (loader) {
+      load(0);
+      if (nch > 1) load(1);
     }
-    for (; j < cnt && (j & 3); ++j) r = r + tg[j] * (nsi * ts[j]);
-    j = run16(j, cnt);
-    for (; j < cnt; ++j) r = r + tg[j] * (nsi * ts[j]);
+    lds_barrier();
+    if (prod) produce(0);
+    lds_barrier();
+    for (int c = 0; c < nch; ++c) {
+      if (prod) {
+        if (c + 1 < nch) produce(c + 1);
+      } else if (loader) {
+        if (c + 2 < nch) load(c + 2);
+      } else if (wave == 0) {
+        const int cnt = min(kJStep, n - c * kJStep);
+        const float4(*src)[kJc] = jb[c & 1];
+        if (cnt == kJStep) {
+          r = chain_add_static<kJStep / 4, kJc>(&src[0][lane], r);
+        } else {
+          const float* sf = reinterpret_cast<const float*>(&src[0][0]);
+          for (int j = 0; j < cnt; ++j) r = r + sf[((j >> 2) * kJc + lane) * 4 + (j & 3)];
+        }
+      }
+      lds_barrier();
+    }
+    if (wave == 0 && i0 + lane < n) lg[i0 + lane] = r;
   }
-  if (i < n) lg[i] = r;
 }
 
 // Local gradients of a layer from the gradient w.r.t. its output: go = the
@@ -506,70 +555,92 @@ __global__ __launch_bounds__(kTrThreads) void tr_local_grad_kernel(
 
 // grad_input[j] = sum over the active list (in order, from +0.0) of
 // lg[a] * w[id_a][j], with the weights before this example's update
-// (layer.rs:203-207).  Each j is one chain of |A| dependent adds, so each
-// block owns one column: all its threads gather the column's products
-// lg[a] * w[id_a][j] into LDS (kGTile at a time, every load of a tile in
-// flight at once), then one lane adds them in order, reading four per LDS
-// load.  The chains of all columns run on separate CUs.
-constexpr int kGTileRows = 16384;  // products staged per pass (64 KB)
-__global__ __launch_bounds__(kTrThreads) void tr_grad_input_kernel(
+// (layer.rs:203-207).  Each j is one chain of |A| dependent adds.  A block owns
+// kGc columns, one chain per lane of wave 0 (the consumer); waves 1..7 gather
+// the products for the next kGStep active rows into LDS (16 lanes read one
+// 64-byte piece of a weight row) while the consumer adds the current ones,
+// four per LDS read.
+constexpr int kGc = 8;          // columns (chains) per block
+constexpr int kGStep = 1024;    // active rows per chunk
+constexpr int kGThreads = 512;
+
+__global__ __launch_bounds__(kGThreads) void tr_grad_input_kernel(
     const float* __restrict__ W, int dim, const uint32_t* __restrict__ aids,
     const int32_t* __restrict__ alen, int cap, const float* __restrict__ lg,
     float* __restrict__ gi) {
-  __shared__ __align__(16) float prod[kGTileRows];
+  __shared__ float4 gb[2][kGStep / 4][kGc];   // two chunks of products, [row/4][column]
+  constexpr int kProdThreads = kGThreads - 64;
+  constexpr int kSlots = kProdThreads / kGc;  // rows gathered per producer pass
+  constexpr int kPer = (kGStep + kSlots - 1) / kSlots;
   const int n = min(alen[0], cap);
-  const int j = blockIdx.x;
-  float r = 0.0f;
-  for (int a0 = 0; a0 < n; a0 += kGTileRows) {
-    const int cnt = min(kGTileRows, n - a0);
-    __syncthreads();
-    constexpr int kU = 8;
-    for (int b0 = 0; b0 < cnt; b0 += kTrThreads * kU) {
-      uint32_t id[kU];
-      float l[kU], w[kU];
-      // unconditional loads (clamped index), so that all of them are in flight
+  const int j0 = blockIdx.x * kGc;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nch = (n + kGStep - 1) / kGStep;
+  const int pt = static_cast<int>(threadIdx.x) - 64;   // producer thread
+  const int col = pt & (kGc - 1), slot = pt / kGc;
+  const int jc = min(j0 + col, dim - 1);
+  // A producer holds the weights and local gradients of the next chunk and
+  // the row ids of the one after (unconditional loads of clamped rows, all in
+  // flight at once), so each load has a chunk's worth of adds to arrive in.
+  uint32_t id[kPer];
+  float l[kPer], w[kPer], ln[kPer];
+  auto fetch_ids = [&](int c) {
+    const int r0 = c * kGStep;
+    const int cnt = min(kGStep, n - r0);
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const int a = min(b0 + u * kTrThreads + static_cast<int>(threadIdx.x), cnt - 1);
-        id[u] = aids[a0 + a];
-        l[u] = lg[a0 + a];
-      }
-#pragma unroll
-      for (int u = 0; u < kU; ++u) w[u] = W[static_cast<size_t>(id[u]) * dim + j];
-#pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const int a = b0 + u * kTrThreads + threadIdx.x;
-        if (a < cnt) prod[a] = l[u] * w[u];
-      }
+    for (int u = 0; u < kPer; ++u) {
+      const int a = r0 + min(slot + u * kSlots, cnt - 1);
+      id[u] = aids[a];
+      ln[u] = lg[a];
     }
-    for (int a = cnt + threadIdx.x; a < ((cnt + 3) & ~3); a += kTrThreads) prod[a] = 0.0f;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      // eight LDS loads (32 products) ahead of the adds
-      const float4* p4 = reinterpret_cast<const float4*>(prod);
-      const int c32 = cnt >> 5;
-      float4 v[8];
+  };
+  auto fetch_w = [&]() {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = p4[q];
-      for (int b = 0; b < c32; ++b) {
-        float4 nv[8];
-        const int nb = min(b + 1, kGTileRows / 32 - 1) * 8;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) nv[q] = p4[nb + q];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          r = r + v[q].x;
-          r = r + v[q].y;
-          r = r + v[q].z;
-          r = r + v[q].w;
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] = nv[q];
-      }
-      for (int a = c32 * 32; a < cnt; ++a) r = r + prod[a];
+    for (int u = 0; u < kPer; ++u) {
+      w[u] = W[static_cast<size_t>(id[u]) * dim + jc];
+      l[u] = ln[u];
     }
+  };
+  auto produce = [&](int c) {
+    float wc[kPer], lc[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      wc[u] = w[u];
+      lc[u] = l[u];
+    }
+    if (c + 1 < nch) fetch_w();           // chunk c + 1 (its ids arrived a chunk ago)
+    if (c + 2 < nch) fetch_ids(c + 2);
+    float* dst = reinterpret_cast<float*>(&gb[c & 1][0][0]);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int rr = slot + u * kSlots;
+      if (rr < kGStep) dst[((rr >> 2) * kGc + col) * 4 + (rr & 3)] = lc[u] * wc[u];
+    }
+  };
+  if (wave > 0 && nch > 0) {
+    fetch_ids(0);
+    fetch_w();
+    if (nch > 1) fetch_ids(1);
+    produce(0);
   }
-  if (threadIdx.x == 0) gi[j] = r;
+  lds_barrier();
+  float r = 0.0f;
+  for (int c = 0; c < nch; ++c) {
+    if (wave > 0) {
+      if (c + 1 < nch) produce(c + 1);
+    } else if (lane < kGc) {
+      const int cnt = min(kGStep, n - c * kGStep);
+      const float4(*src)[kGc] = gb[c & 1];
+      if (cnt == kGStep) {
+        r = chain_add_quads<kGc>(&src[0][lane], kGStep / 4, r);
+      } else {
+        const float* sf = reinterpret_cast<const float*>(&src[0][0]);
+        for (int j = 0; j < cnt; ++j) r = r + sf[((j >> 2) * kGc + lane) * 4 + (j & 3)];
+      }
+    }
+    lds_barrier();
+  }
+  if (wave == 0 && lane < kGc && j0 + lane < dim) gi[j0 + lane] = r;
 }
 
 // Optimizer::update of every active neuron (layer.rs:209-222): grad_weights[j]
@@ -622,13 +693,13 @@ static int layer_backward_launch(kh_slide_layer* l, const float* x, const uint32
     KH_LAUNCHED();
   }
   if (l->act == KH_ACT_SOFTMAX) {
-    hipLaunchKernelGGL(tr_softmax_jacobian_kernel, dim3(ab), dim3(kTrThreads), 0, st, post, go,
-                       alen, cap, lg);
+    hipLaunchKernelGGL(tr_softmax_jacobian_kernel, dim3((unsigned)std::min(ceil_div(cap, kJc), kJBlocks)),
+                       dim3(kJThreads), 0, st, post, go, alen, cap, lg);
     KH_LAUNCHED();
   }
   if (gi) {
-    hipLaunchKernelGGL(tr_grad_input_kernel, dim3(l->dim), dim3(kTrThreads), 0, st, l->w, l->dim,
-                       aids, alen, cap, lg, gi);
+    hipLaunchKernelGGL(tr_grad_input_kernel, dim3((unsigned)ceil_div(l->dim, kGc)), dim3(kGThreads), 0, st,
+                       l->w, l->dim, aids, alen, cap, lg, gi);
     KH_LAUNCHED();
   }
   const int xs = ceil_div(l->dim, kUCols);
