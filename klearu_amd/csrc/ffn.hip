@@ -363,16 +363,54 @@ __global__ __launch_bounds__(64 * kRnWaves) void rmsnorm_kernel(const float* __r
                                                                const float* __restrict__ w, int n,
                                                                float eps, float* __restrict__ y) {
   __shared__ EsLds<kRnChunks, M> es;
+  constexpr int Q = kRnChunks * M / 4 / (64 * kRnWaves);  // float4 of the row per thread
   const float* xr = x + (size_t)blockIdx.x * n;
   float* yr = y + (size_t)blockIdx.x * n;
-  for (int i = threadIdx.x; i < kRnChunks * M; i += blockDim.x) {
+  const int t = threadIdx.x;
+  if ((n & 3) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                        reinterpret_cast<uintptr_t>(y)) & 15) == 0) {
+    // Every load of the row and of the weights is requested before the first
+    // use (clamped, unconditional: see stage_f4), so the row costs one round
+    // trip; four consecutive terms never straddle a chunk (M % 4 == 0).
+    const int n4 = n >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(xr);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 xv[Q], wv[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) xv[q] = x4[min(t + q * 64 * kRnWaves, n4 - 1)];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) wv[q] = w4[min(t + q * 64 * kRnWaves, n4 - 1)];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int i4 = t + q * 64 * kRnWaves;
+      *reinterpret_cast<float4*>(&es.TP[es_slot<kRnChunks, M>(4 * i4)]) =
+          i4 < n4 ? make_float4(__fmul_rn(xv[q].x, xv[q].x), __fmul_rn(xv[q].y, xv[q].y),
+                                __fmul_rn(xv[q].z, xv[q].z), __fmul_rn(xv[q].w, xv[q].w))
+                  : make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
+    }
+    lds_barrier();
+    const float ss = exact_seq_sum<kRnWaves, kRnChunks, M>(n, 0.0f, es);
+    const float inv = rms_inv_exact(ss, n, eps);
+    float4* y4 = reinterpret_cast<float4*>(yr);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int i4 = t + q * 64 * kRnWaves;
+      if (i4 < n4)
+        y4[i4] = make_float4(__fmul_rn(__fmul_rn(xv[q].x, inv), wv[q].x),
+                             __fmul_rn(__fmul_rn(xv[q].y, inv), wv[q].y),
+                             __fmul_rn(__fmul_rn(xv[q].z, inv), wv[q].z),
+                             __fmul_rn(__fmul_rn(xv[q].w, inv), wv[q].w));
+    }
+    return;
+  }
+  for (int i = t; i < kRnChunks * M; i += blockDim.x) {
     const float v = i < n ? xr[i] : 0.0f;
     es.TP[es_slot<kRnChunks, M>(i)] = i < n ? __fmul_rn(v, v) : -0.0f;
   }
   lds_barrier();
   const float ss = exact_seq_sum<kRnWaves, kRnChunks, M>(n, 0.0f, es);
   const float inv = rms_inv_exact(ss, n, eps);
-  for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = __fmul_rn(__fmul_rn(xr[i], inv), w[i]);
+  for (int i = t; i < n; i += blockDim.x) yr[i] = __fmul_rn(__fmul_rn(xr[i], inv), w[i]);
 }
 
 // Rows longer than kRnMaxN: one lane runs the sequential sum.
