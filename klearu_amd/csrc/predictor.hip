@@ -374,6 +374,210 @@ __global__ __launch_bounds__(kL1LdsThreads) void pred_l1_lds_kernel(
   if (lane < kL1Chains && chain < hid) h[(size_t)b * hid + chain] = fmaxf(__fadd_rn(s, bv), 0.0f);
 }
 
+// Layer 1 for a batch of rows (BF16 weights, n_in a multiple of
+// kLbSlots * kLbStage, at most kL1LdsIn): a block owns kLbOut hidden units for
+// kLbRows rows, i.e. 32 chains, one per consumer lane (lanes 32-63 idle).  pred_l1_lds holds every product of its block in LDS, so one block
+// fits per CU and a batch's blocks run in several rounds; here the products
+// pass through a ring of kLbSlots stages, so all blocks of a 16-row batch run
+// at once.
+//  * The rows' x go to LDS once (the block's only barrier) and the producers
+//    hold every weight of the block in registers from the start.
+//  * Producer p forms stages p, p + kLbProd, ... into slot stage % kLbSlots
+//    once the consumer has released that slot, then publishes the stage index
+//    in ready[slot]; the consumer releases a slot by writing the stage index
+//    to freed[slot].  LDS flags, not barriers: no wave waits for another
+//    except on the data it needs.  One consumer and three producers, one wave
+//    per SIMD, so no producer takes issue slots from the chain.
+//  * Quad q of chain c sits at position c ^ (q & 14) of its ring row: the
+//    consumer's 32 lanes still read one contiguous row, and a producer's
+//    write instruction (8 quads x 8 chains) spreads evenly over the banks
+//    instead of hitting one bank group 8 times.  Eight slots of 64 steps give
+//    a producer six stages of slack to refill a slot: it takes about three
+//    times as long to form a stage as the consumer takes to add one.
+//  * The consumer adds each chain's products in step order through a window
+//    of two stages of quads: while stage s is added, its registers are
+//    refilled with stage s + 2, whose flag was checked first (flags are
+//    checked and slots released two stages at a time).  The loop is unrolled by the ring
+//    size, so every LDS address is a fixed register plus an immediate offset.
+// Each chain is the same sequential sum as pred_l1_lds_kernel's.
+constexpr int kLbOut = 8, kLbRows = 4, kLbChains = kLbOut * kLbRows;
+constexpr int kLbStage = 64, kLbSlots = 8, kLbProd = 3;
+constexpr int kLbThreads = 64 * (1 + kLbProd);
+constexpr int kLbStages = kL1LdsIn / kLbStage;
+constexpr int kLbSpp = (kLbStages + kLbProd - 1) / kLbProd;  // stages per producer (at most)
+constexpr int kLbQuads = kLbStage / 4;
+constexpr int kLbRingBytes = kLbSlots * kLbQuads * kLbChains * 16;
+constexpr int kLbLdsBytes = kLbRingBytes + kLbRows * kL1LdsIn * 4;
+constexpr int kLbSpinMax = 1 << 22;  // a flag that never arrives ends the wait (no hang)
+static_assert(kLbRingBytes <= 65536, "ring addressed by immediate offsets");
+
+__device__ __forceinline__ int lb_flag(const int* f) {
+  return __hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lb_publish(int* f, int v) {
+  __hip_atomic_store(f, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ constexpr int lb_swz(int q) { return q & 14; }
+// The consumer's side of the flags: relaxed (no wait), ordered by the LDS
+// itself (a wave's LDS operations execute in issue order) and by compiler
+// barriers, so a flag read can be issued a stage ahead of its use.
+__device__ __forceinline__ int lb_peek(const int* f) {
+  return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lb_release(int* f, int v) {
+  __hip_atomic_store(f, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__global__ __launch_bounds__(kLbThreads) void pred_l1_batch_kernel(
+    const uint16_t* __restrict__ Wb, const float* __restrict__ bias, const float* __restrict__ x,
+    int n_in, int hid, int batch, float* __restrict__ h) {
+  extern __shared__ float4 lb4[];
+  float4* ring = lb4;                                             // [slot][quad][chain]
+  float* xs = reinterpret_cast<float*>(lb4 + kLbRingBytes / 16);  // [kLbRows][n_in]
+  __shared__ int ready[kLbSlots], freed[kLbSlots];
+  const int c0 = blockIdx.x * kLbOut, r0 = blockIdx.y * kLbRows;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nst = n_in / kLbStage;
+  const int n4 = n_in >> 2;
+  // Every x load is requested before the weights and before any store
+  // (clamped, unconditional: see stage_f4); rows past the batch re-read the
+  // last row, their chains unused.
+  constexpr int kXq = (kLbRows * kL1LdsIn / 4 + kLbThreads - 1) / kLbThreads;
+  float4 xv[kXq];
+#pragma unroll
+  for (int q = 0; q < kXq; ++q) {
+    const int i = min((int)threadIdx.x + q * kLbThreads, kLbRows * n4 - 1);
+    const int r = i / n4;
+    xv[q] = reinterpret_cast<const float4*>(x + (size_t)min(r0 + r, batch - 1) * n_in)[i - r * n4];
+  }
+  if (threadIdx.x < kLbSlots) {
+    ready[threadIdx.x] = -1;
+    freed[threadIdx.x] = -1;
+  }
+  // producer p = wave - 1: lane -> (8-step block jl of a stage, output o)
+  const int p = wave - 1, jl = lane >> 3, po = lane & 7;
+  uint4 wr[kLbSpp];
+  if (wave > 0) {
+    const uint4* __restrict__ wv = reinterpret_cast<const uint4*>(Wb);
+#pragma unroll
+    for (int i = 0; i < kLbSpp; ++i) {
+      const int st = min(p + kLbProd * i, nst - 1);  // clamped, unused past nst
+      wr[i] = wv[(size_t)(st * (kLbStage / 8) + jl) * hid + min(c0 + po, hid - 1)];
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kXq; ++q)
+    reinterpret_cast<float4*>(xs)[min((int)threadIdx.x + q * kLbThreads, kLbRows * n4 - 1)] = xv[q];
+  lds_barrier();
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < kLbSpp; ++i) {
+      const int st = p + kLbProd * i;
+      if (st >= nst) break;
+      const int slot = st % kLbSlots;
+      // the consumer must have released this slot's previous stage
+      for (int n = 0; st >= kLbSlots && lb_flag(&freed[slot]) < st - kLbSlots && n < kLbSpinMax; ++n)
+        __builtin_amdgcn_s_sleep(1);
+      const int j0 = st * kLbStage + jl * 8;
+      float4* row0 = ring + (slot * kLbQuads + 2 * jl) * kLbChains;  // quads 2 jl, 2 jl + 1
+      const int sw = lb_swz(2 * jl);  // the same for both quads
+      float w[8];
+      Blk8<uint16_t>::widen(wr[i], w);
+#pragma unroll
+      for (int r = 0; r < kLbRows; ++r) {
+        const float4 xa = reinterpret_cast<const float4*>(xs + r * n_in + j0)[0];
+        const float4 xb = reinterpret_cast<const float4*>(xs + r * n_in + j0)[1];
+        const int c = (r * kLbOut + po) ^ sw;
+        row0[c] = make_float4(__fmul_rn(w[0], xa.x), __fmul_rn(w[1], xa.y), __fmul_rn(w[2], xa.z),
+                              __fmul_rn(w[3], xa.w));
+        row0[kLbChains + c] = make_float4(__fmul_rn(w[4], xb.x), __fmul_rn(w[5], xb.y),
+                                          __fmul_rn(w[6], xb.z), __fmul_rn(w[7], xb.w));
+      }
+      lb_publish(&ready[slot], st);  // every lane stores the same value: no branch
+    }
+    return;
+  }
+  // consumer: lane ch reads quad q of slot sl at ring[(sl * kLbQuads + q) * 32 + (ch ^ swz(q))].
+  // Lanes past the 32 chains leave, so each window read moves 512 bytes of
+  // LDS, not 1 KB (the LDS, shared with the producers, sets the pace).
+  if (lane >= kLbChains) return;
+  const int ch = lane;
+  const float4* cb[16];
+#pragma unroll
+  for (int g = 0; g < 16; g += 2) cb[g] = ring + (ch ^ g);
+  float s = -0.0f;
+  // window of two stages: rq[16 h + q] holds quad q of the stage in slot
+  // parity h; a stage's quads are refilled with those two stages ahead, so a
+  // read has 64 adds (about 400 cycles) to arrive
+  float4 rq[2 * kLbQuads];
+  for (int n = 0; n < kLbSpinMax; ++n) {
+    const int f0 = lb_flag(&ready[0]), f1 = lb_flag(&ready[1]);
+    if (f0 >= 0 && (nst < 2 || f1 >= 1)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+#pragma unroll
+  for (int q = 0; q < 2 * kLbQuads; ++q) rq[q] = cb[lb_swz(q % kLbQuads)][q * kLbChains];
+  // One stage: add slot SL's quads, refilling them from slot SL + 2.
+  auto body = [&](auto slot_c) {
+    constexpr int SL = decltype(slot_c)::value;
+    constexpr int H = SL % 2, NS = (SL + 2) % kLbSlots;
+    constexpr int kRefill = 8;
+#pragma unroll
+    for (int q = 0; q < kLbQuads; q += kRefill) {
+#pragma unroll
+      for (int u = 0; u < kRefill; ++u) {
+        const float4 v = rq[H * kLbQuads + q + u];
+        s = __fadd_rn(s, v.x);
+        s = __fadd_rn(s, v.y);
+        s = __fadd_rn(s, v.z);
+        s = __fadd_rn(s, v.w);
+      }
+#pragma unroll
+      for (int u = 0; u < kRefill; ++u)
+        rq[H * kLbQuads + q + u] = cb[lb_swz(q + u)][(NS * kLbQuads + q + u) * kLbChains];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // pin the chain here: otherwise the adds may be sunk past the next flag
+    // loop, and the window's registers double
+    asm volatile("" : "+v"(s));
+  };
+  // Stages st and st + 1 (slots SL, SL + 1).  Their refills read stages
+  // st + 2 and st + 3, whose flags were read during the previous pair (f2,
+  // f3), so the check costs no wait unless a producer is behind; the flags
+  // the next pair needs are read between this pair's two stages.  The two
+  // slots of the previous pair, whose quads have been added, are released
+  // together.  Past the last stage the refills read stale slots, never added.
+  int f2 = lb_peek(&ready[2]), f3 = lb_peek(&ready[3]);
+  auto pair = [&](auto slot_c, int st) {
+    constexpr int SL = decltype(slot_c)::value;
+    constexpr int S2 = (SL + 2) % kLbSlots, S3 = (SL + 3) % kLbSlots;
+    constexpr int S4 = (SL + 4) % kLbSlots, S5 = (SL + 5) % kLbSlots;
+    for (int n = 0; n < kLbSpinMax; ++n) {
+      if ((st + 2 >= nst || f2 >= st + 2) && (st + 3 >= nst || f3 >= st + 3)) break;
+      __builtin_amdgcn_s_sleep(1);
+      f2 = lb_flag(&ready[S2]);
+      f3 = lb_flag(&ready[S3]);
+    }
+    asm volatile("" ::: "memory");  // no refill read moves above the check
+    // for st == 0 these rewrite the initial -1s
+    lb_release(&freed[(SL + kLbSlots - 2) % kLbSlots], st - 2);
+    lb_release(&freed[(SL + kLbSlots - 1) % kLbSlots], st - 1);
+    body(slot_c);
+    f2 = lb_peek(&ready[S4]);
+    f3 = lb_peek(&ready[S5]);
+    body(std::integral_constant<int, (SL + 1) % kLbSlots>{});
+  };
+  for (int st = 0; st < nst; st += kLbSlots) {
+    pair(std::integral_constant<int, 0>{}, st);
+    pair(std::integral_constant<int, 2>{}, st + 2);
+    pair(std::integral_constant<int, 4>{}, st + 4);
+    pair(std::integral_constant<int, 6>{}, st + 6);
+  }
+  const int r = ch / kLbOut, o = ch % kLbOut;
+  if (r0 + r < batch && c0 + o < hid)
+    h[(size_t)(r0 + r) * hid + c0 + o] = fmaxf(__fadd_rn(s, bias[c0 + o]), 0.0f);
+}
+
 // Layer 2 (short chains): one lane per output, the whole weight row in
 // registers (n_hid <= 256), the hidden vector in LDS.  Scores = sigmoid.
 // One wave per block, so the weight stream is spread over as many CUs as
@@ -1104,6 +1308,22 @@ struct TopkReq {
   bool done = false;
 };
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static std::mutex mu;
+  static std::vector<int> cus;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  if ((int)cus.size() <= dev) cus.resize(dev + 1, 0);
+  if (cus[dev] == 0) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
+                   ? n : 256;
+  }
+  return cus[dev];
+}
+
 static int set_kernel_attrs() {
   static std::once_flag once;
   static int rc = KH_OK;
@@ -1117,6 +1337,7 @@ static int set_kernel_attrs() {
     };
     lds(reinterpret_cast<const void*>(&pred_l1_lds_kernel<uint16_t>), kL1LdsBytes);
     lds(reinterpret_cast<const void*>(&pred_l1_lds_kernel<float>), kL1LdsBytes);
+    lds(reinterpret_cast<const void*>(&pred_l1_batch_kernel), kLbLdsBytes);
     lds(reinterpret_cast<const void*>(&topk_kernel<6>), 136 * 1024);
     lds(reinterpret_cast<const void*>(&topk_kernel<8>), 136 * 1024);
     lds(reinterpret_cast<const void*>(&topk_kernel<11>), 136 * 1024);
@@ -1145,7 +1366,15 @@ static int predict_typed(const kh_predictor* p, const float* x, int64_t batch, f
   }
   int rc = set_kernel_attrs();
   if (rc != KH_OK) return rc;
-  if (p->in_dim <= kL1LdsIn)
+  // pred_l1_lds fits one block per CU; the batched kernel pays off once its
+  // blocks would need more than one round of the device's CUs.
+  if (std::is_same<W, uint16_t>::value && batch > 1 && !nrm.w && p->in_dim <= kL1LdsIn &&
+      p->in_dim % (kLbSlots * kLbStage) == 0 &&
+      (int64_t)ceil_div(p->hid, kL1Chains) * batch > device_cus())
+    hipLaunchKernelGGL(pred_l1_batch_kernel, dim3(ceil_div(p->hid, kLbOut), ceil_div(batch, kLbRows)),
+                       dim3(kLbThreads), kLbLdsBytes, st, static_cast<const uint16_t*>(p->w1b), p->b1,
+                       x, p->in_dim, p->hid, static_cast<int>(batch), hbuf);
+  else if (p->in_dim <= kL1LdsIn)
     hipLaunchKernelGGL(pred_l1_lds_kernel<W>, dim3(ceil_div(p->hid, kL1Chains), batch),
                        dim3(kL1LdsThreads), kL1LdsBytes, st, w1, p->b1, x, p->in_dim, p->hid, hbuf,
                        nrm.w, nrm.inv, nrm.eps);

@@ -32,6 +32,14 @@ def make_predictor(orc, rng, ind, hid, out, bias=False):
     (4096, 256, 11008, 16, False),  # cfg3 batch 16
     (4096, 128, 32, 8, False),     # cfg4 head predictor
     (100, 13, 77, 3, True),        # ragged shapes, biases
+    # the batched layer-1 kernel (BF16, inputs a multiple of 512, more blocks
+    # of 8 hidden units x rows than the device's 256 CUs): one round of the
+    # ring, two rounds, four; rows and hidden units not multiples of the
+    # block's 4 x 8.  Inputs of 128 take the single-row kernel per row.
+    (512, 20, 77, 87, True),
+    (1024, 13, 40, 130, True),
+    (2048, 64, 300, 33, True),
+    (128, 20, 77, 5, True),
 ])
 def test_predictor_scores_bit_exact(kh, orc, ind, hid, out, batch, bias):
     from klearu_amd.dejavu import SparsityPredictor
