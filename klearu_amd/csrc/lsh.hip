@@ -38,6 +38,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "lsh_internal.hpp"
@@ -95,6 +96,175 @@ __global__ __launch_bounds__(kHashDenseMax) void hash_dense_kernel(
   }
   __syncthreads();
   for (int t = threadIdx.x; t < L; t += blockDim.x) codes[row * L + t] = cw[t];
+}
+
+// Per-row hashing with the plane signs in LDS (dim <= kHlMaxDim).  Block
+// (row, g) hashes tables g*tpb .. g*tpb+tpb-1, i.e. planes q = 0..tpb*k-1 of
+// the group, one per thread.  The group's 2-bit signs (kh_hash_family::sg_dev)
+// are staged in LDS while the row's nonzero values are compacted in dimension
+// order; lane q then adds plane q's term of every compacted value in that
+// order, its sign read from LDS.  Two kinds of term are left out against the
+// reference's sum over the plane's nonzero coefficients: none (a zero
+// coefficient adds +0 here, see below) and those whose x value is zero.
+// Adding a zero changes at most the sign of a zero partial sum; every later
+// partial sum that is not zero, and the final s >= 0 test (true for either
+// zero), come out as before, so the code bits are the reference's.
+constexpr int kHlThreads = 256;
+constexpr int kHlWaves = kHlThreads / 64;
+constexpr int kHlMaxDim = 2048;
+constexpr int kHlLoads = 16;   // uint4 sign loads in flight per thread
+constexpr int kHlUnroll = 8;   // compacted values per step (the list is padded to a multiple)
+constexpr int kHlXIter = kHlMaxDim / kHlThreads;
+
+__host__ __device__ constexpr int hl_pad(int n) { return (n + kHlUnroll - 1) / kHlUnroll * kHlUnroll; }
+
+// At most two blocks fit a CU's LDS at cfg-size groups, so the compiler may
+// spend registers on keeping every staging load in flight.
+__global__ __launch_bounds__(kHlThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void hash_dense_lds_kernel(
+    const uint4* __restrict__ sg, int n4, int nw, int k, int L, int tpb, int dim,
+    const float* __restrict__ x, int64_t ldx, uint32_t* __restrict__ codes) {
+  extern __shared__ uint4 hl_lds[];
+  uint32_t* tab = reinterpret_cast<uint32_t*>(hl_lds);  // [dim][nw] sign words
+  uint2* ent = reinterpret_cast<uint2*>(hl_lds + n4);   // (word offset d*nw, x bits), dimension order
+  uint32_t* cw = reinterpret_cast<uint32_t*>(ent + hl_pad(dim));
+  __shared__ int wcount[kHlWaves];
+  const int64_t row = blockIdx.x;
+  const int g = blockIdx.y;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const float* __restrict__ xr = x + row * ldx;
+  // Wave w compacts dims [w*span, (w+1)*span): its values come after wave w-1's.
+  const int span = (dim + kHlThreads - 1) / kHlThreads * 64;
+  // Sign loads first, in flight together with the row's loads.
+  const uint4* __restrict__ src = sg + (size_t)g * n4;
+  uint4 r[kHlLoads];
+#pragma unroll
+  for (int j = 0; j < kHlLoads; ++j) r[j] = src[min(j * kHlThreads + t, n4 - 1)];
+  // The row's loads are unconditional (clamped) and masked afterwards through
+  // an opaque mask, so that the compiler keeps every load in one block, in
+  // flight together, instead of branching around them.
+  float xv[kHlXIter];
+#pragma unroll
+  for (int i = 0; i < kHlXIter; ++i) {
+    const int d = w * span + i * 64 + lane;
+    uint32_t keep = i * 64 < span && d < dim ? ~0u : 0u;
+    asm volatile("" : "+v"(keep));
+    xv[i] = __uint_as_float(__float_as_uint(xr[min(d, dim - 1)]) & keep);
+  }
+  // Clamped indices on both sides (the last uint4 is written with its own
+  // value by several threads) keep the loads out of branches, all in flight.
+  // Two passes cover the largest group (kHlMaxDim * 16 words).
+  static_assert(2 * kHlLoads * kHlThreads * 4 >= kHlMaxDim * 16, "sign staging passes");
+#pragma unroll
+  for (int j = 0; j < kHlLoads; ++j) hl_lds[min(j * kHlThreads + t, n4 - 1)] = r[j];
+  if (n4 > kHlLoads * kHlThreads) {
+    constexpr int i0 = kHlLoads * kHlThreads;
+#pragma unroll
+    for (int j = 0; j < kHlLoads; ++j) r[j] = src[min(i0 + j * kHlThreads + t, n4 - 1)];
+#pragma unroll
+    for (int j = 0; j < kHlLoads; ++j) hl_lds[min(i0 + j * kHlThreads + t, n4 - 1)] = r[j];
+  }
+  uint64_t m[kHlXIter];
+  int cnt = 0;
+  bool nf = false;
+#pragma unroll
+  for (int i = 0; i < kHlXIter; ++i) {
+    m[i] = __ballot(xv[i] != 0.0f);
+    cnt += __popcll(m[i]);
+    nf = nf || !__builtin_isfinite(xv[i]);
+  }
+  // Count of nonzero values | (1 << 16) if one of them is inf or NaN; every
+  // lane stores the same value (no branch).
+  wcount[w] = cnt | (__ballot(nf) ? 1 << 16 : 0);
+  if (t < tpb) cw[t] = 0u;
+  __syncthreads();
+  int base = 0, n = 0, nonfinite = 0;
+#pragma unroll
+  for (int v = 0; v < kHlWaves; ++v) {
+    const int c = wcount[v] & 0xffff;
+    base += v < w ? c : 0;
+    n += c;
+    nonfinite |= wcount[v] >> 16;
+  }
+#pragma unroll
+  for (int i = 0; i < kHlXIter; ++i) {
+    const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m[i] >> 32),
+                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m[i]), 0));
+    if (xv[i] != 0.0f)
+      ent[base + below] = make_uint2(static_cast<uint32_t>((w * span + i * 64 + lane) * nw), __float_as_uint(xv[i]));
+    base += __popcll(m[i]);
+  }
+  const int npad = hl_pad(n);
+  if (n + t < npad) ent[n + t] = make_uint2(0u, 0u);  // +0.0 terms
+  __syncthreads();
+  const int Pb = tpb * k;
+  const uint32_t* __restrict__ tq = tab + min(t >> 4, nw - 1);
+  const int sh = 2 * (t & 15);
+  float s = 0.0f;
+  if (npad > 0 && !nonfinite) {
+    // The 2-bit code read as a signed field is the coefficient (+1, -1, 0),
+    // and fma(v, c, s) rounds s + c*v once with c*v exact: s + v, s - v, or
+    // s + (+-0) for a finite v.  Entries and sign words are read one step of
+    // kHlUnroll ahead, so LDS latency hides behind the previous step's adds.
+    const uint4* __restrict__ e4 = reinterpret_cast<const uint4*>(ent);  // two entries each
+    constexpr int kQ = kHlUnroll / 2;
+    const int last = npad / 2 - kQ;
+    const int up = 30 - sh;  // the plane's field to bits 30-31, then an arithmetic shift
+    uint4 ca[kQ], cb[kQ];
+    uint32_t wa[kHlUnroll];
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) ca[j] = e4[j];
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) {
+      wa[2 * j] = tq[ca[j].x];
+      wa[2 * j + 1] = tq[ca[j].z];
+    }
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) cb[j] = e4[min(kQ, last) + j];
+    for (int e0 = 0; e0 < npad; e0 += kHlUnroll) {
+      uint32_t wb[kHlUnroll];
+#pragma unroll
+      for (int j = 0; j < kQ; ++j) {
+        wb[2 * j] = tq[cb[j].x];
+        wb[2 * j + 1] = tq[cb[j].z];
+      }
+      uint4 cc[kQ];
+#pragma unroll
+      for (int j = 0; j < kQ; ++j) cc[j] = e4[min((e0 + 2 * kHlUnroll) / 2, last) + j];
+#pragma unroll
+      for (int j = 0; j < kQ; ++j) {
+        s = __builtin_fmaf(__uint_as_float(ca[j].y), static_cast<float>(static_cast<int>(wa[2 * j] << up) >> 30), s);
+        s = __builtin_fmaf(__uint_as_float(ca[j].w), static_cast<float>(static_cast<int>(wa[2 * j + 1] << up) >> 30), s);
+      }
+#pragma unroll
+      for (int j = 0; j < kQ; ++j) {
+        ca[j] = cb[j];
+        cb[j] = cc[j];
+      }
+#pragma unroll
+      for (int j = 0; j < kHlUnroll; ++j) wa[j] = wb[j];
+    }
+  } else if (npad > 0) {
+    // A row with inf or NaN: a zero coefficient must add nothing (0 * inf is
+    // NaN), so the term is selected rather than multiplied.
+    for (int e0 = 0; e0 < npad; e0 += kHlUnroll) {
+      uint2 c[kHlUnroll];
+#pragma unroll
+      for (int j = 0; j < kHlUnroll; ++j) c[j] = ent[e0 + j];
+      uint32_t wd[kHlUnroll];
+#pragma unroll
+      for (int j = 0; j < kHlUnroll; ++j) wd[j] = tq[c[j].x];
+#pragma unroll
+      for (int j = 0; j < kHlUnroll; ++j) {
+        const uint32_t b = (wd[j] >> sh) & 3u;
+        const float v = __uint_as_float(c[j].y);
+        s = __fadd_rn(s, b == 1u ? v : (b == 3u ? -v : 0.0f));  // s - v is s + (-v) exactly
+      }
+    }
+  }
+  const int l0 = g * tpb;
+  if (t < Pb && l0 * k + t < L * k && s >= 0.0f) atomicOr(&cw[t / k], 1u << (t % k));
+  __syncthreads();
+  if (t < tpb && l0 + t < L) codes[row * L + l0 + t] = cw[t];
 }
 
 // Matrix-core hashing: a block of 4 waves hashes 64 rows; wave w owns rows
@@ -761,6 +931,24 @@ int hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx, int6
     }
     return KH_OK;
   }
+  if (h->sg_dev) {
+    const size_t lds = sizeof(uint4) * h->sg_n4 + sizeof(uint2) * hl_pad(h->dim) + sizeof(uint32_t) * h->sg_tpb;
+    if (lds <= (size_t)kMaxDynLds) {
+      static std::once_flag once;
+      std::call_once(once, [] {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hash_dense_lds_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds);
+      });
+      for (int64_t b0 = 0; b0 < batch; b0 += INT32_MAX) {
+        const int64_t nb = std::min<int64_t>(batch - b0, INT32_MAX);
+        hipLaunchKernelGGL(hash_dense_lds_kernel, dim3((unsigned)nb, (unsigned)h->sg_groups), dim3(kHlThreads),
+                           lds, st, h->sg_dev, h->sg_n4, h->sg_words, h->k, h->L, h->sg_tpb, h->dim,
+                           x + b0 * ldx, ldx, codes + b0 * h->L);
+        KH_LAUNCHED();
+      }
+      return KH_OK;
+    }
+  }
   const int in_lds = h->dim <= 12288 ? 1 : 0;
   const size_t lds = sizeof(float) * (in_lds ? h->dim : 0) + sizeof(uint32_t) * h->L;
   for (int64_t b0 = 0; b0 < batch; b0 += 65535 * 16) {
@@ -910,6 +1098,36 @@ static int family_finish(kh_hash_family* h, kh_hash_family** out) {
       return KH_ERR_HIP;
     }
   }
+  // 2-bit sign copy for the per-row LDS kernel: whole tables per group, as
+  // few groups as 256 planes per block allow, tables spread evenly over them.
+  if (h->dim <= kHlMaxDim && h->k <= kHlThreads) {
+    const int per = kHlThreads / h->k;
+    h->sg_groups = (h->L + per - 1) / per;
+    h->sg_tpb = (h->L + h->sg_groups - 1) / h->sg_groups;
+    h->sg_words = (h->sg_tpb * h->k + 15) / 16;
+    h->sg_n4 = (h->dim * h->sg_words + 3) / 4;
+    std::vector<uint32_t> sg((size_t)h->sg_groups * h->sg_n4 * 4, 0u);
+    for (int g = 0; g < h->sg_groups; ++g)
+      for (int q = 0; q < h->sg_tpb * h->k; ++q) {
+        const int p = g * h->sg_tpb * h->k + q;
+        if (p >= P) break;
+        const int8_t* pl = h->planes_host.data() + (size_t)p * h->dim;
+        for (int d = 0; d < h->dim; ++d) {
+          const uint32_t code = pl[d] == 1 ? 1u : (pl[d] == -1 ? 3u : 0u);
+          sg[(size_t)g * h->sg_n4 * 4 + (size_t)d * h->sg_words + q / 16] |= code << (2 * (q % 16));
+        }
+      }
+    h->sg_dev = static_cast<uint4*>(dev_alloc(sizeof(uint32_t) * sg.size()));
+    if (!h->sg_dev) {
+      kh_hash_family_destroy(h);
+      return KH_ERR_ALLOC;
+    }
+    if (hipMemcpy(h->sg_dev, sg.data(), sizeof(uint32_t) * sg.size(), hipMemcpyHostToDevice) != hipSuccess) {
+      set_error("plane upload failed");
+      kh_hash_family_destroy(h);
+      return KH_ERR_HIP;
+    }
+  }
   h->planes_dev = static_cast<int8_t*>(dev_alloc(h->planes_host.size()));
   h->nnz = static_cast<int32_t*>(dev_alloc(sizeof(int32_t) * std::max(P, 1)));
   h->ent_t = static_cast<uint32_t*>(dev_alloc(sizeof(uint32_t) * ent.size()));
@@ -985,6 +1203,7 @@ extern "C" int kh_hash_family_destroy(kh_hash_family* h) {
   dev_free(h->nnz);
   dev_free(h->ent_t);
   dev_free(h->bt_dev);
+  dev_free(h->sg_dev);
   dev_free(h->windows_dev);
   dev_free(h->fallback_dev);
   dev_free(h->perms_dev);

@@ -25,6 +25,13 @@ struct kh_hash_family {
   // [ceil(dim/32)][ceil(L*k/16)][64 lanes] x 8 values; null otherwise.
   uint4* bt_dev = nullptr;
   int bt_ksteps = 0, bt_tiles = 0;
+  // 2-bit plane signs for the per-row LDS kernel (dim small enough to stage
+  // them): group g holds tables g*sg_tpb.. (planes q = 0..sg_tpb*k-1 of the
+  // group), as [dim][sg_words] words, plane q in bits 2(q%16), 2(q%16)+1 of
+  // word q/16 (01 = +1, 11 = -1, 00 = no term); each group padded to sg_n4
+  // uint4.  Null when dim or k rule it out.
+  uint4* sg_dev = nullptr;
+  int sg_tpb = 0, sg_groups = 0, sg_words = 0, sg_n4 = 0;
 };
 
 namespace kh {

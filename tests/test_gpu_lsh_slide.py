@@ -106,6 +106,25 @@ def test_hash_dense_matrix_core_path_bit_exact(kh, orc, dim, k, L, batch, srp):
     assert np.all(got[q] == (1 << k) - 1) and np.all(got[q + 1] == (1 << k) - 1)
 
 
+@pytest.mark.parametrize("dim,k,L,batch", [(784, 6, 50, 200), (2048, 9, 50, 40), (2049, 6, 50, 20),
+                                           (1, 1, 256, 17), (33, 24, 50, 30), (100, 7, 37, 64),
+                                           (257, 1, 3, 9), (512, 16, 256, 12)])
+def test_hash_dense_lds_path_bit_exact(kh, orc, dim, k, L, batch):
+    """Batches below 1024 rows with dim <= 2048 hash from LDS-staged 2-bit signs
+    over the row's compacted nonzero values (2049 takes the per-plane kernel):
+    group splits (k 24 -> 10 tables per block, k 1 -> 256), one-dimensional and
+    odd widths, fully dense rows, the hard rows of the matrix-core test."""
+    from klearu_amd.lsh import SimHash
+    rng = np.random.default_rng(dim * 7 + k)
+    fam = SimHash(dim, k, L, 9)
+    x = _hard_rows(rng, batch, dim) if batch >= 10 else rng.standard_normal((batch, dim)).astype(np.float32)
+    x[-1] = rng.uniform(0.5, 1.0, dim).astype(np.float32)  # no zero value
+    if batch > 12:
+        x[-2] = cfg1_inputs(rng, 1, dim)[0]
+    got = fam.hash_dense_batch(x).cpu().numpy().view(np.uint32)
+    np.testing.assert_array_equal(got, orc.hash_dense_batch(fam.planes(), x))
+
+
 def test_hash_sparse_matches_dense(kh, orc):
     from klearu_amd.lsh import SparseVector, SimHash
     rng = np.random.default_rng(5)
