@@ -113,8 +113,16 @@ constexpr int kHlThreads = 256;
 constexpr int kHlWaves = kHlThreads / 64;
 constexpr int kHlMaxDim = 2048;
 constexpr int kHlLoads = 16;   // uint4 sign loads in flight per thread
-constexpr int kHlUnroll = 8;   // compacted values per step (the list is padded to a multiple)
+constexpr int kHlUnroll = 16;  // compacted values per step (the list is padded to a multiple)
 constexpr int kHlXIter = kHlMaxDim / kHlThreads;
+
+// Signed 2-bit field of w at bit sh (v_bfe_i32 written out, so that the
+// conversion that follows is the signed one).
+__device__ __forceinline__ int sfield2(uint32_t w, int sh) {
+  int r;
+  asm("v_bfe_i32 %0, %1, %2, 2" : "=v"(r) : "v"(w), "v"(sh));
+  return r;
+}
 
 __host__ __device__ constexpr int hl_pad(int n) { return (n + kHlUnroll - 1) / kHlUnroll * kHlUnroll; }
 
@@ -203,45 +211,51 @@ __global__ __launch_bounds__(kHlThreads) __attribute__((amdgpu_waves_per_eu(1, 2
   if (npad > 0 && !nonfinite) {
     // The 2-bit code read as a signed field is the coefficient (+1, -1, 0),
     // and fma(v, c, s) rounds s + c*v once with c*v exact: s + v, s - v, or
-    // s + (+-0) for a finite v.  Entries and sign words are read one step of
-    // kHlUnroll ahead, so LDS latency hides behind the previous step's adds.
+    // s + (+-0) for a finite v.  Sign words are read one group of kHlUnroll
+    // ahead and entries two, so LDS latency hides behind the adds.
     const uint4* __restrict__ e4 = reinterpret_cast<const uint4*>(ent);  // two entries each
     constexpr int kQ = kHlUnroll / 2;
     const int last = npad / 2 - kQ;
-    const int up = 30 - sh;  // the plane's field to bits 30-31, then an arithmetic shift
-    uint4 ca[kQ], cb[kQ];
-    uint32_t wa[kHlUnroll];
+    // One step: sign words of the next group, entries of the one after, and
+    // the adds of the current group.  Three register sets rotate through the
+    // roles (current, next, after next) across an unrolled loop of three.
+    auto step = [&](const uint4 (&cx)[kQ], const uint32_t (&wx)[kHlUnroll], const uint4 (&cy)[kQ],
+                    uint32_t (&wy)[kHlUnroll], uint4 (&cz)[kQ], int e) {
 #pragma unroll
-    for (int j = 0; j < kQ; ++j) ca[j] = e4[j];
+      for (int j = 0; j < kQ; ++j) {
+        wy[2 * j] = tq[cy[j].x];
+        wy[2 * j + 1] = tq[cy[j].z];
+      }
+#pragma unroll
+      for (int j = 0; j < kQ; ++j) cz[j] = e4[min((e + 2 * kHlUnroll) / 2, last) + j];
+      // Keeps this step's LDS reads here: left alone, the compiler splits the
+      // entry reads and moves the value halves next to their use a step
+      // later, which exposes the LDS latency on every step.
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < kQ; ++j) {
+        s = __builtin_fmaf(__uint_as_float(cx[j].y), static_cast<float>(sfield2(wx[2 * j], sh)), s);
+        s = __builtin_fmaf(__uint_as_float(cx[j].w), static_cast<float>(sfield2(wx[2 * j + 1], sh)), s);
+      }
+    };
+    uint4 c0[kQ], c1[kQ], c2[kQ];
+    uint32_t w0[kHlUnroll], w1[kHlUnroll], w2[kHlUnroll];
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) c0[j] = e4[j];
 #pragma unroll
     for (int j = 0; j < kQ; ++j) {
-      wa[2 * j] = tq[ca[j].x];
-      wa[2 * j + 1] = tq[ca[j].z];
+      w0[2 * j] = tq[c0[j].x];
+      w0[2 * j + 1] = tq[c0[j].z];
     }
 #pragma unroll
-    for (int j = 0; j < kQ; ++j) cb[j] = e4[min(kQ, last) + j];
-    for (int e0 = 0; e0 < npad; e0 += kHlUnroll) {
-      uint32_t wb[kHlUnroll];
-#pragma unroll
-      for (int j = 0; j < kQ; ++j) {
-        wb[2 * j] = tq[cb[j].x];
-        wb[2 * j + 1] = tq[cb[j].z];
-      }
-      uint4 cc[kQ];
-#pragma unroll
-      for (int j = 0; j < kQ; ++j) cc[j] = e4[min((e0 + 2 * kHlUnroll) / 2, last) + j];
-#pragma unroll
-      for (int j = 0; j < kQ; ++j) {
-        s = __builtin_fmaf(__uint_as_float(ca[j].y), static_cast<float>(static_cast<int>(wa[2 * j] << up) >> 30), s);
-        s = __builtin_fmaf(__uint_as_float(ca[j].w), static_cast<float>(static_cast<int>(wa[2 * j + 1] << up) >> 30), s);
-      }
-#pragma unroll
-      for (int j = 0; j < kQ; ++j) {
-        ca[j] = cb[j];
-        cb[j] = cc[j];
-      }
-#pragma unroll
-      for (int j = 0; j < kHlUnroll; ++j) wa[j] = wb[j];
+    for (int j = 0; j < kQ; ++j) c1[j] = e4[min(kQ, last) + j];
+    for (int e = 0;;) {
+      step(c0, w0, c1, w1, c2, e);
+      if ((e += kHlUnroll) >= npad) break;
+      step(c1, w1, c2, w2, c0, e);
+      if ((e += kHlUnroll) >= npad) break;
+      step(c2, w2, c0, w0, c1, e);
+      if ((e += kHlUnroll) >= npad) break;
     }
   } else if (npad > 0) {
     // A row with inf or NaN: a zero coefficient must add nothing (0 * inf is
