@@ -744,18 +744,21 @@ __global__ __launch_bounds__(kQueryThreads) void query_direct_kernel(
       if (i0 + q * blockDim.x < m) atomicAdd(&sm[id[q]], 1u);
   }
   __syncthreads();
-  int base = 0;
-  for (uint32_t c0 = 0; c0 < id_bound; c0 += blockDim.x) {
-    const uint32_t i = c0 + threadIdx.x;
-    const uint32_t c = i < id_bound ? sm[i] : 0u;
-    const int pos = block_excl_scan(c ? 1 : 0, wsum, &s_total) + base;
-    if (c) {
+  // One scan: thread t owns the ids [t*R, t*R + R) in order, R = ceil(id_bound / threads).
+  const uint32_t R = (id_bound + blockDim.x - 1) / blockDim.x;
+  const uint32_t i0 = threadIdx.x * R, i1 = min(i0 + R, id_bound);
+  int c = 0;
+  for (uint32_t i = i0; i < i1; ++i) c += sm[i] != 0u;
+  int pos = block_excl_scan(c, wsum, &s_total);
+  for (uint32_t i = i0; i < i1; ++i) {
+    const uint32_t v = sm[i];
+    if (v) {
       oids[pos] = i;
-      if (ocnt) ocnt[pos] = c;
+      if (ocnt) ocnt[pos] = v;
+      ++pos;
     }
-    base += s_total;
   }
-  if (threadIdx.x == 0) out_len[row] = base;
+  if (threadIdx.x == 0) out_len[row] = s_total;
 }
 
 // Bitmap path (when the LDS below fits in kMaxDynLds): one presence bit per id.  The
