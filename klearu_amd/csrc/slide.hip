@@ -207,25 +207,43 @@ __global__ __launch_bounds__(kSlideThreads) void select_kernel(
       }
     }
   } else {
-    int base = 0, base_eq = 0;
-    for (int c0 = 0; c0 < m; c0 += blockDim.x) {
-      const int i = c0 + threadIdx.x;
-      int sel = i < m ? 1 : 0;
-      if (mode == KH_SAMPLING_TOPK) {
-        const int c = i < m ? (int)cnt[i] : 0;
-        const int eq = (i < m && c == cstar) ? 1 : 0;
-        const int r = block_excl_scan(eq, wsum, &s_total) + base_eq;
-        base_eq += s_total;
-        sel = (i < m) && (c > cstar || (eq && r < take_eq));
-      }
-      const int id = i < m ? (int)ids[i] : 0;
-      const int keep = sel && (uint32_t)id < (uint32_t)num_neurons;
-      const int pos = block_excl_scan(keep, wsum, &s_total) + base;
-      if (keep) out[pos] = (uint32_t)id;
-      base += s_total;
+    // Thread t owns the candidates [t*R, t*R + R) in order, so one block scan
+    // per quantity gives every output position: the rank among the count ==
+    // c* candidates (top-k), then the position among the kept ones.
+    // No pick at all (no candidates, or top-k of 0) writes nothing: the
+    // all-neurons fallback below then owns the output.
+    const bool topk = mode == KH_SAMPLING_TOPK;
+    n_pre = topk ? min(m, top_k) : m;
+    const int R = n_pre > 0 ? (m + (int)blockDim.x - 1) / (int)blockDim.x : 0;
+    const int i0 = min((int)threadIdx.x * R, m), i1 = min(i0 + R, m);
+    int eq_base = 0;
+    if (topk) {
+      int n_eq = 0;
+      for (int i = i0; i < i1; ++i) n_eq += (int)cnt[i] == cstar ? 1 : 0;
+      eq_base = block_excl_scan(n_eq, wsum, &s_total);
     }
-    n_sel = base;
-    n_pre = mode == KH_SAMPLING_TOPK ? min(m, top_k) : m;
+    int n_keep = 0;
+    for (int i = i0, r = eq_base; i < i1; ++i) {
+      bool sel = true;
+      if (topk) {
+        const int c = (int)cnt[i];
+        sel = c > cstar || (c == cstar && r < take_eq);
+        r += c == cstar ? 1 : 0;
+      }
+      n_keep += sel && ids[i] < (uint32_t)num_neurons ? 1 : 0;
+    }
+    int pos = block_excl_scan(n_keep, wsum, &s_total);
+    n_sel = s_total;
+    for (int i = i0, r = eq_base; i < i1; ++i) {
+      bool sel = true;
+      if (topk) {
+        const int c = (int)cnt[i];
+        sel = c > cstar || (c == cstar && r < take_eq);
+        r += c == cstar ? 1 : 0;
+      }
+      const uint32_t id = ids[i];
+      if (sel && id < (uint32_t)num_neurons) out[pos++] = id;
+    }
   }
   // empty selection -> every neuron (layer.rs:82-84)
   if (n_pre == 0 && fallback) {
