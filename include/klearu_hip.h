@@ -403,6 +403,18 @@ int kh_predictor_create(int input_dim, int hidden_dim, int output_dim, const flo
                         const float* b1_host, const float* w2_host, const float* b2_host,
                         kh_predictor** out);
 int kh_predictor_destroy(kh_predictor* p);
+/* The reference's predictor cannot fail after construction, so this has no
+ * counterpart there: the batched layer-1 kernel (batches of two or more rows)
+ * hands products between its waves through LDS flags whose waits are bounded,
+ * so a lost hand-off ends the kernel instead of hanging it, and is recorded on
+ * the handle.  kh_predictor_status synchronises the device and returns
+ * KH_ERR_HIP (clearing the record) if any call since the last status call
+ * gave up a wait -- its scores are then not trusted -- else KH_OK. */
+int kh_predictor_status(const kh_predictor* p);
+/* Test hook, no counterpart in the reference: the number of sleeps (about 64
+ * cycles each) after which such a wait gives up (default 4194304; at least 1).
+ * A tiny limit forces the give-up path while every kernel still exits. */
+int kh_predictor_set_spin_limit(kh_predictor* p, int spins);
 /* SparsityPredictor::predict (mlp_predictor.rs:102-124) for x_dev[batch][input]:
  * scores_dev[batch][output] (sigmoid), bit-exact with the reference. */
 int kh_predictor_predict(const kh_predictor* p, const float* x_dev, int64_t batch,

@@ -495,7 +495,9 @@ int st_bytes(const kh_safetensors::Tensor& t, const char* name, int64_t* n) {
     return KH_ERR_ARG;
   }
   int64_t ne = numel(t);
-  if (ne < 0 || (uint64_t)ne * (uint64_t)elem_size(t.dtype) != len) {
+  const uint64_t es = (uint64_t)elem_size(t.dtype);
+  // ne > len / es first: the product below then cannot wrap
+  if (ne < 0 || (uint64_t)ne > len / es || (uint64_t)ne * es != len) {
     kh::set_error("tensor %s: %llu bytes do not hold its shape", name, (unsigned long long)len);
     return KH_ERR_ARG;
   }

@@ -13,6 +13,7 @@
 // low 32 bits (an index keeps the low k <= 24 bits).
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <vector>
 
 #include "lsh_internal.hpp"
@@ -242,6 +243,18 @@ int rank_hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx,
   const int64_t n = batch * h->L;
   const unsigned blocks = static_cast<unsigned>((n + kRankThreads - 1) / kRankThreads);
   if (h->kind == KH_FAMILY_MINHASH && h->dim <= kMhMaxStage) {
+    // the staged nonzeros take up to 64 KiB of dynamic LDS next to the static
+    // bins, past the default dynamic limit: raise it once per process
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    std::call_once(once, [] {
+      attr_rc = hipFuncSetAttribute(reinterpret_cast<const void*>(&minhash_rows_kernel<false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds);
+      if (attr_rc == hipSuccess)
+        attr_rc = hipFuncSetAttribute(reinterpret_cast<const void*>(&minhash_rows_kernel<true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds);
+    });
+    KH_HIP(attr_rc);
     for (int64_t b0 = 0; b0 < batch; b0 += kMhMaxRows) {
       hipLaunchKernelGGL(minhash_rows_kernel<false>, dim3(static_cast<unsigned>(std::min(batch - b0, kMhMaxRows))),
                          dim3(kMhThreads), sizeof(uint32_t) * h->dim, st, h->perms_dev, h->dim, h->k, h->L,

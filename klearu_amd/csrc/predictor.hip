@@ -409,6 +409,10 @@ constexpr int kLbQuads = kLbStage / 4;
 constexpr int kLbRingBytes = kLbSlots * kLbQuads * kLbChains * 16;
 constexpr int kLbLdsBytes = kLbRingBytes + kLbRows * kL1LdsIn * 4;
 constexpr int kLbSpinMax = 1 << 22;  // a flag that never arrives ends the wait (no hang)
+// A wait that reaches its spin limit carries on (so the kernel always exits)
+// with a slot that may still be in use or hold stale products: the scores of
+// that call are not trusted, and the kernel records it in *err (read and
+// cleared by kh_predictor_status).
 static_assert(kLbRingBytes <= 65536, "ring addressed by immediate offsets");
 
 __device__ __forceinline__ int lb_flag(const int* f) {
@@ -430,7 +434,7 @@ __device__ __forceinline__ void lb_release(int* f, int v) {
 
 __global__ __launch_bounds__(kLbThreads) void pred_l1_batch_kernel(
     const uint16_t* __restrict__ Wb, const float* __restrict__ bias, const float* __restrict__ x,
-    int n_in, int hid, int batch, float* __restrict__ h) {
+    int n_in, int hid, int batch, float* __restrict__ h, int spin_max, int* __restrict__ err) {
   extern __shared__ float4 lb4[];
   float4* ring = lb4;                                             // [slot][quad][chain]
   float* xs = reinterpret_cast<float*>(lb4 + kLbRingBytes / 16);  // [kLbRows][n_in]
@@ -469,6 +473,7 @@ __global__ __launch_bounds__(kLbThreads) void pred_l1_batch_kernel(
   for (int q = 0; q < kXq; ++q)
     reinterpret_cast<float4*>(xs)[min((int)threadIdx.x + q * kLbThreads, kLbRows * n4 - 1)] = xv[q];
   lds_barrier();
+  bool gave_up = false;
   if (wave > 0) {
 #pragma unroll
     for (int i = 0; i < kLbSpp; ++i) {
@@ -476,8 +481,13 @@ __global__ __launch_bounds__(kLbThreads) void pred_l1_batch_kernel(
       if (st >= nst) break;
       const int slot = st % kLbSlots;
       // the consumer must have released this slot's previous stage
-      for (int n = 0; st >= kLbSlots && lb_flag(&freed[slot]) < st - kLbSlots && n < kLbSpinMax; ++n)
+      for (int n = 0; st >= kLbSlots && lb_flag(&freed[slot]) < st - kLbSlots; ++n) {
+        if (n == spin_max) {
+          gave_up = true;
+          break;
+        }
         __builtin_amdgcn_s_sleep(1);
+      }
       const int j0 = st * kLbStage + jl * 8;
       float4* row0 = ring + (slot * kLbQuads + 2 * jl) * kLbChains;  // quads 2 jl, 2 jl + 1
       const int sw = lb_swz(2 * jl);  // the same for both quads
@@ -495,6 +505,7 @@ __global__ __launch_bounds__(kLbThreads) void pred_l1_batch_kernel(
       }
       lb_publish(&ready[slot], st);  // every lane stores the same value: no branch
     }
+    if (gave_up) *err = 1;
     return;
   }
   // consumer: lane ch reads quad q of slot sl at ring[(sl * kLbQuads + q) * 32 + (ch ^ swz(q))].
@@ -510,9 +521,13 @@ __global__ __launch_bounds__(kLbThreads) void pred_l1_batch_kernel(
   // parity h; a stage's quads are refilled with those two stages ahead, so a
   // read has 64 adds (about 400 cycles) to arrive
   float4 rq[2 * kLbQuads];
-  for (int n = 0; n < kLbSpinMax; ++n) {
+  for (int n = 0;; ++n) {
     const int f0 = lb_flag(&ready[0]), f1 = lb_flag(&ready[1]);
     if (f0 >= 0 && (nst < 2 || f1 >= 1)) break;
+    if (n == spin_max) {
+      gave_up = true;
+      break;
+    }
     __builtin_amdgcn_s_sleep(1);
   }
 #pragma unroll
@@ -552,8 +567,11 @@ __global__ __launch_bounds__(kLbThreads) void pred_l1_batch_kernel(
     constexpr int SL = decltype(slot_c)::value;
     constexpr int S2 = (SL + 2) % kLbSlots, S3 = (SL + 3) % kLbSlots;
     constexpr int S4 = (SL + 4) % kLbSlots, S5 = (SL + 5) % kLbSlots;
-    for (int n = 0; n < kLbSpinMax; ++n) {
-      if ((st + 2 >= nst || f2 >= st + 2) && (st + 3 >= nst || f3 >= st + 3)) break;
+    for (int n = 0; !((st + 2 >= nst || f2 >= st + 2) && (st + 3 >= nst || f3 >= st + 3)); ++n) {
+      if (n == spin_max) {
+        gave_up = true;
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
       f2 = lb_flag(&ready[S2]);
       f3 = lb_flag(&ready[S3]);
@@ -576,6 +594,7 @@ __global__ __launch_bounds__(kLbThreads) void pred_l1_batch_kernel(
   const int r = ch / kLbOut, o = ch % kLbOut;
   if (r0 + r < batch && c0 + o < hid)
     h[(size_t)(r0 + r) * hid + c0 + o] = fmaxf(__fadd_rn(s, bias[c0 + o]), 0.0f);
+  if (gave_up) *err = 1;
 }
 
 // Layer 2 (short chains): one lane per output, the whole weight row in
@@ -1125,6 +1144,8 @@ struct kh_predictor {
   float* b1 = nullptr;
   void* w2b = nullptr;   // [ceil(hid/8)][out][8]
   float* b2 = nullptr;
+  int* err = nullptr;    // device word: a batched layer-1 wait reached its spin limit
+  int spin_max = kLbSpinMax;
   mutable StreamWs ws;   // scratch per stream (PredBufs)
 };
 
@@ -1240,6 +1261,12 @@ extern "C" int kh_predictor_create(int input_dim, int hidden_dim, int output_dim
   if (rc == KH_OK) rc = upload(&b2, b2_host, output_dim);
   p->b1 = static_cast<float*>(b1);
   p->b2 = static_cast<float*>(b2);
+  if (rc == KH_OK) {
+    const int zero = 0;
+    void* e = nullptr;
+    rc = upload(&e, &zero, 1);
+    p->err = static_cast<int*>(e);
+  }
   if (rc != KH_OK) {
     kh_predictor_destroy(p);
     return rc;
@@ -1254,7 +1281,26 @@ extern "C" int kh_predictor_destroy(kh_predictor* p) {
   dev_free(p->b1);
   dev_free(p->w2b);
   dev_free(p->b2);
+  dev_free(p->err);
   delete p;
+  return KH_OK;
+}
+
+extern "C" int kh_predictor_status(const kh_predictor* p) {
+  KH_CHECK_ARG(p != nullptr, "null argument");
+  KH_HIP(hipDeviceSynchronize());
+  int v = 0;
+  KH_HIP(hipMemcpy(&v, p->err, sizeof(int), hipMemcpyDeviceToHost));
+  if (v == 0) return KH_OK;
+  KH_HIP(hipMemset(p->err, 0, sizeof(int)));
+  set_error("a batched layer-1 wait reached its spin limit: the scores of that call are not trusted");
+  return KH_ERR_HIP;
+}
+
+extern "C" int kh_predictor_set_spin_limit(kh_predictor* p, int spins) {
+  KH_CHECK_ARG(p != nullptr, "null argument");
+  KH_CHECK_ARG(spins >= 1, "spin limit %d must be at least 1", spins);
+  p->spin_max = spins;
   return KH_OK;
 }
 
@@ -1373,7 +1419,7 @@ static int predict_typed(const kh_predictor* p, const float* x, int64_t batch, f
       (int64_t)ceil_div(p->hid, kL1Chains) * batch > device_cus())
     hipLaunchKernelGGL(pred_l1_batch_kernel, dim3(ceil_div(p->hid, kLbOut), ceil_div(batch, kLbRows)),
                        dim3(kLbThreads), kLbLdsBytes, st, static_cast<const uint16_t*>(p->w1b), p->b1,
-                       x, p->in_dim, p->hid, static_cast<int>(batch), hbuf);
+                       x, p->in_dim, p->hid, static_cast<int>(batch), hbuf, p->spin_max, p->err);
   else if (p->in_dim <= kL1LdsIn)
     hipLaunchKernelGGL(pred_l1_lds_kernel<W>, dim3(ceil_div(p->hid, kL1Chains), batch),
                        dim3(kL1LdsThreads), kL1LdsBytes, st, w1, p->b1, x, p->in_dim, p->hid, hbuf,

@@ -77,6 +77,15 @@ class SparsityPredictor:
         _lib.call("kh_predictor_weights", self._h, hptr(w1), hptr(b1), hptr(w2), hptr(b2))
         return w1, b1, w2, b2
 
+    def status(self):
+        """Raises KlearuError if a batched call since the last check gave up a
+        bounded wait between its waves (its scores are then not trusted)."""
+        _lib.call("kh_predictor_status", self._h)
+
+    def set_spin_limit(self, spins: int):
+        """Test hook: sleeps after which such a wait gives up (default 4194304)."""
+        _lib.call("kh_predictor_set_spin_limit", self._h, int(spins))
+
     def __del__(self):
         h = getattr(self, "_h", None)
         if h:

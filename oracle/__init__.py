@@ -91,6 +91,7 @@ _sig("or_sigmoid", _f, _f)
 _sig("or_silu", _f, _f)
 _sig("or_sparse_mlp_forward_bf16", None, _u16p, _u16p, _u16p, _int, _int, _f32p, _i64p, _i64, _f32p,
      _f32p)
+_sig("or_rms_inv", _f, _f32p, _i64, _f)
 _sig("or_rmsnorm", None, _f32p, _f32p, _i64, _f)
 _sig("or_rope_tables", None, _int, _int, _f, _f32p, _f32p)
 _sig("or_rope_apply", None, _f32p, _int, _f32p, _f32p, _i64)
@@ -360,6 +361,12 @@ def sparse_mlp_forward_bf16(wg, wu, wd, x, active):
                                    np.ascontiguousarray(wd).reshape(-1), hidden, inter, f32(x),
                                    active, active.size, y, h)
     return y, h[:active.size].copy()
+
+
+def rms_inv(x, eps):
+    """RmsNorm's scale 1/rms of one row (rms_norm.rs:48-52), as an f32."""
+    x = f32(x)
+    return np.float32(lib.or_rms_inv(x, x.size, float(eps)))
 
 
 def rmsnorm(x, w, eps):

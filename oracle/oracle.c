@@ -913,15 +913,21 @@ void or_sparse_mlp_forward_bf16(const uint16_t* wg, const uint16_t* wu, const ui
   free(h);
 }
 
-/* RmsNorm::forward (model/rms_norm.rs:43-64), plain-weight variant. */
-void or_rmsnorm(float* x, const float* w, int64_t n, float eps) {
+/* RmsNorm's scale 1/rms (model/rms_norm.rs:48-52): the sequential f32 sum of
+ * the rounded squares from 0.0, then sqrt(sum/n + eps) and its reciprocal. */
+float or_rms_inv(const float* x, int64_t n, float eps) {
   float ss = 0.0f;
   for (int64_t i = 0; i < n; ++i) {
     float p = x[i] * x[i];
     ss = ss + p;
   }
   float rms = sqrtf(ss / (float)n + eps);
-  float inv = 1.0f / rms;
+  return 1.0f / rms;
+}
+
+/* RmsNorm::forward (model/rms_norm.rs:43-64), plain-weight variant. */
+void or_rmsnorm(float* x, const float* w, int64_t n, float eps) {
+  float inv = or_rms_inv(x, n, eps);
   for (int64_t i = 0; i < n; ++i) {
     float t = x[i] * inv;
     x[i] = t * w[i];

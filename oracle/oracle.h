@@ -158,6 +158,7 @@ void or_sparse_mlp_forward_bf16(const uint16_t* wg, const uint16_t* wu, const ui
                                 int hidden, int inter, const float* x, const int64_t* active,
                                 int64_t k, float* y, float* h);
 float or_silu(float x);
+float or_rms_inv(const float* x, int64_t n, float eps);
 void or_rmsnorm(float* x, const float* w, int64_t n, float eps);
 void or_rope_tables(int head_dim, int max_seq, float theta, float* cos_t, float* sin_t);
 void or_rope_apply(float* x, int half, const float* cos_t, const float* sin_t, int64_t pos);

@@ -236,11 +236,16 @@ def test_safetensors_malformed_files(tmp_path):
 def test_safetensors_bounds_and_sizes_checked_on_read(tmp_path):
     p = tmp_path / "x.safetensors"
     hdr = json.dumps({"oob": {"dtype": "F32", "shape": [4], "data_offsets": [0, 16]},
-                      "short": {"dtype": "F32", "shape": [3], "data_offsets": [0, 8]}}).encode()
+                      "short": {"dtype": "F32", "shape": [3], "data_offsets": [0, 8]},
+                      # 2^62 elements of 4 bytes: the byte count wraps to 0 in 64 bits
+                      "wrap": {"dtype": "F32", "shape": [1 << 62], "data_offsets": [0, 0]}}).encode()
     p.write_bytes(struct.pack("<Q", len(hdr)) + hdr + b"\0" * 8)
     with SafeTensorsFile(str(p)) as st:
         _raises(KH_ERR_ARG, st.tensor_to_f32, "oob")                                 # data out of bounds
         _raises(KH_ERR_ARG, st.tensor_to_f32, "short")                               # bytes != shape
+        _raises(KH_ERR_ARG, _lib.call, "kh_safetensors_read_f32", st._h, b"wrap",    # shape overflows bytes
+                hp(np.empty(1, np.float32)), 1 << 62)
+        _raises(KH_ERR_ARG, _lib.call, "kh_safetensors_read_raw", st._h, b"wrap", hp(np.empty(1, np.float32)), 0)
         _raises(KH_ERR_ARG, st.info, "absent")                                       # MissingWeight
         out = np.empty(5, np.float32)
         _raises(KH_ERR_ARG, _lib.call, "kh_safetensors_read_f32", st._h, b"short", hp(out), 5)

@@ -32,6 +32,14 @@ def close_row(got, ref, kv, what=""):
     return close(got, ref, what)
 
 
+def check_scale(orc, h_in, ws, what):
+    """The RmsNorm scale a fused block wrote (norm_ws) is rms_norm.rs:48-52's, bit for bit."""
+    inv = np.array([orc.rms_inv(h_in, 1e-5)], np.float32)
+    got = ws.cpu().numpy()[:1]
+    print(f"{what}: norm scale {float(got[0])!r} (oracle {float(inv[0])!r})")
+    np.testing.assert_array_equal(got.view(np.uint32), inv.view(np.uint32), err_msg=f"{what}: norm scale")
+
+
 def bf16_round(orc, a):
     return orc.bf16_to_f32(orc.bf16_from_f32(np.asarray(a, np.float32)))
 
@@ -261,9 +269,11 @@ def test_attn_block_chained(kh, orc, H, nh, nkv, d, R, k, pre, steps):
     wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
     hd = torch.from_numpy(rng.standard_normal(H).astype(np.float32)).cuda()
     wnd = torch.from_numpy(wn).cuda()
+    ws = torch.empty(1, dtype=torch.float32, device="cuda")
     for step in range(steps):
         h_in = hd.cpu().numpy().copy()
-        heads = attn_block(p, c.attn, hd, wnd, 1e-5, k)
+        heads = attn_block(p, c.attn, hd, wnd, 1e-5, k, norm_ws=ws)
+        check_scale(orc, h_in, ws, f"step {step}")
         norm = orc.rmsnorm(h_in, wn, 1e-5)
         scores, _ = orc.predictor_predict(w1, b1, w2, b2, norm)
         sel = np.sort(orc.select_top_k(scores, k))
@@ -272,6 +282,43 @@ def test_attn_block_chained(kh, orc, H, nh, nkv, d, R, k, pre, steps):
         want = h_in + c.oracle_step(0, norm, sel.tolist())
         close(hd.cpu().numpy(), want, f"step {step}")
     assert c.attn.current_len(0) == pre + steps
+
+
+@pytest.mark.parametrize("H,nh,d,R,k,pre", [
+    (4096, 32, 128, 128, 16, 2000),   # cfg4 (7B)
+    (2048, 16, 128, 128, 8, 300),     # a 1.1B-class width
+])
+def test_attn_block_hard_norm_rows(kh, orc, H, nh, d, R, k, pre):
+    """kh_dejavu_attn_block fed hidden rows whose sum of squares defeats the
+    exact sum's speculative windows (ties stuck at 2^24, round-up drift),
+    leading zeros, an all-zero row, tiny, huge and wide-range magnitudes: the
+    RmsNorm scale it writes is the reference's bit for bit, the head set is
+    the oracle's, and the residual is within tolerance (rms_norm.rs:43-53,
+    sparse/mod.rs:56-112)."""
+    from hard_rows import hard_hidden_rows
+    from klearu_amd.attention import attn_block
+    from klearu_amd.dejavu import SparsityPredictor
+    rng = np.random.default_rng(83 + H)
+    rows = hard_hidden_rows(rng, H)
+    c = Case(orc, rng, H, nh, nh, d, pre + len(rows) + 4, 1, pre)
+    w1 = orc.bf16_from_f32(rng.normal(0, 0.05, (R, H)).astype(np.float32))
+    w2 = orc.bf16_from_f32(rng.normal(0, 0.3, (nh, R)).astype(np.float32))
+    b1 = rng.normal(0, 0.1, R).astype(np.float32)
+    b2 = rng.normal(0, 0.1, nh).astype(np.float32)
+    p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
+    wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    wnd = torch.from_numpy(wn).cuda()
+    ws = torch.empty(1, dtype=torch.float32, device="cuda")
+    for name, row in rows.items():
+        hd = torch.from_numpy(row.copy()).cuda()
+        ws.fill_(float("nan"))
+        heads = attn_block(p, c.attn, hd, wnd, 1e-5, k, norm_ws=ws)
+        check_scale(orc, row, ws, name)
+        norm = orc.rmsnorm(row, wn, 1e-5)
+        scores, _ = orc.predictor_predict(w1, b1, w2, b2, norm)
+        sel = np.sort(orc.select_top_k(scores, k))
+        np.testing.assert_array_equal(heads.cpu().numpy(), sel, err_msg=name)
+        close(hd.cpu().numpy(), row + c.oracle_step(0, norm, sel.tolist()), name)
 
 
 def test_decoder_layers_chained_7b(kh, orc):
@@ -307,6 +354,7 @@ def test_decoder_layers_chained_7b(kh, orc):
         # attention half
         h_in = hd.cpu().numpy().copy()
         heads = attn_block(hp, c.attn, hd, torch.from_numpy(wn_a).cuda(), 1e-5, kh_, norm_ws=ws)
+        check_scale(orc, h_in, ws, f"layer {layer} attention")
         norm = orc.rmsnorm(h_in, wn_a, 1e-5)
         s, _ = orc.predictor_predict(hw1, hb1, hw2, hb2, norm)
         sel = np.sort(orc.select_top_k(s, kh_))
@@ -315,6 +363,7 @@ def test_decoder_layers_chained_7b(kh, orc):
         # MLP half
         h_in = hd.cpu().numpy().copy()
         act = mlp_block(npred, mlp, hd, torch.from_numpy(wn_m).cuda(), 1e-5, kn, norm_ws=ws)
+        check_scale(orc, h_in, ws, f"layer {layer} MLP")
         norm = orc.rmsnorm(h_in, wn_m, 1e-5)
         s, _ = orc.predictor_predict(nw1, nb1, nw2, nb2, norm)
         sel = np.sort(orc.select_top_k(s, kn))

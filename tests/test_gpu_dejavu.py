@@ -371,18 +371,60 @@ def test_mlp_block_chained_exact(kh, orc, H, I, R, k, layers):
         p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
         h_in = hd.cpu().numpy().copy()
         act = mlp_block(p, mlp, hd, wnd, 1e-5, k, norm_ws=ws)
-        norm = orc.rmsnorm(h_in, wn, 1e-5)
-        scores, _ = orc.predictor_predict(w1, b1, w2, b2, norm)
-        sel = np.sort(orc.select_top_k(scores, k))
-        got = act.cpu().numpy()
-        print(f"layer {layer}: {np.setxor1d(got, sel).size} ids differ")
-        np.testing.assert_array_equal(got, sel)
-        y, _ = orc.sparse_mlp_forward_bf16(wg, wu, wd, norm, sel.astype(np.int64))
-        want = h_in + y
-        out = hd.cpu().numpy()
-        scale = float(np.max(np.abs(want)))
-        print(f"layer {layer}: max-abs {float(np.max(np.abs(out - want))):.3e} (max |hidden| {scale:.3e})")
-        np.testing.assert_allclose(out, want, rtol=RTOL, atol=1e-4 * scale)
+        _check_block(orc, f"layer {layer}", h_in, wn, ws, act, hd, (w1, b1, w2, b2), k, (wg, wu, wd))
+
+
+def _check_block(orc, what, h_in, wn, ws, act, hd, pred, k, ffn):
+    """One kh_dejavu_mlp_block call against the oracle: the RmsNorm scale the
+    block wrote (norm_ws) bit-equal to rms_norm.rs:48-52's, the active set
+    equal to the oracle's own top-k (no boundary swaps), and the updated row
+    within the BF16-weight tolerance of the oracle's residual."""
+    inv = orc.rms_inv(h_in, 1e-5)
+    got_inv = ws.cpu().numpy()[:1]
+    print(f"{what}: norm scale {float(got_inv[0])!r} (oracle {float(inv)!r})")
+    np.testing.assert_array_equal(got_inv.view(np.uint32), np.array([inv], np.float32).view(np.uint32),
+                                  err_msg=f"{what}: norm scale")
+    norm = orc.rmsnorm(h_in, wn, 1e-5)
+    scores, _ = orc.predictor_predict(*pred, norm)
+    sel = np.sort(orc.select_top_k(scores, k))
+    got = act.cpu().numpy()
+    print(f"{what}: {np.setxor1d(got, sel).size} ids differ")
+    np.testing.assert_array_equal(got, sel, err_msg=what)
+    y, _ = orc.sparse_mlp_forward_bf16(*ffn, norm, sel.astype(np.int64))
+    want = h_in + y
+    out = hd.cpu().numpy()
+    scale = float(np.max(np.abs(want)))
+    print(f"{what}: max-abs {float(np.max(np.abs(out - want))):.3e} (max |hidden| {scale:.3e})")
+    np.testing.assert_allclose(out, want, rtol=RTOL, atol=1e-4 * scale, err_msg=what)
+
+
+@pytest.mark.parametrize("H,I,R,k", [
+    (4096, 11008, 256, 1652),   # cfg3 (7B)
+    (2048, 5632, 128, 564),     # cfg2 (1.1B)
+])
+def test_mlp_block_hard_norm_rows(kh, orc, H, I, R, k):
+    """kh_dejavu_mlp_block fed hidden rows whose sum of squares defeats the
+    exact sum's speculative windows (ties stuck at 2^24, round-up drift),
+    leading zeros, an all-zero row, tiny, huge and wide-range magnitudes: the
+    fused predictor kernel's own exact-sum instance must take its sequential
+    fallback and still write the reference's RmsNorm scale bit for bit, and
+    the selection must stay the oracle's (rms_norm.rs:43-53,
+    sparse/mod.rs:115-125)."""
+    from hard_rows import hard_hidden_rows
+    from klearu_amd.dejavu import Mlp, SparsityPredictor, mlp_block
+    rng = np.random.default_rng(57 + H)
+    wg, wu, wd, _, _ = _ffn_case(orc, rng, H, I, k, 1)
+    mlp = Mlp(wg, wu, wd, max_batch=1)
+    w1, b1, w2, b2 = make_predictor(orc, rng, H, R, I, bias=True)
+    p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
+    wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    wnd = torch.from_numpy(wn).cuda()
+    ws = torch.full((1,), float("nan"), dtype=torch.float32, device="cuda")
+    for name, row in hard_hidden_rows(rng, H).items():
+        hd = torch.from_numpy(row.copy()).cuda()
+        ws.fill_(float("nan"))
+        act = mlp_block(p, mlp, hd, wnd, 1e-5, k, norm_ws=ws)
+        _check_block(orc, name, row, wn, ws, act, hd, (w1, b1, w2, b2), k, (wg, wu, wd))
 
 
 def test_batched_norm_select_union_exact(kh, orc):
@@ -433,6 +475,37 @@ def test_sparse_ffn_out_of_range_ids_are_reported(kh, orc):
         good = torch.tensor([3, 7], dtype=torch.int32, device="cuda")
         mlp.forward_sparse_into(xd, good, torch.zeros(batch, H, device="cuda"))
         mlp.status()
+
+
+def test_batched_predictor_wait_give_up_is_reported(kh, orc):
+    """The batched layer-1 kernel (7B shape, batch 16) bounds every wait for
+    its LDS hand-offs.  With the spin limit forced down to one sleep from the
+    host, the consumer gives up waiting for the producers' first stage: the
+    kernel still exits, and kh_predictor_status reports the call.  With the
+    default limit restored the scores are bit-exact again and the status is
+    clean."""
+    from klearu_amd import KlearuError
+    from klearu_amd._lib import KH_ERR_HIP
+    from klearu_amd.dejavu import SparsityPredictor
+    rng = np.random.default_rng(12)
+    H, R, I, B = 4096, 256, 11008, 16
+    w1, b1, w2, b2 = make_predictor(orc, rng, H, R, I, bias=True)
+    p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
+    x = rng.standard_normal((B, H)).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    p.status()
+    p.set_spin_limit(1)
+    p.predict(xd)
+    with pytest.raises(KlearuError) as e:
+        p.status()
+    assert e.value.code == KH_ERR_HIP
+    p.status()   # the record was cleared
+    p.set_spin_limit(1 << 22)
+    got = p.predict(xd).cpu().numpy()
+    p.status()
+    for b in (0, 7, 15):
+        want, _ = orc.predictor_predict(w1, b1, w2, b2, x[b])
+        np.testing.assert_array_equal(got[b].view(np.uint32), want.view(np.uint32))
 
 
 def test_predictor_concurrent_streams(kh, orc):

@@ -119,6 +119,28 @@ def test_rmsnorm_kats(orc):
     assert abs(float(np.sum(x * x)) - 4.0) < 0.01
 
 
+def test_rms_inv_known_answers(orc):
+    """The RmsNorm scale 1/rms (rms_norm.rs:48-52) that the fused decode blocks
+    write out: closed forms and a known answer that only the left-to-right f32
+    sum of squares reproduces."""
+    assert orc.rms_inv(np.full(4, 2.0, np.float32), 0.0) == np.float32(0.5)  # 16/4 = 4, sqrt 2
+    # 4096^2 = 2^24; every later square 1.0 is a tie that rounds back down, so
+    # the sequential sum stays 2^24: 2^24/4096 = 4096, sqrt 64, scale 1/64.
+    # The exact (or any tree-ordered) sum 2^24 + 4095 gives a different scale.
+    stuck = np.ones(4096, np.float32)
+    stuck[0] = 4096.0
+    assert orc.rms_inv(stuck, 0.0) == np.float32(1.0 / 64.0)
+    assert orc.rms_inv(stuck[::-1].copy(), 0.0) != np.float32(1.0 / 64.0)
+    # a zero row: the scale is 1/sqrt(eps), each operation correctly rounded in f32
+    eps = np.float32(1e-5)
+    assert orc.rms_inv(np.zeros(64, np.float32), eps) == np.float32(1.0) / np.sqrt(eps)
+    # RmsNorm::forward is x * scale * w, each product rounded
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(333).astype(np.float32)
+    inv = orc.rms_inv(x, 1e-6)
+    np.testing.assert_array_equal(orc.rmsnorm(x, np.ones(333, np.float32), 1e-6), x * inv)
+
+
 def test_rope_kats(orc):
     c, s = orc.rope_tables(2, 4, 1.0)
     x = np.array([1.0, 0.0], np.float32)
