@@ -45,10 +45,12 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "gather.hpp"
 #include "mfma.hpp"
+#include "pred_l1.hpp"
 
 namespace kh {
 
@@ -111,7 +113,8 @@ __device__ void qkv_plan(const int32_t* __restrict__ heads, int nent, int nh, in
 }
 
 // y[b][row] = Wkvq[row] . x[b] for the K/V rows and the Q rows of selected
-// heads.  The grid has one extra (last) block that writes the o_proj row list.
+// heads, rows from row_base on (kvrows: the K/V rows were projected already).
+// The grid has one extra (last) block that writes the o_proj row list.
 // NORM (batch 1): x is the un-normalised hidden row and RmsNorm (weight nw) is
 // applied while staging it, with the exact scale at norm_inv (written by the
 // head predictor's layer 1 for this row).
@@ -121,7 +124,7 @@ __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
     int D, int nh, const int32_t* __restrict__ heads, int nsel, float* __restrict__ y,
     int ystride, int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows,
     int32_t* __restrict__ urank, const float* __restrict__ nw,
-    const float* __restrict__ norm_inv) {
+    const float* __restrict__ norm_inv, int row_base) {
   extern __shared__ float4 xs4[];  // [kQkvTok][H/4]; the plan block's flags / union list
   __shared__ int wsum[kQkvWaves];
   __shared__ int s_total;
@@ -131,7 +134,7 @@ __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
     qkv_plan(heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_flag + nh, wsum, &s_total);
     return;
   }
-  const int row0 = blockIdx.x * kQkvWaves;
+  const int row0 = row_base + blockIdx.x * kQkvWaves;
   if (row0 >= kvrows) {
     // Q rows of head h (D is a multiple of kQkvWaves): skip unless selected.
     const int h = (row0 - kvrows) / D;
@@ -234,6 +237,108 @@ __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
       const float s = wave_sum(acc[b]);
       if (lane == 0) y[(size_t)b * ystride + row] = s;
     }
+  }
+}
+
+// The head predictor's layer 1 and the K/V projections of one decode step
+// in one launch.  Every kv head is appended to the cache whatever heads the
+// predictor picks (sparse_attention.rs:26-40), so the K and V rows do not
+// wait for the selection: blocks [0, nl1) run layer 1 (pred_l1.hpp: exact
+// RmsNorm, exact chains; one block per CU, which leaves most CUs idle for
+// about 15 us at the 7B shape), the others stream the 2*kvd K/V rows of Wkvq
+// meanwhile.  The launch's LDS request (kL1LdsBytes) keeps one block per CU,
+// so no projection wave shares a CU with a chain.  A K/V block applies
+// RmsNorm with its own scale from an f32 tree sum of the squares: the
+// projected rows carry tolerance anyway (their dot products use a parallel
+// order), and the scale stays within a few ulps of the exact one, which only
+// the selection needs bit for bit.  Row r of wave w of block kb: rows gw,
+// gw + nwaves, ... with gw = kb*8 + w, one 8 KB weight row per wave in flight
+// ahead of the one being added.
+template <typename W>
+__global__ __launch_bounds__(kL1LdsThreads) void attn_pred_kv_kernel(
+    const W* __restrict__ w1, const float* __restrict__ b1, int hid, float* __restrict__ hbuf,
+    const float* __restrict__ x, int H, const float* __restrict__ nw, float* __restrict__ inv_out,
+    float eps, const uint16_t* __restrict__ wkvq, int kvrows, float* __restrict__ y, int nl1) {
+  extern __shared__ float4 lds4[];
+  if ((int)blockIdx.x < nl1) {
+    pred_l1_lds_body<W>(blockIdx.x, 0, w1, b1, x, H, hid, hbuf, nw, inv_out, eps, lds4);
+    return;
+  }
+  static_assert(kL1LdsThreads == 64 * kQkvWaves, "one projection row per wave");
+  float* red = reinterpret_cast<float*>(lds4 + 1024);  // [kQkvWaves], after xn (H <= 4096)
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nwaves = ((int)gridDim.x - nl1) * kQkvWaves;
+  const int gw = ((int)blockIdx.x - nl1) * kQkvWaves + wave;
+  const int nchunk = H >> 3, H4 = H >> 2;
+  // the row and the norm weights first, then the first weight row
+  constexpr int kXq = 4096 / 4 / (64 * kQkvWaves);
+  float4 xv[kXq], wn[kXq];
+#pragma unroll
+  for (int q = 0; q < kXq; ++q) {
+    const int i = min((int)threadIdx.x + q * 64 * kQkvWaves, H4 - 1);
+    xv[q] = reinterpret_cast<const float4*>(x)[i];
+    wn[q] = reinterpret_cast<const float4*>(nw)[i];
+  }
+  int row = gw;
+  uint4 wv[kQkvChunks];
+  {
+    const uint4* __restrict__ w = reinterpret_cast<const uint4*>(wkvq + (size_t)min(row, kvrows - 1) * H);
+#pragma unroll
+    for (int q = 0; q < kQkvChunks; ++q) wv[q] = ld_stream(w + min(lane + 64 * q, nchunk - 1));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // sum of squares: per thread, per wave, then the waves in order
+  float ss = 0.0f;
+#pragma unroll
+  for (int q = 0; q < kXq; ++q)
+    if ((int)threadIdx.x + q * 64 * kQkvWaves < H4)
+      ss += (xv[q].x * xv[q].x + xv[q].y * xv[q].y) + (xv[q].z * xv[q].z + xv[q].w * xv[q].w);
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  lds_barrier();
+  float tot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kQkvWaves; ++i) tot += red[i];
+  const float inv = rms_inv_exact(tot, H, eps);
+#pragma unroll
+  for (int q = 0; q < kXq; ++q) {
+    float4 v = xv[q];
+    v.x = __fmul_rn(__fmul_rn(v.x, inv), wn[q].x);
+    v.y = __fmul_rn(__fmul_rn(v.y, inv), wn[q].y);
+    v.z = __fmul_rn(__fmul_rn(v.z, inv), wn[q].z);
+    v.w = __fmul_rn(__fmul_rn(v.w, inv), wn[q].w);
+    lds4[min((int)threadIdx.x + q * 64 * kQkvWaves, H4 - 1)] = v;  // clamped (see stage_f4)
+  }
+  lds_barrier();
+  const float4* xs4 = lds4;
+  for (; row < kvrows; row += nwaves) {
+    // the next row's weights go out before this row's products (the last
+    // iteration re-reads its own row, unused)
+    uint4 nv[kQkvChunks];
+    const int nrow = min(row + nwaves, kvrows - 1);
+    const uint4* __restrict__ w = reinterpret_cast<const uint4*>(wkvq + (size_t)nrow * H);
+#pragma unroll
+    for (int q = 0; q < kQkvChunks; ++q) nv[q] = ld_stream(w + min(lane + 64 * q, nchunk - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    float a = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kQkvChunks; ++q) {
+      const int c = lane + 64 * q;
+      const int cc = min(c, nchunk - 1);
+      float wf[8];
+      widen16(wv[q], wf, uint16_t());
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wf[e] = c < nchunk ? wf[e] : 0.0f;
+      const float4 x0 = xs4[2 * cc], x1 = xs4[2 * cc + 1];
+      a = fmaf(wf[0], x0.x, a); a = fmaf(wf[1], x0.y, a);
+      a = fmaf(wf[2], x0.z, a); a = fmaf(wf[3], x0.w, a);
+      a = fmaf(wf[4], x1.x, a); a = fmaf(wf[5], x1.y, a);
+      a = fmaf(wf[6], x1.z, a); a = fmaf(wf[7], x1.w, a);
+    }
+    const float sum = wave_sum(a);
+    if (lane == 0) y[row] = sum;
+#pragma unroll
+    for (int q = 0; q < kQkvChunks; ++q) wv[q] = nv[q];
   }
 }
 
@@ -889,6 +994,22 @@ __global__ void mfma_tile16x32_kernel(const uint16_t* __restrict__ W, int rows, 
       *reinterpret_cast<const uint4*>(W + (size_t)(16 * rt + r) * H + 32 * kt + 8 * kb);
 }
 
+// Compute units of the current device (cached per device).
+static int attn_device_cus() {
+  static std::mutex mu;
+  static std::vector<int> cus;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> g(mu);
+  if ((int)cus.size() <= dev) cus.resize(dev + 1, 0);
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 struct kh_sparse_attn {
   int hidden = 0, nh = 0, nkv = 0, d = 0, max_seq = 0, max_batch = 0, kv_f32 = 0;
   uint16_t* wkvq = nullptr;  // [2*kvd + nh*d][hidden]
@@ -1240,10 +1361,12 @@ static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
 
 // nrm.w set (batch 1 only): x is the un-normalised hidden row, normalised
 // inside the projection kernel with the scale at nrm.inv.
+// kv_done (batch 1 with nrm.w): attn_pred_kv_kernel projected the K/V rows,
+// so only the selected heads' Q rows remain.
 template <int NB>
 static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64_t* pos,
                        const int32_t* heads, int nsel, float* out, int accumulate,
-                       hipStream_t st, const NormIn& nrm = NormIn{}) {
+                       hipStream_t st, const NormIn& nrm = NormIn{}, bool kv_done = false) {
   const int H = a->hidden, D = a->d, qd = a->nh * D, kvrows = 2 * a->kvd();
   // 1. projections (+ the o_proj row list in the last block)
   const int rows = kvrows + qd;
@@ -1274,16 +1397,17 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
       set_error("hidden %d too large to stage %d tokens", H, std::min(NB, kQkvTok));
       return KH_ERR_UNSUPPORTED;
     }
+    const int row_base = kv_done ? kvrows : 0;
     if (nrm.w && NB == 1)
-      hipLaunchKernelGGL((attn_qkv_kernel<1, true>), dim3(rows / kQkvWaves + 1),
+      hipLaunchKernelGGL((attn_qkv_kernel<1, true>), dim3((rows - row_base) / kQkvWaves + 1),
                          dim3(64 * kQkvWaves), lds, st, a->wkvq, x, batch, H, kvrows, D, a->nh,
                          heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
-                         a->qrows + qd + 1, nrm.w, nrm.inv);
+                         a->qrows + qd + 1, nrm.w, nrm.inv, row_base);
     else
       hipLaunchKernelGGL(attn_qkv_kernel<NB>, dim3(rows / kQkvWaves + 1), dim3(64 * kQkvWaves),
                          lds, st, a->wkvq, x, batch, H, kvrows, D, a->nh, heads, nsel, a->y,
                          a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1, nullptr,
-                         nullptr);
+                         nullptr, 0);
     KH_LAUNCHED();
   }
   // 2. split-K decode over the cache and the K/V append (then, for batch > 2 or head
@@ -1396,9 +1520,40 @@ extern "C" int kh_dejavu_attn_block(const kh_predictor* p, kh_sparse_attn* a, fl
   nrm.w = norm_w_dev;
   nrm.inv = norm_ws_dev;
   nrm.eps = eps;
-  int rc = predictor_topk_normed(p, hidden_dev, k, heads_dev, nrm, st);
+  PredL1View v;
+  int rc = predictor_l1_view(p, st, &v);
   if (rc != KH_OK) return rc;
-  rc = attn_launch<1>(a, hidden_dev, 1, nullptr, heads_dev, k, hidden_dev, 1, st, nrm);
+  const int kvrows = 2 * a->kvd();
+  const bool overlap = v.in_dim <= kL1LdsIn && kvrows % kQkvWaves == 0;
+  if (overlap) {
+    // head predictor layer 1 + K/V rows, then layer 2 and the top k, then the Q rows
+    static std::once_flag once;
+    static hipError_t arc = hipSuccess;
+    std::call_once(once, [] {
+      arc = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_pred_kv_kernel<uint16_t>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kL1LdsBytes);
+      if (arc == hipSuccess)
+        arc = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_pred_kv_kernel<float>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kL1LdsBytes);
+    });
+    KH_HIP(arc);
+    const int nl1 = ceil_div(v.hid, kL1Chains);
+    const int nkv = std::max(1, std::min(attn_device_cus() - nl1, kvrows / kQkvWaves));
+    if (v.bf16)
+      hipLaunchKernelGGL(attn_pred_kv_kernel<uint16_t>, dim3(nl1 + nkv), dim3(kL1LdsThreads), kL1LdsBytes,
+                         st, static_cast<const uint16_t*>(v.w1b), v.b1, v.hid, v.hbuf, hidden_dev, a->hidden,
+                         norm_w_dev, norm_ws_dev, eps, a->wkvq, kvrows, a->y, nl1);
+    else
+      hipLaunchKernelGGL(attn_pred_kv_kernel<float>, dim3(nl1 + nkv), dim3(kL1LdsThreads), kL1LdsBytes,
+                         st, static_cast<const float*>(v.w1b), v.b1, v.hid, v.hbuf, hidden_dev, a->hidden,
+                         norm_w_dev, norm_ws_dev, eps, a->wkvq, kvrows, a->y, nl1);
+    KH_LAUNCHED();
+    rc = predictor_l2_topk_from_h(p, k, heads_dev, st);
+  } else {
+    rc = predictor_topk_normed(p, hidden_dev, k, heads_dev, nrm, st);
+  }
+  if (rc != KH_OK) return rc;
+  rc = attn_launch<1>(a, hidden_dev, 1, nullptr, heads_dev, k, hidden_dev, 1, st, nrm, overlap);
   if (rc == KH_OK) a->len_host[0] += 1;
   return rc;
 }

@@ -331,6 +331,18 @@ int predictor_in_dim(const kh_predictor* p);
 int predictor_out_dim(const kh_predictor* p);
 int predictor_topk_normed(const kh_predictor* p, const float* hidden, int k, int32_t* ids,
                           const NormIn& nrm, hipStream_t st);
+// Layer 1 of a single-row call launched by another file's kernel (its weights,
+// and the per-stream buffer that layer 2 reads), then layers 2 and the top k
+// in ascending order from that buffer.
+struct PredL1View {
+  const void* w1b = nullptr;   // [ceil(in/8)][hid][8], BF16 bits when bf16
+  const float* b1 = nullptr;
+  int in_dim = 0, hid = 0;
+  bool bf16 = false;
+  float* hbuf = nullptr;       // [hid] layer-1 outputs of one row
+};
+int predictor_l1_view(const kh_predictor* p, hipStream_t st, PredL1View* v);
+int predictor_l2_topk_from_h(const kh_predictor* p, int k, int32_t* ids, hipStream_t st);
 
 // Workgroup barrier that waits only for LDS traffic.  __syncthreads() on gfx9
 // also waits for every outstanding vector-memory load (vmcnt counts loads and

@@ -23,29 +23,9 @@
 
 #include "common.hpp"
 #include "exact_sum.hpp"
+#include "pred_l1.hpp"
 
 namespace kh {
-
-// ---------------------------------------------------------------- predictor
-// Weight element loaders: BF16 bits (predictors whose weights are BF16 values,
-// stored losslessly in half the bytes) or f32.
-template <typename W> struct Blk8;
-template <> struct Blk8<uint16_t> {
-  using V = uint4;  // 8 bf16
-  static __device__ __forceinline__ void widen(const V& v, float o[8]) {
-    o[0] = bf16_lo(v.x); o[1] = bf16_hi(v.x); o[2] = bf16_lo(v.y); o[3] = bf16_hi(v.y);
-    o[4] = bf16_lo(v.z); o[5] = bf16_hi(v.z); o[6] = bf16_lo(v.w); o[7] = bf16_hi(v.w);
-  }
-  static __device__ __forceinline__ V zero() { return make_uint4(0, 0, 0, 0); }
-};
-template <> struct Blk8<float> {
-  struct V { float4 a, b; };
-  static __device__ __forceinline__ void widen(const V& v, float o[8]) {
-    o[0] = v.a.x; o[1] = v.a.y; o[2] = v.a.z; o[3] = v.a.w;
-    o[4] = v.b.x; o[5] = v.b.y; o[6] = v.b.z; o[7] = v.b.w;
-  }
-  static __device__ __forceinline__ V zero() { return V{make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0)}; }
-};
 
 // Layer 1 (long chains).  A block owns kL1Chains consecutive hidden units.
 // Its kL1Prod producer waves request every weight the block needs -- the
@@ -58,13 +38,7 @@ template <> struct Blk8<float> {
 // stage in step order with one ds_read_b128 per four steps.  The time is then
 // set by the chain itself: one dependent add per step, about 6 cycles on
 // gfx950.  Output h[b][i] = max(sum + b1[i], 0).
-constexpr int kL1Chains = 8;
-constexpr int kL1Stage = 128;     // steps per stage
-constexpr int kL1Prod = 4;        // producer waves
-constexpr int kL1Threads = 64 * (1 + kL1Prod);
-constexpr int kL1Q = (kL1Stage / 8) * kL1Chains / 64;  // weight loads per producer lane per stage
 constexpr int kMaxL1In = 8192;    // x row staged in LDS (16 stages per producer)
-static_assert(kL1Q * 64 == (kL1Stage / 8) * kL1Chains, "stage tiling");
 
 template <typename W, int SPP>
 __global__ __launch_bounds__(kL1Threads) void pred_l1_kernel(
@@ -176,202 +150,15 @@ __global__ __launch_bounds__(kL1Threads) void pred_l1_kernel(
     h[(size_t)b * hid + chain] = fmaxf(__fadd_rn(s, bv), 0.0f);
 }
 
-// Layer 1 for n_in <= kL1LdsIn: the block's products w*x for every step are
-// formed into LDS first (kL1Chains * n_in floats; all weight loads of the
-// block are in flight at once), then the consumer wave runs its chains over
-// them with no further barrier, reading 32 steps ahead of the adds.  Wave 0
-// is the consumer, kL1Prod waves the producers; kL1Help more waves only
-// stage x and share the RmsNorm sum (two waves per SIMD run its windows).
-constexpr int kL1LdsIn = 4096;
-constexpr int kL1Help = 3;  // waves that only stage x and share the RmsNorm sum
-constexpr int kL1LdsThreads = 64 * (1 + kL1Prod + kL1Help);
-constexpr int kL1LdsBytes = (kL1Chains + 1) * kL1LdsIn * 4;  // products + x
-
-// With norm_w set, x is the un-normalised hidden row and the kernel applies
-// RmsNorm first (model/rms_norm.rs:43-64): the reference's sequential sum of
-// squares (exact_seq_sum over 32 chunks of 128 terms, run by every wave while
-// the weight loads are in flight), its scale, then (x * inv) * norm_w.  Block 0
-// stores the scale in inv_out[b] for the kernels that consume the same
-// normalised row later.  The norm requires n_in % 4 == 0 (host-checked).
-constexpr int kL1EsChunks = 32;
-constexpr int kL1EsM = kL1LdsIn / kL1EsChunks;  // terms per chunk of the exact sum
-using L1Es = EsLds<kL1EsChunks, kL1EsM>;
-static_assert(sizeof(L1Es) <= sizeof(float4) * (kL1LdsIn / 4) * kL1Chains,
-              "the exact-sum scratch fits in the products region");
-
+// Layer 1 for n_in <= kL1LdsIn (pred_l1.hpp), one block per kL1Chains hidden
+// units of row blockIdx.y.
 template <typename W>
 __global__ __launch_bounds__(kL1LdsThreads) void pred_l1_lds_kernel(
     const W* __restrict__ Wb, const float* __restrict__ bias, const float* __restrict__ x,
     int n_in, int hid, float* __restrict__ h, const float* __restrict__ norm_w,
     float* __restrict__ inv_out, float eps) {
-  using B8 = Blk8<W>;
-  using V = typename B8::V;
-  constexpr int SPP = kL1LdsIn / kL1Stage / kL1Prod;  // stages per producer
   extern __shared__ float4 lds4[];
-  float4(*P)[kL1Chains] = reinterpret_cast<float4(*)[kL1Chains]>(lds4);  // [n_in/4][chain]
-  float* xs = reinterpret_cast<float*>(lds4 + (kL1LdsIn / 4) * kL1Chains);
-  // until the norm is known the products region holds the exact-sum scratch
-  auto& es = *reinterpret_cast<L1Es*>(lds4);
-  const int b = blockIdx.y;
-  const int c0 = blockIdx.x * kL1Chains;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int nblk = (n_in + 7) >> 3;
-  // Waves are placed on the CU's four SIMDs in turn (wave w on SIMD w % 4), so
-  // the producers are waves 1, 2, 3 and 5 and the helpers 4, 6 and 7: the
-  // consumer (wave 0) shares its SIMD only with a helper, which is idle while
-  // the chain runs.
-  static_assert(kL1Prod == 4 && kL1Help == 3, "wave roles");
-  const int p = wave <= 3 ? wave - 1 : (wave == 5 ? 3 : -1);
-  const float* xr = x + (size_t)b * n_in;
-  const int n4 = n_in >> 2;
-  // Every wave first requests its share of x (and of the norm weights), then
-  // the producers request every weight of the block: the small x loads sit
-  // ahead of the weight stream in the CU's queue, so the norm can start after
-  // one round trip while the weights are still arriving.
-  constexpr int kXs = (kL1LdsIn / 4 + kL1LdsThreads - 1) / kL1LdsThreads;  // float4 of x per thread
-  const bool vec = (n_in & 3) == 0;
-  float4 xv[kXs], wn[kXs];
-  const float bv = wave == 0 ? bias[min(c0 + (lane & (kL1Chains - 1)), hid - 1)] : 0.0f;
-  if (vec) {
-#pragma unroll
-    for (int q = 0; q < kXs; ++q)
-      xv[q] = reinterpret_cast<const float4*>(xr)[min((int)threadIdx.x + q * kL1LdsThreads, n4 - 1)];
-    if (norm_w) {
-#pragma unroll
-      for (int q = 0; q < kXs; ++q)
-        wn[q] = reinterpret_cast<const float4*>(norm_w)[min((int)threadIdx.x + q * kL1LdsThreads, n4 - 1)];
-    }
-  }
-  V pre[SPP][kL1Q];
-  const bool prod = p >= 0;
-  if (prod) {
-    const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
-#pragma unroll
-    for (int i = 0; i < SPP; ++i)
-#pragma unroll
-      for (int q = 0; q < kL1Q; ++q) {
-        const int st = p + kL1Prod * i;
-        const int pr = lane + 64 * q;
-        const int jb = min(st * (kL1Stage / 8) + pr / kL1Chains, nblk - 1);
-        const int ch = min(c0 + pr % kL1Chains, hid - 1);
-        pre[i][q] = wv[(size_t)jb * hid + ch];
-      }
-  }
-  if (vec) {
-    if (norm_w) {
-      // squares as Rust forms them (v * v, rounded) for the sequential sum,
-      // -0.0 past the row (four terms never straddle a chunk of 128)
-#pragma unroll
-      for (int q = 0; q < kXs; ++q) {
-        const int i4 = threadIdx.x + q * kL1LdsThreads;
-        if (i4 < kL1LdsIn / 4)
-          *reinterpret_cast<float4*>(&es.TP[es_slot<kL1EsChunks, kL1EsM>(4 * i4)]) =
-              i4 < n4 ? make_float4(__fmul_rn(xv[q].x, xv[q].x), __fmul_rn(xv[q].y, xv[q].y),
-                                    __fmul_rn(xv[q].z, xv[q].z), __fmul_rn(xv[q].w, xv[q].w))
-                      : make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < kXs; ++q)  // clamped, unconditional (see stage_f4)
-        reinterpret_cast<float4*>(xs)[min((int)threadIdx.x + q * kL1LdsThreads, n4 - 1)] = xv[q];
-    }
-  } else {
-    for (int j = threadIdx.x; j < n_in; j += kL1LdsThreads) xs[j] = xr[j];
-  }
-  lds_barrier();
-  if (norm_w) {
-    // sum_sq over the row in the reference's order (rms_norm.rs:48-51)
-    const float ss = exact_seq_sum<kL1LdsThreads / 64, kL1EsChunks, kL1EsM>(n_in, 0.0f, es);
-    const float inv = rms_inv_exact(ss, n_in, eps);
-#pragma unroll
-    for (int q = 0; q < kXs; ++q) {
-      float4 v = xv[q];
-      v.x = __fmul_rn(__fmul_rn(v.x, inv), wn[q].x);
-      v.y = __fmul_rn(__fmul_rn(v.y, inv), wn[q].y);
-      v.z = __fmul_rn(__fmul_rn(v.z, inv), wn[q].z);
-      v.w = __fmul_rn(__fmul_rn(v.w, inv), wn[q].w);
-      reinterpret_cast<float4*>(xs)[min((int)threadIdx.x + q * kL1LdsThreads, n4 - 1)] = v;  // clamped
-    }
-    if (blockIdx.x == 0 && threadIdx.x == 0) inv_out[b] = inv;
-    lds_barrier();
-  }
-  // products of stage p + kL1Prod*i; loads arrive in issue order, so each
-  // stage waits only for its own weights
-  auto make = [&](int i) {
-    const int st = p + kL1Prod * i;
-#pragma unroll
-    for (int q = 0; q < kL1Q; ++q) {
-      const int pr = lane + 64 * q;
-      const int blk = pr / kL1Chains, ch = pr % kL1Chains;
-      const int j0 = (st * (kL1Stage / 8) + blk) * 8;
-      float w[8];
-      B8::widen(pre[i][q], w);
-      // j0 + 7 < kL1LdsIn for every stage: two aligned float4 reads of x
-      const float4 xa = reinterpret_cast<const float4*>(xs)[j0 / 4];
-      const float4 xb = reinterpret_cast<const float4*>(xs)[j0 / 4 + 1];
-      P[j0 / 4][ch] = make_float4(__fmul_rn(w[0], xa.x), __fmul_rn(w[1], xa.y),
-                                  __fmul_rn(w[2], xa.z), __fmul_rn(w[3], xa.w));
-      P[j0 / 4 + 1][ch] = make_float4(__fmul_rn(w[4], xb.x), __fmul_rn(w[5], xb.y),
-                                      __fmul_rn(w[6], xb.z), __fmul_rn(w[7], xb.w));
-    }
-  };
-  // Consumer chain over steps [j0, j1) (j0 a multiple of 4): a window of kWin
-  // quads is in flight; every kRefill quads are added, then their registers
-  // are refilled with the quads kWin ahead, so the only VALU work per step is
-  // the dependent add (LDS addresses are immediate offsets from one base
-  // pointer).  Refilling in batches keeps the waits for the LDS counter to one
-  // per batch: a read and a wait after every quad cost about 2 cycles per add.
-  // Window reads past j1 are never added (they stay inside the block's LDS).
-  constexpr int kWin = 32;    // quads in flight (128 steps)
-  constexpr int kRefill = 8;  // quads added between refills
-  constexpr int kSup = 64;    // quads per unrolled loop body (256 steps)
-  static_assert(kSup % kWin == 0 && kWin % kRefill == 0, "window layout");
-  static_assert((kL1LdsIn / 4 + kWin) * kL1Chains <= (kL1LdsBytes / 16), "window stays in LDS");
-  const int ln = lane < kL1Chains ? lane : kL1Chains - 1;
-  float s = -0.0f;
-  auto run = [&](int j0, int j1) {
-    const float4* bp = &P[j0 >> 2][ln];
-    float4 r[kWin];
-#pragma unroll
-    for (int q = 0; q < kWin; ++q) r[q] = bp[q * kL1Chains];
-    const int nsup = (j1 - j0) / (4 * kSup);
-    for (int c = 0; c < nsup; ++c) {
-#pragma unroll
-      for (int q = 0; q < kSup; q += kRefill) {
-#pragma unroll
-        for (int u = 0; u < kRefill; ++u) {
-          s = __fadd_rn(s, r[(q + u) % kWin].x);
-          s = __fadd_rn(s, r[(q + u) % kWin].y);
-          s = __fadd_rn(s, r[(q + u) % kWin].z);
-          s = __fadd_rn(s, r[(q + u) % kWin].w);
-        }
-#pragma unroll
-        for (int u = 0; u < kRefill; ++u) r[(q + u) % kWin] = bp[(q + u + kWin) * kL1Chains];
-        // keep the refills here: the scheduler would otherwise sink them to their uses
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      bp += kSup * kL1Chains;
-    }
-    const float* Pf = reinterpret_cast<const float*>(lds4);
-    for (int j = j0 + nsup * 4 * kSup; j < j1; ++j)
-      s = __fadd_rn(s, Pf[((j >> 2) * kL1Chains + ln) * 4 + (j & 3)]);
-  };
-  // The first round of stages (one per producer) is published first, so the
-  // chain starts while the producers form the rest.
-  constexpr int kSeg = kL1Prod * kL1Stage;
-  if (prod) make(0);
-  lds_barrier();
-  if (prod) {
-#pragma unroll
-    for (int i = 1; i < SPP; ++i) make(i);
-  } else if (wave == 0) {
-    run(0, min(n_in, kSeg));
-  }
-  lds_barrier();
-  if (wave > 0) return;
-  if (n_in > kSeg) run(kSeg, n_in);
-  const int chain = c0 + lane;
-  if (lane < kL1Chains && chain < hid) h[(size_t)b * hid + chain] = fmaxf(__fadd_rn(s, bv), 0.0f);
+  pred_l1_lds_body<W>(blockIdx.x, blockIdx.y, Wb, bias, x, n_in, hid, h, norm_w, inv_out, eps, lds4);
 }
 
 // Layer 1 for a batch of rows (BF16 weights, n_in a multiple of
@@ -1400,6 +1187,10 @@ static int set_kernel_attrs() {
 // layer 2 also writes the per-block score key bounds; with tk set, layer 2
 // selects the top k itself when the row fits one wave (tk->done).
 template <typename W>
+static int l2_typed(const kh_predictor* p, const float* hbuf, int64_t batch, float* scores,
+                    hipStream_t st, uint32_t* mm, TopkReq* tk);
+
+template <typename W>
 static int predict_typed(const kh_predictor* p, const float* x, int64_t batch, float* scores,
                          float* hbuf, hipStream_t st, const NormIn& nrm, uint32_t* mm,
                          TopkReq* tk) {
@@ -1438,6 +1229,14 @@ static int predict_typed(const kh_predictor* p, const float* x, int64_t batch, f
     hipLaunchKernelGGL((chain_layer_kernel<0, W>), dim3(ceil_div(p->hid, 64), batch), dim3(64), 0,
                        st, w1, p->b1, x, p->in_dim, p->hid, hbuf);
   KH_LAUNCHED();
+  return l2_typed<W>(p, hbuf, batch, scores, st, mm, tk);
+}
+
+// Layer 2 from the layer-1 outputs in hbuf (see predict_typed).
+template <typename W>
+static int l2_typed(const kh_predictor* p, const float* hbuf, int64_t batch, float* scores,
+                    hipStream_t st, uint32_t* mm, TopkReq* tk) {
+  const W* w2 = static_cast<const W*>(p->w2b);
   if (p->hid <= kMaxL2Hid && tk && p->out_dim <= kL2Threads) {
     hipLaunchKernelGGL((pred_l2_kernel<W, true>), dim3(1, batch), dim3(kL2Threads), 0, st, w2,
                        p->b2, hbuf, p->hid, p->out_dim, scores, nullptr, tk->k, tk->order,
@@ -1689,5 +1488,32 @@ int predictor_topk_normed(const kh_predictor* p, const float* hidden, int k, int
   if (rc != KH_OK || tk.done) return rc;
   return topk_launch(b.sbuf, 1, p->out_dim, k, KH_ORDER_ASCENDING, ids, st, nullptr,
                      bounds_ok(p) ? b.mm : nullptr, l2_blocks(p));
+}
+
+int predictor_l1_view(const kh_predictor* p, hipStream_t st, PredL1View* v) {
+  PredBufs b;
+  int rc = pred_bufs(p, st, 1, 0, false, &b);
+  if (rc != KH_OK) return rc;
+  rc = set_kernel_attrs();
+  if (rc != KH_OK) return rc;
+  v->w1b = p->w1b;
+  v->b1 = p->b1;
+  v->in_dim = p->in_dim;
+  v->hid = p->hid;
+  v->bf16 = p->bf16;
+  v->hbuf = b.hbuf;
+  return KH_OK;
+}
+
+int predictor_l2_topk_from_h(const kh_predictor* p, int k, int32_t* ids, hipStream_t st) {
+  PredBufs b;
+  int rc = pred_bufs(p, st, 1, 0, false, &b);
+  if (rc != KH_OK) return rc;
+  TopkReq tk{k, KH_ORDER_ASCENDING, ids};
+  uint32_t* mm = bounds_ok(p) ? b.mm : nullptr;
+  rc = p->bf16 ? l2_typed<uint16_t>(p, b.hbuf, 1, b.sbuf, st, mm, &tk)
+               : l2_typed<float>(p, b.hbuf, 1, b.sbuf, st, mm, &tk);
+  if (rc != KH_OK || tk.done) return rc;
+  return topk_launch(b.sbuf, 1, p->out_dim, k, KH_ORDER_ASCENDING, ids, st, nullptr, mm, l2_blocks(p));
 }
 }  // namespace kh
