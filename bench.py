@@ -48,6 +48,7 @@ sys.path.insert(0, ROOT)
 METRIC = "sparse FFN tokens/s @7B shape; gathered-weight HBM GB/s vs roofline"
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ffn_fused1_cfg3_traffic.txt")
+ROCPROF_FILE = os.path.join(ROOT, "profiles", "roofline_cfg3_rocprof.txt")
 ALL_LEGS = ["cfg3", "cfg3b16", "cfg2", "cfg4", "cfg4b8", "decoder", "cfg1", "cfg5", "train5", "families"]
 
 
@@ -97,14 +98,55 @@ class Timer:
         return e0.elapsed_time(e1) / n     # ms per run
 
 
-def timed_cpu(fn, seconds, min_reps=3):
-    n, t0 = 0, time.perf_counter()
-    while True:
+CPU_MIN_REPS = 20
+
+
+def cpu_env(core):
+    """Host facts recorded with every CPU timing."""
+    import oracle
+    model, flags = "", []
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and not model:
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = line.split(":", 1)[1].split()
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "allowed_cores": len(os.sched_getaffinity(0)), "core": core,
+            "model": model, "avx2": "avx2" in flags, "fma": "fma" in flags,
+            "compiler": "gcc " + oracle.lib.or_compiler_version().decode(errors="replace"),
+            "build": "gcc -O3 -mavx2 -mfma -ffp-contract=off (oracle/Makefile)"}
+
+
+def timed_cpu(fn, seconds, min_reps=CPU_MIN_REPS):
+    """The CPU baseline protocol: this thread pinned to one host core (the last
+    one it may run on; os.sched_setaffinity(0, ...) pins the calling thread, so
+    the GPU runtime's threads are untouched), two warm-up calls, then at least
+    min_reps timed calls and at least `seconds` of them; returns the median
+    seconds per call, the call count, the elapsed seconds and the stats."""
+    allowed = sorted(os.sched_getaffinity(0))
+    core = allowed[-1]
+    os.sched_setaffinity(0, {core})
+    try:
         fn()
-        n += 1
+        fn()
+        times = []
+        t0 = time.perf_counter()
+        while len(times) < min_reps or time.perf_counter() - t0 < seconds:
+            a = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - a)
         el = time.perf_counter() - t0
-        if el >= seconds and n >= min_reps:
-            return el / n, n, el
+    finally:
+        os.sched_setaffinity(0, set(allowed))
+    t = np.array(times)
+    stats = {"stat": f"median of {t.size} timed calls after 2 warm-up calls, one pinned host core",
+             "reps": int(t.size), "p10_p90_ms": [round(float(np.percentile(t, 10)) * 1e3, 4),
+                                                  round(float(np.percentile(t, 90)) * 1e3, 4)],
+             "env": cpu_env(core)}
+    return float(np.median(t)), int(t.size), el, stats
 
 
 # --------------------------------------------------------------------------- Deja Vu FFN
@@ -212,12 +254,12 @@ def cpu_ffn(seconds, seed, H, I, R, frac, layers):
     hstate = rng.standard_normal(H).astype(np.float32)
     scratch = np.zeros(H + I + R + k + H + 16, np.float32)
     act = np.zeros(k, np.int64)
-    per, n, el = timed_cpu(lambda: oracle.lib.or_cpu_dejavu_ffn_layer(
+    per, n, el, st = timed_cpu(lambda: oracle.lib.or_cpu_dejavu_ffn_layer(
         wg.reshape(-1), wu.reshape(-1), wd.reshape(-1), wn, 1e-5, pw1.reshape(-1), pb1, pw2.reshape(-1), pb2,
         R, H, I, k, hstate, scratch, act), seconds)
     return dict(value=round(1.0 / (layers * per), 4), unit="tokens/s", cores=1, kind="port",
                 sample=f"{n} token-layers of one layer at this shape (f32 weights as the reference holds "
-                       f"them) in {el:.1f}s, 1 thread; tokens/s = 1/({layers} x {per * 1e3:.2f} ms)")
+                       f"them) in {el:.1f}s, 1 thread; tokens/s = 1/({layers} x {per * 1e3:.2f} ms median)", **st)
 
 
 # --------------------------------------------------------------------------- attention (cfg4)
@@ -379,13 +421,13 @@ def cpu_attention(seconds, seed, layers):
     scratch = np.zeros(2 * H + 2 * nh * d + 2 * nkv * d + nh + R + S + 16, np.float32)
     heads = np.zeros(k, np.int64)
     wn = np.ones(H, np.float32)
-    per, n, el = timed_cpu(lambda: oracle.lib.or_cpu_sparse_attention_layer(
+    per, n, el, st = timed_cpu(lambda: oracle.lib.or_cpu_sparse_attention_layer(
         wq.reshape(-1), wk.reshape(-1), wv.reshape(-1), wo.reshape(-1), wn, 1e-5, p1.reshape(-1), b1,
         p2.reshape(-1), b2, R, H, nh, nkv, d, k, cos_t, sin_t, kc.reshape(-1), vc.reshape(-1), S, pos, hs,
         scratch, heads), seconds)
     return dict(value=round(1.0 / (layers * per), 4), unit="tokens/s", cores=1, kind="port",
                 sample=f"{n} token-layers at context {S} in {el:.1f}s, 1 thread; "
-                       f"tokens/s = 1/({layers} x {per * 1e3:.2f} ms)")
+                       f"tokens/s = 1/({layers} x {per * 1e3:.2f} ms median)", **st)
 
 
 # --------------------------------------------------------------------------- SLIDE (cfg1, cfg5)
@@ -450,10 +492,10 @@ def slide_cfg1_leg(steps, seed, timer, cpu_seconds):
             i[0] += 1
             oracle.lib.or_slide_forward(pl, dim, 6, 50, 128, d32, l32, Wf, b, n, x, 0, 0, 2, 0, oid, opre, oact)
 
-        per, cnt, el = timed_cpu(one, cpu_seconds, 10)
+        per, cnt, el, st = timed_cpu(one, cpu_seconds)
         res["cpu"] = dict(value=round(1.0 / per, 2), unit="samples/s", cores=1, kind="port",
                           sample=f"{cnt} samples of the same batch (Layer::forward: hash, query, union, "
-                                 f"sequential neuron sums) in {el:.1f}s, 1 thread")
+                                 f"sequential neuron sums) in {el:.1f}s, 1 thread", **st)
     del layer
     return res
 
@@ -535,10 +577,10 @@ def slide_cfg5_leg(steps, seed, timer, cpu_seconds):
                 hcpu[j] = max(oracle.lib.or_neuron_forward_sparse(W1[j], 0.0, r.indices, r.values, r.nnz()), 0.0)
             oracle.lib.or_slide_forward(pl, Hd, 9, 50, 128, d32, l32, W2f, b2, n, hcpu, 0, 0, 2, 3, oid, opre, oact)
 
-        per, cnt, el = timed_cpu(one, cpu_seconds, 5)
+        per, cnt, el, st = timed_cpu(one, cpu_seconds)
         res["cpu"] = dict(value=round(1.0 / per, 2), unit="samples/s", cores=1, kind="port",
                           sample=f"{cnt} samples (sparse hidden layer + Layer::forward with softmax over the "
-                                 f"union, index downloaded from the GPU) in {el:.1f}s, 1 thread")
+                                 f"union, index downloaded from the GPU) in {el:.1f}s, 1 thread", **st)
     del out, hidden
     torch.cuda.empty_cache()
     return res
@@ -620,10 +662,11 @@ def slide_train5_leg(steps, seed, cpu_seconds):
             onet.train_step(x[None, :], [labels[i[0] % B]], 0.001)
             i[0] += 1
 
-        per, cnt_, el = timed_cpu(one, cpu_seconds, 2)
+        per, cnt_, el, st = timed_cpu(one, cpu_seconds)
         res["cpu"] = dict(value=round(1.0 / per, 3), unit="samples/s", cores=1, kind="port",
                           sample=f"{cnt_} examples of Network::train_step (one example per call, no index "
-                                 f"rebuild) from the same untrained state in {el:.1f}s, 1 thread")
+                                 f"rebuild), continuing from the untrained state, in {el:.1f}s, 1 thread",
+                          **st)
         del onet
     del net, hid, out
     torch.cuda.empty_cache()
@@ -660,24 +703,15 @@ def families_leg(steps, seed, timer, cpu_seconds):
         out[name] = dict(unit="samples/s", value=round(B * 1000.0 / ms, 1), ms_per_batch=round(ms, 4))
         if cpu_seconds > 0:
             import oracle
-            tabs = fam.tables()
-            i = [0]
-
-            def one(name=name, tabs=tabs):
-                x = X[i[0] % B]
-                i[0] += 1
-                if name == "minhash":
-                    nz = np.nonzero(x)[0].astype(np.uint32)
-                    for t in range(L):
-                        oracle.lib.or_minhash_hash(tabs.reshape(-1), dim, k, t, nz, nz.size)
-                else:
-                    for t in range(L):
-                        oracle.lib.or_wta_hash_dense(tabs.reshape(-1), k, 8, t, x)
-
-            per, cnt, el = timed_cpu(one, min(cpu_seconds, 3.0), 10)
-            out[name]["cpu"] = dict(value=round(1.0 / per, 1), unit="samples/s", cores=1, kind="port",
-                                    sample=f"{cnt} rows x 50 tables through the oracle's C hash in {el:.1f}s "
-                                           f"(ctypes call per table included)")
+            tabs = np.ascontiguousarray(fam.tables(), np.uint32).reshape(-1)
+            kind = 2 if name == "minhash" else 0   # DWTA hashes dense rows as WTA does (dwta.rs:143-152)
+            cds = np.zeros(B * L, np.uint64)
+            per, cnt, el, st = timed_cpu(
+                lambda kind=kind, tabs=tabs: oracle.lib.or_cpu_rank_hash_batch(kind, tabs, dim, k, 8, L, X, B, cds),
+                min(cpu_seconds, 3.0))
+            out[name]["cpu"] = dict(value=round(B / per, 1), unit="samples/s", cores=1, kind="port",
+                                    sample=f"{cnt} calls of the batch ({B} rows x {L} tables, one C call "
+                                           f"each) in {el:.1f}s, 1 thread", **st)
     # bolt over cfg1's layer
     W = rng.normal(0, 0.01, (n, dim)).astype(np.float32)
     b = np.zeros(n, np.float32)
@@ -694,6 +728,22 @@ def families_leg(steps, seed, timer, cpu_seconds):
     ms = timer.time(run_bolt, steps, 3)
     out["bolt_infer"] = dict(unit="samples/s", value=round(B * 1000.0 / ms, 1), ms_per_batch=round(ms, 4),
                              mean_active=float(np.diff(off.cpu().numpy()).mean()))
+    cpu_idx = None
+    if cpu_seconds > 0:
+        import oracle
+        d_, l_, _ = layer.index.buckets()
+        cpu_idx = (np.ascontiguousarray(layer.index.hash_family.planes(), np.int8).reshape(-1),
+                   np.ascontiguousarray(d_.reshape(-1)), np.ascontiguousarray(l_.reshape(-1)))
+        eff = int(np.float32(100) * np.float32(1.5))   # effective_k (sparse_inference.rs:44)
+        n_out = np.zeros(B, np.int64)
+        acts = np.zeros(B * eff, np.float32)
+        per, cnt, el, st = timed_cpu(lambda: oracle.lib.or_cpu_bolt_batch(
+            cpu_idx[0], dim, k, L, 128, cpu_idx[1], cpu_idx[2], W.reshape(-1), b, X, B, eff, 1, n_out, acts),
+            min(cpu_seconds, 3.0))
+        out["bolt_infer"]["cpu"] = dict(value=round(B / per, 1), unit="samples/s", cores=1, kind="port",
+                                        sample=f"{cnt} calls of the batch ({B} rows: hash, query, top {eff} by "
+                                               f"count, dot + bias + ReLU; one C call each) in {el:.1f}s, "
+                                               f"1 thread", **st)
     tk = torch.empty(B, 32, dtype=torch.int32, device="cuda")
     tn = torch.empty(B, dtype=torch.int32, device="cuda")
 
@@ -701,6 +751,16 @@ def families_leg(steps, seed, timer, cpu_seconds):
         _lib.call("kh_lsh_index_query_top_k", layer.index._h, ptr(Xd), B, 32, ptr(tk), ptr(tn), stream_ptr())
     ms = timer.time(run_pred, steps, 3)
     out["lsh_predictor_top32"] = dict(unit="samples/s", value=round(B * 1000.0 / ms, 1), ms_per_batch=round(ms, 4))
+    if cpu_idx is not None:
+        import oracle
+        n_ids = np.zeros(B, np.int64)
+        tids = np.zeros(B * 32, np.uint32)
+        per, cnt, el, st = timed_cpu(lambda: oracle.lib.or_cpu_lsh_topk_batch(
+            cpu_idx[0], dim, k, L, 128, cpu_idx[1], cpu_idx[2], X, B, 32, n_ids, tids), min(cpu_seconds, 3.0))
+        out["lsh_predictor_top32"]["cpu"] = dict(value=round(B / per, 1), unit="samples/s", cores=1, kind="port",
+                                                 sample=f"{cnt} calls of the batch ({B} rows: hash, query with "
+                                                        f"counts, top 32 by count; one C call each) in "
+                                                        f"{el:.1f}s, 1 thread", **st)
     del layer
     # LibSVM: cfg5-shaped lines (5 labels of 670091, 50-100 features of 135909)
     lines = []
@@ -756,6 +816,65 @@ def traffic_probe(seed):
     torch.cuda.synchronize()
     print(json.dumps({"calibration_kernel": "mul (256 MiB f32 in, 256 MiB out)", "calibration_bytes": 256 << 20,
                       "ffn_calls": L, "algorithmic_bytes_per_call": 3 * k * H * 2}), flush=True)
+
+
+def achievable_bandwidth(timer, burst_bytes, bursts=32, stream_bytes=2 << 30):
+    """The HBM read bandwidth this box delivers, measured in this run with
+    stream_read_kernel (measure.hip): (a) `bursts` reads of distinct
+    burst_bytes buffers back to back in one graph -- one FFN call's gathered
+    bytes per launch, each buffer cold as each layer's weights are -- and (b)
+    one read of a stream_bytes buffer."""
+    import torch
+    from klearu_amd import _lib
+    from klearu_amd._dev import ptr, stream_ptr
+
+    def blocks(nbytes):
+        return int(min(8192, max(1, -(-nbytes // (16 * 256 * 8)))))
+
+    nb = burst_bytes // 16 * 16
+    bufs = [torch.ones(nb, dtype=torch.uint8, device="cuda") for _ in range(bursts)]
+    sink = torch.zeros(8192, dtype=torch.int32, device="cuda")
+
+    def burst():
+        st = stream_ptr()
+        for b in bufs:
+            _lib.call("kh_stream_read", ptr(b), nb, ptr(sink), blocks(nb), st)
+
+    g = timer.graph(burst)
+    ms = timer.time(g.replay, 10, 2)
+    del g, bufs
+    big = torch.ones(stream_bytes, dtype=torch.uint8, device="cuda")
+    ms2 = timer.time(lambda: _lib.call("kh_stream_read", ptr(big), stream_bytes, ptr(sink), blocks(stream_bytes),
+                                       stream_ptr()), 10, 2)
+    del big
+    torch.cuda.empty_cache()
+    return {"burst_bytes": nb, "bursts": bursts, "burst_us": round(ms * 1e3 / bursts, 3),
+            "burst_gbs": round(bursts * nb / (ms * 1e-3) / 1e9, 1), "stream_bytes": stream_bytes,
+            "stream_gbs": round(stream_bytes / (ms2 * 1e-3) / 1e9, 1),
+            "kernel": "stream_read_kernel (measure.hip): 16-byte loads, 8 in flight per thread; HIP events "
+                      "around graph replays (bursts) and back-to-back launches (stream)"}
+
+
+def read_rocprof_roofline(bytes_per_call):
+    """The FFN pair's kernel averages from the committed rocprofv3 summary of
+    `bench.py --only cfg3` (profiles/roofline_cfg3_rocprof.txt), and the
+    fraction of peak they give.  Under the profiler every dispatch waits for
+    the one before it, so these durations exceed the in-graph time per call."""
+    kern = {}
+    try:
+        for line in open(ROCPROF_FILE):
+            if " avg_us:" in line:
+                k, v = line.split(" avg_us:", 1)
+                kern[k.strip()] = float(v.split()[0])
+    except OSError:
+        return None
+    if not kern:
+        return None
+    us = sum(kern.values())
+    gbs = bytes_per_call / (us * 1e-6) / 1e9
+    return {"kernels_avg_us": kern, "pair_us": round(us, 3), "achieved": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "source": "profiles/roofline_cfg3_rocprof.txt (rocprofv3 --kernel-trace --stats; not this run)"}
 
 
 def read_traffic():
@@ -840,6 +959,9 @@ def main():
         log(f"[bench] cfg3b16 step {r16['ms_step']:.3f} ms  ffn {r16['ffn_gbs']:.0f} GB/s |U|={r16['mean_rows']:.0f}")
     del model
     torch.cuda.empty_cache()
+    achievable = achievable_bandwidth(timer, int(r["bytes_per_call"]), args.layers)
+    log(f"[bench] achievable read: {achievable['burst_gbs']:.0f} GB/s in {achievable['burst_bytes'] / 1e6:.1f} MB "
+        f"bursts, {achievable['stream_gbs']:.0f} GB/s streaming {achievable['stream_bytes'] >> 20} MiB")
     if "cfg2" in legs:
         r2 = ffn_leg("cfg2", 22, 2048, 5632, 128, 0.10, 1, min(args.steps, 30), 3, args.seed + 2, None, timer)
         extra["cfg2"] = dict(workload="cfg2: Deja Vu sparse SwiGLU FFN decode, 1.1B shape (H2048, I5632, 22 layers, "
@@ -885,6 +1007,14 @@ def main():
     if "train5" in legs:
         extra["train5"] = slide_train5_leg(min(args.steps, 5), args.seed, leg_cpu)
         log(f"[bench] train5 {extra['train5']['ms_per_step']:.3f} ms per batch of 256")
+    # each leg's HBM rate also as a fraction of this run's measured read bandwidth
+    def add_achievable(d):
+        for key in ("hbm_gbs", "ffn_hbm_gbs"):
+            if isinstance(d.get(key), (int, float)):
+                d["frac_of_achievable"] = round(d[key] / achievable["burst_gbs"], 4)
+                return
+    for v in extra.values():
+        add_achievable(v)
     per_call_ms = r["ms_ffn"] / args.layers
     traffic = read_traffic()
     out = {
@@ -908,7 +1038,12 @@ def main():
                      "hbm_gbs": round(r["ffn_gbs"], 1)},
         "step_hbm_gbs": round(r["step_gbs"], 1),
         "roofline": {"bound": "hbm", "achieved": round(r["ffn_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(r["ffn_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "frac": round(r["ffn_gbs"] / HBM_PEAK_GBS, 4),
+                     "achievable": achievable,
+                     "frac_of_achievable": round(r["ffn_gbs"] / achievable["burst_gbs"], 4),
+                     "frac_of_stream": round(r["ffn_gbs"] / achievable["stream_gbs"], 4),
+                     "rocprof": read_rocprof_roofline(r["bytes_per_call"]),
+                     "traffic": traffic,
                      "traffic_source": "profiles/ffn_fused1_cfg3_traffic.txt (rocprofv3 --pmc FETCH_SIZE and "
                                        "WRITE_SIZE, scaled by a copy kernel; not this run)",
                      "kernel": "kh_sparse_ffn_forward (ffn_fused1_kernel + partials_reduce16_kernel)",

@@ -757,6 +757,16 @@ int kh_predictor_dims(const kh_predictor* p, int* input_dim, int* hidden_dim, in
 int kh_predictor_weights(const kh_predictor* p, float* w1_host, float* b1_host, float* w2_host,
                          float* b2_host);
 
+/* ======================================================================== */
+/* Measurement helper (no counterpart in the reference)                     */
+/* ======================================================================== */
+
+/* Reads `bytes` (a positive multiple of 16) of src_dev with 16-byte loads
+ * from `blocks` blocks of 256 threads: the achievable HBM read bandwidth that
+ * bench.py reports next to each roofline fraction.  sink_dev ([blocks]
+ * uint32) is written only to keep the loads alive (in practice never). */
+int kh_stream_read(const void* src_dev, int64_t bytes, uint32_t* sink_dev, int blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -124,6 +124,7 @@ SIGS = {
     "kh_predictor_create": (I, [I, I, I, P, P, P, P, PP]),
     "kh_predictor_destroy": (I, [P]),
     "kh_predictor_status": (I, [P]),
+    "kh_stream_read": (I, [P, I64, P, I, P]),
     "kh_predictor_set_spin_limit": (I, [P, I]),
     "kh_predictor_predict": (I, [P, P, I64, P, P]),
     "kh_predictor_select_top_k": (I, [P, P, I64, I, I, P, P]),

@@ -126,6 +126,13 @@ _sig("or_compute_loss_gradient", None, _f32p, _u32p, _i64, _u32p, _i64, _i64, _f
 _sig("or_layer_backward", None, _f32p, _f32p, _int, _int, _int, _f32p, _u32p, _i64, _f32p, _f32p, _f32p,
      _i64, _int, _f, _f, _f, _f, _f32p, _f32p, _f32p, _f32p, C.c_double, C.c_uint64, C.c_void_p)
 
+_sig("or_compiler_version", C.c_char_p)
+_sig("or_cpu_rank_hash_batch", None, _int, _u32p, _int, _int, _int, _int, _f32p, _i64, _u64p)
+_sig("or_cpu_bolt_batch", _i64, _i8p, _int, _int, _int, _int, _u32p, _u32p, _f32p, _f32p, _f32p, _i64, _int,
+     _int, _i64p, _f32p)
+_sig("or_cpu_lsh_topk_batch", None, _i8p, _int, _int, _int, _int, _u32p, _u32p, _f32p, _i64, _int, _i64p,
+     _u32p)
+
 ACT = {"relu": 0, "sigmoid": 1, "tanh": 2, "softmax": 3, "identity": 4}
 FIFO, RESERVOIR = 0, 1
 

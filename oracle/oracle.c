@@ -1429,3 +1429,91 @@ void or_layer_backward(float* W, float* bias, int dim, int n, int act, const flo
   free(gw);
   free(lg);
 }
+
+/* ======================================================================== */
+/* CPU baseline drivers (bench.py's cpu legs).  One call runs a whole batch, */
+/* so a timed call holds no per-row interpreter overhead.  Each is a loop   */
+/* over the pinned functions above; tests/test_oracle_families.py checks    */
+/* them against those functions row by row.                                 */
+/* ======================================================================== */
+
+/* The compiler that built this library (recorded with the CPU timings). */
+const char* or_compiler_version(void) { return __VERSION__; }
+
+/* codes[r*num_tables + t] for rows X[rows][dim]: kind 0 WTA / DWTA on dense
+ * rows (dwta.rs:143-152 hashes a dense row as WTA does, wta.rs:83-118), kind 2
+ * MinHash over the row's nonzero dimensions (minhash.rs:55-103). */
+void or_cpu_rank_hash_batch(int kind, const uint32_t* tabs, int dim, int k, int ws, int num_tables,
+                            const float* X, int64_t rows, uint64_t* codes) {
+  uint32_t* nz = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(dim > 0 ? dim : 1));
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* x = X + r * dim;
+    if (kind == 2) {
+      int64_t m = 0;
+      for (int d = 0; d < dim; ++d)
+        if (x[d] != 0.0f) nz[m++] = (uint32_t)d;
+      for (int t = 0; t < num_tables; ++t) codes[r * num_tables + t] = or_minhash_hash(tabs, dim, k, t, nz, m);
+    } else {
+      for (int t = 0; t < num_tables; ++t) codes[r * num_tables + t] = or_wta_hash_dense(tabs, k, ws, t, x);
+    }
+  }
+  free(nz);
+}
+
+/* SparseInferenceEngine::infer over rows (klearu-bolt/src/sparse_inference.rs:36-74):
+ * hash, query, the top_k candidates by (count desc, id asc), dot + bias
+ * (+ ReLU when relu); no fallback to all neurons.  Returns the total number of
+ * outputs; out_n[r] holds each row's count, out_act the activations row after
+ * row (room for rows * top_k). */
+int64_t or_cpu_bolt_batch(const int8_t* planes, int dim, int k, int num_tables, int cap,
+                          const uint32_t* data, const uint32_t* len, const float* W, const float* bias,
+                          const float* X, int64_t rows, int top_k, int relu, int64_t* out_n,
+                          float* out_act) {
+  uint32_t* codes = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)num_tables);
+  const int64_t m = (int64_t)num_tables * cap + 1;
+  uint32_t* ids = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)m);
+  uint32_t* cnt = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)m);
+  uint32_t* sel = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)m);
+  int64_t tot = 0;
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* x = X + r * dim;
+    or_hash_dense_batch(planes, dim, k, num_tables, x, 1, codes);
+    const int64_t u = or_lsh_query(num_tables, k, cap, data, len, codes, ids, cnt);
+    const int64_t a = or_sample_topk(ids, cnt, u, top_k, sel);
+    for (int64_t i = 0; i < a; ++i) {
+      const float z = or_neuron_forward(W + (int64_t)sel[i] * dim, bias[sel[i]], x, dim);
+      out_act[tot + i] = relu ? (z > 0.0f ? z : 0.0f) : z;
+    }
+    out_n[r] = a;
+    tot += a;
+  }
+  free(codes);
+  free(ids);
+  free(cnt);
+  free(sel);
+  return tot;
+}
+
+/* LshSparsityPredictor::predict over rows (klearu-dejavu/src/predictor/lsh_predictor.rs:15-43):
+ * hash, query with counts, the top_k ids by (count desc, id asc), written to
+ * out_ids[r*top_k ...] with out_n[r] of them. */
+void or_cpu_lsh_topk_batch(const int8_t* planes, int dim, int k, int num_tables, int cap,
+                           const uint32_t* data, const uint32_t* len, const float* X, int64_t rows,
+                           int top_k, int64_t* out_n, uint32_t* out_ids) {
+  uint32_t* codes = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)num_tables);
+  const int64_t m = (int64_t)num_tables * cap + 1;
+  uint32_t* ids = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)m);
+  uint32_t* cnt = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)m);
+  uint32_t* sel = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)m);
+  for (int64_t r = 0; r < rows; ++r) {
+    or_hash_dense_batch(planes, dim, k, num_tables, X + r * dim, 1, codes);
+    const int64_t u = or_lsh_query(num_tables, k, cap, data, len, codes, ids, cnt);
+    const int64_t a = or_sample_topk(ids, cnt, u, top_k, sel);
+    for (int64_t i = 0; i < a; ++i) out_ids[r * top_k + i] = sel[i];
+    out_n[r] = a;
+  }
+  free(codes);
+  free(ids);
+  free(cnt);
+  free(sel);
+}

@@ -201,7 +201,20 @@ void or_dejavu_sparse_attention_forward(const float* wq, const float* bq, const 
                                         int num_heads, int head_dim, const float* x,
                                         const int64_t* heads, int64_t n_heads, float* y);
 
+/* ---- CPU baseline drivers (bench.py): loops over the functions above ---- */
+const char* or_compiler_version(void);
+void or_cpu_rank_hash_batch(int kind, const uint32_t* tabs, int dim, int k, int ws, int num_tables,
+                            const float* X, int64_t rows, uint64_t* codes);
+int64_t or_cpu_bolt_batch(const int8_t* planes, int dim, int k, int num_tables, int cap,
+                          const uint32_t* data, const uint32_t* len, const float* W, const float* bias,
+                          const float* X, int64_t rows, int top_k, int relu, int64_t* out_n,
+                          float* out_act);
+void or_cpu_lsh_topk_batch(const int8_t* planes, int dim, int k, int num_tables, int cap,
+                           const uint32_t* data, const uint32_t* len, const float* X, int64_t rows,
+                           int top_k, int64_t* out_n, uint32_t* out_ids);
+
 #ifdef __cplusplus
 }
 #endif
 #endif
+

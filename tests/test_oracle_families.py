@@ -156,3 +156,52 @@ def test_minhash_closed_form():
     h = orc.minhash_hash(p10, 4, 0, [9])
     want = (9 + 9 * P + 9 * P * P + 9 * P ** 3) % (1 << 64) & 15
     assert h == want
+
+
+def test_cpu_baseline_drivers_match_the_pinned_functions():
+    """bench.py's CPU legs time one batch call each (or_cpu_rank_hash_batch,
+    or_cpu_bolt_batch, or_cpu_lsh_topk_batch); each must compute exactly what
+    the pinned per-row functions give: WTA / MinHash codes, bolt's top
+    candidates by (count desc, id asc) with dot + bias + ReLU and no fallback
+    (sparse_inference.rs:36-74), and the LSH predictor's top ids
+    (lsh_predictor.rs:15-43)."""
+    rng = np.random.default_rng(21)
+    dim, k, L, ws, B = 96, 4, 7, 8, 9
+    X = (rng.uniform(0, 1, (B, dim)) * (rng.random((B, dim)) < 0.4)).astype(F)
+    X[0] = 0.0
+    win = orc.wta_windows(dim, k, L, ws, 3)
+    got = np.zeros(B * L, np.uint64)
+    orc.lib.or_cpu_rank_hash_batch(0, np.ascontiguousarray(win, np.uint32).reshape(-1), dim, k, ws, L, X, B, got)
+    want = [orc.wta_hash_dense(win, x, t) for x in X for t in range(L)]
+    np.testing.assert_array_equal(got, np.array(want, np.uint64))
+    perms = orc.minhash_perms(dim, L, 4)
+    orc.lib.or_cpu_rank_hash_batch(2, np.ascontiguousarray(perms, np.uint32).reshape(-1), dim, k, 0, L, X, B, got)
+    want = [orc.minhash_hash_dense(perms, k, t, x) for x in X for t in range(L)]
+    np.testing.assert_array_equal(got, np.array(want, np.uint64))
+    # a FIFO index over n neurons, then bolt and the predictor's top ids
+    n, cap, topk = 120, 16, 11
+    planes = orc.simhash_planes(dim, k, L, 5)
+    W = rng.normal(0, 0.1, (n, dim)).astype(F)
+    bias = rng.normal(0, 0.1, n).astype(F)
+    idx = orc.LshIndex(L, k, cap, orc.FIFO)
+    idx.insert_many(np.arange(n, dtype=np.uint32), orc.hash_dense_batch(planes, W).reshape(-1))
+    pl = np.ascontiguousarray(planes, np.int8).reshape(-1)
+    n_out = np.zeros(B, np.int64)
+    act = np.zeros(B * topk, F)
+    tot = orc.lib.or_cpu_bolt_batch(pl, dim, k, L, cap, idx.data, idx.len, W.reshape(-1), bias, X, B, topk, 1,
+                                    n_out, act)
+    ids = np.zeros(B * topk, np.uint32)
+    n_ids = np.zeros(B, np.int64)
+    orc.lib.or_cpu_lsh_topk_batch(pl, dim, k, L, cap, idx.data, idx.len, X, B, topk, n_ids, ids)
+    pos = 0
+    for r, x in enumerate(X):
+        rid, rc = idx.query(orc.hash_dense_batch(planes, x[None]))
+        sel = [i for i, _ in sorted(zip(rid.tolist(), rc.tolist()), key=lambda t: (-t[1], t[0]))[:topk]]
+        assert n_out[r] == len(sel) and n_ids[r] == len(sel)
+        assert ids[r * topk: r * topk + len(sel)].tolist() == sel
+        for j, i in enumerate(sel):
+            z = orc.neuron_forward(W[i], bias[i], x)
+            assert act[pos + j] == F(max(z, 0.0))
+        pos += len(sel)
+    assert tot == pos
+    assert b"clang" in orc.lib.or_compiler_version() or b"." in orc.lib.or_compiler_version()
