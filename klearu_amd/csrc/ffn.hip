@@ -21,13 +21,20 @@
 //             partials_reduce  adds the partial rows in block order (a kernel
 //                          boundary instead of device-scope fences, which on
 //                          gfx950 write back and invalidate the whole L2).
-//   batch>1:  ffn_gateup   one wave per active neuron, tokens staged in LDS;
-//             gather_rows  (column slice x row group) partials (gather.hpp);
+//   batch>1:  ffn_gateup_lds (hidden a multiple of 256) 32 active neurons per
+//                          block, gate/up rows streamed through LDS with
+//                          contiguous loads, 16x16 tiles on MFMA (x split into
+//                          BF16 hi/lo); otherwise ffn_gateup, one wave per
+//                          active neuron, tokens staged in LDS;
+//             down_lds (hidden a multiple of 512; gather.hpp) row groups x
+//                          512-column slices, rows streamed through LDS, f32
+//                          MFMA; otherwise down_mfma / down_rows / gather_rows;
 //             partials_reduce  as above.
 // No float atomics: the summation order is fixed, so outputs are deterministic.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "exact_sum.hpp"
 #include "gather.hpp"
@@ -117,97 +124,147 @@ __global__ __launch_bounds__(64 * kGuWaves) void ffn_gateup_kernel(
 }
 
 // ---------------------------------------------------------------- batched gate/up on MFMA
-// Tokens 2..16 share the active rows: G[n][t] = sum_k W[n][k] x[t][k] is a
-// 16-row x 16-token tile product per wave on v_mfma_f32_16x16x32_bf16, with
-// the BF16 weight rows as they are stored and x split into two BF16 terms
-// (x = hi + lo + r, |r| <= 2^-17 |x|), so the products are those of f32 x
-// to well within the BF16-weight tolerance and accumulate in f32.
-// Lane (r = lane % 16, kb = lane / 16) holds row r and, in each 64-wide
-// k-step s, k = 64 s + 32 e + 8 kb + [0, 8) for the two MFMAs e = 0, 1.  Both
-// operands use this k order, so every k is summed once, and each load
-// instruction reads 64 contiguous bytes of each of the 16 rows.  Four waves
-// split k in quarters for each 16 rows (more loads in flight, twice the
-// blocks); the first adds the others' accumulators through LDS in a fixed
-// order, so results are deterministic.
-__global__ __launch_bounds__(64 * kMfWaves) void ffn_gateup_mfma_kernel(
+// Batched gate/up (2..16 tokens) with contiguous weight loads.  A block owns
+// kGlRows active neurons (two 16-row MFMA tiles) and streams their gate and
+// up rows through LDS in chunks of kGlK columns: every load instruction reads
+// 512 contiguous bytes of one row (half a wave per row piece), where loading
+// the MFMA operands straight from HBM reads 64 bytes from each of 16 rows per
+// instruction.  Wave w then takes k-step w (32 columns) of each chunk for
+// both tiles: A from LDS (lane (r, kb) reads row 16t + r, columns 8kb..8kb+7
+// of its k-step), B = x of token r split into BF16 hi/lo terms (as in
+// ffn_gateup_mfma_kernel), f32 accumulators.  The next chunk's loads are in
+// flight while the current one is multiplied (two LDS buffers, one barrier
+// per chunk).  The eight waves' k-partial sums are added in wave order
+// through LDS at the end, so the result is deterministic.
+constexpr int kGlRows = 32;
+constexpr int kGlK = 256;
+constexpr int kGlWaves = 8;
+constexpr int kGlRowQ = kGlK / 8 + 1;                // uint4 per LDS row (one of padding)
+constexpr int kGlBuf = 2 * kGlRows * kGlRowQ;        // uint4 per buffer: gate rows, then up rows
+constexpr int kGlLds = 2 * kGlBuf * 16;              // two buffers
+constexpr int kGlSteps = kGlK / 32 / kGlWaves;     // k-steps of each chunk per wave
+constexpr int kGlPer = 2 * kGlRows * (kGlK / 8) / 64 / kGlWaves;  // load instructions per wave per chunk
+static_assert(kGlSteps >= 1 && kGlK / 8 <= 64 && 64 % (kGlK / 8) == 0, "chunk layout");
+static_assert(kGlWaves * 2 * 4 * 64 * 16 <= kGlLds, "the final reduction fits in the buffers");
+
+__global__ __launch_bounds__(64 * kGlWaves) void ffn_gateup_lds_kernel(
     const uint16_t* __restrict__ Wgu, const float* __restrict__ x, int batch, int H,
-    const int32_t* __restrict__ active,
-    int n_active, const int32_t* __restrict__ n_active_dev, int inter, int* __restrict__ err,
-    float* __restrict__ hbuf, int hstride) {
-  constexpr int kGroups = kMfWaves / kMfSplit;
-  __shared__ kh_f32x4 part[kGroups][kMfSplit - 1][4][64];
-  __shared__ uint64_t s_tab[32];  // kExp2Tab, for silu after the tile sums
-  const uint64_t tabv = kExp2Tab[threadIdx.x & 31];  // requested before the weights
+    const int32_t* __restrict__ active, int n_active, const int32_t* __restrict__ n_active_dev,
+    int inter, int* __restrict__ err, float* __restrict__ hbuf, int hstride) {
+  extern __shared__ uint4 gl[];                       // [2][2 * kGlRows][kGlRowQ]
+  __shared__ uint64_t s_tab[32];                      // kExp2Tab, for silu after the sums
+  const uint64_t tabv = kExp2Tab[threadIdx.x & 31];   // requested before the weights
   int n = n_active;
   if (n_active_dev) n = min(n, *n_active_dev);
+  const int base = blockIdx.x * kGlRows;
+  if (base >= n) return;  // whole block idle (uniform)
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int grp = wave / kMfSplit, qtr = wave % kMfSplit;
-  const int base = (blockIdx.x * kGroups + grp) * 16;
-  const bool live = base < n;  // uniform per row group
+  // row pieces this lane loads: of the 2*kGlRows pieces (gate rows, then up
+  // rows), a load instruction covers kPw pieces of kGlK/8 lanes each; lane
+  // reads 16 bytes at column 8*(lane % (kGlK/8))
+  constexpr int kQ = kGlK / 8, kPw = 64 / kQ;
+  const int half = lane / kQ, col = lane % kQ;
+  const uint4* src[kGlPer];
+  int dst[kGlPer];
+#pragma unroll
+  for (int j = 0; j < kGlPer; ++j) {
+    const int piece = (wave * kGlPer + j) * kPw + half;
+    const int gu = piece / kGlRows, row = piece % kGlRows;
+    const int nid = checked_row(active[min(base + row, n - 1)], inter, err);
+    src[j] = reinterpret_cast<const uint4*>(Wgu + ((size_t)nid * 2 + gu) * H) + col;
+    dst[j] = piece * kGlRowQ + col;
+  }
+  const int nch = H / kGlK;
+  uint4 st[kGlPer];
+  auto load = [&](int c) {  // clamped past the last chunk (reread, unused)
+    const int o = min(c, nch - 1) * (kGlK / 8);
+#pragma unroll
+    for (int j = 0; j < kGlPer; ++j) st[j] = ld_stream(src[j] + o);
+  };
+  auto store = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < kGlPer; ++j) gl[b * kGlBuf + dst[j]] = st[j];
+  };
+  // B operand: token r (tokens past the batch re-read the last row, unused),
+  // columns 32 (w*kGlSteps + s) + 8kb .. +8 of each chunk
   const int r = lane & 15, kb = lane >> 4;
-  const int neuron = checked_row(active[min(base + r, max(n, 1) - 1)], inter, err);
-  const int qsteps = H / (64 * kMfSplit);  // k-steps per quarter
-  const int s0 = qtr * qsteps;
-  const uint4* __restrict__ g = reinterpret_cast<const uint4*>(Wgu + (size_t)neuron * 2 * H) + kb + 8 * s0;
-  const uint4* __restrict__ u = g + (H >> 3);
-  // tokens past the batch re-read the last token's row (the same cache lines,
-  // so no extra traffic); their results are never written
-  const int xr = min(r, batch - 1);
-  // x of token r: k-step s, MFMA e reads k = 64 s + 32 e + 8 kb + [0, 8) as two float4
-  const float4* __restrict__ xf = reinterpret_cast<const float4*>(x + (size_t)xr * H) + 2 * kb + 16 * s0;
-  kh_f32x4 cg0 = {0, 0, 0, 0}, cg1 = cg0, cu0 = cg0, cu1 = cg0;
-  if (live) {
-    uint4 bg[kMfDepth][2], bu[kMfDepth][2];
-    float4 bx[kMfDepth][2][2];
-    auto load = [&](int d, int s) {  // clamped, unconditional (past the end: reread, unused)
-      const int o = 8 * min(s, qsteps - 1);
-      bg[d][0] = g[o]; bg[d][1] = g[o + 4];
-      bu[d][0] = u[o]; bu[d][1] = u[o + 4];
-      bx[d][0][0] = xf[2 * o]; bx[d][0][1] = xf[2 * o + 1];
-      bx[d][1][0] = xf[2 * o + 8]; bx[d][1][1] = xf[2 * o + 9];
-    };
+  const float4* __restrict__ xf =
+      reinterpret_cast<const float4*>(x + (size_t)min(r, batch - 1) * H) + (32 * wave * kGlSteps + 8 * kb) / 4;
+  kh_f32x4 acc[2][4];
 #pragma unroll
-    for (int d = 0; d < kMfDepth; ++d) load(d, d);
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) acc[t][a] = kh_f32x4{0, 0, 0, 0};
+  // Issue order per wave: x of chunk c + 1 before the weights of chunk c + 2,
+  // so that waiting for one chunk's x (vector loads complete in order) never
+  // waits for the weights of the chunk after next.
+  load(0);
+  store(0);
+  float4 xn[kGlSteps][2];
+#pragma unroll
+  for (int s = 0; s < kGlSteps; ++s) {
+    xn[s][0] = xf[8 * s];
+    xn[s][1] = xf[8 * s + 1];
+  }
+  load(1);
+  lds_barrier();
+  for (int c = 0; c < nch; ++c) {
+    const uint4* buf = gl + (c & 1) * kGlBuf;
+    float4 xc[kGlSteps][2];
+    const int cn = min(c + 1, nch - 1);  // past the last chunk: reread, unused
+#pragma unroll
+    for (int s = 0; s < kGlSteps; ++s) {
+      xc[s][0] = xn[s][0];
+      xc[s][1] = xn[s][1];
+      xn[s][0] = xf[cn * (kGlK / 4) + 8 * s];
+      xn[s][1] = xf[cn * (kGlK / 4) + 8 * s + 1];
+    }
     __builtin_amdgcn_sched_barrier(0);
-    // qsteps is a multiple of kMfDepth (host-checked): no test inside the
-    // loop, whose branches would make every iteration wait for all loads
-    for (int s = 0; s < qsteps; s += kMfDepth) {
 #pragma unroll
-      for (int d = 0; d < kMfDepth; ++d) {
+    for (int s = 0; s < kGlSteps; ++s) {
+      uint4 xh, xl;
+      split_bf16x8(xc[s][0], xc[s][1], xh, xl);
+      const int q = 4 * (wave * kGlSteps + s) + kb;  // uint4 column of this k-step
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          uint4 xh, xl;
-          split_bf16x8(bx[d][e][0], bx[d][e][1], xh, xl);
-          cg0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bg[d][e]), as_bf16x8(xh), cg0, 0, 0, 0);
-          cg1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bg[d][e]), as_bf16x8(xl), cg1, 0, 0, 0);
-          cu0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bu[d][e]), as_bf16x8(xh), cu0, 0, 0, 0);
-          cu1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bu[d][e]), as_bf16x8(xl), cu1, 0, 0, 0);
-        }
-        load(d, s + d + kMfDepth);
-        // keep the prefetch here: the scheduler would otherwise sink it to its use
-        __builtin_amdgcn_sched_barrier(0);
+      for (int t = 0; t < 2; ++t) {
+        const uint4 ag = buf[(16 * t + r) * kGlRowQ + q];
+        const uint4 au = buf[(kGlRows + 16 * t + r) * kGlRowQ + q];
+        acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ag), as_bf16x8(xh), acc[t][0], 0, 0, 0);
+        acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ag), as_bf16x8(xl), acc[t][1], 0, 0, 0);
+        acc[t][2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(au), as_bf16x8(xh), acc[t][2], 0, 0, 0);
+        acc[t][3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(au), as_bf16x8(xl), acc[t][3], 0, 0, 0);
       }
     }
+    // chunk c + 1 into the other buffer (its last readers passed the previous
+    // barrier), then chunk c + 2's loads go out
+    if (c + 1 < nch) {
+      store((c + 1) & 1);
+      load(c + 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    lds_barrier();
   }
-  // C[n][t]: lane holds rows n = 4 kb + q (q = 0..3) of token t = r
-  if (threadIdx.x < 32) s_tab[threadIdx.x] = tabv;
-  if (qtr > 0) {
-    part[grp][qtr - 1][0][lane] = cg0;
-    part[grp][qtr - 1][1][lane] = cg1;
-    part[grp][qtr - 1][2][lane] = cu0;
-    part[grp][qtr - 1][3][lane] = cu1;
-  }
-  __syncthreads();
-  if (qtr > 0 || !live) return;
-  kh_f32x4 tg = cg0 + cg1, tu = cu0 + cu1;
+  // k-partial sums of the eight waves, added in wave order by waves 0 and 1
+  // (tile t = wave); the buffers are free after the last barrier
+  kh_f32x4* red = reinterpret_cast<kh_f32x4*>(gl);  // [wave][tile][4][64]
 #pragma unroll
-  for (int j = 0; j < kMfSplit - 1; ++j) {
-    tg += part[grp][j][0][lane] + part[grp][j][1][lane];
-    tu += part[grp][j][2][lane] + part[grp][j][3][lane];
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) red[((wave * 2 + t) * 4 + a) * 64 + lane] = acc[t][a];
+  if (threadIdx.x < 32) s_tab[threadIdx.x] = tabv;
+  lds_barrier();
+  if (wave >= 2) return;
+  const int t = wave;
+  kh_f32x4 tg = {0, 0, 0, 0}, tu = tg;
+#pragma unroll
+  for (int w = 0; w < kGlWaves; ++w) {
+    tg += red[((w * 2 + t) * 4 + 0) * 64 + lane] + red[((w * 2 + t) * 4 + 1) * 64 + lane];
+    tu += red[((w * 2 + t) * 4 + 2) * 64 + lane] + red[((w * 2 + t) * 4 + 3) * 64 + lane];
   }
+  // C[row][token]: lane holds rows 4kb + q of tile t for token r
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const int item = base + 4 * kb + q;
+    const int item = base + 16 * t + 4 * kb + q;
     if (r < batch && item < n) hbuf[(size_t)r * hstride + item] = silu_ref_t(tg[q], s_tab) * tu[q];
   }
 }
@@ -588,18 +645,39 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
     set_error("hidden %d too large for %d staged tokens", H, std::min(NB, kGuTok));
     return KH_ERR_UNSUPPORTED;
   }
-  if (NB > 1 && H % (64 * kMfSplit * kMfDepth) == 0) {
-    // several tokens: gate/up as 16 x 16 tile products on MFMA
-    hipLaunchKernelGGL(ffn_gateup_mfma_kernel, dim3(ceil_div(n_active, 16 * (kMfWaves / kMfSplit))),
-                       dim3(64 * kMfWaves), 0, st, f->wgu, x, batch, H, active, n_active,
-                       n_active_dev, f->inter, f->err, hbuf, f->inter);
+  if (NB > 1 && H % kGlK == 0) {
+    // several tokens: gate/up as 16 x 16 tile products on MFMA over rows
+    // staged through LDS with contiguous loads
+    static std::once_flag once;
+    static hipError_t arc = hipSuccess;
+    std::call_once(once, [] {
+      arc = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_gateup_lds_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kGlLds);
+    });
+    KH_HIP(arc);
+    hipLaunchKernelGGL(ffn_gateup_lds_kernel, dim3(ceil_div(n_active, kGlRows)), dim3(64 * kGlWaves), kGlLds,
+                       st, f->wgu, x, batch, H, active, n_active, n_active_dev, f->inter, f->err, hbuf,
+                       f->inter);
   } else {
     hipLaunchKernelGGL(ffn_gateup_kernel<NB>, g1, dim3(64 * kGuWaves), lds1, st, f->wgu, x, batch,
                        H, active, n_active, n_active_dev, f->inter, f->err, hbuf, f->inter);
   }
   KH_LAUNCHED();
   int groups;
-  if (NB > 1 && H % kDmCols == 0) {
+  if (NB > 1 && H % kDlCols == 0) {
+    // several tokens: row groups on the matrix cores (f32 MFMA), weights
+    // staged through LDS with contiguous loads
+    static std::once_flag once;
+    static hipError_t arc = hipSuccess;
+    std::call_once(once, [] {
+      arc = hipFuncSetAttribute(reinterpret_cast<const void*>(&down_lds_kernel<NB>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDlLds);
+    });
+    KH_HIP(arc);
+    groups = ceil_div(n_active, kDlRows);
+    hipLaunchKernelGGL(down_lds_kernel<NB>, dim3(H / kDlCols, groups), dim3(64 * kDlWaves), kDlLds, st,
+                       f->wdt, H, active, n_active, n_active_dev, f->inter, hbuf, f->inter, batch, partial);
+  } else if (NB > 1 && H % kDmCols == 0) {
     // several tokens: 512-row groups on the matrix cores (f32 MFMA)
     static bool dm_attr = false;
     if (!dm_attr) {

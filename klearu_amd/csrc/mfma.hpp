@@ -16,10 +16,6 @@ namespace kh {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 kh_bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float kh_f32x4;
 
-constexpr int kMfSplit = 4;   // waves sharing one 16-row group (k quarters)
-constexpr int kMfWaves = 8;   // 2 row groups of 16 per block
-constexpr int kMfDepth = 4;   // k-steps of loads in flight per wave
-
 __device__ __forceinline__ kh_bf16x8 as_bf16x8(const uint4& v) {
   return __builtin_bit_cast(kh_bf16x8, v);
 }
