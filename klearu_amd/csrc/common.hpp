@@ -331,6 +331,17 @@ int predictor_in_dim(const kh_predictor* p);
 int predictor_out_dim(const kh_predictor* p);
 int predictor_topk_normed(const kh_predictor* p, const float* hidden, int k, int32_t* ids,
                           const NormIn& nrm, hipStream_t st);
+// Layers 1 and 2 of one row into the per-stream score buffer, with layer 2's
+// per-block key bounds, for a consumer kernel that selects the top k itself
+// (rows of more than 64 outputs whose bounds fit; KH_ERR_UNSUPPORTED otherwise,
+// before anything is launched).
+struct PredScores {
+  const float* scores = nullptr;  // [out_dim]
+  const uint32_t* mm = nullptr;   // [nmm] (min key, max key) pairs
+  int n = 0, nmm = 0;
+};
+int predictor_scores_normed(const kh_predictor* p, const float* hidden, const NormIn& nrm,
+                            hipStream_t st, PredScores* out);
 // Layer 1 of a single-row call launched by another file's kernel (its weights,
 // and the per-stream buffer that layer 2 reads), then layers 2 and the top k
 // in ascending order from that buffer.

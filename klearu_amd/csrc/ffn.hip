@@ -39,6 +39,7 @@
 #include "exact_sum.hpp"
 #include "gather.hpp"
 #include "mfma.hpp"
+#include "topk_select.hpp"
 
 namespace kh {
 
@@ -280,18 +281,98 @@ constexpr int kFuWaves = 8;                // neurons (waves) per block; 4 for s
 constexpr int kFuWavesMin = 4;
 constexpr int kFuMaxH = 4096;              // 8 chunks of 16 B per lane per gate/up row
 constexpr int kFuChunks = kFuMaxH / 512;
+constexpr int kFuSelKpt = 22;              // scores per thread of the selecting form (11008 / 512)
+// Dynamic LDS: x [kFuMaxH/4 float4], then h [16 floats] and the block's ids
+// [16 ints], then (selecting form) the staged scores.
+constexpr int kFuStage = kFuMaxH / 4 + 8;  // float4 offset of the staged scores
+constexpr int kFuSelLds = 16 * kFuStage + 4 * kFuSelKpt * 64 * kFuWaves;  // dynamic LDS bound
 
-template <int NW>
+// The ids of ranks [first, first + NW) of the row's top k, in ascending id
+// order (the order of the reference's selection handed to the FFN), chosen by
+// this block from the scores alone: every block runs the same exact selection
+// (topk_select.hpp) over the same scores, so no block waits for another.  The
+// block also writes those ids to active_out.  mm: layer 2's per-block key
+// bounds (nmm <= NT pairs).
+template <int NW, int KPT>
+__device__ __forceinline__ void ffn_select_ids(const float* __restrict__ scores, int n, int k,
+                                               const uint32_t* __restrict__ mm, int nmm, int first,
+                                               float4* smem4, int32_t* s_ids, TopkLds<64 * NW>& sh,
+                                               int32_t* __restrict__ active_out) {
+  constexpr int NT = 64 * NW;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint2 mmv = (int)threadIdx.x < nmm ? reinterpret_cast<const uint2*>(mm)[threadIdx.x]
+                                           : make_uint2(0xffffffffu, 0u);
+  // coalesced loads through LDS, then each thread reads its contiguous range
+  // (n a multiple of 4, host-checked)
+  constexpr int kQ = (KPT + 3) / 4;
+  const float4* __restrict__ s4 = reinterpret_cast<const float4*>(scores);
+  float4 v[kQ];
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) v[q] = s4[min((int)threadIdx.x + q * NT, (n >> 2) - 1)];
+  {
+    const uint32_t a = wave_max_u32(mmv.y), c = wave_min_u32(mmv.x);
+    if (lane == 0) {
+      sh.wmax[wave] = a;
+      sh.wmin[wave] = c;
+    }
+  }
+  float4* stage4 = smem4 + kFuStage;
+#pragma unroll
+  for (int q = 0; q < kQ; ++q)  // clamped, unconditional (see stage_f4)
+    stage4[min((int)threadIdx.x + q * NT, (n >> 2) - 1)] = v[q];
+  for (int i = threadIdx.x; i < (1 << kTopkDigit); i += NT) sh.hist[i] = 0;
+  if (threadIdx.x == 0) sh.s_ncand = 0;
+  lds_barrier();
+  const float* stage = reinterpret_cast<const float*>(stage4);
+  const int kpt = (n + NT - 1) / NT;  // <= KPT (host-checked)
+  const int i0 = threadIdx.x * kpt;
+  const int cnt = max(0, min(kpt, n - i0));
+  uint32_t key[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) key[j] = f32_key(stage[min(i0 + j, n - 1)]);
+  uint32_t mx = 0u, mn = 0xffffffffu;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    mx = max(mx, sh.wmax[w]);
+    mn = min(mn, sh.wmin[w]);
+  }
+  const int kk0 = min(k, n);
+  uint32_t T;
+  int ties;
+  topk_threshold<NT, KPT>(key, cnt, i0, kk0, mx, mn, sh, T, ties);
+  int pos;
+  auto selm = topk_select_mask<NT, KPT>(key, cnt, T, ties, sh, pos);
+  // this thread's selected keys hold ranks pos, pos + 1, ...: keep those in
+  // [first, first + NW)
+  if (pos < first + NW && pos + (int)__popcll((unsigned long long)selm) > first) {
+    int r = pos;
+    while (selm && r < first + NW) {
+      const int j = __ffsll((unsigned long long)selm) - 1;
+      if (r >= first) s_ids[r - first] = i0 + j;
+      ++r;
+      selm &= selm - 1;
+    }
+  }
+  lds_barrier();
+  if ((int)threadIdx.x < NW && first + (int)threadIdx.x < kk0)
+    active_out[first + threadIdx.x] = s_ids[threadIdx.x];
+}
+
+// KPT > 0: the selecting form (ffn_select_ids): active is not read; the block
+// takes ranks [blockIdx.x * NW, ...) of the top n_active of scores[inter].
+template <int NW, int KPT = 0>
 __global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
     const uint16_t* __restrict__ Wgu, const uint16_t* __restrict__ WdT,
     const float* __restrict__ x, int H, const int32_t* __restrict__ active, int n_active,
     const int32_t* __restrict__ n_active_dev, int inter, int* __restrict__ err,
     float* __restrict__ hbuf, float* __restrict__ partial, const float* __restrict__ norm_w,
-    const float* __restrict__ norm_inv) {
+    const float* __restrict__ norm_inv, const float* __restrict__ scores = nullptr,
+    const uint32_t* __restrict__ mm = nullptr, int nmm = 0, int32_t* __restrict__ active_out = nullptr) {
   extern __shared__ float4 smem4[];
   __shared__ uint64_t s_tab[32];                                // kExp2Tab
   float4* xs4 = smem4;                                          // [H/4]
   float* hs = reinterpret_cast<float*>(smem4 + (kFuMaxH >> 2));  // [NW]
+  int32_t* s_ids = reinterpret_cast<int32_t*>(hs + 16);         // [NW]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int first = blockIdx.x * NW;
   // the exp table first (vector loads complete in order, so its store below
@@ -315,8 +396,15 @@ __global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
   for (int q = 0; q < kXq; ++q) wn[q] = nsrc[min((int)threadIdx.x + q * 64 * NW, n4 - 1)];
   const float inv_ld = *(norm_w ? norm_inv : x);  // unconditional scalar load
   int cand[NW];
+  if constexpr (KPT > 0) {
+    __shared__ TopkLds<64 * NW> sh;
+    ffn_select_ids<NW, KPT>(scores, inter, n_active, mm, nmm, first, smem4, s_ids, sh, active_out);
 #pragma unroll
-  for (int k = 0; k < NW; ++k) cand[k] = active[min(first + k, n_active - 1)];
+    for (int k = 0; k < NW; ++k) cand[k] = s_ids[k];  // slots past the count: never used
+  } else {
+#pragma unroll
+    for (int k = 0; k < NW; ++k) cand[k] = active[min(first + k, n_active - 1)];
+  }
   int n = n_active;
   if (n_active_dev) n = min(n, *n_active_dev);
   // A block past the device count still runs (reading row 0, unused) so that
@@ -721,6 +809,25 @@ static bool ffn_fused_ok(const kh_sparse_ffn* f, int64_t batch) {
   return batch == 1 && f->hidden <= kFuMaxH && f->hidden % (8 * kFuWaves) == 0;
 }
 
+// Four neurons per block when the hidden size allows it (a wave's down slice
+// is at most 512 columns) and eight would leave CUs idle: the 1.1B shape
+// (hidden 2048, 564 active) gets 141 blocks instead of 71.
+static int ffn_fused_wave_count(const kh_sparse_ffn* f, int k) {
+  return f->hidden <= 512 * kFuWavesMin && k < 256 * kFuWaves ? kFuWavesMin : kFuWaves;
+}
+// Whether the fused block's FFN selects its own neurons: with 8-wave blocks,
+// when the row's scores fit kFuSelKpt per thread and layer 2's key bounds one
+// slot per thread.  Every block then runs the whole selection (about 7 us at
+// the 7B shape, against 8.4 us for the one-block top-k kernel and its launch);
+// 4-wave blocks would take twice as long per block, which measured slower than
+// the separate top-k at the 1.1B shape.
+static bool ffn_select_ok(const kh_sparse_ffn* f, int k) {
+  const int nw = ffn_fused_wave_count(f, k);
+  const int nt = 64 * nw;
+  return nw == kFuWaves && f->inter > 64 && f->inter % 4 == 0 && f->inter < 65536 &&
+         ceil_div(f->inter, nt) <= kFuSelKpt && ceil_div(f->inter, 64) <= nt;
+}
+
 // Single-token fused FFN + ordered reduce.  With nrm.w set, x is the
 // un-normalised hidden row, normalised in the kernel with the scale at nrm.inv.
 static int ffn_fused_launch(const kh_sparse_ffn* f, const float* x, const int32_t* active,
@@ -730,11 +837,8 @@ static int ffn_fused_launch(const kh_sparse_ffn* f, const float* x, const int32_
   float *hbuf = nullptr, *partial = nullptr;
   int rc = ffn_bufs(f, st, &hbuf, &partial);
   if (rc != KH_OK) return rc;
-  // Four neurons per block when the hidden size allows it (a wave's down
-  // slice is at most 512 columns) and eight would leave CUs idle: the 1.1B
-  // shape (hidden 2048, 564 active) gets 141 blocks instead of 71.
-  const bool small = H <= 512 * kFuWavesMin && n_active < 256 * kFuWaves;
-  const int nw = small ? kFuWavesMin : kFuWaves;
+  const int nw = ffn_fused_wave_count(f, n_active);
+  const bool small = nw == kFuWavesMin;
   const int blocks = ceil_div(n_active, nw);
   const size_t lds = sizeof(float) * ((size_t)kFuMaxH + kFuWaves);
   static std::once_flag once;
@@ -752,6 +856,43 @@ static int ffn_fused_launch(const kh_sparse_ffn* f, const float* x, const int32_
     hipLaunchKernelGGL(ffn_fused1_kernel<kFuWaves>, dim3(blocks), dim3(64 * kFuWaves), lds, st,
                        f->wgu, f->wdt, x, H, active, n_active, n_active_dev, f->inter, f->err, hbuf,
                        partial, nrm.w, nrm.inv);
+  KH_LAUNCHED();
+  partials_reduce_launch(partial, H, blocks, y, accumulate, st);
+  KH_LAUNCHED();
+  return KH_OK;
+}
+
+// The fused block's FFN with its own selection: the top k of the predictor's
+// scores (ps) chosen inside the FFN kernel (ffn_select_ids), written to
+// active_out, then the same FFN and reduce as ffn_fused_launch.
+static int ffn_select_launch(const kh_sparse_ffn* f, const float* x, const PredScores& ps, int k,
+                             int32_t* active_out, float* y, int accumulate, const NormIn& nrm,
+                             hipStream_t st) {
+  const int H = f->hidden;
+  if (ps.n != f->inter || !ffn_select_ok(f, k) || ps.nmm > 64 * ffn_fused_wave_count(f, k)) {
+    set_error("selecting FFN launched outside its limits");
+    return KH_ERR_UNSUPPORTED;
+  }
+  float *hbuf = nullptr, *partial = nullptr;
+  int rc = ffn_bufs(f, st, &hbuf, &partial);
+  if (rc != KH_OK) return rc;
+  const int blocks = ceil_div(k, kFuWaves);
+  const size_t lds = sizeof(float4) * kFuStage + sizeof(float) * (size_t)ps.n;
+  if (lds > (size_t)kFuSelLds) {
+    set_error("selecting FFN: %d scores do not fit its LDS", ps.n);
+    return KH_ERR_UNSUPPORTED;
+  }
+  static std::once_flag once;
+  static hipError_t arc = hipSuccess;
+  // the kernel's static LDS (the selection's histogram) comes on top of this
+  std::call_once(once, [] {
+    arc = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel<kFuWaves, kFuSelKpt>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kFuSelLds);
+  });
+  KH_HIP(arc);
+  hipLaunchKernelGGL((ffn_fused1_kernel<kFuWaves, kFuSelKpt>), dim3(blocks), dim3(64 * kFuWaves), lds, st,
+                     f->wgu, f->wdt, x, H, nullptr, k, nullptr, f->inter, f->err, hbuf, partial, nrm.w,
+                     nrm.inv, ps.scores, ps.mm, ps.nmm, active_out);
   KH_LAUNCHED();
   partials_reduce_launch(partial, H, blocks, y, accumulate, st);
   KH_LAUNCHED();
@@ -848,6 +989,13 @@ extern "C" int kh_dejavu_mlp_block(const kh_predictor* p, const kh_sparse_ffn* f
   nrm.w = norm_w_dev;
   nrm.inv = norm_ws_dev;
   nrm.eps = eps;
+  if (ffn_select_ok(f, k)) {
+    // layers 1 and 2, then the FFN kernel selects its own neurons
+    PredScores ps;
+    int rc = predictor_scores_normed(p, hidden_dev, nrm, st, &ps);
+    if (rc == KH_OK) return ffn_select_launch(f, hidden_dev, ps, k, active_dev, hidden_dev, 1, nrm, st);
+    if (rc != KH_ERR_UNSUPPORTED) return rc;
+  }
   int rc = predictor_topk_normed(p, hidden_dev, k, active_dev, nrm, st);
   if (rc != KH_OK) return rc;
   return ffn_fused_launch(f, hidden_dev, active_dev, k, nullptr, hidden_dev, 1, nrm, st);

@@ -24,6 +24,7 @@
 #include "common.hpp"
 #include "exact_sum.hpp"
 #include "pred_l1.hpp"
+#include "topk_select.hpp"
 
 namespace kh {
 
@@ -533,9 +534,7 @@ __global__ __launch_bounds__(64) void chain_layer_kernel(const W* __restrict__ W
 // ---------------------------------------------------------------- top-k
 constexpr int kTopkThreads = 1024;
 constexpr int kTopkRegMax = kTopkThreads * 64 - 1;  // keys per thread in registers: 16, 32 or 64
-constexpr int kTopkCand = 256;       // boundary bins up to this size are ranked directly
 constexpr int kTopkStage = 32768;    // rows up to this size are loaded through LDS
-constexpr int kTopkDigit = 11;       // radix digit (2048 bins)
 
 // Score-order output: bitonic sort (descending) of the selected (key, ~index)
 // pairs staged in sortbuf, then the indices.
@@ -567,14 +566,9 @@ __device__ void topk_score_order(const uint64_t* __restrict__ src, int kk, int32
 
 // One block per row.  Thread t holds the keys of the contiguous index range
 // [t*kpt, (t+1)*kpt) in registers, so every pass runs from registers and the
-// selected indices come out in ascending order from one exclusive scan.
-//   1. common high bits of all keys (wave/block max and min);
-//   2. radix pass over the next kTopkDigit bits: LDS histogram, block scan
-//      from the top bin down -> the bin holding the k-th key;
-//   3. if that bin holds at most kTopkCand keys, they are gathered and ranked
-//      directly by (key desc, index asc); otherwise radix passes continue;
-//   4. compaction: keys above the k-th key T plus the lowest-index keys equal
-//      to T -- exactly the first k of the reference's stable descending sort.
+// selected indices come out in ascending order from one exclusive scan: the
+// k-th key by topk_threshold (radix passes below the keys' common high bits,
+// then a direct ranking of the boundary bin), then the compaction.
 template <int kTopkPerThread>
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restrict__ scores,
                                                             int n, int k, int order,
@@ -584,13 +578,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
                                                             int nmm,
                                                             uint8_t* __restrict__ marks) {
   extern __shared__ __align__(16) uint64_t sort_lds[];
-  __shared__ unsigned hist[1 << kTopkDigit];
-  __shared__ uint64_t cand[kTopkCand];
-  __shared__ int wsum[kTopkThreads / 64];
-  __shared__ uint32_t uwsum[kTopkThreads / 64];
-  __shared__ uint32_t wmax[kTopkThreads / 64], wmin[kTopkThreads / 64];
-  __shared__ uint32_t s_prefix, s_mask, s_T;
-  __shared__ int s_kk, s_total, s_bincount, s_ncand, s_ties;
+  __shared__ TopkLds<kTopkThreads> sh;
   const int b = blockIdx.x;
   const float* sc = scores + (size_t)b * n;
   const int kk0 = min(k, n);
@@ -610,8 +598,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
     // so waiting for them does not wait for the scores)
     const uint32_t a = wave_max_u32(mmv.y), c = wave_min_u32(mmv.x);
     if (lane == 0) {
-      wmax[wave] = a;
-      wmin[wave] = c;
+      sh.wmax[wave] = a;
+      sh.wmin[wave] = c;
     }
   }
   // Coalesced loads through LDS (a thread's own contiguous range would make
@@ -633,15 +621,13 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
   } else {
     for (int i = threadIdx.x; i < n; i += kTopkThreads) sstage[i] = __float_as_uint(sc[i]);
   }
-  for (int i = threadIdx.x; i < (1 << kTopkDigit); i += kTopkThreads) hist[i] = 0;
-  if (threadIdx.x == 0) s_ncand = 0;
+  for (int i = threadIdx.x; i < (1 << kTopkDigit); i += kTopkThreads) sh.hist[i] = 0;
+  if (threadIdx.x == 0) sh.s_ncand = 0;
   lds_barrier();
   uint32_t key[kTopkPerThread];
 #pragma unroll
   for (int j = 0; j < kTopkPerThread; ++j)
     key[j] = f32_key(staged ? __uint_as_float(sstage[min(i0 + j, n - 1)]) : sc[min(i0 + j, n - 1)]);
-  // 1. bits common to every key: the radix passes start below them (scores
-  // cluster, so a pass over shared high bits would fill one or two bins).
   if (!mm) {
     uint32_t kmax = 0u, kmin = 0xffffffffu;
 #pragma unroll
@@ -653,133 +639,24 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
     kmax = wave_max_u32(kmax);
     kmin = wave_min_u32(kmin);
     if (lane == 0) {
-      wmax[wave] = kmax;
-      wmin[wave] = kmin;
+      sh.wmax[wave] = kmax;
+      sh.wmin[wave] = kmin;
     }
     __syncthreads();
   }
   uint32_t mx = 0u, mn = 0xffffffffu;
 #pragma unroll
   for (int w = 0; w < kTopkThreads / 64; ++w) {
-    mx = max(mx, wmax[w]);
-    mn = min(mn, wmin[w]);
+    mx = max(mx, sh.wmax[w]);
+    mn = min(mn, sh.wmin[w]);
   }
-  const uint32_t diff = mx ^ mn;
-  int hi = diff ? 31 - __clz(diff) : -1;
-  uint32_t mask = hi < 0 ? 0xffffffffu : (hi >= 31 ? 0u : ~((2u << hi) - 1u));
-  uint32_t prefix = mx & mask;
-  int kk = kk0;
-  uint32_t T = prefix;
-  int ties = kk0;
-  bool first = true;
-  while (hi >= 0) {
-    // 2. one radix pass over bits [lo, hi] of the keys matching prefix/mask
-    const int lo = max(0, hi - (kTopkDigit - 1));
-    const int nbins = 2 << (hi - lo);
-    const uint32_t binmask = (uint32_t)nbins - 1u;
-    if (!first) {
-      for (int i = threadIdx.x; i < nbins; i += kTopkThreads) hist[i] = 0;
-      __syncthreads();
-    }
-    first = false;
-#pragma unroll
-    for (int j = 0; j < kTopkPerThread; ++j)
-      if (j < cnt && (key[j] & mask) == prefix) atomicAdd(&hist[(key[j] >> lo) & binmask], 1u);
-    __syncthreads();
-    // Thread t owns bins [nbins-(t+1)*per, nbins-t*per), thread 0 the highest;
-    // the exclusive scan in thread order counts the keys in higher bins.
-    const int per = (nbins + kTopkThreads - 1) / kTopkThreads;
-    const int top = nbins - (int)threadIdx.x * per;
-    const int bot = max(top - per, 0);
-    int local = 0;
-    for (int j = bot; j < top; ++j) local += (int)hist[j];
-    const int above = block_excl_scan(local, wsum, &s_total);
-    if (top > 0 && above < kk && kk <= above + local) {
-      int cum = above, sel = bot;
-      for (int j = top - 1; j >= bot; --j) {
-        if (cum + (int)hist[j] >= kk) {
-          sel = j;
-          break;
-        }
-        cum += (int)hist[j];
-      }
-      s_kk = kk - cum;
-      s_prefix = prefix | ((uint32_t)sel << lo);
-      s_mask = mask | (binmask << lo);
-      s_bincount = (int)hist[sel];
-    }
-    __syncthreads();
-    kk = s_kk;
-    prefix = s_prefix;
-    mask = s_mask;
-    hi = lo - 1;
-    T = prefix;
-    ties = kk;
-    if (hi < 0) break;  // every bit resolved: the bin is one key value
-    if (s_bincount <= kTopkCand) {
-      // 3. rank the boundary bin's keys directly
-#pragma unroll
-      for (int j = 0; j < kTopkPerThread; ++j)
-        if (j < cnt && (key[j] & mask) == prefix) {
-          const int c = atomicAdd(&s_ncand, 1);
-          cand[c] = ((uint64_t)key[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)(i0 + j));
-        }
-      __syncthreads();
-      const int m = s_ncand;
-      // Four threads per candidate: thread t ranks candidate t/4 against a
-      // quarter of the list; the quarters are added across the lane quad.
-      const int ci = (int)threadIdx.x >> 2, part = (int)threadIdx.x & 3;
-      int rank = 0, gt = 0;
-      uint32_t mk = 0u;
-      if (ci < m) {
-        const uint64_t me = cand[ci];
-        mk = (uint32_t)(me >> 32);
-        const int q = (m + 3) >> 2;
-        const int j1 = min(part * q + q, m);
-        for (int j = part * q; j < j1; ++j) {
-          const uint64_t o = cand[j];
-          rank += o > me;
-          gt += (uint32_t)(o >> 32) > mk;
-        }
-      }
-      rank += dpp<kDppQuadSwap1>(rank);
-      rank += dpp<kDppQuadSwap2>(rank);
-      gt += dpp<kDppQuadSwap1>(gt);
-      gt += dpp<kDppQuadSwap2>(gt);
-      if (ci < m && part == 0 && rank == kk - 1) {
-        s_T = mk;
-        s_ties = kk - gt;
-      }
-      __syncthreads();
-      T = s_T;
-      ties = s_ties;
-      break;
-    }
-  }
-  // 4. compaction in ascending index order (one scan of packed counts:
-  // keys > T in the low 16 bits, keys == T in the high 16 bits; n < 65536).
-  // Each thread turns its keys into two bit masks first, so the per-key work
-  // after the scan is one iteration per selected key, not one per key.
-  using M = typename std::conditional<(kTopkPerThread > 32), unsigned long long, uint32_t>::type;
-  auto popc = [](M m) { return (int)__popcll((unsigned long long)m); };
-  auto lowest = [](M m) { return __ffsll((unsigned long long)m) - 1; };
-  auto highest = [](M m) { return 63 - __clzll((unsigned long long)m); };
-  M gtm = 0, eqm = 0;
-#pragma unroll
-  for (int j = 0; j < kTopkPerThread; ++j)
-    if (j < cnt) {
-      gtm |= (M)(key[j] > T) << j;
-      eqm |= (M)(key[j] == T) << j;
-    }
-  const int ceq = popc(eqm);
-  const uint32_t ex = block_excl_scan_u32((uint32_t)popc(gtm) | ((uint32_t)ceq << 16), uwsum);
-  const int gt_before = (int)(ex & 0xffffu), eq_before = (int)(ex >> 16);
-  // keys equal to T are taken in index order until `ties` of them are taken
-  const int take = max(0, min(ceq, ties - eq_before));
-  M em = eqm;
-  for (int t = ceq; t > take; --t) em &= ~((M)1 << highest(em));  // drop the highest
-  M selm = gtm | em;
-  int pos = gt_before + min(eq_before, ties);
+  uint32_t T;
+  int ties;
+  topk_threshold<kTopkThreads, kTopkPerThread>(key, cnt, i0, kk0, mx, mn, sh, T, ties);
+  // compaction in ascending index order: one iteration per selected key
+  int pos;
+  auto selm = topk_select_mask<kTopkThreads, kTopkPerThread>(key, cnt, T, ties, sh, pos);
+  auto lowest = [](unsigned long long m) { return __ffsll(m) - 1; };
   if (order == KH_ORDER_ASCENDING && staged) {
     // ids staged in LDS (the scores there are dead: the keys are in
     // registers), then written with coalesced stores
@@ -1488,6 +1365,21 @@ int predictor_topk_normed(const kh_predictor* p, const float* hidden, int k, int
   if (rc != KH_OK || tk.done) return rc;
   return topk_launch(b.sbuf, 1, p->out_dim, k, KH_ORDER_ASCENDING, ids, st, nullptr,
                      bounds_ok(p) ? b.mm : nullptr, l2_blocks(p));
+}
+
+int predictor_scores_normed(const kh_predictor* p, const float* hidden, const NormIn& nrm,
+                            hipStream_t st, PredScores* out) {
+  if (!bounds_ok(p) || p->out_dim <= kL2Threads) return KH_ERR_UNSUPPORTED;
+  PredBufs b;
+  int rc = pred_bufs(p, st, 1, 0, false, &b);
+  if (rc != KH_OK) return rc;
+  rc = predict_into(p, hidden, 1, b.sbuf, b, st, nrm, true, nullptr);
+  if (rc != KH_OK) return rc;
+  out->scores = b.sbuf;
+  out->mm = b.mm;
+  out->n = p->out_dim;
+  out->nmm = l2_blocks(p);
+  return KH_OK;
 }
 
 int predictor_l1_view(const kh_predictor* p, hipStream_t st, PredL1View* v) {

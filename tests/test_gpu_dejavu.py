@@ -103,12 +103,14 @@ def test_select_top_k_small_rows_ties(kh, orc, out, k, batch):
                                  (20000, 3000), (40000, 4000), (65535, 64), (7, 0),
                                  (11264, 4000), (10001, 1500), (8193, 8193), (6143, 900)])
 def test_topk_ties_and_edges(kh, orc, n, k):
-    """Rows: heavy ties at the threshold (radix passes to the last bit), five
+    """Rows: heavy ties at the threshold (passes down to one key value), five
     distinct values, signed zeros, sigmoid-clustered scores (boundary bin
-    ranked directly) and uniform scores."""
+    ranked directly), uniform scores, and magnitudes from 1e-35 to 1e35 of
+    both signs (key intervals as wide as the f32 range)."""
     from klearu_amd.dejavu import ORDER_ASCENDING, topk_select
     rng = np.random.default_rng(n + k)
-    s = rng.random((5, n)).astype(np.float32)
+    s = rng.random((6, n)).astype(np.float32)
+    s[5] = (np.exp(rng.uniform(-80, 80, n)) * rng.choice([-1.0, 1.0], n)).astype(np.float32)
     s[0, rng.random(n) < 0.5] = 0.5          # heavy ties at the threshold
     s[1] = np.round(s[1] * 4) / 4            # only five distinct values
     s[2, : n // 2] = -0.0                    # -0.0 ties +0.0
@@ -116,7 +118,7 @@ def test_topk_ties_and_edges(kh, orc, n, k):
     s[3] = (1.0 / (1.0 + np.exp(-rng.normal(0, 0.14, n)))).astype(np.float32)
     got = topk_select(torch.from_numpy(s).cuda(), k).cpu().numpy() if k <= 4096 else None
     asc = topk_select(torch.from_numpy(s).cuda(), k, ORDER_ASCENDING).cpu().numpy()
-    for b in range(5):
+    for b in range(6):
         ref = orc.select_top_k(s[b], k)
         if got is not None:
             np.testing.assert_array_equal(got[b], ref)
@@ -425,6 +427,50 @@ def test_mlp_block_hard_norm_rows(kh, orc, H, I, R, k):
         ws.fill_(float("nan"))
         act = mlp_block(p, mlp, hd, wnd, 1e-5, k, norm_ws=ws)
         _check_block(orc, name, row, wn, ws, act, hd, (w1, b1, w2, b2), k, (wg, wu, wd))
+
+
+@pytest.mark.parametrize("case,k", [
+    ("tie group", 1652),   # 5000 identical predictor rows: the k-th score is one of 5000 equal keys
+    ("saturated", 1652),   # scores pinned at 1.0 for about a third of the neurons
+    ("all", 11008),        # every neuron
+    ("one", 1),
+    ("ragged", 1651),      # the last block takes fewer than 8 neurons
+])
+def test_mlp_block_selection_edges(kh, orc, case, k):
+    """The fused block's FFN kernel selects its own neurons from layer 2's
+    scores when its blocks have 8 waves (every block runs the same exact
+    selection): ties broken by the lower index when the k-th score sits in a
+    group of equal keys larger than the directly ranked bin, saturated sigmoid
+    scores, k equal to the whole layer, k = 1 and a partial last block, against
+    the oracle's select_top_k (mlp_predictor.rs:128-135)."""
+    from klearu_amd.dejavu import Mlp, SparsityPredictor, mlp_block
+    H, I, R = 2560, 11008, 128
+    rng = np.random.default_rng(91)
+    wg, wu, wd, _, _ = _ffn_case(orc, rng, H, I, 1, 1)
+    mlp = Mlp(wg, wu, wd, max_batch=1)
+    w1, b1, w2, b2 = make_predictor(orc, rng, H, R, I, bias=True)
+    wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    row = rng.standard_normal(H).astype(np.float32)
+    if case == "tie group":
+        # copy into rows 0..4999 the row of neurons 5000.. that about 1000 of
+        # them outscore, so the copies fill ranks ~1000..6000 around k
+        s0, _ = orc.predictor_predict(w1, b1, w2, b2, orc.rmsnorm(row, wn, 1e-5))
+        r = 5000 + int(np.argsort(-s0[5000:], kind="stable")[1000])
+        w2[:5000] = w2[r]
+        b2[:5000] = b2[r]
+    elif case == "saturated":
+        w2 = bf16(orc, orc.bf16_to_f32(w2) * 250.0)
+    p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
+    hd = torch.from_numpy(row.copy()).cuda()
+    ws = torch.empty(1, dtype=torch.float32, device="cuda")
+    act = mlp_block(p, mlp, hd, torch.from_numpy(wn).cuda(), 1e-5, k, norm_ws=ws)
+    if case in ("tie group", "saturated"):
+        scores, _ = orc.predictor_predict(w1, b1, w2, b2, orc.rmsnorm(row, wn, 1e-5))
+        kth = np.sort(scores)[::-1][k - 1]
+        ties = int(np.sum(scores == kth))
+        print(f"{case}: {ties} scores equal the k-th ({float(kth)!r})")
+        assert ties > 256
+    _check_block(orc, case, row, wn, ws, act, hd, (w1, b1, w2, b2), k, (wg, wu, wd))
 
 
 def test_batched_norm_select_union_exact(kh, orc):
