@@ -46,6 +46,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "gather.hpp"
@@ -112,36 +113,96 @@ __device__ void qkv_plan(const int32_t* __restrict__ heads, int nent, int nh, in
   if (threadIdx.x == 0) *nqrows = nq;
 }
 
+// The head selection of one row (sparse_attention.rs:14-24): the head
+// predictor's layer 2 over its layer-1 outputs hpred (mlp_predictor.rs:114-124,
+// the same chain as pred_l2_kernel) and the top k of its nh <= 64 scores,
+// computed by wave 0 of the block: s_hsel[h] = 1 for a selected head, s_heads
+// the k selected heads in ascending order.  phid <= kAttnSelHid.
+template <typename PW>
+__device__ __forceinline__ void attn_select_heads(const PW* __restrict__ w2, const float* __restrict__ b2,
+                                                  const float* __restrict__ hpred, int phid, int nh, int k,
+                                                  float* s_hp, uint64_t* s_tab, int* s_hsel,
+                                                  int32_t* s_heads) {
+  using V = typename Blk8<PW>::V;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int oc = min(lane, nh - 1);
+  V w[kAttnSelHid / 8];
+  float bv = 0.0f;
+  if (wave == 0) {
+    l2_load<PW, kAttnSelHid>(w2, phid, nh, oc, w);
+    bv = b2[oc];
+  }
+  for (int i = threadIdx.x; i < phid; i += blockDim.x) s_hp[i] = hpred[i];
+  if (threadIdx.x < 32) s_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  __syncthreads();
+  if (wave == 0) {
+    const float score = sigmoid_ref_t(__fadd_rn(l2_chain<PW, kAttnSelHid>(w, phid, s_hp), bv), s_tab);
+    const bool ok = lane < nh;
+    const int rank = l2_wave_rank(f32_key(score), lane, nh);
+    const bool sel = ok && rank < min(k, nh);
+    const uint64_t bal = __ballot(sel);
+    const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0));
+    if (ok) s_hsel[lane] = sel ? 1 : 0;
+    if (sel) s_heads[below] = lane;
+  }
+  __syncthreads();
+}
+
 // y[b][row] = Wkvq[row] . x[b] for the K/V rows and the Q rows of selected
 // heads, rows from row_base on (kvrows: the K/V rows were projected already).
 // The grid has one extra (last) block that writes the o_proj row list.
 // NORM (batch 1): x is the un-normalised hidden row and RmsNorm (weight nw) is
 // applied while staging it, with the exact scale at norm_inv (written by the
 // head predictor's layer 1 for this row).
-template <int NB, bool NORM = false>
+// PW (batch 1, not void): the heads are not read but selected by every block
+// (attn_select_heads over the head predictor's layer-1 outputs hpred and its
+// layer 2 w2 / b2, weights of type PW); the last block writes them to
+// heads_out, which the kernels after this one read.
+template <int NB, bool NORM = false, typename PW = void>
 __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
     const uint16_t* __restrict__ W, const float* __restrict__ x, int batch, int H, int kvrows,
     int D, int nh, const int32_t* __restrict__ heads, int nsel, float* __restrict__ y,
     int ystride, int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows,
     int32_t* __restrict__ urank, const float* __restrict__ nw,
-    const float* __restrict__ norm_inv, int row_base) {
+    const float* __restrict__ norm_inv, int row_base, const PW* __restrict__ w2 = nullptr,
+    const float* __restrict__ b2 = nullptr, const float* __restrict__ hpred = nullptr, int phid = 0,
+    int32_t* __restrict__ heads_out = nullptr) {
   extern __shared__ float4 xs4[];  // [kQkvTok][H/4]; the plan block's flags / union list
   __shared__ int wsum[kQkvWaves];
   __shared__ int s_total;
+  constexpr bool SEL = !std::is_void<PW>::value;
   const int nent = batch * nsel;
-  if (blockIdx.x == gridDim.x - 1) {
-    int* s_flag = reinterpret_cast<int*>(xs4);
-    qkv_plan(heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_flag + nh, wsum, &s_total);
-    return;
+  if constexpr (SEL) {
+    __shared__ int s_hsel[64];
+    __shared__ int32_t s_heads[64];
+    __shared__ __align__(16) float s_hp[kAttnSelHid + 4 * kL2Hw];
+    __shared__ uint64_t s_tab[32];
+    attn_select_heads<PW>(w2, b2, hpred, phid, nh, nsel, s_hp, s_tab, s_hsel, s_heads);
+    if (blockIdx.x == gridDim.x - 1) {
+      if ((int)threadIdx.x < nsel) heads_out[threadIdx.x] = s_heads[threadIdx.x];
+      int* s_flag = reinterpret_cast<int*>(xs4);
+      qkv_plan(s_heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_flag + nh, wsum, &s_total);
+      return;
+    }
+    const int row0 = row_base + blockIdx.x * kQkvWaves;
+    if (row0 >= kvrows && !s_hsel[(row0 - kvrows) / D]) return;
+  } else {
+    if (blockIdx.x == gridDim.x - 1) {
+      int* s_flag = reinterpret_cast<int*>(xs4);
+      qkv_plan(heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_flag + nh, wsum, &s_total);
+      return;
+    }
+    const int row0 = row_base + blockIdx.x * kQkvWaves;
+    if (row0 >= kvrows) {
+      // Q rows of head h (D is a multiple of kQkvWaves): skip unless selected.
+      const int h = (row0 - kvrows) / D;
+      int any = 0;
+      for (int i = threadIdx.x; i < nent; i += blockDim.x) any |= heads[i] == h;
+      if (!__syncthreads_or(any)) return;
+    }
   }
   const int row0 = row_base + blockIdx.x * kQkvWaves;
-  if (row0 >= kvrows) {
-    // Q rows of head h (D is a multiple of kQkvWaves): skip unless selected.
-    const int h = (row0 - kvrows) / D;
-    int any = 0;
-    for (int i = threadIdx.x; i < nent; i += blockDim.x) any |= heads[i] == h;
-    if (!__syncthreads_or(any)) return;
-  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row = row0 + wave;
   const uint4* __restrict__ w = reinterpret_cast<const uint4*>(W + (size_t)row * H);
@@ -1366,7 +1427,8 @@ static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
 template <int NB>
 static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64_t* pos,
                        const int32_t* heads, int nsel, float* out, int accumulate,
-                       hipStream_t st, const NormIn& nrm = NormIn{}, bool kv_done = false) {
+                       hipStream_t st, const NormIn& nrm = NormIn{}, bool kv_done = false,
+                       const PredL1View* hsel = nullptr) {
   const int H = a->hidden, D = a->d, qd = a->nh * D, kvrows = 2 * a->kvd();
   // 1. projections (+ the o_proj row list in the last block)
   const int rows = kvrows + qd;
@@ -1389,6 +1451,11 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
                                  hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
       KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_qkv_kernel<1, true>),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+      // the head selection's static LDS comes on top of the dynamic part
+      KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_qkv_kernel<1, true, uint16_t>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds - 8192));
+      KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_qkv_kernel<1, true, float>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds - 8192));
       attr_set = true;
     }
     const size_t lds = std::max(sizeof(float) * std::min(NB, kQkvTok) * H,
@@ -1398,7 +1465,21 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
       return KH_ERR_UNSUPPORTED;
     }
     const int row_base = kv_done ? kvrows : 0;
-    if (nrm.w && NB == 1)
+    if (nrm.w && NB == 1 && hsel && hsel->bf16)
+      hipLaunchKernelGGL((attn_qkv_kernel<1, true, uint16_t>), dim3((rows - row_base) / kQkvWaves + 1),
+                         dim3(64 * kQkvWaves), lds, st, a->wkvq, x, batch, H, kvrows, D, a->nh,
+                         nullptr, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
+                         a->qrows + qd + 1, nrm.w, nrm.inv, row_base,
+                         static_cast<const uint16_t*>(hsel->w2b), hsel->b2, hsel->hbuf, hsel->hid,
+                         const_cast<int32_t*>(heads));
+    else if (nrm.w && NB == 1 && hsel)
+      hipLaunchKernelGGL((attn_qkv_kernel<1, true, float>), dim3((rows - row_base) / kQkvWaves + 1),
+                         dim3(64 * kQkvWaves), lds, st, a->wkvq, x, batch, H, kvrows, D, a->nh,
+                         nullptr, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
+                         a->qrows + qd + 1, nrm.w, nrm.inv, row_base,
+                         static_cast<const float*>(hsel->w2b), hsel->b2, hsel->hbuf, hsel->hid,
+                         const_cast<int32_t*>(heads));
+    else if (nrm.w && NB == 1)
       hipLaunchKernelGGL((attn_qkv_kernel<1, true>), dim3((rows - row_base) / kQkvWaves + 1),
                          dim3(64 * kQkvWaves), lds, st, a->wkvq, x, batch, H, kvrows, D, a->nh,
                          heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
@@ -1548,6 +1629,13 @@ extern "C" int kh_dejavu_attn_block(const kh_predictor* p, kh_sparse_attn* a, fl
                          st, static_cast<const float*>(v.w1b), v.b1, v.hid, v.hbuf, hidden_dev, a->hidden,
                          norm_w_dev, norm_ws_dev, eps, a->wkvq, kvrows, a->y, nl1);
     KH_LAUNCHED();
+    // layer 2 and the top k inside the Q projection (every block selects the
+    // heads itself, the last one writes them) when the head scores fit a wave
+    if (v.out_dim <= 64 && v.hid <= kAttnSelHid) {
+      rc = attn_launch<1>(a, hidden_dev, 1, nullptr, heads_dev, k, hidden_dev, 1, st, nrm, true, &v);
+      if (rc == KH_OK) a->len_host[0] += 1;
+      return rc;
+    }
     rc = predictor_l2_topk_from_h(p, k, heads_dev, st);
   } else {
     rc = predictor_topk_normed(p, hidden_dev, k, heads_dev, nrm, st);

@@ -348,7 +348,9 @@ int predictor_scores_normed(const kh_predictor* p, const float* hidden, const No
 struct PredL1View {
   const void* w1b = nullptr;   // [ceil(in/8)][hid][8], BF16 bits when bf16
   const float* b1 = nullptr;
-  int in_dim = 0, hid = 0;
+  const void* w2b = nullptr;   // [ceil(hid/8)][out][8], BF16 bits when bf16
+  const float* b2 = nullptr;
+  int in_dim = 0, hid = 0, out_dim = 0;
   bool bf16 = false;
   float* hbuf = nullptr;       // [hid] layer-1 outputs of one row
 };

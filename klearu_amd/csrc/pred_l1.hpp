@@ -1,6 +1,7 @@
 // pred_l1.hpp -- layer 1 of the Deja Vu predictor for rows of at most 4096
 // inputs (crates/klearu-dejavu/src/predictor/mlp_predictor.rs:102-113), as
-// a block body that kernels of predictor.hip and attention.hip launch.
+// a block body that kernels of predictor.hip and attention.hip launch, and
+// layer 2's per-lane chain (mlp_predictor.rs:114-124) for the same files.
 //
 // Each hidden unit is a sequential f32 sum that starts at -0.0 and adds the
 // rounded product w*x term by term (Rust `.map(|(w, x)| w * x).sum()`), with
@@ -239,6 +240,89 @@ __device__ __forceinline__ void pred_l1_lds_body(
   if (n_in > kSeg) run(kSeg, n_in);
   const int chain = c0 + lane;
   if (lane < kL1Chains && chain < hid) h[(size_t)b * hid + chain] = fmaxf(__fadd_rn(s, bv), 0.0f);
+}
+
+// ---------------------------------------------------------------- layer 2
+// One output per lane: sigmoid(b + w . h) with the dot product a sequential
+// f32 sum in input order (mlp_predictor.rs:114-124).  Layer 2's weights are
+// stored blocked-transposed, [ceil(hid/8)][out][8], so the 64 lanes of a wave
+// read 64 adjacent 16-byte blocks.  l2_load requests lane o's whole row (the
+// caller stages h meanwhile); l2_chain runs the sum over h in LDS (n_hid
+// floats plus 4 * kL2Hw of padding, 16-byte aligned).
+constexpr int kMaxL2Hid = 256;
+constexpr int kAttnSelHid = 128;  // head predictors selected inside the Q projection
+constexpr int kL2Hw = 4;  // float4 of the hidden vector read ahead (16 steps)
+
+// MAXH: the largest n_hid the call supports (registers for its row).
+template <typename W, int MAXH = kMaxL2Hid>
+__device__ __forceinline__ void l2_load(const W* __restrict__ Wb, int n_hid, int n_out, int oc,
+                                        typename Blk8<W>::V (&w)[MAXH / 8]) {
+  using B8 = Blk8<W>;
+  using V = typename B8::V;
+  const int nblk = (n_hid + 7) >> 3;
+  const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
+#pragma unroll
+  for (int jb = 0; jb < MAXH / 8; ++jb)
+    w[jb] = jb < nblk ? wv[(size_t)jb * n_out + oc] : B8::zero();
+}
+
+template <typename W, int MAXH = kMaxL2Hid>
+__device__ __forceinline__ float l2_chain(const typename Blk8<W>::V (&w)[MAXH / 8], int n_hid,
+                                          const float* hs) {
+  using B8 = Blk8<W>;
+  const int nblk = (n_hid + 7) >> 3;
+  float s = -0.0f;
+  if ((n_hid & 7) == 0) {
+    // Whole 8-step blocks: no per-step test.  The hidden values come from LDS
+    // through a window of kL2Hw float4 read ahead of their use (pinned, or the
+    // scheduler sinks each read to its use and the chain waits on LDS).
+    const float4* h4 = reinterpret_cast<const float4*>(hs);
+    float4 hw[kL2Hw];
+#pragma unroll
+    for (int q = 0; q < kL2Hw; ++q) hw[q] = h4[q];
+#pragma unroll
+    for (int jb = 0; jb < MAXH / 8; ++jb) {
+      if (jb < nblk) {
+        float wf[8];
+        B8::widen(w[jb], wf);
+        const float4 a = hw[(2 * jb) % kL2Hw], c = hw[(2 * jb + 1) % kL2Hw];
+        s = __fadd_rn(s, __fmul_rn(wf[0], a.x));
+        s = __fadd_rn(s, __fmul_rn(wf[1], a.y));
+        s = __fadd_rn(s, __fmul_rn(wf[2], a.z));
+        s = __fadd_rn(s, __fmul_rn(wf[3], a.w));
+        s = __fadd_rn(s, __fmul_rn(wf[4], c.x));
+        s = __fadd_rn(s, __fmul_rn(wf[5], c.y));
+        s = __fadd_rn(s, __fmul_rn(wf[6], c.z));
+        s = __fadd_rn(s, __fmul_rn(wf[7], c.w));
+        hw[(2 * jb) % kL2Hw] = h4[2 * jb + kL2Hw];
+        hw[(2 * jb + 1) % kL2Hw] = h4[2 * jb + 1 + kL2Hw];
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int jb = 0; jb < MAXH / 8; ++jb) {
+      if (jb < nblk) {
+        float wf[8];
+        B8::widen(w[jb], wf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (jb * 8 + e < n_hid) s = __fadd_rn(s, __fmul_rn(wf[e], hs[jb * 8 + e]));
+      }
+    }
+  }
+  return s;
+}
+
+// Rank of lane o's key among the n_out <= 64 keys of its wave (key desc,
+// index asc: select_top_k's stable descending sort, mlp_predictor.rs:128-131).
+__device__ __forceinline__ int l2_wave_rank(uint32_t key, int o, int n_out) {
+  int rank = 0;
+  for (int j = 0; j < n_out; ++j) {
+    const uint32_t kj = __builtin_amdgcn_readlane(key, j);
+    rank += (kj > key || (kj == key && j < o)) ? 1 : 0;
+  }
+  return rank;
 }
 
 }  // namespace kh

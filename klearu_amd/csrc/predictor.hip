@@ -389,7 +389,6 @@ __global__ __launch_bounds__(kLbThreads) void pred_l1_batch_kernel(
 // registers (n_hid <= 256), the hidden vector in LDS.  Scores = sigmoid.
 // One wave per block, so the weight stream is spread over as many CUs as
 // there are waves.
-constexpr int kMaxL2Hid = 256;
 constexpr int kL2Threads = 64;
 
 // With mm set, each block also writes the (min, max) order-preserving keys of
@@ -406,10 +405,8 @@ __global__ __launch_bounds__(kL2Threads) void pred_l2_kernel(const W* __restrict
                                                       uint32_t* __restrict__ mm, int k = 0,
                                                       int order = 0,
                                                       int32_t* __restrict__ ids = nullptr) {
-  using B8 = Blk8<W>;
-  using V = typename B8::V;
-  constexpr int kHw = 4;  // float4 of the hidden vector read ahead (16 steps)
-  __shared__ __align__(16) float hs[kMaxL2Hid + 4 * kHw];
+  using V = typename Blk8<W>::V;
+  __shared__ __align__(16) float hs[kMaxL2Hid + 4 * kL2Hw];
   __shared__ uint64_t tab[32];
   const int b = blockIdx.y;
   const int o = blockIdx.x * blockDim.x + threadIdx.x;
@@ -422,13 +419,9 @@ __global__ __launch_bounds__(kL2Threads) void pred_l2_kernel(const W* __restrict
                         : make_float4(0, 0, 0, 0);
   const bool ok = o < n_out;
   const int oc = ok ? o : 0;
-  const int nblk = (n_hid + 7) >> 3;
-  const V* __restrict__ wv = reinterpret_cast<const V*>(Wb);
   const float bv = bias[oc];  // used after the chain
   V w[kMaxL2Hid / 8];
-#pragma unroll
-  for (int jb = 0; jb < kMaxL2Hid / 8; ++jb)
-    w[jb] = jb < nblk ? wv[(size_t)jb * n_out + oc] : B8::zero();
+  l2_load<W>(Wb, n_hid, n_out, oc, w);
   if (vec) {
     reinterpret_cast<float4*>(hs)[min((int)threadIdx.x, (n_hid >> 2) - 1)] = hv;  // clamped (see stage_f4)
   } else {
@@ -436,46 +429,7 @@ __global__ __launch_bounds__(kL2Threads) void pred_l2_kernel(const W* __restrict
   }
   if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   __syncthreads();
-  float s = -0.0f;
-  if ((n_hid & 7) == 0) {
-    // Whole 8-step blocks: no per-step test.  The hidden values come from LDS
-    // through a window of kHw float4 read ahead of their use (pinned, or the
-    // scheduler sinks each read to its use and the chain waits on LDS).
-    const float4* h4 = reinterpret_cast<const float4*>(hs);
-    float4 hw[kHw];
-#pragma unroll
-    for (int q = 0; q < kHw; ++q) hw[q] = h4[q];
-#pragma unroll
-    for (int jb = 0; jb < kMaxL2Hid / 8; ++jb) {
-      if (jb < nblk) {
-        float wf[8];
-        B8::widen(w[jb], wf);
-        const float4 a = hw[(2 * jb) % kHw], c = hw[(2 * jb + 1) % kHw];
-        s = __fadd_rn(s, __fmul_rn(wf[0], a.x));
-        s = __fadd_rn(s, __fmul_rn(wf[1], a.y));
-        s = __fadd_rn(s, __fmul_rn(wf[2], a.z));
-        s = __fadd_rn(s, __fmul_rn(wf[3], a.w));
-        s = __fadd_rn(s, __fmul_rn(wf[4], c.x));
-        s = __fadd_rn(s, __fmul_rn(wf[5], c.y));
-        s = __fadd_rn(s, __fmul_rn(wf[6], c.z));
-        s = __fadd_rn(s, __fmul_rn(wf[7], c.w));
-        hw[(2 * jb) % kHw] = h4[2 * jb + kHw];
-        hw[(2 * jb + 1) % kHw] = h4[2 * jb + 1 + kHw];
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int jb = 0; jb < kMaxL2Hid / 8; ++jb) {
-      if (jb < nblk) {
-        float wf[8];
-        B8::widen(w[jb], wf);
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (jb * 8 + e < n_hid) s = __fadd_rn(s, __fmul_rn(wf[e], hs[jb * 8 + e]));
-      }
-    }
-  }
+  const float s = l2_chain<W>(w, n_hid, hs);
   const float score = sigmoid_ref_t(__fadd_rn(s, bv), tab);
   if (ok) out[(size_t)b * n_out + o] = score;
   if (mm) {
@@ -488,12 +442,7 @@ __global__ __launch_bounds__(kL2Threads) void pred_l2_kernel(const W* __restrict
   if constexpr (TOPK) {
     // select_top_k's stable descending sort (mlp_predictor.rs:128-131) over
     // the row's n_out <= 64 scores: lane o's rank among them
-    const uint32_t key = f32_key(score);
-    int rank = 0;
-    for (int j = 0; j < n_out; ++j) {
-      const uint32_t kj = __builtin_amdgcn_readlane(key, j);
-      rank += (kj > key || (kj == key && j < o)) ? 1 : 0;
-    }
+    const int rank = l2_wave_rank(f32_key(score), o, n_out);
     const int kk = min(k, n_out);
     const bool sel = ok && rank < kk;
     const uint64_t bal = __ballot(sel);
@@ -1390,8 +1339,11 @@ int predictor_l1_view(const kh_predictor* p, hipStream_t st, PredL1View* v) {
   if (rc != KH_OK) return rc;
   v->w1b = p->w1b;
   v->b1 = p->b1;
+  v->w2b = p->w2b;
+  v->b2 = p->b2;
   v->in_dim = p->in_dim;
   v->hid = p->hid;
+  v->out_dim = p->out_dim;
   v->bf16 = p->bf16;
   v->hbuf = b.hbuf;
   return KH_OK;
