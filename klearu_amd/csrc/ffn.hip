@@ -281,7 +281,7 @@ constexpr int kFuWaves = 8;                // neurons (waves) per block; 4 for s
 constexpr int kFuWavesMin = 4;
 constexpr int kFuMaxH = 4096;              // 8 chunks of 16 B per lane per gate/up row
 constexpr int kFuChunks = kFuMaxH / 512;
-constexpr int kFuSelKpt = 22;              // scores per thread of the selecting form (11008 / 512)
+constexpr int kFuSelKpt = 22;              // scores per thread of the selecting form (11008 / 512; 11 for 5632)
 // Dynamic LDS: x [kFuMaxH/4 float4], then h [16 floats] and the block's ids
 // [16 ints], then (selecting form) the staged scores.
 constexpr int kFuStage = kFuMaxH / 4 + 8;  // float4 offset of the staged scores
@@ -815,16 +815,15 @@ static bool ffn_fused_ok(const kh_sparse_ffn* f, int64_t batch) {
 static int ffn_fused_wave_count(const kh_sparse_ffn* f, int k) {
   return f->hidden <= 512 * kFuWavesMin && k < 256 * kFuWaves ? kFuWavesMin : kFuWaves;
 }
-// Whether the fused block's FFN selects its own neurons: with 8-wave blocks,
-// when the row's scores fit kFuSelKpt per thread and layer 2's key bounds one
-// slot per thread.  Every block then runs the whole selection (about 7 us at
-// the 7B shape, against 8.4 us for the one-block top-k kernel and its launch);
-// 4-wave blocks would take twice as long per block, which measured slower than
-// the separate top-k at the 1.1B shape.
+// Whether the fused block's FFN selects its own neurons: always with 8-wave
+// blocks (512 threads share the selection), when the row's scores fit
+// kFuSelKpt per thread and layer 2's key bounds one slot per thread.  Every
+// block then runs the whole selection (about 7 us at the 7B shape, against
+// 8.4 us for the one-block top-k kernel and its launch).
 static bool ffn_select_ok(const kh_sparse_ffn* f, int k) {
-  const int nw = ffn_fused_wave_count(f, k);
-  const int nt = 64 * nw;
-  return nw == kFuWaves && f->inter > 64 && f->inter % 4 == 0 && f->inter < 65536 &&
+  (void)k;
+  constexpr int nt = 64 * kFuWaves;
+  return f->inter > 64 && f->inter % 4 == 0 && f->inter < 65536 &&
          ceil_div(f->inter, nt) <= kFuSelKpt && ceil_div(f->inter, 64) <= nt;
 }
 
@@ -869,7 +868,7 @@ static int ffn_select_launch(const kh_sparse_ffn* f, const float* x, const PredS
                              int32_t* active_out, float* y, int accumulate, const NormIn& nrm,
                              hipStream_t st) {
   const int H = f->hidden;
-  if (ps.n != f->inter || !ffn_select_ok(f, k) || ps.nmm > 64 * ffn_fused_wave_count(f, k)) {
+  if (ps.n != f->inter || !ffn_select_ok(f, k) || ps.nmm > 64 * kFuWaves) {
     set_error("selecting FFN launched outside its limits");
     return KH_ERR_UNSUPPORTED;
   }
@@ -888,11 +887,20 @@ static int ffn_select_launch(const kh_sparse_ffn* f, const float* x, const PredS
   std::call_once(once, [] {
     arc = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel<kFuWaves, kFuSelKpt>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kFuSelLds);
+    if (arc == hipSuccess)
+      arc = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_fused1_kernel<kFuWaves, kFuSelKpt / 2>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kFuSelLds);
   });
   KH_HIP(arc);
-  hipLaunchKernelGGL((ffn_fused1_kernel<kFuWaves, kFuSelKpt>), dim3(blocks), dim3(64 * kFuWaves), lds, st,
-                     f->wgu, f->wdt, x, H, nullptr, k, nullptr, f->inter, f->err, hbuf, partial, nrm.w,
-                     nrm.inv, ps.scores, ps.mm, ps.nmm, active_out);
+  // half the key registers when they suffice (the 1.1B shape: 5632 scores)
+  if (ceil_div(ps.n, 64 * kFuWaves) <= kFuSelKpt / 2)
+    hipLaunchKernelGGL((ffn_fused1_kernel<kFuWaves, kFuSelKpt / 2>), dim3(blocks), dim3(64 * kFuWaves), lds,
+                       st, f->wgu, f->wdt, x, H, nullptr, k, nullptr, f->inter, f->err, hbuf, partial,
+                       nrm.w, nrm.inv, ps.scores, ps.mm, ps.nmm, active_out);
+  else
+    hipLaunchKernelGGL((ffn_fused1_kernel<kFuWaves, kFuSelKpt>), dim3(blocks), dim3(64 * kFuWaves), lds, st,
+                       f->wgu, f->wdt, x, H, nullptr, k, nullptr, f->inter, f->err, hbuf, partial, nrm.w,
+                       nrm.inv, ps.scores, ps.mm, ps.nmm, active_out);
   KH_LAUNCHED();
   partials_reduce_launch(partial, H, blocks, y, accumulate, st);
   KH_LAUNCHED();
