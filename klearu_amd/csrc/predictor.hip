@@ -164,10 +164,13 @@ __global__ __launch_bounds__(kL1LdsThreads) void pred_l1_lds_kernel(
 
 // Layer 1 for a batch of rows (BF16 weights, n_in a multiple of
 // kLbSlots * kLbStage, at most kL1LdsIn): a block owns kLbOut hidden units for
-// kLbRows rows, i.e. 32 chains, one per consumer lane (lanes 32-63 idle).  pred_l1_lds holds every product of its block in LDS, so one block
-// fits per CU and a batch's blocks run in several rounds; here the products
-// pass through a ring of kLbSlots stages, so all blocks of a 16-row batch run
-// at once.
+// kLbRows rows, i.e. 16 chains, one per consumer lane (lanes 16-63 leave).
+// pred_l1_lds holds every product of its block in LDS, so one block fits per
+// CU and a batch's blocks run in several rounds; here the products pass
+// through a ring of kLbSlots stages (64 KB of LDS per block with the rows' x),
+// so all blocks of a 16-row batch run at once.  Two rows per block measured
+// 19.2 us per 7B batch-16 call against 22.4 with four (the consumer's window
+// reads move half the bytes); one row per block breaks the ring's swizzle.
 //  * The rows' x go to LDS once (the block's only barrier) and the producers
 //    hold every weight of the block in registers from the start.
 //  * Producer p forms stages p, p + kLbProd, ... into slot stage % kLbSlots
@@ -177,7 +180,7 @@ __global__ __launch_bounds__(kL1LdsThreads) void pred_l1_lds_kernel(
 //    except on the data it needs.  One consumer and three producers, one wave
 //    per SIMD, so no producer takes issue slots from the chain.
 //  * Quad q of chain c sits at position c ^ (q & 14) of its ring row: the
-//    consumer's 32 lanes still read one contiguous row, and a producer's
+//    consumer's 16 lanes still read one contiguous row, and a producer's
 //    write instruction (8 quads x 8 chains) spreads evenly over the banks
 //    instead of hitting one bank group 8 times.  Eight slots of 64 steps give
 //    a producer six stages of slack to refill a slot: it takes about three
@@ -188,7 +191,8 @@ __global__ __launch_bounds__(kL1LdsThreads) void pred_l1_lds_kernel(
 //    checked and slots released two stages at a time).  The loop is unrolled by the ring
 //    size, so every LDS address is a fixed register plus an immediate offset.
 // Each chain is the same sequential sum as pred_l1_lds_kernel's.
-constexpr int kLbOut = 8, kLbRows = 4, kLbChains = kLbOut * kLbRows;
+constexpr int kLbOut = 8, kLbRows = 2, kLbChains = kLbOut * kLbRows;
+static_assert(kLbChains == 16 || kLbChains == 32, "the ring swizzle c ^ (q & 14) stays inside a row");
 constexpr int kLbStage = 64, kLbSlots = 8, kLbProd = 3;
 constexpr int kLbThreads = 64 * (1 + kLbProd);
 constexpr int kLbStages = kL1LdsIn / kLbStage;
@@ -296,8 +300,8 @@ __global__ __launch_bounds__(kLbThreads) void pred_l1_batch_kernel(
     if (gave_up) *err = 1;
     return;
   }
-  // consumer: lane ch reads quad q of slot sl at ring[(sl * kLbQuads + q) * 32 + (ch ^ swz(q))].
-  // Lanes past the 32 chains leave, so each window read moves 512 bytes of
+  // consumer: lane ch reads quad q of slot sl at ring[(sl * kLbQuads + q) * kLbChains + (ch ^ swz(q))].
+  // Lanes past the chains leave, so each window read moves 256 bytes of
   // LDS, not 1 KB (the LDS, shared with the producers, sets the pace).
   if (lane >= kLbChains) return;
   const int ch = lane;
