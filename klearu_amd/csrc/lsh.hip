@@ -931,6 +931,41 @@ __global__ void csr_copy_f32_kernel(const float* __restrict__ src, int stride,
     if (o + j < capacity) dst[o + j] = src[row * (int64_t)stride + j];
 }
 
+// The row offsets and up to three 32-bit arrays' rows in one launch, for
+// batches of at most kCsrPackMax rows: block (x, row) sums lens[0..row) itself
+// (a block reduction, so no block waits for another), block (0, row) writes
+// off[row] (and the last row off[batch]), and every block copies its share of
+// the row into each destination given.  The same result as csr_offsets_kernel
+// followed by one csr_copy kernel per array.
+constexpr int kCsrPackMax = 4096;
+__global__ __launch_bounds__(256) void csr_pack_kernel(
+    const int32_t* __restrict__ lens, int64_t batch, int stride, int64_t capacity,
+    int64_t* __restrict__ off, const uint32_t* __restrict__ s0, uint32_t* __restrict__ d0,
+    const uint32_t* __restrict__ s1, uint32_t* __restrict__ d1, const uint32_t* __restrict__ s2,
+    uint32_t* __restrict__ d2) {
+  __shared__ long long wpart[4];
+  const int64_t row = blockIdx.y;
+  long long part = 0;
+  for (int64_t r = threadIdx.x; r < row; r += blockDim.x) part += lens[r];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m);
+  if ((threadIdx.x & 63) == 0) wpart[threadIdx.x >> 6] = part;
+  __syncthreads();
+  const int64_t o = wpart[0] + wpart[1] + wpart[2] + wpart[3];
+  const int n = lens[row];
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    off[row] = o;
+    if (row == batch - 1) off[batch] = o + n;
+  }
+  const int64_t src = row * (int64_t)stride;
+  for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < n; j += gridDim.x * blockDim.x) {
+    if (o + j >= capacity) break;
+    if (d0) d0[o + j] = s0[src + j];
+    if (d1) d1[o + j] = s1[src + j];
+    if (d2) d2[o + j] = s2[src + j];
+  }
+}
+
 // ------------------------------------------------------------------ host helpers
 int hash_dense_launch(const kh_hash_family* h, const float* x, int64_t ldx, int64_t batch,
                       uint32_t* codes, hipStream_t st) {
@@ -1042,14 +1077,34 @@ int query_stride(const kh_lsh_index* idx) {
 int csr_finish(const uint32_t* qids, const uint32_t* qcnt, const float* f1, const float* f2,
                int stride, const int32_t* ulen, int64_t batch, int64_t* off, uint32_t* ids,
                uint32_t* cnts, float* o1, float* o2, int64_t capacity, hipStream_t st) {
-  hipLaunchKernelGGL(csr_offsets_kernel, dim3(1), dim3(1024), 0, st, ulen, batch, off);
-  KH_LAUNCHED();
+  if (batch <= 0) {
+    KH_HIP(hipMemsetAsync(off, 0, sizeof(int64_t), st));
+    return KH_OK;
+  }
   dim3 g(std::max(1, std::min(64, ceil_div(stride, 256))), (unsigned)batch);
-  if (ids) hipLaunchKernelGGL(csr_copy_u32_kernel, g, dim3(256), 0, st, qids, stride, ulen, off, capacity, ids);
-  if (cnts && qcnt) hipLaunchKernelGGL(csr_copy_u32_kernel, g, dim3(256), 0, st, qcnt, stride, ulen, off, capacity, cnts);
-  if (o1 && f1) hipLaunchKernelGGL(csr_copy_f32_kernel, g, dim3(256), 0, st, f1, stride, ulen, off, capacity, o1);
-  if (o2 && f2) hipLaunchKernelGGL(csr_copy_f32_kernel, g, dim3(256), 0, st, f2, stride, ulen, off, capacity, o2);
-  KH_LAUNCHED();
+  // one launch for the offsets and (up to three) arrays; a fourth array or a
+  // longer batch takes the separate kernels
+  const int narr = (ids ? 1 : 0) + (cnts && qcnt ? 1 : 0) + (o1 && f1 ? 1 : 0) + (o2 && f2 ? 1 : 0);
+  if (batch <= kCsrPackMax && narr <= 3) {
+    const uint32_t* src[3] = {nullptr, nullptr, nullptr};
+    uint32_t* dst[3] = {nullptr, nullptr, nullptr};
+    int a = 0;
+    if (ids) { src[a] = qids; dst[a++] = ids; }
+    if (cnts && qcnt) { src[a] = qcnt; dst[a++] = cnts; }
+    if (o1 && f1) { src[a] = reinterpret_cast<const uint32_t*>(f1); dst[a++] = reinterpret_cast<uint32_t*>(o1); }
+    if (o2 && f2) { src[a] = reinterpret_cast<const uint32_t*>(f2); dst[a++] = reinterpret_cast<uint32_t*>(o2); }
+    hipLaunchKernelGGL(csr_pack_kernel, g, dim3(256), 0, st, ulen, batch, stride, capacity, off, src[0],
+                       dst[0], src[1], dst[1], src[2], dst[2]);
+    KH_LAUNCHED();
+  } else {
+    hipLaunchKernelGGL(csr_offsets_kernel, dim3(1), dim3(1024), 0, st, ulen, batch, off);
+    KH_LAUNCHED();
+    if (ids) hipLaunchKernelGGL(csr_copy_u32_kernel, g, dim3(256), 0, st, qids, stride, ulen, off, capacity, ids);
+    if (cnts && qcnt) hipLaunchKernelGGL(csr_copy_u32_kernel, g, dim3(256), 0, st, qcnt, stride, ulen, off, capacity, cnts);
+    if (o1 && f1) hipLaunchKernelGGL(csr_copy_f32_kernel, g, dim3(256), 0, st, f1, stride, ulen, off, capacity, o1);
+    if (o2 && f2) hipLaunchKernelGGL(csr_copy_f32_kernel, g, dim3(256), 0, st, f2, stride, ulen, off, capacity, o2);
+    KH_LAUNCHED();
+  }
   // Every row holds at most `stride` entries: with room for that many, no
   // overflow is possible and the call stays asynchronous (no host round trip;
   // capturable in a graph).  Otherwise the total is read back to report one.
