@@ -256,13 +256,23 @@ __global__ __launch_bounds__(kSlideThreads) void select_kernel(
 // One block per sample (several per sample without softmax: blockIdx.y takes
 // every gridDim.y-th block of active ids).  x is either dense [batch][dim]
 // (zeros skipped) or CSR.  TRANS: W is the transposed copy [dim][nn].
+// fb_n > 0 (Vanilla sampling read straight from the query, every id below the
+// layer's fb_n neurons): a sample whose candidate list is empty takes all fb_n
+// neurons (layer.rs:82-84), whose ids the blocks write into its aids row; the
+// row lengths the outputs use go to alen_out (vanilla_len decides).
+__device__ __forceinline__ int vanilla_len(const int32_t* alen, int64_t row, int fb_n, bool& all) {
+  const int n = alen[row];
+  all = fb_n > 0 && n == 0;
+  return all ? fb_n : n;
+}
 template <bool SPARSE, bool TRANS>
 __global__ __launch_bounds__(kSlideThreads) void neuron_kernel(
     const float* __restrict__ W, int nn, const float* __restrict__ bias, int dim,
     const float* __restrict__ x, const int64_t* __restrict__ xoff,
     const uint32_t* __restrict__ xidx, const float* __restrict__ xval,
-    const uint32_t* __restrict__ aids, int astride, const int32_t* __restrict__ alen, int act,
-    int max_nz, float* __restrict__ pre, float* __restrict__ post) {
+    uint32_t* __restrict__ aids, int astride, const int32_t* __restrict__ alen, int act,
+    int max_nz, float* __restrict__ pre, float* __restrict__ post, int fb_n = 0,
+    int32_t* __restrict__ alen_out = nullptr) {
   extern __shared__ unsigned char smem[];
   uint32_t* nzi = reinterpret_cast<uint32_t*>(smem);
   float* nzv = reinterpret_cast<float*>(smem + sizeof(uint32_t) * max_nz);
@@ -307,14 +317,17 @@ __global__ __launch_bounds__(kSlideThreads) void neuron_kernel(
     li = nzi;
     lv = nzv;
   }
-  const int n = alen[row];
-  const uint32_t* ids = aids + row * (int64_t)astride;
+  bool all;
+  const int n = vanilla_len(alen, row, fb_n, all);
+  uint32_t* ids = aids + row * (int64_t)astride;
   float* prow = pre + row * (int64_t)astride;
   float* orow = post + row * (int64_t)astride;
+  if (alen_out && blockIdx.y == 0 && threadIdx.x == 0) alen_out[row] = n;
   float lmax = -INFINITY;
   const int a0 = threadIdx.x + blockIdx.y * blockDim.x, astep = blockDim.x * gridDim.y;
   for (int a = a0; a < n; a += astep) {
-    const uint32_t id = ids[a];
+    const uint32_t id = all ? (uint32_t)a : ids[a];
+    if (all) ids[a] = id;
     float s = -0.0f;
     if (TRANS) {
       const float* w = W + id;
@@ -380,8 +393,9 @@ constexpr size_t kTileLds = sizeof(float) * kTileWaves * kTileN * kTileStride;
 
 __global__ __launch_bounds__(kSlideThreads) void neuron_tile_kernel(
     const float* __restrict__ W, const float* __restrict__ bias, int dim, const float* __restrict__ x,
-    const uint32_t* __restrict__ aids, int astride, const int32_t* __restrict__ alen, int act,
-    float* __restrict__ pre, float* __restrict__ post) {
+    uint32_t* __restrict__ aids, int astride, const int32_t* __restrict__ alen, int act,
+    float* __restrict__ pre, float* __restrict__ post, int fb_n = 0,
+    int32_t* __restrict__ alen_out = nullptr) {
   extern __shared__ float tl[];
   __shared__ uint32_t nzi[kTileMaxDim];
   __shared__ float nzv[kTileMaxDim];
@@ -402,10 +416,14 @@ __global__ __launch_bounds__(kSlideThreads) void neuron_tile_kernel(
   }
   __syncthreads();
   const int nnz = s_total;
-  const int n = alen[row];
-  const uint32_t* ids = aids + row * (int64_t)astride;
+  bool all;
+  const int n = vanilla_len(alen, row, fb_n, all);
+  uint32_t* ids = aids + row * (int64_t)astride;
   float* prow = pre + row * (int64_t)astride;
   float* orow = post + row * (int64_t)astride;
+  if (alen_out && threadIdx.x == 0) alen_out[row] = n;
+  if (all)
+    for (int a = threadIdx.x; a < n; a += blockDim.x) ids[a] = (uint32_t)a;
   float* buf = tl + (size_t)wave * kTileN * kTileStride;
   const int q4 = dim >> 2;              // float4 per weight row (<= 32)
   const int c = lane & 31;              // this lane's float4 of a row
@@ -414,7 +432,8 @@ __global__ __launch_bounds__(kSlideThreads) void neuron_tile_kernel(
   float4 v[kTileN / 2];
   // rows of tile t: neuron t*64 + j for j < 64 (clamped to the last active id)
   auto issue = [&](int t) {
-    const uint32_t myid = ids[min(t * kTileN + lane, max(n - 1, 0))];
+    const int ia = min(t * kTileN + lane, max(n - 1, 0));
+    const uint32_t myid = all ? (uint32_t)ia : ids[ia];
 #pragma unroll
     for (int r = 0; r < kTileN / 2; ++r) {
       const uint32_t id = (uint32_t)__shfl((int)myid, 2 * r + half);
@@ -442,7 +461,7 @@ __global__ __launch_bounds__(kSlideThreads) void neuron_tile_kernel(
     float s = -0.0f;
     for (int e = 0; e < nnz; ++e) s = __fadd_rn(s, __fmul_rn(wr[nzi[e]], nzv[e]));
     if (a < n) {
-      const float z = __fadd_rn(s, bias[ids[a]]);
+      const float z = __fadd_rn(s, bias[all ? (uint32_t)a : ids[a]]);
       prow[a] = z;
       lmax = fmaxf(lmax, z);
       if (act != KH_ACT_SOFTMAX) {
@@ -664,7 +683,11 @@ static int slide_forward_common(const kh_slide_layer* lc, const float* x, const 
   const int L = idx->L;
   WsSet* w = l->ws.get(st);
   uint32_t* codes = static_cast<uint32_t*>(w->get(0, sizeof(uint32_t) * batch * L));
-  const int qs = query_stride(idx);
+  // Vanilla sampling with every indexed id below the layer's neuron count
+  // keeps the whole query result (layer.rs:65-90), so the neuron kernel reads
+  // it directly and applies the empty-set fallback itself: no select launch.
+  const bool direct = !ov && l->sampling == KH_SAMPLING_VANILLA && idx->id_bound <= (uint32_t)l->n;
+  const int qs = direct ? std::max(query_stride(idx), l->n) : query_stride(idx);
   uint32_t* qids = static_cast<uint32_t*>(w->get(1, sizeof(uint32_t) * batch * qs));
   uint32_t* qcnt = static_cast<uint32_t*>(w->get(2, sizeof(uint32_t) * batch * qs));
   int32_t* qlen = static_cast<int32_t*>(w->get(3, sizeof(int32_t) * batch));
@@ -677,11 +700,14 @@ static int slide_forward_common(const kh_slide_layer* lc, const float* x, const 
   int rc = xoff ? hash_sparse_launch(idx->h, xoff, xidx, xval, batch, codes, st)
                 : hash_dense_launch(idx->h, x, l->dim, batch, codes, st);
   if (rc != KH_OK) return rc;
-  rc = query_launch(idx, codes, batch, qids, qcnt, qs, qlen, st);
+  rc = query_launch(idx, codes, batch, qids, direct ? nullptr : qcnt, qs, qlen, st);
   if (rc != KH_OK) return rc;
-  rc = ov ? select_launch_with(l->index, KH_SAMPLING_TOPK, ov->top_k, 0, l->n, qids, qcnt, qlen, qs,
-                              batch, aids, as, alen, true, nullptr, false, st)
-          : select_launch(l, qids, qcnt, qlen, qs, batch, aids, as, alen, false, nullptr, st);
+  if (direct)
+    aids = qids;  // stride qs == as
+  else
+    rc = ov ? select_launch_with(l->index, KH_SAMPLING_TOPK, ov->top_k, 0, l->n, qids, qcnt, qlen, qs,
+                                 batch, aids, as, alen, true, nullptr, false, st)
+            : select_launch(l, qids, qcnt, qlen, qs, batch, aids, as, alen, false, nullptr, st);
   if (rc != KH_OK) return rc;
   const int act = ov ? ov->act : l->act;
   const int max_nz = xoff ? 4096 : l->dim;
@@ -691,25 +717,30 @@ static int slide_forward_common(const kh_slide_layer* lc, const float* x, const 
   // blocks (softmax needs the whole row's max and sum in one block).
   constexpr int kNeuronSplit = 4;
   const dim3 ng((unsigned)batch, l->wtn ? kNeuronSplit : 1);
+  // direct: the candidate lengths come from the query, the fallback is the
+  // kernel's, and the kernel writes the lengths the outputs use
+  const int32_t* ilen = direct ? qlen : alen;
+  const int fb_n = direct ? l->n : 0;
+  int32_t* olen = direct ? alen : nullptr;
   if (xoff && l->wtn)
     hipLaunchKernelGGL((neuron_kernel<true, true>), ng, dim3(kSlideThreads), lds, st, l->wtn, l->n,
-                       l->bias, l->dim, nullptr, xoff, xidx, xval, aids, as, alen, act, max_nz,
-                       pre, post);
+                       l->bias, l->dim, nullptr, xoff, xidx, xval, aids, as, ilen, act, max_nz,
+                       pre, post, fb_n, olen);
   else if (xoff)
     hipLaunchKernelGGL((neuron_kernel<true, false>), ng, dim3(kSlideThreads), lds, st, l->w, l->n,
-                       l->bias, l->dim, nullptr, xoff, xidx, xval, aids, as, alen, act, max_nz,
-                       pre, post);
+                       l->bias, l->dim, nullptr, xoff, xidx, xval, aids, as, ilen, act, max_nz,
+                       pre, post, fb_n, olen);
   else if (l->wtn)
     hipLaunchKernelGGL((neuron_kernel<false, true>), ng, dim3(kSlideThreads), lds, st, l->wtn, l->n,
-                       l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, alen, act,
-                       max_nz, pre, post);
+                       l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, ilen, act,
+                       max_nz, pre, post, fb_n, olen);
   else if (l->dim <= kTileMaxDim && l->dim % 4 == 0 && tile_kernel_ready() == KH_OK)
     hipLaunchKernelGGL(neuron_tile_kernel, dim3((unsigned)batch), dim3(kSlideThreads), kTileLds, st, l->w,
-                       l->bias, l->dim, x, aids, as, alen, act, pre, post);
+                       l->bias, l->dim, x, aids, as, ilen, act, pre, post, fb_n, olen);
   else
     hipLaunchKernelGGL((neuron_kernel<false, false>), ng, dim3(kSlideThreads), lds, st, l->w, l->n,
-                       l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, alen, act,
-                       max_nz, pre, post);
+                       l->bias, l->dim, x, nullptr, nullptr, nullptr, aids, as, ilen, act,
+                       max_nz, pre, post, fb_n, olen);
   KH_LAUNCHED();
   return csr_finish(aids, nullptr, pre, post, as, alen, batch, off, act_ids, nullptr, pre_out,
                     act_out, capacity, st);
