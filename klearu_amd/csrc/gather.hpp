@@ -382,7 +382,7 @@ __global__ __launch_bounds__(64 * RW) void partials_reduce_kernel(const float* _
 // for a given number of partial rows.  (A template, so that each translation
 // unit including this header keeps its own copy.)
 constexpr int kRedCols = 32;
-constexpr int kRed16U = 16;     // loads per thread in flight
+constexpr int kRed16U = 32;     // loads per thread in flight (one pass over up to 256 rows)
 template <int C = kRedCols, int U = kRed16U>
 __global__ __launch_bounds__(256) void partials_reduce16_kernel(const float* __restrict__ partial, int H,
                                                                  int groups, float* __restrict__ y,
