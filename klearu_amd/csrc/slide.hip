@@ -552,14 +552,6 @@ __global__ __launch_bounds__(256) void dense_sparse_kernel(const float* __restri
   y[row * (int64_t)n + o] = r;
 }
 
-// out[r][0..n[r]) = src[r*stride ..] (n[r] <= ld), the ids of a top-k pick.
-__global__ void copy_rows_kernel(const uint32_t* __restrict__ src, int stride,
-                                 const int32_t* __restrict__ n, uint32_t* __restrict__ out, int ld) {
-  const int64_t r = blockIdx.x;
-  const int m = min(n[r], ld);
-  for (int i = threadIdx.x; i < m; i += blockDim.x) out[r * ld + i] = src[r * (int64_t)stride + i];
-}
-
 int select_launch_with(const kh_lsh_index* idx, int sampling, int top_k, int threshold,
                        int num_neurons, const uint32_t* qids, const uint32_t* qcnt,
                        const int32_t* qlen, int qs, int64_t batch, uint32_t* aids, int as,
@@ -818,18 +810,12 @@ extern "C" int kh_lsh_index_query_top_k(const kh_lsh_index* idx, const float* x_
   int rc = hash_dense_launch(idx->h, x_dev, idx->h->dim, batch, codes, st);
   if (rc == KH_OK) rc = query_launch(idx, codes, batch, qids, qcnt, qs, qlen, st);
   if (rc != KH_OK) return rc;
-  // count descending, then id, into the codes' slot (the query has read the
-  // codes by then: the calls are ordered on the stream)
+  // count descending, then id, straight into the caller's [batch][top_k]
+  // rows: the count-order selection writes only positions below
+  // min(top_k, candidates)
   const int k = static_cast<int>(std::min<int64_t>(top_k, qs));
-  uint32_t* picks = static_cast<uint32_t*>(w->get(4, sizeof(uint32_t) * batch * std::max(qs, L)));
-  if (!picks) return KH_ERR_ALLOC;
-  rc = select_launch_with(idx, KH_SAMPLING_TOPK, k, 0, 0x7fffffff, qids, qcnt, qlen, qs, batch, picks,
-                          qs, n_dev, true, nullptr, false, st);
-  if (rc != KH_OK || top_k == 0) return rc;
-  hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)batch), dim3(256), 0, st, picks, qs, n_dev, ids_dev,
-                     static_cast<int>(top_k));
-  KH_LAUNCHED();
-  return KH_OK;
+  return select_launch_with(idx, KH_SAMPLING_TOPK, k, 0, 0x7fffffff, qids, qcnt, qlen, qs, batch, ids_dev,
+                            static_cast<int>(top_k), n_dev, true, nullptr, false, st);
 }
 
 extern "C" int kh_dense_layer_create(int input_dim, int num_neurons, const float* w_host,
