@@ -99,12 +99,24 @@ __device__ __forceinline__ void topk_threshold(const uint32_t (&key)[KPT], int c
     ties = kk;
     if (hi < 0) break;  // every bit resolved: the bin is one key value
     if (sh.s_bincount <= kTopkCand) {
+      // Gather the bin's keys: one LDS atomic per wave reserves the wave's
+      // slots (a wave scan of the per-thread counts places each key).
+      using M = typename std::conditional<(KPT > 32), unsigned long long, uint32_t>::type;
+      M cm = 0;
 #pragma unroll
       for (int j = 0; j < KPT; ++j)
-        if (j < cnt && (key[j] & mask) == prefix) {
-          const int c = atomicAdd(&sh.s_ncand, 1);
-          sh.cand[c] = ((uint64_t)key[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)(i0 + j));
-        }
+        if (j < cnt) cm |= (M)((key[j] & mask) == prefix) << j;
+      const int c = (int)__popcll((unsigned long long)cm);
+      const int incl = wave_incl_scan(c);
+      const int wtot = __builtin_amdgcn_readlane(incl, 63);
+      if (wtot) {
+        int base = 0;
+        if ((threadIdx.x & 63) == 63) base = atomicAdd(&sh.s_ncand, wtot);
+        int at = __builtin_amdgcn_readlane(base, 63) + incl - c;
+#pragma unroll
+        for (int j = 0; j < KPT; ++j)
+          if ((cm >> j) & 1u) sh.cand[at++] = ((uint64_t)key[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)(i0 + j));
+      }
       __syncthreads();
       const int m = sh.s_ncand;
       // Four threads per candidate: thread t ranks candidate t/4 against a
