@@ -456,6 +456,88 @@ __global__ __launch_bounds__(kL2Threads) void pred_l2_kernel(const W* __restrict
   }
 }
 
+// Layer 2 for several rows (BF16 weights, n_hid <= kMaxL2Hid, n_hid % 8 == 0):
+// block (x, y) owns outputs [64 x, 64 x + 64) of rows [kL2Rows y, ...).  The
+// outputs' weight rows go to LDS once (one 1 KB direct load per 8-input block,
+// [block][output]), the rows' hidden vectors beside them, and wave w runs the
+// chains of rows 2w and 2w + 1: each weight read from LDS serves both rows.
+// The work is VALU-bound (a separately rounded multiply and add per term), so
+// blocks stay small (two waves) and every CU takes a few.  pred_l2_kernel
+// instead takes one row per block.  The chains, scores and key bounds are
+// pred_l2_kernel's.
+constexpr int kL2Rows = 4;
+constexpr int kL2RowThreads = 32 * kL2Rows;  // two rows per wave
+constexpr int kL2RowHs = kMaxL2Hid + 4;      // LDS row stride of the hidden vectors (floats)
+
+__global__ __launch_bounds__(kL2RowThreads) void pred_l2_rows_kernel(
+    const uint16_t* __restrict__ Wb, const float* __restrict__ bias, const float* __restrict__ hin, int n_hid,
+    int n_out, int batch, float* __restrict__ out, uint32_t* __restrict__ mm) {
+  __shared__ __align__(16) uint4 wl[kMaxL2Hid / 8][64];
+  __shared__ __align__(16) float hs[kL2Rows][kL2RowHs];
+  __shared__ uint64_t tab[32];
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int o = blockIdx.x * 64 + lane;
+  const bool ok = o < n_out;
+  const int oc = ok ? o : n_out - 1;
+  const int rb = blockIdx.y * kL2Rows;
+  const int nblk = n_hid >> 3;
+  const uint4* __restrict__ wv = reinterpret_cast<const uint4*>(Wb);
+  // weight rows: wave w loads 8-input blocks w, w + 8, ... (64 outputs, 1 KB each)
+  for (int jb = wave; jb < nblk; jb += kL2RowThreads / 64)
+    __builtin_amdgcn_global_load_lds(wv + (size_t)jb * n_out + oc, &wl[jb][0], 16, 0, 0);
+  // hidden vectors of the block's rows (rows past the batch repeat the last, unused)
+  const int n4 = n_hid >> 2;
+  for (int i = t; i < kL2Rows * n4; i += kL2RowThreads) {
+    const int r = i / n4, c = i - r * n4;
+    reinterpret_cast<float4*>(&hs[r][0])[c] =
+        reinterpret_cast<const float4*>(hin + (size_t)min(rb + r, batch - 1) * n_hid)[c];
+  }
+  if (t < 32) tab[t] = kExp2Tab[t];
+  const float bv = bias[oc];
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  const int r0 = 2 * wave, r1 = 2 * wave + 1;
+  const float4* h0 = reinterpret_cast<const float4*>(&hs[r0][0]);
+  const float4* h1 = reinterpret_cast<const float4*>(&hs[r1][0]);
+  float s0 = -0.0f, s1 = -0.0f;
+#pragma unroll 4
+  for (int jb = 0; jb < nblk; ++jb) {
+    float wf[8];
+    Blk8<uint16_t>::widen(wl[jb][lane], wf);
+    const float4 a0 = h0[2 * jb], a1 = h0[2 * jb + 1], c0 = h1[2 * jb], c1 = h1[2 * jb + 1];
+    s0 = __fadd_rn(s0, __fmul_rn(wf[0], a0.x));
+    s1 = __fadd_rn(s1, __fmul_rn(wf[0], c0.x));
+    s0 = __fadd_rn(s0, __fmul_rn(wf[1], a0.y));
+    s1 = __fadd_rn(s1, __fmul_rn(wf[1], c0.y));
+    s0 = __fadd_rn(s0, __fmul_rn(wf[2], a0.z));
+    s1 = __fadd_rn(s1, __fmul_rn(wf[2], c0.z));
+    s0 = __fadd_rn(s0, __fmul_rn(wf[3], a0.w));
+    s1 = __fadd_rn(s1, __fmul_rn(wf[3], c0.w));
+    s0 = __fadd_rn(s0, __fmul_rn(wf[4], a1.x));
+    s1 = __fadd_rn(s1, __fmul_rn(wf[4], c1.x));
+    s0 = __fadd_rn(s0, __fmul_rn(wf[5], a1.y));
+    s1 = __fadd_rn(s1, __fmul_rn(wf[5], c1.y));
+    s0 = __fadd_rn(s0, __fmul_rn(wf[6], a1.z));
+    s1 = __fadd_rn(s1, __fmul_rn(wf[6], c1.z));
+    s0 = __fadd_rn(s0, __fmul_rn(wf[7], a1.w));
+    s1 = __fadd_rn(s1, __fmul_rn(wf[7], c1.w));
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int b = rb + (u ? r1 : r0);
+    const float score = sigmoid_ref_t(__fadd_rn(u ? s1 : s0, bv), tab);
+    if (b < batch) {
+      if (ok) out[(size_t)b * n_out + o] = score;
+      if (mm) {
+        const uint32_t key = f32_key(score);
+        const uint32_t kmax = wave_max_u32(ok ? key : 0u);
+        const uint32_t kmin = wave_min_u32(ok ? key : 0xffffffffu);
+        if (lane == 0) reinterpret_cast<uint2*>(mm)[(size_t)b * gridDim.x + blockIdx.x] = make_uint2(kmin, kmax);
+      }
+    }
+  }
+}
+
 // Generic layer for shapes outside the fast kernels' limits: one lane per
 // output, sequential over the input.  act 0 = max(., 0), 1 = sigmoid.
 template <int ACT, typename W>
@@ -1072,7 +1154,11 @@ static int l2_typed(const kh_predictor* p, const float* hbuf, int64_t batch, flo
                        p->b2, hbuf, p->hid, p->out_dim, scores, nullptr, tk->k, tk->order,
                        tk->ids);
     tk->done = true;
-  } else if (p->hid <= kMaxL2Hid)
+  } else if (std::is_same<W, uint16_t>::value && batch > 1 && p->hid <= kMaxL2Hid && p->hid % 8 == 0)
+    hipLaunchKernelGGL(pred_l2_rows_kernel, dim3(l2_blocks(p), ceil_div(batch, kL2Rows)), dim3(kL2RowThreads), 0,
+                       st, reinterpret_cast<const uint16_t*>(w2), p->b2, hbuf, p->hid, p->out_dim,
+                       static_cast<int>(batch), scores, mm);
+  else if (p->hid <= kMaxL2Hid)
     hipLaunchKernelGGL(pred_l2_kernel<W>, dim3(l2_blocks(p), batch), dim3(kL2Threads), 0, st,
                        w2, p->b2, hbuf, p->hid, p->out_dim, scores, mm);
   else

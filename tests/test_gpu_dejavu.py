@@ -40,6 +40,10 @@ def make_predictor(orc, rng, ind, hid, out, bias=False):
     (1024, 13, 40, 130, True),
     (2048, 64, 300, 33, True),
     (128, 20, 77, 5, True),
+    # the batched BF16 layer 2 (hidden units a multiple of 8, rows > 1): the
+    # cases above with 128, 256 and 64 hidden units take it (outputs short of
+    # a 64-block, rows not a multiple of 4); here 3 blocks of 8 inputs.
+    (256, 24, 130, 6, True),
 ])
 def test_predictor_scores_bit_exact(kh, orc, ind, hid, out, batch, bias):
     from klearu_amd.dejavu import SparsityPredictor
