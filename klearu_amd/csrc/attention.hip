@@ -552,17 +552,20 @@ __device__ __forceinline__ void load_f4s(const float* __restrict__ p, float* f) 
 // positions.  Every row then holds exactly what the reference's f32 KvCache
 // holds (kv_cache.rs:33-48), and the bulk of a long prompt streams at BF16 width.
 //
-// Grid (n16 + n32, nsel + 1, batch).
-// Block (s < n16, a < nsel, b): BF16 chunk s (positions s*CH16 ..) of the prefix;
-// block (n16 + c, a, b): f32 chunk c (positions pre[b] + c*CH32 ..) of the rest,
-// including this step's row len[b] (taken from the projection).  Each writes
-// the un-normalised head output po[b][a][slot][D] and (max, exp-sum)
-// pml[b][a][slot] with slot = s, or ceil(pre[b] / CH16) + c: the slots of a
-// sequence follow its positions.  Blocks past the rows exit at once.
-// Block (s, nsel, b): appends this step's roped K and V of kv heads s, s+nsplit,
-// ... at position len[b] (f32 rows; decode blocks never read row len from the
-// cache), and writes zeros for union heads s, s+nsplit, ... that token b did
-// not select (the reference's zero-filled attn_concat, :44).
+// Grid (nsel + 1, batch, nsplit), slot index slowest: every block of slot s
+// is dispatched before any of slot s + 1, so the blocks past a sequence's
+// slots (nsplit covers a full-length cache in f32, far more slots than a
+// BF16 prefix takes) come last and exit while the last chunks run.  The slots
+// of sequence b follow its positions: slots [0, n16b) with n16b =
+// ceil(pre[b] / CH16) are the BF16 chunks of the prefix (slot c: positions
+// c*CH16 ..), then the f32 chunks of the rest (slot n16b + c: positions
+// pre[b] + c*CH32 ..), up to and including this step's row len[b] (taken from
+// the projection).  Block (a < nsel, b, s) takes slot s and writes its
+// un-normalised head output po[b][a][s][D] and (max, exp-sum) pml[b][a][s].
+// Block (nsel, b, s): appends this step's roped K and V of kv heads s,
+// s+nsplit, ... at position len[b] (f32 rows; decode blocks never read row len
+// from the cache), and writes zeros for union heads s, s+nsplit, ... that
+// token b did not select (the reference's zero-filled attn_concat, :44).
 template <typename KV, int D>
 __device__ __forceinline__ void attn_decode_chunk(
     const KV* __restrict__ kc, const KV* __restrict__ vc, int start, int seg_end, int slot,
@@ -577,6 +580,9 @@ __device__ __forceinline__ void attn_decode_chunk(
   constexpr int CH = RPP * NP;                  // positions per chunk
   constexpr int HALF = D / 2;
   constexpr int NW = kAttnThreads / 64;
+  // Only f32 chunks can hold position len (BF16 chunks cover [0, pre) and
+  // pre <= len), so only they load this step's k and v.
+  constexpr bool kCur = std::is_same<KV, float>::value;
   static_assert(LPR <= 64 && kAttnThreads % LPR == 0 && CH <= kAttnThreads, "tiling");
   static_assert(HALF % EPL == 0 && EPL % 4 == 0, "a lane's slice lies in one half of the head");
   __shared__ float s_p[CH];
@@ -605,9 +611,11 @@ __device__ __forceinline__ void attn_decode_chunk(
   float qx[EPL], qp[EPL], kx[EPL], kp[EPL], vn[EPL], cs[EPL], sn[EPL];
   load_f4s<EPL>(qsrc + e0, qx);
   load_f4s<EPL>(qsrc + ep, qp);
-  load_f4s<EPL>(kcur + e0, kx);
-  load_f4s<EPL>(kcur + ep, kp);
-  load_f4s<EPL>(kcur + kvd + e0, vn);
+  if constexpr (kCur) {
+    load_f4s<EPL>(kcur + e0, kx);
+    load_f4s<EPL>(kcur + ep, kp);
+    load_f4s<EPL>(kcur + kvd + e0, vn);
+  }
   load_f4s<EPL>(ct + ec, cs);
   load_f4s<EPL>(st + ec, sn);
   __builtin_amdgcn_sched_barrier(0);
@@ -632,7 +640,7 @@ __device__ __forceinline__ void attn_decode_chunk(
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     qv[e] = qx[e] * cs[e] + (first ? -qp[e] : qp[e]) * sn[e];
-    kn[e] = kx[e] * cs[e] + (first ? -kp[e] : kp[e]) * sn[e];
+    if constexpr (kCur) kn[e] = kx[e] * cs[e] + (first ? -kp[e] : kp[e]) * sn[e];
   }
   // scores: dense_dot(q, k_j) * inv_sqrt_dk (:55-58)
 #pragma unroll
@@ -640,9 +648,11 @@ __device__ __forceinline__ void attn_decode_chunk(
     const int j = start + p * RPP + r0;
     float kf[EPL];
     widen16(kr[p], kf, KV());
-    if (j == len) {
+    if constexpr (kCur) {
+      if (j == len) {
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) kf[e] = kn[e];
+        for (int e = 0; e < EPL; ++e) kf[e] = kn[e];
+      }
     }
     float d = 0.0f;
 #pragma unroll
@@ -684,9 +694,11 @@ __device__ __forceinline__ void attn_decode_chunk(
     if (jj < n) {
       float vf[EPL];
       widen16(vr[p], vf, KV());
-      if (start + jj == len) {
+      if constexpr (kCur) {
+        if (start + jj == len) {
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) vf[e] = vn[e];
+          for (int e = 0; e < EPL; ++e) vf[e] = vn[e];
+        }
       }
       const float pj = s_p[jj];
 #pragma unroll
@@ -715,7 +727,7 @@ __device__ __forceinline__ void attn_decode_chunk(
 template <int D>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     const uint16_t* __restrict__ kc16, const uint16_t* __restrict__ vc16, float* __restrict__ kc32,
-    float* __restrict__ vc32, const int32_t* __restrict__ pre, int n16, const float* __restrict__ y,
+    float* __restrict__ vc32, const int32_t* __restrict__ pre, const float* __restrict__ y,
     int ystride, int nkv, int nh, const int32_t* __restrict__ heads, int nsel,
     const int32_t* __restrict__ lens, const int64_t* __restrict__ positions,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, int max_seq, float inv_sqrt,
@@ -723,7 +735,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     float* __restrict__ cat, int catstride) {
   constexpr int HALF = D / 2;
   constexpr int CH16 = attn_chunk<uint16_t, D>(), CH32 = attn_chunk<float, D>();
-  const int s = blockIdx.x, a = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
+  const int a = blockIdx.x, b = blockIdx.y, s = blockIdx.z, t = threadIdx.x;
   const int len = lens[b];
   const bool valid = len < max_seq;  // a full cache refuses the step for this sequence
   int64_t pos = positions ? positions[b] : len;
@@ -736,7 +748,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   if (a == nsel) {
     if (valid) {
       // KvCache::append (kv_cache.rs:33-48) of the roped k (sparse_attention.rs:33-39)
-      for (int hh = s; hh < nkv; hh += nsplit) {
+      for (int hh = s; hh < nkv; hh += (int)gridDim.z) {
         const float* kx = yb + (size_t)hh * D;
         const float* vx = kx + kvd;
         const size_t dst = (((size_t)b * nkv + hh) * max_seq + len) * D;
@@ -749,7 +761,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
         }
       }
     }
-    for (int hu = s; hu < nh; hu += nsplit) {
+    for (int hu = s; hu < nh; hu += (int)gridDim.z) {
       const int u = urank[hu];
       if (u < 0) continue;
       int sel = 0;
@@ -762,14 +774,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   }
   if (!valid) return;
   const int pb = pre[b];
-  if (s < n16) {
+  const int n16b = (pb + CH16 - 1) / CH16;
+  const int ns = n16b + (len + 1 - pb + CH32 - 1) / CH32;
+  if (s >= ns) return;
+  if (s < n16b)
     attn_decode_chunk<uint16_t, D>(kc16, vc16, s * CH16, pb, s, yb, kvd, nh, nkv, hb, a, b, len, ct, st,
                                    max_seq, inv_sqrt, nsel, nsplit, po, pml);
-  } else {
-    const int c = s - n16;
-    attn_decode_chunk<float, D>(kc32, vc32, pb + c * CH32, len + 1, (pb + CH16 - 1) / CH16 + c, yb, kvd, nh,
-                                nkv, hb, a, b, len, ct, st, max_seq, inv_sqrt, nsel, nsplit, po, pml);
-  }
+  else
+    attn_decode_chunk<float, D>(kc32, vc32, pb + (s - n16b) * CH32, len + 1, s, yb, kvd, nh, nkv, hb, a, b, len,
+                                ct, st, max_seq, inv_sqrt, nsel, nsplit, po, pml);
 }
 
 // Decode slots of a sequence: the BF16 chunks covering rows [0, pre), then the
@@ -1404,11 +1417,11 @@ extern "C" int kh_sparse_attn_clear(kh_sparse_attn* a, void* stream) {
 
 template <int D>
 static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
-                              const int32_t* heads, int nsel, int n16, int nsplit, float* po,
+                              const int32_t* heads, int nsel, int nsplit, float* po,
                               float2* pml, bool merge, hipStream_t st) {
   const int qd = a->nh * D;
-  hipLaunchKernelGGL(attn_decode_kernel<D>, dim3(nsplit, nsel + 1, batch), dim3(kAttnThreads), 0, st,
-                     a->kc16, a->vc16, a->kc32, a->vc32, a->pre, n16, a->y, a->ystride(), a->nkv, a->nh,
+  hipLaunchKernelGGL(attn_decode_kernel<D>, dim3(nsel + 1, batch, nsplit), dim3(kAttnThreads), 0, st,
+                     a->kc16, a->vc16, a->kc32, a->vc32, a->pre, a->y, a->ystride(), a->nkv, a->nh,
                      heads, nsel, a->lens, pos, a->cos_t, a->sin_t, a->max_seq,
                      1.0f / sqrtf(static_cast<float>(D)), nsplit, a->qrows + qd + 1, po, pml, a->cat, qd);
   KH_LAUNCHED();
@@ -1510,9 +1523,9 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   // separate merge, one block per (entry, token), is faster)
   constexpr int kFoldNB = NB <= 2 ? NB : 2;
   const bool fold = NB <= 2 && nsel <= kOprojMaxSel;
-  int rc = D == 64 ? attn_decode_launch<64>(a, batch, pos, heads, nsel, n16, nsplit, po, pml, !fold, st)
-         : D == 128 ? attn_decode_launch<128>(a, batch, pos, heads, nsel, n16, nsplit, po, pml, !fold, st)
-                    : attn_decode_launch<256>(a, batch, pos, heads, nsel, n16, nsplit, po, pml, !fold, st);
+  int rc = D == 64 ? attn_decode_launch<64>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st)
+         : D == 128 ? attn_decode_launch<128>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st)
+                    : attn_decode_launch<256>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st);
   if (rc != KH_OK) return rc;
   // 3. o_proj over the union heads' rows of WoT, then the ordered reduce
   const int nslices = ceil_div(H, kSlice);
