@@ -1528,8 +1528,11 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
                     : attn_decode_launch<256>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st);
   if (rc != KH_OK) return rc;
   // 3. o_proj over the union heads' rows of WoT, then the ordered reduce
+  //    (batch > 2: 128-row groups on the BF16 matrix cores)
+  constexpr int kDbRowsAttn = 128;
+  const bool bf_oproj = !fold && H % kDbCols == 0 && ceil_div(qd, kDbRowsAttn) <= kMaxGroups;
   const int nslices = ceil_div(H, kSlice);
-  const int groups = gather_groups(qd, nslices);
+  const int groups = bf_oproj ? ceil_div(qd, kDbRowsAttn) : gather_groups(qd, nslices);
   if (groups == 0) {
     set_error("num_heads*head_dim %d too large for the o_proj gather", qd);
     return KH_ERR_UNSUPPORTED;
@@ -1540,7 +1543,18 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
     hipLaunchKernelGGL(attn_oproj_kernel<kFoldNB>, dim3(nslices, groups), dim3(kOprojThreads), 0,
                        st, a->wot, H, D, a->qrows, qd, a->qrows + qd, po, pml, nsplit, ch16, ch32,
                        a->pre, heads, nsel, a->lens, a->max_seq, batch, groups, partial);
-  else
+  else if (bf_oproj) {
+    static std::once_flag once;
+    static hipError_t arc = hipSuccess;
+    std::call_once(once, [] {
+      arc = hipFuncSetAttribute(reinterpret_cast<const void*>(&down_bf_kernel<NB, kDbRowsAttn>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)db_lds(kDbRowsAttn));
+    });
+    KH_HIP(arc);
+    hipLaunchKernelGGL((down_bf_kernel<NB, kDbRowsAttn>), dim3(H / kDbCols, groups), dim3(64 * kDbWaves),
+                       db_lds(kDbRowsAttn), st, a->wot, H, a->qrows, qd, a->qrows + qd, qd, a->cat, qd, batch,
+                       partial);
+  } else
     hipLaunchKernelGGL(gather_rows_kernel<NB>, dim3(nslices, groups), dim3(kDownThreads), 0, st,
                        a->wot, H, a->qrows, qd, a->qrows + qd, qd, a->cat, qd, batch, groups,
                        partial);

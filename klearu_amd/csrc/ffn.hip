@@ -26,9 +26,10 @@
 //                          contiguous loads, 16x16 tiles on MFMA (x split into
 //                          BF16 hi/lo); otherwise ffn_gateup, one wave per
 //                          active neuron, tokens staged in LDS;
-//             down_lds (hidden a multiple of 512; gather.hpp) row groups x
-//                          512-column slices, rows streamed through LDS, f32
-//                          MFMA; otherwise down_mfma / down_rows / gather_rows;
+//             down_bf (hidden a multiple of 512; gather.hpp) 256-row groups
+//                          x 512-column slices, rows staged transposed through
+//                          LDS, BF16 MFMA with h split into hi/lo; otherwise
+//                          down_mfma / down_rows / gather_rows;
 //             partials_reduce  as above.
 // No float atomics: the summation order is fixed, so outputs are deterministic.
 #include <algorithm>
@@ -752,18 +753,20 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
   }
   KH_LAUNCHED();
   int groups;
-  if (NB > 1 && H % kDlCols == 0) {
-    // several tokens: row groups on the matrix cores (f32 MFMA), weights
-    // staged through LDS with contiguous loads
+  constexpr int kDbRowsFfn = 256;
+  if (NB > 1 && H % kDbCols == 0 && ceil_div(n_active, kDbRowsFfn) <= kMaxGroups) {
+    // several tokens: 256-row groups on the BF16 matrix cores, weights
+    // staged transposed through LDS with contiguous loads
+    constexpr int GR = kDbRowsFfn;
     static std::once_flag once;
     static hipError_t arc = hipSuccess;
     std::call_once(once, [] {
-      arc = hipFuncSetAttribute(reinterpret_cast<const void*>(&down_lds_kernel<NB>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDlLds);
+      arc = hipFuncSetAttribute(reinterpret_cast<const void*>(&down_bf_kernel<NB, GR>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)db_lds(GR));
     });
     KH_HIP(arc);
-    groups = ceil_div(n_active, kDlRows);
-    hipLaunchKernelGGL(down_lds_kernel<NB>, dim3(H / kDlCols, groups), dim3(64 * kDlWaves), kDlLds, st,
+    groups = ceil_div(n_active, GR);
+    hipLaunchKernelGGL((down_bf_kernel<NB, GR>), dim3(H / kDbCols, groups), dim3(64 * kDbWaves), db_lds(GR), st,
                        f->wdt, H, active, n_active, n_active_dev, f->inter, hbuf, f->inter, batch, partial);
   } else if (NB > 1 && H % kDmCols == 0) {
     // several tokens: 512-row groups on the matrix cores (f32 MFMA)

@@ -451,140 +451,150 @@ inline int gather_groups(int n_rows, int nslices) {
   return groups;
 }
 
-// Down projection of up to 16 tokens with contiguous weight loads: as
-// down_mfma_kernel (f32 MFMA 16x16x4, A = h, B = the weight rows as stored),
-// but each load instruction reads one kDlCols-column piece of a row (a full
-// wave, 1 KB) into LDS, double-buffered in chunks of kDlChunk rows, and the
-// MFMA operands are read from there (kDlPer rows of each chunk per wave; the
-// loads of the next chunk are in flight while one is multiplied).  A block
-// covers kDlCols columns and kDlRows active rows; wave w takes the column
-// quarter w % 4 and the row half w / 4 of every chunk, and the two halves are
-// added in order through LDS.  Measured at the 7B shape, batch 16 (|U| about
-// 7858): 20.8 us against 23.0 for down_mfma_kernel; a second register stage
-// (two chunks in flight) or 64-row chunks were slower (21.3 / 22.6 us).
-constexpr int kDlCols = 512;
-constexpr int kDlRows = 256;
-constexpr int kDlChunk = 32;
-constexpr int kDlWaves = 8;
-constexpr int kDlRowQ = kDlCols / 8 + 1;  // uint4 per LDS row (one of padding)
-constexpr size_t kDlLds = sizeof(int) * kDlRows + sizeof(float) * kDlRows * 16 +
-                          sizeof(uint4) * 2 * kDlChunk * kDlRowQ;
-constexpr int kDlPer = kDlChunk / kDlWaves;  // rows each wave loads per chunk
-static_assert(kDlChunk % kDlWaves == 0 && kDlChunk % 8 == 0, "chunk rows split over the waves and the two row halves");
-static_assert(sizeof(float) * 16 * kDlCols <= sizeof(uint4) * 2 * kDlChunk * kDlRowQ,
-              "the row-half sums fit in the weight buffers");
+// Down projection of up to 16 tokens on the BF16 matrix cores: the products
+// sum_r h[t][r] M[rows[r]][c] as v_mfma_f32_16x16x32_bf16 with h split into
+// BF16 hi and lo terms (h = hi + lo + e, |e| <= 2^-17 |h|; the products with
+// the BF16 weights are exact in f32), an eighth of the matrix-core time of
+// the f32 MFMA.  The MFMA takes 8 consecutive k (here rows) per lane, so each
+// 32-row chunk is stored transposed in LDS: wave w loads rows 8 w .. 8 w + 7
+// of the chunk (16 bytes of 8 columns per lane, 1 KB per row piece), packs
+// each column's 8 values into 16 bytes and writes them at [8-column group]
+// [column][8-row block] (column stride kDbE, group stride kDbG: 8 lanes'
+// 16-byte writes and 8 lanes' 16-byte operand reads each fall in distinct
+// banks).  Block (slice, group): kDbCols columns x GR rows; wave w owns the
+// columns [128 w, 128 w + 128) (8 tiles of 16) over every row, so no sum
+// across waves is needed.  Chunks are double-buffered: the loads of chunk
+// c + 2 are in flight while chunk c is multiplied.  Rows past the group's
+// count reread its last row with h = 0.  Partial rows partial[group][token][H]
+// as gather_rows_kernel's.  Measured at the 7B shape: batch 16, |U| about
+// 7858, 256-row groups: 17.8 us against 21.1 for the same tiling on f32 MFMA
+// (B read from row-major LDS); batch 8 o_proj over about 30 heads, 128-row
+// groups: 10.2 us against 14.5 for gather_rows_kernel.  Two chunks in flight
+// in registers, h staged after the first weight loads, or a slice-major
+// weight copy (each block's rows contiguous) changed it by 0.3-0.6 us.
+constexpr int kDbCols = 512;
+constexpr int kDbChunk = 32;                  // rows per chunk (the MFMA's k)
+constexpr int kDbWaves = 4;
+constexpr int kDbE = 2 * kDbChunk + 16;       // bytes per column (64 data)
+constexpr int kDbG = 8 * kDbE + 16;           // bytes per 8-column group
+constexpr int kDbBuf = (kDbCols / 8) * kDbG;  // bytes per chunk buffer
+static_assert(kDbChunk == 8 * kDbWaves && kDbCols == 128 * kDbWaves, "tiling");
 
-template <int NB>
-__global__ __launch_bounds__(64 * kDlWaves) void down_lds_kernel(
+__host__ __device__ constexpr int db_hs(int GR) { return GR + 8; }  // h row stride (BF16 values)
+__host__ __device__ constexpr size_t db_lds(int GR) {
+  return 2 * (size_t)kDbBuf + 2 * sizeof(uint16_t) * 16 * db_hs(GR) + sizeof(int) * GR;
+}
+
+template <int NB, int GR>
+__global__ __launch_bounds__(64 * kDbWaves) void down_bf_kernel(
     const uint16_t* __restrict__ WdT, int H, const int32_t* __restrict__ active, int n_active,
     const int32_t* __restrict__ n_active_dev, int nrows, const float* __restrict__ hbuf,
     int hstride, int batch, float* __restrict__ partial) {
-  static_assert(NB <= 16, "16 token rows per MFMA tile");
-  extern __shared__ uint4 dl_lds[];
-  uint4* wbuf = dl_lds;                                                      // [2][kDlChunk][kDlRowQ]
-  float* s_h = reinterpret_cast<float*>(dl_lds + 2 * kDlChunk * kDlRowQ);   // [kDlRows][16]
-  int* s_ids = reinterpret_cast<int*>(s_h + kDlRows * 16);                  // [kDlRows]
+  static_assert(NB <= 16 && GR % kDbChunk == 0, "tiling");
+  constexpr int HS = db_hs(GR);
+  constexpr int NT = 64 * kDbWaves;
+  extern __shared__ uint4 db_lds_mem[];
+  uint8_t* wbuf = reinterpret_cast<uint8_t*>(db_lds_mem);                // [2][kDbBuf]
+  uint16_t* s_hh = reinterpret_cast<uint16_t*>(wbuf + 2 * kDbBuf);      // [16][HS]
+  uint16_t* s_hl = s_hh + 16 * HS;                                       // [16][HS]
+  int* s_ids = reinterpret_cast<int*>(s_hl + 16 * HS);                   // [GR]
   int n = n_active;
   if (n_active_dev) n = min(n, *n_active_dev);
   const int slice = blockIdx.x, grp = blockIdx.y;
   const int tid = threadIdx.x;
-  const int r0 = grp * kDlRows;
-  const int nr = max(0, min(kDlRows, n - r0));
-  const int last = max(n, 1) - 1;
+  const int r0 = grp * GR;
+  const int nr = max(0, min(GR, n - r0));
   if (nr == 0) {
     // a group past the device count contributes zeros (the reduce adds every group)
     for (int t = 0; t < batch; ++t)
-      for (int c = tid; c < kDlCols; c += 64 * kDlWaves)
-        partial[((size_t)grp * NB + t) * H + slice * kDlCols + c] = 0.0f;
+      for (int c = tid; c < kDbCols; c += NT) partial[((size_t)grp * NB + t) * H + slice * kDbCols + c] = 0.0f;
     return;
   }
-  for (int i = tid; i < kDlRows; i += 64 * kDlWaves) s_ids[i] = checked_row(active[min(r0 + i, last)], nrows, nullptr);
+  const int last = n - 1;
+  for (int i = tid; i < GR; i += NT) s_ids[i] = checked_row(active[min(r0 + i, last)], nrows, nullptr);
+  // h of token t, rows 8 j .. 8 j + 7 -> BF16 hi and lo terms (0 past the batch and past nr)
+  for (int i = tid; i < 16 * GR / 8; i += NT) {
+    const int t = i / (GR / 8), j = i - t * (GR / 8);
+    const float* src = hbuf + (size_t)min(t, batch - 1) * hstride;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int r = 8 * j + e;
+      v[e] = (t < batch && r < nr) ? src[min(r0 + r, last)] : 0.0f;
+    }
+    uint4 hi, lo;
+    split_bf16x8(make_float4(v[0], v[1], v[2], v[3]), make_float4(v[4], v[5], v[6], v[7]), hi, lo);
+    *reinterpret_cast<uint4*>(s_hh + t * HS + 8 * j) = hi;
+    *reinterpret_cast<uint4*>(s_hl + t * HS + 8 * j) = lo;
+  }
   lds_barrier();
   const int wave = tid >> 6, lane = tid & 63;
-  const int nch = (nr + kDlChunk - 1) / kDlChunk;
-  const uint16_t* __restrict__ wcol = WdT + (size_t)slice * kDlCols + 8 * lane;
-  uint4 st[kDlPer];
+  const int nch = (nr + kDbChunk - 1) / kDbChunk;
+  const uint16_t* __restrict__ wcol = WdT + (size_t)slice * kDbCols + 8 * lane;
+  uint4 st[8];
   auto load = [&](int c) {  // clamped: rows past nr reread the last row (h = 0)
 #pragma unroll
-    for (int i = 0; i < kDlPer; ++i) {
-      const int r = min(c * kDlChunk + kDlPer * wave + i, nr - 1);
+    for (int i = 0; i < 8; ++i) {
+      const int r = min(c * kDbChunk + 8 * wave + i, nr - 1);
       st[i] = ld_stream(reinterpret_cast<const uint4*>(wcol + (size_t)s_ids[r] * H));
     }
   };
+  // column 8 lane + e of rows 8 wave .. 8 wave + 7 -> 16 bytes at [lane][e][wave]
   auto store = [&](int b) {
+    uint8_t* dst = wbuf + b * kDbBuf + lane * kDbG + 16 * wave;
 #pragma unroll
-    for (int i = 0; i < kDlPer; ++i) wbuf[(b * kDlChunk + kDlPer * wave + i) * kDlRowQ + lane] = st[i];
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+      uint32_t w[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint4 v = st[i];
+        w[i] = (e >> 1) == 0 ? v.x : (e >> 1) == 1 ? v.y : (e >> 1) == 2 ? v.z : v.w;
+      }
+      *reinterpret_cast<uint4*>(dst + e * kDbE) =
+          make_uint4(__builtin_amdgcn_perm(w[1], w[0], sel), __builtin_amdgcn_perm(w[3], w[2], sel),
+                     __builtin_amdgcn_perm(w[5], w[4], sel), __builtin_amdgcn_perm(w[7], w[6], sel));
+    }
   };
   load(0);
   __builtin_amdgcn_sched_barrier(0);
-  // h of token t, row r -> s_h[r * 16 + t] (0 past the batch and past nr)
-  constexpr int kHPer = kDlRows * 16 / (64 * kDlWaves);
-  {
-    float v[kHPer];
-#pragma unroll
-    for (int q = 0; q < kHPer; ++q) {
-      const int i = tid + q * 64 * kDlWaves;
-      const int t = i / kDlRows, r = i - t * kDlRows;
-      v[q] = hbuf[(size_t)min(t, batch - 1) * hstride + min(r0 + r, last)];
-    }
-#pragma unroll
-    for (int q = 0; q < kHPer; ++q) {
-      const int i = tid + q * 64 * kDlWaves;
-      const int t = i / kDlRows, r = i - t * kDlRows;
-      s_h[r * 16 + t] = (t < batch && r < nr) ? v[q] : 0.0f;
-    }
-  }
   store(0);
-  load(1);
+  if (nch > 1) load(1);
   __builtin_amdgcn_sched_barrier(0);
   lds_barrier();
-  const int kq = lane >> 4, p = lane & 15;
-  const int cq = wave & 3, rh = wave >> 2;
+  // operands: A[t][k] = h[t][chunk row k], lane: t = lane % 16, k = 8 (lane / 16) + i;
+  // B[k][n] = M[chunk row k][column 128 wave + 16 j + n], n = lane % 16
+  const int t = lane & 15, kq = lane >> 4;
+  const int bcol = 128 * wave + t;  // + 16 j
   kh_f32x4 acc[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = kh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  auto mul = [&](int c) {
-    const uint4* buf = wbuf + (c & 1) * kDlChunk * kDlRowQ;
-#pragma unroll
-    for (int kg = 0; kg < kDlChunk / 8; ++kg) {
-      // rows 4g + kq of the chunk, g = rh * 4 + kg; columns 128 cq + 8 p + e
-      const int rl = 4 * (rh * (kDlChunk / 8) + kg) + kq;
-      const float a = s_h[min(c * kDlChunk + rl, kDlRows - 1) * 16 + p];
-      const uint4 w = buf[rl * kDlRowQ + 16 * cq + p];
-      const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float bv = (e & 1) ? bf16_hi(wv[e >> 1]) : bf16_lo(wv[e >> 1]);
-        acc[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv, acc[e], 0, 0, 0);
-      }
-    }
-  };
+  for (int j = 0; j < 8; ++j) acc[j] = kh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   for (int c = 0; c < nch; ++c) {
-    mul(c);
+    const uint8_t* buf = wbuf + (c & 1) * kDbBuf;
+    const uint4 ah = *reinterpret_cast<const uint4*>(s_hh + t * HS + c * kDbChunk + 8 * kq);
+    const uint4 al = *reinterpret_cast<const uint4*>(s_hl + t * HS + c * kDbChunk + 8 * kq);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int col = bcol + 16 * j;
+      const uint4 b = *reinterpret_cast<const uint4*>(buf + (col >> 3) * kDbG + (col & 7) * kDbE + 16 * kq);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ah), as_bf16x8(b), acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(al), as_bf16x8(b), acc[j], 0, 0, 0);
+    }
     if (c + 1 < nch) {
       store((c + 1) & 1);
-      load(c + 2);
+      if (c + 2 < nch) load(c + 2);
       __builtin_amdgcn_sched_barrier(0);
     }
     lds_barrier();
   }
-  // D[token 4kq + q][column 128 cq + 8p + e]: the second row half through LDS
-  float* red = reinterpret_cast<float*>(wbuf);  // [16][kDlCols]
-  if (rh == 1) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) red[(4 * kq + q) * kDlCols + 128 * cq + 8 * p + e] = acc[e][q];
-  }
-  lds_barrier();
-  if (rh == 1) return;
+  // C[token 4 kq + q][column 16 j + t]
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const int t = 4 * kq + q;
-    if (t < batch) {
-      float* o = partial + ((size_t)grp * NB + t) * H + slice * kDlCols + 128 * cq + 8 * p;
+    const int tok = 4 * kq + q;
+    if (tok < batch) {
+      float* o = partial + ((size_t)grp * NB + tok) * H + slice * kDbCols + bcol;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = acc[e][q] + red[t * kDlCols + 128 * cq + 8 * p + e];
+      for (int j = 0; j < 8; ++j) o[16 * j] = acc[j][q];
     }
   }
 }
