@@ -268,7 +268,7 @@ def attn_leg(name, L, B, steps, warmup, seed, timer, cpu_seconds):
     from klearu_amd import _lib
     from klearu_amd._dev import ptr, stream_ptr
     from klearu_amd.attention import SparseAttention
-    from klearu_amd.dejavu import ORDER_ASCENDING, SparsityPredictor
+    from klearu_amd.dejavu import SparsityPredictor
 
     H, nh, nkv, d, S, R, k = 4096, 32, 32, 128, 2048, 128, 16
     pre = S - (warmup + steps + 8)        # every replay appends one position per sequence
@@ -295,7 +295,6 @@ def attn_leg(name, L, B, steps, warmup, seed, timer, cpu_seconds):
     log(f"[bench] {name}: {L} attention layers ready in {time.time() - t0:.1f}s (cache {pre}, batch {B})")
     w_norm = torch.ones(H, device="cuda")
     hidden = torch.randn(B, H, generator=g, device="cuda")
-    norm = torch.empty_like(hidden)
     heads = [torch.empty(B, k, dtype=torch.int32, device="cuda") for _ in range(L)]
     norm_ws = torch.empty(B, dtype=torch.float32, device="cuda")
 
@@ -307,11 +306,11 @@ def attn_leg(name, L, B, steps, warmup, seed, timer, cpu_seconds):
                 _lib.call("kh_dejavu_attn_block", preds[l]._h, layers[l]._h, ptr(hidden), ptr(w_norm), 1e-5, k,
                           ptr(heads[l]), ptr(norm_ws), st)
             return
+        # batched fused block: each row's exact RmsNorm inside the predictor's layer 1,
+        # the head predictor's layer 2 and top k inside the q/k/v projection
         for l in range(L):
-            _lib.call("kh_rmsnorm", ptr(hidden), ptr(w_norm), B, H, 1e-5, ptr(norm), st)
-            _lib.call("kh_predictor_select_top_k", preds[l]._h, ptr(norm), B, k, ORDER_ASCENDING, ptr(heads[l]), st)
-            _lib.call("kh_sparse_attn_forward", layers[l]._h, ptr(norm), B, None, ptr(heads[l]), k, ptr(hidden),
-                      1, st)
+            _lib.call("kh_dejavu_attn_block_batch", preds[l]._h, layers[l]._h, ptr(hidden), B, ptr(w_norm), 1e-5,
+                      k, ptr(heads[l]), ptr(norm_ws), st)
 
     gr = timer.graph(step)
     ms = timer.time(gr.replay, steps, warmup)

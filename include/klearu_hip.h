@@ -649,6 +649,19 @@ int kh_sparse_attn_forward(kh_sparse_attn* a, const float* x_dev, int64_t batch,
 int kh_dejavu_attn_block(const kh_predictor* p, kh_sparse_attn* a, float* hidden_dev,
                          const float* norm_w_dev, float eps, int k, int32_t* heads_dev,
                          float* norm_ws_dev, void* stream);
+/* kh_dejavu_attn_block for sequences 0..batch-1, one decode step each
+ * (sparse/mod.rs:56-112 per token; the reference decodes a batch one token at
+ * a time): hidden_dev[batch][hidden] in place, heads_dev[batch][k] (ascending
+ * per row), norm_ws_dev[batch] the rows' RmsNorm scales.  Each row's norm and
+ * head selection are bit-identical to the reference's; layer 2 of the head
+ * predictor and the top k run inside the q/k/v projection.  batch 1 is
+ * kh_dejavu_attn_block.  Requires, beyond kh_dejavu_attn_block's limits,
+ * hidden a multiple of 1024, at most 64 heads and a head predictor with at
+ * most 128 hidden units (else KH_ERR_UNSUPPORTED: use kh_rmsnorm,
+ * kh_predictor_select_top_k and kh_sparse_attn_forward). */
+int kh_dejavu_attn_block_batch(const kh_predictor* p, kh_sparse_attn* a, float* hidden_dev,
+                               int64_t batch, const float* norm_w_dev, float eps, int k,
+                               int32_t* heads_dev, float* norm_ws_dev, void* stream);
 
 /* ======================================================================== */
 /* On-disk formats: safetensors weights and predictor JSON files            */

@@ -152,3 +152,19 @@ def attn_block(predictor, attn: SparseAttention, hidden: torch.Tensor, norm_w: t
     _lib.call("kh_dejavu_attn_block", predictor._h, attn._h, ptr(hidden), ptr(norm_w), float(eps), k, ptr(heads),
               ptr(norm_ws), stream_ptr(stream))
     return heads
+
+
+def attn_block_batch(predictor, attn: SparseAttention, hidden: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                     k: int, heads: torch.Tensor | None = None, norm_ws: torch.Tensor | None = None, stream=None):
+    """attn_block for sequences 0..B-1 of hidden [B][hidden], one decode step each (the
+    reference decodes a batch one token at a time, crates/klearu-llm/src/sparse/mod.rs:56-112):
+    each row's norm and head selection are the reference's, bit for bit.  `norm_ws` [B]
+    receives the rows' RmsNorm scales.  Returns the heads [B][k] (ascending per row)."""
+    B = hidden.shape[0]
+    if norm_ws is None:
+        norm_ws = torch.empty(B, dtype=torch.float32, device=hidden.device)
+    if heads is None:
+        heads = torch.empty(B, k, dtype=torch.int32, device=hidden.device)
+    _lib.call("kh_dejavu_attn_block_batch", predictor._h, attn._h, ptr(hidden), B, ptr(norm_w), float(eps), k,
+              ptr(heads), ptr(norm_ws), stream_ptr(stream))
+    return heads

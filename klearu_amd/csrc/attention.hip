@@ -149,6 +149,46 @@ __device__ __forceinline__ void attn_select_heads(const PW* __restrict__ w2, con
   __syncthreads();
 }
 
+// The head selections of rows 0 .. batch-1 as attn_select_heads, one row per
+// wave (rows w, w + waves, ...) over the head predictor's layer-1 outputs
+// hpred[batch][phid]: s_any[h] = 1 when some row selected head h, s_heads[b k
+// + i] the k heads of row b in ascending order.  s_hp holds batch rows of
+// kSelHs floats.  Every wave of the block takes part.
+constexpr int kSelHs = kAttnSelHid + 4 * kL2Hw;
+template <typename PW>
+__device__ __forceinline__ void attn_select_heads_rows(const PW* __restrict__ w2, const float* __restrict__ b2,
+                                                       const float* __restrict__ hpred, int phid, int nh, int k,
+                                                       int batch, float* s_hp, uint64_t* s_tab, int* s_any,
+                                                       int32_t* s_heads) {
+  using V = typename Blk8<PW>::V;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int oc = min(lane, nh - 1);
+  V w[kAttnSelHid / 8];
+  l2_load<PW, kAttnSelHid>(w2, phid, nh, oc, w);
+  const float bv = b2[oc];
+  for (int i = threadIdx.x; i < batch * phid; i += blockDim.x) {
+    const int b = i / phid;
+    s_hp[b * kSelHs + (i - b * phid)] = hpred[i];
+  }
+  if (threadIdx.x < 32) s_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  if (threadIdx.x < 64) s_any[threadIdx.x] = 0;
+  __syncthreads();
+  for (int b = wave; b < batch; b += nw) {
+    const float score = sigmoid_ref_t(__fadd_rn(l2_chain<PW, kAttnSelHid>(w, phid, s_hp + b * kSelHs), bv), s_tab);
+    const bool ok = lane < nh;
+    const int rank = l2_wave_rank(f32_key(score), lane, nh);
+    const bool sel = ok && rank < min(k, nh);
+    const uint64_t bal = __ballot(sel);
+    const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0));
+    if (sel) {
+      s_heads[b * k + below] = lane;
+      s_any[lane] = 1;  // several waves may write the same 1
+    }
+  }
+  __syncthreads();
+}
+
 // y[b][row] = Wkvq[row] . x[b] for the K/V rows and the Q rows of selected
 // heads, rows from row_base on (kvrows: the K/V rows were projected already).
 // The grid has one extra (last) block that writes the o_proj row list.
@@ -409,6 +449,11 @@ __global__ __launch_bounds__(kL1LdsThreads) void attn_pred_kv_kernel(
 // taking one eighth of k; x is split into BF16 hi/lo terms as for the batched
 // FFN, and the eighths are added in a fixed order through LDS.  The last
 // block writes the o_proj row list as attn_qkv_kernel does.
+// PW (not void): the heads are selected, not read: the Q-row blocks and the
+// last block run every row's head predictor layer 2 and top k
+// (attn_select_heads_rows over hpred[batch][phid]); the last block writes
+// them to heads_out[batch][nsel] for the kernels after this one.  The K/V
+// blocks do not wait for the selection.
 constexpr int kQmTiles = 4;                  // 16-row tiles per wave
 constexpr int kQmSplit = 8;                  // waves per block, one k-eighth each
 constexpr int kQmDepth = 2;                  // k-steps of loads in flight per wave
@@ -418,32 +463,54 @@ constexpr int kQmAlign = 64 * kQmSplit * kQmDepth;  // hidden must be a multiple
 // instruction of a wave reads one contiguous 1 KB tile instead of 64 bytes
 // from each of 16 rows: measured 5.9 TB/s for such a stream against 3.2 TB/s
 // for the row-major gather.
-template <bool TILED>
+template <bool TILED, typename PW = void>
 __global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
     const uint16_t* __restrict__ W, const float* __restrict__ x, int batch, int H, int kvrows,
     int rows, int D, int nh,
     const int32_t* __restrict__ heads, int nsel, float* __restrict__ y, int ystride,
-    int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows, int32_t* __restrict__ urank) {
+    int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows, int32_t* __restrict__ urank,
+    const PW* __restrict__ w2 = nullptr, const float* __restrict__ b2 = nullptr,
+    const float* __restrict__ hpred = nullptr, int phid = 0, int32_t* __restrict__ heads_out = nullptr) {
   constexpr int T = kQmTiles, S = kQmSplit, DEP = kQmDepth;
+  constexpr bool SEL = !std::is_void<PW>::value;
   __shared__ kh_f32x4 part[S - 1][2 * T][64];
   __shared__ int s_flag[kMaxAttnHeads], s_uh[kMaxAttnHeads];
   __shared__ int wsum[S];
   __shared__ int s_total;
   const int nent = batch * nsel;
-  if (blockIdx.x == gridDim.x - 1) {
-    qkv_plan(heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_uh, wsum, &s_total);
-    return;
-  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int base = blockIdx.x * kQmRows;
+  const bool plan = blockIdx.x == gridDim.x - 1;
   bool live = base < rows;
-  if (live && base >= kvrows) {
-    // Q rows of head h (D is a multiple of 64): skipped unless some token selected h
-    const int h = (base - kvrows) / D;
-    int any = 0;
-    for (int i = lane; i < nent; i += 64) any |= heads[i] == h;
-    live = __ballot(any) != 0;
+  // selection scratch in the partial-sum array (written only after the k loop)
+  static_assert(sizeof(part) >= sizeof(float) * 16 * kSelHs + sizeof(int) * (64 + 16 * 64) +
+                                    sizeof(uint64_t) * 32, "selection scratch fits");
+  uint64_t* s_tab = reinterpret_cast<uint64_t*>(&part[0][0][0]);
+  int* s_any = reinterpret_cast<int*>(s_tab + 32);
+  int32_t* s_heads = s_any + 64;
+  float* s_hp = reinterpret_cast<float*>(s_heads + 16 * 64);
+  if constexpr (SEL) {
+    if (plan) {
+      attn_select_heads_rows<PW>(w2, b2, hpred, phid, nh, nsel, batch, s_hp, s_tab, s_any, s_heads);
+      for (int i = threadIdx.x; i < nent; i += blockDim.x) heads_out[i] = s_heads[i];
+      qkv_plan(s_heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_uh, wsum, &s_total);
+      return;
+    }
+  } else {
+    if (plan) {
+      qkv_plan(heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_uh, wsum, &s_total);
+      return;
+    }
+    if (live && base >= kvrows) {
+      // Q rows of head h (D is a multiple of 64): skipped unless some token selected h
+      const int h = (base - kvrows) / D;
+      int any = 0;
+      for (int i = lane; i < nent; i += 64) any |= heads[i] == h;
+      live = __ballot(any) != 0;
+    }
   }
+  // SEL: a Q-row block selects the heads after issuing its first weight loads
+  const bool sel_q = SEL && live && base >= kvrows;
   const int r = lane & 15, kb = lane >> 4;
   const int qsteps = H / (64 * S);  // k-steps per eighth
   const int s0 = wave * qsteps;
@@ -464,28 +531,53 @@ __global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
   kh_f32x4 c[T][2];
 #pragma unroll
   for (int t = 0; t < T; ++t) c[t][0] = c[t][1] = kh_f32x4{0, 0, 0, 0};
-  if (live) {
-    uint4 bw[DEP][T][2];
-    float4 bx[DEP][2][2];
-    auto load = [&](int d, int st) {  // clamped, unconditional (past the end: reread, unused)
-      const int o = 8 * min(st, qsteps - 1);
+  uint4 bw[DEP][T][2];
+  float4 bx[DEP][2][2];
+  // clamped, unconditional (past the end: reread, unused)
+  auto loadw = [&](int d, int st) {
+    const int o = 8 * min(st, qsteps - 1);
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        if constexpr (TILED) {  // k-step sg = s0 + st covers the 32-k tiles 2 sg and 2 sg + 1
-          const size_t tl = (size_t)2 * (s0 + min(st, qsteps - 1)) * 64;
-          bw[d][t][0] = ld_stream(wp[t] + tl);
-          bw[d][t][1] = ld_stream(wp[t] + tl + 64);
-        } else {
-          bw[d][t][0] = ld_stream(wp[t] + o);
-          bw[d][t][1] = ld_stream(wp[t] + o + 4);
-        }
+    for (int t = 0; t < T; ++t) {
+      if constexpr (TILED) {  // k-step sg = s0 + st covers the 32-k tiles 2 sg and 2 sg + 1
+        const size_t tl = (size_t)2 * (s0 + min(st, qsteps - 1)) * 64;
+        bw[d][t][0] = ld_stream(wp[t] + tl);
+        bw[d][t][1] = ld_stream(wp[t] + tl + 64);
+      } else {
+        bw[d][t][0] = ld_stream(wp[t] + o);
+        bw[d][t][1] = ld_stream(wp[t] + o + 4);
       }
-      bx[d][0][0] = xf[2 * o]; bx[d][0][1] = xf[2 * o + 1];
-      bx[d][1][0] = xf[2 * o + 8]; bx[d][1][1] = xf[2 * o + 9];
-    };
+    }
+  };
+  auto loadx = [&](int d, int st) {
+    const int o = 8 * min(st, qsteps - 1);
+    bx[d][0][0] = xf[2 * o]; bx[d][0][1] = xf[2 * o + 1];
+    bx[d][1][0] = xf[2 * o + 8]; bx[d][1][1] = xf[2 * o + 9];
+  };
+  auto load = [&](int d, int st) {
+    loadw(d, st);
+    loadx(d, st);
+  };
+  if constexpr (SEL) {
+    if (sel_q) {
+      loadw(0, 0);  // in flight during the selection
+      __builtin_amdgcn_sched_barrier(0);
+      attn_select_heads_rows<PW>(w2, b2, hpred, phid, nh, nsel, batch, s_hp, s_tab, s_any, s_heads);
+      live = s_any[(base - kvrows) / D] != 0;
+      __syncthreads();  // every wave has read s_any before part is written
+      if (live) {
+        loadx(0, 0);
+#pragma unroll
+        for (int d = 1; d < DEP; ++d) load(d, d);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  if (live && !sel_q) {
 #pragma unroll
     for (int d = 0; d < DEP; ++d) load(d, d);
     __builtin_amdgcn_sched_barrier(0);
+  }
+  if (live) {
     // qsteps is a multiple of DEP (host-checked): no test inside the loop
     for (int st = 0; st < qsteps; st += DEP) {
 #pragma unroll
@@ -1105,6 +1197,7 @@ struct kh_sparse_attn {
   uint16_t* wkvq_t = nullptr;  // wkvq in 16 x 32 tiles (mfma_tile16x32) for the batched projections
   std::vector<int64_t> len_host, pre_host;
   Scratch po, pml, partial;
+  Scratch xn;  // normalised rows of the batched fused block
   int kvd() const { return nkv * d; }
   int ystride() const { return 2 * nkv * d + nh * d; }
   size_t seq_elems() const { return (size_t)nkv * max_seq * d; }
@@ -1435,6 +1528,9 @@ static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
 
 // nrm.w set (batch 1 only): x is the un-normalised hidden row, normalised
 // inside the projection kernel with the scale at nrm.inv.
+// hsel with batch > 1: x holds the normalised rows, and the heads are selected
+// inside the projection (the head predictor's layer 2 over hsel->hbuf) and
+// written to heads.
 // kv_done (batch 1 with nrm.w): attn_pred_kv_kernel projected the K/V rows,
 // so only the selected heads' Q rows remain.
 template <int NB>
@@ -1446,17 +1542,41 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   // 1. projections (+ the o_proj row list in the last block)
   const int rows = kvrows + qd;
   if (NB > 1 && H % kQmAlign == 0 && !nrm.w) {
-    if (a->wkvq_t)
-      hipLaunchKernelGGL(attn_qkv_mfma_kernel<true>, dim3(ceil_div(rows, kQmRows) + 1),
-                         dim3(64 * kQmSplit), 0, st, a->wkvq_t, x, batch, H, kvrows, rows, D,
-                         a->nh, heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
-                         a->qrows + qd + 1);
-    else
-      hipLaunchKernelGGL(attn_qkv_mfma_kernel<false>, dim3(ceil_div(rows, kQmRows) + 1),
-                         dim3(64 * kQmSplit), 0, st, a->wkvq, x, batch, H, kvrows, rows, D,
-                         a->nh, heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
-                         a->qrows + qd + 1);
+    const dim3 g(ceil_div(rows, kQmRows) + 1), blk(64 * kQmSplit);
+    const uint16_t* w = a->wkvq_t ? a->wkvq_t : a->wkvq;
+    int32_t* hout = const_cast<int32_t*>(heads);
+    if (!hsel) {
+      if (a->wkvq_t)
+        hipLaunchKernelGGL(attn_qkv_mfma_kernel<true>, g, blk, 0, st, w, x, batch, H, kvrows, rows, D, a->nh,
+                           heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1);
+      else
+        hipLaunchKernelGGL(attn_qkv_mfma_kernel<false>, g, blk, 0, st, w, x, batch, H, kvrows, rows, D, a->nh,
+                           heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1);
+    } else if (hsel->bf16) {
+      const uint16_t* w2 = static_cast<const uint16_t*>(hsel->w2b);
+      if (a->wkvq_t)
+        hipLaunchKernelGGL((attn_qkv_mfma_kernel<true, uint16_t>), g, blk, 0, st, w, x, batch, H, kvrows, rows, D,
+                           a->nh, nullptr, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1,
+                           w2, hsel->b2, hsel->hbuf, hsel->hid, hout);
+      else
+        hipLaunchKernelGGL((attn_qkv_mfma_kernel<false, uint16_t>), g, blk, 0, st, w, x, batch, H, kvrows, rows,
+                           D, a->nh, nullptr, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
+                           a->qrows + qd + 1, w2, hsel->b2, hsel->hbuf, hsel->hid, hout);
+    } else {
+      const float* w2 = static_cast<const float*>(hsel->w2b);
+      if (a->wkvq_t)
+        hipLaunchKernelGGL((attn_qkv_mfma_kernel<true, float>), g, blk, 0, st, w, x, batch, H, kvrows, rows, D,
+                           a->nh, nullptr, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1,
+                           w2, hsel->b2, hsel->hbuf, hsel->hid, hout);
+      else
+        hipLaunchKernelGGL((attn_qkv_mfma_kernel<false, float>), g, blk, 0, st, w, x, batch, H, kvrows, rows, D,
+                           a->nh, nullptr, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1,
+                           w2, hsel->b2, hsel->hbuf, hsel->hid, hout);
+    }
     KH_LAUNCHED();
+  } else if (NB > 1 && hsel) {
+    set_error("the batched fused attention block needs hidden a multiple of %d", kQmAlign);
+    return KH_ERR_UNSUPPORTED;
   } else {
     static bool attr_set = false;
     if (!attr_set) {
@@ -1670,5 +1790,54 @@ extern "C" int kh_dejavu_attn_block(const kh_predictor* p, kh_sparse_attn* a, fl
   if (rc != KH_OK) return rc;
   rc = attn_launch<1>(a, hidden_dev, 1, nullptr, heads_dev, k, hidden_dev, 1, st, nrm, overlap);
   if (rc == KH_OK) a->len_host[0] += 1;
+  return rc;
+}
+
+extern "C" int kh_dejavu_attn_block_batch(const kh_predictor* p, kh_sparse_attn* a, float* hidden_dev,
+                                          int64_t batch, const float* norm_w_dev, float eps, int k,
+                                          int32_t* heads_dev, float* norm_ws_dev, void* stream) {
+  KH_CHECK_ARG(p && a && hidden_dev && norm_w_dev && heads_dev && norm_ws_dev, "null argument");
+  KH_CHECK_ARG(batch >= 1 && batch <= a->max_batch, "batch %lld not in [1,%d]", (long long)batch,
+               a->max_batch);
+  if (batch == 1)
+    return kh_dejavu_attn_block(p, a, hidden_dev, norm_w_dev, eps, k, heads_dev, norm_ws_dev, stream);
+  KH_CHECK_ARG(k >= 1 && k <= a->nh, "k %d not in [1,%d]", k, a->nh);
+  KH_CHECK_ARG(predictor_in_dim(p) == a->hidden && predictor_out_dim(p) == a->nh,
+               "predictor %d->%d does not match the attention (hidden %d, %d heads)",
+               predictor_in_dim(p), predictor_out_dim(p), a->hidden, a->nh);
+  if (a->hidden % kQmAlign != 0 || a->hidden > kL1LdsIn || a->nh > 64) {
+    set_error("the batched fused attention block needs hidden a multiple of %d and at most %d, and at "
+              "most 64 heads (got hidden %d, %d heads)", kQmAlign, kL1LdsIn, a->hidden, a->nh);
+    return KH_ERR_UNSUPPORTED;
+  }
+  for (int64_t b = 0; b < batch; ++b)
+    if (a->len_host[b] >= a->max_seq) {
+      set_error("KV cache of sequence %lld is full (%d positions)", (long long)b, a->max_seq);
+      return KH_ERR_CAPACITY;
+    }
+  hipStream_t st = as_stream(stream);
+  NormIn nrm;
+  nrm.w = norm_w_dev;
+  nrm.inv = norm_ws_dev;
+  nrm.eps = eps;
+  float* xn = static_cast<float*>(a->xn.get(sizeof(float) * batch * a->hidden));
+  if (!xn) return KH_ERR_ALLOC;
+  PredL1View v;
+  int rc = predictor_l1_normed(p, hidden_dev, batch, nrm, xn, st, &v);
+  if (rc != KH_OK) return rc;
+  if (v.hid > kAttnSelHid) {
+    set_error("the batched fused attention block selects heads of predictors with at most %d hidden "
+              "units (got %d)", kAttnSelHid, v.hid);
+    return KH_ERR_UNSUPPORTED;
+  }
+  const int b = static_cast<int>(batch);
+  switch (b <= 2 ? 2 : b <= 4 ? 4 : b <= 8 ? 8 : 16) {
+    case 2: rc = attn_launch<2>(a, xn, b, nullptr, heads_dev, k, hidden_dev, 1, st, NormIn{}, false, &v); break;
+    case 4: rc = attn_launch<4>(a, xn, b, nullptr, heads_dev, k, hidden_dev, 1, st, NormIn{}, false, &v); break;
+    case 8: rc = attn_launch<8>(a, xn, b, nullptr, heads_dev, k, hidden_dev, 1, st, NormIn{}, false, &v); break;
+    default: rc = attn_launch<16>(a, xn, b, nullptr, heads_dev, k, hidden_dev, 1, st, NormIn{}, false, &v); break;
+  }
+  if (rc == KH_OK)
+    for (int64_t i = 0; i < batch; ++i) a->len_host[i] += 1;
   return rc;
 }

@@ -356,6 +356,8 @@ struct PredL1View {
 };
 int predictor_l1_view(const kh_predictor* p, hipStream_t st, PredL1View* v);
 int predictor_l2_topk_from_h(const kh_predictor* p, int k, int32_t* ids, hipStream_t st);
+int predictor_l1_normed(const kh_predictor* p, const float* hidden, int64_t batch, const NormIn& nrm,
+                        float* xn, hipStream_t st, PredL1View* v);
 
 // Workgroup barrier that waits only for LDS traffic.  __syncthreads() on gfx9
 // also waits for every outstanding vector-memory load (vmcnt counts loads and

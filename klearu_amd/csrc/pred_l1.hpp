@@ -59,7 +59,8 @@ constexpr int kL1LdsBytes = (kL1Chains + 1) * kL1LdsIn * 4;  // products + x
 // squares (exact_seq_sum over 32 chunks of 128 terms, run by every wave while
 // the weight loads are in flight), its scale, then (x * inv) * norm_w.  Block 0
 // stores the scale in inv_out[b] for the kernels that consume the same
-// normalised row later.  The norm requires n_in % 4 == 0 (host-checked).
+// normalised row later, and, with xn_out set, the normalised row itself at
+// xn_out[b][n_in].  The norm requires n_in % 4 == 0 (host-checked).
 constexpr int kL1EsChunks = 32;
 constexpr int kL1EsM = kL1LdsIn / kL1EsChunks;  // terms per chunk of the exact sum
 using L1Es = EsLds<kL1EsChunks, kL1EsM>;
@@ -73,7 +74,8 @@ template <typename W>
 __device__ __forceinline__ void pred_l1_lds_body(
     const int bx, const int b, const W* __restrict__ Wb, const float* __restrict__ bias,
     const float* __restrict__ x, int n_in, int hid, float* __restrict__ h,
-    const float* __restrict__ norm_w, float* __restrict__ inv_out, float eps, float4* lds4) {
+    const float* __restrict__ norm_w, float* __restrict__ inv_out, float eps, float4* lds4,
+    float* __restrict__ xn_out = nullptr) {
   using B8 = Blk8<W>;
   using V = typename B8::V;
   constexpr int SPP = kL1LdsIn / kL1Stage / kL1Prod;  // stages per producer
@@ -159,6 +161,8 @@ __device__ __forceinline__ void pred_l1_lds_body(
       v.z = __fmul_rn(__fmul_rn(v.z, inv), wn[q].z);
       v.w = __fmul_rn(__fmul_rn(v.w, inv), wn[q].w);
       reinterpret_cast<float4*>(xs)[min((int)threadIdx.x + q * kL1LdsThreads, n4 - 1)] = v;  // clamped
+      if (xn_out && bx == 0)
+        reinterpret_cast<float4*>(xn_out + (size_t)b * n_in)[min((int)threadIdx.x + q * kL1LdsThreads, n4 - 1)] = v;
     }
     if (bx == 0 && threadIdx.x == 0) inv_out[b] = inv;
     lds_barrier();

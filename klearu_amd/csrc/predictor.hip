@@ -157,9 +157,9 @@ template <typename W>
 __global__ __launch_bounds__(kL1LdsThreads) void pred_l1_lds_kernel(
     const W* __restrict__ Wb, const float* __restrict__ bias, const float* __restrict__ x,
     int n_in, int hid, float* __restrict__ h, const float* __restrict__ norm_w,
-    float* __restrict__ inv_out, float eps) {
+    float* __restrict__ inv_out, float eps, float* __restrict__ xn_out = nullptr) {
   extern __shared__ float4 lds4[];
-  pred_l1_lds_body<W>(blockIdx.x, blockIdx.y, Wb, bias, x, n_in, hid, h, norm_w, inv_out, eps, lds4);
+  pred_l1_lds_body<W>(blockIdx.x, blockIdx.y, Wb, bias, x, n_in, hid, h, norm_w, inv_out, eps, lds4, xn_out);
 }
 
 // Layer 1 for a batch of rows (BF16 weights, n_in a multiple of
@@ -1427,6 +1427,43 @@ int predictor_l1_view(const kh_predictor* p, hipStream_t st, PredL1View* v) {
   if (rc != KH_OK) return rc;
   rc = set_kernel_attrs();
   if (rc != KH_OK) return rc;
+  v->w1b = p->w1b;
+  v->b1 = p->b1;
+  v->w2b = p->w2b;
+  v->b2 = p->b2;
+  v->in_dim = p->in_dim;
+  v->hid = p->hid;
+  v->out_dim = p->out_dim;
+  v->bf16 = p->bf16;
+  v->hbuf = b.hbuf;
+  return KH_OK;
+}
+
+// Layer 1 of RmsNorm(hidden[b]) for rows b < batch (the norm inside the
+// layer-1 blocks, each row's scale written to nrm.inv[b] and the normalised
+// rows to xn[batch][in_dim]) into the per-stream layer-1 buffer that v->hbuf
+// then names ([batch][hid]).
+int predictor_l1_normed(const kh_predictor* p, const float* hidden, int64_t batch, const NormIn& nrm,
+                        float* xn, hipStream_t st, PredL1View* v) {
+  if (!nrm.w || !nrm.inv || p->in_dim > kL1LdsIn || p->in_dim % 4 != 0) {
+    set_error("the fused RmsNorm needs predictor inputs that are a multiple of 4 and at most %d", kL1LdsIn);
+    return KH_ERR_UNSUPPORTED;
+  }
+  PredBufs b;
+  int rc = pred_bufs(p, st, batch, 0, false, &b);
+  if (rc != KH_OK) return rc;
+  rc = set_kernel_attrs();
+  if (rc != KH_OK) return rc;
+  const dim3 g(ceil_div(p->hid, kL1Chains), static_cast<unsigned>(batch));
+  if (p->bf16)
+    hipLaunchKernelGGL(pred_l1_lds_kernel<uint16_t>, g, dim3(kL1LdsThreads), kL1LdsBytes, st,
+                       static_cast<const uint16_t*>(p->w1b), p->b1, hidden, p->in_dim, p->hid, b.hbuf, nrm.w,
+                       nrm.inv, nrm.eps, xn);
+  else
+    hipLaunchKernelGGL(pred_l1_lds_kernel<float>, g, dim3(kL1LdsThreads), kL1LdsBytes, st,
+                       static_cast<const float*>(p->w1b), p->b1, hidden, p->in_dim, p->hid, b.hbuf, nrm.w,
+                       nrm.inv, nrm.eps, xn);
+  KH_LAUNCHED();
   v->w1b = p->w1b;
   v->b1 = p->b1;
   v->w2b = p->w2b;

@@ -284,6 +284,79 @@ def test_attn_block_chained(kh, orc, H, nh, nkv, d, R, k, pre, steps):
     assert c.attn.current_len(0) == pre + steps
 
 
+def _head_predictor(orc, rng, H, nh, R):
+    from klearu_amd.dejavu import SparsityPredictor
+    w1 = orc.bf16_from_f32(rng.normal(0, 0.05, (R, H)).astype(np.float32))
+    w2 = orc.bf16_from_f32(rng.normal(0, 0.3, (nh, R)).astype(np.float32))
+    b1 = rng.normal(0, 0.1, R).astype(np.float32)
+    b2 = rng.normal(0, 0.1, nh).astype(np.float32)
+    return (w1, b1, w2, b2), SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
+
+
+def _batch_block_step(orc, c, pw, p, hd, wn, wnd, ws, k, what):
+    """One kh_dejavu_attn_block_batch call checked row by row against the oracle."""
+    from klearu_amd.attention import attn_block_batch
+    w1, b1, w2, b2 = pw
+    h_in = hd.cpu().numpy().copy()
+    ws.fill_(float("nan"))
+    heads = attn_block_batch(p, c.attn, hd, wnd, 1e-5, k, norm_ws=ws).cpu().numpy()
+    got = hd.cpu().numpy()
+    scales = ws.cpu().numpy()
+    for b in range(h_in.shape[0]):
+        inv = np.array([orc.rms_inv(h_in[b], 1e-5)], np.float32)
+        np.testing.assert_array_equal(scales[b:b + 1].view(np.uint32), inv.view(np.uint32),
+                                      err_msg=f"{what} row {b}: norm scale")
+        norm = orc.rmsnorm(h_in[b], wn, 1e-5)
+        scores, _ = orc.predictor_predict(w1, b1, w2, b2, norm)
+        sel = np.sort(orc.select_top_k(scores, k))
+        np.testing.assert_array_equal(heads[b], sel, err_msg=f"{what} row {b}: heads")
+        close(got[b], h_in[b] + c.oracle_step(b, norm, sel.tolist()), f"{what} row {b}")
+
+
+@pytest.mark.parametrize("H,nh,nkv,d,R,k,pre,B,steps", [
+    (4096, 32, 32, 128, 128, 16, 2000, 8, 2),   # cfg4 (7B), batch 8
+    (1024, 16, 4, 64, 64, 5, 70, 3, 3),         # GQA, ragged batch
+    (1024, 8, 8, 128, 128, 8, 40, 16, 2),       # k = every head, batch 16
+])
+def test_attn_block_batch_chained(kh, orc, H, nh, nkv, d, R, k, pre, B, steps):
+    """kh_dejavu_attn_block_batch: every row's RmsNorm scale is the
+    reference's bit for bit (rms_norm.rs:43-53), its head set equals the
+    oracle's own top k (selected inside the q/k/v projection here), and the
+    updated rows match the oracle's residual from that selection
+    (crates/klearu-llm/src/sparse/mod.rs:56-112, one token per sequence) within
+    the BF16-weight tolerance, over several steps and cache lengths."""
+    rng = np.random.default_rng(57 + H + B)
+    lens = [max(0, pre - 3 * b) for b in range(B)]  # row 15 of batch 16: an empty cache
+    c = Case(orc, rng, H, nh, nkv, d, pre + steps + 4, B, lens)
+    pw, p = _head_predictor(orc, rng, H, nh, R)
+    wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    wnd = torch.from_numpy(wn).cuda()
+    hd = torch.from_numpy(rng.standard_normal((B, H)).astype(np.float32)).cuda()
+    ws = torch.empty(B, dtype=torch.float32, device="cuda")
+    for step in range(steps):
+        _batch_block_step(orc, c, pw, p, hd, wn, wnd, ws, k, f"step {step}")
+    for b in range(B):
+        assert c.attn.current_len(b) == lens[b] + steps
+
+
+def test_attn_block_batch_hard_norm_rows(kh, orc):
+    """kh_dejavu_attn_block_batch fed the hard RmsNorm rows (ties stuck at
+    2^24, round-up drift, leading zeros, all-zero, tiny, huge, wide-range) as
+    one batch at the 7B shape: scales, heads and residuals as above."""
+    from hard_rows import hard_hidden_rows
+    H, nh, d, R, k, pre = 4096, 32, 128, 128, 16, 600
+    rng = np.random.default_rng(97)
+    rows = list(hard_hidden_rows(rng, H).values())[:16]
+    B = len(rows)
+    c = Case(orc, rng, H, nh, nh, d, pre + 4, B, pre)
+    pw, p = _head_predictor(orc, rng, H, nh, R)
+    wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    wnd = torch.from_numpy(wn).cuda()
+    hd = torch.from_numpy(np.stack(rows).astype(np.float32)).cuda()
+    ws = torch.empty(B, dtype=torch.float32, device="cuda")
+    _batch_block_step(orc, c, pw, p, hd, wn, wnd, ws, k, "hard rows")
+
+
 @pytest.mark.parametrize("H,nh,d,R,k,pre", [
     (4096, 32, 128, 128, 16, 2000),   # cfg4 (7B)
     (2048, 16, 128, 128, 8, 300),     # a 1.1B-class width
