@@ -514,6 +514,17 @@ int kh_rmsnorm(const float* x_dev, const float* w_dev, int64_t batch, int n, flo
 int kh_dejavu_mlp_block(const kh_predictor* p, const kh_sparse_ffn* f, float* hidden_dev,
                         const float* norm_w_dev, float eps, int k, int32_t* active_dev,
                         float* norm_ws_dev, void* stream);
+/* kh_dejavu_mlp_block for rows 0..batch-1 of hidden_dev[batch][hidden]
+ * (sparse/mod.rs:115-142 per row): each row's RmsNorm (scale to
+ * norm_ws_dev[batch]) and top-k ids (active_dev[batch][k], ascending) are the
+ * reference's bit for bit, and the FFN runs over the union of the rows'
+ * selections, as kh_rmsnorm, kh_predictor_select_top_k_union and
+ * kh_sparse_ffn_forward would in sequence (the union is taken inside the
+ * FFN's gate/up kernel where the shape allows).  batch 1 is
+ * kh_dejavu_mlp_block.  Requires hidden <= 8192. */
+int kh_dejavu_mlp_block_batch(const kh_predictor* p, const kh_sparse_ffn* f, float* hidden_dev,
+                              int64_t batch, const float* norm_w_dev, float eps, int k,
+                              int32_t* active_dev, float* norm_ws_dev, void* stream);
 
 /* ======================================================================== */
 /* klearu-dejavu transformer layer: f32 Linear with bias, SparseMlp,        */

@@ -140,6 +140,7 @@ SIGS = {
     "kh_sparse_ffn_status": (I, [P]),
     "kh_rmsnorm": (I, [P, P, I64, I, F, P, P]),
     "kh_dejavu_mlp_block": (I, [P, P, P, P, F, I, P, P, P]),
+    "kh_dejavu_mlp_block_batch": (I, [P, P, P, I64, P, F, I, P, P, P]),
     "kh_dejavu_attn_block": (I, [P, P, P, P, F, I, P, P, P]),
     "kh_dejavu_attn_block_batch": (I, [P, P, P, I64, P, F, I, P, P, P]),
     "kh_sparse_attn_create": (I, [I, I, I, I, I, I, F, I, P, P, P, P, PP]),

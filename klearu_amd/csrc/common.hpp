@@ -356,6 +356,8 @@ struct PredL1View {
 };
 int predictor_l1_view(const kh_predictor* p, hipStream_t st, PredL1View* v);
 int predictor_l2_topk_from_h(const kh_predictor* p, int k, int32_t* ids, hipStream_t st);
+int predictor_select_marks(const kh_predictor* p, const float* x, int64_t batch, int k, int32_t* ids,
+                           hipStream_t st, uint8_t** marks);
 int predictor_l1_normed(const kh_predictor* p, const float* hidden, int64_t batch, const NormIn& nrm,
                         float* xn, hipStream_t st, PredL1View* v);
 

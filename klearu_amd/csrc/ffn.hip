@@ -140,6 +140,7 @@ __global__ __launch_bounds__(64 * kGuWaves) void ffn_gateup_kernel(
 // through LDS at the end, so the result is deterministic.
 constexpr int kGlRows = 32;
 constexpr int kGlK = 256;
+constexpr int kGlMarkPer = 16;  // mark words per thread: intermediate sizes up to 32768
 constexpr int kGlWaves = 8;
 constexpr int kGlRowQ = kGlK / 8 + 1;                // uint4 per LDS row (one of padding)
 constexpr int kGlBuf = 2 * kGlRows * kGlRowQ;        // uint4 per buffer: gate rows, then up rows
@@ -152,13 +153,54 @@ static_assert(kGlWaves * 2 * 4 * 64 * 16 <= kGlLds, "the final reduction fits in
 __global__ __launch_bounds__(64 * kGlWaves) void ffn_gateup_lds_kernel(
     const uint16_t* __restrict__ Wgu, const float* __restrict__ x, int batch, int H,
     const int32_t* __restrict__ active, int n_active, const int32_t* __restrict__ n_active_dev,
-    int inter, int* __restrict__ err, float* __restrict__ hbuf, int hstride) {
+    int inter, int* __restrict__ err, float* __restrict__ hbuf, int hstride,
+    const uint32_t* __restrict__ marks = nullptr, int32_t* __restrict__ uni_out = nullptr,
+    int32_t* __restrict__ count_out = nullptr) {
   extern __shared__ uint4 gl[];                       // [2][2 * kGlRows][kGlRowQ]
   __shared__ uint64_t s_tab[32];                      // kExp2Tab, for silu after the sums
+  __shared__ int s_uid[kGlRows];                      // marks: this block's union ids
+  __shared__ int s_ws[kGlWaves];
+  __shared__ int s_tot;
   const uint64_t tabv = kExp2Tab[threadIdx.x & 31];   // requested before the weights
   int n = n_active;
-  if (n_active_dev) n = min(n, *n_active_dev);
   const int base = blockIdx.x * kGlRows;
+  if (marks) {
+    // The active rows are the union of the byte marks (one byte per neuron, 1
+    // when some token selected it), in ascending id order: thread t counts the
+    // marks of words [t per, (t + 1) per), a block scan places them, and each
+    // block keeps the ids at union positions [base, base + kGlRows) (and writes
+    // them to uni_out, block 0 the count, for the down projection).
+    const int nwd = (inter + 3) >> 2;
+    const int per = (nwd + (int)blockDim.x - 1) / (int)blockDim.x;  // <= kGlMarkPer (host-checked)
+    const int w0 = (int)threadIdx.x * per;
+    uint32_t wd[kGlMarkPer];
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < kGlMarkPer; ++j) {
+      wd[j] = (j < per && w0 + j < nwd) ? marks[w0 + j] : 0u;
+      cnt += __popc(wd[j]);  // set bytes hold 1
+    }
+    int u = block_excl_scan(cnt, s_ws, &s_tot);
+#pragma unroll
+    for (int j = 0; j < kGlMarkPer; ++j) {
+      uint32_t m = wd[j];
+      while (m) {
+        const int bit = __ffs(m) - 1;
+        if (u >= base && u < base + kGlRows) {
+          const int id = 4 * (w0 + j) + (bit >> 3);
+          s_uid[u - base] = id;
+          uni_out[u] = id;
+        }
+        ++u;
+        m &= m - 1;
+      }
+    }
+    n = s_tot;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *count_out = n;
+    __syncthreads();
+  } else if (n_active_dev) {
+    n = min(n, *n_active_dev);
+  }
   if (base >= n) return;  // whole block idle (uniform)
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // row pieces this lane loads: of the 2*kGlRows pieces (gate rows, then up
@@ -172,7 +214,7 @@ __global__ __launch_bounds__(64 * kGlWaves) void ffn_gateup_lds_kernel(
   for (int j = 0; j < kGlPer; ++j) {
     const int piece = (wave * kGlPer + j) * kPw + half;
     const int gu = piece / kGlRows, row = piece % kGlRows;
-    const int nid = checked_row(active[min(base + row, n - 1)], inter, err);
+    const int nid = marks ? s_uid[min(row, n - 1 - base)] : checked_row(active[min(base + row, n - 1)], inter, err);
     src[j] = reinterpret_cast<const uint4*>(Wgu + ((size_t)nid * 2 + gu) * H) + col;
     dst[j] = piece * kGlRowQ + col;
   }
@@ -499,7 +541,7 @@ __global__ __launch_bounds__(64 * NW) void ffn_fused1_kernel(
 // RmsNorm::forward (crates/klearu-llm/src/model/rms_norm.rs:43-64): one block
 // of kRnWaves waves per row.  The row's squares are staged in LDS and summed in
 // the reference's sequential order (exact_seq_sum, 32 chunks of M terms); then
-// y = (x * inv) * w.
+// y = (x * inv) * w, and inv_out[row] = inv when inv_out is set.
 constexpr int kRnWaves = 8;
 constexpr int kRnChunks = 32;
 constexpr int kRnMaxN = kRnChunks * 256;  // rows up to 8192 (longer rows: rmsnorm_seq_kernel)
@@ -507,7 +549,8 @@ constexpr int kRnMaxN = kRnChunks * 256;  // rows up to 8192 (longer rows: rmsno
 template <int M>
 __global__ __launch_bounds__(64 * kRnWaves) void rmsnorm_kernel(const float* __restrict__ x,
                                                                const float* __restrict__ w, int n,
-                                                               float eps, float* __restrict__ y) {
+                                                               float eps, float* __restrict__ y,
+                                                               float* __restrict__ inv_out = nullptr) {
   __shared__ EsLds<kRnChunks, M> es;
   constexpr int Q = kRnChunks * M / 4 / (64 * kRnWaves);  // float4 of the row per thread
   const float* xr = x + (size_t)blockIdx.x * n;
@@ -537,6 +580,7 @@ __global__ __launch_bounds__(64 * kRnWaves) void rmsnorm_kernel(const float* __r
     lds_barrier();
     const float ss = exact_seq_sum<kRnWaves, kRnChunks, M>(n, 0.0f, es);
     const float inv = rms_inv_exact(ss, n, eps);
+    if (inv_out && t == 0) inv_out[blockIdx.x] = inv;
     float4* y4 = reinterpret_cast<float4*>(yr);
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
@@ -556,6 +600,7 @@ __global__ __launch_bounds__(64 * kRnWaves) void rmsnorm_kernel(const float* __r
   lds_barrier();
   const float ss = exact_seq_sum<kRnWaves, kRnChunks, M>(n, 0.0f, es);
   const float inv = rms_inv_exact(ss, n, eps);
+  if (inv_out && t == 0) inv_out[blockIdx.x] = inv;
   for (int i = t; i < n; i += blockDim.x) yr[i] = __fmul_rn(__fmul_rn(xr[i], inv), w[i]);
 }
 
@@ -590,7 +635,7 @@ struct kh_sparse_ffn {
   mutable StreamWs ws;
 };
 
-enum { kFwH, kFwPartial };
+enum { kFwH, kFwPartial, kFwXn, kFwUni, kFwCount };
 
 static size_t partial_rows(int inter, int nbt) {
   return std::max<size_t>((size_t)kMaxGroups * nbt, (size_t)ceil_div(inter, kFuWavesMin));
@@ -714,10 +759,13 @@ static int ffn_bufs(const kh_sparse_ffn* f, hipStream_t st, float** hbuf, float*
   return *hbuf && *partial ? KH_OK : KH_ERR_ALLOC;
 }
 
+// marks (ffn_marks_ok): the active rows are the union of these byte marks,
+// computed inside the gate/up kernel, which writes it to active[] and its size
+// to n_active_dev (both outputs then); the down kernel clears the marks.
 template <int NB>
 static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const int32_t* active,
                       int n_active, const int32_t* n_active_dev, float* y, int accumulate,
-                      hipStream_t st) {
+                      hipStream_t st, const uint8_t* marks = nullptr) {
   const int H = f->hidden;
   float *hbuf = nullptr, *partial = nullptr;
   int rc = ffn_bufs(f, st, &hbuf, &partial);
@@ -746,7 +794,11 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
     KH_HIP(arc);
     hipLaunchKernelGGL(ffn_gateup_lds_kernel, dim3(ceil_div(n_active, kGlRows)), dim3(64 * kGlWaves), kGlLds,
                        st, f->wgu, x, batch, H, active, n_active, n_active_dev, f->inter, f->err, hbuf,
-                       f->inter);
+                       f->inter, reinterpret_cast<const uint32_t*>(marks), const_cast<int32_t*>(active),
+                       const_cast<int32_t*>(n_active_dev));
+  } else if (marks) {
+    set_error("the union from marks needs the staged gate/up kernel");
+    return KH_ERR_UNSUPPORTED;
   } else {
     hipLaunchKernelGGL(ffn_gateup_kernel<NB>, g1, dim3(64 * kGuWaves), lds1, st, f->wgu, x, batch,
                        H, active, n_active, n_active_dev, f->inter, f->err, hbuf, f->inter);
@@ -767,7 +819,11 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
     KH_HIP(arc);
     groups = ceil_div(n_active, GR);
     hipLaunchKernelGGL((down_bf_kernel<NB, GR>), dim3(H / kDbCols, groups), dim3(64 * kDbWaves), db_lds(GR), st,
-                       f->wdt, H, active, n_active, n_active_dev, f->inter, hbuf, f->inter, batch, partial);
+                       f->wdt, H, active, n_active, n_active_dev, f->inter, hbuf, f->inter, batch, partial,
+                       const_cast<uint32_t*>(reinterpret_cast<const uint32_t*>(marks)), (f->inter + 3) >> 2);
+  } else if (marks) {
+    set_error("the union from marks needs the BF16 down kernel");
+    return KH_ERR_UNSUPPORTED;
   } else if (NB > 1 && H % kDmCols == 0) {
     // several tokens: 512-row groups on the matrix cores (f32 MFMA)
     static bool dm_attr = false;
@@ -810,6 +866,13 @@ static int ffn_launch(const kh_sparse_ffn* f, const float* x, int batch, const i
 
 static bool ffn_fused_ok(const kh_sparse_ffn* f, int64_t batch) {
   return batch == 1 && f->hidden <= kFuMaxH && f->hidden % (8 * kFuWaves) == 0;
+}
+
+// ffn_launch can take the active rows as the union of byte marks (the staged
+// gate/up and BF16 down kernels, intermediate sizes up to 32768).
+static bool ffn_marks_ok(const kh_sparse_ffn* f, int64_t batch) {
+  return batch > 1 && !ffn_fused_ok(f, batch) && f->hidden % kGlK == 0 && f->hidden % kDbCols == 0 &&
+         f->inter <= kGlMarkPer * 4 * 64 * kGlWaves && ceil_div(f->inter, 256) <= kMaxGroups;
 }
 
 // Four neurons per block when the hidden size allows it (a wave's down slice
@@ -1010,4 +1073,58 @@ extern "C" int kh_dejavu_mlp_block(const kh_predictor* p, const kh_sparse_ffn* f
   int rc = predictor_topk_normed(p, hidden_dev, k, active_dev, nrm, st);
   if (rc != KH_OK) return rc;
   return ffn_fused_launch(f, hidden_dev, active_dev, k, nullptr, hidden_dev, 1, nrm, st);
+}
+
+extern "C" int kh_dejavu_mlp_block_batch(const kh_predictor* p, const kh_sparse_ffn* f, float* hidden_dev,
+                                         int64_t batch, const float* norm_w_dev, float eps, int k,
+                                         int32_t* active_dev, float* norm_ws_dev, void* stream) {
+  KH_CHECK_ARG(p && f && hidden_dev && norm_w_dev && active_dev && norm_ws_dev, "null argument");
+  KH_CHECK_ARG(batch >= 1 && batch <= f->max_batch, "batch %lld not in [1,%d]", (long long)batch,
+               f->max_batch);
+  if (batch == 1)
+    return kh_dejavu_mlp_block(p, f, hidden_dev, norm_w_dev, eps, k, active_dev, norm_ws_dev, stream);
+  KH_CHECK_ARG(k >= 1 && k <= f->inter, "k %d not in [1,%d]", k, f->inter);
+  KH_CHECK_ARG(predictor_in_dim(p) == f->hidden && predictor_out_dim(p) == f->inter,
+               "predictor %d->%d does not match the FFN (hidden %d, intermediate %d)",
+               predictor_in_dim(p), predictor_out_dim(p), f->hidden, f->inter);
+  const int H = f->hidden;
+  if (H > kRnMaxN) {
+    set_error("the batched fused block needs hidden <= %d (got %d)", kRnMaxN, H);
+    return KH_ERR_UNSUPPORTED;
+  }
+  hipStream_t st = as_stream(stream);
+  WsSet* w = f->ws.get(st);
+  float* xn = static_cast<float*>(w->get(kFwXn, sizeof(float) * f->max_batch * H));
+  int32_t* uni = static_cast<int32_t*>(w->get(kFwUni, sizeof(int32_t) * f->inter));
+  int32_t* cnt = static_cast<int32_t*>(w->get(kFwCount, sizeof(int32_t)));
+  if (!xn || !uni || !cnt) return KH_ERR_ALLOC;
+  // the exact RmsNorm of every row, its scale to norm_ws_dev
+  if (H <= kRnChunks * 128)
+    hipLaunchKernelGGL(rmsnorm_kernel<128>, dim3(batch), dim3(64 * kRnWaves), 0, st, hidden_dev, norm_w_dev, H,
+                       eps, xn, norm_ws_dev);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<256>, dim3(batch), dim3(64 * kRnWaves), 0, st, hidden_dev, norm_w_dev, H,
+                       eps, xn, norm_ws_dev);
+  KH_LAUNCHED();
+  // the neurons: each row's top k with byte marks, their union taken inside
+  // the FFN's gate/up kernel; else the union kernel and the plain FFN
+  const uint8_t* marks = nullptr;
+  int rc = KH_ERR_UNSUPPORTED;
+  if (ffn_marks_ok(f, batch)) {
+    uint8_t* m = nullptr;
+    rc = predictor_select_marks(p, xn, batch, k, active_dev, st, &m);
+    if (rc != KH_OK && rc != KH_ERR_UNSUPPORTED) return rc;
+    marks = m;
+  }
+  if (rc == KH_ERR_UNSUPPORTED) {
+    rc = kh_predictor_select_top_k_union(p, xn, batch, k, active_dev, uni, cnt, stream);
+    if (rc != KH_OK) return rc;
+  }
+  const int b = static_cast<int>(batch);
+  switch (ffn_tmpl(batch)) {
+    case 2: return ffn_launch<2>(f, xn, b, uni, f->inter, cnt, hidden_dev, 1, st, marks);
+    case 4: return ffn_launch<4>(f, xn, b, uni, f->inter, cnt, hidden_dev, 1, st, marks);
+    case 8: return ffn_launch<8>(f, xn, b, uni, f->inter, cnt, hidden_dev, 1, st, marks);
+    default: return ffn_launch<16>(f, xn, b, uni, f->inter, cnt, hidden_dev, 1, st, marks);
+  }
 }

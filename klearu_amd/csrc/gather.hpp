@@ -489,10 +489,16 @@ template <int NB, int GR>
 __global__ __launch_bounds__(64 * kDbWaves) void down_bf_kernel(
     const uint16_t* __restrict__ WdT, int H, const int32_t* __restrict__ active, int n_active,
     const int32_t* __restrict__ n_active_dev, int nrows, const float* __restrict__ hbuf,
-    int hstride, int batch, float* __restrict__ partial) {
+    int hstride, int batch, float* __restrict__ partial, uint32_t* __restrict__ clear = nullptr,
+    int nclear = 0) {
   static_assert(NB <= 16 && GR % kDbChunk == 0, "tiling");
   constexpr int HS = db_hs(GR);
   constexpr int NT = 64 * kDbWaves;
+  // clear[0, nclear): words the launch before this one read (the union marks)
+  if (clear)
+    for (int i = (blockIdx.y * gridDim.x + blockIdx.x) * NT + threadIdx.x; i < nclear;
+         i += gridDim.x * gridDim.y * NT)
+      clear[i] = 0u;
   extern __shared__ uint4 db_lds_mem[];
   uint8_t* wbuf = reinterpret_cast<uint8_t*>(db_lds_mem);                // [2][kDbBuf]
   uint16_t* s_hh = reinterpret_cast<uint16_t*>(wbuf + 2 * kDbBuf);      // [16][HS]

@@ -1476,6 +1476,27 @@ int predictor_l1_normed(const kh_predictor* p, const float* hidden, int64_t batc
   return KH_OK;
 }
 
+// Scores of rows 0..batch-1 of x (normalised rows) and their top k, ids
+// ascending into ids[batch][k], with the selected neurons' byte marks set in
+// the per-stream marks buffer *marks (zero between calls: the caller's
+// consumer clears them), as kh_predictor_select_top_k_union before its union
+// kernel.  Needs 64 < out_dim <= 32768.
+int predictor_select_marks(const kh_predictor* p, const float* x, int64_t batch, int k, int32_t* ids,
+                           hipStream_t st, uint8_t** marks) {
+  const int n = p->out_dim;
+  if (n <= 64 || n > 32768) return KH_ERR_UNSUPPORTED;
+  PredBufs b;
+  int rc = pred_bufs(p, st, batch, 0, true, &b);
+  if (rc != KH_OK) return rc;
+  rc = predict_into(p, x, batch, b.sbuf, b, st, NormIn{}, true, nullptr);
+  if (rc != KH_OK) return rc;
+  rc = topk_launch(b.sbuf, batch, n, k, KH_ORDER_ASCENDING, ids, st, nullptr, bounds_ok(p) ? b.mm : nullptr,
+                   l2_blocks(p), b.marks);
+  if (rc != KH_OK) return rc;
+  *marks = b.marks;
+  return KH_OK;
+}
+
 int predictor_l2_topk_from_h(const kh_predictor* p, int k, int32_t* ids, hipStream_t st) {
   PredBufs b;
   int rc = pred_bufs(p, st, 1, 0, false, &b);

@@ -298,3 +298,20 @@ def mlp_block(predictor: SparsityPredictor, mlp: Mlp, hidden: torch.Tensor, norm
     _lib.call("kh_dejavu_mlp_block", predictor._h, mlp._h, ptr(hidden), ptr(norm_w), float(eps), k, ptr(active),
               ptr(norm_ws), stream_ptr(stream))
     return active
+
+
+def mlp_block_batch(predictor: SparsityPredictor, mlp: Mlp, hidden: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                    k: int, active: torch.Tensor | None = None, norm_ws: torch.Tensor | None = None, stream=None):
+    """mlp_block for rows 0..B-1 of hidden [B][hidden] (crates/klearu-llm/src/sparse/mod.rs:115-142
+    per row): each row's norm and top-k selection are the reference's, bit for bit, and the FFN
+    runs over the union of the rows' selections, the shared active set of
+    Mlp.forward_sparse_into with the union from select_top_k_union.  `norm_ws` [B] receives the
+    rows' RmsNorm scales.  Returns the active ids [B][k] (ascending per row)."""
+    B = hidden.shape[0]
+    if norm_ws is None:
+        norm_ws = torch.empty(B, dtype=torch.float32, device=hidden.device)
+    if active is None:
+        active = torch.empty(B, k, dtype=torch.int32, device=hidden.device)
+    _lib.call("kh_dejavu_mlp_block_batch", predictor._h, mlp._h, ptr(hidden), B, ptr(norm_w), float(eps), k,
+              ptr(active), ptr(norm_ws), stream_ptr(stream))
+    return active

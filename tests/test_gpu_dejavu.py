@@ -500,6 +500,50 @@ def test_batched_norm_select_union_exact(kh, orc):
     np.testing.assert_array_equal(uni.cpu().numpy(), np.array(sorted(want_u), np.int32))
 
 
+@pytest.mark.parametrize("H,R,I,k,B", [
+    (4096, 256, 11008, 1652, 16),  # cfg3 batch 16: union from the marks inside the gate/up kernel
+    (512, 64, 1000, 150, 3),       # small, the same path
+    (384, 32, 700, 90, 5),         # hidden not a multiple of 512: the union kernel, then the FFN
+])
+def test_mlp_block_batch_matches_unfused(kh, orc, H, R, I, k, B):
+    """kh_dejavu_mlp_block_batch over three chained calls: every row's RmsNorm
+    scale and top-k ids equal the oracle's (rms_norm.rs:43-53,
+    mlp_predictor.rs:127-132), and the updated rows equal, bit for bit, what
+    kh_rmsnorm + kh_predictor_select_top_k_union + kh_sparse_ffn_forward
+    produce from the same rows (the same FFN over the same union); the second
+    and third calls show the union marks were cleared in between."""
+    from klearu_amd.dejavu import Mlp, SparsityPredictor, mlp_block_batch, rmsnorm
+    rng = np.random.default_rng(H + I + B)
+    w1, b1, w2, b2 = make_predictor(orc, rng, H, R, I, bias=True)
+    p = SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2)
+    wg, wu, wd, x, _ = _ffn_case(orc, rng, H, I, 1, B)
+    mlp = Mlp(wg, wu, wd, max_batch=B)
+    wn = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    wnd = torch.from_numpy(wn).cuda()
+    hd = torch.from_numpy(x.copy()).cuda()
+    ws = torch.empty(B, dtype=torch.float32, device="cuda")
+    for call in range(3):
+        h_in = hd.clone()
+        ws.fill_(float("nan"))
+        act = mlp_block_batch(p, mlp, hd, wnd, 1e-5, k, norm_ws=ws).cpu().numpy()
+        # the unfused sequence on the same input rows
+        nd = rmsnorm(h_in, wnd, 1e-5)
+        ids, uni, cnt = p.select_top_k_union(nd, k)
+        want = h_in.clone()
+        mlp.forward_sparse_into(nd, uni, want, n_active_dev=cnt, accumulate=True)
+        np.testing.assert_array_equal(hd.cpu().numpy(), want.cpu().numpy(), err_msg=f"call {call}: rows")
+        hn = h_in.cpu().numpy()
+        scales = ws.cpu().numpy()
+        for b in range(B):
+            inv = np.array([orc.rms_inv(hn[b], 1e-5)], np.float32)
+            np.testing.assert_array_equal(scales[b:b + 1].view(np.uint32), inv.view(np.uint32),
+                                          err_msg=f"call {call} row {b}: norm scale")
+            norm = orc.rmsnorm(hn[b], wn, 1e-5)
+            scores, _ = orc.predictor_predict(w1, b1, w2, b2, norm)
+            np.testing.assert_array_equal(act[b], np.sort(orc.select_top_k(scores, k)),
+                                          err_msg=f"call {call} row {b}: ids")
+
+
 def test_sparse_ffn_out_of_range_ids_are_reported(kh, orc):
     """An active id outside [0, intermediate) (the reference panics in
     get_weights, crates/klearu-accel/src/memory/mod.rs:87-92) reads no memory
