@@ -153,18 +153,23 @@ __device__ __forceinline__ void attn_select_heads(const PW* __restrict__ w2, con
 // wave (rows w, w + waves, ...) over the head predictor's layer-1 outputs
 // hpred[batch][phid]: s_any[h] = 1 when some row selected head h, s_heads[b k
 // + i] the k heads of row b in ascending order.  s_hp holds batch rows of
-// kSelHs floats.  Every wave of the block takes part.
+// kSelHs floats.  The block copies W2 (blocked [ceil(phid/8)][nh][8]) to s_w2
+// once and every wave reads its lanes' rows from there: many blocks run the
+// same selection, and per-wave reads of W2 from global memory would all hit
+// the same few L2 lines.  Every wave of the block takes part.
 constexpr int kSelHs = kAttnSelHid + 4 * kL2Hw;
 template <typename PW>
 __device__ __forceinline__ void attn_select_heads_rows(const PW* __restrict__ w2, const float* __restrict__ b2,
                                                        const float* __restrict__ hpred, int phid, int nh, int k,
                                                        int batch, float* s_hp, uint64_t* s_tab, int* s_any,
-                                                       int32_t* s_heads) {
-  using V = typename Blk8<PW>::V;
+                                                       int32_t* s_heads, typename Blk8<PW>::V* s_w2) {
+  using B8 = Blk8<PW>;
+  using V = typename B8::V;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int oc = min(lane, nh - 1);
-  V w[kAttnSelHid / 8];
-  l2_load<PW, kAttnSelHid>(w2, phid, nh, oc, w);
+  const int nblk = (phid + 7) >> 3;
+  const V* __restrict__ wv = reinterpret_cast<const V*>(w2);
+  for (int i = threadIdx.x; i < nblk * nh; i += blockDim.x) s_w2[i] = wv[i];
   const float bv = b2[oc];
   for (int i = threadIdx.x; i < batch * phid; i += blockDim.x) {
     const int b = i / phid;
@@ -173,6 +178,9 @@ __device__ __forceinline__ void attn_select_heads_rows(const PW* __restrict__ w2
   if (threadIdx.x < 32) s_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   if (threadIdx.x < 64) s_any[threadIdx.x] = 0;
   __syncthreads();
+  V w[kAttnSelHid / 8];
+#pragma unroll
+  for (int jb = 0; jb < kAttnSelHid / 8; ++jb) w[jb] = jb < nblk ? s_w2[jb * nh + oc] : B8::zero();
   for (int b = wave; b < batch; b += nw) {
     const float score = sigmoid_ref_t(__fadd_rn(l2_chain<PW, kAttnSelHid>(w, phid, s_hp + b * kSelHs), bv), s_tab);
     const bool ok = lane < nh;
@@ -443,76 +451,43 @@ __global__ __launch_bounds__(kL1LdsThreads) void attn_pred_kv_kernel(
   }
 }
 
-// Batched q/k/v projections (2..16 tokens) on the matrix cores: the K and V
-// rows and the Q rows of heads that some token selected, 64 rows per block
-// (four 16-row tiles per wave sharing the x operand), each of the 8 waves
-// taking one eighth of k; x is split into BF16 hi/lo terms as for the batched
-// FFN, and the eighths are added in a fixed order through LDS.  The last
-// block writes the o_proj row list as attn_qkv_kernel does.
-// PW (not void): the heads are selected, not read: the Q-row blocks and the
-// last block run every row's head predictor layer 2 and top k
-// (attn_select_heads_rows over hpred[batch][phid]); the last block writes
-// them to heads_out[batch][nsel] for the kernels after this one.  The K/V
-// blocks do not wait for the selection.
-constexpr int kQmTiles = 4;                  // 16-row tiles per wave
+// RmsNorm's output of four elements: (v * inv) * w, each product rounded
+// (rms_norm.rs:53-63, the same products as the layer-1 block body's).
+__device__ __forceinline__ float4 rms_apply4(const float4& v, float inv, const float4& w) {
+  return make_float4(__fmul_rn(__fmul_rn(v.x, inv), w.x), __fmul_rn(__fmul_rn(v.y, inv), w.y),
+                     __fmul_rn(__fmul_rn(v.z, inv), w.z), __fmul_rn(__fmul_rn(v.w, inv), w.w));
+}
+
+// Batched q/k/v projections (2..16 tokens) on the matrix cores.  A block
+// takes 16*T rows (T 16-row tiles per wave sharing the x operand), each of its
+// 8 waves one eighth of k; x is split into BF16 hi/lo terms as for the batched
+// FFN, and the eighths are added in a fixed order through LDS.
+constexpr int kQmTiles = 4;                  // 16-row tiles per wave (whole projection)
 constexpr int kQmSplit = 8;                  // waves per block, one k-eighth each
 constexpr int kQmDepth = 2;                  // k-steps of loads in flight per wave
 constexpr int kQmRows = 16 * kQmTiles;       // rows per block
 constexpr int kQmAlign = 64 * kQmSplit * kQmDepth;  // hidden must be a multiple
+constexpr int kQqTiles = 1, kQqDepth = 4;    // the Q rows alone (the K/V rows projected before)
+constexpr int kQqAlign = 64 * kQmSplit * kQqDepth;
 // TILED: W is the tiled copy (mfma_tile16x32), so that each weight load
 // instruction of a wave reads one contiguous 1 KB tile instead of 64 bytes
 // from each of 16 rows: measured 5.9 TB/s for such a stream against 3.2 TB/s
 // for the row-major gather.
-template <bool TILED, typename PW = void>
-__global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
-    const uint16_t* __restrict__ W, const float* __restrict__ x, int batch, int H, int kvrows,
-    int rows, int D, int nh,
-    const int32_t* __restrict__ heads, int nsel, float* __restrict__ y, int ystride,
-    int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows, int32_t* __restrict__ urank,
-    const PW* __restrict__ w2 = nullptr, const float* __restrict__ b2 = nullptr,
-    const float* __restrict__ hpred = nullptr, int phid = 0, int32_t* __restrict__ heads_out = nullptr) {
-  constexpr int T = kQmTiles, S = kQmSplit, DEP = kQmDepth;
-  constexpr bool SEL = !std::is_void<PW>::value;
-  __shared__ kh_f32x4 part[S - 1][2 * T][64];
-  __shared__ int s_flag[kMaxAttnHeads], s_uh[kMaxAttnHeads];
-  __shared__ int wsum[S];
-  __shared__ int s_total;
-  const int nent = batch * nsel;
+
+// Rows [base, base + 16 T) of W times the batch's x rows: y[b][row] for
+// b < batch and row < rows.  part: LDS for the waves' partial tiles,
+// [kQmSplit - 1][2 T][64].  NORM: x row b is normalised as it is read,
+// (x * inv[b]) * nw, with the scales inv in LDS.  Every thread of the block
+// calls it (one barrier).
+template <bool TILED, int T, int DEP, bool NORM>
+__device__ __forceinline__ void qkv_mfma_rows(const uint16_t* __restrict__ W, const float* __restrict__ x,
+                                              int batch, int H, int rows, int base, float* __restrict__ y,
+                                              int ystride, kh_f32x4* part, const float* __restrict__ nw,
+                                              const float* inv) {
+  constexpr int S = kQmSplit;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int base = blockIdx.x * kQmRows;
-  const bool plan = blockIdx.x == gridDim.x - 1;
-  bool live = base < rows;
-  // selection scratch in the partial-sum array (written only after the k loop)
-  static_assert(sizeof(part) >= sizeof(float) * 16 * kSelHs + sizeof(int) * (64 + 16 * 64) +
-                                    sizeof(uint64_t) * 32, "selection scratch fits");
-  uint64_t* s_tab = reinterpret_cast<uint64_t*>(&part[0][0][0]);
-  int* s_any = reinterpret_cast<int*>(s_tab + 32);
-  int32_t* s_heads = s_any + 64;
-  float* s_hp = reinterpret_cast<float*>(s_heads + 16 * 64);
-  if constexpr (SEL) {
-    if (plan) {
-      attn_select_heads_rows<PW>(w2, b2, hpred, phid, nh, nsel, batch, s_hp, s_tab, s_any, s_heads);
-      for (int i = threadIdx.x; i < nent; i += blockDim.x) heads_out[i] = s_heads[i];
-      qkv_plan(s_heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_uh, wsum, &s_total);
-      return;
-    }
-  } else {
-    if (plan) {
-      qkv_plan(heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_uh, wsum, &s_total);
-      return;
-    }
-    if (live && base >= kvrows) {
-      // Q rows of head h (D is a multiple of 64): skipped unless some token selected h
-      const int h = (base - kvrows) / D;
-      int any = 0;
-      for (int i = lane; i < nent; i += 64) any |= heads[i] == h;
-      live = __ballot(any) != 0;
-    }
-  }
-  // SEL: a Q-row block selects the heads after issuing its first weight loads
-  const bool sel_q = SEL && live && base >= kvrows;
   const int r = lane & 15, kb = lane >> 4;
-  const int qsteps = H / (64 * S);  // k-steps per eighth
+  const int qsteps = H / (64 * S);  // k-steps per eighth, a multiple of DEP (host-checked)
   const int s0 = wave * qsteps;
   const uint4* __restrict__ wp[T];
 #pragma unroll
@@ -528,13 +503,15 @@ __global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
   const int xr = min(r, batch - 1);
   // x of token r: k-step s, MFMA e reads k = 64 s + 32 e + 8 kb + [0, 8) as two float4
   const float4* __restrict__ xf = reinterpret_cast<const float4*>(x + (size_t)xr * H) + 2 * kb + 16 * s0;
+  const float4* __restrict__ nwf = reinterpret_cast<const float4*>(nw) + 2 * kb + 16 * s0;  // NORM
+  const float iv = NORM ? inv[xr] : 1.0f;
   kh_f32x4 c[T][2];
 #pragma unroll
   for (int t = 0; t < T; ++t) c[t][0] = c[t][1] = kh_f32x4{0, 0, 0, 0};
   uint4 bw[DEP][T][2];
   float4 bx[DEP][2][2];
-  // clamped, unconditional (past the end: reread, unused)
-  auto loadw = [&](int d, int st) {
+  float4 bn[DEP][2][2];  // NORM: the norm weights at the same k
+  auto load = [&](int d, int st) {  // clamped, unconditional (past the end: reread, unused)
     const int o = 8 * min(st, qsteps - 1);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -547,78 +524,164 @@ __global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
         bw[d][t][1] = ld_stream(wp[t] + o + 4);
       }
     }
-  };
-  auto loadx = [&](int d, int st) {
-    const int o = 8 * min(st, qsteps - 1);
     bx[d][0][0] = xf[2 * o]; bx[d][0][1] = xf[2 * o + 1];
     bx[d][1][0] = xf[2 * o + 8]; bx[d][1][1] = xf[2 * o + 9];
-  };
-  auto load = [&](int d, int st) {
-    loadw(d, st);
-    loadx(d, st);
-  };
-  if constexpr (SEL) {
-    if (sel_q) {
-      loadw(0, 0);  // in flight during the selection
-      __builtin_amdgcn_sched_barrier(0);
-      attn_select_heads_rows<PW>(w2, b2, hpred, phid, nh, nsel, batch, s_hp, s_tab, s_any, s_heads);
-      live = s_any[(base - kvrows) / D] != 0;
-      __syncthreads();  // every wave has read s_any before part is written
-      if (live) {
-        loadx(0, 0);
-#pragma unroll
-        for (int d = 1; d < DEP; ++d) load(d, d);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    if constexpr (NORM) {
+      bn[d][0][0] = nwf[2 * o]; bn[d][0][1] = nwf[2 * o + 1];
+      bn[d][1][0] = nwf[2 * o + 8]; bn[d][1][1] = nwf[2 * o + 9];
     }
-  }
-  if (live && !sel_q) {
+  };
 #pragma unroll
-    for (int d = 0; d < DEP; ++d) load(d, d);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  if (live) {
-    // qsteps is a multiple of DEP (host-checked): no test inside the loop
-    for (int st = 0; st < qsteps; st += DEP) {
+  for (int d = 0; d < DEP; ++d) load(d, d);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int st = 0; st < qsteps; st += DEP) {
 #pragma unroll
-      for (int d = 0; d < DEP; ++d) {
+    for (int d = 0; d < DEP; ++d) {
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          uint4 xh, xl;
+      for (int e = 0; e < 2; ++e) {
+        uint4 xh, xl;
+        if constexpr (NORM)
+          split_bf16x8(rms_apply4(bx[d][e][0], iv, bn[d][e][0]), rms_apply4(bx[d][e][1], iv, bn[d][e][1]), xh, xl);
+        else
           split_bf16x8(bx[d][e][0], bx[d][e][1], xh, xl);
 #pragma unroll
-          for (int t = 0; t < T; ++t) {
-            c[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bw[d][t][e]), as_bf16x8(xh), c[t][0], 0, 0, 0);
-            c[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bw[d][t][e]), as_bf16x8(xl), c[t][1], 0, 0, 0);
-          }
+        for (int t = 0; t < T; ++t) {
+          c[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bw[d][t][e]), as_bf16x8(xh), c[t][0], 0, 0, 0);
+          c[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bw[d][t][e]), as_bf16x8(xl), c[t][1], 0, 0, 0);
         }
-        load(d, st + d + DEP);
-        // keep the prefetch here: the scheduler would otherwise sink it to its use
-        __builtin_amdgcn_sched_barrier(0);
       }
+      load(d, st + d + DEP);
+      // keep the prefetch here: the scheduler would otherwise sink it to its use
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   // C[row][token]: lane holds rows 16 t + 4 kb + q (q = 0..3) of token r
   if (wave > 0) {
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      part[wave - 1][2 * t][lane] = c[t][0];
-      part[wave - 1][2 * t + 1][lane] = c[t][1];
+      part[((wave - 1) * 2 * T + 2 * t) * 64 + lane] = c[t][0];
+      part[((wave - 1) * 2 * T + 2 * t + 1) * 64 + lane] = c[t][1];
     }
   }
   __syncthreads();
-  if (wave > 0 || !live) return;
+  if (wave > 0) return;
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     kh_f32x4 acc = c[t][0] + c[t][1];
 #pragma unroll
-    for (int j = 0; j < S - 1; ++j) acc += part[j][2 * t][lane] + part[j][2 * t + 1][lane];
+    for (int j = 0; j < S - 1; ++j) acc += part[(j * 2 * T + 2 * t) * 64 + lane] + part[(j * 2 * T + 2 * t + 1) * 64 + lane];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int item = base + 16 * t + 4 * kb + q;
       if (r < batch && item < rows) y[(size_t)r * ystride + item] = acc[q];
     }
   }
+}
+
+// The projections of rows [row_base, rows) (the K and V rows, then the Q rows
+// of heads that some token selected), 16*T rows per block over
+// qkv_mfma_rows.  The last block also writes the o_proj row list, as
+// attn_qkv_kernel's extra block does.
+// PW (not void): the heads are selected, not read: the Q-row blocks and the
+// last block run every row's head predictor layer 2 and top k
+// (attn_select_heads_rows over hpred[batch][phid]); the last block writes
+// them to heads_out[batch][nsel] for the kernels after this one.  The K/V
+// blocks do not wait for the selection.
+template <bool TILED, typename PW = void, int T = kQmTiles, int DEP = kQmDepth>
+__global__ __launch_bounds__(64 * kQmSplit) void attn_qkv_mfma_kernel(
+    const uint16_t* __restrict__ W, const float* __restrict__ x, int batch, int H, int kvrows,
+    int rows, int D, int nh,
+    const int32_t* __restrict__ heads, int nsel, float* __restrict__ y, int ystride,
+    int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows, int32_t* __restrict__ urank,
+    int row_base = 0, const PW* __restrict__ w2 = nullptr, const float* __restrict__ b2 = nullptr,
+    const float* __restrict__ hpred = nullptr, int phid = 0, int32_t* __restrict__ heads_out = nullptr) {
+  constexpr int S = kQmSplit;
+  constexpr bool SEL = !std::is_void<PW>::value;
+  using WV = typename Blk8<typename std::conditional<SEL, PW, uint16_t>::type>::V;
+  __shared__ kh_f32x4 part[(S - 1) * 2 * T * 64];
+  __shared__ WV s_w2[SEL ? kAttnSelHid / 8 * 64 : 1];  // the head predictor's W2 (SEL)
+  __shared__ int s_flag[kMaxAttnHeads], s_uh[kMaxAttnHeads];
+  __shared__ int wsum[S];
+  __shared__ int s_total;
+  const int nent = batch * nsel;
+  const int lane = threadIdx.x & 63;
+  const int base = row_base + blockIdx.x * 16 * T;
+  // the last block also writes the plan (first: a grid of one block more than
+  // the CUs would run that block in a second round)
+  const bool plan = blockIdx.x == gridDim.x - 1;
+  bool live = true;  // base < rows for every block
+  if constexpr (SEL) {
+    if (plan || base >= kvrows) {
+      // selection scratch in the (not yet used) partial-sum array
+      static_assert(sizeof(part) >= sizeof(float) * 16 * kSelHs + sizeof(int) * (64 + 16 * 64) +
+                                        sizeof(uint64_t) * 32, "selection scratch fits");
+      uint64_t* s_tab = reinterpret_cast<uint64_t*>(part);
+      int* s_any = reinterpret_cast<int*>(s_tab + 32);
+      int32_t* s_heads = s_any + 64;
+      float* s_hp = reinterpret_cast<float*>(s_heads + 16 * 64);
+      attn_select_heads_rows<PW>(w2, b2, hpred, phid, nh, nsel, batch, s_hp, s_tab, s_any, s_heads, s_w2);
+      if (plan) {
+        for (int i = threadIdx.x; i < nent; i += blockDim.x) heads_out[i] = s_heads[i];
+        qkv_plan(s_heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_uh, wsum, &s_total);
+      }
+      if (base >= kvrows) live = s_any[(base - kvrows) / D] != 0;
+      __syncthreads();  // every wave has read s_any before part is written
+    }
+  } else {
+    if (plan) qkv_plan(heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_uh, wsum, &s_total);
+    if (base >= kvrows) {
+      // Q rows of head h (D is a multiple of 16 T): skipped unless some token selected h
+      const int h = (base - kvrows) / D;
+      int any = 0;
+      for (int i = lane; i < nent; i += 64) any |= heads[i] == h;
+      live = __ballot(any) != 0;
+    }
+  }
+  if (!live) return;  // uniform
+  qkv_mfma_rows<TILED, T, DEP, false>(W, x, batch, H, rows, base, y, ystride, part, nullptr, nullptr);
+}
+
+// The head predictor's layer 1 and the K/V projections of a batched decode
+// step in one launch (the batch-1 form is attn_pred_kv_kernel): blocks
+// [0, nl1 * batch) run layer 1 of row b = block / nl1 (pred_l1.hpp: exact
+// RmsNorm, exact chains; block 0 of each row writes the row's scale to
+// inv_out and the normalised row to xn_out), the others project 16 kQmTiles
+// K/V rows each (qkv_mfma_rows) meanwhile.  The launch asks for the layer-1
+// LDS size, so one block fits per CU.  A K/V block normalises x with scales
+// of its own, from an f32 tree sum of the squares per row: the projected rows
+// carry tolerance anyway, and only the selection needs the exact scale.
+template <typename W, bool TILED>
+__global__ __launch_bounds__(kL1LdsThreads) void attn_pred_kv_mfma_kernel(
+    const W* __restrict__ w1, const float* __restrict__ b1, int hid, float* __restrict__ hbuf,
+    const float* __restrict__ x, int batch, int H, const float* __restrict__ nw, float* __restrict__ inv_out,
+    float eps, float* __restrict__ xn_out, const uint16_t* __restrict__ wkvq, int rows, float* __restrict__ y,
+    int ystride, int nl1) {
+  static_assert(kL1LdsThreads == 64 * kQmSplit, "one k-eighth per wave");
+  static_assert(sizeof(float4) * 16 + sizeof(kh_f32x4) * (kQmSplit - 1) * 2 * kQmTiles * 64 <= kL1LdsBytes,
+                "the K/V blocks' LDS fits the launch's");
+  extern __shared__ float4 lds4[];
+  const int nlb = nl1 * batch;
+  if ((int)blockIdx.x < nlb) {
+    pred_l1_lds_body<W>((int)blockIdx.x % nl1, (int)blockIdx.x / nl1, w1, b1, x, H, hid, hbuf, nw, inv_out,
+                        eps, lds4, xn_out);
+    return;
+  }
+  float* s_inv = reinterpret_cast<float*>(lds4);               // [16]
+  kh_f32x4* part = reinterpret_cast<kh_f32x4*>(lds4 + 16);     // [S - 1][2 T][64]
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int b = wave; b < batch; b += kQmSplit) {
+    const float4* xb = reinterpret_cast<const float4*>(x + (size_t)b * H);
+    float ss = 0.0f;
+    for (int i = lane; i < (H >> 2); i += 64) {
+      const float4 v = xb[i];
+      ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) s_inv[b] = rms_inv_exact(ss, H, eps);
+  }
+  __syncthreads();
+  qkv_mfma_rows<TILED, kQmTiles, kQmDepth, true>(wkvq, x, batch, H, rows, ((int)blockIdx.x - nlb) * kQmRows, y,
+                                                 ystride, part, nw, s_inv);
 }
 
 // Cache positions per decode block: kAttnPasses rows per thread.
@@ -1526,13 +1589,27 @@ static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
   return KH_OK;
 }
 
+// attn_qkv_mfma_kernel over rows [row_base, kvrows + qd) (+ the plan block);
+// hsel (PW not void): the heads selected inside from hsel's layer-1 outputs.
+template <bool TILED, typename PW, int T, int DEP>
+static void qm_launch(kh_sparse_attn* a, const uint16_t* w, const float* x, int batch, const int32_t* heads,
+                      int nsel, int row_base, const PredL1View* hsel, int32_t* hout, hipStream_t st) {
+  const int H = a->hidden, D = a->d, qd = a->nh * D, kvrows = 2 * a->kvd(), rows = kvrows + qd;
+  const dim3 g(ceil_div(rows - row_base, 16 * T)), blk(64 * kQmSplit);
+  hipLaunchKernelGGL((attn_qkv_mfma_kernel<TILED, PW, T, DEP>), g, blk, 0, st, w, x, batch, H, kvrows, rows, D,
+                     a->nh, heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1, row_base,
+                     hsel ? static_cast<const PW*>(hsel->w2b) : nullptr, hsel ? hsel->b2 : nullptr,
+                     hsel ? hsel->hbuf : nullptr, hsel ? hsel->hid : 0, hout);
+}
+
 // nrm.w set (batch 1 only): x is the un-normalised hidden row, normalised
 // inside the projection kernel with the scale at nrm.inv.
 // hsel with batch > 1: x holds the normalised rows, and the heads are selected
 // inside the projection (the head predictor's layer 2 over hsel->hbuf) and
 // written to heads.
-// kv_done (batch 1 with nrm.w): attn_pred_kv_kernel projected the K/V rows,
-// so only the selected heads' Q rows remain.
+// kv_done (batch 1 with nrm.w, or batch > 1 with hsel): attn_pred_kv_kernel or
+// attn_pred_kv_mfma_kernel projected the K/V rows, so only the selected heads'
+// Q rows remain.
 template <int NB>
 static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64_t* pos,
                        const int32_t* heads, int nsel, float* out, int accumulate,
@@ -1542,36 +1619,31 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   // 1. projections (+ the o_proj row list in the last block)
   const int rows = kvrows + qd;
   if (NB > 1 && H % kQmAlign == 0 && !nrm.w) {
-    const dim3 g(ceil_div(rows, kQmRows) + 1), blk(64 * kQmSplit);
-    const uint16_t* w = a->wkvq_t ? a->wkvq_t : a->wkvq;
+    const bool t = a->wkvq_t != nullptr;
+    const uint16_t* w = t ? a->wkvq_t : a->wkvq;
     int32_t* hout = const_cast<int32_t*>(heads);
     if (!hsel) {
-      if (a->wkvq_t)
-        hipLaunchKernelGGL(attn_qkv_mfma_kernel<true>, g, blk, 0, st, w, x, batch, H, kvrows, rows, D, a->nh,
-                           heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1);
-      else
-        hipLaunchKernelGGL(attn_qkv_mfma_kernel<false>, g, blk, 0, st, w, x, batch, H, kvrows, rows, D, a->nh,
-                           heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1);
+      if (t) qm_launch<true, void, kQmTiles, kQmDepth>(a, w, x, batch, heads, nsel, 0, nullptr, nullptr, st);
+      else qm_launch<false, void, kQmTiles, kQmDepth>(a, w, x, batch, heads, nsel, 0, nullptr, nullptr, st);
+    } else if (kv_done) {
+      // the K/V rows are projected: the Q rows alone, one 16-row tile per block
+      if (H % kQqAlign != 0) {
+        set_error("the overlapped batched attention block needs hidden a multiple of %d", kQqAlign);
+        return KH_ERR_UNSUPPORTED;
+      }
+      if (hsel->bf16) {
+        if (t) qm_launch<true, uint16_t, kQqTiles, kQqDepth>(a, w, x, batch, nullptr, nsel, kvrows, hsel, hout, st);
+        else qm_launch<false, uint16_t, kQqTiles, kQqDepth>(a, w, x, batch, nullptr, nsel, kvrows, hsel, hout, st);
+      } else {
+        if (t) qm_launch<true, float, kQqTiles, kQqDepth>(a, w, x, batch, nullptr, nsel, kvrows, hsel, hout, st);
+        else qm_launch<false, float, kQqTiles, kQqDepth>(a, w, x, batch, nullptr, nsel, kvrows, hsel, hout, st);
+      }
     } else if (hsel->bf16) {
-      const uint16_t* w2 = static_cast<const uint16_t*>(hsel->w2b);
-      if (a->wkvq_t)
-        hipLaunchKernelGGL((attn_qkv_mfma_kernel<true, uint16_t>), g, blk, 0, st, w, x, batch, H, kvrows, rows, D,
-                           a->nh, nullptr, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1,
-                           w2, hsel->b2, hsel->hbuf, hsel->hid, hout);
-      else
-        hipLaunchKernelGGL((attn_qkv_mfma_kernel<false, uint16_t>), g, blk, 0, st, w, x, batch, H, kvrows, rows,
-                           D, a->nh, nullptr, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
-                           a->qrows + qd + 1, w2, hsel->b2, hsel->hbuf, hsel->hid, hout);
+      if (t) qm_launch<true, uint16_t, kQmTiles, kQmDepth>(a, w, x, batch, nullptr, nsel, 0, hsel, hout, st);
+      else qm_launch<false, uint16_t, kQmTiles, kQmDepth>(a, w, x, batch, nullptr, nsel, 0, hsel, hout, st);
     } else {
-      const float* w2 = static_cast<const float*>(hsel->w2b);
-      if (a->wkvq_t)
-        hipLaunchKernelGGL((attn_qkv_mfma_kernel<true, float>), g, blk, 0, st, w, x, batch, H, kvrows, rows, D,
-                           a->nh, nullptr, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1,
-                           w2, hsel->b2, hsel->hbuf, hsel->hid, hout);
-      else
-        hipLaunchKernelGGL((attn_qkv_mfma_kernel<false, float>), g, blk, 0, st, w, x, batch, H, kvrows, rows, D,
-                           a->nh, nullptr, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd, a->qrows + qd + 1,
-                           w2, hsel->b2, hsel->hbuf, hsel->hid, hout);
+      if (t) qm_launch<true, float, kQmTiles, kQmDepth>(a, w, x, batch, nullptr, nsel, 0, hsel, hout, st);
+      else qm_launch<false, float, kQmTiles, kQmDepth>(a, w, x, batch, nullptr, nsel, 0, hsel, hout, st);
     }
     KH_LAUNCHED();
   } else if (NB > 1 && hsel) {
@@ -1823,19 +1895,52 @@ extern "C" int kh_dejavu_attn_block_batch(const kh_predictor* p, kh_sparse_attn*
   float* xn = static_cast<float*>(a->xn.get(sizeof(float) * batch * a->hidden));
   if (!xn) return KH_ERR_ALLOC;
   PredL1View v;
-  int rc = predictor_l1_normed(p, hidden_dev, batch, nrm, xn, st, &v);
+  int rc = predictor_l1_view(p, st, &v, batch);
   if (rc != KH_OK) return rc;
   if (v.hid > kAttnSelHid) {
     set_error("the batched fused attention block selects heads of predictors with at most %d hidden "
               "units (got %d)", kAttnSelHid, v.hid);
     return KH_ERR_UNSUPPORTED;
   }
+  const int kvrows = 2 * a->kvd();
+  const bool kv_done = kvrows % kQmRows == 0 && a->hidden % kQqAlign == 0 && a->wkvq_t;
+  if (kv_done) {
+    // the head predictor's layer 1 and the K/V rows in one launch, then the
+    // selected heads' Q rows
+    static std::once_flag once;
+    static hipError_t arc = hipSuccess;
+    std::call_once(once, [] {
+      arc = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_pred_kv_mfma_kernel<uint16_t, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kL1LdsBytes);
+      if (arc == hipSuccess)
+        arc = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_pred_kv_mfma_kernel<float, true>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kL1LdsBytes);
+    });
+    KH_HIP(arc);
+    const int nl1 = ceil_div(v.hid, kL1Chains);
+    const dim3 g(nl1 * static_cast<unsigned>(batch) + kvrows / kQmRows);
+    const int rows = kvrows + a->nh * a->d;
+    if (v.bf16)
+      hipLaunchKernelGGL((attn_pred_kv_mfma_kernel<uint16_t, true>), g, dim3(kL1LdsThreads), kL1LdsBytes, st,
+                         static_cast<const uint16_t*>(v.w1b), v.b1, v.hid, v.hbuf, hidden_dev,
+                         static_cast<int>(batch), a->hidden, norm_w_dev, norm_ws_dev, eps, xn, a->wkvq_t, rows,
+                         a->y, a->ystride(), nl1);
+    else
+      hipLaunchKernelGGL((attn_pred_kv_mfma_kernel<float, true>), g, dim3(kL1LdsThreads), kL1LdsBytes, st,
+                         static_cast<const float*>(v.w1b), v.b1, v.hid, v.hbuf, hidden_dev,
+                         static_cast<int>(batch), a->hidden, norm_w_dev, norm_ws_dev, eps, xn, a->wkvq_t, rows,
+                         a->y, a->ystride(), nl1);
+    KH_LAUNCHED();
+  } else {
+    rc = predictor_l1_normed(p, hidden_dev, batch, nrm, xn, st, &v);
+    if (rc != KH_OK) return rc;
+  }
   const int b = static_cast<int>(batch);
   switch (b <= 2 ? 2 : b <= 4 ? 4 : b <= 8 ? 8 : 16) {
-    case 2: rc = attn_launch<2>(a, xn, b, nullptr, heads_dev, k, hidden_dev, 1, st, NormIn{}, false, &v); break;
-    case 4: rc = attn_launch<4>(a, xn, b, nullptr, heads_dev, k, hidden_dev, 1, st, NormIn{}, false, &v); break;
-    case 8: rc = attn_launch<8>(a, xn, b, nullptr, heads_dev, k, hidden_dev, 1, st, NormIn{}, false, &v); break;
-    default: rc = attn_launch<16>(a, xn, b, nullptr, heads_dev, k, hidden_dev, 1, st, NormIn{}, false, &v); break;
+    case 2: rc = attn_launch<2>(a, xn, b, nullptr, heads_dev, k, hidden_dev, 1, st, NormIn{}, kv_done, &v); break;
+    case 4: rc = attn_launch<4>(a, xn, b, nullptr, heads_dev, k, hidden_dev, 1, st, NormIn{}, kv_done, &v); break;
+    case 8: rc = attn_launch<8>(a, xn, b, nullptr, heads_dev, k, hidden_dev, 1, st, NormIn{}, kv_done, &v); break;
+    default: rc = attn_launch<16>(a, xn, b, nullptr, heads_dev, k, hidden_dev, 1, st, NormIn{}, kv_done, &v); break;
   }
   if (rc == KH_OK)
     for (int64_t i = 0; i < batch; ++i) a->len_host[i] += 1;

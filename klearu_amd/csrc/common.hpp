@@ -354,7 +354,7 @@ struct PredL1View {
   bool bf16 = false;
   float* hbuf = nullptr;       // [hid] layer-1 outputs of one row
 };
-int predictor_l1_view(const kh_predictor* p, hipStream_t st, PredL1View* v);
+int predictor_l1_view(const kh_predictor* p, hipStream_t st, PredL1View* v, int64_t batch = 1);
 int predictor_l2_topk_from_h(const kh_predictor* p, int k, int32_t* ids, hipStream_t st);
 int predictor_select_marks(const kh_predictor* p, const float* x, int64_t batch, int k, int32_t* ids,
                            hipStream_t st, uint8_t** marks);

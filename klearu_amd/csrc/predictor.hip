@@ -1421,9 +1421,9 @@ int predictor_scores_normed(const kh_predictor* p, const float* hidden, const No
   return KH_OK;
 }
 
-int predictor_l1_view(const kh_predictor* p, hipStream_t st, PredL1View* v) {
+int predictor_l1_view(const kh_predictor* p, hipStream_t st, PredL1View* v, int64_t batch) {
   PredBufs b;
-  int rc = pred_bufs(p, st, 1, 0, false, &b);
+  int rc = pred_bufs(p, st, batch, 0, false, &b);
   if (rc != KH_OK) return rc;
   rc = set_kernel_attrs();
   if (rc != KH_OK) return rc;

@@ -317,6 +317,8 @@ def _batch_block_step(orc, c, pw, p, hd, wn, wnd, ws, k, what):
     (4096, 32, 32, 128, 128, 16, 2000, 8, 2),   # cfg4 (7B), batch 8
     (1024, 16, 4, 64, 64, 5, 70, 3, 3),         # GQA, ragged batch
     (1024, 8, 8, 128, 128, 8, 40, 16, 2),       # k = every head, batch 16
+    # hidden a multiple of 2048: the K/V rows in the head predictor's launch
+    (2048, 16, 4, 64, 64, 6, 90, 5, 2),         # GQA
 ])
 def test_attn_block_batch_chained(kh, orc, H, nh, nkv, d, R, k, pre, B, steps):
     """kh_dejavu_attn_block_batch: every row's RmsNorm scale is the
