@@ -1122,9 +1122,16 @@ extern "C" int kh_dejavu_mlp_block_batch(const kh_predictor* p, const kh_sparse_
   }
   const int b = static_cast<int>(batch);
   switch (ffn_tmpl(batch)) {
-    case 2: return ffn_launch<2>(f, xn, b, uni, f->inter, cnt, hidden_dev, 1, st, marks);
-    case 4: return ffn_launch<4>(f, xn, b, uni, f->inter, cnt, hidden_dev, 1, st, marks);
-    case 8: return ffn_launch<8>(f, xn, b, uni, f->inter, cnt, hidden_dev, 1, st, marks);
-    default: return ffn_launch<16>(f, xn, b, uni, f->inter, cnt, hidden_dev, 1, st, marks);
+    case 2: rc = ffn_launch<2>(f, xn, b, uni, f->inter, cnt, hidden_dev, 1, st, marks); break;
+    case 4: rc = ffn_launch<4>(f, xn, b, uni, f->inter, cnt, hidden_dev, 1, st, marks); break;
+    case 8: rc = ffn_launch<8>(f, xn, b, uni, f->inter, cnt, hidden_dev, 1, st, marks); break;
+    default: rc = ffn_launch<16>(f, xn, b, uni, f->inter, cnt, hidden_dev, 1, st, marks); break;
   }
+  if (rc != KH_OK && marks) {
+    // the marks must be zero for the next call: clear them where the down kernel did not
+    const int nw = (f->inter + 3) >> 2;
+    hipLaunchKernelGGL(fill_f32_kernel<>, dim3(ceil_div(nw, 256)), dim3(256), 0, st,
+                       reinterpret_cast<float*>(const_cast<uint8_t*>(marks)), (int64_t)nw, 0.0f);
+  }
+  return rc;
 }
