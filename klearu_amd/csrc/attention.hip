@@ -149,6 +149,28 @@ __device__ __forceinline__ void attn_select_heads(const PW* __restrict__ w2, con
   __syncthreads();
 }
 
+// The head selection of a batch-1 decode step whose projections, the Q rows
+// of every head included, are done: the head predictor's layer 2 and top k
+// (attn_select_heads) into heads_out[k], then the o_proj row list (qkv_plan).
+// One block.
+constexpr int kSelPlanThreads = 256;
+template <typename PW>
+__global__ __launch_bounds__(kSelPlanThreads) void attn_select_plan_kernel(
+    const PW* __restrict__ w2, const float* __restrict__ b2, const float* __restrict__ hpred, int phid, int nh,
+    int k, int D, int32_t* __restrict__ heads_out, int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows,
+    int32_t* __restrict__ urank) {
+  __shared__ int s_hsel[64];
+  __shared__ int32_t s_heads[64];
+  __shared__ __align__(16) float s_hp[kAttnSelHid + 4 * kL2Hw];
+  __shared__ uint64_t s_tab[32];
+  __shared__ int s_flag[64], s_uh[64];
+  __shared__ int wsum[kSelPlanThreads / 64];
+  __shared__ int s_total;
+  attn_select_heads<PW>(w2, b2, hpred, phid, nh, k, s_hp, s_tab, s_hsel, s_heads);
+  if ((int)threadIdx.x < k) heads_out[threadIdx.x] = s_heads[threadIdx.x];
+  qkv_plan(s_heads, k, nh, D, qrows, nqrows, urank, s_flag, s_uh, wsum, &s_total);
+}
+
 // The head selections of rows 0 .. batch-1 as attn_select_heads, one row per
 // wave (rows w, w + waves, ...) over the head predictor's layer-1 outputs
 // hpred[batch][phid]: s_any[h] = 1 when some row selected head h, s_heads[b k
@@ -203,44 +225,23 @@ __device__ __forceinline__ void attn_select_heads_rows(const PW* __restrict__ w2
 // NORM (batch 1): x is the un-normalised hidden row and RmsNorm (weight nw) is
 // applied while staging it, with the exact scale at norm_inv (written by the
 // head predictor's layer 1 for this row).
-// PW (batch 1, not void): the heads are not read but selected by every block
-// (attn_select_heads over the head predictor's layer-1 outputs hpred and its
-// layer 2 w2 / b2, weights of type PW); the last block writes them to
-// heads_out, which the kernels after this one read.
-template <int NB, bool NORM = false, typename PW = void>
+template <int NB, bool NORM = false>
 __global__ __launch_bounds__(64 * kQkvWaves) void attn_qkv_kernel(
     const uint16_t* __restrict__ W, const float* __restrict__ x, int batch, int H, int kvrows,
     int D, int nh, const int32_t* __restrict__ heads, int nsel, float* __restrict__ y,
     int ystride, int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows,
     int32_t* __restrict__ urank, const float* __restrict__ nw,
-    const float* __restrict__ norm_inv, int row_base, const PW* __restrict__ w2 = nullptr,
-    const float* __restrict__ b2 = nullptr, const float* __restrict__ hpred = nullptr, int phid = 0,
-    int32_t* __restrict__ heads_out = nullptr) {
+    const float* __restrict__ norm_inv, int row_base) {
   extern __shared__ float4 xs4[];  // [kQkvTok][H/4]; the plan block's flags / union list
   __shared__ int wsum[kQkvWaves];
   __shared__ int s_total;
-  constexpr bool SEL = !std::is_void<PW>::value;
   const int nent = batch * nsel;
-  if constexpr (SEL) {
-    __shared__ int s_hsel[64];
-    __shared__ int32_t s_heads[64];
-    __shared__ __align__(16) float s_hp[kAttnSelHid + 4 * kL2Hw];
-    __shared__ uint64_t s_tab[32];
-    attn_select_heads<PW>(w2, b2, hpred, phid, nh, nsel, s_hp, s_tab, s_hsel, s_heads);
-    if (blockIdx.x == gridDim.x - 1) {
-      if ((int)threadIdx.x < nsel) heads_out[threadIdx.x] = s_heads[threadIdx.x];
-      int* s_flag = reinterpret_cast<int*>(xs4);
-      qkv_plan(s_heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_flag + nh, wsum, &s_total);
-      return;
-    }
-    const int row0 = row_base + blockIdx.x * kQkvWaves;
-    if (row0 >= kvrows && !s_hsel[(row0 - kvrows) / D]) return;
-  } else {
-    if (blockIdx.x == gridDim.x - 1) {
-      int* s_flag = reinterpret_cast<int*>(xs4);
-      qkv_plan(heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_flag + nh, wsum, &s_total);
-      return;
-    }
+  if (blockIdx.x == gridDim.x - 1) {
+    int* s_flag = reinterpret_cast<int*>(xs4);
+    qkv_plan(heads, nent, nh, D, qrows, nqrows, urank, s_flag, s_flag + nh, wsum, &s_total);
+    return;
+  }
+  {
     const int row0 = row_base + blockIdx.x * kQkvWaves;
     if (row0 >= kvrows) {
       // Q rows of head h (D is a multiple of kQkvWaves): skip unless selected.
@@ -1609,16 +1610,18 @@ static void qm_launch(kh_sparse_attn* a, const uint16_t* w, const float* x, int 
 // written to heads.
 // kv_done (batch 1 with nrm.w, or batch > 1 with hsel): attn_pred_kv_kernel or
 // attn_pred_kv_mfma_kernel projected the K/V rows, so only the selected heads'
-// Q rows remain.
+// Q rows remain.  qkv_done: every projection and the o_proj row list are done
+// (attn_pred_kv_kernel and attn_select_plan_kernel).
 template <int NB>
 static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64_t* pos,
                        const int32_t* heads, int nsel, float* out, int accumulate,
                        hipStream_t st, const NormIn& nrm = NormIn{}, bool kv_done = false,
-                       const PredL1View* hsel = nullptr) {
+                       const PredL1View* hsel = nullptr, bool qkv_done = false) {
   const int H = a->hidden, D = a->d, qd = a->nh * D, kvrows = 2 * a->kvd();
-  // 1. projections (+ the o_proj row list in the last block)
+  // 1. projections (+ the o_proj row list in the last block), unless done
   const int rows = kvrows + qd;
-  if (NB > 1 && H % kQmAlign == 0 && !nrm.w) {
+  if (qkv_done) {
+  } else if (NB > 1 && H % kQmAlign == 0 && !nrm.w) {
     const bool t = a->wkvq_t != nullptr;
     const uint16_t* w = t ? a->wkvq_t : a->wkvq;
     int32_t* hout = const_cast<int32_t*>(heads);
@@ -1656,11 +1659,6 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
                                  hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
       KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_qkv_kernel<1, true>),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
-      // the head selection's static LDS comes on top of the dynamic part
-      KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_qkv_kernel<1, true, uint16_t>),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds - 8192));
-      KH_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_qkv_kernel<1, true, float>),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds - 8192));
       attr_set = true;
     }
     const size_t lds = std::max(sizeof(float) * std::min(NB, kQkvTok) * H,
@@ -1670,21 +1668,7 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
       return KH_ERR_UNSUPPORTED;
     }
     const int row_base = kv_done ? kvrows : 0;
-    if (nrm.w && NB == 1 && hsel && hsel->bf16)
-      hipLaunchKernelGGL((attn_qkv_kernel<1, true, uint16_t>), dim3((rows - row_base) / kQkvWaves + 1),
-                         dim3(64 * kQkvWaves), lds, st, a->wkvq, x, batch, H, kvrows, D, a->nh,
-                         nullptr, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
-                         a->qrows + qd + 1, nrm.w, nrm.inv, row_base,
-                         static_cast<const uint16_t*>(hsel->w2b), hsel->b2, hsel->hbuf, hsel->hid,
-                         const_cast<int32_t*>(heads));
-    else if (nrm.w && NB == 1 && hsel)
-      hipLaunchKernelGGL((attn_qkv_kernel<1, true, float>), dim3((rows - row_base) / kQkvWaves + 1),
-                         dim3(64 * kQkvWaves), lds, st, a->wkvq, x, batch, H, kvrows, D, a->nh,
-                         nullptr, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
-                         a->qrows + qd + 1, nrm.w, nrm.inv, row_base,
-                         static_cast<const float*>(hsel->w2b), hsel->b2, hsel->hbuf, hsel->hid,
-                         const_cast<int32_t*>(heads));
-    else if (nrm.w && NB == 1)
+    if (nrm.w && NB == 1)
       hipLaunchKernelGGL((attn_qkv_kernel<1, true>), dim3((rows - row_base) / kQkvWaves + 1),
                          dim3(64 * kQkvWaves), lds, st, a->wkvq, x, batch, H, kvrows, D, a->nh,
                          heads, nsel, a->y, a->ystride(), a->qrows, a->qrows + qd,
@@ -1838,20 +1822,33 @@ extern "C" int kh_dejavu_attn_block(const kh_predictor* p, kh_sparse_attn* a, fl
     });
     KH_HIP(arc);
     const int nl1 = ceil_div(v.hid, kL1Chains);
-    const int nkv = std::max(1, std::min(attn_device_cus() - nl1, kvrows / kQkvWaves));
+    // when the head scores fit a wave, the launch also projects the Q rows of
+    // every head (the selection, one small kernel after it, then only picks);
+    // else the K/V rows, and the Q projection selects after it
+    const bool all_q = v.out_dim <= 64 && v.hid <= kAttnSelHid;
+    const int prow = all_q ? kvrows + a->nh * a->d : kvrows;
+    const int nkv = std::max(1, std::min(attn_device_cus() - nl1, prow / kQkvWaves));
     if (v.bf16)
       hipLaunchKernelGGL(attn_pred_kv_kernel<uint16_t>, dim3(nl1 + nkv), dim3(kL1LdsThreads), kL1LdsBytes,
                          st, static_cast<const uint16_t*>(v.w1b), v.b1, v.hid, v.hbuf, hidden_dev, a->hidden,
-                         norm_w_dev, norm_ws_dev, eps, a->wkvq, kvrows, a->y, nl1);
+                         norm_w_dev, norm_ws_dev, eps, a->wkvq, prow, a->y, nl1);
     else
       hipLaunchKernelGGL(attn_pred_kv_kernel<float>, dim3(nl1 + nkv), dim3(kL1LdsThreads), kL1LdsBytes,
                          st, static_cast<const float*>(v.w1b), v.b1, v.hid, v.hbuf, hidden_dev, a->hidden,
-                         norm_w_dev, norm_ws_dev, eps, a->wkvq, kvrows, a->y, nl1);
+                         norm_w_dev, norm_ws_dev, eps, a->wkvq, prow, a->y, nl1);
     KH_LAUNCHED();
-    // layer 2 and the top k inside the Q projection (every block selects the
-    // heads itself, the last one writes them) when the head scores fit a wave
-    if (v.out_dim <= 64 && v.hid <= kAttnSelHid) {
-      rc = attn_launch<1>(a, hidden_dev, 1, nullptr, heads_dev, k, hidden_dev, 1, st, nrm, true, &v);
+    if (all_q) {
+      const int qd = a->nh * a->d;
+      if (v.bf16)
+        hipLaunchKernelGGL(attn_select_plan_kernel<uint16_t>, dim3(1), dim3(kSelPlanThreads), 0, st,
+                           static_cast<const uint16_t*>(v.w2b), v.b2, v.hbuf, v.hid, a->nh, k, a->d, heads_dev,
+                           a->qrows, a->qrows + qd, a->qrows + qd + 1);
+      else
+        hipLaunchKernelGGL(attn_select_plan_kernel<float>, dim3(1), dim3(kSelPlanThreads), 0, st,
+                           static_cast<const float*>(v.w2b), v.b2, v.hbuf, v.hid, a->nh, k, a->d, heads_dev,
+                           a->qrows, a->qrows + qd, a->qrows + qd + 1);
+      KH_LAUNCHED();
+      rc = attn_launch<1>(a, hidden_dev, 1, nullptr, heads_dev, k, hidden_dev, 1, st, nrm, true, nullptr, true);
       if (rc == KH_OK) a->len_host[0] += 1;
       return rc;
     }

@@ -248,6 +248,7 @@ def test_rejects_bad_shapes(kh, orc):
 @pytest.mark.parametrize("H,nh,nkv,d,R,k,pre,steps", [
     (4096, 32, 32, 128, 128, 16, 2000, 4),   # cfg4 (7B): 32 heads x 128, cache ~2048, top 50% of heads
     (512, 8, 4, 64, 32, 3, 20, 3),           # GQA, small
+    (512, 8, 8, 64, 160, 3, 20, 2),          # head predictor wider than a wave's chain: separate top k
 ])
 def test_attn_block_chained(kh, orc, H, nh, nkv, d, R, k, pre, steps):
     """kh_dejavu_attn_block over several decode steps against the oracle's
