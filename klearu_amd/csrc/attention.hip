@@ -149,28 +149,6 @@ __device__ __forceinline__ void attn_select_heads(const PW* __restrict__ w2, con
   __syncthreads();
 }
 
-// The head selection of a batch-1 decode step whose projections, the Q rows
-// of every head included, are done: the head predictor's layer 2 and top k
-// (attn_select_heads) into heads_out[k], then the o_proj row list (qkv_plan).
-// One block.
-constexpr int kSelPlanThreads = 256;
-template <typename PW>
-__global__ __launch_bounds__(kSelPlanThreads) void attn_select_plan_kernel(
-    const PW* __restrict__ w2, const float* __restrict__ b2, const float* __restrict__ hpred, int phid, int nh,
-    int k, int D, int32_t* __restrict__ heads_out, int32_t* __restrict__ qrows, int32_t* __restrict__ nqrows,
-    int32_t* __restrict__ urank) {
-  __shared__ int s_hsel[64];
-  __shared__ int32_t s_heads[64];
-  __shared__ __align__(16) float s_hp[kAttnSelHid + 4 * kL2Hw];
-  __shared__ uint64_t s_tab[32];
-  __shared__ int s_flag[64], s_uh[64];
-  __shared__ int wsum[kSelPlanThreads / 64];
-  __shared__ int s_total;
-  attn_select_heads<PW>(w2, b2, hpred, phid, nh, k, s_hp, s_tab, s_hsel, s_heads);
-  if ((int)threadIdx.x < k) heads_out[threadIdx.x] = s_heads[threadIdx.x];
-  qkv_plan(s_heads, k, nh, D, qrows, nqrows, urank, s_flag, s_uh, wsum, &s_total);
-}
-
 // The head selections of rows 0 .. batch-1 as attn_select_heads, one row per
 // wave (rows w, w + waves, ...) over the head predictor's layer-1 outputs
 // hpred[batch][phid]: s_any[h] = 1 when some row selected head h, s_heads[b k
@@ -880,7 +858,13 @@ __device__ __forceinline__ void attn_decode_chunk(
 }
 
 
-template <int D>
+// PW (not void; batch 1, with the projections of every head done): the heads
+// are selected, not read: every live chunk block runs the head predictor's
+// layer 2 and top k (attn_select_heads over hpred), and block (0, 0, 0) writes
+// them to heads_out and the o_proj row list to qrows_out / nqrows_out for the
+// kernel after this one.  The union is then the token's own selection, so the
+// append blocks zero-fill nothing.
+template <int D, typename PW = void>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     const uint16_t* __restrict__ kc16, const uint16_t* __restrict__ vc16, float* __restrict__ kc32,
     float* __restrict__ vc32, const int32_t* __restrict__ pre, const float* __restrict__ y,
@@ -888,7 +872,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     const int32_t* __restrict__ lens, const int64_t* __restrict__ positions,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, int max_seq, float inv_sqrt,
     int nsplit, const int32_t* __restrict__ urank, float* __restrict__ po, float2* __restrict__ pml,
-    float* __restrict__ cat, int catstride) {
+    float* __restrict__ cat, int catstride, const PW* __restrict__ w2 = nullptr,
+    const float* __restrict__ b2 = nullptr, const float* __restrict__ hpred = nullptr, int phid = 0,
+    int32_t* __restrict__ heads_out = nullptr, int32_t* __restrict__ qrows_out = nullptr,
+    int32_t* __restrict__ nqrows_out = nullptr) {
+  constexpr bool SEL = !std::is_void<PW>::value;
+  __shared__ int s_hsel[SEL ? 64 : 1];
+  __shared__ int32_t s_heads[SEL ? 64 : 1];
+  __shared__ __align__(16) float s_hp[SEL ? kAttnSelHid + 4 * kL2Hw : 4];
+  __shared__ uint64_t s_stab[SEL ? 32 : 1];
   constexpr int HALF = D / 2;
   constexpr int CH16 = attn_chunk<uint16_t, D>(), CH32 = attn_chunk<float, D>();
   const int a = blockIdx.x, b = blockIdx.y, s = blockIdx.z, t = threadIdx.x;
@@ -900,7 +892,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   const float* yb = y + (size_t)b * ystride;
   const float* ct = cos_t + pos * HALF;
   const float* st = sin_t + pos * HALF;
-  const int32_t* hb = heads + (size_t)b * nsel;
+  const int32_t* hb = SEL ? s_heads : heads + (size_t)b * nsel;
   if (a == nsel) {
     if (valid) {
       // KvCache::append (kv_cache.rs:33-48) of the roped k (sparse_attention.rs:33-39)
@@ -917,14 +909,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
         }
       }
     }
-    for (int hu = s; hu < nh; hu += (int)gridDim.z) {
-      const int u = urank[hu];
-      if (u < 0) continue;
-      int sel = 0;
-      if (valid)
-        for (int i = 0; i < nsel; ++i) sel |= hb[i] == hu;
-      if (!sel)
-        for (int i = t; i < D; i += kAttnThreads) cat[(size_t)b * catstride + (size_t)u * D + i] = 0.0f;
+    if constexpr (!SEL) {
+      for (int hu = s; hu < nh; hu += (int)gridDim.z) {
+        const int u = urank[hu];
+        if (u < 0) continue;
+        int sel = 0;
+        if (valid)
+          for (int i = 0; i < nsel; ++i) sel |= hb[i] == hu;
+        if (!sel)
+          for (int i = t; i < D; i += kAttnThreads) cat[(size_t)b * catstride + (size_t)u * D + i] = 0.0f;
+      }
     }
     return;
   }
@@ -933,6 +927,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   const int n16b = (pb + CH16 - 1) / CH16;
   const int ns = n16b + (len + 1 - pb + CH32 - 1) / CH32;
   if (s >= ns) return;
+  if constexpr (SEL) {
+    attn_select_heads<PW>(w2, b2, hpred, phid, nh, nsel, s_hp, s_stab, s_hsel, s_heads);
+    if (a == 0 && s == 0) {
+      for (int i = t; i < nsel; i += kAttnThreads) heads_out[i] = s_heads[i];
+      // the o_proj rows: each selected head's D rows, heads ascending
+      for (int i = t; i < nsel * D; i += kAttnThreads) qrows_out[i] = s_heads[i / D] * D + i % D;
+      if (t == 0) *nqrows_out = nsel * D;
+    }
+  }
   if (s < n16b)
     attn_decode_chunk<uint16_t, D>(kc16, vc16, s * CH16, pb, s, yb, kvd, nh, nkv, hb, a, b, len, ct, st,
                                    max_seq, inv_sqrt, nsel, nsplit, po, pml);
@@ -1575,12 +1578,26 @@ extern "C" int kh_sparse_attn_clear(kh_sparse_attn* a, void* stream) {
 template <int D>
 static int attn_decode_launch(kh_sparse_attn* a, int batch, const int64_t* pos,
                               const int32_t* heads, int nsel, int nsplit, float* po,
-                              float2* pml, bool merge, hipStream_t st) {
+                              float2* pml, bool merge, hipStream_t st, const PredL1View* hsel = nullptr) {
   const int qd = a->nh * D;
-  hipLaunchKernelGGL(attn_decode_kernel<D>, dim3(nsel + 1, batch, nsplit), dim3(kAttnThreads), 0, st,
-                     a->kc16, a->vc16, a->kc32, a->vc32, a->pre, a->y, a->ystride(), a->nkv, a->nh,
-                     heads, nsel, a->lens, pos, a->cos_t, a->sin_t, a->max_seq,
-                     1.0f / sqrtf(static_cast<float>(D)), nsplit, a->qrows + qd + 1, po, pml, a->cat, qd);
+  const dim3 g(nsel + 1, batch, nsplit);
+  const float isq = 1.0f / sqrtf(static_cast<float>(D));
+  if (!hsel)
+    hipLaunchKernelGGL(attn_decode_kernel<D>, g, dim3(kAttnThreads), 0, st, a->kc16, a->vc16, a->kc32, a->vc32,
+                       a->pre, a->y, a->ystride(), a->nkv, a->nh, heads, nsel, a->lens, pos, a->cos_t, a->sin_t,
+                       a->max_seq, isq, nsplit, a->qrows + qd + 1, po, pml, a->cat, qd);
+  else if (hsel->bf16)
+    hipLaunchKernelGGL((attn_decode_kernel<D, uint16_t>), g, dim3(kAttnThreads), 0, st, a->kc16, a->vc16, a->kc32,
+                       a->vc32, a->pre, a->y, a->ystride(), a->nkv, a->nh, nullptr, nsel, a->lens, pos, a->cos_t,
+                       a->sin_t, a->max_seq, isq, nsplit, a->qrows + qd + 1, po, pml, a->cat, qd,
+                       static_cast<const uint16_t*>(hsel->w2b), hsel->b2, hsel->hbuf, hsel->hid,
+                       const_cast<int32_t*>(heads), a->qrows, a->qrows + qd);
+  else
+    hipLaunchKernelGGL((attn_decode_kernel<D, float>), g, dim3(kAttnThreads), 0, st, a->kc16, a->vc16, a->kc32,
+                       a->vc32, a->pre, a->y, a->ystride(), a->nkv, a->nh, nullptr, nsel, a->lens, pos, a->cos_t,
+                       a->sin_t, a->max_seq, isq, nsplit, a->qrows + qd + 1, po, pml, a->cat, qd,
+                       static_cast<const float*>(hsel->w2b), hsel->b2, hsel->hbuf, hsel->hid,
+                       const_cast<int32_t*>(heads), a->qrows, a->qrows + qd);
   KH_LAUNCHED();
   if (!merge) return KH_OK;
   hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(nsel, batch), dim3(D), 0, st, po, pml, nsplit,
@@ -1610,8 +1627,9 @@ static void qm_launch(kh_sparse_attn* a, const uint16_t* w, const float* x, int 
 // written to heads.
 // kv_done (batch 1 with nrm.w, or batch > 1 with hsel): attn_pred_kv_kernel or
 // attn_pred_kv_mfma_kernel projected the K/V rows, so only the selected heads'
-// Q rows remain.  qkv_done: every projection and the o_proj row list are done
-// (attn_pred_kv_kernel and attn_select_plan_kernel).
+// Q rows remain.  qkv_done: every projection is done (attn_pred_kv_kernel); with
+// hsel at batch 1 the decode kernel selects the heads and writes the o_proj
+// row list.
 template <int NB>
 static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64_t* pos,
                        const int32_t* heads, int nsel, float* out, int accumulate,
@@ -1699,9 +1717,11 @@ static int attn_launch(kh_sparse_attn* a, const float* x, int batch, const int64
   // separate merge, one block per (entry, token), is faster)
   constexpr int kFoldNB = NB <= 2 ? NB : 2;
   const bool fold = NB <= 2 && nsel <= kOprojMaxSel;
-  int rc = D == 64 ? attn_decode_launch<64>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st)
-         : D == 128 ? attn_decode_launch<128>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st)
-                    : attn_decode_launch<256>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st);
+  // qkv_done with hsel (batch 1): the decode kernel selects the heads
+  const PredL1View* dsel = qkv_done && NB == 1 && fold ? hsel : nullptr;
+  int rc = D == 64 ? attn_decode_launch<64>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st, dsel)
+         : D == 128 ? attn_decode_launch<128>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st, dsel)
+                    : attn_decode_launch<256>(a, batch, pos, heads, nsel, nsplit, po, pml, !fold, st, dsel);
   if (rc != KH_OK) return rc;
   // 3. o_proj over the union heads' rows of WoT, then the ordered reduce
   //    (batch > 2: 128-row groups on the BF16 matrix cores)
@@ -1838,17 +1858,8 @@ extern "C" int kh_dejavu_attn_block(const kh_predictor* p, kh_sparse_attn* a, fl
                          norm_w_dev, norm_ws_dev, eps, a->wkvq, prow, a->y, nl1);
     KH_LAUNCHED();
     if (all_q) {
-      const int qd = a->nh * a->d;
-      if (v.bf16)
-        hipLaunchKernelGGL(attn_select_plan_kernel<uint16_t>, dim3(1), dim3(kSelPlanThreads), 0, st,
-                           static_cast<const uint16_t*>(v.w2b), v.b2, v.hbuf, v.hid, a->nh, k, a->d, heads_dev,
-                           a->qrows, a->qrows + qd, a->qrows + qd + 1);
-      else
-        hipLaunchKernelGGL(attn_select_plan_kernel<float>, dim3(1), dim3(kSelPlanThreads), 0, st,
-                           static_cast<const float*>(v.w2b), v.b2, v.hbuf, v.hid, a->nh, k, a->d, heads_dev,
-                           a->qrows, a->qrows + qd, a->qrows + qd + 1);
-      KH_LAUNCHED();
-      rc = attn_launch<1>(a, hidden_dev, 1, nullptr, heads_dev, k, hidden_dev, 1, st, nrm, true, nullptr, true);
+      // the decode kernel's blocks select the heads themselves
+      rc = attn_launch<1>(a, hidden_dev, 1, nullptr, heads_dev, k, hidden_dev, 1, st, nrm, true, &v, true);
       if (rc == KH_OK) a->len_host[0] += 1;
       return rc;
     }
