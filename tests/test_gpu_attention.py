@@ -448,6 +448,87 @@ def test_decoder_layers_chained_7b(kh, orc):
         close(hd.cpu().numpy(), h_in + y, f"layer {layer} MLP")
 
 
+def _decoder_layer(orc, seed, H, nh, nkv, d, I, Rh, Rn, pre, max_seq, B):
+    """A sparse decoder layer's handles from one seed: the attention weights and
+    preloaded caches, the head predictor, the neuron predictor and the MLP."""
+    from klearu_amd.dejavu import Mlp, SparsityPredictor
+    rng = np.random.default_rng(seed)
+    bf = lambda a: orc.bf16_from_f32(np.asarray(a, np.float32))  # noqa: E731
+    c = Case(orc, rng, H, nh, nkv, d, max_seq, B, pre)
+    _, hp = _head_predictor(orc, rng, H, nh, Rh)
+    nw1, nw2 = bf(rng.normal(0, 0.02, (Rn, H))), bf(rng.normal(0, 0.02, (I, Rn)))
+    nb1, nb2 = rng.normal(0, 0.1, Rn).astype(np.float32), rng.normal(0, 0.1, I).astype(np.float32)
+    npred = SparsityPredictor(orc.bf16_to_f32(nw1), nb1, orc.bf16_to_f32(nw2), nb2)
+    wg, wu = bf(rng.normal(0, 0.02, (I, H))), bf(rng.normal(0, 0.02, (I, H)))
+    mlp = Mlp(wg, wu, bf(rng.normal(0, 0.02, (H, I))), max_batch=B)
+    return c.attn, hp, npred, mlp
+
+
+@pytest.mark.parametrize("B", [1, 4])
+def test_decoder_layer_graph_replays_match_eager(kh, orc, B):
+    """One sparse decoder layer step (kh_dejavu_attn_block[_batch], then
+    kh_dejavu_mlp_block[_batch]) captured in a HIP graph, as bench.py times it,
+    and replayed step after step while the KV caches grow on the device.  A
+    twin layer (the same weights and caches) runs the same steps eagerly on
+    the same stream between the replays.  After every replay the rows, head
+    sets, neuron sets and RmsNorm scales equal the eager step's bit for bit
+    (the same kernels on the same inputs), and so do the cache lengths read
+    back from the device."""
+    from klearu_amd.attention import attn_block, attn_block_batch
+    from klearu_amd.dejavu import mlp_block, mlp_block_batch
+    H, nh, nkv, d, I, Rh, Rn, kh_, kn, pre, steps = 2048, 32, 4, 64, 5632, 64, 128, 8, 845, 150, 5
+    pres = [pre - 5 * b for b in range(B)]  # ragged caches
+    eager = _decoder_layer(orc, 77, H, nh, nkv, d, I, Rh, Rn, pres, pre + steps + 8, B)
+    graph = _decoder_layer(orc, 77, H, nh, nkv, d, I, Rh, Rn, pres, pre + steps + 8, B)
+    rng = np.random.default_rng(5)
+    x0 = torch.from_numpy(rng.standard_normal((B, H)).astype(np.float32)).cuda()
+    wn_a = torch.from_numpy(rng.uniform(0.5, 1.5, H).astype(np.float32)).cuda()
+    wn_m = torch.from_numpy(rng.uniform(0.5, 1.5, H).astype(np.float32)).cuda()
+
+    def state():
+        return dict(h=x0.clone(), heads=torch.full((B, kh_), -1, dtype=torch.int32, device="cuda"),
+                    act=torch.full((B, kn), -1, dtype=torch.int32, device="cuda"),
+                    wsa=torch.zeros(B, device="cuda"), wsm=torch.zeros(B, device="cuda"))
+
+    def step(layer, t, s):
+        attn, hp, npred, mlp = layer
+        if B == 1:
+            attn_block(hp, attn, t["h"][0], wn_a, 1e-5, kh_, heads=t["heads"][0], norm_ws=t["wsa"], stream=s)
+            mlp_block(npred, mlp, t["h"][0], wn_m, 1e-5, kn, active=t["act"][0], norm_ws=t["wsm"], stream=s)
+        else:
+            attn_block_batch(hp, attn, t["h"], wn_a, 1e-5, kh_, heads=t["heads"], norm_ws=t["wsa"], stream=s)
+            mlp_block_batch(npred, mlp, t["h"], wn_m, 1e-5, kn, active=t["act"], norm_ws=t["wsm"], stream=s)
+
+    def same(te, tg, what):
+        for key in ("h", "wsa", "wsm"):
+            np.testing.assert_array_equal(tg[key].cpu().numpy().view(np.uint32), te[key].cpu().numpy().view(np.uint32),
+                                          err_msg=f"{what}: {key}")
+        for key in ("heads", "act"):
+            np.testing.assert_array_equal(tg[key].cpu().numpy(), te[key].cpu().numpy(), err_msg=f"{what}: {key}")
+
+    te, tg = state(), state()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        step(eager, te, s)  # the warm-up call sizes the scratch buffers the capture records
+        step(graph, tg, s)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            step(graph, tg, s)
+    torch.cuda.synchronize()
+    same(te, tg, "warm-up step")
+    for i in range(steps):
+        with torch.cuda.stream(s):
+            step(eager, te, s)
+            s.synchronize()
+            g.replay()
+        torch.cuda.synchronize()
+        print(f"B={B} replay {i}: heads {tg['heads'][0, :4].tolist()} ...", flush=True)
+        same(te, tg, f"replay {i}")
+        for b in range(B):
+            assert graph[0].current_len(b) == eager[0].current_len(b) == pres[b] + 2 + i
+
+
 @pytest.mark.parametrize("pre", [0, 200])
 def test_bf16_handle_matches_unrounded_reference_cache(kh, orc, pre):
     """A default (KH_KV_BF16) handle over many decode steps against the oracle's
