@@ -47,14 +47,14 @@ SIGS = {
     "kh_version": (I, []),
     "kh_dense_dot_dense": (I, [P, I64, I64, P, I64, P, P]),
     "kh_expf": (I, [P, P, I64, P]),
-    "kh_dejavu_linear_create": (I, [I, I, P, P, P]),
+    "kh_dejavu_linear_create": (I, [I, I, P, P, PP]),
     "kh_dejavu_linear_destroy": (I, [P]),
     "kh_dejavu_linear_forward": (I, [P, P, I64, P, P]),
     "kh_dejavu_linear_forward_sparse": (I, [P, P, I64, P, I64, P, P]),
-    "kh_dejavu_sparse_mlp_create": (I, [I, I, P]),
+    "kh_dejavu_sparse_mlp_create": (I, [I, I, PP]),
     "kh_dejavu_sparse_mlp_destroy": (I, [P]),
     "kh_dejavu_sparse_mlp_forward": (I, [P, P, I64, P, P, P, P, I64, P, P]),
-    "kh_dejavu_sparse_attention_create": (I, [I, I, I, P]),
+    "kh_dejavu_sparse_attention_create": (I, [I, I, I, PP]),
     "kh_dejavu_sparse_attention_destroy": (I, [P]),
     "kh_dejavu_sparse_attention_forward": (I, [P, P, I64, P, P, P, P, P, I64, P, P]),
     "kh_sparse_dot_dense": (I, [P, P, I64, P, I64, P, P]),
@@ -96,7 +96,7 @@ SIGS = {
     "kh_slide_layer_init_optimizer": (I, [P, I, F, F, F, F]),
     "kh_slide_layer_weights": (I, [P, P, P]),
     "kh_slide_layer_backward": (I, [P, P, P, P, P, P, P, I64, C.c_double, U64, P, P]),
-    "kh_slide_network_create": (I, [P, I, I, F, F, F, F, U64, C.c_double, PP]),
+    "kh_slide_network_create": (I, [PP, I, I, F, F, F, F, U64, C.c_double, PP]),
     "kh_slide_network_destroy": (I, [P]),
     "kh_slide_network_train_step": (I, [P, P, I64, P, P, C.c_double, P, P]),
     "kh_slide_network_predict": (I, [P, P, I64, P, P]),
