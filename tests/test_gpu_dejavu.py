@@ -646,3 +646,60 @@ def test_predictor_concurrent_streams(kh, orc):
     for t in th:
         t.join()
     assert not errors, errors
+
+
+@pytest.mark.parametrize("B", [1, 16])
+def test_mlp_block_graph_replays_match_eager_7b(kh, orc, B):
+    """The headline step at cfg3's shape (hidden 4096, intermediate 11008, top
+    1652; batch 1 and 16): kh_dejavu_mlp_block[_batch] captured in a HIP graph
+    as bench.py times it, replayed several times with eager calls of a twin
+    (the same weights, its own handles) on the same stream between the replays.
+    After every replay the rows, neuron sets and RmsNorm scales equal the eager
+    call's bit for bit."""
+    from klearu_amd.dejavu import Mlp, SparsityPredictor, mlp_block, mlp_block_batch
+    H, I, R, k, calls = 4096, 11008, 256, 1652, 4
+    rng = np.random.default_rng(11 + B)
+    bf = lambda a: orc.bf16_from_f32(np.asarray(a, np.float32))  # noqa: E731
+    w1, w2 = bf(rng.normal(0, 0.02, (R, H))), bf(rng.normal(0, 0.02, (I, R)))
+    b1, b2 = rng.normal(0, 0.1, R).astype(np.float32), rng.normal(0, 0.1, I).astype(np.float32)
+    wg, wu, wd = bf(rng.normal(0, 0.02, (I, H))), bf(rng.normal(0, 0.02, (I, H))), bf(rng.normal(0, 0.02, (H, I)))
+    wn = torch.from_numpy(rng.uniform(0.5, 1.5, H).astype(np.float32)).cuda()
+    x0 = torch.from_numpy(rng.standard_normal((B, H)).astype(np.float32)).cuda()
+
+    def twin():
+        return dict(p=SparsityPredictor(orc.bf16_to_f32(w1), b1, orc.bf16_to_f32(w2), b2),
+                    mlp=Mlp(wg, wu, wd, max_batch=B), h=x0.clone(),
+                    act=torch.full((B, k), -1, dtype=torch.int32, device="cuda"),
+                    ws=torch.zeros(B, device="cuda"))
+
+    def call(t, s):
+        if B == 1:
+            mlp_block(t["p"], t["mlp"], t["h"][0], wn, 1e-5, k, active=t["act"][0], norm_ws=t["ws"], stream=s)
+        else:
+            mlp_block_batch(t["p"], t["mlp"], t["h"], wn, 1e-5, k, active=t["act"], norm_ws=t["ws"], stream=s)
+
+    def same(te, tg, what):
+        for key in ("h", "ws"):
+            np.testing.assert_array_equal(tg[key].cpu().numpy().view(np.uint32), te[key].cpu().numpy().view(np.uint32),
+                                          err_msg=f"{what}: {key}")
+        np.testing.assert_array_equal(tg["act"].cpu().numpy(), te["act"].cpu().numpy(), err_msg=f"{what}: ids")
+
+    te, tg = twin(), twin()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        call(te, s)  # the warm-up call sizes the scratch buffers the capture records
+        call(tg, s)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            call(tg, s)
+    torch.cuda.synchronize()
+    same(te, tg, "warm-up call")
+    for i in range(calls):
+        with torch.cuda.stream(s):
+            call(te, s)
+            s.synchronize()
+            g.replay()
+        torch.cuda.synchronize()
+        print(f"B={B} replay {i}: first ids {tg['act'][0, :4].tolist()}", flush=True)
+        same(te, tg, f"replay {i}")
