@@ -354,6 +354,7 @@ def test_rmsnorm_bit_exact(kh, orc):
 @pytest.mark.parametrize("H,I,R,k,layers", [
     (4096, 11008, 256, 1652, 4),   # cfg3 (7B): hidden 4096, 11008 neurons, rank 256, top 15%
     (2048, 5632, 128, 564, 3),     # cfg2 (1.1B): top 10%
+    (2048, 5632, 128, 563, 2),     # cfg2, ragged: the last 8-neuron block takes 3
 ])
 def test_mlp_block_chained_exact(kh, orc, H, I, R, k, layers):
     """kh_dejavu_mlp_block chained over several layers against the oracle's
